@@ -1,0 +1,727 @@
+// sh_api.hip — the C ABI declared in include/stories_hip.h: model lifetime, weight upload,
+// the device-resident decode loop (one captured HIP graph per token forward), and the
+// device quantizer entry points.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "sh_internal.hpp"
+
+namespace sh {
+
+static thread_local std::string g_err;
+static thread_local int g_device = 0;
+
+void set_error(const std::string &msg) { g_err = msg; }
+
+bool hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return true;
+    set_error(std::string(what) + ": " + hipGetErrorString(e));
+    return false;
+}
+
+bool gemv_supported(int cols, bool pairs);
+
+namespace {
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+size_t weight_elem_bytes(int dtype) { return dtype == SH_DTYPE_W8A8 ? 1 : 2; }
+size_t kv_elem_bytes(int kv) { return kv == SH_KV_F32 ? 4 : 2; }
+
+bool valid_config(const sh_config &c, int dtype) {
+    auto fail = [](const std::string &m) {
+        set_error("invalid config: " + m);
+        return false;
+    };
+    if (dtype != SH_DTYPE_F16 && dtype != SH_DTYPE_BF16 && dtype != SH_DTYPE_W8A8)
+        return fail("dtype must be SH_DTYPE_F16, SH_DTYPE_BF16 or SH_DTYPE_W8A8");
+    if (c.dim <= 0 || c.hidden <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
+        c.vocab <= 0 || c.max_seq <= 0)
+        return fail("sizes must be positive");
+    if (c.n_heads % c.n_kv_heads) return fail("n_heads must be a multiple of n_kv_heads");
+    if (c.head_dim != 32 && c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
+        return fail("head_dim must be 32, 64, 128 or 256");
+    if (c.max_seq > kMaxSeqLds) return fail("max_seq above 4096");
+    if (c.kv_dtype < SH_KV_F32 || c.kv_dtype > SH_KV_BF16) return fail("kv_dtype");
+    if (c.max_batch < 1) return fail("max_batch must be >= 1");
+    const int qdim = c.n_heads * c.head_dim;
+    if (!gemv_supported(c.dim, true)) return fail("dim has no GEMV tiling");
+    if (!gemv_supported(qdim, false)) return fail("n_heads*head_dim has no GEMV tiling");
+    if (!gemv_supported(c.hidden, false)) return fail("hidden has no GEMV tiling");
+    if (dtype == SH_DTYPE_W8A8) return fail("W8A8 decode is not available in this build");
+    return true;
+}
+
+struct HostBuf {
+    std::vector<uint8_t> v;
+};
+
+// Algorithmic bytes of one forward at position pos: every weight byte once, norms, the
+// K/V rows 0..pos read, one K/V row written, the embedding row and the logits written.
+double forward_bytes(const sh_model *m, int pos) {
+    const sh_config &c = m->cfg;
+    const double eb = (double)weight_elem_bytes(m->dtype);
+    const double D = c.dim, F = c.hidden, Q = m->qdim, KV = m->kvdim;
+    double per_layer = eb * ((Q + 2 * KV) * D + D * Q + 2 * F * D + D * F) + 4.0 * 2 * D;
+    if (c.qk_norm) per_layer += 4.0 * 2 * c.head_dim;
+    const double kvb = (double)kv_elem_bytes(c.kv_dtype);
+    per_layer += kvb * 2 * KV * (double)(pos + 1);  // K and V rows read
+    per_layer += kvb * 2 * KV;                        // K and V row written
+    double total = per_layer * c.n_layers;
+    total += eb * (double)c.vocab * D + 4.0 * D;      // classifier rows + final norm
+    total += 2.0 * D;                                 // embedding row
+    total += 4.0 * c.vocab;                           // logits written
+    return total;
+}
+
+hipError_t ensure_step_graph(sh_model *m) {
+    if (m->step_ready) return hipSuccess;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return e;
+    hipError_t e2 = enqueue_decode_step(m);
+    e = hipStreamEndCapture(m->stream, &g);
+    if (e2 != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return e2;
+    }
+    if (e != hipSuccess) return e;
+    e = hipGraphInstantiate(&m->step_exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return e;
+    m->step_ready = true;
+    return hipSuccess;
+}
+
+bool ready(const sh_model *m) {
+    if (!m) {
+        set_error("nil model");
+        return false;
+    }
+    if (m->uploaded_layers != m->cfg.n_layers || !m->globals_uploaded) {
+        set_error("model weights are not fully uploaded");
+        return false;
+    }
+    return true;
+}
+
+uint64_t splitmix64(uint64_t x) {
+    uint64_t z = x + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+template <typename F>
+void parallel_ranges(size_t n, F fn) {
+    unsigned hw = std::thread::hardware_concurrency();
+    unsigned nt = std::max(1u, std::min(hw ? hw : 1u, 16u));
+    if (n < (1u << 16)) nt = 1;
+    std::vector<std::thread> th;
+    const size_t chunk = (n + nt - 1) / nt;
+    for (unsigned t = 0; t < nt; t++) {
+        const size_t a = t * chunk, b = std::min(n, a + chunk);
+        if (a >= b) break;
+        th.emplace_back([=] { fn(a, b); });
+    }
+    for (auto &t : th) t.join();
+}
+
+uint16_t host_bf16_bits(float x);
+
+}  // namespace
+}  // namespace sh
+
+using namespace sh;
+
+extern "C" {
+
+int sh_init(int32_t device) {
+    int n = 0;
+    if (!hip_ok(hipGetDeviceCount(&n), "hipGetDeviceCount")) return -1;
+    if (device < 0 || device >= n) {
+        set_error("sh_init: device " + std::to_string(device) + " out of range");
+        return -1;
+    }
+    if (!hip_ok(hipSetDevice(device), "hipSetDevice")) return -1;
+    g_device = device;
+    return 0;
+}
+
+size_t sh_last_error(char *buf, size_t len) {
+    if (buf && len) {
+        const size_t n = std::min(len - 1, g_err.size());
+        memcpy(buf, g_err.data(), n);
+        buf[n] = 0;
+    }
+    return g_err.size();
+}
+
+int sh_config_stories110m(sh_config *c) {
+    if (!c) return -1;
+    memset(c, 0, sizeof(*c));
+    c->dim = 768;
+    c->hidden = 2048;
+    c->n_layers = 12;
+    c->n_heads = 12;
+    c->n_kv_heads = 12;
+    c->head_dim = 64;
+    c->vocab = 32000;
+    c->max_seq = 256;
+    c->rope_theta = 10000.0;
+    c->norm_eps = 1e-5;
+    c->qk_norm_eps = 1e-6;
+    c->residual_scale = 1.0f;
+    c->qk_norm = 0;
+    c->tied_embed = 1;
+    c->kv_dtype = SH_KV_F32;
+    c->max_batch = 1;
+    return 0;
+}
+
+int sh_config_qwen3_06b(sh_config *c) {
+    if (!c) return -1;
+    memset(c, 0, sizeof(*c));
+    c->dim = 1024;
+    c->hidden = 3072;
+    c->n_layers = 28;
+    c->n_heads = 16;
+    c->n_kv_heads = 8;
+    c->head_dim = 128;
+    c->vocab = 151936;
+    c->max_seq = 2048;
+    c->rope_theta = 1000000.0;
+    c->norm_eps = 1e-6;
+    c->qk_norm_eps = 1e-6;
+    c->residual_scale = 1.0f;
+    c->qk_norm = 1;
+    c->tied_embed = 1;
+    c->kv_dtype = SH_KV_BF16;
+    c->max_batch = 1;
+    return 0;
+}
+
+sh_model *sh_model_create(const sh_config *cfg, int32_t dtype) {
+    if (!cfg) {
+        set_error("sh_model_create: nil config");
+        return nullptr;
+    }
+    if (!valid_config(*cfg, dtype)) return nullptr;
+    if (!hip_ok(hipSetDevice(g_device), "hipSetDevice")) return nullptr;
+    sh_model *m = new sh_model();
+    memset((void *)m, 0, sizeof(*m));
+    m->cfg = *cfg;
+    m->dtype = dtype;
+    m->device = g_device;
+    const sh_config &c = m->cfg;
+    m->qdim = c.n_heads * c.head_dim;
+    m->kvdim = c.n_kv_heads * c.head_dim;
+    m->qkv_rows = m->qdim + 2 * m->kvdim;
+    const size_t D = c.dim, F = c.hidden, V = c.vocab;
+    const size_t eb = weight_elem_bytes(dtype);
+    const bool w8 = dtype == SH_DTYPE_W8A8;
+
+    // weight arena layout
+    std::vector<size_t> offs;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align_up(off + bytes, 256);
+        return o;
+    };
+    struct LOff {
+        size_t wqkv, wo, w13, w2, sqkv, so, s13, s2, ra, rf, qn, kn;
+    };
+    std::vector<LOff> lo(c.n_layers);
+    for (int l = 0; l < c.n_layers; l++) {
+        lo[l].wqkv = take(eb * m->qkv_rows * D);
+        lo[l].wo = take(eb * D * m->qdim);
+        lo[l].w13 = take(eb * 2 * F * D);
+        lo[l].w2 = take(eb * D * F);
+        lo[l].sqkv = w8 ? take(4 * m->qkv_rows) : 0;
+        lo[l].so = w8 ? take(4 * D) : 0;
+        lo[l].s13 = w8 ? take(4 * 2 * F) : 0;
+        lo[l].s2 = w8 ? take(4 * D) : 0;
+        lo[l].ra = take(4 * D);
+        lo[l].rf = take(4 * D);
+        lo[l].qn = c.qk_norm ? take(4 * c.head_dim) : 0;
+        lo[l].kn = c.qk_norm ? take(4 * c.head_dim) : 0;
+    }
+    const size_t o_embed = take(2 * V * D);
+    const bool own_cls = !c.tied_embed || w8;
+    const size_t o_cls = own_cls ? take(eb * V * D) : 0;
+    const size_t o_scls = w8 ? take(4 * V) : 0;
+    const size_t o_rmsf = take(4 * D);
+    m->arena_bytes = off;
+
+    auto fail = [&](const char *what, hipError_t e) -> sh_model * {
+        hip_ok(e, what);
+        sh_model_destroy(m);
+        return nullptr;
+    };
+    hipError_t e;
+    if ((e = hipMalloc(&m->arena, m->arena_bytes)) != hipSuccess) return fail("hipMalloc arena", e);
+    uint8_t *A = (uint8_t *)m->arena;
+    m->layers = new LayerDev[c.n_layers];
+    for (int l = 0; l < c.n_layers; l++) {
+        LayerDev &L = m->layers[l];
+        L.wqkv = A + lo[l].wqkv;
+        L.wo = A + lo[l].wo;
+        L.w13 = A + lo[l].w13;
+        L.w2 = A + lo[l].w2;
+        L.s_qkv = w8 ? (float *)(A + lo[l].sqkv) : nullptr;
+        L.s_o = w8 ? (float *)(A + lo[l].so) : nullptr;
+        L.s_13 = w8 ? (float *)(A + lo[l].s13) : nullptr;
+        L.s_2 = w8 ? (float *)(A + lo[l].s2) : nullptr;
+        L.rms_att = (float *)(A + lo[l].ra);
+        L.rms_ffn = (float *)(A + lo[l].rf);
+        L.q_norm = c.qk_norm ? (float *)(A + lo[l].qn) : nullptr;
+        L.k_norm = c.qk_norm ? (float *)(A + lo[l].kn) : nullptr;
+    }
+    m->embed = A + o_embed;
+    m->cls = own_cls ? (void *)(A + o_cls) : m->embed;
+    m->s_cls = w8 ? (float *)(A + o_scls) : nullptr;
+    m->rms_final = (float *)(A + o_rmsf);
+
+    m->kv_elems = (size_t)c.max_batch * c.n_layers * c.max_seq * m->kvdim;
+    const size_t kvb = kv_elem_bytes(c.kv_dtype) * m->kv_elems;
+    if ((e = hipMalloc(&m->kcache, kvb)) != hipSuccess) return fail("hipMalloc kcache", e);
+    if ((e = hipMalloc(&m->vcache, kvb)) != hipSuccess) return fail("hipMalloc vcache", e);
+
+    // RoPE tables, infer.go:97-107: float64 angle, float32 cos/sin
+    const int half = c.head_dim / 2;
+    std::vector<float> rc((size_t)c.max_seq * half), rs((size_t)c.max_seq * half);
+    for (int pos = 0; pos < c.max_seq; pos++)
+        for (int i = 0; i < half; i++) {
+            const double freq =
+                (double)pos / pow(c.rope_theta, (double)(2 * i) / (double)c.head_dim);
+            rc[(size_t)pos * half + i] = (float)cos(freq);
+            rs[(size_t)pos * half + i] = (float)sin(freq);
+        }
+    if ((e = hipMalloc(&m->rope_cos, rc.size() * 4)) != hipSuccess) return fail("hipMalloc rope", e);
+    if ((e = hipMalloc(&m->rope_sin, rs.size() * 4)) != hipSuccess) return fail("hipMalloc rope", e);
+    if ((e = hipMemcpy(m->rope_cos, rc.data(), rc.size() * 4, hipMemcpyHostToDevice)) != hipSuccess)
+        return fail("hipMemcpy rope", e);
+    if ((e = hipMemcpy(m->rope_sin, rs.data(), rs.size() * 4, hipMemcpyHostToDevice)) != hipSuccess)
+        return fail("hipMemcpy rope", e);
+
+    const size_t widest = std::max({D, (size_t)m->qkv_rows, 2 * F, (size_t)m->qdim});
+    m->n_partials = gemv_partials(m);
+    if (m->n_partials <= 0) return fail("classifier tiling", hipErrorInvalidValue);
+    if ((e = hipMalloc(&m->x, 4 * D)) != hipSuccess) return fail("hipMalloc x", e);
+    if ((e = hipMalloc(&m->x2, 4 * D)) != hipSuccess) return fail("hipMalloc x2", e);
+    if ((e = hipMalloc(&m->qkv, 4 * widest)) != hipSuccess) return fail("hipMalloc qkv", e);
+    if ((e = hipMalloc(&m->att, 4 * widest)) != hipSuccess) return fail("hipMalloc att", e);
+    if ((e = hipMalloc(&m->gate, 4 * F)) != hipSuccess) return fail("hipMalloc gate", e);
+    if ((e = hipMalloc(&m->logits, 4 * V)) != hipSuccess) return fail("hipMalloc logits", e);
+    if ((e = hipMalloc(&m->partials, sizeof(ArgmaxPartial) * m->n_partials)) != hipSuccess)
+        return fail("hipMalloc partials", e);
+    if ((e = hipMalloc(&m->tokens, 4 * (c.max_seq + 1))) != hipSuccess) return fail("hipMalloc tokens", e);
+    if ((e = hipMalloc(&m->argmax_hist, 4 * (c.max_seq + 1))) != hipSuccess)
+        return fail("hipMalloc hist", e);
+    if ((e = hipMalloc(&m->state, sizeof(DecodeState))) != hipSuccess) return fail("hipMalloc state", e);
+    if ((e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking)) != hipSuccess)
+        return fail("hipStreamCreate", e);
+    if ((e = hipEventCreate(&m->ev0)) != hipSuccess) return fail("hipEventCreate", e);
+    if ((e = hipEventCreate(&m->ev1)) != hipSuccess) return fail("hipEventCreate", e);
+    if ((e = hipMemsetAsync(m->kcache, 0, kvb, m->stream)) != hipSuccess) return fail("memset kv", e);
+    if ((e = hipMemsetAsync(m->vcache, 0, kvb, m->stream)) != hipSuccess) return fail("memset kv", e);
+    if ((e = hipMemsetAsync(m->tokens, 0, 4 * (c.max_seq + 1), m->stream)) != hipSuccess)
+        return fail("memset tokens", e);
+    if ((e = hipStreamSynchronize(m->stream)) != hipSuccess) return fail("sync", e);
+    return m;
+}
+
+void sh_model_destroy(sh_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    if (m->step_ready) (void)hipGraphExecDestroy(m->step_exec);
+    (void)hipFree(m->arena);
+    (void)hipFree(m->kcache);
+    (void)hipFree(m->vcache);
+    (void)hipFree(m->rope_cos);
+    (void)hipFree(m->rope_sin);
+    (void)hipFree(m->x);
+    (void)hipFree(m->x2);
+    (void)hipFree(m->qkv);
+    (void)hipFree(m->att);
+    (void)hipFree(m->gate);
+    (void)hipFree(m->logits);
+    (void)hipFree(m->partials);
+    (void)hipFree(m->tokens);
+    (void)hipFree(m->argmax_hist);
+    (void)hipFree(m->state);
+    if (m->ev0) (void)hipEventDestroy(m->ev0);
+    if (m->ev1) (void)hipEventDestroy(m->ev1);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete[] m->layers;
+    delete m;
+}
+
+static int upload_matrix(sh_model *m, float *staging, const float *host, int rows, int cols,
+                         void *dst, float *scales, int stride, int offset) {
+    const size_t n = (size_t)rows * cols;
+    if (!hip_ok(hipMemcpyAsync(staging, host, n * 4, hipMemcpyHostToDevice, m->stream),
+                "upload weights"))
+        return -1;
+    hipError_t e;
+    if (m->dtype == SH_DTYPE_W8A8)
+        e = launch_quantize_rows(staging, (int8_t *)dst, scales, rows, cols, stride, offset, stride,
+                                 offset, m->stream);
+    else
+        e = launch_convert_rows(staging, dst, rows, cols, m->dtype, stride, offset, m->stream);
+    if (!hip_ok(e, "convert weights")) return -1;
+    // staging is reused by the next matrix
+    return hip_ok(hipStreamSynchronize(m->stream), "upload sync") ? 0 : -1;
+}
+
+int sh_model_upload_layer(sh_model *m, int32_t layer, const float *wq, const float *wk,
+                          const float *wv, const float *wo, const float *w1, const float *w2,
+                          const float *w3, const float *rms_att, const float *rms_ffn,
+                          const float *q_norm, const float *k_norm) {
+    if (!m) {
+        set_error("sh_model_upload_layer: nil model");
+        return -1;
+    }
+    const sh_config &c = m->cfg;
+    if (layer < 0 || layer >= c.n_layers) {
+        set_error("sh_model_upload_layer: layer out of range");
+        return -1;
+    }
+    if (!wq || !wk || !wv || !wo || !w1 || !w2 || !w3 || !rms_att || !rms_ffn ||
+        (c.qk_norm && (!q_norm || !k_norm))) {
+        set_error("sh_model_upload_layer: missing tensor");
+        return -1;
+    }
+    (void)hipSetDevice(m->device);
+    const int D = c.dim, F = c.hidden;
+    const size_t biggest = std::max({(size_t)m->qdim * D, (size_t)F * D});
+    float *staging = nullptr;
+    if (!hip_ok(hipMalloc(&staging, biggest * 4), "hipMalloc staging")) return -1;
+    LayerDev &L = m->layers[layer];
+    const size_t eb = weight_elem_bytes(m->dtype);
+    int rc = 0;
+    rc |= upload_matrix(m, staging, wq, m->qdim, D, L.wqkv, L.s_qkv, 1, 0);
+    rc |= upload_matrix(m, staging, wk, m->kvdim, D, L.wqkv, L.s_qkv, 1, m->qdim);
+    rc |= upload_matrix(m, staging, wv, m->kvdim, D, L.wqkv, L.s_qkv, 1, m->qdim + m->kvdim);
+    rc |= upload_matrix(m, staging, wo, D, m->qdim, L.wo, L.s_o, 1, 0);
+    rc |= upload_matrix(m, staging, w1, F, D, L.w13, L.s_13, 2, 0);
+    rc |= upload_matrix(m, staging, w3, F, D, L.w13, L.s_13, 2, 1);
+    rc |= upload_matrix(m, staging, w2, D, F, L.w2, L.s_2, 1, 0);
+    (void)eb;
+    (void)hipFree(staging);
+    if (rc) return -1;
+    if (!hip_ok(hipMemcpy(L.rms_att, rms_att, 4 * D, hipMemcpyHostToDevice), "upload rms_att") ||
+        !hip_ok(hipMemcpy(L.rms_ffn, rms_ffn, 4 * D, hipMemcpyHostToDevice), "upload rms_ffn"))
+        return -1;
+    if (c.qk_norm &&
+        (!hip_ok(hipMemcpy(L.q_norm, q_norm, 4 * c.head_dim, hipMemcpyHostToDevice), "upload q_norm") ||
+         !hip_ok(hipMemcpy(L.k_norm, k_norm, 4 * c.head_dim, hipMemcpyHostToDevice), "upload k_norm")))
+        return -1;
+    m->uploaded_layers = std::min(m->uploaded_layers + 1, c.n_layers);
+    return 0;
+}
+
+int sh_model_upload_globals(sh_model *m, const float *embed, const float *rms_final,
+                            const float *cls) {
+    if (!m) {
+        set_error("sh_model_upload_globals: nil model");
+        return -1;
+    }
+    const sh_config &c = m->cfg;
+    if (!embed || !rms_final || (!c.tied_embed && !cls)) {
+        set_error("sh_model_upload_globals: missing tensor");
+        return -1;
+    }
+    (void)hipSetDevice(m->device);
+    const size_t n = (size_t)c.vocab * c.dim;
+    float *staging = nullptr;
+    if (!hip_ok(hipMalloc(&staging, n * 4), "hipMalloc staging")) return -1;
+    int rc = 0;
+    // the lookup table: fp16 for F16 and W8A8, bf16 for BF16
+    const int lookup_dtype = m->dtype == SH_DTYPE_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16;
+    if (!hip_ok(hipMemcpy(staging, embed, n * 4, hipMemcpyHostToDevice), "upload embed")) rc = -1;
+    if (!rc && !hip_ok(launch_convert_rows(staging, m->embed, c.vocab, c.dim, lookup_dtype, 1, 0,
+                                           m->stream), "convert embed"))
+        rc = -1;
+    if (!rc && !hip_ok(hipStreamSynchronize(m->stream), "sync")) rc = -1;
+    if (!rc && m->cls != m->embed) {
+        const float *src = c.tied_embed ? embed : cls;
+        rc = upload_matrix(m, staging, src, c.vocab, c.dim, m->cls, m->s_cls, 1, 0);
+    }
+    (void)hipFree(staging);
+    if (rc) return -1;
+    if (!hip_ok(hipMemcpy(m->rms_final, rms_final, 4 * c.dim, hipMemcpyHostToDevice), "upload rms_final"))
+        return -1;
+    m->globals_uploaded = true;
+    return 0;
+}
+
+int sh_reset_cache(sh_model *m) {
+    if (!m) {
+        set_error("sh_reset_cache: nil model");
+        return -1;
+    }
+    (void)hipSetDevice(m->device);
+    const size_t kvb = kv_elem_bytes(m->cfg.kv_dtype) * m->kv_elems;
+    if (!hip_ok(hipMemsetAsync(m->kcache, 0, kvb, m->stream), "reset kcache") ||
+        !hip_ok(hipMemsetAsync(m->vcache, 0, kvb, m->stream), "reset vcache") ||
+        !hip_ok(hipStreamSynchronize(m->stream), "reset sync"))
+        return -1;
+    return 0;
+}
+
+int sh_decode_step(sh_model *m, int32_t token, int32_t pos, float *logits, int32_t *argmax_out) {
+    if (!ready(m)) return -1;
+    const sh_config &c = m->cfg;
+    if (token < 0 || token >= c.vocab) {
+        set_error("token out of range: " + std::to_string(token));
+        return -1;
+    }
+    if (pos < 0 || pos >= c.max_seq) {
+        set_error("position out of range: " + std::to_string(pos));
+        return -1;
+    }
+    (void)hipSetDevice(m->device);
+    if (!hip_ok(ensure_step_graph(m), "capture decode step")) return -1;
+    DecodeState st{};
+    st.pos = pos;
+    st.n_prompt = c.max_seq + 1;  // never append: this call only evaluates
+    if (!hip_ok(hipMemcpyAsync(m->state, &st, sizeof(st), hipMemcpyHostToDevice, m->stream), "state") ||
+        !hip_ok(hipMemcpyAsync(m->tokens + pos, &token, 4, hipMemcpyHostToDevice, m->stream), "token") ||
+        !hip_ok(hipGraphLaunch(m->step_exec, m->stream), "hipGraphLaunch"))
+        return -1;
+    if (logits &&
+        !hip_ok(hipMemcpyAsync(logits, m->logits, 4 * (size_t)c.vocab, hipMemcpyDeviceToHost, m->stream),
+                "copy logits"))
+        return -1;
+    int32_t am = 0;
+    if (!hip_ok(hipMemcpyAsync(&am, m->argmax_hist + pos, 4, hipMemcpyDeviceToHost, m->stream), "argmax") ||
+        !hip_ok(hipStreamSynchronize(m->stream), "decode step"))
+        return -1;
+    if (argmax_out) *argmax_out = am;
+    return 0;
+}
+
+int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32_t max_new,
+                     int32_t *out_tokens, int32_t *n_out, int32_t *stopped_eos) {
+    if (!ready(m)) return -1;
+    if (!out_tokens || !n_out || !stopped_eos) {
+        set_error("sh_greedy_decode: nil output");
+        return -1;
+    }
+    const sh_config &c = m->cfg;
+    // infer.go:140-163: defaults, empty prompt -> [BOS], keep the last max_seq ids, validate
+    if (max_new <= 0) max_new = 64;
+    const int32_t bos = kBos;
+    if (n_prompt <= 0 || !prompt) {
+        prompt = &bos;
+        n_prompt = 1;
+    }
+    if (n_prompt > c.max_seq) {
+        prompt += n_prompt - c.max_seq;
+        n_prompt = c.max_seq;
+    }
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= c.vocab) {
+            set_error("prompt token[" + std::to_string(i) + "]=" + std::to_string(prompt[i]) +
+                      " out of range");
+            return -1;
+        }
+    (void)hipSetDevice(m->device);
+    if (!hip_ok(ensure_step_graph(m), "capture decode step")) return -1;
+    // infer.go:179: generate while step < maxNew and len(tokens) < maxSeq
+    const int generated = std::min(max_new, c.max_seq - n_prompt);
+    const int forwards = n_prompt - 1 + generated;
+    DecodeState st{};
+    st.pos = 0;
+    st.n_prompt = n_prompt;
+    const size_t kvb = kv_elem_bytes(c.kv_dtype) * m->kv_elems;
+    if (!hip_ok(hipMemcpyAsync(m->tokens, prompt, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, m->stream),
+                "prompt") ||
+        !hip_ok(hipMemcpyAsync(m->state, &st, sizeof(st), hipMemcpyHostToDevice, m->stream), "state"))
+        return -1;
+    // timed region: cache reset (infer.go:165-168) and every forward
+    if (!hip_ok(hipEventRecord(m->ev0, m->stream), "event")) return -1;
+    if (!hip_ok(hipMemsetAsync(m->kcache, 0, kvb, m->stream), "reset kcache") ||
+        !hip_ok(hipMemsetAsync(m->vcache, 0, kvb, m->stream), "reset vcache"))
+        return -1;
+    for (int f = 0; f < forwards; f++)
+        if (!hip_ok(hipGraphLaunch(m->step_exec, m->stream), "hipGraphLaunch")) return -1;
+    if (!hip_ok(hipEventRecord(m->ev1, m->stream), "event")) return -1;
+    const int total = n_prompt + generated;
+    if (!hip_ok(hipMemcpyAsync(out_tokens, m->tokens, 4 * (size_t)total, hipMemcpyDeviceToHost, m->stream),
+                "copy tokens") ||
+        !hip_ok(hipStreamSynchronize(m->stream), "greedy decode"))
+        return -1;
+    // infer.go:190-193: stop after EOS
+    int n = n_prompt;
+    int eos = 0;
+    for (int i = n_prompt; i < total; i++) {
+        n = i + 1;
+        if (out_tokens[i] == kEos) {
+            eos = 1;
+            break;
+        }
+    }
+    *n_out = n;
+    *stopped_eos = eos;
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, m->ev0, m->ev1);
+    double bytes = 0;
+    for (int p = 0; p < forwards; p++) bytes += forward_bytes(m, p);
+    m->last.gpu_ms = ms;
+    m->last.forwards = forwards;
+    m->last.tokens_out = n - n_prompt;
+    m->last.bytes_per_forward_mean = forwards ? bytes / forwards : 0;
+    return 0;
+}
+
+int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *logits_cf) {
+    if (!ready(m)) return -1;
+    if (!tokens || !logits_cf || seq <= 0 || seq > m->cfg.max_seq) {
+        set_error("sh_prefill_logits: bad arguments");
+        return -1;
+    }
+    set_error("sh_prefill_logits: not available in this build");
+    return -1;
+}
+
+int sh_stats(const sh_model *m, sh_timing *out) {
+    if (!m || !out) {
+        set_error("sh_stats: nil argument");
+        return -1;
+    }
+    *out = m->last;
+    return 0;
+}
+
+int sh_quantize_i8(const float *src, int32_t rows, int32_t cols, int8_t *dst, float *scales,
+                   int32_t per_row) {
+    if (rows < 0 || cols < 0 || (!src && rows * cols) || (!dst && rows * cols) || !scales) {
+        set_error("sh_quantize_i8: bad arguments");
+        return -1;
+    }
+    (void)hipSetDevice(g_device);
+    const size_t n = (size_t)rows * cols;
+    const size_t ns = per_row ? (size_t)std::max(rows, 1) : 1;
+    float *dsrc = nullptr, *dsc = nullptr, *work = nullptr;
+    int8_t *ddst = nullptr;
+    int rc = -1;
+    if (hip_ok(hipMalloc(&dsrc, std::max<size_t>(n, 1) * 4), "hipMalloc") &&
+        hip_ok(hipMalloc(&ddst, std::max<size_t>(n, 1)), "hipMalloc") &&
+        hip_ok(hipMalloc(&dsc, ns * 4), "hipMalloc") && hip_ok(hipMalloc(&work, 16), "hipMalloc") &&
+        (n == 0 || hip_ok(hipMemcpy(dsrc, src, n * 4, hipMemcpyHostToDevice), "copy src"))) {
+        hipError_t e = per_row ? launch_quantize_rows(dsrc, ddst, dsc, rows, cols, 1, 0, 1, 0, nullptr)
+                               : launch_quantize_tensor(dsrc, ddst, dsc, n, work, nullptr);
+        if (hip_ok(e, "quantize") && hip_ok(hipDeviceSynchronize(), "quantize sync") &&
+            (n == 0 || hip_ok(hipMemcpy(dst, ddst, n, hipMemcpyDeviceToHost), "copy q")) &&
+            hip_ok(hipMemcpy(scales, dsc, (per_row ? (size_t)rows : 1) * 4, hipMemcpyDeviceToHost),
+                   "copy scales"))
+            rc = 0;
+    }
+    (void)hipFree(dsrc);
+    (void)hipFree(ddst);
+    (void)hipFree(dsc);
+    (void)hipFree(work);
+    return rc;
+}
+
+int sh_dequantize_i8(const int8_t *q, const float *scales, int32_t rows, int32_t cols,
+                     int32_t per_row, float *dst) {
+    if (rows < 0 || cols < 0 || !scales || ((!q || !dst) && rows * cols)) {
+        set_error("sh_dequantize_i8: bad arguments");
+        return -1;
+    }
+    const size_t n = (size_t)rows * cols;
+    if (n == 0) return 0;
+    (void)hipSetDevice(g_device);
+    const size_t ns = per_row ? (size_t)rows : 1;
+    int8_t *dq = nullptr;
+    float *ds = nullptr, *dd = nullptr;
+    int rc = -1;
+    if (hip_ok(hipMalloc(&dq, n), "hipMalloc") && hip_ok(hipMalloc(&ds, ns * 4), "hipMalloc") &&
+        hip_ok(hipMalloc(&dd, n * 4), "hipMalloc") &&
+        hip_ok(hipMemcpy(dq, q, n, hipMemcpyHostToDevice), "copy q") &&
+        hip_ok(hipMemcpy(ds, scales, ns * 4, hipMemcpyHostToDevice), "copy scales") &&
+        hip_ok(launch_dequantize(dq, ds, rows, cols, per_row, dd, nullptr), "dequantize") &&
+        hip_ok(hipDeviceSynchronize(), "dequantize sync") &&
+        hip_ok(hipMemcpy(dst, dd, n * 4, hipMemcpyDeviceToHost), "copy dst"))
+        rc = 0;
+    (void)hipFree(dq);
+    (void)hipFree(ds);
+    (void)hipFree(dd);
+    return rc;
+}
+
+int sh_synth_normal(float *dst, size_t n, uint64_t seed, uint64_t tensor_id, float std_) {
+    if (!dst && n) {
+        set_error("sh_synth_normal: nil destination");
+        return -1;
+    }
+    const uint64_t key = splitmix64(seed ^ splitmix64(tensor_id + 0x632BE59BD9B4E019ull));
+    parallel_ranges(n, [=](size_t a, size_t b) {
+        const double two_pi = 6.283185307179586476925286766559;
+        for (size_t i = a; i < b; i++) {
+            const uint64_t r1 = splitmix64(key + 2 * (uint64_t)i);
+            const uint64_t r2 = splitmix64(key + 2 * (uint64_t)i + 1);
+            const double u1 = (double)((r1 >> 11) + 1) * (1.0 / 9007199254740992.0);
+            const double u2 = (double)(r2 >> 11) * (1.0 / 9007199254740992.0);
+            const double z = sqrt(-2.0 * log(u1)) * cos(two_pi * u2);
+            dst[i] = (float)(z * (double)std_);
+        }
+    });
+    return 0;
+}
+
+int sh_synth_tokens(int32_t *dst, size_t n, uint64_t seed, int32_t vocab) {
+    if ((!dst && n) || vocab <= 0) {
+        set_error("sh_synth_tokens: bad arguments");
+        return -1;
+    }
+    const uint64_t key = splitmix64(seed ^ 0x7A3C15E2D4B9F681ull);
+    for (size_t i = 0; i < n; i++) dst[i] = (int32_t)(splitmix64(key + i) % (uint64_t)vocab);
+    return 0;
+}
+
+int sh_round_dtype(float *data, size_t n, int32_t dtype) {
+    if (!data && n) {
+        set_error("sh_round_dtype: nil data");
+        return -1;
+    }
+    if (dtype != SH_DTYPE_F16 && dtype != SH_DTYPE_BF16) {
+        set_error("sh_round_dtype: dtype must be SH_DTYPE_F16 or SH_DTYPE_BF16");
+        return -1;
+    }
+    parallel_ranges(n, [=](size_t a, size_t b) {
+        for (size_t i = a; i < b; i++) {
+            if (dtype == SH_DTYPE_BF16) {
+                const uint32_t u = (uint32_t)host_bf16_bits(data[i]) << 16;
+                memcpy(&data[i], &u, 4);
+            } else {
+                data[i] = (float)(_Float16)data[i];
+            }
+        }
+    });
+    return 0;
+}
+
+}  // extern "C"
+
+namespace sh {
+namespace {
+uint16_t host_bf16_bits(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+}  // namespace
+}  // namespace sh

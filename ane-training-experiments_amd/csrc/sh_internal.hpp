@@ -1,0 +1,101 @@
+// sh_internal.hpp — device-side data layout of a model and the kernel launchers shared by
+// the C ABI (sh_api.hip) and the kernels (sh_kernels.hip). gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "stories_hip.h"
+
+namespace sh {
+
+constexpr int kBlock = 256;          // threads per workgroup (4 wave64)
+constexpr int kMaxCols = 4096;       // widest GEMV input staged in LDS
+constexpr int kMaxSeqLds = 4096;     // attention scores kept in LDS
+constexpr int kBos = 1;              // infer.go:10
+constexpr int kEos = 2;              // infer.go:11
+
+// Per-layer device tensors. Row-major [out, in] weights in the storage type (fp16 / bf16
+// bits, or int8 with one fp32 scale per row for W8A8).
+struct LayerDev {
+    void *wqkv;      // [H*hd + 2*KVH*hd, D]: Wq rows, then Wk rows, then Wv rows
+    void *wo;        // [D, H*hd]
+    void *w13;       // [2F, D]: row 2r = W1 row r, row 2r+1 = W3 row r
+    void *w2;        // [D, F]
+    float *s_qkv, *s_o, *s_13, *s_2;   // W8A8 row scales (NULL otherwise)
+    float *rms_att, *rms_ffn;          // [D]
+    float *q_norm, *k_norm;            // [hd] (qk_norm only)
+};
+
+// Device-resident decode state (one sequence).
+struct DecodeState {
+    int32_t pos;        // position of the token the next forward consumes
+    int32_t n_prompt;   // tokens[0, n_prompt) are prompt ids, later ones are generated
+    int32_t pad[2];
+};
+
+struct ArgmaxPartial {
+    float v;
+    int32_t i;
+};
+
+}  // namespace sh
+
+struct sh_model {
+    sh_config cfg;
+    int32_t dtype;
+    int device;
+    hipStream_t stream;
+    int qdim, kvdim, qkv_rows;
+
+    void *arena;          // one allocation holding every weight tensor
+    size_t arena_bytes;
+    sh::LayerDev *layers; // host array of n_layers
+    void *embed;          // [V, D] fp16/bf16 bits (lookup; W8A8 keeps fp16 here)
+    void *cls;            // [V, D] classifier rows in the storage type (== embed when tied
+                          // and not W8A8)
+    float *s_cls;         // W8A8 classifier row scales
+    float *rms_final;     // [D]
+    int uploaded_layers;
+    bool globals_uploaded;
+
+    void *kcache, *vcache;   // [L][max_seq][KVH*hd] in kv_dtype
+    size_t kv_elems;
+    float *rope_cos, *rope_sin;  // [max_seq][hd/2]
+
+    // activations (fp32)
+    float *x, *x2, *qkv, *att, *gate, *logits;
+    sh::ArgmaxPartial *partials;
+    int n_partials;
+    int32_t *tokens;       // [max_seq + 1]
+    int32_t *argmax_hist;  // [max_seq + 1]: argmax produced by the forward at each position
+    sh::DecodeState *state;
+
+    hipGraphExec_t step_exec;
+    bool step_ready;
+    hipEvent_t ev0, ev1;
+    sh_timing last;
+};
+
+namespace sh {
+
+void set_error(const std::string &msg);
+bool hip_ok(hipError_t e, const char *what);
+
+// Launchers (sh_kernels.hip). All enqueue on m->stream.
+hipError_t launch_convert_rows(const float *src, void *dst, int rows, int cols, int dtype,
+                               int dst_row_stride, int dst_row_offset, hipStream_t s);
+hipError_t launch_quantize_rows(const float *src, int8_t *dst, float *scales, int rows,
+                                int cols, int dst_row_stride, int dst_row_offset,
+                                int scale_stride, int scale_offset, hipStream_t s);
+hipError_t launch_quantize_tensor(const float *src, int8_t *dst, float *scale, size_t n,
+                                  float *work, hipStream_t s);
+hipError_t launch_dequantize(const int8_t *q, const float *scales, int rows, int cols,
+                             int per_row, float *dst, hipStream_t s);
+// One token forward at the device-resident position (DecodeState.pos), then argmax and
+// state advance.
+hipError_t enqueue_decode_step(sh_model *m);
+int gemv_partials(const sh_model *m);
+
+}  // namespace sh

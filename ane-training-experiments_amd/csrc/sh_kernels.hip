@@ -1,0 +1,645 @@
+// sh_kernels.hip — batch-1 decode kernels for gfx950 (wave64, CDNA4).
+//
+// One token forward (ane/stories/infer.go:204-245) is a chain of HBM-bound GEMVs with
+// small fused prologues/epilogues:
+//   embed      x = Embed[token]                                  (infer.go:212-213)
+//   qkv        RMSNorm(x) -> [Wq;Wk;Wv] GEMV                     (infer.go:218-221)
+//   attention  per q head: QK-norm, RoPE, KV append, softmax, P.V (infer.go:222-224)
+//   wo         x2 = x + alpha * Wo.att                            (infer.go:225-228)
+//   w13        RMSNorm(x2) -> [W1;W3] GEMV -> silu(h1)*h3         (infer.go:230-235)
+//   w2         x = x2 + alpha * W2.gate                           (infer.go:236-239)
+//   classifier RMSNorm(x) -> Cls GEMV -> logits + block argmax    (infer.go:242-243)
+//   finalize   argmax over blocks, append the token, advance pos  (infer.go:185-186)
+//
+// GEMV layout: weights row-major [rows, cols] in fp16/bf16. A group of LPR lanes owns one
+// row; each lane streams CPL 16-byte chunks (8 weights) of it, so LPR consecutive lanes
+// read LPR*16 contiguous bytes. A wave covers 64/LPR adjacent rows; workgroups stride the
+// row groups. The input vector is staged (and RMS-normalised) once per workgroup in LDS,
+// then each lane keeps its CPL*8 input values in registers for every row it visits.
+// Accumulation is fp32 FMA; transcendental and normalisation arithmetic follows the
+// reference's float64 steps.
+#include <hip/hip_fp16.h>
+#include <math.h>
+
+#include "sh_internal.hpp"
+
+namespace sh {
+namespace {
+
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GATE = 2, EPI_LOGITS = 3 };
+
+__device__ __forceinline__ float f16_to_f(uint32_t b) {
+    return __half2float(__ushort_as_half((unsigned short)b));
+}
+__device__ __forceinline__ float bf16_to_f(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ uint16_t f_to_f16(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+__device__ __forceinline__ uint16_t f_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+template <int WT>
+__device__ __forceinline__ void unpack8(const uint4 &v, float *f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if constexpr (WT == SH_DTYPE_F16) {
+            f[2 * i] = f16_to_f(w[i] & 0xffffu);
+            f[2 * i + 1] = f16_to_f(w[i] >> 16);
+        } else {
+            f[2 * i] = __uint_as_float(w[i] << 16);
+            f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+}
+
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Sum over the workgroup; every thread gets the total. Waves are combined in a fixed order.
+__device__ double block_sum_d(double v, double *red) {
+    v = wave_sum_d(v);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double s = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) s += red[w];
+    return s;
+}
+
+__device__ float block_max_f(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) s = fmaxf(s, red[w]);
+    return s;
+}
+
+// (v, i) beats (bv, bi) when larger, or equal with a lower index: the first maximum of
+// infer.go:373-383 independent of reduction order.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+struct GemvParams {
+    const void *W;
+    int rows, cols;
+    const float *xin;        // input vector [cols]
+    const float *gain;       // RMSNorm gain; NULL = use xin unnormalised
+    double eps;
+    int epi;
+    float *out;
+    const float *resid;      // EPI_RESID
+    float alpha;             // EPI_RESID
+    ArgmaxPartial *partials; // EPI_LOGITS: one per workgroup
+};
+
+// infer.go:301-311 rmsNormVec staged into LDS: float64 sum of squares, float32 rrms,
+// (x * rrms) * w in float32.
+__device__ void stage_input(float *xs, const GemvParams &p, double *red) {
+    double ss = 0;
+    for (int i = threadIdx.x; i < p.cols; i += blockDim.x) {
+        float v = p.xin[i];
+        xs[i] = v;
+        ss += (double)v * (double)v;
+    }
+    if (p.gain) {
+        double tot = block_sum_d(ss, red);
+        float rrms = (float)(1.0 / sqrt(tot / (double)p.cols + p.eps));
+        for (int i = threadIdx.x; i < p.cols; i += blockDim.x) xs[i] = xs[i] * rrms * p.gain[i];
+    }
+    __syncthreads();
+}
+
+template <int LPR, int CPL, int WT>
+__global__ __launch_bounds__(kBlock) void k_gemv(GemvParams p) {
+    constexpr int G = 64 / LPR;
+    __shared__ float xs[kMaxCols];
+    __shared__ double red[kBlock / 64];
+    __shared__ ArgmaxPartial cand[kBlock / 64 * G];
+
+    stage_input(xs, p, red);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, grp = lane / LPR;
+    float xr[CPL * 8];
+#pragma unroll
+    for (int j = 0; j < CPL; j++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) xr[j * 8 + e] = xs[(sub + j * LPR) * 8 + e];
+
+    float best_v = -INFINITY;
+    int best_i = 0x7fffffff;
+    const int waves_total = gridDim.x * (kBlock / 64);
+    const uint16_t *W = (const uint16_t *)p.W;
+
+    for (int rg = blockIdx.x * (kBlock / 64) + wave; rg * G < p.rows; rg += 2 * waves_total) {
+        const int rowA = rg * G + grp;
+        const int rowB = (rg + waves_total) * G + grp;
+        uint4 wa[CPL], wb[CPL];
+        if (rowA < p.rows) {
+            const uint4 *src = (const uint4 *)(W + (size_t)rowA * p.cols);
+#pragma unroll
+            for (int j = 0; j < CPL; j++) wa[j] = src[sub + j * LPR];
+        }
+        if (rowB < p.rows) {
+            const uint4 *src = (const uint4 *)(W + (size_t)rowB * p.cols);
+#pragma unroll
+            for (int j = 0; j < CPL; j++) wb[j] = src[sub + j * LPR];
+        }
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            const int row = half ? rowB : rowA;
+            float acc = 0.f;
+            if (row < p.rows) {
+#pragma unroll
+                for (int j = 0; j < CPL; j++) {
+                    float f[8];
+                    unpack8<WT>(half ? wb[j] : wa[j], f);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc = fmaf(f[e], xr[j * 8 + e], acc);
+                }
+            }
+            acc = group_sum<LPR>(acc);
+            if (p.epi == EPI_GATE) {
+                // rows 2r (W1) and 2r+1 (W3) sit in adjacent lane groups of one wave
+                const float h3 = __shfl_down(acc, LPR, 64);
+                if (sub == 0 && (grp & 1) == 0 && row < p.rows) {
+                    // infer.go:324-326 silu, then * h3 (infer.go:234)
+                    const float s = acc / (1.0f + (float)exp(-(double)acc));
+                    p.out[row >> 1] = s * h3;
+                }
+            } else if (sub == 0 && row < p.rows) {
+                if (p.epi == EPI_RESID) {
+                    p.out[row] = p.resid[row] + p.alpha * acc;
+                } else {
+                    p.out[row] = acc;
+                    if (p.epi == EPI_LOGITS && acc > best_v) {
+                        best_v = acc;
+                        best_i = row;
+                    }
+                }
+            }
+        }
+    }
+    if (p.epi == EPI_LOGITS) {
+        if (sub == 0) cand[wave * G + grp] = ArgmaxPartial{best_v, best_i};
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            ArgmaxPartial b = cand[0];
+            for (int k = 1; k < (kBlock / 64) * G; k++)
+                if (better(cand[k].v, cand[k].i, b.v, b.i)) b = cand[k];
+            p.partials[blockIdx.x] = b;
+        }
+    }
+}
+
+template <int WT>
+__global__ __launch_bounds__(kBlock) void k_embed(const uint16_t *embed, int dim, int vocab,
+                                                  const int32_t *tokens,
+                                                  const DecodeState *st, float *x) {
+    const int tok = tokens[st->pos];
+    const bool ok = tok >= 0 && tok < vocab;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+        float v = 0.f;
+        if (ok) {
+            const uint32_t b = embed[(size_t)tok * dim + i];
+            v = WT == SH_DTYPE_F16 ? f16_to_f(b) : bf16_to_f(b);
+        }
+        x[i] = v;
+    }
+}
+
+template <int KVT>
+__device__ __forceinline__ float kv_load(const void *base, size_t i) {
+    if constexpr (KVT == SH_KV_F32) return ((const float *)base)[i];
+    else if constexpr (KVT == SH_KV_F16) return f16_to_f(((const uint16_t *)base)[i]);
+    else return bf16_to_f(((const uint16_t *)base)[i]);
+}
+template <int KVT>
+__device__ __forceinline__ void kv_store(void *base, size_t i, float v) {
+    if constexpr (KVT == SH_KV_F32) ((float *)base)[i] = v;
+    else if constexpr (KVT == SH_KV_F16) ((uint16_t *)base)[i] = f_to_f16(v);
+    else ((uint16_t *)base)[i] = f_to_bf16(v);
+}
+template <int KVT>
+__device__ __forceinline__ float kv_round(float v) {
+    if constexpr (KVT == SH_KV_F32) return v;
+    else if constexpr (KVT == SH_KV_F16) return f16_to_f(f_to_f16(v));
+    else return bf16_to_f(f_to_bf16(v));
+}
+
+struct AttnParams {
+    const float *qkv;  // [qdim | kvdim | kvdim] raw projections of this layer
+    int qdim, kvdim, hd, n_heads, n_kv_heads, max_seq, layer;
+    void *kcache, *vcache;  // [L][max_seq][kvdim]
+    const float *rope_cos, *rope_sin;
+    const float *q_norm, *k_norm;
+    double qk_eps;
+    int qk_norm;
+    float inv_sqrt_hd;  // float32(1/sqrt(hd)), infer.go:277
+    const DecodeState *st;
+    float *att;  // [qdim]
+};
+
+// One workgroup per query head h; it reads kv head h / (H/KVH). The first query head of a
+// kv group writes that head's roped K and V row at `pos`; every head uses its own copy of
+// the current row, so no workgroup reads a row another writes in this launch.
+template <int KVT>
+__global__ __launch_bounds__(kBlock) void k_attn_decode(AttnParams p) {
+    __shared__ float qs[256], ks[256], vs[256];
+    __shared__ float sc[kMaxSeqLds];
+    __shared__ float part[kBlock];
+    __shared__ double redd[kBlock / 64];
+    __shared__ float redf[kBlock / 64];
+    const int h = blockIdx.x, group = p.n_heads / p.n_kv_heads, kvh = h / group;
+    const int hd = p.hd, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = p.st->pos;
+
+    for (int i = tid; i < hd; i += blockDim.x) {
+        qs[i] = p.qkv[h * hd + i];
+        ks[i] = p.qkv[p.qdim + kvh * hd + i];
+        vs[i] = p.qkv[p.qdim + p.kvdim + kvh * hd + i];
+    }
+    __syncthreads();
+    if (p.qk_norm) {
+        // per-head RMSNorm (rmsNormVec over hd): wave 0 normalises q, wave 1 k
+        if (wave < 2) {
+            float *v = wave == 0 ? qs : ks;
+            const float *g = wave == 0 ? p.q_norm : p.k_norm;
+            double ss = 0;
+            for (int i = lane; i < hd; i += 64) ss += (double)v[i] * (double)v[i];
+            ss = wave_sum_d(ss);
+            const float rr = (float)(1.0 / sqrt(ss / (double)hd + p.qk_eps));
+            for (int i = lane; i < hd; i += 64) v[i] = v[i] * rr * g[i];
+        }
+        __syncthreads();
+    }
+    // infer.go:247-265 RoPE on interleaved pairs (2i, 2i+1)
+    const int half = hd / 2;
+    for (int i = tid; i < 2 * half; i += blockDim.x) {
+        float *v = i < half ? qs : ks;
+        const int pi = i < half ? i : i - half;
+        const float c = p.rope_cos[pos * half + pi], s = p.rope_sin[pos * half + pi];
+        const float e = v[2 * pi], o = v[2 * pi + 1];
+        v[2 * pi] = e * c - o * s;
+        v[2 * pi + 1] = e * s + o * c;
+    }
+    __syncthreads();
+    // infer.go:267-271 storeKV, in the cache's storage type
+    const size_t lbase = (size_t)p.layer * p.max_seq * p.kvdim + (size_t)kvh * hd;
+    for (int i = tid; i < hd; i += blockDim.x) {
+        ks[i] = kv_round<KVT>(ks[i]);
+        vs[i] = kv_round<KVT>(vs[i]);
+        if (h % group == 0) {
+            kv_store<KVT>(p.kcache, lbase + (size_t)pos * p.kvdim + i, ks[i]);
+            kv_store<KVT>(p.vcache, lbase + (size_t)pos * p.kvdim + i, vs[i]);
+        }
+    }
+    __syncthreads();
+    // infer.go:280-288 scores
+    for (int t = wave; t <= pos; t += kBlock / 64) {
+        float d = 0.f;
+        if (t == pos) {
+            for (int i = lane; i < hd; i += 64) d = fmaf(qs[i], ks[i], d);
+        } else {
+            const size_t rb = lbase + (size_t)t * p.kvdim;
+            for (int i = lane; i < hd; i += 64) d = fmaf(qs[i], kv_load<KVT>(p.kcache, rb + i), d);
+        }
+        d = wave_sum(d);
+        if (lane == 0) sc[t] = d * p.inv_sqrt_hd;
+    }
+    __syncthreads();
+    // infer.go:328-345 softmaxPrefix
+    float mx = -INFINITY;
+    for (int t = tid; t <= pos; t += blockDim.x) mx = fmaxf(mx, sc[t]);
+    mx = block_max_f(mx, redf);
+    double sum = 0;
+    for (int t = tid; t <= pos; t += blockDim.x) {
+        const float e = (float)exp((double)(sc[t] - mx));
+        sc[t] = e;
+        sum += (double)e;
+    }
+    sum = block_sum_d(sum, redd);
+    const float inv = (float)(1.0 / sum);
+    // infer.go:290-297 P.V: thread -> (dim i, position group g)
+    const int ngroups = blockDim.x / hd;
+    const int i = tid % hd, g = tid / hd;
+    float acc = 0.f;
+    if (g < ngroups) {
+        for (int t = g; t <= pos; t += ngroups) {
+            const float pt = sc[t] * inv;
+            const float vv = t == pos ? vs[i]
+                                      : kv_load<KVT>(p.vcache, lbase + (size_t)t * p.kvdim + i);
+            acc = fmaf(pt, vv, acc);
+        }
+    }
+    part[tid] = acc;
+    __syncthreads();
+    if (tid < hd) {
+        float s = 0.f;
+        for (int k = 0; k < ngroups; k++) s += part[k * hd + tid];
+        p.att[h * hd + tid] = s;
+    }
+}
+
+// Cross-workgroup argmax of the classifier, then the decode loop's bookkeeping
+// (infer.go:179-186): record the id, append it after the prompt, advance the position.
+__global__ __launch_bounds__(kBlock) void k_argmax_finalize(const ArgmaxPartial *parts, int n,
+                                                            DecodeState *st, int32_t *tokens,
+                                                            int32_t *hist, int max_seq) {
+    __shared__ ArgmaxPartial sp[kBlock];
+    ArgmaxPartial b{-INFINITY, 0x7fffffff};
+    for (int k = threadIdx.x; k < n; k += blockDim.x)
+        if (better(parts[k].v, parts[k].i, b.v, b.i)) b = parts[k];
+    sp[threadIdx.x] = b;
+    __syncthreads();
+    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s && better(sp[threadIdx.x + s].v, sp[threadIdx.x + s].i,
+                                           sp[threadIdx.x].v, sp[threadIdx.x].i))
+            sp[threadIdx.x] = sp[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int pos = st->pos;
+        const int next = sp[0].i == 0x7fffffff ? 0 : sp[0].i;
+        hist[pos] = next;
+        if (pos + 1 <= max_seq && pos + 1 >= st->n_prompt) tokens[pos + 1] = next;
+        st->pos = pos + 1;
+    }
+}
+
+// ---- upload-time conversion and the W8A8 quantizer ---------------------------------------
+
+__global__ void k_convert_rows(const float *src, void *dst, int rows, int cols, int dtype,
+                               int stride, int offset) {
+    const size_t n = (size_t)rows * cols;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / cols, c = i % cols;
+        const size_t o = (r * stride + offset) * (size_t)cols + c;
+        ((uint16_t *)dst)[o] = dtype == SH_DTYPE_BF16 ? f_to_bf16(src[i]) : f_to_f16(src[i]);
+    }
+}
+
+// bridge/ane_bridge.m:386-392: clamp to [-128, 127], add +-0.5, truncate toward zero.
+__device__ __forceinline__ int8_t quantize_value(float v) {
+    if (v > 127.0f) v = 127.0f;
+    if (v < -128.0f) v = -128.0f;
+    return (int8_t)(int)(v + (v >= 0 ? 0.5f : -0.5f));
+}
+
+// One workgroup per row: max|x| (ane_bridge.m:377-381), scale = max/127 with 0 -> 1
+// (:382-383), q = quantize(x / scale) with a correctly rounded division (:388).
+__global__ __launch_bounds__(kBlock) void k_quantize_rows(const float *src, int8_t *dst,
+                                                          float *scales, int cols, int stride,
+                                                          int offset, int sstride, int soff) {
+    __shared__ float red[kBlock / 64];
+    const int r = blockIdx.x;
+    const float *row = src + (size_t)r * cols;
+    float m = 0.f;
+    for (int c = threadIdx.x; c < cols; c += blockDim.x) m = fmaxf(m, fabsf(row[c]));
+    m = block_max_f(m, red);
+    float scale = m / 127.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    int8_t *out = dst + ((size_t)r * stride + offset) * cols;
+    for (int c = threadIdx.x; c < cols; c += blockDim.x) out[c] = quantize_value(__fdiv_rn(row[c], scale));
+    if (threadIdx.x == 0) scales[(size_t)r * sstride + soff] = scale;
+}
+
+__global__ __launch_bounds__(kBlock) void k_absmax_bits(const float *src, size_t n,
+                                                        unsigned int *out) {
+    __shared__ float red[kBlock / 64];
+    float m = 0.f;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        m = fmaxf(m, fabsf(src[i]));
+    m = block_max_f(m, red);
+    // non-negative floats order like their bit patterns
+    if (threadIdx.x == 0) atomicMax(out, __float_as_uint(m));
+}
+
+__global__ void k_quantize_with(const float *src, size_t n, const unsigned int *maxbits,
+                                int8_t *dst, float *scale_out) {
+    float scale = __uint_as_float(*maxbits) / 127.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = quantize_value(__fdiv_rn(src[i], scale));
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+}
+
+__global__ void k_dequantize(const int8_t *q, const float *scales, int rows, int cols,
+                             int per_row, float *dst) {
+    const size_t n = (size_t)rows * cols;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const float s = per_row ? scales[i / cols] : scales[0];
+        dst[i] = (float)q[i] * s;
+    }
+}
+
+__global__ void k_zero_u32(unsigned int *p) { *p = 0u; }
+
+// ---- GEMV dispatch -----------------------------------------------------------------------
+
+typedef void (*GemvKernel)(GemvParams);
+
+template <int WT>
+GemvKernel pick_gemv(int cols, int epi, int *lpr_out) {
+    // Lane groups of 64 only when no epilogue pairs adjacent rows.
+    const bool pairs = epi == EPI_GATE;
+#define SH_CASE(C, L, P)                 \
+    case C:                              \
+        *lpr_out = L;                    \
+        return &k_gemv<L, P, WT>;
+    if (!pairs) {
+        switch (cols) {
+            SH_CASE(1536, 64, 3)
+            SH_CASE(2048, 64, 4)
+            SH_CASE(3072, 64, 6)
+            SH_CASE(4096, 64, 8)
+            default: break;
+        }
+    }
+    switch (cols) {
+        SH_CASE(64, 8, 1)
+        SH_CASE(128, 16, 1)
+        SH_CASE(192, 8, 3)
+        SH_CASE(256, 32, 1)
+        SH_CASE(384, 16, 3)
+        SH_CASE(512, 32, 2)
+        SH_CASE(768, 32, 3)
+        SH_CASE(1024, 32, 4)
+        SH_CASE(1536, 32, 6)
+        SH_CASE(2048, 32, 8)
+        default: break;
+    }
+#undef SH_CASE
+    return nullptr;
+}
+
+int gemv_grid(int rows, int lpr) {
+    const int rows_per_block = (kBlock / 64) * (64 / lpr);
+    int blocks = (rows + rows_per_block - 1) / rows_per_block;
+    // each wave walks two row groups per pass; cap the grid so the RMSNorm prologue is
+    // amortised over several passes on the large classifier
+    blocks = (blocks + 1) / 2;
+    return blocks > 2048 ? 2048 : (blocks < 1 ? 1 : blocks);
+}
+
+hipError_t launch_gemv(const sh_model *m, const GemvParams &p, hipStream_t s) {
+    int lpr = 0;
+    GemvKernel k = m->dtype == SH_DTYPE_BF16 ? pick_gemv<SH_DTYPE_BF16>(p.cols, p.epi, &lpr)
+                                             : pick_gemv<SH_DTYPE_F16>(p.cols, p.epi, &lpr);
+    if (!k) return hipErrorInvalidValue;
+    const int grid = gemv_grid(p.rows, lpr);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kBlock), 0, s, p);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemv_supported(int cols, bool pairs) {
+    int lpr = 0;
+    return pick_gemv<SH_DTYPE_F16>(cols, pairs ? EPI_GATE : EPI_STORE, &lpr) != nullptr;
+}
+
+int gemv_partials(const sh_model *m) {
+    int lpr = 0;
+    GemvKernel k = m->dtype == SH_DTYPE_BF16
+                       ? pick_gemv<SH_DTYPE_BF16>(m->cfg.dim, EPI_LOGITS, &lpr)
+                       : pick_gemv<SH_DTYPE_F16>(m->cfg.dim, EPI_LOGITS, &lpr);
+    if (!k) return -1;
+    return gemv_grid(m->cfg.vocab, lpr);
+}
+
+hipError_t enqueue_decode_step(sh_model *m) {
+    const sh_config &c = m->cfg;
+    hipStream_t s = m->stream;
+    hipError_t e;
+    if (m->dtype == SH_DTYPE_BF16)
+        hipLaunchKernelGGL(k_embed<SH_DTYPE_BF16>, dim3(1), dim3(kBlock), 0, s,
+                           (const uint16_t *)m->embed, c.dim, c.vocab, m->tokens, m->state, m->x);
+    else
+        hipLaunchKernelGGL(k_embed<SH_DTYPE_F16>, dim3(1), dim3(kBlock), 0, s,
+                           (const uint16_t *)m->embed, c.dim, c.vocab, m->tokens, m->state, m->x);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+
+    for (int l = 0; l < c.n_layers; l++) {
+        const LayerDev &L = m->layers[l];
+        GemvParams g{};
+        g.W = L.wqkv; g.rows = m->qkv_rows; g.cols = c.dim; g.xin = m->x;
+        g.gain = L.rms_att; g.eps = c.norm_eps; g.epi = EPI_STORE; g.out = m->qkv;
+        if ((e = launch_gemv(m, g, s)) != hipSuccess) return e;
+
+        AttnParams a{};
+        a.qkv = m->qkv; a.qdim = m->qdim; a.kvdim = m->kvdim; a.hd = c.head_dim;
+        a.n_heads = c.n_heads; a.n_kv_heads = c.n_kv_heads; a.max_seq = c.max_seq; a.layer = l;
+        a.kcache = m->kcache; a.vcache = m->vcache; a.rope_cos = m->rope_cos;
+        a.rope_sin = m->rope_sin; a.q_norm = L.q_norm; a.k_norm = L.k_norm;
+        a.qk_eps = c.qk_norm_eps; a.qk_norm = c.qk_norm;
+        a.inv_sqrt_hd = (float)(1.0 / sqrt((double)c.head_dim));
+        a.st = m->state; a.att = m->att;
+        switch (c.kv_dtype) {
+        case SH_KV_F16:
+            hipLaunchKernelGGL(k_attn_decode<SH_KV_F16>, dim3(c.n_heads), dim3(kBlock), 0, s, a);
+            break;
+        case SH_KV_BF16:
+            hipLaunchKernelGGL(k_attn_decode<SH_KV_BF16>, dim3(c.n_heads), dim3(kBlock), 0, s, a);
+            break;
+        default:
+            hipLaunchKernelGGL(k_attn_decode<SH_KV_F32>, dim3(c.n_heads), dim3(kBlock), 0, s, a);
+            break;
+        }
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+
+        g = GemvParams{};
+        g.W = L.wo; g.rows = c.dim; g.cols = m->qdim; g.xin = m->att; g.epi = EPI_RESID;
+        g.out = m->x2; g.resid = m->x; g.alpha = c.residual_scale;
+        if ((e = launch_gemv(m, g, s)) != hipSuccess) return e;
+
+        g = GemvParams{};
+        g.W = L.w13; g.rows = 2 * c.hidden; g.cols = c.dim; g.xin = m->x2; g.gain = L.rms_ffn;
+        g.eps = c.norm_eps; g.epi = EPI_GATE; g.out = m->gate;
+        if ((e = launch_gemv(m, g, s)) != hipSuccess) return e;
+
+        g = GemvParams{};
+        g.W = L.w2; g.rows = c.dim; g.cols = c.hidden; g.xin = m->gate; g.epi = EPI_RESID;
+        g.out = m->x; g.resid = m->x2; g.alpha = c.residual_scale;
+        if ((e = launch_gemv(m, g, s)) != hipSuccess) return e;
+    }
+    GemvParams g{};
+    g.W = m->cls; g.rows = c.vocab; g.cols = c.dim; g.xin = m->x; g.gain = m->rms_final;
+    g.eps = c.norm_eps; g.epi = EPI_LOGITS; g.out = m->logits; g.partials = m->partials;
+    if ((e = launch_gemv(m, g, s)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(kBlock), 0, s, m->partials,
+                       m->n_partials, m->state, m->tokens, m->argmax_hist, c.max_seq);
+    return hipGetLastError();
+}
+
+hipError_t launch_convert_rows(const float *src, void *dst, int rows, int cols, int dtype,
+                               int dst_row_stride, int dst_row_offset, hipStream_t s) {
+    const size_t n = (size_t)rows * cols;
+    size_t blocks = (n + kBlock - 1) / kBlock;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_convert_rows, dim3((unsigned)blocks), dim3(kBlock), 0, s, src, dst,
+                       rows, cols, dtype, dst_row_stride, dst_row_offset);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_rows(const float *src, int8_t *dst, float *scales, int rows,
+                                int cols, int dst_row_stride, int dst_row_offset,
+                                int scale_stride, int scale_offset, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_quantize_rows, dim3(rows), dim3(kBlock), 0, s, src, dst, scales, cols,
+                       dst_row_stride, dst_row_offset, scale_stride, scale_offset);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_tensor(const float *src, int8_t *dst, float *scale, size_t n,
+                                  float *work, hipStream_t s) {
+    unsigned int *bits = (unsigned int *)work;
+    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(1), 0, s, bits);
+    size_t blocks = (n + kBlock - 1) / kBlock;
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_absmax_bits, dim3((unsigned)blocks), dim3(kBlock), 0, s, src, n, bits);
+    hipLaunchKernelGGL(k_quantize_with, dim3((unsigned)blocks), dim3(kBlock), 0, s, src, n, bits,
+                       dst, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequantize(const int8_t *q, const float *scales, int rows, int cols,
+                             int per_row, float *dst, hipStream_t s) {
+    const size_t n = (size_t)rows * cols;
+    size_t blocks = (n + kBlock - 1) / kBlock;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_dequantize, dim3((unsigned)blocks), dim3(kBlock), 0, s, q, scales, rows,
+                       cols, per_row, dst);
+    return hipGetLastError();
+}
+
+}  // namespace sh

@@ -1,0 +1,353 @@
+"""ctypes binding of libstories_hip.so (declared in include/stories_hip.h).
+
+Python-side mirror of the reference's decode API for tests, the smoke check and the
+benchmark. It mirrors ane/stories (NewDecoder / EvalNextLogits / Decode / ResetCache,
+ane/stories/infer.go:61-202) and ane/storiesane (EvalLogits, engine.go:363-376) on top of the
+C ABI. There is no fallback: if the shared library is missing, importing `load()` raises.
+
+Synthetic weights (the N(0, std) configurations) come from the library's own deterministic
+generator, `sh_synth_normal`, keyed by (seed, tensor id):
+    embedding 1, untied classifier 2,
+    layer l: 16*(l+1) + {0: wq, 1: wk, 2: wv, 3: wo, 4: w1, 5: w2, 6: w3}.
+RMSNorm and QK-norm gains are 1, as in stories.RandomInit (ane/stories/weights.go:142-149).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libstories_hip.so")
+
+SH_DTYPE_F16 = 1
+SH_DTYPE_BF16 = 2
+SH_DTYPE_W8A8 = 3
+SH_KV_F32 = 0
+SH_KV_F16 = 1
+SH_KV_BF16 = 2
+
+BOS = 1
+EOS = 2
+
+
+class ShConfig(C.Structure):
+    _fields_ = [
+        ("dim", C.c_int32),
+        ("hidden", C.c_int32),
+        ("n_layers", C.c_int32),
+        ("n_heads", C.c_int32),
+        ("n_kv_heads", C.c_int32),
+        ("head_dim", C.c_int32),
+        ("vocab", C.c_int32),
+        ("max_seq", C.c_int32),
+        ("rope_theta", C.c_double),
+        ("norm_eps", C.c_double),
+        ("qk_norm_eps", C.c_double),
+        ("residual_scale", C.c_float),
+        ("qk_norm", C.c_int32),
+        ("tied_embed", C.c_int32),
+        ("kv_dtype", C.c_int32),
+        ("max_batch", C.c_int32),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+    @property
+    def qdim(self) -> int:
+        return self.n_heads * self.head_dim
+
+    @property
+    def kvdim(self) -> int:
+        return self.n_kv_heads * self.head_dim
+
+
+class ShTiming(C.Structure):
+    _fields_ = [
+        ("gpu_ms", C.c_double),
+        ("forwards", C.c_int64),
+        ("tokens_out", C.c_int64),
+        ("bytes_per_forward_mean", C.c_double),
+    ]
+
+
+class ShError(RuntimeError):
+    pass
+
+
+_F = C.POINTER(C.c_float)
+_I32 = C.POINTER(C.c_int32)
+_lib = None
+
+# every entry point of include/stories_hip.h with its ctypes signature
+SIGNATURES = {
+    "sh_init": (C.c_int, [C.c_int32]),
+    "sh_last_error": (C.c_size_t, [C.c_char_p, C.c_size_t]),
+    "sh_config_stories110m": (C.c_int, [C.POINTER(ShConfig)]),
+    "sh_config_qwen3_06b": (C.c_int, [C.POINTER(ShConfig)]),
+    "sh_model_create": (C.c_void_p, [C.POINTER(ShConfig), C.c_int32]),
+    "sh_model_upload_layer": (C.c_int, [C.c_void_p, C.c_int32] + [_F] * 11),
+    "sh_model_upload_globals": (C.c_int, [C.c_void_p, _F, _F, _F]),
+    "sh_reset_cache": (C.c_int, [C.c_void_p]),
+    "sh_decode_step": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, _F, _I32]),
+    "sh_greedy_decode": (C.c_int, [C.c_void_p, _I32, C.c_int32, C.c_int32, _I32, _I32, _I32]),
+    "sh_prefill_logits": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint16), C.c_int32, _F]),
+    "sh_stats": (C.c_int, [C.c_void_p, C.POINTER(ShTiming)]),
+    "sh_model_destroy": (None, [C.c_void_p]),
+    "sh_quantize_i8": (C.c_int, [_F, C.c_int32, C.c_int32, C.POINTER(C.c_int8), _F, C.c_int32]),
+    "sh_dequantize_i8": (C.c_int, [C.POINTER(C.c_int8), _F, C.c_int32, C.c_int32, C.c_int32, _F]),
+    "sh_synth_normal": (C.c_int, [_F, C.c_size_t, C.c_uint64, C.c_uint64, C.c_float]),
+    "sh_synth_tokens": (C.c_int, [_I32, C.c_size_t, C.c_uint64, C.c_int32]),
+    "sh_round_dtype": (C.c_int, [_F, C.c_size_t, C.c_int32]),
+}
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Loads the HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ShError(f"{path} is missing: build it with __graft_entry__.build()")
+    lib = C.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    lib = load()
+    buf = C.create_string_buffer(4096)
+    lib.sh_last_error(buf, len(buf))
+    return buf.value.decode(errors="replace")
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise ShError(f"{what}: {last_error()}")
+
+
+def _fp(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_F)
+
+
+def init(device: int = 0) -> None:
+    _check(load().sh_init(device), "sh_init")
+
+
+def stories110m_config() -> ShConfig:
+    c = ShConfig()
+    _check(load().sh_config_stories110m(C.byref(c)), "sh_config_stories110m")
+    return c
+
+
+def qwen3_06b_config() -> ShConfig:
+    c = ShConfig()
+    _check(load().sh_config_qwen3_06b(C.byref(c)), "sh_config_qwen3_06b")
+    return c
+
+
+def make_config(**kw) -> ShConfig:
+    """A config from keyword fields; unspecified fields take the Stories110M defaults."""
+    c = stories110m_config()
+    for k, v in kw.items():
+        if not hasattr(c, k):
+            raise KeyError(k)
+        setattr(c, k, v)
+    return c
+
+
+# ---- synthetic inputs ------------------------------------------------------------------
+
+def synth_normal(n: int, seed: int, tensor_id: int, std: float) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    _check(load().sh_synth_normal(_fp(out), n, seed, tensor_id, std), "sh_synth_normal")
+    return out
+
+
+def synth_tokens(n: int, seed: int, vocab: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    _check(load().sh_synth_tokens(out.ctypes.data_as(_I32), n, seed, vocab), "sh_synth_tokens")
+    return out
+
+
+def round_dtype(a: np.ndarray, dtype: int) -> np.ndarray:
+    """Rounds a copy of fp32 `a` to the values `dtype` stores (round to nearest even)."""
+    out = np.ascontiguousarray(a, dtype=np.float32).copy()
+    _check(load().sh_round_dtype(_fp(out), out.size, dtype), "sh_round_dtype")
+    return out
+
+
+LAYER_KEYS = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
+
+
+def layer_shapes(cfg: ShConfig) -> dict:
+    D, F, Q, KV = cfg.dim, cfg.hidden, cfg.qdim, cfg.kvdim
+    return {"wq": (Q, D), "wk": (KV, D), "wv": (KV, D), "wo": (D, Q),
+            "w1": (F, D), "w2": (D, F), "w3": (F, D)}
+
+
+@dataclass
+class Weights:
+    """Host fp32 weights in the reference's layout (ane/stories/weights.go:13-24)."""
+    layers: list
+    embed: np.ndarray
+    rms_final: np.ndarray
+    cls: np.ndarray | None  # None when tied to embed
+
+    def rounded(self, dtype: int) -> "Weights":
+        """The values the device computes with. fp16 / bf16: every matrix rounded (norm
+        gains stay fp32). W8A8: matrices stay fp32 (a CPU check quantizes them itself), the
+        lookup table is fp16, and the classifier is quantized from the fp32 rows, so the
+        tied classifier is returned explicitly as `cls`."""
+        if dtype == SH_DTYPE_W8A8:
+            cls = self.cls if self.cls is not None else self.embed
+            return Weights(self.layers, round_dtype(self.embed, SH_DTYPE_F16), self.rms_final, cls)
+        if dtype not in (SH_DTYPE_F16, SH_DTYPE_BF16):
+            return self
+        layers = []
+        for lw in self.layers:
+            d = dict(lw)
+            for k in LAYER_KEYS:
+                d[k] = round_dtype(lw[k], dtype)
+            layers.append(d)
+        embed = round_dtype(self.embed, dtype)
+        cls = None if self.cls is None else round_dtype(self.cls, dtype)
+        return Weights(layers, embed, self.rms_final, cls)
+
+
+def synth_weights(cfg: ShConfig, seed: int, std: float = 0.02) -> Weights:
+    """N(0, std) matrices and unit norm gains for `cfg` (see the module docstring)."""
+    shapes = layer_shapes(cfg)
+    layers = []
+    for l in range(cfg.n_layers):
+        lw = {}
+        for j, k in enumerate(LAYER_KEYS):
+            r, c = shapes[k]
+            lw[k] = synth_normal(r * c, seed, 16 * (l + 1) + j, std).reshape(r, c)
+        lw["rms_att"] = np.ones(cfg.dim, np.float32)
+        lw["rms_ffn"] = np.ones(cfg.dim, np.float32)
+        if cfg.qk_norm:
+            lw["q_norm"] = np.ones(cfg.head_dim, np.float32)
+            lw["k_norm"] = np.ones(cfg.head_dim, np.float32)
+        layers.append(lw)
+    embed = synth_normal(cfg.vocab * cfg.dim, seed, 1, std).reshape(cfg.vocab, cfg.dim)
+    cls = None
+    if not cfg.tied_embed:
+        cls = synth_normal(cfg.vocab * cfg.dim, seed, 2, std).reshape(cfg.vocab, cfg.dim)
+    return Weights(layers, embed, np.ones(cfg.dim, np.float32), cls)
+
+
+# ---- model -----------------------------------------------------------------------------
+
+class Model:
+    """A device-resident model: stories.Decoder (infer.go:30-59) + storiesane.Engine
+    (engine.go:67-146) surface over the C ABI."""
+
+    def __init__(self, cfg: ShConfig, dtype: int):
+        self.lib = load()
+        self.cfg = cfg
+        self.dtype = dtype
+        self.h = self.lib.sh_model_create(C.byref(cfg), dtype)
+        if not self.h:
+            raise ShError(f"sh_model_create: {last_error()}")
+
+    def upload(self, w: Weights) -> None:
+        for l, lw in enumerate(w.layers):
+            arrs = [np.ascontiguousarray(lw[k], np.float32) for k in LAYER_KEYS]
+            arrs += [np.ascontiguousarray(lw["rms_att"], np.float32),
+                     np.ascontiguousarray(lw["rms_ffn"], np.float32)]
+            qn = lw.get("q_norm")
+            kn = lw.get("k_norm")
+            qn = None if qn is None else np.ascontiguousarray(qn, np.float32)
+            kn = None if kn is None else np.ascontiguousarray(kn, np.float32)
+            _check(self.lib.sh_model_upload_layer(self.h, l, *[_fp(a) for a in arrs], _fp(qn), _fp(kn)),
+                   f"sh_model_upload_layer({l})")
+        embed = np.ascontiguousarray(w.embed, np.float32)
+        cls = None if w.cls is None else np.ascontiguousarray(w.cls, np.float32)
+        _check(self.lib.sh_model_upload_globals(self.h, _fp(embed), _fp(np.ascontiguousarray(w.rms_final, np.float32)), _fp(cls)),
+               "sh_model_upload_globals")
+
+    def reset_cache(self) -> None:
+        _check(self.lib.sh_reset_cache(self.h), "sh_reset_cache")
+
+    def eval_next_logits(self, token: int, pos: int, want_logits: bool = True):
+        """(*Decoder).EvalNextLogits (infer.go:72-77): returns (logits or None, argmax)."""
+        logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        am = C.c_int32(0)
+        _check(self.lib.sh_decode_step(self.h, token, pos, _fp(logits), C.byref(am)), "sh_decode_step")
+        return logits, am.value
+
+    def greedy_decode(self, prompt, max_new: int):
+        """(*Decoder).Decode with Temperature 0 (infer.go:136-202).
+        Returns (tokens, prompt_length, stopped_on_eos)."""
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
+        out = np.zeros(self.cfg.max_seq, np.int32)
+        n_out = C.c_int32(0)
+        eos = C.c_int32(0)
+        pp = p.ctypes.data_as(_I32) if p.size else None
+        _check(self.lib.sh_greedy_decode(self.h, pp, p.size, max_new, out.ctypes.data_as(_I32),
+                                         C.byref(n_out), C.byref(eos)), "sh_greedy_decode")
+        plen = min(max(p.size, 1), self.cfg.max_seq)
+        return out[: n_out.value].copy(), plen, bool(eos.value)
+
+    def eval_logits(self, tokens) -> np.ndarray:
+        """(*Engine).EvalLogits (engine.go:363-376): channel-first [V, S] logits."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint16))
+        out = np.empty((self.cfg.vocab, t.size), np.float32)
+        _check(self.lib.sh_prefill_logits(self.h, t.ctypes.data_as(C.POINTER(C.c_uint16)), t.size, _fp(out)),
+               "sh_prefill_logits")
+        return out
+
+    def stats(self) -> dict:
+        t = ShTiming()
+        _check(self.lib.sh_stats(self.h, C.byref(t)), "sh_stats")
+        return {"gpu_ms": t.gpu_ms, "forwards": t.forwards, "tokens_out": t.tokens_out,
+                "bytes_per_forward_mean": t.bytes_per_forward_mean}
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.sh_model_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def quantize_i8(src: np.ndarray, per_row: bool):
+    """Device int8 quantizer (bridge/ane_bridge.m:374-399). Returns (q, scales)."""
+    a = np.ascontiguousarray(src, np.float32)
+    rows, cols = (a.shape if a.ndim == 2 else (1, a.size))
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows if per_row else 1, np.float32)
+    _check(load().sh_quantize_i8(_fp(a), rows, cols, q.ctypes.data_as(C.POINTER(C.c_int8)), _fp(s), int(per_row)),
+           "sh_quantize_i8")
+    return q, s
+
+
+def dequantize_i8(q: np.ndarray, scales: np.ndarray, per_row: bool) -> np.ndarray:
+    qq = np.ascontiguousarray(q, np.int8)
+    rows, cols = qq.shape
+    out = np.empty((rows, cols), np.float32)
+    s = np.ascontiguousarray(scales, np.float32)
+    _check(load().sh_dequantize_i8(qq.ctypes.data_as(C.POINTER(C.c_int8)), _fp(s), rows, cols, int(per_row), _fp(out)),
+           "sh_dequantize_i8")
+    return out

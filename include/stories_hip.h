@@ -1,0 +1,145 @@
+/*
+ * stories_hip.h — C ABI of libstories_hip.so, the MI355X (gfx950) token loop for
+ * Stories110M- and Qwen3-shaped Llama models.
+ *
+ * This is the drop-in boundary. Each entry point names the reference interface it replaces
+ * (paths relative to the reference tree). The conventions follow the reference's own C ABI,
+ * bridge/ane_bridge.h: opaque handle types (:17-18), int status 0 on success / negative on
+ * failure (:27), NULL from constructors on failure (:38-42), caller-owned input and output
+ * buffers, and the error text of the calling thread's last failure via sh_last_error
+ * (stories_trainer_bridge.h:36). Plain pointers and sizes only; no C++ or torch types.
+ *
+ * Threading: a model handle is single-threaded, like stories.Decoder (infer.go:30-59); two
+ * threads must not call into one handle at the same time. Distinct handles are independent.
+ * Host pointers are read or written only during the call (cgo pointer rules).
+ */
+#ifndef STORIES_HIP_H
+#define STORIES_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct sh_model sh_model;
+
+/* Weight storage types. Host weights are always fp32; upload rounds them on the device. */
+enum {
+    SH_DTYPE_F16 = 1,   /* fp16 weights (round to nearest even), fp32 activations */
+    SH_DTYPE_BF16 = 2,  /* bf16 weights (round to nearest even), fp32 activations */
+    SH_DTYPE_W8A8 = 3   /* int8 weights per output row + int8 per-tensor activations */
+};
+
+/* KV-cache storage types. */
+enum { SH_KV_F32 = 0, SH_KV_F16 = 1, SH_KV_BF16 = 2 };
+
+/* Model shape and numerics. Replaces the compile-time constants of ane/stories/config.go:3-18
+ * (and training/training_dynamic/models/qwen3_06b.h:6-16) with a runtime description. */
+typedef struct sh_config {
+    int32_t dim;          /* D: residual width (config.go:4 Dim) */
+    int32_t hidden;       /* F: SwiGLU width (config.go:5 Hidden) */
+    int32_t n_layers;     /* config.go:8 NLayers */
+    int32_t n_heads;      /* query heads (config.go:6 Heads) */
+    int32_t n_kv_heads;   /* key/value heads; q head h reads kv head h / (H/KVH) */
+    int32_t head_dim;     /* hd; Stories D/H = 64 */
+    int32_t vocab;        /* config.go:9 Vocab */
+    int32_t max_seq;      /* KV-cache positions (infer.go:84-89 clamps Stories to 256) */
+    double rope_theta;    /* infer.go:102 (10000) */
+    double norm_eps;      /* infer.go:307 (1e-5) */
+    double qk_norm_eps;   /* per-head Q/K RMSNorm eps, when qk_norm != 0 */
+    float residual_scale; /* alpha in x + alpha*branch: 1 (infer.go:227,238) or
+                             1/sqrt(2L) (ane/storiesane/residual.go:9) */
+    int32_t qk_norm;      /* 1: RMSNorm every q and k head before RoPE */
+    int32_t tied_embed;   /* 1: classifier rows are the embedding (weights.go:22) */
+    int32_t kv_dtype;     /* SH_KV_* */
+    int32_t max_batch;    /* sequences for the batched entry points (>= 1) */
+} sh_config;
+
+/* Timing of the last decode / prefill call, from HIP events on the library's stream. */
+typedef struct sh_timing {
+    double gpu_ms;          /* device time of the last call's timed region */
+    int64_t forwards;       /* token forwards (one per position) in that region */
+    int64_t tokens_out;     /* tokens produced (greedy) in that region */
+    double bytes_per_forward_mean; /* algorithmic bytes per forward, averaged */
+} sh_timing;
+
+/* ---- library ------------------------------------------------------------------------ */
+/* bridge/ane_bridge.h:27 ane_bridge_init: 0 on success, -1 on failure. Selects the device
+ * this thread's subsequent sh_model_create calls use. */
+int sh_init(int32_t device);
+/* stories_trainer_bridge.h:36: copies this thread's last error text into buf (NUL-ended,
+ * truncated to len) and returns the full length. */
+size_t sh_last_error(char *buf, size_t len);
+/* Default shapes: ane/stories/config.go:3-10 (Stories110M, alpha 1, fp32 KV) and
+ * training/training_dynamic/models/qwen3_06b.h:6-16 (theta 1e6, QK-norm, tied, bf16 KV). */
+int sh_config_stories110m(sh_config *cfg);
+int sh_config_qwen3_06b(sh_config *cfg);
+
+/* ---- model -------------------------------------------------------------------------- */
+/* stories.NewDecoder (ane/stories/infer.go:80-133) / storiesane.Open (engine.go:149):
+ * allocates device weights, KV cache and RoPE tables. NULL on failure. */
+sh_model *sh_model_create(const sh_config *cfg, int32_t dtype);
+/* Uploads one layer of stories.LayerWeights (ane/stories/weights.go:13-17), fp32 row-major
+ * [out, in]: wq [H*hd, D], wk/wv [KVH*hd, D], wo [D, H*hd], w1/w3 [F, D], w2 [D, F],
+ * rms_att/rms_ffn [D], q_norm/k_norm [hd] (NULL unless cfg.qk_norm). */
+int sh_model_upload_layer(sh_model *m, int32_t layer, const float *wq, const float *wk,
+                          const float *wv, const float *wo, const float *w1, const float *w2,
+                          const float *w3, const float *rms_att, const float *rms_ffn,
+                          const float *q_norm, const float *k_norm);
+/* ModelWeights.Embed [V, D] and RMSFinal [D] (weights.go:19-24); cls [V, D] or NULL when
+ * cfg.tied_embed (the Embed rows are the classifier, infer.go:243). */
+int sh_model_upload_globals(sh_model *m, const float *embed, const float *rms_final,
+                            const float *cls);
+/* (*Decoder).ResetCache (infer.go:61-70). */
+int sh_reset_cache(sh_model *m);
+/* (*Decoder).EvalNextLogits (infer.go:72-77) = forwardOne (infer.go:204-245): one token
+ * at one position through the KV cache. logits (V floats) may be NULL; argmax_out (first
+ * maximum, infer.go:373-383) may be NULL. */
+int sh_decode_step(sh_model *m, int32_t token, int32_t pos, float *logits,
+                   int32_t *argmax_out);
+/* (*Decoder).Decode with Temperature 0 (infer.go:136-202): clears the cache, feeds the
+ * prompt (last max_seq ids; [BOS] if empty), generates up to max_new tokens (64 if <= 0),
+ * stops after EOS=2 or at max_seq tokens. out_tokens (capacity max_seq) receives prompt +
+ * generated ids, *n_out their count, *stopped_eos whether EOS ended the loop. The whole
+ * loop runs on the device; the host sees only the final ids. */
+int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32_t max_new,
+                     int32_t *out_tokens, int32_t *n_out, int32_t *stopped_eos);
+/* (*Engine).EvalLogits (ane/storiesane/engine.go:363-376) = evalLogitsCPUInto
+ * (engine.go:804-842): the full causal forward of `seq` tokens (seq <= max_seq), logits
+ * channel-first [V, seq] (logits[v*seq + t]). Out-of-range ids give a zero embedding
+ * column (cpu.go:41-72). Residual scale = cfg.residual_scale. */
+int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *logits_cf);
+/* Timing of the last sh_greedy_decode / sh_prefill_logits call. */
+int sh_stats(const sh_model *m, sh_timing *out);
+/* (*Engine).Close (engine.go:480): frees device memory. NULL is allowed. */
+void sh_model_destroy(sh_model *m);
+
+/* ---- W8A8 quantizer (bridge/ane_bridge.m:374-399), run on the device --------------- */
+/* per_row == 0: one scale for the whole tensor, exactly the bridge formula
+ * (scale = max|x|/127, 0 -> 1; q = (int8)(clamp(x/scale, -128, 127) +- 0.5)).
+ * per_row != 0: the same formula applied to each row on its own; scales has `rows`
+ * entries. Bit-exact with the bridge's C code. */
+int sh_quantize_i8(const float *src, int32_t rows, int32_t cols, int8_t *dst, float *scales,
+                   int32_t per_row);
+/* dst[r, c] = (float)q[r, c] * scale(r) (constexpr_affine_dequantize with zero point 0,
+ * ane_int8_bench.m:62-70). */
+int sh_dequantize_i8(const int8_t *q, const float *scales, int32_t rows, int32_t cols,
+                     int32_t per_row, float *dst);
+
+/* ---- host helpers (no device work) -------------------------------------------------- */
+/* Deterministic synthetic weights, replacing stories.RandomInit (weights.go:124-153) for
+ * the N(0, std) configurations: element i of tensor `tensor_id` is a Box-Muller normal of
+ * two splitmix64 draws keyed by (seed, tensor_id, i). Same values on every host. */
+int sh_synth_normal(float *dst, size_t n, uint64_t seed, uint64_t tensor_id, float std);
+/* Uniform token ids in [0, vocab) keyed by seed (prompts of the synthetic configs). */
+int sh_synth_tokens(int32_t *dst, size_t n, uint64_t seed, int32_t vocab);
+/* Rounds fp32 data in place to the values a dtype stores (SH_DTYPE_F16 / SH_DTYPE_BF16:
+ * round to nearest even), so a CPU check can consume exactly the device's weights. */
+int sh_round_dtype(float *data, size_t n, int32_t dtype);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

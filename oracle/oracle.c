@@ -1,0 +1,734 @@
+/*
+ * oracle.c — CPU restatement of the reference's Stories110M / Qwen3-shaped token loop.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h). Build: oracle/Makefile
+ * (gcc -O2 -ffp-contract=off -fopenmp). Nothing here is shipped or measured as the product.
+ *
+ * Reference files restated (paths relative to the reference tree):
+ *   ane/stories/infer.go            KV-cache Decoder: forwardOne, attend, rmsNormVec, matVec,
+ *                                   silu, softmaxPrefix, argmax, RoPE tables, Decode loop
+ *   ane/stories/cpu.go              EmbedLookup (CF), RMSNorm (CF, float64 product),
+ *                                   MatMulVocabSeq
+ *   ane/storiesane/engine.go        evalLogitsCPUInto (the full-sequence forward)
+ *   ane/storiesane/forward_common.go, accel_other.go, rope.go, residual.go, decode.go
+ *   bridge/ane_bridge.m:374-399     symmetric int8 quantizer
+ *   training/training_dynamic/io.h:437-457  GQA head mapping kv = h / (H/KVH)
+ *
+ * Extensions beyond the reference (each switched off for the Stories configuration):
+ * GQA, per-head Q/K RMSNorm, configurable RoPE theta / eps / residual scale, K/V storage
+ * rounding, and per-output-row W8A8 projections.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define OR_BOS 1
+#define OR_EOS 2
+
+/* ------------------------------------------------------------------------------------ */
+/* dtype rounding (IEEE round-to-nearest-even, the rounding of v_cvt_f16_f32 and of      */
+/* numpy/torch casts). The reference's own converter (ane/mil/generator.go:151-184) only */
+/* feeds the ANE path; both sides here consume the same RNE-rounded values.              */
+
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+float or_half_round(float x) {
+    uint32_t u = f2u(x);
+    uint32_t sign = u & 0x80000000u;
+    uint32_t absu = u & 0x7fffffffu;
+    if (absu >= 0x7f800000u) return x;                       /* inf / nan pass through */
+    float a = u2f(absu);
+    if (a >= 65520.0f) return u2f(sign | 0x7f800000u);       /* rounds to inf */
+    if (a < 6.103515625e-05f) {                              /* fp16 subnormal range */
+        /* quantum 2^-24: round-to-nearest-even of a / 2^-24 */
+        double q = (double)a * 16777216.0;
+        double r = nearbyint(q);                             /* default mode: ties to even */
+        float m = (float)(r / 16777216.0);
+        return sign ? -m : m;
+    }
+    /* normal: keep 10 mantissa bits, RNE on the 13 dropped bits */
+    uint32_t lsb = (absu >> 13) & 1u;
+    uint32_t rounded = absu + 0x0fffu + lsb;
+    rounded &= ~0x1fffu;
+    return u2f(sign | rounded);
+}
+
+float or_bf16_round(float x) {
+    uint32_t u = f2u(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return x;          /* nan */
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7fffu + lsb;
+    u &= 0xffff0000u;
+    return u2f(u);
+}
+
+static float kv_round(int kv_dtype, float v) {
+    if (kv_dtype == OR_KV_F16) return or_half_round(v);
+    if (kv_dtype == OR_KV_BF16) return or_bf16_round(v);
+    return v;
+}
+
+/* ------------------------------------------------------------------------------------ */
+/* infer.go:301-311 rmsNormVec: float64 sum of squares, float32 rrms, (x*rrms)*w float32 */
+void or_rms_norm_vec(float *out, const float *x, const float *w, int n, double eps) {
+    double sum = 0;
+    for (int i = 0; i < n; i++) {
+        double v = (double)x[i];
+        sum += v * v;
+    }
+    float rrms = (float)(1.0 / sqrt(sum / (double)n + eps));
+    for (int i = 0; i < n; i++) out[i] = x[i] * rrms * w[i];
+}
+
+/* infer.go:313-322 matVec: out[r] = sum over c in order of row[c]*in[c], float32.
+ * Four rows are walked together so the CPU overlaps their independent add chains; each
+ * row's own sum keeps the reference order. */
+static void mat_vec_range(float *out, const float *mat, const float *in, int r0, int r1,
+                          int cols) {
+    int r = r0;
+    for (; r + 4 <= r1; r += 4) {
+        const float *a = mat + (size_t)r * cols;
+        const float *b = a + cols, *c = b + cols, *d = c + cols;
+        float s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+        for (int k = 0; k < cols; k++) {
+            float xv = in[k];
+            s0 += a[k] * xv;
+            s1 += b[k] * xv;
+            s2 += c[k] * xv;
+            s3 += d[k] * xv;
+        }
+        out[r] = s0; out[r + 1] = s1; out[r + 2] = s2; out[r + 3] = s3;
+    }
+    for (; r < r1; r++) {
+        const float *a = mat + (size_t)r * cols;
+        float s = 0;
+        for (int k = 0; k < cols; k++) s += a[k] * in[k];
+        out[r] = s;
+    }
+}
+
+void or_mat_vec(float *out, const float *mat, const float *in, int rows, int cols,
+                int threads) {
+    if (threads <= 1 || rows < 256) {
+        mat_vec_range(out, mat, in, 0, rows, cols);
+        return;
+    }
+    int chunks = (rows + 63) / 64;
+#pragma omp parallel for num_threads(threads) schedule(static)
+    for (int ch = 0; ch < chunks; ch++) {
+        int r0 = ch * 64, r1 = r0 + 64 > rows ? rows : r0 + 64;
+        mat_vec_range(out, mat, in, r0, r1, cols);
+    }
+}
+
+/* infer.go:324-326 silu: x / (1 + float32(exp(float64(-x)))) */
+float or_silu(float x) { return x / (1.0f + (float)exp((double)(-x))); }
+
+/* infer.go:328-345 softmaxPrefix: float32 max, float32(exp(float64(s-mx))), float64 sum of
+ * the rounded terms, float32 inverse, float32 scale. */
+void or_softmax_prefix(float *dst, const float *src, int n) {
+    float mx = src[0];
+    for (int i = 1; i < n; i++)
+        if (src[i] > mx) mx = src[i];
+    double sum = 0;
+    for (int i = 0; i < n; i++) {
+        float e = (float)exp((double)(src[i] - mx));
+        dst[i] = e;
+        sum += (double)e;
+    }
+    float inv = (float)(1.0 / sum);
+    for (int i = 0; i < n; i++) dst[i] *= inv;
+}
+
+/* infer.go:373-383 argmax: first maximum (strict >) */
+int32_t or_argmax(const float *v, int n) {
+    int32_t best = 0;
+    float bv = v[0];
+    for (int i = 1; i < n; i++)
+        if (v[i] > bv) { bv = v[i]; best = i; }
+    return best;
+}
+
+/* infer.go:97-107 / rope.go:5-24: freq = pos / theta^(2i/hd) in float64, float32 cos/sin,
+ * table [max_seq][hd/2] */
+void or_rope_tables(float *cos_out, float *sin_out, int max_seq, int head_dim, double theta) {
+    int half = head_dim / 2;
+    for (int pos = 0; pos < max_seq; pos++)
+        for (int i = 0; i < half; i++) {
+            double freq = (double)pos / pow(theta, (double)(2 * i) / (double)head_dim);
+            cos_out[pos * half + i] = (float)cos(freq);
+            sin_out[pos * half + i] = (float)sin(freq);
+        }
+}
+
+/* ------------------------------------------------------------------------------------ */
+/* bridge/ane_bridge.m:374-399: scale = max|x|/127 (0 -> 1); v = x/scale; clamp to        */
+/* [-128,127]; q = (int8)(v + (v >= 0 ? 0.5 : -0.5)) (round half away, then truncate).    */
+int8_t or_quantize_value(float v) {
+    if (v > 127.0f) v = 127.0f;
+    if (v < -128.0f) v = -128.0f;
+    return (int8_t)(v + (v >= 0 ? 0.5f : -0.5f));
+}
+
+float or_absmax_scale(const float *src, size_t n) {
+    float max_abs = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        float a = src[i] < 0 ? -src[i] : src[i];
+        if (a > max_abs) max_abs = a;
+    }
+    float scale = max_abs / 127.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    return scale;
+}
+
+void or_quantize_tensor(const float *src, size_t n, int8_t *dst, float *scale_out) {
+    float scale = or_absmax_scale(src, n);
+    for (size_t i = 0; i < n; i++) dst[i] = or_quantize_value(src[i] / scale);
+    *scale_out = scale;
+}
+
+/* The bridge formula applied to each output row on its own (one row = the bridge call). */
+void or_quantize_rows(const float *src, int rows, int cols, int8_t *dst, float *scales) {
+    for (int r = 0; r < rows; r++)
+        or_quantize_tensor(src + (size_t)r * cols, (size_t)cols, dst + (size_t)r * cols,
+                           &scales[r]);
+}
+
+void or_dequantize_rows(const int8_t *q, const float *scales, int rows, int cols,
+                        float *dst) {
+    for (int r = 0; r < rows; r++)
+        for (int c = 0; c < cols; c++)
+            dst[(size_t)r * cols + c] = (float)q[(size_t)r * cols + c] * scales[r];
+}
+
+/* W8A8 projection: per-tensor activation quantization of `in`, exact int32 dot product per
+ * row, y = (float)acc * (s_w[r] * s_a). */
+void or_mat_vec_w8a8(float *out, const int8_t *wq, const float *wscale, const float *in,
+                     int rows, int cols, int threads) {
+    int8_t *qa = (int8_t *)malloc((size_t)cols);
+    float sa;
+    or_quantize_tensor(in, (size_t)cols, qa, &sa);
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static) if (threads > 1 && rows >= 256)
+    for (int r = 0; r < rows; r++) {
+        const int8_t *row = wq + (size_t)r * cols;
+        int32_t acc = 0;
+        for (int c = 0; c < cols; c++) acc += (int32_t)row[c] * (int32_t)qa[c];
+        out[r] = (float)acc * (wscale[r] * sa);
+    }
+    free(qa);
+}
+
+/* ------------------------------------------------------------------------------------ */
+/* KV-cache decoder: ane/stories/infer.go                                                */
+
+enum { P_WQ, P_WK, P_WV, P_WO, P_W1, P_W2, P_W3, P_N };
+
+struct or_decoder {
+    or_config cfg;
+    or_layer *layers;
+    const float *embed, *rms_final, *cls;
+    int threads;
+    int qdim, kvdim, hd;
+    float *kc, *vc;           /* [L][max_seq][kvdim] */
+    float *rcos, *rsin;       /* [max_seq][hd/2] */
+    float *x, *xn, *q, *k, *v, *att, *x2, *x2n, *h1, *h3, *ff, *scores, *probs, *logits;
+    /* W8A8 */
+    int8_t *q8[64][P_N];
+    float *s8[64][P_N];
+    int8_t *cls8;
+    float *cls_s;
+};
+
+static const float *layer_mat(const or_layer *l, int p) {
+    switch (p) {
+    case P_WQ: return l->wq;
+    case P_WK: return l->wk;
+    case P_WV: return l->wv;
+    case P_WO: return l->wo;
+    case P_W1: return l->w1;
+    case P_W2: return l->w2;
+    default: return l->w3;
+    }
+}
+
+static void mat_shape(const or_decoder *d, int p, int *rows, int *cols) {
+    const or_config *c = &d->cfg;
+    switch (p) {
+    case P_WQ: *rows = d->qdim; *cols = c->dim; break;
+    case P_WK: case P_WV: *rows = d->kvdim; *cols = c->dim; break;
+    case P_WO: *rows = c->dim; *cols = d->qdim; break;
+    case P_W1: case P_W3: *rows = c->hidden; *cols = c->dim; break;
+    default: *rows = c->dim; *cols = c->hidden; break;
+    }
+}
+
+or_decoder *or_decoder_new(const or_config *cfg, const or_weights *w, int threads) {
+    if (!cfg || !w || cfg->n_layers > 64 || cfg->n_layers <= 0) return NULL;
+    if (cfg->n_kv_heads <= 0 || cfg->n_heads % cfg->n_kv_heads) return NULL;
+    or_decoder *d = (or_decoder *)calloc(1, sizeof(*d));
+    d->cfg = *cfg;
+    d->threads = threads < 1 ? 1 : threads;
+    d->hd = cfg->head_dim;
+    d->qdim = cfg->n_heads * cfg->head_dim;
+    d->kvdim = cfg->n_kv_heads * cfg->head_dim;
+    d->layers = (or_layer *)malloc(sizeof(or_layer) * cfg->n_layers);
+    memcpy(d->layers, w->layers, sizeof(or_layer) * cfg->n_layers);
+    d->embed = w->embed;
+    d->rms_final = w->rms_final;
+    d->cls = w->cls ? w->cls : w->embed;
+    size_t kvn = (size_t)cfg->n_layers * cfg->max_seq * d->kvdim;
+    d->kc = (float *)calloc(kvn, sizeof(float));
+    d->vc = (float *)calloc(kvn, sizeof(float));
+    int half = d->hd / 2;
+    d->rcos = (float *)malloc(sizeof(float) * cfg->max_seq * half);
+    d->rsin = (float *)malloc(sizeof(float) * cfg->max_seq * half);
+    or_rope_tables(d->rcos, d->rsin, cfg->max_seq, d->hd, cfg->rope_theta);
+    int big = cfg->dim > d->qdim ? cfg->dim : d->qdim;
+    d->x = (float *)calloc(cfg->dim, sizeof(float));
+    d->xn = (float *)calloc(cfg->dim, sizeof(float));
+    d->q = (float *)calloc(d->qdim, sizeof(float));
+    d->k = (float *)calloc(d->kvdim, sizeof(float));
+    d->v = (float *)calloc(d->kvdim, sizeof(float));
+    d->att = (float *)calloc(big, sizeof(float));
+    d->x2 = (float *)calloc(cfg->dim, sizeof(float));
+    d->x2n = (float *)calloc(cfg->dim, sizeof(float));
+    d->h1 = (float *)calloc(cfg->hidden, sizeof(float));
+    d->h3 = (float *)calloc(cfg->hidden, sizeof(float));
+    d->ff = (float *)calloc(cfg->dim, sizeof(float));
+    d->scores = (float *)calloc(cfg->max_seq, sizeof(float));
+    d->probs = (float *)calloc(cfg->max_seq, sizeof(float));
+    d->logits = (float *)calloc(cfg->vocab, sizeof(float));
+    if (cfg->w8a8) {
+        for (int l = 0; l < cfg->n_layers; l++)
+            for (int p = 0; p < P_N; p++) {
+                int rows, cols;
+                mat_shape(d, p, &rows, &cols);
+                d->q8[l][p] = (int8_t *)malloc((size_t)rows * cols);
+                d->s8[l][p] = (float *)malloc(sizeof(float) * rows);
+                or_quantize_rows(layer_mat(&d->layers[l], p), rows, cols, d->q8[l][p],
+                                 d->s8[l][p]);
+            }
+        d->cls8 = (int8_t *)malloc((size_t)cfg->vocab * cfg->dim);
+        d->cls_s = (float *)malloc(sizeof(float) * cfg->vocab);
+        or_quantize_rows(d->cls, cfg->vocab, cfg->dim, d->cls8, d->cls_s);
+    }
+    return d;
+}
+
+void or_decoder_free(or_decoder *d) {
+    if (!d) return;
+    if (d->cfg.w8a8) {
+        for (int l = 0; l < d->cfg.n_layers; l++)
+            for (int p = 0; p < P_N; p++) { free(d->q8[l][p]); free(d->s8[l][p]); }
+        free(d->cls8);
+        free(d->cls_s);
+    }
+    free(d->layers); free(d->kc); free(d->vc); free(d->rcos); free(d->rsin);
+    free(d->x); free(d->xn); free(d->q); free(d->k); free(d->v); free(d->att);
+    free(d->x2); free(d->x2n); free(d->h1); free(d->h3); free(d->ff);
+    free(d->scores); free(d->probs); free(d->logits);
+    free(d);
+}
+
+/* infer.go:61-70 ResetCache */
+void or_decoder_reset(or_decoder *d) {
+    size_t kvn = (size_t)d->cfg.n_layers * d->cfg.max_seq * d->kvdim;
+    memset(d->kc, 0, kvn * sizeof(float));
+    memset(d->vc, 0, kvn * sizeof(float));
+}
+
+static void project(or_decoder *d, int l, int p, float *out, const float *in) {
+    int rows, cols;
+    mat_shape(d, p, &rows, &cols);
+    if (d->cfg.w8a8)
+        or_mat_vec_w8a8(out, d->q8[l][p], d->s8[l][p], in, rows, cols, d->threads);
+    else
+        or_mat_vec(out, layer_mat(&d->layers[l], p), in, rows, cols, d->threads);
+}
+
+/* infer.go:247-265 applyRoPE on n_heads heads of vec (interleaved pairs 2i, 2i+1) */
+static void apply_rope(const or_decoder *d, float *vec, int n_heads, int pos) {
+    int stride = d->hd / 2;
+    for (int h = 0; h < n_heads; h++) {
+        int base = h * d->hd;
+        int rb = pos * stride;
+        for (int i = 0; i < stride; i++) {
+            float c = d->rcos[rb + i], s = d->rsin[rb + i];
+            float e = vec[base + 2 * i], o = vec[base + 2 * i + 1];
+            vec[base + 2 * i] = e * c - o * s;
+            vec[base + 2 * i + 1] = e * s + o * c;
+        }
+    }
+}
+
+/* infer.go:273-299 attend; q head h reads kv head h / (H/KVH) (io.h:437-457 mapping) */
+static void attend(or_decoder *d, int layer, int pos) {
+    const or_config *c = &d->cfg;
+    int hd = d->hd;
+    int group = c->n_heads / c->n_kv_heads;
+    float inv_sqrt_hd = (float)(1.0 / sqrt((double)hd));
+    for (int h = 0; h < c->n_heads; h++) {
+        int qb = h * hd;
+        int kb0 = (h / group) * hd;
+        for (int t = 0; t <= pos; t++) {
+            const float *kr = d->kc + ((size_t)layer * c->max_seq + t) * d->kvdim + kb0;
+            float dot = 0;
+            for (int i = 0; i < hd; i++) dot += d->q[qb + i] * kr[i];
+            d->scores[t] = dot * inv_sqrt_hd;
+        }
+        or_softmax_prefix(d->probs, d->scores, pos + 1);
+        for (int i = 0; i < hd; i++) {
+            float sum = 0;
+            for (int t = 0; t <= pos; t++) {
+                const float *vr = d->vc + ((size_t)layer * c->max_seq + t) * d->kvdim + kb0;
+                sum += d->probs[t] * vr[i];
+            }
+            d->att[qb + i] = sum;
+        }
+    }
+}
+
+/* infer.go:204-245 forwardOne */
+int or_forward_one(or_decoder *d, int token, int pos, float *logits_out) {
+    const or_config *c = &d->cfg;
+    if (token < 0 || token >= c->vocab) return -1;
+    if (pos < 0 || pos >= c->max_seq) return -1;
+    int D = c->dim, F = c->hidden, hd = d->hd;
+    float alpha = c->residual_scale;
+    memcpy(d->x, d->embed + (size_t)token * D, sizeof(float) * D);
+    for (int l = 0; l < c->n_layers; l++) {
+        const or_layer *L = &d->layers[l];
+        or_rms_norm_vec(d->xn, d->x, L->rms_att, D, c->norm_eps);
+        project(d, l, P_WQ, d->q, d->xn);
+        project(d, l, P_WK, d->k, d->xn);
+        project(d, l, P_WV, d->v, d->xn);
+        if (c->qk_norm) {
+            for (int h = 0; h < c->n_heads; h++)
+                or_rms_norm_vec(d->q + h * hd, d->q + h * hd, L->q_norm, hd, c->qk_norm_eps);
+            for (int h = 0; h < c->n_kv_heads; h++)
+                or_rms_norm_vec(d->k + h * hd, d->k + h * hd, L->k_norm, hd, c->qk_norm_eps);
+        }
+        apply_rope(d, d->q, c->n_heads, pos);
+        apply_rope(d, d->k, c->n_kv_heads, pos);
+        /* infer.go:267-271 storeKV (rounded to the cache's storage type) */
+        size_t base = ((size_t)l * c->max_seq + pos) * d->kvdim;
+        for (int i = 0; i < d->kvdim; i++) {
+            d->kc[base + i] = kv_round(c->kv_dtype, d->k[i]);
+            d->vc[base + i] = kv_round(c->kv_dtype, d->v[i]);
+        }
+        attend(d, l, pos);
+        project(d, l, P_WO, d->x2, d->att);
+        for (int i = 0; i < D; i++) d->x2[i] = d->x[i] + alpha * d->x2[i];
+        or_rms_norm_vec(d->x2n, d->x2, L->rms_ffn, D, c->norm_eps);
+        project(d, l, P_W1, d->h1, d->x2n);
+        project(d, l, P_W3, d->h3, d->x2n);
+        for (int i = 0; i < F; i++) d->h1[i] = or_silu(d->h1[i]) * d->h3[i];
+        project(d, l, P_W2, d->ff, d->h1);
+        for (int i = 0; i < D; i++) d->x[i] = d->x2[i] + alpha * d->ff[i];
+    }
+    or_rms_norm_vec(d->xn, d->x, d->rms_final, D, c->norm_eps);
+    if (c->w8a8)
+        or_mat_vec_w8a8(d->logits, d->cls8, d->cls_s, d->xn, c->vocab, D, d->threads);
+    else
+        or_mat_vec(d->logits, d->cls, d->xn, c->vocab, D, d->threads);
+    if (logits_out) memcpy(logits_out, d->logits, sizeof(float) * c->vocab);
+    return 0;
+}
+
+const float *or_decoder_tap(const or_decoder *d, int which) {
+    switch (which) {
+    case 0: return d->x;
+    case 1: return d->q;
+    case 2: return d->k;
+    case 3: return d->v;
+    case 4: return d->att;
+    case 5: return d->h1;
+    default: return d->logits;
+    }
+}
+
+static float top2_margin(const float *v, int n) {
+    float a = -INFINITY, b = -INFINITY;
+    for (int i = 0; i < n; i++) {
+        if (v[i] > a) { b = a; a = v[i]; }
+        else if (v[i] > b) b = v[i];
+    }
+    return a - b;
+}
+
+/* infer.go:136-202 Decode with temperature <= 1e-6 (argmax sampling, infer.go:347-350) */
+int or_greedy_decode(or_decoder *d, const int32_t *prompt, int n_prompt, int max_new,
+                     int32_t *out_tokens, int32_t *n_out, int32_t *stopped_eos,
+                     float *margins) {
+    const or_config *c = &d->cfg;
+    if (max_new <= 0) max_new = 64;
+    int32_t bos = OR_BOS;
+    if (n_prompt <= 0) { prompt = &bos; n_prompt = 1; }
+    if (n_prompt > c->max_seq) { prompt += n_prompt - c->max_seq; n_prompt = c->max_seq; }
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= c->vocab) return -1;
+    or_decoder_reset(d);
+    int n = 0;
+    for (int i = 0; i < n_prompt; i++) out_tokens[n++] = prompt[i];
+    for (int pos = 0; pos < n_prompt - 1; pos++)
+        if (or_forward_one(d, prompt[pos], pos, NULL)) return -1;
+    *stopped_eos = 0;
+    for (int step = 0; step < max_new && n < c->max_seq; step++) {
+        int pos = n - 1;
+        if (or_forward_one(d, out_tokens[pos], pos, NULL)) return -1;
+        int32_t next = or_argmax(d->logits, c->vocab);
+        if (margins) margins[step] = top2_margin(d->logits, c->vocab);
+        out_tokens[n++] = next;
+        if (next == OR_EOS) { *stopped_eos = 1; break; }
+    }
+    *n_out = n;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------ */
+/* Full-sequence channel-first forward: ane/storiesane/engine.go:804-842                 */
+
+/* cpu.go:41-72 EmbedLookup: out[d*S+t] = embed[tok*D+d]; out-of-range token -> zero column */
+void or_embed_lookup_cf(float *out, const float *embed, int vocab, const uint16_t *tokens,
+                        int dim, int seq) {
+    for (int t = 0; t < seq; t++) {
+        int tok = tokens[t];
+        for (int d = 0; d < dim; d++)
+            out[(size_t)d * seq + t] =
+                (tok < 0 || tok >= vocab) ? 0.0f : embed[(size_t)tok * dim + d];
+    }
+}
+
+/* accel_other.go:11-28 rmsNormCFWithRRMSImpl: float64 sum, float32 scale, x*scale*w */
+static void rms_norm_cf(float *out, const float *x, const float *w, int dim, int seq,
+                        double eps) {
+    for (int t = 0; t < seq; t++) {
+        double sum = 0;
+        for (int i = 0; i < dim; i++) {
+            double v = (double)x[(size_t)i * seq + t];
+            sum += v * v;
+        }
+        float scale = (float)(1.0 / sqrt(sum / (double)dim + eps));
+        for (int i = 0; i < dim; i++)
+            out[(size_t)i * seq + t] = x[(size_t)i * seq + t] * scale * w[i];
+    }
+}
+
+/* forward_common.go:35-46 linearCF: out[o*S+t] = sum over i in order of W[o,i]*in[i*S+t].
+ * The input is first transposed to [S][in] (pure data movement) so the ordered sums read
+ * contiguous memory. */
+static void linear_cf(float *out, const float *wts, const float *in, int out_ch, int in_ch,
+                      int seq, int threads) {
+    float *inT = (float *)malloc(sizeof(float) * (size_t)in_ch * seq);
+    for (int i = 0; i < in_ch; i++)
+        for (int t = 0; t < seq; t++) inT[(size_t)t * in_ch + i] = in[(size_t)i * seq + t];
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int o = 0; o < out_ch; o++) {
+        const float *row = wts + (size_t)o * in_ch;
+        int t = 0;
+        for (; t + 4 <= seq; t += 4) {
+            const float *a = inT + (size_t)t * in_ch;
+            const float *b = a + in_ch, *c = b + in_ch, *e = c + in_ch;
+            float s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+            for (int i = 0; i < in_ch; i++) {
+                float wv = row[i];
+                s0 += wv * a[i];
+                s1 += wv * b[i];
+                s2 += wv * c[i];
+                s3 += wv * e[i];
+            }
+            out[(size_t)o * seq + t] = s0;
+            out[(size_t)o * seq + t + 1] = s1;
+            out[(size_t)o * seq + t + 2] = s2;
+            out[(size_t)o * seq + t + 3] = s3;
+        }
+        for (; t < seq; t++) {
+            const float *a = inT + (size_t)t * in_ch;
+            float s = 0;
+            for (int i = 0; i < in_ch; i++) s += row[i] * a[i];
+            out[(size_t)o * seq + t] = s;
+        }
+    }
+    free(inT);
+}
+
+/* rope.go:26-46 applyRoPECFInPlace: e' = e*c - o*s, o' = o*c + e*s */
+static void rope_cf(float *x, int heads, int hd, int seq, const float *rc, const float *rs) {
+    int half = hd / 2;
+    for (int h = 0; h < heads; h++)
+        for (int i = 0; i < half; i++) {
+            size_t even = (size_t)(h * hd + 2 * i) * seq, odd = even + seq;
+            for (int t = 0; t < seq; t++) {
+                float c = rc[t * half + i], s = rs[t * half + i];
+                float e = x[even + t], o = x[odd + t];
+                x[even + t] = e * c - o * s;
+                x[odd + t] = o * c + e * s;
+            }
+        }
+}
+
+/* Per-head RMSNorm of q or k in channel-first layout (extension: Qwen3-shaped QK-norm),
+ * the rmsNormVec arithmetic (infer.go:301-311) over each head's hd values at each t. */
+static void qk_norm_cf(float *x, int heads, int hd, int seq, const float *g, double eps) {
+    for (int h = 0; h < heads; h++)
+        for (int t = 0; t < seq; t++) {
+            double sum = 0;
+            for (int i = 0; i < hd; i++) {
+                double v = (double)x[(size_t)(h * hd + i) * seq + t];
+                sum += v * v;
+            }
+            float rr = (float)(1.0 / sqrt(sum / (double)hd + eps));
+            for (int i = 0; i < hd; i++) {
+                size_t o = (size_t)(h * hd + i) * seq + t;
+                x[o] = x[o] * rr * g[i];
+            }
+        }
+}
+
+/* accel_other.go:190-207 softmaxRowAccel: float64 exp terms summed unrounded */
+static void softmax_row(float *out, const float *in, int n) {
+    float maxv = in[0];
+    for (int i = 1; i < n; i++)
+        if (in[i] > maxv) maxv = in[i];
+    double sum = 0;
+    for (int i = 0; i < n; i++) {
+        double e = exp((double)(in[i] - maxv));
+        out[i] = (float)e;
+        sum += e;
+    }
+    float inv = (float)(1.0 / sum);
+    for (int i = 0; i < n; i++) out[i] *= inv;
+}
+
+/* forward_common.go:5-33 causalAttentionCF: masked scores = -65504, softmax over the whole
+ * row, P.V over the whole row. q head h reads kv head h / (H/KVH). */
+static void causal_attention_cf(float *out, const float *qf, const float *kf,
+                                const float *vf, int heads, int kv_heads, int hd, int seq,
+                                int threads) {
+    float scale = (float)(1.0 / sqrt((double)hd));
+    int group = heads / kv_heads;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int h = 0; h < heads; h++) {
+        float *scores = (float *)malloc(sizeof(float) * seq);
+        float *probs = (float *)malloc(sizeof(float) * seq);
+        int qb = h * hd, kb = (h / group) * hd;
+        for (int t = 0; t < seq; t++) {
+            for (int j = 0; j < seq; j++) {
+                if (j > t) { scores[j] = -65504.0f; continue; }
+                float sum = 0;
+                for (int i = 0; i < hd; i++)
+                    sum += qf[(size_t)(qb + i) * seq + t] * kf[(size_t)(kb + i) * seq + j];
+                scores[j] = sum * scale;
+            }
+            softmax_row(probs, scores, seq);
+            for (int i = 0; i < hd; i++) {
+                float sum = 0;
+                for (int j = 0; j < seq; j++) sum += probs[j] * vf[(size_t)(kb + i) * seq + j];
+                out[(size_t)(qb + i) * seq + t] = sum;
+            }
+        }
+        free(scores);
+        free(probs);
+    }
+}
+
+/* cpu.go:97-111 RMSNorm: float64 rrms and a float64 product rounded once */
+static void rms_norm_final_cf(float *out, const float *x, const float *w, int d, int s,
+                              double eps) {
+    for (int t = 0; t < s; t++) {
+        double sum = 0;
+        for (int i = 0; i < d; i++) {
+            double v = (double)x[(size_t)i * s + t];
+            sum += v * v;
+        }
+        double rrms = 1.0 / sqrt(sum / (double)d + eps);
+        for (int i = 0; i < d; i++)
+            out[(size_t)i * s + t] = (float)((double)x[(size_t)i * s + t] * rrms * (double)w[i]);
+    }
+}
+
+/* cpu.go:276-300 MatMulVocabSeq: logits[v*S+t] = sum over d in order of E[v,d]*x[d*S+t] */
+static void matmul_vocab_seq(float *logits, const float *embed, const float *x, int vocab,
+                             int dim, int seq, int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int v = 0; v < vocab; v++) {
+        float *acc = logits + (size_t)v * seq;
+        const float *eb = embed + (size_t)v * dim;
+        for (int t = 0; t < seq; t++) acc[t] = 0;
+        for (int d = 0; d < dim; d++) {
+            float wv = eb[d];
+            const float *xd = x + (size_t)d * seq;
+            for (int t = 0; t < seq; t++) acc[t] += wv * xd[t];
+        }
+    }
+}
+
+void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t *tokens,
+                       int seq, float *logits_cf, int threads) {
+    int D = cfg->dim, F = cfg->hidden, H = cfg->n_heads, KVH = cfg->n_kv_heads;
+    int hd = cfg->head_dim, qd = H * hd, kvd = KVH * hd;
+    size_t S = (size_t)seq;
+    float alpha = cfg->residual_scale;
+    float *x = (float *)malloc(sizeof(float) * D * S);
+    float *next = (float *)malloc(sizeof(float) * D * S);
+    float *xn = (float *)malloc(sizeof(float) * D * S);
+    float *qf = (float *)malloc(sizeof(float) * qd * S);
+    float *kf = (float *)malloc(sizeof(float) * kvd * S);
+    float *vf = (float *)malloc(sizeof(float) * kvd * S);
+    float *att = (float *)malloc(sizeof(float) * qd * S);
+    float *x2 = (float *)malloc(sizeof(float) * D * S);
+    float *h1 = (float *)malloc(sizeof(float) * F * S);
+    float *h3 = (float *)malloc(sizeof(float) * F * S);
+    float *gate = (float *)malloc(sizeof(float) * F * S);
+    float *ff = (float *)malloc(sizeof(float) * D * S);
+    float *rc = (float *)malloc(sizeof(float) * S * (hd / 2));
+    float *rs = (float *)malloc(sizeof(float) * S * (hd / 2));
+    or_rope_tables(rc, rs, seq, hd, cfg->rope_theta);            /* engine.go:218 */
+
+    or_embed_lookup_cf(x, w->embed, cfg->vocab, tokens, D, seq);
+    float *cur = x;
+    for (int l = 0; l < cfg->n_layers; l++) {
+        const or_layer *L = &w->layers[l];
+        rms_norm_cf(xn, cur, L->rms_att, D, seq, cfg->norm_eps);
+        linear_cf(qf, L->wq, xn, qd, D, seq, threads);
+        linear_cf(kf, L->wk, xn, kvd, D, seq, threads);
+        if (cfg->qk_norm) {
+            qk_norm_cf(qf, H, hd, seq, L->q_norm, cfg->qk_norm_eps);
+            qk_norm_cf(kf, KVH, hd, seq, L->k_norm, cfg->qk_norm_eps);
+        }
+        rope_cf(qf, H, hd, seq, rc, rs);
+        rope_cf(kf, KVH, hd, seq, rc, rs);
+        linear_cf(vf, L->wv, xn, kvd, D, seq, threads);
+        causal_attention_cf(att, qf, kf, vf, H, KVH, hd, seq, threads);
+        linear_cf(x2, L->wo, att, D, qd, seq, threads);
+        for (size_t i = 0; i < D * S; i++) x2[i] = cur[i] + alpha * x2[i];   /* residual.go:19 */
+        rms_norm_cf(xn, x2, L->rms_ffn, D, seq, cfg->norm_eps);
+        linear_cf(h1, L->w1, xn, F, D, seq, threads);
+        linear_cf(h3, L->w3, xn, F, D, seq, threads);
+        for (size_t i = 0; i < F * S; i++) {                    /* accel_other.go:128-133 */
+            float sig = (float)(1.0 / (1.0 + exp((double)(-h1[i]))));
+            gate[i] = (h1[i] * sig) * h3[i];
+        }
+        linear_cf(ff, L->w2, gate, D, F, seq, threads);
+        for (size_t i = 0; i < D * S; i++) next[i] = x2[i] + alpha * ff[i];
+        float *tmp = cur; cur = next; next = tmp;
+    }
+    rms_norm_final_cf(xn, cur, w->rms_final, D, seq, cfg->norm_eps);
+    matmul_vocab_seq(logits_cf, w->cls ? w->cls : w->embed, xn, cfg->vocab, D, seq, threads);
+    free(x); free(next); free(xn); free(qf); free(kf); free(vf); free(att); free(x2);
+    free(h1); free(h3); free(gate); free(ff); free(rc); free(rs);
+}
+
+/* decode.go:83-94 fillDecodeWindow: BOS-left-pad the last `seq` tokens */
+void or_fill_decode_window(uint16_t *dst, int seq, const int32_t *tokens, int n) {
+    for (int i = 0; i < seq; i++) dst[i] = OR_BOS;
+    if (n >= seq) { tokens += n - seq; n = seq; }
+    int start = seq - n;
+    for (int i = 0; i < n; i++) dst[start + i] = (uint16_t)tokens[i];
+}

@@ -1,0 +1,96 @@
+/*
+ * oracle.h — CPU restatement of the reference's Stories110M / Qwen3-shaped token loop.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker or the timed CPU
+ * baseline. The product (libstories_hip.so) never links, loads or calls it.
+ *
+ * Every function restates a reference function, cited file:line (paths relative to the
+ * reference tree). Float semantics follow the reference's Go code on a non-FMA target:
+ * float32 arithmetic evaluated left to right, float64 where the reference converts to
+ * float64, compiled with -ffp-contract=off so no multiply-add is fused.
+ */
+#ifndef STORIES_ORACLE_H
+#define STORIES_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Storage rounding applied to K/V when they enter the cache. */
+enum { OR_KV_F32 = 0, OR_KV_F16 = 1, OR_KV_BF16 = 2 };
+
+typedef struct or_config {
+    int32_t dim, hidden, n_layers, n_heads, n_kv_heads, head_dim, vocab, max_seq;
+    double rope_theta;     /* 10000 in infer.go:102 / rope.go:13 */
+    double norm_eps;       /* 1e-5 in infer.go:307, accel_other.go:21, cpu.go:104 */
+    double qk_norm_eps;    /* per-head Q/K RMSNorm eps (used when qk_norm != 0) */
+    float residual_scale;  /* alpha: 1 for infer.go:227,238; 1/sqrt(2L) for residual.go:9 */
+    int32_t qk_norm;       /* 1: RMSNorm each q/k head before RoPE */
+    int32_t kv_dtype;      /* OR_KV_* */
+    int32_t w8a8;          /* 1: int8 weights per output row + per-tensor int8 activations */
+} or_config;
+
+typedef struct or_layer {
+    const float *wq, *wk, *wv, *wo;   /* [H*hd, D], [KVH*hd, D], [KVH*hd, D], [D, H*hd] */
+    const float *w1, *w2, *w3;        /* [F, D], [D, F], [F, D] */
+    const float *rms_att, *rms_ffn;   /* [D] */
+    const float *q_norm, *k_norm;     /* [hd] (qk_norm only) */
+} or_layer;
+
+typedef struct or_weights {
+    const or_layer *layers;   /* n_layers entries */
+    const float *embed;       /* [V, D] row-major, weights.go:22 */
+    const float *rms_final;   /* [D] */
+    const float *cls;         /* [V, D] classifier rows; equals embed when tied */
+} or_weights;
+
+typedef struct or_decoder or_decoder;
+
+/* ---- scalar building blocks (exported so tests can pin them one by one) ---- */
+float or_half_round(float x);   /* float32 -> fp16 (round to nearest even) -> float32 */
+float or_bf16_round(float x);   /* float32 -> bf16 (round to nearest even) -> float32 */
+void or_rms_norm_vec(float *out, const float *x, const float *w, int n, double eps);
+void or_mat_vec(float *out, const float *mat, const float *in, int rows, int cols, int threads);
+float or_silu(float x);
+void or_softmax_prefix(float *dst, const float *src, int n);
+int32_t or_argmax(const float *v, int n);
+void or_rope_tables(float *cos_out, float *sin_out, int max_seq, int head_dim, double theta);
+
+/* ---- W8A8 quantizer (bridge/ane_bridge.m:374-399) ---- */
+int8_t or_quantize_value(float v_over_scale);
+float or_absmax_scale(const float *src, size_t n);
+void or_quantize_tensor(const float *src, size_t n, int8_t *dst, float *scale_out);
+void or_quantize_rows(const float *src, int rows, int cols, int8_t *dst, float *scales);
+void or_dequantize_rows(const int8_t *q, const float *scales, int rows, int cols, float *dst);
+void or_mat_vec_w8a8(float *out, const int8_t *wq, const float *wscale, const float *in,
+                     int rows, int cols, int threads);
+
+/* ---- KV-cache decoder (ane/stories/infer.go) ---- */
+or_decoder *or_decoder_new(const or_config *cfg, const or_weights *w, int threads);
+void or_decoder_free(or_decoder *d);
+void or_decoder_reset(or_decoder *d);
+/* forwardOne (infer.go:204-245). logits_out may be NULL. Returns 0 or -1. */
+int or_forward_one(or_decoder *d, int token, int pos, float *logits_out);
+/* Decode with temperature 0 (infer.go:136-202). out_tokens holds prompt + generated
+ * (capacity max_seq). margins (optional, capacity max_new) receives top1-top2 gaps. */
+int or_greedy_decode(or_decoder *d, const int32_t *prompt, int n_prompt, int max_new,
+                     int32_t *out_tokens, int32_t *n_out, int32_t *stopped_eos,
+                     float *margins);
+/* Debug taps of the last forward_one: 0 x(residual out), 1 q, 2 k, 3 v, 4 att, 5 gate. */
+const float *or_decoder_tap(const or_decoder *d, int which);
+
+/* ---- full-sequence channel-first forward (ane/storiesane/engine.go:804-842) ---- */
+void or_embed_lookup_cf(float *out, const float *embed, int vocab, const uint16_t *tokens,
+                        int dim, int seq);
+void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t *tokens,
+                       int seq, float *logits_cf, int threads);
+void or_fill_decode_window(uint16_t *dst, int seq, const int32_t *tokens, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

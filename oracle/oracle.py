@@ -1,0 +1,213 @@
+"""ctypes wrapper of oracle/liboracle.so — the CPU restatement of the reference's token loop.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, as the checker or the timed CPU baseline. The product never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+OR_KV_F32, OR_KV_F16, OR_KV_BF16 = 0, 1, 2
+
+_F = C.POINTER(C.c_float)
+_I32 = C.POINTER(C.c_int32)
+
+
+class OrConfig(C.Structure):
+    _fields_ = [
+        ("dim", C.c_int32), ("hidden", C.c_int32), ("n_layers", C.c_int32),
+        ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32), ("head_dim", C.c_int32),
+        ("vocab", C.c_int32), ("max_seq", C.c_int32),
+        ("rope_theta", C.c_double), ("norm_eps", C.c_double), ("qk_norm_eps", C.c_double),
+        ("residual_scale", C.c_float), ("qk_norm", C.c_int32), ("kv_dtype", C.c_int32),
+        ("w8a8", C.c_int32),
+    ]
+
+
+class OrLayer(C.Structure):
+    _fields_ = [(k, _F) for k in ("wq", "wk", "wv", "wo", "w1", "w2", "w3",
+                                  "rms_att", "rms_ffn", "q_norm", "k_norm")]
+
+
+class OrWeights(C.Structure):
+    _fields_ = [("layers", C.POINTER(OrLayer)), ("embed", _F), ("rms_final", _F), ("cls", _F)]
+
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+    lib = C.CDLL(LIB_PATH)
+    sig = {
+        "or_half_round": (C.c_float, [C.c_float]),
+        "or_bf16_round": (C.c_float, [C.c_float]),
+        "or_rms_norm_vec": (None, [_F, _F, _F, C.c_int, C.c_double]),
+        "or_mat_vec": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_int]),
+        "or_silu": (C.c_float, [C.c_float]),
+        "or_softmax_prefix": (None, [_F, _F, C.c_int]),
+        "or_argmax": (C.c_int32, [_F, C.c_int]),
+        "or_rope_tables": (None, [_F, _F, C.c_int, C.c_int, C.c_double]),
+        "or_quantize_value": (C.c_int8, [C.c_float]),
+        "or_absmax_scale": (C.c_float, [_F, C.c_size_t]),
+        "or_quantize_tensor": (None, [_F, C.c_size_t, C.POINTER(C.c_int8), _F]),
+        "or_quantize_rows": (None, [_F, C.c_int, C.c_int, C.POINTER(C.c_int8), _F]),
+        "or_dequantize_rows": (None, [C.POINTER(C.c_int8), _F, C.c_int, C.c_int, _F]),
+        "or_mat_vec_w8a8": (None, [_F, C.POINTER(C.c_int8), _F, _F, C.c_int, C.c_int, C.c_int]),
+        "or_decoder_new": (C.c_void_p, [C.POINTER(OrConfig), C.POINTER(OrWeights), C.c_int]),
+        "or_decoder_free": (None, [C.c_void_p]),
+        "or_decoder_reset": (None, [C.c_void_p]),
+        "or_forward_one": (C.c_int, [C.c_void_p, C.c_int, C.c_int, _F]),
+        "or_greedy_decode": (C.c_int, [C.c_void_p, _I32, C.c_int, C.c_int, _I32, _I32, _I32, _F]),
+        "or_decoder_tap": (_F, [C.c_void_p, C.c_int]),
+        "or_embed_lookup_cf": (None, [_F, _F, C.c_int, C.POINTER(C.c_uint16), C.c_int, C.c_int]),
+        "or_eval_logits_cf": (None, [C.POINTER(OrConfig), C.POINTER(OrWeights), C.POINTER(C.c_uint16),
+                                     C.c_int, _F, C.c_int]),
+        "or_fill_decode_window": (None, [C.POINTER(C.c_uint16), C.c_int, _I32, C.c_int]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def fp(a):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags.c_contiguous, (a.dtype, a.flags)
+    return a.ctypes.data_as(_F)
+
+
+def config_from(sh_cfg, w8a8: bool = False, kv_dtype: int | None = None) -> OrConfig:
+    """OrConfig from the product's ShConfig (same field meanings)."""
+    c = OrConfig()
+    for k in ("dim", "hidden", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab", "max_seq",
+              "rope_theta", "norm_eps", "qk_norm_eps", "residual_scale", "qk_norm"):
+        setattr(c, k, getattr(sh_cfg, k))
+    c.kv_dtype = sh_cfg.kv_dtype if kv_dtype is None else kv_dtype
+    c.w8a8 = int(w8a8)
+    return c
+
+
+class _WeightsHolder:
+    """Keeps numpy arrays alive behind an OrWeights struct."""
+
+    def __init__(self, w, n_layers: int):
+        self.keep = []
+        layers = (OrLayer * n_layers)()
+        for l in range(n_layers):
+            lw = w.layers[l]
+            for k in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att", "rms_ffn", "q_norm", "k_norm"):
+                a = lw.get(k)
+                if a is None:
+                    setattr(layers[l], k, None)
+                    continue
+                a = np.ascontiguousarray(a, np.float32)
+                self.keep.append(a)
+                setattr(layers[l], k, fp(a))
+        self.layers = layers
+        emb = np.ascontiguousarray(w.embed, np.float32)
+        rmsf = np.ascontiguousarray(w.rms_final, np.float32)
+        self.keep += [emb, rmsf]
+        cls = None
+        if w.cls is not None:
+            cls = np.ascontiguousarray(w.cls, np.float32)
+            self.keep.append(cls)
+        self.s = OrWeights(C.cast(layers, C.POINTER(OrLayer)), fp(emb), fp(rmsf), fp(cls))
+
+
+class Decoder:
+    """or_decoder: the restated stories.Decoder (ane/stories/infer.go)."""
+
+    def __init__(self, cfg: OrConfig, weights, threads: int = 1):
+        self.lib = load()
+        self.cfg = cfg
+        self.w = _WeightsHolder(weights, cfg.n_layers)
+        self.h = self.lib.or_decoder_new(C.byref(cfg), C.byref(self.w.s), threads)
+        if not self.h:
+            raise RuntimeError("or_decoder_new failed")
+
+    def forward_one(self, token: int, pos: int) -> np.ndarray:
+        out = np.empty(self.cfg.vocab, np.float32)
+        if self.lib.or_forward_one(self.h, token, pos, fp(out)):
+            raise ValueError("or_forward_one: out of range")
+        return out
+
+    def tap(self, which: int, n: int) -> np.ndarray:
+        p = self.lib.or_decoder_tap(self.h, which)
+        return np.ctypeslib.as_array(p, shape=(n,)).copy()
+
+    def reset(self) -> None:
+        self.lib.or_decoder_reset(self.h)
+
+    def greedy_decode(self, prompt, max_new: int):
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
+        out = np.zeros(self.cfg.max_seq, np.int32)
+        margins = np.full(max(max_new, 64), np.nan, np.float32)
+        n_out = C.c_int32(0)
+        eos = C.c_int32(0)
+        pp = p.ctypes.data_as(_I32) if p.size else None
+        rc = self.lib.or_greedy_decode(self.h, pp, p.size, max_new, out.ctypes.data_as(_I32),
+                                       C.byref(n_out), C.byref(eos), fp(margins))
+        if rc:
+            raise ValueError("or_greedy_decode: invalid prompt")
+        return out[: n_out.value].copy(), bool(eos.value), margins
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.or_decoder_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def eval_logits_cf(cfg: OrConfig, weights, tokens, threads: int = 1) -> np.ndarray:
+    """or_eval_logits_cf: engine.go:804-842, channel-first [V, S]."""
+    t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint16))
+    holder = _WeightsHolder(weights, cfg.n_layers)
+    out = np.empty((cfg.vocab, t.size), np.float32)
+    load().or_eval_logits_cf(C.byref(cfg), C.byref(holder.s), t.ctypes.data_as(C.POINTER(C.c_uint16)),
+                             t.size, fp(out), threads)
+    return out
+
+
+def quantize_rows(src: np.ndarray):
+    a = np.ascontiguousarray(src, np.float32)
+    rows, cols = a.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    load().or_quantize_rows(fp(a), rows, cols, q.ctypes.data_as(C.POINTER(C.c_int8)), fp(s))
+    return q, s
+
+
+def quantize_tensor(src: np.ndarray):
+    a = np.ascontiguousarray(src, np.float32)
+    q = np.empty(a.shape, np.int8)
+    s = C.c_float(0)
+    load().or_quantize_tensor(fp(a.reshape(-1)), a.size, q.ctypes.data_as(C.POINTER(C.c_int8)), C.byref(s))
+    return q, np.float32(s.value)
+
+
+def dequantize_rows(q: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    qq = np.ascontiguousarray(q, np.int8)
+    rows, cols = qq.shape
+    out = np.empty((rows, cols), np.float32)
+    load().or_dequantize_rows(qq.ctypes.data_as(C.POINTER(C.c_int8)), fp(np.ascontiguousarray(scales, np.float32)),
+                              rows, cols, fp(out))
+    return out

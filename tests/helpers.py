@@ -1,0 +1,86 @@
+"""Helpers shared by the test modules: small model shapes, synthetic weights and an
+independent float64 forward written with torch library routines (rms_norm, silu,
+scaled_dot_product_attention, complex-number RoPE) used to pin the oracle."""
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+import stories_hip as sh
+
+
+def tiny_config(**kw):
+    """A small Llama shape that every kernel tiling supports."""
+    base = dict(dim=128, hidden=256, n_layers=2, n_heads=4, n_kv_heads=4, head_dim=32,
+                vocab=512, max_seq=64, rope_theta=10000.0, norm_eps=1e-5, qk_norm_eps=1e-6,
+                residual_scale=1.0, qk_norm=0, tied_embed=1, kv_dtype=sh.SH_KV_F32, max_batch=1)
+    base.update(kw)
+    return sh.make_config(**base)
+
+
+def tiny_gqa_config(**kw):
+    base = dict(n_heads=4, n_kv_heads=2, qk_norm=1, rope_theta=1e6, norm_eps=1e-6,
+                kv_dtype=sh.SH_KV_BF16)
+    base.update(kw)
+    return tiny_config(**base)
+
+
+def random_gains(w, seed):
+    """Replace unit norm gains with random positive ones (so a dropped gain is visible)."""
+    rng = np.random.default_rng(seed)
+    for lw in w.layers:
+        for k in ("rms_att", "rms_ffn", "q_norm", "k_norm"):
+            if k in lw:
+                lw[k] = (0.5 + rng.random(lw[k].shape)).astype(np.float32)
+    w.rms_final = (0.5 + rng.random(w.rms_final.shape)).astype(np.float32)
+    return w
+
+
+def torch_forward_f64(cfg, w, tokens, alpha=None):
+    """Full causal forward in float64 with torch library ops; returns logits [S, V].
+
+    Standard Llama block: pre-RMSNorm attention with interleaved-pair RoPE computed as a
+    complex rotation, optional per-head Q/K RMSNorm, grouped K/V heads, SwiGLU FFN,
+    residual x + alpha * branch, final RMSNorm and the classifier rows (tied: embedding)."""
+    d = torch.float64
+    alpha = cfg.residual_scale if alpha is None else alpha
+    S = len(tokens)
+    H, KVH, hd = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    E = torch.tensor(w.embed, dtype=d)
+    tok = torch.tensor(np.asarray(tokens, dtype=np.int64))
+    x = E[tok]  # [S, D]
+    pos = torch.arange(S, dtype=d)
+    inv_freq = torch.tensor([cfg.rope_theta ** (-(2.0 * i) / hd) for i in range(hd // 2)], dtype=d)
+    ang = pos[:, None] * inv_freq[None, :]
+    rot = torch.polar(torch.ones_like(ang), ang)  # [S, hd/2]
+
+    def rope(t):  # t [S, heads, hd], pairs (2i, 2i+1) as complex numbers
+        c = torch.view_as_complex(t.reshape(S, t.shape[1], hd // 2, 2).contiguous())
+        return torch.view_as_real(c * rot[:, None, :]).reshape(S, t.shape[1], hd)
+
+    for lw in w.layers:
+        T = lambda k: torch.tensor(lw[k], dtype=d)
+        xn = F.rms_norm(x, (cfg.dim,), T("rms_att"), eps=cfg.norm_eps)
+        q = (xn @ T("wq").T).reshape(S, H, hd)
+        k = (xn @ T("wk").T).reshape(S, KVH, hd)
+        v = (xn @ T("wv").T).reshape(S, KVH, hd)
+        if cfg.qk_norm:
+            q = F.rms_norm(q, (hd,), T("q_norm"), eps=cfg.qk_norm_eps)
+            k = F.rms_norm(k, (hd,), T("k_norm"), eps=cfg.qk_norm_eps)
+        q, k = rope(q), rope(k)
+        att = F.scaled_dot_product_attention(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1),
+                                             is_causal=True, enable_gqa=(H != KVH))
+        att = att.transpose(0, 1).reshape(S, H * hd)
+        x2 = x + alpha * (att @ T("wo").T)
+        x2n = F.rms_norm(x2, (cfg.dim,), T("rms_ffn"), eps=cfg.norm_eps)
+        g = F.silu(x2n @ T("w1").T) * (x2n @ T("w3").T)
+        x = x2 + alpha * (g @ T("w2").T)
+    xn = F.rms_norm(x, (cfg.dim,), torch.tensor(w.rms_final, dtype=d), eps=cfg.norm_eps)
+    cls = E if w.cls is None else torch.tensor(w.cls, dtype=d)
+    return (xn @ cls.T).numpy()
+
+
+def deepnet_alpha(n_layers):
+    """ane/storiesane/residual.go:9: 1/sqrt(2*NLayers), as float32."""
+    return float(np.float32(1.0 / math.sqrt(2.0 * n_layers)))

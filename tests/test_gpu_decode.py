@@ -1,0 +1,185 @@
+"""GPU parity of the batch-1 decode path against the CPU oracle, through the C ABI.
+
+Bars (stated per test): logits within max-abs 2e-2 of the fp32 oracle fed the same
+dtype-rounded weights, greedy token streams identical, int8 quantize/dequantize bit-exact.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import stories_hip as sh
+from helpers import random_gains, tiny_config, tiny_gqa_config
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 2e-2  # max-abs logits bar
+THREADS = max(1, min(16, os.cpu_count() or 1))
+
+
+def build(cfg, dtype, seed, std=0.02, gains_seed=None):
+    w = sh.synth_weights(cfg, seed=seed, std=std)
+    if gains_seed is not None:
+        w = random_gains(w, gains_seed)
+    m = sh.Model(cfg, dtype)
+    m.upload(w)
+    ref = oracle.Decoder(oracle.config_from(cfg, w8a8=(dtype == sh.SH_DTYPE_W8A8)),
+                         w.rounded(dtype), threads=THREADS)
+    return m, ref, w
+
+
+def check_steps(m, ref, tokens, tol=LOGIT_TOL):
+    worst = 0.0
+    for pos, tok in enumerate(tokens):
+        got, am = m.eval_next_logits(int(tok), pos)
+        want = ref.forward_one(int(tok), pos)
+        err = float(np.max(np.abs(got - want)))
+        worst = max(worst, err)
+        assert err <= tol, f"pos {pos}: max-abs {err}"
+        assert am == int(np.argmax(got))
+        assert am == int(np.argmax(want)), f"pos {pos}: argmax {am} vs {np.argmax(want)}"
+    print(f"max-abs logits error over {len(tokens)} positions: {worst:.3e}")
+    return worst
+
+
+@pytest.mark.parametrize("dtype,kv", [(sh.SH_DTYPE_F16, sh.SH_KV_F32), (sh.SH_DTYPE_F16, sh.SH_KV_F16),
+                                      (sh.SH_DTYPE_BF16, sh.SH_KV_BF16)])
+def test_decode_step_tiny(gpu, dtype, kv):
+    cfg = tiny_config(kv_dtype=kv)
+    m, ref, _ = build(cfg, dtype, seed=101, std=0.08, gains_seed=102)
+    toks = sh.synth_tokens(40, 103, cfg.vocab)
+    worst = check_steps(m, ref, toks)
+    assert worst < 1e-3
+    m.close()
+
+
+def test_decode_step_tiny_gqa_qknorm(gpu):
+    cfg = tiny_gqa_config()
+    m, ref, _ = build(cfg, sh.SH_DTYPE_BF16, seed=111, std=0.08, gains_seed=112)
+    toks = sh.synth_tokens(48, 113, cfg.vocab)
+    assert check_steps(m, ref, toks) < 1e-3
+    m.close()
+
+
+def test_decode_step_tiny_residual_scale(gpu):
+    cfg = tiny_config(residual_scale=0.5, n_layers=3)
+    m, ref, _ = build(cfg, sh.SH_DTYPE_F16, seed=121, std=0.08)
+    assert check_steps(m, ref, sh.synth_tokens(16, 122, cfg.vocab)) < 1e-3
+    m.close()
+
+
+def test_eval_next_logits_repeatable_and_cache_reset(gpu):
+    cfg = tiny_config()
+    m, ref, _ = build(cfg, sh.SH_DTYPE_F16, seed=131, std=0.08)
+    a, _ = m.eval_next_logits(5, 0)
+    b, _ = m.eval_next_logits(7, 1)
+    a2, _ = m.eval_next_logits(5, 0)
+    np.testing.assert_array_equal(a, a2)
+    m.reset_cache()
+    b2, _ = m.eval_next_logits(7, 1)  # position 0 of the cache is zero now
+    assert not np.array_equal(b, b2)
+    with pytest.raises(sh.ShError):
+        m.eval_next_logits(cfg.vocab, 0)
+    with pytest.raises(sh.ShError):
+        m.eval_next_logits(1, cfg.max_seq)
+    m.close()
+
+
+def test_greedy_decode_tiny_bookkeeping(gpu):
+    cfg = tiny_config(max_seq=24)
+    m, ref, w = build(cfg, sh.SH_DTYPE_F16, seed=141, std=0.08)
+    p = sh.synth_tokens(5, 142, cfg.vocab)
+    got, plen, eos = m.greedy_decode(p, 12)
+    want, weos, _ = ref.greedy_decode(p, 12)
+    assert plen == 5 and got.tolist() == want.tolist() and eos == weos
+    # maxSeq stop, over-long prompt, empty prompt, invalid id (infer.go:152-163, :179)
+    got, _, _ = m.greedy_decode(sh.synth_tokens(21, 143, cfg.vocab), 10)
+    want, _, _ = ref.greedy_decode(sh.synth_tokens(21, 143, cfg.vocab), 10)
+    assert len(got) == 24 and got.tolist() == want.tolist()
+    long = sh.synth_tokens(30, 144, cfg.vocab)
+    got, plen, _ = m.greedy_decode(long, 4)
+    assert plen == 24 and got.tolist() == long[-24:].tolist()
+    got, plen, _ = m.greedy_decode([], 3)
+    want, _, _ = ref.greedy_decode([], 3)
+    assert plen == 1 and got.tolist() == want.tolist()
+    with pytest.raises(sh.ShError):
+        m.greedy_decode([1, cfg.vocab + 3], 4)
+    m.close()
+
+
+def test_greedy_decode_stops_on_eos(gpu):
+    cfg = tiny_config(max_seq=32, tied_embed=0)
+    w = sh.synth_weights(cfg, seed=151, std=0.08)
+    for lw in w.layers:
+        for k in sh.LAYER_KEYS:
+            lw[k] = np.zeros_like(lw[k])
+    w.embed = np.full_like(w.embed, 0.01)
+    w.cls = np.zeros_like(w.embed)
+    w.cls[2] = 1.0  # every step's argmax is EOS=2
+    m = sh.Model(cfg, sh.SH_DTYPE_F16)
+    m.upload(w)
+    got, _, eos = m.greedy_decode([5, 9, 11], 10)
+    assert eos and got.tolist() == [5, 9, 11, 2]
+    m.close()
+
+
+def test_quantize_bit_exact(gpu):
+    rng = np.random.default_rng(161)
+    w = (rng.standard_normal((300, 257)) * 0.02).astype(np.float32)
+    w[7] = 0.0
+    w[9, :5] = [1.0, -1.0, 0.5, -0.25, 3.0]
+    s9 = np.float32(3.0) / np.float32(127.0)
+    w[11, :4] = np.array([127.0, 0.5, -0.5, 2.5], np.float32) * (np.float32(1.0) / np.float32(127.0))
+    q, s = sh.quantize_i8(w, per_row=True)
+    qo, so = oracle.quantize_rows(w)
+    np.testing.assert_array_equal(q, qo)
+    np.testing.assert_array_equal(s.view(np.uint32), so.view(np.uint32))
+    assert s[9] == s9 and s[7] == 1.0
+    qt, st = sh.quantize_i8(w, per_row=False)
+    qto, sto = oracle.quantize_tensor(w)
+    np.testing.assert_array_equal(qt, qto)
+    assert st[0] == sto
+    dq = sh.dequantize_i8(q, s, per_row=True)
+    np.testing.assert_array_equal(dq.view(np.uint32), oracle.dequantize_rows(qo, so).view(np.uint32))
+    # empty and all-zero tensors: scale 1 (ane_bridge.m:383)
+    qz, sz = sh.quantize_i8(np.zeros((4, 8), np.float32), per_row=False)
+    assert sz[0] == 1.0 and not qz.any()
+
+
+# ---- full-size configurations --------------------------------------------------------------
+
+def test_stories110m_fp16_greedy_128(gpu):
+    """Stories110M fp16 greedy decode: seed-0 N(0, 0.02) weights, 16-id prompt from seed 1,
+    128 new tokens; token stream identical to the oracle's, logits within 2e-2."""
+    cfg = sh.stories110m_config()
+    m, ref, _ = build(cfg, sh.SH_DTYPE_F16, seed=0)
+    prompt = sh.synth_tokens(16, 1, cfg.vocab)
+    got, plen, eos = m.greedy_decode(prompt, 128)
+    want, weos, margins = ref.greedy_decode(prompt, 128)
+    print(f"generated {len(got) - plen} tokens; smallest top-2 margin {np.nanmin(margins):.3e}")
+    assert got.tolist() == want.tolist() and eos == weos
+    assert len(got) == 16 + 128 or eos
+    # logits along the same stream
+    m.reset_cache()
+    ref.reset()
+    check_steps(m, ref, got[:40])
+    st = m.stats()
+    assert st["forwards"] == 0 or st["gpu_ms"] > 0
+    m.close()
+
+
+def test_qwen3_shaped_bf16_greedy(gpu):
+    """Qwen3-0.6B-shaped bf16 decode (GQA 16/8, hd 128, QK-norm, theta 1e6, tied, bf16 KV):
+    seed-3 weights, 32-id prompt from seed 3, 256 new tokens, identical to the oracle."""
+    cfg = sh.qwen3_06b_config()
+    m, ref, _ = build(cfg, sh.SH_DTYPE_BF16, seed=3)
+    prompt = sh.synth_tokens(32, 3, cfg.vocab)
+    got, plen, eos = m.greedy_decode(prompt, 256)
+    want, weos, margins = ref.greedy_decode(prompt, 256)
+    print(f"generated {len(got) - plen} tokens; smallest top-2 margin {np.nanmin(margins):.3e}")
+    assert got.tolist() == want.tolist() and eos == weos
+    m.reset_cache()
+    ref.reset()
+    check_steps(m, ref, got[:8])
+    m.close()
