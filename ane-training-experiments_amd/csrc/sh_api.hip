@@ -2,6 +2,7 @@
 // the device-resident decode loop (one captured HIP graph per token forward), and the
 // device quantizer entry points.
 #include <math.h>
+#include <stdio.h>
 #include <string.h>
 
 #include <algorithm>
@@ -96,6 +97,52 @@ hipError_t ensure_step_graph(sh_model *m) {
     if (e != hipSuccess) return e;
     m->step_ready = true;
     return hipSuccess;
+}
+
+// Runs n_forwards forwards from pos0 with the persistent kernel (epochs advance; the
+// hand-over buffers are cleared before the 32-bit epoch space runs out).
+bool run_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt) {
+    const uint64_t need = (uint64_t)n_forwards * (uint64_t)(m->cfg.n_layers + 1);
+    if ((uint64_t)m->epoch + need >= 0xF0000000ull) {
+        const sh_config &c = m->cfg;
+        struct {
+            uint64_t *p;
+            size_t n;
+        } ll[] = {{m->ll_qkv, (size_t)m->qkv_rows}, {m->ll_att, (size_t)m->qdim},
+                  {m->ll_x2, (size_t)c.dim},        {m->ll_gate, (size_t)c.hidden},
+                  {m->ll_x, (size_t)c.dim},         {m->ll_pv, 2 * (size_t)m->p_grid},
+                  {m->ll_pi, 2 * (size_t)m->p_grid}};
+        for (auto &b : ll)
+            if (!hip_ok(hipMemsetAsync(b.p, 0, 8 * b.n, m->stream), "clear hand-over")) return false;
+        m->epoch = 1;
+    }
+    if (!hip_ok(hipMemsetAsync(m->p_err, 0, 4, m->stream), "clear err")) return false;
+    return hip_ok(launch_persistent(m, pos0, n_forwards, n_prompt), "persistent decode launch");
+}
+
+bool check_persistent_err(sh_model *m) {
+    int err = 0;
+    if (!hip_ok(hipMemcpy(&err, m->p_err, 4, hipMemcpyDeviceToHost), "read err")) return false;
+    if (err) {
+        set_error("persistent decode: a hand-over wait exceeded its time bound");
+        return false;
+    }
+    return true;
+}
+
+// Enqueues n forwards at positions pos0.. (tokens[pos] feeds each; from n_prompt on the
+// argmax is appended): one persistent launch, or one graph replay per forward.
+bool launch_forwards(sh_model *m, int pos0, int n, int n_prompt) {
+    if (m->persistent) return run_persistent(m, pos0, n, n_prompt);
+    if (!hip_ok(ensure_step_graph(m), "capture decode step")) return false;
+    DecodeState st{};
+    st.pos = pos0;
+    st.n_prompt = n_prompt;
+    if (!hip_ok(hipMemcpyAsync(m->state, &st, sizeof(st), hipMemcpyHostToDevice, m->stream), "state"))
+        return false;
+    for (int f = 0; f < n; f++)
+        if (!hip_ok(hipGraphLaunch(m->step_exec, m->stream), "hipGraphLaunch")) return false;
+    return true;
 }
 
 bool ready(const sh_model *m) {
@@ -334,6 +381,53 @@ sh_model *sh_model_create(const sh_config *cfg, int32_t dtype) {
     if ((e = hipMemsetAsync(m->tokens, 0, 4 * (c.max_seq + 1), m->stream)) != hipSuccess)
         return fail("memset tokens", e);
     if ((e = hipStreamSynchronize(m->stream)) != hipSuccess) return fail("sync", e);
+
+    // persistent decode kernel: chosen when the shape has an instantiation and fits the CUs
+    {
+        std::string why;
+        hipError_t ge = hipSuccess;
+        if (!persistent_supported(m)) {
+            why = "shape/dtype has no persistent-kernel instantiation";
+        } else if ((ge = persistent_grid(m, &m->p_grid, &why)) == hipSuccess) {
+            m->persistent = true;
+        } else {
+            why += std::string("; grid: ") + hipGetErrorString(ge);
+        }
+        const std::string note =
+            m->persistent ? "persistent decode kernel, grid " + std::to_string(m->p_grid) + " (" + why + ")"
+                          : "per-stage kernels in a HIP graph (" + why + ")";
+        snprintf(m->path_note, sizeof(m->path_note), "%s", note.c_str());
+    }
+    if (m->persistent) {
+        const size_t lpb = persistent_layer_ptr_bytes(c.n_layers);
+        std::vector<uint8_t> lp(lpb);
+        persistent_fill_layer_ptrs(m, lp.data());
+        if ((e = hipMalloc(&m->p_layers, lpb)) != hipSuccess) return fail("hipMalloc layer ptrs", e);
+        if ((e = hipMemcpy(m->p_layers, lp.data(), lpb, hipMemcpyHostToDevice)) != hipSuccess)
+            return fail("upload layer ptrs", e);
+        struct {
+            uint64_t **p;
+            size_t n;
+        } ll[] = {{&m->ll_qkv, (size_t)m->qkv_rows}, {&m->ll_att, (size_t)m->qdim},
+                  {&m->ll_x2, D},                    {&m->ll_gate, F},
+                  {&m->ll_x, D},                     {&m->ll_pv, 2 * (size_t)m->p_grid},
+                  {&m->ll_pi, 2 * (size_t)m->p_grid}};
+        for (auto &b : ll) {
+            if ((e = hipMalloc(b.p, 8 * b.n)) != hipSuccess) return fail("hipMalloc hand-over", e);
+            if ((e = hipMemset(*b.p, 0, 8 * b.n)) != hipSuccess) return fail("clear hand-over", e);
+        }
+        if ((e = hipMalloc(&m->p_err, 64)) != hipSuccess) return fail("hipMalloc err", e);
+        if ((e = hipMemset(m->p_err, 0, 64)) != hipSuccess) return fail("clear err", e);
+        int rate_khz = 0;
+        if ((e = hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, m->device)) != hipSuccess)
+            return fail("wall clock rate", e);
+        m->spin_ticks = (long long)(rate_khz > 0 ? rate_khz : 100000) * 1000LL * 2;  // 2 s
+        m->epoch = 1;  // cleared words carry epoch 0
+        const size_t tb = 2 * (5 * (size_t)c.n_layers + 3) * sizeof(long long);
+        if ((e = hipMalloc(&m->trace_buf, tb)) != hipSuccess) return fail("hipMalloc trace", e);
+        if ((e = hipMemset(m->trace_buf, 0, tb)) != hipSuccess) return fail("clear trace", e);
+    }
+    m->trace_f = -1;
     return m;
 }
 
@@ -357,6 +451,16 @@ void sh_model_destroy(sh_model *m) {
     (void)hipFree(m->tokens);
     (void)hipFree(m->argmax_hist);
     (void)hipFree(m->state);
+    (void)hipFree(m->p_layers);
+    (void)hipFree(m->ll_qkv);
+    (void)hipFree(m->ll_att);
+    (void)hipFree(m->ll_x2);
+    (void)hipFree(m->ll_gate);
+    (void)hipFree(m->ll_x);
+    (void)hipFree(m->ll_pv);
+    (void)hipFree(m->ll_pi);
+    (void)hipFree(m->p_err);
+    (void)hipFree(m->trace_buf);
     if (m->ev0) (void)hipEventDestroy(m->ev0);
     if (m->ev1) (void)hipEventDestroy(m->ev1);
     if (m->stream) (void)hipStreamDestroy(m->stream);
@@ -489,13 +593,9 @@ int sh_decode_step(sh_model *m, int32_t token, int32_t pos, float *logits, int32
         return -1;
     }
     (void)hipSetDevice(m->device);
-    if (!hip_ok(ensure_step_graph(m), "capture decode step")) return -1;
-    DecodeState st{};
-    st.pos = pos;
-    st.n_prompt = c.max_seq + 1;  // never append: this call only evaluates
-    if (!hip_ok(hipMemcpyAsync(m->state, &st, sizeof(st), hipMemcpyHostToDevice, m->stream), "state") ||
-        !hip_ok(hipMemcpyAsync(m->tokens + pos, &token, 4, hipMemcpyHostToDevice, m->stream), "token") ||
-        !hip_ok(hipGraphLaunch(m->step_exec, m->stream), "hipGraphLaunch"))
+    // never append: this call only evaluates
+    if (!hip_ok(hipMemcpyAsync(m->tokens + pos, &token, 4, hipMemcpyHostToDevice, m->stream), "token") ||
+        !launch_forwards(m, pos, 1, c.max_seq + 1))
         return -1;
     if (logits &&
         !hip_ok(hipMemcpyAsync(logits, m->logits, 4 * (size_t)c.vocab, hipMemcpyDeviceToHost, m->stream),
@@ -503,7 +603,8 @@ int sh_decode_step(sh_model *m, int32_t token, int32_t pos, float *logits, int32
         return -1;
     int32_t am = 0;
     if (!hip_ok(hipMemcpyAsync(&am, m->argmax_hist + pos, 4, hipMemcpyDeviceToHost, m->stream), "argmax") ||
-        !hip_ok(hipStreamSynchronize(m->stream), "decode step"))
+        !hip_ok(hipStreamSynchronize(m->stream), "decode step") ||
+        (m->persistent && !check_persistent_err(m)))
         return -1;
     if (argmax_out) *argmax_out = am;
     return 0;
@@ -535,30 +636,25 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
             return -1;
         }
     (void)hipSetDevice(m->device);
-    if (!hip_ok(ensure_step_graph(m), "capture decode step")) return -1;
     // infer.go:179: generate while step < maxNew and len(tokens) < maxSeq
     const int generated = std::min(max_new, c.max_seq - n_prompt);
     const int forwards = n_prompt - 1 + generated;
-    DecodeState st{};
-    st.pos = 0;
-    st.n_prompt = n_prompt;
     const size_t kvb = kv_elem_bytes(c.kv_dtype) * m->kv_elems;
     if (!hip_ok(hipMemcpyAsync(m->tokens, prompt, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, m->stream),
-                "prompt") ||
-        !hip_ok(hipMemcpyAsync(m->state, &st, sizeof(st), hipMemcpyHostToDevice, m->stream), "state"))
+                "prompt"))
         return -1;
     // timed region: cache reset (infer.go:165-168) and every forward
     if (!hip_ok(hipEventRecord(m->ev0, m->stream), "event")) return -1;
     if (!hip_ok(hipMemsetAsync(m->kcache, 0, kvb, m->stream), "reset kcache") ||
         !hip_ok(hipMemsetAsync(m->vcache, 0, kvb, m->stream), "reset vcache"))
         return -1;
-    for (int f = 0; f < forwards; f++)
-        if (!hip_ok(hipGraphLaunch(m->step_exec, m->stream), "hipGraphLaunch")) return -1;
+    if (forwards > 0 && !launch_forwards(m, 0, forwards, n_prompt)) return -1;
     if (!hip_ok(hipEventRecord(m->ev1, m->stream), "event")) return -1;
     const int total = n_prompt + generated;
     if (!hip_ok(hipMemcpyAsync(out_tokens, m->tokens, 4 * (size_t)total, hipMemcpyDeviceToHost, m->stream),
                 "copy tokens") ||
-        !hip_ok(hipStreamSynchronize(m->stream), "greedy decode"))
+        !hip_ok(hipStreamSynchronize(m->stream), "greedy decode") ||
+        (m->persistent && !check_persistent_err(m)))
         return -1;
     // infer.go:190-193: stop after EOS
     int n = n_prompt;
@@ -580,6 +676,8 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
     m->last.forwards = forwards;
     m->last.tokens_out = n - n_prompt;
     m->last.bytes_per_forward_mean = forwards ? bytes / forwards : 0;
+    m->last.persistent = m->persistent ? 1 : 0;
+    m->last.grid = m->persistent ? m->p_grid : 0;
     return 0;
 }
 
@@ -591,6 +689,46 @@ int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *l
     }
     set_error("sh_prefill_logits: not available in this build");
     return -1;
+}
+
+int sh_trace_forward(sh_model *m, int32_t forward) {
+    if (!m || !m->persistent) {
+        set_error("sh_trace_forward: tracing needs the persistent decode kernel");
+        return -1;
+    }
+    m->trace_f = forward < 0 ? -1 : forward;
+    return 0;
+}
+
+int sh_trace_read(sh_model *m, int64_t *out, int32_t cap, int32_t *n_out, double *ticks_per_s) {
+    if (!m || !m->persistent || !out || !n_out || !ticks_per_s) {
+        set_error("sh_trace_read: bad arguments");
+        return -1;
+    }
+    const int n = 2 * (5 * m->cfg.n_layers + 3);
+    if (cap < n) {
+        set_error("sh_trace_read: capacity below 2*(5*n_layers+3)");
+        return -1;
+    }
+    (void)hipSetDevice(m->device);
+    if (!hip_ok(hipMemcpy(out, m->trace_buf, sizeof(int64_t) * n, hipMemcpyDeviceToHost), "read trace"))
+        return -1;
+    int rate_khz = 0;
+    if (!hip_ok(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, m->device), "clock rate"))
+        return -1;
+    *n_out = n;
+    *ticks_per_s = (double)rate_khz * 1000.0;
+    return 0;
+}
+
+size_t sh_model_describe(const sh_model *m, char *buf, size_t len) {
+    const std::string d = m ? std::string(m->path_note) : std::string("nil model");
+    if (buf && len) {
+        const size_t n = std::min(len - 1, d.size());
+        memcpy(buf, d.data(), n);
+        buf[n] = 0;
+    }
+    return d.size();
 }
 
 int sh_stats(const sh_model *m, sh_timing *out) {

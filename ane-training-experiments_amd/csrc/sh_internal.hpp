@@ -76,6 +76,18 @@ struct sh_model {
     bool step_ready;
     hipEvent_t ev0, ev1;
     sh_timing last;
+
+    // persistent decode kernel (sh_persistent.hip); unused when `persistent` is false
+    bool persistent;
+    int p_grid;
+    void *p_layers;         // device array of per-layer weight pointers
+    uint64_t *ll_qkv, *ll_att, *ll_x2, *ll_gate, *ll_x, *ll_pv, *ll_pi;
+    int *p_err;
+    uint32_t epoch;         // next unused hand-over epoch
+    long long spin_ticks;   // wait bound in constant-clock ticks
+    char path_note[512];    // which decode path runs, and why
+    long long *trace_buf;   // device: 2 x (5L + 3) stage timestamps
+    int trace_f;            // forward index traced in the next launch, -1 = off
 };
 
 namespace sh {
@@ -97,5 +109,11 @@ hipError_t launch_dequantize(const int8_t *q, const float *scales, int rows, int
 // state advance.
 hipError_t enqueue_decode_step(sh_model *m);
 int gemv_partials(const sh_model *m);
+
+bool persistent_supported(const sh_model *m);
+hipError_t persistent_grid(const sh_model *m, int *grid_out, std::string *why);
+hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt);
+size_t persistent_layer_ptr_bytes(int n_layers);
+void persistent_fill_layer_ptrs(const sh_model *m, void *host);
 
 }  // namespace sh

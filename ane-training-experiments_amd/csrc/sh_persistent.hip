@@ -1,0 +1,1012 @@
+// sh_persistent.hip — the whole greedy decode loop as one persistent, cooperatively
+// launched kernel for gfx950.
+//
+// Why: one token forward (ane/stories/infer.go:204-245) is ~5 dependent GEMV-sized stages
+// per layer. Launched as separate kernels, even inside a HIP graph, each stage pays ~1.6 us
+// of dispatch; a grid-wide atomic barrier costs more. Here every workgroup stays resident
+// for all forwards and the stages hand data over through "LL" words: each element of an
+// inter-stage vector is one 64-bit word (float bits | 32-bit epoch) written with a single
+// agent-scope store, so a consumer that reads the expected epoch also holds the value; no
+// fences or counters are needed. Epochs are unique per (forward, layer), so buffers are
+// never cleared.
+//
+// Stages of one forward (vw = wave index spread over the grid):
+//   per layer l (epoch e):
+//     qkv   rows of [Wq;Wk;Wv] . rmsnorm(x)          -> ll_qkv          (all workgroups)
+//     attn  per kv head g: QK-norm, RoPE, KV append, softmax, P.V for its q heads
+//                                                    -> ll_att          (workgroups 0..KVH-1)
+//     wo    x2 = x + alpha * Wo . att                -> ll_x2
+//     w13   gate = silu(W1 . n) * (W3 . n), n = rmsnorm(x2) -> ll_gate
+//     w2    x = x2 + alpha * W2 . gate               -> ll_x
+//   classifier: logits = Cls . rmsnorm(x), per-workgroup (max, first index) -> ll_pv/ll_pi
+//   argmax: every workgroup reduces the partials itself and knows the next token.
+// Layer 0 reads x straight from the embedding row, so it needs no hand-over.
+//
+// Weight tiles of a stage are loaded into registers before the stage's input is polled,
+// so HBM streaming overlaps the hand-over latency. Each kv head's cache rows are written
+// and read by the same workgroup (same CU), so the cache needs no cross-CU coherence.
+// A consumer polls only when it has outputs to produce in that stage; every produced
+// element is consumed downstream, so no buffer is overwritten before all its pollers read
+// it. Every wait is bounded (spin_limit ticks of the constant-rate clock): on expiry the
+// kernel sets *err and all workgroups exit.
+#include <hip/hip_fp16.h>
+#include <math.h>
+
+#include <algorithm>
+#include <string>
+
+#include "sh_internal.hpp"
+
+namespace sh {
+namespace {
+
+// Address-space-qualified pointers: weights and caches are global memory, staged rows are
+// LDS. Without the qualifier, pointers fetched from memory compile to FLAT accesses.
+#define SH_GLOBAL __attribute__((address_space(1)))
+#define SH_LDS __attribute__((address_space(3)))
+
+// Plain clang vectors: loadable through address-space-qualified pointers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPB = 512;           // threads per workgroup
+constexpr int kPW = kPB / 64;      // waves per workgroup
+constexpr int kXs = 4096;          // staged input vector
+constexpr int kScores = 4096;      // attention scores: group * max_seq
+constexpr int kMaxGroup = 2;       // q heads per kv head
+constexpr int kKvStage = 96 * 1024; // LDS bytes for one kv head's cached K and V rows
+
+struct LayerPtrs {
+    const uint16_t *wqkv, *wo, *w13, *w2;
+    const float *rms_att, *rms_ffn, *q_norm, *k_norm;
+};
+
+struct PParams {
+    int D, F, H, KVH, hd, V, max_seq, L, qdim, kvdim, qkv_rows;
+    float alpha, inv_sqrt_hd;
+    double eps, qk_eps;
+    int qk_norm;
+    const LayerPtrs *layers;
+    const uint16_t *embed, *cls;
+    const float *rms_final;
+    void *kcache, *vcache;
+    const float *rope_cos, *rope_sin;
+    uint64_t *ll_qkv, *ll_att, *ll_x2, *ll_gate, *ll_x, *ll_pv, *ll_pi;
+    float *logits;
+    int32_t *tokens, *hist;
+    int pos0, n_forwards, n_prompt;
+    uint32_t epoch0;
+    int *err;
+    long long spin_limit;
+    long long *trace;  // stage timestamps of forward trace_f (workgroups 0 and grid-1)
+    int trace_f;
+};
+
+__device__ __forceinline__ float h2f(uint32_t b) {
+    return __half2float(__ushort_as_half((unsigned short)b));
+}
+template <int WT>
+__device__ __forceinline__ float w2f(uint32_t b) {
+    if constexpr (WT == SH_DTYPE_F16) return h2f(b);
+    else return __uint_as_float(b << 16);
+}
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+template <int WT>
+__device__ __forceinline__ void unpack8(const u32x4 &v, float *f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if constexpr (WT == SH_DTYPE_F16) {
+            f[2 * i] = h2f(w[i] & 0xffffu);
+            f[2 * i + 1] = h2f(w[i] >> 16);
+        } else {
+            f[2 * i] = __uint_as_float(w[i] << 16);
+            f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+}
+
+template <int KVT>
+__device__ __forceinline__ float kv_ld(const void *b, size_t i) {
+    if constexpr (KVT == SH_KV_F32) return ((const float *)b)[i];
+    else if constexpr (KVT == SH_KV_F16) return h2f(((const uint16_t *)b)[i]);
+    else return __uint_as_float((uint32_t)((const uint16_t *)b)[i] << 16);
+}
+template <int KVT>
+__device__ __forceinline__ float kv_rnd(float v) {
+    if constexpr (KVT == SH_KV_F32) return v;
+    else if constexpr (KVT == SH_KV_F16) return h2f(f2h(v));
+    else return __uint_as_float((uint32_t)f2bf(v) << 16);
+}
+template <int KVT>
+__device__ __forceinline__ void kv_st(void *b, size_t i, float v) {
+    if constexpr (KVT == SH_KV_F32) ((float *)b)[i] = v;
+    else if constexpr (KVT == SH_KV_F16) ((uint16_t *)b)[i] = f2h(v);
+    else ((uint16_t *)b)[i] = f2bf(v);
+}
+
+// Eight consecutive cache elements starting at a multiple of 8.
+template <int KVT>
+__device__ __forceinline__ void kv_ld8(const void *b, size_t i, float *out) {
+    if constexpr (KVT == SH_KV_F32) {
+        const float4 a = ((const float4 *)b)[i / 4], c = ((const float4 *)b)[i / 4 + 1];
+        out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+        out[4] = c.x; out[5] = c.y; out[6] = c.z; out[7] = c.w;
+    } else {
+        const uint4 v = ((const uint4 *)b)[i / 8];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if constexpr (KVT == SH_KV_F16) {
+                out[2 * k] = h2f(w[k] & 0xffffu);
+                out[2 * k + 1] = h2f(w[k] >> 16);
+            } else {
+                out[2 * k] = __uint_as_float(w[k] << 16);
+                out[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+            }
+        }
+    }
+}
+
+// Workgroup barrier that orders LDS traffic only. __syncthreads() also waits for every
+// outstanding global store of the wave (loads and stores share one counter on this
+// architecture), which would stall each barrier behind the write-through acknowledgement of
+// the hand-over stores. Global data is never exchanged between waves of one workgroup
+// inside a forward, so LDS ordering is all the barriers here need.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Workgroup-wide AND of a per-thread flag, over LDS (two barriers, so the flag array can be
+// reused by the next call).
+__device__ __forceinline__ bool block_and(bool ok) {
+    __shared__ int flags[kPW];
+    const bool w = __all(ok);
+    if ((threadIdx.x & 63) == 0) flags[threadIdx.x >> 6] = w;
+    lds_barrier();
+    bool r = true;
+#pragma unroll
+    for (int i = 0; i < kPW; i++) r = r && flags[i];
+    lds_barrier();
+    return r;
+}
+
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = N / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ double block_sum_d(double v, double *red) {
+    v = wave_sum_d(v);
+    lds_barrier();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    lds_barrier();
+    double s = 0;
+    for (int w = 0; w < kPW; w++) s += red[w];
+    return s;
+}
+__device__ __forceinline__ float block_max_f(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    lds_barrier();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    lds_barrier();
+    float s = red[0];
+    for (int w = 1; w < kPW; w++) s = fmaxf(s, red[w]);
+    return s;
+}
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// ---- LL hand-over ---------------------------------------------------------------------------
+__device__ __forceinline__ void ll_put(uint64_t *p, float v, uint32_t e) {
+    __hip_atomic_store(p, ((uint64_t)e << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_put_u(uint64_t *p, uint32_t v, uint32_t e) {
+    __hip_atomic_store(p, ((uint64_t)e << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ll_get(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool aborted(const PParams &p) {
+    return __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+
+// Spin until *src carries epoch e; false on timeout or abort (then *err is set). Kept out
+// of line: it only runs when a value is not there yet, and one copy keeps the kernel small
+// enough for the instruction cache.
+__device__ __noinline__ bool ll_spin(const uint64_t *src, uint32_t e, uint64_t *v, int *err,
+                                     long long limit) {
+    const long long t0 = wall_clock64();
+    while (true) {
+        __builtin_amdgcn_s_sleep(1);
+        const uint64_t w = ll_get(src);
+        if ((uint32_t)(w >> 32) == e) {
+            *v = w;
+            return true;
+        }
+        if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return false;
+        if (wall_clock64() - t0 > limit) {
+            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+    }
+}
+
+__device__ __forceinline__ bool ll_wait_word(const uint64_t *src, uint32_t e, uint64_t &v, const PParams &p) {
+    if ((uint32_t)(v >> 32) == e) return true;
+    return ll_spin(src, e, &v, p.err, p.spin_limit);
+}
+
+// Block-wide wait: once every word j < n (located by map.src(j)) carries epoch e, its value
+// is in *map.dst(j). Each thread requests all of its K words at once and, while any is
+// missing, re-requests the missing ones together, so a poll costs one memory round trip
+// whatever the number of words. Returns false for the whole block on timeout/abort.
+template <int K, typename Map>
+__device__ __forceinline__ bool ll_wait_batch(int n, uint32_t e, const PParams &p, const Map &map) {
+    uint64_t v[K];
+    unsigned need = 0;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int j = threadIdx.x + k * kPB;
+        if (j < n) {
+            v[k] = ll_get(map.src(j));
+            need |= 1u << k;
+        }
+    }
+    bool ok = true;
+    long long t0 = 0;
+    while (true) {
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            if ((need >> k) & 1u) {
+                if ((uint32_t)(v[k] >> 32) == e) {
+                    *map.dst(threadIdx.x + k * kPB) = __uint_as_float((uint32_t)v[k]);
+                    need &= ~(1u << k);
+                }
+            }
+        }
+        if (!need) break;
+        const long long now = wall_clock64();
+        if (!t0) {
+            t0 = now;
+        } else if (now - t0 > p.spin_limit) {
+            __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = false;
+            break;
+        }
+        if (aborted(p)) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < K; k++)
+            if ((need >> k) & 1u) v[k] = ll_get(map.src(threadIdx.x + k * kPB));
+    }
+    return block_and(ok);
+}
+
+struct VecMap {
+    const uint64_t *s;
+    float *d;
+    __device__ const uint64_t *src(int j) const { return s + j; }
+    __device__ float *dst(int j) const { return d + j; }
+};
+
+// Block-wide: dst[i] = value of src[i] once every word of src[0, n) carries epoch e;
+// n <= K * kPB.
+template <int K>
+__device__ __forceinline__ bool ll_wait_vec(const uint64_t *src, int n, uint32_t e, float *dst, const PParams &p) {
+    return ll_wait_batch<K>(n, e, p, VecMap{src, dst});
+}
+
+// Stage this stage's input in LDS: from an LL vector (epoch e) or, when emb_row is given,
+// from an embedding row; then rmsNormVec (infer.go:301-311) with `gain` if non-null.
+template <int WT, int COLS>
+__device__ __forceinline__ bool stage_input(float *xs, int n, const uint64_t *ll, uint32_t e,
+                            const uint16_t *emb_row, const float *gain, double eps, double *red,
+                            const PParams &p) {
+    if (emb_row) {
+        for (int i = threadIdx.x; i < n; i += kPB) xs[i] = w2f<WT>(emb_row[i]);
+        lds_barrier();
+    } else if (!ll_wait_vec<(COLS + kPB - 1) / kPB>(ll, n, e, xs, p)) {
+        return false;
+    }
+    if (gain) {
+        double ss = 0;
+        for (int i = threadIdx.x; i < n; i += kPB) ss += (double)xs[i] * (double)xs[i];
+        const double tot = block_sum_d(ss, red);
+        const float rrms = (float)(1.0 / sqrt(tot / (double)n + eps));
+        for (int i = threadIdx.x; i < n; i += kPB) xs[i] = xs[i] * rrms * gain[i];
+        lds_barrier();
+    }
+    return true;
+}
+
+enum { E_STORE = 0, E_RESID = 1, E_GATE = 2, E_CLS = 3 };
+
+struct StageIO {
+    const uint64_t *in_ll;      // input vector (LL) or NULL when emb_row is used
+    const uint16_t *emb_row;
+    const float *gain;
+    uint64_t *out_ll;           // LL output (E_STORE / E_RESID / E_GATE)
+    const uint64_t *res_ll;     // E_RESID residual from an LL vector
+    const uint16_t *res_emb;    // E_RESID residual from the embedding row (layer 0)
+    uint32_t e_in, e_res, e_out;
+};
+
+// One GEMV stage over W [rows, cols]. Row groups of G = 64/LPR rows are dealt to waves
+// vw = wave * gridDim.x + blockIdx.x. Weight tiles of the first U groups are loaded before
+// the input is polled. Returns false on timeout/abort. For E_CLS, *best_v/*best_i receive
+// this wave's (max, first index).
+template <int LPR, int CPL, int WT, int U>
+__device__ __forceinline__ bool gemv_stage(const PParams &p, const uint16_t *__restrict__ W, int rows, int cols,
+                           int epi, const StageIO &io, float *xs, double *red, float &best_v,
+                           int &best_i) {
+    constexpr int G = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, grp = lane / LPR;
+    const int NW = gridDim.x * kPW;
+    const int vw = wave * gridDim.x + blockIdx.x;
+    const int ngroups = (rows + G - 1) / G;
+    // does this workgroup own any row group? (waves of one workgroup are vw, vw+grid, ...)
+    const bool wg_has_work = (int)blockIdx.x < ngroups;
+    if (!wg_has_work) return true;
+
+    u32x4 w[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int row = (vw + u * NW) * G + grp;
+        if (row < rows) {
+            const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(W + (size_t)row * cols);
+#pragma unroll
+            for (int j = 0; j < CPL; j++) w[u][j] = src[sub + j * LPR];
+        }
+    }
+    if (!stage_input<WT, LPR * CPL * 8>(xs, cols, io.in_ll, io.e_in, io.emb_row, io.gain, p.eps, red, p))
+        return false;
+    float xr[CPL * 8];
+#pragma unroll
+    for (int j = 0; j < CPL; j++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) xr[j * 8 + e] = xs[(sub + j * LPR) * 8 + e];
+
+    bool ok = true;
+    for (int g0 = vw; g0 < ngroups; g0 += U * NW) {
+        float acc[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            acc[u] = 0.f;
+            const int row = (g0 + u * NW) * G + grp;
+            if (row < rows) {
+#pragma unroll
+                for (int j = 0; j < CPL; j++) {
+                    float f[8];
+                    unpack8<WT>(w[u][j], f);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[u] = fmaf(f[e], xr[j * 8 + e], acc[u]);
+                }
+            }
+        }
+        // next tiles are issued before this batch's reductions and stores
+        const int gn = g0 + U * NW;
+        if (gn < ngroups) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int row = (gn + u * NW) * G + grp;
+                if (row < rows) {
+                    const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(W + (size_t)row * cols);
+#pragma unroll
+                    for (int j = 0; j < CPL; j++) w[u][j] = src[sub + j * LPR];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int row = (g0 + u * NW) * G + grp;
+            const float a = group_sum<LPR>(acc[u]);
+            if (epi == E_GATE) {
+                const float h3 = __shfl_down(a, LPR, 64);
+                if (sub == 0 && (grp & 1) == 0 && row < rows) {
+                    const float s = a / (1.0f + (float)exp(-(double)a));   // infer.go:324-326
+                    ll_put(io.out_ll + (row >> 1), s * h3, io.e_out);
+                }
+            } else if (sub == 0 && row < rows) {
+                if (epi == E_STORE) {
+                    ll_put(io.out_ll + row, a, io.e_out);
+                } else if (epi == E_RESID) {
+                    float r;
+                    if (io.res_emb) {
+                        r = w2f<WT>(io.res_emb[row]);
+                    } else {
+                        uint64_t v = ll_get(io.res_ll + row);
+                        ok = ok && ll_wait_word(io.res_ll + row, io.e_res, v, p);
+                        r = __uint_as_float((uint32_t)v);
+                    }
+                    if (ok) ll_put(io.out_ll + row, r + p.alpha * a, io.e_out);
+                } else {  // E_CLS
+                    p.logits[row] = a;
+                    if (a > best_v) {
+                        best_v = a;
+                        best_i = row;
+                    }
+                }
+            }
+        }
+    }
+    // xs is rewritten by the next stage: every wave must be done reading it
+    return block_and(ok);
+}
+
+// Three LL segments (q heads, k, v of one kv head) waited for as one vector.
+struct QkvMap {
+    const uint64_t *q, *k, *v;
+    float *dq, *dk, *dv;
+    int nq, hd;
+    __device__ const uint64_t *src(int j) const {
+        return j < nq ? q + j : (j < nq + hd ? k + (j - nq) : v + (j - nq - hd));
+    }
+    __device__ float *dst(int j) const {
+        return j < nq ? dq + j : (j < nq + hd ? dk + (j - nq) : dv + (j - nq - hd));
+    }
+};
+
+// Asynchronous copy of cached rows [0, rows) of one kv head into LDS (global_load_lds:
+// each lane moves 16 bytes; one wave instruction fills 1 KB of LDS). Row t of the head
+// starts at element base + t*stride; rows are RB bytes long and land contiguously.
+template <int RB>
+__device__ __forceinline__ void kv_rows_to_lds(const uint8_t *cache, size_t base_bytes, size_t stride_bytes,
+                                               int rows, uint8_t *lds) {
+    constexpr int LPRW = RB / 16;            // lanes per row
+    constexpr int RPI = 64 / LPRW;           // rows per wave instruction
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r_in = lane / LPRW, c_in = (lane % LPRW) * 16;
+    for (int r0 = wave * RPI; r0 < rows; r0 += kPW * RPI) {
+        const int r = r0 + r_in < rows ? r0 + r_in : r0;   // a spare lane re-reads a valid row
+        const uint8_t *g = cache + base_bytes + (size_t)r * stride_bytes + c_in;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
+                                         (__attribute__((address_space(3))) void *)(lds + (size_t)r0 * RB),
+                                         16, 0, 0);
+    }
+}
+
+// Rows of one kv head's cache that live in LDS during its attention stage.
+template <int KVT, int HD>
+struct KvStage {
+    static constexpr int EB = KVT == SH_KV_F32 ? 4 : 2;   // bytes per cache element
+    static constexpr int RB = HD * EB;                     // bytes per row
+    static constexpr int ROWS = kKvStage / (2 * RB);       // K rows, then as many V rows
+};
+
+// Starts the asynchronous copy of kv head g's cached rows [0, min(pos, ROWS)) of layer l
+// into LDS. Issued at the start of the layer, so it overlaps the qkv stage.
+template <int KVT, int HD>
+__device__ __forceinline__ void attn_prefetch(const PParams &p, int l, int g, int pos, uint8_t *kvlds) {
+    using S = KvStage<KVT, HD>;
+    const size_t lbase = (size_t)l * p.max_seq * p.kvdim + (size_t)g * HD;
+    const int nst = pos < S::ROWS ? pos : S::ROWS;
+    kv_rows_to_lds<S::RB>((const uint8_t *)p.kcache, lbase * S::EB, (size_t)p.kvdim * S::EB, nst, kvlds);
+    kv_rows_to_lds<S::RB>((const uint8_t *)p.vcache, lbase * S::EB, (size_t)p.kvdim * S::EB, nst,
+                          kvlds + (size_t)S::ROWS * S::RB);
+}
+
+template <int KVT>
+__device__ __forceinline__ float kv_get(const SH_LDS uint8_t *row, int e) {
+    if constexpr (KVT == SH_KV_F32) return ((const SH_LDS float *)row)[e];
+    else if constexpr (KVT == SH_KV_F16) return h2f(((const SH_LDS uint16_t *)row)[e]);
+    else return __uint_as_float((uint32_t)((const SH_LDS uint16_t *)row)[e] << 16);
+}
+template <int KVT>
+__device__ __forceinline__ void kv_put(SH_LDS uint8_t *row, int e, float v) {
+    if constexpr (KVT == SH_KV_F32) ((SH_LDS float *)row)[e] = v;
+    else if constexpr (KVT == SH_KV_F16) ((SH_LDS uint16_t *)row)[e] = f2h(v);
+    else ((SH_LDS uint16_t *)row)[e] = f2bf(v);
+}
+// 16 bytes of a cache row as floats: 4 (fp32) or 8 (fp16 / bf16) elements.
+template <int KVT>
+__device__ __forceinline__ void kv_unpack16(const u32x4 &v, float *f) {
+    if constexpr (KVT == SH_KV_F32) {
+        f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+        f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+    } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if constexpr (KVT == SH_KV_F16) {
+                f[2 * k] = h2f(w[k] & 0xffffu);
+                f[2 * k + 1] = h2f(w[k] >> 16);
+            } else {
+                f[2 * k] = __uint_as_float(w[k] << 16);
+                f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+            }
+        }
+    }
+}
+
+// Attention for kv head g (one workgroup) and its `group` query heads (infer.go:273-299).
+// q, k and v arrive through one batched poll; the cached rows were copied into LDS by
+// attn_prefetch, rows beyond the LDS capacity are read from the cache. Scores: one thread
+// per position, walking the head in an order rotated by the position so the LDS reads of a
+// wave fall in distinct banks. Softmax: one wave per head. P.V: one thread per (dim,
+// position group), partial sums combined through LDS.
+template <int KVT, int HD>
+__device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
+                           float *ks, float *vs, float *sc, float *part, uint8_t *kvlds,
+                           double *red, float *redf) {
+    using S = KvStage<KVT, HD>;
+    constexpr int hd = HD, ngr = kPB / HD;
+    const int group = p.H / p.KVH, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const LayerPtrs &Lp = p.layers[l];
+    const size_t lbase = (size_t)l * p.max_seq * p.kvdim + (size_t)g * hd;
+    SH_LDS uint8_t *kst = (SH_LDS uint8_t *)kvlds;
+    SH_LDS uint8_t *vst = kst + (size_t)S::ROWS * S::RB;
+    const SH_LDS float *qsl = (const SH_LDS float *)qs;
+
+    QkvMap qm{p.ll_qkv + (size_t)g * group * hd, p.ll_qkv + p.qdim + (size_t)g * hd,
+              p.ll_qkv + p.qdim + p.kvdim + (size_t)g * hd, qs, ks, vs, group * hd, hd};
+    if (!ll_wait_batch<(kMaxGroup + 2) * 256 / kPB>(group * hd + 2 * hd, e, p, qm)) return false;
+    if (p.qk_norm) {
+        // per-head RMSNorm: wave w < group normalises q head w, wave `group` normalises k
+        if (wave <= group) {
+            float *v = wave < group ? qs + wave * hd : ks;
+            const float *gn = wave < group ? Lp.q_norm : Lp.k_norm;
+            double ss = 0;
+            for (int i = lane; i < hd; i += 64) ss += (double)v[i] * (double)v[i];
+            ss = wave_sum_d(ss);
+            const float rr = (float)(1.0 / sqrt(ss / (double)hd + p.qk_eps));
+            for (int i = lane; i < hd; i += 64) v[i] = v[i] * rr * gn[i];
+        }
+        lds_barrier();
+    }
+    // infer.go:247-265 RoPE, interleaved pairs, on every q head and on k
+    const int half = hd / 2;
+    for (int i = tid; i < (group + 1) * half; i += kPB) {
+        const int h = i / half, pi = i % half;
+        float *v = h < group ? qs + h * hd : ks;
+        const float c = p.rope_cos[pos * half + pi], s = p.rope_sin[pos * half + pi];
+        const float ev = v[2 * pi], ov = v[2 * pi + 1];
+        v[2 * pi] = ev * c - ov * s;
+        v[2 * pi + 1] = ev * s + ov * c;
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // the LDS copies of the cached rows have landed
+    lds_barrier();
+    // infer.go:267-271 storeKV in the cache's storage type; row pos also joins the LDS rows
+    for (int i = tid; i < hd; i += kPB) {
+        ks[i] = kv_rnd<KVT>(ks[i]);
+        vs[i] = kv_rnd<KVT>(vs[i]);
+        kv_st<KVT>(p.kcache, lbase + (size_t)pos * p.kvdim + i, ks[i]);
+        kv_st<KVT>(p.vcache, lbase + (size_t)pos * p.kvdim + i, vs[i]);
+        if (pos < S::ROWS) {
+            kv_put<KVT>(kst + (size_t)pos * S::RB, i, ks[i]);
+            kv_put<KVT>(vst + (size_t)pos * S::RB, i, vs[i]);
+        }
+    }
+    lds_barrier();
+    // scores (infer.go:280-288): 16-byte chunks of the row, visited from a chunk index
+    // rotated by t so the lanes of a wave read distinct LDS banks
+    for (int t = tid; t <= pos; t += kPB) {
+        float d[kMaxGroup];
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++) d[h] = 0.f;
+        if (t < S::ROWS) {
+            constexpr int NCH = S::RB / 16, EPC = 16 / S::EB;
+            const SH_LDS u32x4 *row = (const SH_LDS u32x4 *)(kst + (size_t)t * S::RB);
+#pragma unroll 4
+            for (int c0 = 0; c0 < NCH; c0++) {
+                const int c = (c0 + t) & (NCH - 1);
+                float kf[EPC];
+                const u32x4 kv4 = row[c];
+                kv_unpack16<KVT>(kv4, kf);
+#pragma unroll
+                for (int h = 0; h < kMaxGroup; h++) {
+                    if (h >= group) continue;
+                    const SH_LDS f32x4 *q4 = (const SH_LDS f32x4 *)(qsl + h * hd + c * EPC);
+#pragma unroll
+                    for (int e4 = 0; e4 < EPC / 4; e4++) {
+                        const f32x4 qv = q4[e4];
+                        d[h] = fmaf(qv.x, kf[4 * e4 + 0], d[h]);
+                        d[h] = fmaf(qv.y, kf[4 * e4 + 1], d[h]);
+                        d[h] = fmaf(qv.z, kf[4 * e4 + 2], d[h]);
+                        d[h] = fmaf(qv.w, kf[4 * e4 + 3], d[h]);
+                    }
+                }
+            }
+        } else {
+            const size_t rb = lbase + (size_t)t * p.kvdim;
+#pragma unroll 8
+            for (int k = 0; k < hd; k++) {
+                const float kv = t == pos ? ks[k] : kv_ld<KVT>(p.kcache, rb + k);
+#pragma unroll
+                for (int h = 0; h < kMaxGroup; h++)
+                    if (h < group) d[h] = fmaf(qs[h * hd + k], kv, d[h]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++)
+            if (h < group) sc[h * p.max_seq + t] = d[h] * p.inv_sqrt_hd;
+    }
+    lds_barrier();
+    // infer.go:328-345 softmaxPrefix: wave h handles head h; sc then holds probabilities
+    if (wave < group) {
+        float *s = sc + wave * p.max_seq;
+        float mx = -INFINITY;
+        for (int t = lane; t <= pos; t += 64) mx = fmaxf(mx, s[t]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        double sum = 0;
+        for (int t = lane; t <= pos; t += 64) {
+            const float ev = (float)exp((double)(s[t] - mx));
+            s[t] = ev;
+            sum += (double)ev;
+        }
+        sum = wave_sum_d(sum);
+        const float inv = (float)(1.0 / sum);
+        for (int t = lane; t <= pos; t += 64) s[t] = s[t] * inv;
+    }
+    lds_barrier();
+    // P.V (infer.go:290-297)
+    const int vi = tid % hd, tg = tid / hd;
+    float acc[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++) acc[h] = 0.f;
+    const int tl = pos < S::ROWS ? pos : S::ROWS - 1;   // last position held in LDS
+#pragma unroll 4
+    for (int t = tg; t <= tl; t += ngr) {
+        const float vv = kv_get<KVT>(vst + (size_t)t * S::RB, vi);
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++)
+            if (h < group) acc[h] = fmaf(sc[h * p.max_seq + t], vv, acc[h]);
+    }
+    for (int t = tl + 1 + ((tg - (tl + 1) % ngr + ngr) % ngr); t <= pos; t += ngr) {
+        const float vv = t == pos ? vs[vi] : kv_ld<KVT>(p.vcache, lbase + (size_t)t * p.kvdim + vi);
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++)
+            if (h < group) acc[h] = fmaf(sc[h * p.max_seq + t], vv, acc[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++)
+        if (h < group) part[(h * ngr + tg) * hd + vi] = acc[h];
+    lds_barrier();
+    for (int k = tid; k < group * hd; k += kPB) {
+        const int h = k / hd, ii = k % hd;
+        float sum = 0.f;
+        for (int r = 0; r < ngr; r++) sum += part[(h * ngr + r) * hd + ii];
+        ll_put(p.ll_att + (size_t)(g * group + h) * hd + ii, sum, e);
+    }
+    lds_barrier();
+    return true;
+}
+
+template <int WT, int KVT, int HD, int LD, int CD, int LQ, int CQ, int LF, int CF>
+__global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
+    __shared__ float xs[kXs];
+    __shared__ __attribute__((aligned(16))) float qs[kMaxGroup * 256];
+    __shared__ float ks[256], vs[256];
+    __shared__ float sc[kScores];
+    __shared__ float part[kPW * kMaxGroup * 256];
+    __shared__ __attribute__((aligned(16))) uint8_t kvlds[kKvStage];
+    __shared__ double red[kPW];
+    __shared__ float redf[kPW];
+    __shared__ ArgmaxPartial cand[kPW];
+    __shared__ int next_tok;
+
+    const int L = p.L;
+    const int n_stamps = 5 * L + 3;
+    int tok_next = 0;
+    for (int f = 0; f < p.n_forwards; f++) {
+        const int pos = p.pos0 + f;
+        const bool tracing = p.trace && f == p.trace_f && threadIdx.x == 0 &&
+                             (blockIdx.x == 0 || blockIdx.x == gridDim.x - 1);
+        long long *tr = p.trace + (blockIdx.x == 0 ? 0 : n_stamps);
+        int ts = 0;
+        auto stamp = [&]() {
+            if (tracing) tr[ts] = wall_clock64();
+            ts++;
+        };
+        stamp();
+        const int tok = pos < p.n_prompt ? p.tokens[pos] : tok_next;
+        const bool tok_ok = tok >= 0 && tok < p.V;
+        const uint16_t *emb_row = p.embed + (size_t)(tok_ok ? tok : 0) * p.D;
+        const uint32_t base = p.epoch0 + (uint32_t)f * (uint32_t)(L + 1);
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int l = 0; l < L; l++) {
+            const uint32_t e = base + (uint32_t)l + 1;
+            const LayerPtrs &Lp = p.layers[l];
+            if ((int)blockIdx.x < p.KVH) attn_prefetch<KVT, HD>(p, l, blockIdx.x, pos, kvlds);
+            StageIO io{};
+            // qkv
+            io.in_ll = l ? p.ll_x : nullptr;
+            io.emb_row = l ? nullptr : emb_row;
+            io.gain = Lp.rms_att;
+            io.out_ll = p.ll_qkv;
+            io.e_in = e - 1;
+            io.e_out = e;
+            if (!gemv_stage<LD, CD, WT, 2>(p, Lp.wqkv, p.qkv_rows, p.D, E_STORE, io, xs, red, bv, bi))
+                return;
+            stamp();
+            // attention
+            if ((int)blockIdx.x < p.KVH &&
+                !attn_stage<KVT, HD>(p, l, blockIdx.x, pos, e, qs, ks, vs, sc, part, kvlds, red, redf))
+                return;
+            stamp();
+            // wo + residual
+            io = StageIO{};
+            io.in_ll = p.ll_att;
+            io.out_ll = p.ll_x2;
+            io.res_ll = l ? p.ll_x : nullptr;
+            io.res_emb = l ? nullptr : emb_row;
+            io.e_in = e;
+            io.e_res = e - 1;
+            io.e_out = e;
+            if (!gemv_stage<LQ, CQ, WT, 2>(p, Lp.wo, p.D, p.qdim, E_RESID, io, xs, red, bv, bi))
+                return;
+            stamp();
+            // w1/w3 + silu gate
+            io = StageIO{};
+            io.in_ll = p.ll_x2;
+            io.gain = Lp.rms_ffn;
+            io.out_ll = p.ll_gate;
+            io.e_in = e;
+            io.e_out = e;
+            if (!gemv_stage<LD, CD, WT, 2>(p, Lp.w13, 2 * p.F, p.D, E_GATE, io, xs, red, bv, bi))
+                return;
+            stamp();
+            // w2 + residual
+            io = StageIO{};
+            io.in_ll = p.ll_gate;
+            io.out_ll = p.ll_x;
+            io.res_ll = p.ll_x2;
+            io.e_in = e;
+            io.e_res = e;
+            io.e_out = e;
+            if (!gemv_stage<LF, CF, WT, 2>(p, Lp.w2, p.D, p.F, E_RESID, io, xs, red, bv, bi))
+                return;
+            stamp();
+        }
+        // classifier over rmsnorm(x) (infer.go:242-243)
+        const uint32_t ec = base + (uint32_t)L + 1;
+        StageIO io{};
+        io.in_ll = p.ll_x;
+        io.gain = p.rms_final;
+        io.e_in = base + (uint32_t)L;
+        if (!gemv_stage<LD, CD, WT, 2>(p, p.cls, p.V, p.D, E_CLS, io, xs, red, bv, bi)) return;
+        stamp();
+        // this workgroup's (max, first index)
+        {
+            float v = bv;
+            int idx = bi;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(v, off, 64);
+                const int oi = __shfl_xor(idx, off, 64);
+                if (better(ov, oi, v, idx)) {
+                    v = ov;
+                    idx = oi;
+                }
+            }
+            if ((threadIdx.x & 63) == 0) cand[threadIdx.x >> 6] = ArgmaxPartial{v, idx};
+            lds_barrier();
+            if (threadIdx.x == 0) {
+                ArgmaxPartial b = cand[0];
+                for (int w = 1; w < kPW; w++)
+                    if (better(cand[w].v, cand[w].i, b.v, b.i)) b = cand[w];
+                const int slot = (f & 1) * gridDim.x + blockIdx.x;
+                ll_put(p.ll_pv + slot, b.v, ec);
+                ll_put_u(p.ll_pi + slot, (uint32_t)b.i, ec);
+            }
+        }
+        // next token: needed to generate, and always after the last forward of a launch
+        if (pos + 1 >= p.n_prompt || f == p.n_forwards - 1) {
+            bool ok = true;
+            float v = -INFINITY;
+            int idx = 0x7fffffff;
+            const int n = gridDim.x;
+            const uint64_t *pv = p.ll_pv + (f & 1) * n, *pi = p.ll_pi + (f & 1) * n;
+            for (int k = threadIdx.x; k < n; k += kPB) {
+                uint64_t a = ll_get(pv + k), b = ll_get(pi + k);
+                ok = ok && ll_wait_word(pv + k, ec, a, p) && ll_wait_word(pi + k, ec, b, p);
+                const float cv = __uint_as_float((uint32_t)a);
+                const int ci = (int)(uint32_t)b;
+                if (better(cv, ci, v, idx)) {
+                    v = cv;
+                    idx = ci;
+                }
+            }
+            if (!block_and(ok)) return;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(v, off, 64);
+                const int oi = __shfl_xor(idx, off, 64);
+                if (better(ov, oi, v, idx)) {
+                    v = ov;
+                    idx = oi;
+                }
+            }
+            if ((threadIdx.x & 63) == 0) cand[threadIdx.x >> 6] = ArgmaxPartial{v, idx};
+            lds_barrier();
+            if (threadIdx.x == 0) {
+                ArgmaxPartial b = cand[0];
+                for (int w = 1; w < kPW; w++)
+                    if (better(cand[w].v, cand[w].i, b.v, b.i)) b = cand[w];
+                const int nt = b.i == 0x7fffffff ? 0 : b.i;
+                next_tok = nt;
+                if (blockIdx.x == 0) {
+                    p.hist[pos] = nt;
+                    if (pos + 1 <= p.max_seq && pos + 1 >= p.n_prompt) p.tokens[pos + 1] = nt;
+                }
+            }
+            lds_barrier();
+            tok_next = next_tok;
+        }
+        stamp();
+    }
+}
+
+typedef void (*PersistentKernel)(PParams);
+
+// Lanes per row of the three GEMV widths, matching pick_shape's instantiations.
+void shape_lanes(int D, int Q, int F, int *ld, int *lq, int *lf) {
+    if (D == 768 && Q == 768 && F == 2048) { *ld = 32; *lq = 32; *lf = 64; }
+    else if (D == 1024 && Q == 2048 && F == 3072) { *ld = 32; *lq = 64; *lf = 64; }
+    else { *ld = 16; *lq = 16; *lf = 32; }
+}
+
+template <int WT, int KVT>
+PersistentKernel pick_shape(int D, int Q, int F, int HDv) {
+    if (D == 768 && Q == 768 && F == 2048 && HDv == 64)
+        return &k_decode_persistent<WT, KVT, 64, 32, 3, 32, 3, 64, 4>;
+    if (D == 1024 && Q == 2048 && F == 3072 && HDv == 128)
+        return &k_decode_persistent<WT, KVT, 128, 32, 4, 64, 4, 64, 6>;
+    if (D == 128 && Q == 128 && F == 256 && HDv == 32)
+        return &k_decode_persistent<WT, KVT, 32, 16, 1, 16, 1, 32, 1>;
+    return nullptr;
+}
+
+PersistentKernel pick_persistent(int dtype, int kv, int D, int Q, int F, int HDv) {
+    if (dtype == SH_DTYPE_F16) {
+        if (kv == SH_KV_F32) return pick_shape<SH_DTYPE_F16, SH_KV_F32>(D, Q, F, HDv);
+        if (kv == SH_KV_F16) return pick_shape<SH_DTYPE_F16, SH_KV_F16>(D, Q, F, HDv);
+        return pick_shape<SH_DTYPE_F16, SH_KV_BF16>(D, Q, F, HDv);
+    }
+    if (dtype == SH_DTYPE_BF16) {
+        if (kv == SH_KV_F32) return pick_shape<SH_DTYPE_BF16, SH_KV_F32>(D, Q, F, HDv);
+        if (kv == SH_KV_F16) return pick_shape<SH_DTYPE_BF16, SH_KV_F16>(D, Q, F, HDv);
+        return pick_shape<SH_DTYPE_BF16, SH_KV_BF16>(D, Q, F, HDv);
+    }
+    return nullptr;
+}
+
+}  // namespace
+
+bool persistent_supported(const sh_model *m) {
+    const sh_config &c = m->cfg;
+    const int group = c.n_heads / c.n_kv_heads;
+    if (!pick_persistent(m->dtype, c.kv_dtype, c.dim, m->qdim, c.hidden, c.head_dim)) return false;
+    if (group > kMaxGroup || group * c.max_seq > kScores || c.head_dim > 256) return false;
+    if (c.dim > kXs || m->qdim > kXs || c.hidden > kXs) return false;
+    if (kPB % c.head_dim) return false;
+    return true;
+}
+
+hipError_t persistent_grid(const sh_model *m, int *grid_out, std::string *why) {
+    const sh_config &c = m->cfg;
+    PersistentKernel k = pick_persistent(m->dtype, c.kv_dtype, c.dim, m->qdim, c.hidden, c.head_dim);
+    if (!k) return hipErrorInvalidValue;
+    int cus = 0, per_cu = 0;
+    hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device);
+    if (e != hipSuccess) return e;
+    hipFuncAttributes fa{};
+    if (hipFuncGetAttributes(&fa, (const void *)k) == hipSuccess)
+        *why = "k_decode_persistent: " + std::to_string(fa.numRegs) + " VGPRs, " +
+               std::to_string(fa.sharedSizeBytes) + " B LDS, " + std::to_string(fa.localSizeBytes) +
+               " B scratch, max " + std::to_string(fa.maxThreadsPerBlock) + " threads";
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k, kPB, 0);
+    if (e != hipSuccess) return e;
+    *why += "; " + std::to_string(per_cu) + " workgroup(s) of " + std::to_string(kPB) + " per CU";
+    if (per_cu < 1) return hipErrorInvalidConfiguration;
+    // One workgroup per CU, and no more workgroups than row groups in the smallest GEMV
+    // stage: every workgroup then owns rows in every stage, so it polls every stage's input
+    // in order, which is what keeps single-buffered hand-over vectors safe.
+    int grid = cus;
+    int ld = 0, lq = 0, lf = 0;
+    shape_lanes(c.dim, m->qdim, c.hidden, &ld, &lq, &lf);
+    auto groups = [](int rows, int lpr) { return (rows + 64 / lpr - 1) / (64 / lpr); };
+    grid = std::min(grid, groups(m->qkv_rows, ld));
+    grid = std::min(grid, groups(c.dim, lq));
+    grid = std::min(grid, groups(2 * c.hidden, ld));
+    grid = std::min(grid, groups(c.dim, lf));
+    grid = std::min(grid, groups(c.vocab, ld));
+    grid = std::min(grid, kPB);  // one argmax partial per thread
+    if (grid < c.n_kv_heads) return hipErrorInvalidConfiguration;
+    *grid_out = grid;
+    return hipSuccess;
+}
+
+hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt) {
+    const sh_config &c = m->cfg;
+    PersistentKernel k = pick_persistent(m->dtype, c.kv_dtype, c.dim, m->qdim, c.hidden, c.head_dim);
+    if (!k) return hipErrorInvalidValue;
+    PParams p{};
+    p.D = c.dim;
+    p.F = c.hidden;
+    p.H = c.n_heads;
+    p.KVH = c.n_kv_heads;
+    p.hd = c.head_dim;
+    p.V = c.vocab;
+    p.max_seq = c.max_seq;
+    p.L = c.n_layers;
+    p.qdim = m->qdim;
+    p.kvdim = m->kvdim;
+    p.qkv_rows = m->qkv_rows;
+    p.alpha = c.residual_scale;
+    p.inv_sqrt_hd = (float)(1.0 / sqrt((double)c.head_dim));
+    p.eps = c.norm_eps;
+    p.qk_eps = c.qk_norm_eps;
+    p.qk_norm = c.qk_norm;
+    p.layers = (const LayerPtrs *)m->p_layers;
+    p.embed = (const uint16_t *)m->embed;
+    p.cls = (const uint16_t *)m->cls;
+    p.rms_final = m->rms_final;
+    p.kcache = m->kcache;
+    p.vcache = m->vcache;
+    p.rope_cos = m->rope_cos;
+    p.rope_sin = m->rope_sin;
+    p.ll_qkv = m->ll_qkv;
+    p.ll_att = m->ll_att;
+    p.ll_x2 = m->ll_x2;
+    p.ll_gate = m->ll_gate;
+    p.ll_x = m->ll_x;
+    p.ll_pv = m->ll_pv;
+    p.ll_pi = m->ll_pi;
+    p.logits = m->logits;
+    p.tokens = m->tokens;
+    p.hist = m->argmax_hist;
+    p.pos0 = pos0;
+    p.n_forwards = n_forwards;
+    p.n_prompt = n_prompt;
+    p.epoch0 = m->epoch;
+    p.err = m->p_err;
+    p.spin_limit = m->spin_ticks;
+    p.trace = m->trace_f >= 0 ? m->trace_buf : nullptr;
+    p.trace_f = m->trace_f;
+    m->epoch += (uint32_t)n_forwards * (uint32_t)(c.n_layers + 1);
+    void *args[] = {&p};
+    return hipLaunchCooperativeKernel((const void *)k, dim3(m->p_grid), dim3(kPB), args, 0, m->stream);
+}
+
+size_t persistent_layer_ptr_bytes(int n_layers) { return sizeof(LayerPtrs) * (size_t)n_layers; }
+
+void persistent_fill_layer_ptrs(const sh_model *m, void *host) {
+    LayerPtrs *lp = (LayerPtrs *)host;
+    for (int l = 0; l < m->cfg.n_layers; l++) {
+        const LayerDev &L = m->layers[l];
+        lp[l].wqkv = (const uint16_t *)L.wqkv;
+        lp[l].wo = (const uint16_t *)L.wo;
+        lp[l].w13 = (const uint16_t *)L.w13;
+        lp[l].w2 = (const uint16_t *)L.w2;
+        lp[l].rms_att = L.rms_att;
+        lp[l].rms_ffn = L.rms_ffn;
+        lp[l].q_norm = L.q_norm;
+        lp[l].k_norm = L.k_norm;
+    }
+}
+
+}  // namespace sh

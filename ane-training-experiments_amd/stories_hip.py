@@ -71,6 +71,8 @@ class ShTiming(C.Structure):
         ("forwards", C.c_int64),
         ("tokens_out", C.c_int64),
         ("bytes_per_forward_mean", C.c_double),
+        ("persistent", C.c_int32),
+        ("grid", C.c_int32),
     ]
 
 
@@ -96,6 +98,9 @@ SIGNATURES = {
     "sh_greedy_decode": (C.c_int, [C.c_void_p, _I32, C.c_int32, C.c_int32, _I32, _I32, _I32]),
     "sh_prefill_logits": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint16), C.c_int32, _F]),
     "sh_stats": (C.c_int, [C.c_void_p, C.POINTER(ShTiming)]),
+    "sh_model_describe": (C.c_size_t, [C.c_void_p, C.c_char_p, C.c_size_t]),
+    "sh_trace_forward": (C.c_int, [C.c_void_p, C.c_int32]),
+    "sh_trace_read": (C.c_int, [C.c_void_p, C.POINTER(C.c_int64), C.c_int32, _I32, C.POINTER(C.c_double)]),
     "sh_model_destroy": (None, [C.c_void_p]),
     "sh_quantize_i8": (C.c_int, [_F, C.c_int32, C.c_int32, C.POINTER(C.c_int8), _F, C.c_int32]),
     "sh_dequantize_i8": (C.c_int, [C.POINTER(C.c_int8), _F, C.c_int32, C.c_int32, C.c_int32, _F]),
@@ -308,11 +313,41 @@ class Model:
                "sh_prefill_logits")
         return out
 
+    def trace_forward(self, forward: int) -> None:
+        _check(self.lib.sh_trace_forward(self.h, forward), "sh_trace_forward")
+
+    def trace_read(self) -> dict:
+        """Stage durations (us) of the traced forward for workgroup 0 and the last one."""
+        L = self.cfg.n_layers
+        n = 2 * (5 * L + 3)
+        buf = np.zeros(n, np.int64)
+        cnt = C.c_int32(0)
+        rate = C.c_double(0)
+        _check(self.lib.sh_trace_read(self.h, buf.ctypes.data_as(C.POINTER(C.c_int64)), n, C.byref(cnt),
+                                      C.byref(rate)), "sh_trace_read")
+        out = {}
+        names = ["qkv", "attn", "wo", "w13", "w2"]
+        for w, label in ((0, "wg0"), (1, "wg_last")):
+            t = buf[w * (n // 2):(w + 1) * (n // 2)].astype(np.float64) * 1e6 / rate.value
+            d = np.diff(t)
+            per = {k: d[j:5 * L:5].sum() for j, k in enumerate(names)}
+            per["classifier"] = d[5 * L]
+            per["argmax"] = d[5 * L + 1]
+            per["total"] = t[-1] - t[0]
+            out[label] = per
+        return out
+
+    def describe(self) -> str:
+        buf = C.create_string_buffer(1024)
+        self.lib.sh_model_describe(self.h, buf, len(buf))
+        return buf.value.decode(errors="replace")
+
     def stats(self) -> dict:
         t = ShTiming()
         _check(self.lib.sh_stats(self.h, C.byref(t)), "sh_stats")
         return {"gpu_ms": t.gpu_ms, "forwards": t.forwards, "tokens_out": t.tokens_out,
-                "bytes_per_forward_mean": t.bytes_per_forward_mean}
+                "bytes_per_forward_mean": t.bytes_per_forward_mean,
+                "persistent": bool(t.persistent), "grid": t.grid}
 
     def close(self) -> None:
         if self.h:

@@ -114,7 +114,8 @@ def main() -> int:
             "kv_cache": "fp32", "parallelism": "none (1 GPU)",
         },
         "roofline": {
-            "kernel": "token forward (all kernels of one position)",
+            "kernel": ("k_decode_persistent (whole decode in one launch; per-forward figures)"
+                       if st["persistent"] else "token forward (all kernels of one position)"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

@@ -63,6 +63,8 @@ typedef struct sh_timing {
     int64_t forwards;       /* token forwards (one per position) in that region */
     int64_t tokens_out;     /* tokens produced (greedy) in that region */
     double bytes_per_forward_mean; /* algorithmic bytes per forward, averaged */
+    int32_t persistent;     /* 1: the persistent decode kernel ran; 0: per-stage kernels */
+    int32_t grid;           /* workgroups of the persistent kernel */
 } sh_timing;
 
 /* ---- library ------------------------------------------------------------------------ */
@@ -111,6 +113,18 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
  * channel-first [V, seq] (logits[v*seq + t]). Out-of-range ids give a zero embedding
  * column (cpu.go:41-72). Residual scale = cfg.residual_scale. */
 int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *logits_cf);
+/* Human-readable description of the decode path this model runs (persistent kernel or
+ * per-stage kernels) and why; returns the full length. No reference counterpart: the
+ * reference reports its ANE/CPU choice through Diagnostics (ane/storiesane/diagnostics.go). */
+size_t sh_model_describe(const sh_model *m, char *buf, size_t len);
+/* Stage trace of the persistent decode kernel (a tracing aid like the reference's per-step
+ * metrics, ane/storiesane/metrics.go:13-60): arm with the index of a forward within the next
+ * decode launch (-1 disarms); after it, sh_trace_read returns 2 x (5*n_layers + 3)
+ * constant-clock timestamps — workgroup 0 then the last workgroup: forward start, then after
+ * each layer's qkv, attention, wo, w13 and w2 stages, after the classifier, after the argmax.
+ * -1 when the model does not run the persistent kernel. */
+int sh_trace_forward(sh_model *m, int32_t forward);
+int sh_trace_read(sh_model *m, int64_t *out, int32_t cap, int32_t *n_out, double *ticks_per_s);
 /* Timing of the last sh_greedy_decode / sh_prefill_logits call. */
 int sh_stats(const sh_model *m, sh_timing *out);
 /* (*Engine).Close (engine.go:480): frees device memory. NULL is allowed. */

@@ -24,6 +24,7 @@ def build(cfg, dtype, seed, std=0.02, gains_seed=None):
         w = random_gains(w, gains_seed)
     m = sh.Model(cfg, dtype)
     m.upload(w)
+    print(m.describe())
     ref = oracle.Decoder(oracle.config_from(cfg, w8a8=(dtype == sh.SH_DTYPE_W8A8)),
                          w.rounded(dtype), threads=THREADS)
     return m, ref, w
@@ -51,6 +52,19 @@ def test_decode_step_tiny(gpu, dtype, kv):
     toks = sh.synth_tokens(40, 103, cfg.vocab)
     worst = check_steps(m, ref, toks)
     assert worst < 1e-3
+    m.close()
+
+
+def test_decode_step_graph_path_shape(gpu):
+    """A shape without a persistent-kernel instantiation runs the per-stage graph path."""
+    cfg = tiny_config(dim=256, hidden=512, n_heads=8, n_kv_heads=4, head_dim=32)
+    m, ref, _ = build(cfg, sh.SH_DTYPE_F16, seed=105, std=0.06, gains_seed=106)
+    assert check_steps(m, ref, sh.synth_tokens(24, 107, cfg.vocab)) < 1e-3
+    p = sh.synth_tokens(6, 108, cfg.vocab)
+    got, _, _ = m.greedy_decode(p, 20)
+    want, _, _ = ref.greedy_decode(p, 20)
+    assert got.tolist() == want.tolist()
+    assert not m.stats()["persistent"]
     m.close()
 
 
@@ -160,6 +174,12 @@ def test_stories110m_fp16_greedy_128(gpu):
     print(f"generated {len(got) - plen} tokens; smallest top-2 margin {np.nanmin(margins):.3e}")
     assert got.tolist() == want.tolist() and eos == weos
     assert len(got) == 16 + 128 or eos
+    st = m.stats()
+    print(f"persistent={st['persistent']} grid={st['grid']} {st['gpu_ms']:.3f} ms for {st['forwards']} forwards")
+    assert st["persistent"]
+    # a second decode reuses the model (epochs advance, cache is cleared)
+    again, _, _ = m.greedy_decode(prompt, 128)
+    assert again.tolist() == got.tolist()
     # logits along the same stream
     m.reset_cache()
     ref.reset()
@@ -179,6 +199,9 @@ def test_qwen3_shaped_bf16_greedy(gpu):
     want, weos, margins = ref.greedy_decode(prompt, 256)
     print(f"generated {len(got) - plen} tokens; smallest top-2 margin {np.nanmin(margins):.3e}")
     assert got.tolist() == want.tolist() and eos == weos
+    st = m.stats()
+    print(f"persistent={st['persistent']} grid={st['grid']} {st['gpu_ms']:.3f} ms for {st['forwards']} forwards")
+    assert st["persistent"]
     m.reset_cache()
     ref.reset()
     check_steps(m, ref, got[:8])
