@@ -80,6 +80,16 @@ double forward_bytes(const sh_model *m, int pos) {
     return total;
 }
 
+// Compulsory HBM bytes of one full-sequence forward: every weight once, the embedding rows,
+// the logits written. Activations of a few MB stay in the 256 MB of L2 + MALL.
+double prefill_bytes(const sh_model *m, int S) {
+    const sh_config &c = m->cfg;
+    const double eb = (double)weight_elem_bytes(m->dtype);
+    const double D = c.dim, F = c.hidden, Q = m->qdim, KV = m->kvdim;
+    double per_layer = eb * ((Q + 2 * KV) * D + D * Q + 2 * F * D + D * F) + 4.0 * 2 * D;
+    return per_layer * c.n_layers + eb * (double)c.vocab * D + eb * D * S + 4.0 * c.vocab * S;
+}
+
 hipError_t ensure_step_graph(sh_model *m) {
     if (m->step_ready) return hipSuccess;
     hipGraph_t g = nullptr;
@@ -461,6 +471,7 @@ void sh_model_destroy(sh_model *m) {
     (void)hipFree(m->ll_pi);
     (void)hipFree(m->p_err);
     (void)hipFree(m->trace_buf);
+    (void)hipFree(m->pf_arena);
     if (m->ev0) (void)hipEventDestroy(m->ev0);
     if (m->ev1) (void)hipEventDestroy(m->ev1);
     if (m->stream) (void)hipStreamDestroy(m->stream);
@@ -687,8 +698,34 @@ int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *l
         set_error("sh_prefill_logits: bad arguments");
         return -1;
     }
-    set_error("sh_prefill_logits: not available in this build");
-    return -1;
+    std::string why;
+    if (!prefill_supported(m, &why)) {
+        set_error("sh_prefill_logits: " + why);
+        return -1;
+    }
+    (void)hipSetDevice(m->device);
+    if (!hip_ok(prefill_alloc(m, seq), "prefill scratch")) return -1;
+    std::vector<int32_t> ids(tokens, tokens + seq);   // out-of-range ids embed as zeros
+    if (!hip_ok(hipMemcpyAsync(m->pf_tokens, ids.data(), sizeof(int32_t) * seq,
+                               hipMemcpyHostToDevice, m->stream), "prefill tokens"))
+        return -1;
+    if (!hip_ok(hipEventRecord(m->ev0, m->stream), "event")) return -1;
+    if (!hip_ok(enqueue_prefill(m, seq, true, -1), "prefill")) return -1;
+    if (!hip_ok(hipEventRecord(m->ev1, m->stream), "event")) return -1;
+    const size_t n = (size_t)m->cfg.vocab * seq;
+    if (!hip_ok(hipMemcpyAsync(logits_cf, m->pf_logits, sizeof(float) * n,
+                               hipMemcpyDeviceToHost, m->stream), "prefill logits"))
+        return -1;
+    if (!hip_ok(hipStreamSynchronize(m->stream), "prefill sync")) return -1;
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, m->ev0, m->ev1);
+    m->last.gpu_ms = ms;
+    m->last.forwards = 1;
+    m->last.tokens_out = seq;
+    m->last.bytes_per_forward_mean = prefill_bytes(m, seq);
+    m->last.persistent = 0;
+    m->last.grid = 0;
+    return 0;
 }
 
 int sh_trace_forward(sh_model *m, int32_t forward) {

@@ -88,6 +88,14 @@ struct sh_model {
     char path_note[512];    // which decode path runs, and why
     long long *trace_buf;   // device: 2 x (5L + 3) stage timestamps
     int trace_f;            // forward index traced in the next launch, -1 = off
+
+    // full-sequence forward (sh_prefill.hip): token-major scratch for up to pf_cap tokens
+    void *pf_arena;
+    int pf_cap;
+    int32_t *pf_tokens;                        // [S]
+    float *pf_x, *pf_x2, *pf_qkv, *pf_logits;  // [S,D] [S,D] [S,qkv_rows] [V,S]
+    float *pf_q, *pf_k, *pf_v;                 // roped q, k and v: [S,qdim] [S,kvdim] x2
+    uint16_t *pf_xn, *pf_att, *pf_gate;        // GEMM operands: hi plane, then lo plane
 };
 
 namespace sh {
@@ -114,6 +122,11 @@ bool persistent_supported(const sh_model *m);
 hipError_t persistent_grid(const sh_model *m, int *grid_out, std::string *why);
 hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt);
 size_t persistent_layer_ptr_bytes(int n_layers);
+bool prefill_supported(const sh_model *m, std::string *why);
+hipError_t prefill_alloc(sh_model *m, int S);
+// Full causal forward of pf_tokens[0, S): logits [V, S] into pf_logits when `logits`;
+// kv_seq >= 0 also writes KV-cache rows [0, S) of every layer.
+hipError_t enqueue_prefill(sh_model *m, int S, bool logits, int kv_seq);
 void persistent_fill_layer_ptrs(const sh_model *m, void *host);
 
 }  // namespace sh

@@ -198,16 +198,6 @@ __device__ __forceinline__ double block_sum_d(double v, double *red) {
     for (int w = 0; w < kPW; w++) s += red[w];
     return s;
 }
-__device__ __forceinline__ float block_max_f(float v, float *red) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    lds_barrier();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    lds_barrier();
-    float s = red[0];
-    for (int w = 1; w < kPW; w++) s = fmaxf(s, red[w]);
-    return s;
-}
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }

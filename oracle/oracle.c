@@ -692,6 +692,7 @@ void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t
     or_rope_tables(rc, rs, seq, hd, cfg->rope_theta);            /* engine.go:218 */
 
     or_embed_lookup_cf(x, w->embed, cfg->vocab, tokens, D, seq);
+    float *bufs[2] = {x, next};   /* cur and next swap every layer */
     float *cur = x;
     for (int l = 0; l < cfg->n_layers; l++) {
         const or_layer *L = &w->layers[l];
@@ -721,7 +722,7 @@ void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t
     }
     rms_norm_final_cf(xn, cur, w->rms_final, D, seq, cfg->norm_eps);
     matmul_vocab_seq(logits_cf, w->cls ? w->cls : w->embed, xn, cfg->vocab, D, seq, threads);
-    free(x); free(next); free(xn); free(qf); free(kf); free(vf); free(att); free(x2);
+    free(bufs[0]); free(bufs[1]); free(xn); free(qf); free(kf); free(vf); free(att); free(x2);
     free(h1); free(h3); free(gate); free(ff); free(rc); free(rs);
 }
 

@@ -233,9 +233,10 @@ def test_decoder_residual_scale_matches_float64_forward():
         np.testing.assert_allclose(dec.forward_one(int(tok), t), ref[t], atol=2e-5, rtol=0)
 
 
-@pytest.mark.parametrize("alpha", [1.0, None])
-def test_eval_logits_cf_matches_float64_forward(alpha):
-    cfg = tiny_config(residual_scale=deepnet_alpha(2) if alpha is None else alpha)
+@pytest.mark.parametrize("alpha,layers", [(1.0, 2), (None, 2), (None, 3)])
+def test_eval_logits_cf_matches_float64_forward(alpha, layers):
+    cfg = tiny_config(n_layers=layers,
+                      residual_scale=deepnet_alpha(layers) if alpha is None else alpha)
     w = random_gains(sh.synth_weights(cfg, seed=31, std=0.08), 32)
     toks = sh.synth_tokens(24, 33, cfg.vocab)
     got = oracle.eval_logits_cf(oracle.config_from(cfg), w, toks, threads=2)
