@@ -1,0 +1,443 @@
+// stories-generate — command-line decoder over libstories_hip.so, the C++ host counterpart
+// of cmd/stories-generate-go/main.go. Same flags and output lines; the decode itself runs
+// on the GPU through the C ABI (include/stories_hip.h).
+//
+//   stories-generate [-model stories110M.bin] [-tokenizer tokenizer.bin] [-prompt-ids 1,2]
+//                    [-max-new 64] [-temperature 0.8] [-seed N] [-seq 256]
+//
+// Flags beyond the reference's (all optional):
+//   -shape stories110m|qwen3-0.6b   model shape when no -model file is given
+//   -dtype fp16|bf16                weight storage (default fp16; bf16 for qwen3-0.6b)
+//   -kv f32|f16|bf16                KV-cache storage
+//   -synthetic-seed S, -synthetic-std X
+//                                   N(0, X) weights keyed by S (the library's sh_synth_normal
+//                                   streams) when no -model file is given
+//   -prompt-len N, -prompt-seed S   a synthetic prompt of N uniform ids instead of -prompt-ids
+//   -bench-steps K, -bench-warmup W greedy decode W untimed + K timed times and print one
+//                                   JSON object (device times, bytes, tokens) instead of text
+//   -inspect                        load the model file, print its header and per-tensor
+//                                   sums as JSON, touch no GPU
+//   -detokenize 5,6,7               print text= for these ids with -tokenizer, touch no GPU
+//   -copy-calibrate BYTES           with -bench-steps: first time the library's plain copy
+//                                   kernel over BYTES and report its GB/s
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <chrono>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "llama2_file.hpp"
+#include "stories_hip.h"
+
+namespace {
+
+[[noreturn]] void fatalf(const char *fmt, const std::string &a = "") {
+    fprintf(stderr, fmt, a.c_str());
+    fputc('\n', stderr);
+    exit(1);
+}
+
+std::string lib_error() {
+    char buf[1024];
+    sh_last_error(buf, sizeof buf);
+    return buf;
+}
+
+// Go flag package syntax: -name value, -name=value, --name; booleans take no value.
+struct Flags {
+    std::map<std::string, std::string> v;
+    std::map<std::string, bool> is_bool;
+    void def(const char *name, const char *dflt, bool boolean = false) {
+        v[name] = dflt;
+        is_bool[name] = boolean;
+    }
+    void parse(int argc, char **argv) {
+        for (int i = 1; i < argc; i++) {
+            std::string a = argv[i];
+            if (a.size() < 2 || a[0] != '-') fatalf("unexpected argument %s", a);
+            a = a.substr(a[1] == '-' ? 2 : 1);
+            std::string val;
+            const size_t eq = a.find('=');
+            const bool has_eq = eq != std::string::npos;
+            if (has_eq) {
+                val = a.substr(eq + 1);
+                a = a.substr(0, eq);
+            }
+            if (!v.count(a)) fatalf("flag provided but not defined: -%s", a);
+            if (is_bool[a]) {
+                v[a] = has_eq ? val : "true";
+            } else {
+                if (!has_eq) {
+                    if (i + 1 >= argc) fatalf("flag needs an argument: -%s", a);
+                    val = argv[++i];
+                }
+                v[a] = val;
+            }
+        }
+    }
+    std::string s(const char *n) const { return v.at(n); }
+    long long i(const char *n) const { return strtoll(v.at(n).c_str(), nullptr, 10); }
+    double f(const char *n) const { return strtod(v.at(n).c_str(), nullptr); }
+    bool b(const char *n) const { return v.at(n) == "true" || v.at(n) == "1"; }
+};
+
+// main.go:121-142 parseTokenList: empty -> [1]; blanks skipped.
+std::vector<int32_t> parse_token_list(const std::string &s) {
+    std::vector<int32_t> out;
+    size_t p = 0;
+    int idx = 0;
+    while (p <= s.size()) {
+        size_t q = s.find(',', p);
+        if (q == std::string::npos) q = s.size();
+        std::string t = s.substr(p, q - p);
+        const size_t a = t.find_first_not_of(" \t\n"), b = t.find_last_not_of(" \t\n");
+        t = a == std::string::npos ? "" : t.substr(a, b - a + 1);
+        if (!t.empty()) {
+            char *end = nullptr;
+            const long v = strtol(t.c_str(), &end, 10);
+            if (*end) fatalf("parse prompt tokens: token[%s] is not an integer",
+                             std::to_string(idx) + "]=\"" + t);
+            out.push_back((int32_t)v);
+        }
+        idx++;
+        p = q + 1;
+    }
+    if (out.empty()) out.push_back(1);
+    return out;
+}
+
+// Host-side sampler for temperature > 1e-6: the inverse-CDF rule of infer.go:347-371 over
+// float64 exp terms. Uniform draws come from splitmix64 (53-bit doubles) seeded by -seed;
+// Go's math/rand stream is not reproduced, so sampled ids differ from the reference's.
+struct Sampler {
+    uint64_t state;
+    double uniform() {
+        uint64_t z = (state += 0x9e3779b97f4a7c15ull);
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        z ^= z >> 31;
+        return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+    }
+    int sample(const float *logits, int n, float temperature) {
+        float mx = logits[0];
+        for (int i = 1; i < n; i++)
+            if (logits[i] > mx) mx = logits[i];
+        const double inv_t = (double)(1.0f / temperature);
+        double total = 0;
+        for (int i = 0; i < n; i++) total += exp(((double)logits[i] - (double)mx) * inv_t);
+        const double target = uniform() * total;
+        double acc = 0;
+        for (int i = 0; i < n; i++) {
+            acc += exp(((double)logits[i] - (double)mx) * inv_t);
+            if (acc >= target) return i;
+        }
+        return n - 1;
+    }
+};
+
+std::string join_ints(const std::vector<int32_t> &v) {
+    std::string s;
+    for (size_t i = 0; i < v.size(); i++) {
+        if (i) s += ",";
+        s += std::to_string(v[i]);
+    }
+    return s;
+}
+
+std::string json_escape(const std::string &s) {
+    std::string o;
+    for (char c : s) {
+        if (c == '"' || c == '\\') {
+            o += '\\';
+            o += c;
+        } else if ((unsigned char)c < 0x20) {
+            char b[8];
+            snprintf(b, sizeof b, "\\u%04x", (unsigned char)c);
+            o += b;
+        } else {
+            o += c;
+        }
+    }
+    return o;
+}
+
+// Go's time.Duration.Round(time.Millisecond).String() for the elapsed field.
+std::string go_duration(double seconds) {
+    const long long ms = llround(seconds * 1e3);
+    char b[64];
+    if (ms < 1000) snprintf(b, sizeof b, "%lldms", ms);
+    else if (ms < 60000) snprintf(b, sizeof b, "%.3gs", ms / 1e3);
+    else snprintf(b, sizeof b, "%lldm%.3gs", ms / 60000, (ms % 60000) / 1e3);
+    return b;
+}
+
+void synth_weights(const sh_config &c, uint64_t seed, float std_, stories::HostWeights &w) {
+    w.resize(c);
+    for (int l = 0; l < c.n_layers; l++) {
+        stories::HostLayer &L = w.layers[l];
+        std::vector<float> *mats[7] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.w1, &L.w2, &L.w3};
+        for (int k = 0; k < 7; k++)
+            if (sh_synth_normal(mats[k]->data(), mats[k]->size(), seed, 16 * (uint64_t)(l + 1) + k, std_))
+                fatalf("synthetic weights: %s", lib_error());
+    }
+    if (sh_synth_normal(w.embed.data(), w.embed.size(), seed, 1, std_))
+        fatalf("synthetic weights: %s", lib_error());
+    if (!c.tied_embed && sh_synth_normal(w.cls.data(), w.cls.size(), seed, 2, std_))
+        fatalf("synthetic weights: %s", lib_error());
+}
+
+sh_model *open_model(const sh_config &c, int dtype, const stories::HostWeights &w) {
+    sh_model *m = sh_model_create(&c, dtype);
+    if (!m) fatalf("decode: %s", lib_error());
+    for (int l = 0; l < c.n_layers; l++) {
+        const stories::HostLayer &L = w.layers[l];
+        if (sh_model_upload_layer(m, l, L.wq.data(), L.wk.data(), L.wv.data(), L.wo.data(),
+                                  L.w1.data(), L.w2.data(), L.w3.data(), L.rms_att.data(),
+                                  L.rms_ffn.data(), c.qk_norm ? L.q_norm.data() : nullptr,
+                                  c.qk_norm ? L.k_norm.data() : nullptr))
+            fatalf("decode: %s", lib_error());
+    }
+    if (sh_model_upload_globals(m, w.embed.data(), w.rms_final.data(),
+                                c.tied_embed ? nullptr : w.cls.data()))
+        fatalf("decode: %s", lib_error());
+    return m;
+}
+
+struct DecodeResult {
+    std::vector<int32_t> tokens;
+    int prompt_length = 0;
+    bool stopped_eos = false;
+};
+
+// (*Decoder).Decode (infer.go:136-202). Greedy runs entirely on the device; a sampled
+// decode feeds the prompt on the device and draws each id on the host from the logits.
+DecodeResult decode(sh_model *m, const sh_config &c, const std::vector<int32_t> &prompt_in,
+                    int max_new, float temperature, Sampler &rng) {
+    DecodeResult r;
+    if (max_new <= 0) max_new = 64;
+    if (temperature < 0) temperature = 0;
+    if (temperature <= 1e-6f) {
+        std::vector<int32_t> out(c.max_seq);
+        int32_t n = 0, eos = 0;
+        if (sh_greedy_decode(m, prompt_in.data(), (int32_t)prompt_in.size(), max_new, out.data(),
+                             &n, &eos))
+            fatalf("decode: %s", lib_error());
+        std::vector<int32_t> p = prompt_in.empty() ? std::vector<int32_t>{1} : prompt_in;
+        r.prompt_length = (int)std::min(p.size(), (size_t)c.max_seq);
+        r.tokens.assign(out.begin(), out.begin() + n);
+        r.stopped_eos = eos != 0;
+        return r;
+    }
+    std::vector<int32_t> prompt = prompt_in.empty() ? std::vector<int32_t>{1} : prompt_in;
+    if ((int)prompt.size() > c.max_seq) prompt.erase(prompt.begin(), prompt.end() - c.max_seq);
+    for (size_t i = 0; i < prompt.size(); i++)
+        if (prompt[i] < 0 || prompt[i] >= c.vocab)
+            fatalf("decode: %s", "prompt token[" + std::to_string(i) + "]=" +
+                                     std::to_string(prompt[i]) + " out of range");
+    if (sh_reset_cache(m)) fatalf("decode: %s", lib_error());
+    r.tokens = prompt;
+    r.prompt_length = (int)prompt.size();
+    for (size_t pos = 0; pos + 1 < prompt.size(); pos++)
+        if (sh_decode_step(m, prompt[pos], (int32_t)pos, nullptr, nullptr))
+            fatalf("decode: %s", lib_error());
+    std::vector<float> logits(c.vocab);
+    for (int step = 0; step < max_new && (int)r.tokens.size() < c.max_seq; step++) {
+        const int pos = (int)r.tokens.size() - 1;
+        if (sh_decode_step(m, r.tokens[pos], pos, logits.data(), nullptr))
+            fatalf("decode: %s", lib_error());
+        const int next = rng.sample(logits.data(), c.vocab, temperature);
+        r.tokens.push_back(next);
+        if (next == 2) {
+            r.stopped_eos = true;
+            break;
+        }
+    }
+    return r;
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+    Flags fl;
+    fl.def("model", "");
+    fl.def("ckpt", "");
+    fl.def("tokenizer", "");
+    fl.def("prompt-ids", "1");
+    fl.def("max-new", "64");
+    fl.def("temperature", "0.8");
+    const std::string now = std::to_string(
+        (long long)std::chrono::system_clock::now().time_since_epoch().count());
+    fl.def("seed", now.c_str());
+    fl.def("seq", "256");
+    fl.def("ane", "false", true);
+    fl.def("shape", "stories110m");
+    fl.def("dtype", "");
+    fl.def("kv", "");
+    fl.def("synthetic-seed", "0");
+    fl.def("synthetic-std", "0.02");
+    fl.def("prompt-len", "0");
+    fl.def("prompt-seed", "1");
+    fl.def("bench-steps", "0");
+    fl.def("bench-warmup", "2");
+    fl.def("inspect", "false", true);
+    fl.def("detokenize", "");
+    fl.def("copy-calibrate", "0");
+    fl.parse(argc, argv);
+
+    if (!fl.s("detokenize").empty()) {
+        stories::Tokenizer tok;
+        std::string err;
+        const int vocab = fl.s("shape") == "qwen3-0.6b" ? 151936 : 32000;
+        if (fl.s("tokenizer").empty()) fatalf("%s", "-detokenize needs -tokenizer");
+        if (!tok.load(fl.s("tokenizer"), vocab, &err)) fatalf("load tokenizer: %s", err);
+        std::string text;
+        for (int32_t id : parse_token_list(fl.s("detokenize"))) text += tok.decode(id);
+        printf("text=%s\n", text.c_str());
+        return 0;
+    }
+
+    if (!fl.s("ckpt").empty())
+        fatalf("decode: %s", "checkpoint files (-ckpt) are not read by this build; use -model");
+    if (fl.b("ane"))
+        fatalf("decode: %s", "the full-window engine (-ane) is not part of this build; the "
+                             "default KV-cache decoder runs on the GPU");
+
+    // ---- model description and host weights ----
+    sh_config c{};
+    stories::HostWeights w;
+    std::string source;
+    const std::string shape = fl.s("shape");
+    if (!fl.s("model").empty() && fl.s("model") != "synthetic") {
+        std::string err;
+        stories::Llama2Header hdr{};
+        if (!stories::load_llama2_file(fl.s("model"), &hdr, &w, &err)) fatalf("decode: %s", err);
+        if (fl.b("inspect")) {
+            printf("%s\n", stories::describe_json(hdr, w).c_str());
+            return 0;
+        }
+        stories::config_from_header(hdr, &c);
+        source = "pretrained";
+    } else {
+        if (fl.b("inspect")) fatalf("%s", "-inspect needs -model");
+        if (shape == "qwen3-0.6b") sh_config_qwen3_06b(&c);
+        else if (shape == "stories110m") sh_config_stories110m(&c);
+        else fatalf("unknown -shape %s", shape);
+        source = "synthetic";
+    }
+    // infer.go:84-89: maxSeq <= 0 -> 256, clamped to 256 for the Stories decoder
+    long long seq = fl.i("seq");
+    if (seq <= 0) seq = 256;
+    if (shape == "stories110m" && seq > 256) seq = 256;
+    c.max_seq = (int32_t)seq;
+    int dtype = shape == "qwen3-0.6b" ? SH_DTYPE_BF16 : SH_DTYPE_F16;
+    if (fl.s("dtype") == "fp16") dtype = SH_DTYPE_F16;
+    else if (fl.s("dtype") == "bf16") dtype = SH_DTYPE_BF16;
+    else if (fl.s("dtype") == "w8a8") dtype = SH_DTYPE_W8A8;
+    else if (!fl.s("dtype").empty()) fatalf("unknown -dtype %s", fl.s("dtype"));
+    if (fl.s("kv") == "f32") c.kv_dtype = SH_KV_F32;
+    else if (fl.s("kv") == "f16") c.kv_dtype = SH_KV_F16;
+    else if (fl.s("kv") == "bf16") c.kv_dtype = SH_KV_BF16;
+    else if (!fl.s("kv").empty()) fatalf("unknown -kv %s", fl.s("kv"));
+    if (source == "synthetic")
+        synth_weights(c, (uint64_t)fl.i("synthetic-seed"), (float)fl.f("synthetic-std"), w);
+
+    std::vector<int32_t> prompt;
+    if (fl.i("prompt-len") > 0) {
+        prompt.resize(fl.i("prompt-len"));
+        if (sh_synth_tokens(prompt.data(), prompt.size(), (uint64_t)fl.i("prompt-seed"), c.vocab))
+            fatalf("prompt: %s", lib_error());
+    } else {
+        prompt = parse_token_list(fl.s("prompt-ids"));
+    }
+    stories::Tokenizer tok;
+    const bool have_tok = !fl.s("tokenizer").empty();
+    if (have_tok) {
+        std::string err;
+        if (!tok.load(fl.s("tokenizer"), c.vocab, &err)) fatalf("load tokenizer: %s", err);
+    }
+
+    if (sh_init(0)) fatalf("decode: %s", lib_error());
+    sh_model *m = open_model(c, dtype, w);
+    w = stories::HostWeights();   // device holds the weights now
+    Sampler rng{(uint64_t)fl.i("seed")};
+    const int max_new = (int)fl.i("max-new");
+    const float temperature = (float)fl.f("temperature");
+
+    const int steps = (int)fl.i("bench-steps");
+    if (steps > 0) {
+        // Greedy decode timing for bench harnesses: W untimed runs, then K timed ones.
+        double copy_ms = 0, copy_gbs = 0;
+        const long long copy_bytes = fl.i("copy-calibrate");
+        if (copy_bytes > 0 && sh_copy_calibrate((size_t)copy_bytes, 5, &copy_ms, &copy_gbs))
+            fatalf("copy calibrate: %s", lib_error());
+        for (int i = 0; i < fl.i("bench-warmup"); i++) decode(m, c, prompt, max_new, 0.f, rng);
+        std::vector<double> gpu_ms, bytes;
+        std::vector<long long> fwd, gen;
+        DecodeResult last;
+        int persistent = 0, grid = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < steps; i++) {
+            last = decode(m, c, prompt, max_new, 0.f, rng);
+            sh_timing t{};
+            if (sh_stats(m, &t)) fatalf("stats: %s", lib_error());
+            gpu_ms.push_back(t.gpu_ms);
+            fwd.push_back(t.forwards);
+            gen.push_back(t.tokens_out);
+            bytes.push_back(t.bytes_per_forward_mean);
+            persistent = t.persistent;
+            grid = t.grid;
+        }
+        const double wall = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        char desc[1024];
+        sh_model_describe(m, desc, sizeof desc);
+        std::string js = "{\"steps\": " + std::to_string(steps) +
+                         ", \"warmup\": " + std::to_string(fl.i("bench-warmup")) +
+                         ", \"wall_s\": " + std::to_string(wall) + ", \"gpu_ms\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(gpu_ms[i]);
+        js += "], \"forwards\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(fwd[i]);
+        js += "], \"generated\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(gen[i]);
+        js += "], \"bytes_per_forward_mean\": [";
+        for (int i = 0; i < steps; i++) {
+            char b[64];
+            snprintf(b, sizeof b, "%.1f", bytes[i]);
+            js += (i ? ", " : "") + std::string(b);
+        }
+        js += "], \"persistent\": " + std::to_string(persistent) +
+              ", \"grid\": " + std::to_string(grid) +
+              ", \"copy_bytes\": " + std::to_string(copy_bytes) +
+              ", \"copy_gbs\": " + std::to_string(copy_gbs) +
+              ", \"prompt_length\": " + std::to_string(last.prompt_length) +
+              ", \"tokens\": [" + join_ints(last.tokens) + "]" +
+              ", \"describe\": \"" + json_escape(desc) + "\"}";
+        printf("%s\n", js.c_str());
+        fflush(stdout);
+        sh_model_destroy(m);
+        return 0;
+    }
+
+    const auto t0 = std::chrono::steady_clock::now();
+    DecodeResult res = decode(m, c, prompt, max_new, temperature, rng);
+    const double elapsed = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    const int new_tokens = (int)res.tokens.size() - res.prompt_length;
+    const double tps = elapsed > 0 ? new_tokens / elapsed : 0.0;
+    printf("source=%s prompt_tokens=%d generated_tokens=%d elapsed=%s tok/s=%.2f eos=%s\n",
+           source.c_str(), res.prompt_length, new_tokens, go_duration(elapsed).c_str(), tps,
+           res.stopped_eos ? "true" : "false");
+    printf("tokens=%s\n", join_ints(res.tokens).c_str());
+    if (have_tok) {
+        std::string text;
+        for (size_t i = res.prompt_length; i < res.tokens.size(); i++) text += tok.decode(res.tokens[i]);
+        printf("text=%s\n", text.c_str());
+    } else {
+        printf("text=(tokenizer not provided)\n");
+    }
+    sh_model_destroy(m);
+    return 0;
+}

@@ -855,6 +855,39 @@ int sh_synth_normal(float *dst, size_t n, uint64_t seed, uint64_t tensor_id, flo
     return 0;
 }
 
+int sh_copy_calibrate(size_t bytes, int32_t reps, double *ms_per_copy, double *gbps) {
+    if (bytes == 0 || bytes % 16 || reps <= 0 || !ms_per_copy || !gbps) {
+        set_error("sh_copy_calibrate: bytes must be a positive multiple of 16, reps > 0");
+        return -1;
+    }
+    void *a = nullptr, *b = nullptr;
+    hipStream_t s = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    bool ok = hip_ok(hipMalloc(&a, bytes), "calibrate alloc") &&
+              hip_ok(hipMalloc(&b, bytes), "calibrate alloc") &&
+              hip_ok(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "calibrate stream") &&
+              hip_ok(hipEventCreate(&e0), "calibrate event") &&
+              hip_ok(hipEventCreate(&e1), "calibrate event") &&
+              hip_ok(hipMemsetAsync(a, 0x5a, bytes, s), "calibrate fill") &&
+              hip_ok(launch_copy_calibrate(a, b, bytes, s), "calibrate copy") &&
+              hip_ok(hipEventRecord(e0, s), "calibrate event");
+    for (int r = 0; ok && r < reps; r++) ok = hip_ok(launch_copy_calibrate(a, b, bytes, s), "calibrate copy");
+    ok = ok && hip_ok(hipEventRecord(e1, s), "calibrate event") &&
+         hip_ok(hipStreamSynchronize(s), "calibrate sync");
+    float ms = 0;
+    if (ok) ok = hip_ok(hipEventElapsedTime(&ms, e0, e1), "calibrate time");
+    if (ok) {
+        *ms_per_copy = ms / reps;
+        *gbps = 2.0 * (double)bytes / (*ms_per_copy * 1e-3) / 1e9;
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) (void)hipStreamDestroy(s);
+    (void)hipFree(a);
+    (void)hipFree(b);
+    return ok ? 0 : -1;
+}
+
 int sh_synth_tokens(int32_t *dst, size_t n, uint64_t seed, int32_t vocab) {
     if ((!dst && n) || vocab <= 0) {
         set_error("sh_synth_tokens: bad arguments");

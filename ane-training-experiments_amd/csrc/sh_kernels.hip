@@ -642,4 +642,23 @@ hipError_t launch_dequantize(const int8_t *q, const float *scales, int rows, int
     return hipGetLastError();
 }
 
+// Plain streaming copy: every lane moves 16-byte words, grid-stride. Reads and writes
+// exactly n16 * 16 bytes.
+__global__ __launch_bounds__(kBlock) void k_copy_calibrate(const uint4 *__restrict__ src,
+                                                           uint4 *__restrict__ dst, size_t n16) {
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n16;
+         i += (size_t)gridDim.x * kBlock)
+        dst[i] = src[i];
+}
+
+hipError_t launch_copy_calibrate(const void *src, void *dst, size_t bytes, hipStream_t s) {
+    const size_t n16 = bytes / 16;
+    size_t blocks = (n16 + kBlock - 1) / kBlock;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_copy_calibrate, dim3((unsigned)blocks), dim3(kBlock), 0, s,
+                       (const uint4 *)src, (uint4 *)dst, n16);
+    return hipGetLastError();
+}
+
 }  // namespace sh

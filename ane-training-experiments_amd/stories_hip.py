@@ -87,6 +87,7 @@ _lib = None
 # every entry point of include/stories_hip.h with its ctypes signature
 SIGNATURES = {
     "sh_init": (C.c_int, [C.c_int32]),
+    "sh_copy_calibrate": (C.c_int, [C.c_size_t, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "sh_last_error": (C.c_size_t, [C.c_char_p, C.c_size_t]),
     "sh_config_stories110m": (C.c_int, [C.POINTER(ShConfig)]),
     "sh_config_qwen3_06b": (C.c_int, [C.POINTER(ShConfig)]),
@@ -365,6 +366,13 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+def copy_calibrate(nbytes: int, reps: int = 10):
+    """sh_copy_calibrate: (ms per copy, GB/s) of the plain copy kernel over nbytes."""
+    ms, gbps = C.c_double(0), C.c_double(0)
+    _check(load().sh_copy_calibrate(nbytes, reps, C.byref(ms), C.byref(gbps)), "sh_copy_calibrate")
+    return ms.value, gbps.value
 
 
 def quantize_i8(src: np.ndarray, per_row: bool):

@@ -142,6 +142,15 @@ int sh_quantize_i8(const float *src, int32_t rows, int32_t cols, int8_t *dst, fl
 int sh_dequantize_i8(const int8_t *q, const float *scales, int32_t rows, int32_t cols,
                      int32_t per_row, float *dst);
 
+/* ---- measurement --------------------------------------------------------------------- */
+/* No reference counterpart. Copies `bytes` (a multiple of 16) between two fresh device
+ * buffers with a plain 16-byte-per-lane copy kernel (k_copy_calibrate), `reps` times after
+ * one untimed run, and reports the mean kernel time. The read + write bytes of that kernel
+ * are known exactly, so profiler byte counters read over it give the scale that turns the
+ * same counters over another kernel into bytes; *gbps is the measured copy bandwidth, a
+ * practical HBM ceiling beside the datasheet figure. */
+int sh_copy_calibrate(size_t bytes, int32_t reps, double *ms_per_copy, double *gbps);
+
 /* ---- host helpers (no device work) -------------------------------------------------- */
 /* Deterministic synthetic weights, replacing stories.RandomInit (weights.go:124-153) for
  * the N(0, std) configurations: element i of tensor `tensor_id` is a Box-Muller normal of

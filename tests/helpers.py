@@ -84,3 +84,35 @@ def torch_forward_f64(cfg, w, tokens, alpha=None):
 def deepnet_alpha(n_layers):
     """ane/storiesane/residual.go:9: 1/sqrt(2*NLayers), as float32."""
     return float(np.float32(1.0 / math.sqrt(2.0 * n_layers)))
+
+
+# ---- llama2.c files (ane/stories/weights.go:49-122, tokenizer.go:16-97) --------------------
+
+LLAMA2_ORDER = ("rms_att", "wq", "wk", "wv", "wo", "rms_ffn", "w1", "w2", "w3")
+
+
+def write_llama2_bin(path, cfg, w, seq_len=None, negative_vocab=False):
+    """Writes `w` in the llama2.c checkpoint layout LoadPretrained reads: the seven-int32
+    header, embed, then each per-layer tensor for all layers in LLAMA2_ORDER, rms_final."""
+    vocab = -cfg.vocab if negative_vocab else cfg.vocab
+    hdr = np.array([cfg.dim, cfg.hidden, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, vocab,
+                    cfg.max_seq if seq_len is None else seq_len], "<i4")
+    with open(path, "wb") as f:
+        f.write(hdr.tobytes())
+        f.write(np.ascontiguousarray(w.embed, "<f4").tobytes())
+        for key in LLAMA2_ORDER:
+            for lw in w.layers:
+                f.write(np.ascontiguousarray(lw[key], "<f4").tobytes())
+        f.write(np.ascontiguousarray(w.rms_final, "<f4").tobytes())
+
+
+def write_tokenizer_bin(path, pieces, max_len=None):
+    """tokenizer.bin: int32 max_token_len, then per id (float32 score, int32 len, bytes)."""
+    blobs = [p.encode("utf-8") if isinstance(p, str) else p for p in pieces]
+    ml = max(1, max(len(b) for b in blobs)) if max_len is None else max_len
+    with open(path, "wb") as f:
+        f.write(np.array([ml], "<i4").tobytes())
+        for i, b in enumerate(blobs):
+            f.write(np.array([-float(i)], "<f4").tobytes())
+            f.write(np.array([len(b)], "<i4").tobytes())
+            f.write(b)

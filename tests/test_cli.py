@@ -1,0 +1,158 @@
+"""The stories-generate host program (cmd/stories-generate-go/main.go counterpart): llama2.c
+model and tokenizer file readers and flag handling on the CPU (-inspect / -detokenize touch
+no GPU); greedy and sampled decodes through the C ABI on the GPU."""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+import stories_hip as sh
+from helpers import LLAMA2_ORDER, tiny_config, write_llama2_bin, write_tokenizer_bin
+
+CLI = os.path.join(os.path.dirname(sh.LIB_PATH), "stories-generate")
+
+
+def run(*args, check=True):
+    if not os.path.exists(CLI):
+        pytest.fail(f"{CLI} is not built (make -C ane-training-experiments_amd)")
+    p = subprocess.run([CLI, *map(str, args)], capture_output=True, text=True, timeout=300)
+    if check and p.returncode != 0:
+        raise AssertionError(f"exit {p.returncode}: {p.stderr}")
+    return p
+
+
+def distinct_weights(cfg, seed):
+    """Weights whose tensors all have different sums, so a swapped read order shows."""
+    w = sh.synth_weights(cfg, seed=seed, std=0.05)
+    for l, lw in enumerate(w.layers):
+        for j, k in enumerate(LLAMA2_ORDER):
+            lw[k] = (lw[k] + np.float32(0.001 * (1 + j + 10 * l))).astype(np.float32)
+    w.rms_final = (w.rms_final * np.float32(1.5)).astype(np.float32)
+    return w
+
+
+def gqa_file_config():
+    return tiny_config(n_heads=4, n_kv_heads=2, max_seq=64)
+
+
+def test_inspect_reads_llama2_layout(tmp_path):
+    cfg = gqa_file_config()
+    w = distinct_weights(cfg, 301)
+    path = tmp_path / "m.bin"
+    write_llama2_bin(path, cfg, w)
+    got = json.loads(run("-model", path, "-inspect").stdout)
+    assert got["header"] == {"dim": 128, "hidden": 256, "n_layers": 2, "n_heads": 4,
+                             "n_kv_heads": 2, "vocab": 512, "seq_len": 64}
+    assert got["shared_classifier"] is True
+    want = {"embed": w.embed, "rms_final": w.rms_final}
+    for k in LLAMA2_ORDER:
+        want[k] = np.concatenate([lw[k].ravel() for lw in w.layers])
+    for k, v in want.items():
+        assert got["sums"][k] == pytest.approx(float(np.sum(v, dtype=np.float64)), rel=1e-12, abs=1e-12), k
+
+
+def test_inspect_negative_vocab_and_errors(tmp_path):
+    cfg = gqa_file_config()
+    w = distinct_weights(cfg, 302)
+    path = tmp_path / "neg.bin"
+    write_llama2_bin(path, cfg, w, negative_vocab=True)
+    got = json.loads(run("-model", path, "-inspect").stdout)
+    assert got["header"]["vocab"] == -512 and got["shared_classifier"] is False
+    # truncated inside layer 1's w3: the error names the tensor (weights.go:116-118)
+    data = path.read_bytes()
+    cut = tmp_path / "cut.bin"
+    cut.write_bytes(data[:len(data) - 4 * cfg.dim - 100])
+    p = run("-model", cut, "-inspect", check=False)
+    assert p.returncode == 1 and "read w3[1]: unexpected EOF" in p.stderr
+    cut.write_bytes(data[:20])
+    p = run("-model", cut, "-inspect", check=False)
+    assert p.returncode == 1 and "read config: unexpected EOF" in p.stderr
+    bad = tmp_path / "bad.bin"
+    bad.write_bytes(np.array([128, 256, 2, 5, 5, 512, 64], "<i4").tobytes())
+    p = run("-model", bad, "-inspect", check=False)
+    assert p.returncode == 1 and "config mismatch" in p.stderr
+    p = run("-model", tmp_path / "missing.bin", "-inspect", check=False)
+    assert p.returncode == 1 and "open" in p.stderr
+
+
+def test_detokenize(tmp_path):
+    pieces = ["<unk>", "<s>", "</s>"] + [f"p{i}" for i in range(3, 32000)]
+    pieces[65] = "<0x41>"      # byte token -> "A"
+    pieces[66] = "<0x0a>"      # lowercase hex -> "\n"
+    pieces[67] = "<0xZZ>"      # not hex: kept literally
+    pieces[68] = "<0x4>"       # wrong length: kept literally
+    pieces[69] = " world"
+    path = tmp_path / "tok.bin"
+    write_tokenizer_bin(path, pieces)
+    p = run("-tokenizer", path, "-detokenize", "65,69,66,67,68,-1,32000,5")
+    assert p.stdout == "text=A world\n<0xZZ><0x4>p5\n"
+    bad = tmp_path / "bad.bin"
+    write_tokenizer_bin(bad, pieces, max_len=0)
+    p = run("-tokenizer", bad, "-detokenize", "5", check=False)
+    assert p.returncode == 1 and "bad tokenizer header: max token len=0" in p.stderr
+    short = tmp_path / "short.bin"
+    write_tokenizer_bin(short, pieces[:100])
+    p = run("-tokenizer", short, "-detokenize", "5", check=False)
+    assert p.returncode == 1 and "unexpected EOF at token 100" in p.stderr
+
+
+def test_flag_errors():
+    p = run("-no-such-flag", "1", check=False)
+    assert p.returncode == 1 and "flag provided but not defined: -no-such-flag" in p.stderr
+    p = run("-prompt-ids", "1,x", "-inspect", check=False)
+    assert p.returncode == 1
+
+
+# ---- GPU ---------------------------------------------------------------------------------
+
+@pytest.mark.gpu
+def test_cli_greedy_decode_of_llama2_file_matches_oracle(tmp_path):
+    """-model file, -temperature 0: the token stream equals the oracle's greedy decode of the
+    same file weights (fp16-rounded), config from the file header (theta 1e4, eps 1e-5)."""
+    cfg = gqa_file_config()
+    w = sh.synth_weights(cfg, seed=311, std=0.08)
+    path = tmp_path / "m.bin"
+    write_llama2_bin(path, cfg, w)
+    p = run("-model", path, "-prompt-ids", "5, 9,11", "-max-new", "40", "-temperature", "0",
+            "-seq", "64", "-seed", "1")
+    lines = p.stdout.splitlines()
+    assert lines[0].startswith("source=pretrained prompt_tokens=3 ")
+    got = [int(t) for t in lines[1].split("=", 1)[1].split(",")]
+    assert lines[2] == "text=(tokenizer not provided)"
+    ref = oracle.Decoder(oracle.config_from(cfg), w.rounded(sh.SH_DTYPE_F16), threads=4)
+    want, eos, _ = ref.greedy_decode([5, 9, 11], 40)
+    assert got == want.tolist()
+    assert f"generated_tokens={len(got) - 3} " in lines[0] and f"eos={'true' if eos else 'false'}" in lines[0]
+
+
+@pytest.mark.gpu
+def test_cli_sampled_decode_is_seeded(tmp_path):
+    """-temperature 0.8: ids drawn on the host from device logits; the same -seed gives the
+    same stream (the reference's math/rand stream itself is not reproduced)."""
+    cfg = gqa_file_config()
+    path = tmp_path / "m.bin"
+    write_llama2_bin(path, cfg, sh.synth_weights(cfg, seed=321, std=0.08))
+    a = run("-model", path, "-prompt-ids", "1", "-max-new", "30", "-temperature", "0.8",
+            "-seq", "64", "-seed", "7").stdout.splitlines()[1]
+    b = run("-model", path, "-prompt-ids", "1", "-max-new", "30", "-temperature", "0.8",
+            "-seq", "64", "-seed", "7").stdout.splitlines()[1]
+    assert a == b
+    ids = [int(t) for t in a.split("=", 1)[1].split(",")]
+    assert all(0 <= t < cfg.vocab for t in ids) and len(ids) >= 2
+
+
+@pytest.mark.gpu
+def test_cli_bench_mode_stories110m():
+    p = run("-shape", "stories110m", "-prompt-len", "16", "-prompt-seed", "1", "-max-new", "128",
+            "-bench-steps", "2", "-bench-warmup", "1")
+    r = json.loads(p.stdout)
+    assert r["steps"] == 2 and len(r["gpu_ms"]) == 2 and r["persistent"] == 1
+    assert r["forwards"] == [143, 143] and r["generated"] == [128, 128]
+    cfg = sh.stories110m_config()
+    w = sh.synth_weights(cfg, seed=0, std=0.02)
+    ref = oracle.Decoder(oracle.config_from(cfg), w.rounded(sh.SH_DTYPE_F16), threads=16)
+    want, _, _ = ref.greedy_decode(sh.synth_tokens(16, 1, cfg.vocab), 128)
+    assert r["tokens"] == want.tolist()
