@@ -54,7 +54,6 @@ bool valid_config(const sh_config &c, int dtype) {
     if (!gemv_supported(c.dim, true)) return fail("dim has no GEMV tiling");
     if (!gemv_supported(qdim, false)) return fail("n_heads*head_dim has no GEMV tiling");
     if (!gemv_supported(c.hidden, false)) return fail("hidden has no GEMV tiling");
-    if (dtype == SH_DTYPE_W8A8) return fail("W8A8 decode is not available in this build");
     return true;
 }
 
@@ -69,12 +68,14 @@ double forward_bytes(const sh_model *m, int pos) {
     const double eb = (double)weight_elem_bytes(m->dtype);
     const double D = c.dim, F = c.hidden, Q = m->qdim, KV = m->kvdim;
     double per_layer = eb * ((Q + 2 * KV) * D + D * Q + 2 * F * D + D * F) + 4.0 * 2 * D;
+    if (m->dtype == SH_DTYPE_W8A8) per_layer += 4.0 * ((Q + 2 * KV) + D + 2 * F + D);  // row scales
     if (c.qk_norm) per_layer += 4.0 * 2 * c.head_dim;
     const double kvb = (double)kv_elem_bytes(c.kv_dtype);
     per_layer += kvb * 2 * KV * (double)(pos + 1);  // K and V rows read
     per_layer += kvb * 2 * KV;                        // K and V row written
     double total = per_layer * c.n_layers;
     total += eb * (double)c.vocab * D + 4.0 * D;      // classifier rows + final norm
+    if (m->dtype == SH_DTYPE_W8A8) total += 4.0 * c.vocab;   // classifier row scales
     total += 2.0 * D;                                 // embedding row
     total += 4.0 * c.vocab;                           // logits written
     return total;
@@ -407,6 +408,12 @@ sh_model *sh_model_create(const sh_config *cfg, int32_t dtype) {
             m->persistent ? "persistent decode kernel, grid " + std::to_string(m->p_grid) + " (" + why + ")"
                           : "per-stage kernels in a HIP graph (" + why + ")";
         snprintf(m->path_note, sizeof(m->path_note), "%s", note.c_str());
+        if (w8 && !m->persistent) {
+            // the per-stage kernels have no int8 GEMV; W8A8 runs only in the persistent kernel
+            set_error("invalid config: W8A8 decode needs a persistent-kernel shape (" + why + ")");
+            sh_model_destroy(m);
+            return nullptr;
+        }
     }
     if (m->persistent) {
         const size_t lpb = persistent_layer_ptr_bytes(c.n_layers);
@@ -726,6 +733,44 @@ int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *l
     m->last.persistent = 0;
     m->last.grid = 0;
     return 0;
+}
+
+int sh_decode_tap(const sh_model *m, int32_t which, float *out, int32_t n) {
+    if (!m || !out) {
+        set_error("sh_decode_tap: bad arguments");
+        return -1;
+    }
+    const sh_config &c = m->cfg;
+    int len = 0;
+    const float *dense = nullptr;      // per-stage path buffers (fp32)
+    const uint64_t *words = nullptr;   // persistent path hand-over words (value | epoch)
+    switch (which) {
+    case SH_TAP_X: len = c.dim; dense = m->x; words = m->ll_x; break;
+    case SH_TAP_QKV: len = m->qkv_rows; dense = m->qkv; words = m->ll_qkv; break;
+    case SH_TAP_ATT: len = m->qdim; dense = m->att; words = m->ll_att; break;
+    case SH_TAP_GATE: len = c.hidden; dense = m->gate; words = m->ll_gate; break;
+    case SH_TAP_X2: len = c.dim; dense = m->x2; words = m->ll_x2; break;
+    default:
+        set_error("sh_decode_tap: unknown tap");
+        return -1;
+    }
+    if (n != len) {
+        set_error("sh_decode_tap: n must be " + std::to_string(len));
+        return -1;
+    }
+    (void)hipSetDevice(m->device);
+    if (!hip_ok(hipStreamSynchronize(m->stream), "tap sync")) return -1;
+    if (m->persistent) {
+        std::vector<uint64_t> w(len);
+        if (!hip_ok(hipMemcpy(w.data(), words, 8 * (size_t)len, hipMemcpyDeviceToHost), "tap read"))
+            return -1;
+        for (int i = 0; i < len; i++) {
+            const uint32_t b = (uint32_t)w[i];
+            memcpy(&out[i], &b, 4);
+        }
+        return 0;
+    }
+    return hip_ok(hipMemcpy(out, dense, 4 * (size_t)len, hipMemcpyDeviceToHost), "tap read") ? 0 : -1;
 }
 
 int sh_trace_forward(sh_model *m, int32_t forward) {

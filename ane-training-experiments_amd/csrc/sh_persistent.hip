@@ -57,7 +57,8 @@ constexpr int kMaxGroup = 2;       // q heads per kv head
 constexpr int kKvStage = 96 * 1024; // LDS bytes for one kv head's cached K and V rows
 
 struct LayerPtrs {
-    const uint16_t *wqkv, *wo, *w13, *w2;
+    const void *wqkv, *wo, *w13, *w2;          // fp16 / bf16 bits, or int8 (W8A8)
+    const float *s_qkv, *s_o, *s_13, *s_2;     // W8A8 per-row weight scales
     const float *rms_att, *rms_ffn, *q_norm, *k_norm;
 };
 
@@ -67,7 +68,9 @@ struct PParams {
     double eps, qk_eps;
     int qk_norm;
     const LayerPtrs *layers;
-    const uint16_t *embed, *cls;
+    const uint16_t *embed;
+    const void *cls;
+    const float *s_cls;                        // W8A8 classifier row scales
     const float *rms_final;
     void *kcache, *vcache;
     const float *rope_cos, *rope_sin;
@@ -85,10 +88,11 @@ struct PParams {
 __device__ __forceinline__ float h2f(uint32_t b) {
     return __half2float(__ushort_as_half((unsigned short)b));
 }
+// 16-bit value of a lookup table (embedding rows): fp16 for F16 and W8A8 models, bf16 for BF16.
 template <int WT>
 __device__ __forceinline__ float w2f(uint32_t b) {
-    if constexpr (WT == SH_DTYPE_F16) return h2f(b);
-    else return __uint_as_float(b << 16);
+    if constexpr (WT == SH_DTYPE_BF16) return __uint_as_float(b << 16);
+    else return h2f(b);
 }
 __device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
 __device__ __forceinline__ uint16_t f2bf(float f) {
@@ -183,6 +187,34 @@ __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
     for (int off = N / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;
+}
+template <int N>
+__device__ __forceinline__ int group_sum_i(int v) {
+#pragma unroll
+    for (int off = N / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float block_max_d(float v, double *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    lds_barrier();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = (double)v;
+    lds_barrier();
+    float m = (float)red[0];
+    for (int w = 1; w < kPW; w++) m = fmaxf(m, (float)red[w]);
+    return m;
+}
+
+// Elements per 16-byte weight chunk and bytes per weight element.
+template <int WT> constexpr int chunk_elems() { return WT == SH_DTYPE_W8A8 ? 16 : 8; }
+template <int WT> constexpr int elem_bytes() { return WT == SH_DTYPE_W8A8 ? 1 : 2; }
+
+// The bridge quantizer for one value (ane_bridge.m:390-396): x / scale with IEEE division,
+// clamp to [-128, 127], round half away from zero by +-0.5 and truncation.
+__device__ __forceinline__ uint32_t quant8(float x, float scale) {
+    float v = __fdiv_rn(x, scale);
+    v = fminf(fmaxf(v, -128.0f), 127.0f);
+    return (uint32_t)(int)(v >= 0.0f ? v + 0.5f : v - 0.5f) & 0xffu;
 }
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
@@ -311,7 +343,7 @@ __device__ __forceinline__ bool ll_wait_vec(const uint64_t *src, int n, uint32_t
 template <int WT, int COLS>
 __device__ __forceinline__ bool stage_input(float *xs, int n, const uint64_t *ll, uint32_t e,
                             const uint16_t *emb_row, const float *gain, double eps, double *red,
-                            const PParams &p) {
+                            const PParams &p, uint32_t *xq, float *sa) {
     if (emb_row) {
         for (int i = threadIdx.x; i < n; i += kPB) xs[i] = w2f<WT>(emb_row[i]);
         lds_barrier();
@@ -324,6 +356,20 @@ __device__ __forceinline__ bool stage_input(float *xs, int n, const uint64_t *ll
         const double tot = block_sum_d(ss, red);
         const float rrms = (float)(1.0 / sqrt(tot / (double)n + eps));
         for (int i = threadIdx.x; i < n; i += kPB) xs[i] = xs[i] * rrms * gain[i];
+        lds_barrier();
+    }
+    if constexpr (WT == SH_DTYPE_W8A8) {
+        // per-tensor activation quantization (W8A8 decode): s_a = max|x|/127 (0 -> 1),
+        // stored as packed int8 words for v_dot4_i32_i8
+        float mx = 0.0f;
+        for (int i = threadIdx.x; i < n; i += kPB) mx = fmaxf(mx, fabsf(xs[i]));
+        mx = block_max_d(mx, red);
+        float s = __fdiv_rn(mx, 127.0f);
+        if (s == 0.0f) s = 1.0f;
+        *sa = s;
+        for (int i = threadIdx.x; i < n / 4; i += kPB)
+            xq[i] = quant8(xs[4 * i], s) | quant8(xs[4 * i + 1], s) << 8 |
+                    quant8(xs[4 * i + 2], s) << 16 | quant8(xs[4 * i + 3], s) << 24;
         lds_barrier();
     }
     return true;
@@ -346,10 +392,15 @@ struct StageIO {
 // the input is polled. Returns false on timeout/abort. For E_CLS, *best_v/*best_i receive
 // this wave's (max, first index).
 template <int LPR, int CPL, int WT, int U>
-__device__ __forceinline__ bool gemv_stage(const PParams &p, const uint16_t *__restrict__ W, int rows, int cols,
-                           int epi, const StageIO &io, float *xs, double *red, float &best_v,
-                           int &best_i) {
+__device__ __forceinline__ bool gemv_stage(const PParams &p, const void *__restrict__ W,
+                           const float *__restrict__ wscale, int rows, int cols,
+                           int epi, const StageIO &io, float *xs, uint32_t *xq, double *red,
+                           float &best_v, int &best_i) {
     constexpr int G = 64 / LPR;
+    constexpr int EPC = chunk_elems<WT>();
+    constexpr bool Q8 = WT == SH_DTYPE_W8A8;
+    const SH_GLOBAL uint8_t *Wb = (const SH_GLOBAL uint8_t *)W;
+    const size_t row_bytes = (size_t)cols * elem_bytes<WT>();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane % LPR, grp = lane / LPR;
     const int NW = gridDim.x * kPW;
@@ -364,33 +415,52 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const uint16_t *__r
     for (int u = 0; u < U; u++) {
         const int row = (vw + u * NW) * G + grp;
         if (row < rows) {
-            const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(W + (size_t)row * cols);
+            const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(Wb + (size_t)row * row_bytes);
 #pragma unroll
             for (int j = 0; j < CPL; j++) w[u][j] = src[sub + j * LPR];
         }
     }
-    if (!stage_input<WT, LPR * CPL * 8>(xs, cols, io.in_ll, io.e_in, io.emb_row, io.gain, p.eps, red, p))
+    float sa = 1.0f;
+    if (!stage_input<WT, LPR * CPL * EPC>(xs, cols, io.in_ll, io.e_in, io.emb_row, io.gain, p.eps,
+                                          red, p, xq, &sa))
         return false;
-    float xr[CPL * 8];
+    // this lane's slice of the input: floats, or packed int8 words for W8A8
+    float xr[Q8 ? 1 : CPL * 8];
+    uint32_t xr8[Q8 ? CPL * 4 : 1];
 #pragma unroll
-    for (int j = 0; j < CPL; j++)
+    for (int j = 0; j < CPL; j++) {
+        if constexpr (Q8) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) xr[j * 8 + e] = xs[(sub + j * LPR) * 8 + e];
+            for (int e = 0; e < 4; e++) xr8[j * 4 + e] = xq[(sub + j * LPR) * 4 + e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) xr[j * 8 + e] = xs[(sub + j * LPR) * 8 + e];
+        }
+    }
 
     bool ok = true;
     for (int g0 = vw; g0 < ngroups; g0 += U * NW) {
         float acc[U];
+        int acci[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             acc[u] = 0.f;
+            acci[u] = 0;
             const int row = (g0 + u * NW) * G + grp;
             if (row < rows) {
 #pragma unroll
                 for (int j = 0; j < CPL; j++) {
-                    float f[8];
-                    unpack8<WT>(w[u][j], f);
+                    if constexpr (Q8) {
+                        const uint32_t ww[4] = {w[u][j].x, w[u][j].y, w[u][j].z, w[u][j].w};
 #pragma unroll
-                    for (int e = 0; e < 8; e++) acc[u] = fmaf(f[e], xr[j * 8 + e], acc[u]);
+                        for (int e = 0; e < 4; e++)
+                            acci[u] = __builtin_amdgcn_sdot4((int)ww[e], (int)xr8[j * 4 + e], acci[u], false);
+                    } else {
+                        float f[8];
+                        unpack8<WT>(w[u][j], f);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) acc[u] = fmaf(f[e], xr[j * 8 + e], acc[u]);
+                    }
                 }
             }
         }
@@ -401,7 +471,7 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const uint16_t *__r
             for (int u = 0; u < U; u++) {
                 const int row = (gn + u * NW) * G + grp;
                 if (row < rows) {
-                    const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(W + (size_t)row * cols);
+                    const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(Wb + (size_t)row * row_bytes);
 #pragma unroll
                     for (int j = 0; j < CPL; j++) w[u][j] = src[sub + j * LPR];
                 }
@@ -410,7 +480,14 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const uint16_t *__r
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int row = (g0 + u * NW) * G + grp;
-            const float a = group_sum<LPR>(acc[u]);
+            float a;
+            if constexpr (Q8) {
+                // exact int32 dot, then (float)acc * (s_w[r] * s_a) (one fixed order)
+                const int ai = group_sum_i<LPR>(acci[u]);
+                a = row < rows ? (float)ai * (wscale[row] * sa) : 0.0f;
+            } else {
+                a = group_sum<LPR>(acc[u]);
+            }
             if (epi == E_GATE) {
                 const float h3 = __shfl_down(a, LPR, 64);
                 if (sub == 0 && (grp & 1) == 0 && row < rows) {
@@ -531,11 +608,17 @@ __device__ __forceinline__ void kv_unpack16(const u32x4 &v, float *f) {
 
 // Attention for kv head g (one workgroup) and its `group` query heads (infer.go:273-299).
 // q, k and v arrive through one batched poll; the cached rows were copied into LDS by
-// attn_prefetch, rows beyond the LDS capacity are read from the cache. Scores: one thread
-// per position, walking the head in an order rotated by the position so the LDS reads of a
-// wave fall in distinct banks. Softmax: one wave per head. P.V: one thread per (dim,
-// position group), partial sums combined through LDS.
-template <int KVT, int HD>
+// attn_prefetch, rows beyond the LDS capacity are read from the cache. Softmax: one wave
+// per head.
+// Default order (EXACT = false): scores one thread per position, walking the head in an
+// order rotated by the position so the LDS reads of a wave fall in distinct banks; P.V one
+// thread per (dim, position group), partial sums combined through LDS.
+// EXACT = true keeps the reference's float summation order, each product and sum rounded
+// on its own: a score is the sequential sum over i of q[i]*k[i] (infer.go:284-286), an
+// output element the sequential sum over t of p[t]*v[t][i] (:292-295). The W8A8 model
+// uses it: its activations are re-quantized after attention, and a last-bit difference
+// that moves x/s across a rounding boundary would change an int8 input.
+template <int KVT, int HD, bool EXACT>
 __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
                            float *ks, float *vs, float *sc, float *part, uint8_t *kvlds,
                            double *red, float *redf) {
@@ -572,8 +655,9 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
         float *v = h < group ? qs + h * hd : ks;
         const float c = p.rope_cos[pos * half + pi], s = p.rope_sin[pos * half + pi];
         const float ev = v[2 * pi], ov = v[2 * pi + 1];
-        v[2 * pi] = ev * c - ov * s;
-        v[2 * pi + 1] = ev * s + ov * c;
+        // each product rounded before the sum, as the reference computes it
+        v[2 * pi] = __fsub_rn(__fmul_rn(ev, c), __fmul_rn(ov, s));
+        v[2 * pi + 1] = __fadd_rn(__fmul_rn(ev, s), __fmul_rn(ov, c));
     }
     __builtin_amdgcn_s_waitcnt(0);   // the LDS copies of the cached rows have landed
     lds_barrier();
@@ -600,7 +684,7 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
             const SH_LDS u32x4 *row = (const SH_LDS u32x4 *)(kst + (size_t)t * S::RB);
 #pragma unroll 4
             for (int c0 = 0; c0 < NCH; c0++) {
-                const int c = (c0 + t) & (NCH - 1);
+                const int c = EXACT ? c0 : (c0 + t) & (NCH - 1);
                 float kf[EPC];
                 const u32x4 kv4 = row[c];
                 kv_unpack16<KVT>(kv4, kf);
@@ -611,10 +695,17 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
 #pragma unroll
                     for (int e4 = 0; e4 < EPC / 4; e4++) {
                         const f32x4 qv = q4[e4];
-                        d[h] = fmaf(qv.x, kf[4 * e4 + 0], d[h]);
-                        d[h] = fmaf(qv.y, kf[4 * e4 + 1], d[h]);
-                        d[h] = fmaf(qv.z, kf[4 * e4 + 2], d[h]);
-                        d[h] = fmaf(qv.w, kf[4 * e4 + 3], d[h]);
+                        if constexpr (EXACT) {
+                            d[h] = __fadd_rn(d[h], __fmul_rn(qv.x, kf[4 * e4 + 0]));
+                            d[h] = __fadd_rn(d[h], __fmul_rn(qv.y, kf[4 * e4 + 1]));
+                            d[h] = __fadd_rn(d[h], __fmul_rn(qv.z, kf[4 * e4 + 2]));
+                            d[h] = __fadd_rn(d[h], __fmul_rn(qv.w, kf[4 * e4 + 3]));
+                        } else {
+                            d[h] = fmaf(qv.x, kf[4 * e4 + 0], d[h]);
+                            d[h] = fmaf(qv.y, kf[4 * e4 + 1], d[h]);
+                            d[h] = fmaf(qv.z, kf[4 * e4 + 2], d[h]);
+                            d[h] = fmaf(qv.w, kf[4 * e4 + 3], d[h]);
+                        }
                     }
                 }
             }
@@ -624,16 +715,21 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
             for (int k = 0; k < hd; k++) {
                 const float kv = t == pos ? ks[k] : kv_ld<KVT>(p.kcache, rb + k);
 #pragma unroll
-                for (int h = 0; h < kMaxGroup; h++)
-                    if (h < group) d[h] = fmaf(qs[h * hd + k], kv, d[h]);
+                for (int h = 0; h < kMaxGroup; h++) {
+                    if (h >= group) continue;
+                    if constexpr (EXACT) d[h] = __fadd_rn(d[h], __fmul_rn(qs[h * hd + k], kv));
+                    else d[h] = fmaf(qs[h * hd + k], kv, d[h]);
+                }
             }
         }
 #pragma unroll
         for (int h = 0; h < kMaxGroup; h++)
-            if (h < group) sc[h * p.max_seq + t] = d[h] * p.inv_sqrt_hd;
+            if (h < group) sc[h * p.max_seq + t] = __fmul_rn(d[h], p.inv_sqrt_hd);
     }
     lds_barrier();
-    // infer.go:328-345 softmaxPrefix: wave h handles head h; sc then holds probabilities
+    // infer.go:328-345 softmaxPrefix: wave h handles head h; sc then holds probabilities.
+    // The float64 sum of the exp terms is combined in lane/tree order; that reorders float64
+    // additions only, a relative difference near 1e-16 before the sum is rounded to float.
     if (wave < group) {
         float *s = sc + wave * p.max_seq;
         float mx = -INFINITY;
@@ -651,6 +747,23 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
         for (int t = lane; t <= pos; t += 64) s[t] = s[t] * inv;
     }
     lds_barrier();
+    if constexpr (EXACT) {
+        // P.V in the reference's order: thread (h, i) sums p[t] * v[t][i] over t = 0..pos
+        for (int k = tid; k < group * hd; k += kPB) {
+            const int h = k / hd, ii = k % hd;
+            const float *ph = sc + h * p.max_seq;
+            const int tl = pos < S::ROWS ? pos : S::ROWS - 1;
+            float sum = 0.f;
+            for (int t = 0; t <= tl; t++) sum = __fadd_rn(sum, __fmul_rn(ph[t], kv_get<KVT>(vst + (size_t)t * S::RB, ii)));
+            for (int t = tl + 1; t <= pos; t++) {
+                const float vv = t == pos ? vs[ii] : kv_ld<KVT>(p.vcache, lbase + (size_t)t * p.kvdim + ii);
+                sum = __fadd_rn(sum, __fmul_rn(ph[t], vv));
+            }
+            ll_put(p.ll_att + (size_t)(g * group + h) * hd + ii, sum, e);
+        }
+        lds_barrier();
+        return true;
+    }
     // P.V (infer.go:290-297)
     const int vi = tid % hd, tg = tid / hd;
     float acc[kMaxGroup];
@@ -687,6 +800,7 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
 template <int WT, int KVT, int HD, int LD, int CD, int LQ, int CQ, int LF, int CF>
 __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     __shared__ float xs[kXs];
+    __shared__ __attribute__((aligned(16))) uint32_t xq[WT == SH_DTYPE_W8A8 ? kXs / 4 : 1];
     __shared__ __attribute__((aligned(16))) float qs[kMaxGroup * 256];
     __shared__ float ks[256], vs[256];
     __shared__ float sc[kScores];
@@ -729,12 +843,13 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.out_ll = p.ll_qkv;
             io.e_in = e - 1;
             io.e_out = e;
-            if (!gemv_stage<LD, CD, WT, 2>(p, Lp.wqkv, p.qkv_rows, p.D, E_STORE, io, xs, red, bv, bi))
+            if (!gemv_stage<LD, CD, WT, 2>(p, Lp.wqkv, Lp.s_qkv, p.qkv_rows, p.D, E_STORE, io, xs, xq, red, bv, bi))
                 return;
             stamp();
             // attention
             if ((int)blockIdx.x < p.KVH &&
-                !attn_stage<KVT, HD>(p, l, blockIdx.x, pos, e, qs, ks, vs, sc, part, kvlds, red, redf))
+                !attn_stage<KVT, HD, WT == SH_DTYPE_W8A8>(p, l, blockIdx.x, pos, e, qs, ks, vs, sc,
+                                                          part, kvlds, red, redf))
                 return;
             stamp();
             // wo + residual
@@ -746,7 +861,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.e_in = e;
             io.e_res = e - 1;
             io.e_out = e;
-            if (!gemv_stage<LQ, CQ, WT, 2>(p, Lp.wo, p.D, p.qdim, E_RESID, io, xs, red, bv, bi))
+            if (!gemv_stage<LQ, CQ, WT, 2>(p, Lp.wo, Lp.s_o, p.D, p.qdim, E_RESID, io, xs, xq, red, bv, bi))
                 return;
             stamp();
             // w1/w3 + silu gate
@@ -756,7 +871,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.out_ll = p.ll_gate;
             io.e_in = e;
             io.e_out = e;
-            if (!gemv_stage<LD, CD, WT, 2>(p, Lp.w13, 2 * p.F, p.D, E_GATE, io, xs, red, bv, bi))
+            if (!gemv_stage<LD, CD, WT, 2>(p, Lp.w13, Lp.s_13, 2 * p.F, p.D, E_GATE, io, xs, xq, red, bv, bi))
                 return;
             stamp();
             // w2 + residual
@@ -767,7 +882,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.e_in = e;
             io.e_res = e;
             io.e_out = e;
-            if (!gemv_stage<LF, CF, WT, 2>(p, Lp.w2, p.D, p.F, E_RESID, io, xs, red, bv, bi))
+            if (!gemv_stage<LF, CF, WT, 2>(p, Lp.w2, Lp.s_2, p.D, p.F, E_RESID, io, xs, xq, red, bv, bi))
                 return;
             stamp();
         }
@@ -777,7 +892,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
         io.in_ll = p.ll_x;
         io.gain = p.rms_final;
         io.e_in = base + (uint32_t)L;
-        if (!gemv_stage<LD, CD, WT, 2>(p, p.cls, p.V, p.D, E_CLS, io, xs, red, bv, bi)) return;
+        if (!gemv_stage<LD, CD, WT, 2>(p, p.cls, p.s_cls, p.V, p.D, E_CLS, io, xs, xq, red, bv, bi)) return;
         stamp();
         // this workgroup's (max, first index)
         {
@@ -852,21 +967,32 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
 
 typedef void (*PersistentKernel)(PParams);
 
-// Lanes per row of the three GEMV widths, matching pick_shape's instantiations.
-void shape_lanes(int D, int Q, int F, int *ld, int *lq, int *lf) {
-    if (D == 768 && Q == 768 && F == 2048) { *ld = 32; *lq = 32; *lf = 64; }
-    else if (D == 1024 && Q == 2048 && F == 3072) { *ld = 32; *lq = 64; *lf = 64; }
-    else { *ld = 16; *lq = 16; *lf = 32; }
+// Lanes per row of the three GEMV widths, matching pick_shape's instantiations. A row of
+// width C is covered by LPR lanes x CPL 16-byte chunks (8 fp16/bf16 or 16 int8 values).
+void shape_lanes(int dtype, int D, int Q, int F, int *ld, int *lq, int *lf) {
+    const bool q8 = dtype == SH_DTYPE_W8A8;
+    if (D == 768 && Q == 768 && F == 2048) { *ld = q8 ? 16 : 32; *lq = q8 ? 16 : 32; *lf = q8 ? 32 : 64; }
+    else if (D == 1024 && Q == 2048 && F == 3072) { *ld = 32; *lq = q8 ? 32 : 64; *lf = 64; }
+    else { *ld = q8 ? 8 : 16; *lq = q8 ? 8 : 16; *lf = q8 ? 16 : 32; }
 }
 
 template <int WT, int KVT>
 PersistentKernel pick_shape(int D, int Q, int F, int HDv) {
-    if (D == 768 && Q == 768 && F == 2048 && HDv == 64)
-        return &k_decode_persistent<WT, KVT, 64, 32, 3, 32, 3, 64, 4>;
-    if (D == 1024 && Q == 2048 && F == 3072 && HDv == 128)
-        return &k_decode_persistent<WT, KVT, 128, 32, 4, 64, 4, 64, 6>;
-    if (D == 128 && Q == 128 && F == 256 && HDv == 32)
-        return &k_decode_persistent<WT, KVT, 32, 16, 1, 16, 1, 32, 1>;
+    if constexpr (WT == SH_DTYPE_W8A8) {
+        if (D == 768 && Q == 768 && F == 2048 && HDv == 64)
+            return &k_decode_persistent<WT, KVT, 64, 16, 3, 16, 3, 32, 4>;
+        if (D == 1024 && Q == 2048 && F == 3072 && HDv == 128)
+            return &k_decode_persistent<WT, KVT, 128, 32, 2, 32, 4, 64, 3>;
+        if (D == 128 && Q == 128 && F == 256 && HDv == 32)
+            return &k_decode_persistent<WT, KVT, 32, 8, 1, 8, 1, 16, 1>;
+    } else {
+        if (D == 768 && Q == 768 && F == 2048 && HDv == 64)
+            return &k_decode_persistent<WT, KVT, 64, 32, 3, 32, 3, 64, 4>;
+        if (D == 1024 && Q == 2048 && F == 3072 && HDv == 128)
+            return &k_decode_persistent<WT, KVT, 128, 32, 4, 64, 4, 64, 6>;
+        if (D == 128 && Q == 128 && F == 256 && HDv == 32)
+            return &k_decode_persistent<WT, KVT, 32, 16, 1, 16, 1, 32, 1>;
+    }
     return nullptr;
 }
 
@@ -880,6 +1006,11 @@ PersistentKernel pick_persistent(int dtype, int kv, int D, int Q, int F, int HDv
         if (kv == SH_KV_F32) return pick_shape<SH_DTYPE_BF16, SH_KV_F32>(D, Q, F, HDv);
         if (kv == SH_KV_F16) return pick_shape<SH_DTYPE_BF16, SH_KV_F16>(D, Q, F, HDv);
         return pick_shape<SH_DTYPE_BF16, SH_KV_BF16>(D, Q, F, HDv);
+    }
+    if (dtype == SH_DTYPE_W8A8) {
+        if (kv == SH_KV_F32) return pick_shape<SH_DTYPE_W8A8, SH_KV_F32>(D, Q, F, HDv);
+        if (kv == SH_KV_F16) return pick_shape<SH_DTYPE_W8A8, SH_KV_F16>(D, Q, F, HDv);
+        return pick_shape<SH_DTYPE_W8A8, SH_KV_BF16>(D, Q, F, HDv);
     }
     return nullptr;
 }
@@ -917,7 +1048,7 @@ hipError_t persistent_grid(const sh_model *m, int *grid_out, std::string *why) {
     // in order, which is what keeps single-buffered hand-over vectors safe.
     int grid = cus;
     int ld = 0, lq = 0, lf = 0;
-    shape_lanes(c.dim, m->qdim, c.hidden, &ld, &lq, &lf);
+    shape_lanes(m->dtype, c.dim, m->qdim, c.hidden, &ld, &lq, &lf);
     auto groups = [](int rows, int lpr) { return (rows + 64 / lpr - 1) / (64 / lpr); };
     grid = std::min(grid, groups(m->qkv_rows, ld));
     grid = std::min(grid, groups(c.dim, lq));
@@ -953,7 +1084,8 @@ hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt
     p.qk_norm = c.qk_norm;
     p.layers = (const LayerPtrs *)m->p_layers;
     p.embed = (const uint16_t *)m->embed;
-    p.cls = (const uint16_t *)m->cls;
+    p.cls = m->cls;
+    p.s_cls = m->s_cls;
     p.rms_final = m->rms_final;
     p.kcache = m->kcache;
     p.vcache = m->vcache;
@@ -988,10 +1120,14 @@ void persistent_fill_layer_ptrs(const sh_model *m, void *host) {
     LayerPtrs *lp = (LayerPtrs *)host;
     for (int l = 0; l < m->cfg.n_layers; l++) {
         const LayerDev &L = m->layers[l];
-        lp[l].wqkv = (const uint16_t *)L.wqkv;
-        lp[l].wo = (const uint16_t *)L.wo;
-        lp[l].w13 = (const uint16_t *)L.w13;
-        lp[l].w2 = (const uint16_t *)L.w2;
+        lp[l].wqkv = L.wqkv;
+        lp[l].wo = L.wo;
+        lp[l].w13 = L.w13;
+        lp[l].w2 = L.w2;
+        lp[l].s_qkv = L.s_qkv;
+        lp[l].s_o = L.s_o;
+        lp[l].s_13 = L.s_13;
+        lp[l].s_2 = L.s_2;
         lp[l].rms_att = L.rms_att;
         lp[l].rms_ffn = L.rms_ffn;
         lp[l].q_norm = L.q_norm;

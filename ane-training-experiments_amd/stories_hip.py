@@ -28,6 +28,7 @@ SH_DTYPE_W8A8 = 3
 SH_KV_F32 = 0
 SH_KV_F16 = 1
 SH_KV_BF16 = 2
+SH_TAP_X, SH_TAP_QKV, SH_TAP_ATT, SH_TAP_GATE, SH_TAP_X2 = 0, 1, 4, 5, 6
 
 BOS = 1
 EOS = 2
@@ -87,6 +88,7 @@ _lib = None
 # every entry point of include/stories_hip.h with its ctypes signature
 SIGNATURES = {
     "sh_init": (C.c_int, [C.c_int32]),
+    "sh_decode_tap": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_float), C.c_int32]),
     "sh_copy_calibrate": (C.c_int, [C.c_size_t, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "sh_last_error": (C.c_size_t, [C.c_char_p, C.c_size_t]),
     "sh_config_stories110m": (C.c_int, [C.POINTER(ShConfig)]),
@@ -312,6 +314,14 @@ class Model:
         out = np.empty((self.cfg.vocab, t.size), np.float32)
         _check(self.lib.sh_prefill_logits(self.h, t.ctypes.data_as(C.POINTER(C.c_uint16)), t.size, _fp(out)),
                "sh_prefill_logits")
+        return out
+
+    def tap(self, which: int) -> np.ndarray:
+        """sh_decode_tap: an intermediate vector of the last layer of the last forward."""
+        n = {SH_TAP_X: self.cfg.dim, SH_TAP_QKV: self.cfg.qdim + 2 * self.cfg.kvdim,
+             SH_TAP_ATT: self.cfg.qdim, SH_TAP_GATE: self.cfg.hidden, SH_TAP_X2: self.cfg.dim}[which]
+        out = np.empty(n, np.float32)
+        _check(self.lib.sh_decode_tap(self.h, which, _fp(out), n), "sh_decode_tap")
         return out
 
     def trace_forward(self, forward: int) -> None:

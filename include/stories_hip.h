@@ -125,6 +125,14 @@ size_t sh_model_describe(const sh_model *m, char *buf, size_t len);
  * -1 when the model does not run the persistent kernel. */
 int sh_trace_forward(sh_model *m, int32_t forward);
 int sh_trace_read(sh_model *m, int64_t *out, int32_t cap, int32_t *n_out, double *ticks_per_s);
+/* Intermediate vectors of the last layer of the last token forward (the counterpart of the
+ * reference engine's cache taps, ane/storiesane/engine_test.go:154-239, which compare the
+ * engine's x2/q/k/v/att outputs with the CPU functions). which: SH_TAP_X the layer output
+ * (D), SH_TAP_QKV the q|k|v projection before QK-norm and RoPE (H*hd + 2*KVH*hd),
+ * SH_TAP_ATT attention output (H*hd), SH_TAP_GATE silu(W1 x) * W3 x (F), SH_TAP_X2 the
+ * residual after attention (D). n must equal that length. */
+enum { SH_TAP_X = 0, SH_TAP_QKV = 1, SH_TAP_ATT = 4, SH_TAP_GATE = 5, SH_TAP_X2 = 6 };
+int sh_decode_tap(const sh_model *m, int32_t which, float *out, int32_t n);
 /* Timing of the last sh_greedy_decode / sh_prefill_logits call. */
 int sh_stats(const sh_model *m, sh_timing *out);
 /* (*Engine).Close (engine.go:480): frees device memory. NULL is allowed. */

@@ -449,6 +449,7 @@ const float *or_decoder_tap(const or_decoder *d, int which) {
     case 3: return d->v;
     case 4: return d->att;
     case 5: return d->h1;
+    case 6: return d->x2;
     default: return d->logits;
     }
 }

@@ -80,7 +80,8 @@ int or_forward_one(or_decoder *d, int token, int pos, float *logits_out);
 int or_greedy_decode(or_decoder *d, const int32_t *prompt, int n_prompt, int max_new,
                      int32_t *out_tokens, int32_t *n_out, int32_t *stopped_eos,
                      float *margins);
-/* Debug taps of the last forward_one: 0 x(residual out), 1 q, 2 k, 3 v, 4 att, 5 gate. */
+/* Debug taps of the last forward_one (last layer): 0 x (residual out), 1 q and 2 k (after
+ * QK-norm and RoPE), 3 v, 4 att, 5 gate, 6 x2 (residual after attention). */
 const float *or_decoder_tap(const or_decoder *d, int which);
 
 /* ---- full-sequence channel-first forward (ane/storiesane/engine.go:804-842) ---- */
