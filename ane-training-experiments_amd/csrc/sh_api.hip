@@ -479,6 +479,8 @@ void sh_model_destroy(sh_model *m) {
     (void)hipFree(m->p_err);
     (void)hipFree(m->trace_buf);
     (void)hipFree(m->pf_arena);
+    if (m->bt_ready) (void)hipGraphExecDestroy(m->bt_exec);
+    (void)hipFree(m->bt_arena);
     if (m->ev0) (void)hipEventDestroy(m->ev0);
     if (m->ev1) (void)hipEventDestroy(m->ev1);
     if (m->stream) (void)hipStreamDestroy(m->stream);
@@ -696,6 +698,7 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
     m->last.bytes_per_forward_mean = forwards ? bytes / forwards : 0;
     m->last.persistent = m->persistent ? 1 : 0;
     m->last.grid = m->persistent ? m->p_grid : 0;
+    m->last.prefill_ms = 0;
     return 0;
 }
 
@@ -711,13 +714,20 @@ int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *l
         return -1;
     }
     (void)hipSetDevice(m->device);
-    if (!hip_ok(prefill_alloc(m, seq), "prefill scratch")) return -1;
-    std::vector<int32_t> ids(tokens, tokens + seq);   // out-of-range ids embed as zeros
-    if (!hip_ok(hipMemcpyAsync(m->pf_tokens, ids.data(), sizeof(int32_t) * seq,
-                               hipMemcpyHostToDevice, m->stream), "prefill tokens"))
+    if (!hip_ok(prefill_alloc(m, seq, true), "prefill scratch")) return -1;
+    // rows: the ids (out-of-range ones embed as zeros), positions 0..seq-1, one sequence
+    std::vector<int32_t> rows(3 * (size_t)seq);
+    for (int t = 0; t < seq; t++) {
+        rows[t] = tokens[t];
+        rows[seq + t] = t;
+        rows[2 * (size_t)seq + t] = 0;
+    }
+    if (!hip_ok(hipMemcpyAsync(m->pf_tokens, rows.data(), 4 * (size_t)seq, hipMemcpyHostToDevice, m->stream), "prefill tokens") ||
+        !hip_ok(hipMemcpyAsync(m->pf_rowpos, rows.data() + seq, 4 * (size_t)seq, hipMemcpyHostToDevice, m->stream), "prefill rows") ||
+        !hip_ok(hipMemcpyAsync(m->pf_rowseq, rows.data() + 2 * (size_t)seq, 4 * (size_t)seq, hipMemcpyHostToDevice, m->stream), "prefill rows"))
         return -1;
     if (!hip_ok(hipEventRecord(m->ev0, m->stream), "event")) return -1;
-    if (!hip_ok(enqueue_prefill(m, seq, true, -1), "prefill")) return -1;
+    if (!hip_ok(enqueue_prefill(m, seq, seq, true, false), "prefill")) return -1;
     if (!hip_ok(hipEventRecord(m->ev1, m->stream), "event")) return -1;
     const size_t n = (size_t)m->cfg.vocab * seq;
     if (!hip_ok(hipMemcpyAsync(logits_cf, m->pf_logits, sizeof(float) * n,
@@ -730,6 +740,134 @@ int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *l
     m->last.forwards = 1;
     m->last.tokens_out = seq;
     m->last.bytes_per_forward_mean = prefill_bytes(m, seq);
+    m->last.persistent = 0;
+    m->last.grid = 0;
+    m->last.prefill_ms = ms;
+    return 0;
+}
+
+// Algorithmic bytes of one batched step with every sequence at position pos: the weights once,
+// then per sequence its K/V rows 0..pos read, one K/V row written, the logits written and
+// read back by the argmax, and its embedding row.
+double batch_step_bytes(const sh_model *m, int B, int pos) {
+    const sh_config &c = m->cfg;
+    const double eb = (double)weight_elem_bytes(m->dtype);
+    const double D = c.dim, F = c.hidden, Q = m->qdim, KV = m->kvdim;
+    double w = (eb * ((Q + 2 * KV) * D + D * Q + 2 * F * D + D * F) + 4.0 * 2 * D) * c.n_layers;
+    if (c.qk_norm) w += 4.0 * 2 * c.head_dim * c.n_layers;
+    w += eb * (double)c.vocab * D + 4.0 * D;
+    const double kvb = (double)kv_elem_bytes(c.kv_dtype);
+    const double per_seq = kvb * 2 * KV * c.n_layers * (double)(pos + 2) + 8.0 * c.vocab + 2.0 * D;
+    return w + B * per_seq;
+}
+
+int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
+                           int32_t prompt_len, int32_t max_new, int32_t *out_tokens,
+                           int32_t *n_out) {
+    if (!ready(m)) return -1;
+    const sh_config &c = m->cfg;
+    if (!prompts || !out_tokens || !n_out || n_seqs < 1 || prompt_len < 1 ||
+        prompt_len > c.max_seq) {
+        set_error("sh_batch_greedy_decode: bad arguments");
+        return -1;
+    }
+    std::string why;
+    if (!batch_supported(m, n_seqs, &why)) {
+        set_error("sh_batch_greedy_decode: " + why);
+        return -1;
+    }
+    for (size_t i = 0; i < (size_t)n_seqs * prompt_len; i++)
+        if (prompts[i] < 0 || prompts[i] >= c.vocab) {   // infer.go:160-163
+            set_error("sh_batch_greedy_decode: prompt token[" + std::to_string(i % prompt_len) +
+                      "] of sequence " + std::to_string(i / prompt_len) + " out of range");
+            return -1;
+        }
+    if (max_new <= 0) max_new = 64;                       // infer.go:140-143
+    const int B = n_seqs, P = prompt_len;
+    const int steps = std::min(max_new, c.max_seq - P);   // stop at len == maxSeq
+    (void)hipSetDevice(m->device);
+    if (!hip_ok(batch_alloc(m, B), "batch scratch")) return -1;
+    hipStream_t s = m->stream;
+    // prompt rows 0..P-2 of every sequence: one causal forward that fills the caches
+    const int S = B * (P - 1);
+    std::vector<int32_t> rows(3 * (size_t)std::max(S, 1));
+    if (S > 0) {
+        if (!hip_ok(prefill_alloc(m, S, false), "prefill scratch")) return -1;
+        for (int b = 0; b < B; b++)
+            for (int t = 0; t < P - 1; t++) {
+                const size_t r = (size_t)b * (P - 1) + t;
+                rows[r] = prompts[(size_t)b * P + t];
+                rows[S + r] = t;
+                rows[2 * (size_t)S + r] = b;
+            }
+        if (!hip_ok(hipMemcpyAsync(m->pf_tokens, rows.data(), 4 * (size_t)S, hipMemcpyHostToDevice, s), "rows") ||
+            !hip_ok(hipMemcpyAsync(m->pf_rowpos, rows.data() + S, 4 * (size_t)S, hipMemcpyHostToDevice, s), "rows") ||
+            !hip_ok(hipMemcpyAsync(m->pf_rowseq, rows.data() + 2 * (size_t)S, 4 * (size_t)S, hipMemcpyHostToDevice, s), "rows"))
+            return -1;
+    }
+    // device state: token P-1 at position P-1 next; history rows start with the prompt
+    const size_t hs = (size_t)c.max_seq + 1;
+    std::vector<int32_t> hist((size_t)B * hs, 0), tok(B), pos(B, P - 1);
+    for (int b = 0; b < B; b++) {
+        memcpy(&hist[(size_t)b * hs], prompts + (size_t)b * P, 4 * (size_t)P);
+        tok[b] = prompts[(size_t)b * P + P - 1];
+    }
+    if (!hip_ok(hipMemcpyAsync(m->bt_hist, hist.data(), 4 * hist.size(), hipMemcpyHostToDevice, s), "hist") ||
+        !hip_ok(hipMemcpyAsync(m->bt_tok, tok.data(), 4 * (size_t)B, hipMemcpyHostToDevice, s), "tok") ||
+        !hip_ok(hipMemcpyAsync(m->bt_pos, pos.data(), 4 * (size_t)B, hipMemcpyHostToDevice, s), "pos"))
+        return -1;
+    if (!m->bt_ready || m->bt_graph_b != B) {
+        if (m->bt_ready) (void)hipGraphExecDestroy(m->bt_exec);
+        m->bt_ready = false;
+        hipGraph_t g = nullptr;
+        if (!hip_ok(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "capture")) return -1;
+        const hipError_t e2 = enqueue_batch_step(m, B);
+        const hipError_t e3 = hipStreamEndCapture(s, &g);
+        if (!hip_ok(e2, "batch step") || !hip_ok(e3, "end capture")) {
+            if (g) (void)hipGraphDestroy(g);
+            return -1;
+        }
+        const hipError_t e4 = hipGraphInstantiate(&m->bt_exec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (!hip_ok(e4, "instantiate batch step")) return -1;
+        m->bt_ready = true;
+        m->bt_graph_b = B;
+    }
+    hipEvent_t e0 = m->ev0, e1 = m->ev1, e2 = nullptr;
+    if (!hip_ok(hipEventCreate(&e2), "event")) return -1;
+    bool ok = hip_ok(hipEventRecord(e0, s), "event");
+    if (ok && S > 0) ok = hip_ok(enqueue_prefill(m, S, P - 1, false, true), "batch prefill");
+    ok = ok && hip_ok(hipEventRecord(e1, s), "event");
+    for (int i = 0; ok && i < steps; i++) ok = hip_ok(hipGraphLaunch(m->bt_exec, s), "batch step");
+    ok = ok && hip_ok(hipEventRecord(e2, s), "event") && hip_ok(hipStreamSynchronize(s), "batch sync");
+    ok = ok && hip_ok(hipMemcpy(hist.data(), m->bt_hist, 4 * hist.size(), hipMemcpyDeviceToHost), "read tokens");
+    float pre_ms = 0, dec_ms = 0;
+    if (ok) {
+        (void)hipEventElapsedTime(&pre_ms, e0, e1);
+        (void)hipEventElapsedTime(&dec_ms, e1, e2);
+    }
+    (void)hipEventDestroy(e2);
+    if (!ok) return -1;
+    const size_t stride = (size_t)P + max_new;
+    int64_t kept = 0;
+    for (int b = 0; b < B; b++) {
+        int n = P + steps;
+        for (int i = P; i < P + steps; i++)
+            if (hist[(size_t)b * hs + i] == kEos) {   // infer.go:189-192: EOS is kept
+                n = i + 1;
+                break;
+            }
+        memcpy(out_tokens + (size_t)b * stride, &hist[(size_t)b * hs], 4 * (size_t)n);
+        n_out[b] = n;
+        kept += n - P;
+    }
+    double bytes = 0;
+    for (int i = 0; i < steps; i++) bytes += batch_step_bytes(m, B, P - 1 + i);
+    m->last.gpu_ms = dec_ms;
+    m->last.prefill_ms = pre_ms;
+    m->last.forwards = steps;
+    m->last.tokens_out = kept;
+    m->last.bytes_per_forward_mean = steps ? bytes / steps : 0;
     m->last.persistent = 0;
     m->last.grid = 0;
     return 0;

@@ -94,8 +94,24 @@ struct sh_model {
     int pf_cap;
     int32_t *pf_tokens;                        // [S]
     float *pf_x, *pf_x2, *pf_qkv, *pf_logits;  // [S,D] [S,D] [S,qkv_rows] [V,S]
+    int32_t *pf_rowpos, *pf_rowseq;            // [S] position and sequence of each row
     float *pf_q, *pf_k, *pf_v;                 // roped q, k and v: [S,qdim] [S,kvdim] x2
     uint16_t *pf_xn, *pf_att, *pf_gate;        // GEMM operands: hi plane, then lo plane
+
+    // batched decode (sh_prefill.hip): B sequences stepped together, state on the device
+    void *bt_arena;
+    int bt_cap, bt_nch;
+    int32_t *bt_tok, *bt_pos, *bt_seq;         // [B] next token, its position, sequence index
+    int32_t *bt_hist;                          // [B][max_seq + 1] token history
+    float *bt_x, *bt_x2, *bt_qkv, *bt_q, *bt_k, *bt_v, *bt_logits;
+    uint16_t *bt_xn, *bt_att, *bt_gate;        // GEMM operand planes
+    float *bt_pm, *bt_pl, *bt_pacc;            // attention chunk partials
+    float *bt_part;                            // skinny-GEMM K-range partials
+    float *bt_apv;                             // argmax partials (value, index)
+    int32_t *bt_api;
+    hipGraphExec_t bt_exec;                    // one captured step for bt_graph_b sequences
+    bool bt_ready;
+    int bt_graph_b;
 };
 
 namespace sh {
@@ -124,10 +140,15 @@ hipError_t persistent_grid(const sh_model *m, int *grid_out, std::string *why);
 hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt);
 size_t persistent_layer_ptr_bytes(int n_layers);
 bool prefill_supported(const sh_model *m, std::string *why);
-hipError_t prefill_alloc(sh_model *m, int S);
-// Full causal forward of pf_tokens[0, S): logits [V, S] into pf_logits when `logits`;
-// kv_seq >= 0 also writes KV-cache rows [0, S) of every layer.
-hipError_t enqueue_prefill(sh_model *m, int S, bool logits, int kv_seq);
+hipError_t prefill_alloc(sh_model *m, int S, bool logits);
+// Causal forward of the rows pf_tokens[0, S) (positions pf_rowpos, sequences pf_rowseq,
+// at most seg_max rows per sequence): logits [V, S] into pf_logits when `logits`; fill_kv
+// writes every row's K/V into its sequence's cache (decode numerics).
+hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fill_kv);
+bool batch_supported(const sh_model *m, int B, std::string *why);
+hipError_t batch_alloc(sh_model *m, int B);
+// One greedy step of B sequences (token bt_tok at bt_pos each), argmax into bt_hist.
+hipError_t enqueue_batch_step(sh_model *m, int B);
 void persistent_fill_layer_ptrs(const sh_model *m, void *host);
 
 }  // namespace sh

@@ -19,6 +19,9 @@
 #include <hip/hip_fp16.h>
 #include <math.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "sh_internal.hpp"
 
 namespace sh {
@@ -83,7 +86,11 @@ __global__ __launch_bounds__(kT) void k_rmsnorm_rows(const float *x, const float
     __shared__ double red[kT / 64];
     const float *row = x + (size_t)blockIdx.x * dim;
     double ss = 0;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) ss += (double)row[i] * (double)row[i];
+    for (int i4 = threadIdx.x; i4 < dim / 4; i4 += blockDim.x) {   // dim % 4 == 0
+        const f32x4 v = *(const f32x4 *)(row + 4 * i4);
+        ss += (double)v.x * (double)v.x + (double)v.y * (double)v.y +
+              (double)v.z * (double)v.z + (double)v.w * (double)v.w;
+    }
     const double tot = block_sum(ss, red);
     const double rr = 1.0 / sqrt(tot / (double)dim + eps);
     const float scale = (float)rr;
@@ -106,7 +113,17 @@ struct GemmArgs {
     float alpha;
     uint16_t *out16;     // G_GATE: [M, N/2] operand planes (lo at M*N/2)
     int dt;
+    int decode_forms;    // G_GATE: 1 = infer.go:324-326 silu, 0 = accel_other.go:128-133
+    int partial_only;    // skinny GEMM: always leave K-range partials, no epilogue
 };
+
+// silu(h1) * h3: decode form x / (1 + float32(exp(-x))) (infer.go:324-326), or the
+// full-sequence form (h1 * float32(1 / (1 + exp(-h1)))) * h3 (accel_other.go:128-133).
+__device__ __forceinline__ float silu_gate(float h1, float h3, int decode_forms) {
+    if (decode_forms) return (h1 / (1.0f + (float)exp(-(double)h1))) * h3;
+    const float sig = (float)(1.0 / (1.0 + exp(-(double)h1)));
+    return (h1 * sig) * h3;
+}
 
 template <int DT>
 __device__ __forceinline__ f32x4 mfma16(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
@@ -178,12 +195,9 @@ __global__ __launch_bounds__(kT) void k_gemm_nt(GemmArgs g) {
                 if (g.epi == G_GATE) {
                     // rows 2q (W1) and 2q+1 (W3) of the weight are adjacent columns here
                     const float h3 = __shfl_xor(v, 1, 64);
-                    if ((n & 1) == 0 && m < g.M) {
-                        // accel_other.go:128-133 siluGateForwardAccel
-                        const float sig = (float)(1.0 / (1.0 + exp(-(double)v)));
+                    if ((n & 1) == 0 && m < g.M)
                         store_op(g.out16, (size_t)m * (g.N / 2) + (n >> 1), (size_t)g.M * (g.N / 2),
-                                 (v * sig) * h3, g.dt);
-                    }
+                                 silu_gate(v, h3, g.decode_forms), g.dt);
                 } else if (m < g.M) {
                     if (g.epi == G_STORE) g.out[(size_t)m * g.N + n] = v;
                     else if (g.epi == G_RESID)
@@ -194,32 +208,55 @@ __global__ __launch_bounds__(kT) void k_gemm_nt(GemmArgs g) {
         }
 }
 
-// Per token: optional per-head RMSNorm of q and k, RoPE on q and k (rope.go:26-46:
-// e' = e*c - o*s, o' = o*c + e*s); q, k, v written fp32 token-major; optionally the roped k
-// and v also enter the KV cache (kcache/vcache point at this sequence's layer slab).
 template <int KVT>
-__global__ __launch_bounds__(kT) void k_qk_rope(const float *qkv, int qdim, int kvdim, int hd,
-                                                int qk_norm, const float *q_norm,
-                                                const float *k_norm, double qk_eps,
-                                                const float *rope_cos, const float *rope_sin,
-                                                float *qo, float *ko, float *vo,
-                                                void *kcache, void *vcache, int write_cache) {
-    __shared__ float row[4096];
-    const int t = blockIdx.x;
-    const int n = qdim + 2 * kvdim;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) row[i] = qkv[(size_t)t * n + i];
-    __syncthreads();
+__device__ __forceinline__ float kv_round(float v) {
+    if constexpr (KVT == SH_KV_F32) return v;
+    else if constexpr (KVT == SH_KV_F16) return bits_to_f(f_to_bits(v, SH_DTYPE_F16), SH_DTYPE_F16);
+    else return bits_to_f(f_to_bits(v, SH_DTYPE_BF16), SH_DTYPE_BF16);
+}
+template <int KVT>
+__device__ __forceinline__ void kv_store(void *base, size_t o, float v) {
+    if constexpr (KVT == SH_KV_F32) ((float *)base)[o] = v;
+    else ((uint16_t *)base)[o] = f_to_bits(v, KVT == SH_KV_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16);
+}
+
+// Row t of the token-major activations is token rowpos[t] of sequence rowseq[t].
+// Per row: optional per-head RMSNorm of q and k, RoPE at the row's position (rope.go:26-46:
+// e' = e*c - o*s, o' = o*c + e*s); q written fp32 token-major, k and v too when ko/vo are
+// given. With write_cache the roped k and v also enter the cache at (rowseq[t], layer,
+// rowpos[t]) — kcache/vcache point at sequence 0's slab of this layer, kv_seq_stride
+// elements apart per sequence — and ko/vo then carry the values as the cache stores them,
+// so attention sees what a token-by-token decode would see (infer.go:267-271 stores k and v
+// before attending).
+struct QkRopeArgs {
+    int qdim, kvdim, hd, qk_norm;
+    const float *q_norm, *k_norm;
+    double qk_eps;
+    const float *rope_cos, *rope_sin;
+    const int32_t *rowpos, *rowseq;
+    float *qo, *ko, *vo;
+    void *kcache, *vcache;
+    size_t kv_seq_stride;
+    int write_cache;
+};
+
+// Finishes row t held in LDS (q | k | v, qdim + 2*kvdim floats).
+template <int KVT>
+__device__ __forceinline__ void qk_rope_row(float *row, int t, const QkRopeArgs &a) {
+    const int tp = a.rowpos[t];
+    const size_t kv_row = (size_t)a.rowseq[t] * a.kv_seq_stride + (size_t)tp * a.kvdim;
+    const int qdim = a.qdim, kvdim = a.kvdim, hd = a.hd, n = qdim + 2 * kvdim;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int heads = (qdim + kvdim) / hd;   // q heads, then k heads
-    if (qk_norm) {
+    if (a.qk_norm) {
         for (int h = wave; h < heads; h += nw) {
             float *v = row + h * hd;
-            const float *g = h < qdim / hd ? q_norm : k_norm;
+            const float *g = h < qdim / hd ? a.q_norm : a.k_norm;
             double ss = 0;
             for (int i = lane; i < hd; i += 64) ss += (double)v[i] * (double)v[i];
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-            const float rr = (float)(1.0 / sqrt(ss / (double)hd + qk_eps));
+            const float rr = (float)(1.0 / sqrt(ss / (double)hd + a.qk_eps));
             for (int i = lane; i < hd; i += 64) v[i] = v[i] * rr * g[i];
         }
         __syncthreads();
@@ -227,7 +264,7 @@ __global__ __launch_bounds__(kT) void k_qk_rope(const float *qkv, int qdim, int 
     const int half = hd / 2;
     for (int p = threadIdx.x; p < (qdim + kvdim) / 2; p += blockDim.x) {
         const int pi = p % half;
-        const float c = rope_cos[t * half + pi], s = rope_sin[t * half + pi];
+        const float c = a.rope_cos[tp * half + pi], s = a.rope_sin[tp * half + pi];
         const float e = row[2 * p], o = row[2 * p + 1];
         row[2 * p] = e * c - o * s;
         row[2 * p + 1] = o * c + e * s;
@@ -236,49 +273,98 @@ __global__ __launch_bounds__(kT) void k_qk_rope(const float *qkv, int qdim, int 
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const float v = row[i];
         if (i < qdim) {
-            qo[(size_t)t * qdim + i] = v;
+            a.qo[(size_t)t * qdim + i] = v;
         } else if (i < qdim + kvdim) {
             const int j = i - qdim;
-            ko[(size_t)t * kvdim + j] = v;
-            if (write_cache) {
-                const size_t o = (size_t)t * kvdim + j;
-                if (KVT == SH_KV_F32) ((float *)kcache)[o] = v;
-                else ((uint16_t *)kcache)[o] = f_to_bits(v, KVT == SH_KV_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16);
-            }
+            if (a.write_cache) kv_store<KVT>(a.kcache, kv_row + j, v);
+            if (a.ko) a.ko[(size_t)t * kvdim + j] = a.write_cache ? kv_round<KVT>(v) : v;
         } else {
             const int j = i - qdim - kvdim;
-            vo[(size_t)t * kvdim + j] = v;
-            if (write_cache) {
-                const size_t o = (size_t)t * kvdim + j;
-                if (KVT == SH_KV_F32) ((float *)vcache)[o] = v;
-                else ((uint16_t *)vcache)[o] = f_to_bits(v, KVT == SH_KV_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16);
-            }
+            if (a.write_cache) kv_store<KVT>(a.vcache, kv_row + j, v);
+            if (a.vo) a.vo[(size_t)t * kvdim + j] = a.write_cache ? kv_round<KVT>(v) : v;
         }
     }
 }
 
-// Causal attention (forward_common.go:5-33): one wave per (query t, head h). Lanes walk the
-// keys j <= t in blocks of 64; scores are kept in LDS, then the softmax of
-// accel_other.go:190-207 (float64 exp terms summed unrounded, p = float32(e) * float32(1/sum);
-// masked keys contribute exactly 0) and P.V with lanes over the head dims.
+template <int KVT>
+__global__ __launch_bounds__(kT) void k_qk_rope(const float *qkv, QkRopeArgs a) {
+    __shared__ __attribute__((aligned(16))) float row[4096];
+    const int t = blockIdx.x;
+    const int n = a.qdim + 2 * a.kvdim;
+#pragma unroll 4
+    for (int i4 = threadIdx.x; i4 < n / 4; i4 += blockDim.x)   // n % 4 == 0
+        *(f32x4 *)(row + 4 * i4) = *(const f32x4 *)(qkv + (size_t)t * n + 4 * i4);
+    __syncthreads();
+    qk_rope_row<KVT>(row, t, a);
+}
+
+// Batched decode: row m of the q|k|v projection is the sum of the skinny GEMM's K-range
+// partials ([ranges][M][n], added in range order), then qk_rope_row.
+template <int KVT>
+__global__ __launch_bounds__(1024) void k_row_qkv(const float *partial, int ranges, int M, QkRopeArgs a) {
+    __shared__ __attribute__((aligned(16))) float row[4096];
+    const int m = blockIdx.x;
+    const int n = a.qdim + 2 * a.kvdim;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = 0.f;
+        for (int r = 0; r < ranges; r++) v += partial[((size_t)r * M + m) * n + i];
+        row[i] = v;
+    }
+    __syncthreads();
+    qk_rope_row<KVT>(row, m, a);
+}
+
+// Batched decode: row m of a residual projection, x_out = resid + alpha * (sum of the K-range
+// partials), then rmsNormVec of x_out with `gain` (infer.go:301-311) as a GEMM operand row.
+__global__ __launch_bounds__(1024) void k_row_resid_norm(const float *partial, int ranges, int M,
+                                                         int D, const float *resid, float alpha,
+                                                         float *x_out, const float *gain,
+                                                         double eps, int dt, uint16_t *xn) {
+    __shared__ float row[4096];
+    __shared__ double red[1024 / 64];
+    const int m = blockIdx.x;
+    double ss = 0;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+        float v = 0.f;
+        for (int r = 0; r < ranges; r++) v += partial[((size_t)r * M + m) * D + i];
+        const float x = resid[(size_t)m * D + i] + alpha * v;
+        x_out[(size_t)m * D + i] = x;
+        row[i] = x;
+        ss += (double)x * (double)x;
+    }
+    const double tot = block_sum(ss, red);
+    const float scale = (float)(1.0 / sqrt(tot / (double)D + eps));
+    for (int i = threadIdx.x; i < D; i += blockDim.x)
+        store_op(xn, (size_t)m * D + i, (size_t)M * D, row[i] * scale * gain[i], dt);
+}
+
+// Causal attention (forward_common.go:5-33): one wave per (query t, head h). Row t is
+// position rowpos[t] of its sequence, whose rows are the rowpos[t] rows before it, so the keys
+// are j in [t - rowpos[t], t]. Lanes walk the keys in blocks of 64; scores are kept in LDS,
+// then the softmax and P.V with lanes over the head dims. decode_forms = 0 is the
+// full-sequence form (accel_other.go:190-207: float64 exp terms summed unrounded); 1 is the
+// decode form (infer.go:328-345: the float32-rounded terms summed). Both scale by
+// float32(1/sum) and give masked keys exactly 0.
 __global__ __launch_bounds__(kT) void k_attn_prefill(const float *qf, const float *kf,
-                                                     const float *vf, int S, int H, int KVH,
-                                                     int hd, float scale, int dt,
+                                                     const float *vf, int S, int seg_max,
+                                                     const int32_t *rowpos, int H, int KVH,
+                                                     int hd, float scale, int dt, int decode_forms,
                                                      uint16_t *att, size_t plane) {
-    extern __shared__ float sh_scores[];   // [waves][S]
+    extern __shared__ float sh_scores[];   // [waves][seg_max]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = blockIdx.x * (blockDim.x >> 6) + wave;
     const int h = blockIdx.y;
     if (t >= S) return;
     const int qdim = H * hd, kvdim = KVH * hd, kvh = h / (H / KVH);
-    float *sc = sh_scores + (size_t)wave * S;
+    const int j0 = t - rowpos[t], n = rowpos[t] + 1;   // keys j0 .. t
+    float *sc = sh_scores + (size_t)wave * seg_max;
     const float *q = qf + (size_t)t * qdim + h * hd;
     float mx = -INFINITY;
-    for (int j0 = 0; j0 <= t; j0 += 64) {
-        const int j = j0 + lane;
+    for (int b = 0; b < n; b += 64) {
+        const int jj = b + lane;
         float s = -INFINITY;
-        if (j <= t) {
-            const float *k = kf + (size_t)j * kvdim + kvh * hd;
+        if (jj < n) {
+            const float *k = kf + (size_t)(j0 + jj) * kvdim + kvh * hd;
             float d = 0.f;
             for (int i = 0; i < hd; i += 4) {
                 const f32x4 qa = *(const f32x4 *)(q + i), ka = *(const f32x4 *)(k + i);
@@ -286,17 +372,17 @@ __global__ __launch_bounds__(kT) void k_attn_prefill(const float *qf, const floa
                 for (int w = 0; w < 4; w++) d = fmaf(qa[w], ka[w], d);
             }
             s = d * scale;
-            sc[j] = s;
+            sc[jj] = s;
         }
         mx = fmaxf(mx, s);
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     double sum = 0;
-    for (int j = lane; j <= t; j += 64) {
-        const double e = exp((double)(sc[j] - mx));
-        sc[j] = (float)e;
-        sum += e;
+    for (int jj = lane; jj < n; jj += 64) {
+        const double e = exp((double)(sc[jj] - mx));
+        sc[jj] = (float)e;
+        sum += decode_forms ? (double)(float)e : e;
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
@@ -304,9 +390,397 @@ __global__ __launch_bounds__(kT) void k_attn_prefill(const float *qf, const floa
     __builtin_amdgcn_wave_barrier();
     for (int i = lane; i < hd; i += 64) {
         float a = 0.f;
-        for (int j = 0; j <= t; j++)
-            a = fmaf(sc[j] * inv, vf[(size_t)j * kvdim + kvh * hd + i], a);
+        for (int jj = 0; jj < n; jj++)
+            a = fmaf(sc[jj] * inv, vf[(size_t)(j0 + jj) * kvdim + kvh * hd + i], a);
         store_op(att, (size_t)t * qdim + h * hd + i, plane, a, dt);
+    }
+}
+
+// Epilogue of the skinny GEMM for output columns n, n+1 of row m.
+__device__ __forceinline__ void skinny_epilogue(const GemmArgs &g, int m, int n, float v0, float v1) {
+    if (g.epi == G_GATE) {
+        // columns 2q (W1) and 2q+1 (W3) of the interleaved weight rows
+        store_op(g.out16, (size_t)m * (g.N / 2) + (n >> 1), (size_t)g.M * (g.N / 2),
+                 silu_gate(v0, v1, g.decode_forms), g.dt);
+        return;
+    }
+    const float v[2] = {v0, v1};
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        if (g.epi == G_STORE) g.out[(size_t)m * g.N + n + j] = v[j];
+        else if (g.epi == G_RESID)
+            g.out[(size_t)m * g.N + n + j] = g.resid[(size_t)m * g.N + n + j] + g.alpha * v[j];
+        else g.out[(size_t)(n + j) * g.M + m] = v[j];
+    }
+}
+
+// Skinny GEMM for batched decode: C[M, N] = A[M, K] . W[N, K]^T with M <= 32 token rows.
+// Workgroup (x, y) owns 16 output columns and the K range [y*kc, (y+1)*kc); its four waves
+// each take a quarter of that range for both 16-row MFMA blocks (hi and lo operand planes),
+// issuing two k-steps of loads before their MFMAs, and the four partial tiles are added
+// through LDS in a fixed order. With one K range the epilogue runs here; otherwise the tile
+// goes to `partial` ([ranges][M][N]) for k_gemm_skinny_reduce. Needs kc % 128 == 0,
+// N % 16 == 0.
+template <int DT>
+__global__ __launch_bounds__(kT) void k_gemm_skinny(GemmArgs g, float *partial, int kc) {
+    __shared__ float part[4][32][17];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * 16;
+    const int lr = lane & 15, lk = (lane >> 4) * 8;
+    const int kq = kc / 4, kb = blockIdx.y * kc + wave * kq;
+    const size_t lo = (size_t)g.M * g.K;
+    const bool ok0 = lr < g.M, ok1 = 16 + lr < g.M;
+    const uint16_t *a0 = g.A + (size_t)(ok0 ? lr : 0) * g.K + lk;
+    const uint16_t *a1 = g.A + (size_t)(ok1 ? 16 + lr : 0) * g.K + lk;
+    const uint16_t *bp = g.B + (size_t)(n0 + lr) * g.K + lk;
+    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+    f32x4 c0 = f32x4{0.f, 0.f, 0.f, 0.f}, c1 = c0;
+    for (int k = kb; k < kb + kq; k += 64) {
+        const bool two = k + 32 < kb + kq;
+        u32x4 b[2], x0[2], x0l[2], x1[2], x1l[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int kk = k + 32 * u;
+            const bool in = u == 0 || two;
+            b[u] = in ? *(const u32x4 *)(bp + kk) : zero;
+            x0[u] = in && ok0 ? *(const u32x4 *)(a0 + kk) : zero;
+            x0l[u] = in && ok0 ? *(const u32x4 *)(a0 + lo + kk) : zero;
+            x1[u] = in && ok1 ? *(const u32x4 *)(a1 + kk) : zero;
+            x1l[u] = in && ok1 ? *(const u32x4 *)(a1 + lo + kk) : zero;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            c0 = mfma16<DT>(x0[u], b[u], c0);
+            c0 = mfma16<DT>(x0l[u], b[u], c0);
+            c1 = mfma16<DT>(x1[u], b[u], c1);
+            c1 = mfma16<DT>(x1l[u], b[u], c1);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        part[wave][4 * (lane >> 4) + r][lr] = c0[r];
+        part[wave][16 + 4 * (lane >> 4) + r][lr] = c1[r];
+    }
+    __syncthreads();
+    const int m = threadIdx.x >> 3, nn = (threadIdx.x & 7) * 2;   // columns nn, nn+1 of row m
+    if (m >= g.M) return;
+    float v[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+        v[j] = ((part[0][m][nn + j] + part[1][m][nn + j]) + part[2][m][nn + j]) + part[3][m][nn + j];
+    if (gridDim.y == 1 && !g.partial_only) {
+        skinny_epilogue(g, m, n0 + nn, v[0], v[1]);
+    } else {
+        float *dst = partial + ((size_t)blockIdx.y * g.M + m) * g.N + n0 + nn;
+        dst[0] = v[0];
+        dst[1] = v[1];
+    }
+}
+
+// Adds the K-range partials of the skinny GEMM in range order, then the epilogue.
+__global__ __launch_bounds__(kT) void k_gemm_skinny_reduce(GemmArgs g, const float *partial, int ranges) {
+    const int idx = blockIdx.x * kT + threadIdx.x;
+    const int half = g.N / 2;
+    if (idx >= g.M * half) return;
+    const int m = idx / half, n = (idx % half) * 2;
+    float v0 = 0.f, v1 = 0.f;
+    for (int r = 0; r < ranges; r++) {
+        const float *src = partial + ((size_t)r * g.M + m) * g.N + n;
+        v0 += src[0];
+        v1 += src[1];
+    }
+    skinny_epilogue(g, m, n, v0, v1);
+}
+
+constexpr int kMaxGroupB = 4;          // q heads per kv head in the batched attention
+constexpr int kKvTile = 32 * 1024;     // LDS bytes for one chunk of K rows (and as many for V)
+
+// Keys per split of the batched attention for a cache row of row_bytes: a chunk's K rows
+// fill kKvTile, at most 256.
+__host__ __device__ constexpr int attn_chunk(int row_bytes) {
+    return kKvTile / row_bytes < 256 ? kKvTile / row_bytes : 256;
+}
+
+// Copies rows [0, n) of a cache slab (row r at byte r*stride) into LDS, rows of rb bytes
+// packed back to back, with global_load_lds (each lane moves 16 bytes; a wave instruction
+// fills 1 KB). Rows n..cap-1 of the tile re-read row n-1, so every lane reads valid memory.
+__device__ __forceinline__ void rows_to_lds(const uint8_t *src, size_t stride, int n, int cap,
+                                            int rb, uint8_t *lds) {
+    const int lpr = rb / 16, rpi = 64 / lpr;   // lanes per row, rows per wave instruction
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int r_in = lane / lpr, c_in = (lane % lpr) * 16;
+    for (int r0 = wave * rpi; r0 < cap; r0 += nw * rpi) {
+        int r = r0 + r_in;
+        if (r >= n) r = n - 1;
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void *)(src + (size_t)r * stride + c_in),
+            (__attribute__((address_space(3))) void *)(lds + (size_t)r0 * rb), 16, 0, 0);
+    }
+}
+
+template <int KVT>
+__device__ __forceinline__ float kv_elem(const uint8_t *row, int i) {
+    if constexpr (KVT == SH_KV_F32) return ((const float *)row)[i];
+    else return bits_to_f(((const uint16_t *)row)[i], KVT == SH_KV_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16);
+}
+
+// Batched decode attention, split over the keys (one workgroup per (chunk, kv head,
+// sequence); two fit on a CU): the chunk's K and V rows are copied into LDS in one burst,
+// then the scores of the group's q heads (one thread per key, 16-byte slices visited in a
+// rotated order so a wave's LDS reads spread over the banks), the chunk's max m and sum l
+// of exp(s - m), and the unnormalised P.V (thread = one 16-byte slice of the V rows over a
+// share of the keys; shares added through LDS, reusing the K tile), written as partials
+// for k_attn_batch_combine. Sequence b attends to positions 0..pos[b] of its cache.
+template <int KVT>
+__global__ __launch_bounds__(kT) void k_attn_batch_partial(
+    const float *q, const void *kc, const void *vc, size_t kv_seq_stride, const int32_t *pos,
+    int H, int KVH, int hd, float scale, int nch, float *pm, float *pl, float *pacc) {
+    __shared__ __attribute__((aligned(16))) uint8_t kt[kKvTile];
+    __shared__ __attribute__((aligned(16))) uint8_t vt[kKvTile];
+    __shared__ __attribute__((aligned(16))) float qs[kMaxGroupB * 256];
+    __shared__ float sc[kMaxGroupB][256];
+    __shared__ float redm[kMaxGroupB][kT / 64];
+    constexpr int EB = KVT == SH_KV_F32 ? 4 : 2;
+    const int rb = hd * EB, C = attn_chunk(rb);
+    const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int P = pos[b] + 1;
+    const int t0 = c * C;
+    if (t0 >= P) return;
+    const int n = min(C, P - t0);
+    const int group = H / KVH, qdim = H * hd, kvdim = KVH * hd;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t base = ((size_t)b * kv_seq_stride + (size_t)t0 * kvdim + (size_t)g * hd) * EB;
+    rows_to_lds((const uint8_t *)kc + base, (size_t)kvdim * EB, n, n, rb, kt);
+    rows_to_lds((const uint8_t *)vc + base, (size_t)kvdim * EB, n, n, rb, vt);
+    for (int i = threadIdx.x; i < group * hd; i += kT)
+        qs[i] = q[(size_t)b * qdim + (size_t)g * group * hd + i];
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // scores: thread t <-> key t0 + t
+    const int nsl = rb / 16;                   // 16-byte slices per row
+    constexpr int EPS = 16 / EB;               // elements per slice
+    for (int t = threadIdx.x; t < n; t += kT) {
+        float d[kMaxGroupB] = {0.f, 0.f, 0.f, 0.f};
+        const u32x4 *row = (const u32x4 *)(kt + (size_t)t * rb);
+#pragma unroll 4
+        for (int s0 = 0; s0 < nsl; s0++) {
+            const int sl = (s0 + t) % nsl;
+            const u32x4 raw = row[sl];
+            float kf[8];
+            if constexpr (KVT == SH_KV_F32) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) kf[e] = __uint_as_float(raw[e]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int dtk = KVT == SH_KV_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16;
+                    kf[2 * e] = bits_to_f(raw[e] & 0xffffu, dtk);
+                    kf[2 * e + 1] = bits_to_f(raw[e] >> 16, dtk);
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < kMaxGroupB; h++) {
+                if (h >= group) break;
+#pragma unroll
+                for (int e = 0; e < EPS; e++) d[h] = fmaf(qs[h * hd + sl * EPS + e], kf[e], d[h]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < kMaxGroupB; h++)
+            if (h < group) sc[h][t] = d[h] * scale;
+    }
+    __syncthreads();
+    // per head: chunk max, exp terms, their sum
+    for (int h = 0; h < group; h++) {
+        float mx = -INFINITY;
+        for (int t = threadIdx.x; t < n; t += kT) mx = fmaxf(mx, sc[h][t]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        if (lane == 0) redm[h][wave] = mx;
+    }
+    __syncthreads();
+    float mh[kMaxGroupB];
+    for (int h = 0; h < group; h++) {
+        mh[h] = redm[h][0];
+        for (int w = 1; w < kT / 64; w++) mh[h] = fmaxf(mh[h], redm[h][w]);
+    }
+    __syncthreads();
+    for (int h = 0; h < group; h++) {
+        float sum = 0.f;
+        for (int t = threadIdx.x; t < n; t += kT) {
+            const float e = expf(sc[h][t] - mh[h]);
+            sc[h][t] = e;
+            sum += e;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        if (lane == 0) redm[h][wave] = sum;
+    }
+    __syncthreads();
+    const size_t pbase = ((size_t)b * H + (size_t)g * group) * nch + c;
+    if (threadIdx.x < group) {
+        const int h = threadIdx.x;
+        float l = 0.f;
+        for (int w = 0; w < kT / 64; w++) l += redm[h][w];
+        pm[pbase + (size_t)h * nch] = mh[h];
+        pl[pbase + (size_t)h * nch] = l;
+    }
+    // P.V from LDS: thread (slice, key set) accumulates EPS dims of every head over the keys
+    // t = ks, ks + nks, ...; the key-set partials go to LDS (the K tile is free now) and are
+    // added in key-set order
+    const int nks = kT / nsl;
+    const int sl = threadIdx.x % nsl, ks = threadIdx.x / nsl;
+    float acc[kMaxGroupB][8];
+#pragma unroll
+    for (int h = 0; h < kMaxGroupB; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[h][e] = 0.f;
+#pragma unroll 4
+    for (int t = ks; t < n; t += nks) {
+        const u32x4 raw = ((const u32x4 *)(vt + (size_t)t * rb))[sl];
+        float vf[8];
+        if constexpr (KVT == SH_KV_F32) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) vf[e] = __uint_as_float(raw[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int dtk = KVT == SH_KV_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16;
+                vf[2 * e] = bits_to_f(raw[e] & 0xffffu, dtk);
+                vf[2 * e + 1] = bits_to_f(raw[e] >> 16, dtk);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < kMaxGroupB; h++) {
+            if (h >= group) break;
+            const float p = sc[h][t];
+#pragma unroll
+            for (int e = 0; e < EPS; e++) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
+        }
+    }
+    float *pv = (float *)kt;   // [nks][group * hd]
+    const int gw = group * hd;
+#pragma unroll
+    for (int h = 0; h < kMaxGroupB; h++) {
+        if (h >= group) break;
+#pragma unroll
+        for (int e = 0; e < EPS; e++) pv[(size_t)ks * gw + h * hd + sl * EPS + e] = acc[h][e];
+    }
+    __syncthreads();
+    for (int k = threadIdx.x; k < gw; k += kT) {
+        float a = 0.f;
+        for (int r = 0; r < nks; r++) a += pv[(size_t)r * gw + k];
+        pacc[(pbase + (size_t)(k / hd) * nch) * hd + k % hd] = a;
+    }
+}
+
+// Merges the chunk partials of (q head h, sequence b): out = sum_c e^(m_c - M) acc_c /
+// sum_c e^(m_c - M) l_c, written as a GEMM operand row.
+__global__ __launch_bounds__(256) void k_attn_batch_combine(const float *pm, const float *pl,
+                                                            const float *pacc, const int32_t *pos,
+                                                            int H, int hd, int nch, int chunk,
+                                                            int B, int dt, uint16_t *att) {
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int nc = (pos[b] + chunk) / chunk;   // chunks holding keys 0..pos
+    const size_t pb = ((size_t)b * H + h) * nch;
+    float M = -INFINITY;
+    for (int c = 0; c < nc; c++) M = fmaxf(M, pm[pb + c]);
+    float L = 0.f;
+    for (int c = 0; c < nc; c++) L += expf(pm[pb + c] - M) * pl[pb + c];
+    const float invL = 1.0f / L;
+    const size_t plane = (size_t)B * H * hd;
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+        float a = 0.f;
+        for (int c = 0; c < nc; c++) a += expf(pm[pb + c] - M) * pacc[(pb + c) * hd + i];
+        store_op(att, (size_t)b * H * hd + (size_t)h * hd + i, plane, a * invL, dt);
+    }
+}
+
+constexpr int kArgChunk = 4096;   // logits per workgroup of the first argmax pass
+
+// First pass of the row argmax (infer.go:373-383, first maximum) of logits [B, V]: workgroup
+// (blk, b) scans logits [blk*4096, (blk+1)*4096) of row b, 16 consecutive values per thread
+// read as four float4, and writes its (max, first index). Needs V % 4 == 0.
+__global__ __launch_bounds__(kT) void k_argmax_part(const float *logits, int V, int nblk,
+                                                    float *pv, int32_t *pi) {
+    __shared__ float bv[kT / 64];
+    __shared__ int bi[kT / 64];
+    const int blk = blockIdx.x, b = blockIdx.y;
+    const float *row = logits + (size_t)b * V;
+    const int i0 = blk * kArgChunk + threadIdx.x * 16;
+    f32x4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        x[u] = i0 + 4 * u < V ? *(const f32x4 *)(row + i0 + 4 * u)
+                              : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (x[u][e] > v) {   // ascending indices: strict > keeps the first maximum
+                v = x[u][e];
+                idx = i0 + 4 * u + e;
+            }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = v;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        v = bv[0];
+        idx = bi[0];
+        for (int w = 1; w < kT / 64; w++)
+            if (bv[w] > v || (bv[w] == v && bi[w] < idx)) {
+                v = bv[w];
+                idx = bi[w];
+            }
+        pv[(size_t)b * nblk + blk] = v;
+        pi[(size_t)b * nblk + blk] = idx;
+    }
+}
+
+// Second pass: one wave per row reduces the partials, then the sequence advances:
+// hist[b][pos+1] = next, tok[b] = next, pos[b] += 1.
+__global__ __launch_bounds__(64) void k_argmax_advance(const float *pv, const int32_t *pi,
+                                                       int nblk, int32_t *tok, int32_t *pos,
+                                                       int32_t *hist, int hist_stride) {
+    const int b = blockIdx.x, lane = threadIdx.x;
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int k = lane; k < nblk; k += 64) {
+        const float cv = pv[(size_t)b * nblk + k];
+        const int ci = pi[(size_t)b * nblk + k];
+        if (cv > v || (cv == v && ci < idx)) {
+            v = cv;
+            idx = ci;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    if (lane == 0) {
+        const int next = idx == 0x7fffffff ? 0 : idx;
+        const int p = pos[b];
+        hist[(size_t)b * hist_stride + p + 1] = next;
+        tok[b] = next;
+        pos[b] = p + 1;
     }
 }
 
@@ -338,12 +812,13 @@ bool prefill_supported(const sh_model *m, std::string *why) {
     return true;
 }
 
-hipError_t prefill_alloc(sh_model *m, int S) {
-    if (m->pf_cap >= S) return hipSuccess;
+hipError_t prefill_alloc(sh_model *m, int S, bool logits) {
+    if (m->pf_cap >= S && (!logits || m->pf_logits)) return hipSuccess;
     const sh_config &c = m->cfg;
     (void)hipFree(m->pf_arena);
     m->pf_arena = nullptr;
     m->pf_cap = 0;
+    m->pf_logits = nullptr;
     const size_t D = c.dim, F = c.hidden, Q = m->qdim, KV = m->kvdim, R = m->qkv_rows, V = c.vocab;
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -351,14 +826,17 @@ hipError_t prefill_alloc(sh_model *m, int S) {
         off += (bytes + 255) / 256 * 256;
         return o;
     };
-    const size_t o_tok = take(4 * S), o_x = take(4 * S * D), o_x2 = take(4 * S * D),
-                 o_xn = take(4 * S * D), o_qkv = take(4 * S * R), o_q = take(4 * S * Q),
-                 o_k = take(4 * S * KV), o_v = take(4 * S * KV), o_att = take(4 * S * Q),
-                 o_gate = take(4 * S * F), o_log = take(4 * V * S);
+    const size_t o_tok = take(4 * S), o_pos = take(4 * S), o_seq = take(4 * S),
+                 o_x = take(4 * S * D), o_x2 = take(4 * S * D), o_xn = take(4 * S * D),
+                 o_qkv = take(4 * S * R), o_q = take(4 * S * Q), o_k = take(4 * S * KV),
+                 o_v = take(4 * S * KV), o_att = take(4 * S * Q), o_gate = take(4 * S * F),
+                 o_log = logits ? take(4 * V * S) : 0;
     hipError_t e = hipMalloc(&m->pf_arena, off);
     if (e != hipSuccess) return e;
     uint8_t *A = (uint8_t *)m->pf_arena;
     m->pf_tokens = (int32_t *)(A + o_tok);
+    m->pf_rowpos = (int32_t *)(A + o_pos);
+    m->pf_rowseq = (int32_t *)(A + o_seq);
     m->pf_x = (float *)(A + o_x);
     m->pf_x2 = (float *)(A + o_x2);
     m->pf_xn = (uint16_t *)(A + o_xn);
@@ -368,14 +846,66 @@ hipError_t prefill_alloc(sh_model *m, int S) {
     m->pf_v = (float *)(A + o_v);
     m->pf_att = (uint16_t *)(A + o_att);
     m->pf_gate = (uint16_t *)(A + o_gate);
-    m->pf_logits = (float *)(A + o_log);
+    m->pf_logits = logits ? (float *)(A + o_log) : nullptr;
     m->pf_cap = S;
     return hipSuccess;
 }
 
-// Enqueues the whole forward for pf_tokens[0, S); logits (if wanted) land in pf_logits as
-// [V, S]. kv_seq >= 0 fills that sequence's KV cache rows [0, S) on the way.
-hipError_t enqueue_prefill(sh_model *m, int S, bool logits, int kv_seq) {
+namespace {
+
+void *kv_layer_base(const sh_model *m, void *cache, int l) {
+    const size_t kvb = m->cfg.kv_dtype == SH_KV_F32 ? 4 : 2;
+    return (uint8_t *)cache + (size_t)l * m->cfg.max_seq * m->kvdim * kvb;
+}
+size_t kv_seq_stride(const sh_model *m) {
+    return (size_t)m->cfg.n_layers * m->cfg.max_seq * m->kvdim;
+}
+
+QkRopeArgs qk_rope_args(const sh_model *m, const LayerDev &L, const int32_t *rowpos,
+                        const int32_t *rowseq, float *q, float *k, float *v, int l, bool fill) {
+    const sh_config &c = m->cfg;
+    QkRopeArgs a{};
+    a.qdim = m->qdim;
+    a.kvdim = m->kvdim;
+    a.hd = c.head_dim;
+    a.qk_norm = c.qk_norm;
+    a.q_norm = L.q_norm;
+    a.k_norm = L.k_norm;
+    a.qk_eps = c.qk_norm_eps;
+    a.rope_cos = m->rope_cos;
+    a.rope_sin = m->rope_sin;
+    a.rowpos = rowpos;
+    a.rowseq = rowseq;
+    a.qo = q;
+    a.ko = k;
+    a.vo = v;
+    a.kcache = fill ? kv_layer_base(m, m->kcache, l) : nullptr;
+    a.vcache = fill ? kv_layer_base(m, m->vcache, l) : nullptr;
+    a.kv_seq_stride = kv_seq_stride(m);
+    a.write_cache = fill ? 1 : 0;
+    return a;
+}
+
+hipError_t launch_qk_rope(const sh_model *m, const LayerDev &L, int rows, const float *qkv,
+                          const int32_t *rowpos, const int32_t *rowseq, float *q, float *k,
+                          float *v, int l, bool fill, hipStream_t s) {
+    const QkRopeArgs a = qk_rope_args(m, L, rowpos, rowseq, q, k, v, l, fill);
+    const int kv = m->cfg.kv_dtype;
+    if (kv == SH_KV_F32) hipLaunchKernelGGL(k_qk_rope<SH_KV_F32>, dim3(rows), dim3(kT), 0, s, qkv, a);
+    else if (kv == SH_KV_F16) hipLaunchKernelGGL(k_qk_rope<SH_KV_F16>, dim3(rows), dim3(kT), 0, s, qkv, a);
+    else hipLaunchKernelGGL(k_qk_rope<SH_KV_BF16>, dim3(rows), dim3(kT), 0, s, qkv, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// Enqueues the forward of the S rows pf_tokens[0, S) (row t = position pf_rowpos[t] of
+// sequence pf_rowseq[t]; a sequence's rows are consecutive, at most seg_max of them). With
+// logits, the full-sequence classifier lands in pf_logits as [V, S]. With fill_kv, every
+// row's k and v enter its sequence's KV cache and the layers use the decode forms of the
+// softmax sum and SiLU, so the cache holds what a token-by-token decode of the same prompt
+// would have written.
+hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fill_kv) {
     const sh_config &c = m->cfg;
     const int dt = m->dtype;
     const int D = c.dim, F = c.hidden;
@@ -385,9 +915,6 @@ hipError_t enqueue_prefill(sh_model *m, int S, bool logits, int kv_seq) {
                        m->pf_tokens, c.vocab, D, dt, m->pf_x);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const float scale = (float)(1.0 / sqrt((double)c.head_dim));
-    const size_t kv_layer = (size_t)c.max_seq * m->kvdim;
-    const size_t kv_seq_stride = kv_layer * c.n_layers;
-    const size_t kvb = c.kv_dtype == SH_KV_F32 ? 4 : 2;
     for (int l = 0; l < c.n_layers; l++) {
         const LayerDev &L = m->layers[l];
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x, L.rms_att, D,
@@ -396,24 +923,14 @@ hipError_t enqueue_prefill(sh_model *m, int S, bool logits, int kv_seq) {
         g.A = m->pf_xn; g.B = (const uint16_t *)L.wqkv; g.M = S; g.N = m->qkv_rows; g.K = D;
         g.epi = G_STORE; g.out = m->pf_qkv; g.dt = dt;
         if ((e = gemm(g, dt, s)) != hipSuccess) return e;
-        void *kc = nullptr, *vc = nullptr;
-        if (kv_seq >= 0) {
-            const size_t o = ((size_t)kv_seq * kv_seq_stride + (size_t)l * kv_layer) * kvb;
-            kc = (uint8_t *)m->kcache + o;
-            vc = (uint8_t *)m->vcache + o;
-        }
-#define SH_QKR(KVT)                                                                           \
-    hipLaunchKernelGGL(k_qk_rope<KVT>, dim3(S), dim3(kT), 0, s, m->pf_qkv, m->qdim, m->kvdim,  \
-                       c.head_dim, c.qk_norm, L.q_norm, L.k_norm, c.qk_norm_eps, m->rope_cos,  \
-                       m->rope_sin, m->pf_q, m->pf_k, m->pf_v, kc, vc, kv_seq >= 0 ? 1 : 0)
-        if (c.kv_dtype == SH_KV_F32) SH_QKR(SH_KV_F32);
-        else if (c.kv_dtype == SH_KV_F16) SH_QKR(SH_KV_F16);
-        else SH_QKR(SH_KV_BF16);
-#undef SH_QKR
+        if ((e = launch_qk_rope(m, L, S, m->pf_qkv, m->pf_rowpos, m->pf_rowseq, m->pf_q,
+                                m->pf_k, m->pf_v, l, fill_kv, s)) != hipSuccess)
+            return e;
         const int wpb = kT / 64;
         hipLaunchKernelGGL(k_attn_prefill, dim3((S + wpb - 1) / wpb, c.n_heads), dim3(kT),
-                           sizeof(float) * wpb * S, s, m->pf_q, m->pf_k, m->pf_v, S, c.n_heads,
-                           c.n_kv_heads, c.head_dim, scale, dt, m->pf_att, (size_t)S * m->qdim);
+                           sizeof(float) * wpb * seg_max, s, m->pf_q, m->pf_k, m->pf_v, S,
+                           seg_max, m->pf_rowpos, c.n_heads, c.n_kv_heads, c.head_dim, scale, dt,
+                           fill_kv ? 1 : 0, m->pf_att, (size_t)S * m->qdim);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         g = GemmArgs{};
         g.A = m->pf_att; g.B = (const uint16_t *)L.wo; g.M = S; g.N = D; g.K = m->qdim;
@@ -423,7 +940,7 @@ hipError_t enqueue_prefill(sh_model *m, int S, bool logits, int kv_seq) {
                            c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D);
         g = GemmArgs{};
         g.A = m->pf_xn; g.B = (const uint16_t *)L.w13; g.M = S; g.N = 2 * F; g.K = D;
-        g.epi = G_GATE; g.out16 = m->pf_gate; g.dt = dt;
+        g.epi = G_GATE; g.out16 = m->pf_gate; g.dt = dt; g.decode_forms = fill_kv ? 1 : 0;
         if ((e = gemm(g, dt, s)) != hipSuccess) return e;
         g = GemmArgs{};
         g.A = m->pf_gate; g.B = (const uint16_t *)L.w2; g.M = S; g.N = D; g.K = F;
@@ -437,6 +954,210 @@ hipError_t enqueue_prefill(sh_model *m, int S, bool logits, int kv_seq) {
     g.A = m->pf_xn; g.B = (const uint16_t *)m->cls; g.M = S; g.N = c.vocab; g.K = D;
     g.epi = G_LOGITS_CF; g.out = m->pf_logits; g.dt = dt;
     return gemm(g, dt, s);
+}
+
+
+namespace {
+// K range per workgroup of the skinny GEMM: 256 (four waves x two k-steps, every load in
+// flight at once) when that splits K evenly and the columns alone give too few workgroups.
+int skinny_kc(int N, int K) { return (N / 16 < 2048 && K % 256 == 0) ? 256 : K; }
+
+hipError_t skinny(const GemmArgs &g, int dt, float *partial, hipStream_t s) {
+    if (g.K % 128 || g.N % 16 || g.M > 32) return hipErrorInvalidValue;
+    const int kc = skinny_kc(g.N, g.K), ranges = g.K / kc;
+    const dim3 grid(g.N / 16, ranges);
+    if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL(k_gemm_skinny<SH_DTYPE_BF16>, grid, dim3(kT), 0, s, g, partial, kc);
+    else hipLaunchKernelGGL(k_gemm_skinny<SH_DTYPE_F16>, grid, dim3(kT), 0, s, g, partial, kc);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || ranges == 1 || g.partial_only) return e;
+    const int pairs = g.M * (g.N / 2);
+    hipLaunchKernelGGL(k_gemm_skinny_reduce, dim3((pairs + kT - 1) / kT), dim3(kT), 0, s, g,
+                       (const float *)partial, ranges);
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t batch_alloc(sh_model *m, int B) {
+    if (m->bt_cap >= B) return hipSuccess;
+    const sh_config &c = m->cfg;
+    if (m->bt_ready) {
+        (void)hipGraphExecDestroy(m->bt_exec);
+        m->bt_ready = false;
+    }
+    (void)hipFree(m->bt_arena);
+    m->bt_arena = nullptr;
+    m->bt_cap = 0;
+    const size_t D = c.dim, F = c.hidden, Q = m->qdim, KV = m->kvdim, R = m->qkv_rows, V = c.vocab;
+    const size_t W = std::max({D, Q, F});
+    const int chunk = attn_chunk(c.head_dim * (c.kv_dtype == SH_KV_F32 ? 4 : 2));
+    const size_t nch = ((size_t)c.max_seq + chunk - 1) / chunk;
+    m->bt_nch = (int)nch;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += (bytes + 255) / 256 * 256;
+        return o;
+    };
+    const size_t o_tok = take(4 * B), o_pos = take(4 * B), o_seq = take(4 * B),
+                 o_hist = take(4 * (size_t)B * (c.max_seq + 1)), o_x = take(4 * B * D),
+                 o_x2 = take(4 * B * D), o_xn = take(4 * B * W), o_qkv = take(4 * B * R),
+                 o_q = take(4 * B * Q), o_k = take(4 * B * KV), o_v = take(4 * B * KV),
+                 o_att = take(4 * B * Q), o_gate = take(4 * B * F), o_log = take(4 * B * V),
+                 o_pm = take(4 * B * c.n_heads * nch), o_pl = take(4 * B * c.n_heads * nch),
+                 o_pacc = take(4 * B * c.n_heads * nch * c.head_dim);
+    // skinny-GEMM K-range partials: the largest (ranges x N) of the layer projections
+    size_t part = 0;
+    for (auto nk : {std::make_pair(R, D), std::make_pair(D, Q), std::make_pair(2 * F, D),
+                    std::make_pair(D, F)}) {
+        const size_t kc = skinny_kc((int)nk.first, (int)nk.second);
+        part = std::max(part, nk.second / kc * nk.first);
+    }
+    if (skinny_kc((int)V, (int)D) != D)   // a split classifier GEMM keeps partials too
+        part = std::max(part, D / skinny_kc((int)V, (int)D) * V);
+    const size_t o_part = take(4 * B * std::max(part, (size_t)1));
+    const size_t nblk = (V + kArgChunk - 1) / kArgChunk;
+    const size_t o_apv = take(4 * B * nblk), o_api = take(4 * B * nblk);
+    hipError_t e = hipMalloc(&m->bt_arena, off);
+    if (e != hipSuccess) return e;
+    uint8_t *A = (uint8_t *)m->bt_arena;
+    m->bt_tok = (int32_t *)(A + o_tok);
+    m->bt_pos = (int32_t *)(A + o_pos);
+    m->bt_seq = (int32_t *)(A + o_seq);
+    m->bt_hist = (int32_t *)(A + o_hist);
+    m->bt_x = (float *)(A + o_x);
+    m->bt_x2 = (float *)(A + o_x2);
+    m->bt_xn = (uint16_t *)(A + o_xn);
+    m->bt_qkv = (float *)(A + o_qkv);
+    m->bt_q = (float *)(A + o_q);
+    m->bt_k = (float *)(A + o_k);
+    m->bt_v = (float *)(A + o_v);
+    m->bt_att = (uint16_t *)(A + o_att);
+    m->bt_gate = (uint16_t *)(A + o_gate);
+    m->bt_logits = (float *)(A + o_log);
+    m->bt_pm = (float *)(A + o_pm);
+    m->bt_pl = (float *)(A + o_pl);
+    m->bt_pacc = (float *)(A + o_pacc);
+    m->bt_part = (float *)(A + o_part);
+    m->bt_apv = (float *)(A + o_apv);
+    m->bt_api = (int32_t *)(A + o_api);
+    m->bt_cap = B;
+    std::vector<int32_t> seq(B);
+    for (int b = 0; b < B; b++) seq[b] = b;
+    return hipMemcpy(m->bt_seq, seq.data(), 4 * (size_t)B, hipMemcpyHostToDevice);
+}
+
+
+bool batch_supported(const sh_model *m, int B, std::string *why) {
+    if (!prefill_supported(m, why)) return false;
+    const sh_config &c = m->cfg;
+    if (B < 1 || B > 32 || B > c.max_batch) {
+        *why = "batch must be 1..min(32, max_batch)";
+        return false;
+    }
+    if (c.dim % 128 || m->qdim % 128 || c.hidden % 128) {
+        *why = "batched decode needs dim, n_heads*head_dim and hidden multiples of 128";
+        return false;
+    }
+    if (c.n_heads / c.n_kv_heads > kMaxGroupB || (c.n_heads / c.n_kv_heads) * c.head_dim > kT) {
+        *why = "batched decode needs (q heads per kv head) * head_dim <= 256";
+        return false;
+    }
+    return true;
+}
+
+// One decode step for the B sequences: token bt_tok[b] at position bt_pos[b] of sequence b
+// (its K/V appended to the cache), logits [B, V], then argmax and advance (bt_hist row b,
+// column pos+1). Everything reads its positions from device memory, so the step can be
+// captured once and replayed.
+hipError_t enqueue_batch_step(sh_model *m, int B) {
+    const sh_config &c = m->cfg;
+    const int dt = m->dtype;
+    const int D = c.dim, F = c.hidden;
+    hipStream_t s = m->stream;
+    hipError_t e;
+    hipLaunchKernelGGL(k_embed_rows, dim3(B), dim3(kT), 0, s, (const uint16_t *)m->embed, m->bt_tok,
+                       c.vocab, D, dt, m->bt_x);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(B), dim3(kT), 0, s, m->bt_x, m->layers[0].rms_att, D,
+                       c.norm_eps, 0, dt, m->bt_xn, (size_t)B * D);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const float scale = (float)(1.0 / sqrt((double)c.head_dim));
+    const int nch = m->bt_nch;
+    const int chunk = attn_chunk(c.head_dim * (c.kv_dtype == SH_KV_F32 ? 4 : 2));
+    auto ranges = [](int N, int K) { return K / skinny_kc(N, K); };
+    for (int l = 0; l < c.n_layers; l++) {
+        const LayerDev &L = m->layers[l];
+        // q|k|v projection; row kernel: K-range sum, QK-norm, RoPE, KV append, q out
+        GemmArgs g{};
+        g.A = m->bt_xn; g.B = (const uint16_t *)L.wqkv; g.M = B; g.N = m->qkv_rows; g.K = D;
+        g.dt = dt; g.partial_only = 1;
+        if ((e = skinny(g, dt, m->bt_part, s)) != hipSuccess) return e;
+        const QkRopeArgs qa = qk_rope_args(m, L, m->bt_pos, m->bt_seq, m->bt_q, nullptr, nullptr, l, true);
+        const int rq = ranges(m->qkv_rows, D);
+        if (c.kv_dtype == SH_KV_F32)
+            hipLaunchKernelGGL(k_row_qkv<SH_KV_F32>, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part, rq, B, qa);
+        else if (c.kv_dtype == SH_KV_F16)
+            hipLaunchKernelGGL(k_row_qkv<SH_KV_F16>, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part, rq, B, qa);
+        else
+            hipLaunchKernelGGL(k_row_qkv<SH_KV_BF16>, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part, rq, B, qa);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        // attention over each sequence's cache, split over the keys, then merged
+        const void *kc = kv_layer_base(m, m->kcache, l), *vc = kv_layer_base(m, m->vcache, l);
+        const dim3 grid(nch, c.n_kv_heads, B);
+        if (c.kv_dtype == SH_KV_F32)
+            hipLaunchKernelGGL(k_attn_batch_partial<SH_KV_F32>, grid, dim3(kT), 0, s, m->bt_q, kc, vc,
+                               kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, c.head_dim,
+                               scale, nch, m->bt_pm, m->bt_pl, m->bt_pacc);
+        else if (c.kv_dtype == SH_KV_F16)
+            hipLaunchKernelGGL(k_attn_batch_partial<SH_KV_F16>, grid, dim3(kT), 0, s, m->bt_q, kc, vc,
+                               kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, c.head_dim,
+                               scale, nch, m->bt_pm, m->bt_pl, m->bt_pacc);
+        else
+            hipLaunchKernelGGL(k_attn_batch_partial<SH_KV_BF16>, grid, dim3(kT), 0, s, m->bt_q, kc, vc,
+                               kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, c.head_dim,
+                               scale, nch, m->bt_pm, m->bt_pl, m->bt_pacc);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_attn_batch_combine, dim3(c.n_heads, B), dim3(256), 0, s, m->bt_pm,
+                           m->bt_pl, m->bt_pacc, m->bt_pos, c.n_heads, c.head_dim, nch, chunk, B,
+                           dt, m->bt_att);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        // Wo; row kernel: x2 = x + alpha * (att . Wo^T), then rmsnorm(x2) with rms_ffn
+        g = GemmArgs{};
+        g.A = m->bt_att; g.B = (const uint16_t *)L.wo; g.M = B; g.N = D; g.K = m->qdim;
+        g.dt = dt; g.partial_only = 1;
+        if ((e = skinny(g, dt, m->bt_part, s)) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_row_resid_norm, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part,
+                           ranges(D, m->qdim), B, D, (const float *)m->bt_x, c.residual_scale,
+                           m->bt_x2, L.rms_ffn, c.norm_eps, dt, m->bt_xn);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        // W1/W3 with the SiLU gate
+        g = GemmArgs{};
+        g.A = m->bt_xn; g.B = (const uint16_t *)L.w13; g.M = B; g.N = 2 * F; g.K = D;
+        g.epi = G_GATE; g.out16 = m->bt_gate; g.dt = dt; g.decode_forms = 1;
+        if ((e = skinny(g, dt, m->bt_part, s)) != hipSuccess) return e;
+        // W2; row kernel: x = x2 + alpha * (gate . W2^T), then rmsnorm(x) with the next
+        // layer's rms_att, or rms_final (rmsNormVec, infer.go:242) after the last layer
+        g = GemmArgs{};
+        g.A = m->bt_gate; g.B = (const uint16_t *)L.w2; g.M = B; g.N = D; g.K = F;
+        g.dt = dt; g.partial_only = 1;
+        if ((e = skinny(g, dt, m->bt_part, s)) != hipSuccess) return e;
+        const float *next_gain = l + 1 < c.n_layers ? m->layers[l + 1].rms_att : m->rms_final;
+        hipLaunchKernelGGL(k_row_resid_norm, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part,
+                           ranges(D, F), B, D, (const float *)m->bt_x2, c.residual_scale, m->bt_x,
+                           next_gain, c.norm_eps, dt, m->bt_xn);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    GemmArgs g{};
+    g.A = m->bt_xn; g.B = (const uint16_t *)m->cls; g.M = B; g.N = c.vocab; g.K = D;
+    g.epi = G_STORE; g.out = m->bt_logits; g.dt = dt;
+    if ((e = skinny(g, dt, m->bt_part, s)) != hipSuccess) return e;
+    const int nblk = (c.vocab + kArgChunk - 1) / kArgChunk;
+    hipLaunchKernelGGL(k_argmax_part, dim3(nblk, B), dim3(kT), 0, s, m->bt_logits, c.vocab, nblk,
+                       m->bt_apv, m->bt_api);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_argmax_advance, dim3(B), dim3(64), 0, s, m->bt_apv, m->bt_api, nblk,
+                       m->bt_tok, m->bt_pos, m->bt_hist, c.max_seq + 1);
+    return hipGetLastError();
 }
 
 }  // namespace sh

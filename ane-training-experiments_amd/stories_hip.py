@@ -74,6 +74,7 @@ class ShTiming(C.Structure):
         ("bytes_per_forward_mean", C.c_double),
         ("persistent", C.c_int32),
         ("grid", C.c_int32),
+        ("prefill_ms", C.c_double),
     ]
 
 
@@ -88,6 +89,8 @@ _lib = None
 # every entry point of include/stories_hip.h with its ctypes signature
 SIGNATURES = {
     "sh_init": (C.c_int, [C.c_int32]),
+    "sh_batch_greedy_decode": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32), C.c_int32, C.c_int32, C.c_int32,
+                                         C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "sh_decode_tap": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_float), C.c_int32]),
     "sh_copy_calibrate": (C.c_int, [C.c_size_t, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "sh_last_error": (C.c_size_t, [C.c_char_p, C.c_size_t]),
@@ -324,6 +327,20 @@ class Model:
         _check(self.lib.sh_decode_tap(self.h, which, _fp(out), n), "sh_decode_tap")
         return out
 
+    def batch_greedy_decode(self, prompts, max_new: int):
+        """sh_batch_greedy_decode: list of token arrays (prompt + generated, EOS-truncated)."""
+        p = np.ascontiguousarray(np.asarray(prompts, dtype=np.int32))
+        if p.ndim != 2:
+            raise ValueError("prompts must be a 2-D array [n_seqs, prompt_len]")
+        n, plen = p.shape
+        stride = plen + (max_new if max_new > 0 else 64)
+        out = np.zeros((n, stride), np.int32)
+        cnt = np.zeros(n, np.int32)
+        _check(self.lib.sh_batch_greedy_decode(self.h, p.ctypes.data_as(_I32), n, plen, max_new,
+                                                out.ctypes.data_as(_I32), cnt.ctypes.data_as(_I32)),
+               "sh_batch_greedy_decode")
+        return [out[i, :cnt[i]].copy() for i in range(n)]
+
     def trace_forward(self, forward: int) -> None:
         _check(self.lib.sh_trace_forward(self.h, forward), "sh_trace_forward")
 
@@ -358,7 +375,7 @@ class Model:
         _check(self.lib.sh_stats(self.h, C.byref(t)), "sh_stats")
         return {"gpu_ms": t.gpu_ms, "forwards": t.forwards, "tokens_out": t.tokens_out,
                 "bytes_per_forward_mean": t.bytes_per_forward_mean,
-                "persistent": bool(t.persistent), "grid": t.grid}
+                "persistent": bool(t.persistent), "grid": t.grid, "prefill_ms": t.prefill_ms}
 
     def close(self) -> None:
         if self.h:

@@ -65,6 +65,7 @@ typedef struct sh_timing {
     double bytes_per_forward_mean; /* algorithmic bytes per forward, averaged */
     int32_t persistent;     /* 1: the persistent decode kernel ran; 0: per-stage kernels */
     int32_t grid;           /* workgroups of the persistent kernel */
+    double prefill_ms;      /* sh_batch_greedy_decode: device time of the prompt prefill */
 } sh_timing;
 
 /* ---- library ------------------------------------------------------------------------ */
@@ -113,6 +114,19 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
  * channel-first [V, seq] (logits[v*seq + t]). Out-of-range ids give a zero embedding
  * column (cpu.go:41-72). Residual scale = cfg.residual_scale. */
 int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *logits_cf);
+/* Batched greedy decode: n_seqs independent (*Decoder).Decode runs with Temperature 0
+ * (infer.go:136-202 each), stepped together on the device. No single reference entry point
+ * does this; it is n_seqs decoders sharing one weight stream per step. prompts: n_seqs rows of
+ * prompt_len ids (1 <= prompt_len <= max_seq, ids in [0, vocab)); max_new <= 0 means 64. The
+ * first prompt_len - 1 ids of every row go through one causal forward that fills the KV
+ * caches; then each step feeds every sequence's latest token, so step i yields token
+ * prompt_len + i of every row. A row stops after EOS=2 or at max_seq tokens. out_tokens holds
+ * n_seqs rows of stride prompt_len + (max_new > 0 ? max_new : 64); n_out[s] is row s's count.
+ * Needs fp16 or bf16 weights, n_seqs <= min(32, cfg.max_batch). sh_stats then reports the
+ * decode steps (forwards = steps, tokens_out = tokens kept) and the prefill time. */
+int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
+                           int32_t prompt_len, int32_t max_new, int32_t *out_tokens,
+                           int32_t *n_out);
 /* Human-readable description of the decode path this model runs (persistent kernel or
  * per-stage kernels) and why; returns the full length. No reference counterpart: the
  * reference reports its ANE/CPU choice through Diagnostics (ane/storiesane/diagnostics.go). */

@@ -1,0 +1,141 @@
+"""GPU parity of the batched greedy decode (n sequences stepped together; the Qwen3-shaped
+32 x 1024-prefill configuration at full size) against the oracle's single-sequence Decode
+(infer.go:136-202) of each row, through the C ABI.
+
+Bar: every row's token stream identical to its own greedy decode. The prompt goes through
+one causal forward that fills the KV caches (decode numerics, K/V rounded to the cache type
+before attending), then lockstep steps with split-key attention, so logits differ from the
+token-by-token oracle by float rounding only."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import stories_hip as sh
+from helpers import random_gains, tiny_config, tiny_gqa_config
+
+pytestmark = pytest.mark.gpu
+
+THREADS = max(1, min(16, os.cpu_count() or 1))
+
+
+def build(cfg, dtype, seed, std=0.02, gains_seed=None):
+    w = sh.synth_weights(cfg, seed=seed, std=std)
+    if gains_seed is not None:
+        w = random_gains(w, gains_seed)
+    m = sh.Model(cfg, dtype)
+    m.upload(w)
+    ref = oracle.Decoder(oracle.config_from(cfg), w.rounded(dtype), threads=THREADS)
+    return m, ref
+
+
+def check_rows(m, ref, prompts, max_new):
+    got = m.batch_greedy_decode(prompts, max_new)
+    worst = np.inf
+    for b, p in enumerate(prompts):
+        ref.reset()
+        want, _, margins = ref.greedy_decode(p, max_new)
+        worst = min(worst, float(np.nanmin(margins)) if len(margins) else np.inf)
+        assert got[b].tolist() == want.tolist(), f"row {b}"
+    st = m.stats()
+    print(f"{len(prompts)} rows: smallest top-2 margin {worst:.3e}; prefill {st['prefill_ms']:.3f} ms, "
+          f"{st['forwards']} steps in {st['gpu_ms']:.3f} ms")
+    return got
+
+
+@pytest.mark.parametrize("dtype,kv", [(sh.SH_DTYPE_F16, sh.SH_KV_F32), (sh.SH_DTYPE_BF16, sh.SH_KV_BF16)])
+def test_batch_tiny(gpu, dtype, kv):
+    cfg = tiny_config(kv_dtype=kv, max_batch=4)
+    m, ref = build(cfg, dtype, seed=601, std=0.08, gains_seed=602)
+    prompts = sh.synth_tokens(3 * 10, 603, cfg.vocab).reshape(3, 10)
+    check_rows(m, ref, prompts, 20)
+    # again with another batch size and prompt length (the step graph is rebuilt)
+    prompts = sh.synth_tokens(4 * 5, 604, cfg.vocab).reshape(4, 5)
+    check_rows(m, ref, prompts, 12)
+    m.close()
+
+
+def test_batch_tiny_gqa_qknorm(gpu):
+    cfg = tiny_gqa_config(max_batch=2)
+    m, ref = build(cfg, sh.SH_DTYPE_BF16, seed=611, std=0.08, gains_seed=612)
+    prompts = sh.synth_tokens(2 * 16, 613, cfg.vocab).reshape(2, 16)
+    check_rows(m, ref, prompts, 24)
+    m.close()
+
+
+def test_batch_bookkeeping(gpu):
+    cfg = tiny_config(max_seq=40, max_batch=3)
+    m, ref = build(cfg, sh.SH_DTYPE_F16, seed=621, std=0.08)
+    # one-token prompts (no prefill), and the max_seq stop (30 + 10 = 40 tokens)
+    check_rows(m, ref, sh.synth_tokens(3, 622, cfg.vocab).reshape(3, 1), 8)
+    got = check_rows(m, ref, sh.synth_tokens(2 * 30, 623, cfg.vocab).reshape(2, 30), 25)
+    assert all(len(g) == 40 for g in got)
+    with pytest.raises(sh.ShError):
+        m.batch_greedy_decode(np.full((2, 4), cfg.vocab, np.int32), 4)
+    with pytest.raises(sh.ShError):
+        m.batch_greedy_decode(np.ones((4, 4), np.int32), 4)   # above max_batch
+    m.close()
+
+
+def test_batch_eos(gpu):
+    cfg = tiny_config(max_seq=32, tied_embed=0, max_batch=2)
+    w = sh.synth_weights(cfg, seed=631, std=0.08)
+    for lw in w.layers:
+        for k in sh.LAYER_KEYS:
+            lw[k] = np.zeros_like(lw[k])
+    w.embed = np.full_like(w.embed, 0.01)
+    w.cls = np.zeros_like(w.embed)
+    w.cls[2] = 1.0   # every argmax is EOS=2
+    m = sh.Model(cfg, sh.SH_DTYPE_F16)
+    m.upload(w)
+    got = m.batch_greedy_decode(np.array([[5, 9, 11], [7, 8, 9]], np.int32), 10)
+    assert [g.tolist() for g in got] == [[5, 9, 11, 2], [7, 8, 9, 2]]
+    m.close()
+
+
+def test_batch_qwen3_shaped_short(gpu):
+    cfg = sh.qwen3_06b_config()
+    cfg.max_batch = 2
+    m, ref = build(cfg, sh.SH_DTYPE_BF16, seed=3)
+    prompts = sh.synth_tokens(2 * 24, 641, cfg.vocab).reshape(2, 24)
+    check_rows(m, ref, prompts, 16)
+    m.close()
+
+
+def test_batch_qwen3_shaped_32x1024(gpu):
+    """The batched configuration: 32 sequences, 1024-id prompts (seed 4), 128 greedy steps,
+    bf16 KV. Exact: row 0 decoded alone (a batch of 1) equals row 0 of the batch of 32 (rows
+    do not interact). Against the single-sequence decode of the same prompt (itself pinned
+    to the oracle): identical tokens, except that where the streams part, the batch's token
+    must be within the 2e-2 logits bar of the maximum of the single path's logits there (the
+    two prompt paths round some bf16 cache entries differently, which can break a near-tie
+    either way)."""
+    cfg = sh.qwen3_06b_config()
+    cfg.max_batch = 32
+    w = sh.synth_weights(cfg, seed=3, std=0.02)
+    m = sh.Model(cfg, sh.SH_DTYPE_BF16)
+    m.upload(w)
+    prompts = sh.synth_tokens(32 * 1024, 4, cfg.vocab).reshape(32, 1024)
+    got = m.batch_greedy_decode(prompts, 128)
+    st = m.stats()
+    print(f"prefill {st['prefill_ms']:.1f} ms; {st['forwards']} steps in {st['gpu_ms']:.1f} ms = "
+          f"{st['tokens_out'] / (st['gpu_ms'] / 1e3):.0f} tokens/s, "
+          f"{st['bytes_per_forward_mean'] * st['forwards'] / (st['gpu_ms'] / 1e3) / 1e9:.0f} GB/s")
+    assert all(len(g) == 1024 + 128 or g[-1] == 2 for g in got)
+    alone = m.batch_greedy_decode(prompts[:1], 128)
+    assert alone[0].tolist() == got[0].tolist()
+    for b in (0, 31):
+        single, _, _ = m.greedy_decode(prompts[b], 128)
+        diff = [i for i in range(min(len(single), len(got[b]))) if single[i] != got[b][i]]
+        if not diff:
+            assert len(single) == len(got[b])
+            continue
+        i = diff[0]
+        m.reset_cache()
+        for p in range(i):
+            lg, _ = m.eval_next_logits(int(got[b][p]), p, want_logits=(p == i - 1))
+        gap = float(lg.max() - lg[int(got[b][i])])
+        print(f"row {b}: streams part at {i}; batch token {gap:.2e} below the single path's max")
+        assert gap <= 2e-2
+    m.close()
