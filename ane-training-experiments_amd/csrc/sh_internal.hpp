@@ -95,6 +95,8 @@ struct sh_model {
     int32_t *pf_tokens;                        // [S]
     float *pf_x, *pf_x2, *pf_qkv, *pf_logits;  // [S,D] [S,D] [S,qkv_rows] [V,S]
     int32_t *pf_rowpos, *pf_rowseq;            // [S] position and sequence of each row
+    float *pf_part;                            // K-range partials of split GEMMs
+    size_t pf_part_cap;                        // elements of pf_part
     float *pf_q, *pf_k, *pf_v;                 // roped q, k and v: [S,qdim] [S,kvdim] x2
     uint16_t *pf_xn, *pf_att, *pf_gate;        // GEMM operands: hi plane, then lo plane
 
@@ -107,6 +109,7 @@ struct sh_model {
     uint16_t *bt_xn, *bt_att, *bt_gate;        // GEMM operand planes
     float *bt_pm, *bt_pl, *bt_pacc;            // attention chunk partials
     float *bt_part;                            // skinny-GEMM K-range partials
+    size_t bt_part_cap;                        // elements of bt_part
     float *bt_apv;                             // argmax partials (value, index)
     int32_t *bt_api;
     hipGraphExec_t bt_exec;                    // one captured step for bt_graph_b sequences

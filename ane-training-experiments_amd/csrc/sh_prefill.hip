@@ -135,75 +135,109 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4 &a, const u32x4 &b, const f3
                                                       __builtin_bit_cast(half8, b), c, 0, 0, 0);
 }
 
-// Workgroup tile 64 x 64 (4 waves of 32 x 32 = 2 x 2 MFMA blocks), K step 32.
-// Requires K % 32 == 0 and N % 64 == 0; rows >= M read zeros and are not written.
-template <int DT>
-__global__ __launch_bounds__(kT) void k_gemm_nt(GemmArgs g) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int m0 = blockIdx.x * 64 + (wave >> 1) * 32;
-    const int n0 = blockIdx.y * 64 + (wave & 1) * 32;
-    const int lr = lane & 15, lk = (lane >> 4) * 8;
-    f32x4 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
-    const uint16_t *arow[2], *brow[2];
-    const size_t lo = (size_t)g.M * g.K;
-    bool aok[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int m = m0 + i * 16 + lr;
-        aok[i] = m < g.M;
-        arow[i] = g.A + (size_t)(aok[i] ? m : 0) * g.K + lk;
-        brow[i] = g.B + (size_t)(n0 + i * 16 + lr) * g.K + lk;
+// Epilogue of one output element pair (columns n, n+1 of row m) is shared with the skinny
+// GEMM (skinny_epilogue); the tiled GEMM applies it per element with the same forms.
+__device__ __forceinline__ void tile_epilogue(const GemmArgs &g, int m, int n, float v, float v_right) {
+    if (g.epi == G_GATE) {
+        if ((n & 1) == 0)
+            store_op(g.out16, (size_t)m * (g.N / 2) + (n >> 1), (size_t)g.M * (g.N / 2),
+                     silu_gate(v, v_right, g.decode_forms), g.dt);
+    } else if (g.epi == G_STORE) {
+        g.out[(size_t)m * g.N + n] = v;
+    } else if (g.epi == G_RESID) {
+        g.out[(size_t)m * g.N + n] = g.resid[(size_t)m * g.N + n] + g.alpha * v;
+    } else {
+        g.out[(size_t)n * g.M + m] = v;   // logits[v*S + t]
     }
-    for (int k0 = 0; k0 < g.K; k0 += 64) {
-        u32x4 a[2][2], al[2][2], b[2][2];
+}
+
+// Tiled MFMA GEMM: C[M, N] = A[M, K] . W[N, K]^T, A as hi/lo operand planes. Workgroup tile
+// BM x BN (2 x 2 waves of BM/2 x BN/2, 16 x 16 x 32 MFMA blocks), K in steps of 32 through
+// two LDS buffers: the next step's A hi, A lo and W rows are loaded into registers while
+// the MFMAs of this step read the other buffer. LDS rows are 64 data bytes padded to 80, so
+// the 16 rows x 4 chunks a wave reads for one fragment spread over the banks. Workgroup z
+// covers K range [z*kc, (z+1)*kc); with more than one range the tile goes to `partial`
+// ([ranges][M][N]) and k_gemm_skinny_reduce finishes it. Needs N % BN == 0, kc % 32 == 0.
+template <int DT, int BM, int BN>
+__global__ __launch_bounds__(kT) void k_gemm_tiled(GemmArgs g, float *partial, int kc) {
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+    constexpr int RS = 80;                       // LDS bytes per tile row (64 + 16 pad)
+    constexpr int R = 2 * BM + BN;               // tile rows: A hi, A lo, W
+    constexpr int PER = R * 4 / kT;              // 16-byte chunks per thread per step
+    static_assert(R * 4 % kT == 0, "tile chunks must split evenly over the workgroup");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][R * RS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int kbeg = blockIdx.z * kc, kend = kbeg + kc;
+    const size_t lo = (size_t)g.M * g.K;
+    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+    u32x4 stage[PER];
+    auto gload = [&](int k) {
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const int k = k0 + s * 32;
-            const bool kin = k < g.K;
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                a[s][i] = (aok[i] && kin) ? *(const u32x4 *)(arow[i] + k) : zero;
-                al[s][i] = (aok[i] && kin) ? *(const u32x4 *)(arow[i] + lo + k) : zero;
-                b[s][i] = kin ? *(const u32x4 *)(brow[i] + k) : zero;
+        for (int j = 0; j < PER; j++) {
+            const int ci = tid + j * kT, r = ci >> 2, c = ci & 3;
+            if (r < 2 * BM) {
+                const int m = m0 + (r < BM ? r : r - BM);
+                const uint16_t *src = g.A + (r < BM ? 0 : lo) + (size_t)m * g.K + k + c * 8;
+                stage[j] = m < g.M ? *(const u32x4 *)src : zero;
+            } else {
+                stage[j] = *(const u32x4 *)(g.B + (size_t)(n0 + r - 2 * BM) * g.K + k + c * 8);
             }
         }
+    };
+    auto lstore = [&](int buf) {
 #pragma unroll
-        for (int s = 0; s < 2; s++)
+        for (int j = 0; j < PER; j++) {
+            const int ci = tid + j * kT;
+            *(u32x4 *)(&lds[buf][(ci >> 2) * RS + (ci & 3) * 16]) = stage[j];
+        }
+    };
+    f32x4 acc[FM][FN];
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    acc[i][j] = mfma16<DT>(a[s][i], b[s][j], acc[i][j]);
-                    acc[i][j] = mfma16<DT>(al[s][i], b[s][j], acc[i][j]);
-                }
+        for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    gload(kbeg);
+    lstore(0);
+    __syncthreads();
+    int buf = 0;
+    const int fr = lane & 15, fc = (lane >> 4) * 16;   // fragment row, byte offset of k chunk
+    for (int k = kbeg; k < kend; k += 32) {
+        const bool more = k + 32 < kend;
+        if (more) gload(k + 32);
+        const uint8_t *L = lds[buf];
+        u32x4 bfr[FN];
+#pragma unroll
+        for (int j = 0; j < FN; j++) bfr[j] = *(const u32x4 *)(L + (2 * BM + wn + j * 16 + fr) * RS + fc);
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const u32x4 ah = *(const u32x4 *)(L + (wm + i * 16 + fr) * RS + fc);
+            const u32x4 al = *(const u32x4 *)(L + (BM + wm + i * 16 + fr) * RS + fc);
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                acc[i][j] = mfma16<DT>(ah, bfr[j], acc[i][j]);
+                acc[i][j] = mfma16<DT>(al, bfr[j], acc[i][j]);
+            }
+        }
+        if (more) lstore(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
     }
-    // D layout: lane holds column lr of the 16x16 block, rows 4*(lane/16) + r
+    // D layout: lane holds column fr of each 16 x 16 block, rows 4*(lane/16) + r
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + j * 16 + lr;
+        for (int j = 0; j < FN; j++) {
+            const int n = n0 + wn + j * 16 + fr;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = m0 + i * 16 + (lane >> 4) * 4 + r;
+                const int m = m0 + wm + i * 16 + (lane >> 4) * 4 + r;
                 const float v = acc[i][j][r];
-                if (g.epi == G_GATE) {
-                    // rows 2q (W1) and 2q+1 (W3) of the weight are adjacent columns here
-                    const float h3 = __shfl_xor(v, 1, 64);
-                    if ((n & 1) == 0 && m < g.M)
-                        store_op(g.out16, (size_t)m * (g.N / 2) + (n >> 1), (size_t)g.M * (g.N / 2),
-                                 silu_gate(v, h3, g.decode_forms), g.dt);
-                } else if (m < g.M) {
-                    if (g.epi == G_STORE) g.out[(size_t)m * g.N + n] = v;
-                    else if (g.epi == G_RESID)
-                        g.out[(size_t)m * g.N + n] = g.resid[(size_t)m * g.N + n] + g.alpha * v;
-                    else g.out[(size_t)n * g.M + m] = v;   // logits[v*S + t]
-                }
+                const float vr = __shfl_xor(v, 1, 64);   // column n ^ 1, same row
+                if (m >= g.M) continue;
+                if (gridDim.z > 1) partial[((size_t)blockIdx.z * g.M + m) * g.N + n] = v;
+                else tile_epilogue(g, m, n, v, vr);
             }
         }
 }
@@ -784,11 +818,42 @@ __global__ __launch_bounds__(64) void k_argmax_advance(const float *pv, const in
     }
 }
 
-hipError_t gemm(const GemmArgs &g, int dt, hipStream_t s) {
+// Tile shape and K split of the tiled GEMM: 128 x 128 tiles for long inputs, else 64 x 64
+// with K split (ranges of >= 256, dividing K) until there are about 512 workgroups.
+struct GemmPlan {
+    int big, ranges, kc;
+};
+GemmPlan gemm_plan(int M, int N, int K) {
+    GemmPlan p{};
+    p.big = M >= 1024 && N % 128 == 0;
+    const int tiles = p.big ? ((M + 127) / 128) * (N / 128) : ((M + 63) / 64) * (N / 64);
+    p.ranges = 1;
+    for (int r : {2, 3, 4, 6, 8, 12, 16})
+        if (K % (32 * r) == 0 && K / r >= 256 && tiles * r <= 768) p.ranges = r;
+    if (tiles >= 512) p.ranges = 1;
+    p.kc = K / p.ranges;
+    return p;
+}
+
+hipError_t gemm(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipStream_t s) {
     if (g.K % 32 || g.N % 64) return hipErrorInvalidValue;
-    dim3 grid((g.M + 63) / 64, g.N / 64);
-    if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL(k_gemm_nt<SH_DTYPE_BF16>, grid, dim3(kT), 0, s, g);
-    else hipLaunchKernelGGL(k_gemm_nt<SH_DTYPE_F16>, grid, dim3(kT), 0, s, g);
+    const GemmPlan p = gemm_plan(g.M, g.N, g.K);
+    if (p.ranges > 1 && (!partial || (size_t)p.ranges * g.M * g.N > part_cap))
+        return hipErrorInvalidValue;   // the partial buffer must hold every K range
+    if (p.big) {
+        const dim3 grid((g.M + 127) / 128, g.N / 128, p.ranges);
+        if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_BF16, 128, 128>), grid, dim3(kT), 0, s, g, partial, p.kc);
+        else hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_F16, 128, 128>), grid, dim3(kT), 0, s, g, partial, p.kc);
+    } else {
+        const dim3 grid((g.M + 63) / 64, g.N / 64, p.ranges);
+        if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_BF16, 64, 64>), grid, dim3(kT), 0, s, g, partial, p.kc);
+        else hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_F16, 64, 64>), grid, dim3(kT), 0, s, g, partial, p.kc);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.ranges == 1) return e;
+    const int pairs = g.M * (g.N / 2);
+    hipLaunchKernelGGL(k_gemm_skinny_reduce, dim3((pairs + kT - 1) / kT), dim3(kT), 0, s, g,
+                       (const float *)partial, p.ranges);
     return hipGetLastError();
 }
 
@@ -812,12 +877,32 @@ bool prefill_supported(const sh_model *m, std::string *why) {
     return true;
 }
 
+// K-range partial elements the split GEMMs of an S-row forward need. A shorter input has
+// fewer tiles and so may split K further: the need is not monotonic in S.
+static size_t prefill_part_need(const sh_model *m, int S) {
+    const sh_config &c = m->cfg;
+    const size_t D = c.dim, F = c.hidden, Q = m->qdim, R = m->qkv_rows, V = c.vocab;
+    size_t part = 1;
+    for (auto nk : {std::make_pair(R, D), std::make_pair(D, Q), std::make_pair(2 * F, D),
+                    std::make_pair(D, F), std::make_pair(V, D)}) {
+        const GemmPlan gp = gemm_plan(S, (int)nk.first, (int)nk.second);
+        if (gp.ranges > 1) part = std::max(part, (size_t)gp.ranges * S * nk.first);
+    }
+    return part;
+}
+
 hipError_t prefill_alloc(sh_model *m, int S, bool logits) {
-    if (m->pf_cap >= S && (!logits || m->pf_logits)) return hipSuccess;
+    const size_t need = prefill_part_need(m, S);
+    if (m->pf_cap >= S && (!logits || m->pf_logits) && m->pf_part_cap >= need) return hipSuccess;
+    const bool want_logits = logits || m->pf_logits;
+    S = std::max(S, m->pf_cap);
+    const size_t part = std::max({need, m->pf_part_cap, prefill_part_need(m, S)});
+    logits = want_logits;
     const sh_config &c = m->cfg;
     (void)hipFree(m->pf_arena);
     m->pf_arena = nullptr;
     m->pf_cap = 0;
+    m->pf_part_cap = 0;
     m->pf_logits = nullptr;
     const size_t D = c.dim, F = c.hidden, Q = m->qdim, KV = m->kvdim, R = m->qkv_rows, V = c.vocab;
     size_t off = 0;
@@ -831,6 +916,7 @@ hipError_t prefill_alloc(sh_model *m, int S, bool logits) {
                  o_qkv = take(4 * S * R), o_q = take(4 * S * Q), o_k = take(4 * S * KV),
                  o_v = take(4 * S * KV), o_att = take(4 * S * Q), o_gate = take(4 * S * F),
                  o_log = logits ? take(4 * V * S) : 0;
+    const size_t o_part = take(4 * part);   // K-range partials of the split GEMMs
     hipError_t e = hipMalloc(&m->pf_arena, off);
     if (e != hipSuccess) return e;
     uint8_t *A = (uint8_t *)m->pf_arena;
@@ -847,6 +933,8 @@ hipError_t prefill_alloc(sh_model *m, int S, bool logits) {
     m->pf_att = (uint16_t *)(A + o_att);
     m->pf_gate = (uint16_t *)(A + o_gate);
     m->pf_logits = logits ? (float *)(A + o_log) : nullptr;
+    m->pf_part = (float *)(A + o_part);
+    m->pf_part_cap = part;
     m->pf_cap = S;
     return hipSuccess;
 }
@@ -922,7 +1010,7 @@ hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fi
         GemmArgs g{};
         g.A = m->pf_xn; g.B = (const uint16_t *)L.wqkv; g.M = S; g.N = m->qkv_rows; g.K = D;
         g.epi = G_STORE; g.out = m->pf_qkv; g.dt = dt;
-        if ((e = gemm(g, dt, s)) != hipSuccess) return e;
+        if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
         if ((e = launch_qk_rope(m, L, S, m->pf_qkv, m->pf_rowpos, m->pf_rowseq, m->pf_q,
                                 m->pf_k, m->pf_v, l, fill_kv, s)) != hipSuccess)
             return e;
@@ -935,17 +1023,17 @@ hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fi
         g = GemmArgs{};
         g.A = m->pf_att; g.B = (const uint16_t *)L.wo; g.M = S; g.N = D; g.K = m->qdim;
         g.epi = G_RESID; g.out = m->pf_x2; g.resid = m->pf_x; g.alpha = c.residual_scale; g.dt = dt;
-        if ((e = gemm(g, dt, s)) != hipSuccess) return e;
+        if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x2, L.rms_ffn, D,
                            c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D);
         g = GemmArgs{};
         g.A = m->pf_xn; g.B = (const uint16_t *)L.w13; g.M = S; g.N = 2 * F; g.K = D;
         g.epi = G_GATE; g.out16 = m->pf_gate; g.dt = dt; g.decode_forms = fill_kv ? 1 : 0;
-        if ((e = gemm(g, dt, s)) != hipSuccess) return e;
+        if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
         g = GemmArgs{};
         g.A = m->pf_gate; g.B = (const uint16_t *)L.w2; g.M = S; g.N = D; g.K = F;
         g.epi = G_RESID; g.out = m->pf_x; g.resid = m->pf_x2; g.alpha = c.residual_scale; g.dt = dt;
-        if ((e = gemm(g, dt, s)) != hipSuccess) return e;
+        if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
     }
     if (!logits) return hipSuccess;
     hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x, m->rms_final, D,
@@ -953,7 +1041,7 @@ hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fi
     GemmArgs g{};
     g.A = m->pf_xn; g.B = (const uint16_t *)m->cls; g.M = S; g.N = c.vocab; g.K = D;
     g.epi = G_LOGITS_CF; g.out = m->pf_logits; g.dt = dt;
-    return gemm(g, dt, s);
+    return gemm(g, dt, m->pf_part, m->pf_part_cap, s);
 }
 
 
@@ -962,9 +1050,11 @@ namespace {
 // flight at once) when that splits K evenly and the columns alone give too few workgroups.
 int skinny_kc(int N, int K) { return (N / 16 < 2048 && K % 256 == 0) ? 256 : K; }
 
-hipError_t skinny(const GemmArgs &g, int dt, float *partial, hipStream_t s) {
+hipError_t skinny(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipStream_t s) {
     if (g.K % 128 || g.N % 16 || g.M > 32) return hipErrorInvalidValue;
     const int kc = skinny_kc(g.N, g.K), ranges = g.K / kc;
+    if ((ranges > 1 || g.partial_only) && (size_t)ranges * g.M * g.N > part_cap)
+        return hipErrorInvalidValue;   // the partial buffer must hold every K range
     const dim3 grid(g.N / 16, ranges);
     if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL(k_gemm_skinny<SH_DTYPE_BF16>, grid, dim3(kT), 0, s, g, partial, kc);
     else hipLaunchKernelGGL(k_gemm_skinny<SH_DTYPE_F16>, grid, dim3(kT), 0, s, g, partial, kc);
@@ -1038,6 +1128,7 @@ hipError_t batch_alloc(sh_model *m, int B) {
     m->bt_pl = (float *)(A + o_pl);
     m->bt_pacc = (float *)(A + o_pacc);
     m->bt_part = (float *)(A + o_part);
+    m->bt_part_cap = (size_t)B * std::max(part, (size_t)1);
     m->bt_apv = (float *)(A + o_apv);
     m->bt_api = (int32_t *)(A + o_api);
     m->bt_cap = B;
@@ -1091,7 +1182,7 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         GemmArgs g{};
         g.A = m->bt_xn; g.B = (const uint16_t *)L.wqkv; g.M = B; g.N = m->qkv_rows; g.K = D;
         g.dt = dt; g.partial_only = 1;
-        if ((e = skinny(g, dt, m->bt_part, s)) != hipSuccess) return e;
+        if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         const QkRopeArgs qa = qk_rope_args(m, L, m->bt_pos, m->bt_seq, m->bt_q, nullptr, nullptr, l, true);
         const int rq = ranges(m->qkv_rows, D);
         if (c.kv_dtype == SH_KV_F32)
@@ -1125,7 +1216,7 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         g = GemmArgs{};
         g.A = m->bt_att; g.B = (const uint16_t *)L.wo; g.M = B; g.N = D; g.K = m->qdim;
         g.dt = dt; g.partial_only = 1;
-        if ((e = skinny(g, dt, m->bt_part, s)) != hipSuccess) return e;
+        if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         hipLaunchKernelGGL(k_row_resid_norm, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part,
                            ranges(D, m->qdim), B, D, (const float *)m->bt_x, c.residual_scale,
                            m->bt_x2, L.rms_ffn, c.norm_eps, dt, m->bt_xn);
@@ -1134,13 +1225,13 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         g = GemmArgs{};
         g.A = m->bt_xn; g.B = (const uint16_t *)L.w13; g.M = B; g.N = 2 * F; g.K = D;
         g.epi = G_GATE; g.out16 = m->bt_gate; g.dt = dt; g.decode_forms = 1;
-        if ((e = skinny(g, dt, m->bt_part, s)) != hipSuccess) return e;
+        if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         // W2; row kernel: x = x2 + alpha * (gate . W2^T), then rmsnorm(x) with the next
         // layer's rms_att, or rms_final (rmsNormVec, infer.go:242) after the last layer
         g = GemmArgs{};
         g.A = m->bt_gate; g.B = (const uint16_t *)L.w2; g.M = B; g.N = D; g.K = F;
         g.dt = dt; g.partial_only = 1;
-        if ((e = skinny(g, dt, m->bt_part, s)) != hipSuccess) return e;
+        if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         const float *next_gain = l + 1 < c.n_layers ? m->layers[l + 1].rms_att : m->rms_final;
         hipLaunchKernelGGL(k_row_resid_norm, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part,
                            ranges(D, F), B, D, (const float *)m->bt_x2, c.residual_scale, m->bt_x,
@@ -1150,7 +1241,7 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
     GemmArgs g{};
     g.A = m->bt_xn; g.B = (const uint16_t *)m->cls; g.M = B; g.N = c.vocab; g.K = D;
     g.epi = G_STORE; g.out = m->bt_logits; g.dt = dt;
-    if ((e = skinny(g, dt, m->bt_part, s)) != hipSuccess) return e;
+    if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
     const int nblk = (c.vocab + kArgChunk - 1) / kArgChunk;
     hipLaunchKernelGGL(k_argmax_part, dim3(nblk, B), dim3(kT), 0, s, m->bt_logits, c.vocab, nblk,
                        m->bt_apv, m->bt_api);
