@@ -481,6 +481,8 @@ void sh_model_destroy(sh_model *m) {
     (void)hipFree(m->pf_arena);
     if (m->bt_ready) (void)hipGraphExecDestroy(m->bt_exec);
     (void)hipFree(m->bt_arena);
+    if (m->wd_ready) (void)hipGraphExecDestroy(m->wd_exec);
+    (void)hipFree(m->wd_arena);
     if (m->ev0) (void)hipEventDestroy(m->ev0);
     if (m->ev1) (void)hipEventDestroy(m->ev1);
     if (m->stream) (void)hipStreamDestroy(m->stream);
@@ -870,6 +872,96 @@ int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
     m->last.bytes_per_forward_mean = steps ? bytes / steps : 0;
     m->last.persistent = 0;
     m->last.grid = 0;
+    return 0;
+}
+
+int sh_window_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32_t seq,
+                            int32_t max_new, int32_t *out_tokens, int32_t *n_out,
+                            int32_t *stopped_eos) {
+    if (!ready(m)) return -1;
+    const sh_config &c = m->cfg;
+    if ((!prompt && n_prompt > 0) || n_prompt < 0 || !out_tokens || !n_out || !stopped_eos ||
+        seq < 1 || seq > c.max_seq) {
+        set_error("sh_window_greedy_decode: bad arguments");
+        return -1;
+    }
+    std::string why;
+    if (!prefill_supported(m, &why)) {
+        set_error("sh_window_greedy_decode: " + why);
+        return -1;
+    }
+    if (max_new <= 0) max_new = 64;                         // decode.go:22-25
+    std::vector<int32_t> toks;                              // decode.go:35-46
+    if (n_prompt == 0) toks.push_back(kBos);
+    else toks.assign(prompt + (n_prompt > seq ? n_prompt - seq : 0), prompt + n_prompt);
+    for (size_t i = 0; i < toks.size(); i++)
+        if (toks[i] < 0 || toks[i] >= c.vocab) {
+            set_error("sh_window_greedy_decode: prompt token[" + std::to_string(i) + "]=" +
+                      std::to_string(toks[i]) + " out of range");
+            return -1;
+        }
+    const int P = (int)toks.size();
+    (void)hipSetDevice(m->device);
+    if (!hip_ok(prefill_alloc(m, seq, false), "window scratch") ||
+        !hip_ok(window_alloc(m, max_new), "window scratch"))
+        return -1;
+    hipStream_t s = m->stream;
+    // the window (fillDecodeWindow), rows at positions 0..seq-1 of one sequence
+    std::vector<int32_t> rows(3 * (size_t)seq, kBos);
+    for (int i = 0; i < P; i++) rows[seq - P + i] = toks[i];
+    for (int t = 0; t < seq; t++) {
+        rows[seq + t] = t;
+        rows[2 * (size_t)seq + t] = 0;
+    }
+    const int32_t zero = 0;
+    if (!hip_ok(hipMemcpyAsync(m->pf_tokens, rows.data(), 4 * (size_t)seq, hipMemcpyHostToDevice, s), "window") ||
+        !hip_ok(hipMemcpyAsync(m->pf_rowpos, rows.data() + seq, 4 * (size_t)seq, hipMemcpyHostToDevice, s), "window") ||
+        !hip_ok(hipMemcpyAsync(m->pf_rowseq, rows.data() + 2 * (size_t)seq, 4 * (size_t)seq, hipMemcpyHostToDevice, s), "window") ||
+        !hip_ok(hipMemcpyAsync(m->wd_count, &zero, 4, hipMemcpyHostToDevice, s), "window"))
+        return -1;
+    if (!m->wd_ready || m->wd_seq != seq) {
+        if (m->wd_ready) (void)hipGraphExecDestroy(m->wd_exec);
+        m->wd_ready = false;
+        hipGraph_t g = nullptr;
+        if (!hip_ok(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "capture")) return -1;
+        const hipError_t e2 = enqueue_window_step(m, seq);
+        const hipError_t e3 = hipStreamEndCapture(s, &g);
+        if (!hip_ok(e2, "window step") || !hip_ok(e3, "end capture")) {
+            if (g) (void)hipGraphDestroy(g);
+            return -1;
+        }
+        const hipError_t e4 = hipGraphInstantiate(&m->wd_exec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (!hip_ok(e4, "instantiate window step")) return -1;
+        m->wd_ready = true;
+        m->wd_seq = seq;
+    }
+    bool ok = hip_ok(hipEventRecord(m->ev0, s), "event");
+    for (int i = 0; ok && i < max_new; i++) ok = hip_ok(hipGraphLaunch(m->wd_exec, s), "window step");
+    ok = ok && hip_ok(hipEventRecord(m->ev1, s), "event") && hip_ok(hipStreamSynchronize(s), "window sync");
+    std::vector<int32_t> gen(max_new);
+    ok = ok && hip_ok(hipMemcpy(gen.data(), m->wd_hist, 4 * (size_t)max_new, hipMemcpyDeviceToHost), "read tokens");
+    if (!ok) return -1;
+    memcpy(out_tokens, toks.data(), 4 * (size_t)P);
+    int n = P, eos = 0;
+    for (int i = 0; i < max_new; i++) {
+        out_tokens[n++] = gen[i];
+        if (gen[i] == kEos) {   // decode.go:66-69: EOS is kept, the loop ends
+            eos = 1;
+            break;
+        }
+    }
+    *n_out = n;
+    *stopped_eos = eos;
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, m->ev0, m->ev1);
+    m->last.gpu_ms = ms;
+    m->last.forwards = max_new;
+    m->last.tokens_out = n - P;
+    m->last.bytes_per_forward_mean = prefill_bytes(m, seq);
+    m->last.persistent = 0;
+    m->last.grid = 0;
+    m->last.prefill_ms = 0;
     return 0;
 }
 

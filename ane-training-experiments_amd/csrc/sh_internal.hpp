@@ -115,6 +115,17 @@ struct sh_model {
     hipGraphExec_t bt_exec;                    // one captured step for bt_graph_b sequences
     bool bt_ready;
     int bt_graph_b;
+
+    // window decode (sh_prefill.hip): the window lives in pf_tokens
+    void *wd_arena;
+    int wd_cap;                                // tokens wd_hist holds
+    uint16_t *wd_xn;                           // last row, normalised (operand planes)
+    float *wd_logits, *wd_part, *wd_apv;
+    size_t wd_part_cap;
+    int32_t *wd_api, *wd_hist, *wd_count;
+    hipGraphExec_t wd_exec;                    // one captured step for window length wd_seq
+    bool wd_ready;
+    int wd_seq;
 };
 
 namespace sh {
@@ -152,6 +163,9 @@ bool batch_supported(const sh_model *m, int B, std::string *why);
 hipError_t batch_alloc(sh_model *m, int B);
 // One greedy step of B sequences (token bt_tok at bt_pos each), argmax into bt_hist.
 hipError_t enqueue_batch_step(sh_model *m, int B);
+hipError_t window_alloc(sh_model *m, int max_new);
+// One full-window decode step over pf_tokens[0, seq): next token into wd_hist, window shift.
+hipError_t enqueue_window_step(sh_model *m, int seq);
 void persistent_fill_layer_ptrs(const sh_model *m, void *host);
 
 }  // namespace sh

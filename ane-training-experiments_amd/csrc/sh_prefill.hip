@@ -818,6 +818,56 @@ __global__ __launch_bounds__(64) void k_argmax_advance(const float *pv, const in
     }
 }
 
+// Window decode step tail (decode.go:55-70): reduce the argmax partials of the last
+// column's logits, record the token (hist[*count]), shift the window left by one and append
+// it (fillDecodeWindow of the grown token list, :83-94).
+__global__ __launch_bounds__(kT) void k_window_advance(const float *pv, const int32_t *pi, int nblk,
+                                                       int32_t *window, int seq, int32_t *hist,
+                                                       int32_t *count) {
+    __shared__ int next_s;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        float v = -INFINITY;
+        int idx = 0x7fffffff;
+        for (int k = lane; k < nblk; k += 64)
+            if (pv[k] > v || (pv[k] == v && pi[k] < idx)) {
+                v = pv[k];
+                idx = pi[k];
+            }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(v, off, 64);
+            const int oi = __shfl_xor(idx, off, 64);
+            if (ov > v || (ov == v && oi < idx)) {
+                v = ov;
+                idx = oi;
+            }
+        }
+        if (lane == 0) {
+            next_s = idx == 0x7fffffff ? 0 : idx;
+            const int c = *count;
+            hist[c] = next_s;
+            *count = c + 1;
+        }
+    }
+    __syncthreads();
+    // the shift reads window[i + 1] before any thread overwrites it: stage in registers
+    // (seq <= 4096, so at most 16 values per thread)
+    int vals[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int i = threadIdx.x + k * kT;
+        if (i < seq - 1) vals[k] = window[i + 1];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int i = threadIdx.x + k * kT;
+        if (i < seq - 1) window[i] = vals[k];
+    }
+    if (threadIdx.x == 0) window[seq - 1] = next_s;
+}
+
 // Tile shape and K split of the tiled GEMM: 128 x 128 tiles for long inputs, else 64 x 64
 // with K split (ranges of >= 256, dividing K) until there are about 512 workgroups.
 struct GemmPlan {
@@ -899,6 +949,10 @@ hipError_t prefill_alloc(sh_model *m, int S, bool logits) {
     const size_t part = std::max({need, m->pf_part_cap, prefill_part_need(m, S)});
     logits = want_logits;
     const sh_config &c = m->cfg;
+    if (m->wd_ready) {   // the captured window step points into this scratch
+        (void)hipGraphExecDestroy(m->wd_exec);
+        m->wd_ready = false;
+    }
     (void)hipFree(m->pf_arena);
     m->pf_arena = nullptr;
     m->pf_cap = 0;
@@ -1248,6 +1302,69 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_argmax_advance, dim3(B), dim3(64), 0, s, m->bt_apv, m->bt_api, nblk,
                        m->bt_tok, m->bt_pos, m->bt_hist, c.max_seq + 1);
+    return hipGetLastError();
+}
+
+
+hipError_t window_alloc(sh_model *m, int max_new) {
+    const sh_config &c = m->cfg;
+    if (m->wd_arena && m->wd_cap >= max_new) return hipSuccess;
+    (void)hipFree(m->wd_arena);
+    m->wd_arena = nullptr;
+    m->wd_cap = 0;
+    if (m->wd_ready) {
+        (void)hipGraphExecDestroy(m->wd_exec);
+        m->wd_ready = false;
+    }
+    const size_t D = c.dim, V = c.vocab;
+    const size_t ranges = D / skinny_kc((int)V, (int)D);
+    const size_t nblk = (V + kArgChunk - 1) / kArgChunk;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += (bytes + 255) / 256 * 256;
+        return o;
+    };
+    const size_t o_xn = take(4 * D), o_log = take(4 * V), o_part = take(4 * ranges * V),
+                 o_apv = take(4 * nblk), o_api = take(4 * nblk), o_hist = take(4 * (size_t)max_new),
+                 o_cnt = take(4);
+    hipError_t e = hipMalloc(&m->wd_arena, off);
+    if (e != hipSuccess) return e;
+    uint8_t *A = (uint8_t *)m->wd_arena;
+    m->wd_xn = (uint16_t *)(A + o_xn);
+    m->wd_logits = (float *)(A + o_log);
+    m->wd_part = (float *)(A + o_part);
+    m->wd_part_cap = ranges * V;
+    m->wd_apv = (float *)(A + o_apv);
+    m->wd_api = (int32_t *)(A + o_api);
+    m->wd_hist = (int32_t *)(A + o_hist);
+    m->wd_count = (int32_t *)(A + o_cnt);
+    m->wd_cap = max_new;
+    return hipSuccess;
+}
+
+// One window decode step over the `seq` ids in pf_tokens: the full causal forward
+// (evalLogitsCPUInto numerics), stories.RMSNorm of the last row (cpu.go:97-111), its logits
+// (MatMulVocabSeq's column seq-1), argmax, window shift.
+hipError_t enqueue_window_step(sh_model *m, int seq) {
+    const sh_config &c = m->cfg;
+    const int dt = m->dtype, D = c.dim;
+    hipStream_t s = m->stream;
+    hipError_t e;
+    if ((e = enqueue_prefill(m, seq, seq, false, false)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(1), dim3(kT), 0, s, m->pf_x + (size_t)(seq - 1) * D,
+                       m->rms_final, D, c.norm_eps, 1, dt, m->wd_xn, (size_t)D);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    GemmArgs g{};
+    g.A = m->wd_xn; g.B = (const uint16_t *)m->cls; g.M = 1; g.N = c.vocab; g.K = D;
+    g.epi = G_STORE; g.out = m->wd_logits; g.dt = dt;
+    if ((e = skinny(g, dt, m->wd_part, m->wd_part_cap, s)) != hipSuccess) return e;
+    const int nblk = (c.vocab + kArgChunk - 1) / kArgChunk;
+    hipLaunchKernelGGL(k_argmax_part, dim3(nblk, 1), dim3(kT), 0, s, m->wd_logits, c.vocab, nblk,
+                       m->wd_apv, m->wd_api);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_window_advance, dim3(1), dim3(kT), 0, s, m->wd_apv, m->wd_api, nblk,
+                       m->pf_tokens, seq, m->wd_hist, m->wd_count);
     return hipGetLastError();
 }
 

@@ -89,6 +89,8 @@ _lib = None
 # every entry point of include/stories_hip.h with its ctypes signature
 SIGNATURES = {
     "sh_init": (C.c_int, [C.c_int32]),
+    "sh_window_greedy_decode": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32), C.c_int32, C.c_int32, C.c_int32,
+                                          C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "sh_batch_greedy_decode": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32), C.c_int32, C.c_int32, C.c_int32,
                                          C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "sh_decode_tap": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_float), C.c_int32]),
@@ -326,6 +328,17 @@ class Model:
         out = np.empty(n, np.float32)
         _check(self.lib.sh_decode_tap(self.h, which, _fp(out), n), "sh_decode_tap")
         return out
+
+    def window_greedy_decode(self, prompt, seq: int, max_new: int):
+        """(*Engine).Decode with Temperature 0 (decode.go:18-94): (tokens, prompt_len, eos)."""
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
+        plen = max(1, min(p.size, seq))
+        out = np.zeros(plen + (max_new if max_new > 0 else 64), np.int32)
+        n, eos = C.c_int32(0), C.c_int32(0)
+        _check(self.lib.sh_window_greedy_decode(self.h, p.ctypes.data_as(_I32) if p.size else None, p.size,
+                                                 seq, max_new, out.ctypes.data_as(_I32), C.byref(n),
+                                                 C.byref(eos)), "sh_window_greedy_decode")
+        return out[:n.value].copy(), plen, bool(eos.value)
 
     def batch_greedy_decode(self, prompts, max_new: int):
         """sh_batch_greedy_decode: list of token arrays (prompt + generated, EOS-truncated)."""

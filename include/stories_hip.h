@@ -114,6 +114,16 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
  * channel-first [V, seq] (logits[v*seq + t]). Out-of-range ids give a zero embedding
  * column (cpu.go:41-72). Residual scale = cfg.residual_scale. */
 int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *logits_cf);
+/* (*Engine).Decode with Temperature 0 (ane/storiesane/decode.go:18-94): every step runs the
+ * full causal forward (as sh_prefill_logits) over the last `seq` tokens left-padded with BOS
+ * (fillDecodeWindow, :83-94) and appends the argmax of the last position's logits. The prompt
+ * is [BOS] if empty and its last `seq` ids are kept; max_new <= 0 means 64; stops after EOS=2
+ * (there is no max_seq stop: the window slides). seq <= cfg.max_seq; fp16 or bf16 weights.
+ * out_tokens (capacity min(n_prompt, seq) + max_new, or 1 + max_new for an empty prompt)
+ * receives prompt + generated ids. The loop runs on the device. */
+int sh_window_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32_t seq,
+                            int32_t max_new, int32_t *out_tokens, int32_t *n_out,
+                            int32_t *stopped_eos);
 /* Batched greedy decode: n_seqs independent (*Decoder).Decode runs with Temperature 0
  * (infer.go:136-202 each), stepped together on the device. No single reference entry point
  * does this; it is n_seqs decoders sharing one weight stream per step. prompts: n_seqs rows of

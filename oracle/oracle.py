@@ -187,6 +187,15 @@ def eval_logits_cf(cfg: OrConfig, weights, tokens, threads: int = 1) -> np.ndarr
     return out
 
 
+def fill_decode_window(seq: int, tokens) -> np.ndarray:
+    """or_fill_decode_window: decode.go:83-94, the last `seq` ids left-padded with BOS."""
+    t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32))
+    out = np.empty(seq, np.uint16)
+    load().or_fill_decode_window(out.ctypes.data_as(C.POINTER(C.c_uint16)), seq,
+                                 t.ctypes.data_as(C.POINTER(C.c_int32)), t.size)
+    return out
+
+
 def quantize_rows(src: np.ndarray):
     a = np.ascontiguousarray(src, np.float32)
     rows, cols = a.shape
