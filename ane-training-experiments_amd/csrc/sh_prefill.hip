@@ -372,6 +372,146 @@ __global__ __launch_bounds__(1024) void k_row_resid_norm(const float *partial, i
         store_op(xn, (size_t)m * D + i, (size_t)M * D, row[i] * scale * gain[i], dt);
 }
 
+// Tiled causal attention for the full-sequence forward (forward_common.go:5-33, flash
+// style): workgroup = 64 query rows x one head. Row t is position rowpos[t] of its
+// sequence, whose rows are the rowpos[t] rows before it, so its keys are
+// j in [t - rowpos[t], t]; only the key blocks some row of the block can see are visited.
+// Per 64-key block: K and V rows staged in LDS (rows padded by 4 floats), scores as 4 x 4
+// register tiles (thread = 4 queries x 4 keys), then an online softmax (running max m and
+// sum l per row, earlier terms rescaled by exp(m_old - m_new)) and P.V with one thread per
+// (query, quarter of the head dims). fp32 throughout; masked keys contribute exactly 0.
+template <int HD>
+__global__ __launch_bounds__(kT) void k_attn_prefill_tiled(const float *qf, const float *kf,
+                                                           const float *vf, int S,
+                                                           const int32_t *rowpos, int H,
+                                                           int KVH, float scale, int dt,
+                                                           uint16_t *att, size_t plane) {
+    constexpr int B = 64, RSF = HD + 4;          // block rows, LDS row stride (floats)
+    constexpr int DQ = HD / 4;                   // dims per thread in P.V
+    __shared__ __attribute__((aligned(16))) float qs[B * RSF];
+    __shared__ __attribute__((aligned(16))) float ks[B * RSF];
+    __shared__ __attribute__((aligned(16))) float vs[B * RSF];
+    __shared__ float ps[B * (B + 4)];
+    const int tid = threadIdx.x;
+    const int q0 = blockIdx.x * B, h = blockIdx.y;
+    const int qdim = H * HD, kvdim = KVH * HD, kvh = h / (H / KVH);
+    // keys this block can see: from the first row's sequence start to its last row
+    const int kstart = q0 - rowpos[q0];
+    const int qlast = min(q0 + B, S) - 1;
+    // stage the query block
+    for (int c = tid; c < B * (HD / 4); c += kT) {
+        const int r = c / (HD / 4), d = (c % (HD / 4)) * 4;
+        const int t = q0 + r;
+        *(f32x4 *)&qs[r * RSF + d] = t < S ? *(const f32x4 *)(qf + (size_t)t * qdim + h * HD + d)
+                                           : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int tq = tid >> 4, tk = tid & 15;      // score tile: queries 4tq.., keys 4tk..
+    const int pq = tid >> 2, pd = (tid & 3) * DQ; // softmax / P.V: query pq, dims pd..
+    const int t_own = q0 + pq;
+    float m_run = -INFINITY, l_run = 0.f;
+    float acc[DQ];
+#pragma unroll
+    for (int d = 0; d < DQ; d++) acc[d] = 0.f;
+    int jlo[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int t = q0 + 4 * tq + i;
+        jlo[i] = t < S ? t - rowpos[t] : 0x7fffffff;
+    }
+    for (int kb = kstart & ~(B - 1); kb <= qlast; kb += B) {
+        __syncthreads();   // previous block's P.V is done with ks/vs/ps
+        for (int c = tid; c < B * (HD / 4); c += kT) {
+            const int r = c / (HD / 4), d = (c % (HD / 4)) * 4;
+            const int j = kb + r;
+            const bool ok = j < S;
+            *(f32x4 *)&ks[r * RSF + d] = ok ? *(const f32x4 *)(kf + (size_t)j * kvdim + kvh * HD + d)
+                                            : f32x4{0.f, 0.f, 0.f, 0.f};
+            *(f32x4 *)&vs[r * RSF + d] = ok ? *(const f32x4 *)(vf + (size_t)j * kvdim + kvh * HD + d)
+                                            : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        __syncthreads();
+        float sc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) sc[i][j] = 0.f;
+#pragma unroll 4
+        for (int d = 0; d < HD; d += 4) {
+            f32x4 qv[4], kv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) qv[i] = *(const f32x4 *)&qs[(4 * tq + i) * RSF + d];
+#pragma unroll
+            for (int j = 0; j < 4; j++) kv[j] = *(const f32x4 *)&ks[(4 * tk + j) * RSF + d];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    sc[i][j] = fmaf(qv[i].x, kv[j].x, sc[i][j]);
+                    sc[i][j] = fmaf(qv[i].y, kv[j].y, sc[i][j]);
+                    sc[i][j] = fmaf(qv[i].z, kv[j].z, sc[i][j]);
+                    sc[i][j] = fmaf(qv[i].w, kv[j].w, sc[i][j]);
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = q0 + 4 * tq + i;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int jg = kb + 4 * tk + j;
+                const bool vis = jg >= jlo[i] && jg <= t;
+                ps[(4 * tq + i) * (B + 4) + 4 * tk + j] = vis ? sc[i][j] * scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // online softmax for row pq: four threads share the row, 16 keys each
+        float *prow = ps + pq * (B + 4);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 16; j++) mx = fmaxf(mx, prow[(tid & 3) * 16 + j]);
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        const float m_new = fmaxf(m_run, mx);
+        float sum = 0.f;
+        if (m_new != -INFINITY) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int jj = (tid & 3) * 16 + j;
+                const float sv = prow[jj];
+                const float e = sv == -INFINITY ? 0.f : expf(sv - m_new);
+                prow[jj] = e;
+                sum += e;
+            }
+        }
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        const float rescale = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+        l_run = l_run * rescale + sum;
+        m_run = m_new;
+#pragma unroll
+        for (int d = 0; d < DQ; d++) acc[d] *= rescale;
+        __syncthreads();   // every row's probabilities are in ps
+        if (m_new != -INFINITY) {
+            for (int j = 0; j < B; j++) {
+                const float pj = prow[j];
+                const float *vr = &vs[j * RSF + pd];
+#pragma unroll
+                for (int d = 0; d < DQ; d += 4) {
+                    const f32x4 v4 = *(const f32x4 *)(vr + d);
+                    acc[d] = fmaf(pj, v4.x, acc[d]);
+                    acc[d + 1] = fmaf(pj, v4.y, acc[d + 1]);
+                    acc[d + 2] = fmaf(pj, v4.z, acc[d + 2]);
+                    acc[d + 3] = fmaf(pj, v4.w, acc[d + 3]);
+                }
+            }
+        }
+    }
+    if (t_own >= S) return;
+    const float inv = 1.0f / l_run;
+#pragma unroll
+    for (int d = 0; d < DQ; d++)
+        store_op(att, (size_t)t_own * qdim + h * HD + pd + d, plane, acc[d] * inv, dt);
+}
+
 // Causal attention (forward_common.go:5-33): one wave per (query t, head h). Row t is
 // position rowpos[t] of its sequence, whose rows are the rowpos[t] rows before it, so the keys
 // are j in [t - rowpos[t], t]. Lanes walk the keys in blocks of 64; scores are kept in LDS,
@@ -1068,11 +1208,25 @@ hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fi
         if ((e = launch_qk_rope(m, L, S, m->pf_qkv, m->pf_rowpos, m->pf_rowseq, m->pf_q,
                                 m->pf_k, m->pf_v, l, fill_kv, s)) != hipSuccess)
             return e;
-        const int wpb = kT / 64;
-        hipLaunchKernelGGL(k_attn_prefill, dim3((S + wpb - 1) / wpb, c.n_heads), dim3(kT),
-                           sizeof(float) * wpb * seg_max, s, m->pf_q, m->pf_k, m->pf_v, S,
-                           seg_max, m->pf_rowpos, c.n_heads, c.n_kv_heads, c.head_dim, scale, dt,
-                           fill_kv ? 1 : 0, m->pf_att, (size_t)S * m->qdim);
+        {
+            const dim3 grid((S + 63) / 64, c.n_heads);
+            const size_t plane = (size_t)S * m->qdim;
+#define SH_ATT(HDV)                                                                            \
+    hipLaunchKernelGGL(k_attn_prefill_tiled<HDV>, grid, dim3(kT), 0, s, m->pf_q, m->pf_k,       \
+                       m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale, dt, m->pf_att, \
+                       plane)
+            if (c.head_dim == 32) SH_ATT(32);
+            else if (c.head_dim == 64) SH_ATT(64);
+            else if (c.head_dim == 128) SH_ATT(128);
+            else {
+                const int wpb = kT / 64;
+                hipLaunchKernelGGL(k_attn_prefill, dim3((S + wpb - 1) / wpb, c.n_heads), dim3(kT),
+                                   sizeof(float) * wpb * seg_max, s, m->pf_q, m->pf_k, m->pf_v, S,
+                                   seg_max, m->pf_rowpos, c.n_heads, c.n_kv_heads, c.head_dim,
+                                   scale, dt, fill_kv ? 1 : 0, m->pf_att, plane);
+            }
+#undef SH_ATT
+        }
         if ((e = hipGetLastError()) != hipSuccess) return e;
         g = GemmArgs{};
         g.A = m->pf_att; g.B = (const uint16_t *)L.wo; g.M = S; g.N = D; g.K = m->qdim;
