@@ -344,6 +344,17 @@ template <int WT, int COLS>
 __device__ __forceinline__ bool stage_input(float *xs, int n, const uint64_t *ll, uint32_t e,
                             const uint16_t *emb_row, const float *gain, double eps, double *red,
                             const PParams &p, uint32_t *xq, float *sa) {
+    // the gain is loaded into registers before the input is polled, so its memory latency
+    // overlaps the hand-over instead of following it
+    constexpr int GK = (COLS + kPB - 1) / kPB;
+    float gr[GK];
+    if (gain) {
+#pragma unroll
+        for (int k = 0; k < GK; k++) {
+            const int i = threadIdx.x + k * kPB;
+            gr[k] = i < n ? gain[i] : 0.f;
+        }
+    }
     if (emb_row) {
         for (int i = threadIdx.x; i < n; i += kPB) xs[i] = w2f<WT>(emb_row[i]);
         lds_barrier();
@@ -355,7 +366,11 @@ __device__ __forceinline__ bool stage_input(float *xs, int n, const uint64_t *ll
         for (int i = threadIdx.x; i < n; i += kPB) ss += (double)xs[i] * (double)xs[i];
         const double tot = block_sum_d(ss, red);
         const float rrms = (float)(1.0 / sqrt(tot / (double)n + eps));
-        for (int i = threadIdx.x; i < n; i += kPB) xs[i] = xs[i] * rrms * gain[i];
+#pragma unroll
+        for (int k = 0; k < GK; k++) {
+            const int i = threadIdx.x + k * kPB;
+            if (i < n) xs[i] = xs[i] * rrms * gr[k];
+        }
         lds_barrier();
     }
     if constexpr (WT == SH_DTYPE_W8A8) {
@@ -673,9 +688,42 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
         }
     }
     lds_barrier();
-    // scores (infer.go:280-288): 16-byte chunks of the row, visited from a chunk index
-    // rotated by t so the lanes of a wave read distinct LDS banks
-    for (int t = tid; t <= pos; t += kPB) {
+    // scores (infer.go:280-288)
+    int t_first = tid;   // first position this thread scores one per thread
+    if constexpr (!EXACT) {
+        // cached rows in LDS: each row's RB bytes are split over RB/16 lanes, every lane
+        // holding its 16-byte slice of q in registers; a wave reads consecutive rows, so its
+        // LDS reads are one contiguous block; the slices' partial dots are added by shuffles
+        constexpr int LPK = S::RB / 16, EPC = 16 / S::EB, PPW = 64 / LPK;
+        const int sl = lane % LPK, rin = lane / LPK;
+        float qr[kMaxGroup][EPC];
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++)
+#pragma unroll
+            for (int e = 0; e < EPC; e++) qr[h][e] = h < group ? qs[h * hd + sl * EPC + e] : 0.f;
+        const int tl = pos < S::ROWS ? pos : S::ROWS - 1;
+        for (int t0 = wave * PPW; t0 <= tl; t0 += kPW * PPW) {
+            const int t = t0 + rin;
+            const bool valid = t <= tl;
+            float kf[EPC];
+            const u32x4 kv4 = ((const SH_LDS u32x4 *)(kst + (size_t)(valid ? t : tl) * S::RB))[sl];
+            kv_unpack16<KVT>(kv4, kf);
+#pragma unroll
+            for (int h = 0; h < kMaxGroup; h++) {
+                if (h >= group) continue;
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < EPC; e++) d = fmaf(qr[h][e], kf[e], d);
+#pragma unroll
+                for (int off = LPK / 2; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
+                if (valid && sl == 0) sc[h * p.max_seq + t] = d * p.inv_sqrt_hd;
+            }
+        }
+        t_first = tl + 1 + tid;   // rows beyond the LDS stage: one per thread below
+    }
+    // one thread per position: 16-byte chunks of the row in order (EXACT: the reference's
+    // summation order), or positions beyond the LDS stage read from the cache
+    for (int t = t_first; t <= pos; t += kPB) {
         float d[kMaxGroup];
 #pragma unroll
         for (int h = 0; h < kMaxGroup; h++) d[h] = 0.f;
@@ -684,7 +732,7 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
             const SH_LDS u32x4 *row = (const SH_LDS u32x4 *)(kst + (size_t)t * S::RB);
 #pragma unroll 4
             for (int c0 = 0; c0 < NCH; c0++) {
-                const int c = EXACT ? c0 : (c0 + t) & (NCH - 1);
+                const int c = c0;
                 float kf[EPC];
                 const u32x4 kv4 = row[c];
                 kv_unpack16<KVT>(kv4, kf);
