@@ -142,6 +142,118 @@ std::string describe_json(const Llama2Header &h, const HostWeights &w) {
     return s;
 }
 
+void config_from_blzt(const BlztMeta &h, sh_config *c) {
+    Llama2Header l{h.dim, h.hidden, h.n_layers, h.heads, h.heads, h.vocab, h.seq};
+    config_from_header(l, c);
+}
+
+bool load_blzt_checkpoint(const std::string &path, BlztMeta *meta, HostWeights *w, std::string *err) {
+    FILE *f = fopen(path.c_str(), "rb");
+    if (!f) {
+        *err = "open " + path + ": " + strerror(errno);
+        return false;
+    }
+    bool ok = true;
+    auto rd = [&](void *dst, size_t n) {
+        if (ok && fread(dst, 1, n, f) != n) {
+            *err = "unexpected EOF";
+            ok = false;
+        }
+    };
+    int32_t magic = 0;
+    BlztMeta &m = *meta;
+    memset(&m, 0, sizeof m);
+    rd(&magic, 4);
+    rd(&m.version, 4);
+    if (ok && (magic != 0x424C5A54 || (m.version != 2 && m.version != 3))) {   // ckpt.go:279-281
+        char b[96];
+        snprintf(b, sizeof b, "bad checkpoint header magic=%x version=%d", (unsigned)magic, m.version);
+        *err = b;
+        ok = false;
+    }
+    rd(&m.step, 4);
+    rd(&m.total_steps, 4);
+    rd(&m.n_layers, 4);
+    rd(&m.vocab, 4);
+    rd(&m.dim, 4);
+    rd(&m.hidden, 4);
+    rd(&m.heads, 4);
+    rd(&m.seq, 4);
+    if (ok && (m.n_layers <= 0 || m.vocab <= 0 || m.dim <= 0 || m.hidden <= 0 || m.heads <= 0 ||
+               m.dim % m.heads)) {
+        *err = "checkpoint config mismatch";
+        ok = false;
+    }
+    rd(&m.lr, 4);
+    rd(&m.loss, 4);
+    rd(&m.cum_compile, 8);
+    rd(&m.cum_train, 8);
+    rd(&m.cum_wall, 8);
+    rd(&m.cum_steps, 4);
+    rd(&m.cum_batches, 4);
+    rd(&m.adam_t, 4);
+    int32_t reserved[3];
+    rd(reserved, 12);
+    if (!ok) {
+        fclose(f);
+        return false;
+    }
+    sh_config c;
+    config_from_blzt(m, &c);
+    w->resize(c);
+    const char *names[] = {"wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att", "rms_ffn"};
+    std::vector<float> HostLayer::*members[] = {&HostLayer::wq, &HostLayer::wk, &HostLayer::wv,
+                                                &HostLayer::wo, &HostLayer::w1, &HostLayer::w2,
+                                                &HostLayer::w3, &HostLayer::rms_att,
+                                                &HostLayer::rms_ffn};
+    size_t layer_floats = 0;
+    for (int l = 0; ok && l < m.n_layers; l++)
+        for (int k = 0; ok && k < 9; k++) {
+            std::vector<float> &v = w->layers[l].*members[k];
+            ok = read_f32s(f, v, std::string(names[k]) + "[" + std::to_string(l) + "]", err);
+            if (l == 0) layer_floats += v.size();
+        }
+    // every layer's Adam moments (M and V of the nine tensors), then RMSFinal
+    auto skip = [&](size_t floats) {
+        if (ok && fseek(f, (long)(floats * 4), SEEK_CUR) != 0) {
+            *err = "skip optimizer state: seek failed";
+            ok = false;
+        }
+    };
+    skip(2 * layer_floats * (size_t)m.n_layers);
+    ok = ok && read_f32s(f, w->rms_final, "rms_final", err);
+    skip(2 * (size_t)m.dim);
+    ok = ok && read_f32s(f, w->embed, "embed", err);
+    // the file must hold Embed's moments too: a short file fails as the reference's read would
+    if (ok) {
+        const long here = ftell(f);
+        fseek(f, 0, SEEK_END);
+        const long end = ftell(f);
+        if (end - here < (long)(2 * w->embed.size() * 4)) {
+            *err = "read embed optimizer state: unexpected EOF";
+            ok = false;
+        }
+    }
+    fclose(f);
+    return ok;
+}
+
+std::string describe_blzt_json(const BlztMeta &h, const HostWeights &w) {
+    char b[640];
+    snprintf(b, sizeof b,
+             "{\"checkpoint\": {\"version\": %d, \"step\": %d, \"total_steps\": %d, "
+             "\"n_layers\": %d, \"vocab\": %d, \"dim\": %d, \"hidden\": %d, \"heads\": %d, "
+             "\"seq\": %d, \"lr\": %.9g, \"loss\": %.9g, \"cum_compile\": %.17g, "
+             "\"cum_train\": %.17g, \"cum_wall\": %.17g, \"cum_steps\": %d, \"cum_batches\": %d, "
+             "\"adam_t\": %d}, ",
+             h.version, h.step, h.total_steps, h.n_layers, h.vocab, h.dim, h.hidden, h.heads, h.seq,
+             h.lr, h.loss, h.cum_compile, h.cum_train, h.cum_wall, h.cum_steps, h.cum_batches,
+             h.adam_t);
+    Llama2Header l{h.dim, h.hidden, h.n_layers, h.heads, h.heads, h.vocab, h.seq};
+    std::string s = describe_json(l, w);
+    return std::string(b) + s.substr(1);   // merge the two objects
+}
+
 bool Tokenizer::load(const std::string &path, int vocab, std::string *err) {
     FILE *f = fopen(path.c_str(), "rb");
     if (!f) {

@@ -42,6 +42,25 @@ void config_from_header(const Llama2Header &h, sh_config *c);
 // {"header": {...}, "sums": {"embed": s, "wq": s, ...}} with float64 sums over all layers.
 std::string describe_json(const Llama2Header &h, const HostWeights &w);
 
+// Training checkpoint header and meta (ane/stories/ckpt.go:237-447, magic "BLZT",
+// versions 2 and 3).
+struct BlztMeta {
+    int32_t version, step, total_steps, n_layers, vocab, dim, hidden, heads, seq;
+    float lr, loss;
+    double cum_compile, cum_train, cum_wall;
+    int32_t cum_steps, cum_batches, adam_t;
+};
+
+// loadCheckpointFile (ckpt.go:249-447) without optimizer state: the header, then per layer
+// Wq, Wk, Wv, Wo, W1, W2, W3, RMSAtt, RMSFFN, then every layer's Adam moments (skipped),
+// RMSFinal and its moments (skipped), Embed and its moments (skipped). The reference accepts
+// only the Stories110M constants; here the shapes come from the header (wq/wk/wv/wo are
+// dim x dim, w1/w3 hidden x dim, w2 dim x hidden, as that format has no grouped heads), so
+// small checkpoints of the same layout load too. Errors follow the reference's wording.
+bool load_blzt_checkpoint(const std::string &path, BlztMeta *meta, HostWeights *w, std::string *err);
+void config_from_blzt(const BlztMeta &h, sh_config *c);
+std::string describe_blzt_json(const BlztMeta &h, const HostWeights &w);
+
 // tokenizer.go:16-97.
 class Tokenizer {
   public:

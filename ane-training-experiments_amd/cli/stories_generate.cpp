@@ -301,8 +301,6 @@ int main(int argc, char **argv) {
         return 0;
     }
 
-    if (!fl.s("ckpt").empty())
-        fatalf("decode: %s", "checkpoint files (-ckpt) are not read by this build; use -model");
     if (fl.b("ane"))
         fatalf("decode: %s", "the full-window engine (-ane) is not part of this build; the "
                              "default KV-cache decoder runs on the GPU");
@@ -312,7 +310,17 @@ int main(int argc, char **argv) {
     stories::HostWeights w;
     std::string source;
     const std::string shape = fl.s("shape");
-    if (!fl.s("model").empty() && fl.s("model") != "synthetic") {
+    if (!fl.s("ckpt").empty()) {   // main.go:113-122: a checkpoint overrides -model
+        std::string err;
+        stories::BlztMeta meta{};
+        if (!stories::load_blzt_checkpoint(fl.s("ckpt"), &meta, &w, &err)) fatalf("decode: %s", err);
+        if (fl.b("inspect")) {
+            printf("%s\n", stories::describe_blzt_json(meta, w).c_str());
+            return 0;
+        }
+        stories::config_from_blzt(meta, &c);
+        source = "checkpoint";
+    } else if (!fl.s("model").empty() && fl.s("model") != "synthetic") {
         std::string err;
         stories::Llama2Header hdr{};
         if (!stories::load_llama2_file(fl.s("model"), &hdr, &w, &err)) fatalf("decode: %s", err);

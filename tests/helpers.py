@@ -116,3 +116,31 @@ def write_tokenizer_bin(path, pieces, max_len=None):
             f.write(np.array([-float(i)], "<f4").tobytes())
             f.write(np.array([len(b)], "<i4").tobytes())
             f.write(b)
+
+
+BLZT_LAYER_ORDER = ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att", "rms_ffn")
+
+
+def write_blzt(path, cfg, w, version=3, meta=None, opt_value=0.25):
+    """A training checkpoint in the layout ane/stories/ckpt.go:13-176 writes: header and meta,
+    per layer Wq..W3, RMSAtt, RMSFFN; every layer's Adam M and V (filled with opt_value so a
+    reader that does not skip them exactly reads garbage); RMSFinal, its M and V; Embed, its
+    M and V. The format has no grouped heads: wk/wv are dim x dim."""
+    meta = dict(step=7, total_steps=100, lr=3e-4, loss=2.5, cum_compile=1.25, cum_train=2.5,
+                cum_wall=3.75, cum_steps=6, cum_batches=12, adam_t=7) | (meta or {})
+    with open(path, "wb") as f:
+        f.write(np.array([0x424C5A54, version, meta["step"], meta["total_steps"], cfg.n_layers,
+                          cfg.vocab, cfg.dim, cfg.hidden, cfg.n_heads, cfg.max_seq], "<i4").tobytes())
+        f.write(np.array([meta["lr"], meta["loss"]], "<f4").tobytes())
+        f.write(np.array([meta["cum_compile"], meta["cum_train"], meta["cum_wall"]], "<f8").tobytes())
+        f.write(np.array([meta["cum_steps"], meta["cum_batches"], meta["adam_t"], 0, 0, 0], "<i4").tobytes())
+        for lw in w.layers:
+            for k in BLZT_LAYER_ORDER:
+                f.write(np.ascontiguousarray(lw[k], "<f4").tobytes())
+        for lw in w.layers:
+            for k in BLZT_LAYER_ORDER:
+                f.write(np.full(2 * lw[k].size, opt_value, "<f4").tobytes())
+        f.write(np.ascontiguousarray(w.rms_final, "<f4").tobytes())
+        f.write(np.full(2 * w.rms_final.size, opt_value, "<f4").tobytes())
+        f.write(np.ascontiguousarray(w.embed, "<f4").tobytes())
+        f.write(np.full(2 * w.embed.size, opt_value, "<f4").tobytes())

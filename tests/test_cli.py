@@ -10,7 +10,7 @@ import pytest
 
 import oracle
 import stories_hip as sh
-from helpers import LLAMA2_ORDER, tiny_config, write_llama2_bin, write_tokenizer_bin
+from helpers import BLZT_LAYER_ORDER, LLAMA2_ORDER, tiny_config, write_blzt, write_llama2_bin, write_tokenizer_bin
 
 CLI = os.path.join(os.path.dirname(sh.LIB_PATH), "stories-generate")
 
@@ -76,6 +76,52 @@ def test_inspect_negative_vocab_and_errors(tmp_path):
     assert p.returncode == 1 and "config mismatch" in p.stderr
     p = run("-model", tmp_path / "missing.bin", "-inspect", check=False)
     assert p.returncode == 1 and "open" in p.stderr
+
+
+@pytest.mark.parametrize("version", [2, 3])
+def test_inspect_reads_blzt_checkpoint(tmp_path, version):
+    cfg = tiny_config(max_seq=64)
+    w = distinct_weights(cfg, 305)
+    for lw in w.layers:
+        lw["rms_att"] = (lw["rms_att"] * np.float32(1.25)).astype(np.float32)
+    path = tmp_path / "c.bin"
+    write_blzt(path, cfg, w, version=version)
+    got = json.loads(run("-ckpt", path, "-inspect").stdout)
+    ck = got["checkpoint"]
+    assert (ck["version"], ck["step"], ck["total_steps"], ck["n_layers"], ck["vocab"], ck["dim"],
+            ck["hidden"], ck["heads"], ck["seq"]) == (version, 7, 100, 2, 512, 128, 256, 4, 64)
+    assert ck["lr"] == pytest.approx(3e-4) and ck["loss"] == 2.5 and ck["cum_wall"] == 3.75
+    assert (ck["cum_steps"], ck["cum_batches"], ck["adam_t"]) == (6, 12, 7)
+    want = {"embed": w.embed, "rms_final": w.rms_final}
+    for k in BLZT_LAYER_ORDER:
+        want[k] = np.concatenate([lw[k].ravel() for lw in w.layers])
+    for k, v in want.items():
+        assert got["sums"][k] == pytest.approx(float(np.sum(v, dtype=np.float64)), rel=1e-12, abs=1e-12), k
+
+
+def test_blzt_errors(tmp_path):
+    cfg = tiny_config(max_seq=64)
+    w = distinct_weights(cfg, 306)
+    path = tmp_path / "c.bin"
+    write_blzt(path, cfg, w, version=3)
+    data = path.read_bytes()
+    bad = tmp_path / "bad.bin"
+    bad.write_bytes(data[:4] + np.array([4], "<i4").tobytes() + data[8:])
+    p = run("-ckpt", bad, "-inspect", check=False)
+    assert p.returncode == 1 and "bad checkpoint header magic=424c5a54 version=4" in p.stderr
+    bad.write_bytes(np.array([0x12345678], "<i4").tobytes() + data[4:])
+    p = run("-ckpt", bad, "-inspect", check=False)
+    assert p.returncode == 1 and "bad checkpoint header magic=12345678" in p.stderr
+    hdr = np.frombuffer(data[:40], "<i4").copy()
+    hdr[8] = 5                                     # heads not dividing dim
+    bad.write_bytes(hdr.tobytes() + data[40:])
+    p = run("-ckpt", bad, "-inspect", check=False)
+    assert p.returncode == 1 and "checkpoint config mismatch" in p.stderr
+    for cut, what in ((len(data) - 8, "embed optimizer state"), (len(data) - 2 * 512 * 128 * 4 - 100, "embed"),
+                      (200, "wq[0]")):
+        bad.write_bytes(data[:cut])
+        p = run("-ckpt", bad, "-inspect", check=False)
+        assert p.returncode == 1 and what in p.stderr and "unexpected EOF" in p.stderr, (what, p.stderr)
 
 
 def test_detokenize(tmp_path):
@@ -156,3 +202,17 @@ def test_cli_bench_mode_stories110m():
     ref = oracle.Decoder(oracle.config_from(cfg), w.rounded(sh.SH_DTYPE_F16), threads=16)
     want, _, _ = ref.greedy_decode(sh.synth_tokens(16, 1, cfg.vocab), 128)
     assert r["tokens"] == want.tolist()
+
+
+@pytest.mark.gpu
+def test_cli_decode_from_blzt_checkpoint(tmp_path):
+    """-ckpt: the same weights as a llama2.c file and as a checkpoint decode to the same ids."""
+    cfg = tiny_config(max_seq=64)
+    w = sh.synth_weights(cfg, seed=331, std=0.08)
+    ck, mb = tmp_path / "c.bin", tmp_path / "m.bin"
+    write_blzt(ck, cfg, w)
+    write_llama2_bin(mb, cfg, w)
+    args = ("-prompt-ids", "4,5,6", "-max-new", "24", "-temperature", "0", "-seq", "64")
+    a = run("-ckpt", ck, *args).stdout.splitlines()
+    b = run("-model", mb, *args).stdout.splitlines()
+    assert a[0].startswith("source=checkpoint") and a[1] == b[1]
