@@ -110,6 +110,12 @@ hipError_t ensure_step_graph(sh_model *m) {
     return hipSuccess;
 }
 
+// Hand-over words of a stage's output vector (padded producer blocks), of the gate vector
+// and of the argmax partials (two forwards' slots per workgroup).
+size_t stage_words(const sh_model *m, int st) { return (size_t)m->p_own[st].n * (size_t)m->p_ostride[st]; }
+size_t gate_words(const sh_model *m) { return stage_words(m, 2); }
+size_t arg_words(const sh_model *m) { return 2 * (size_t)m->p_grid * kArgSlot; }
+
 // Runs n_forwards forwards from pos0 with the persistent kernel (epochs advance; the
 // hand-over buffers are cleared before the 32-bit epoch space runs out).
 bool run_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt) {
@@ -120,9 +126,9 @@ bool run_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt) {
             uint64_t *p;
             size_t n;
         } ll[] = {{m->ll_qkv, (size_t)m->qkv_rows}, {m->ll_att, (size_t)m->qdim},
-                  {m->ll_x2, (size_t)c.dim},        {m->ll_gate, (size_t)c.hidden},
-                  {m->ll_x, (size_t)c.dim},         {m->ll_pv, 2 * (size_t)m->p_grid},
-                  {m->ll_pi, 2 * (size_t)m->p_grid}};
+                  {m->ll_x2, stage_words(m, 1)},    {m->ll_gate, gate_words(m)},
+                  {m->ll_x, stage_words(m, 3)},     {m->ll_pv, arg_words(m)},
+                  {m->ll_pi, arg_words(m)}};
         for (auto &b : ll)
             if (!hip_ok(hipMemsetAsync(b.p, 0, 8 * b.n, m->stream), "clear hand-over")) return false;
         m->epoch = 1;
@@ -399,7 +405,7 @@ sh_model *sh_model_create(const sh_config *cfg, int32_t dtype) {
         hipError_t ge = hipSuccess;
         if (!persistent_supported(m)) {
             why = "shape/dtype has no persistent-kernel instantiation";
-        } else if ((ge = persistent_grid(m, &m->p_grid, &why)) == hipSuccess) {
+        } else if ((ge = persistent_plan(m, &why)) == hipSuccess) {
             m->persistent = true;
         } else {
             why += std::string("; grid: ") + hipGetErrorString(ge);
@@ -426,9 +432,9 @@ sh_model *sh_model_create(const sh_config *cfg, int32_t dtype) {
             uint64_t **p;
             size_t n;
         } ll[] = {{&m->ll_qkv, (size_t)m->qkv_rows}, {&m->ll_att, (size_t)m->qdim},
-                  {&m->ll_x2, D},                    {&m->ll_gate, F},
-                  {&m->ll_x, D},                     {&m->ll_pv, 2 * (size_t)m->p_grid},
-                  {&m->ll_pi, 2 * (size_t)m->p_grid}};
+                  {&m->ll_x2, stage_words(m, 1)},    {&m->ll_gate, gate_words(m)},
+                  {&m->ll_x, stage_words(m, 3)},     {&m->ll_pv, arg_words(m)},
+                  {&m->ll_pi, arg_words(m)}};
         for (auto &b : ll) {
             if ((e = hipMalloc(b.p, 8 * b.n)) != hipSuccess) return fail("hipMalloc hand-over", e);
             if ((e = hipMemset(*b.p, 0, 8 * b.n)) != hipSuccess) return fail("clear hand-over", e);
@@ -440,7 +446,7 @@ sh_model *sh_model_create(const sh_config *cfg, int32_t dtype) {
             return fail("wall clock rate", e);
         m->spin_ticks = (long long)(rate_khz > 0 ? rate_khz : 100000) * 1000LL * 2;  // 2 s
         m->epoch = 1;  // cleared words carry epoch 0
-        const size_t tb = 2 * (5 * (size_t)c.n_layers + 3) * sizeof(long long);
+        const size_t tb = (size_t)m->p_grid * (5 * (size_t)c.n_layers + 3) * sizeof(long long);
         if ((e = hipMalloc(&m->trace_buf, tb)) != hipSuccess) return fail("hipMalloc trace", e);
         if ((e = hipMemset(m->trace_buf, 0, tb)) != hipSuccess) return fail("clear trace", e);
     }
@@ -991,11 +997,19 @@ int sh_decode_tap(const sh_model *m, int32_t which, float *out, int32_t n) {
     (void)hipSetDevice(m->device);
     if (!hip_ok(hipStreamSynchronize(m->stream), "tap sync")) return -1;
     if (m->persistent) {
-        std::vector<uint64_t> w(len);
-        if (!hip_ok(hipMemcpy(w.data(), words, 8 * (size_t)len, hipMemcpyDeviceToHost), "tap read"))
+        // x, x2 and the gate vector are stored in padded blocks, one per producer workgroup
+        int st = -1;
+        if (which == SH_TAP_X) st = 3;
+        if (which == SH_TAP_X2) st = 1;
+        if (which == SH_TAP_GATE) st = 2;
+        const int per = st < 0 ? len : (st == 2 ? m->p_own[2].per / 2 : m->p_own[st].per);
+        const int stride = st < 0 ? len : m->p_ostride[st];
+        const size_t nw = st < 0 ? (size_t)len : stage_words(m, st);
+        std::vector<uint64_t> w(nw);
+        if (!hip_ok(hipMemcpy(w.data(), words, 8 * nw, hipMemcpyDeviceToHost), "tap read"))
             return -1;
         for (int i = 0; i < len; i++) {
-            const uint32_t b = (uint32_t)w[i];
+            const uint32_t b = (uint32_t)w[(size_t)(i / per) * stride + i % per];
             memcpy(&out[i], &b, 4);
         }
         return 0;
@@ -1017,9 +1031,9 @@ int sh_trace_read(sh_model *m, int64_t *out, int32_t cap, int32_t *n_out, double
         set_error("sh_trace_read: bad arguments");
         return -1;
     }
-    const int n = 2 * (5 * m->cfg.n_layers + 3);
+    const int n = m->p_grid * (5 * m->cfg.n_layers + 3);
     if (cap < n) {
-        set_error("sh_trace_read: capacity below 2*(5*n_layers+3)");
+        set_error("sh_trace_read: capacity below grid*(5*n_layers+3)");
         return -1;
     }
     (void)hipSetDevice(m->device);

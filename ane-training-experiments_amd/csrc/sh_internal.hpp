@@ -40,6 +40,12 @@ struct ArgmaxPartial {
     int32_t i;
 };
 
+// Rows of one GEMV stage of the persistent decode kernel: workgroup off + i (mod grid), for
+// i < n, owns rows [i*per, (i+1)*per), so the hand-over words it writes are contiguous.
+struct StageOwn {
+    int off, n, per;
+};
+
 }  // namespace sh
 
 struct sh_model {
@@ -80,6 +86,10 @@ struct sh_model {
     // persistent decode kernel (sh_persistent.hip); unused when `persistent` is false
     bool persistent;
     int p_grid;
+    // GEMV stage ownership (qkv, wo, w13, w2, classifier): workgroups off .. off+n-1 (mod
+    // grid) own row blocks of `per` rows in order
+    sh::StageOwn p_own[5];
+    int p_ostride[5];       // hand-over words between consecutive workgroups' output blocks
     void *p_layers;         // device array of per-layer weight pointers
     uint64_t *ll_qkv, *ll_att, *ll_x2, *ll_gate, *ll_x, *ll_pv, *ll_pi;
     int *p_err;
@@ -150,7 +160,8 @@ hipError_t enqueue_decode_step(sh_model *m);
 int gemv_partials(const sh_model *m);
 
 bool persistent_supported(const sh_model *m);
-hipError_t persistent_grid(const sh_model *m, int *grid_out, std::string *why);
+hipError_t persistent_plan(sh_model *m, std::string *why);
+constexpr int kArgSlot = 16;  // hand-over words per argmax partial slot (one 128-byte line)
 hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt);
 size_t persistent_layer_ptr_bytes(int n_layers);
 bool prefill_supported(const sh_model *m, std::string *why);

@@ -10,13 +10,14 @@
 // fences or counters are needed. Epochs are unique per (forward, layer), so buffers are
 // never cleared.
 //
-// Stages of one forward (vw = wave index spread over the grid):
+// Stages of one forward (each GEMV stage on its own range of workgroups, which own blocks
+// of consecutive rows; persistent_plan places them):
 //   per layer l (epoch e):
-//     qkv   rows of [Wq;Wk;Wv] . rmsnorm(x)          -> ll_qkv          (all workgroups)
+//     qkv   rows of [Wq;Wk;Wv] . rmsnorm(x)          -> ll_qkv
 //     attn  per kv head g: QK-norm, RoPE, KV append, softmax, P.V for its q heads
 //                                                    -> ll_att          (workgroups 0..KVH-1)
 //     wo    x2 = x + alpha * Wo . att                -> ll_x2
-//     w13   gate = silu(W1 . n) * (W3 . n), n = rmsnorm(x2) -> ll_gate
+//     w13   gate = silu(W1 . n) * (W3 . n), n = rmsnorm(x2) -> ll_gate (every workgroup)
 //     w2    x = x2 + alpha * W2 . gate               -> ll_x
 //   classifier: logits = Cls . rmsnorm(x), per-workgroup (max, first index) -> ll_pv/ll_pi
 //   argmax: every workgroup reduces the partials itself and knows the next token.
@@ -36,6 +37,7 @@
 #include <string>
 
 #include "sh_internal.hpp"
+#include "sh_wave.hpp"
 
 namespace sh {
 namespace {
@@ -54,6 +56,7 @@ constexpr int kPW = kPB / 64;      // waves per workgroup
 constexpr int kXs = 4096;          // staged input vector
 constexpr int kScores = 4096;      // attention scores: group * max_seq
 constexpr int kMaxGroup = 2;       // q heads per kv head
+constexpr int kMaxRes = 32;        // residual rows a workgroup owns in a residual stage
 constexpr int kKvStage = 96 * 1024; // LDS bytes for one kv head's cached K and V rows
 
 struct LayerPtrs {
@@ -83,6 +86,9 @@ struct PParams {
     long long spin_limit;
     long long *trace;  // stage timestamps of forward trace_f (workgroups 0 and grid-1)
     int trace_f;
+    StageOwn own[5];   // qkv, wo, w13, w2, classifier
+    int ostride[5];    // words between consecutive workgroups' output blocks, per stage
+    uint32_t omagic[5];  // ceil(2^31 / elements per output block), per stage
 };
 
 __device__ __forceinline__ float h2f(uint32_t b) {
@@ -182,21 +188,8 @@ __device__ __forceinline__ bool block_and(bool ok) {
     return r;
 }
 
-template <int N>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = N / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-template <int N>
-__device__ __forceinline__ int group_sum_i(int v) {
-#pragma unroll
-    for (int off = N / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
 __device__ __forceinline__ float block_max_d(float v, double *red) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    v = wmax<64>(v);
     lds_barrier();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = (double)v;
     lds_barrier();
@@ -215,20 +208,6 @@ __device__ __forceinline__ uint32_t quant8(float x, float scale) {
     float v = __fdiv_rn(x, scale);
     v = fminf(fmaxf(v, -128.0f), 127.0f);
     return (uint32_t)(int)(v >= 0.0f ? v + 0.5f : v - 0.5f) & 0xffu;
-}
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-__device__ __forceinline__ double block_sum_d(double v, double *red) {
-    v = wave_sum_d(v);
-    lds_barrier();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    lds_barrier();
-    double s = 0;
-    for (int w = 0; w < kPW; w++) s += red[w];
-    return s;
 }
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
@@ -275,12 +254,13 @@ __device__ __forceinline__ bool ll_wait_word(const uint64_t *src, uint32_t e, ui
     return ll_spin(src, e, &v, p.err, p.spin_limit);
 }
 
-// Block-wide wait: once every word j < n (located by map.src(j)) carries epoch e, its value
-// is in *map.dst(j). Each thread requests all of its K words at once and, while any is
+// Block-wide wait: once every word j < n (located by map.src(j)) carries epoch map.ep(j),
+// its value is in *map.dst(j). Starts with a workgroup barrier, after the first requests
+// are issued: the LDS a stage writes is free once every wave has passed it. Each thread requests all of its K words at once and, while any is
 // missing, re-requests the missing ones together, so a poll costs one memory round trip
 // whatever the number of words. Returns false for the whole block on timeout/abort.
 template <int K, typename Map>
-__device__ __forceinline__ bool ll_wait_batch(int n, uint32_t e, const PParams &p, const Map &map) {
+__device__ __forceinline__ bool ll_wait_batch(int n, const PParams &p, const Map &map) {
     uint64_t v[K];
     unsigned need = 0;
 #pragma unroll
@@ -291,13 +271,16 @@ __device__ __forceinline__ bool ll_wait_batch(int n, uint32_t e, const PParams &
             need |= 1u << k;
         }
     }
+    // every wave is done with the destination's previous contents (stages end without a
+    // barrier; this one overlaps the first round trip)
+    lds_barrier();
     bool ok = true;
     long long t0 = 0;
     while (true) {
 #pragma unroll
         for (int k = 0; k < K; k++) {
             if ((need >> k) & 1u) {
-                if ((uint32_t)(v[k] >> 32) == e) {
+                if ((uint32_t)(v[k] >> 32) == map.ep(threadIdx.x + k * kPB)) {
                     *map.dst(threadIdx.x + k * kPB) = __uint_as_float((uint32_t)v[k]);
                     need &= ~(1u << k);
                 }
@@ -327,64 +310,199 @@ __device__ __forceinline__ bool ll_wait_batch(int n, uint32_t e, const PParams &
 struct VecMap {
     const uint64_t *s;
     float *d;
+    uint32_t e;
     __device__ const uint64_t *src(int j) const { return s + j; }
     __device__ float *dst(int j) const { return d + j; }
+    __device__ uint32_t ep(int) const { return e; }
+};
+
+// Hand-over vectors are written in producer blocks: the workgroup of rank r in a stage
+// writes its `per` consecutive elements at words [r * stride, r * stride + per), stride a
+// multiple of 16, so each producer's block sits on 128-byte lines of its own. Element i of
+// the vector is word (i / per) * stride + i % per. A dense vector is one block (per =
+// stride = kDense). i / per is taken as mulhi(2i, magic), magic = ceil(2^31 / per): with
+// e = magic * per - 2^31 < per the quotient is exact while i * per < 2^31 (every index and
+// block here is below 2^16); per = 1 gives magic = 2^31, per = kDense gives 2.
+constexpr int kDense = 1 << 30;
+__device__ __forceinline__ int ll_index(int i, int per, int stride, uint32_t magic) {
+    const int q = (int)__umulhi((uint32_t)i << 1, magic);
+    return q * stride + (i - q * per);
+}
+
+// A stage input staged in LDS: elements [0, n) of the input vector (epoch e), then the
+// stage's residual rows r0 .. r0 + (count - n) - 1 of the residual vector (epoch er), polled
+// together so the residual costs no round trip of its own. (Both sources are addressed from
+// one base, without a select between two pointers: that form trips an instruction-
+// selection error in the gfx950 backend.)
+struct InputMap {
+    const uint64_t *s;            // input vector words
+    ptrdiff_t roff;               // residual vector words, relative to s
+    float *d;
+    int n, per, stride;
+    int r0, rper, rstride;
+    uint32_t magic, rmagic;
+    uint32_t e, er;
+    __device__ const uint64_t *src(int j) const {
+        return s + (j < n ? (ptrdiff_t)ll_index(j, per, stride, magic)
+                          : roff + ll_index(r0 + j - n, rper, rstride, rmagic));
+    }
+    __device__ float *dst(int j) const { return d + j; }
+    __device__ uint32_t ep(int j) const { return j < n ? e : er; }
 };
 
 // Block-wide: dst[i] = value of src[i] once every word of src[0, n) carries epoch e;
 // n <= K * kPB.
 template <int K>
 __device__ __forceinline__ bool ll_wait_vec(const uint64_t *src, int n, uint32_t e, float *dst, const PParams &p) {
-    return ll_wait_batch<K>(n, e, p, VecMap{src, dst});
+    return ll_wait_batch<K>(n, p, VecMap{src, dst, e});
 }
 
-// Stage this stage's input in LDS: from an LL vector (epoch e) or, when emb_row is given,
-// from an embedding row; then rmsNormVec (infer.go:301-311) with `gain` if non-null.
-template <int WT, int COLS>
-__device__ __forceinline__ bool stage_input(float *xs, int n, const uint64_t *ll, uint32_t e,
-                            const uint16_t *emb_row, const float *gain, double eps, double *red,
-                            const PParams &p, uint32_t *xq, float *sa) {
+// This thread's words j = threadIdx.x + k*kPB (k < K, j < n) of an input map, into
+// registers once each carries its epoch (other entries of val are left as they are).
+// Starts with a workgroup barrier after the first requests (the LDS the stage writes next
+// is then free). *ok is this thread's outcome; the caller combines it over the workgroup.
+template <int K>
+__device__ __forceinline__ void ll_poll_regs(int n, const PParams &p, const InputMap &map, float (&val)[K], bool &ok) {
+    uint64_t v[K];
+    unsigned need = 0;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int j = threadIdx.x + k * kPB;
+        if (j < n) {
+            v[k] = ll_get(map.src(j));
+            need |= 1u << k;
+        }
+    }
+    lds_barrier();
+    ok = true;
+    long long t0 = 0;
+    while (true) {
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            if (((need >> k) & 1u) && (uint32_t)(v[k] >> 32) == map.ep(threadIdx.x + k * kPB)) {
+                val[k] = __uint_as_float((uint32_t)v[k]);
+                need &= ~(1u << k);
+            }
+        }
+        if (!need) break;
+        const long long now = wall_clock64();
+        if (!t0) {
+            t0 = now;
+        } else if (now - t0 > p.spin_limit) {
+            __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = false;
+            break;
+        }
+        if (aborted(p)) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < K; k++)
+            if ((need >> k) & 1u) v[k] = ll_get(map.src(threadIdx.x + k * kPB));
+    }
+}
+
+// Stage this stage's input in LDS: xs[0, n) from an LL vector (map) or, when emb_row is
+// given, from an embedding row; xs[n, count) receives the residual rows polled with it.
+// With NORM (the stage's `gain`), rmsNormVec (infer.go:301-311): ss = sum of x^2 in float64, rrms =
+// float32(1 / sqrt(ss/n + eps)).
+//   fp16 / bf16: xs = x * gain and *rscale = rrms, applied by the caller to each finished
+//                dot product (sum w*(x*g) * rrms instead of sum w*((x*rrms)*g): the float
+//                rounding of each term differs, by about 1 ulp).
+//   W8A8:        the reference's order, xs = (x * rrms) * gain, then the per-tensor int8
+//                quantization (its boundaries must see the reference's values).
+// Barriers: the poll's first (frees LDS), one after the partial sums (and the ok flags), and
+// for W8A8 two more around the quantization.
+template <int WT, int COLS, bool NORM>
+__device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &map, int count,
+                            const uint16_t *emb_row, const uint16_t *res_emb, const float *gain,
+                            double eps, double *red, int *okw, const PParams &p, uint32_t *xq,
+                            float *sa, float *rscale) {
+    constexpr int K = (COLS + kMaxRes + kPB - 1) / kPB;
+    constexpr bool Q8 = WT == SH_DTYPE_W8A8;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // the gain is loaded into registers before the input is polled, so its memory latency
     // overlaps the hand-over instead of following it
-    constexpr int GK = (COLS + kPB - 1) / kPB;
-    float gr[GK];
-    if (gain) {
+    float gr[NORM ? K : 1];
+    if constexpr (NORM) {
 #pragma unroll
-        for (int k = 0; k < GK; k++) {
+        for (int k = 0; k < K; k++) {
             const int i = threadIdx.x + k * kPB;
-            gr[k] = i < n ? gain[i] : 0.f;
+            gr[k] = i < n ? gain[i] : 1.f;
         }
     }
+    // residual rows from the embedding row (layer 0) instead of a hand-over vector
+    float val[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int j = threadIdx.x + k * kPB;
+        val[k] = res_emb && j >= n && j < count ? w2f<WT>(res_emb[map.r0 + j - n]) : 0.f;
+    }
+    bool ok = true;
     if (emb_row) {
-        for (int i = threadIdx.x; i < n; i += kPB) xs[i] = w2f<WT>(emb_row[i]);
-        lds_barrier();
-    } else if (!ll_wait_vec<(COLS + kPB - 1) / kPB>(ll, n, e, xs, p)) {
-        return false;
-    }
-    if (gain) {
-        double ss = 0;
-        for (int i = threadIdx.x; i < n; i += kPB) ss += (double)xs[i] * (double)xs[i];
-        const double tot = block_sum_d(ss, red);
-        const float rrms = (float)(1.0 / sqrt(tot / (double)n + eps));
 #pragma unroll
-        for (int k = 0; k < GK; k++) {
+        for (int k = 0; k < K; k++) {
             const int i = threadIdx.x + k * kPB;
-            if (i < n) xs[i] = xs[i] * rrms * gr[k];
+            if (i < n) val[k] = w2f<WT>(emb_row[i]);
         }
         lds_barrier();
+    } else {
+        ll_poll_regs<K>(res_emb ? n : count, p, map, val, ok);
     }
-    if constexpr (WT == SH_DTYPE_W8A8) {
-        // per-tensor activation quantization (W8A8 decode): s_a = max|x|/127 (0 -> 1),
-        // stored as packed int8 words for v_dot4_i32_i8
-        float mx = 0.0f;
-        for (int i = threadIdx.x; i < n; i += kPB) mx = fmaxf(mx, fabsf(xs[i]));
-        mx = block_max_d(mx, red);
+    double ss = 0;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int j = threadIdx.x + k * kPB;
+        if (j < n) {
+            if constexpr (NORM) ss += (double)val[k] * (double)val[k];
+            if constexpr (!Q8) xs[j] = NORM ? val[k] * gr[NORM ? k : 0] : val[k];
+        } else if (j < count) {
+            xs[j] = val[k];   // residual rows
+        }
+    }
+    if constexpr (NORM) ss = wsum_d64(ss);
+    const bool wok = __all(ok);
+    if (lane == 0) {
+        red[wave] = ss;
+        okw[wave] = wok;
+    }
+    lds_barrier();
+    bool all_ok = true;
+    double tot = 0;
+#pragma unroll
+    for (int w = 0; w < kPW; w++) {
+        all_ok = all_ok && okw[w];
+        tot += red[w];
+    }
+    if (!all_ok) return false;
+    const float rrms = NORM ? (float)(1.0 / sqrt(tot / (double)n + eps)) : 1.f;
+    if constexpr (!Q8) {
+        *rscale = rrms;
+    } else {
+        *rscale = 1.f;
+        // xs = (x * rrms) * g in the reference's order; s_a = max|xs| / 127 (0 -> 1);
+        // each element quantized on its own thread into a byte of xq (ane_bridge.m:374-399)
+        float mx = 0.f;
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int j = threadIdx.x + k * kPB;
+            if (j < n) {
+                if constexpr (NORM) val[k] = val[k] * rrms * gr[NORM ? k : 0];
+                mx = fmaxf(mx, fabsf(val[k]));
+            }
+        }
+        mx = block_max_d(mx, red);   // two barriers; the second also orders the okw reads
         float s = __fdiv_rn(mx, 127.0f);
         if (s == 0.0f) s = 1.0f;
         *sa = s;
-        for (int i = threadIdx.x; i < n / 4; i += kPB)
-            xq[i] = quant8(xs[4 * i], s) | quant8(xs[4 * i + 1], s) << 8 |
-                    quant8(xs[4 * i + 2], s) << 16 | quant8(xs[4 * i + 3], s) << 24;
+        SH_LDS uint8_t *xb = (SH_LDS uint8_t *)xq;
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int j = threadIdx.x + k * kPB;
+            if (j < n) xb[j] = (uint8_t)quant8(val[k], s);
+        }
         lds_barrier();
     }
     return true;
@@ -400,17 +518,24 @@ struct StageIO {
     const uint64_t *res_ll;     // E_RESID residual from an LL vector
     const uint16_t *res_emb;    // E_RESID residual from the embedding row (layer 0)
     uint32_t e_in, e_res, e_out;
+    int in_per, in_stride;      // input vector layout (in_per 0: dense)
+    int res_per, res_stride;    // residual vector layout
+    uint32_t in_magic, res_magic;   // ceil(2^31 / per) of the two layouts
+    int out_stride;             // words between consecutive workgroups' output blocks
 };
 
-// One GEMV stage over W [rows, cols]. Row groups of G = 64/LPR rows are dealt to waves
-// vw = wave * gridDim.x + blockIdx.x. Weight tiles of the first U groups are loaded before
-// the input is polled. Returns false on timeout/abort. For E_CLS, *best_v/*best_i receive
-// this wave's (max, first index).
-template <int LPR, int CPL, int WT, int U>
-__device__ __forceinline__ bool gemv_stage(const PParams &p, const void *__restrict__ W,
+// One GEMV stage over W [rows, cols]. The workgroup owns the row block of its rank in the
+// stage's ownership `o` (none: it skips the stage without polling); inside the block, row
+// group k of G = 64/LPR rows belongs to wave k % kPW. Blocks of consecutive rows keep each
+// hand-over line written by one workgroup, so no line has several writers racing to it.
+// Weight tiles of the first U groups of each wave are loaded before the input is polled.
+// Returns false on timeout/abort. For E_CLS, *best_v/*best_i receive this wave's (max,
+// first index).
+template <int LPR, int CPL, int WT, int U, bool NORM>
+__device__ __forceinline__ bool gemv_stage(const PParams &p, const StageOwn o, const void *__restrict__ W,
                            const float *__restrict__ wscale, int rows, int cols,
                            int epi, const StageIO &io, float *xs, uint32_t *xq, double *red,
-                           float &best_v, int &best_i) {
+                           int *okw, float &best_v, int &best_i) {
     constexpr int G = 64 / LPR;
     constexpr int EPC = chunk_elems<WT>();
     constexpr bool Q8 = WT == SH_DTYPE_W8A8;
@@ -418,26 +543,47 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const void *__restr
     const size_t row_bytes = (size_t)cols * elem_bytes<WT>();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane % LPR, grp = lane / LPR;
-    const int NW = gridDim.x * kPW;
-    const int vw = wave * gridDim.x + blockIdx.x;
-    const int ngroups = (rows + G - 1) / G;
-    // does this workgroup own any row group? (waves of one workgroup are vw, vw+grid, ...)
-    const bool wg_has_work = (int)blockIdx.x < ngroups;
-    if (!wg_has_work) return true;
+    int rank = (int)blockIdx.x - o.off;
+    if (rank < 0) rank += gridDim.x;
+    if (rank >= o.n) return true;
+    const int r0 = rank * o.per;
+    const int r1 = min(rows, r0 + o.per);
+    if (r0 >= r1) return true;
+    // first row of this wave's k-th group (wave-uniform) and this lane's row in it
+    auto gbase = [&](int k) { return r0 + (wave + k * kPW) * G; };
 
     u32x4 w[U][CPL];
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        const int row = (vw + u * NW) * G + grp;
-        if (row < rows) {
+        const int row = gbase(u) + grp;
+        if (row < r1) {
             const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(Wb + (size_t)row * row_bytes);
 #pragma unroll
             for (int j = 0; j < CPL; j++) w[u][j] = src[sub + j * LPR];
         }
     }
     float sa = 1.0f;
-    if (!stage_input<WT, LPR * CPL * EPC>(xs, cols, io.in_ll, io.e_in, io.emb_row, io.gain, p.eps,
-                                          red, p, xq, &sa))
+    // residual rows, polled with the input (or read from the embedding row in layer 0), land
+    // in xs[cols, cols + r1 - r0)
+    const int nres = epi == E_RESID ? r1 - r0 : 0;
+    InputMap im{};
+    im.s = io.in_ll;
+    im.roff = io.res_ll ? io.res_ll - io.in_ll : 0;
+    im.d = xs;
+    im.n = cols;
+    im.per = io.in_per > 0 ? io.in_per : kDense;
+    im.stride = io.in_per > 0 ? io.in_stride : kDense;
+    im.magic = io.in_per > 0 ? io.in_magic : 2u;   // ceil(2^31 / kDense)
+    im.r0 = r0;
+    im.rper = io.res_per > 0 ? io.res_per : kDense;
+    im.rstride = io.res_per > 0 ? io.res_stride : kDense;
+    im.rmagic = io.res_per > 0 ? io.res_magic : 2u;
+    im.e = io.e_in;
+    im.er = io.e_res;
+    float rscale = 1.f;
+    if (!stage_input<WT, LPR * CPL * EPC, NORM>(xs, cols, im, cols + nres, io.emb_row,
+                                          epi == E_RESID ? io.res_emb : nullptr, io.gain, p.eps,
+                                          red, okw, p, xq, &sa, &rscale))
         return false;
     // this lane's slice of the input: floats, or packed int8 words for W8A8
     float xr[Q8 ? 1 : CPL * 8];
@@ -454,15 +600,15 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const void *__restr
     }
 
     bool ok = true;
-    for (int g0 = vw; g0 < ngroups; g0 += U * NW) {
+    for (int k0 = 0; gbase(k0) < r1; k0 += U) {
         float acc[U];
         int acci[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             acc[u] = 0.f;
             acci[u] = 0;
-            const int row = (g0 + u * NW) * G + grp;
-            if (row < rows) {
+            const int row = gbase(k0 + u) + grp;
+            if (row < r1) {
 #pragma unroll
                 for (int j = 0; j < CPL; j++) {
                     if constexpr (Q8) {
@@ -480,12 +626,11 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const void *__restr
             }
         }
         // next tiles are issued before this batch's reductions and stores
-        const int gn = g0 + U * NW;
-        if (gn < ngroups) {
+        if (gbase(k0 + U) < r1) {
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const int row = (gn + u * NW) * G + grp;
-                if (row < rows) {
+                const int row = gbase(k0 + U + u) + grp;
+                if (row < r1) {
                     const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(Wb + (size_t)row * row_bytes);
 #pragma unroll
                     for (int j = 0; j < CPL; j++) w[u][j] = src[sub + j * LPR];
@@ -494,34 +639,30 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const void *__restr
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int row = (g0 + u * NW) * G + grp;
+            const int row = gbase(k0 + u) + grp;
             float a;
             if constexpr (Q8) {
                 // exact int32 dot, then (float)acc * (s_w[r] * s_a) (one fixed order)
-                const int ai = group_sum_i<LPR>(acci[u]);
-                a = row < rows ? (float)ai * (wscale[row] * sa) : 0.0f;
+                const int ai = wsum_i<LPR>(acci[u]);
+                a = row < r1 ? (float)ai * (wscale[row] * sa) : 0.0f;
             } else {
-                a = group_sum<LPR>(acc[u]);
+                a = wsum<LPR>(acc[u]) * rscale;
             }
             if (epi == E_GATE) {
-                const float h3 = __shfl_down(a, LPR, 64);
-                if (sub == 0 && (grp & 1) == 0 && row < rows) {
+                // rows (2i, 2i+1) = (W1 row i, W3 row i) sit in adjacent lane groups; the
+                // owner's gate block starts at rank * out_stride
+                float h3 = 0.f;
+                if constexpr (LPR < 64) h3 = from_lane_up<LPR>(a);
+                if (sub == 0 && (grp & 1) == 0 && row < r1) {
                     const float s = a / (1.0f + (float)exp(-(double)a));   // infer.go:324-326
-                    ll_put(io.out_ll + (row >> 1), s * h3, io.e_out);
+                    ll_put(io.out_ll + (size_t)rank * io.out_stride + ((row - r0) >> 1), s * h3, io.e_out);
                 }
-            } else if (sub == 0 && row < rows) {
+            } else if (sub == 0 && row < r1) {
+                uint64_t *out = io.out_ll + (size_t)rank * io.out_stride + (row - r0);
                 if (epi == E_STORE) {
-                    ll_put(io.out_ll + row, a, io.e_out);
+                    ll_put(out, a, io.e_out);
                 } else if (epi == E_RESID) {
-                    float r;
-                    if (io.res_emb) {
-                        r = w2f<WT>(io.res_emb[row]);
-                    } else {
-                        uint64_t v = ll_get(io.res_ll + row);
-                        ok = ok && ll_wait_word(io.res_ll + row, io.e_res, v, p);
-                        r = __uint_as_float((uint32_t)v);
-                    }
-                    if (ok) ll_put(io.out_ll + row, r + p.alpha * a, io.e_out);
+                    ll_put(out, xs[cols + row - r0] + p.alpha * a, io.e_out);
                 } else {  // E_CLS
                     p.logits[row] = a;
                     if (a > best_v) {
@@ -532,21 +673,22 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const void *__restr
             }
         }
     }
-    // xs is rewritten by the next stage: every wave must be done reading it
-    return block_and(ok);
+    // no closing barrier: the next stage's poll starts with one before it writes LDS
+    return ok;
 }
 
 // Three LL segments (q heads, k, v of one kv head) waited for as one vector.
 struct QkvMap {
-    const uint64_t *q, *k, *v;
-    float *dq, *dk, *dv;
+    const uint64_t *base;       // ll_qkv (dense: qkv blocks are whole lines)
+    float *d;                   // q heads, k, v staged contiguously
+    size_t qo, ko, vo;          // word offsets of the group's q heads, k and v in ll_qkv
     int nq, hd;
+    uint32_t e;
     __device__ const uint64_t *src(int j) const {
-        return j < nq ? q + j : (j < nq + hd ? k + (j - nq) : v + (j - nq - hd));
+        return base + (j < nq ? qo + j : (j < nq + hd ? ko + (j - nq) : vo + (j - nq - hd)));
     }
-    __device__ float *dst(int j) const {
-        return j < nq ? dq + j : (j < nq + hd ? dk + (j - nq) : dv + (j - nq - hd));
-    }
+    __device__ float *dst(int j) const { return d + j; }
+    __device__ uint32_t ep(int) const { return e; }
 };
 
 // Asynchronous copy of cached rows [0, rows) of one kv head into LDS (global_load_lds:
@@ -635,8 +777,7 @@ __device__ __forceinline__ void kv_unpack16(const u32x4 &v, float *f) {
 // that moves x/s across a rounding boundary would change an int8 input.
 template <int KVT, int HD, bool EXACT>
 __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
-                           float *ks, float *vs, float *sc, float *part, uint8_t *kvlds,
-                           double *red, float *redf) {
+                           float *sc, float *part, uint8_t *kvlds, double *red, float *redf) {
     using S = KvStage<KVT, HD>;
     constexpr int hd = HD, ngr = kPB / HD;
     const int group = p.H / p.KVH, tid = threadIdx.x;
@@ -647,17 +788,21 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
     SH_LDS uint8_t *vst = kst + (size_t)S::ROWS * S::RB;
     const SH_LDS float *qsl = (const SH_LDS float *)qs;
 
-    QkvMap qm{p.ll_qkv + (size_t)g * group * hd, p.ll_qkv + p.qdim + (size_t)g * hd,
-              p.ll_qkv + p.qdim + p.kvdim + (size_t)g * hd, qs, ks, vs, group * hd, hd};
-    if (!ll_wait_batch<(kMaxGroup + 2) * 256 / kPB>(group * hd + 2 * hd, e, p, qm)) return false;
+    // qs holds the group's q heads, then k (at kofs), then v (at vofs): one LDS array
+    // addressed by offsets, so no pointer ever selects between two LDS arrays
+    const int kofs = group * hd, vofs = kofs + hd;
+    float *ks = qs + kofs, *vs = qs + vofs;
+    QkvMap qm{p.ll_qkv, qs, (size_t)g * group * hd, p.qdim + (size_t)g * hd,
+              p.qdim + p.kvdim + (size_t)g * hd, group * hd, hd, e};
+    if (!ll_wait_batch<(kMaxGroup + 2) * 256 / kPB>(group * hd + 2 * hd, p, qm)) return false;
     if (p.qk_norm) {
         // per-head RMSNorm: wave w < group normalises q head w, wave `group` normalises k
         if (wave <= group) {
-            float *v = wave < group ? qs + wave * hd : ks;
+            float *v = qs + (wave < group ? wave : group) * hd;
             const float *gn = wave < group ? Lp.q_norm : Lp.k_norm;
             double ss = 0;
             for (int i = lane; i < hd; i += 64) ss += (double)v[i] * (double)v[i];
-            ss = wave_sum_d(ss);
+            ss = wsum_d64(ss);
             const float rr = (float)(1.0 / sqrt(ss / (double)hd + p.qk_eps));
             for (int i = lane; i < hd; i += 64) v[i] = v[i] * rr * gn[i];
         }
@@ -667,7 +812,7 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
     const int half = hd / 2;
     for (int i = tid; i < (group + 1) * half; i += kPB) {
         const int h = i / half, pi = i % half;
-        float *v = h < group ? qs + h * hd : ks;
+        float *v = qs + h * hd;   // h == group: k
         const float c = p.rope_cos[pos * half + pi], s = p.rope_sin[pos * half + pi];
         const float ev = v[2 * pi], ov = v[2 * pi + 1];
         // each product rounded before the sum, as the reference computes it
@@ -714,8 +859,7 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
                 float d = 0.f;
 #pragma unroll
                 for (int e = 0; e < EPC; e++) d = fmaf(qr[h][e], kf[e], d);
-#pragma unroll
-                for (int off = LPK / 2; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
+                d = wsum<LPK>(d);
                 if (valid && sl == 0) sc[h * p.max_seq + t] = d * p.inv_sqrt_hd;
             }
         }
@@ -782,15 +926,14 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
         float *s = sc + wave * p.max_seq;
         float mx = -INFINITY;
         for (int t = lane; t <= pos; t += 64) mx = fmaxf(mx, s[t]);
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        mx = wmax<64>(mx);
         double sum = 0;
         for (int t = lane; t <= pos; t += 64) {
             const float ev = (float)exp((double)(s[t] - mx));
             s[t] = ev;
             sum += (double)ev;
         }
-        sum = wave_sum_d(sum);
+        sum = wsum_d64(sum);
         const float inv = (float)(1.0 / sum);
         for (int t = lane; t <= pos; t += 64) s[t] = s[t] * inv;
     }
@@ -849,12 +992,12 @@ template <int WT, int KVT, int HD, int LD, int CD, int LQ, int CQ, int LF, int C
 __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     __shared__ float xs[kXs];
     __shared__ __attribute__((aligned(16))) uint32_t xq[WT == SH_DTYPE_W8A8 ? kXs / 4 : 1];
-    __shared__ __attribute__((aligned(16))) float qs[kMaxGroup * 256];
-    __shared__ float ks[256], vs[256];
+    __shared__ __attribute__((aligned(16))) float qs[(kMaxGroup + 2) * 256];   // q heads, k, v
     __shared__ float sc[kScores];
     __shared__ float part[kPW * kMaxGroup * 256];
     __shared__ __attribute__((aligned(16))) uint8_t kvlds[kKvStage];
     __shared__ double red[kPW];
+    __shared__ int okw[kPW];
     __shared__ float redf[kPW];
     __shared__ ArgmaxPartial cand[kPW];
     __shared__ int next_tok;
@@ -864,9 +1007,8 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     int tok_next = 0;
     for (int f = 0; f < p.n_forwards; f++) {
         const int pos = p.pos0 + f;
-        const bool tracing = p.trace && f == p.trace_f && threadIdx.x == 0 &&
-                             (blockIdx.x == 0 || blockIdx.x == gridDim.x - 1);
-        long long *tr = p.trace + (blockIdx.x == 0 ? 0 : n_stamps);
+        const bool tracing = p.trace && f == p.trace_f && threadIdx.x == 0;
+        long long *tr = p.trace + (size_t)blockIdx.x * n_stamps;
         int ts = 0;
         auto stamp = [&]() {
             if (tracing) tr[ts] = wall_clock64();
@@ -886,17 +1028,21 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             StageIO io{};
             // qkv
             io.in_ll = l ? p.ll_x : nullptr;
+            io.in_per = p.own[3].per;
+            io.in_stride = p.ostride[3];
+            io.in_magic = p.omagic[3];
             io.emb_row = l ? nullptr : emb_row;
             io.gain = Lp.rms_att;
             io.out_ll = p.ll_qkv;
+            io.out_stride = p.ostride[0];
             io.e_in = e - 1;
             io.e_out = e;
-            if (!gemv_stage<LD, CD, WT, 2>(p, Lp.wqkv, Lp.s_qkv, p.qkv_rows, p.D, E_STORE, io, xs, xq, red, bv, bi))
+            if (!gemv_stage<LD, CD, WT, 2, true>(p, p.own[0], Lp.wqkv, Lp.s_qkv, p.qkv_rows, p.D, E_STORE, io, xs, xq, red, okw, bv, bi))
                 return;
             stamp();
             // attention
             if ((int)blockIdx.x < p.KVH &&
-                !attn_stage<KVT, HD, WT == SH_DTYPE_W8A8>(p, l, blockIdx.x, pos, e, qs, ks, vs, sc,
+                !attn_stage<KVT, HD, WT == SH_DTYPE_W8A8>(p, l, blockIdx.x, pos, e, qs, sc,
                                                           part, kvlds, red, redf))
                 return;
             stamp();
@@ -904,33 +1050,48 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io = StageIO{};
             io.in_ll = p.ll_att;
             io.out_ll = p.ll_x2;
+            io.out_stride = p.ostride[1];
             io.res_ll = l ? p.ll_x : nullptr;
+            io.res_per = p.own[3].per;
+            io.res_stride = p.ostride[3];
+            io.res_magic = p.omagic[3];
             io.res_emb = l ? nullptr : emb_row;
             io.e_in = e;
             io.e_res = e - 1;
             io.e_out = e;
-            if (!gemv_stage<LQ, CQ, WT, 2>(p, Lp.wo, Lp.s_o, p.D, p.qdim, E_RESID, io, xs, xq, red, bv, bi))
+            if (!gemv_stage<LQ, CQ, WT, 2, false>(p, p.own[1], Lp.wo, Lp.s_o, p.D, p.qdim, E_RESID, io, xs, xq, red, okw, bv, bi))
                 return;
             stamp();
             // w1/w3 + silu gate
             io = StageIO{};
             io.in_ll = p.ll_x2;
+            io.in_per = p.own[1].per;
+            io.in_stride = p.ostride[1];
+            io.in_magic = p.omagic[1];
             io.gain = Lp.rms_ffn;
             io.out_ll = p.ll_gate;
+            io.out_stride = p.ostride[2];
             io.e_in = e;
             io.e_out = e;
-            if (!gemv_stage<LD, CD, WT, 2>(p, Lp.w13, Lp.s_13, 2 * p.F, p.D, E_GATE, io, xs, xq, red, bv, bi))
+            if (!gemv_stage<LD, CD, WT, 2, true>(p, p.own[2], Lp.w13, Lp.s_13, 2 * p.F, p.D, E_GATE, io, xs, xq, red, okw, bv, bi))
                 return;
             stamp();
             // w2 + residual
             io = StageIO{};
             io.in_ll = p.ll_gate;
+            io.in_per = p.own[2].per / 2;
+            io.in_stride = p.ostride[2];
+            io.in_magic = p.omagic[2];
             io.out_ll = p.ll_x;
+            io.out_stride = p.ostride[3];
             io.res_ll = p.ll_x2;
+            io.res_per = p.own[1].per;
+            io.res_stride = p.ostride[1];
+            io.res_magic = p.omagic[1];
             io.e_in = e;
             io.e_res = e;
             io.e_out = e;
-            if (!gemv_stage<LF, CF, WT, 2>(p, Lp.w2, Lp.s_2, p.D, p.F, E_RESID, io, xs, xq, red, bv, bi))
+            if (!gemv_stage<LF, CF, WT, 2, false>(p, p.own[3], Lp.w2, Lp.s_2, p.D, p.F, E_RESID, io, xs, xq, red, okw, bv, bi))
                 return;
             stamp();
         }
@@ -938,30 +1099,25 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
         const uint32_t ec = base + (uint32_t)L + 1;
         StageIO io{};
         io.in_ll = p.ll_x;
+        io.in_per = p.own[3].per;
+        io.in_stride = p.ostride[3];
+        io.in_magic = p.omagic[3];
         io.gain = p.rms_final;
         io.e_in = base + (uint32_t)L;
-        if (!gemv_stage<LD, CD, WT, 2>(p, p.cls, p.s_cls, p.V, p.D, E_CLS, io, xs, xq, red, bv, bi)) return;
+        if (!gemv_stage<LD, CD, WT, 4, true>(p, p.own[4], p.cls, p.s_cls, p.V, p.D, E_CLS, io, xs, xq, red, okw, bv, bi)) return;
         stamp();
         // this workgroup's (max, first index)
         {
             float v = bv;
             int idx = bi;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(v, off, 64);
-                const int oi = __shfl_xor(idx, off, 64);
-                if (better(ov, oi, v, idx)) {
-                    v = ov;
-                    idx = oi;
-                }
-            }
+            wargmax(v, idx);
             if ((threadIdx.x & 63) == 0) cand[threadIdx.x >> 6] = ArgmaxPartial{v, idx};
             lds_barrier();
             if (threadIdx.x == 0) {
                 ArgmaxPartial b = cand[0];
                 for (int w = 1; w < kPW; w++)
                     if (better(cand[w].v, cand[w].i, b.v, b.i)) b = cand[w];
-                const int slot = (f & 1) * gridDim.x + blockIdx.x;
+                const size_t slot = ((size_t)(f & 1) * gridDim.x + blockIdx.x) * kArgSlot;
                 ll_put(p.ll_pv + slot, b.v, ec);
                 ll_put_u(p.ll_pi + slot, (uint32_t)b.i, ec);
             }
@@ -972,10 +1128,12 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             float v = -INFINITY;
             int idx = 0x7fffffff;
             const int n = gridDim.x;
-            const uint64_t *pv = p.ll_pv + (f & 1) * n, *pi = p.ll_pi + (f & 1) * n;
+            const uint64_t *pv = p.ll_pv + (size_t)(f & 1) * n * kArgSlot;
+            const uint64_t *pi = p.ll_pi + (size_t)(f & 1) * n * kArgSlot;
             for (int k = threadIdx.x; k < n; k += kPB) {
-                uint64_t a = ll_get(pv + k), b = ll_get(pi + k);
-                ok = ok && ll_wait_word(pv + k, ec, a, p) && ll_wait_word(pi + k, ec, b, p);
+                const size_t o = (size_t)k * kArgSlot;
+                uint64_t a = ll_get(pv + o), b = ll_get(pi + o);
+                ok = ok && ll_wait_word(pv + o, ec, a, p) && ll_wait_word(pi + o, ec, b, p);
                 const float cv = __uint_as_float((uint32_t)a);
                 const int ci = (int)(uint32_t)b;
                 if (better(cv, ci, v, idx)) {
@@ -984,15 +1142,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 }
             }
             if (!block_and(ok)) return;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(v, off, 64);
-                const int oi = __shfl_xor(idx, off, 64);
-                if (better(ov, oi, v, idx)) {
-                    v = ov;
-                    idx = oi;
-                }
-            }
+            wargmax(v, idx);
             if ((threadIdx.x & 63) == 0) cand[threadIdx.x >> 6] = ArgmaxPartial{v, idx};
             lds_barrier();
             if (threadIdx.x == 0) {
@@ -1070,12 +1220,23 @@ bool persistent_supported(const sh_model *m) {
     const int group = c.n_heads / c.n_kv_heads;
     if (!pick_persistent(m->dtype, c.kv_dtype, c.dim, m->qdim, c.hidden, c.head_dim)) return false;
     if (group > kMaxGroup || group * c.max_seq > kScores || c.head_dim > 256) return false;
-    if (c.dim > kXs || m->qdim > kXs || c.hidden > kXs) return false;
+    // staged input plus the residual rows polled with it
+    if (c.dim + kMaxRes > kXs || m->qdim + kMaxRes > kXs || c.hidden + kMaxRes > kXs) return false;
     if (kPB % c.head_dim) return false;
     return true;
 }
 
-hipError_t persistent_grid(const sh_model *m, int *grid_out, std::string *why) {
+// Grid and stage ownership. The grid is one workgroup per CU (at most kPB, one argmax
+// partial per thread), shrunk until the w13 stage's row blocks cover every workgroup: that
+// stage then depends on every workgroup having finished the previous forward's classifier,
+// which keeps the single-buffered ll_x vector safe while prompt forwards run without an
+// argmax exchange. The other stages use as few workgroups as fill one pass of their waves
+// (blocks of 16 rows or a multiple, so every producer's hand-over words fill whole 128-byte
+// lines), placed so that a workgroup's previous stage ends before the stage's input is
+// ready and its weight loads overlap the wait: attention on workgroups [0, KVH), qkv right
+// after them, wo after qkv. w2 spreads over every workgroup (a few rows each), so the weight
+// tiles it loads after the w13 stage stay small.
+hipError_t persistent_plan(sh_model *m, std::string *why) {
     const sh_config &c = m->cfg;
     PersistentKernel k = pick_persistent(m->dtype, c.kv_dtype, c.dim, m->qdim, c.hidden, c.head_dim);
     if (!k) return hipErrorInvalidValue;
@@ -1091,21 +1252,51 @@ hipError_t persistent_grid(const sh_model *m, int *grid_out, std::string *why) {
     if (e != hipSuccess) return e;
     *why += "; " + std::to_string(per_cu) + " workgroup(s) of " + std::to_string(kPB) + " per CU";
     if (per_cu < 1) return hipErrorInvalidConfiguration;
-    // One workgroup per CU, and no more workgroups than row groups in the smallest GEMV
-    // stage: every workgroup then owns rows in every stage, so it polls every stage's input
-    // in order, which is what keeps single-buffered hand-over vectors safe.
-    int grid = cus;
     int ld = 0, lq = 0, lf = 0;
     shape_lanes(m->dtype, c.dim, m->qdim, c.hidden, &ld, &lq, &lf);
-    auto groups = [](int rows, int lpr) { return (rows + 64 / lpr - 1) / (64 / lpr); };
-    grid = std::min(grid, groups(m->qkv_rows, ld));
-    grid = std::min(grid, groups(c.dim, lq));
-    grid = std::min(grid, groups(2 * c.hidden, ld));
-    grid = std::min(grid, groups(c.dim, lf));
-    grid = std::min(grid, groups(c.vocab, ld));
-    grid = std::min(grid, kPB);  // one argmax partial per thread
+    auto cdiv = [](int a, int b) { return (a + b - 1) / b; };
+    auto up = [&](int a, int b) { return cdiv(a, b) * b; };
+    const int rows13 = 2 * c.hidden;
+    int grid = std::min(cus, kPB);
+    grid = std::min(grid, rows13 / 2);
+    auto per13_for = [&](int g) { return up(cdiv(rows13, g), 2); };
+    while (grid > 1 && cdiv(rows13, per13_for(grid)) != grid) grid--;
     if (grid < c.n_kv_heads) return hipErrorInvalidConfiguration;
-    *grid_out = grid;
+    const int KVH = c.n_kv_heads;
+    // rows per workgroup: one pass of kPW waves of G = 64/L rows, rounded to 16
+    auto one_pass = [&](int lanes) { return up(kPW * (64 / lanes), 16); };
+    auto fit = [&](int rows, int per) {
+        while (cdiv(rows, per) > grid) per += 16;
+        return per;
+    };
+    // w2 on every workgroup (its weights are the second largest; a few rows each keeps the
+    // weight tiles loaded after the w13 stage small)
+    const int per_w2 = cdiv(c.dim, grid);
+    const int n_w2 = cdiv(c.dim, per_w2);
+    int per_qkv = fit(m->qkv_rows, one_pass(ld));
+    while (KVH + cdiv(m->qkv_rows, per_qkv) > grid && per_qkv < m->qkv_rows) per_qkv += 16;
+    const int n_qkv = cdiv(m->qkv_rows, per_qkv);
+    const int per_wo = fit(c.dim, std::min(one_pass(lq), kMaxRes));
+    const int n_wo = cdiv(c.dim, per_wo);
+    const int off_qkv = KVH + n_qkv <= grid ? KVH : 0;
+    int off_wo = off_qkv + n_qkv;
+    if (off_wo + n_wo > grid) off_wo = KVH + n_wo <= grid ? KVH : 0;
+    const int per13 = per13_for(grid);
+    m->p_grid = grid;
+    m->p_own[0] = StageOwn{off_qkv, n_qkv, per_qkv};
+    m->p_own[1] = StageOwn{off_wo, n_wo, per_wo};
+    m->p_own[2] = StageOwn{0, grid, per13};
+    m->p_own[3] = StageOwn{0, n_w2, per_w2};
+    m->p_own[4] = StageOwn{0, grid, cdiv(c.vocab, grid)};
+    if (per_wo > kMaxRes || per_w2 > kMaxRes) return hipErrorInvalidConfiguration;
+    m->p_ostride[0] = per_qkv;   // a multiple of 16: qkv stays dense for the attention stage
+    m->p_ostride[1] = up(per_wo, 16);
+    m->p_ostride[2] = up(per13 / 2, 16);
+    m->p_ostride[3] = up(per_w2, 16);
+    m->p_ostride[4] = 0;
+    *why += "; rows/workgroups qkv " + std::to_string(per_qkv) + "x" + std::to_string(n_qkv) + " wo " +
+            std::to_string(per_wo) + "x" + std::to_string(n_wo) + " w13 " + std::to_string(per13) + "x" +
+            std::to_string(grid) + " w2 " + std::to_string(per_w2) + "x" + std::to_string(n_w2);
     return hipSuccess;
 }
 
@@ -1157,6 +1348,13 @@ hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt
     p.spin_limit = m->spin_ticks;
     p.trace = m->trace_f >= 0 ? m->trace_buf : nullptr;
     p.trace_f = m->trace_f;
+    for (int i = 0; i < 5; i++) {
+        p.own[i] = m->p_own[i];
+        p.ostride[i] = m->p_ostride[i];
+        // elements per output block: rows, or row pairs for the gate vector
+        const int per = i == 2 ? m->p_own[i].per / 2 : m->p_own[i].per;
+        p.omagic[i] = per > 0 ? (uint32_t)((0x80000000ull + (uint64_t)per - 1) / (uint64_t)per) : 0u;
+    }
     m->epoch += (uint32_t)n_forwards * (uint32_t)(c.n_layers + 1);
     void *args[] = {&p};
     return hipLaunchCooperativeKernel((const void *)k, dim3(m->p_grid), dim3(kPB), args, 0, m->stream);

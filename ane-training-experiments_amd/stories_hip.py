@@ -357,25 +357,30 @@ class Model:
     def trace_forward(self, forward: int) -> None:
         _check(self.lib.sh_trace_forward(self.h, forward), "sh_trace_forward")
 
-    def trace_read(self) -> dict:
-        """Stage durations (us) of the traced forward for workgroup 0 and the last one."""
+    def trace_stamps(self) -> np.ndarray:
+        """Timestamps (us, from the earliest forward start) of the traced forward:
+        [grid, 5 * n_layers + 3], one row per workgroup."""
         L = self.cfg.n_layers
-        n = 2 * (5 * L + 3)
+        n = self.stats()["grid"] * (5 * L + 3)
         buf = np.zeros(n, np.int64)
         cnt = C.c_int32(0)
         rate = C.c_double(0)
         _check(self.lib.sh_trace_read(self.h, buf.ctypes.data_as(C.POINTER(C.c_int64)), n, C.byref(cnt),
                                       C.byref(rate)), "sh_trace_read")
-        out = {}
+        t = buf[:cnt.value].reshape(-1, 5 * L + 3).astype(np.float64)
+        return (t - t[:, 0].min()) * 1e6 / rate.value
+
+    def trace_read(self) -> dict:
+        """Critical-path stage durations (us) of the traced forward, summed over layers: a
+        stage ends when its last workgroup stamps it."""
+        L = self.cfg.n_layers
+        ends = self.trace_stamps().max(axis=0)
+        d = np.diff(ends)
         names = ["qkv", "attn", "wo", "w13", "w2"]
-        for w, label in ((0, "wg0"), (1, "wg_last")):
-            t = buf[w * (n // 2):(w + 1) * (n // 2)].astype(np.float64) * 1e6 / rate.value
-            d = np.diff(t)
-            per = {k: d[j:5 * L:5].sum() for j, k in enumerate(names)}
-            per["classifier"] = d[5 * L]
-            per["argmax"] = d[5 * L + 1]
-            per["total"] = t[-1] - t[0]
-            out[label] = per
+        out = {k: float(d[j:5 * L:5].sum()) for j, k in enumerate(names)}
+        out["classifier"] = float(d[5 * L])
+        out["argmax"] = float(d[5 * L + 1])
+        out["total"] = float(ends[-1] - ends[0])
         return out
 
     def describe(self) -> str:
