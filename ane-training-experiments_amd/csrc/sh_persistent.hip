@@ -407,7 +407,7 @@ __device__ __forceinline__ void ll_poll_regs(int n, const PParams &p, const Inpu
 // Stage this stage's input in LDS: xs[0, n) from an LL vector (map) or, when emb_row is
 // given, from an embedding row; xs[n, count) receives the residual rows polled with it.
 // With NORM (the stage's `gain`), rmsNormVec (infer.go:301-311): ss = sum of x^2 in float64, rrms =
-// float32(1 / sqrt(ss/n + eps)).
+// float32(1 / sqrt(ss/n + eps)); the fp16/bf16 models take ss and rrms in float (rsqrt).
 //   fp16 / bf16: xs = x * gain and *rscale = rrms, applied by the caller to each finished
 //                dot product (sum w*(x*g) * rrms instead of sum w*((x*rrms)*g): the float
 //                rounding of each term differs, by about 1 ulp).
@@ -451,18 +451,22 @@ __device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &ma
     } else {
         ll_poll_regs<K>(res_emb ? n : count, p, map, val, ok);
     }
+    // sum of squares: float64 as the reference for W8A8, float for the fp16/bf16 models
     double ss = 0;
+    float ssf = 0.f;
 #pragma unroll
     for (int k = 0; k < K; k++) {
         const int j = threadIdx.x + k * kPB;
         if (j < n) {
-            if constexpr (NORM) ss += (double)val[k] * (double)val[k];
+            if constexpr (NORM && Q8) ss += (double)val[k] * (double)val[k];
+            if constexpr (NORM && !Q8) ssf += val[k] * val[k];
             if constexpr (!Q8) xs[j] = NORM ? val[k] * gr[NORM ? k : 0] : val[k];
         } else if (j < count) {
             xs[j] = val[k];   // residual rows
         }
     }
-    if constexpr (NORM) ss = wsum_d64(ss);
+    if constexpr (NORM && Q8) ss = wsum_d64(ss);
+    if constexpr (NORM && !Q8) ss = (double)wsum<64>(ssf);
     const bool wok = __all(ok);
     if (lane == 0) {
         red[wave] = ss;
@@ -477,7 +481,9 @@ __device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &ma
         tot += red[w];
     }
     if (!all_ok) return false;
-    const float rrms = NORM ? (float)(1.0 / sqrt(tot / (double)n + eps)) : 1.f;
+    float rrms = 1.f;
+    if constexpr (NORM && Q8) rrms = (float)(1.0 / sqrt(tot / (double)n + eps));
+    if constexpr (NORM && !Q8) rrms = rsqrtf((float)tot / (float)n + (float)eps);
     if constexpr (!Q8) {
         *rscale = rrms;
     } else {
@@ -654,7 +660,8 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const StageOwn o, c
                 float h3 = 0.f;
                 if constexpr (LPR < 64) h3 = from_lane_up<LPR>(a);
                 if (sub == 0 && (grp & 1) == 0 && row < r1) {
-                    const float s = a / (1.0f + (float)exp(-(double)a));   // infer.go:324-326
+                    // infer.go:324-326 (float64 exp; float expf for the fp16/bf16 models)
+                    const float s = Q8 ? a / (1.0f + (float)exp(-(double)a)) : a / (1.0f + expf(-a));
                     ll_put(io.out_ll + (size_t)rank * io.out_stride + ((row - r0) >> 1), s * h3, io.e_out);
                 }
             } else if (sub == 0 && row < r1) {
@@ -988,6 +995,196 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
     return true;
 }
 
+
+// Attention for the fp16 / bf16 models (the W8A8 model keeps attn_stage<..., true>): the
+// same mathematics in fewer dependent steps, rounded differently in the last bits.
+//  - RoPE factors are loaded before the poll; QK-norm and the softmax use float math;
+//  - scores are lane-sliced dot products over the cached rows (LDS rows two blocks per trip,
+//    rows beyond the LDS stage read from the cache the same way), each wave tracking the
+//    running maximum of its scores;
+//  - the softmax runs on all waves; the exp terms are left unnormalised and the P.V sums are
+//    scaled by 1/sum at the end (p.v/sum instead of (p/sum).v);
+//  - three workgroup barriers after the cache append, none at the end (the next stage's poll
+//    starts with one).
+template <int KVT, int HD>
+__device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
+                                                float *sc, float *part, uint8_t *kvlds, float *redf) {
+    using S = KvStage<KVT, HD>;
+    constexpr int hd = HD, ngr = kPB / HD;
+    constexpr int LPK = S::RB / 16, EPC = 16 / S::EB, PPW = 64 / LPK;
+    const int group = p.H / p.KVH, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int ms = p.max_seq;
+    const LayerPtrs &Lp = p.layers[l];
+    const size_t lbase = (size_t)l * ms * p.kvdim + (size_t)g * hd;
+    SH_LDS uint8_t *kst = (SH_LDS uint8_t *)kvlds;
+    SH_LDS uint8_t *vst = kst + (size_t)S::ROWS * S::RB;
+    const int kofs = group * hd, vofs = kofs + hd;
+    float *ks = qs + kofs, *vs = qs + vofs;
+    const int half = hd / 2;
+    // this thread's RoPE pair (q heads, then k) and its factors, before the poll
+    const bool rope_t = tid < (group + 1) * half;
+    const int rpi = tid % half;
+    float rc = 0.f, rs = 0.f;
+    if (rope_t) {
+        rc = p.rope_cos[pos * half + rpi];
+        rs = p.rope_sin[pos * half + rpi];
+    }
+    QkvMap qm{p.ll_qkv, qs, (size_t)g * group * hd, p.qdim + (size_t)g * hd,
+              p.qdim + p.kvdim + (size_t)g * hd, group * hd, hd, e};
+    if (!ll_wait_batch<(kMaxGroup + 2) * 256 / kPB>(group * hd + 2 * hd, p, qm)) return false;
+    if (p.qk_norm) {
+        // per-head RMSNorm: wave w < group normalises q head w, wave `group` normalises k
+        if (wave <= group) {
+            float *v = qs + (wave < group ? wave : group) * hd;
+            const float *gn = wave < group ? Lp.q_norm : Lp.k_norm;
+            float ss = 0.f;
+            for (int i = lane; i < hd; i += 64) ss += v[i] * v[i];
+            ss = wsum<64>(ss);
+            const float rr = rsqrtf(ss / (float)hd + (float)p.qk_eps);
+            for (int i = lane; i < hd; i += 64) v[i] = v[i] * rr * gn[i];
+        }
+        lds_barrier();
+    }
+    if (rope_t) {   // infer.go:247-265, interleaved pairs
+        float *v = qs + (tid / half) * hd;
+        const float ev = v[2 * rpi], ov = v[2 * rpi + 1];
+        v[2 * rpi] = ev * rc - ov * rs;
+        v[2 * rpi + 1] = ev * rs + ov * rc;
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // the LDS copies of the cached rows have landed
+    lds_barrier();
+    // infer.go:267-271 storeKV in the cache's storage type; row pos also joins the LDS rows
+    for (int i = tid; i < hd; i += kPB) {
+        ks[i] = kv_rnd<KVT>(ks[i]);
+        vs[i] = kv_rnd<KVT>(vs[i]);
+        kv_st<KVT>(p.kcache, lbase + (size_t)pos * p.kvdim + i, ks[i]);
+        kv_st<KVT>(p.vcache, lbase + (size_t)pos * p.kvdim + i, vs[i]);
+        if (pos < S::ROWS) {
+            kv_put<KVT>(kst + (size_t)pos * S::RB, i, ks[i]);
+            kv_put<KVT>(vst + (size_t)pos * S::RB, i, vs[i]);
+        }
+    }
+    lds_barrier();
+    // scores (infer.go:280-288) and each wave's maximum
+    const int sl = lane % LPK, rin = lane / LPK;
+    float qr[kMaxGroup][EPC];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++)
+#pragma unroll
+        for (int q = 0; q < EPC; q++) qr[h][q] = h < group ? qs[h * hd + sl * EPC + q] : 0.f;
+    float mx[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++) mx[h] = -INFINITY;
+    auto score_row = [&](const float (&kf)[EPC], int t, bool valid) {
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++) {
+            if (h >= group) continue;
+            float d = 0.f;
+#pragma unroll
+            for (int q = 0; q < EPC; q++) d = fmaf(qr[h][q], kf[q], d);
+            d = wsum<LPK>(d) * p.inv_sqrt_hd;
+            if (valid) {
+                if (sl == 0) sc[h * ms + t] = d;
+                mx[h] = fmaxf(mx[h], d);
+            }
+        }
+    };
+    const int tl = pos < S::ROWS ? pos : S::ROWS - 1;   // last position held in LDS
+    for (int t0 = wave * PPW; t0 <= tl; t0 += 2 * kPW * PPW) {
+        const int ta = t0 + rin, tb = t0 + kPW * PPW + rin;
+        const bool va = ta <= tl, vb = tb <= tl;
+        const u32x4 ka = ((const SH_LDS u32x4 *)(kst + (size_t)(va ? ta : tl) * S::RB))[sl];
+        const u32x4 kb = ((const SH_LDS u32x4 *)(kst + (size_t)(vb ? tb : tl) * S::RB))[sl];
+        float fa[EPC], fb[EPC];
+        kv_unpack16<KVT>(ka, fa);
+        kv_unpack16<KVT>(kb, fb);
+        score_row(fa, ta, va);
+        score_row(fb, tb, vb);
+    }
+    if (pos > tl) {
+        // rows beyond the LDS stage, from the cache (row pos from the staged k)
+        float kpos[EPC];
+#pragma unroll
+        for (int q = 0; q < EPC; q++) kpos[q] = ks[sl * EPC + q];
+        const SH_GLOBAL uint8_t *kc = (const SH_GLOBAL uint8_t *)p.kcache;
+        for (int t0 = tl + 1 + wave * PPW; t0 <= pos; t0 += kPW * PPW) {
+            const int t = t0 + rin;
+            const bool valid = t <= pos;
+            const int tr = valid && t < pos ? t : tl;   // a row in the cache (row pos is not read)
+            const u32x4 kv4 = ((const SH_GLOBAL u32x4 *)(kc + (lbase + (size_t)tr * p.kvdim) * S::EB))[sl];
+            float kf[EPC];
+            kv_unpack16<KVT>(kv4, kf);
+            if (t == pos) {
+#pragma unroll
+                for (int q = 0; q < EPC; q++) kf[q] = kpos[q];
+            }
+            score_row(kf, t, valid);
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++) {
+        const float m = wmax<64>(mx[h]);
+        if (lane == 0 && h < group) redf[wave * kMaxGroup + h] = m;
+    }
+    lds_barrier();
+    // softmax (infer.go:328-345) on every wave: unnormalised exp terms and their sums
+    float gmx[kMaxGroup], sum[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++) {
+        gmx[h] = -INFINITY;
+        sum[h] = 0.f;
+        if (h < group)
+            for (int w = 0; w < kPW; w++) gmx[h] = fmaxf(gmx[h], redf[w * kMaxGroup + h]);
+    }
+    for (int t = tid; t <= pos; t += kPB) {
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++) {
+            if (h >= group) continue;
+            const float ev = expf(sc[h * ms + t] - gmx[h]);
+            sc[h * ms + t] = ev;
+            sum[h] += ev;
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++) {
+        const float sw = wsum<64>(sum[h]);
+        if (lane == 0 && h < group) redf[(kPW + wave) * kMaxGroup + h] = sw;
+    }
+    lds_barrier();
+    // P.V (infer.go:290-297): thread (position group tg, dim vi), partials through LDS
+    const int vi = tid % hd, tg = tid / hd;
+    float acc[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++) acc[h] = 0.f;
+#pragma unroll 4
+    for (int t = tg; t <= tl; t += ngr) {
+        const float vv = kv_get<KVT>(vst + (size_t)t * S::RB, vi);
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++)
+            if (h < group) acc[h] = fmaf(sc[h * ms + t], vv, acc[h]);
+    }
+    for (int t = tl + 1 + ((tg - (tl + 1) % ngr + ngr) % ngr); t <= pos; t += ngr) {
+        const float vc = kv_ld<KVT>(p.vcache, lbase + (size_t)(t < pos ? t : tl) * p.kvdim + vi);
+        const float vv = t == pos ? vs[vi] : vc;
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++)
+            if (h < group) acc[h] = fmaf(sc[h * ms + t], vv, acc[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++)
+        if (h < group) part[(h * ngr + tg) * hd + vi] = acc[h];
+    lds_barrier();
+    for (int k = tid; k < group * hd; k += kPB) {
+        const int h = k / hd, ii = k % hd;
+        float tot = 0.f, o = 0.f;
+        for (int w = 0; w < kPW; w++) tot += redf[(kPW + w) * kMaxGroup + h];
+        for (int r = 0; r < ngr; r++) o += part[(h * ngr + r) * hd + ii];
+        ll_put(p.ll_att + (size_t)(g * group + h) * hd + ii, o / tot, e);
+    }
+    return true;
+}
+
 template <int WT, int KVT, int HD, int LD, int CD, int LQ, int CQ, int LF, int CF>
 __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     __shared__ float xs[kXs];
@@ -998,7 +1195,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t kvlds[kKvStage];
     __shared__ double red[kPW];
     __shared__ int okw[kPW];
-    __shared__ float redf[kPW];
+    __shared__ float redf[2 * kPW * kMaxGroup];
     __shared__ ArgmaxPartial cand[kPW];
     __shared__ int next_tok;
 
@@ -1041,10 +1238,14 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 return;
             stamp();
             // attention
-            if ((int)blockIdx.x < p.KVH &&
-                !attn_stage<KVT, HD, WT == SH_DTYPE_W8A8>(p, l, blockIdx.x, pos, e, qs, sc,
-                                                          part, kvlds, red, redf))
-                return;
+            if ((int)blockIdx.x < p.KVH) {
+                bool aok;
+                if constexpr (WT == SH_DTYPE_W8A8)
+                    aok = attn_stage<KVT, HD, true>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf);
+                else
+                    aok = attn_stage_fast<KVT, HD>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf);
+                if (!aok) return;
+            }
             stamp();
             // wo + residual
             io = StageIO{};
