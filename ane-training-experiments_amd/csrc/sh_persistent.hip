@@ -57,6 +57,7 @@ constexpr int kXs = 4096;          // staged input vector
 constexpr int kScores = 4096;      // attention scores: group * max_seq
 constexpr int kMaxGroup = 2;       // q heads per kv head
 constexpr int kMaxRes = 32;        // residual rows a workgroup owns in a residual stage
+constexpr int kMaxPer = 256;       // rows a workgroup owns in a GEMV stage with hand-over output
 constexpr int kKvStage = 96 * 1024; // LDS bytes for one kv head's cached K and V rows
 
 struct LayerPtrs {
@@ -541,7 +542,7 @@ template <int LPR, int CPL, int WT, int U, bool NORM>
 __device__ __forceinline__ bool gemv_stage(const PParams &p, const StageOwn o, const void *__restrict__ W,
                            const float *__restrict__ wscale, int rows, int cols,
                            int epi, const StageIO &io, float *xs, uint32_t *xq, double *red,
-                           int *okw, float &best_v, int &best_i) {
+                           int *okw, float *ostage, float &best_v, int &best_i) {
     constexpr int G = 64 / LPR;
     constexpr int EPC = chunk_elems<WT>();
     constexpr bool Q8 = WT == SH_DTYPE_W8A8;
@@ -662,14 +663,13 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const StageOwn o, c
                 if (sub == 0 && (grp & 1) == 0 && row < r1) {
                     // infer.go:324-326 (float64 exp; float expf for the fp16/bf16 models)
                     const float s = Q8 ? a / (1.0f + (float)exp(-(double)a)) : a / (1.0f + expf(-a));
-                    ll_put(io.out_ll + (size_t)rank * io.out_stride + ((row - r0) >> 1), s * h3, io.e_out);
+                    ostage[(row - r0) >> 1] = s * h3;
                 }
             } else if (sub == 0 && row < r1) {
-                uint64_t *out = io.out_ll + (size_t)rank * io.out_stride + (row - r0);
                 if (epi == E_STORE) {
-                    ll_put(out, a, io.e_out);
+                    ostage[row - r0] = a;
                 } else if (epi == E_RESID) {
-                    ll_put(out, xs[cols + row - r0] + p.alpha * a, io.e_out);
+                    ostage[row - r0] = xs[cols + row - r0] + p.alpha * a;
                 } else {  // E_CLS
                     p.logits[row] = a;
                     if (a > best_v) {
@@ -679,6 +679,15 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const StageOwn o, c
                 }
             }
         }
+    }
+    // The block's outputs leave in one store instruction per 64 words: a hand-over line
+    // written by one wave instruction becomes visible as a whole, about a microsecond
+    // sooner than the same line written word by word from several waves.
+    if (epi != E_CLS) {
+        lds_barrier();
+        const int nout = epi == E_GATE ? (r1 - r0) >> 1 : r1 - r0;
+        uint64_t *out = io.out_ll + (size_t)rank * io.out_stride;
+        for (int i = threadIdx.x; i < nout; i += kPB) ll_put(out + i, ostage[i], io.e_out);
     }
     // no closing barrier: the next stage's poll starts with one before it writes LDS
     return ok;
@@ -1006,13 +1015,15 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
 //    scaled by 1/sum at the end (p.v/sum instead of (p/sum).v);
 //  - three workgroup barriers after the cache append, none at the end (the next stage's poll
 //    starts with one).
-template <int KVT, int HD>
+template <int KVT, int HD, int GROUP>
 __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
                                                 float *sc, float *part, uint8_t *kvlds, float *redf) {
     using S = KvStage<KVT, HD>;
     constexpr int hd = HD, ngr = kPB / HD;
     constexpr int LPK = S::RB / 16, EPC = 16 / S::EB, PPW = 64 / LPK;
-    const int group = p.H / p.KVH, tid = threadIdx.x;
+    constexpr int group = GROUP;   // q heads per kv head, known at compile time so the loops
+                                   // below carry no per-row branches
+    const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int ms = p.max_seq;
     const LayerPtrs &Lp = p.layers[l];
@@ -1032,7 +1043,7 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
     }
     QkvMap qm{p.ll_qkv, qs, (size_t)g * group * hd, p.qdim + (size_t)g * hd,
               p.qdim + p.kvdim + (size_t)g * hd, group * hd, hd, e};
-    if (!ll_wait_batch<(kMaxGroup + 2) * 256 / kPB>(group * hd + 2 * hd, p, qm)) return false;
+    if (!ll_wait_batch<(GROUP + 2) * 256 / kPB>(group * hd + 2 * hd, p, qm)) return false;
     if (p.qk_norm) {
         // per-head RMSNorm: wave w < group normalises q head w, wave `group` normalises k
         if (wave <= group) {
@@ -1068,17 +1079,17 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
     lds_barrier();
     // scores (infer.go:280-288) and each wave's maximum
     const int sl = lane % LPK, rin = lane / LPK;
-    float qr[kMaxGroup][EPC];
+    float qr[GROUP][EPC];
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; h++)
+    for (int h = 0; h < GROUP; h++)
 #pragma unroll
         for (int q = 0; q < EPC; q++) qr[h][q] = h < group ? qs[h * hd + sl * EPC + q] : 0.f;
-    float mx[kMaxGroup];
+    float mx[GROUP];
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; h++) mx[h] = -INFINITY;
+    for (int h = 0; h < GROUP; h++) mx[h] = -INFINITY;
     auto score_row = [&](const float (&kf)[EPC], int t, bool valid) {
 #pragma unroll
-        for (int h = 0; h < kMaxGroup; h++) {
+        for (int h = 0; h < GROUP; h++) {
             if (h >= group) continue;
             float d = 0.f;
 #pragma unroll
@@ -1123,23 +1134,23 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
         }
     }
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; h++) {
+    for (int h = 0; h < GROUP; h++) {
         const float m = wmax<64>(mx[h]);
-        if (lane == 0 && h < group) redf[wave * kMaxGroup + h] = m;
+        if (lane == 0 && h < group) redf[wave * GROUP + h] = m;
     }
     lds_barrier();
     // softmax (infer.go:328-345) on every wave: unnormalised exp terms and their sums
-    float gmx[kMaxGroup], sum[kMaxGroup];
+    float gmx[GROUP], sum[GROUP];
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; h++) {
+    for (int h = 0; h < GROUP; h++) {
         gmx[h] = -INFINITY;
         sum[h] = 0.f;
         if (h < group)
-            for (int w = 0; w < kPW; w++) gmx[h] = fmaxf(gmx[h], redf[w * kMaxGroup + h]);
+            for (int w = 0; w < kPW; w++) gmx[h] = fmaxf(gmx[h], redf[w * GROUP + h]);
     }
     for (int t = tid; t <= pos; t += kPB) {
 #pragma unroll
-        for (int h = 0; h < kMaxGroup; h++) {
+        for (int h = 0; h < GROUP; h++) {
             if (h >= group) continue;
             const float ev = expf(sc[h * ms + t] - gmx[h]);
             sc[h * ms + t] = ev;
@@ -1147,38 +1158,49 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
         }
     }
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; h++) {
+    for (int h = 0; h < GROUP; h++) {
         const float sw = wsum<64>(sum[h]);
-        if (lane == 0 && h < group) redf[(kPW + wave) * kMaxGroup + h] = sw;
+        if (lane == 0 && h < group) redf[(kPW + wave) * GROUP + h] = sw;
     }
     lds_barrier();
-    // P.V (infer.go:290-297): thread (position group tg, dim vi), partials through LDS
+    // P.V (infer.go:290-297): thread (position group tg, dim vi), partials through LDS; the
+    // LDS rows are read four at a time (clamped indices, zero weights past the end), so the
+    // reads of a batch are in flight together
     const int vi = tid % hd, tg = tid / hd;
-    float acc[kMaxGroup];
+    float acc[GROUP];
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; h++) acc[h] = 0.f;
-#pragma unroll 4
-    for (int t = tg; t <= tl; t += ngr) {
-        const float vv = kv_get<KVT>(vst + (size_t)t * S::RB, vi);
+    for (int h = 0; h < GROUP; h++) acc[h] = 0.f;
+    for (int t = tg; t <= tl; t += 4 * ngr) {
+        float vv[4], pw[GROUP][4];
 #pragma unroll
-        for (int h = 0; h < kMaxGroup; h++)
-            if (h < group) acc[h] = fmaf(sc[h * ms + t], vv, acc[h]);
+        for (int u = 0; u < 4; u++) {
+            const int tt = t + u * ngr;
+            const int tc = tt <= tl ? tt : tl;
+            vv[u] = kv_get<KVT>(vst + (size_t)tc * S::RB, vi);
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) {
+                const float w = sc[h * ms + tc];
+                pw[h][u] = tt <= tl ? w : 0.f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) acc[h] = fmaf(pw[h][u], vv[u], acc[h]);
     }
     for (int t = tl + 1 + ((tg - (tl + 1) % ngr + ngr) % ngr); t <= pos; t += ngr) {
         const float vc = kv_ld<KVT>(p.vcache, lbase + (size_t)(t < pos ? t : tl) * p.kvdim + vi);
         const float vv = t == pos ? vs[vi] : vc;
 #pragma unroll
-        for (int h = 0; h < kMaxGroup; h++)
-            if (h < group) acc[h] = fmaf(sc[h * ms + t], vv, acc[h]);
+        for (int h = 0; h < GROUP; h++) acc[h] = fmaf(sc[h * ms + t], vv, acc[h]);
     }
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; h++)
-        if (h < group) part[(h * ngr + tg) * hd + vi] = acc[h];
+    for (int h = 0; h < GROUP; h++) part[(h * ngr + tg) * hd + vi] = acc[h];
     lds_barrier();
     for (int k = tid; k < group * hd; k += kPB) {
         const int h = k / hd, ii = k % hd;
         float tot = 0.f, o = 0.f;
-        for (int w = 0; w < kPW; w++) tot += redf[(kPW + w) * kMaxGroup + h];
+        for (int w = 0; w < kPW; w++) tot += redf[(kPW + w) * GROUP + h];
         for (int r = 0; r < ngr; r++) o += part[(h * ngr + r) * hd + ii];
         ll_put(p.ll_att + (size_t)(g * group + h) * hd + ii, o / tot, e);
     }
@@ -1195,6 +1217,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t kvlds[kKvStage];
     __shared__ double red[kPW];
     __shared__ int okw[kPW];
+    __shared__ float ostage[kMaxPer];   // a GEMV stage's output block, before its stores
     __shared__ float redf[2 * kPW * kMaxGroup];
     __shared__ ArgmaxPartial cand[kPW];
     __shared__ int next_tok;
@@ -1234,7 +1257,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.out_stride = p.ostride[0];
             io.e_in = e - 1;
             io.e_out = e;
-            if (!gemv_stage<LD, CD, WT, 2, true>(p, p.own[0], Lp.wqkv, Lp.s_qkv, p.qkv_rows, p.D, E_STORE, io, xs, xq, red, okw, bv, bi))
+            if (!gemv_stage<LD, CD, WT, 2, true>(p, p.own[0], Lp.wqkv, Lp.s_qkv, p.qkv_rows, p.D, E_STORE, io, xs, xq, red, okw, ostage, bv, bi))
                 return;
             stamp();
             // attention
@@ -1242,8 +1265,10 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 bool aok;
                 if constexpr (WT == SH_DTYPE_W8A8)
                     aok = attn_stage<KVT, HD, true>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf);
+                else if (p.H == p.KVH)
+                    aok = attn_stage_fast<KVT, HD, 1>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf);
                 else
-                    aok = attn_stage_fast<KVT, HD>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf);
+                    aok = attn_stage_fast<KVT, HD, 2>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf);
                 if (!aok) return;
             }
             stamp();
@@ -1260,7 +1285,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.e_in = e;
             io.e_res = e - 1;
             io.e_out = e;
-            if (!gemv_stage<LQ, CQ, WT, 2, false>(p, p.own[1], Lp.wo, Lp.s_o, p.D, p.qdim, E_RESID, io, xs, xq, red, okw, bv, bi))
+            if (!gemv_stage<LQ, CQ, WT, 2, false>(p, p.own[1], Lp.wo, Lp.s_o, p.D, p.qdim, E_RESID, io, xs, xq, red, okw, ostage, bv, bi))
                 return;
             stamp();
             // w1/w3 + silu gate
@@ -1274,7 +1299,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.out_stride = p.ostride[2];
             io.e_in = e;
             io.e_out = e;
-            if (!gemv_stage<LD, CD, WT, 2, true>(p, p.own[2], Lp.w13, Lp.s_13, 2 * p.F, p.D, E_GATE, io, xs, xq, red, okw, bv, bi))
+            if (!gemv_stage<LD, CD, WT, 2, true>(p, p.own[2], Lp.w13, Lp.s_13, 2 * p.F, p.D, E_GATE, io, xs, xq, red, okw, ostage, bv, bi))
                 return;
             stamp();
             // w2 + residual
@@ -1292,7 +1317,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.e_in = e;
             io.e_res = e;
             io.e_out = e;
-            if (!gemv_stage<LF, CF, WT, 2, false>(p, p.own[3], Lp.w2, Lp.s_2, p.D, p.F, E_RESID, io, xs, xq, red, okw, bv, bi))
+            if (!gemv_stage<LF, CF, WT, 2, false>(p, p.own[3], Lp.w2, Lp.s_2, p.D, p.F, E_RESID, io, xs, xq, red, okw, ostage, bv, bi))
                 return;
             stamp();
         }
@@ -1305,7 +1330,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
         io.in_magic = p.omagic[3];
         io.gain = p.rms_final;
         io.e_in = base + (uint32_t)L;
-        if (!gemv_stage<LD, CD, WT, 4, true>(p, p.own[4], p.cls, p.s_cls, p.V, p.D, E_CLS, io, xs, xq, red, okw, bv, bi)) return;
+        if (!gemv_stage<LD, CD, WT, 4, true>(p, p.own[4], p.cls, p.s_cls, p.V, p.D, E_CLS, io, xs, xq, red, okw, ostage, bv, bi)) return;
         stamp();
         // this workgroup's (max, first index)
         {
@@ -1490,6 +1515,7 @@ hipError_t persistent_plan(sh_model *m, std::string *why) {
     m->p_own[3] = StageOwn{0, n_w2, per_w2};
     m->p_own[4] = StageOwn{0, grid, cdiv(c.vocab, grid)};
     if (per_wo > kMaxRes || per_w2 > kMaxRes) return hipErrorInvalidConfiguration;
+    if (per_qkv > kMaxPer || per13 > kMaxPer) return hipErrorInvalidConfiguration;
     m->p_ostride[0] = per_qkv;   // a multiple of 16: qkv stays dense for the attention stage
     m->p_ostride[1] = up(per_wo, 16);
     m->p_ostride[2] = up(per13 / 2, 16);
