@@ -229,32 +229,6 @@ __device__ __forceinline__ bool aborted(const PParams &p) {
     return __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
-// Spin until *src carries epoch e; false on timeout or abort (then *err is set). Kept out
-// of line: it only runs when a value is not there yet, and one copy keeps the kernel small
-// enough for the instruction cache.
-__device__ __noinline__ bool ll_spin(const uint64_t *src, uint32_t e, uint64_t *v, int *err,
-                                     long long limit) {
-    const long long t0 = wall_clock64();
-    while (true) {
-        __builtin_amdgcn_s_sleep(1);
-        const uint64_t w = ll_get(src);
-        if ((uint32_t)(w >> 32) == e) {
-            *v = w;
-            return true;
-        }
-        if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return false;
-        if (wall_clock64() - t0 > limit) {
-            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return false;
-        }
-    }
-}
-
-__device__ __forceinline__ bool ll_wait_word(const uint64_t *src, uint32_t e, uint64_t &v, const PParams &p) {
-    if ((uint32_t)(v >> 32) == e) return true;
-    return ll_spin(src, e, &v, p.err, p.spin_limit);
-}
-
 // Block-wide wait: once every word j < n (located by map.src(j)) carries epoch map.ep(j),
 // its value is in *map.dst(j). Starts with a workgroup barrier, after the first requests
 // are issued: the LDS a stage writes is free once every wave has passed it. Each thread requests all of its K words at once and, while any is
@@ -529,6 +503,7 @@ struct StageIO {
     int res_per, res_stride;    // residual vector layout
     uint32_t in_magic, res_magic;   // ceil(2^31 / per) of the two layouts
     int out_stride;             // words between consecutive workgroups' output blocks
+    float *logits;              // E_CLS: logits output, or NULL when not read back
 };
 
 // One GEMV stage over W [rows, cols]. The workgroup owns the row block of its rank in the
@@ -671,7 +646,7 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const StageOwn o, c
                 } else if (epi == E_RESID) {
                     ostage[row - r0] = xs[cols + row - r0] + p.alpha * a;
                 } else {  // E_CLS
-                    p.logits[row] = a;
+                    if (io.logits) io.logits[row] = a;
                     if (a > best_v) {
                         best_v = a;
                         best_i = row;
@@ -1329,6 +1304,9 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
         io.in_stride = p.ostride[3];
         io.in_magic = p.omagic[3];
         io.gain = p.rms_final;
+        // only the launch's last forward leaves its logits: the host reads them after a
+        // one-forward launch, and stores queued ahead of the argmax poll delay it
+        io.logits = f == p.n_forwards - 1 ? p.logits : nullptr;
         io.e_in = base + (uint32_t)L;
         if (!gemv_stage<LD, CD, WT, 4, true>(p, p.own[4], p.cls, p.s_cls, p.V, p.D, E_CLS, io, xs, xq, red, okw, ostage, bv, bi)) return;
         stamp();
@@ -1356,16 +1334,30 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             const int n = gridDim.x;
             const uint64_t *pv = p.ll_pv + (size_t)(f & 1) * n * kArgSlot;
             const uint64_t *pi = p.ll_pi + (size_t)(f & 1) * n * kArgSlot;
-            for (int k = threadIdx.x; k < n; k += kPB) {
-                const size_t o = (size_t)k * kArgSlot;
+            // one partial per thread (n <= kPB); its value and index words polled together
+            if ((int)threadIdx.x < n) {
+                const size_t o = (size_t)threadIdx.x * kArgSlot;
                 uint64_t a = ll_get(pv + o), b = ll_get(pi + o);
-                ok = ok && ll_wait_word(pv + o, ec, a, p) && ll_wait_word(pi + o, ec, b, p);
-                const float cv = __uint_as_float((uint32_t)a);
-                const int ci = (int)(uint32_t)b;
-                if (better(cv, ci, v, idx)) {
-                    v = cv;
-                    idx = ci;
+                long long t0 = 0;
+                while ((uint32_t)(a >> 32) != ec || (uint32_t)(b >> 32) != ec) {
+                    const long long now = wall_clock64();
+                    if (!t0) {
+                        t0 = now;
+                    } else if (now - t0 > p.spin_limit) {
+                        __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        ok = false;
+                        break;
+                    }
+                    if (aborted(p)) {
+                        ok = false;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                    if ((uint32_t)(a >> 32) != ec) a = ll_get(pv + o);
+                    if ((uint32_t)(b >> 32) != ec) b = ll_get(pi + o);
                 }
+                v = __uint_as_float((uint32_t)a);
+                idx = (int)(uint32_t)b;
             }
             if (!block_and(ok)) return;
             wargmax(v, idx);
