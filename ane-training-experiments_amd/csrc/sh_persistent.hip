@@ -1016,6 +1016,17 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
         rc = p.rope_cos[pos * half + rpi];
         rs = p.rope_sin[pos * half + rpi];
     }
+    // QK-norm gains of this wave's head (wave w < group: q head w, wave group: k)
+    constexpr int GPL = (HD + 63) / 64;
+    float gq[GPL];
+#pragma unroll
+    for (int q = 0; q < GPL; q++) gq[q] = 0.f;
+    if (p.qk_norm && wave <= group) {
+        const float *gn = wave < group ? Lp.q_norm : Lp.k_norm;
+#pragma unroll
+        for (int q = 0; q < GPL; q++)
+            if (lane + 64 * q < hd) gq[q] = gn[lane + 64 * q];
+    }
     QkvMap qm{p.ll_qkv, qs, (size_t)g * group * hd, p.qdim + (size_t)g * hd,
               p.qdim + p.kvdim + (size_t)g * hd, group * hd, hd, e};
     if (!ll_wait_batch<(GROUP + 2) * 256 / kPB>(group * hd + 2 * hd, p, qm)) return false;
@@ -1023,12 +1034,13 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
         // per-head RMSNorm: wave w < group normalises q head w, wave `group` normalises k
         if (wave <= group) {
             float *v = qs + (wave < group ? wave : group) * hd;
-            const float *gn = wave < group ? Lp.q_norm : Lp.k_norm;
             float ss = 0.f;
             for (int i = lane; i < hd; i += 64) ss += v[i] * v[i];
             ss = wsum<64>(ss);
             const float rr = rsqrtf(ss / (float)hd + (float)p.qk_eps);
-            for (int i = lane; i < hd; i += 64) v[i] = v[i] * rr * gn[i];
+#pragma unroll
+            for (int q = 0; q < GPL; q++)
+                if (lane + 64 * q < hd) v[lane + 64 * q] = v[lane + 64 * q] * rr * gq[q];
         }
         lds_barrier();
     }
@@ -1093,19 +1105,28 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
         float kpos[EPC];
 #pragma unroll
         for (int q = 0; q < EPC; q++) kpos[q] = ks[sl * EPC + q];
+        // four row blocks per trip, their cache reads in flight together
         const SH_GLOBAL uint8_t *kc = (const SH_GLOBAL uint8_t *)p.kcache;
-        for (int t0 = tl + 1 + wave * PPW; t0 <= pos; t0 += kPW * PPW) {
-            const int t = t0 + rin;
-            const bool valid = t <= pos;
-            const int tr = valid && t < pos ? t : tl;   // a row in the cache (row pos is not read)
-            const u32x4 kv4 = ((const SH_GLOBAL u32x4 *)(kc + (lbase + (size_t)tr * p.kvdim) * S::EB))[sl];
-            float kf[EPC];
-            kv_unpack16<KVT>(kv4, kf);
-            if (t == pos) {
+        for (int tb = tl + 1 + wave * PPW; tb <= pos; tb += 4 * kPW * PPW) {
+            u32x4 kv4[4];
 #pragma unroll
-                for (int q = 0; q < EPC; q++) kf[q] = kpos[q];
+            for (int u = 0; u < 4; u++) {
+                const int t = tb + u * kPW * PPW + rin;
+                const int tr = t < pos ? t : tl;   // a row in the cache (row pos is not read)
+                kv4[u] = ((const SH_GLOBAL u32x4 *)(kc + (lbase + (size_t)tr * p.kvdim) * S::EB))[sl];
             }
-            score_row(kf, t, valid);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (tb + u * kPW * PPW > pos) continue;   // uniform over the wave
+                const int t = tb + u * kPW * PPW + rin;
+                float kf[EPC];
+                kv_unpack16<KVT>(kv4[u], kf);
+                if (t == pos) {
+#pragma unroll
+                    for (int q = 0; q < EPC; q++) kf[q] = kpos[q];
+                }
+                score_row(kf, t, t <= pos);
+            }
         }
     }
 #pragma unroll
@@ -1163,11 +1184,22 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
 #pragma unroll
             for (int h = 0; h < GROUP; h++) acc[h] = fmaf(pw[h][u], vv[u], acc[h]);
     }
-    for (int t = tl + 1 + ((tg - (tl + 1) % ngr + ngr) % ngr); t <= pos; t += ngr) {
-        const float vc = kv_ld<KVT>(p.vcache, lbase + (size_t)(t < pos ? t : tl) * p.kvdim + vi);
-        const float vv = t == pos ? vs[vi] : vc;
+    // rows beyond the LDS stage: cache reads eight at a time (row pos from the staged v)
+    for (int t = tl + 1 + ((tg - (tl + 1) % ngr + ngr) % ngr); t <= pos; t += 8 * ngr) {
+        float vc[8];
 #pragma unroll
-        for (int h = 0; h < GROUP; h++) acc[h] = fmaf(sc[h * ms + t], vv, acc[h]);
+        for (int u = 0; u < 8; u++) {
+            const int tt = t + u * ngr;
+            vc[u] = kv_ld<KVT>(p.vcache, lbase + (size_t)(tt < pos ? tt : tl) * p.kvdim + vi);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int tt = t + u * ngr;
+            if (tt > pos) continue;
+            const float vv = tt == pos ? vs[vi] : vc[u];
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) acc[h] = fmaf(sc[h * ms + tt], vv, acc[h]);
+        }
     }
 #pragma unroll
     for (int h = 0; h < GROUP; h++) part[(h * ngr + tg) * hd + vi] = acc[h];
@@ -1260,7 +1292,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.e_in = e;
             io.e_res = e - 1;
             io.e_out = e;
-            if (!gemv_stage<LQ, CQ, WT, 2, false>(p, p.own[1], Lp.wo, Lp.s_o, p.D, p.qdim, E_RESID, io, xs, xq, red, okw, ostage, bv, bi))
+            if (!gemv_stage<LQ, CQ, WT, 1, false>(p, p.own[1], Lp.wo, Lp.s_o, p.D, p.qdim, E_RESID, io, xs, xq, red, okw, ostage, bv, bi))
                 return;
             stamp();
             // w1/w3 + silu gate
@@ -1292,7 +1324,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.e_in = e;
             io.e_res = e;
             io.e_out = e;
-            if (!gemv_stage<LF, CF, WT, 2, false>(p, p.own[3], Lp.w2, Lp.s_2, p.D, p.F, E_RESID, io, xs, xq, red, okw, ostage, bv, bi))
+            if (!gemv_stage<LF, CF, WT, 1, false>(p, p.own[3], Lp.w2, Lp.s_2, p.D, p.F, E_RESID, io, xs, xq, red, okw, ostage, bv, bi))
                 return;
             stamp();
         }
@@ -1448,12 +1480,11 @@ bool persistent_supported(const sh_model *m) {
 // partial per thread), shrunk until the w13 stage's row blocks cover every workgroup: that
 // stage then depends on every workgroup having finished the previous forward's classifier,
 // which keeps the single-buffered ll_x vector safe while prompt forwards run without an
-// argmax exchange. The other stages use as few workgroups as fill one pass of their waves
-// (blocks of 16 rows or a multiple, so every producer's hand-over words fill whole 128-byte
-// lines), placed so that a workgroup's previous stage ends before the stage's input is
-// ready and its weight loads overlap the wait: attention on workgroups [0, KVH), qkv right
-// after them, wo after qkv. w2 spreads over every workgroup (a few rows each), so the weight
-// tiles it loads after the w13 stage stay small.
+// argmax exchange. qkv takes blocks of 16 rows over as many workgroups as that needs, after
+// the attention workgroups [0, KVH) when it fits; wo takes about 24 KB of weights per
+// workgroup, placed after qkv when it fits (its workgroups then idle through qkv and
+// attention, so their weight tiles arrive before att does); w2 spreads over every workgroup
+// (a few rows each), so the weight tiles it loads after the w13 stage stay small.
 hipError_t persistent_plan(sh_model *m, std::string *why) {
     const sh_config &c = m->cfg;
     PersistentKernel k = pick_persistent(m->dtype, c.kv_dtype, c.dim, m->qdim, c.hidden, c.head_dim);
@@ -1470,8 +1501,6 @@ hipError_t persistent_plan(sh_model *m, std::string *why) {
     if (e != hipSuccess) return e;
     *why += "; " + std::to_string(per_cu) + " workgroup(s) of " + std::to_string(kPB) + " per CU";
     if (per_cu < 1) return hipErrorInvalidConfiguration;
-    int ld = 0, lq = 0, lf = 0;
-    shape_lanes(m->dtype, c.dim, m->qdim, c.hidden, &ld, &lq, &lf);
     auto cdiv = [](int a, int b) { return (a + b - 1) / b; };
     auto up = [&](int a, int b) { return cdiv(a, b) * b; };
     const int rows13 = 2 * c.hidden;
@@ -1481,20 +1510,19 @@ hipError_t persistent_plan(sh_model *m, std::string *why) {
     while (grid > 1 && cdiv(rows13, per13_for(grid)) != grid) grid--;
     if (grid < c.n_kv_heads) return hipErrorInvalidConfiguration;
     const int KVH = c.n_kv_heads;
-    // rows per workgroup: one pass of kPW waves of G = 64/L rows, rounded to 16
-    auto one_pass = [&](int lanes) { return up(kPW * (64 / lanes), 16); };
-    auto fit = [&](int rows, int per) {
-        while (cdiv(rows, per) > grid) per += 16;
-        return per;
-    };
+    const int wbytes = m->dtype == SH_DTYPE_W8A8 ? 1 : 2;   // bytes per weight
     // w2 on every workgroup (its weights are the second largest; a few rows each keeps the
     // weight tiles loaded after the w13 stage small)
     const int per_w2 = cdiv(c.dim, grid);
     const int n_w2 = cdiv(c.dim, per_w2);
-    int per_qkv = fit(m->qkv_rows, one_pass(ld));
-    while (KVH + cdiv(m->qkv_rows, per_qkv) > grid && per_qkv < m->qkv_rows) per_qkv += 16;
+    // qkv: blocks of 16 rows (whole lines of the dense qkv vector) spread over the grid,
+    // after the attention workgroups when they fit
+    const int per_qkv = up(cdiv(m->qkv_rows, grid), 16);
     const int n_qkv = cdiv(m->qkv_rows, per_qkv);
-    const int per_wo = fit(c.dim, std::min(one_pass(lq), kMaxRes));
+    // wo: about 24 KB of weights per workgroup (its workgroups are idle through qkv and
+    // attention, so their tiles arrive long before att), at most kMaxRes rows
+    int per_wo = std::max(1, std::min(kMaxRes, 24576 / (m->qdim * wbytes)));
+    if (cdiv(c.dim, per_wo) > grid) per_wo = cdiv(c.dim, grid);
     const int n_wo = cdiv(c.dim, per_wo);
     const int off_qkv = KVH + n_qkv <= grid ? KVH : 0;
     int off_wo = off_qkv + n_qkv;
