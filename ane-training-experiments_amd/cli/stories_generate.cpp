@@ -20,6 +20,9 @@
 //   -detokenize 5,6,7               print text= for these ids with -tokenizer, touch no GPU
 //   -copy-calibrate BYTES           with -bench-steps: first time the library's plain copy
 //                                   kernel over BYTES and report its GB/s
+//   -batch B                        with -bench-steps: B synthetic prompts of -prompt-len ids
+//                                   (-prompt-seed) decoded together (sh_batch_greedy_decode);
+//                                   the JSON object reports the prefill and per-step times
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -287,6 +290,7 @@ int main(int argc, char **argv) {
     fl.def("inspect", "false", true);
     fl.def("detokenize", "");
     fl.def("copy-calibrate", "0");
+    fl.def("batch", "0");
     fl.parse(argc, argv);
 
     if (!fl.s("detokenize").empty()) {
@@ -353,6 +357,12 @@ int main(int argc, char **argv) {
     else if (!fl.s("kv").empty()) fatalf("unknown -kv %s", fl.s("kv"));
     if (source == "synthetic")
         synth_weights(c, (uint64_t)fl.i("synthetic-seed"), (float)fl.f("synthetic-std"), w);
+    const int batch = (int)fl.i("batch");
+    if (batch > 0) {
+        if (fl.i("bench-steps") <= 0 || fl.i("prompt-len") <= 0)
+            fatalf("%s", "-batch needs -bench-steps and -prompt-len");
+        c.max_batch = batch;
+    }
 
     std::vector<int32_t> prompt;
     if (fl.i("prompt-len") > 0) {
@@ -377,6 +387,53 @@ int main(int argc, char **argv) {
     const float temperature = (float)fl.f("temperature");
 
     const int steps = (int)fl.i("bench-steps");
+    if (steps > 0 && batch > 0) {
+        // Batched greedy decode timing: B prompts of prompt-len ids, max-new steps each.
+        const int plen = (int)fl.i("prompt-len");
+        std::vector<int32_t> prompts((size_t)batch * plen);
+        if (sh_synth_tokens(prompts.data(), prompts.size(), (uint64_t)fl.i("prompt-seed"), c.vocab))
+            fatalf("prompts: %s", lib_error());
+        const int stride = plen + (max_new > 0 ? max_new : 64);
+        std::vector<int32_t> out((size_t)batch * stride), n_out(batch);
+        auto run = [&]() {
+            if (sh_batch_greedy_decode(m, prompts.data(), batch, plen, max_new, out.data(), n_out.data()))
+                fatalf("batch decode: %s", lib_error());
+        };
+        for (int i = 0; i < fl.i("bench-warmup"); i++) run();
+        std::vector<double> dec_ms, pre_ms;
+        std::vector<long long> fwd, gen;
+        double bytes = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < steps; i++) {
+            run();
+            sh_timing t{};
+            if (sh_stats(m, &t)) fatalf("stats: %s", lib_error());
+            dec_ms.push_back(t.gpu_ms);
+            pre_ms.push_back(t.prefill_ms);
+            fwd.push_back(t.forwards);
+            gen.push_back(t.tokens_out);
+            bytes = t.bytes_per_forward_mean;
+        }
+        const double wall = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        std::string js = "{\"batch\": " + std::to_string(batch) + ", \"prompt_len\": " + std::to_string(plen) +
+                         ", \"steps\": " + std::to_string(steps) + ", \"wall_s\": " + std::to_string(wall) +
+                         ", \"decode_ms\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(dec_ms[i]);
+        js += "], \"prefill_ms\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(pre_ms[i]);
+        js += "], \"decode_steps\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(fwd[i]);
+        js += "], \"tokens_out\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(gen[i]);
+        char b[64];
+        snprintf(b, sizeof b, "%.1f", bytes);
+        js += "], \"bytes_per_step_mean\": " + std::string(b) + ", \"tokens_row0\": [" +
+              join_ints(std::vector<int32_t>(out.begin(), out.begin() + n_out[0])) + "]}";
+        printf("%s\n", js.c_str());
+        fflush(stdout);
+        sh_model_destroy(m);
+        return 0;
+    }
     if (steps > 0) {
         // Greedy decode timing for bench harnesses: W untimed runs, then K timed ones.
         double copy_ms = 0, copy_gbs = 0;

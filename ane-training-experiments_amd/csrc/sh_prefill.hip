@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "sh_internal.hpp"
+#include "sh_wave.hpp"
 
 namespace sh {
 namespace {
@@ -651,6 +652,71 @@ __global__ __launch_bounds__(kT) void k_gemm_skinny(GemmArgs g, float *partial, 
     }
 }
 
+// Skinny GEMM with the activation rows shared through LDS: workgroup (x, y) owns 64 output
+// columns (16 per wave) and the K range [y*kc, (y+1)*kc), walked in 256-wide chunks. Each
+// chunk's A rows (hi and lo planes, 32 rows, rows padded to 264 elements so the MFMA reads of
+// 16 rows fall in distinct banks) are copied into LDS once for the four waves; each wave
+// loads its 16 weight rows for the chunk (eight 16-byte loads per lane, in flight while A is
+// staged) and issues four MFMAs per 32-wide k-step. The wave tiles go through LDS to the same
+// epilogue / partial layout as k_gemm_skinny. Needs kc % 256 == 0 and N % 64 == 0.
+constexpr int kSkA = 264;   // padded row of a staged A chunk (elements)
+template <int DT>
+__global__ __launch_bounds__(kT) void k_gemm_skinny64(GemmArgs g, float *partial, int kc) {
+    __shared__ __attribute__((aligned(16))) uint16_t as[2][32][kSkA];
+    __shared__ float part[4][32][17];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nw0 = blockIdx.x * 64 + wave * 16;
+    const int lr = lane & 15, lk = (lane >> 4) * 8;
+    const size_t lo = (size_t)g.M * g.K;
+    const int kbeg = blockIdx.y * kc;
+    const uint16_t *bp = g.B + (size_t)(nw0 + lr) * g.K + lk;
+    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+    f32x4 c0 = f32x4{0.f, 0.f, 0.f, 0.f}, c1 = c0;
+    for (int k0 = kbeg; k0 < kbeg + kc; k0 += 256) {
+        u32x4 b[8];
+#pragma unroll
+        for (int st = 0; st < 8; st++) b[st] = *(const u32x4 *)(bp + k0 + 32 * st);
+        // the previous chunk's A reads are done (LDS only; the weight loads stay in flight)
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        for (int i = threadIdx.x; i < 2 * 32 * 32; i += kT) {
+            const int pl = i >> 10, r = (i >> 5) & 31, u = i & 31;
+            const u32x4 v = r < g.M ? *(const u32x4 *)(g.A + pl * lo + (size_t)r * g.K + k0 + u * 8) : zero;
+            *(u32x4 *)&as[pl][r][u * 8] = v;
+        }
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            const int kk = 32 * st + lk;
+            const u32x4 x0 = *(const u32x4 *)&as[0][lr][kk], x0l = *(const u32x4 *)&as[1][lr][kk];
+            const u32x4 x1 = *(const u32x4 *)&as[0][16 + lr][kk], x1l = *(const u32x4 *)&as[1][16 + lr][kk];
+            c0 = mfma16<DT>(x0, b[st], c0);
+            c0 = mfma16<DT>(x0l, b[st], c0);
+            c1 = mfma16<DT>(x1, b[st], c1);
+            c1 = mfma16<DT>(x1l, b[st], c1);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        part[wave][4 * (lane >> 4) + r][lr] = c0[r];
+        part[wave][16 + 4 * (lane >> 4) + r][lr] = c1[r];
+    }
+    __syncthreads();
+    const int m = threadIdx.x >> 3, nn = (threadIdx.x & 7) * 2;   // columns nn, nn+1 of row m
+    if (m >= g.M) return;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int n = blockIdx.x * 64 + t * 16 + nn;
+        const float v0 = part[t][m][nn], v1 = part[t][m][nn + 1];
+        if (gridDim.y == 1 && !g.partial_only) {
+            skinny_epilogue(g, m, n, v0, v1);
+        } else {
+            float *dst = partial + ((size_t)blockIdx.y * g.M + m) * g.N + n;
+            dst[0] = v0;
+            dst[1] = v1;
+        }
+    }
+}
+
 // Adds the K-range partials of the skinny GEMM in range order, then the epilogue.
 __global__ __launch_bounds__(kT) void k_gemm_skinny_reduce(GemmArgs g, const float *partial, int ranges) {
     const int idx = blockIdx.x * kT + threadIdx.x;
@@ -846,6 +912,246 @@ __global__ __launch_bounds__(kT) void k_attn_batch_partial(
         for (int r = 0; r < nks; r++) a += pv[(size_t)r * gw + k];
         pacc[(pbase + (size_t)(k / hd) * nch) * hd + k % hd] = a;
     }
+}
+
+constexpr int kAT = 512;                  // threads of the streaming batched attention
+constexpr int kChunkBytes = 16 * 1024;    // bytes of K rows per streamed chunk (as many of V)
+
+// Batched decode attention that streams the cache (flash decoding): workgroup (split, kv
+// head g, sequence b) walks its share of the chunks of C = 16 KB / row-bytes keys. Chunk
+// i+1's K and V rows are copied into LDS (global_load_lds, four instructions per wave per
+// chunk) while chunk i is computed, so the cache is read at the rate the CU can take it.
+// Per chunk: lane-sliced scores of the group's q heads (RB/16 lanes per row, the slice dot
+// products added by DPP), the running maximum and the rescaled sum of exp terms (online
+// softmax), and P.V by thread (dim, key group) with the chunk's weights from LDS. One split
+// writes the output row directly (a GEMM operand, hi/lo planes); several splits leave
+// (m, l, acc) partials for k_attn_split_combine. Sequence b attends to 0..pos[b].
+template <int KVT, int HD, int GROUP>
+__global__ __launch_bounds__(kAT) void k_attn_batch_stream(
+    const float *q, const void *kc, const void *vc, size_t kv_seq_stride, const int32_t *pos,
+    int H, int KVH, float scale, int nsplit, int nch_buf, int dt, size_t plane, uint16_t *att,
+    float *pm, float *pl, float *pacc) {
+    constexpr int EB = KVT == SH_KV_F32 ? 4 : 2;
+    constexpr int RB = HD * EB;                        // bytes per cache row
+    constexpr int C = kChunkBytes / RB;                // keys per chunk
+    constexpr int LPK = RB / 16, EPC = 16 / EB, PPW = 64 / LPK;
+    constexpr int NW = kAT / 64;
+    constexpr int NKG = kAT / HD;                      // key groups of the P.V threads
+    constexpr int SB = C / (NW * PPW);                 // row blocks per wave per chunk
+    static_assert(C % (NW * PPW) == 0 && C % (4 * NKG) == 0, "chunk tiling");
+    __shared__ __attribute__((aligned(16))) uint8_t kbuf[2][kChunkBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t vbuf[2][kChunkBytes];
+    __shared__ float sc[GROUP][C];
+    __shared__ float redm[NW][GROUP], redl[NW][GROUP];
+    __shared__ float part[NKG][GROUP][HD];
+    const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int P = pos[b] + 1;
+    const int nchunks = (P + C - 1) / C;
+    const int cps = (nchunks + nsplit - 1) / nsplit;
+    const int c0 = split * cps, c1 = min(nchunks, c0 + cps);
+    if (c0 >= c1) return;
+    const int qdim = H * HD, kvdim = KVH * HD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t sbase = (size_t)b * kv_seq_stride + (size_t)g * HD;
+    const int sl = lane % LPK, rin = lane / LPK;
+    float qr[GROUP][EPC];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++)
+#pragma unroll
+        for (int e = 0; e < EPC; e++) qr[h][e] = q[(size_t)b * qdim + (size_t)(g * GROUP + h) * HD + sl * EPC + e];
+    auto dma = [&](int ci, int buf) {
+        const int t0 = ci * C, n = min(C, P - t0);
+        const size_t off = (sbase + (size_t)t0 * kvdim) * EB;
+        rows_to_lds((const uint8_t *)kc + off, (size_t)kvdim * EB, n, C, RB, kbuf[buf]);
+        rows_to_lds((const uint8_t *)vc + off, (size_t)kvdim * EB, n, C, RB, vbuf[buf]);
+    };
+    float m_run[GROUP], L[GROUP], acc[GROUP];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) {
+        m_run[h] = -INFINITY;
+        L[h] = 0.f;
+        acc[h] = 0.f;
+    }
+    const int d = tid % HD, kg = tid / HD;
+    dma(c0, 0);
+    for (int ci = c0; ci < c1; ci++) {
+        const int buf = (ci - c0) & 1;
+        if (ci + 1 < c1) {
+            dma(ci + 1, buf ^ 1);
+            __asm__ __volatile__("s_waitcnt vmcnt(4)" ::: "memory");   // chunk ci has landed
+        } else {
+            __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const int n = min(C, P - ci * C);
+        // scores and each wave's maximum
+        float mx[GROUP];
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) mx[h] = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+            const int t = (wave + j * NW) * PPW + rin;
+            const u32x4 k4 = ((const u32x4 *)(kbuf[buf] + (size_t)t * RB))[sl];
+            float kf[EPC];
+            if constexpr (KVT == SH_KV_F32) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) kf[e] = __uint_as_float(k4[e]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int dtk = KVT == SH_KV_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16;
+                    kf[2 * e] = bits_to_f(k4[e] & 0xffffu, dtk);
+                    kf[2 * e + 1] = bits_to_f(k4[e] >> 16, dtk);
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) {
+                float dd = 0.f;
+#pragma unroll
+                for (int e = 0; e < EPC; e++) dd = fmaf(qr[h][e], kf[e], dd);
+                dd = wsum<LPK>(dd) * scale;
+                if (t < n) {
+                    if (sl == 0) sc[h][t] = dd;
+                    mx[h] = fmaxf(mx[h], dd);
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            const float m = wmax<64>(mx[h]);
+            if (lane == 0) redm[wave][h] = m;
+        }
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        float mnew[GROUP], alpha[GROUP], ls[GROUP];
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            float m = m_run[h];
+#pragma unroll
+            for (int w = 0; w < NW; w++) m = fmaxf(m, redm[w][h]);
+            alpha[h] = expf(m_run[h] - m);   // 0 before the first chunk
+            mnew[h] = m;
+            ls[h] = 0.f;
+        }
+        // exp terms (zero past the chunk's keys, so P.V reads whole chunks)
+        for (int i = tid; i < GROUP * C; i += kAT) {
+            const int h = i / C, t = i % C;
+#pragma unroll
+            for (int hh = 0; hh < GROUP; hh++) {
+                if (hh != h) continue;
+                const float p = t < n ? expf(sc[hh][t] - mnew[hh]) : 0.f;
+                sc[hh][t] = p;
+                ls[hh] += p;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            const float s = wsum<64>(ls[h]);
+            if (lane == 0) redl[wave][h] = s;
+        }
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            float s = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) s += redl[w][h];
+            L[h] = L[h] * alpha[h] + s;
+            m_run[h] = mnew[h];
+            acc[h] *= alpha[h];
+        }
+        // P.V: keys kg, kg + NKG, ... of the chunk, four per batch
+#pragma unroll
+        for (int j = 0; j < C / NKG; j += 4) {
+            float vv[4], pw[GROUP][4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int t = kg + (j + u) * NKG;
+                vv[u] = kv_elem<KVT>(vbuf[buf] + (size_t)t * RB, d);
+#pragma unroll
+                for (int h = 0; h < GROUP; h++) pw[h][u] = sc[h][t];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int h = 0; h < GROUP; h++) acc[h] = fmaf(pw[h][u], vv[u], acc[h]);
+        }
+        // the chunk's buffers and sc are rewritten next
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) part[kg][h][d] = acc[h];
+    __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    for (int i = tid; i < GROUP * HD; i += kAT) {
+        const int h = i / HD, dd = i % HD;
+        float o = 0.f;
+#pragma unroll
+        for (int r = 0; r < NKG; r++) o += part[r][h][dd];
+        float lh = 0.f, mh = 0.f;
+#pragma unroll
+        for (int hh = 0; hh < GROUP; hh++)
+            if (hh == h) {
+                lh = L[hh];
+                mh = m_run[hh];
+            }
+        if (nsplit == 1) {
+            store_op(att, (size_t)b * qdim + (size_t)(g * GROUP + h) * HD + dd, plane, o / lh, dt);
+        } else {
+            const size_t pb = ((size_t)b * H + (size_t)g * GROUP + h) * nch_buf + split;
+            pacc[pb * HD + dd] = o;
+            if (dd == 0) {
+                pm[pb] = mh;
+                pl[pb] = lh;
+            }
+        }
+    }
+}
+
+// Merges the split partials of k_attn_batch_stream for (q head h, sequence b): the splits
+// holding keys are recomputed from pos[b] as the kernel did; out = sum_s e^(m_s - M) acc_s /
+// sum_s e^(m_s - M) l_s, written as a GEMM operand row.
+__global__ __launch_bounds__(256) void k_attn_split_combine(const float *pm, const float *pl,
+                                                            const float *pacc, const int32_t *pos,
+                                                            int H, int hd, int nsplit, int chunk,
+                                                            int nch_buf, int B, int dt, uint16_t *att) {
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int P = pos[b] + 1;
+    const int nchunks = (P + chunk - 1) / chunk;
+    const int cps = (nchunks + nsplit - 1) / nsplit;
+    const int ns = (nchunks + cps - 1) / cps;
+    const size_t pb = ((size_t)b * H + h) * nch_buf;
+    float M = -INFINITY;
+    for (int c = 0; c < ns; c++) M = fmaxf(M, pm[pb + c]);
+    float Lsum = 0.f;
+    for (int c = 0; c < ns; c++) Lsum += expf(pm[pb + c] - M) * pl[pb + c];
+    const float invL = 1.0f / Lsum;
+    const size_t plane = (size_t)B * H * hd;
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+        float a = 0.f;
+        for (int c = 0; c < ns; c++) a += expf(pm[pb + c] - M) * pacc[(pb + c) * hd + i];
+        store_op(att, (size_t)b * H * hd + (size_t)h * hd + i, plane, a * invL, dt);
+    }
+}
+
+// The streaming kernel for (kv type, head dim, group), or null when it has no instance.
+typedef void (*AttnStreamKernel)(const float *, const void *, const void *, size_t, const int32_t *, int, int,
+                                 float, int, int, int, size_t, uint16_t *, float *, float *, float *);
+template <int KVT>
+AttnStreamKernel pick_attn_stream_kv(int hd, int group) {
+    switch (hd * 8 + group) {
+    case 32 * 8 + 1: return &k_attn_batch_stream<KVT, 32, 1>;
+    case 32 * 8 + 2: return &k_attn_batch_stream<KVT, 32, 2>;
+    case 32 * 8 + 4: return &k_attn_batch_stream<KVT, 32, 4>;
+    case 64 * 8 + 1: return &k_attn_batch_stream<KVT, 64, 1>;
+    case 64 * 8 + 2: return &k_attn_batch_stream<KVT, 64, 2>;
+    case 64 * 8 + 4: return &k_attn_batch_stream<KVT, 64, 4>;
+    case 128 * 8 + 1: return &k_attn_batch_stream<KVT, 128, 1>;
+    case 128 * 8 + 2: return &k_attn_batch_stream<KVT, 128, 2>;
+    default: return nullptr;
+    }
+}
+AttnStreamKernel pick_attn_stream(int kv, int hd, int group) {
+    if (kv == SH_KV_F32) return pick_attn_stream_kv<SH_KV_F32>(hd, group);
+    if (kv == SH_KV_F16) return pick_attn_stream_kv<SH_KV_F16>(hd, group);
+    return pick_attn_stream_kv<SH_KV_BF16>(hd, group);
 }
 
 // Merges the chunk partials of (q head h, sequence b): out = sum_c e^(m_c - M) acc_c /
@@ -1263,9 +1569,15 @@ hipError_t skinny(const GemmArgs &g, int dt, float *partial, size_t part_cap, hi
     const int kc = skinny_kc(g.N, g.K), ranges = g.K / kc;
     if ((ranges > 1 || g.partial_only) && (size_t)ranges * g.M * g.N > part_cap)
         return hipErrorInvalidValue;   // the partial buffer must hold every K range
-    const dim3 grid(g.N / 16, ranges);
-    if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL(k_gemm_skinny<SH_DTYPE_BF16>, grid, dim3(kT), 0, s, g, partial, kc);
-    else hipLaunchKernelGGL(k_gemm_skinny<SH_DTYPE_F16>, grid, dim3(kT), 0, s, g, partial, kc);
+    if (g.N % 64 == 0 && kc % 256 == 0) {
+        const dim3 grid(g.N / 64, ranges);
+        if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL(k_gemm_skinny64<SH_DTYPE_BF16>, grid, dim3(kT), 0, s, g, partial, kc);
+        else hipLaunchKernelGGL(k_gemm_skinny64<SH_DTYPE_F16>, grid, dim3(kT), 0, s, g, partial, kc);
+    } else {
+        const dim3 grid(g.N / 16, ranges);
+        if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL(k_gemm_skinny<SH_DTYPE_BF16>, grid, dim3(kT), 0, s, g, partial, kc);
+        else hipLaunchKernelGGL(k_gemm_skinny<SH_DTYPE_F16>, grid, dim3(kT), 0, s, g, partial, kc);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || ranges == 1 || g.partial_only) return e;
     const int pairs = g.M * (g.N / 2);
@@ -1382,7 +1694,14 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const float scale = (float)(1.0 / sqrt((double)c.head_dim));
     const int nch = m->bt_nch;
-    const int chunk = attn_chunk(c.head_dim * (c.kv_dtype == SH_KV_F32 ? 4 : 2));
+    const int kvb = c.kv_dtype == SH_KV_F32 ? 4 : 2;
+    const int chunk = attn_chunk(c.head_dim * kvb);
+    // streaming attention: enough splits of each sequence's keys to give about one
+    // workgroup per CU, within the partial buffers (nch slots per head and sequence)
+    const AttnStreamKernel astream = pick_attn_stream(c.kv_dtype, c.head_dim, c.n_heads / c.n_kv_heads);
+    const int schunk = kChunkBytes / (c.head_dim * kvb);
+    int nsplit = std::max(1, (512 + B * c.n_kv_heads - 1) / (B * c.n_kv_heads));
+    nsplit = std::min({nsplit, nch, (c.max_seq + schunk - 1) / schunk});
     auto ranges = [](int N, int K) { return K / skinny_kc(N, K); };
     for (int l = 0; l < c.n_layers; l++) {
         const LayerDev &L = m->layers[l];
@@ -1400,10 +1719,25 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         else
             hipLaunchKernelGGL(k_row_qkv<SH_KV_BF16>, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part, rq, B, qa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // attention over each sequence's cache, split over the keys, then merged
+        // attention over each sequence's cache, streamed by workgroup (split, kv head,
+        // sequence); shapes without a streaming instance split over fixed chunks and merge
         const void *kc = kv_layer_base(m, m->kcache, l), *vc = kv_layer_base(m, m->vcache, l);
+        if (astream) {
+            hipLaunchKernelGGL(astream, dim3(nsplit, c.n_kv_heads, B), dim3(kAT), 0, s, m->bt_q, kc, vc,
+                               kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, scale, nsplit, nch,
+                               dt, (size_t)B * c.n_heads * c.head_dim, m->bt_att, m->bt_pm, m->bt_pl,
+                               m->bt_pacc);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            if (nsplit > 1) {
+                hipLaunchKernelGGL(k_attn_split_combine, dim3(c.n_heads, B), dim3(256), 0, s, m->bt_pm,
+                                   m->bt_pl, m->bt_pacc, m->bt_pos, c.n_heads, c.head_dim, nsplit,
+                                   schunk, nch, B, dt, m->bt_att);
+                if ((e = hipGetLastError()) != hipSuccess) return e;
+            }
+        }
         const dim3 grid(nch, c.n_kv_heads, B);
-        if (c.kv_dtype == SH_KV_F32)
+        if (astream) {
+        } else if (c.kv_dtype == SH_KV_F32)
             hipLaunchKernelGGL(k_attn_batch_partial<SH_KV_F32>, grid, dim3(kT), 0, s, m->bt_q, kc, vc,
                                kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, c.head_dim,
                                scale, nch, m->bt_pm, m->bt_pl, m->bt_pacc);
@@ -1415,11 +1749,13 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
             hipLaunchKernelGGL(k_attn_batch_partial<SH_KV_BF16>, grid, dim3(kT), 0, s, m->bt_q, kc, vc,
                                kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, c.head_dim,
                                scale, nch, m->bt_pm, m->bt_pl, m->bt_pacc);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(k_attn_batch_combine, dim3(c.n_heads, B), dim3(256), 0, s, m->bt_pm,
-                           m->bt_pl, m->bt_pacc, m->bt_pos, c.n_heads, c.head_dim, nch, chunk, B,
-                           dt, m->bt_att);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (!astream) {
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            hipLaunchKernelGGL(k_attn_batch_combine, dim3(c.n_heads, B), dim3(256), 0, s, m->bt_pm,
+                               m->bt_pl, m->bt_pacc, m->bt_pos, c.n_heads, c.head_dim, nch, chunk, B,
+                               dt, m->bt_att);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
         // Wo; row kernel: x2 = x + alpha * (att . Wo^T), then rmsnorm(x2) with rms_ffn
         g = GemmArgs{};
         g.A = m->bt_att; g.B = (const uint16_t *)L.wo; g.M = B; g.N = D; g.K = m->qdim;

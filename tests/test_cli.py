@@ -145,11 +145,16 @@ def test_detokenize(tmp_path):
     assert p.returncode == 1 and "unexpected EOF at token 100" in p.stderr
 
 
-def test_flag_errors():
+def test_flag_errors(tmp_path):
     p = run("-no-such-flag", "1", check=False)
     assert p.returncode == 1 and "flag provided but not defined: -no-such-flag" in p.stderr
     p = run("-prompt-ids", "1,x", "-inspect", check=False)
     assert p.returncode == 1
+    cfg = gqa_file_config()
+    path = tmp_path / "m.bin"
+    write_llama2_bin(path, cfg, sh.synth_weights(cfg, seed=1, std=0.05))
+    p = run("-model", path, "-batch", "2", check=False)
+    assert p.returncode == 1 and "-batch needs -bench-steps and -prompt-len" in p.stderr
 
 
 # ---- GPU ---------------------------------------------------------------------------------
@@ -202,6 +207,25 @@ def test_cli_bench_mode_stories110m():
     ref = oracle.Decoder(oracle.config_from(cfg), w.rounded(sh.SH_DTYPE_F16), threads=16)
     want, _, _ = ref.greedy_decode(sh.synth_tokens(16, 1, cfg.vocab), 128)
     assert r["tokens"] == want.tolist()
+
+
+@pytest.mark.gpu
+def test_cli_batch_bench_mode(tmp_path):
+    """-batch: sequences decoded together; row 0's stream equals the oracle's greedy decode of
+    its prompt."""
+    cfg = gqa_file_config()
+    w = sh.synth_weights(cfg, seed=331, std=0.08)
+    path = tmp_path / "m.bin"
+    write_llama2_bin(path, cfg, w)
+    p = run("-model", path, "-batch", "3", "-prompt-len", "5", "-prompt-seed", "7", "-max-new", "20",
+            "-bench-steps", "2", "-bench-warmup", "1", "-seq", "64")
+    r = json.loads(p.stdout)
+    assert r["batch"] == 3 and r["steps"] == 2 and len(r["decode_ms"]) == 2
+    assert r["decode_steps"] == [20, 20] and all(v > 0 for v in r["prefill_ms"])
+    ref = oracle.Decoder(oracle.config_from(cfg), w.rounded(sh.SH_DTYPE_F16), threads=4)
+    prompts = sh.synth_tokens(3 * 5, 7, cfg.vocab).reshape(3, 5)
+    want, _, _ = ref.greedy_decode(prompts[0], 20)
+    assert r["tokens_row0"] == want.tolist()
 
 
 @pytest.mark.gpu
