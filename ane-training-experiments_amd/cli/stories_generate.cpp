@@ -23,6 +23,9 @@
 //   -batch B                        with -bench-steps: B synthetic prompts of -prompt-len ids
 //                                   (-prompt-seed) decoded together (sh_batch_greedy_decode);
 //                                   the JSON object reports the prefill and per-step times
+//   -eval-logits                    with -bench-steps: time sh_prefill_logits (the storiesane
+//                                   EvalLogits forward) over the -prompt-len synthetic ids and
+//                                   report device times and the forward's FLOPs
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -291,6 +294,7 @@ int main(int argc, char **argv) {
     fl.def("detokenize", "");
     fl.def("copy-calibrate", "0");
     fl.def("batch", "0");
+    fl.def("eval-logits", "false", true);
     fl.parse(argc, argv);
 
     if (!fl.s("detokenize").empty()) {
@@ -363,6 +367,12 @@ int main(int argc, char **argv) {
             fatalf("%s", "-batch needs -bench-steps and -prompt-len");
         c.max_batch = batch;
     }
+    if (fl.b("eval-logits")) {
+        if (fl.i("bench-steps") <= 0 || fl.i("prompt-len") <= 0)
+            fatalf("%s", "-eval-logits needs -bench-steps and -prompt-len");
+        // the storiesane engine scales each residual branch by 1/sqrt(2 L) (residual.go:9)
+        if (shape == "stories110m") c.residual_scale = (float)(1.0 / sqrt(2.0 * c.n_layers));
+    }
 
     std::vector<int32_t> prompt;
     if (fl.i("prompt-len") > 0) {
@@ -429,6 +439,47 @@ int main(int argc, char **argv) {
         snprintf(b, sizeof b, "%.1f", bytes);
         js += "], \"bytes_per_step_mean\": " + std::string(b) + ", \"tokens_row0\": [" +
               join_ints(std::vector<int32_t>(out.begin(), out.begin() + n_out[0])) + "]}";
+        printf("%s\n", js.c_str());
+        fflush(stdout);
+        sh_model_destroy(m);
+        return 0;
+    }
+    if (steps > 0 && fl.b("eval-logits")) {
+        // Full-sequence forward timing: W untimed, then K timed EvalLogits calls over the
+        // prompt. FLOPs: 2 per weight per row for every projection and the classifier, and
+        // the attention's QK^T and P.V over the full S x S square per head (the count the
+        // reference's channel-first forward performs).
+        const int S = (int)prompt.size();
+        if (S > c.max_seq) fatalf("%s", "-prompt-len exceeds -seq (" + std::to_string(c.max_seq) + ")");
+        std::vector<uint16_t> ids(prompt.begin(), prompt.end());
+        std::vector<float> logits((size_t)c.vocab * S);
+        auto run = [&]() {
+            if (sh_prefill_logits(m, ids.data(), S, logits.data()))
+                fatalf("eval logits: %s", lib_error());
+        };
+        for (int i = 0; i < fl.i("bench-warmup"); i++) run();
+        std::vector<double> gpu_ms;
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < steps; i++) {
+            run();
+            sh_timing t{};
+            if (sh_stats(m, &t)) fatalf("stats: %s", lib_error());
+            gpu_ms.push_back(t.gpu_ms);
+        }
+        const double wall = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        const double qdim = (double)c.n_heads * c.head_dim, kvdim = (double)c.n_kv_heads * c.head_dim;
+        const double per_layer = (double)c.dim * (qdim + 2 * kvdim) + qdim * c.dim + 3.0 * c.dim * c.hidden;
+        const double params = per_layer * c.n_layers + (double)c.vocab * c.dim;
+        const double flops = 2.0 * S * params + 4.0 * c.n_layers * c.n_heads * (double)S * S * c.head_dim;
+        double sum = 0;
+        for (float v : logits) sum += v;
+        char b[160];
+        snprintf(b, sizeof b, "], \"flops\": %.6e, \"logits_sum\": %.6e}", flops, sum);
+        std::string js = "{\"seq\": " + std::to_string(S) + ", \"steps\": " + std::to_string(steps) +
+                         ", \"warmup\": " + std::to_string(fl.i("bench-warmup")) +
+                         ", \"wall_s\": " + std::to_string(wall) + ", \"gpu_ms\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(gpu_ms[i]);
+        js += b;
         printf("%s\n", js.c_str());
         fflush(stdout);
         sh_model_destroy(m);

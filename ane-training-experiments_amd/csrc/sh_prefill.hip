@@ -373,144 +373,232 @@ __global__ __launch_bounds__(1024) void k_row_resid_norm(const float *partial, i
         store_op(xn, (size_t)m * D + i, (size_t)M * D, row[i] * scale * gain[i], dt);
 }
 
-// Tiled causal attention for the full-sequence forward (forward_common.go:5-33, flash
-// style): workgroup = 64 query rows x one head. Row t is position rowpos[t] of its
-// sequence, whose rows are the rowpos[t] rows before it, so its keys are
-// j in [t - rowpos[t], t]; only the key blocks some row of the block can see are visited.
-// Per 64-key block: K and V rows staged in LDS (rows padded by 4 floats), scores as 4 x 4
-// register tiles (thread = 4 queries x 4 keys), then an online softmax (running max m and
-// sum l per row, earlier terms rescaled by exp(m_old - m_new)) and P.V with one thread per
-// (query, quarter of the head dims). fp32 throughout; masked keys contribute exactly 0.
-template <int HD>
-__global__ __launch_bounds__(kT) void k_attn_prefill_tiled(const float *qf, const float *kf,
-                                                           const float *vf, int S,
-                                                           const int32_t *rowpos, int H,
-                                                           int KVH, float scale, int dt,
-                                                           uint16_t *att, size_t plane) {
-    constexpr int B = 64, RSF = HD + 4;          // block rows, LDS row stride (floats)
-    constexpr int DQ = HD / 4;                   // dims per thread in P.V
-    __shared__ __attribute__((aligned(16))) float qs[B * RSF];
-    __shared__ __attribute__((aligned(16))) float ks[B * RSF];
-    __shared__ __attribute__((aligned(16))) float vs[B * RSF];
-    __shared__ float ps[B * (B + 4)];
-    const int tid = threadIdx.x;
-    const int q0 = blockIdx.x * B, h = blockIdx.y;
+// Two 16-bit operand values packed as the MFMA expects (element 2i in the low half).
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return (uint32_t)f_to_bits(a, DT) | ((uint32_t)f_to_bits(b, DT) << 16);
+}
+// hi = round(v), lo = round(v - hi) for 8 consecutive values, as two MFMA operands.
+template <int DT>
+__device__ __forceinline__ void split8(const float *f, u32x4 &hi, u32x4 &lo) {
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) r[e] = f[e] - bits_to_f(f_to_bits(f[e], DT), DT);
+    hi = u32x4{pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3]), pack2<DT>(f[4], f[5]), pack2<DT>(f[6], f[7])};
+    lo = u32x4{pack2<DT>(r[0], r[1]), pack2<DT>(r[2], r[3]), pack2<DT>(r[4], r[5]), pack2<DT>(r[6], r[7])};
+}
+// max / sum over the four lanes l, l^16, l^32, l^48 (the four row groups of a wave)
+__device__ __forceinline__ float max_rows(float v) {
+    SwapPair s = swap16(__float_as_uint(v));
+    v = fmaxf(__uint_as_float(s.a), __uint_as_float(s.b));
+    s = swap32(__float_as_uint(v));
+    return fmaxf(__uint_as_float(s.a), __uint_as_float(s.b));
+}
+__device__ __forceinline__ float sum_rows(float v) {
+    SwapPair s = swap16(__float_as_uint(v));
+    v = __uint_as_float(s.a) + __uint_as_float(s.b);
+    s = swap32(__float_as_uint(v));
+    return __uint_as_float(s.a) + __uint_as_float(s.b);
+}
+
+// Causal attention of the full-sequence forward on MFMA (forward_common.go:5-33, flash
+// style). Workgroup = 64 query rows x one head, wave w owning rows q0+16w .. +15; row t is
+// position rowpos[t] of its sequence, whose keys are j in [t - rowpos[t], t], and only the
+// 64-key blocks some row of the workgroup can see are visited.
+//
+// Per key block the workgroup stages K ([key][dim]) and V transposed ([dim][key]) in LDS as
+// 16-bit operand planes. Each wave computes S^T = K . Q^T with v_mfma_f32_16x16x32 (A = K
+// rows, B = its 16 queries), so a lane holds one query (lane % 16) and 16 of the block's
+// keys: key 16j + 4(lane/16) + r of tile j, register r. An online softmax per query (running
+// max uniform over the query's four lanes, per-lane partial sums) gives P, which is already
+// in the B-operand layout of O^T = V^T . P^T (lane = query, k slots = the lane's 8 keys of a
+// 32-key step), and V^T rows are read in the same key order. O^T accumulates per lane as
+// query lane % 16, dims 16i + 4(lane/16) + r, so the softmax rescale is per lane.
+//
+// Operands are hi/lo pairs of the model's 16-bit type: Q and P always; K and V too (LO) when
+// they are fp32 rather than values already rounded to this type by the KV cache. The products
+// hi.hi + lo.hi + hi.lo keep about 16 (bf16) or 22 (fp16) significant bits, fp32 accumulate.
+template <int DT, int HD, bool LO>
+__global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const float *kf,
+                                                          const float *vf, int S,
+                                                          const int32_t *rowpos, int H, int KVH,
+                                                          float scale, uint16_t *att, size_t plane) {
+    constexpr int BQ = 64, BK = 64, NP = LO ? 2 : 1;
+    constexpr int KRS = HD * 2 + 16;              // LDS bytes per K row (16-byte pad)
+    constexpr int VRS = BK * 2 + 8;               // LDS bytes per V^T row (8-byte pad)
+    constexpr int KT = BK * HD / 8;               // K staging tasks: (key, 8 dims)
+    constexpr int VT = (BK / 4) * (HD / 4);       // V staging tasks: (4 keys, 4 dims)
+    constexpr int KPT = (KT + kT - 1) / kT, VPT = (VT + kT - 1) / kT;
+    constexpr int NS = HD / 32, NO = HD / 16;     // QK k-steps, O^T tiles
+    __shared__ __attribute__((aligned(16))) uint8_t ks[NP][BK * KRS];
+    __shared__ __attribute__((aligned(16))) uint8_t vts[NP][HD * VRS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g4 = lane >> 4, ql = lane & 15;
+    const int q0 = blockIdx.x * BQ, h = blockIdx.y;
     const int qdim = H * HD, kvdim = KVH * HD, kvh = h / (H / KVH);
-    // keys this block can see: from the first row's sequence start to its last row
     const int kstart = q0 - rowpos[q0];
-    const int qlast = min(q0 + B, S) - 1;
-    // stage the query block
-    for (int c = tid; c < B * (HD / 4); c += kT) {
-        const int r = c / (HD / 4), d = (c % (HD / 4)) * 4;
-        const int t = q0 + r;
-        *(f32x4 *)&qs[r * RSF + d] = t < S ? *(const f32x4 *)(qf + (size_t)t * qdim + h * HD + d)
-                                           : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    const int tq = tid >> 4, tk = tid & 15;      // score tile: queries 4tq.., keys 4tk..
-    const int pq = tid >> 2, pd = (tid & 3) * DQ; // softmax / P.V: query pq, dims pd..
-    const int t_own = q0 + pq;
-    float m_run = -INFINITY, l_run = 0.f;
-    float acc[DQ];
+    const int qlast = min(q0 + BQ, S) - 1;
+
+    // this lane's query and its Q operand planes (B operand: dims 32s + 8*g4 .. +7)
+    const int t = q0 + 16 * wave + ql;
+    const bool tok = t < S;
+    const int jlo = tok ? t - rowpos[t] : 0x7fffffff;
+    u32x4 qh[NS], qlo[NS];
 #pragma unroll
-    for (int d = 0; d < DQ; d++) acc[d] = 0.f;
-    int jlo[4];
+    for (int s = 0; s < NS; s++) {
+        float f[8];
+        if (tok) {
+            const f32x4 a = *(const f32x4 *)(qf + (size_t)t * qdim + h * HD + 32 * s + 8 * g4);
+            const f32x4 b = *(const f32x4 *)(qf + (size_t)t * qdim + h * HD + 32 * s + 8 * g4 + 4);
+            f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+        } else {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int t = q0 + 4 * tq + i;
-        jlo[i] = t < S ? t - rowpos[t] : 0x7fffffff;
-    }
-    for (int kb = kstart & ~(B - 1); kb <= qlast; kb += B) {
-        __syncthreads();   // previous block's P.V is done with ks/vs/ps
-        for (int c = tid; c < B * (HD / 4); c += kT) {
-            const int r = c / (HD / 4), d = (c % (HD / 4)) * 4;
-            const int j = kb + r;
-            const bool ok = j < S;
-            *(f32x4 *)&ks[r * RSF + d] = ok ? *(const f32x4 *)(kf + (size_t)j * kvdim + kvh * HD + d)
-                                            : f32x4{0.f, 0.f, 0.f, 0.f};
-            *(f32x4 *)&vs[r * RSF + d] = ok ? *(const f32x4 *)(vf + (size_t)j * kvdim + kvh * HD + d)
-                                            : f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int e = 0; e < 8; e++) f[e] = 0.f;
         }
-        __syncthreads();
-        float sc[4][4];
+        split8<DT>(f, qh[s], qlo[s]);
+    }
+    const int wlast = min(q0 + 16 * wave + 15, S - 1);   // the wave's last row
+
+    // staging registers for the next key block
+    f32x4 kst[KPT][2], vst[VPT][4];
+    auto gload = [&](int kb) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) sc[i][j] = 0.f;
-#pragma unroll 4
-        for (int d = 0; d < HD; d += 4) {
-            f32x4 qv[4], kv[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) qv[i] = *(const f32x4 *)&qs[(4 * tq + i) * RSF + d];
-#pragma unroll
-            for (int j = 0; j < 4; j++) kv[j] = *(const f32x4 *)&ks[(4 * tk + j) * RSF + d];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    sc[i][j] = fmaf(qv[i].x, kv[j].x, sc[i][j]);
-                    sc[i][j] = fmaf(qv[i].y, kv[j].y, sc[i][j]);
-                    sc[i][j] = fmaf(qv[i].z, kv[j].z, sc[i][j]);
-                    sc[i][j] = fmaf(qv[i].w, kv[j].w, sc[i][j]);
-                }
+        for (int u = 0; u < KPT; u++) {
+            const int c = tid + u * kT;
+            if (KT % kT != 0 && c >= KT) break;
+            const int r = c / (HD / 8), d = (c % (HD / 8)) * 8, j = kb + r;
+            const float *src = kf + (size_t)j * kvdim + kvh * HD + d;
+            kst[u][0] = j < S ? *(const f32x4 *)src : f32x4{0.f, 0.f, 0.f, 0.f};
+            kst[u][1] = j < S ? *(const f32x4 *)(src + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = q0 + 4 * tq + i;
+        for (int u = 0; u < VPT; u++) {
+            const int c = tid + u * kT;
+            if (VT % kT != 0 && c >= VT) break;
+            const int kq = c / (HD / 4), d = (c % (HD / 4)) * 4;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int jg = kb + 4 * tk + j;
-                const bool vis = jg >= jlo[i] && jg <= t;
-                ps[(4 * tq + i) * (B + 4) + 4 * tk + j] = vis ? sc[i][j] * scale : -INFINITY;
+            for (int i = 0; i < 4; i++) {
+                const int j = kb + 4 * kq + i;
+                vst[u][i] = j < S ? *(const f32x4 *)(vf + (size_t)j * kvdim + kvh * HD + d)
+                                  : f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int u = 0; u < KPT; u++) {
+            const int c = tid + u * kT;
+            if (KT % kT != 0 && c >= KT) break;
+            const int r = c / (HD / 8), d = (c % (HD / 8)) * 8;
+            const float f[8] = {kst[u][0].x, kst[u][0].y, kst[u][0].z, kst[u][0].w,
+                                kst[u][1].x, kst[u][1].y, kst[u][1].z, kst[u][1].w};
+            u32x4 hi, lo;
+            split8<DT>(f, hi, lo);
+            *(u32x4 *)&ks[0][r * KRS + d * 2] = hi;
+            if constexpr (LO) *(u32x4 *)&ks[NP - 1][r * KRS + d * 2] = lo;
+        }
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            const int c = tid + u * kT;
+            if (VT % kT != 0 && c >= VT) break;
+            const int kq = c / (HD / 4), d = (c % (HD / 4)) * 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {   // dim d + i: keys 4kq .. 4kq+3
+                const float a0 = vst[u][0][i], a1 = vst[u][1][i], a2 = vst[u][2][i], a3 = vst[u][3][i];
+                const uint32_t h01 = pack2<DT>(a0, a1), h23 = pack2<DT>(a2, a3);
+                *(uint2 *)&vts[0][(d + i) * VRS + 8 * kq] = uint2{h01, h23};
+                if constexpr (LO) {
+                    const float r0 = a0 - bits_to_f(f_to_bits(a0, DT), DT);
+                    const float r1 = a1 - bits_to_f(f_to_bits(a1, DT), DT);
+                    const float r2 = a2 - bits_to_f(f_to_bits(a2, DT), DT);
+                    const float r3 = a3 - bits_to_f(f_to_bits(a3, DT), DT);
+                    *(uint2 *)&vts[NP - 1][(d + i) * VRS + 8 * kq] =
+                        uint2{pack2<DT>(r0, r1), pack2<DT>(r2, r3)};
+                }
+            }
+        }
+    };
+
+    float m_run = -INFINITY, l_part = 0.f;
+    f32x4 o[NO];
+#pragma unroll
+    for (int i = 0; i < NO; i++) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int kb0 = kstart & ~(BK - 1);
+    gload(kb0);
+    for (int kb = kb0; kb <= qlast; kb += BK) {
+        __syncthreads();   // every wave is done reading the previous block
+        lstore();
         __syncthreads();
-        // online softmax for row pq: four threads share the row, 16 keys each
-        float *prow = ps + pq * (B + 4);
+        if (kb + BK <= qlast) gload(kb + BK);
+        if (q0 + 16 * wave >= S || wlast < kb) continue;   // no row of this wave sees the block
+        // S^T tiles: keys 16j + 4*g4 + r (register r) for query ql
+        f32x4 sc[BK / 16];
+#pragma unroll
+        for (int j = 0; j < BK / 16; j++) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                const int off = (16 * j + ql) * KRS + 64 * s + 16 * g4;
+                const u32x4 kh = *(const u32x4 *)&ks[0][off];
+                acc = mfma16<DT>(kh, qh[s], acc);
+                acc = mfma16<DT>(kh, qlo[s], acc);
+                if constexpr (LO) acc = mfma16<DT>(*(const u32x4 *)&ks[NP - 1][off], qh[s], acc);
+            }
+            sc[j] = acc;
+        }
         float mx = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 16; j++) mx = fmaxf(mx, prow[(tid & 3) * 16 + j]);
-        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-        const float m_new = fmaxf(m_run, mx);
-        float sum = 0.f;
-        if (m_new != -INFINITY) {
+        for (int j = 0; j < BK / 16; j++)
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const int jj = (tid & 3) * 16 + j;
-                const float sv = prow[jj];
-                const float e = sv == -INFINITY ? 0.f : expf(sv - m_new);
-                prow[jj] = e;
-                sum += e;
+            for (int r = 0; r < 4; r++) {
+                const int jg = kb + 16 * j + 4 * g4 + r;
+                const float v = (jg >= jlo && jg <= t) ? sc[j][r] * scale : -INFINITY;
+                sc[j][r] = v;
+                mx = fmaxf(mx, v);
             }
-        }
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
+        mx = max_rows(mx);
+        const float m_new = fmaxf(m_run, mx);
         const float rescale = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
-        l_run = l_run * rescale + sum;
         m_run = m_new;
+        l_part *= rescale;
 #pragma unroll
-        for (int d = 0; d < DQ; d++) acc[d] *= rescale;
-        __syncthreads();   // every row's probabilities are in ps
-        if (m_new != -INFINITY) {
-            for (int j = 0; j < B; j++) {
-                const float pj = prow[j];
-                const float *vr = &vs[j * RSF + pd];
+        for (int i = 0; i < NO; i++) o[i] *= rescale;
+        // P (unnormalised) as B operands of O^T = V^T . P^T, two 32-key steps
 #pragma unroll
-                for (int d = 0; d < DQ; d += 4) {
-                    const f32x4 v4 = *(const f32x4 *)(vr + d);
-                    acc[d] = fmaf(pj, v4.x, acc[d]);
-                    acc[d + 1] = fmaf(pj, v4.y, acc[d + 1]);
-                    acc[d + 2] = fmaf(pj, v4.z, acc[d + 2]);
-                    acc[d + 3] = fmaf(pj, v4.w, acc[d + 3]);
+        for (int s2 = 0; s2 < BK / 32; s2++) {
+            float p[8];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float a = sc[2 * s2][r], b = sc[2 * s2 + 1][r];
+                p[r] = a == -INFINITY ? 0.f : expf(a - m_new);
+                p[4 + r] = b == -INFINITY ? 0.f : expf(b - m_new);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) l_part += p[e];
+            u32x4 ph, pl;
+            split8<DT>(p, ph, pl);
+#pragma unroll
+            for (int i = 0; i < NO; i++) {
+                const int off = (16 * i + ql) * VRS + 64 * s2 + 8 * g4;
+                const uint2 a0 = *(const uint2 *)&vts[0][off], a1 = *(const uint2 *)&vts[0][off + 32];
+                const u32x4 vh = u32x4{a0.x, a0.y, a1.x, a1.y};
+                o[i] = mfma16<DT>(vh, ph, o[i]);
+                o[i] = mfma16<DT>(vh, pl, o[i]);
+                if constexpr (LO) {
+                    const uint2 b0 = *(const uint2 *)&vts[NP - 1][off], b1 = *(const uint2 *)&vts[NP - 1][off + 32];
+                    o[i] = mfma16<DT>(u32x4{b0.x, b0.y, b1.x, b1.y}, ph, o[i]);
                 }
             }
         }
     }
-    if (t_own >= S) return;
-    const float inv = 1.0f / l_run;
+    const float l_tot = sum_rows(l_part);
+    if (!tok) return;
+    const float inv = 1.0f / l_tot;
 #pragma unroll
-    for (int d = 0; d < DQ; d++)
-        store_op(att, (size_t)t_own * qdim + h * HD + pd + d, plane, acc[d] * inv, dt);
+    for (int i = 0; i < NO; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            store_op(att, (size_t)t * qdim + h * HD + 16 * i + 4 * g4 + r, plane, o[i][r] * inv, DT);
 }
 
 // Causal attention (forward_common.go:5-33): one wave per (query t, head h). Row t is
@@ -1485,6 +1573,42 @@ hipError_t launch_qk_rope(const sh_model *m, const LayerDev &L, int rows, const 
     return hipGetLastError();
 }
 
+// Causal attention of the S rows: the MFMA kernel for head dims 32 / 64 / 128, its K and V
+// carried as hi/lo planes unless fill_kv has already rounded them to the model's 16-bit type.
+hipError_t launch_attn_prefill(const sh_model *m, int S, int seg_max, bool fill_kv, float scale,
+                               hipStream_t s) {
+    const sh_config &c = m->cfg;
+    const int dt = m->dtype;
+    const size_t plane = (size_t)S * m->qdim;
+    const bool exact = fill_kv && ((c.kv_dtype == SH_KV_BF16 && dt == SH_DTYPE_BF16) ||
+                                   (c.kv_dtype == SH_KV_F16 && dt == SH_DTYPE_F16));
+    const dim3 grid((S + 63) / 64, c.n_heads);
+#define SH_ATT(DTV, HDV, LOV)                                                                   \
+    hipLaunchKernelGGL((k_attn_prefill_mfma<DTV, HDV, LOV>), grid, dim3(kT), 0, s, m->pf_q,     \
+                       m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale,        \
+                       m->pf_att, plane)
+#define SH_ATT_HD(DTV, LOV)                                                                     \
+    if (c.head_dim == 32) SH_ATT(DTV, 32, LOV);                                                  \
+    else if (c.head_dim == 64) SH_ATT(DTV, 64, LOV);                                             \
+    else SH_ATT(DTV, 128, LOV);
+    if (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) {
+        if (dt == SH_DTYPE_BF16) {
+            if (exact) { SH_ATT_HD(SH_DTYPE_BF16, false) } else { SH_ATT_HD(SH_DTYPE_BF16, true) }
+        } else {
+            if (exact) { SH_ATT_HD(SH_DTYPE_F16, false) } else { SH_ATT_HD(SH_DTYPE_F16, true) }
+        }
+    } else {
+        const int wpb = kT / 64;
+        hipLaunchKernelGGL(k_attn_prefill, dim3((S + wpb - 1) / wpb, c.n_heads), dim3(kT),
+                           sizeof(float) * wpb * seg_max, s, m->pf_q, m->pf_k, m->pf_v, S,
+                           seg_max, m->pf_rowpos, c.n_heads, c.n_kv_heads, c.head_dim, scale, dt,
+                           fill_kv ? 1 : 0, m->pf_att, plane);
+    }
+#undef SH_ATT_HD
+#undef SH_ATT
+    return hipGetLastError();
+}
+
 }  // namespace
 
 // Enqueues the forward of the S rows pf_tokens[0, S) (row t = position pf_rowpos[t] of
@@ -1514,25 +1638,7 @@ hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fi
         if ((e = launch_qk_rope(m, L, S, m->pf_qkv, m->pf_rowpos, m->pf_rowseq, m->pf_q,
                                 m->pf_k, m->pf_v, l, fill_kv, s)) != hipSuccess)
             return e;
-        {
-            const dim3 grid((S + 63) / 64, c.n_heads);
-            const size_t plane = (size_t)S * m->qdim;
-#define SH_ATT(HDV)                                                                            \
-    hipLaunchKernelGGL(k_attn_prefill_tiled<HDV>, grid, dim3(kT), 0, s, m->pf_q, m->pf_k,       \
-                       m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale, dt, m->pf_att, \
-                       plane)
-            if (c.head_dim == 32) SH_ATT(32);
-            else if (c.head_dim == 64) SH_ATT(64);
-            else if (c.head_dim == 128) SH_ATT(128);
-            else {
-                const int wpb = kT / 64;
-                hipLaunchKernelGGL(k_attn_prefill, dim3((S + wpb - 1) / wpb, c.n_heads), dim3(kT),
-                                   sizeof(float) * wpb * seg_max, s, m->pf_q, m->pf_k, m->pf_v, S,
-                                   seg_max, m->pf_rowpos, c.n_heads, c.n_kv_heads, c.head_dim,
-                                   scale, dt, fill_kv ? 1 : 0, m->pf_att, plane);
-            }
-#undef SH_ATT
-        }
+        if ((e = launch_attn_prefill(m, S, seg_max, fill_kv, scale, s)) != hipSuccess) return e;
         if ((e = hipGetLastError()) != hipSuccess) return e;
         g = GemmArgs{};
         g.A = m->pf_att; g.B = (const uint16_t *)L.wo; g.M = S; g.N = D; g.K = m->qdim;

@@ -155,6 +155,8 @@ def test_flag_errors(tmp_path):
     write_llama2_bin(path, cfg, sh.synth_weights(cfg, seed=1, std=0.05))
     p = run("-model", path, "-batch", "2", check=False)
     assert p.returncode == 1 and "-batch needs -bench-steps and -prompt-len" in p.stderr
+    p = run("-model", path, "-eval-logits", "-bench-steps", "2", check=False)
+    assert p.returncode == 1 and "-eval-logits needs -bench-steps and -prompt-len" in p.stderr
 
 
 # ---- GPU ---------------------------------------------------------------------------------
