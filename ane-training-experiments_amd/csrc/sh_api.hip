@@ -196,6 +196,49 @@ void parallel_ranges(size_t n, F fn) {
     for (auto &t : th) t.join();
 }
 
+// Shared set-up of the channel-first seams: checks, prefill scratch for seq rows, the rows'
+// positions 0..seq-1 of one sequence, and x_cf [dim, seq] copied into pf_cf.
+bool seam_begin(sh_model *m, const char *what, const float *x_cf, int32_t seq, void *out,
+                bool logits) {
+    if (!ready(m)) return false;
+    if (!x_cf || !out || seq <= 0 || seq > m->cfg.max_seq) {
+        set_error(std::string(what) + ": bad arguments");
+        return false;
+    }
+    std::string why;
+    if (!prefill_supported(m, &why)) {
+        set_error(std::string(what) + ": " + why);
+        return false;
+    }
+    (void)hipSetDevice(m->device);
+    if (!hip_ok(prefill_alloc(m, seq, logits), "prefill scratch")) return false;
+    std::vector<int32_t> rows(2 * (size_t)seq);
+    for (int t = 0; t < seq; t++) {
+        rows[t] = t;
+        rows[(size_t)seq + t] = 0;
+    }
+    const size_t xb = sizeof(float) * (size_t)m->cfg.dim * seq;
+    return hip_ok(hipMemcpyAsync(m->pf_rowpos, rows.data(), 4 * (size_t)seq, hipMemcpyHostToDevice, m->stream), "seam rows") &&
+           hip_ok(hipMemcpyAsync(m->pf_rowseq, rows.data() + seq, 4 * (size_t)seq, hipMemcpyHostToDevice, m->stream), "seam rows") &&
+           hip_ok(hipMemcpyAsync(m->pf_cf, x_cf, xb, hipMemcpyHostToDevice, m->stream), "seam input") &&
+           hip_ok(hipEventRecord(m->ev0, m->stream), "event");
+}
+
+// Copies `bytes` of device results to the host, waits, and records the device time.
+bool seam_end(sh_model *m, const void *dev, void *host, size_t bytes, int seq) {
+    if (!hip_ok(hipEventRecord(m->ev1, m->stream), "event") ||
+        !hip_ok(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, m->stream), "seam output") ||
+        !hip_ok(hipStreamSynchronize(m->stream), "seam sync"))
+        return false;
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, m->ev0, m->ev1);
+    m->last = sh_timing{};
+    m->last.gpu_ms = ms;
+    m->last.forwards = 1;
+    m->last.tokens_out = seq;
+    return true;
+}
+
 uint16_t host_bf16_bits(float x);
 
 }  // namespace
@@ -1207,6 +1250,137 @@ int sh_round_dtype(float *data, size_t n, int32_t dtype) {
         }
     });
     return 0;
+}
+
+int sh_layer_forward_cf(sh_model *m, int32_t layer, const float *x_cf, int32_t seq,
+                        float *out_cf) {
+    if (m && (layer < 0 || layer >= m->cfg.n_layers)) {
+        set_error("sh_layer_forward_cf: layer out of range");
+        return -1;
+    }
+    if (!seam_begin(m, "sh_layer_forward_cf", x_cf, seq, out_cf, false)) return -1;
+    if (!hip_ok(enqueue_layer_cf(m, layer, seq), "layer forward")) return -1;
+    return seam_end(m, m->pf_cf, out_cf, sizeof(float) * (size_t)m->cfg.dim * seq, seq) ? 0 : -1;
+}
+
+int sh_rms_final_cf(sh_model *m, const float *x_cf, int32_t seq, float *out_cf) {
+    if (!seam_begin(m, "sh_rms_final_cf", x_cf, seq, out_cf, false)) return -1;
+    if (!hip_ok(enqueue_rms_final_cf(m, seq), "final rmsnorm")) return -1;
+    return seam_end(m, m->pf_cf, out_cf, sizeof(float) * (size_t)m->cfg.dim * seq, seq) ? 0 : -1;
+}
+
+int sh_classifier_cf(sh_model *m, const float *xnorm_cf, int32_t seq, float *logits_cf) {
+    if (!seam_begin(m, "sh_classifier_cf", xnorm_cf, seq, logits_cf, true)) return -1;
+    if (!hip_ok(enqueue_classifier_cf(m, seq), "classifier")) return -1;
+    return seam_end(m, m->pf_logits, logits_cf, sizeof(float) * (size_t)m->cfg.vocab * seq, seq) ? 0 : -1;
+}
+
+int sh_matmul_vocab_seq(const float *embed, const float *x_cf, int32_t vocab, int32_t dim,
+                        int32_t seq, float *logits_cf) {
+    if (!embed || !x_cf || !logits_cf || vocab <= 0 || dim <= 0 || seq <= 0) {
+        set_error("sh_matmul_vocab_seq: bad arguments");
+        return -1;
+    }
+    if (dim % 32 || vocab % 64) {
+        set_error("sh_matmul_vocab_seq: needs dim % 32 == 0 and vocab % 64 == 0");
+        return -1;
+    }
+    (void)hipSetDevice(g_device);
+    const size_t V = vocab, D = dim, S = seq;
+    const size_t part = gemm_partial_elems(seq, vocab, dim);
+    float *e32 = nullptr, *xcf = nullptr, *xr = nullptr, *lg = nullptr, *pp = nullptr;
+    uint16_t *w16 = nullptr, *planes = nullptr;
+    int rc = -1;
+    if (hip_ok(hipMalloc(&e32, 4 * V * D), "hipMalloc") && hip_ok(hipMalloc(&w16, 2 * V * D), "hipMalloc") &&
+        hip_ok(hipMalloc(&xcf, 4 * D * S), "hipMalloc") && hip_ok(hipMalloc(&xr, 4 * D * S), "hipMalloc") &&
+        hip_ok(hipMalloc(&planes, 4 * D * S), "hipMalloc") && hip_ok(hipMalloc(&lg, 4 * V * S), "hipMalloc") &&
+        (part == 0 || hip_ok(hipMalloc(&pp, 4 * part), "hipMalloc")) &&
+        hip_ok(hipMemcpy(e32, embed, 4 * V * D, hipMemcpyHostToDevice), "copy embed") &&
+        hip_ok(hipMemcpy(xcf, x_cf, 4 * D * S, hipMemcpyHostToDevice), "copy x") &&
+        hip_ok(launch_convert_rows(e32, w16, vocab, dim, SH_DTYPE_F16, 1, 0, nullptr), "convert embed") &&
+        hip_ok(enqueue_transpose(xcf, dim, seq, xr, nullptr), "transpose x") &&
+        hip_ok(enqueue_linear_rows(xr, seq, dim, w16, vocab, SH_DTYPE_F16, planes, lg, true, pp, part, nullptr),
+               "vocab matmul") &&
+        hip_ok(hipDeviceSynchronize(), "vocab matmul sync") &&
+        hip_ok(hipMemcpy(logits_cf, lg, 4 * V * S, hipMemcpyDeviceToHost), "copy logits"))
+        rc = 0;
+    (void)hipFree(e32);
+    (void)hipFree(w16);
+    (void)hipFree(xcf);
+    (void)hipFree(xr);
+    (void)hipFree(planes);
+    (void)hipFree(lg);
+    (void)hipFree(pp);
+    return rc;
+}
+
+}  // extern "C"
+
+struct sh_conv {
+    int out_dim, in_dim, device;
+    uint16_t *w;   // [out_dim, in_dim] fp16 bits
+};
+
+extern "C" {
+
+sh_conv *sh_conv_create(const float *w, int32_t out_dim, int32_t in_dim) {
+    if (!w || out_dim <= 0 || in_dim <= 0) {
+        set_error("sh_conv_create: bad arguments");
+        return nullptr;
+    }
+    if (in_dim % 32 || out_dim % 64) {
+        set_error("sh_conv_create: needs in_dim % 32 == 0 and out_dim % 64 == 0");
+        return nullptr;
+    }
+    (void)hipSetDevice(g_device);
+    const size_t n = (size_t)out_dim * in_dim;
+    float *w32 = nullptr;
+    sh_conv *c = new sh_conv{out_dim, in_dim, g_device, nullptr};
+    const bool ok = hip_ok(hipMalloc(&c->w, 2 * n), "hipMalloc") && hip_ok(hipMalloc(&w32, 4 * n), "hipMalloc") &&
+                    hip_ok(hipMemcpy(w32, w, 4 * n, hipMemcpyHostToDevice), "copy weights") &&
+                    hip_ok(launch_convert_rows(w32, c->w, out_dim, in_dim, SH_DTYPE_F16, 1, 0, nullptr),
+                           "convert weights") &&
+                    hip_ok(hipDeviceSynchronize(), "conv create sync");
+    (void)hipFree(w32);
+    if (!ok) {
+        sh_conv_destroy(c);
+        return nullptr;
+    }
+    return c;
+}
+
+int sh_conv_eval(sh_conv *c, const float *x, int32_t s, float *out) {
+    if (!c || !x || !out || s <= 0) {
+        set_error("sh_conv_eval: bad arguments");
+        return -1;
+    }
+    (void)hipSetDevice(c->device);
+    const size_t S = s, I = c->in_dim, O = c->out_dim;
+    const size_t part = gemm_partial_elems(s, c->out_dim, c->in_dim);
+    float *xr = nullptr, *y = nullptr, *pp = nullptr;
+    uint16_t *planes = nullptr;
+    int rc = -1;
+    if (hip_ok(hipMalloc(&xr, 4 * S * I), "hipMalloc") && hip_ok(hipMalloc(&planes, 4 * S * I), "hipMalloc") &&
+        hip_ok(hipMalloc(&y, 4 * S * O), "hipMalloc") && (part == 0 || hip_ok(hipMalloc(&pp, 4 * part), "hipMalloc")) &&
+        hip_ok(hipMemcpy(xr, x, 4 * S * I, hipMemcpyHostToDevice), "copy x") &&
+        hip_ok(enqueue_linear_rows(xr, s, c->in_dim, c->w, c->out_dim, SH_DTYPE_F16, planes, y, false, pp, part,
+                                   nullptr),
+               "conv eval") &&
+        hip_ok(hipDeviceSynchronize(), "conv eval sync") &&
+        hip_ok(hipMemcpy(out, y, 4 * S * O, hipMemcpyDeviceToHost), "copy out"))
+        rc = 0;
+    (void)hipFree(xr);
+    (void)hipFree(planes);
+    (void)hipFree(y);
+    (void)hipFree(pp);
+    return rc;
+}
+
+void sh_conv_destroy(sh_conv *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipFree(c->w);
+    delete c;
 }
 
 }  // extern "C"

@@ -108,6 +108,7 @@ struct sh_model {
     float *pf_part;                            // K-range partials of split GEMMs
     size_t pf_part_cap;                        // elements of pf_part
     float *pf_q, *pf_k, *pf_v;                 // roped q, k and v: [S,qdim] [S,kvdim] x2
+    float *pf_cf;                              // [D,S] channel-first staging of the seams
     uint16_t *pf_xn, *pf_att, *pf_gate;        // GEMM operands: hi plane, then lo plane
 
     // batched decode (sh_prefill.hip): B sequences stepped together, state on the device
@@ -144,8 +145,10 @@ void set_error(const std::string &msg);
 bool hip_ok(hipError_t e, const char *what);
 
 // Launchers (sh_kernels.hip). All enqueue on m->stream.
+// Source row r (of `cols` values) lands in destination row r * dst_row_step + dst_row_offset,
+// both counted in rows of `cols` elements (a plain contiguous copy is step 1, offset 0).
 hipError_t launch_convert_rows(const float *src, void *dst, int rows, int cols, int dtype,
-                               int dst_row_stride, int dst_row_offset, hipStream_t s);
+                               int dst_row_step, int dst_row_offset, hipStream_t s);
 hipError_t launch_quantize_rows(const float *src, int8_t *dst, float *scales, int rows,
                                 int cols, int dst_row_stride, int dst_row_offset,
                                 int scale_stride, int scale_offset, hipStream_t s);
@@ -170,6 +173,20 @@ hipError_t prefill_alloc(sh_model *m, int S, bool logits);
 // at most seg_max rows per sequence): logits [V, S] into pf_logits when `logits`; fill_kv
 // writes every row's K/V into its sequence's cache (decode numerics).
 hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fill_kv);
+// Plugin seams over channel-first [D, S] data in pf_cf (rows at positions 0..S-1 of one
+// sequence in pf_rowpos / pf_rowseq): one layer (result back in pf_cf), the final RMSNorm
+// (result in pf_cf), the classifier (logits [V, S] in pf_logits).
+hipError_t enqueue_layer_cf(sh_model *m, int l, int S);
+hipError_t enqueue_rms_final_cf(sh_model *m, int S);
+hipError_t enqueue_classifier_cf(sh_model *m, int S);
+// Model-free products for the stateless seams: partial elements the split GEMM needs, and
+// out = x [M, K] . w [N, K]^T (w in the 16-bit type dt; x converted to operand planes in
+// `planes`, 2*M*K elements), written [M, N] or channel-first [N, M].
+size_t gemm_partial_elems(int M, int N, int K);
+hipError_t enqueue_linear_rows(const float *x, int M, int K, const uint16_t *w, int N, int dt,
+                               uint16_t *planes, float *out, bool cf, float *partial,
+                               size_t part_cap, hipStream_t s);
+hipError_t enqueue_transpose(const float *src, int rows, int cols, float *dst, hipStream_t s);
 bool batch_supported(const sh_model *m, int B, std::string *why);
 hipError_t batch_alloc(sh_model *m, int B);
 // One greedy step of B sequences (token bt_tok at bt_pos each), argmax into bt_hist.

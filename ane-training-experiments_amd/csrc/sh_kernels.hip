@@ -600,12 +600,12 @@ hipError_t enqueue_decode_step(sh_model *m) {
 }
 
 hipError_t launch_convert_rows(const float *src, void *dst, int rows, int cols, int dtype,
-                               int dst_row_stride, int dst_row_offset, hipStream_t s) {
+                               int dst_row_step, int dst_row_offset, hipStream_t s) {
     const size_t n = (size_t)rows * cols;
     size_t blocks = (n + kBlock - 1) / kBlock;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(k_convert_rows, dim3((unsigned)blocks), dim3(kBlock), 0, s, src, dst,
-                       rows, cols, dtype, dst_row_stride, dst_row_offset);
+                       rows, cols, dtype, dst_row_step, dst_row_offset);
     return hipGetLastError();
 }
 

@@ -80,10 +80,12 @@ __global__ __launch_bounds__(kT) void k_embed_rows(const uint16_t *embed, const 
 
 // One token row per workgroup. final_form = 0: rmsNormCFWithRRMSImpl (accel_other.go:11-28,
 // float32 scale, x*scale*w in float32); 1: stories.RMSNorm (cpu.go:97-111, float64 product
-// rounded once). The normalised row is written as a GEMM operand (hi/lo planes).
+// rounded once). The normalised row is written as a GEMM operand (hi/lo planes), or as fp32
+// rows into out32 when that is given.
 __global__ __launch_bounds__(kT) void k_rmsnorm_rows(const float *x, const float *w, int dim,
                                                      double eps, int final_form, int dt,
-                                                     uint16_t *out, size_t plane) {
+                                                     uint16_t *out, size_t plane,
+                                                     float *out32 = nullptr) {
     __shared__ double red[kT / 64];
     const float *row = x + (size_t)blockIdx.x * dim;
     double ss = 0;
@@ -98,8 +100,33 @@ __global__ __launch_bounds__(kT) void k_rmsnorm_rows(const float *x, const float
     const size_t o = (size_t)blockIdx.x * dim;
     for (int i = threadIdx.x; i < dim; i += blockDim.x) {
         const float v = final_form ? (float)((double)row[i] * rr * (double)w[i]) : row[i] * scale * w[i];
-        store_op(out, o + i, plane, v, dt);
+        if (out32) out32[o + i] = v;
+        else store_op(out, o + i, plane, v, dt);
     }
+}
+
+// dst [cols, rows] = src [rows, cols]^T, fp32, through 32 x 33 LDS tiles (the channel-first
+// <-> token-major conversion at the plugin-seam entry points).
+__global__ __launch_bounds__(kT) void k_transpose(const float *src, int rows, int cols, float *dst) {
+    __shared__ float tile[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int j = ty; j < 32; j += kT / 32) {
+        const int r = r0 + j, c = c0 + tx;
+        if (r < rows && c < cols) tile[j][tx] = src[(size_t)r * cols + c];
+    }
+    __syncthreads();
+    for (int j = ty; j < 32; j += kT / 32) {
+        const int c = c0 + j, r = r0 + tx;
+        if (c < cols && r < rows) dst[(size_t)c * rows + r] = tile[tx][j];
+    }
+}
+
+// fp32 values as GEMM operand planes (hi at i, lo `plane` further).
+__global__ __launch_bounds__(kT) void k_to_planes(const float *x, size_t n, int dt, uint16_t *out,
+                                                  size_t plane) {
+    const size_t i = (size_t)blockIdx.x * kT + threadIdx.x;
+    if (i < n) store_op(out, i, plane, x[i], dt);
 }
 
 enum { G_STORE = 0, G_RESID = 1, G_GATE = 2, G_LOGITS_CF = 3 };
@@ -1007,15 +1034,16 @@ constexpr int kChunkBytes = 16 * 1024;    // bytes of K rows per streamed chunk 
 
 // Batched decode attention that streams the cache (flash decoding): workgroup (split, kv
 // head g, sequence b) walks its share of the chunks of C = 16 KB / row-bytes keys. Chunk
-// i+1's K and V rows are copied into LDS (global_load_lds, four instructions per wave per
-// chunk) while chunk i is computed, so the cache is read at the rate the CU can take it.
+// i+1's K and V rows are loaded into registers (64 bytes per thread) while chunk i is
+// computed from LDS, then written to the other pair of LDS buffers. (An LDS DMA would not
+// overlap: the compiler makes every LDS read wait for all DMA in flight.)
 // Per chunk: lane-sliced scores of the group's q heads (RB/16 lanes per row, the slice dot
 // products added by DPP), the running maximum and the rescaled sum of exp terms (online
 // softmax), and P.V by thread (dim, key group) with the chunk's weights from LDS. One split
 // writes the output row directly (a GEMM operand, hi/lo planes); several splits leave
 // (m, l, acc) partials for k_attn_split_combine. Sequence b attends to 0..pos[b].
 template <int KVT, int HD, int GROUP>
-__global__ __launch_bounds__(kAT) void k_attn_batch_stream(
+__global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 ? 2 : 4))) void k_attn_batch_stream(
     const float *q, const void *kc, const void *vc, size_t kv_seq_stride, const int32_t *pos,
     int H, int KVH, float scale, int nsplit, int nch_buf, int dt, size_t plane, uint16_t *att,
     float *pm, float *pl, float *pacc) {
@@ -1047,11 +1075,29 @@ __global__ __launch_bounds__(kAT) void k_attn_batch_stream(
     for (int h = 0; h < GROUP; h++)
 #pragma unroll
         for (int e = 0; e < EPC; e++) qr[h][e] = q[(size_t)b * qdim + (size_t)(g * GROUP + h) * HD + sl * EPC + e];
-    auto dma = [&](int ci, int buf) {
+    // Next-chunk prefetch through registers: thread tid holds 16-byte pieces tid + kAT*u of
+    // the chunk's K rows and of its V rows (rows packed back to back); rows past the
+    // sequence's last key re-read that key, so every load is in bounds.
+    constexpr int PPT = kChunkBytes / 16 / kAT;        // pieces per thread per operand
+    static_assert(kChunkBytes % (16 * kAT) == 0, "chunk pieces split evenly");
+    u32x4 pk[PPT], pv[PPT];
+    auto fetch = [&](int ci) {
         const int t0 = ci * C, n = min(C, P - t0);
         const size_t off = (sbase + (size_t)t0 * kvdim) * EB;
-        rows_to_lds((const uint8_t *)kc + off, (size_t)kvdim * EB, n, C, RB, kbuf[buf]);
-        rows_to_lds((const uint8_t *)vc + off, (size_t)kvdim * EB, n, C, RB, vbuf[buf]);
+#pragma unroll
+        for (int u = 0; u < PPT; u++) {
+            const int pi = tid + kAT * u, r = min(pi / LPK, n - 1), c = pi % LPK;
+            const size_t o = off + (size_t)r * kvdim * EB + (size_t)c * 16;
+            pk[u] = *(const u32x4 *)((const uint8_t *)kc + o);
+            pv[u] = *(const u32x4 *)((const uint8_t *)vc + o);
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < PPT; u++) {
+            *(u32x4 *)(kbuf[buf] + (size_t)(tid + kAT * u) * 16) = pk[u];
+            *(u32x4 *)(vbuf[buf] + (size_t)(tid + kAT * u) * 16) = pv[u];
+        }
     };
     float m_run[GROUP], L[GROUP], acc[GROUP];
 #pragma unroll
@@ -1061,16 +1107,12 @@ __global__ __launch_bounds__(kAT) void k_attn_batch_stream(
         acc[h] = 0.f;
     }
     const int d = tid % HD, kg = tid / HD;
-    dma(c0, 0);
+    fetch(c0);
+    stash(0);
+    __syncthreads();
     for (int ci = c0; ci < c1; ci++) {
         const int buf = (ci - c0) & 1;
-        if (ci + 1 < c1) {
-            dma(ci + 1, buf ^ 1);
-            __asm__ __volatile__("s_waitcnt vmcnt(4)" ::: "memory");   // chunk ci has landed
-        } else {
-            __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-        __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (ci + 1 < c1) fetch(ci + 1);   // in flight while chunk ci is consumed
         const int n = min(C, P - ci * C);
         // scores and each wave's maximum
         float mx[GROUP];
@@ -1162,8 +1204,10 @@ __global__ __launch_bounds__(kAT) void k_attn_batch_stream(
 #pragma unroll
                 for (int h = 0; h < GROUP; h++) acc[h] = fmaf(pw[h][u], vv[u], acc[h]);
         }
-        // the chunk's buffers and sc are rewritten next
-        __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // chunk ci+1 into the other buffers (read last in chunk ci-1, before the previous
+        // barrier); then every wave is done with this chunk's buffers and sc
+        if (ci + 1 < c1) stash(buf ^ 1);
+        __syncthreads();
     }
 #pragma unroll
     for (int h = 0; h < GROUP; h++) part[kg][h][d] = acc[h];
@@ -1503,7 +1547,7 @@ hipError_t prefill_alloc(sh_model *m, int S, bool logits) {
                  o_x = take(4 * S * D), o_x2 = take(4 * S * D), o_xn = take(4 * S * D),
                  o_qkv = take(4 * S * R), o_q = take(4 * S * Q), o_k = take(4 * S * KV),
                  o_v = take(4 * S * KV), o_att = take(4 * S * Q), o_gate = take(4 * S * F),
-                 o_log = logits ? take(4 * V * S) : 0;
+                 o_log = logits ? take(4 * V * S) : 0, o_cf = take(4 * S * D);
     const size_t o_part = take(4 * part);   // K-range partials of the split GEMMs
     hipError_t e = hipMalloc(&m->pf_arena, off);
     if (e != hipSuccess) return e;
@@ -1521,6 +1565,7 @@ hipError_t prefill_alloc(sh_model *m, int S, bool logits) {
     m->pf_att = (uint16_t *)(A + o_att);
     m->pf_gate = (uint16_t *)(A + o_gate);
     m->pf_logits = logits ? (float *)(A + o_log) : nullptr;
+    m->pf_cf = (float *)(A + o_cf);
     m->pf_part = (float *)(A + o_part);
     m->pf_part_cap = part;
     m->pf_cap = S;
@@ -1617,51 +1662,127 @@ hipError_t launch_attn_prefill(const sh_model *m, int S, int seg_max, bool fill_
 // row's k and v enter its sequence's KV cache and the layers use the decode forms of the
 // softmax sum and SiLU, so the cache holds what a token-by-token decode of the same prompt
 // would have written.
-hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fill_kv) {
+namespace {
+
+// One layer of the forward over the S token-major rows in pf_x (rows as in enqueue_prefill);
+// the layer's output replaces pf_x.
+hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv) {
     const sh_config &c = m->cfg;
     const int dt = m->dtype;
     const int D = c.dim, F = c.hidden;
     hipStream_t s = m->stream;
     hipError_t e;
+    const float scale = (float)(1.0 / sqrt((double)c.head_dim));
+    const LayerDev &L = m->layers[l];
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x, L.rms_att, D,
+                       c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D, nullptr);
+    GemmArgs g{};
+    g.A = m->pf_xn; g.B = (const uint16_t *)L.wqkv; g.M = S; g.N = m->qkv_rows; g.K = D;
+    g.epi = G_STORE; g.out = m->pf_qkv; g.dt = dt;
+    if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
+    if ((e = launch_qk_rope(m, L, S, m->pf_qkv, m->pf_rowpos, m->pf_rowseq, m->pf_q,
+                            m->pf_k, m->pf_v, l, fill_kv, s)) != hipSuccess)
+        return e;
+    if ((e = launch_attn_prefill(m, S, seg_max, fill_kv, scale, s)) != hipSuccess) return e;
+    g = GemmArgs{};
+    g.A = m->pf_att; g.B = (const uint16_t *)L.wo; g.M = S; g.N = D; g.K = m->qdim;
+    g.epi = G_RESID; g.out = m->pf_x2; g.resid = m->pf_x; g.alpha = c.residual_scale; g.dt = dt;
+    if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x2, L.rms_ffn, D,
+                       c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D, nullptr);
+    g = GemmArgs{};
+    g.A = m->pf_xn; g.B = (const uint16_t *)L.w13; g.M = S; g.N = 2 * F; g.K = D;
+    g.epi = G_GATE; g.out16 = m->pf_gate; g.dt = dt; g.decode_forms = fill_kv ? 1 : 0;
+    if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
+    g = GemmArgs{};
+    g.A = m->pf_gate; g.B = (const uint16_t *)L.w2; g.M = S; g.N = D; g.K = F;
+    g.epi = G_RESID; g.out = m->pf_x; g.resid = m->pf_x2; g.alpha = c.residual_scale; g.dt = dt;
+    return gemm(g, dt, m->pf_part, m->pf_part_cap, s);
+}
+
+// logits [V, S] = classifier . (the operand planes in pf_xn)
+hipError_t enqueue_classifier(sh_model *m, int S) {
+    GemmArgs g{};
+    g.A = m->pf_xn; g.B = (const uint16_t *)m->cls; g.M = S; g.N = m->cfg.vocab; g.K = m->cfg.dim;
+    g.epi = G_LOGITS_CF; g.out = m->pf_logits; g.dt = m->dtype;
+    return gemm(g, m->dtype, m->pf_part, m->pf_part_cap, m->stream);
+}
+
+hipError_t launch_transpose(const float *src, int rows, int cols, float *dst, hipStream_t s) {
+    hipLaunchKernelGGL(k_transpose, dim3((cols + 31) / 32, (rows + 31) / 32), dim3(kT), 0, s, src,
+                       rows, cols, dst);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fill_kv) {
+    const sh_config &c = m->cfg;
+    const int dt = m->dtype;
+    const int D = c.dim;
+    hipStream_t s = m->stream;
+    hipError_t e;
     hipLaunchKernelGGL(k_embed_rows, dim3(S), dim3(kT), 0, s, (const uint16_t *)m->embed,
                        m->pf_tokens, c.vocab, D, dt, m->pf_x);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const float scale = (float)(1.0 / sqrt((double)c.head_dim));
-    for (int l = 0; l < c.n_layers; l++) {
-        const LayerDev &L = m->layers[l];
-        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x, L.rms_att, D,
-                           c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D);
-        GemmArgs g{};
-        g.A = m->pf_xn; g.B = (const uint16_t *)L.wqkv; g.M = S; g.N = m->qkv_rows; g.K = D;
-        g.epi = G_STORE; g.out = m->pf_qkv; g.dt = dt;
-        if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
-        if ((e = launch_qk_rope(m, L, S, m->pf_qkv, m->pf_rowpos, m->pf_rowseq, m->pf_q,
-                                m->pf_k, m->pf_v, l, fill_kv, s)) != hipSuccess)
-            return e;
-        if ((e = launch_attn_prefill(m, S, seg_max, fill_kv, scale, s)) != hipSuccess) return e;
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        g = GemmArgs{};
-        g.A = m->pf_att; g.B = (const uint16_t *)L.wo; g.M = S; g.N = D; g.K = m->qdim;
-        g.epi = G_RESID; g.out = m->pf_x2; g.resid = m->pf_x; g.alpha = c.residual_scale; g.dt = dt;
-        if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
-        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x2, L.rms_ffn, D,
-                           c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D);
-        g = GemmArgs{};
-        g.A = m->pf_xn; g.B = (const uint16_t *)L.w13; g.M = S; g.N = 2 * F; g.K = D;
-        g.epi = G_GATE; g.out16 = m->pf_gate; g.dt = dt; g.decode_forms = fill_kv ? 1 : 0;
-        if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
-        g = GemmArgs{};
-        g.A = m->pf_gate; g.B = (const uint16_t *)L.w2; g.M = S; g.N = D; g.K = F;
-        g.epi = G_RESID; g.out = m->pf_x; g.resid = m->pf_x2; g.alpha = c.residual_scale; g.dt = dt;
-        if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
-    }
+    for (int l = 0; l < c.n_layers; l++)
+        if ((e = enqueue_layer(m, l, S, seg_max, fill_kv)) != hipSuccess) return e;
     if (!logits) return hipSuccess;
     hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x, m->rms_final, D,
-                       c.norm_eps, 1, dt, m->pf_xn, (size_t)S * D);
+                       c.norm_eps, 1, dt, m->pf_xn, (size_t)S * D, nullptr);
+    return enqueue_classifier(m, S);
+}
+
+hipError_t enqueue_layer_cf(sh_model *m, int l, int S) {
+    const int D = m->cfg.dim;
+    hipError_t e;
+    if ((e = launch_transpose(m->pf_cf, D, S, m->pf_x, m->stream)) != hipSuccess) return e;
+    if ((e = enqueue_layer(m, l, S, S, false)) != hipSuccess) return e;
+    return launch_transpose(m->pf_x, S, D, m->pf_cf, m->stream);
+}
+
+hipError_t enqueue_rms_final_cf(sh_model *m, int S) {
+    const int D = m->cfg.dim;
+    hipError_t e;
+    if ((e = launch_transpose(m->pf_cf, D, S, m->pf_x, m->stream)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, m->stream, m->pf_x, m->rms_final, D,
+                       m->cfg.norm_eps, 1, m->dtype, nullptr, (size_t)0, m->pf_x2);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    return launch_transpose(m->pf_x2, S, D, m->pf_cf, m->stream);
+}
+
+hipError_t enqueue_classifier_cf(sh_model *m, int S) {
+    const int D = m->cfg.dim;
+    hipError_t e;
+    if ((e = launch_transpose(m->pf_cf, D, S, m->pf_x, m->stream)) != hipSuccess) return e;
+    const size_t n = (size_t)S * D;
+    hipLaunchKernelGGL(k_to_planes, dim3((unsigned)((n + kT - 1) / kT)), dim3(kT), 0, m->stream,
+                       m->pf_x, n, m->dtype, m->pf_xn, n);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    return enqueue_classifier(m, S);
+}
+
+size_t gemm_partial_elems(int M, int N, int K) {
+    const GemmPlan p = gemm_plan(M, N, K);
+    return p.ranges > 1 ? (size_t)p.ranges * M * N : 0;
+}
+
+hipError_t enqueue_linear_rows(const float *x, int M, int K, const uint16_t *w, int N, int dt,
+                               uint16_t *planes, float *out, bool cf, float *partial,
+                               size_t part_cap, hipStream_t s) {
+    const size_t n = (size_t)M * K;
+    hipLaunchKernelGGL(k_to_planes, dim3((unsigned)((n + kT - 1) / kT)), dim3(kT), 0, s, x, n, dt,
+                       planes, n);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     GemmArgs g{};
-    g.A = m->pf_xn; g.B = (const uint16_t *)m->cls; g.M = S; g.N = c.vocab; g.K = D;
-    g.epi = G_LOGITS_CF; g.out = m->pf_logits; g.dt = dt;
-    return gemm(g, dt, m->pf_part, m->pf_part_cap, s);
+    g.A = planes; g.B = w; g.M = M; g.N = N; g.K = K;
+    g.epi = cf ? G_LOGITS_CF : G_STORE; g.out = out; g.dt = dt;
+    return gemm(g, dt, partial, part_cap, s);
+}
+
+hipError_t enqueue_transpose(const float *src, int rows, int cols, float *dst, hipStream_t s) {
+    return launch_transpose(src, rows, cols, dst, s);
 }
 
 

@@ -115,6 +115,13 @@ SIGNATURES = {
     "sh_synth_normal": (C.c_int, [_F, C.c_size_t, C.c_uint64, C.c_uint64, C.c_float]),
     "sh_synth_tokens": (C.c_int, [_I32, C.c_size_t, C.c_uint64, C.c_int32]),
     "sh_round_dtype": (C.c_int, [_F, C.c_size_t, C.c_int32]),
+    "sh_layer_forward_cf": (C.c_int, [C.c_void_p, C.c_int32, _F, C.c_int32, _F]),
+    "sh_rms_final_cf": (C.c_int, [C.c_void_p, _F, C.c_int32, _F]),
+    "sh_classifier_cf": (C.c_int, [C.c_void_p, _F, C.c_int32, _F]),
+    "sh_matmul_vocab_seq": (C.c_int, [_F, _F, C.c_int32, C.c_int32, C.c_int32, _F]),
+    "sh_conv_create": (C.c_void_p, [_F, C.c_int32, C.c_int32]),
+    "sh_conv_eval": (C.c_int, [C.c_void_p, _F, C.c_int32, _F]),
+    "sh_conv_destroy": (None, [C.c_void_p]),
 }
 
 
@@ -321,6 +328,27 @@ class Model:
                "sh_prefill_logits")
         return out
 
+    def layer_forward_cf(self, layer: int, x_cf: np.ndarray) -> np.ndarray:
+        """One layer over channel-first [dim, seq] (the storiesane layerForward.run seam)."""
+        x = np.ascontiguousarray(x_cf, np.float32)
+        out = np.empty_like(x)
+        _check(self.lib.sh_layer_forward_cf(self.h, layer, _fp(x), x.shape[1], _fp(out)), "sh_layer_forward_cf")
+        return out
+
+    def rms_final_cf(self, x_cf: np.ndarray) -> np.ndarray:
+        """The final RMSNorm over channel-first [dim, seq] (offload.runRMSForward)."""
+        x = np.ascontiguousarray(x_cf, np.float32)
+        out = np.empty_like(x)
+        _check(self.lib.sh_rms_final_cf(self.h, _fp(x), x.shape[1], _fp(out)), "sh_rms_final_cf")
+        return out
+
+    def classifier_cf(self, xnorm_cf: np.ndarray) -> np.ndarray:
+        """logits [vocab, seq] from channel-first [dim, seq] (offload.runClassifierForward)."""
+        x = np.ascontiguousarray(xnorm_cf, np.float32)
+        out = np.empty((self.cfg.vocab, x.shape[1]), np.float32)
+        _check(self.lib.sh_classifier_cf(self.h, _fp(x), x.shape[1], _fp(out)), "sh_classifier_cf")
+        return out
+
     def tap(self, which: int) -> np.ndarray:
         """sh_decode_tap: an intermediate vector of the last layer of the last forward."""
         n = {SH_TAP_X: self.cfg.dim, SH_TAP_QKV: self.cfg.qdim + 2 * self.cfg.kvdim,
@@ -418,6 +446,45 @@ def copy_calibrate(nbytes: int, reps: int = 10):
     ms, gbps = C.c_double(0), C.c_double(0)
     _check(load().sh_copy_calibrate(nbytes, reps, C.byref(ms), C.byref(gbps)), "sh_copy_calibrate")
     return ms.value, gbps.value
+
+
+def matmul_vocab_seq(embed: np.ndarray, x_cf: np.ndarray) -> np.ndarray:
+    """logits [vocab, seq] = embed [vocab, dim] . x [dim, seq] (matMulVocabSeqAccelerate)."""
+    lib = load()
+    e = np.ascontiguousarray(embed, np.float32)
+    x = np.ascontiguousarray(x_cf, np.float32)
+    out = np.empty((e.shape[0], x.shape[1]), np.float32)
+    _check(lib.sh_matmul_vocab_seq(_fp(e), _fp(x), e.shape[0], e.shape[1], x.shape[1], _fp(out)),
+           "sh_matmul_vocab_seq")
+    return out
+
+
+class Conv:
+    """A compiled 1x1 conv (model.Kernel) for forward.ConvEval: y [s, out] = x [s, in] . w^T."""
+
+    def __init__(self, w: np.ndarray):
+        self.lib = load()
+        self.w = np.ascontiguousarray(w, np.float32)
+        self.h = self.lib.sh_conv_create(_fp(self.w), self.w.shape[0], self.w.shape[1])
+        if not self.h:
+            raise ShError(f"sh_conv_create: {last_error()}")
+
+    def eval(self, x: np.ndarray) -> np.ndarray:
+        a = np.ascontiguousarray(x, np.float32).reshape(-1, self.w.shape[1])
+        out = np.empty((a.shape[0], self.w.shape[0]), np.float32)
+        _check(self.lib.sh_conv_eval(self.h, _fp(a), a.shape[0], _fp(out)), "sh_conv_eval")
+        return out
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.sh_conv_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def quantize_i8(src: np.ndarray, per_row: bool):

@@ -114,6 +114,40 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
  * channel-first [V, seq] (logits[v*seq + t]). Out-of-range ids give a zero embedding
  * column (cpu.go:41-72). Residual scale = cfg.residual_scale. */
 int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *logits_cf);
+/* ---- storiesane plugin seams over channel-first data (the _other.go stubs' HIP side) ---- */
+/* compileStoriesLayerForwardFunc + (*layerForward).run (ane/storiesane/layer_other.go:27-37,
+ * called per layer from engine.go:784): one transformer layer of the uploaded model over
+ * x_cf [dim, seq] (x_cf[d*seq + t]) at positions 0..seq-1, result out_cf [dim, seq]; the
+ * numerics of evalLogitsCPUInto's layer body (engine.go:815-838: rmsNormCF, q/k/v, RoPE,
+ * causal attention, Wo, x2 = x + a*o, rmsNormCF, W1/W3, SiLU gate, W2, x = x2 + a*ff with
+ * a = cfg.residual_scale). The KV cache is not touched. out_cf may equal x_cf. */
+int sh_layer_forward_cf(sh_model *m, int32_t layer, const float *x_cf, int32_t seq,
+                        float *out_cf);
+/* offload.runRMSForward (offload_other.go:22-24; offload_darwin.go:345-356): the final
+ * RMSNorm with the model's rms_final over x_cf [dim, seq] (stories.RMSNorm numerics,
+ * cpu.go:97-111) into out_cf [dim, seq]. out_cf may equal x_cf. */
+int sh_rms_final_cf(sh_model *m, const float *x_cf, int32_t seq, float *out_cf);
+/* offload.runClassifierForward (offload_other.go:25-27; offload_darwin.go:358-):
+ * logits_cf [vocab, seq] = classifier [vocab, dim] . xnorm_cf [dim, seq] (MatMulVocabSeq's
+ * product, cpu.go:276-300) with the model's classifier rows. */
+int sh_classifier_cf(sh_model *m, const float *xnorm_cf, int32_t seq, float *logits_cf);
+/* matMulVocabSeqAccelerate (ane/stories/gemm_stub.go:5-7, called by MatMulVocabSeq at
+ * cpu.go:276-278; "true = handled" there, 0 here): logits [vocab, seq] = embed [vocab, dim] .
+ * x [dim, seq], channel-first, from host fp32 arrays. No model is needed: embed is rounded to
+ * fp16 on the device for each call (x keeps ~22 significant bits as hi/lo operand planes).
+ * Needs dim % 32 == 0 and vocab % 64 == 0; otherwise -1 and the caller keeps its CPU loop. */
+int sh_matmul_vocab_seq(const float *embed, const float *x_cf, int32_t vocab, int32_t dim,
+                        int32_t seq, float *logits_cf);
+/* forward.ConvEval (ane/forward/conv.go:11-52) over a compiled 1x1-conv kernel
+ * (model.Kernel, ane/model/model_other.go:41-93): sh_conv_create uploads w [out_dim, in_dim]
+ * (rounded to fp16) and returns NULL on failure; sh_conv_eval takes x row-major [s, in_dim]
+ * and writes out row-major [s, out_dim], out[t*out_dim + o] = sum_i w[o, i] x[t*in_dim + i]
+ * (ConvEval's channel-first transposes are folded into the product). Needs in_dim % 32 == 0
+ * and out_dim % 64 == 0. sh_conv_destroy accepts NULL. */
+typedef struct sh_conv sh_conv;
+sh_conv *sh_conv_create(const float *w, int32_t out_dim, int32_t in_dim);
+int sh_conv_eval(sh_conv *c, const float *x, int32_t s, float *out);
+void sh_conv_destroy(sh_conv *c);
 /* (*Engine).Decode with Temperature 0 (ane/storiesane/decode.go:18-94): every step runs the
  * full causal forward (as sh_prefill_logits) over the last `seq` tokens left-padded with BOS
  * (fillDecodeWindow, :83-94) and appends the argmax of the last position's logits. The prompt

@@ -670,14 +670,14 @@ static void matmul_vocab_seq(float *logits, const float *embed, const float *x, 
     }
 }
 
-void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t *tokens,
-                       int seq, float *logits_cf, int threads) {
+/* One layer of evalLogitsCPUInto (engine.go:815-838): x_cf [D,S] -> out_cf [D,S] at
+ * positions 0..S-1. out_cf may not alias x_cf. */
+void or_layer_forward_cf(const or_config *cfg, const or_layer *L, const float *x_cf, int seq,
+                         float *out_cf, int threads) {
     int D = cfg->dim, F = cfg->hidden, H = cfg->n_heads, KVH = cfg->n_kv_heads;
     int hd = cfg->head_dim, qd = H * hd, kvd = KVH * hd;
     size_t S = (size_t)seq;
     float alpha = cfg->residual_scale;
-    float *x = (float *)malloc(sizeof(float) * D * S);
-    float *next = (float *)malloc(sizeof(float) * D * S);
     float *xn = (float *)malloc(sizeof(float) * D * S);
     float *qf = (float *)malloc(sizeof(float) * qd * S);
     float *kf = (float *)malloc(sizeof(float) * kvd * S);
@@ -691,40 +691,61 @@ void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t
     float *rc = (float *)malloc(sizeof(float) * S * (hd / 2));
     float *rs = (float *)malloc(sizeof(float) * S * (hd / 2));
     or_rope_tables(rc, rs, seq, hd, cfg->rope_theta);            /* engine.go:218 */
-
-    or_embed_lookup_cf(x, w->embed, cfg->vocab, tokens, D, seq);
-    float *bufs[2] = {x, next};   /* cur and next swap every layer */
-    float *cur = x;
-    for (int l = 0; l < cfg->n_layers; l++) {
-        const or_layer *L = &w->layers[l];
-        rms_norm_cf(xn, cur, L->rms_att, D, seq, cfg->norm_eps);
-        linear_cf(qf, L->wq, xn, qd, D, seq, threads);
-        linear_cf(kf, L->wk, xn, kvd, D, seq, threads);
-        if (cfg->qk_norm) {
-            qk_norm_cf(qf, H, hd, seq, L->q_norm, cfg->qk_norm_eps);
-            qk_norm_cf(kf, KVH, hd, seq, L->k_norm, cfg->qk_norm_eps);
-        }
-        rope_cf(qf, H, hd, seq, rc, rs);
-        rope_cf(kf, KVH, hd, seq, rc, rs);
-        linear_cf(vf, L->wv, xn, kvd, D, seq, threads);
-        causal_attention_cf(att, qf, kf, vf, H, KVH, hd, seq, threads);
-        linear_cf(x2, L->wo, att, D, qd, seq, threads);
-        for (size_t i = 0; i < D * S; i++) x2[i] = cur[i] + alpha * x2[i];   /* residual.go:19 */
-        rms_norm_cf(xn, x2, L->rms_ffn, D, seq, cfg->norm_eps);
-        linear_cf(h1, L->w1, xn, F, D, seq, threads);
-        linear_cf(h3, L->w3, xn, F, D, seq, threads);
-        for (size_t i = 0; i < F * S; i++) {                    /* accel_other.go:128-133 */
-            float sig = (float)(1.0 / (1.0 + exp((double)(-h1[i]))));
-            gate[i] = (h1[i] * sig) * h3[i];
-        }
-        linear_cf(ff, L->w2, gate, D, F, seq, threads);
-        for (size_t i = 0; i < D * S; i++) next[i] = x2[i] + alpha * ff[i];
-        float *tmp = cur; cur = next; next = tmp;
+    rms_norm_cf(xn, x_cf, L->rms_att, D, seq, cfg->norm_eps);
+    linear_cf(qf, L->wq, xn, qd, D, seq, threads);
+    linear_cf(kf, L->wk, xn, kvd, D, seq, threads);
+    if (cfg->qk_norm) {
+        qk_norm_cf(qf, H, hd, seq, L->q_norm, cfg->qk_norm_eps);
+        qk_norm_cf(kf, KVH, hd, seq, L->k_norm, cfg->qk_norm_eps);
     }
-    rms_norm_final_cf(xn, cur, w->rms_final, D, seq, cfg->norm_eps);
-    matmul_vocab_seq(logits_cf, w->cls ? w->cls : w->embed, xn, cfg->vocab, D, seq, threads);
-    free(bufs[0]); free(bufs[1]); free(xn); free(qf); free(kf); free(vf); free(att); free(x2);
+    rope_cf(qf, H, hd, seq, rc, rs);
+    rope_cf(kf, KVH, hd, seq, rc, rs);
+    linear_cf(vf, L->wv, xn, kvd, D, seq, threads);
+    causal_attention_cf(att, qf, kf, vf, H, KVH, hd, seq, threads);
+    linear_cf(x2, L->wo, att, D, qd, seq, threads);
+    for (size_t i = 0; i < D * S; i++) x2[i] = x_cf[i] + alpha * x2[i];   /* residual.go:19 */
+    rms_norm_cf(xn, x2, L->rms_ffn, D, seq, cfg->norm_eps);
+    linear_cf(h1, L->w1, xn, F, D, seq, threads);
+    linear_cf(h3, L->w3, xn, F, D, seq, threads);
+    for (size_t i = 0; i < F * S; i++) {                    /* accel_other.go:128-133 */
+        float sig = (float)(1.0 / (1.0 + exp((double)(-h1[i]))));
+        gate[i] = (h1[i] * sig) * h3[i];
+    }
+    linear_cf(ff, L->w2, gate, D, F, seq, threads);
+    for (size_t i = 0; i < D * S; i++) out_cf[i] = x2[i] + alpha * ff[i];
+    free(xn); free(qf); free(kf); free(vf); free(att); free(x2);
     free(h1); free(h3); free(gate); free(ff); free(rc); free(rs);
+}
+
+void or_rms_norm_final_cf(float *out, const float *x, const float *w, int dim, int seq,
+                          double eps) {
+    rms_norm_final_cf(out, x, w, dim, seq, eps);
+}
+
+void or_matmul_vocab_seq(float *logits, const float *embed, const float *x, int vocab, int dim,
+                         int seq, int threads) {
+    matmul_vocab_seq(logits, embed, x, vocab, dim, seq, threads);
+}
+
+void or_linear_cf(float *out, const float *w, const float *in, int out_ch, int in_ch, int seq,
+                  int threads) {
+    linear_cf(out, w, in, out_ch, in_ch, seq, threads);
+}
+
+void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t *tokens,
+                       int seq, float *logits_cf, int threads) {
+    int D = cfg->dim;
+    size_t S = (size_t)seq;
+    float *x = (float *)malloc(sizeof(float) * D * S);
+    float *next = (float *)malloc(sizeof(float) * D * S);
+    or_embed_lookup_cf(x, w->embed, cfg->vocab, tokens, D, seq);
+    for (int l = 0; l < cfg->n_layers; l++) {
+        or_layer_forward_cf(cfg, &w->layers[l], x, seq, next, threads);
+        float *tmp = x; x = next; next = tmp;   /* cur and next swap every layer */
+    }
+    rms_norm_final_cf(next, x, w->rms_final, D, seq, cfg->norm_eps);
+    matmul_vocab_seq(logits_cf, w->cls ? w->cls : w->embed, next, cfg->vocab, D, seq, threads);
+    free(x); free(next);
 }
 
 /* decode.go:83-94 fillDecodeWindow: BOS-left-pad the last `seq` tokens */

@@ -89,6 +89,18 @@ void or_embed_lookup_cf(float *out, const float *embed, int vocab, const uint16_
                         int dim, int seq);
 void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t *tokens,
                        int seq, float *logits_cf, int threads);
+/* One layer of the channel-first forward (engine.go:815-838), x_cf [D,S] -> out_cf [D,S]. */
+void or_layer_forward_cf(const or_config *cfg, const or_layer *L, const float *x_cf, int seq,
+                         float *out_cf, int threads);
+/* cpu.go:97-111 RMSNorm (final form) over channel-first [dim, seq]. */
+void or_rms_norm_final_cf(float *out, const float *x, const float *w, int dim, int seq,
+                          double eps);
+/* cpu.go:276-300 MatMulVocabSeq: logits [vocab, seq] = embed [vocab, dim] . x [dim, seq]. */
+void or_matmul_vocab_seq(float *logits, const float *embed, const float *x, int vocab, int dim,
+                         int seq, int threads);
+/* forward_common.go:35-46 linearCF: out [out_ch, seq] = W [out_ch, in_ch] . in [in_ch, seq]. */
+void or_linear_cf(float *out, const float *w, const float *in, int out_ch, int in_ch, int seq,
+                  int threads);
 void or_fill_decode_window(uint16_t *dst, int seq, const int32_t *tokens, int n);
 
 #ifdef __cplusplus

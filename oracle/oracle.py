@@ -74,6 +74,10 @@ def load() -> C.CDLL:
         "or_eval_logits_cf": (None, [C.POINTER(OrConfig), C.POINTER(OrWeights), C.POINTER(C.c_uint16),
                                      C.c_int, _F, C.c_int]),
         "or_fill_decode_window": (None, [C.POINTER(C.c_uint16), C.c_int, _I32, C.c_int]),
+        "or_layer_forward_cf": (None, [C.POINTER(OrConfig), C.POINTER(OrLayer), _F, C.c_int, _F, C.c_int]),
+        "or_rms_norm_final_cf": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_double]),
+        "or_matmul_vocab_seq": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_int, C.c_int]),
+        "or_linear_cf": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_int, C.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -184,6 +188,43 @@ def eval_logits_cf(cfg: OrConfig, weights, tokens, threads: int = 1) -> np.ndarr
     out = np.empty((cfg.vocab, t.size), np.float32)
     load().or_eval_logits_cf(C.byref(cfg), C.byref(holder.s), t.ctypes.data_as(C.POINTER(C.c_uint16)),
                              t.size, fp(out), threads)
+    return out
+
+
+def layer_forward_cf(cfg: OrConfig, weights, layer: int, x_cf: np.ndarray, threads: int = 1) -> np.ndarray:
+    """or_layer_forward_cf: one layer of engine.go:815-838 over channel-first [D, S]."""
+    x = np.ascontiguousarray(x_cf, np.float32)
+    holder = _WeightsHolder(weights, cfg.n_layers)
+    out = np.empty_like(x)
+    load().or_layer_forward_cf(C.byref(cfg), C.byref(holder.layers[layer]), fp(x), x.shape[1], fp(out),
+                               threads)
+    return out
+
+
+def rms_norm_final_cf(x_cf: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """or_rms_norm_final_cf: cpu.go:97-111 over channel-first [D, S]."""
+    x = np.ascontiguousarray(x_cf, np.float32)
+    g = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    load().or_rms_norm_final_cf(fp(out), fp(x), fp(g), x.shape[0], x.shape[1], eps)
+    return out
+
+
+def matmul_vocab_seq(embed: np.ndarray, x_cf: np.ndarray, threads: int = 1) -> np.ndarray:
+    """or_matmul_vocab_seq: cpu.go:276-300, logits [V, S] = embed [V, D] . x [D, S]."""
+    e = np.ascontiguousarray(embed, np.float32)
+    x = np.ascontiguousarray(x_cf, np.float32)
+    out = np.empty((e.shape[0], x.shape[1]), np.float32)
+    load().or_matmul_vocab_seq(fp(out), fp(e), fp(x), e.shape[0], e.shape[1], x.shape[1], threads)
+    return out
+
+
+def linear_cf(w: np.ndarray, x_cf: np.ndarray, threads: int = 1) -> np.ndarray:
+    """or_linear_cf: forward_common.go:35-46, out [O, S] = W [O, I] . in [I, S]."""
+    wt = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x_cf, np.float32)
+    out = np.empty((wt.shape[0], x.shape[1]), np.float32)
+    load().or_linear_cf(fp(out), fp(wt), fp(x), wt.shape[0], wt.shape[1], x.shape[1], threads)
     return out
 
 

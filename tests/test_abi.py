@@ -84,3 +84,19 @@ def test_invalid_configs_are_rejected_with_a_message(field, value):
 def test_bad_dtype_rejected():
     with pytest.raises(sh.ShError):
         sh.Model(sh.stories110m_config(), 7)
+
+
+def test_stateless_seams_reject_unsupported_shapes():
+    lib = sh.load()
+    e = np.zeros((100, 48), np.float32)
+    x = np.zeros((48, 3), np.float32)
+    out = np.zeros((100, 3), np.float32)
+    fp = lambda a: a.ctypes.data_as(sh.C.POINTER(sh.C.c_float))
+    assert lib.sh_matmul_vocab_seq(fp(e), fp(x), 100, 48, 3, fp(out)) == -1
+    assert "dim % 32 == 0 and vocab % 64 == 0" in sh.last_error()
+    assert lib.sh_matmul_vocab_seq(None, fp(x), 100, 48, 3, fp(out)) == -1
+    assert "bad arguments" in sh.last_error()
+    assert not lib.sh_conv_create(fp(e), 100, 48)
+    assert "in_dim % 32 == 0 and out_dim % 64 == 0" in sh.last_error()
+    assert lib.sh_conv_eval(None, fp(x), 3, fp(out)) == -1
+    lib.sh_conv_destroy(None)

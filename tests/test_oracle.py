@@ -369,3 +369,34 @@ def test_kv_storage_rounding():
         a = d32.forward_one(t + 3, t)
         b = d16.forward_one(t + 3, t)
     assert 0 < np.max(np.abs(a - b)) < 1e-2
+
+
+# ---- seam pieces: the channel-first forward factored as the plugin seams use it ------------
+
+def test_seam_pieces_compose_to_eval_logits_exactly():
+    cfg = tiny_config(n_layers=3, residual_scale=deepnet_alpha(3))
+    w = random_gains(sh.synth_weights(cfg, seed=101, std=0.08), 102)
+    toks = sh.synth_tokens(19, 103, cfg.vocab)
+    ocfg = oracle.config_from(cfg)
+    x = np.ascontiguousarray(w.embed[toks].T)
+    for layer in range(cfg.n_layers):
+        x = oracle.layer_forward_cf(ocfg, w, layer, x, threads=2)
+    xn = oracle.rms_norm_final_cf(x, w.rms_final, cfg.norm_eps)
+    logits = oracle.matmul_vocab_seq(w.embed, xn, threads=2)
+    np.testing.assert_array_equal(logits, oracle.eval_logits_cf(ocfg, w, toks, threads=2))
+
+
+def test_linear_vocab_matmul_and_final_norm_against_float64():
+    rng = np.random.default_rng(104)
+    wt = rng.standard_normal((48, 80)).astype(np.float32)
+    x = rng.standard_normal((80, 13)).astype(np.float32)
+    ref = wt.astype(np.float64) @ x.astype(np.float64)
+    np.testing.assert_allclose(oracle.linear_cf(wt, x), ref, atol=1e-4, rtol=0)
+    np.testing.assert_allclose(oracle.matmul_vocab_seq(wt, x), ref, atol=1e-4, rtol=0)
+    # an operand transposed or an index swapped would fail the non-square case above; the
+    # final RMSNorm (cpu.go:97-111) against its float64 closed form, with non-unit gains
+    g = (0.5 + rng.random(80)).astype(np.float32)
+    got = oracle.rms_norm_final_cf(x, g, 1e-5)
+    xd = x.astype(np.float64)
+    want = xd / np.sqrt((xd ** 2).mean(axis=0, keepdims=True) + 1e-5) * g[:, None]
+    np.testing.assert_allclose(got, want, atol=1e-6, rtol=1e-6)
