@@ -199,8 +199,17 @@ void parallel_ranges(size_t n, F fn) {
 // Shared set-up of the channel-first seams: checks, prefill scratch for seq rows, the rows'
 // positions 0..seq-1 of one sequence, and x_cf [dim, seq] copied into pf_cf.
 bool seam_begin(sh_model *m, const char *what, const float *x_cf, int32_t seq, void *out,
-                bool logits) {
-    if (!ready(m)) return false;
+                bool logits, bool need_globals) {
+    if (!m) {
+        set_error("nil model");
+        return false;
+    }
+    // the layer seam needs only the layers (a one-layer model per compiled layer, as
+    // compileStoriesLayerForwardFunc makes them); the final norm and classifier the globals
+    if (m->uploaded_layers != m->cfg.n_layers || (need_globals && !m->globals_uploaded)) {
+        set_error(std::string(what) + ": model weights are not fully uploaded");
+        return false;
+    }
     if (!x_cf || !out || seq <= 0 || seq > m->cfg.max_seq) {
         set_error(std::string(what) + ": bad arguments");
         return false;
@@ -1258,19 +1267,19 @@ int sh_layer_forward_cf(sh_model *m, int32_t layer, const float *x_cf, int32_t s
         set_error("sh_layer_forward_cf: layer out of range");
         return -1;
     }
-    if (!seam_begin(m, "sh_layer_forward_cf", x_cf, seq, out_cf, false)) return -1;
+    if (!seam_begin(m, "sh_layer_forward_cf", x_cf, seq, out_cf, false, false)) return -1;
     if (!hip_ok(enqueue_layer_cf(m, layer, seq), "layer forward")) return -1;
     return seam_end(m, m->pf_cf, out_cf, sizeof(float) * (size_t)m->cfg.dim * seq, seq) ? 0 : -1;
 }
 
 int sh_rms_final_cf(sh_model *m, const float *x_cf, int32_t seq, float *out_cf) {
-    if (!seam_begin(m, "sh_rms_final_cf", x_cf, seq, out_cf, false)) return -1;
+    if (!seam_begin(m, "sh_rms_final_cf", x_cf, seq, out_cf, false, true)) return -1;
     if (!hip_ok(enqueue_rms_final_cf(m, seq), "final rmsnorm")) return -1;
     return seam_end(m, m->pf_cf, out_cf, sizeof(float) * (size_t)m->cfg.dim * seq, seq) ? 0 : -1;
 }
 
 int sh_classifier_cf(sh_model *m, const float *xnorm_cf, int32_t seq, float *logits_cf) {
-    if (!seam_begin(m, "sh_classifier_cf", xnorm_cf, seq, logits_cf, true)) return -1;
+    if (!seam_begin(m, "sh_classifier_cf", xnorm_cf, seq, logits_cf, true, true)) return -1;
     if (!hip_ok(enqueue_classifier_cf(m, seq), "classifier")) return -1;
     return seam_end(m, m->pf_logits, logits_cf, sizeof(float) * (size_t)m->cfg.vocab * seq, seq) ? 0 : -1;
 }

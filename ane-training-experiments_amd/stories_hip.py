@@ -281,17 +281,20 @@ class Model:
         if not self.h:
             raise ShError(f"sh_model_create: {last_error()}")
 
+    def _upload_layer(self, l: int, lw: dict) -> None:
+        arrs = [np.ascontiguousarray(lw[k], np.float32) for k in LAYER_KEYS]
+        arrs += [np.ascontiguousarray(lw["rms_att"], np.float32),
+                 np.ascontiguousarray(lw["rms_ffn"], np.float32)]
+        qn = lw.get("q_norm")
+        kn = lw.get("k_norm")
+        qn = None if qn is None else np.ascontiguousarray(qn, np.float32)
+        kn = None if kn is None else np.ascontiguousarray(kn, np.float32)
+        _check(self.lib.sh_model_upload_layer(self.h, l, *[_fp(a) for a in arrs], _fp(qn), _fp(kn)),
+               f"sh_model_upload_layer({l})")
+
     def upload(self, w: Weights) -> None:
         for l, lw in enumerate(w.layers):
-            arrs = [np.ascontiguousarray(lw[k], np.float32) for k in LAYER_KEYS]
-            arrs += [np.ascontiguousarray(lw["rms_att"], np.float32),
-                     np.ascontiguousarray(lw["rms_ffn"], np.float32)]
-            qn = lw.get("q_norm")
-            kn = lw.get("k_norm")
-            qn = None if qn is None else np.ascontiguousarray(qn, np.float32)
-            kn = None if kn is None else np.ascontiguousarray(kn, np.float32)
-            _check(self.lib.sh_model_upload_layer(self.h, l, *[_fp(a) for a in arrs], _fp(qn), _fp(kn)),
-                   f"sh_model_upload_layer({l})")
+            self._upload_layer(l, lw)
         embed = np.ascontiguousarray(w.embed, np.float32)
         cls = None if w.cls is None else np.ascontiguousarray(w.cls, np.float32)
         _check(self.lib.sh_model_upload_globals(self.h, _fp(embed), _fp(np.ascontiguousarray(w.rms_final, np.float32)), _fp(cls)),

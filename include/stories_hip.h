@@ -120,7 +120,9 @@ int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *l
  * x_cf [dim, seq] (x_cf[d*seq + t]) at positions 0..seq-1, result out_cf [dim, seq]; the
  * numerics of evalLogitsCPUInto's layer body (engine.go:815-838: rmsNormCF, q/k/v, RoPE,
  * causal attention, Wo, x2 = x + a*o, rmsNormCF, W1/W3, SiLU gate, W2, x = x2 + a*ff with
- * a = cfg.residual_scale). The KV cache is not touched. out_cf may equal x_cf. */
+ * a = cfg.residual_scale). The KV cache is not touched. out_cf may equal x_cf. Needs the
+ * model's layers uploaded, not its globals: a model with n_layers = 1 holding one layer is
+ * the counterpart of one compiled layerForward. */
 int sh_layer_forward_cf(sh_model *m, int32_t layer, const float *x_cf, int32_t seq,
                         float *out_cf);
 /* offload.runRMSForward (offload_other.go:22-24; offload_darwin.go:345-356): the final

@@ -56,6 +56,24 @@ def test_layer_forward_cf_matches_oracle(gpu, make_cfg, dtype, seq):
     m.close()
 
 
+def test_one_layer_model_is_a_compiled_layer(gpu):
+    # compileStoriesLayerForwardFunc's counterpart: a model holding one layer and no globals
+    cfg = tiny_config(residual_scale=0.5)
+    m, ocfg, ow = build(cfg, sh.SH_DTYPE_F16, 65)
+    x = embed_cf(ow, sh.synth_tokens(21, 66, cfg.vocab))
+    one = tiny_config(residual_scale=0.5, n_layers=1)
+    lm = sh.Model(one, sh.SH_DTYPE_F16)
+    src = sh.synth_weights(cfg, seed=65, std=0.05)
+    src = random_gains(src, 66)
+    lw = src.layers[1]
+    lm._upload_layer(0, lw)
+    with pytest.raises(sh.ShError, match="not fully uploaded"):
+        lm.rms_final_cf(x)
+    np.testing.assert_array_equal(lm.layer_forward_cf(0, x), m.layer_forward_cf(1, x))
+    lm.close()
+    m.close()
+
+
 def test_rms_final_and_classifier_cf_match_oracle(gpu):
     cfg = tiny_config()
     m, ocfg, ow = build(cfg, sh.SH_DTYPE_F16, 71)
