@@ -12,6 +12,8 @@
 //   -synthetic-seed S, -synthetic-std X
 //                                   N(0, X) weights keyed by S (the library's sh_synth_normal
 //                                   streams) when no -model file is given
+//   -layers N                       with synthetic weights: only the first N layers of the
+//                                   shape (per-layer kernels unchanged; for short profiles)
 //   -prompt-len N, -prompt-seed S   a synthetic prompt of N uniform ids instead of -prompt-ids
 //   -bench-steps K, -bench-warmup W greedy decode W untimed + K timed times and print one
 //                                   JSON object (device times, bytes, tokens) instead of text
@@ -295,6 +297,7 @@ int main(int argc, char **argv) {
     fl.def("copy-calibrate", "0");
     fl.def("batch", "0");
     fl.def("eval-logits", "false", true);
+    fl.def("layers", "0");
     fl.parse(argc, argv);
 
     if (!fl.s("detokenize").empty()) {
@@ -344,6 +347,7 @@ int main(int argc, char **argv) {
         else if (shape == "stories110m") sh_config_stories110m(&c);
         else fatalf("unknown -shape %s", shape);
         source = "synthetic";
+        if (fl.i("layers") > 0) c.n_layers = (int32_t)fl.i("layers");
     }
     // infer.go:84-89: maxSeq <= 0 -> 256, clamped to 256 for the Stories decoder
     long long seq = fl.i("seq");

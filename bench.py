@@ -23,6 +23,19 @@ The JSON line also carries:
                 measured in this run;
   cpu_baseline  the CPU restatement of infer.go (oracle/, test infrastructure) timed on
                 one host core over the same decode, with its token stream compared.
+
+`--workload` selects one of the other measured configurations instead (same JSON contract,
+each with its own roofline and a bounded CPU sample):
+  prefill      Stories110M EvalLogits forward, S = 256 (ids seed 2), α = 1/sqrt(24): MFMA-bound;
+               achieved = forward FLOPs / device time; CPU: the oracle's channel-first forward
+               on up to 16 host threads (the reference's GOMAXPROCS-parallel path).
+  w8a8         Stories110M W8A8 greedy decode, 16-id prompt + 128 new: HBM-bound; CPU: the
+               oracle's W8A8 decoder on one core.
+  qwen-decode  Qwen3-0.6B-shaped bf16 greedy decode, 32-id prompt (seed 3) + 256 new:
+               HBM-bound; CPU: the oracle decoder on one core over a prefix of the same decode.
+  batch        Qwen3-0.6B-shaped, 32 sequences x (1024-id prompt, seed 4) + 128 greedy steps:
+               HBM/KV-bound; value = generated tokens per second of the decode steps;
+               CPU: the oracle decoder on one core over a short prefix of sequence 0.
 """
 import argparse
 import json
@@ -56,15 +69,11 @@ def traffic_per_launch():
         return None
 
 
-def gpu_leg(steps, warmup):
-    """Runs the timed decodes in the host program and returns its JSON result."""
+def run_cli(args):
+    """Runs the host program with `args` and returns its JSON result."""
     if not os.path.exists(CLI):
         raise SystemExit(f"{CLI} is not built: run `make -C {PKG}` (or __graft_entry__.build())")
-    cmd = [CLI, "-shape", "stories110m", "-dtype", "fp16", "-synthetic-seed", "0",
-           "-synthetic-std", "0.02", "-prompt-len", str(PROMPT_LEN), "-prompt-seed", "1",
-           "-max-new", str(NEW_TOKENS), "-bench-steps", str(steps), "-bench-warmup", str(warmup),
-           "-copy-calibrate", str(COPY_BYTES)]
-    p = subprocess.run(cmd, capture_output=True, text=True)
+    p = subprocess.run([CLI] + [str(a) for a in args], capture_output=True, text=True)
     sys.stderr.write(p.stderr)
     result = None
     for line in p.stdout.splitlines():
@@ -81,6 +90,14 @@ def gpu_leg(steps, warmup):
     if result is None:
         raise SystemExit("stories-generate printed no result")
     return result
+
+
+def gpu_leg(steps, warmup):
+    """Runs the timed decodes in the host program and returns its JSON result."""
+    return run_cli(["-shape", "stories110m", "-dtype", "fp16", "-synthetic-seed", "0",
+                    "-synthetic-std", "0.02", "-prompt-len", PROMPT_LEN, "-prompt-seed", "1",
+                    "-max-new", NEW_TOKENS, "-bench-steps", steps, "-bench-warmup", warmup,
+                    "-copy-calibrate", COPY_BYTES])
 
 
 def cpu_baseline(gpu_tokens):
@@ -109,18 +126,223 @@ def cpu_baseline(gpu_tokens):
     }
 
 
+def host_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def decode_line(r, steps, metric, workload, dtype, data, config, cpu):
+    """JSON line of a greedy-decode workload measured by the host program's -bench-steps."""
+    gen_tokens = sum(r["generated"])
+    forwards = sum(r["forwards"])
+    gpu_ms = sum(r["gpu_ms"])
+    bytes_total = sum(b * f for b, f in zip(r["bytes_per_forward_mean"], r["forwards"]))
+    wall = r["wall_s"]
+    launch_ms = gpu_ms / steps
+    bytes_launch = bytes_total / steps
+    achieved = bytes_launch / (launch_ms / 1e3) / 1e9 if gpu_ms > 0 else 0.0
+    persistent = bool(r["persistent"])
+    line = {
+        "metric": metric, "value": round(gen_tokens / wall, 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": r["warmup"], "ms_per_step": round(wall * 1e3 / steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": data, "config": dict(workload=workload, **config),
+        "roofline": {
+            "kernel": ("k_decode_persistent (one launch = one whole decode)" if persistent
+                       else "per-stage decode kernels (all launches of one decode)"),
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "bytes_per_launch": round(bytes_launch), "launch_ms": round(launch_ms, 4),
+            "forwards_per_launch": forwards // steps,
+            "us_per_forward": round(gpu_ms * 1e3 / max(forwards, 1), 3),
+        },
+    }
+    if cpu is not None:
+        line["cpu_baseline"] = cpu(r["tokens"])
+    return line
+
+
+def workload_w8a8(args):
+    r = run_cli(["-shape", "stories110m", "-dtype", "w8a8", "-synthetic-seed", "0",
+                 "-synthetic-std", "0.02", "-prompt-len", PROMPT_LEN, "-prompt-seed", "1",
+                 "-max-new", NEW_TOKENS, "-bench-steps", args.steps, "-bench-warmup", args.warmup])
+
+    def cpu(gpu_tokens):
+        import oracle
+        import stories_hip as sh
+        cfg = sh.stories110m_config()
+        w = sh.synth_weights(cfg, seed=0, std=0.02)
+        prompt = sh.synth_tokens(PROMPT_LEN, 1, cfg.vocab)
+        dec = oracle.Decoder(oracle.config_from(cfg, w8a8=True), w.rounded(sh.SH_DTYPE_W8A8), threads=1)
+        t0 = time.perf_counter()
+        toks, _, _ = dec.greedy_decode(prompt, NEW_TOKENS)
+        dt = time.perf_counter() - t0
+        gen = len(toks) - len(prompt)
+        return {"value": round(gen / dt, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+                "sample": f"full workload: {len(prompt)}-id prompt + {gen} new tokens, C restatement of "
+                          f"infer.go with the W8A8 matVec, 1 thread, {dt:.2f} s",
+                "tokens_match_gpu": toks.tolist() == gpu_tokens}
+
+    return decode_line(r, args.steps, "batch-1 W8A8 decode tokens/sec (Stories110M)",
+                       "Stories110M W8A8 batch-1 greedy decode, 16-id prompt + 128 new tokens", "int8",
+                       "synthetic: N(0,0.02) weights seed 0, per-row int8 + fp32 scales, 16-id prompt seed 1",
+                       {"layers": 12, "dim": 768, "vocab": 32000, "batch": 1, "prompt_tokens": PROMPT_LEN,
+                        "new_tokens": NEW_TOKENS, "kv_cache": "fp32", "parallelism": "none (1 GPU)"},
+                       None if args.no_cpu_baseline else cpu)
+
+
+QWEN_PROMPT, QWEN_NEW, QWEN_CPU_NEW = 32, 256, 4
+
+
+def workload_qwen_decode(args):
+    r = run_cli(["-shape", "qwen3-0.6b", "-dtype", "bf16", "-synthetic-seed", "3",
+                 "-synthetic-std", "0.02", "-seq", QWEN_PROMPT + QWEN_NEW, "-prompt-len", QWEN_PROMPT,
+                 "-prompt-seed", "3", "-max-new", QWEN_NEW, "-bench-steps", args.steps,
+                 "-bench-warmup", args.warmup])
+
+    def cpu(gpu_tokens):
+        import oracle
+        import stories_hip as sh
+        cfg = sh.qwen3_06b_config()
+        cfg.max_seq = QWEN_PROMPT + QWEN_NEW
+        w = sh.synth_weights(cfg, seed=3, std=0.02).rounded(sh.SH_DTYPE_BF16)
+        prompt = sh.synth_tokens(QWEN_PROMPT, 3, cfg.vocab)
+        dec = oracle.Decoder(oracle.config_from(cfg), w, threads=1)
+        t0 = time.perf_counter()
+        toks, _, _ = dec.greedy_decode(prompt, QWEN_CPU_NEW)
+        dt = time.perf_counter() - t0
+        forwards = len(toks) - 1
+        return {"value": round(forwards / dt, 3), "unit": "token forwards/s", "cores": 1, "kind": "port",
+                "sample": f"{len(prompt)}-id prompt + {QWEN_CPU_NEW} new tokens of the same decode "
+                          f"({forwards} token forwards, the oracle decoder, 1 thread, {dt:.2f} s)",
+                "tokens_match_gpu": toks.tolist() == gpu_tokens[:len(toks)]}
+
+    return decode_line(r, args.steps, "batch-1 decode tokens/sec (Qwen3-0.6B-shaped)",
+                       "Qwen3-0.6B-shaped bf16 batch-1 greedy decode, 32-id prompt + 256 new tokens", "bf16",
+                       "synthetic: N(0,0.02) weights seed 3 (bf16), 32-id prompt seed 3",
+                       {"layers": 28, "dim": 1024, "heads": 16, "kv_heads": 8, "head_dim": 128,
+                        "hidden": 3072, "vocab": 151936, "batch": 1, "prompt_tokens": QWEN_PROMPT,
+                        "new_tokens": QWEN_NEW, "kv_cache": "bf16", "parallelism": "none (1 GPU)"},
+                       None if args.no_cpu_baseline else cpu)
+
+
+PREFILL_S = 256
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def workload_prefill(args):
+    r = run_cli(["-shape", "stories110m", "-dtype", "fp16", "-synthetic-seed", "0",
+                 "-synthetic-std", "0.02", "-eval-logits", "-prompt-len", PREFILL_S, "-prompt-seed", "2",
+                 "-bench-steps", args.steps, "-bench-warmup", args.warmup])
+    steps = r["steps"]
+    gpu_ms = sum(r["gpu_ms"]) / steps
+    tflops = r["flops"] / (gpu_ms / 1e3) / 1e12
+    line = {
+        "metric": "EvalLogits full-sequence forward tokens/sec (Stories110M, S=256)",
+        "value": round(PREFILL_S * steps / r["wall_s"], 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": r["warmup"], "ms_per_step": round(r["wall_s"] * 1e3 / steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic: N(0,0.02) weights seed 0 (fp16), 256 ids seed 2",
+        "config": {"workload": "Stories110M EvalLogits forward, S=256, residual scale 1/sqrt(24)",
+                   "layers": 12, "dim": 768, "vocab": 32000, "seq": PREFILL_S, "parallelism": "none (1 GPU)"},
+        "roofline": {
+            "kernel": "the forward's kernels together (MFMA GEMMs, MFMA attention, row kernels)",
+            "bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+            "flops_per_forward": r["flops"], "forward_ms": round(gpu_ms, 4),
+        },
+    }
+    if not args.no_cpu_baseline:
+        import oracle
+        import stories_hip as sh
+        cfg = sh.stories110m_config()
+        cfg.residual_scale = 1.0 / (24.0 ** 0.5)
+        w = sh.synth_weights(cfg, seed=0, std=0.02).rounded(sh.SH_DTYPE_F16)
+        toks = sh.synth_tokens(PREFILL_S, 2, cfg.vocab)
+        th = host_threads()
+        t0 = time.perf_counter()
+        logits = oracle.eval_logits_cf(oracle.config_from(cfg), w, toks, threads=th)
+        dt = time.perf_counter() - t0
+        line["cpu_baseline"] = {
+            "value": round(PREFILL_S / dt, 2), "unit": "tokens/s", "cores": th, "kind": "port",
+            "sample": f"the full forward once (C restatement of engine.go:804-842, {th} threads, {dt:.2f} s)",
+            "logits_sum_cpu": float(logits.sum(dtype="float64")), "logits_sum_gpu": r["logits_sum"],
+        }
+    return line
+
+
+BATCH_B, BATCH_PROMPT, BATCH_NEW, BATCH_CPU_NEW = 32, 1024, 128, 2
+
+
+def workload_batch(args):
+    r = run_cli(["-shape", "qwen3-0.6b", "-dtype", "bf16", "-synthetic-seed", "3",
+                 "-synthetic-std", "0.02", "-seq", BATCH_PROMPT + BATCH_NEW, "-batch", BATCH_B,
+                 "-prompt-len", BATCH_PROMPT, "-prompt-seed", "4", "-max-new", BATCH_NEW,
+                 "-bench-steps", args.steps, "-bench-warmup", args.warmup])
+    steps = r["steps"]
+    dec_s = sum(r["decode_ms"]) / 1e3
+    pre_s = sum(r["prefill_ms"]) / 1e3
+    tokens = sum(r["tokens_out"])
+    step_ms = sum(r["decode_ms"]) / max(sum(r["decode_steps"]), 1)
+    achieved = r["bytes_per_step_mean"] / (step_ms / 1e3) / 1e9
+    line = {
+        "metric": "batched decode tokens/sec, aggregate (Qwen3-0.6B-shaped, 32 sequences)",
+        "value": round(tokens / dec_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+        "warmup": args.warmup, "ms_per_step": round(r["wall_s"] * 1e3 / steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: N(0,0.02) weights seed 3 (bf16), 32 prompts of 1024 ids seed 4",
+        "config": {"workload": "Qwen3-0.6B-shaped batched greedy decode, 32 x (1024-id prompt + 128 steps)",
+                   "layers": 28, "dim": 1024, "vocab": 151936, "batch": BATCH_B, "prompt_tokens": BATCH_PROMPT,
+                   "new_tokens": BATCH_NEW, "kv_cache": "bf16", "parallelism": "none (1 GPU)"},
+        "job_tokens_per_s_with_prefill": round(tokens / (dec_s + pre_s), 1),
+        "prefill_ms": round(pre_s * 1e3 / steps, 3),
+        "roofline": {
+            "kernel": "one decode step's kernels together (captured graph)", "bound": "hbm",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "bytes_per_step": r["bytes_per_step_mean"], "step_ms": round(step_ms, 4),
+        },
+    }
+    if not args.no_cpu_baseline:
+        import oracle
+        import stories_hip as sh
+        cfg = sh.qwen3_06b_config()
+        cfg.max_seq = BATCH_PROMPT + BATCH_NEW
+        w = sh.synth_weights(cfg, seed=3, std=0.02).rounded(sh.SH_DTYPE_BF16)
+        prompt = sh.synth_tokens(BATCH_B * BATCH_PROMPT, 4, cfg.vocab)[:16]
+        dec = oracle.Decoder(oracle.config_from(cfg), w, threads=1)
+        t0 = time.perf_counter()
+        toks, _, _ = dec.greedy_decode(prompt, BATCH_CPU_NEW)
+        dt = time.perf_counter() - t0
+        forwards = len(toks) - 1
+        line["cpu_baseline"] = {
+            "value": round(forwards / dt, 3), "unit": "token forwards/s", "cores": 1, "kind": "port",
+            "sample": f"one sequence: the first 16 ids of prompt 0 + {BATCH_CPU_NEW} new tokens "
+                      f"({forwards} token forwards of the oracle decoder, 1 thread, {dt:.2f} s); a CPU "
+                      f"decodes the 32 sequences one forward at a time",
+        }
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "prefill", "w8a8", "qwen-decode", "batch"])
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
               "this build has no multi-GPU path", file=sys.stderr)
         return 2
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    if args.workload != "decode":
+        fn = {"prefill": workload_prefill, "w8a8": workload_w8a8, "qwen-decode": workload_qwen_decode,
+              "batch": workload_batch}[args.workload]
+        print(json.dumps(fn(args)))
+        return 0
 
     r = gpu_leg(args.steps, args.warmup)
     steps = r["steps"]
