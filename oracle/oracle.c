@@ -755,3 +755,479 @@ void or_fill_decode_window(uint16_t *dst, int seq, const int32_t *tokens, int n)
     int start = seq - n;
     for (int i = 0; i < n; i++) dst[start + i] = (uint16_t)tokens[i];
 }
+
+/* ------------------------------------------------------------------------------------ */
+/* Training step: ane/storiesane/train_full.go (CPU path), loss.go, rmsnorm.go,          */
+/* accel_other.go, ane/stories/cpu.go. Channel-first [C, S] like the reference.          */
+
+/* cpu.go:74-95 EmbedBackward: dEmbed[tok*D+d] += dx[d*S+t] for in-range ids */
+void or_embed_backward(float *dembed, const float *dx, const uint16_t *tokens, int vocab,
+                       int dim, int seq) {
+    for (int t = 0; t < seq; t++) {
+        int tok = tokens[t];
+        if (tok >= vocab) continue;
+        for (int d = 0; d < dim; d++) dembed[(size_t)tok * dim + d] += dx[(size_t)d * seq + t];
+    }
+}
+
+/* accel_other.go:11-28 rmsNormCFWithRRMSImpl, keeping the per-token scale */
+static void rms_norm_cf_rrms(float *out, float *rrms, const float *x, const float *w, int dim,
+                             int seq, double eps) {
+    for (int t = 0; t < seq; t++) {
+        double sum = 0;
+        for (int i = 0; i < dim; i++) {
+            double v = (double)x[(size_t)i * seq + t];
+            sum += v * v;
+        }
+        float scale = (float)(1.0 / sqrt(sum / (double)dim + eps));
+        rrms[t] = scale;
+        for (int i = 0; i < dim; i++)
+            out[(size_t)i * seq + t] = x[(size_t)i * seq + t] * scale * w[i];
+    }
+}
+
+/* train_full.go:228-245 linearBackwardDXCF: dx[i*S+t] = sum over o in order of W[o,i]*dy[o*S+t] */
+static void linear_backward_dx_cf(float *dx, const float *w, const float *dy, int out_ch,
+                                  int in_ch, int seq, int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int i = 0; i < in_ch; i++) {
+        float *row = dx + (size_t)i * seq;
+        for (int t = 0; t < seq; t++) row[t] = 0;
+        for (int o = 0; o < out_ch; o++) {
+            float wt = w[(size_t)o * in_ch + i];
+            const float *dyr = dy + (size_t)o * seq;
+            for (int t = 0; t < seq; t++) row[t] += wt * dyr[t];
+        }
+    }
+}
+
+/* train_full.go:199-217 accumLinearGradCF: dW[o,i] += sum over t in order of dy[o*S+t]*x[i*S+t] */
+static void accum_linear_grad_cf(float *dw, const float *dy, const float *x, int out_ch,
+                                 int in_ch, int seq, int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int o = 0; o < out_ch; o++) {
+        const float *dyr = dy + (size_t)o * seq;
+        for (int i = 0; i < in_ch; i++) {
+            const float *xr = x + (size_t)i * seq;
+            float sum = 0;
+            for (int t = 0; t < seq; t++) sum += dyr[t] * xr[t];
+            dw[(size_t)o * in_ch + i] += sum;
+        }
+    }
+}
+
+/* train_full.go:247-301 causalAttentionBackwardCF. Gradients of the post-RoPE q and k (the
+ * reference does not rotate them back); heads are independent, so they run in parallel. */
+static void causal_attention_backward_cf(float *dq, float *dk, float *dv, const float *dout,
+                                         const float *q, const float *k, const float *v,
+                                         int heads, int hd, int seq, int threads) {
+    size_t n = (size_t)heads * hd * seq;
+    memset(dq, 0, sizeof(float) * n);
+    memset(dk, 0, sizeof(float) * n);
+    memset(dv, 0, sizeof(float) * n);
+    float scale = (float)(1.0 / sqrt((double)hd));
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int h = 0; h < heads; h++) {
+        float *scores = (float *)malloc(sizeof(float) * seq);
+        float *probs = (float *)malloc(sizeof(float) * seq);
+        float *dscores = (float *)malloc(sizeof(float) * seq);
+        int base = h * hd;
+        for (int t = 0; t < seq; t++) {
+            float maxv = -INFINITY;
+            for (int s = 0; s <= t; s++) {
+                float sum = 0;
+                for (int i = 0; i < hd; i++)
+                    sum += q[(size_t)(base + i) * seq + t] * k[(size_t)(base + i) * seq + s];
+                scores[s] = sum * scale;
+                if (scores[s] > maxv) maxv = scores[s];
+            }
+            double total = 0;
+            for (int s = 0; s <= t; s++) {
+                double e = exp((double)(scores[s] - maxv));
+                probs[s] = (float)e;
+                total += e;
+            }
+            float inv_total = (float)(1.0 / total);
+            for (int s = 0; s <= t; s++) probs[s] *= inv_total;
+            float ds_sum = 0;
+            for (int s = 0; s <= t; s++) {
+                float dot = 0;
+                for (int i = 0; i < hd; i++)
+                    dot += dout[(size_t)(base + i) * seq + t] * v[(size_t)(base + i) * seq + s];
+                dscores[s] = dot;
+                ds_sum += probs[s] * dot;
+            }
+            for (int s = 0; s <= t; s++) {
+                float ds = probs[s] * (dscores[s] - ds_sum) * scale;
+                for (int i = 0; i < hd; i++) {
+                    size_t qi = (size_t)(base + i) * seq;
+                    dq[qi + t] += ds * k[qi + s];
+                    dk[qi + s] += ds * q[qi + t];
+                    dv[qi + s] += probs[s] * dout[qi + t];
+                }
+            }
+        }
+        free(scores);
+        free(probs);
+        free(dscores);
+    }
+}
+
+/* accel_other.go:77-84 siluBackwardAccel */
+static void silu_backward(float *dh1, float *dh3, const float *dgate, const float *h1,
+                          const float *h3, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        float sig = (float)(1.0 / (1.0 + exp((double)(-h1[i]))));
+        float silu_grad = sig * (1 + h1[i] * (1 - sig));
+        dh1[i] = dgate[i] * h3[i] * silu_grad;
+        dh3[i] = dgate[i] * (h1[i] * sig);
+    }
+}
+
+/* rmsnorm.go:32-47 rmsNormBackwardWithRRMS: dx[i,t] = (dy - x*dot*r^2/d) * r * w (float64),
+ * dot = sum_i dy*x*w, dw[i] += float32(float64(dy*x) * r), t in order for each i. The exact
+ * gradient's second term carries no w[i] factor: this form equals it for unit gains only. */
+void or_rms_norm_backward_cf(float *dx, float *dw, const float *dy, const float *x,
+                             const float *w, const float *rrms, int d, int s, int threads);
+static void rms_norm_backward_cf(float *dx, float *dw, const float *dy, const float *x,
+                                 const float *w, const float *rrms, int d, int s, int threads) {
+    or_rms_norm_backward_cf(dx, dw, dy, x, w, rrms, d, s, threads);
+}
+void or_rms_norm_backward_cf(float *dx, float *dw, const float *dy, const float *x,
+                             const float *w, const float *rrms, int d, int s, int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int t = 0; t < s; t++) {
+        double r = (double)rrms[t];
+        double r2 = (r * r) / (double)d;
+        double dot = 0;
+        for (int i = 0; i < d; i++)
+            dot += (double)(dy[(size_t)i * s + t] * x[(size_t)i * s + t] * w[i]);
+        for (int i = 0; i < d; i++) {
+            double v = (double)dy[(size_t)i * s + t] - (double)x[(size_t)i * s + t] * dot * r2;
+            dx[(size_t)i * s + t] = (float)(v * r * (double)w[i]);
+        }
+    }
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int i = 0; i < d; i++)
+        for (int t = 0; t < s; t++)
+            dw[i] += (float)((double)(dy[(size_t)i * s + t] * x[(size_t)i * s + t]) * (double)rrms[t]);
+}
+
+/* cpu.go:173-253 CrossEntropyLoss: column softmax (float32 exp terms summed in float64),
+ * loss -= log(max(p, 1e-10)) at the target, dLogits = probs - onehot, columns of invalid
+ * targets zeroed, valid columns scaled by 1/valid. Returns the mean loss. */
+float or_cross_entropy_loss(float *dlogits, const float *logits, const uint16_t *targets,
+                            int v, int s) {
+    double loss = 0;
+    int valid = 0;
+    for (int t = 0; t < s; t++) {
+        float mx = logits[t];
+        for (int i = 1; i < v; i++)
+            if (logits[(size_t)i * s + t] > mx) mx = logits[(size_t)i * s + t];
+        double sum = 0;
+        for (int i = 0; i < v; i++) {
+            float e = (float)exp((double)(logits[(size_t)i * s + t] - mx));
+            dlogits[(size_t)i * s + t] = e;
+            sum += (double)e;
+        }
+        float inv = (float)(1.0 / sum);
+        int tgt = targets[t];
+        for (int i = 0; i < v; i++) dlogits[(size_t)i * s + t] *= inv;
+        if (tgt < 0 || tgt >= v) {
+            for (int i = 0; i < v; i++) dlogits[(size_t)i * s + t] = 0;
+            continue;
+        }
+        float p = dlogits[(size_t)tgt * s + t];
+        if (p < 1e-10f) p = 1e-10f;
+        loss -= log((double)p);
+        dlogits[(size_t)tgt * s + t] -= 1;
+        valid++;
+    }
+    if (valid == 0) return 0;
+    float inv_valid = (float)(1.0 / (double)valid);
+    for (int t = 0; t < s; t++) {
+        int tgt = targets[t];
+        if (tgt < 0 || tgt >= v) continue;
+        for (int i = 0; i < v; i++) dlogits[(size_t)i * s + t] *= inv_valid;
+    }
+    return (float)(loss / (double)valid);
+}
+
+/* cpu.go:306-333 MatMulEmbedTScale: dx[d*S+t] = (sum over v in order of E[v,d]*dL[v*S+t]) * scale */
+static void matmul_embed_t_scale(float *dx, const float *embed, const float *dl, int vocab,
+                                 int dim, int seq, float scale, int threads) {
+    if (scale == 0) {
+        memset(dx, 0, sizeof(float) * (size_t)dim * seq);
+        return;
+    }
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int d = 0; d < dim; d++) {
+        float *acc = dx + (size_t)d * seq;
+        for (int t = 0; t < seq; t++) acc[t] = 0;
+        for (int vv = 0; vv < vocab; vv++) {
+            float wv = embed[(size_t)vv * dim + d];
+            const float *dlv = dl + (size_t)vv * seq;
+            for (int t = 0; t < seq; t++) acc[t] += wv * dlv[t];
+        }
+        for (int t = 0; t < seq; t++) acc[t] = acc[t] * scale;
+    }
+}
+
+/* train_full.go:525-587 compactEmbedGrad with cpu.go:339-358 MatMulGradEmbedScale: the
+ * classifier's embedding gradient, rows of the distinct in-range target ids only,
+ * g[v,d] = (sum over t in order of dL[v*S+t]*x[d*S+t]) * scale; every other row 0. The full
+ * product replaces it when the distinct ids exceed half of stories.Vocab (32000). */
+static void compact_embed_grad(float *gembed, const float *dl, const float *xnorm,
+                               const uint16_t *targets, int vocab, int dim, int seq,
+                               float scale, int threads) {
+    memset(gembed, 0, sizeof(float) * (size_t)vocab * dim);
+    if (scale == 0) return;
+    unsigned char *seen = (unsigned char *)calloc((size_t)vocab, 1);
+    int *rows = (int *)malloc(sizeof(int) * (size_t)(seq > 0 ? seq : 1));
+    int n = 0;
+    for (int t = 0; t < seq; t++) {
+        int tok = targets[t];
+        if (tok >= vocab || seen[tok]) continue;
+        seen[tok] = 1;
+        rows[n++] = tok;
+    }
+    int full = n <= 0 || n > 32000 / 2;
+    int nr = full ? vocab : n;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int r = 0; r < nr; r++) {
+        int vv = full ? r : rows[r];
+        for (int d = 0; d < dim; d++) {
+            float sum = 0;
+            for (int t = 0; t < seq; t++)
+                sum += dl[(size_t)vv * seq + t] * xnorm[(size_t)d * seq + t];
+            gembed[(size_t)vv * dim + d] = sum * scale;
+        }
+    }
+    free(seen);
+    free(rows);
+}
+
+/* train_full.go:926-969 adamBiasCorrectionInv + adamUpdateCFWithInv */
+static void adam_update(float *w, const float *g, float *m, float *v, size_t n, float lr,
+                        float b1, float b2, float eps, float wd, float inv_bc1, float inv_bc2) {
+    for (size_t i = 0; i < n; i++) {
+        m[i] = b1 * m[i] + (1 - b1) * g[i];
+        v[i] = b2 * v[i] + (1 - b2) * g[i] * g[i];
+        float mh = m[i] * inv_bc1;
+        float vh = v[i] * inv_bc2;
+        float update = mh / ((float)sqrt((double)vh) + eps);
+        if (wd != 0) update += wd * w[i];
+        w[i] -= lr * update;
+    }
+}
+
+static void scale_slice(float *v, size_t n, float s) {
+    for (size_t i = 0; i < n; i++) v[i] *= s;
+}
+
+static double sum_squares(const float *v, size_t n) {
+    double s = 0;
+    for (size_t i = 0; i < n; i++) s += (double)v[i] * (double)v[i];
+    return s;
+}
+
+/* Tensors of one layer in the order or_train_layer lists them, with their element counts. */
+static void train_layer_tensors(const or_config *cfg, or_train_layer *l, float **p, size_t *n) {
+    size_t D = cfg->dim, F = cfg->hidden;
+    p[0] = l->wq; n[0] = D * D;
+    p[1] = l->wk; n[1] = D * D;
+    p[2] = l->wv; n[2] = D * D;
+    p[3] = l->wo; n[3] = D * D;
+    p[4] = l->w1; n[4] = F * D;
+    p[5] = l->w2; n[5] = D * F;
+    p[6] = l->w3; n[6] = F * D;
+    p[7] = l->rms_att; n[7] = D;
+    p[8] = l->rms_ffn; n[8] = D;
+}
+
+float or_train_step(const or_config *cfg, or_train_params *p, or_train_params *m,
+                    or_train_params *v, or_train_params *grads, const or_train_hparams *hp,
+                    int step_t, const uint16_t *input, const uint16_t *target, int seq,
+                    int apply, int threads) {
+    const int D = cfg->dim, F = cfg->hidden, H = cfg->n_heads, hd = cfg->head_dim;
+    const int V = cfg->vocab, L = cfg->n_layers;
+    const size_t S = (size_t)seq, DS = (size_t)D * S, FS = (size_t)F * S;
+    const float alpha = cfg->residual_scale;
+    const double eps = cfg->norm_eps;
+    /* per-layer caches (train_full.go:46-70 newLayerCache) */
+    float *cache = (float *)malloc(sizeof(float) * (size_t)L * (11 * DS + 3 * FS + 2 * S));
+    float *c = cache;
+#define TAKE(n) (c += (n), c - (n))
+    float *rc = (float *)malloc(sizeof(float) * S * (hd / 2));
+    float *rs = (float *)malloc(sizeof(float) * S * (hd / 2));
+    or_rope_tables(rc, rs, seq, hd, cfg->rope_theta);   /* rope.go:5-24 buildRoPETables */
+    typedef struct { float *x, *xn, *q, *k, *v, *att, *x2, *x2n, *h1, *h3, *gate, *ra, *rf; } lc;
+    lc *lcs = (lc *)malloc(sizeof(lc) * L);
+    float *cur = (float *)malloc(sizeof(float) * DS), *next = (float *)malloc(sizeof(float) * DS);
+    float *tmp = (float *)malloc(sizeof(float) * DS);
+    /* forwardTrainingCPU (train_full.go:368-396) */
+    or_embed_lookup_cf(cur, p->embed, V, input, D, seq);
+    for (int l = 0; l < L; l++) {
+        lc *C = &lcs[l];
+        or_train_layer *W = &p->layers[l];
+        C->x = TAKE(DS); C->xn = TAKE(DS); C->q = TAKE(DS); C->k = TAKE(DS); C->v = TAKE(DS);
+        C->att = TAKE(DS); C->x2 = TAKE(DS); C->x2n = TAKE(DS); C->h1 = TAKE(FS); C->h3 = TAKE(FS);
+        C->gate = TAKE(FS); C->ra = TAKE(S); C->rf = TAKE(S);
+        memcpy(C->x, cur, sizeof(float) * DS);
+        rms_norm_cf_rrms(C->xn, C->ra, C->x, W->rms_att, D, seq, eps);
+        linear_cf(C->q, W->wq, C->xn, D, D, seq, threads);
+        linear_cf(C->k, W->wk, C->xn, D, D, seq, threads);
+        rope_cf(C->q, H, hd, seq, rc, rs);
+        rope_cf(C->k, H, hd, seq, rc, rs);
+        linear_cf(C->v, W->wv, C->xn, D, D, seq, threads);
+        causal_attention_cf(C->att, C->q, C->k, C->v, H, H, hd, seq, threads);
+        linear_cf(next, W->wo, C->att, D, D, seq, threads);
+        for (size_t i = 0; i < DS; i++) C->x2[i] = C->x[i] + alpha * next[i];   /* residual.go:19 */
+        rms_norm_cf_rrms(C->x2n, C->rf, C->x2, W->rms_ffn, D, seq, eps);
+        linear_cf(C->h1, W->w1, C->x2n, F, D, seq, threads);
+        linear_cf(C->h3, W->w3, C->x2n, F, D, seq, threads);
+        for (size_t i = 0; i < FS; i++) {                    /* accel_other.go:70-75 */
+            float sig = (float)(1.0 / (1.0 + exp((double)(-C->h1[i]))));
+            C->gate[i] = (C->h1[i] * sig) * C->h3[i];
+        }
+        linear_cf(next, W->w2, C->gate, D, F, seq, threads);
+        for (size_t i = 0; i < DS; i++) next[i] = C->x2[i] + alpha * next[i];
+        float *sw = cur; cur = next; next = sw;
+    }
+    /* runFinalHead, CPU path (train_full.go:435-523) */
+    float *xnf = (float *)malloc(sizeof(float) * DS), *rfin = (float *)malloc(sizeof(float) * S);
+    float *logits = (float *)malloc(sizeof(float) * (size_t)V * S);
+    rms_norm_cf_rrms(xnf, rfin, cur, p->rms_final, D, seq, eps);
+    matmul_vocab_seq(logits, p->embed, xnf, V, D, seq, threads);
+    float loss = or_cross_entropy_loss(logits, logits, target, V, seq);
+    const float grad_scale = hp->loss_scale;   /* scale = 1 (logits already scaled) x loss scale */
+    float *dy = (float *)malloc(sizeof(float) * DS), *dcur = (float *)malloc(sizeof(float) * DS);
+    float *dprev = (float *)malloc(sizeof(float) * DS);
+    or_train_params *g = grads;
+    memset(g->rms_final, 0, sizeof(float) * D);
+    matmul_embed_t_scale(dy, p->embed, logits, V, D, seq, grad_scale, threads);
+    compact_embed_grad(g->embed, logits, xnf, target, V, D, seq, grad_scale, threads);
+    rms_norm_backward_cf(dcur, g->rms_final, dy, cur, p->rms_final, rfin, D, seq, threads);
+    /* backwardAndApply, CPU path (train_full.go:776-848) */
+    float *dout = (float *)malloc(sizeof(float) * DS), *gx2 = (float *)malloc(sizeof(float) * DS);
+    float *dx2s = (float *)malloc(sizeof(float) * DS), *gxn = (float *)malloc(sizeof(float) * DS);
+    float *ggate = (float *)malloc(sizeof(float) * FS), *gh1 = (float *)malloc(sizeof(float) * FS);
+    float *gh3 = (float *)malloc(sizeof(float) * FS), *gatt = (float *)malloc(sizeof(float) * DS);
+    float *gq = (float *)malloc(sizeof(float) * DS), *gk = (float *)malloc(sizeof(float) * DS);
+    float *gv = (float *)malloc(sizeof(float) * DS);
+    for (int l = L - 1; l >= 0; l--) {
+        lc *C = &lcs[l];
+        or_train_layer *W = &p->layers[l], *G = &g->layers[l];
+        float *gt[9];
+        size_t gn[9];
+        train_layer_tensors(cfg, G, gt, gn);
+        for (int i = 0; i < 9; i++) memset(gt[i], 0, sizeof(float) * gn[i]);   /* clearLayerGrad */
+        for (size_t i = 0; i < DS; i++) dout[i] = dcur[i] * alpha;           /* scaleInto */
+        /* backwardFFNCPU (train_full.go:618-627) */
+        memcpy(gx2, dcur, sizeof(float) * DS);
+        linear_backward_dx_cf(ggate, W->w2, dout, D, F, seq, threads);
+        silu_backward(gh1, gh3, ggate, C->h1, C->h3, FS);
+        linear_backward_dx_cf(gxn, W->w1, gh1, F, D, seq, threads);
+        linear_backward_dx_cf(dprev, W->w3, gh3, F, D, seq, threads);
+        for (size_t i = 0; i < DS; i++) gxn[i] += dprev[i];
+        rms_norm_backward_cf(dprev, G->rms_ffn, gxn, C->x2, W->rms_ffn, C->rf, D, seq, threads);
+        for (size_t i = 0; i < DS; i++) gx2[i] += dprev[i];
+        accum_linear_grad_cf(G->w2, dout, C->gate, D, F, seq, threads);
+        accum_linear_grad_cf(G->w1, gh1, C->x2n, F, D, seq, threads);
+        accum_linear_grad_cf(G->w3, gh3, C->x2n, F, D, seq, threads);
+        for (size_t i = 0; i < DS; i++) dx2s[i] = gx2[i] * alpha;
+        /* backwardAttentionCPU (train_full.go:674-693) */
+        linear_backward_dx_cf(gatt, W->wo, dx2s, D, D, seq, threads);
+        causal_attention_backward_cf(gq, gk, gv, gatt, C->q, C->k, C->v, H, hd, seq, threads);
+        linear_backward_dx_cf(gxn, W->wq, gq, D, D, seq, threads);
+        linear_backward_dx_cf(dprev, W->wk, gk, D, D, seq, threads);
+        for (size_t i = 0; i < DS; i++) gxn[i] += dprev[i];
+        linear_backward_dx_cf(dprev, W->wv, gv, D, D, seq, threads);
+        for (size_t i = 0; i < DS; i++) gxn[i] += dprev[i];
+        rms_norm_backward_cf(dprev, G->rms_att, gxn, C->x, W->rms_att, C->ra, D, seq, threads);
+        for (size_t i = 0; i < DS; i++) dprev[i] += gx2[i];
+        accum_linear_grad_cf(G->wo, dx2s, C->att, D, D, seq, threads);
+        accum_linear_grad_cf(G->wq, gq, C->xn, D, D, seq, threads);
+        accum_linear_grad_cf(G->wk, gk, C->xn, D, D, seq, threads);
+        accum_linear_grad_cf(G->wv, gv, C->xn, D, D, seq, threads);
+        float *sw = dcur; dcur = dprev; dprev = sw;
+    }
+    or_embed_backward(g->embed, dcur, input, V, D, seq);
+    /* loss-scale undo, clipping (train_full.go:149-181), Adam (:875-969) */
+    if (hp->loss_scale != 0 && hp->loss_scale != 1) {
+        float inv = (float)(1.0 / (double)hp->loss_scale);
+        for (int l = 0; l < L; l++) {
+            float *gt[9];
+            size_t gn[9];
+            train_layer_tensors(cfg, &g->layers[l], gt, gn);
+            for (int i = 0; i < 9; i++) scale_slice(gt[i], gn[i], inv);
+        }
+        scale_slice(g->rms_final, D, inv);
+        scale_slice(g->embed, (size_t)V * D, inv);
+    }
+    if (hp->grad_clip > 0) {
+        double norm2 = 0;
+        for (int l = 0; l < L; l++) {
+            float *gt[9];
+            size_t gn[9];
+            train_layer_tensors(cfg, &g->layers[l], gt, gn);
+            for (int i = 0; i < 9; i++) norm2 += sum_squares(gt[i], gn[i]);
+        }
+        norm2 += sum_squares(g->rms_final, D);
+        norm2 += sum_squares(g->embed, (size_t)V * D);
+        if (norm2 > 0) {
+            float norm = (float)sqrt(norm2);
+            if (norm > hp->grad_clip) {
+                float sc = hp->grad_clip / norm;
+                for (int l = 0; l < L; l++) {
+                    float *gt[9];
+                    size_t gn[9];
+                    train_layer_tensors(cfg, &g->layers[l], gt, gn);
+                    for (int i = 0; i < 9; i++) scale_slice(gt[i], gn[i], sc);
+                }
+                scale_slice(g->rms_final, D, sc);
+                scale_slice(g->embed, (size_t)V * D, sc);
+            }
+        }
+    }
+    if (apply) {
+        float inv_bc1 = 1 / (float)(1.0 - pow((double)hp->beta1, (double)step_t));
+        float inv_bc2 = 1 / (float)(1.0 - pow((double)hp->beta2, (double)step_t));
+        for (int l = 0; l < L; l++) {
+            float *pw[9], *gw[9], *mw[9], *vw[9];
+            size_t n[9];
+            train_layer_tensors(cfg, &p->layers[l], pw, n);
+            train_layer_tensors(cfg, &g->layers[l], gw, n);
+            train_layer_tensors(cfg, &m->layers[l], mw, n);
+            train_layer_tensors(cfg, &v->layers[l], vw, n);
+            for (int i = 0; i < 9; i++)
+                adam_update(pw[i], gw[i], mw[i], vw[i], n[i], hp->lr, hp->beta1, hp->beta2, hp->eps,
+                            i < 7 ? hp->weight_decay : 0, inv_bc1, inv_bc2);
+        }
+        adam_update(p->rms_final, g->rms_final, m->rms_final, v->rms_final, D, hp->lr, hp->beta1,
+                    hp->beta2, hp->eps, 0, inv_bc1, inv_bc2);
+        adam_update(p->embed, g->embed, m->embed, v->embed, (size_t)V * D, hp->lr, hp->beta1,
+                    hp->beta2, hp->eps, hp->weight_decay, inv_bc1, inv_bc2);
+    }
+#undef TAKE
+    free(cache); free(rc); free(rs); free(lcs); free(cur); free(next); free(tmp); free(xnf);
+    free(rfin); free(logits); free(dy); free(dcur); free(dprev); free(dout); free(gx2); free(dx2s);
+    free(gxn); free(ggate); free(gh1); free(gh3); free(gatt); free(gq); free(gk); free(gv);
+    return loss;
+}
+
+/* engine.go:725-732 drand48Seed / nextFloat64, and Step's window choice (engine.go:307-316):
+ * returns the start of the next (input, target) window of `seq` tokens in a stream of n. */
+uint64_t or_drand48_seed(int64_t seed) { return (((uint64_t)seed & 0xffffffffull) << 16) | 0x330E; }
+double or_drand48_next(uint64_t *state) {
+    *state = (0x5DEECE66Dull * *state + 0xBull) & ((1ull << 48) - 1);
+    return (double)*state / (double)(1ull << 48);
+}
+uint64_t or_train_window(uint64_t *state, int64_t n_tokens, int seq) {
+    uint64_t limit = (uint64_t)(n_tokens - seq - 1), pos = 0;
+    if (limit > 0) {
+        pos = (uint64_t)(or_drand48_next(state) * (double)limit);
+        if (pos >= limit) pos = limit - 1;
+    }
+    return pos;
+}

@@ -103,6 +103,42 @@ void or_linear_cf(float *out, const float *w, const float *in, int out_ch, int i
                   int threads);
 void or_fill_decode_window(uint16_t *dst, int seq, const int32_t *tokens, int n);
 
+/* ---- training step (ane/storiesane/train_full.go CPU path; MHA Stories-shaped models) ---- */
+typedef struct or_train_layer {
+    float *wq, *wk, *wv, *wo, *w1, *w2, *w3, *rms_att, *rms_ffn;
+} or_train_layer;
+typedef struct or_train_params {
+    or_train_layer *layers;   /* n_layers entries */
+    float *embed;             /* [V, D], also the classifier (tied) */
+    float *rms_final;         /* [D] */
+} or_train_params;
+typedef struct or_train_hparams {
+    float lr, beta1, beta2, eps, weight_decay, grad_clip, loss_scale;
+} or_train_hparams;
+/* rmsnorm.go:32-47 rmsNormBackwardWithRRMS over channel-first [d, s] with the forward's
+ * per-token rrms; dw accumulates. */
+void or_rms_norm_backward_cf(float *dx, float *dw, const float *dy, const float *x,
+                             const float *w, const float *rrms, int d, int s, int threads);
+/* cpu.go:74-95 EmbedBackward: dembed [vocab, dim] += dx [dim, seq] at each in-range token row. */
+void or_embed_backward(float *dembed, const float *dx, const uint16_t *tokens, int vocab,
+                       int dim, int seq);
+/* cpu.go:173-253 CrossEntropyLoss over logits [v, s] channel-first; dlogits may equal logits. */
+float or_cross_entropy_loss(float *dlogits, const float *logits, const uint16_t *targets,
+                            int v, int s);
+/* One Engine.Step body without the window choice: forwardTrainingCPU, runFinalHead (CPU
+ * path), backwardAndApply (CPU path, accumulation 1). p holds the fp32 weights (updated in
+ * place when apply != 0), m and v the Adam moments, grads receives the gradients Adam applies
+ * (after the loss-scale undo and clipping); step_t is the 1-based Adam step. Returns the loss. */
+float or_train_step(const or_config *cfg, or_train_params *p, or_train_params *m,
+                    or_train_params *v, or_train_params *grads, const or_train_hparams *hp,
+                    int step_t, const uint16_t *input, const uint16_t *target, int seq,
+                    int apply, int threads);
+/* engine.go:725-732 and :307-316: drand48 state from a seed, its next float64, and the start
+ * of the next training window. */
+uint64_t or_drand48_seed(int64_t seed);
+double or_drand48_next(uint64_t *state);
+uint64_t or_train_window(uint64_t *state, int64_t n_tokens, int seq);
+
 #ifdef __cplusplus
 }
 #endif

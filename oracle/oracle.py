@@ -39,6 +39,22 @@ class OrWeights(C.Structure):
     _fields_ = [("layers", C.POINTER(OrLayer)), ("embed", _F), ("rms_final", _F), ("cls", _F)]
 
 
+class OrTrainLayer(C.Structure):
+    _fields_ = [(k, _F) for k in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att", "rms_ffn")]
+
+
+class OrTrainParams(C.Structure):
+    _fields_ = [("layers", C.POINTER(OrTrainLayer)), ("embed", _F), ("rms_final", _F)]
+
+
+class OrTrainHparams(C.Structure):
+    _fields_ = [(k, C.c_float) for k in ("lr", "beta1", "beta2", "eps", "weight_decay", "grad_clip",
+                                          "loss_scale")]
+
+
+TRAIN_KEYS = ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att", "rms_ffn")
+
+
 _lib = None
 
 
@@ -78,6 +94,15 @@ def load() -> C.CDLL:
         "or_rms_norm_final_cf": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_double]),
         "or_matmul_vocab_seq": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_int, C.c_int]),
         "or_linear_cf": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_int, C.c_int]),
+        "or_rms_norm_backward_cf": (None, [_F, _F, _F, _F, _F, _F, C.c_int, C.c_int, C.c_int]),
+        "or_embed_backward": (None, [_F, _F, C.POINTER(C.c_uint16), C.c_int, C.c_int, C.c_int]),
+        "or_cross_entropy_loss": (C.c_float, [_F, _F, C.POINTER(C.c_uint16), C.c_int, C.c_int]),
+        "or_train_step": (C.c_float, [C.POINTER(OrConfig), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.POINTER(OrTrainHparams), C.c_int, C.POINTER(C.c_uint16),
+                                      C.POINTER(C.c_uint16), C.c_int, C.c_int, C.c_int]),
+        "or_drand48_seed": (C.c_uint64, [C.c_int64]),
+        "or_drand48_next": (C.c_double, [C.POINTER(C.c_uint64)]),
+        "or_train_window": (C.c_uint64, [C.POINTER(C.c_uint64), C.c_int64, C.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -226,6 +251,84 @@ def linear_cf(w: np.ndarray, x_cf: np.ndarray, threads: int = 1) -> np.ndarray:
     out = np.empty((wt.shape[0], x.shape[1]), np.float32)
     load().or_linear_cf(fp(out), fp(wt), fp(x), wt.shape[0], wt.shape[1], x.shape[1], threads)
     return out
+
+
+class TrainParams:
+    """Mutable fp32 training tensors (weights, a gradient set or Adam moments): a list of
+    per-layer dicts keyed like TRAIN_KEYS, plus embed and rms_final, behind or_train_params."""
+
+    def __init__(self, layers, embed, rms_final):
+        self.layers = [{k: np.ascontiguousarray(l[k], np.float32) for k in TRAIN_KEYS} for l in layers]
+        self.embed = np.ascontiguousarray(embed, np.float32)
+        self.rms_final = np.ascontiguousarray(rms_final, np.float32)
+        self._ls = (OrTrainLayer * len(self.layers))()
+        for i, l in enumerate(self.layers):
+            for k in TRAIN_KEYS:
+                setattr(self._ls[i], k, fp(l[k]))
+        self.s = OrTrainParams(C.cast(self._ls, C.POINTER(OrTrainLayer)), fp(self.embed), fp(self.rms_final))
+
+    @classmethod
+    def from_weights(cls, w):
+        return cls(w.layers, w.embed, w.rms_final)
+
+    @classmethod
+    def zeros_like(cls, other):
+        return cls([{k: np.zeros_like(l[k]) for k in TRAIN_KEYS} for l in other.layers],
+                   np.zeros_like(other.embed), np.zeros_like(other.rms_final))
+
+    def tensors(self):
+        """(name, array) pairs in a fixed order."""
+        out = []
+        for i, l in enumerate(self.layers):
+            out += [(f"layers.{i}.{k}", l[k]) for k in TRAIN_KEYS]
+        return out + [("rms_final", self.rms_final), ("embed", self.embed)]
+
+
+def hparams(lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, grad_clip=0.0, loss_scale=256.0):
+    """Engine defaults (engine.go:160-186)."""
+    return OrTrainHparams(lr, beta1, beta2, eps, weight_decay, grad_clip, loss_scale)
+
+
+def train_step(cfg: OrConfig, params: TrainParams, m: TrainParams, v: TrainParams, grads: TrainParams,
+               hp: OrTrainHparams, step_t: int, inp, tgt, apply: bool = True, threads: int = 1) -> float:
+    """or_train_step: one Engine.Step body (train_full.go CPU path) on a given window."""
+    i = np.ascontiguousarray(np.asarray(inp, dtype=np.uint16))
+    t = np.ascontiguousarray(np.asarray(tgt, dtype=np.uint16))
+    assert i.size == t.size
+    return load().or_train_step(C.byref(cfg), C.byref(params.s), C.byref(m.s), C.byref(v.s), C.byref(grads.s),
+                                C.byref(hp), step_t, i.ctypes.data_as(C.POINTER(C.c_uint16)),
+                                t.ctypes.data_as(C.POINTER(C.c_uint16)), i.size, int(apply), threads)
+
+
+def cross_entropy_loss(logits_cf: np.ndarray, targets):
+    """or_cross_entropy_loss: cpu.go:173-253; returns (loss, dlogits)."""
+    lg = np.ascontiguousarray(logits_cf, np.float32)
+    t = np.ascontiguousarray(np.asarray(targets, dtype=np.uint16))
+    d = np.empty_like(lg)
+    loss = load().or_cross_entropy_loss(fp(d), fp(lg), t.ctypes.data_as(C.POINTER(C.c_uint16)),
+                                        lg.shape[0], lg.shape[1])
+    return loss, d
+
+
+def rms_norm_backward_cf(dy_cf, x_cf, w, rrms):
+    """or_rms_norm_backward_cf: rmsnorm.go:32-47; returns (dx [d, s], dw [d])."""
+    dy = np.ascontiguousarray(dy_cf, np.float32)
+    x = np.ascontiguousarray(x_cf, np.float32)
+    g = np.ascontiguousarray(w, np.float32)
+    r = np.ascontiguousarray(rrms, np.float32)
+    dx = np.empty_like(x)
+    dw = np.zeros(x.shape[0], np.float32)
+    load().or_rms_norm_backward_cf(fp(dx), fp(dw), fp(dy), fp(x), fp(g), fp(r), x.shape[0], x.shape[1], 1)
+    return dx, dw
+
+
+def embed_backward(dembed: np.ndarray, dx_cf: np.ndarray, tokens) -> None:
+    """or_embed_backward: cpu.go:74-95, in place on dembed [V, D]."""
+    assert dembed.dtype == np.float32 and dembed.flags.c_contiguous
+    x = np.ascontiguousarray(dx_cf, np.float32)
+    t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint16))
+    load().or_embed_backward(fp(dembed), fp(x), t.ctypes.data_as(C.POINTER(C.c_uint16)),
+                             dembed.shape[0], dembed.shape[1], x.shape[1])
 
 
 def fill_decode_window(seq: int, tokens) -> np.ndarray:
