@@ -1,0 +1,1034 @@
+// sh_train.hip — the storiesane training step (ane/storiesane/engine.go:295-361 Step,
+// train_full.go forwardTrainingCPU / runFinalHead / backwardAndApply) on gfx950, fp32.
+//
+// The reference trains in float32 on the CPU; so does this path: fp32 master weights, fp32
+// activations, and every GEMM on v_mfma_f32_16x16x4_f32 (fp32 operands, exact products, fp32
+// accumulation), so the step tracks the CPU's arithmetic rather than a 16-bit rounding of it.
+// Activations are token-major ([S, C], row t = token t); the reference's channel-first
+// [C, S] layout only changes addressing.
+//
+// Parameters, gradients and the two Adam moments live in four arenas of identical layout:
+// the matrices first (per layer Wq|Wk|Wv rows, Wo, W1|W3 rows, W2; then the embedding, which
+// is also the classifier), then the gains (per layer rms_att, rms_ffn; then rms_final). Adam
+// is two launches, one per region (weight decay applies to the matrices and the embedding,
+// not to the gains: train_full.go:909-919, :955-956).
+//
+// The reference's shortcuts are kept, since the step must match it:
+//   - attention backward (train_full.go:247-301) gives gradients of the post-RoPE q and k,
+//     which feed the projections' gradients without being rotated back;
+//   - the RMSNorm backward (rmsnorm.go:32-47) multiplies its x.dot term by the gain;
+//   - the classifier's embedding gradient covers only the rows of the window's target ids
+//     (compactEmbedGrad, train_full.go:525-587).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "sh_internal.hpp"
+#include "sh_wave.hpp"
+
+namespace sh {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kTT = 256;   // threads of the row kernels
+
+// ---- fp32 MFMA GEMM ----------------------------------------------------------------------
+// C[M, N] = sum_k A(m, k) B(k, n) with A(m, k) = A[m*lda + k] (AK) or A[k*lda + m], and
+// B(k, n) = B[n*ldb + k] (BK) or B[k*ldb + n]. Epilogue: EPI_STORE C = alpha*acc,
+// EPI_RESID C = R + alpha*acc (R row-major with ldc). 64 x 64 tiles of 2 x 2 waves, K in
+// blocks of 16 staged through LDS as [k][m] / [k][n] rows (padded by 16 floats, so the 16
+// lanes of one MFMA operand read and the four k rows hit distinct banks), the next block
+// loaded into registers while the current one is consumed. v_mfma_f32_16x16x4_f32 operands:
+// lane l holds A[row l%16][k l/16] and B[k l/16][column l%16]; the result rows
+// 4*(l/16) + r of column l%16. Leading dimensions and the base pointers are multiples of 4
+// floats; tails in M, N and K are zero-filled.
+enum { EPI_STORE = 0, EPI_RESID = 1 };
+constexpr int kGM = 64, kGN = 64, kGK = 16, kGP = 16;
+
+template <bool AK>
+__device__ __forceinline__ f32x4 gemm_load(const float *A, int lda, int rows, int K, int r0, int k0,
+                                           int tid) {
+    // AK: thread -> (row r0 + tid/4, k k0 + 4*(tid%4) .. +3); else (k k0 + tid/16, rows 4*(tid%16) ..)
+    int r, k;
+    if constexpr (AK) {
+        r = r0 + tid / 4;
+        k = k0 + (tid % 4) * 4;
+        if (r < rows && k + 3 < K) return *(const f32x4 *)(A + (size_t)r * lda + k);
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (r < rows)
+            for (int e = 0; e < 4; e++)
+                if (k + e < K) v[e] = A[(size_t)r * lda + k + e];
+        return v;
+    } else {
+        k = k0 + tid / 16;
+        r = r0 + (tid % 16) * 4;
+        if (k < K && r + 3 < rows) return *(const f32x4 *)(A + (size_t)k * lda + r);
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (k < K)
+            for (int e = 0; e < 4; e++)
+                if (r + e < rows) v[e] = A[(size_t)k * lda + r + e];
+        return v;
+    }
+}
+
+template <bool AK>
+__device__ __forceinline__ void gemm_stage(float (*S)[kGM + kGP], f32x4 v, int tid) {
+    if constexpr (AK) {
+        const int r = tid / 4, k = (tid % 4) * 4;
+        for (int e = 0; e < 4; e++) S[k + e][r] = v[e];
+    } else {
+        *(f32x4 *)&S[tid / 16][(tid % 16) * 4] = v;
+    }
+}
+
+template <bool AK, bool BK, int EPI>
+__global__ __launch_bounds__(256) void k_sgemm(const float *A, int lda, const float *B, int ldb,
+                                               float *C, int ldc, int M, int N, int K, float alpha,
+                                               const float *R) {
+    __shared__ __attribute__((aligned(16))) float As[2][kGK][kGM + kGP];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kGK][kGN + kGP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    const int m0 = blockIdx.y * kGM, n0 = blockIdx.x * kGN;
+    f32x4 acc[2][2];
+    for (int i = 0; i < 2; i++)
+        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 ra = gemm_load<AK>(A, lda, M, K, m0, 0, tid);
+    f32x4 rb = gemm_load<BK>(B, ldb, N, K, n0, 0, tid);
+    gemm_stage<AK>(As[0], ra, tid);
+    gemm_stage<BK>(Bs[0], rb, tid);
+    __syncthreads();
+    int buf = 0;
+    const int lr = lane & 15, lk = lane >> 4;
+    for (int k0 = 0; k0 < K; k0 += kGK) {
+        const bool more = k0 + kGK < K;
+        if (more) {
+            ra = gemm_load<AK>(A, lda, M, K, m0, k0 + kGK, tid);
+            rb = gemm_load<BK>(B, ldb, N, K, n0, k0 + kGK, tid);
+        }
+#pragma unroll
+        for (int kk = 0; kk < kGK; kk += 4) {
+            const float a0 = As[buf][kk + lk][wm + lr], a1 = As[buf][kk + lk][wm + 16 + lr];
+            const float b0 = Bs[buf][kk + lk][wn + lr], b1 = Bs[buf][kk + lk][wn + 16 + lr];
+            acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        if (more) {
+            gemm_stage<AK>(As[buf ^ 1], ra, tid);
+            gemm_stage<BK>(Bs[buf ^ 1], rb, tid);
+        }
+        __syncthreads();
+        buf ^= 1;
+    }
+    for (int i = 0; i < 2; i++)
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn + j * 16 + lr;
+            if (n >= N) continue;
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm + i * 16 + lk * 4 + r;
+                if (m >= M) continue;
+                const size_t o = (size_t)m * ldc + n;
+                if constexpr (EPI == EPI_STORE) C[o] = alpha * acc[i][j][r];
+                else C[o] = R[o] + alpha * acc[i][j][r];
+            }
+        }
+}
+
+// ---- row kernels -------------------------------------------------------------------------
+
+__device__ __forceinline__ double block_sum_d(double v, double *red) {
+    v = wsum_d64(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double s = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) s += red[w];
+    return s;
+}
+
+// cpu.go:41-72 EmbedLookup, token-major: out-of-range ids give a zero row.
+__global__ void k_tr_embed(const float *embed, const uint16_t *tok, int vocab, int D, float *x) {
+    const int t = blockIdx.x, id = tok[t];
+    for (int i = threadIdx.x; i < D; i += blockDim.x)
+        x[(size_t)t * D + i] = id < vocab ? embed[(size_t)id * D + i] : 0.f;
+}
+
+// accel_other.go:11-28 rmsNormCFWithRRMSImpl per row: float64 sum of squares, float32 scale,
+// out = x*scale*w; the scale is kept for the backward.
+__global__ __launch_bounds__(kTT) void k_tr_rmsnorm(const float *x, const float *w, int D, double eps,
+                                                    float *out, float *rrms) {
+    __shared__ double red[kTT / 64];
+    const float *row = x + (size_t)blockIdx.x * D;
+    double ss = 0;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) ss += (double)row[i] * (double)row[i];
+    const double tot = block_sum_d(ss, red);
+    const float scale = (float)(1.0 / sqrt(tot / (double)D + eps));
+    if (threadIdx.x == 0) rrms[blockIdx.x] = scale;
+    for (int i = threadIdx.x; i < D; i += blockDim.x)
+        out[(size_t)blockIdx.x * D + i] = row[i] * scale * w[i];
+}
+
+// rope.go:26-46 on the q and k parts of row t of qkv [S, 3D] (e' = e*c - o*s, o' = o*c + e*s).
+__global__ void k_tr_rope(float *qkv, int D, int hd, const float *cs, const float *sn) {
+    const int t = blockIdx.x, half = hd / 2;
+    for (int p = threadIdx.x; p < D; p += blockDim.x) {   // D pairs: D/2 in q, D/2 in k
+        const int col = 2 * p, i = (col % hd) / 2;
+        const float c = cs[t * half + i], s = sn[t * half + i];
+        float *e = qkv + (size_t)t * 3 * D + col;
+        const float ev = e[0], ov = e[1];
+        e[0] = ev * c - ov * s;
+        e[1] = ov * c + ev * s;
+    }
+}
+
+// forward_common.go:5-33 causalAttentionCF for (query t, head h), one wave: float32 scores
+// summed over the head dims in order, softmax with float64 exp terms and sum (masked keys
+// weigh exactly 0), then att[t] = sum over keys in order of p*v.
+__global__ __launch_bounds__(64) void k_tr_attn_fwd(const float *qkv, int S, int D, int hd, float scale,
+                                                    float *att) {
+    extern __shared__ float sc[];
+    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const size_t ld = 3 * (size_t)D;
+    const float *q = qkv + (size_t)t * ld + h * hd;
+    float mx = -INFINITY;
+    for (int s = lane; s <= t; s += 64) {
+        const float *k = qkv + (size_t)s * ld + D + h * hd;
+        float sum = 0.f;
+        for (int i = 0; i < hd; i++) sum += q[i] * k[i];
+        sum *= scale;
+        sc[s] = sum;
+        mx = fmaxf(mx, sum);
+    }
+    mx = wmax<64>(mx);
+    double tot = 0;
+    for (int s = lane; s <= t; s += 64) {
+        const double e = exp((double)(sc[s] - mx));
+        sc[s] = (float)e;
+        tot += e;
+    }
+    tot = wsum_d64(tot);
+    const float inv = (float)(1.0 / tot);
+    __syncthreads();
+    for (int s = lane; s <= t; s += 64) sc[s] *= inv;
+    __syncthreads();
+    if (lane < hd) {
+        float a = 0.f;
+        for (int s = 0; s <= t; s++) a += sc[s] * qkv[(size_t)s * ld + 2 * D + h * hd + lane];
+        att[(size_t)t * D + h * hd + lane] = a;
+    }
+}
+
+// train_full.go:247-301 for query t, head h: the row's probabilities recomputed as the
+// reference does (float32 scores, max over s <= t, float64 exp and total, float32 inverse),
+// dscore_s = dOut[t] . v[s], dsSum = sum_s p_s*dscore_s (in s order), ds_s =
+// p_s*(dscore_s - dsSum)*scale, dq[t] = sum_s ds_s*k[s]. The row's max, inverse total and
+// dsSum go to `stats` for the key-side kernel.
+__global__ __launch_bounds__(64) void k_tr_attn_bwd_q(const float *qkv, const float *dout, int S, int D,
+                                                      int hd, float scale, float *dqkv, float *stats) {
+    extern __shared__ float sh[];
+    float *pr = sh, *dsc = sh + S;
+    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, H = D / hd;
+    const size_t ld = 3 * (size_t)D;
+    const float *q = qkv + (size_t)t * ld + h * hd;
+    const float *go = dout + (size_t)t * D + h * hd;
+    float mx = -INFINITY;
+    for (int s = lane; s <= t; s += 64) {
+        const float *k = qkv + (size_t)s * ld + D + h * hd;
+        const float *v = qkv + (size_t)s * ld + 2 * D + h * hd;
+        float sum = 0.f, dot = 0.f;
+        for (int i = 0; i < hd; i++) sum += q[i] * k[i];
+        for (int i = 0; i < hd; i++) dot += go[i] * v[i];
+        sum *= scale;
+        pr[s] = sum;
+        dsc[s] = dot;
+        mx = fmaxf(mx, sum);
+    }
+    mx = wmax<64>(mx);
+    double tot = 0;
+    for (int s = lane; s <= t; s += 64) {
+        const double e = exp((double)(pr[s] - mx));
+        pr[s] = (float)e;
+        tot += e;
+    }
+    tot = wsum_d64(tot);
+    const float inv = (float)(1.0 / tot);
+    __syncthreads();
+    for (int s = lane; s <= t; s += 64) pr[s] *= inv;
+    __syncthreads();
+    __shared__ float dss_sh;
+    if (lane == 0) {
+        float d = 0.f;
+        for (int s = 0; s <= t; s++) d += pr[s] * dsc[s];
+        dss_sh = d;
+        float *st = stats + ((size_t)h * S + t) * 3;
+        st[0] = mx;
+        st[1] = inv;
+        st[2] = d;
+    }
+    __syncthreads();
+    const float dss = dss_sh;
+    for (int s = lane; s <= t; s += 64) dsc[s] = pr[s] * (dsc[s] - dss) * scale;
+    __syncthreads();
+    if (lane < hd) {
+        float a = 0.f;
+        for (int s = 0; s <= t; s++) a += dsc[s] * qkv[(size_t)s * ld + D + h * hd + lane];
+        dqkv[(size_t)t * ld + h * hd + lane] = a;
+    }
+    (void)H;
+}
+
+// Key side of train_full.go:247-301 for key s, head h: for every query t >= s the same p and
+// ds as k_tr_attn_bwd_q (same operation order, from the row stats), then dk[s] = sum over t
+// in order of ds*q[t] and dv[s] = sum over t in order of p*dOut[t].
+__global__ __launch_bounds__(64) void k_tr_attn_bwd_kv(const float *qkv, const float *dout, int S, int D,
+                                                       int hd, float scale, const float *stats,
+                                                       float *dqkv) {
+    extern __shared__ float sh[];
+    float *pr = sh, *ds = sh + S;
+    const int s = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const size_t ld = 3 * (size_t)D;
+    const float *k = qkv + (size_t)s * ld + D + h * hd;
+    const float *v = qkv + (size_t)s * ld + 2 * D + h * hd;
+    for (int t = s + lane; t < S; t += 64) {
+        const float *q = qkv + (size_t)t * ld + h * hd;
+        const float *go = dout + (size_t)t * D + h * hd;
+        float sum = 0.f, dot = 0.f;
+        for (int i = 0; i < hd; i++) sum += q[i] * k[i];
+        for (int i = 0; i < hd; i++) dot += go[i] * v[i];
+        sum *= scale;
+        const float *st = stats + ((size_t)h * S + t) * 3;
+        const float p = (float)exp((double)(sum - st[0])) * st[1];
+        pr[t] = p;
+        ds[t] = p * (dot - st[2]) * scale;
+    }
+    __syncthreads();
+    if (lane < hd) {
+        float dk = 0.f, dv = 0.f;
+        for (int t = s; t < S; t++) {
+            dk += ds[t] * qkv[(size_t)t * ld + h * hd + lane];
+            dv += pr[t] * dout[(size_t)t * D + h * hd + lane];
+        }
+        dqkv[(size_t)s * ld + D + h * hd + lane] = dk;
+        dqkv[(size_t)s * ld + 2 * D + h * hd + lane] = dv;
+    }
+}
+
+// accel_other.go:70-75 siluGateForwardAccel on row t of h13 = [h1 | h3] ([S, 2F]).
+__global__ void k_tr_silu_gate(const float *h13, int F, size_t n, float *gate) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t t = i / F, j = i % F;
+        const float h1 = h13[t * 2 * F + j], h3 = h13[t * 2 * F + F + j];
+        const float sig = (float)(1.0 / (1.0 + exp(-(double)h1)));
+        gate[i] = (h1 * sig) * h3;
+    }
+}
+
+// accel_other.go:77-84 siluBackwardAccel: dh13 = [dh1 | dh3] per row.
+__global__ void k_tr_silu_bwd(const float *dgate, const float *h13, int F, size_t n, float *dh13) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t t = i / F, j = i % F;
+        const float h1 = h13[t * 2 * F + j], h3 = h13[t * 2 * F + F + j];
+        const float sig = (float)(1.0 / (1.0 + exp(-(double)h1)));
+        const float sg = sig * (1 + h1 * (1 - sig));
+        dh13[t * 2 * F + j] = dgate[i] * h3 * sg;
+        dh13[t * 2 * F + F + j] = dgate[i] * (h1 * sig);
+    }
+}
+
+// rmsnorm.go:32-47 per row: dot = sum_i dy*x*w (float64), dx = (dy - x*dot*r^2/D)*r*w in float64
+// rounded once.
+__global__ __launch_bounds__(kTT) void k_tr_rms_bwd_dx(const float *dy, const float *x, const float *w,
+                                                       const float *rrms, int D, float *dx) {
+    __shared__ double red[kTT / 64];
+    const size_t o = (size_t)blockIdx.x * D;
+    double dot = 0;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) dot += (double)(dy[o + i] * x[o + i] * w[i]);
+    dot = block_sum_d(dot, red);
+    const double r = (double)rrms[blockIdx.x], r2 = (r * r) / (double)D;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+        const double v = (double)dy[o + i] - (double)x[o + i] * dot * r2;
+        dx[o + i] = (float)(v * r * (double)w[i]);
+    }
+}
+
+// rmsnorm.go:32-47 gain gradient: dw[i] = sum over t in order of float32(float64(dy*x)*r).
+__global__ void k_tr_rms_bwd_dw(const float *dy, const float *x, const float *rrms, int S, int D, float *dw) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= D) return;
+    float acc = 0.f;
+    for (int t = 0; t < S; t++)
+        acc += (float)((double)(dy[(size_t)t * D + i] * x[(size_t)t * D + i]) * (double)rrms[t]);
+    dw[i] = acc;
+}
+
+// cpu.go:173-253 CrossEntropyLoss for row t of logits [S, V] (in place -> dLogits): float32
+// exp terms summed in float64, probabilities, then at the target p (floored at 1e-10) gives
+// -log p and dLogits -= 1; a row with an out-of-range target is zeroed.
+__global__ __launch_bounds__(kTT) void k_tr_ce_rows(float *lg, const uint16_t *tgt, int V, double *row_loss,
+                                                    int *row_valid) {
+    __shared__ double red[kTT / 64];
+    __shared__ float redf[kTT / 64];
+    float *row = lg + (size_t)blockIdx.x * V;
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) mx = fmaxf(mx, row[i]);
+    mx = wmax<64>(mx);
+    if ((threadIdx.x & 63) == 0) redf[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = redf[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) mx = fmaxf(mx, redf[w]);
+    double sum = 0;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) {
+        const float e = (float)exp((double)(row[i] - mx));
+        row[i] = e;
+        sum += (double)e;
+    }
+    sum = block_sum_d(sum, red);
+    const float inv = (float)(1.0 / sum);
+    for (int i = threadIdx.x; i < V; i += blockDim.x) row[i] *= inv;
+    __syncthreads();
+    const int t = tgt[blockIdx.x];
+    if (t >= V) {
+        for (int i = threadIdx.x; i < V; i += blockDim.x) row[i] = 0.f;
+        if (threadIdx.x == 0) {
+            row_loss[blockIdx.x] = 0;
+            row_valid[blockIdx.x] = 0;
+        }
+        return;
+    }
+    if (threadIdx.x == 0) {
+        float p = row[t];
+        if (p < 1e-10f) p = 1e-10f;
+        row_loss[blockIdx.x] = -log((double)p);
+        row[t] -= 1.f;
+        row_valid[blockIdx.x] = 1;
+    }
+}
+
+// The mean loss (float64 sum over rows in order) and 1/valid for the row scaling.
+__global__ void k_tr_ce_total(const double *row_loss, const int *row_valid, int S, float *out) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    double loss = 0;
+    int valid = 0;
+    for (int t = 0; t < S; t++) {
+        loss += row_loss[t];
+        valid += row_valid[t];
+    }
+    out[0] = valid ? (float)(loss / (double)valid) : 0.f;
+    out[1] = valid ? (float)(1.0 / (double)valid) : 0.f;
+}
+
+__global__ void k_tr_scale_rows(float *lg, const int *row_valid, const float *inv_valid, int V) {
+    if (!row_valid[blockIdx.x]) return;
+    const float s = inv_valid[1];
+    for (int i = threadIdx.x; i < V; i += blockDim.x) lg[(size_t)blockIdx.x * V + i] *= s;
+}
+
+// dlc[t][u] = dL[t][ids[u]] (the compact classifier gradient's operand, ld = ldc).
+__global__ void k_tr_gather_cols(const float *dl, int V, const int32_t *ids, int U, int ldc, float *dlc) {
+    const int t = blockIdx.x;
+    for (int u = threadIdx.x; u < ldc; u += blockDim.x)
+        dlc[(size_t)t * ldc + u] = u < U ? dl[(size_t)t * V + ids[u]] : 0.f;
+}
+
+__global__ void k_tr_scatter_rows(const float *gc, const int32_t *ids, int D, float *gembed) {
+    const int u = blockIdx.x;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) gembed[(size_t)ids[u] * D + i] = gc[(size_t)u * D + i];
+}
+
+// cpu.go:74-95 EmbedBackward: rows of the input ids += dx rows, t in order for each column.
+__global__ void k_tr_embed_bwd(const float *dx, const uint16_t *tok, int S, int V, int D, float *gembed) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= D) return;
+    for (int t = 0; t < S; t++)
+        if (tok[t] < V) gembed[(size_t)tok[t] * D + i] += dx[(size_t)t * D + i];
+}
+
+__global__ void k_tr_fill(float *p, size_t n, float v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+__global__ void k_tr_scale(float *p, size_t n, float s) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] *= s;
+}
+
+// out = a + s*b (s = 0: out = a + b as float32 adds)
+__global__ void k_tr_axpy(const float *a, const float *b, float s, int plain_add, size_t n, float *out) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = plain_add ? a[i] + b[i] : a[i] * s;
+}
+
+// Sum of squares of p[0, n) into per-block float64 partials (block order fixed).
+__global__ __launch_bounds__(kTT) void k_tr_sumsq(const float *p, size_t n, double *part) {
+    __shared__ double red[kTT / 64];
+    double s = 0;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        s += (double)p[i] * (double)p[i];
+    s = block_sum_d(s, red);
+    if (threadIdx.x == 0) part[blockIdx.x] = s;
+}
+
+// train_full.go:932-969 adamUpdateCFWithInv, element-wise in float32.
+__global__ void k_tr_adam(float *w, const float *g, float *m, float *v, size_t n, float lr, float b1, float b2,
+                          float eps, float wd, float ibc1, float ibc2) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const float gi = g[i];
+        const float mi = b1 * m[i] + (1 - b1) * gi;
+        const float vi = b2 * v[i] + (1 - b2) * gi * gi;
+        m[i] = mi;
+        v[i] = vi;
+        const float mh = mi * ibc1, vh = vi * ibc2;
+        float up = mh / ((float)sqrt((double)vh) + eps);
+        if (wd != 0) up += wd * w[i];
+        w[i] -= lr * up;
+    }
+}
+
+}  // namespace
+}  // namespace sh
+
+// ---- host side ---------------------------------------------------------------------------
+
+struct sh_trainer {
+    sh_config cfg;
+    sh_train_options opt;
+    int device;
+    hipStream_t stream;
+    int S, D, F, H, hd, V, L;
+    // parameter arenas (weights, gradients, Adam m and v), identical layout
+    size_t n_mat, n_all;
+    float *p, *g, *m, *v;
+    std::vector<size_t> o_qkv, o_wo, o_w13, o_w2, o_ra, o_rf;
+    size_t o_embed, o_rfin;
+    // activations (token-major) and scratch, one allocation
+    void *act;
+    struct Layer {
+        float *x, *xn, *ra, *qkv, *att, *x2, *x2n, *rf, *h13, *gate;
+    };
+    std::vector<Layer> lc;
+    float *xL, *xnf, *rfin, *logits, *dy, *dcur, *dprev, *dout, *gx2, *dx2s, *gxn, *gatt, *ggate,
+        *dh13, *dqkv, *stats, *dlc, *gc, *loss, *cos_t, *sin_t;
+    double *row_loss, *sq_part;
+    int *row_valid;
+    int32_t *ids;
+    uint16_t *tok_in, *tok_tgt;
+    int ldc_u;   // padded compact width
+    std::vector<uint16_t> tokens;
+    uint64_t rng;
+    sh_train_state state;
+    hipEvent_t ev0, ev1;
+    bool uploaded_globals;
+    std::vector<bool> uploaded;
+};
+
+namespace sh {
+namespace {
+
+constexpr int kSqParts = 1024;
+
+template <bool AK, bool BK, int EPI>
+hipError_t sgemm(hipStream_t s, const float *A, int lda, const float *B, int ldb, float *C, int ldc, int M,
+                 int N, int K, float alpha, const float *R = nullptr) {
+    const dim3 grid((N + kGN - 1) / kGN, (M + kGM - 1) / kGM);
+    hipLaunchKernelGGL((k_sgemm<AK, BK, EPI>), grid, dim3(256), 0, s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R);
+    return hipGetLastError();
+}
+
+unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 8192); }
+
+// Forward (train_full.go:368-396) for the window in tok_in, then runFinalHead's CPU path
+// (:435-523): logits, CrossEntropyLoss, dy = E^T dL * loss scale, the compact classifier
+// embedding gradient, the final RMSNorm backward.
+hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale) {
+    hipStream_t s = T->stream;
+    const int S = T->S, D = T->D, F = T->F, hd = T->hd, V = T->V;
+    const float alpha = T->cfg.residual_scale, scale = (float)(1.0 / sqrt((double)hd));
+    const double eps = T->cfg.norm_eps;
+    hipError_t e;
+    float *cur = T->lc[0].x;
+    hipLaunchKernelGGL(k_tr_embed, dim3(S), dim3(256), 0, s, T->p + T->o_embed, T->tok_in, V, D, cur);
+    for (int l = 0; l < T->L; l++) {
+        sh_trainer::Layer &C = T->lc[l];   // C.x == cur: the previous layer wrote it there
+        hipLaunchKernelGGL(k_tr_rmsnorm, dim3(S), dim3(kTT), 0, s, C.x, T->p + T->o_ra[l], D, eps, C.xn, C.ra);
+        if ((e = sgemm<true, true, EPI_STORE>(s, C.xn, D, T->p + T->o_qkv[l], D, C.qkv, 3 * D, S, 3 * D, D, 1.f)))
+            return e;
+        hipLaunchKernelGGL(k_tr_rope, dim3(S), dim3(256), 0, s, C.qkv, D, hd, T->cos_t, T->sin_t);
+        hipLaunchKernelGGL(k_tr_attn_fwd, dim3(S, T->H), dim3(64), sizeof(float) * S, s, C.qkv, S, D, hd, scale,
+                           C.att);
+        if ((e = sgemm<true, true, EPI_RESID>(s, C.att, D, T->p + T->o_wo[l], D, C.x2, D, S, D, D, alpha, C.x)))
+            return e;
+        hipLaunchKernelGGL(k_tr_rmsnorm, dim3(S), dim3(kTT), 0, s, C.x2, T->p + T->o_rf[l], D, eps, C.x2n, C.rf);
+        if ((e = sgemm<true, true, EPI_STORE>(s, C.x2n, D, T->p + T->o_w13[l], D, C.h13, 2 * F, S, 2 * F, D, 1.f)))
+            return e;
+        const size_t nf = (size_t)S * F;
+        hipLaunchKernelGGL(k_tr_silu_gate, dim3(blocks_for(nf)), dim3(256), 0, s, C.h13, F, nf, C.gate);
+        float *next = l + 1 < T->L ? T->lc[l + 1].x : T->xL;
+        if ((e = sgemm<true, true, EPI_RESID>(s, C.gate, F, T->p + T->o_w2[l], F, next, D, S, D, F, alpha, C.x2)))
+            return e;
+        cur = next;
+    }
+    // final head
+    hipLaunchKernelGGL(k_tr_rmsnorm, dim3(S), dim3(kTT), 0, s, T->xL, T->p + T->o_rfin, D, eps, T->xnf, T->rfin);
+    if ((e = sgemm<true, true, EPI_STORE>(s, T->xnf, D, T->p + T->o_embed, D, T->logits, V, S, V, D, 1.f)))
+        return e;
+    hipLaunchKernelGGL(k_tr_ce_rows, dim3(S), dim3(kTT), 0, s, T->logits, T->tok_tgt, V, T->row_loss, T->row_valid);
+    hipLaunchKernelGGL(k_tr_ce_total, dim3(1), dim3(64), 0, s, T->row_loss, T->row_valid, S, T->loss);
+    hipLaunchKernelGGL(k_tr_scale_rows, dim3(S), dim3(256), 0, s, T->logits, T->row_valid, T->loss, V);
+    // dy[t][d] = (sum_v dL[t][v] E[v][d]) * loss scale (MatMulEmbedTScale)
+    if ((e = sgemm<true, false, EPI_STORE>(s, T->logits, V, T->p + T->o_embed, D, T->dy, D, S, D, V, loss_scale)))
+        return e;
+    // classifier embedding gradient on the target rows: gc[u][d] = (sum_t dL[t][ids u] xnf[t][d]) * scale
+    float *gemb = T->g + T->o_embed;
+    hipLaunchKernelGGL(k_tr_fill, dim3(blocks_for((size_t)V * D)), dim3(256), 0, s, gemb, (size_t)V * D, 0.f);
+    if (U > 0) {
+        hipLaunchKernelGGL(k_tr_gather_cols, dim3(S), dim3(256), 0, s, T->logits, V, T->ids, U, T->ldc_u, T->dlc);
+        if ((e = sgemm<false, false, EPI_STORE>(s, T->dlc, T->ldc_u, T->xnf, D, T->gc, D, U, D, S, loss_scale)))
+            return e;
+        hipLaunchKernelGGL(k_tr_scatter_rows, dim3(U), dim3(256), 0, s, T->gc, T->ids, D, gemb);
+    }
+    // final RMSNorm backward: dcur and the rms_final gradient
+    hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->dy, T->xL, T->p + T->o_rfin, T->rfin, D,
+                       T->dcur);
+    hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 255) / 256), dim3(256), 0, s, T->dy, T->xL, T->rfin, S, D,
+                       T->g + T->o_rfin);
+    return hipGetLastError();
+}
+
+// backwardAndApply's layer loop (train_full.go:776-848, CPU path), EmbedBackward, the
+// loss-scale undo, clipping and Adam (:826-847).
+hipError_t tr_backward_apply(sh_trainer *T, float loss_scale, int step_t) {
+    hipStream_t s = T->stream;
+    const int S = T->S, D = T->D, F = T->F, hd = T->hd;
+    const float alpha = T->cfg.residual_scale, scale = (float)(1.0 / sqrt((double)hd));
+    const size_t SD = (size_t)S * D;
+    hipError_t e;
+    for (int l = T->L - 1; l >= 0; l--) {
+        sh_trainer::Layer &C = T->lc[l];
+        hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dcur, T->dcur, alpha, 0, SD, T->dout);
+        // FFN: ggate = dout . W2, (dh1, dh3), gxn = [dh1|dh3] . [W1;W3], RMS backward
+        if ((e = sgemm<true, false, EPI_STORE>(s, T->dout, D, T->p + T->o_w2[l], F, T->ggate, F, S, F, D, 1.f)))
+            return e;
+        const size_t nf = (size_t)S * F;
+        hipLaunchKernelGGL(k_tr_silu_bwd, dim3(blocks_for(nf)), dim3(256), 0, s, T->ggate, C.h13, F, nf, T->dh13);
+        if ((e = sgemm<true, false, EPI_STORE>(s, T->dh13, 2 * F, T->p + T->o_w13[l], D, T->gxn, D, S, D, 2 * F, 1.f)))
+            return e;
+        hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x2, T->p + T->o_rf[l], C.rf, D,
+                           T->dprev);
+        hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 255) / 256), dim3(256), 0, s, T->gxn, C.x2, C.rf, S, D,
+                           T->g + T->o_rf[l]);
+        hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dcur, T->dprev, 0.f, 1, SD, T->gx2);
+        // weight gradients: dW2 = dout^T gate, d[W1;W3] = [dh1|dh3]^T x2n
+        if ((e = sgemm<false, false, EPI_STORE>(s, T->dout, D, C.gate, F, T->g + T->o_w2[l], F, D, F, S, 1.f)))
+            return e;
+        if ((e = sgemm<false, false, EPI_STORE>(s, T->dh13, 2 * F, C.x2n, D, T->g + T->o_w13[l], D, 2 * F, D, S,
+                                                1.f)))
+            return e;
+        hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->gx2, T->gx2, alpha, 0, SD, T->dx2s);
+        // attention: gatt = dx2s . Wo, (dq, dk, dv), gxn = [dq|dk|dv] . [Wq;Wk;Wv], RMS backward
+        if ((e = sgemm<true, false, EPI_STORE>(s, T->dx2s, D, T->p + T->o_wo[l], D, T->gatt, D, S, D, D, 1.f)))
+            return e;
+        hipLaunchKernelGGL(k_tr_attn_bwd_q, dim3(S, T->H), dim3(64), 2 * sizeof(float) * S, s, C.qkv, T->gatt, S,
+                           D, hd, scale, T->dqkv, T->stats);
+        hipLaunchKernelGGL(k_tr_attn_bwd_kv, dim3(S, T->H), dim3(64), 2 * sizeof(float) * S, s, C.qkv, T->gatt,
+                           S, D, hd, scale, T->stats, T->dqkv);
+        if ((e = sgemm<true, false, EPI_STORE>(s, T->dqkv, 3 * D, T->p + T->o_qkv[l], D, T->gxn, D, S, D, 3 * D,
+                                               1.f)))
+            return e;
+        hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x, T->p + T->o_ra[l], C.ra, D,
+                           T->dprev);
+        hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 255) / 256), dim3(256), 0, s, T->gxn, C.x, C.ra, S, D,
+                           T->g + T->o_ra[l]);
+        hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dprev, T->gx2, 0.f, 1, SD, T->dcur);
+        // dWo = dx2s^T att, d[Wq;Wk;Wv] = [dq|dk|dv]^T xn
+        if ((e = sgemm<false, false, EPI_STORE>(s, T->dx2s, D, C.att, D, T->g + T->o_wo[l], D, D, D, S, 1.f)))
+            return e;
+        if ((e = sgemm<false, false, EPI_STORE>(s, T->dqkv, 3 * D, C.xn, D, T->g + T->o_qkv[l], D, 3 * D, D, S,
+                                                1.f)))
+            return e;
+    }
+    hipLaunchKernelGGL(k_tr_embed_bwd, dim3((D + 255) / 256), dim3(256), 0, s, T->dcur, T->tok_in, S, T->V, D,
+                       T->g + T->o_embed);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (loss_scale != 0 && loss_scale != 1) {
+        const float inv = (float)(1.0 / (double)loss_scale);
+        hipLaunchKernelGGL(k_tr_scale, dim3(blocks_for(T->n_all)), dim3(256), 0, s, T->g, T->n_all, inv);
+    }
+    if (T->opt.grad_clip > 0) {
+        hipLaunchKernelGGL(k_tr_sumsq, dim3(kSqParts), dim3(kTT), 0, s, T->g, T->n_all, T->sq_part);
+        std::vector<double> part(kSqParts);
+        if ((e = hipMemcpyAsync(part.data(), T->sq_part, sizeof(double) * kSqParts, hipMemcpyDeviceToHost, s)) ||
+            (e = hipStreamSynchronize(s)))
+            return e;
+        double norm2 = 0;
+        for (double x : part) norm2 += x;
+        if (norm2 > 0) {
+            const float norm = (float)sqrt(norm2);
+            if (norm > T->opt.grad_clip) {
+                const float sc = T->opt.grad_clip / norm;
+                hipLaunchKernelGGL(k_tr_scale, dim3(blocks_for(T->n_all)), dim3(256), 0, s, T->g, T->n_all, sc);
+            }
+        }
+    }
+    const float ibc1 = 1.f / (float)(1.0 - pow((double)T->opt.beta1, (double)step_t));
+    const float ibc2 = 1.f / (float)(1.0 - pow((double)T->opt.beta2, (double)step_t));
+    const sh_train_options &o = T->opt;
+    hipLaunchKernelGGL(k_tr_adam, dim3(blocks_for(T->n_mat)), dim3(256), 0, s, T->p, T->g, T->m, T->v, T->n_mat,
+                       o.lr, o.beta1, o.beta2, o.eps, o.weight_decay, ibc1, ibc2);
+    const size_t ng = T->n_all - T->n_mat;
+    hipLaunchKernelGGL(k_tr_adam, dim3(blocks_for(ng)), dim3(256), 0, s, T->p + T->n_mat, T->g + T->n_mat,
+                       T->m + T->n_mat, T->v + T->n_mat, ng, o.lr, o.beta1, o.beta2, o.eps, 0.f, ibc1, ibc2);
+    return hipGetLastError();
+}
+
+// Distinct in-range target ids in order of first appearance (buildCompactVocab,
+// train_full.go:560-587); an empty list when they exceed half of stories.Vocab (32000).
+std::vector<int32_t> compact_ids(const uint16_t *tgt, int S, int V) {
+    std::vector<int32_t> ids;
+    std::vector<char> seen(V, 0);
+    for (int t = 0; t < S; t++) {
+        const int tok = tgt[t];
+        if (tok >= V || seen[tok]) continue;
+        seen[tok] = 1;
+        ids.push_back(tok);
+    }
+    if ((int)ids.size() > 32000 / 2) ids.clear();
+    return ids;
+}
+
+bool tr_ready(const sh_trainer *T) {
+    if (!T) {
+        set_error("nil trainer");
+        return false;
+    }
+    for (bool u : T->uploaded)
+        if (!u) {
+            set_error("trainer weights are not fully uploaded");
+            return false;
+        }
+    if (!T->uploaded_globals) {
+        set_error("trainer weights are not fully uploaded");
+        return false;
+    }
+    return true;
+}
+
+// One step on a given window: forward, loss, backward, Adam; the loss comes back.
+bool tr_step_window(sh_trainer *T, const uint16_t *in, const uint16_t *tgt, float *loss_out) {
+    (void)hipSetDevice(T->device);
+    const int S = T->S;
+    std::vector<int32_t> ids = compact_ids(tgt, S, T->V);
+    const int U = (int)ids.size();
+    if (!hip_ok(hipMemcpyAsync(T->tok_in, in, 2 * (size_t)S, hipMemcpyHostToDevice, T->stream), "tokens") ||
+        !hip_ok(hipMemcpyAsync(T->tok_tgt, tgt, 2 * (size_t)S, hipMemcpyHostToDevice, T->stream), "targets") ||
+        (U && !hip_ok(hipMemcpyAsync(T->ids, ids.data(), 4 * (size_t)U, hipMemcpyHostToDevice, T->stream), "ids")) ||
+        !hip_ok(hipEventRecord(T->ev0, T->stream), "event"))
+        return false;
+    const int step_t = (int)T->state.adam_t + 1;
+    if (!hip_ok(tr_forward_head(T, U, T->opt.loss_scale), "training forward") ||
+        !hip_ok(tr_backward_apply(T, T->opt.loss_scale, step_t), "training backward") ||
+        !hip_ok(hipEventRecord(T->ev1, T->stream), "event"))
+        return false;
+    float lv[2];
+    if (!hip_ok(hipMemcpyAsync(lv, T->loss, sizeof lv, hipMemcpyDeviceToHost, T->stream), "loss") ||
+        !hip_ok(hipStreamSynchronize(T->stream), "step sync"))
+        return false;
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, T->ev0, T->ev1);
+    T->state.adam_t = (uint32_t)step_t;
+    T->state.last_loss = lv[0];
+    T->state.cum_steps++;
+    T->state.last_step_ms = ms;
+    if (loss_out) *loss_out = lv[0];
+    return true;
+}
+
+}  // namespace
+}  // namespace sh
+
+using namespace sh;
+
+extern "C" {
+
+sh_trainer *sh_trainer_create(const sh_config *cfg, const sh_train_options *opt_in) {
+    if (!cfg) {
+        set_error("sh_trainer_create: nil config");
+        return nullptr;
+    }
+    const sh_config &c = *cfg;
+    if (c.dim <= 0 || c.hidden <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.head_dim <= 0 || c.vocab <= 0 ||
+        c.n_heads * c.head_dim != c.dim || c.n_kv_heads != c.n_heads || c.qk_norm || c.head_dim > 64 ||
+        c.head_dim % 2 || c.dim % 4 || c.hidden % 4 || c.vocab % 4 || c.vocab > 65535) {
+        set_error("sh_trainer_create: the training step needs a Stories-shaped model: n_heads*head_dim == dim, "
+                  "n_kv_heads == n_heads, no qk_norm, even head_dim <= 64, dim/hidden/vocab multiples of 4, "
+                  "vocab <= 65535");
+        return nullptr;
+    }
+    sh_train_options o{};
+    if (opt_in) o = *opt_in;
+    // Open's defaults (engine.go:153-186)
+    if (o.seq <= 0) o.seq = 256;
+    if (o.lr <= 0) o.lr = 3e-4f;
+    if (o.accum_steps <= 0) o.accum_steps = 1;
+    if (o.seed == 0) o.seed = 42;
+    if (o.beta1 <= 0) o.beta1 = 0.9f;
+    if (o.beta2 <= 0) o.beta2 = 0.999f;
+    if (o.eps <= 0) o.eps = 1e-8f;
+    if (o.grad_clip < 0) o.grad_clip = 0;
+    if (o.loss_scale <= 0) o.loss_scale = 256;
+    if (o.accum_steps != 1) {
+        set_error("sh_trainer_create: gradient accumulation (accum_steps > 1) is not supported");
+        return nullptr;
+    }
+    if (o.seq > 4096) {
+        set_error("sh_trainer_create: seq must be <= 4096");
+        return nullptr;
+    }
+    sh_trainer *T = new sh_trainer();
+    T->cfg = c;
+    T->opt = o;
+    T->device = 0;
+    (void)hipGetDevice(&T->device);
+    T->S = o.seq;
+    T->D = c.dim;
+    T->F = c.hidden;
+    T->H = c.n_heads;
+    T->hd = c.head_dim;
+    T->V = c.vocab;
+    T->L = c.n_layers;
+    T->uploaded.assign(T->L, false);
+    T->uploaded_globals = false;
+    const size_t D = T->D, F = T->F, V = T->V, S = T->S;
+    size_t off = 0;
+    for (int l = 0; l < T->L; l++) {
+        T->o_qkv.push_back(off); off += 3 * D * D;
+        T->o_wo.push_back(off); off += D * D;
+        T->o_w13.push_back(off); off += 2 * F * D;
+        T->o_w2.push_back(off); off += D * F;
+    }
+    T->o_embed = off; off += V * D;
+    T->n_mat = off;
+    for (int l = 0; l < T->L; l++) {
+        T->o_ra.push_back(off); off += D;
+        T->o_rf.push_back(off); off += D;
+    }
+    T->o_rfin = off; off += D;
+    T->n_all = off;
+    T->ldc_u = (int)((S + 3) / 4 * 4);
+    // activations: per layer x, xn, qkv, att, x2, x2n, h13, gate, ra, rf; then the head and scratch
+    size_t a = 0;
+    auto take = [&](size_t bytes) { size_t o2 = a; a += (bytes + 255) / 256 * 256; return o2; };
+    struct Off { size_t x, xn, ra, qkv, att, x2, x2n, rf, h13, gate; };
+    std::vector<Off> lo(T->L);
+    for (int l = 0; l < T->L; l++) {
+        lo[l].x = take(4 * S * D); lo[l].xn = take(4 * S * D); lo[l].ra = take(4 * S);
+        lo[l].qkv = take(4 * S * 3 * D); lo[l].att = take(4 * S * D); lo[l].x2 = take(4 * S * D);
+        lo[l].x2n = take(4 * S * D); lo[l].rf = take(4 * S); lo[l].h13 = take(4 * S * 2 * F);
+        lo[l].gate = take(4 * S * F);
+    }
+    const size_t o_xL = take(4 * S * D), o_xnf = take(4 * S * D), o_rfin = take(4 * S), o_lg = take(4 * S * V),
+                 o_dy = take(4 * S * D), o_dcur = take(4 * S * D), o_dprev = take(4 * S * D),
+                 o_dout = take(4 * S * D), o_gx2 = take(4 * S * D), o_dx2s = take(4 * S * D),
+                 o_gxn = take(4 * S * D), o_gatt = take(4 * S * D), o_ggate = take(4 * S * F),
+                 o_dh13 = take(4 * S * 2 * F), o_dqkv = take(4 * S * 3 * D), o_stats = take(4 * 3 * T->H * S),
+                 o_dlc = take(4 * S * T->ldc_u), o_gc = take(4 * S * D), o_loss = take(16),
+                 o_cos = take(4 * S * (T->hd / 2)), o_sin = take(4 * S * (T->hd / 2)), o_rl = take(8 * S),
+                 o_sq = take(8 * kSqParts), o_rv = take(4 * S), o_ids = take(4 * S), o_ti = take(2 * S),
+                 o_tt = take(2 * S);
+    bool ok = hip_ok(hipStreamCreate(&T->stream), "stream") && hip_ok(hipEventCreate(&T->ev0), "event") &&
+              hip_ok(hipEventCreate(&T->ev1), "event") &&
+              hip_ok(hipMalloc(&T->p, 4 * T->n_all), "hipMalloc params") &&
+              hip_ok(hipMalloc(&T->g, 4 * T->n_all), "hipMalloc grads") &&
+              hip_ok(hipMalloc(&T->m, 4 * T->n_all), "hipMalloc adam m") &&
+              hip_ok(hipMalloc(&T->v, 4 * T->n_all), "hipMalloc adam v") &&
+              hip_ok(hipMalloc(&T->act, a), "hipMalloc activations") &&
+              hip_ok(hipMemset(T->p, 0, 4 * T->n_all), "clear") && hip_ok(hipMemset(T->g, 0, 4 * T->n_all), "clear") &&
+              hip_ok(hipMemset(T->m, 0, 4 * T->n_all), "clear") && hip_ok(hipMemset(T->v, 0, 4 * T->n_all), "clear");
+    if (!ok) {
+        sh_trainer_destroy(T);
+        return nullptr;
+    }
+    uint8_t *A = (uint8_t *)T->act;
+    T->lc.resize(T->L);
+    for (int l = 0; l < T->L; l++) {
+        auto &C = T->lc[l];
+        C.x = (float *)(A + lo[l].x); C.xn = (float *)(A + lo[l].xn); C.ra = (float *)(A + lo[l].ra);
+        C.qkv = (float *)(A + lo[l].qkv); C.att = (float *)(A + lo[l].att); C.x2 = (float *)(A + lo[l].x2);
+        C.x2n = (float *)(A + lo[l].x2n); C.rf = (float *)(A + lo[l].rf); C.h13 = (float *)(A + lo[l].h13);
+        C.gate = (float *)(A + lo[l].gate);
+    }
+    T->xL = (float *)(A + o_xL); T->xnf = (float *)(A + o_xnf); T->rfin = (float *)(A + o_rfin);
+    T->logits = (float *)(A + o_lg); T->dy = (float *)(A + o_dy); T->dcur = (float *)(A + o_dcur);
+    T->dprev = (float *)(A + o_dprev); T->dout = (float *)(A + o_dout); T->gx2 = (float *)(A + o_gx2);
+    T->dx2s = (float *)(A + o_dx2s); T->gxn = (float *)(A + o_gxn); T->gatt = (float *)(A + o_gatt);
+    T->ggate = (float *)(A + o_ggate); T->dh13 = (float *)(A + o_dh13); T->dqkv = (float *)(A + o_dqkv);
+    T->stats = (float *)(A + o_stats); T->dlc = (float *)(A + o_dlc); T->gc = (float *)(A + o_gc);
+    T->loss = (float *)(A + o_loss); T->cos_t = (float *)(A + o_cos); T->sin_t = (float *)(A + o_sin);
+    T->row_loss = (double *)(A + o_rl); T->sq_part = (double *)(A + o_sq); T->row_valid = (int *)(A + o_rv);
+    T->ids = (int32_t *)(A + o_ids); T->tok_in = (uint16_t *)(A + o_ti); T->tok_tgt = (uint16_t *)(A + o_tt);
+    // rope.go:5-24 buildRoPETables(seq, headDim): float64 angles, float32 cos / sin
+    const int half = T->hd / 2;
+    std::vector<float> cs((size_t)S * half), sn((size_t)S * half);
+    for (size_t p = 0; p < S; p++)
+        for (int i = 0; i < half; i++) {
+            const double f = (double)p / pow(c.rope_theta, (double)(2 * i) / (double)T->hd);
+            cs[p * half + i] = (float)cos(f);
+            sn[p * half + i] = (float)sin(f);
+        }
+    if (!hip_ok(hipMemcpy(T->cos_t, cs.data(), 4 * cs.size(), hipMemcpyHostToDevice), "rope tables") ||
+        !hip_ok(hipMemcpy(T->sin_t, sn.data(), 4 * sn.size(), hipMemcpyHostToDevice), "rope tables")) {
+        sh_trainer_destroy(T);
+        return nullptr;
+    }
+    T->rng = (((uint64_t)o.seed & 0xffffffffull) << 16) | 0x330E;   // engine.go:725-727
+    T->state = sh_train_state{};
+    return T;
+}
+
+int sh_trainer_upload_layer(sh_trainer *T, int32_t layer, const float *wq, const float *wk, const float *wv,
+                            const float *wo, const float *w1, const float *w2, const float *w3,
+                            const float *rms_att, const float *rms_ffn) {
+    if (!T || layer < 0 || layer >= T->L || !wq || !wk || !wv || !wo || !w1 || !w2 || !w3 || !rms_att ||
+        !rms_ffn) {
+        set_error("sh_trainer_upload_layer: bad arguments");
+        return -1;
+    }
+    (void)hipSetDevice(T->device);
+    const size_t D = T->D, F = T->F;
+    float *p = T->p;
+    const bool ok =
+        hip_ok(hipMemcpy(p + T->o_qkv[layer], wq, 4 * D * D, hipMemcpyHostToDevice), "upload") &&
+        hip_ok(hipMemcpy(p + T->o_qkv[layer] + D * D, wk, 4 * D * D, hipMemcpyHostToDevice), "upload") &&
+        hip_ok(hipMemcpy(p + T->o_qkv[layer] + 2 * D * D, wv, 4 * D * D, hipMemcpyHostToDevice), "upload") &&
+        hip_ok(hipMemcpy(p + T->o_wo[layer], wo, 4 * D * D, hipMemcpyHostToDevice), "upload") &&
+        hip_ok(hipMemcpy(p + T->o_w13[layer], w1, 4 * F * D, hipMemcpyHostToDevice), "upload") &&
+        hip_ok(hipMemcpy(p + T->o_w13[layer] + F * D, w3, 4 * F * D, hipMemcpyHostToDevice), "upload") &&
+        hip_ok(hipMemcpy(p + T->o_w2[layer], w2, 4 * D * F, hipMemcpyHostToDevice), "upload") &&
+        hip_ok(hipMemcpy(p + T->o_ra[layer], rms_att, 4 * D, hipMemcpyHostToDevice), "upload") &&
+        hip_ok(hipMemcpy(p + T->o_rf[layer], rms_ffn, 4 * D, hipMemcpyHostToDevice), "upload");
+    if (ok) T->uploaded[layer] = true;
+    return ok ? 0 : -1;
+}
+
+int sh_trainer_upload_globals(sh_trainer *T, const float *embed, const float *rms_final) {
+    if (!T || !embed || !rms_final) {
+        set_error("sh_trainer_upload_globals: bad arguments");
+        return -1;
+    }
+    (void)hipSetDevice(T->device);
+    const bool ok = hip_ok(hipMemcpy(T->p + T->o_embed, embed, 4 * (size_t)T->V * T->D, hipMemcpyHostToDevice),
+                           "upload") &&
+                    hip_ok(hipMemcpy(T->p + T->o_rfin, rms_final, 4 * (size_t)T->D, hipMemcpyHostToDevice), "upload");
+    if (ok) T->uploaded_globals = true;
+    return ok ? 0 : -1;
+}
+
+int sh_trainer_set_tokens(sh_trainer *T, const uint16_t *tokens, int64_t n) {
+    if (!T || (!tokens && n)) {
+        set_error("sh_trainer_set_tokens: bad arguments");
+        return -1;
+    }
+    T->tokens.assign(tokens, tokens + n);
+    return 0;
+}
+
+int sh_trainer_step(sh_trainer *T, float *loss) {
+    if (!tr_ready(T)) return -1;
+    const int S = T->S;
+    if ((int64_t)T->tokens.size() < S + 1) {
+        set_error("sh_trainer_step: not enough tokens");   // engine.go:299-301
+        return -1;
+    }
+    // engine.go:307-316: the window start from drand48
+    const uint64_t limit = (uint64_t)(T->tokens.size() - S - 1);
+    uint64_t pos = 0;
+    if (limit > 0) {
+        T->rng = (0x5DEECE66Dull * T->rng + 0xBull) & ((1ull << 48) - 1);
+        pos = (uint64_t)((double)T->rng / (double)(1ull << 48) * (double)limit);
+        if (pos >= limit) pos = limit - 1;
+    }
+    T->state.token_pos = pos + S;
+    return tr_step_window(T, T->tokens.data() + pos, T->tokens.data() + pos + 1, loss) ? 0 : -1;
+}
+
+int sh_trainer_step_window(sh_trainer *T, const uint16_t *input, const uint16_t *target, float *loss) {
+    if (!tr_ready(T)) return -1;
+    if (!input || !target) {
+        set_error("sh_trainer_step_window: bad arguments");
+        return -1;
+    }
+    return tr_step_window(T, input, target, loss) ? 0 : -1;
+}
+
+int sh_trainer_read(const sh_trainer *T, int32_t which, const char *name, float *dst, size_t n) {
+    if (!T || !name || !dst || which < 0 || which > 3) {
+        set_error("sh_trainer_read: bad arguments");
+        return -1;
+    }
+    const float *base = which == SH_TRAIN_PARAMS ? T->p : which == SH_TRAIN_GRADS ? T->g
+                        : which == SH_TRAIN_ADAM_M ? T->m : T->v;
+    const size_t D = T->D, F = T->F;
+    size_t off = 0, len = 0;
+    const std::string s(name);
+    int layer = -1;
+    char key[32] = {0};
+    if (s == "embed") {
+        off = T->o_embed;
+        len = (size_t)T->V * D;
+    } else if (s == "rms_final") {
+        off = T->o_rfin;
+        len = D;
+    } else if (sscanf(name, "layers.%d.%31s", &layer, key) == 2 && layer >= 0 && layer < T->L) {
+        const std::string k(key);
+        if (k == "wq") { off = T->o_qkv[layer]; len = D * D; }
+        else if (k == "wk") { off = T->o_qkv[layer] + D * D; len = D * D; }
+        else if (k == "wv") { off = T->o_qkv[layer] + 2 * D * D; len = D * D; }
+        else if (k == "wo") { off = T->o_wo[layer]; len = D * D; }
+        else if (k == "w1") { off = T->o_w13[layer]; len = F * D; }
+        else if (k == "w3") { off = T->o_w13[layer] + F * D; len = F * D; }
+        else if (k == "w2") { off = T->o_w2[layer]; len = D * F; }
+        else if (k == "rms_att") { off = T->o_ra[layer]; len = D; }
+        else if (k == "rms_ffn") { off = T->o_rf[layer]; len = D; }
+    }
+    if (!len) {
+        set_error(std::string("sh_trainer_read: unknown tensor ") + name);
+        return -1;
+    }
+    if (n != len) {
+        set_error(std::string("sh_trainer_read: ") + name + " has " + std::to_string(len) + " values");
+        return -1;
+    }
+    (void)hipSetDevice(T->device);
+    return hip_ok(hipMemcpy(dst, base + off, 4 * len, hipMemcpyDeviceToHost), "read") ? 0 : -1;
+}
+
+int sh_trainer_state(const sh_trainer *T, sh_train_state *out) {
+    if (!T || !out) {
+        set_error("sh_trainer_state: nil argument");
+        return -1;
+    }
+    *out = T->state;
+    return 0;
+}
+
+void sh_trainer_destroy(sh_trainer *T) {
+    if (!T) return;
+    (void)hipSetDevice(T->device);
+    (void)hipFree(T->p);
+    (void)hipFree(T->g);
+    (void)hipFree(T->m);
+    (void)hipFree(T->v);
+    (void)hipFree(T->act);
+    if (T->stream) (void)hipStreamDestroy(T->stream);
+    if (T->ev0) (void)hipEventDestroy(T->ev0);
+    if (T->ev1) (void)hipEventDestroy(T->ev1);
+    delete T;
+}
+
+}  // extern "C"

@@ -122,6 +122,15 @@ SIGNATURES = {
     "sh_conv_create": (C.c_void_p, [_F, C.c_int32, C.c_int32]),
     "sh_conv_eval": (C.c_int, [C.c_void_p, _F, C.c_int32, _F]),
     "sh_conv_destroy": (None, [C.c_void_p]),
+    "sh_trainer_create": (C.c_void_p, [C.POINTER(ShConfig), C.c_void_p]),
+    "sh_trainer_upload_layer": (C.c_int, [C.c_void_p, C.c_int32] + [_F] * 9),
+    "sh_trainer_upload_globals": (C.c_int, [C.c_void_p, _F, _F]),
+    "sh_trainer_set_tokens": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint16), C.c_int64]),
+    "sh_trainer_step": (C.c_int, [C.c_void_p, _F]),
+    "sh_trainer_step_window": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), _F]),
+    "sh_trainer_read": (C.c_int, [C.c_void_p, C.c_int32, C.c_char_p, _F, C.c_size_t]),
+    "sh_trainer_state": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "sh_trainer_destroy": (None, [C.c_void_p]),
 }
 
 
@@ -481,6 +490,86 @@ class Conv:
     def close(self) -> None:
         if self.h:
             self.lib.sh_conv_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class TrainOptions(C.Structure):
+    """sh_train_options (storiesane.Options); zero fields take the engine's defaults."""
+    _fields_ = [("seq", C.c_int32), ("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float),
+                ("eps", C.c_float), ("weight_decay", C.c_float), ("grad_clip", C.c_float),
+                ("loss_scale", C.c_float), ("seed", C.c_int64), ("accum_steps", C.c_int32)]
+
+
+class TrainState(C.Structure):
+    _fields_ = [("token_pos", C.c_uint64), ("last_loss", C.c_float), ("cum_steps", C.c_uint32),
+                ("adam_t", C.c_uint32), ("last_step_ms", C.c_double)]
+
+
+SH_TRAIN_PARAMS, SH_TRAIN_GRADS, SH_TRAIN_ADAM_M, SH_TRAIN_ADAM_V = 0, 1, 2, 3
+TRAIN_KEYS = ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att", "rms_ffn")
+
+
+class Trainer:
+    """The storiesane training engine (Engine.Step) on the device, fp32."""
+
+    def __init__(self, cfg: ShConfig, **opts):
+        self.lib = load()
+        self.cfg = cfg
+        self.opt = TrainOptions(**opts)
+        self.h = self.lib.sh_trainer_create(C.byref(cfg), C.byref(self.opt))
+        if not self.h:
+            raise ShError(f"sh_trainer_create: {last_error()}")
+        self.seq = self.opt.seq if self.opt.seq > 0 else 256
+
+    def upload(self, w: Weights) -> None:
+        for l, lw in enumerate(w.layers):
+            arrs = [np.ascontiguousarray(lw[k], np.float32) for k in TRAIN_KEYS]
+            _check(self.lib.sh_trainer_upload_layer(self.h, l, *[_fp(a) for a in arrs]),
+                   f"sh_trainer_upload_layer({l})")
+        e = np.ascontiguousarray(w.embed, np.float32)
+        r = np.ascontiguousarray(w.rms_final, np.float32)
+        _check(self.lib.sh_trainer_upload_globals(self.h, _fp(e), _fp(r)), "sh_trainer_upload_globals")
+
+    def set_tokens(self, tokens) -> None:
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint16))
+        self._tokens = t
+        _check(self.lib.sh_trainer_set_tokens(self.h, t.ctypes.data_as(C.POINTER(C.c_uint16)), t.size),
+               "sh_trainer_set_tokens")
+
+    def step(self) -> float:
+        loss = C.c_float(0)
+        _check(self.lib.sh_trainer_step(self.h, C.byref(loss)), "sh_trainer_step")
+        return loss.value
+
+    def step_window(self, inp, tgt) -> float:
+        i = np.ascontiguousarray(np.asarray(inp, dtype=np.uint16))
+        t = np.ascontiguousarray(np.asarray(tgt, dtype=np.uint16))
+        loss = C.c_float(0)
+        _check(self.lib.sh_trainer_step_window(self.h, i.ctypes.data_as(C.POINTER(C.c_uint16)),
+                                               t.ctypes.data_as(C.POINTER(C.c_uint16)), C.byref(loss)),
+               "sh_trainer_step_window")
+        return loss.value
+
+    def read(self, which: int, name: str, shape) -> np.ndarray:
+        out = np.empty(shape, np.float32)
+        _check(self.lib.sh_trainer_read(self.h, which, name.encode(), _fp(out), out.size), "sh_trainer_read")
+        return out
+
+    def state(self) -> dict:
+        st = TrainState()
+        _check(self.lib.sh_trainer_state(self.h, C.byref(st)), "sh_trainer_state")
+        return {"token_pos": st.token_pos, "last_loss": st.last_loss, "cum_steps": st.cum_steps,
+                "adam_t": st.adam_t, "last_step_ms": st.last_step_ms}
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.sh_trainer_destroy(self.h)
             self.h = None
 
     def __del__(self):

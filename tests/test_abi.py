@@ -100,3 +100,13 @@ def test_stateless_seams_reject_unsupported_shapes():
     assert "in_dim % 32 == 0 and out_dim % 64 == 0" in sh.last_error()
     assert lib.sh_conv_eval(None, fp(x), 3, fp(out)) == -1
     lib.sh_conv_destroy(None)
+
+
+def test_trainer_refuses_unsupported_models_and_options():
+    cfg = sh.make_config(dim=64, hidden=128, n_layers=1, n_heads=4, n_kv_heads=2, head_dim=16, vocab=96,
+                         max_seq=32)
+    with pytest.raises(sh.ShError, match="Stories-shaped"):
+        sh.Trainer(cfg, seq=8)
+    cfg.n_kv_heads = 4
+    with pytest.raises(sh.ShError, match="accumulation"):
+        sh.Trainer(cfg, seq=8, accum_steps=4)
