@@ -12,6 +12,9 @@
 //   -synthetic-seed S, -synthetic-std X
 //                                   N(0, X) weights keyed by S (the library's sh_synth_normal
 //                                   streams) when no -model file is given
+//   -train                          with -bench-steps: time the training Step (sh_trainer_step)
+//                                   at -seq tokens over a synthetic stream (-prompt-seed),
+//                                   -lr, window seed -seed; one JSON object
 //   -layers N                       with synthetic weights: only the first N layers of the
 //                                   shape (per-layer kernels unchanged; for short profiles)
 //   -prompt-len N, -prompt-seed S   a synthetic prompt of N uniform ids instead of -prompt-ids
@@ -298,6 +301,8 @@ int main(int argc, char **argv) {
     fl.def("batch", "0");
     fl.def("eval-logits", "false", true);
     fl.def("layers", "0");
+    fl.def("train", "false", true);
+    fl.def("lr", "3e-4");
     fl.parse(argc, argv);
 
     if (!fl.s("detokenize").empty()) {
@@ -394,6 +399,63 @@ int main(int argc, char **argv) {
     }
 
     if (sh_init(0)) fatalf("decode: %s", lib_error());
+    if (fl.b("train")) {
+        // Engine.Step timing (engine.go:295-361): W untimed + K timed steps over drand48
+        // windows of a synthetic token stream. FLOPs per step: the forward's, dX's and dW's
+        // products (6 per weight per token), plus attention over the full S x S square per
+        // head (forward QK^T and P.V, backward four products of the same size).
+        const int steps = (int)fl.i("bench-steps");
+        if (steps <= 0) fatalf("%s", "-train needs -bench-steps");
+        sh_train_options o{};
+        o.seq = (int32_t)c.max_seq;
+        o.lr = (float)fl.f("lr");
+        o.seed = fl.i("seed") ? fl.i("seed") : 42;
+        c.residual_scale = (float)(1.0 / sqrt(2.0 * c.n_layers));   // residual.go:9
+        sh_trainer *tr = sh_trainer_create(&c, &o);
+        if (!tr) fatalf("train: %s", lib_error());
+        for (int l = 0; l < c.n_layers; l++) {
+            const stories::HostLayer &L = w.layers[l];
+            if (sh_trainer_upload_layer(tr, l, L.wq.data(), L.wk.data(), L.wv.data(), L.wo.data(), L.w1.data(),
+                                        L.w2.data(), L.w3.data(), L.rms_att.data(), L.rms_ffn.data()))
+                fatalf("train: %s", lib_error());
+        }
+        if (sh_trainer_upload_globals(tr, w.embed.data(), w.rms_final.data())) fatalf("train: %s", lib_error());
+        std::vector<int32_t> stream32(1 << 16);
+        if (sh_synth_tokens(stream32.data(), stream32.size(), (uint64_t)fl.i("prompt-seed"), c.vocab))
+            fatalf("train: %s", lib_error());
+        std::vector<uint16_t> stream(stream32.begin(), stream32.end());
+        if (sh_trainer_set_tokens(tr, stream.data(), (int64_t)stream.size())) fatalf("train: %s", lib_error());
+        float loss = 0;
+        for (int i = 0; i < fl.i("bench-warmup"); i++)
+            if (sh_trainer_step(tr, &loss)) fatalf("train: %s", lib_error());
+        std::vector<double> ms;
+        std::vector<float> losses;
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < steps; i++) {
+            if (sh_trainer_step(tr, &loss)) fatalf("train: %s", lib_error());
+            sh_train_state st{};
+            sh_trainer_state(tr, &st);
+            ms.push_back(st.last_step_ms);
+            losses.push_back(loss);
+        }
+        const double wall = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        const double S = o.seq, D = c.dim, F = c.hidden;
+        const double flops = 6.0 * S * (c.n_layers * (4.0 * D * D + 3.0 * D * F) + (double)c.vocab * D) +
+                             12.0 * c.n_layers * S * S * D;
+        std::string js = "{\"seq\": " + std::to_string(o.seq) + ", \"steps\": " + std::to_string(steps) +
+                         ", \"warmup\": " + std::to_string(fl.i("bench-warmup")) + ", \"wall_s\": " +
+                         std::to_string(wall) + ", \"step_ms\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(ms[i]);
+        js += "], \"loss\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(losses[i]);
+        char b[64];
+        snprintf(b, sizeof b, "%.6e", flops);
+        js += "], \"flops\": " + std::string(b) + "}";
+        printf("%s\n", js.c_str());
+        fflush(stdout);
+        sh_trainer_destroy(tr);
+        return 0;
+    }
     sh_model *m = open_model(c, dtype, w);
     w = stories::HostWeights();   // device holds the weights now
     Sampler rng{(uint64_t)fl.i("seed")};

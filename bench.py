@@ -36,6 +36,9 @@ each with its own roofline and a bounded CPU sample):
   batch        Qwen3-0.6B-shaped, 32 sequences x (1024-id prompt, seed 4) + 128 greedy steps:
                HBM/KV-bound; value = generated tokens per second of the decode steps;
                CPU: the oracle decoder on one core over a short prefix of sequence 0.
+  train        Stories110M training Step (storiesane Engine.Step), S = 256, fp32, over drand48
+               windows of a synthetic stream: MFMA-bound (fp32 peak); value = trained tokens
+               per second; CPU: the oracle's step on up to 16 host threads.
 """
 import argparse
 import json
@@ -323,6 +326,59 @@ def workload_batch(args):
     return line
 
 
+TRAIN_S = 256
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def workload_train(args):
+    r = run_cli(["-shape", "stories110m", "-synthetic-seed", "0", "-synthetic-std", "0.02", "-train",
+                 "-seq", TRAIN_S, "-prompt-seed", "5", "-bench-steps", args.steps, "-bench-warmup", args.warmup])
+    steps = r["steps"]
+    step_ms = sum(r["step_ms"]) / steps
+    tflops = r["flops"] / (step_ms / 1e3) / 1e12
+    line = {
+        "metric": "training tokens/sec (Stories110M Engine.Step, S=256)",
+        "value": round(TRAIN_S * steps / r["wall_s"], 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+        "warmup": r["warmup"], "ms_per_step": round(r["wall_s"] * 1e3 / steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic: N(0,0.02) fp32 weights seed 0, 65536-id token stream seed 5, drand48 windows seed 42",
+        "config": {"workload": "Stories110M training step (forward, cross-entropy, backward, Adam), S=256",
+                   "layers": 12, "dim": 768, "vocab": 32000, "seq": TRAIN_S, "lr": 3e-4, "loss_scale": 256,
+                   "parallelism": "none (1 GPU)"},
+        "loss_first_last": [r["loss"][0], r["loss"][-1]],
+        "roofline": {
+            "kernel": "the step's kernels together (fp32 MFMA GEMMs, attention, row kernels, Adam)",
+            "bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None,
+            "flops_per_step": r["flops"], "step_ms": round(step_ms, 4),
+        },
+    }
+    if not args.no_cpu_baseline:
+        import oracle
+        import stories_hip as sh
+        cfg = sh.stories110m_config()
+        cfg.residual_scale = 1.0 / (24.0 ** 0.5)
+        w = sh.synth_weights(cfg, seed=0, std=0.02)
+        p = oracle.TrainParams.from_weights(w)
+        m, v, g = (oracle.TrainParams.zeros_like(p) for _ in range(3))
+        stream = sh.synth_tokens(1 << 16, 5, cfg.vocab).astype("uint16")
+        L = oracle.load()
+        st = oracle.C.c_uint64(L.or_drand48_seed(42))
+        pos = L.or_train_window(oracle.C.byref(st), stream.size, TRAIN_S)
+        th = host_threads()
+        t0 = time.perf_counter()
+        loss = oracle.train_step(oracle.config_from(cfg), p, m, v, g, oracle.hparams(), 1,
+                                 stream[pos:pos + TRAIN_S], stream[pos + 1:pos + 1 + TRAIN_S], threads=th)
+        dt = time.perf_counter() - t0
+        line["cpu_baseline"] = {
+            "value": round(TRAIN_S / dt, 2), "unit": "tokens/s", "cores": th, "kind": "port",
+            "sample": f"the first step of the same run (C restatement of train_full.go's CPU path, {th} threads, "
+                      f"{dt:.2f} s)",
+            "loss_cpu": loss,
+        }
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -330,7 +386,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "prefill", "w8a8", "qwen-decode", "batch"])
+                    choices=["decode", "prefill", "w8a8", "qwen-decode", "batch", "train"])
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -340,7 +396,7 @@ def main() -> int:
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     if args.workload != "decode":
         fn = {"prefill": workload_prefill, "w8a8": workload_w8a8, "qwen-decode": workload_qwen_decode,
-              "batch": workload_batch}[args.workload]
+              "batch": workload_batch, "train": workload_train}[args.workload]
         print(json.dumps(fn(args)))
         return 0
 
