@@ -46,7 +46,7 @@ constexpr int kTT = 256;   // threads of the row kernels
 // lane l holds A[row l%16][k l/16] and B[k l/16][column l%16]; the result rows
 // 4*(l/16) + r of column l%16. Leading dimensions and the base pointers are multiples of 4
 // floats; tails in M, N and K are zero-filled.
-enum { EPI_STORE = 0, EPI_RESID = 1 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_PART = 2 };
 constexpr int kGM = 64, kGN = 64, kGK = 16, kGP = 16;
 
 template <bool AK>
@@ -88,7 +88,7 @@ __device__ __forceinline__ void gemm_stage(float (*S)[kGM + kGP], f32x4 v, int t
 template <bool AK, bool BK, int EPI>
 __global__ __launch_bounds__(256) void k_sgemm(const float *A, int lda, const float *B, int ldb,
                                                float *C, int ldc, int M, int N, int K, float alpha,
-                                               const float *R) {
+                                               const float *R, int kc) {
     __shared__ __attribute__((aligned(16))) float As[2][kGK][kGM + kGP];
     __shared__ __attribute__((aligned(16))) float Bs[2][kGK][kGN + kGP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -97,14 +97,17 @@ __global__ __launch_bounds__(256) void k_sgemm(const float *A, int lda, const fl
     f32x4 acc[2][2];
     for (int i = 0; i < 2; i++)
         for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    f32x4 ra = gemm_load<AK>(A, lda, M, K, m0, 0, tid);
-    f32x4 rb = gemm_load<BK>(B, ldb, N, K, n0, 0, tid);
+    // workgroup z covers k in [z*kc, min(K, (z+1)*kc)) (EPI_PART: one partial tile per z)
+    const int kb = blockIdx.z * kc, ke = min(K, kb + kc);
+    K = ke;
+    f32x4 ra = gemm_load<AK>(A, lda, M, K, m0, kb, tid);
+    f32x4 rb = gemm_load<BK>(B, ldb, N, K, n0, kb, tid);
     gemm_stage<AK>(As[0], ra, tid);
     gemm_stage<BK>(Bs[0], rb, tid);
     __syncthreads();
     int buf = 0;
     const int lr = lane & 15, lk = lane >> 4;
-    for (int k0 = 0; k0 < K; k0 += kGK) {
+    for (int k0 = kb; k0 < K; k0 += kGK) {
         const bool more = k0 + kGK < K;
         if (more) {
             ra = gemm_load<AK>(A, lda, M, K, m0, k0 + kGK, tid);
@@ -135,9 +138,23 @@ __global__ __launch_bounds__(256) void k_sgemm(const float *A, int lda, const fl
                 if (m >= M) continue;
                 const size_t o = (size_t)m * ldc + n;
                 if constexpr (EPI == EPI_STORE) C[o] = alpha * acc[i][j][r];
-                else C[o] = R[o] + alpha * acc[i][j][r];
+                else if constexpr (EPI == EPI_RESID) C[o] = R[o] + alpha * acc[i][j][r];
+                else C[(size_t)blockIdx.z * M * ldc + o] = acc[i][j][r];
             }
         }
+}
+
+// C = alpha * (sum over the K ranges in order of the partial tiles [ranges][M][ldc]), plus R
+// when it is given (the residual epilogue).
+__global__ void k_tr_reduce_ranges(const float *P, int ranges, int M, int N, int ldc, float alpha, const float *R,
+                                   float *C) {
+    const size_t n = (size_t)M * N;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
+        const size_t m = e / N, c = e % N, o = m * ldc + c;
+        float v = 0.f;
+        for (int z = 0; z < ranges; z++) v += P[(size_t)z * M * ldc + o];
+        C[o] = R ? R[o] + alpha * v : alpha * v;
+    }
 }
 
 // ---- row kernels -------------------------------------------------------------------------
@@ -319,6 +336,263 @@ __global__ __launch_bounds__(64) void k_tr_attn_bwd_kv(const float *qkv, const f
     }
 }
 
+// ---- blocked attention (S <= kAttnMaxS): 16 rows of one head per workgroup, 64-row
+// blocks staged in LDS; each dot product and each sum over keys or queries runs in the
+// reference's order, so the results equal the one-wave-per-row kernels above.
+constexpr int kAQ = 16;          // queries (or keys) per workgroup
+constexpr int kAB = 64;          // rows per staged block
+constexpr int kAttnMaxS = 256;   // score rows kept in LDS: 2 x 16 x S floats (<= 64 KB dynamic)
+constexpr int kAPad = 68;        // LDS row stride (floats) of a staged block: 16-byte rows, and
+                                 // 16 rows 4 banks apart for the float4 reads
+
+// sum over i in order of a[i]*b[i] (float32, no fusing), four at a time from LDS (hd % 4 == 0)
+__device__ __forceinline__ float dot_lds(const float *a, const float *b, int hd) {
+    float sum = 0.f;
+#pragma unroll 4
+    for (int i = 0; i < hd; i += 4) {
+        const f32x4 x = *(const f32x4 *)(a + i), y = *(const f32x4 *)(b + i);
+        sum += x.x * y.x;
+        sum += x.y * y.y;
+        sum += x.z * y.z;
+        sum += x.w * y.w;
+    }
+    return sum;
+}
+
+// float64 sum over the 16 lanes of a row group (each holding one value), uniform result.
+__device__ __forceinline__ double sum16_d64(double v) {
+    auto step = [](double x, auto ctrl_tag) {
+        constexpr int Cc = decltype(ctrl_tag)::value;
+        const uint64_t b = (uint64_t)__double_as_longlong(x);
+        const uint32_t lo = dpp_u<Cc>((uint32_t)b), hi = dpp_u<Cc>((uint32_t)(b >> 32));
+        return x + __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+    };
+    v = step(v, std::integral_constant<int, kDppXor1>{});
+    v = step(v, std::integral_constant<int, kDppXor2>{});
+    v = step(v, std::integral_constant<int, kDppHalfMirror>{});
+    v = step(v, std::integral_constant<int, kDppMirror>{});
+    return v;
+}
+
+// Stages rows r0 .. r0+nr-1 (nr <= 64; rows at or past n skipped, or zero-filled when
+// `zero`) of columns c0 .. c0+hd-1 of a row-major matrix (row stride ld, hd % 4 == 0) into
+// LDS [nr][kAPad]: every thread issues its (at most four) 16-byte loads before any LDS store,
+// so the loads are in flight together. blockDim.x == 256.
+__device__ __forceinline__ void stage_rows(float *dst, const float *src, size_t ld, int c0, int r0, int n, int hd,
+                                           int nr = kAB, bool zero = false) {
+    const int per = hd / 4, total = nr * per;   // total <= 1024
+    f32x4 v[4];
+    int rr[4], cc[4];
+    bool ok[4], in[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int e = threadIdx.x + 256 * k;
+        rr[k] = e / per;
+        cc[k] = (e % per) * 4;
+        in[k] = e < total;
+        ok[k] = in[k] && r0 + rr[k] < n;
+        v[k] = ok[k] ? *(const f32x4 *)(src + (size_t)(r0 + rr[k]) * ld + c0 + cc[k]) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (ok[k] || (zero && in[k])) *(f32x4 *)(dst + rr[k] * kAPad + cc[k]) = v[k];
+}
+
+// Forward for queries q0 .. q0+15 of head h (forward_common.go:5-33 order): scores per
+// (query, key) summed over the head dims in order, row softmax (float64 exp and total,
+// float32 inverse), att = sum over keys in order of p*v.
+__global__ __launch_bounds__(256) void k_tr_attn_fwd_blk(const float *qkv, int S, int D, int hd, float scale,
+                                                         float *att) {
+    extern __shared__ __attribute__((aligned(16))) float sh[];
+    float *qs = sh, *kv = qs + kAQ * kAPad, *sc = kv + kAB * kAPad;   // sc [16][S]
+    const int q0 = blockIdx.x * kAQ, h = blockIdx.y, tid = threadIdx.x;
+    const size_t ld = 3 * (size_t)D;
+    const int qn = min(kAQ, S - q0), kend = min(S, q0 + kAQ);   // keys 0 .. kend-1
+    stage_rows(qs, qkv, ld, h * hd, q0, S, hd, kAQ, true);
+    const int q = tid / 16, j = tid % 16, t = q0 + q;
+    for (int kb = 0; kb < kend; kb += kAB) {
+        __syncthreads();
+        stage_rows(kv, qkv, ld, D + h * hd, kb, kend, hd);
+        __syncthreads();
+        for (int u = 0; u < kAB / 16; u++) {
+            const int s = kb + j + 16 * u;
+            if (s < kend && q < qn && s <= t) sc[q * S + s] = dot_lds(qs + q * kAPad, kv + (s - kb) * kAPad, hd) * scale;
+        }
+    }
+    __syncthreads();
+    // softmax of row q over keys 0..t: the 16 lanes of the row group share it
+    float mx = -INFINITY;
+    if (q < qn)
+        for (int s = j; s <= t; s += 16) mx = fmaxf(mx, sc[q * S + s]);
+    mx = wmax<16>(mx);
+    double tot = 0;
+    if (q < qn)
+        for (int s = j; s <= t; s += 16) {
+            const double ev = exp((double)(sc[q * S + s] - mx));
+            sc[q * S + s] = (float)ev;
+            tot += ev;
+        }
+    tot = sum16_d64(tot);
+    const float inv = (float)(1.0 / tot);
+    if (q < qn)
+        for (int s = j; s <= t; s += 16) sc[q * S + s] *= inv;
+    // P.V: thread (q, dims j, j+16, ...) sums over keys in order
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < kend; kb += kAB) {
+        __syncthreads();
+        stage_rows(kv, qkv, ld, 2 * D + h * hd, kb, kend, hd);
+        __syncthreads();
+        if (q < qn) {
+            const int se = min(t + 1, min(kend, kb + kAB));
+#pragma unroll 4
+            for (int s = kb; s < se; s++) {
+                const float p = sc[q * S + s];
+                for (int c = 0; c < 4; c++)
+                    if (j + 16 * c < hd) a[c] += p * kv[(s - kb) * kAPad + j + 16 * c];
+            }
+        }
+    }
+    if (q < qn)
+        for (int c = 0; c < 4; c++)
+            if (j + 16 * c < hd) att[(size_t)t * D + h * hd + j + 16 * c] = a[c];
+}
+
+// Query side of train_full.go:247-301 for queries q0 .. q0+15 of head h, in the reference's
+// order (see k_tr_attn_bwd_q); writes dq and the row stats.
+__global__ __launch_bounds__(256) void k_tr_attn_bwd_q_blk(const float *qkv, const float *dout, int S, int D,
+                                                           int hd, float scale, float *dqkv, float *stats) {
+    extern __shared__ __attribute__((aligned(16))) float sh[];
+    float *qs = sh, *gs = qs + kAQ * kAPad, *kv = gs + kAQ * kAPad, *pr = kv + kAB * kAPad, *dsc = pr + kAQ * S;
+    __shared__ float dss_sh[kAQ];
+    const int q0 = blockIdx.x * kAQ, h = blockIdx.y, tid = threadIdx.x;
+    const size_t ld = 3 * (size_t)D;
+    const int qn = min(kAQ, S - q0), kend = min(S, q0 + kAQ);
+    stage_rows(qs, qkv, ld, h * hd, q0, S, hd, kAQ, true);
+    stage_rows(gs, dout, D, h * hd, q0, S, hd, kAQ, true);
+    const int q = tid / 16, j = tid % 16, t = q0 + q;
+    for (int kb = 0; kb < kend; kb += kAB) {   // scores (K blocks), then dscores (V blocks)
+        __syncthreads();
+        stage_rows(kv, qkv, ld, D + h * hd, kb, kend, hd);
+        __syncthreads();
+        for (int u = 0; u < kAB / 16; u++) {
+            const int s = kb + j + 16 * u;
+            if (s < kend && q < qn && s <= t) pr[q * S + s] = dot_lds(qs + q * kAPad, kv + (s - kb) * kAPad, hd) * scale;
+        }
+        __syncthreads();
+        stage_rows(kv, qkv, ld, 2 * D + h * hd, kb, kend, hd);
+        __syncthreads();
+        for (int u = 0; u < kAB / 16; u++) {
+            const int s = kb + j + 16 * u;
+            if (s < kend && q < qn && s <= t) dsc[q * S + s] = dot_lds(gs + q * kAPad, kv + (s - kb) * kAPad, hd);
+        }
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    if (q < qn)
+        for (int s = j; s <= t; s += 16) mx = fmaxf(mx, pr[q * S + s]);
+    mx = wmax<16>(mx);
+    double tot = 0;
+    if (q < qn)
+        for (int s = j; s <= t; s += 16) {
+            const double ev = exp((double)(pr[q * S + s] - mx));
+            pr[q * S + s] = (float)ev;
+            tot += ev;
+        }
+    tot = sum16_d64(tot);
+    const float inv = (float)(1.0 / tot);
+    if (q < qn)
+        for (int s = j; s <= t; s += 16) pr[q * S + s] *= inv;
+    __syncthreads();
+    if (j == 0 && q < qn) {   // dsSum in key order
+        float d = 0.f;
+#pragma unroll 8
+        for (int s = 0; s <= t; s++) d += pr[q * S + s] * dsc[q * S + s];
+        dss_sh[q] = d;
+        float *st = stats + ((size_t)h * S + t) * 3;
+        st[0] = mx;
+        st[1] = inv;
+        st[2] = d;
+    }
+    __syncthreads();
+    if (q < qn) {
+        const float dss = dss_sh[q];
+        for (int s = j; s <= t; s += 16) dsc[q * S + s] = pr[q * S + s] * (dsc[q * S + s] - dss) * scale;
+    }
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < kend; kb += kAB) {   // dq = sum over keys in order of ds*k
+        __syncthreads();
+        stage_rows(kv, qkv, ld, D + h * hd, kb, kend, hd);
+        __syncthreads();
+        if (q < qn) {
+            const int se = min(t + 1, min(kend, kb + kAB));
+#pragma unroll 4
+            for (int s = kb; s < se; s++) {
+                const float d = dsc[q * S + s];
+                for (int c = 0; c < 4; c++)
+                    if (j + 16 * c < hd) a[c] += d * kv[(s - kb) * kAPad + j + 16 * c];
+            }
+        }
+    }
+    if (q < qn)
+        for (int c = 0; c < 4; c++)
+            if (j + 16 * c < hd) dqkv[(size_t)t * ld + h * hd + j + 16 * c] = a[c];
+}
+
+// Key side for keys s0 .. s0+15 of head h (see k_tr_attn_bwd_kv): query blocks of 64 in
+// ascending order, p and ds per (key, query) from the row stats, then dk and dv summed over
+// queries in order.
+__global__ __launch_bounds__(256) void k_tr_attn_bwd_kv_blk(const float *qkv, const float *dout, int S, int D,
+                                                            int hd, float scale, const float *stats,
+                                                            float *dqkv) {
+    __shared__ __attribute__((aligned(16))) float ks[kAQ * kAPad], vs[kAQ * kAPad], qb[kAB * kAPad], gb[kAB * kAPad];
+    __shared__ float pp[kAQ][kAB], dd[kAQ][kAB];
+    const int s0 = blockIdx.x * kAQ, h = blockIdx.y, tid = threadIdx.x;
+    const size_t ld = 3 * (size_t)D;
+    const int sn = min(kAQ, S - s0);
+    stage_rows(ks, qkv, ld, D + h * hd, s0, S, hd, kAQ, true);
+    stage_rows(vs, qkv, ld, 2 * D + h * hd, s0, S, hd, kAQ, true);
+    const int kk = tid / 16, j = tid % 16, s = s0 + kk;
+    float dk[4] = {0.f, 0.f, 0.f, 0.f}, dv[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int tb = s0 - s0 % kAB; tb < S; tb += kAB) {
+        __syncthreads();
+        stage_rows(qb, qkv, ld, h * hd, tb, S, hd);
+        stage_rows(gb, dout, D, h * hd, tb, S, hd);
+        __syncthreads();
+        for (int u = 0; u < kAB / 16; u++) {
+            const int tl = j + 16 * u, t = tb + tl;
+            float p = 0.f, d = 0.f;
+            if (kk < sn && t < S && t >= s) {
+                const float sum = dot_lds(qb + tl * kAPad, ks + kk * kAPad, hd) * scale;
+                const float dot = dot_lds(gb + tl * kAPad, vs + kk * kAPad, hd);
+                const float *st = stats + ((size_t)h * S + t) * 3;
+                p = (float)exp((double)(sum - st[0])) * st[1];
+                d = p * (dot - st[2]) * scale;
+            }
+            pp[kk][tl] = p;
+            dd[kk][tl] = d;
+        }
+        __syncthreads();
+        if (kk < sn) {
+            const int tl0 = max(0, s - tb), tl1 = min(kAB, S - tb);
+#pragma unroll 4
+            for (int tl = tl0; tl < tl1; tl++) {
+                const float p = pp[kk][tl], d = dd[kk][tl];
+                for (int c = 0; c < 4; c++)
+                    if (j + 16 * c < hd) {
+                        dk[c] += d * qb[tl * kAPad + j + 16 * c];
+                        dv[c] += p * gb[tl * kAPad + j + 16 * c];
+                    }
+            }
+        }
+    }
+    if (kk < sn)
+        for (int c = 0; c < 4; c++)
+            if (j + 16 * c < hd) {
+                dqkv[(size_t)s * ld + D + h * hd + j + 16 * c] = dk[c];
+                dqkv[(size_t)s * ld + 2 * D + h * hd + j + 16 * c] = dv[c];
+            }
+}
+
 // accel_other.go:70-75 siluGateForwardAccel on row t of h13 = [h1 | h3] ([S, 2F]).
 __global__ void k_tr_silu_gate(const float *h13, int F, size_t n, float *gate) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
@@ -358,12 +632,24 @@ __global__ __launch_bounds__(kTT) void k_tr_rms_bwd_dx(const float *dy, const fl
 }
 
 // rmsnorm.go:32-47 gain gradient: dw[i] = sum over t in order of float32(float64(dy*x)*r).
-__global__ void k_tr_rms_bwd_dw(const float *dy, const float *x, const float *rrms, int S, int D, float *dw) {
+__global__ __launch_bounds__(64) void k_tr_rms_bwd_dw(const float *dy, const float *x, const float *rrms, int S,
+                                                      int D, float *dw) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= D) return;
     float acc = 0.f;
-    for (int t = 0; t < S; t++)
-        acc += (float)((double)(dy[(size_t)t * D + i] * x[(size_t)t * D + i]) * (double)rrms[t]);
+    int t = 0;
+    for (; t + 8 <= S; t += 8) {   // eight rows' loads in flight, the sum still in row order
+        float a[8], b[8], r[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            a[u] = dy[(size_t)(t + u) * D + i];
+            b[u] = x[(size_t)(t + u) * D + i];
+            r[u] = rrms[t + u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc += (float)((double)(a[u] * b[u]) * (double)r[u]);
+    }
+    for (; t < S; t++) acc += (float)((double)(dy[(size_t)t * D + i] * x[(size_t)t * D + i]) * (double)rrms[t]);
     dw[i] = acc;
 }
 
@@ -441,22 +727,23 @@ __global__ void k_tr_scatter_rows(const float *gc, const int32_t *ids, int D, fl
     for (int i = threadIdx.x; i < D; i += blockDim.x) gembed[(size_t)ids[u] * D + i] = gc[(size_t)u * D + i];
 }
 
-// cpu.go:74-95 EmbedBackward: rows of the input ids += dx rows, t in order for each column.
-__global__ void k_tr_embed_bwd(const float *dx, const uint16_t *tok, int S, int V, int D, float *gembed) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= D) return;
-    for (int t = 0; t < S; t++)
-        if (tok[t] < V) gembed[(size_t)tok[t] * D + i] += dx[(size_t)t * D + i];
+// cpu.go:74-95 EmbedBackward: row id of the embedding gradient += dx rows of its positions, in
+// position order. Workgroup u owns distinct input id ids[u] (positions occ[off[u] .. off[u+1]),
+// ascending), so rows are independent and each sum keeps the reference's order.
+__global__ void k_tr_embed_bwd(const float *dx, const int32_t *ids, const int32_t *off, const int32_t *occ,
+                               int D, float *gembed) {
+    const int u = blockIdx.x;
+    float *row = gembed + (size_t)ids[u] * D;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+        float acc = row[i];
+        for (int k = off[u]; k < off[u + 1]; k++) acc += dx[(size_t)occ[k] * D + i];
+        row[i] = acc;
+    }
 }
 
 __global__ void k_tr_fill(float *p, size_t n, float v) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         p[i] = v;
-}
-
-__global__ void k_tr_scale(float *p, size_t n, float s) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        p[i] *= s;
 }
 
 // out = a + s*b (s = 0: out = a + b as float32 adds)
@@ -466,20 +753,28 @@ __global__ void k_tr_axpy(const float *a, const float *b, float s, int plain_add
 }
 
 // Sum of squares of p[0, n) into per-block float64 partials (block order fixed).
-__global__ __launch_bounds__(kTT) void k_tr_sumsq(const float *p, size_t n, double *part) {
+__global__ __launch_bounds__(kTT) void k_tr_sumsq(const float *p, size_t n, float inv_ls, double *part) {
     __shared__ double red[kTT / 64];
     double s = 0;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        s += (double)p[i] * (double)p[i];
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const float x = inv_ls != 1.f ? p[i] * inv_ls : p[i];
+        s += (double)x * (double)x;
+    }
     s = block_sum_d(s, red);
     if (threadIdx.x == 0) part[blockIdx.x] = s;
 }
 
 // train_full.go:932-969 adamUpdateCFWithInv, element-wise in float32.
-__global__ void k_tr_adam(float *w, const float *g, float *m, float *v, size_t n, float lr, float b1, float b2,
-                          float eps, float wd, float ibc1, float ibc2) {
+// The gradient is first multiplied by the loss-scale inverse and then by the clipping factor
+// (train_full.go:829-836, :149-181; each a float32 multiply, skipped when it is 1), and
+// written back as Adam applies it.
+__global__ void k_tr_adam(float *w, float *g, float *m, float *v, size_t n, float lr, float b1, float b2,
+                          float eps, float wd, float ibc1, float ibc2, float inv_ls, float clip) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        const float gi = g[i];
+        float gi = g[i];
+        if (inv_ls != 1.f) gi *= inv_ls;
+        if (clip != 1.f) gi *= clip;
+        if (inv_ls != 1.f || clip != 1.f) g[i] = gi;
         const float mi = b1 * m[i] + (1 - b1) * gi;
         const float vi = b2 * v[i] + (1 - b2) * gi * gi;
         m[i] = mi;
@@ -517,7 +812,9 @@ struct sh_trainer {
         *dh13, *dqkv, *stats, *dlc, *gc, *loss, *cos_t, *sin_t;
     double *row_loss, *sq_part;
     int *row_valid;
-    int32_t *ids;
+    int32_t *ids, *in_ids, *in_off, *in_occ;   // compact target ids; input ids' positions
+    float *part;                               // split-K partial tiles
+    size_t part_cap;
     uint16_t *tok_in, *tok_tgt;
     int ldc_u;   // padded compact width
     std::vector<uint16_t> tokens;
@@ -533,15 +830,39 @@ namespace {
 
 constexpr int kSqParts = 1024;
 
+unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 8192); }
+
 template <bool AK, bool BK, int EPI>
 hipError_t sgemm(hipStream_t s, const float *A, int lda, const float *B, int ldb, float *C, int ldc, int M,
                  int N, int K, float alpha, const float *R = nullptr) {
     const dim3 grid((N + kGN - 1) / kGN, (M + kGM - 1) / kGM);
-    hipLaunchKernelGGL((k_sgemm<AK, BK, EPI>), grid, dim3(256), 0, s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R);
+    hipLaunchKernelGGL((k_sgemm<AK, BK, EPI>), grid, dim3(256), 0, s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R, K);
     return hipGetLastError();
 }
 
-unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 8192); }
+// C = alpha * A.B with K split into ranges when the tiles alone leave most CUs idle: range
+// partials in `part`, then their sum in range order (k_tr_reduce_ranges). Falls back to one
+// range when `part` cannot hold them.
+template <bool AK, bool BK>
+hipError_t sgemm_split(hipStream_t s, const float *A, int lda, const float *B, int ldb, float *C, int ldc, int M,
+                       int N, int K, float alpha, float *part, size_t part_cap, const float *R = nullptr) {
+    const int tiles = ((N + kGN - 1) / kGN) * ((M + kGM - 1) / kGM);
+    int ranges = 1;
+    if (tiles < 192 && K >= 512) ranges = std::min(16, std::max(1, K / 256));
+    if (ranges > 1 && (size_t)ranges * M * ldc > part_cap) ranges = 1;
+    if (ranges == 1)
+        return R ? sgemm<AK, BK, EPI_RESID>(s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R)
+                 : sgemm<AK, BK, EPI_STORE>(s, A, lda, B, ldb, C, ldc, M, N, K, alpha);
+    const int kc = (K / ranges + kGK - 1) / kGK * kGK;
+    ranges = (K + kc - 1) / kc;
+    const dim3 grid((N + kGN - 1) / kGN, (M + kGM - 1) / kGM, ranges);
+    hipLaunchKernelGGL((k_sgemm<AK, BK, EPI_PART>), grid, dim3(256), 0, s, A, lda, B, ldb, part, ldc, M, N, K, 1.f,
+                       nullptr, kc);
+    const size_t n = (size_t)M * N;
+    hipLaunchKernelGGL(k_tr_reduce_ranges, dim3(blocks_for(n)), dim3(256), 0, s, part, ranges, M, N, ldc, alpha, R,
+                       C);
+    return hipGetLastError();
+}
 
 // Forward (train_full.go:368-396) for the window in tok_in, then runFinalHead's CPU path
 // (:435-523): logits, CrossEntropyLoss, dy = E^T dL * loss scale, the compact classifier
@@ -557,20 +878,28 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale) {
     for (int l = 0; l < T->L; l++) {
         sh_trainer::Layer &C = T->lc[l];   // C.x == cur: the previous layer wrote it there
         hipLaunchKernelGGL(k_tr_rmsnorm, dim3(S), dim3(kTT), 0, s, C.x, T->p + T->o_ra[l], D, eps, C.xn, C.ra);
-        if ((e = sgemm<true, true, EPI_STORE>(s, C.xn, D, T->p + T->o_qkv[l], D, C.qkv, 3 * D, S, 3 * D, D, 1.f)))
+        if ((e = sgemm_split<true, true>(s, C.xn, D, T->p + T->o_qkv[l], D, C.qkv, 3 * D, S, 3 * D, D, 1.f, T->part,
+                                         T->part_cap)))
             return e;
         hipLaunchKernelGGL(k_tr_rope, dim3(S), dim3(256), 0, s, C.qkv, D, hd, T->cos_t, T->sin_t);
-        hipLaunchKernelGGL(k_tr_attn_fwd, dim3(S, T->H), dim3(64), sizeof(float) * S, s, C.qkv, S, D, hd, scale,
-                           C.att);
-        if ((e = sgemm<true, true, EPI_RESID>(s, C.att, D, T->p + T->o_wo[l], D, C.x2, D, S, D, D, alpha, C.x)))
+        if (S <= kAttnMaxS)
+            hipLaunchKernelGGL(k_tr_attn_fwd_blk, dim3((S + kAQ - 1) / kAQ, T->H), dim3(256),
+                               sizeof(float) * (kAQ * kAPad + kAB * kAPad + kAQ * S), s, C.qkv, S, D, hd, scale, C.att);
+        else
+            hipLaunchKernelGGL(k_tr_attn_fwd, dim3(S, T->H), dim3(64), sizeof(float) * S, s, C.qkv, S, D, hd, scale,
+                               C.att);
+        if ((e = sgemm_split<true, true>(s, C.att, D, T->p + T->o_wo[l], D, C.x2, D, S, D, D, alpha, T->part,
+                                         T->part_cap, C.x)))
             return e;
         hipLaunchKernelGGL(k_tr_rmsnorm, dim3(S), dim3(kTT), 0, s, C.x2, T->p + T->o_rf[l], D, eps, C.x2n, C.rf);
-        if ((e = sgemm<true, true, EPI_STORE>(s, C.x2n, D, T->p + T->o_w13[l], D, C.h13, 2 * F, S, 2 * F, D, 1.f)))
+        if ((e = sgemm_split<true, true>(s, C.x2n, D, T->p + T->o_w13[l], D, C.h13, 2 * F, S, 2 * F, D, 1.f, T->part,
+                                         T->part_cap)))
             return e;
         const size_t nf = (size_t)S * F;
         hipLaunchKernelGGL(k_tr_silu_gate, dim3(blocks_for(nf)), dim3(256), 0, s, C.h13, F, nf, C.gate);
         float *next = l + 1 < T->L ? T->lc[l + 1].x : T->xL;
-        if ((e = sgemm<true, true, EPI_RESID>(s, C.gate, F, T->p + T->o_w2[l], F, next, D, S, D, F, alpha, C.x2)))
+        if ((e = sgemm_split<true, true>(s, C.gate, F, T->p + T->o_w2[l], F, next, D, S, D, F, alpha, T->part,
+                                         T->part_cap, C.x2)))
             return e;
         cur = next;
     }
@@ -582,7 +911,8 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale) {
     hipLaunchKernelGGL(k_tr_ce_total, dim3(1), dim3(64), 0, s, T->row_loss, T->row_valid, S, T->loss);
     hipLaunchKernelGGL(k_tr_scale_rows, dim3(S), dim3(256), 0, s, T->logits, T->row_valid, T->loss, V);
     // dy[t][d] = (sum_v dL[t][v] E[v][d]) * loss scale (MatMulEmbedTScale)
-    if ((e = sgemm<true, false, EPI_STORE>(s, T->logits, V, T->p + T->o_embed, D, T->dy, D, S, D, V, loss_scale)))
+    if ((e = sgemm_split<true, false>(s, T->logits, V, T->p + T->o_embed, D, T->dy, D, S, D, V, loss_scale,
+                                      T->part, T->part_cap)))
         return e;
     // classifier embedding gradient on the target rows: gc[u][d] = (sum_t dL[t][ids u] xnf[t][d]) * scale
     float *gemb = T->g + T->o_embed;
@@ -596,14 +926,14 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale) {
     // final RMSNorm backward: dcur and the rms_final gradient
     hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->dy, T->xL, T->p + T->o_rfin, T->rfin, D,
                        T->dcur);
-    hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 255) / 256), dim3(256), 0, s, T->dy, T->xL, T->rfin, S, D,
+    hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 63) / 64), dim3(64), 0, s, T->dy, T->xL, T->rfin, S, D,
                        T->g + T->o_rfin);
     return hipGetLastError();
 }
 
 // backwardAndApply's layer loop (train_full.go:776-848, CPU path), EmbedBackward, the
 // loss-scale undo, clipping and Adam (:826-847).
-hipError_t tr_backward_apply(sh_trainer *T, float loss_scale, int step_t) {
+hipError_t tr_backward_apply(sh_trainer *T, float loss_scale, int step_t, int n_in) {
     hipStream_t s = T->stream;
     const int S = T->S, D = T->D, F = T->F, hd = T->hd;
     const float alpha = T->cfg.residual_scale, scale = (float)(1.0 / sqrt((double)hd));
@@ -613,15 +943,17 @@ hipError_t tr_backward_apply(sh_trainer *T, float loss_scale, int step_t) {
         sh_trainer::Layer &C = T->lc[l];
         hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dcur, T->dcur, alpha, 0, SD, T->dout);
         // FFN: ggate = dout . W2, (dh1, dh3), gxn = [dh1|dh3] . [W1;W3], RMS backward
-        if ((e = sgemm<true, false, EPI_STORE>(s, T->dout, D, T->p + T->o_w2[l], F, T->ggate, F, S, F, D, 1.f)))
+        if ((e = sgemm_split<true, false>(s, T->dout, D, T->p + T->o_w2[l], F, T->ggate, F, S, F, D, 1.f, T->part,
+                                          T->part_cap)))
             return e;
         const size_t nf = (size_t)S * F;
         hipLaunchKernelGGL(k_tr_silu_bwd, dim3(blocks_for(nf)), dim3(256), 0, s, T->ggate, C.h13, F, nf, T->dh13);
-        if ((e = sgemm<true, false, EPI_STORE>(s, T->dh13, 2 * F, T->p + T->o_w13[l], D, T->gxn, D, S, D, 2 * F, 1.f)))
+        if ((e = sgemm_split<true, false>(s, T->dh13, 2 * F, T->p + T->o_w13[l], D, T->gxn, D, S, D, 2 * F, 1.f,
+                                          T->part, T->part_cap)))
             return e;
         hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x2, T->p + T->o_rf[l], C.rf, D,
                            T->dprev);
-        hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 255) / 256), dim3(256), 0, s, T->gxn, C.x2, C.rf, S, D,
+        hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 63) / 64), dim3(64), 0, s, T->gxn, C.x2, C.rf, S, D,
                            T->g + T->o_rf[l]);
         hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dcur, T->dprev, 0.f, 1, SD, T->gx2);
         // weight gradients: dW2 = dout^T gate, d[W1;W3] = [dh1|dh3]^T x2n
@@ -632,18 +964,27 @@ hipError_t tr_backward_apply(sh_trainer *T, float loss_scale, int step_t) {
             return e;
         hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->gx2, T->gx2, alpha, 0, SD, T->dx2s);
         // attention: gatt = dx2s . Wo, (dq, dk, dv), gxn = [dq|dk|dv] . [Wq;Wk;Wv], RMS backward
-        if ((e = sgemm<true, false, EPI_STORE>(s, T->dx2s, D, T->p + T->o_wo[l], D, T->gatt, D, S, D, D, 1.f)))
+        if ((e = sgemm_split<true, false>(s, T->dx2s, D, T->p + T->o_wo[l], D, T->gatt, D, S, D, D, 1.f, T->part,
+                                          T->part_cap)))
             return e;
-        hipLaunchKernelGGL(k_tr_attn_bwd_q, dim3(S, T->H), dim3(64), 2 * sizeof(float) * S, s, C.qkv, T->gatt, S,
-                           D, hd, scale, T->dqkv, T->stats);
-        hipLaunchKernelGGL(k_tr_attn_bwd_kv, dim3(S, T->H), dim3(64), 2 * sizeof(float) * S, s, C.qkv, T->gatt,
-                           S, D, hd, scale, T->stats, T->dqkv);
-        if ((e = sgemm<true, false, EPI_STORE>(s, T->dqkv, 3 * D, T->p + T->o_qkv[l], D, T->gxn, D, S, D, 3 * D,
-                                               1.f)))
+        if (S <= kAttnMaxS) {
+            hipLaunchKernelGGL(k_tr_attn_bwd_q_blk, dim3((S + kAQ - 1) / kAQ, T->H), dim3(256),
+                               sizeof(float) * (2 * kAQ * kAPad + kAB * kAPad + 2 * kAQ * S), s, C.qkv, T->gatt, S,
+                               D, hd, scale, T->dqkv, T->stats);
+            hipLaunchKernelGGL(k_tr_attn_bwd_kv_blk, dim3((S + kAQ - 1) / kAQ, T->H), dim3(256), 0, s, C.qkv,
+                               T->gatt, S, D, hd, scale, T->stats, T->dqkv);
+        } else {
+            hipLaunchKernelGGL(k_tr_attn_bwd_q, dim3(S, T->H), dim3(64), 2 * sizeof(float) * S, s, C.qkv, T->gatt,
+                               S, D, hd, scale, T->dqkv, T->stats);
+            hipLaunchKernelGGL(k_tr_attn_bwd_kv, dim3(S, T->H), dim3(64), 2 * sizeof(float) * S, s, C.qkv, T->gatt,
+                               S, D, hd, scale, T->stats, T->dqkv);
+        }
+        if ((e = sgemm_split<true, false>(s, T->dqkv, 3 * D, T->p + T->o_qkv[l], D, T->gxn, D, S, D, 3 * D, 1.f,
+                                          T->part, T->part_cap)))
             return e;
         hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x, T->p + T->o_ra[l], C.ra, D,
                            T->dprev);
-        hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 255) / 256), dim3(256), 0, s, T->gxn, C.x, C.ra, S, D,
+        hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 63) / 64), dim3(64), 0, s, T->gxn, C.x, C.ra, S, D,
                            T->g + T->o_ra[l]);
         hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dprev, T->gx2, 0.f, 1, SD, T->dcur);
         // dWo = dx2s^T att, d[Wq;Wk;Wv] = [dq|dk|dv]^T xn
@@ -653,15 +994,14 @@ hipError_t tr_backward_apply(sh_trainer *T, float loss_scale, int step_t) {
                                                 1.f)))
             return e;
     }
-    hipLaunchKernelGGL(k_tr_embed_bwd, dim3((D + 255) / 256), dim3(256), 0, s, T->dcur, T->tok_in, S, T->V, D,
-                       T->g + T->o_embed);
+    if (n_in > 0)
+        hipLaunchKernelGGL(k_tr_embed_bwd, dim3(n_in), dim3(256), 0, s, T->dcur, T->in_ids, T->in_off, T->in_occ, D,
+                           T->g + T->o_embed);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (loss_scale != 0 && loss_scale != 1) {
-        const float inv = (float)(1.0 / (double)loss_scale);
-        hipLaunchKernelGGL(k_tr_scale, dim3(blocks_for(T->n_all)), dim3(256), 0, s, T->g, T->n_all, inv);
-    }
+    const float inv = (loss_scale != 0 && loss_scale != 1) ? (float)(1.0 / (double)loss_scale) : 1.f;
+    float clip = 1.f;
     if (T->opt.grad_clip > 0) {
-        hipLaunchKernelGGL(k_tr_sumsq, dim3(kSqParts), dim3(kTT), 0, s, T->g, T->n_all, T->sq_part);
+        hipLaunchKernelGGL(k_tr_sumsq, dim3(kSqParts), dim3(kTT), 0, s, T->g, T->n_all, inv, T->sq_part);
         std::vector<double> part(kSqParts);
         if ((e = hipMemcpyAsync(part.data(), T->sq_part, sizeof(double) * kSqParts, hipMemcpyDeviceToHost, s)) ||
             (e = hipStreamSynchronize(s)))
@@ -670,20 +1010,18 @@ hipError_t tr_backward_apply(sh_trainer *T, float loss_scale, int step_t) {
         for (double x : part) norm2 += x;
         if (norm2 > 0) {
             const float norm = (float)sqrt(norm2);
-            if (norm > T->opt.grad_clip) {
-                const float sc = T->opt.grad_clip / norm;
-                hipLaunchKernelGGL(k_tr_scale, dim3(blocks_for(T->n_all)), dim3(256), 0, s, T->g, T->n_all, sc);
-            }
+            if (norm > T->opt.grad_clip) clip = T->opt.grad_clip / norm;
         }
     }
     const float ibc1 = 1.f / (float)(1.0 - pow((double)T->opt.beta1, (double)step_t));
     const float ibc2 = 1.f / (float)(1.0 - pow((double)T->opt.beta2, (double)step_t));
     const sh_train_options &o = T->opt;
     hipLaunchKernelGGL(k_tr_adam, dim3(blocks_for(T->n_mat)), dim3(256), 0, s, T->p, T->g, T->m, T->v, T->n_mat,
-                       o.lr, o.beta1, o.beta2, o.eps, o.weight_decay, ibc1, ibc2);
+                       o.lr, o.beta1, o.beta2, o.eps, o.weight_decay, ibc1, ibc2, inv, clip);
     const size_t ng = T->n_all - T->n_mat;
     hipLaunchKernelGGL(k_tr_adam, dim3(blocks_for(ng)), dim3(256), 0, s, T->p + T->n_mat, T->g + T->n_mat,
-                       T->m + T->n_mat, T->v + T->n_mat, ng, o.lr, o.beta1, o.beta2, o.eps, 0.f, ibc1, ibc2);
+                       T->m + T->n_mat, T->v + T->n_mat, ng, o.lr, o.beta1, o.beta2, o.eps, 0.f, ibc1, ibc2, inv,
+                       clip);
     return hipGetLastError();
 }
 
@@ -725,14 +1063,41 @@ bool tr_step_window(sh_trainer *T, const uint16_t *in, const uint16_t *tgt, floa
     const int S = T->S;
     std::vector<int32_t> ids = compact_ids(tgt, S, T->V);
     const int U = (int)ids.size();
+    // the input ids' positions, grouped by id (order of first appearance), positions ascending
+    std::vector<int32_t> in_ids, in_off(1, 0), in_occ;
+    {
+        std::vector<int32_t> slot(T->V, -1);
+        std::vector<std::vector<int32_t>> pos;
+        for (int t = 0; t < S; t++) {
+            const int tok = in[t];
+            if (tok >= T->V) continue;
+            if (slot[tok] < 0) {
+                slot[tok] = (int32_t)in_ids.size();
+                in_ids.push_back(tok);
+                pos.emplace_back();
+            }
+            pos[slot[tok]].push_back(t);
+        }
+        for (auto &p : pos) {
+            in_occ.insert(in_occ.end(), p.begin(), p.end());
+            in_off.push_back((int32_t)in_occ.size());
+        }
+    }
+    const int n_in = (int)in_ids.size();
     if (!hip_ok(hipMemcpyAsync(T->tok_in, in, 2 * (size_t)S, hipMemcpyHostToDevice, T->stream), "tokens") ||
         !hip_ok(hipMemcpyAsync(T->tok_tgt, tgt, 2 * (size_t)S, hipMemcpyHostToDevice, T->stream), "targets") ||
         (U && !hip_ok(hipMemcpyAsync(T->ids, ids.data(), 4 * (size_t)U, hipMemcpyHostToDevice, T->stream), "ids")) ||
+        (n_in && !hip_ok(hipMemcpyAsync(T->in_ids, in_ids.data(), 4 * (size_t)n_in, hipMemcpyHostToDevice,
+                                        T->stream), "ids")) ||
+        (n_in && !hip_ok(hipMemcpyAsync(T->in_off, in_off.data(), 4 * (size_t)(n_in + 1), hipMemcpyHostToDevice,
+                                        T->stream), "ids")) ||
+        (n_in && !hip_ok(hipMemcpyAsync(T->in_occ, in_occ.data(), 4 * in_occ.size(), hipMemcpyHostToDevice,
+                                        T->stream), "ids")) ||
         !hip_ok(hipEventRecord(T->ev0, T->stream), "event"))
         return false;
     const int step_t = (int)T->state.adam_t + 1;
     if (!hip_ok(tr_forward_head(T, U, T->opt.loss_scale), "training forward") ||
-        !hip_ok(tr_backward_apply(T, T->opt.loss_scale, step_t), "training backward") ||
+        !hip_ok(tr_backward_apply(T, T->opt.loss_scale, step_t, n_in), "training backward") ||
         !hip_ok(hipEventRecord(T->ev1, T->stream), "event"))
         return false;
     float lv[2];
@@ -764,10 +1129,10 @@ sh_trainer *sh_trainer_create(const sh_config *cfg, const sh_train_options *opt_
     const sh_config &c = *cfg;
     if (c.dim <= 0 || c.hidden <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.head_dim <= 0 || c.vocab <= 0 ||
         c.n_heads * c.head_dim != c.dim || c.n_kv_heads != c.n_heads || c.qk_norm || c.head_dim > 64 ||
-        c.head_dim % 2 || c.dim % 4 || c.hidden % 4 || c.vocab % 4 || c.vocab > 65535) {
+        c.head_dim % 4 || c.dim % 4 || c.hidden % 4 || c.vocab % 4 || c.vocab > 65535) {
         set_error("sh_trainer_create: the training step needs a Stories-shaped model: n_heads*head_dim == dim, "
-                  "n_kv_heads == n_heads, no qk_norm, even head_dim <= 64, dim/hidden/vocab multiples of 4, "
-                  "vocab <= 65535");
+                  "n_kv_heads == n_heads, no qk_norm, head_dim <= 64 and a multiple of 4, dim/hidden/vocab "
+                  "multiples of 4, vocab <= 65535");
         return nullptr;
     }
     sh_train_options o{};
@@ -840,7 +1205,8 @@ sh_trainer *sh_trainer_create(const sh_config *cfg, const sh_train_options *opt_
                  o_dlc = take(4 * S * T->ldc_u), o_gc = take(4 * S * D), o_loss = take(16),
                  o_cos = take(4 * S * (T->hd / 2)), o_sin = take(4 * S * (T->hd / 2)), o_rl = take(8 * S),
                  o_sq = take(8 * kSqParts), o_rv = take(4 * S), o_ids = take(4 * S), o_ti = take(2 * S),
-                 o_tt = take(2 * S);
+                 o_tt = take(2 * S), o_iid = take(4 * S), o_ioff = take(4 * (S + 1)), o_iocc = take(4 * S),
+                 o_part = take(4 * 16 * S * std::max(3 * D, 2 * F));
     bool ok = hip_ok(hipStreamCreate(&T->stream), "stream") && hip_ok(hipEventCreate(&T->ev0), "event") &&
               hip_ok(hipEventCreate(&T->ev1), "event") &&
               hip_ok(hipMalloc(&T->p, 4 * T->n_all), "hipMalloc params") &&
@@ -872,6 +1238,9 @@ sh_trainer *sh_trainer_create(const sh_config *cfg, const sh_train_options *opt_
     T->loss = (float *)(A + o_loss); T->cos_t = (float *)(A + o_cos); T->sin_t = (float *)(A + o_sin);
     T->row_loss = (double *)(A + o_rl); T->sq_part = (double *)(A + o_sq); T->row_valid = (int *)(A + o_rv);
     T->ids = (int32_t *)(A + o_ids); T->tok_in = (uint16_t *)(A + o_ti); T->tok_tgt = (uint16_t *)(A + o_tt);
+    T->in_ids = (int32_t *)(A + o_iid); T->in_off = (int32_t *)(A + o_ioff); T->in_occ = (int32_t *)(A + o_iocc);
+    T->part = (float *)(A + o_part);
+    T->part_cap = 16 * S * std::max(3 * D, 2 * F);
     // rope.go:5-24 buildRoPETables(seq, headDim): float64 angles, float32 cos / sin
     const int half = T->hd / 2;
     std::vector<float> cs((size_t)S * half), sn((size_t)S * half);
