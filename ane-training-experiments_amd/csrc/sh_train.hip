@@ -631,12 +631,16 @@ __global__ __launch_bounds__(kTT) void k_tr_rms_bwd_dx(const float *dy, const fl
     }
 }
 
-// rmsnorm.go:32-47 gain gradient: dw[i] = sum over t in order of float32(float64(dy*x)*r).
+// rmsnorm.go:32-47 gain gradient: the sum over t in order of float32(float64(dy*x)*r), stored
+// (kDwStore), continued from dw[i] as rmsNormBackward does into an accumulator (kDwContinue, the
+// layer gains under backwardAndAccumulate), or formed on its own and then added to dw[i]
+// (kDwAdd: the final gain, addSlice at train_full.go:767).
+enum { kDwStore = 0, kDwContinue = 1, kDwAdd = 2 };
 __global__ __launch_bounds__(64) void k_tr_rms_bwd_dw(const float *dy, const float *x, const float *rrms, int S,
-                                                      int D, float *dw) {
+                                                      int D, int mode, float *dw) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= D) return;
-    float acc = 0.f;
+    float acc = mode == kDwContinue ? dw[i] : 0.f;
     int t = 0;
     for (; t + 8 <= S; t += 8) {   // eight rows' loads in flight, the sum still in row order
         float a[8], b[8], r[8];
@@ -650,7 +654,7 @@ __global__ __launch_bounds__(64) void k_tr_rms_bwd_dw(const float *dy, const flo
         for (int u = 0; u < 8; u++) acc += (float)((double)(a[u] * b[u]) * (double)r[u]);
     }
     for (; t < S; t++) acc += (float)((double)(dy[(size_t)t * D + i] * x[(size_t)t * D + i]) * (double)rrms[t]);
-    dw[i] = acc;
+    dw[i] = mode == kDwAdd ? dw[i] + acc : acc;
 }
 
 // cpu.go:173-253 CrossEntropyLoss for row t of logits [S, V] (in place -> dLogits): float32
@@ -722,9 +726,12 @@ __global__ void k_tr_gather_cols(const float *dl, int V, const int32_t *ids, int
         dlc[(size_t)t * ldc + u] = u < U ? dl[(size_t)t * V + ids[u]] : 0.f;
 }
 
-__global__ void k_tr_scatter_rows(const float *gc, const int32_t *ids, int D, float *gembed) {
+// Compact classifier rows into the embedding gradient: stored, or added (add != 0) when the
+// gradient region accumulates over windows.
+__global__ void k_tr_scatter_rows(const float *gc, const int32_t *ids, int D, int add, float *gembed) {
     const int u = blockIdx.x;
-    for (int i = threadIdx.x; i < D; i += blockDim.x) gembed[(size_t)ids[u] * D + i] = gc[(size_t)u * D + i];
+    float *row = gembed + (size_t)ids[u] * D;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) row[i] = add ? row[i] + gc[(size_t)u * D + i] : gc[(size_t)u * D + i];
 }
 
 // cpu.go:74-95 EmbedBackward: row id of the embedding gradient += dx rows of its positions, in
@@ -864,10 +871,20 @@ hipError_t sgemm_split(hipStream_t s, const float *A, int lda, const float *B, i
     return hipGetLastError();
 }
 
+// dW GEMM into the gradient arena: stored, or added onto what it holds (acc) when gradients
+// accumulate over windows.
+template <bool AK, bool BK>
+hipError_t sgemm_grad(hipStream_t s, const float *A, int lda, const float *B, int ldb, float *C, int ldc, int M,
+                      int N, int K, bool acc) {
+    return acc ? sgemm<AK, BK, EPI_RESID>(s, A, lda, B, ldb, C, ldc, M, N, K, 1.f, C)
+               : sgemm<AK, BK, EPI_STORE>(s, A, lda, B, ldb, C, ldc, M, N, K, 1.f);
+}
+
 // Forward (train_full.go:368-396) for the window in tok_in, then runFinalHead's CPU path
 // (:435-523): logits, CrossEntropyLoss, dy = E^T dL * loss scale, the compact classifier
-// embedding gradient, the final RMSNorm backward.
-hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale) {
+// embedding gradient, the final RMSNorm backward. acc: the gradient arena holds earlier
+// windows' sums, which this window's embedding and final-gain gradients add onto.
+hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale, bool acc) {
     hipStream_t s = T->stream;
     const int S = T->S, D = T->D, F = T->F, hd = T->hd, V = T->V;
     const float alpha = T->cfg.residual_scale, scale = (float)(1.0 / sqrt((double)hd));
@@ -916,24 +933,26 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale) {
         return e;
     // classifier embedding gradient on the target rows: gc[u][d] = (sum_t dL[t][ids u] xnf[t][d]) * scale
     float *gemb = T->g + T->o_embed;
-    hipLaunchKernelGGL(k_tr_fill, dim3(blocks_for((size_t)V * D)), dim3(256), 0, s, gemb, (size_t)V * D, 0.f);
+    if (!acc)
+        hipLaunchKernelGGL(k_tr_fill, dim3(blocks_for((size_t)V * D)), dim3(256), 0, s, gemb, (size_t)V * D, 0.f);
     if (U > 0) {
         hipLaunchKernelGGL(k_tr_gather_cols, dim3(S), dim3(256), 0, s, T->logits, V, T->ids, U, T->ldc_u, T->dlc);
         if ((e = sgemm<false, false, EPI_STORE>(s, T->dlc, T->ldc_u, T->xnf, D, T->gc, D, U, D, S, loss_scale)))
             return e;
-        hipLaunchKernelGGL(k_tr_scatter_rows, dim3(U), dim3(256), 0, s, T->gc, T->ids, D, gemb);
+        hipLaunchKernelGGL(k_tr_scatter_rows, dim3(U), dim3(256), 0, s, T->gc, T->ids, D, (int)acc, gemb);
     }
     // final RMSNorm backward: dcur and the rms_final gradient
     hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->dy, T->xL, T->p + T->o_rfin, T->rfin, D,
                        T->dcur);
     hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 63) / 64), dim3(64), 0, s, T->dy, T->xL, T->rfin, S, D,
-                       T->g + T->o_rfin);
+                       acc ? kDwAdd : kDwStore, T->g + T->o_rfin);
     return hipGetLastError();
 }
 
-// backwardAndApply's layer loop (train_full.go:776-848, CPU path), EmbedBackward, the
-// loss-scale undo, clipping and Adam (:826-847).
-hipError_t tr_backward_apply(sh_trainer *T, float loss_scale, int step_t, int n_in) {
+// The layer loop of backwardAndApply (train_full.go:776-848) or backwardAndAccumulate
+// (:709-774), CPU path, then EmbedBackward. acc: layer gradients add onto the arena's sums
+// (no clearLayerGrad), as the accumulate loop writes into e.accum directly.
+hipError_t tr_backward(sh_trainer *T, int n_in, bool acc) {
     hipStream_t s = T->stream;
     const int S = T->S, D = T->D, F = T->F, hd = T->hd;
     const float alpha = T->cfg.residual_scale, scale = (float)(1.0 / sqrt((double)hd));
@@ -954,13 +973,12 @@ hipError_t tr_backward_apply(sh_trainer *T, float loss_scale, int step_t, int n_
         hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x2, T->p + T->o_rf[l], C.rf, D,
                            T->dprev);
         hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 63) / 64), dim3(64), 0, s, T->gxn, C.x2, C.rf, S, D,
-                           T->g + T->o_rf[l]);
+                           acc ? kDwContinue : kDwStore, T->g + T->o_rf[l]);
         hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dcur, T->dprev, 0.f, 1, SD, T->gx2);
         // weight gradients: dW2 = dout^T gate, d[W1;W3] = [dh1|dh3]^T x2n
-        if ((e = sgemm<false, false, EPI_STORE>(s, T->dout, D, C.gate, F, T->g + T->o_w2[l], F, D, F, S, 1.f)))
+        if ((e = sgemm_grad<false, false>(s, T->dout, D, C.gate, F, T->g + T->o_w2[l], F, D, F, S, acc)))
             return e;
-        if ((e = sgemm<false, false, EPI_STORE>(s, T->dh13, 2 * F, C.x2n, D, T->g + T->o_w13[l], D, 2 * F, D, S,
-                                                1.f)))
+        if ((e = sgemm_grad<false, false>(s, T->dh13, 2 * F, C.x2n, D, T->g + T->o_w13[l], D, 2 * F, D, S, acc)))
             return e;
         hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->gx2, T->gx2, alpha, 0, SD, T->dx2s);
         // attention: gatt = dx2s . Wo, (dq, dk, dv), gxn = [dq|dk|dv] . [Wq;Wk;Wv], RMS backward
@@ -985,20 +1003,27 @@ hipError_t tr_backward_apply(sh_trainer *T, float loss_scale, int step_t, int n_
         hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x, T->p + T->o_ra[l], C.ra, D,
                            T->dprev);
         hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 63) / 64), dim3(64), 0, s, T->gxn, C.x, C.ra, S, D,
-                           T->g + T->o_ra[l]);
+                           acc ? kDwContinue : kDwStore, T->g + T->o_ra[l]);
         hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dprev, T->gx2, 0.f, 1, SD, T->dcur);
         // dWo = dx2s^T att, d[Wq;Wk;Wv] = [dq|dk|dv]^T xn
-        if ((e = sgemm<false, false, EPI_STORE>(s, T->dx2s, D, C.att, D, T->g + T->o_wo[l], D, D, D, S, 1.f)))
+        if ((e = sgemm_grad<false, false>(s, T->dx2s, D, C.att, D, T->g + T->o_wo[l], D, D, D, S, acc)))
             return e;
-        if ((e = sgemm<false, false, EPI_STORE>(s, T->dqkv, 3 * D, C.xn, D, T->g + T->o_qkv[l], D, 3 * D, D, S,
-                                                1.f)))
+        if ((e = sgemm_grad<false, false>(s, T->dqkv, 3 * D, C.xn, D, T->g + T->o_qkv[l], D, 3 * D, D, S, acc)))
             return e;
     }
     if (n_in > 0)
         hipLaunchKernelGGL(k_tr_embed_bwd, dim3(n_in), dim3(256), 0, s, T->dcur, T->in_ids, T->in_off, T->in_occ, D,
                            T->g + T->o_embed);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    const float inv = (loss_scale != 0 && loss_scale != 1) ? (float)(1.0 / (double)loss_scale) : 1.f;
+    return hipGetLastError();
+}
+
+// The gradient arena times `inv` (the loss-scale undo of backwardAndApply, train_full.go:829-836,
+// or flushPending's 1/pending/loss scale, engine.go:544-548), clipping (clipLayerGradients,
+// :149-181) and Adam at 1-based step step_t (:838-842); k_tr_adam leaves the applied gradients
+// in the arena.
+hipError_t tr_apply(sh_trainer *T, float inv, int step_t) {
+    hipStream_t s = T->stream;
+    hipError_t e;
     float clip = 1.f;
     if (T->opt.grad_clip > 0) {
         hipLaunchKernelGGL(k_tr_sumsq, dim3(kSqParts), dim3(kTT), 0, s, T->g, T->n_all, inv, T->sq_part);
@@ -1057,7 +1082,22 @@ bool tr_ready(const sh_trainer *T) {
     return true;
 }
 
-// One step on a given window: forward, loss, backward, Adam; the loss comes back.
+// flushPending (engine.go:540-565): the accumulated sums times float32(1/pending) / loss scale,
+// clipped, then Adam; the arena keeps the applied gradients and the next window overwrites it.
+bool tr_flush(sh_trainer *T) {
+    if (T->state.pending_steps == 0) return true;
+    float scale = (float)(1.0 / (double)T->state.pending_steps);
+    if (T->opt.loss_scale > 0) scale /= T->opt.loss_scale;
+    if (!hip_ok(tr_apply(T, scale, (int)T->state.adam_t + 1), "optimizer step")) return false;
+    T->state.adam_t++;
+    T->state.pending_steps = 0;
+    T->state.cum_batches++;
+    return true;
+}
+
+// One step on a given window: forward, loss, backward, then Adam (or, with accumulation, the
+// gradients added to the pending sums and Adam once AccumSteps windows are in); the loss comes
+// back.
 bool tr_step_window(sh_trainer *T, const uint16_t *in, const uint16_t *tgt, float *loss_out) {
     (void)hipSetDevice(T->device);
     const int S = T->S;
@@ -1095,18 +1135,28 @@ bool tr_step_window(sh_trainer *T, const uint16_t *in, const uint16_t *tgt, floa
                                         T->stream), "ids")) ||
         !hip_ok(hipEventRecord(T->ev0, T->stream), "event"))
         return false;
-    const int step_t = (int)T->state.adam_t + 1;
-    if (!hip_ok(tr_forward_head(T, U, T->opt.loss_scale), "training forward") ||
-        !hip_ok(tr_backward_apply(T, T->opt.loss_scale, step_t, n_in), "training backward") ||
-        !hip_ok(hipEventRecord(T->ev1, T->stream), "event"))
+    // AccumSteps > 1: the first window after a flush stores its gradients, later ones add
+    const bool accumulate = T->opt.accum_steps > 1;
+    const bool acc = accumulate && T->state.pending_steps > 0;
+    if (!hip_ok(tr_forward_head(T, U, T->opt.loss_scale, acc), "training forward") ||
+        !hip_ok(tr_backward(T, n_in, acc), "training backward"))
         return false;
+    if (!accumulate) {
+        const float ls = T->opt.loss_scale;
+        const float inv = (ls != 0 && ls != 1) ? (float)(1.0 / (double)ls) : 1.f;
+        if (!hip_ok(tr_apply(T, inv, (int)T->state.adam_t + 1), "optimizer step")) return false;
+        T->state.adam_t++;   // train_full.go:844-845
+        T->state.cum_batches++;
+    } else if (++T->state.pending_steps >= (uint32_t)T->opt.accum_steps) {   // train_full.go:769-772
+        if (!tr_flush(T)) return false;
+    }
+    if (!hip_ok(hipEventRecord(T->ev1, T->stream), "event")) return false;
     float lv[2];
     if (!hip_ok(hipMemcpyAsync(lv, T->loss, sizeof lv, hipMemcpyDeviceToHost, T->stream), "loss") ||
         !hip_ok(hipStreamSynchronize(T->stream), "step sync"))
         return false;
     float ms = 0;
     (void)hipEventElapsedTime(&ms, T->ev0, T->ev1);
-    T->state.adam_t = (uint32_t)step_t;
     T->state.last_loss = lv[0];
     T->state.cum_steps++;
     T->state.last_step_ms = ms;
@@ -1147,10 +1197,6 @@ sh_trainer *sh_trainer_create(const sh_config *cfg, const sh_train_options *opt_
     if (o.eps <= 0) o.eps = 1e-8f;
     if (o.grad_clip < 0) o.grad_clip = 0;
     if (o.loss_scale <= 0) o.loss_scale = 256;
-    if (o.accum_steps != 1) {
-        set_error("sh_trainer_create: gradient accumulation (accum_steps > 1) is not supported");
-        return nullptr;
-    }
     if (o.seq > 4096) {
         set_error("sh_trainer_create: seq must be <= 4096");
         return nullptr;
@@ -1333,6 +1379,15 @@ int sh_trainer_step_window(sh_trainer *T, const uint16_t *input, const uint16_t 
         return -1;
     }
     return tr_step_window(T, input, target, loss) ? 0 : -1;
+}
+
+int sh_trainer_flush(sh_trainer *T) {
+    if (!T) {
+        set_error("storiesane flush: engine is closed");   // engine.go:399-401
+        return -1;
+    }
+    (void)hipSetDevice(T->device);
+    return tr_flush(T) && hip_ok(hipStreamSynchronize(T->stream), "flush sync") ? 0 : -1;
 }
 
 int sh_trainer_read(const sh_trainer *T, int32_t which, const char *name, float *dst, size_t n) {

@@ -128,6 +128,7 @@ SIGNATURES = {
     "sh_trainer_set_tokens": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint16), C.c_int64]),
     "sh_trainer_step": (C.c_int, [C.c_void_p, _F]),
     "sh_trainer_step_window": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), _F]),
+    "sh_trainer_flush": (C.c_int, [C.c_void_p]),
     "sh_trainer_read": (C.c_int, [C.c_void_p, C.c_int32, C.c_char_p, _F, C.c_size_t]),
     "sh_trainer_state": (C.c_int, [C.c_void_p, C.c_void_p]),
     "sh_trainer_destroy": (None, [C.c_void_p]),
@@ -508,7 +509,8 @@ class TrainOptions(C.Structure):
 
 class TrainState(C.Structure):
     _fields_ = [("token_pos", C.c_uint64), ("last_loss", C.c_float), ("cum_steps", C.c_uint32),
-                ("adam_t", C.c_uint32), ("last_step_ms", C.c_double)]
+                ("adam_t", C.c_uint32), ("last_step_ms", C.c_double), ("cum_batches", C.c_uint32),
+                ("pending_steps", C.c_uint32)]
 
 
 SH_TRAIN_PARAMS, SH_TRAIN_GRADS, SH_TRAIN_ADAM_M, SH_TRAIN_ADAM_V = 0, 1, 2, 3
@@ -556,6 +558,10 @@ class Trainer:
                "sh_trainer_step_window")
         return loss.value
 
+    def flush(self) -> None:
+        """Engine.Flush: applies pending accumulated gradients (no-op when none are pending)."""
+        _check(self.lib.sh_trainer_flush(self.h), "sh_trainer_flush")
+
     def read(self, which: int, name: str, shape) -> np.ndarray:
         out = np.empty(shape, np.float32)
         _check(self.lib.sh_trainer_read(self.h, which, name.encode(), _fp(out), out.size), "sh_trainer_read")
@@ -565,7 +571,8 @@ class Trainer:
         st = TrainState()
         _check(self.lib.sh_trainer_state(self.h, C.byref(st)), "sh_trainer_state")
         return {"token_pos": st.token_pos, "last_loss": st.last_loss, "cum_steps": st.cum_steps,
-                "adam_t": st.adam_t, "last_step_ms": st.last_step_ms}
+                "adam_t": st.adam_t, "last_step_ms": st.last_step_ms, "cum_batches": st.cum_batches,
+                "pending_steps": st.pending_steps}
 
     def close(self) -> None:
         if self.h:

@@ -202,19 +202,23 @@ void sh_model_destroy(sh_model *m);
 /* ---- training: ane/storiesane Engine.Step (engine.go:295-361, train_full.go) ------------ */
 /* Options (storiesane.Options, engine.go:15-32); zero / negative fields take Open's defaults
  * (engine.go:153-186): seq 256, lr 3e-4, beta1 0.9, beta2 0.999, eps 1e-8, loss_scale 256,
- * seed 42, accum_steps 1; grad_clip 0 = off; weight_decay 0. accum_steps > 1 is refused. */
+ * seed 42, accum_steps 1; grad_clip 0 = off; weight_decay 0. accum_steps > 1 accumulates the
+ * gradients of that many windows and applies Adam to their mean (backwardAndAccumulate,
+ * train_full.go:709-774; flushPending, engine.go:540-565). */
 typedef struct sh_train_options {
     int32_t seq;
     float lr, beta1, beta2, eps, weight_decay, grad_clip, loss_scale;
     int64_t seed;
     int32_t accum_steps;
 } sh_train_options;
-/* storiesane.State (engine.go:35-44) subset, plus the last step's device time. */
+/* storiesane.State (engine.go:35-44) without the wall-clock totals, plus the last step's
+ * device time. */
 typedef struct sh_train_state {
     uint64_t token_pos;
     float last_loss;
     uint32_t cum_steps, adam_t;
     double last_step_ms;
+    uint32_t cum_batches, pending_steps;
 } sh_train_state;
 typedef struct sh_trainer sh_trainer;
 enum { SH_TRAIN_PARAMS = 0, SH_TRAIN_GRADS = 1, SH_TRAIN_ADAM_M = 2, SH_TRAIN_ADAM_V = 3 };
@@ -231,14 +235,18 @@ int sh_trainer_upload_globals(sh_trainer *t, const float *embed, const float *rm
 int sh_trainer_set_tokens(sh_trainer *t, const uint16_t *tokens, int64_t n);
 /* (*Engine).Step (engine.go:295-361): picks the window with drand48 (engine.go:307-316,
  * :725-732), runs forwardTraining, runFinalHead and backwardAndUpdate on the device (the
- * reference's CPU-path numerics, accumulation 1) and returns the loss. "not enough tokens"
- * when the stream is shorter than seq + 1. */
+ * reference's CPU-path numerics) and returns the loss. "not enough tokens" when the stream is
+ * shorter than seq + 1. */
 int sh_trainer_step(sh_trainer *t, float *loss);
 /* The same step on a given (input, target) window of seq ids, without the window choice. */
 int sh_trainer_step_window(sh_trainer *t, const uint16_t *input, const uint16_t *target,
                            float *loss);
-/* Copies one tensor of a set (SH_TRAIN_PARAMS / GRADS — the last step's gradients as Adam
- * applied them / ADAM_M / ADAM_V) to dst: name "embed", "rms_final" or "layers.<l>.<key>"
+/* (*Engine).Flush (engine.go:398-410): applies the pending accumulated gradients, if any
+ * (scaled by 1/pending, loss scale undone, clipped, Adam). */
+int sh_trainer_flush(sh_trainer *t);
+/* Copies one tensor of a set (SH_TRAIN_PARAMS / GRADS / ADAM_M / ADAM_V) to dst. GRADS holds
+ * the gradients Adam last applied, or, while accumulated windows are pending, their sum (still
+ * multiplied by the loss scale). name is "embed", "rms_final" or "layers.<l>.<key>"
  * with key wq wk wv wo w1 w2 w3 rms_att rms_ffn; n must be its element count. No reference
  * counterpart (the engine's weights are Go slices the caller reads directly). */
 int sh_trainer_read(const sh_trainer *t, int32_t which, const char *name, float *dst, size_t n);

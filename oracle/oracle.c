@@ -1045,10 +1045,14 @@ static void train_layer_tensors(const or_config *cfg, or_train_layer *l, float *
     p[8] = l->rms_ffn; n[8] = D;
 }
 
-float or_train_step(const or_config *cfg, or_train_params *p, or_train_params *m,
-                    or_train_params *v, or_train_params *grads, const or_train_hparams *hp,
-                    int step_t, const uint16_t *input, const uint16_t *target, int seq,
-                    int apply, int threads) {
+/* Forward, final head and backward of one window (train_full.go:368-396, :435-523 and the
+ * layer loops of :709-774 / :776-848, CPU path). accumulate == 0: grads receives this window's
+ * gradients (clearLayerGrad, train_full.go:783). accumulate != 0: grads is the accumulator;
+ * layer gradients add onto it in place, the final-gain and embedding gradients of the window are
+ * formed on their own and then added (addSlice, train_full.go:767-768). Returns the loss. */
+static float train_gradients(const or_config *cfg, const or_train_params *p, or_train_params *grads,
+                             const or_train_hparams *hp, const uint16_t *input,
+                             const uint16_t *target, int seq, int accumulate, int threads) {
     const int D = cfg->dim, F = cfg->hidden, H = cfg->n_heads, hd = cfg->head_dim;
     const int V = cfg->vocab, L = cfg->n_layers;
     const size_t S = (size_t)seq, DS = (size_t)D * S, FS = (size_t)F * S;
@@ -1104,10 +1108,13 @@ float or_train_step(const or_config *cfg, or_train_params *p, or_train_params *m
     float *dy = (float *)malloc(sizeof(float) * DS), *dcur = (float *)malloc(sizeof(float) * DS);
     float *dprev = (float *)malloc(sizeof(float) * DS);
     or_train_params *g = grads;
-    memset(g->rms_final, 0, sizeof(float) * D);
+    /* the window's own final-gain and embedding gradients (e.gRMS, e.gEmbed) */
+    float *g_rms = accumulate ? (float *)malloc(sizeof(float) * D) : g->rms_final;
+    float *g_emb = accumulate ? (float *)malloc(sizeof(float) * (size_t)V * D) : g->embed;
+    memset(g_rms, 0, sizeof(float) * D);
     matmul_embed_t_scale(dy, p->embed, logits, V, D, seq, grad_scale, threads);
-    compact_embed_grad(g->embed, logits, xnf, target, V, D, seq, grad_scale, threads);
-    rms_norm_backward_cf(dcur, g->rms_final, dy, cur, p->rms_final, rfin, D, seq, threads);
+    compact_embed_grad(g_emb, logits, xnf, target, V, D, seq, grad_scale, threads);
+    rms_norm_backward_cf(dcur, g_rms, dy, cur, p->rms_final, rfin, D, seq, threads);
     /* backwardAndApply, CPU path (train_full.go:776-848) */
     float *dout = (float *)malloc(sizeof(float) * DS), *gx2 = (float *)malloc(sizeof(float) * DS);
     float *dx2s = (float *)malloc(sizeof(float) * DS), *gxn = (float *)malloc(sizeof(float) * DS);
@@ -1121,7 +1128,8 @@ float or_train_step(const or_config *cfg, or_train_params *p, or_train_params *m
         float *gt[9];
         size_t gn[9];
         train_layer_tensors(cfg, G, gt, gn);
-        for (int i = 0; i < 9; i++) memset(gt[i], 0, sizeof(float) * gn[i]);   /* clearLayerGrad */
+        if (!accumulate)
+            for (int i = 0; i < 9; i++) memset(gt[i], 0, sizeof(float) * gn[i]);   /* clearLayerGrad */
         for (size_t i = 0; i < DS; i++) dout[i] = dcur[i] * alpha;           /* scaleInto */
         /* backwardFFNCPU (train_full.go:618-627) */
         memcpy(gx2, dcur, sizeof(float) * DS);
@@ -1152,19 +1160,38 @@ float or_train_step(const or_config *cfg, or_train_params *p, or_train_params *m
         accum_linear_grad_cf(G->wv, gv, C->xn, D, D, seq, threads);
         float *sw = dcur; dcur = dprev; dprev = sw;
     }
-    or_embed_backward(g->embed, dcur, input, V, D, seq);
-    /* loss-scale undo, clipping (train_full.go:149-181), Adam (:875-969) */
-    if (hp->loss_scale != 0 && hp->loss_scale != 1) {
-        float inv = (float)(1.0 / (double)hp->loss_scale);
-        for (int l = 0; l < L; l++) {
-            float *gt[9];
-            size_t gn[9];
-            train_layer_tensors(cfg, &g->layers[l], gt, gn);
-            for (int i = 0; i < 9; i++) scale_slice(gt[i], gn[i], inv);
-        }
-        scale_slice(g->rms_final, D, inv);
-        scale_slice(g->embed, (size_t)V * D, inv);
+    or_embed_backward(g_emb, dcur, input, V, D, seq);
+    if (accumulate) {
+        for (int i = 0; i < D; i++) g->rms_final[i] += g_rms[i];
+        for (size_t i = 0; i < (size_t)V * D; i++) g->embed[i] += g_emb[i];
+        free(g_rms);
+        free(g_emb);
     }
+#undef TAKE
+    free(cache); free(rc); free(rs); free(lcs); free(cur); free(next); free(tmp); free(xnf);
+    free(rfin); free(logits); free(dy); free(dcur); free(dprev); free(dout); free(gx2); free(dx2s);
+    free(gxn); free(ggate); free(gh1); free(gh3); free(gatt); free(gq); free(gk); free(gv);
+    return loss;
+}
+
+/* Every gradient tensor of the model scaled by s (scaleModelGrad, train_full.go:133-139). */
+static void scale_all(const or_config *cfg, or_train_params *g, float s) {
+    for (int l = 0; l < cfg->n_layers; l++) {
+        float *gt[9];
+        size_t gn[9];
+        train_layer_tensors(cfg, &g->layers[l], gt, gn);
+        for (int i = 0; i < 9; i++) scale_slice(gt[i], gn[i], s);
+    }
+    scale_slice(g->rms_final, cfg->dim, s);
+    scale_slice(g->embed, (size_t)cfg->vocab * cfg->dim, s);
+}
+
+/* clipLayerGradients (train_full.go:149-181), then Adam at 1-based step step_t
+ * (adamBiasCorrectionInv / adamUpdateCFWithInv, :926-969; applyLayerAdamAll, :875-924). */
+static void clip_and_adam(const or_config *cfg, or_train_params *p, or_train_params *m,
+                          or_train_params *v, or_train_params *g, const or_train_hparams *hp,
+                          int step_t, int apply) {
+    const int D = cfg->dim, V = cfg->vocab, L = cfg->n_layers;
     if (hp->grad_clip > 0) {
         double norm2 = 0;
         for (int l = 0; l < L; l++) {
@@ -1177,43 +1204,56 @@ float or_train_step(const or_config *cfg, or_train_params *p, or_train_params *m
         norm2 += sum_squares(g->embed, (size_t)V * D);
         if (norm2 > 0) {
             float norm = (float)sqrt(norm2);
-            if (norm > hp->grad_clip) {
-                float sc = hp->grad_clip / norm;
-                for (int l = 0; l < L; l++) {
-                    float *gt[9];
-                    size_t gn[9];
-                    train_layer_tensors(cfg, &g->layers[l], gt, gn);
-                    for (int i = 0; i < 9; i++) scale_slice(gt[i], gn[i], sc);
-                }
-                scale_slice(g->rms_final, D, sc);
-                scale_slice(g->embed, (size_t)V * D, sc);
-            }
+            if (norm > hp->grad_clip) scale_all(cfg, g, hp->grad_clip / norm);
         }
     }
-    if (apply) {
-        float inv_bc1 = 1 / (float)(1.0 - pow((double)hp->beta1, (double)step_t));
-        float inv_bc2 = 1 / (float)(1.0 - pow((double)hp->beta2, (double)step_t));
-        for (int l = 0; l < L; l++) {
-            float *pw[9], *gw[9], *mw[9], *vw[9];
-            size_t n[9];
-            train_layer_tensors(cfg, &p->layers[l], pw, n);
-            train_layer_tensors(cfg, &g->layers[l], gw, n);
-            train_layer_tensors(cfg, &m->layers[l], mw, n);
-            train_layer_tensors(cfg, &v->layers[l], vw, n);
-            for (int i = 0; i < 9; i++)
-                adam_update(pw[i], gw[i], mw[i], vw[i], n[i], hp->lr, hp->beta1, hp->beta2, hp->eps,
-                            i < 7 ? hp->weight_decay : 0, inv_bc1, inv_bc2);
-        }
-        adam_update(p->rms_final, g->rms_final, m->rms_final, v->rms_final, D, hp->lr, hp->beta1,
-                    hp->beta2, hp->eps, 0, inv_bc1, inv_bc2);
-        adam_update(p->embed, g->embed, m->embed, v->embed, (size_t)V * D, hp->lr, hp->beta1,
-                    hp->beta2, hp->eps, hp->weight_decay, inv_bc1, inv_bc2);
+    if (!apply) return;
+    float inv_bc1 = 1 / (float)(1.0 - pow((double)hp->beta1, (double)step_t));
+    float inv_bc2 = 1 / (float)(1.0 - pow((double)hp->beta2, (double)step_t));
+    for (int l = 0; l < L; l++) {
+        float *pw[9], *gw[9], *mw[9], *vw[9];
+        size_t n[9];
+        train_layer_tensors(cfg, &p->layers[l], pw, n);
+        train_layer_tensors(cfg, &g->layers[l], gw, n);
+        train_layer_tensors(cfg, &m->layers[l], mw, n);
+        train_layer_tensors(cfg, &v->layers[l], vw, n);
+        for (int i = 0; i < 9; i++)
+            adam_update(pw[i], gw[i], mw[i], vw[i], n[i], hp->lr, hp->beta1, hp->beta2, hp->eps,
+                        i < 7 ? hp->weight_decay : 0, inv_bc1, inv_bc2);
     }
-#undef TAKE
-    free(cache); free(rc); free(rs); free(lcs); free(cur); free(next); free(tmp); free(xnf);
-    free(rfin); free(logits); free(dy); free(dcur); free(dprev); free(dout); free(gx2); free(dx2s);
-    free(gxn); free(ggate); free(gh1); free(gh3); free(gatt); free(gq); free(gk); free(gv);
+    adam_update(p->rms_final, g->rms_final, m->rms_final, v->rms_final, D, hp->lr, hp->beta1,
+                hp->beta2, hp->eps, 0, inv_bc1, inv_bc2);
+    adam_update(p->embed, g->embed, m->embed, v->embed, (size_t)V * D, hp->lr, hp->beta1,
+                hp->beta2, hp->eps, hp->weight_decay, inv_bc1, inv_bc2);
+}
+
+float or_train_step(const or_config *cfg, or_train_params *p, or_train_params *m,
+                    or_train_params *v, or_train_params *grads, const or_train_hparams *hp,
+                    int step_t, const uint16_t *input, const uint16_t *target, int seq,
+                    int apply, int threads) {
+    float loss = train_gradients(cfg, p, grads, hp, input, target, seq, 0, threads);
+    /* loss-scale undo (train_full.go:826-835) */
+    if (hp->loss_scale != 0 && hp->loss_scale != 1)
+        scale_all(cfg, grads, (float)(1.0 / (double)hp->loss_scale));
+    clip_and_adam(cfg, p, m, v, grads, hp, step_t, apply);
     return loss;
+}
+
+float or_train_accumulate(const or_config *cfg, const or_train_params *p, or_train_params *accum,
+                          const or_train_hparams *hp, const uint16_t *input,
+                          const uint16_t *target, int seq, int threads) {
+    return train_gradients(cfg, p, accum, hp, input, target, seq, 1, threads);
+}
+
+void or_train_flush(const or_config *cfg, or_train_params *p, or_train_params *m,
+                    or_train_params *v, or_train_params *accum, const or_train_hparams *hp,
+                    int step_t, int pending) {
+    if (pending <= 0) return;
+    /* engine.go:544-547: float32(1/pending), then divided by the loss scale in float32 */
+    float s = (float)(1.0 / (double)pending);
+    if (hp->loss_scale > 0) s /= hp->loss_scale;
+    scale_all(cfg, accum, s);
+    clip_and_adam(cfg, p, m, v, accum, hp, step_t, 1);
 }
 
 /* engine.go:725-732 drand48Seed / nextFloat64, and Step's window choice (engine.go:307-316):

@@ -133,6 +133,19 @@ float or_train_step(const or_config *cfg, or_train_params *p, or_train_params *m
                     or_train_params *v, or_train_params *grads, const or_train_hparams *hp,
                     int step_t, const uint16_t *input, const uint16_t *target, int seq,
                     int apply, int threads);
+/* One Engine.Step body with AccumSteps > 1 before the flush (backwardAndAccumulate,
+ * train_full.go:709-774, CPU path): this window's gradients (still multiplied by the loss scale)
+ * are added onto accum. Returns the loss. */
+float or_train_accumulate(const or_config *cfg, const or_train_params *p, or_train_params *accum,
+                          const or_train_hparams *hp, const uint16_t *input,
+                          const uint16_t *target, int seq, int threads);
+/* flushPending (engine.go:540-565) after `pending` accumulated windows: accum scaled by
+ * float32(1/pending) / loss scale, clipped, then Adam at 1-based step step_t. On return accum
+ * holds the gradients Adam applied; the reference clears it next (clearModelGrad), which is
+ * left to the caller. pending <= 0 does nothing. */
+void or_train_flush(const or_config *cfg, or_train_params *p, or_train_params *m,
+                    or_train_params *v, or_train_params *accum, const or_train_hparams *hp,
+                    int step_t, int pending);
 /* engine.go:725-732 and :307-316: drand48 state from a seed, its next float64, and the start
  * of the next training window. */
 uint64_t or_drand48_seed(int64_t seed);

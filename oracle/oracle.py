@@ -100,6 +100,11 @@ def load() -> C.CDLL:
         "or_train_step": (C.c_float, [C.POINTER(OrConfig), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.POINTER(OrTrainHparams), C.c_int, C.POINTER(C.c_uint16),
                                       C.POINTER(C.c_uint16), C.c_int, C.c_int, C.c_int]),
+        "or_train_accumulate": (C.c_float, [C.POINTER(OrConfig), C.c_void_p, C.c_void_p,
+                                            C.POINTER(OrTrainHparams), C.POINTER(C.c_uint16),
+                                            C.POINTER(C.c_uint16), C.c_int, C.c_int]),
+        "or_train_flush": (None, [C.POINTER(OrConfig), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                  C.POINTER(OrTrainHparams), C.c_int, C.c_int]),
         "or_drand48_seed": (C.c_uint64, [C.c_int64]),
         "or_drand48_next": (C.c_double, [C.POINTER(C.c_uint64)]),
         "or_train_window": (C.c_uint64, [C.POINTER(C.c_uint64), C.c_int64, C.c_int]),
@@ -276,6 +281,11 @@ class TrainParams:
         return cls([{k: np.zeros_like(l[k]) for k in TRAIN_KEYS} for l in other.layers],
                    np.zeros_like(other.embed), np.zeros_like(other.rms_final))
 
+    def clear(self):
+        """All tensors set to zero in place (clearModelGrad, train_full.go:110-119)."""
+        for _, a in self.tensors():
+            a.fill(0)
+
     def tensors(self):
         """(name, array) pairs in a fixed order."""
         out = []
@@ -298,6 +308,24 @@ def train_step(cfg: OrConfig, params: TrainParams, m: TrainParams, v: TrainParam
     return load().or_train_step(C.byref(cfg), C.byref(params.s), C.byref(m.s), C.byref(v.s), C.byref(grads.s),
                                 C.byref(hp), step_t, i.ctypes.data_as(C.POINTER(C.c_uint16)),
                                 t.ctypes.data_as(C.POINTER(C.c_uint16)), i.size, int(apply), threads)
+
+
+def train_accumulate(cfg: OrConfig, params: TrainParams, accum: TrainParams, hp: OrTrainHparams, inp, tgt,
+                     threads: int = 1) -> float:
+    """or_train_accumulate: backwardAndAccumulate (train_full.go:709-774) on a given window."""
+    i = np.ascontiguousarray(np.asarray(inp, dtype=np.uint16))
+    t = np.ascontiguousarray(np.asarray(tgt, dtype=np.uint16))
+    assert i.size == t.size
+    return load().or_train_accumulate(C.byref(cfg), C.byref(params.s), C.byref(accum.s), C.byref(hp),
+                                      i.ctypes.data_as(C.POINTER(C.c_uint16)),
+                                      t.ctypes.data_as(C.POINTER(C.c_uint16)), i.size, threads)
+
+
+def train_flush(cfg: OrConfig, params: TrainParams, m: TrainParams, v: TrainParams, accum: TrainParams,
+                hp: OrTrainHparams, step_t: int, pending: int) -> None:
+    """or_train_flush: flushPending (engine.go:540-565); accum keeps the applied gradients."""
+    load().or_train_flush(C.byref(cfg), C.byref(params.s), C.byref(m.s), C.byref(v.s), C.byref(accum.s),
+                          C.byref(hp), step_t, pending)
 
 
 def cross_entropy_loss(logits_cf: np.ndarray, targets):

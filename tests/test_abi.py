@@ -108,5 +108,8 @@ def test_trainer_refuses_unsupported_models_and_options():
     with pytest.raises(sh.ShError, match="Stories-shaped"):
         sh.Trainer(cfg, seq=8)
     cfg.n_kv_heads = 4
-    with pytest.raises(sh.ShError, match="accumulation"):
-        sh.Trainer(cfg, seq=8, accum_steps=4)
+    with pytest.raises(sh.ShError, match="seq must be <= 4096"):
+        sh.Trainer(cfg, seq=8192, accum_steps=4)
+    lib = sh.load()
+    assert lib.sh_trainer_flush(None) == -1   # engine.go:399-401
+    assert "engine is closed" in sh.last_error()

@@ -215,3 +215,90 @@ def test_window_rng_is_drand48():
     for _ in range(4):
         u = L.or_drand48_next(ctypes.byref(st2))
         assert L.or_train_window(ctypes.byref(st), 1000, 256) == int(u * (1000 - 256 - 1))
+
+
+# ---- gradient accumulation (backwardAndAccumulate + flushPending) -------------------------
+
+def test_accumulate_one_window_then_flush_is_the_plain_step():
+    # with one pending window the flush scale float32(1)/256 is the plain step's 1/256, and
+    # adding onto zero sums changes nothing: the result is bit-identical
+    cfg = train_config()
+    ocfg = oracle.config_from(cfg)
+    _, p1, inp, tgt = setup(cfg, 241, gains=True)
+    _, p2, _, _ = setup(cfg, 241, gains=True)
+    hp = oracle.hparams(lr=1e-3, weight_decay=0.1, grad_clip=5e-2)
+    m1, v1, g1 = (oracle.TrainParams.zeros_like(p1) for _ in range(3))
+    m2, v2, acc = (oracle.TrainParams.zeros_like(p2) for _ in range(3))
+    l1 = oracle.train_step(ocfg, p1, m1, v1, g1, hp, 1, inp, tgt, threads=2)
+    l2 = oracle.train_accumulate(ocfg, p2, acc, hp, inp, tgt, threads=2)
+    oracle.train_flush(ocfg, p2, m2, v2, acc, hp, 1, 1)
+    assert l1 == l2
+    for a, b in ((p1, p2), (m1, m2), (v1, v2), (g1, acc)):
+        for (name, x), (_, y) in zip(a.tensors(), b.tensors()):
+            assert np.array_equal(x, y), name
+
+
+def test_accumulated_sums_are_the_sum_of_window_gradients():
+    # d(L_a + L_b) = dL_a + dL_b: the accumulator after two windows against the plain step's
+    # gradients of each (times the loss scale, a power of two). Products and the embedding and
+    # final-gain rows add once per window, exactly; the layer gains' sums continue over the
+    # second window's rows (rmsNormBackward into the accumulator), a rounding-level difference.
+    cfg = train_config()
+    ocfg = oracle.config_from(cfg)
+    _, p, inp, tgt = setup(cfg, 251, gains=True)
+    toks_b = sh.synth_tokens(13, 252, cfg.vocab)
+    hp = oracle.hparams()
+    z = lambda: oracle.TrainParams.zeros_like(p)
+    ga, gb, acc = z(), z(), z()
+    oracle.train_step(ocfg, p, z(), z(), ga, hp, 1, inp, tgt, apply=False)
+    oracle.train_step(ocfg, p, z(), z(), gb, hp, 1, toks_b[:-1], toks_b[1:], apply=False)
+    oracle.train_accumulate(ocfg, p, acc, hp, inp, tgt)
+    oracle.train_accumulate(ocfg, p, acc, hp, toks_b[:-1], toks_b[1:])
+    for (name, a), (_, b), (_, s) in zip(ga.tensors(), gb.tensors(), acc.tensors()):
+        want = a * np.float32(256) + b * np.float32(256)
+        if name.endswith(("rms_att", "rms_ffn")):
+            np.testing.assert_allclose(s, want, rtol=1e-5, atol=1e-7 * float(np.max(np.abs(want))), err_msg=name)
+        else:
+            assert np.array_equal(s, want), name
+
+
+def test_flush_of_a_repeated_window_is_one_plain_step():
+    # the mean of two identical windows is that window's gradient: scale 1/(2*256) is exact,
+    # so products, embedding and final gain match the plain step bit for bit
+    cfg = train_config()
+    ocfg = oracle.config_from(cfg)
+    _, p1, inp, tgt = setup(cfg, 261)
+    _, p2, _, _ = setup(cfg, 261)
+    hp = oracle.hparams(lr=1e-3)
+    m1, v1, g1 = (oracle.TrainParams.zeros_like(p1) for _ in range(3))
+    m2, v2, acc = (oracle.TrainParams.zeros_like(p2) for _ in range(3))
+    oracle.train_step(ocfg, p1, m1, v1, g1, hp, 1, inp, tgt)
+    oracle.train_accumulate(ocfg, p2, acc, hp, inp, tgt)
+    oracle.train_accumulate(ocfg, p2, acc, hp, inp, tgt)
+    oracle.train_flush(ocfg, p2, m2, v2, acc, hp, 1, 2)
+    for (name, a), (_, b) in zip(p1.tensors(), p2.tensors()):
+        if name.endswith(("rms_att", "rms_ffn")):
+            assert float(np.max(np.abs(a - b))) <= 1e-6, name
+        else:
+            assert np.array_equal(a, b), name
+
+
+def test_flush_pending_reference_case():
+    # ane/storiesane/engine_test.go:107-152 TestFlushPendingAppliesUpdate: two pending windows,
+    # lr 1e-3, loss scale, betas and eps zero, no layers. Adam's step 1 with beta 0 is
+    # w - lr * g/|g|, and the applied gradients are the sums halved. (The reference's embedding
+    # has 3 values against a 2-value gain; here dim 2, vocab 2.)
+    c = oracle.OrConfig()
+    c.dim, c.vocab, c.n_layers = 2, 2, 0
+    p = oracle.TrainParams([], np.array([[1, 2], [3, 4]], np.float32), np.array([1, 1], np.float32))
+    acc = oracle.TrainParams([], np.array([[3, 6], [9, 12]], np.float32), np.array([2, 4], np.float32))
+    m, v = oracle.TrainParams.zeros_like(p), oracle.TrainParams.zeros_like(p)
+    hp = oracle.hparams(lr=1e-3, beta1=0.0, beta2=0.0, eps=0.0, loss_scale=0.0)
+    oracle.train_flush(c, p, m, v, acc, hp, 1, 2)
+    lr = np.float32(1e-3)
+    assert np.array_equal(p.rms_final, np.float32(1) - lr * np.ones(2, np.float32))
+    assert np.array_equal(p.embed, np.array([[1, 2], [3, 4]], np.float32) - lr)
+    assert acc.rms_final.tolist() == [1, 2] and acc.embed.tolist() == [[1.5, 3], [4.5, 6]]
+    # nothing pending: no update
+    oracle.train_flush(c, p, m, v, acc, hp, 2, 0)
+    assert np.array_equal(p.rms_final, np.float32(1) - lr * np.ones(2, np.float32))
