@@ -179,6 +179,29 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &g, int m, int n, f
     }
 }
 
+// A wave's FM x FN blocks of 16 x 16 results (rows from mb, columns from nb) to the K-range
+// partials (more than one range) or through the epilogue. D layout: lane holds column
+// lane%16 of each block, rows 4*(lane/16) + r.
+template <int FM, int FN>
+__device__ __forceinline__ void tile_out(const GemmArgs &g, float *partial, const f32x4 (&acc)[FM][FN], int mb,
+                                         int nb, int lane) {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int n = nb + j * 16 + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = mb + i * 16 + (lane >> 4) * 4 + r;
+                const float v = acc[i][j][r];
+                const float vr = __shfl_xor(v, 1, 64);   // column n ^ 1, same row
+                if (m >= g.M) continue;
+                if (gridDim.z > 1) partial[((size_t)blockIdx.z * g.M + m) * g.N + n] = v;
+                else tile_epilogue(g, m, n, v, vr);
+            }
+        }
+}
+
 // Tiled MFMA GEMM: C[M, N] = A[M, K] . W[N, K]^T, A as hi/lo operand planes. Workgroup tile
 // BM x BN (2 x 2 waves of BM/2 x BN/2, 16 x 16 x 32 MFMA blocks), K in steps of 32 through
 // two LDS buffers: the next step's A hi, A lo and W rows are loaded into registers while
@@ -252,22 +275,82 @@ __global__ __launch_bounds__(kT) void k_gemm_tiled(GemmArgs g, float *partial, i
         __syncthreads();
         buf ^= 1;
     }
-    // D layout: lane holds column fr of each 16 x 16 block, rows 4*(lane/16) + r
+    tile_out<FM, FN>(g, partial, acc, m0 + wm, n0 + wn, lane);
+}
+
+// Burst form of k_gemm_tiled for K ranges that are a multiple of 32*NB: each burst issues
+// the global loads of NB consecutive K steps at once and then feeds them through the two LDS
+// buffers a step at a time, so a workgroup waits out one load latency per burst rather than
+// one per step (short K ranges of small-M products are latency-bound, not MFMA-bound). The
+// LDS tiles, fragments and epilogue are k_gemm_tiled's. One barrier per step suffices: a
+// buffer is rewritten two steps after it was read, and every wave has passed the barrier
+// between.
+template <int DT, int BM, int BN, int NB>
+__global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, int kc) {
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+    constexpr int RS = 80;
+    constexpr int R = 2 * BM + BN;
+    constexpr int PER = R * 4 / kT;
+    static_assert(kT == 256 && BM % 64 == 0 && NB % 2 == 0, "64 rows per chunk index; bursts of even length");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][R * RS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int kbeg = blockIdx.z * kc, kend = kbeg + kc;
+    const size_t lo = (size_t)g.M * g.K;
+    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+    u32x4 stage[NB][PER];
+    f32x4 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int n = n0 + wn + j * 16 + fr;
+        for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int fr = lane & 15, fc = (lane >> 4) * 16;
+    for (int kb = kbeg; kb < kend; kb += NB * 32) {
+        // chunk j of a thread is row 64*j + tid/4 of the tile (A hi, A lo or W by j alone, as
+        // BM is a multiple of 64), 16 bytes at k + 8*(tid%4); rows past M load row M-1 and
+        // are zeroed, so no load sits under a branch and the waits count loads in order
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm + i * 16 + (lane >> 4) * 4 + r;
-                const float v = acc[i][j][r];
-                const float vr = __shfl_xor(v, 1, 64);   // column n ^ 1, same row
-                if (m >= g.M) continue;
-                if (gridDim.z > 1) partial[((size_t)blockIdx.z * g.M + m) * g.N + n] = v;
-                else tile_epilogue(g, m, n, v, vr);
+        for (int st = 0; st < NB; st++) {
+            const int k = kb + st * 32 + (tid & 3) * 8;
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int rr = j * 64 + (tid >> 2);
+                if (j * 64 < 2 * BM) {
+                    const int m = m0 + (j * 64 < BM ? rr : rr - BM);
+                    const uint16_t *src = g.A + (j * 64 < BM ? 0 : lo) + (size_t)min(m, g.M - 1) * g.K + k;
+                    const u32x4 v = *(const u32x4 *)src;
+                    stage[st][j] = m < g.M ? v : zero;
+                } else {
+                    stage[st][j] = *(const u32x4 *)(g.B + (size_t)(n0 + rr - 2 * BM) * g.K + k);
+                }
             }
         }
+#pragma unroll
+        for (int st = 0; st < NB; st++) {
+            uint8_t *L = lds[st & 1];
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int ci = tid + j * kT;
+                *(u32x4 *)(&L[(ci >> 2) * RS + (ci & 3) * 16]) = stage[st][j];
+            }
+            __syncthreads();
+            u32x4 bfr[FN];
+#pragma unroll
+            for (int j = 0; j < FN; j++) bfr[j] = *(const u32x4 *)(L + (2 * BM + wn + j * 16 + fr) * RS + fc);
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                const u32x4 ah = *(const u32x4 *)(L + (wm + i * 16 + fr) * RS + fc);
+                const u32x4 al = *(const u32x4 *)(L + (BM + wm + i * 16 + fr) * RS + fc);
+#pragma unroll
+                for (int j = 0; j < FN; j++) {
+                    acc[i][j] = mfma16<DT>(ah, bfr[j], acc[i][j]);
+                    acc[i][j] = mfma16<DT>(al, bfr[j], acc[i][j]);
+                }
+            }
+        }
+    }
+    tile_out<FM, FN>(g, partial, acc, m0 + wm, n0 + wn, lane);
 }
 
 template <int KVT>
@@ -376,12 +459,15 @@ __global__ __launch_bounds__(1024) void k_row_qkv(const float *partial, int rang
     qk_rope_row<KVT>(row, m, a);
 }
 
-// Batched decode: row m of a residual projection, x_out = resid + alpha * (sum of the K-range
-// partials), then rmsNormVec of x_out with `gain` (infer.go:301-311) as a GEMM operand row.
+// Row m of a residual projection, x_out = resid + alpha * (sum of the K-range partials, in
+// range order), then x_out normalised with `gain` as a GEMM operand row: final_form 0 is
+// rmsNormVec / rmsNormCFWithRRMSImpl (infer.go:301-311, accel_other.go:11-28: float32 scale,
+// x*scale*w), 1 is stories.RMSNorm (cpu.go:97-111: the float64 product rounded once).
 __global__ __launch_bounds__(1024) void k_row_resid_norm(const float *partial, int ranges, int M,
                                                          int D, const float *resid, float alpha,
                                                          float *x_out, const float *gain,
-                                                         double eps, int dt, uint16_t *xn) {
+                                                         double eps, int final_form, int dt,
+                                                         uint16_t *xn) {
     __shared__ float row[4096];
     __shared__ double red[1024 / 64];
     const int m = blockIdx.x;
@@ -395,9 +481,11 @@ __global__ __launch_bounds__(1024) void k_row_resid_norm(const float *partial, i
         ss += (double)x * (double)x;
     }
     const double tot = block_sum(ss, red);
-    const float scale = (float)(1.0 / sqrt(tot / (double)D + eps));
+    const double rr = 1.0 / sqrt(tot / (double)D + eps);
+    const float scale = (float)rr;
     for (int i = threadIdx.x; i < D; i += blockDim.x)
-        store_op(xn, (size_t)m * D + i, (size_t)M * D, row[i] * scale * gain[i], dt);
+        store_op(xn, (size_t)m * D + i, (size_t)M * D,
+                 final_form ? (float)((double)row[i] * rr * (double)gain[i]) : row[i] * scale * gain[i], dt);
 }
 
 // Two 16-bit operand values packed as the MFMA expects (element 2i in the low half).
@@ -429,45 +517,57 @@ __device__ __forceinline__ float sum_rows(float v) {
 }
 
 // Causal attention of the full-sequence forward on MFMA (forward_common.go:5-33, flash
-// style). Workgroup = 64 query rows x one head, wave w owning rows q0+16w .. +15; row t is
-// position rowpos[t] of its sequence, whose keys are j in [t - rowpos[t], t], and only the
-// 64-key blocks some row of the workgroup can see are visited.
+// style). Workgroup = 16 query rows x one head; row t is position rowpos[t] of its sequence,
+// whose keys are j in [t - rowpos[t], t]. The key blocks (BK keys) that some row of the tile
+// can see are dealt round-robin to the four waves, each with its own LDS slice, so a short
+// tile's blocks run side by side rather than one after another; the waves' softmax states
+// (running max, sum, unnormalised O) are merged through LDS at the end. S/16 x H workgroups
+// keep the CUs busy at S = 256, where S/64 x H did not.
 //
-// Per key block the workgroup stages K ([key][dim]) and V transposed ([dim][key]) in LDS as
-// 16-bit operand planes. Each wave computes S^T = K . Q^T with v_mfma_f32_16x16x32 (A = K
-// rows, B = its 16 queries), so a lane holds one query (lane % 16) and 16 of the block's
-// keys: key 16j + 4(lane/16) + r of tile j, register r. An online softmax per query (running
-// max uniform over the query's four lanes, per-lane partial sums) gives P, which is already
-// in the B-operand layout of O^T = V^T . P^T (lane = query, k slots = the lane's 8 keys of a
+// Per key block a wave stages K ([key][dim]) and V transposed ([dim][key]) in its LDS slice as
+// 16-bit operand planes, then computes S^T = K . Q^T with v_mfma_f32_16x16x32 (A = K rows,
+// B = the 16 queries), so a lane holds one query (lane % 16) and 16 of the block's keys: key
+// 16j + 4(lane/16) + r of tile j, register r. An online softmax per query (running max
+// uniform over the query's four lanes, per-lane partial sums) gives P, which is already in
+// the B-operand layout of O^T = V^T . P^T (lane = query, k slots = the lane's 8 keys of a
 // 32-key step), and V^T rows are read in the same key order. O^T accumulates per lane as
 // query lane % 16, dims 16i + 4(lane/16) + r, so the softmax rescale is per lane.
 //
 // Operands are hi/lo pairs of the model's 16-bit type: Q and P always; K and V too (LO) when
 // they are fp32 rather than values already rounded to this type by the KV cache. The products
 // hi.hi + lo.hi + hi.lo keep about 16 (bf16) or 22 (fp16) significant bits, fp32 accumulate.
+template <int HD> constexpr int attn_bk() { return HD >= 128 ? 32 : 64; }
+template <int HD> constexpr size_t attn_lds_bytes() {
+    // per wave: K rows (HD*2 + 16 bytes) and V^T rows (BK*2 + 8 bytes), hi and lo planes
+    return (size_t)4 * 2 * (attn_bk<HD>() * (HD * 2 + 16) + HD * (attn_bk<HD>() * 2 + 8));
+}
 template <int DT, int HD, bool LO>
 __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const float *kf,
                                                           const float *vf, int S,
                                                           const int32_t *rowpos, int H, int KVH,
                                                           float scale, uint16_t *att, size_t plane) {
-    constexpr int BQ = 64, BK = 64, NP = LO ? 2 : 1;
+    constexpr int BQ = 16, BK = attn_bk<HD>(), NP = LO ? 2 : 1, NW = kT / 64;
     constexpr int KRS = HD * 2 + 16;              // LDS bytes per K row (16-byte pad)
     constexpr int VRS = BK * 2 + 8;               // LDS bytes per V^T row (8-byte pad)
-    constexpr int KT = BK * HD / 8;               // K staging tasks: (key, 8 dims)
-    constexpr int VT = (BK / 4) * (HD / 4);       // V staging tasks: (4 keys, 4 dims)
-    constexpr int KPT = (KT + kT - 1) / kT, VPT = (VT + kT - 1) / kT;
+    constexpr int KPT = BK * HD / 8 / 64;         // K staging tasks (key, 8 dims) per lane
+    constexpr int VPT = (BK / 4) * (HD / 4) / 64; // V staging tasks (4 keys, 4 dims) per lane
     constexpr int NS = HD / 32, NO = HD / 16;     // QK k-steps, O^T tiles
-    __shared__ __attribute__((aligned(16))) uint8_t ks[NP][BK * KRS];
-    __shared__ __attribute__((aligned(16))) uint8_t vts[NP][HD * VRS];
+    constexpr int KSL = BK * KRS, VSL = HD * VRS; // one plane of a wave's K / V^T slice
+    constexpr int OLD = HD + 4;                   // merge: floats per (wave, query) O row
+    static_assert(KPT * 64 * 8 == BK * HD && VPT * 64 * 16 == BK * HD, "staging splits evenly");
+    static_assert((size_t)NW * (BQ * OLD + 2 * BQ) * 4 <= attn_lds_bytes<HD>(), "merge fits");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[attn_lds_bytes<HD>()];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g4 = lane >> 4, ql = lane & 15;
     const int q0 = blockIdx.x * BQ, h = blockIdx.y;
     const int qdim = H * HD, kvdim = KVH * HD, kvh = h / (H / KVH);
-    const int kstart = q0 - rowpos[q0];
     const int qlast = min(q0 + BQ, S) - 1;
+    const int kb0 = (q0 - rowpos[q0]) & ~(BK - 1);
+    uint8_t *ksl = lds + (size_t)wave * NP * (KSL + VSL);   // this wave's K planes, then V^T
+    uint8_t *vsl = ksl + NP * KSL;
 
     // this lane's query and its Q operand planes (B operand: dims 32s + 8*g4 .. +7)
-    const int t = q0 + 16 * wave + ql;
+    const int t = q0 + ql;
     const bool tok = t < S;
     const int jlo = tok ? t - rowpos[t] : 0x7fffffff;
     u32x4 qh[NS], qlo[NS];
@@ -484,63 +584,57 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
         }
         split8<DT>(f, qh[s], qlo[s]);
     }
-    const int wlast = min(q0 + 16 * wave + 15, S - 1);   // the wave's last row
 
-    // staging registers for the next key block
+    // staging registers for the wave's next key block
     f32x4 kst[KPT][2], vst[VPT][4];
     auto gload = [&](int kb) {
 #pragma unroll
         for (int u = 0; u < KPT; u++) {
-            const int c = tid + u * kT;
-            if (KT % kT != 0 && c >= KT) break;
+            const int c = lane + u * 64;
             const int r = c / (HD / 8), d = (c % (HD / 8)) * 8, j = kb + r;
-            const float *src = kf + (size_t)j * kvdim + kvh * HD + d;
-            kst[u][0] = j < S ? *(const f32x4 *)src : f32x4{0.f, 0.f, 0.f, 0.f};
-            kst[u][1] = j < S ? *(const f32x4 *)(src + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const float *src = kf + (size_t)min(j, S - 1) * kvdim + kvh * HD + d;
+            const f32x4 a = *(const f32x4 *)src, b = *(const f32x4 *)(src + 4);
+            kst[u][0] = j < S ? a : f32x4{0.f, 0.f, 0.f, 0.f};
+            kst[u][1] = j < S ? b : f32x4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
         for (int u = 0; u < VPT; u++) {
-            const int c = tid + u * kT;
-            if (VT % kT != 0 && c >= VT) break;
+            const int c = lane + u * 64;
             const int kq = c / (HD / 4), d = (c % (HD / 4)) * 4;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int j = kb + 4 * kq + i;
-                vst[u][i] = j < S ? *(const f32x4 *)(vf + (size_t)j * kvdim + kvh * HD + d)
-                                  : f32x4{0.f, 0.f, 0.f, 0.f};
+                const f32x4 a = *(const f32x4 *)(vf + (size_t)min(j, S - 1) * kvdim + kvh * HD + d);
+                vst[u][i] = j < S ? a : f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
     };
     auto lstore = [&]() {
 #pragma unroll
         for (int u = 0; u < KPT; u++) {
-            const int c = tid + u * kT;
-            if (KT % kT != 0 && c >= KT) break;
+            const int c = lane + u * 64;
             const int r = c / (HD / 8), d = (c % (HD / 8)) * 8;
             const float f[8] = {kst[u][0].x, kst[u][0].y, kst[u][0].z, kst[u][0].w,
                                 kst[u][1].x, kst[u][1].y, kst[u][1].z, kst[u][1].w};
             u32x4 hi, lo;
             split8<DT>(f, hi, lo);
-            *(u32x4 *)&ks[0][r * KRS + d * 2] = hi;
-            if constexpr (LO) *(u32x4 *)&ks[NP - 1][r * KRS + d * 2] = lo;
+            *(u32x4 *)&ksl[r * KRS + d * 2] = hi;
+            if constexpr (LO) *(u32x4 *)&ksl[KSL + r * KRS + d * 2] = lo;
         }
 #pragma unroll
         for (int u = 0; u < VPT; u++) {
-            const int c = tid + u * kT;
-            if (VT % kT != 0 && c >= VT) break;
+            const int c = lane + u * 64;
             const int kq = c / (HD / 4), d = (c % (HD / 4)) * 4;
 #pragma unroll
             for (int i = 0; i < 4; i++) {   // dim d + i: keys 4kq .. 4kq+3
                 const float a0 = vst[u][0][i], a1 = vst[u][1][i], a2 = vst[u][2][i], a3 = vst[u][3][i];
-                const uint32_t h01 = pack2<DT>(a0, a1), h23 = pack2<DT>(a2, a3);
-                *(uint2 *)&vts[0][(d + i) * VRS + 8 * kq] = uint2{h01, h23};
+                *(uint2 *)&vsl[(d + i) * VRS + 8 * kq] = uint2{pack2<DT>(a0, a1), pack2<DT>(a2, a3)};
                 if constexpr (LO) {
                     const float r0 = a0 - bits_to_f(f_to_bits(a0, DT), DT);
                     const float r1 = a1 - bits_to_f(f_to_bits(a1, DT), DT);
                     const float r2 = a2 - bits_to_f(f_to_bits(a2, DT), DT);
                     const float r3 = a3 - bits_to_f(f_to_bits(a3, DT), DT);
-                    *(uint2 *)&vts[NP - 1][(d + i) * VRS + 8 * kq] =
-                        uint2{pack2<DT>(r0, r1), pack2<DT>(r2, r3)};
+                    *(uint2 *)&vsl[VSL + (d + i) * VRS + 8 * kq] = uint2{pack2<DT>(r0, r1), pack2<DT>(r2, r3)};
                 }
             }
         }
@@ -550,14 +644,15 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
     f32x4 o[NO];
 #pragma unroll
     for (int i = 0; i < NO; i++) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int kb0 = kstart & ~(BK - 1);
-    gload(kb0);
-    for (int kb = kb0; kb <= qlast; kb += BK) {
-        __syncthreads();   // every wave is done reading the previous block
-        lstore();
-        __syncthreads();
-        if (kb + BK <= qlast) gload(kb + BK);
-        if (q0 + 16 * wave >= S || wlast < kb) continue;   // no row of this wave sees the block
+    const int nb = (qlast - kb0) / BK + 1;   // key blocks some row of the tile can see
+    int bi = wave;                           // this wave's block index
+    if (bi < nb) gload(kb0 + bi * BK);
+    for (; bi < nb; bi += NW) {
+        const int kb = kb0 + bi * BK;
+        lstore();                            // the wave's own slice: its LDS ops stay in order
+        if (bi + NW < nb) gload(kb + NW * BK);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
         // S^T tiles: keys 16j + 4*g4 + r (register r) for query ql
         f32x4 sc[BK / 16];
 #pragma unroll
@@ -566,10 +661,10 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
 #pragma unroll
             for (int s = 0; s < NS; s++) {
                 const int off = (16 * j + ql) * KRS + 64 * s + 16 * g4;
-                const u32x4 kh = *(const u32x4 *)&ks[0][off];
+                const u32x4 kh = *(const u32x4 *)&ksl[off];
                 acc = mfma16<DT>(kh, qh[s], acc);
                 acc = mfma16<DT>(kh, qlo[s], acc);
-                if constexpr (LO) acc = mfma16<DT>(*(const u32x4 *)&ks[NP - 1][off], qh[s], acc);
+                if constexpr (LO) acc = mfma16<DT>(*(const u32x4 *)&ksl[KSL + off], qh[s], acc);
             }
             sc[j] = acc;
         }
@@ -590,7 +685,7 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
         l_part *= rescale;
 #pragma unroll
         for (int i = 0; i < NO; i++) o[i] *= rescale;
-        // P (unnormalised) as B operands of O^T = V^T . P^T, two 32-key steps
+        // P (unnormalised) as B operands of O^T = V^T . P^T, 32-key steps
 #pragma unroll
         for (int s2 = 0; s2 < BK / 32; s2++) {
             float p[8];
@@ -607,25 +702,48 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
 #pragma unroll
             for (int i = 0; i < NO; i++) {
                 const int off = (16 * i + ql) * VRS + 64 * s2 + 8 * g4;
-                const uint2 a0 = *(const uint2 *)&vts[0][off], a1 = *(const uint2 *)&vts[0][off + 32];
+                const uint2 a0 = *(const uint2 *)&vsl[off], a1 = *(const uint2 *)&vsl[off + 32];
                 const u32x4 vh = u32x4{a0.x, a0.y, a1.x, a1.y};
                 o[i] = mfma16<DT>(vh, ph, o[i]);
                 o[i] = mfma16<DT>(vh, pl, o[i]);
                 if constexpr (LO) {
-                    const uint2 b0 = *(const uint2 *)&vts[NP - 1][off], b1 = *(const uint2 *)&vts[NP - 1][off + 32];
+                    const uint2 b0 = *(const uint2 *)&vsl[VSL + off], b1 = *(const uint2 *)&vsl[VSL + off + 32];
                     o[i] = mfma16<DT>(u32x4{b0.x, b0.y, b1.x, b1.y}, ph, o[i]);
                 }
             }
         }
+        // the next lstore rewrites this slice: its reads above must be issued first
+        __builtin_amdgcn_wave_barrier();
     }
-    const float l_tot = sum_rows(l_part);
-    if (!tok) return;
-    const float inv = 1.0f / l_tot;
+    // merge: wave w's (max, sum, O) for query q at mo[w][q], lo[w][q], oo[w][q][dim]
+    const float l_w = sum_rows(l_part);
+    __syncthreads();   // every wave is done with its K / V slices
+    float *oo = (float *)lds;
+    float *mo = oo + NW * BQ * OLD, *lsum = mo + NW * BQ;
+    if (g4 == 0) {
+        mo[wave * BQ + ql] = m_run;
+        lsum[wave * BQ + ql] = l_w;
+    }
 #pragma unroll
     for (int i = 0; i < NO; i++)
+        *(f32x4 *)&oo[(wave * BQ + ql) * OLD + 16 * i + 4 * g4] = o[i];
+    __syncthreads();
+    for (int e = tid; e < BQ * HD; e += kT) {
+        const int q = e / HD, d = e % HD, tq = q0 + q;
+        if (tq >= S) continue;
+        float mm = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-            store_op(att, (size_t)t * qdim + h * HD + 16 * i + 4 * g4 + r, plane, o[i][r] * inv, DT);
+        for (int w = 0; w < NW; w++) mm = fmaxf(mm, mo[w * BQ + q]);
+        float lt = 0.f, ot = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float mw = mo[w * BQ + q];
+            const float f = mw == -INFINITY ? 0.f : expf(mw - mm);
+            lt += lsum[w * BQ + q] * f;
+            ot += oo[(w * BQ + q) * OLD + d] * f;
+        }
+        store_op(att, (size_t)tq * qdim + h * HD + d, plane, ot * (1.0f / lt), DT);
+    }
 }
 
 // Causal attention (forward_common.go:5-33): one wave per (query t, head h). Row t is
@@ -1463,22 +1581,39 @@ GemmPlan gemm_plan(int M, int N, int K) {
     return p;
 }
 
-hipError_t gemm(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipStream_t s) {
+// ranges_out given: K-range partials are left for the caller's row kernel (*ranges_out > 1)
+// instead of being summed here; with one range the epilogue runs as usual.
+hipError_t gemm(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipStream_t s,
+                int *ranges_out = nullptr) {
     if (g.K % 32 || g.N % 64) return hipErrorInvalidValue;
     const GemmPlan p = gemm_plan(g.M, g.N, g.K);
     if (p.ranges > 1 && (!partial || (size_t)p.ranges * g.M * g.N > part_cap))
         return hipErrorInvalidValue;   // the partial buffer must hold every K range
+    // burst loads where the K range allows them (8 steps of 32 per burst for 64 x 64 tiles,
+    // 4 for 128 x 128, whose staging registers are twice as many per step)
+    const bool bf = dt == SH_DTYPE_BF16;
     if (p.big) {
         const dim3 grid((g.M + 127) / 128, g.N / 128, p.ranges);
-        if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_BF16, 128, 128>), grid, dim3(kT), 0, s, g, partial, p.kc);
-        else hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_F16, 128, 128>), grid, dim3(kT), 0, s, g, partial, p.kc);
+        if (p.kc % 128 == 0) {
+            if (bf) hipLaunchKernelGGL((k_gemm_burst<SH_DTYPE_BF16, 128, 128, 4>), grid, dim3(kT), 0, s, g, partial, p.kc);
+            else hipLaunchKernelGGL((k_gemm_burst<SH_DTYPE_F16, 128, 128, 4>), grid, dim3(kT), 0, s, g, partial, p.kc);
+        } else {
+            if (bf) hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_BF16, 128, 128>), grid, dim3(kT), 0, s, g, partial, p.kc);
+            else hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_F16, 128, 128>), grid, dim3(kT), 0, s, g, partial, p.kc);
+        }
     } else {
         const dim3 grid((g.M + 63) / 64, g.N / 64, p.ranges);
-        if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_BF16, 64, 64>), grid, dim3(kT), 0, s, g, partial, p.kc);
-        else hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_F16, 64, 64>), grid, dim3(kT), 0, s, g, partial, p.kc);
+        if (p.kc % 256 == 0) {
+            if (bf) hipLaunchKernelGGL((k_gemm_burst<SH_DTYPE_BF16, 64, 64, 8>), grid, dim3(kT), 0, s, g, partial, p.kc);
+            else hipLaunchKernelGGL((k_gemm_burst<SH_DTYPE_F16, 64, 64, 8>), grid, dim3(kT), 0, s, g, partial, p.kc);
+        } else {
+            if (bf) hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_BF16, 64, 64>), grid, dim3(kT), 0, s, g, partial, p.kc);
+            else hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_F16, 64, 64>), grid, dim3(kT), 0, s, g, partial, p.kc);
+        }
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.ranges == 1) return e;
+    if (ranges_out) *ranges_out = p.ranges;
+    if (e != hipSuccess || p.ranges == 1 || ranges_out) return e;
     const int pairs = g.M * (g.N / 2);
     hipLaunchKernelGGL(k_gemm_skinny_reduce, dim3((pairs + kT - 1) / kT), dim3(kT), 0, s, g,
                        (const float *)partial, p.ranges);
@@ -1498,8 +1633,8 @@ bool prefill_supported(const sh_model *m, std::string *why) {
         *why = "full-sequence forward needs dims that are multiples of 64";
         return false;
     }
-    if (m->qkv_rows > 4096) {
-        *why = "q/k/v width above 4096";
+    if (m->qkv_rows > 4096 || c.dim > 4096) {
+        *why = "q/k/v width or dim above 4096";
         return false;
     }
     return true;
@@ -1627,7 +1762,7 @@ hipError_t launch_attn_prefill(const sh_model *m, int S, int seg_max, bool fill_
     const size_t plane = (size_t)S * m->qdim;
     const bool exact = fill_kv && ((c.kv_dtype == SH_KV_BF16 && dt == SH_DTYPE_BF16) ||
                                    (c.kv_dtype == SH_KV_F16 && dt == SH_DTYPE_F16));
-    const dim3 grid((S + 63) / 64, c.n_heads);
+    const dim3 grid((S + 15) / 16, c.n_heads);
 #define SH_ATT(DTV, HDV, LOV)                                                                   \
     hipLaunchKernelGGL((k_attn_prefill_mfma<DTV, HDV, LOV>), grid, dim3(kT), 0, s, m->pf_q,     \
                        m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale,        \
@@ -1665,8 +1800,14 @@ hipError_t launch_attn_prefill(const sh_model *m, int S, int seg_max, bool fill_
 namespace {
 
 // One layer of the forward over the S token-major rows in pf_x (rows as in enqueue_prefill);
-// the layer's output replaces pf_x.
-hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv) {
+// the layer's output replaces pf_x. in_normed: pf_xn already holds pf_x normalised with this
+// layer's rms_att. next_gain (optional): the gain the caller normalises the output with next
+// (next_final: stories.RMSNorm's form); where the last projection leaves K-range partials, the
+// row kernel that sums them also writes those normalised rows to pf_xn and *out_normed says
+// so. Split projections hand their partials to such row kernels rather than to a separate
+// sum: q|k|v to the QK-norm/RoPE rows, Wo and W2 to the residual + RMSNorm rows.
+hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, bool in_normed,
+                         const float *next_gain, int next_final, bool *out_normed) {
     const sh_config &c = m->cfg;
     const int dt = m->dtype;
     const int D = c.dim, F = c.hidden;
@@ -1674,22 +1815,40 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv) {
     hipError_t e;
     const float scale = (float)(1.0 / sqrt((double)c.head_dim));
     const LayerDev &L = m->layers[l];
-    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x, L.rms_att, D,
-                       c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D, nullptr);
+    if (out_normed) *out_normed = false;
+    if (!in_normed)
+        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x, L.rms_att, D,
+                           c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D, nullptr);
+    int ranges = 1;
     GemmArgs g{};
     g.A = m->pf_xn; g.B = (const uint16_t *)L.wqkv; g.M = S; g.N = m->qkv_rows; g.K = D;
     g.epi = G_STORE; g.out = m->pf_qkv; g.dt = dt;
-    if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
-    if ((e = launch_qk_rope(m, L, S, m->pf_qkv, m->pf_rowpos, m->pf_rowseq, m->pf_q,
-                            m->pf_k, m->pf_v, l, fill_kv, s)) != hipSuccess)
+    if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;
+    if (ranges > 1) {
+        const QkRopeArgs a = qk_rope_args(m, L, m->pf_rowpos, m->pf_rowseq, m->pf_q, m->pf_k, m->pf_v, l,
+                                          fill_kv);
+        const float *pp = m->pf_part;
+        const int kv = c.kv_dtype;
+        if (kv == SH_KV_F32) hipLaunchKernelGGL(k_row_qkv<SH_KV_F32>, dim3(S), dim3(1024), 0, s, pp, ranges, S, a);
+        else if (kv == SH_KV_F16) hipLaunchKernelGGL(k_row_qkv<SH_KV_F16>, dim3(S), dim3(1024), 0, s, pp, ranges, S, a);
+        else hipLaunchKernelGGL(k_row_qkv<SH_KV_BF16>, dim3(S), dim3(1024), 0, s, pp, ranges, S, a);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    } else if ((e = launch_qk_rope(m, L, S, m->pf_qkv, m->pf_rowpos, m->pf_rowseq, m->pf_q, m->pf_k,
+                                   m->pf_v, l, fill_kv, s)) != hipSuccess) {
         return e;
+    }
     if ((e = launch_attn_prefill(m, S, seg_max, fill_kv, scale, s)) != hipSuccess) return e;
     g = GemmArgs{};
     g.A = m->pf_att; g.B = (const uint16_t *)L.wo; g.M = S; g.N = D; g.K = m->qdim;
     g.epi = G_RESID; g.out = m->pf_x2; g.resid = m->pf_x; g.alpha = c.residual_scale; g.dt = dt;
-    if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x2, L.rms_ffn, D,
-                       c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D, nullptr);
+    if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;
+    if (ranges > 1)
+        hipLaunchKernelGGL(k_row_resid_norm, dim3(S), dim3(1024), 0, s, (const float *)m->pf_part, ranges, S, D,
+                           (const float *)m->pf_x, c.residual_scale, m->pf_x2, L.rms_ffn, c.norm_eps, 0, dt,
+                           m->pf_xn);
+    else
+        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x2, L.rms_ffn, D,
+                           c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D, nullptr);
     g = GemmArgs{};
     g.A = m->pf_xn; g.B = (const uint16_t *)L.w13; g.M = S; g.N = 2 * F; g.K = D;
     g.epi = G_GATE; g.out16 = m->pf_gate; g.dt = dt; g.decode_forms = fill_kv ? 1 : 0;
@@ -1697,7 +1856,14 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv) {
     g = GemmArgs{};
     g.A = m->pf_gate; g.B = (const uint16_t *)L.w2; g.M = S; g.N = D; g.K = F;
     g.epi = G_RESID; g.out = m->pf_x; g.resid = m->pf_x2; g.alpha = c.residual_scale; g.dt = dt;
-    return gemm(g, dt, m->pf_part, m->pf_part_cap, s);
+    if (!next_gain) return gemm(g, dt, m->pf_part, m->pf_part_cap, s);
+    if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;
+    if (ranges == 1) return hipSuccess;
+    hipLaunchKernelGGL(k_row_resid_norm, dim3(S), dim3(1024), 0, s, (const float *)m->pf_part, ranges, S, D,
+                       (const float *)m->pf_x2, c.residual_scale, m->pf_x, next_gain, c.norm_eps, next_final, dt,
+                       m->pf_xn);
+    if (out_normed) *out_normed = true;
+    return hipGetLastError();
 }
 
 // logits [V, S] = classifier . (the operand planes in pf_xn)
@@ -1725,11 +1891,17 @@ hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fi
     hipLaunchKernelGGL(k_embed_rows, dim3(S), dim3(kT), 0, s, (const uint16_t *)m->embed,
                        m->pf_tokens, c.vocab, D, dt, m->pf_x);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    for (int l = 0; l < c.n_layers; l++)
-        if ((e = enqueue_layer(m, l, S, seg_max, fill_kv)) != hipSuccess) return e;
+    bool normed = false;
+    for (int l = 0; l < c.n_layers; l++) {
+        const bool last = l + 1 == c.n_layers;
+        const float *next = !last ? m->layers[l + 1].rms_att : logits ? m->rms_final : nullptr;
+        if ((e = enqueue_layer(m, l, S, seg_max, fill_kv, normed, next, last ? 1 : 0, &normed)) != hipSuccess)
+            return e;
+    }
     if (!logits) return hipSuccess;
-    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x, m->rms_final, D,
-                       c.norm_eps, 1, dt, m->pf_xn, (size_t)S * D, nullptr);
+    if (!normed)
+        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x, m->rms_final, D,
+                           c.norm_eps, 1, dt, m->pf_xn, (size_t)S * D, nullptr);
     return enqueue_classifier(m, S);
 }
 
@@ -1737,7 +1909,7 @@ hipError_t enqueue_layer_cf(sh_model *m, int l, int S) {
     const int D = m->cfg.dim;
     hipError_t e;
     if ((e = launch_transpose(m->pf_cf, D, S, m->pf_x, m->stream)) != hipSuccess) return e;
-    if ((e = enqueue_layer(m, l, S, S, false)) != hipSuccess) return e;
+    if ((e = enqueue_layer(m, l, S, S, false, false, nullptr, 0, nullptr)) != hipSuccess) return e;
     return launch_transpose(m->pf_x, S, D, m->pf_cf, m->stream);
 }
 
@@ -1990,7 +2162,7 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         hipLaunchKernelGGL(k_row_resid_norm, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part,
                            ranges(D, m->qdim), B, D, (const float *)m->bt_x, c.residual_scale,
-                           m->bt_x2, L.rms_ffn, c.norm_eps, dt, m->bt_xn);
+                           m->bt_x2, L.rms_ffn, c.norm_eps, 0, dt, m->bt_xn);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // W1/W3 with the SiLU gate
         g = GemmArgs{};
@@ -2006,7 +2178,7 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         const float *next_gain = l + 1 < c.n_layers ? m->layers[l + 1].rms_att : m->rms_final;
         hipLaunchKernelGGL(k_row_resid_norm, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part,
                            ranges(D, F), B, D, (const float *)m->bt_x2, c.residual_scale, m->bt_x,
-                           next_gain, c.norm_eps, dt, m->bt_xn);
+                           next_gain, c.norm_eps, 0, dt, m->bt_xn);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     GemmArgs g{};
