@@ -341,9 +341,11 @@ __global__ __launch_bounds__(64) void k_tr_attn_bwd_kv(const float *qkv, const f
 // reference's order, so the results equal the one-wave-per-row kernels above.
 constexpr int kAQ = 16;          // queries (or keys) per workgroup
 constexpr int kAB = 64;          // rows per staged block
-constexpr int kAttnMaxS = 256;   // score rows kept in LDS: 2 x 16 x S floats (<= 64 KB dynamic)
+constexpr int kAttnMaxS = 256;   // score rows kept in LDS: 2 x 16 x (S + 16) floats (<= 64 KB dynamic)
 constexpr int kAPad = 68;        // LDS row stride (floats) of a staged block: 16-byte rows, and
                                  // 16 rows 4 banks apart for the float4 reads
+constexpr int kSPad = 16;        // extra floats per score row in LDS: the four rows a wave
+                                 // touches start 16 banks apart instead of on one bank
 
 // sum over i in order of a[i]*b[i] (float32, no fusing), four at a time from LDS (hd % 4 == 0)
 __device__ __forceinline__ float dot_lds(const float *a, const float *b, int hd) {
@@ -408,6 +410,7 @@ __global__ __launch_bounds__(256) void k_tr_attn_fwd_blk(const float *qkv, int S
     const int q0 = blockIdx.x * kAQ, h = blockIdx.y, tid = threadIdx.x;
     const size_t ld = 3 * (size_t)D;
     const int qn = min(kAQ, S - q0), kend = min(S, q0 + kAQ);   // keys 0 .. kend-1
+    const int SP = S + kSPad;
     stage_rows(qs, qkv, ld, h * hd, q0, S, hd, kAQ, true);
     const int q = tid / 16, j = tid % 16, t = q0 + q;
     for (int kb = 0; kb < kend; kb += kAB) {
@@ -416,26 +419,26 @@ __global__ __launch_bounds__(256) void k_tr_attn_fwd_blk(const float *qkv, int S
         __syncthreads();
         for (int u = 0; u < kAB / 16; u++) {
             const int s = kb + j + 16 * u;
-            if (s < kend && q < qn && s <= t) sc[q * S + s] = dot_lds(qs + q * kAPad, kv + (s - kb) * kAPad, hd) * scale;
+            if (s < kend && q < qn && s <= t) sc[q * SP + s] = dot_lds(qs + q * kAPad, kv + (s - kb) * kAPad, hd) * scale;
         }
     }
     __syncthreads();
     // softmax of row q over keys 0..t: the 16 lanes of the row group share it
     float mx = -INFINITY;
     if (q < qn)
-        for (int s = j; s <= t; s += 16) mx = fmaxf(mx, sc[q * S + s]);
+        for (int s = j; s <= t; s += 16) mx = fmaxf(mx, sc[q * SP + s]);
     mx = wmax<16>(mx);
     double tot = 0;
     if (q < qn)
         for (int s = j; s <= t; s += 16) {
-            const double ev = exp((double)(sc[q * S + s] - mx));
-            sc[q * S + s] = (float)ev;
+            const double ev = exp((double)(sc[q * SP + s] - mx));
+            sc[q * SP + s] = (float)ev;
             tot += ev;
         }
     tot = sum16_d64(tot);
     const float inv = (float)(1.0 / tot);
     if (q < qn)
-        for (int s = j; s <= t; s += 16) sc[q * S + s] *= inv;
+        for (int s = j; s <= t; s += 16) sc[q * SP + s] *= inv;
     // P.V: thread (q, dims j, j+16, ...) sums over keys in order
     float a[4] = {0.f, 0.f, 0.f, 0.f};
     for (int kb = 0; kb < kend; kb += kAB) {
@@ -446,7 +449,7 @@ __global__ __launch_bounds__(256) void k_tr_attn_fwd_blk(const float *qkv, int S
             const int se = min(t + 1, min(kend, kb + kAB));
 #pragma unroll 4
             for (int s = kb; s < se; s++) {
-                const float p = sc[q * S + s];
+                const float p = sc[q * SP + s];
                 for (int c = 0; c < 4; c++)
                     if (j + 16 * c < hd) a[c] += p * kv[(s - kb) * kAPad + j + 16 * c];
             }
@@ -462,11 +465,12 @@ __global__ __launch_bounds__(256) void k_tr_attn_fwd_blk(const float *qkv, int S
 __global__ __launch_bounds__(256) void k_tr_attn_bwd_q_blk(const float *qkv, const float *dout, int S, int D,
                                                            int hd, float scale, float *dqkv, float *stats) {
     extern __shared__ __attribute__((aligned(16))) float sh[];
-    float *qs = sh, *gs = qs + kAQ * kAPad, *kv = gs + kAQ * kAPad, *pr = kv + kAB * kAPad, *dsc = pr + kAQ * S;
+    float *qs = sh, *gs = qs + kAQ * kAPad, *kv = gs + kAQ * kAPad, *pr = kv + kAB * kAPad, *dsc = pr + kAQ * (S + kSPad);
     __shared__ float dss_sh[kAQ];
     const int q0 = blockIdx.x * kAQ, h = blockIdx.y, tid = threadIdx.x;
     const size_t ld = 3 * (size_t)D;
     const int qn = min(kAQ, S - q0), kend = min(S, q0 + kAQ);
+    const int SP = S + kSPad;
     stage_rows(qs, qkv, ld, h * hd, q0, S, hd, kAQ, true);
     stage_rows(gs, dout, D, h * hd, q0, S, hd, kAQ, true);
     const int q = tid / 16, j = tid % 16, t = q0 + q;
@@ -476,37 +480,37 @@ __global__ __launch_bounds__(256) void k_tr_attn_bwd_q_blk(const float *qkv, con
         __syncthreads();
         for (int u = 0; u < kAB / 16; u++) {
             const int s = kb + j + 16 * u;
-            if (s < kend && q < qn && s <= t) pr[q * S + s] = dot_lds(qs + q * kAPad, kv + (s - kb) * kAPad, hd) * scale;
+            if (s < kend && q < qn && s <= t) pr[q * SP + s] = dot_lds(qs + q * kAPad, kv + (s - kb) * kAPad, hd) * scale;
         }
         __syncthreads();
         stage_rows(kv, qkv, ld, 2 * D + h * hd, kb, kend, hd);
         __syncthreads();
         for (int u = 0; u < kAB / 16; u++) {
             const int s = kb + j + 16 * u;
-            if (s < kend && q < qn && s <= t) dsc[q * S + s] = dot_lds(gs + q * kAPad, kv + (s - kb) * kAPad, hd);
+            if (s < kend && q < qn && s <= t) dsc[q * SP + s] = dot_lds(gs + q * kAPad, kv + (s - kb) * kAPad, hd);
         }
     }
     __syncthreads();
     float mx = -INFINITY;
     if (q < qn)
-        for (int s = j; s <= t; s += 16) mx = fmaxf(mx, pr[q * S + s]);
+        for (int s = j; s <= t; s += 16) mx = fmaxf(mx, pr[q * SP + s]);
     mx = wmax<16>(mx);
     double tot = 0;
     if (q < qn)
         for (int s = j; s <= t; s += 16) {
-            const double ev = exp((double)(pr[q * S + s] - mx));
-            pr[q * S + s] = (float)ev;
+            const double ev = exp((double)(pr[q * SP + s] - mx));
+            pr[q * SP + s] = (float)ev;
             tot += ev;
         }
     tot = sum16_d64(tot);
     const float inv = (float)(1.0 / tot);
     if (q < qn)
-        for (int s = j; s <= t; s += 16) pr[q * S + s] *= inv;
+        for (int s = j; s <= t; s += 16) pr[q * SP + s] *= inv;
     __syncthreads();
     if (j == 0 && q < qn) {   // dsSum in key order
         float d = 0.f;
 #pragma unroll 8
-        for (int s = 0; s <= t; s++) d += pr[q * S + s] * dsc[q * S + s];
+        for (int s = 0; s <= t; s++) d += pr[q * SP + s] * dsc[q * SP + s];
         dss_sh[q] = d;
         float *st = stats + ((size_t)h * S + t) * 3;
         st[0] = mx;
@@ -516,7 +520,7 @@ __global__ __launch_bounds__(256) void k_tr_attn_bwd_q_blk(const float *qkv, con
     __syncthreads();
     if (q < qn) {
         const float dss = dss_sh[q];
-        for (int s = j; s <= t; s += 16) dsc[q * S + s] = pr[q * S + s] * (dsc[q * S + s] - dss) * scale;
+        for (int s = j; s <= t; s += 16) dsc[q * SP + s] = pr[q * SP + s] * (dsc[q * SP + s] - dss) * scale;
     }
     float a[4] = {0.f, 0.f, 0.f, 0.f};
     for (int kb = 0; kb < kend; kb += kAB) {   // dq = sum over keys in order of ds*k
@@ -527,7 +531,7 @@ __global__ __launch_bounds__(256) void k_tr_attn_bwd_q_blk(const float *qkv, con
             const int se = min(t + 1, min(kend, kb + kAB));
 #pragma unroll 4
             for (int s = kb; s < se; s++) {
-                const float d = dsc[q * S + s];
+                const float d = dsc[q * SP + s];
                 for (int c = 0; c < 4; c++)
                     if (j + 16 * c < hd) a[c] += d * kv[(s - kb) * kAPad + j + 16 * c];
             }
@@ -545,7 +549,7 @@ __global__ __launch_bounds__(256) void k_tr_attn_bwd_kv_blk(const float *qkv, co
                                                             int hd, float scale, const float *stats,
                                                             float *dqkv) {
     __shared__ __attribute__((aligned(16))) float ks[kAQ * kAPad], vs[kAQ * kAPad], qb[kAB * kAPad], gb[kAB * kAPad];
-    __shared__ float pp[kAQ][kAB], dd[kAQ][kAB];
+    __shared__ float pp[kAQ][kAB + kSPad], dd[kAQ][kAB + kSPad];
     const int s0 = blockIdx.x * kAQ, h = blockIdx.y, tid = threadIdx.x;
     const size_t ld = 3 * (size_t)D;
     const int sn = min(kAQ, S - s0);
@@ -793,6 +797,334 @@ __global__ void k_tr_adam(float *w, float *g, float *m, float *v, size_t n, floa
     }
 }
 
+// ---- fp32 MFMA attention (flash form) ----------------------------------------------------
+// The forward (forward_common.go:5-33) and causalAttentionBackwardCF (train_full.go:247-301)
+// on v_mfma_f32_16x16x4_f32: fp32 operands, exact products, fp32 accumulation, so they differ
+// from the reference's sequential sums only in summation order. Tiles of 16 queries (or keys)
+// per workgroup, head dims a multiple of 16, any S. Two product forms:
+//  - tile_dot: C[16 rows][16 cols] = sum_d A[row][d] B[col][d], A and B row-major in LDS; the
+//    result lane l holds column l%16, rows 4(l/16) + r in register r.
+//  - tile_acc: C'[dims][16 cols] += M^T . T with T a tile in that result layout (lane l: column
+//    l%16, k-rows 4(l/16) + r in register r) and M rows [k][dim] in LDS; MFMA r pairs lane
+//    group l/16 with k-row 4(l/16) + r, so T feeds the B operand straight from registers.
+// Row strides of HD + 4 floats keep both forms' LDS reads on distinct banks.
+constexpr int kMQ = 16;   // query (or key) rows per workgroup
+constexpr int kMB = 64;   // key (or query) rows per wave-block
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+template <int HD>
+__device__ __forceinline__ f32x4 tile_dot(const float *a, const float *b, int lane) {
+    constexpr int P = HD + 4;
+    const int r = lane & 15, k = lane >> 4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < HD; d += 4) acc = mfma4(a[r * P + d + k], b[r * P + d + k], acc);
+    return acc;
+}
+// tile_dot with the B rows already in registers (breg[d/4] = B[l%16][d + l/16])
+template <int HD>
+__device__ __forceinline__ f32x4 tile_dot_rb(const float *a, const float *breg, int lane) {
+    constexpr int P = HD + 4;
+    const int r = lane & 15, k = lane >> 4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < HD; d += 4) acc = mfma4(a[r * P + d + k], breg[d / 4], acc);
+    return acc;
+}
+template <int HD>
+__device__ __forceinline__ void tile_acc(f32x4 (&acc)[HD / 16], const float *m, const f32x4 &t, int lane) {
+    constexpr int P = HD + 4;
+    const int c = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int i = 0; i < HD / 16; i++) acc[i] = mfma4(m[(4 * kg + r) * P + 16 * i + c], t[r], acc[i]);
+}
+// max / sum over the four lanes l, l^16, l^32, l^48 (one result column)
+__device__ __forceinline__ float col_max(float v) {
+    SwapPair s = swap16(__float_as_uint(v));
+    v = fmaxf(__uint_as_float(s.a), __uint_as_float(s.b));
+    s = swap32(__float_as_uint(v));
+    return fmaxf(__uint_as_float(s.a), __uint_as_float(s.b));
+}
+__device__ __forceinline__ float col_sum(float v) {
+    SwapPair s = swap16(__float_as_uint(v));
+    v = __uint_as_float(s.a) + __uint_as_float(s.b);
+    s = swap32(__float_as_uint(v));
+    return __uint_as_float(s.a) + __uint_as_float(s.b);
+}
+// rows r0 .. r0+nr-1 (zero past n) of columns c0 .. c0+HD-1 of a row-major matrix into LDS
+// [nr][HD + 4], by `nt` threads starting at thread index `t0`; loads first, then stores
+template <int HD, int NR>
+__device__ __forceinline__ void stage_tile(float *dst, const float *src, size_t ld, int c0, int r0, int n, int t0,
+                                           int nt) {
+    constexpr int PER = HD / 4, TOT = NR * PER;
+    for (int e0 = 0; e0 < TOT; e0 += 4 * nt) {
+        f32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int e = e0 + t0 + u * nt, r = e / PER, c = (e % PER) * 4;
+            const bool ok = e < TOT && r0 + r < n;
+            v[u] = ok ? *(const f32x4 *)(src + (size_t)(r0 + r) * ld + c0 + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int e = e0 + t0 + u * nt, r = e / PER, c = (e % PER) * 4;
+            if (e < TOT) *(f32x4 *)(dst + r * (HD + 4) + c) = v[u];
+        }
+    }
+}
+template <int HD> constexpr size_t mf_lds_bytes() {
+    return sizeof(float) * (size_t)(2 * kMQ * (HD + 4) + 4 * 2 * kMB * (HD + 4));
+}
+
+// Forward for queries q0 .. q0+15 of head h: the key blocks up to the tile's last query dealt
+// round-robin to the four waves (own LDS slices); per block S^T = K.Q^T, the online softmax
+// per query (float64 exp of score - running max, as the reference's exp), O^T += V^T.P^T;
+// the waves' (max, sum, O) merged at the end. att = O / sum; stats[t] = (max, 1/sum).
+template <int HD>
+__global__ __launch_bounds__(256) void k_tr_attn_fwd_mf(const float *qkv, int S, int D, float scale, float *att,
+                                                        float *stats) {
+    constexpr int P = HD + 4, NO = HD / 16;
+    __shared__ __attribute__((aligned(16))) float lds[mf_lds_bytes<HD>() / sizeof(float)];
+    float *qs = lds, *slice = lds + 2 * kMQ * P;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int q0 = blockIdx.x * kMQ, h = blockIdx.y;
+    const size_t ld = 3 * (size_t)D;
+    float *kb_s = slice + wave * 2 * kMB * P, *vb_s = kb_s + kMB * P;
+    stage_tile<HD, kMQ>(qs, qkv, ld, h * HD, q0, S, tid, 256);
+    __syncthreads();
+    const int qlast = min(q0 + kMQ, S) - 1;
+    const int nb = qlast / kMB + 1;
+    const int c = lane & 15, kg = lane >> 4, t = q0 + c;
+    float m_run = -INFINITY, l_part = 0.f;
+    f32x4 o[NO];
+#pragma unroll
+    for (int i = 0; i < NO; i++) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int bi = wave; bi < nb; bi += 4) {
+        const int kb = bi * kMB;
+        stage_tile<HD, kMB>(kb_s, qkv, ld, D + h * HD, kb, S, lane, 64);
+        stage_tile<HD, kMB>(vb_s, qkv, ld, 2 * D + h * HD, kb, S, lane, 64);
+        __builtin_amdgcn_wave_barrier();
+        const int nj = min(kMB, qlast + 1 - kb + 15) / 16;   // 16-key tiles some query can see
+        for (int j = 0; j < nj; j++) {
+            f32x4 sc = tile_dot<HD>(kb_s + 16 * j * P, qs, lane);
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = kb + 16 * j + 4 * kg + r;
+                sc[r] = key <= t ? sc[r] * scale : -INFINITY;
+                mx = fmaxf(mx, sc[r]);
+            }
+            mx = col_max(mx);
+            // a column with no visible key yet keeps max -inf and gets p = 0 (no branch: the
+            // MFMAs below run on the whole wave)
+            const float m_new = fmaxf(m_run, mx);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            const float rs = m_run == -INFINITY ? 0.f : (float)exp((double)(m_run - m_use));
+            m_run = m_new;
+            l_part *= rs;
+#pragma unroll
+            for (int i = 0; i < NO; i++) o[i] *= rs;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                sc[r] = sc[r] == -INFINITY ? 0.f : (float)exp((double)(sc[r] - m_use));
+                l_part += sc[r];
+            }
+            tile_acc<HD>(o, vb_s + 16 * j * P, sc, lane);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    // merge the waves: (max, sum) per query column, O^T per (dim, query)
+    const float l_w = col_sum(l_part);
+    __syncthreads();
+    float *oo = slice, *mo = oo + 4 * HD * kMQ, *lo = mo + 4 * kMQ;
+    if (kg == 0) {
+        mo[wave * kMQ + c] = m_run;
+        lo[wave * kMQ + c] = l_w;
+    }
+#pragma unroll
+    for (int i = 0; i < NO; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) oo[(wave * HD + 16 * i + 4 * kg + r) * kMQ + c] = o[i][r];
+    __syncthreads();
+    for (int e = tid; e < kMQ * HD; e += 256) {
+        const int q = e / HD, d = e % HD, tq = q0 + q;
+        if (tq >= S) continue;
+        float mm = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) mm = fmaxf(mm, mo[w * kMQ + q]);
+        float lt = 0.f, ot = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float mw = mo[w * kMQ + q];
+            const float f = mw == -INFINITY ? 0.f : (float)exp((double)(mw - mm));
+            lt += lo[w * kMQ + q] * f;
+            ot += oo[(w * HD + d) * kMQ + q] * f;
+        }
+        const float inv = (float)(1.0 / (double)lt);
+        att[(size_t)tq * D + h * HD + d] = ot * inv;
+        if (d == 0) {
+            float *st = stats + ((size_t)h * S + tq) * 3;
+            st[0] = mm;
+            st[1] = inv;
+        }
+    }
+}
+
+// Query side of the backward for queries q0 .. q0+15 of head h: dsSum_t = dO_t . O_t (equal
+// to the reference's sum over keys of p*dp), then per key block (waves round-robin)
+// P^T from the forward's (max, 1/sum), dP^T = V.dO^T, dS^T = P^T (dP^T - dsSum) scale,
+// dQ^T += K^T.dS^T; the waves' dQ summed at the end. stats[t][2] = dsSum for the key side.
+template <int HD>
+__global__ __launch_bounds__(256) void k_tr_attn_bwd_q_mf(const float *qkv, const float *att, const float *dout,
+                                                          int S, int D, float scale, float *dqkv, float *stats) {
+    constexpr int P = HD + 4, NO = HD / 16;
+    __shared__ __attribute__((aligned(16))) float lds[mf_lds_bytes<HD>() / sizeof(float)];
+    __shared__ float dsum[kMQ];
+    float *qs = lds, *gs = lds + kMQ * P, *slice = lds + 2 * kMQ * P;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int q0 = blockIdx.x * kMQ, h = blockIdx.y;
+    const size_t ld = 3 * (size_t)D;
+    float *kb_s = slice + wave * 2 * kMB * P, *vb_s = kb_s + kMB * P;
+    stage_tile<HD, kMQ>(qs, qkv, ld, h * HD, q0, S, tid, 256);
+    stage_tile<HD, kMQ>(gs, dout, D, h * HD, q0, S, tid, 256);
+    if (tid < kMQ) {
+        const int t = q0 + tid;
+        float d = 0.f;
+        if (t < S) {
+            const float *a = att + (size_t)t * D + h * HD, *g = dout + (size_t)t * D + h * HD;
+            for (int i = 0; i < HD; i++) d += g[i] * a[i];
+            stats[((size_t)h * S + t) * 3 + 2] = d;
+        }
+        dsum[tid] = d;
+    }
+    __syncthreads();
+    const int qlast = min(q0 + kMQ, S) - 1;
+    const int nb = qlast / kMB + 1;
+    const int c = lane & 15, kg = lane >> 4, t = q0 + c;
+    float mq = 0.f, iq = 0.f;
+    if (t < S) {
+        mq = stats[((size_t)h * S + t) * 3];
+        iq = stats[((size_t)h * S + t) * 3 + 1];
+    }
+    const float dq_sum = dsum[c];
+    f32x4 dq[NO];
+#pragma unroll
+    for (int i = 0; i < NO; i++) dq[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int bi = wave; bi < nb; bi += 4) {
+        const int kb = bi * kMB;
+        stage_tile<HD, kMB>(kb_s, qkv, ld, D + h * HD, kb, S, lane, 64);
+        stage_tile<HD, kMB>(vb_s, qkv, ld, 2 * D + h * HD, kb, S, lane, 64);
+        __builtin_amdgcn_wave_barrier();
+        const int nj = min(kMB, qlast + 1 - kb + 15) / 16;
+        for (int j = 0; j < nj; j++) {
+            const f32x4 sc = tile_dot<HD>(kb_s + 16 * j * P, qs, lane);
+            const f32x4 dp = tile_dot<HD>(vb_s + 16 * j * P, gs, lane);
+            f32x4 ds;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int key = kb + 16 * j + 4 * kg + r;
+                const float p = key <= t ? (float)exp((double)(sc[r] * scale - mq)) * iq : 0.f;
+                ds[r] = p * (dp[r] - dq_sum) * scale;
+            }
+            tile_acc<HD>(dq, kb_s + 16 * j * P, ds, lane);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    float *oo = slice;
+#pragma unroll
+    for (int i = 0; i < NO; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) oo[(wave * HD + 16 * i + 4 * kg + r) * kMQ + c] = dq[i][r];
+    __syncthreads();
+    for (int e = tid; e < kMQ * HD; e += 256) {
+        const int q = e / HD, d = e % HD, tq = q0 + q;
+        if (tq >= S) continue;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) v += oo[(w * HD + d) * kMQ + q];
+        dqkv[(size_t)tq * ld + h * HD + d] = v;
+    }
+}
+
+// Key side for keys s0 .. s0+15 of head h: the 16-query tiles from the key tile on dealt
+// round-robin to the waves; per tile S = Q.K^T and dP = dO.V^T (K and V rows held in
+// registers as B operands), P and dS from the row stats, dV^T += dO^T.P, dK^T += Q^T.dS;
+// the waves' sums merged at the end.
+template <int HD>
+__global__ __launch_bounds__(256) void k_tr_attn_bwd_kv_mf(const float *qkv, const float *dout, int S, int D,
+                                                           float scale, const float *stats, float *dqkv) {
+    constexpr int P = HD + 4, NO = HD / 16;
+    __shared__ __attribute__((aligned(16))) float lds[mf_lds_bytes<HD>() / sizeof(float)];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int s0 = blockIdx.x * kMQ, h = blockIdx.y;
+    const size_t ld = 3 * (size_t)D;
+    float *qt = lds + wave * 2 * kMB * P, *gt = qt + kMQ * P;   // the wave's query tile rows
+    const int c = lane & 15, kg = lane >> 4, key = s0 + c;
+    // K and V rows of key `key` as B operands: kreg[d/4] = K[key][d + kg]
+    float kreg[HD / 4], vreg[HD / 4];
+#pragma unroll
+    for (int d = 0; d < HD; d += 4) {
+        const bool ok = key < S;
+        kreg[d / 4] = ok ? qkv[(size_t)key * ld + D + h * HD + d + kg] : 0.f;
+        vreg[d / 4] = ok ? qkv[(size_t)key * ld + 2 * D + h * HD + d + kg] : 0.f;
+    }
+    f32x4 dk[NO], dv[NO];
+#pragma unroll
+    for (int i = 0; i < NO; i++) dk[i] = dv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int ntiles = (S + kMQ - 1) / kMQ;
+    for (int qt_i = blockIdx.x + wave; qt_i < ntiles; qt_i += 4) {
+        const int tq0 = qt_i * kMQ;
+        stage_tile<HD, kMQ>(qt, qkv, ld, h * HD, tq0, S, lane, 64);
+        stage_tile<HD, kMQ>(gt, dout, D, h * HD, tq0, S, lane, 64);
+        __builtin_amdgcn_wave_barrier();
+        const f32x4 sc = tile_dot_rb<HD>(qt, kreg, lane);   // rows: queries tq0 + 4kg + r; column: key
+        const f32x4 dp = tile_dot_rb<HD>(gt, vreg, lane);
+        f32x4 p, ds;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int tq = tq0 + 4 * kg + r;
+            float pv = 0.f, dv_ = 0.f;
+            if (tq < S && key <= tq) {
+                const float *st = stats + ((size_t)h * S + tq) * 3;
+                pv = (float)exp((double)(sc[r] * scale - st[0])) * st[1];
+                dv_ = pv * (dp[r] - st[2]) * scale;
+            }
+            p[r] = pv;
+            ds[r] = dv_;
+        }
+        tile_acc<HD>(dv, gt, p, lane);
+        tile_acc<HD>(dk, qt, ds, lane);
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    float *ok_ = lds, *ov = lds + 4 * HD * kMQ;
+#pragma unroll
+    for (int i = 0; i < NO; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            ok_[(wave * HD + 16 * i + 4 * kg + r) * kMQ + c] = dk[i][r];
+            ov[(wave * HD + 16 * i + 4 * kg + r) * kMQ + c] = dv[i][r];
+        }
+    __syncthreads();
+    for (int e = tid; e < kMQ * HD; e += 256) {
+        const int k = e / HD, d = e % HD, s = s0 + k;
+        if (s >= S) continue;
+        float a = 0.f, b = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            a += ok_[(w * HD + d) * kMQ + k];
+            b += ov[(w * HD + d) * kMQ + k];
+        }
+        dqkv[(size_t)s * ld + D + h * HD + d] = a;
+        dqkv[(size_t)s * ld + 2 * D + h * HD + d] = b;
+    }
+}
+
 }  // namespace
 }  // namespace sh
 
@@ -899,9 +1231,17 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale, bool acc) {
                                          T->part_cap)))
             return e;
         hipLaunchKernelGGL(k_tr_rope, dim3(S), dim3(256), 0, s, C.qkv, D, hd, T->cos_t, T->sin_t);
-        if (S <= kAttnMaxS)
+        float *st = T->stats + (size_t)l * 3 * T->H * S;   // this layer's (max, 1/sum, dsSum) rows
+        if (hd == 64)
+            hipLaunchKernelGGL(k_tr_attn_fwd_mf<64>, dim3((S + kMQ - 1) / kMQ, T->H), dim3(256), 0, s, C.qkv, S, D,
+                               scale, C.att, st);
+        else if (hd == 32)
+            hipLaunchKernelGGL(k_tr_attn_fwd_mf<32>, dim3((S + kMQ - 1) / kMQ, T->H), dim3(256), 0, s, C.qkv, S, D,
+                               scale, C.att, st);
+        else if (S <= kAttnMaxS)
             hipLaunchKernelGGL(k_tr_attn_fwd_blk, dim3((S + kAQ - 1) / kAQ, T->H), dim3(256),
-                               sizeof(float) * (kAQ * kAPad + kAB * kAPad + kAQ * S), s, C.qkv, S, D, hd, scale, C.att);
+                               sizeof(float) * (kAQ * kAPad + kAB * kAPad + kAQ * (S + kSPad)), s, C.qkv, S, D, hd, scale,
+                               C.att);
         else
             hipLaunchKernelGGL(k_tr_attn_fwd, dim3(S, T->H), dim3(64), sizeof(float) * S, s, C.qkv, S, D, hd, scale,
                                C.att);
@@ -985,17 +1325,31 @@ hipError_t tr_backward(sh_trainer *T, int n_in, bool acc) {
         if ((e = sgemm_split<true, false>(s, T->dx2s, D, T->p + T->o_wo[l], D, T->gatt, D, S, D, D, 1.f, T->part,
                                           T->part_cap)))
             return e;
-        if (S <= kAttnMaxS) {
+        float *st = T->stats + (size_t)l * 3 * T->H * S;   // the forward's (max, 1/sum) rows
+        const dim3 tiles((S + kMQ - 1) / kMQ, T->H);
+        if (hd == 64 || hd == 32) {
+            if (hd == 64) {
+                hipLaunchKernelGGL(k_tr_attn_bwd_q_mf<64>, tiles, dim3(256), 0, s, C.qkv, C.att, T->gatt, S, D, scale,
+                                   T->dqkv, st);
+                hipLaunchKernelGGL(k_tr_attn_bwd_kv_mf<64>, tiles, dim3(256), 0, s, C.qkv, T->gatt, S, D, scale, st,
+                                   T->dqkv);
+            } else {
+                hipLaunchKernelGGL(k_tr_attn_bwd_q_mf<32>, tiles, dim3(256), 0, s, C.qkv, C.att, T->gatt, S, D, scale,
+                                   T->dqkv, st);
+                hipLaunchKernelGGL(k_tr_attn_bwd_kv_mf<32>, tiles, dim3(256), 0, s, C.qkv, T->gatt, S, D, scale, st,
+                                   T->dqkv);
+            }
+        } else if (S <= kAttnMaxS) {
             hipLaunchKernelGGL(k_tr_attn_bwd_q_blk, dim3((S + kAQ - 1) / kAQ, T->H), dim3(256),
-                               sizeof(float) * (2 * kAQ * kAPad + kAB * kAPad + 2 * kAQ * S), s, C.qkv, T->gatt, S,
-                               D, hd, scale, T->dqkv, T->stats);
+                               sizeof(float) * (2 * kAQ * kAPad + kAB * kAPad + 2 * kAQ * (S + kSPad)), s, C.qkv, T->gatt, S,
+                               D, hd, scale, T->dqkv, st);
             hipLaunchKernelGGL(k_tr_attn_bwd_kv_blk, dim3((S + kAQ - 1) / kAQ, T->H), dim3(256), 0, s, C.qkv,
-                               T->gatt, S, D, hd, scale, T->stats, T->dqkv);
+                               T->gatt, S, D, hd, scale, st, T->dqkv);
         } else {
             hipLaunchKernelGGL(k_tr_attn_bwd_q, dim3(S, T->H), dim3(64), 2 * sizeof(float) * S, s, C.qkv, T->gatt,
-                               S, D, hd, scale, T->dqkv, T->stats);
+                               S, D, hd, scale, T->dqkv, st);
             hipLaunchKernelGGL(k_tr_attn_bwd_kv, dim3(S, T->H), dim3(64), 2 * sizeof(float) * S, s, C.qkv, T->gatt,
-                               S, D, hd, scale, T->stats, T->dqkv);
+                               S, D, hd, scale, st, T->dqkv);
         }
         if ((e = sgemm_split<true, false>(s, T->dqkv, 3 * D, T->p + T->o_qkv[l], D, T->gxn, D, S, D, 3 * D, 1.f,
                                           T->part, T->part_cap)))
@@ -1247,7 +1601,7 @@ sh_trainer *sh_trainer_create(const sh_config *cfg, const sh_train_options *opt_
                  o_dy = take(4 * S * D), o_dcur = take(4 * S * D), o_dprev = take(4 * S * D),
                  o_dout = take(4 * S * D), o_gx2 = take(4 * S * D), o_dx2s = take(4 * S * D),
                  o_gxn = take(4 * S * D), o_gatt = take(4 * S * D), o_ggate = take(4 * S * F),
-                 o_dh13 = take(4 * S * 2 * F), o_dqkv = take(4 * S * 3 * D), o_stats = take(4 * 3 * T->H * S),
+                 o_dh13 = take(4 * S * 2 * F), o_dqkv = take(4 * S * 3 * D), o_stats = take(4 * 3 * T->H * S * T->L),
                  o_dlc = take(4 * S * T->ldc_u), o_gc = take(4 * S * D), o_loss = take(16),
                  o_cos = take(4 * S * (T->hd / 2)), o_sin = take(4 * S * (T->hd / 2)), o_rl = take(8 * S),
                  o_sq = take(8 * kSqParts), o_rv = take(4 * S), o_ids = take(4 * S), o_ti = take(2 * S),
