@@ -635,30 +635,45 @@ __global__ __launch_bounds__(kTT) void k_tr_rms_bwd_dx(const float *dy, const fl
     }
 }
 
-// rmsnorm.go:32-47 gain gradient: the sum over t in order of float32(float64(dy*x)*r), stored
+// rmsnorm.go:32-47 gain gradient: the sum over t of float32(float64(dy*x)*r) (eight strided
+// row groups, each in row order, then added in group order), stored
 // (kDwStore), continued from dw[i] as rmsNormBackward does into an accumulator (kDwContinue, the
 // layer gains under backwardAndAccumulate), or formed on its own and then added to dw[i]
 // (kDwAdd: the final gain, addSlice at train_full.go:767).
 enum { kDwStore = 0, kDwContinue = 1, kDwAdd = 2 };
-__global__ __launch_bounds__(64) void k_tr_rms_bwd_dw(const float *dy, const float *x, const float *rrms, int S,
-                                                      int D, int mode, float *dw) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= D) return;
-    float acc = mode == kDwContinue ? dw[i] : 0.f;
-    int t = 0;
-    for (; t + 8 <= S; t += 8) {   // eight rows' loads in flight, the sum still in row order
-        float a[8], b[8], r[8];
+constexpr int kDwCols = 32, kDwGroups = 8;   // columns per workgroup, row groups per column
+__global__ __launch_bounds__(256) void k_tr_rms_bwd_dw(const float *dy, const float *x, const float *rrms, int S,
+                                                       int D, int mode, float *dw) {
+    // thread (row group g, column c): rows g, g + 8, ... summed in order; the eight group sums
+    // then added in group order (each lane pair of a wave reads 2 rows x 128 bytes)
+    __shared__ float part[kDwGroups][kDwCols];
+    const int c = threadIdx.x % kDwCols, g = threadIdx.x / kDwCols;
+    const int i = blockIdx.x * kDwCols + c;
+    float acc = 0.f;
+    if (i < D) {
+        int t = g;
+        for (; t + 3 * kDwGroups < S; t += 4 * kDwGroups) {   // four rows' loads in flight
+            float a[4], b[4], r[4];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            a[u] = dy[(size_t)(t + u) * D + i];
-            b[u] = x[(size_t)(t + u) * D + i];
-            r[u] = rrms[t + u];
+            for (int u = 0; u < 4; u++) {
+                a[u] = dy[(size_t)(t + u * kDwGroups) * D + i];
+                b[u] = x[(size_t)(t + u * kDwGroups) * D + i];
+                r[u] = rrms[t + u * kDwGroups];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) acc += (float)((double)(a[u] * b[u]) * (double)r[u]);
         }
-#pragma unroll
-        for (int u = 0; u < 8; u++) acc += (float)((double)(a[u] * b[u]) * (double)r[u]);
+        for (; t < S; t += kDwGroups)
+            acc += (float)((double)(dy[(size_t)t * D + i] * x[(size_t)t * D + i]) * (double)rrms[t]);
     }
-    for (; t < S; t++) acc += (float)((double)(dy[(size_t)t * D + i] * x[(size_t)t * D + i]) * (double)rrms[t]);
-    dw[i] = mode == kDwAdd ? dw[i] + acc : acc;
+    part[g][c] = acc;
+    __syncthreads();
+    if (g == 0 && i < D) {
+        float sum = mode == kDwContinue ? dw[i] : 0.f;
+#pragma unroll
+        for (int k = 0; k < kDwGroups; k++) sum += part[k][c];
+        dw[i] = mode == kDwAdd ? dw[i] + sum : sum;
+    }
 }
 
 // cpu.go:173-253 CrossEntropyLoss for row t of logits [S, V] (in place -> dLogits): float32
@@ -779,22 +794,27 @@ __global__ __launch_bounds__(kTT) void k_tr_sumsq(const float *p, size_t n, floa
 // The gradient is first multiplied by the loss-scale inverse and then by the clipping factor
 // (train_full.go:829-836, :149-181; each a float32 multiply, skipped when it is 1), and
 // written back as Adam applies it.
+__device__ __forceinline__ void adam_elem(float &w, float &g, float &m, float &v, bool wb, float lr, float b1,
+                                          float b2, float eps, float wd, float ibc1, float ibc2, float inv_ls,
+                                          float clip) {
+    float gi = g;
+    if (inv_ls != 1.f) gi *= inv_ls;
+    if (clip != 1.f) gi *= clip;
+    if (wb) g = gi;
+    const float mi = b1 * m + (1 - b1) * gi;
+    const float vi = b2 * v + (1 - b2) * gi * gi;
+    m = mi;
+    v = vi;
+    const float mh = mi * ibc1, vh = vi * ibc2;
+    float up = mh / ((float)sqrt((double)vh) + eps);
+    if (wd != 0) up += wd * w;
+    w -= lr * up;
+}
 __global__ void k_tr_adam(float *w, float *g, float *m, float *v, size_t n, float lr, float b1, float b2,
                           float eps, float wd, float ibc1, float ibc2, float inv_ls, float clip) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        float gi = g[i];
-        if (inv_ls != 1.f) gi *= inv_ls;
-        if (clip != 1.f) gi *= clip;
-        if (inv_ls != 1.f || clip != 1.f) g[i] = gi;
-        const float mi = b1 * m[i] + (1 - b1) * gi;
-        const float vi = b2 * v[i] + (1 - b2) * gi * gi;
-        m[i] = mi;
-        v[i] = vi;
-        const float mh = mi * ibc1, vh = vi * ibc2;
-        float up = mh / ((float)sqrt((double)vh) + eps);
-        if (wd != 0) up += wd * w[i];
-        w[i] -= lr * up;
-    }
+    const bool wb = inv_ls != 1.f || clip != 1.f;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        adam_elem(w[i], g[i], m[i], v[i], wb, lr, b1, b2, eps, wd, ibc1, ibc2, inv_ls, clip);
 }
 
 // ---- fp32 MFMA attention (flash form) ----------------------------------------------------
@@ -1284,7 +1304,7 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale, bool acc) {
     // final RMSNorm backward: dcur and the rms_final gradient
     hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->dy, T->xL, T->p + T->o_rfin, T->rfin, D,
                        T->dcur);
-    hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 63) / 64), dim3(64), 0, s, T->dy, T->xL, T->rfin, S, D,
+    hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + kDwCols - 1) / kDwCols), dim3(256), 0, s, T->dy, T->xL, T->rfin, S, D,
                        acc ? kDwAdd : kDwStore, T->g + T->o_rfin);
     return hipGetLastError();
 }
@@ -1312,7 +1332,7 @@ hipError_t tr_backward(sh_trainer *T, int n_in, bool acc) {
             return e;
         hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x2, T->p + T->o_rf[l], C.rf, D,
                            T->dprev);
-        hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 63) / 64), dim3(64), 0, s, T->gxn, C.x2, C.rf, S, D,
+        hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + kDwCols - 1) / kDwCols), dim3(256), 0, s, T->gxn, C.x2, C.rf, S, D,
                            acc ? kDwContinue : kDwStore, T->g + T->o_rf[l]);
         hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dcur, T->dprev, 0.f, 1, SD, T->gx2);
         // weight gradients: dW2 = dout^T gate, d[W1;W3] = [dh1|dh3]^T x2n
@@ -1356,7 +1376,7 @@ hipError_t tr_backward(sh_trainer *T, int n_in, bool acc) {
             return e;
         hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x, T->p + T->o_ra[l], C.ra, D,
                            T->dprev);
-        hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + 63) / 64), dim3(64), 0, s, T->gxn, C.x, C.ra, S, D,
+        hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + kDwCols - 1) / kDwCols), dim3(256), 0, s, T->gxn, C.x, C.ra, S, D,
                            acc ? kDwContinue : kDwStore, T->g + T->o_ra[l]);
         hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dprev, T->gx2, 0.f, 1, SD, T->dcur);
         // dWo = dx2s^T att, d[Wq;Wk;Wv] = [dq|dk|dv]^T xn
