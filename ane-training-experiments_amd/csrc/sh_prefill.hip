@@ -746,6 +746,194 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
     }
 }
 
+// The same attention with 64 queries x one head per workgroup (16 per wave) and the key
+// blocks (64 keys) staged once per workgroup for all four waves, the next block loaded into
+// registers while the current one is consumed. It stages a quarter of the K/V traffic of the
+// 16-query form, which wins once the grid fills the chip on its own (long or many sequences);
+// the 16-query form wins on short inputs, whose S/64 x H workgroups leave CUs idle.
+template <int DT, int HD, bool LO>
+__global__ __launch_bounds__(kT) void k_attn_prefill_mfma64(const float *qf, const float *kf,
+                                                          const float *vf, int S,
+                                                          const int32_t *rowpos, int H, int KVH,
+                                                          float scale, uint16_t *att, size_t plane) {
+    constexpr int BQ = 64, BK = 64, NP = LO ? 2 : 1;
+    constexpr int KRS = HD * 2 + 16;              // LDS bytes per K row (16-byte pad)
+    constexpr int VRS = BK * 2 + 8;               // LDS bytes per V^T row (8-byte pad)
+    constexpr int KT = BK * HD / 8;               // K staging tasks: (key, 8 dims)
+    constexpr int VT = (BK / 4) * (HD / 4);       // V staging tasks: (4 keys, 4 dims)
+    constexpr int KPT = (KT + kT - 1) / kT, VPT = (VT + kT - 1) / kT;
+    constexpr int NS = HD / 32, NO = HD / 16;     // QK k-steps, O^T tiles
+    __shared__ __attribute__((aligned(16))) uint8_t ks[NP][BK * KRS];
+    __shared__ __attribute__((aligned(16))) uint8_t vts[NP][HD * VRS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g4 = lane >> 4, ql = lane & 15;
+    const int q0 = blockIdx.x * BQ, h = blockIdx.y;
+    const int qdim = H * HD, kvdim = KVH * HD, kvh = h / (H / KVH);
+    const int kstart = q0 - rowpos[q0];
+    const int qlast = min(q0 + BQ, S) - 1;
+
+    // this lane's query and its Q operand planes (B operand: dims 32s + 8*g4 .. +7)
+    const int t = q0 + 16 * wave + ql;
+    const bool tok = t < S;
+    const int jlo = tok ? t - rowpos[t] : 0x7fffffff;
+    u32x4 qh[NS], qlo[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        float f[8];
+        if (tok) {
+            const f32x4 a = *(const f32x4 *)(qf + (size_t)t * qdim + h * HD + 32 * s + 8 * g4);
+            const f32x4 b = *(const f32x4 *)(qf + (size_t)t * qdim + h * HD + 32 * s + 8 * g4 + 4);
+            f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) f[e] = 0.f;
+        }
+        split8<DT>(f, qh[s], qlo[s]);
+    }
+    const int wlast = min(q0 + 16 * wave + 15, S - 1);   // the wave's last row
+
+    // staging registers for the next key block
+    f32x4 kst[KPT][2], vst[VPT][4];
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int u = 0; u < KPT; u++) {
+            const int c = tid + u * kT;
+            if (KT % kT != 0 && c >= KT) break;
+            const int r = c / (HD / 8), d = (c % (HD / 8)) * 8, j = kb + r;
+            const float *src = kf + (size_t)j * kvdim + kvh * HD + d;
+            kst[u][0] = j < S ? *(const f32x4 *)src : f32x4{0.f, 0.f, 0.f, 0.f};
+            kst[u][1] = j < S ? *(const f32x4 *)(src + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            const int c = tid + u * kT;
+            if (VT % kT != 0 && c >= VT) break;
+            const int kq = c / (HD / 4), d = (c % (HD / 4)) * 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int j = kb + 4 * kq + i;
+                vst[u][i] = j < S ? *(const f32x4 *)(vf + (size_t)j * kvdim + kvh * HD + d)
+                                  : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int u = 0; u < KPT; u++) {
+            const int c = tid + u * kT;
+            if (KT % kT != 0 && c >= KT) break;
+            const int r = c / (HD / 8), d = (c % (HD / 8)) * 8;
+            const float f[8] = {kst[u][0].x, kst[u][0].y, kst[u][0].z, kst[u][0].w,
+                                kst[u][1].x, kst[u][1].y, kst[u][1].z, kst[u][1].w};
+            u32x4 hi, lo;
+            split8<DT>(f, hi, lo);
+            *(u32x4 *)&ks[0][r * KRS + d * 2] = hi;
+            if constexpr (LO) *(u32x4 *)&ks[NP - 1][r * KRS + d * 2] = lo;
+        }
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            const int c = tid + u * kT;
+            if (VT % kT != 0 && c >= VT) break;
+            const int kq = c / (HD / 4), d = (c % (HD / 4)) * 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {   // dim d + i: keys 4kq .. 4kq+3
+                const float a0 = vst[u][0][i], a1 = vst[u][1][i], a2 = vst[u][2][i], a3 = vst[u][3][i];
+                const uint32_t h01 = pack2<DT>(a0, a1), h23 = pack2<DT>(a2, a3);
+                *(uint2 *)&vts[0][(d + i) * VRS + 8 * kq] = uint2{h01, h23};
+                if constexpr (LO) {
+                    const float r0 = a0 - bits_to_f(f_to_bits(a0, DT), DT);
+                    const float r1 = a1 - bits_to_f(f_to_bits(a1, DT), DT);
+                    const float r2 = a2 - bits_to_f(f_to_bits(a2, DT), DT);
+                    const float r3 = a3 - bits_to_f(f_to_bits(a3, DT), DT);
+                    *(uint2 *)&vts[NP - 1][(d + i) * VRS + 8 * kq] =
+                        uint2{pack2<DT>(r0, r1), pack2<DT>(r2, r3)};
+                }
+            }
+        }
+    };
+
+    float m_run = -INFINITY, l_part = 0.f;
+    f32x4 o[NO];
+#pragma unroll
+    for (int i = 0; i < NO; i++) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int kb0 = kstart & ~(BK - 1);
+    gload(kb0);
+    for (int kb = kb0; kb <= qlast; kb += BK) {
+        __syncthreads();   // every wave is done reading the previous block
+        lstore();
+        __syncthreads();
+        if (kb + BK <= qlast) gload(kb + BK);
+        if (q0 + 16 * wave >= S || wlast < kb) continue;   // no row of this wave sees the block
+        // S^T tiles: keys 16j + 4*g4 + r (register r) for query ql
+        f32x4 sc[BK / 16];
+#pragma unroll
+        for (int j = 0; j < BK / 16; j++) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                const int off = (16 * j + ql) * KRS + 64 * s + 16 * g4;
+                const u32x4 kh = *(const u32x4 *)&ks[0][off];
+                acc = mfma16<DT>(kh, qh[s], acc);
+                acc = mfma16<DT>(kh, qlo[s], acc);
+                if constexpr (LO) acc = mfma16<DT>(*(const u32x4 *)&ks[NP - 1][off], qh[s], acc);
+            }
+            sc[j] = acc;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < BK / 16; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int jg = kb + 16 * j + 4 * g4 + r;
+                const float v = (jg >= jlo && jg <= t) ? sc[j][r] * scale : -INFINITY;
+                sc[j][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = max_rows(mx);
+        const float m_new = fmaxf(m_run, mx);
+        const float rescale = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+        m_run = m_new;
+        l_part *= rescale;
+#pragma unroll
+        for (int i = 0; i < NO; i++) o[i] *= rescale;
+        // P (unnormalised) as B operands of O^T = V^T . P^T, two 32-key steps
+#pragma unroll
+        for (int s2 = 0; s2 < BK / 32; s2++) {
+            float p[8];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float a = sc[2 * s2][r], b = sc[2 * s2 + 1][r];
+                p[r] = a == -INFINITY ? 0.f : expf(a - m_new);
+                p[4 + r] = b == -INFINITY ? 0.f : expf(b - m_new);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) l_part += p[e];
+            u32x4 ph, pl;
+            split8<DT>(p, ph, pl);
+#pragma unroll
+            for (int i = 0; i < NO; i++) {
+                const int off = (16 * i + ql) * VRS + 64 * s2 + 8 * g4;
+                const uint2 a0 = *(const uint2 *)&vts[0][off], a1 = *(const uint2 *)&vts[0][off + 32];
+                const u32x4 vh = u32x4{a0.x, a0.y, a1.x, a1.y};
+                o[i] = mfma16<DT>(vh, ph, o[i]);
+                o[i] = mfma16<DT>(vh, pl, o[i]);
+                if constexpr (LO) {
+                    const uint2 b0 = *(const uint2 *)&vts[NP - 1][off], b1 = *(const uint2 *)&vts[NP - 1][off + 32];
+                    o[i] = mfma16<DT>(u32x4{b0.x, b0.y, b1.x, b1.y}, ph, o[i]);
+                }
+            }
+        }
+    }
+    const float l_tot = sum_rows(l_part);
+    if (!tok) return;
+    const float inv = 1.0f / l_tot;
+#pragma unroll
+    for (int i = 0; i < NO; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            store_op(att, (size_t)t * qdim + h * HD + 16 * i + 4 * g4 + r, plane, o[i][r] * inv, DT);
+}
+
 // Causal attention (forward_common.go:5-33): one wave per (query t, head h). Row t is
 // position rowpos[t] of its sequence, whose rows are the rowpos[t] rows before it, so the keys
 // are j in [t - rowpos[t], t]. Lanes walk the keys in blocks of 64; scores are kept in LDS,
@@ -1762,11 +1950,20 @@ hipError_t launch_attn_prefill(const sh_model *m, int S, int seg_max, bool fill_
     const size_t plane = (size_t)S * m->qdim;
     const bool exact = fill_kv && ((c.kv_dtype == SH_KV_BF16 && dt == SH_DTYPE_BF16) ||
                                    (c.kv_dtype == SH_KV_F16 && dt == SH_DTYPE_F16));
-    const dim3 grid((S + 15) / 16, c.n_heads);
+    // 64-query tiles when their grid alone covers the CUs, else 16-query tiles
+    const bool wide = (size_t)((S + 63) / 64) * c.n_heads >= 256;
+    const dim3 grid = wide ? dim3((S + 63) / 64, c.n_heads) : dim3((S + 15) / 16, c.n_heads);
 #define SH_ATT(DTV, HDV, LOV)                                                                   \
-    hipLaunchKernelGGL((k_attn_prefill_mfma<DTV, HDV, LOV>), grid, dim3(kT), 0, s, m->pf_q,     \
-                       m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale,        \
-                       m->pf_att, plane)
+    do {                                                                                        \
+        if (wide)                                                                               \
+            hipLaunchKernelGGL((k_attn_prefill_mfma64<DTV, HDV, LOV>), grid, dim3(kT), 0, s,     \
+                               m->pf_q, m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads,             \
+                               c.n_kv_heads, scale, m->pf_att, plane);                           \
+        else                                                                                    \
+            hipLaunchKernelGGL((k_attn_prefill_mfma<DTV, HDV, LOV>), grid, dim3(kT), 0, s,       \
+                               m->pf_q, m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads,             \
+                               c.n_kv_heads, scale, m->pf_att, plane);                           \
+    } while (0)
 #define SH_ATT_HD(DTV, LOV)                                                                     \
     if (c.head_dim == 32) SH_ATT(DTV, 32, LOV);                                                  \
     else if (c.head_dim == 64) SH_ATT(DTV, 64, LOV);                                             \
