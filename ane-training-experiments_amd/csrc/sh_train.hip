@@ -144,6 +144,69 @@ __global__ __launch_bounds__(256) void k_sgemm(const float *A, int lda, const fl
         }
 }
 
+// k_sgemm for tile-aligned shapes (M, N multiples of 64, every K range a multiple of 64): the
+// loads of four K blocks (64 k) issue together, with no bounds checks and so no branches, and
+// then pass through the two LDS buffers one block at a time (one barrier per block: a buffer
+// is rewritten two blocks after it was read). A workgroup then waits out one load latency
+// per four blocks instead of one per block.
+template <bool AK, bool BK, int EPI>
+__global__ __launch_bounds__(256) void k_sgemm_nb(const float *A, int lda, const float *B, int ldb, float *C,
+                                                  int ldc, int M, int N, int K, float alpha, const float *R,
+                                                  int kc) {
+    constexpr int NB = 4;
+    __shared__ __attribute__((aligned(16))) float As[2][kGK][kGM + kGP];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kGK][kGN + kGP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    const int m0 = blockIdx.y * kGM, n0 = blockIdx.x * kGN;
+    f32x4 acc[2][2];
+    for (int i = 0; i < 2; i++)
+        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int kb = blockIdx.z * kc, ke = min(K, kb + kc);
+    // this thread's 16-byte chunk of a K block: AK (row tid/4, k 4*(tid%4)), else (k tid/16,
+    // rows 4*(tid%16)); likewise for B
+    const float *pa = AK ? A + (size_t)(m0 + tid / 4) * lda + (tid % 4) * 4 : A + (size_t)(tid / 16) * lda + m0 + (tid % 16) * 4;
+    const float *pb = BK ? B + (size_t)(n0 + tid / 4) * ldb + (tid % 4) * 4 : B + (size_t)(tid / 16) * ldb + n0 + (tid % 16) * 4;
+    const size_t sa = AK ? kGK : (size_t)kGK * lda, sb = BK ? kGK : (size_t)kGK * ldb;   // per K block
+    const int lr = lane & 15, lk = lane >> 4;
+    for (int k0 = kb; k0 < ke; k0 += NB * kGK) {
+        f32x4 ra[NB], rb[NB];
+        const size_t oa = AK ? (size_t)k0 : (size_t)k0 * lda, ob = BK ? (size_t)k0 : (size_t)k0 * ldb;
+#pragma unroll
+        for (int u = 0; u < NB; u++) {
+            ra[u] = *(const f32x4 *)(pa + oa + u * sa);
+            rb[u] = *(const f32x4 *)(pb + ob + u * sb);
+        }
+#pragma unroll
+        for (int u = 0; u < NB; u++) {
+            const int buf = u & 1;
+            gemm_stage<AK>(As[buf], ra[u], tid);
+            gemm_stage<BK>(Bs[buf], rb[u], tid);
+            __syncthreads();
+#pragma unroll
+            for (int kk = 0; kk < kGK; kk += 4) {
+                const float a0 = As[buf][kk + lk][wm + lr], a1 = As[buf][kk + lk][wm + 16 + lr];
+                const float b0 = Bs[buf][kk + lk][wn + lr], b1 = Bs[buf][kk + lk][wn + 16 + lr];
+                acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+            }
+        }
+    }
+    for (int i = 0; i < 2; i++)
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn + j * 16 + lr;
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm + i * 16 + lk * 4 + r;
+                const size_t o = (size_t)m * ldc + n;
+                if constexpr (EPI == EPI_STORE) C[o] = alpha * acc[i][j][r];
+                else if constexpr (EPI == EPI_RESID) C[o] = R[o] + alpha * acc[i][j][r];
+                else C[(size_t)blockIdx.z * M * ldc + o] = acc[i][j][r];
+            }
+        }
+}
+
 // C = alpha * (sum over the K ranges in order of the partial tiles [ranges][M][ldc]), plus R
 // when it is given (the residual epilogue).
 __global__ void k_tr_reduce_ranges(const float *P, int ranges, int M, int N, int ldc, float alpha, const float *R,
@@ -1191,11 +1254,17 @@ constexpr int kSqParts = 1024;
 
 unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 8192); }
 
+// tile-aligned shapes (and 16-byte aligned rows) take the burst-load kernel
+bool sgemm_aligned(int M, int N, int K, int kc) { return M % 64 == 0 && N % 64 == 0 && K % 64 == 0 && kc % 64 == 0; }
+
 template <bool AK, bool BK, int EPI>
 hipError_t sgemm(hipStream_t s, const float *A, int lda, const float *B, int ldb, float *C, int ldc, int M,
                  int N, int K, float alpha, const float *R = nullptr) {
     const dim3 grid((N + kGN - 1) / kGN, (M + kGM - 1) / kGM);
-    hipLaunchKernelGGL((k_sgemm<AK, BK, EPI>), grid, dim3(256), 0, s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R, K);
+    if (sgemm_aligned(M, N, K, K))
+        hipLaunchKernelGGL((k_sgemm_nb<AK, BK, EPI>), grid, dim3(256), 0, s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R, K);
+    else
+        hipLaunchKernelGGL((k_sgemm<AK, BK, EPI>), grid, dim3(256), 0, s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R, K);
     return hipGetLastError();
 }
 
@@ -1212,11 +1281,17 @@ hipError_t sgemm_split(hipStream_t s, const float *A, int lda, const float *B, i
     if (ranges == 1)
         return R ? sgemm<AK, BK, EPI_RESID>(s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R)
                  : sgemm<AK, BK, EPI_STORE>(s, A, lda, B, ldb, C, ldc, M, N, K, alpha);
-    const int kc = (K / ranges + kGK - 1) / kGK * kGK;
+    int kc = (K / ranges + kGK - 1) / kGK * kGK;
+    const bool al = sgemm_aligned(M, N, K, 64);
+    if (al) kc = (K / ranges + 63) / 64 * 64;   // ranges of whole 64-k bursts
     ranges = (K + kc - 1) / kc;
     const dim3 grid((N + kGN - 1) / kGN, (M + kGM - 1) / kGM, ranges);
-    hipLaunchKernelGGL((k_sgemm<AK, BK, EPI_PART>), grid, dim3(256), 0, s, A, lda, B, ldb, part, ldc, M, N, K, 1.f,
-                       nullptr, kc);
+    if (al)
+        hipLaunchKernelGGL((k_sgemm_nb<AK, BK, EPI_PART>), grid, dim3(256), 0, s, A, lda, B, ldb, part, ldc, M, N, K,
+                           1.f, nullptr, kc);
+    else
+        hipLaunchKernelGGL((k_sgemm<AK, BK, EPI_PART>), grid, dim3(256), 0, s, A, lda, B, ldb, part, ldc, M, N, K,
+                           1.f, nullptr, kc);
     const size_t n = (size_t)M * N;
     hipLaunchKernelGGL(k_tr_reduce_ranges, dim3(blocks_for(n)), dim3(256), 0, s, part, ranges, M, N, ldc, alpha, R,
                        C);
