@@ -144,16 +144,16 @@ __global__ __launch_bounds__(256) void k_sgemm(const float *A, int lda, const fl
         }
 }
 
-// k_sgemm for tile-aligned shapes (M, N multiples of 64, every K range a multiple of 64): the
-// loads of four K blocks (64 k) issue together, with no bounds checks and so no branches, and
-// then pass through the two LDS buffers one block at a time (one barrier per block: a buffer
-// is rewritten two blocks after it was read). A workgroup then waits out one load latency
-// per four blocks instead of one per block.
+// k_sgemm for tile-aligned shapes (M, N multiples of 64, every K range a multiple of 128): the
+// loads of eight K blocks (128 k) issue together, with no bounds checks and so no branches,
+// and then pass through the two LDS buffers one block at a time (one barrier per block: a
+// buffer is rewritten two blocks after it was read). A workgroup then waits out one load
+// latency per eight blocks instead of one per block.
 template <bool AK, bool BK, int EPI>
 __global__ __launch_bounds__(256) void k_sgemm_nb(const float *A, int lda, const float *B, int ldb, float *C,
                                                   int ldc, int M, int N, int K, float alpha, const float *R,
                                                   int kc) {
-    constexpr int NB = 4;
+    constexpr int NB = 8;
     __shared__ __attribute__((aligned(16))) float As[2][kGK][kGM + kGP];
     __shared__ __attribute__((aligned(16))) float Bs[2][kGK][kGN + kGP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1255,7 +1255,7 @@ constexpr int kSqParts = 1024;
 unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 8192); }
 
 // tile-aligned shapes (and 16-byte aligned rows) take the burst-load kernel
-bool sgemm_aligned(int M, int N, int K, int kc) { return M % 64 == 0 && N % 64 == 0 && K % 64 == 0 && kc % 64 == 0; }
+bool sgemm_aligned(int M, int N, int K, int kc) { return M % 64 == 0 && N % 64 == 0 && K % 128 == 0 && kc % 128 == 0; }
 
 template <bool AK, bool BK, int EPI>
 hipError_t sgemm(hipStream_t s, const float *A, int lda, const float *B, int ldb, float *C, int ldc, int M,
@@ -1282,8 +1282,8 @@ hipError_t sgemm_split(hipStream_t s, const float *A, int lda, const float *B, i
         return R ? sgemm<AK, BK, EPI_RESID>(s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R)
                  : sgemm<AK, BK, EPI_STORE>(s, A, lda, B, ldb, C, ldc, M, N, K, alpha);
     int kc = (K / ranges + kGK - 1) / kGK * kGK;
-    const bool al = sgemm_aligned(M, N, K, 64);
-    if (al) kc = (K / ranges + 63) / 64 * 64;   // ranges of whole 64-k bursts
+    const bool al = sgemm_aligned(M, N, K, 128);
+    if (al) kc = (K / ranges + 127) / 128 * 128;   // ranges of whole 128-k bursts
     ranges = (K + kc - 1) / kc;
     const dim3 grid((N + kGN - 1) / kGN, (M + kGM - 1) / kGM, ranges);
     if (al)
