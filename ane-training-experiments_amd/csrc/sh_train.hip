@@ -873,11 +873,34 @@ __device__ __forceinline__ void adam_elem(float &w, float &g, float &m, float &v
     if (wd != 0) up += wd * w;
     w -= lr * up;
 }
+// Four independent elements per thread per pass (i, i + stride, ...), all sixteen loads issued
+// before any arithmetic, so each thread keeps four times the bytes in flight.
 __global__ void k_tr_adam(float *w, float *g, float *m, float *v, size_t n, float lr, float b1, float b2,
                           float eps, float wd, float ibc1, float ibc2, float inv_ls, float clip) {
     const bool wb = inv_ls != 1.f || clip != 1.f;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        adam_elem(w[i], g[i], m[i], v[i], wb, lr, b1, b2, eps, wd, ibc1, ibc2, inv_ls, clip);
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + 3 * stride < n; i += 4 * stride) {
+        float wa[4], ga[4], ma[4], va[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const size_t j = i + u * stride;
+            wa[u] = w[j];
+            ga[u] = g[j];
+            ma[u] = m[j];
+            va[u] = v[j];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const size_t j = i + u * stride;
+            adam_elem(wa[u], ga[u], ma[u], va[u], wb, lr, b1, b2, eps, wd, ibc1, ibc2, inv_ls, clip);
+            w[j] = wa[u];
+            m[j] = ma[u];
+            v[j] = va[u];
+            if (wb) g[j] = ga[u];
+        }
+    }
+    for (; i < n; i += stride) adam_elem(w[i], g[i], m[i], v[i], wb, lr, b1, b2, eps, wd, ibc1, ibc2, inv_ls, clip);
 }
 
 // ---- fp32 MFMA attention (flash form) ----------------------------------------------------
