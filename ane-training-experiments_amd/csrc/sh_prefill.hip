@@ -1752,14 +1752,16 @@ __global__ __launch_bounds__(kT) void k_window_advance(const float *pv, const in
     if (threadIdx.x == 0) window[seq - 1] = next_s;
 }
 
-// Tile shape and K split of the tiled GEMM: 128 x 128 tiles for long inputs, else 64 x 64
-// with K split (ranges of >= 256, dividing K) until there are about 512 workgroups.
+// Tile shape and K split of the tiled GEMM: 128 x 128 tiles for long inputs and for very wide
+// outputs (the classifier: half the re-reads of the activation planes; 48 vs 57 us at
+// S = 256, N = 32000), else 64 x 64 with K split (ranges of >= 256, dividing K) until there
+// are about 512 workgroups.
 struct GemmPlan {
     int big, ranges, kc;
 };
 GemmPlan gemm_plan(int M, int N, int K) {
     GemmPlan p{};
-    p.big = M >= 1024 && N % 128 == 0;
+    p.big = (M >= 1024 || (M >= 256 && N >= 16384)) && N % 128 == 0;
     const int tiles = p.big ? ((M + 127) / 128) * (N / 128) : ((M + 63) / 64) * (N / 64);
     p.ranges = 1;
     for (int r : {2, 3, 4, 6, 8, 12, 16})
