@@ -121,7 +121,6 @@ size_t arg_words(const sh_model *m) { return 2 * (size_t)m->p_grid * kArgSlot; }
 bool run_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt) {
     const uint64_t need = (uint64_t)n_forwards * (uint64_t)(m->cfg.n_layers + 1);
     if ((uint64_t)m->epoch + need >= 0xF0000000ull) {
-        const sh_config &c = m->cfg;
         struct {
             uint64_t *p;
             size_t n;

@@ -1415,15 +1415,6 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
 
 typedef void (*PersistentKernel)(PParams);
 
-// Lanes per row of the three GEMV widths, matching pick_shape's instantiations. A row of
-// width C is covered by LPR lanes x CPL 16-byte chunks (8 fp16/bf16 or 16 int8 values).
-void shape_lanes(int dtype, int D, int Q, int F, int *ld, int *lq, int *lf) {
-    const bool q8 = dtype == SH_DTYPE_W8A8;
-    if (D == 768 && Q == 768 && F == 2048) { *ld = q8 ? 16 : 32; *lq = q8 ? 16 : 32; *lf = q8 ? 32 : 64; }
-    else if (D == 1024 && Q == 2048 && F == 3072) { *ld = 32; *lq = q8 ? 32 : 64; *lf = 64; }
-    else { *ld = q8 ? 8 : 16; *lq = q8 ? 8 : 16; *lf = q8 ? 16 : 32; }
-}
-
 template <int WT, int KVT>
 PersistentKernel pick_shape(int D, int Q, int F, int HDv) {
     if constexpr (WT == SH_DTYPE_W8A8) {
