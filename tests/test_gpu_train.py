@@ -198,6 +198,34 @@ def test_gradient_accumulation_matches_oracle(gpu):
     tr.close()
 
 
+def test_twenty_step_loss_delta_gate(gpu):
+    """The reference's training parity gate (scripts/pure_go_parity_gate.sh:13-14: 20 steps,
+    max loss delta 0.01 between implementations): 20 Step() calls over drand48 windows, device
+    against oracle, every loss within 0.01 (and the losses fall)."""
+    cfg = train_config()
+    seq = 16
+    w, tr = make(cfg, 351, seq, lr=3e-3, seed=11)
+    stream = sh.synth_tokens(400, 352, cfg.vocab)
+    tr.set_tokens(stream)
+    p = oracle.TrainParams.from_weights(w)
+    m, v, g = (oracle.TrainParams.zeros_like(p) for _ in range(3))
+    L = oracle.load()
+    st = oracle.C.c_uint64(L.or_drand48_seed(11))
+    ocfg, hp = oracle.config_from(cfg), oracle.hparams(lr=3e-3)
+    worst, got_all = 0.0, []
+    for t in range(1, 21):
+        pos = L.or_train_window(oracle.C.byref(st), stream.size, seq)
+        want = oracle.train_step(ocfg, p, m, v, g, hp, t, stream[pos:pos + seq], stream[pos + 1:pos + 1 + seq],
+                                 threads=THREADS)
+        got = tr.step()
+        got_all.append(got)
+        worst = max(worst, abs(got - want))
+    print(f"20 steps: max loss delta {worst:.2e}, loss {got_all[0]:.4f} -> {got_all[-1]:.4f}")
+    assert worst <= 0.01
+    assert np.mean(got_all[-5:]) < np.mean(got_all[:5])
+    tr.close()
+
+
 def test_train_errors(gpu):
     cfg = train_config()
     _, tr = make(cfg, 331, 16)

@@ -302,3 +302,33 @@ def test_flush_pending_reference_case():
     # nothing pending: no update
     oracle.train_flush(c, p, m, v, acc, hp, 2, 0)
     assert np.array_equal(p.rms_final, np.float32(1) - lr * np.ones(2, np.float32))
+
+
+def test_rms_grad_weights_reference_fixture():
+    # ane/storiesane/engine_test.go:376-400 TestRMSNormGradWeightsMatchesCPUBackward: dim 3,
+    # seq 2, its dy / x / w; dw[i] = sum_t dy*x*rrms_t with rrms_t = 1/sqrt(mean_i x^2 + 1e-5)
+    dy = np.array([[0.1, 0.2], [0.3, 0.4], [0.5, 0.6]], np.float32)
+    x = np.array([[1.0, 2.0], [3.0, 4.0], [5.0, 6.0]], np.float32)
+    w = np.array([1.1, 0.9, 1.2], np.float32)
+    r = (1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(0) + 1e-5)).astype(np.float32)
+    _, dw = oracle.rms_norm_backward_cf(dy, x, w, r)
+    want = (dy.astype(np.float64) * x.astype(np.float64) * r.astype(np.float64)).sum(1)
+    np.testing.assert_allclose(dw, want, atol=1e-5, rtol=0)
+
+
+def test_cross_entropy_reference_fixture():
+    # ane/storiesane/engine_test.go:402-448 TestCrossEntropyLossFromProbsMatchesCPU: vocab 4,
+    # seq 3, targets (3, 2, 9) with 9 out of range; loss and gradient against float64
+    logits = np.array([[0.4, -0.2, 1.3], [0.1, 0.7, -0.1], [-0.3, 0.5, 0.2], [1.0, -0.4, 0.0]], np.float32)
+    tg = [3, 2, 9]
+    loss, d = oracle.cross_entropy_loss(logits, tg)
+    z = logits.astype(np.float64)
+    p = np.exp(z - z.max(0)) / np.exp(z - z.max(0)).sum(0)
+    want_loss = -(np.log(p[3, 0]) + np.log(p[2, 1])) / 2
+    g = p.copy()
+    g[3, 0] -= 1
+    g[2, 1] -= 1
+    g[:, :2] /= 2
+    g[:, 2] = 0
+    assert abs(loss - want_loss) <= 1e-5
+    np.testing.assert_allclose(d, g, atol=1e-5, rtol=0)
