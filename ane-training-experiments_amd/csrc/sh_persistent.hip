@@ -936,7 +936,11 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
             const float *ph = sc + h * p.max_seq;
             const int tl = pos < S::ROWS ? pos : S::ROWS - 1;
             float sum = 0.f;
+            // unrolled so the loads of eight positions issue ahead of their adds, which stay
+            // one after another in position order
+#pragma unroll 8
             for (int t = 0; t <= tl; t++) sum = __fadd_rn(sum, __fmul_rn(ph[t], kv_get<KVT>(vst + (size_t)t * S::RB, ii)));
+#pragma unroll 8
             for (int t = tl + 1; t <= pos; t++) {
                 const float vv = t == pos ? vs[ii] : kv_ld<KVT>(p.vcache, lbase + (size_t)t * p.kvdim + ii);
                 sum = __fadd_rn(sum, __fmul_rn(ph[t], vv));
