@@ -742,10 +742,11 @@ __global__ __launch_bounds__(256) void k_tr_rms_bwd_dw(const float *dy, const fl
 // cpu.go:173-253 CrossEntropyLoss for row t of logits [S, V] (in place -> dLogits): float32
 // exp terms summed in float64, probabilities, then at the target p (floored at 1e-10) gives
 // -log p and dLogits -= 1; a row with an out-of-range target is zeroed.
-__global__ __launch_bounds__(kTT) void k_tr_ce_rows(float *lg, const uint16_t *tgt, int V, double *row_loss,
-                                                    int *row_valid) {
-    __shared__ double red[kTT / 64];
-    __shared__ float redf[kTT / 64];
+constexpr int kCeT = 1024;   // threads per vocabulary row: three passes over V floats each
+__global__ __launch_bounds__(kCeT) void k_tr_ce_rows(float *lg, const uint16_t *tgt, int V, double *row_loss,
+                                                     int *row_valid) {
+    __shared__ double red[kCeT / 64];
+    __shared__ float redf[kCeT / 64];
     float *row = lg + (size_t)blockIdx.x * V;
     float mx = -INFINITY;
     for (int i = threadIdx.x; i < V; i += blockDim.x) mx = fmaxf(mx, row[i]);
@@ -1382,9 +1383,9 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale, bool acc) {
     hipLaunchKernelGGL(k_tr_rmsnorm, dim3(S), dim3(kTT), 0, s, T->xL, T->p + T->o_rfin, D, eps, T->xnf, T->rfin);
     if ((e = sgemm<true, true, EPI_STORE>(s, T->xnf, D, T->p + T->o_embed, D, T->logits, V, S, V, D, 1.f)))
         return e;
-    hipLaunchKernelGGL(k_tr_ce_rows, dim3(S), dim3(kTT), 0, s, T->logits, T->tok_tgt, V, T->row_loss, T->row_valid);
+    hipLaunchKernelGGL(k_tr_ce_rows, dim3(S), dim3(kCeT), 0, s, T->logits, T->tok_tgt, V, T->row_loss, T->row_valid);
     hipLaunchKernelGGL(k_tr_ce_total, dim3(1), dim3(64), 0, s, T->row_loss, T->row_valid, S, T->loss);
-    hipLaunchKernelGGL(k_tr_scale_rows, dim3(S), dim3(256), 0, s, T->logits, T->row_valid, T->loss, V);
+    hipLaunchKernelGGL(k_tr_scale_rows, dim3(S), dim3(1024), 0, s, T->logits, T->row_valid, T->loss, V);
     // dy[t][d] = (sum_v dL[t][v] E[v][d]) * loss scale (MatMulEmbedTScale)
     if ((e = sgemm_split<true, false>(s, T->logits, V, T->p + T->o_embed, D, T->dy, D, S, D, V, loss_scale,
                                       T->part, T->part_cap)))
