@@ -684,8 +684,11 @@ __global__ void k_tr_silu_bwd(const float *dgate, const float *h13, int F, size_
 
 // rmsnorm.go:32-47 per row: dot = sum_i dy*x*w (float64), dx = (dy - x*dot*r^2/D)*r*w in float64
 // rounded once.
+// addend given: dx = addend + the gradient (the backward's residual add, the gradient rounded
+// to float32 first as when it is stored and then added).
 __global__ __launch_bounds__(kTT) void k_tr_rms_bwd_dx(const float *dy, const float *x, const float *w,
-                                                       const float *rrms, int D, float *dx) {
+                                                       const float *rrms, int D, float *dx,
+                                                       const float *addend = nullptr) {
     __shared__ double red[kTT / 64];
     const size_t o = (size_t)blockIdx.x * D;
     double dot = 0;
@@ -694,7 +697,8 @@ __global__ __launch_bounds__(kTT) void k_tr_rms_bwd_dx(const float *dy, const fl
     const double r = (double)rrms[blockIdx.x], r2 = (r * r) / (double)D;
     for (int i = threadIdx.x; i < D; i += blockDim.x) {
         const double v = (double)dy[o + i] - (double)x[o + i] * dot * r2;
-        dx[o + i] = (float)(v * r * (double)w[i]);
+        const float g = (float)(v * r * (double)w[i]);
+        dx[o + i] = addend ? addend[o + i] + g : g;
     }
 }
 
@@ -836,11 +840,6 @@ __global__ void k_tr_fill(float *p, size_t n, float v) {
         p[i] = v;
 }
 
-// out = a + s*b (s = 0: out = a + b as float32 adds)
-__global__ void k_tr_axpy(const float *a, const float *b, float s, int plain_add, size_t n, float *out) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        out[i] = plain_add ? a[i] + b[i] : a[i] * s;
-}
 
 // Sum of squares of p[0, n) into per-block float64 partials (block order fixed).
 __global__ __launch_bounds__(kTT) void k_tr_sumsq(const float *p, size_t n, float inv_ls, double *part) {
@@ -1254,7 +1253,7 @@ struct sh_trainer {
         float *x, *xn, *ra, *qkv, *att, *x2, *x2n, *rf, *h13, *gate;
     };
     std::vector<Layer> lc;
-    float *xL, *xnf, *rfin, *logits, *dy, *dcur, *dprev, *dout, *gx2, *dx2s, *gxn, *gatt, *ggate,
+    float *xL, *xnf, *rfin, *logits, *dy, *dcur, *gx2, *gxn, *gatt, *ggate,
         *dh13, *dqkv, *stats, *dlc, *gc, *loss, *cos_t, *sin_t;
     double *row_loss, *sq_part;
     int *row_valid;
@@ -1326,9 +1325,9 @@ hipError_t sgemm_split(hipStream_t s, const float *A, int lda, const float *B, i
 // accumulate over windows.
 template <bool AK, bool BK>
 hipError_t sgemm_grad(hipStream_t s, const float *A, int lda, const float *B, int ldb, float *C, int ldc, int M,
-                      int N, int K, bool acc) {
-    return acc ? sgemm<AK, BK, EPI_RESID>(s, A, lda, B, ldb, C, ldc, M, N, K, 1.f, C)
-               : sgemm<AK, BK, EPI_STORE>(s, A, lda, B, ldb, C, ldc, M, N, K, 1.f);
+                      int N, int K, bool acc, float alpha = 1.f) {
+    return acc ? sgemm<AK, BK, EPI_RESID>(s, A, lda, B, ldb, C, ldc, M, N, K, alpha, C)
+               : sgemm<AK, BK, EPI_STORE>(s, A, lda, B, ldb, C, ldc, M, N, K, alpha);
 }
 
 // Forward (train_full.go:368-396) for the window in tok_in, then runFinalHead's CPU path
@@ -1419,9 +1418,9 @@ hipError_t tr_backward(sh_trainer *T, int n_in, bool acc) {
     hipError_t e;
     for (int l = T->L - 1; l >= 0; l--) {
         sh_trainer::Layer &C = T->lc[l];
-        hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dcur, T->dcur, alpha, 0, SD, T->dout);
-        // FFN: ggate = dout . W2, (dh1, dh3), gxn = [dh1|dh3] . [W1;W3], RMS backward
-        if ((e = sgemm_split<true, false>(s, T->dout, D, T->p + T->o_w2[l], F, T->ggate, F, S, F, D, 1.f, T->part,
+        // FFN: ggate = dout . W2 with dout = alpha dcur (the scale applied to the product),
+        // (dh1, dh3), gxn = [dh1|dh3] . [W1;W3], RMS backward
+        if ((e = sgemm_split<true, false>(s, T->dcur, D, T->p + T->o_w2[l], F, T->ggate, F, S, F, D, alpha, T->part,
                                           T->part_cap)))
             return e;
         const size_t nf = (size_t)S * F;
@@ -1429,19 +1428,19 @@ hipError_t tr_backward(sh_trainer *T, int n_in, bool acc) {
         if ((e = sgemm_split<true, false>(s, T->dh13, 2 * F, T->p + T->o_w13[l], D, T->gxn, D, S, D, 2 * F, 1.f,
                                           T->part, T->part_cap)))
             return e;
+        // gx2 = dcur + the RMS backward's dx
         hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x2, T->p + T->o_rf[l], C.rf, D,
-                           T->dprev);
+                           T->gx2, T->dcur);
         hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + kDwCols - 1) / kDwCols), dim3(256), 0, s, T->gxn, C.x2, C.rf, S, D,
                            acc ? kDwContinue : kDwStore, T->g + T->o_rf[l]);
-        hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dcur, T->dprev, 0.f, 1, SD, T->gx2);
-        // weight gradients: dW2 = dout^T gate, d[W1;W3] = [dh1|dh3]^T x2n
-        if ((e = sgemm_grad<false, false>(s, T->dout, D, C.gate, F, T->g + T->o_w2[l], F, D, F, S, acc)))
+        // weight gradients: dW2 = dout^T gate (alpha dcur^T gate), d[W1;W3] = [dh1|dh3]^T x2n
+        if ((e = sgemm_grad<false, false>(s, T->dcur, D, C.gate, F, T->g + T->o_w2[l], F, D, F, S, acc, alpha)))
             return e;
         if ((e = sgemm_grad<false, false>(s, T->dh13, 2 * F, C.x2n, D, T->g + T->o_w13[l], D, 2 * F, D, S, acc)))
             return e;
-        hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->gx2, T->gx2, alpha, 0, SD, T->dx2s);
-        // attention: gatt = dx2s . Wo, (dq, dk, dv), gxn = [dq|dk|dv] . [Wq;Wk;Wv], RMS backward
-        if ((e = sgemm_split<true, false>(s, T->dx2s, D, T->p + T->o_wo[l], D, T->gatt, D, S, D, D, 1.f, T->part,
+        // attention: gatt = dx2s . Wo with dx2s = alpha gx2, (dq, dk, dv),
+        // gxn = [dq|dk|dv] . [Wq;Wk;Wv], RMS backward
+        if ((e = sgemm_split<true, false>(s, T->gx2, D, T->p + T->o_wo[l], D, T->gatt, D, S, D, D, alpha, T->part,
                                           T->part_cap)))
             return e;
         float *st = T->stats + (size_t)l * 3 * T->H * S;   // the forward's (max, 1/sum) rows
@@ -1473,13 +1472,13 @@ hipError_t tr_backward(sh_trainer *T, int n_in, bool acc) {
         if ((e = sgemm_split<true, false>(s, T->dqkv, 3 * D, T->p + T->o_qkv[l], D, T->gxn, D, S, D, 3 * D, 1.f,
                                           T->part, T->part_cap)))
             return e;
+        // the next layer's dcur = gx2 + the RMS backward's dx
         hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x, T->p + T->o_ra[l], C.ra, D,
-                           T->dprev);
+                           T->dcur, T->gx2);
         hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + kDwCols - 1) / kDwCols), dim3(256), 0, s, T->gxn, C.x, C.ra, S, D,
                            acc ? kDwContinue : kDwStore, T->g + T->o_ra[l]);
-        hipLaunchKernelGGL(k_tr_axpy, dim3(blocks_for(SD)), dim3(256), 0, s, T->dprev, T->gx2, 0.f, 1, SD, T->dcur);
-        // dWo = dx2s^T att, d[Wq;Wk;Wv] = [dq|dk|dv]^T xn
-        if ((e = sgemm_grad<false, false>(s, T->dx2s, D, C.att, D, T->g + T->o_wo[l], D, D, D, S, acc)))
+        // dWo = dx2s^T att (alpha gx2^T att), d[Wq;Wk;Wv] = [dq|dk|dv]^T xn
+        if ((e = sgemm_grad<false, false>(s, T->gx2, D, C.att, D, T->g + T->o_wo[l], D, D, D, S, acc, alpha)))
             return e;
         if ((e = sgemm_grad<false, false>(s, T->dqkv, 3 * D, C.xn, D, T->g + T->o_qkv[l], D, 3 * D, D, S, acc)))
             return e;
@@ -1717,8 +1716,7 @@ sh_trainer *sh_trainer_create(const sh_config *cfg, const sh_train_options *opt_
         lo[l].gate = take(4 * S * F);
     }
     const size_t o_xL = take(4 * S * D), o_xnf = take(4 * S * D), o_rfin = take(4 * S), o_lg = take(4 * S * V),
-                 o_dy = take(4 * S * D), o_dcur = take(4 * S * D), o_dprev = take(4 * S * D),
-                 o_dout = take(4 * S * D), o_gx2 = take(4 * S * D), o_dx2s = take(4 * S * D),
+                 o_dy = take(4 * S * D), o_dcur = take(4 * S * D), o_gx2 = take(4 * S * D),
                  o_gxn = take(4 * S * D), o_gatt = take(4 * S * D), o_ggate = take(4 * S * F),
                  o_dh13 = take(4 * S * 2 * F), o_dqkv = take(4 * S * 3 * D), o_stats = take(4 * 3 * T->H * S * T->L),
                  o_dlc = take(4 * S * T->ldc_u), o_gc = take(4 * S * D), o_loss = take(16),
@@ -1750,8 +1748,8 @@ sh_trainer *sh_trainer_create(const sh_config *cfg, const sh_train_options *opt_
     }
     T->xL = (float *)(A + o_xL); T->xnf = (float *)(A + o_xnf); T->rfin = (float *)(A + o_rfin);
     T->logits = (float *)(A + o_lg); T->dy = (float *)(A + o_dy); T->dcur = (float *)(A + o_dcur);
-    T->dprev = (float *)(A + o_dprev); T->dout = (float *)(A + o_dout); T->gx2 = (float *)(A + o_gx2);
-    T->dx2s = (float *)(A + o_dx2s); T->gxn = (float *)(A + o_gxn); T->gatt = (float *)(A + o_gatt);
+    T->gx2 = (float *)(A + o_gx2);
+    T->gxn = (float *)(A + o_gxn); T->gatt = (float *)(A + o_gatt);
     T->ggate = (float *)(A + o_ggate); T->dh13 = (float *)(A + o_dh13); T->dqkv = (float *)(A + o_dqkv);
     T->stats = (float *)(A + o_stats); T->dlc = (float *)(A + o_dlc); T->gc = (float *)(A + o_gc);
     T->loss = (float *)(A + o_loss); T->cos_t = (float *)(A + o_cos); T->sin_t = (float *)(A + o_sin);
