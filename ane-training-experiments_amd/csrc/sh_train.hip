@@ -255,6 +255,55 @@ __global__ __launch_bounds__(kTT) void k_tr_rmsnorm(const float *x, const float 
 }
 
 // rope.go:26-46 on the q and k parts of row t of qkv [S, 3D] (e' = e*c - o*s, o' = o*c + e*s).
+// A split product's K-range partials ([ranges][rows][ld]) handed to the forward row kernel
+// that consumes the product instead of a separate sum: Y = R + alpha * (partials summed in
+// range order), R optional — k_tr_reduce_ranges' arithmetic. p == nullptr: none.
+struct PartIn {
+    const float *p;
+    int ranges;
+    size_t stride;   // floats per range
+    const float *R;
+    float alpha;
+};
+__device__ __forceinline__ void sum_part_row(const PartIn &q, int t, int ld, int n, float *y) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const size_t o = (size_t)t * ld + i;
+        float v = 0.f;
+        for (int z = 0; z < q.ranges; z++) v += q.p[(size_t)z * q.stride + o];
+        y[o] = q.R ? q.R[o] + q.alpha * v : q.alpha * v;
+    }
+}
+constexpr int kPT = 1024;   // threads of the row kernels that sum partials
+// k_tr_rmsnorm on row t of Y (written to x first)
+__global__ __launch_bounds__(kPT) void k_tr_rmsnorm_part(float *x, const float *w, int D, double eps, float *out,
+                                                         float *rrms, PartIn q) {
+    __shared__ double red[kPT / 64];
+    sum_part_row(q, blockIdx.x, D, D, x);   // each thread re-reads only its own columns below
+    const float *row = x + (size_t)blockIdx.x * D;
+    double ss = 0;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) ss += (double)row[i] * (double)row[i];
+    const double tot = block_sum_d(ss, red);
+    const float scale = (float)(1.0 / sqrt(tot / (double)D + eps));
+    if (threadIdx.x == 0) rrms[blockIdx.x] = scale;
+    for (int i = threadIdx.x; i < D; i += blockDim.x)
+        out[(size_t)blockIdx.x * D + i] = row[i] * scale * w[i];
+}
+__global__ void k_tr_rope(float *qkv, int D, int hd, const float *cs, const float *sn);
+// k_tr_rope on row t of the q|k|v product (summed into qkv first)
+__global__ __launch_bounds__(kPT) void k_tr_rope_part(float *qkv, int D, int hd, const float *cs, const float *sn,
+                                                      PartIn q) {
+    const int t = blockIdx.x, half = hd / 2;
+    sum_part_row(q, t, 3 * D, 3 * D, qkv);
+    __syncthreads();
+    for (int p = threadIdx.x; p < D; p += blockDim.x) {
+        const int col = 2 * p, i = (col % hd) / 2;
+        const float c = cs[t * half + i], s = sn[t * half + i];
+        float *e = qkv + (size_t)t * 3 * D + col;
+        const float ev = e[0], ov = e[1];
+        e[0] = ev * c - ov * s;
+        e[1] = ov * c + ev * s;
+    }
+}
 __global__ void k_tr_rope(float *qkv, int D, int hd, const float *cs, const float *sn) {
     const int t = blockIdx.x, half = hd / 2;
     for (int p = threadIdx.x; p < D; p += blockDim.x) {   // D pairs: D/2 in q, D/2 in k
@@ -1295,8 +1344,12 @@ hipError_t sgemm(hipStream_t s, const float *A, int lda, const float *B, int ldb
 // partials in `part`, then their sum in range order (k_tr_reduce_ranges). Falls back to one
 // range when `part` cannot hold them.
 template <bool AK, bool BK>
+// handoff given: with more than one range the partials are left for the consuming row kernel
+// (handoff->p set, C not written); with one range C is written and handoff->p stays null.
 hipError_t sgemm_split(hipStream_t s, const float *A, int lda, const float *B, int ldb, float *C, int ldc, int M,
-                       int N, int K, float alpha, float *part, size_t part_cap, const float *R = nullptr) {
+                       int N, int K, float alpha, float *part, size_t part_cap, const float *R = nullptr,
+                       PartIn *handoff = nullptr) {
+    if (handoff) *handoff = PartIn{};
     const int tiles = ((N + kGN - 1) / kGN) * ((M + kGM - 1) / kGM);
     int ranges = 1;
     if (tiles < 192 && K >= 512) ranges = std::min(16, std::max(1, K / 256));
@@ -1315,6 +1368,10 @@ hipError_t sgemm_split(hipStream_t s, const float *A, int lda, const float *B, i
     else
         hipLaunchKernelGGL((k_sgemm<AK, BK, EPI_PART>), grid, dim3(256), 0, s, A, lda, B, ldb, part, ldc, M, N, K,
                            1.f, nullptr, kc);
+    if (handoff) {
+        *handoff = PartIn{part, ranges, (size_t)M * ldc, R, alpha};
+        return hipGetLastError();
+    }
     const size_t n = (size_t)M * N;
     hipLaunchKernelGGL(k_tr_reduce_ranges, dim3(blocks_for(n)), dim3(256), 0, s, part, ranges, M, N, ldc, alpha, R,
                        C);
@@ -1342,13 +1399,21 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale, bool acc) {
     hipError_t e;
     float *cur = T->lc[0].x;
     hipLaunchKernelGGL(k_tr_embed, dim3(S), dim3(256), 0, s, T->p + T->o_embed, T->tok_in, V, D, cur);
+    // split products hand their partials to the row kernel that consumes them; hx: the
+    // previous layer's W2 product, summed by this layer's RMSNorm
+    PartIn hx{}, hq{}, hw{};
+    auto rmsnorm = [&](float *x, const float *g, float *out, float *rr, const PartIn &q) {
+        if (q.p) hipLaunchKernelGGL(k_tr_rmsnorm_part, dim3(S), dim3(kPT), 0, s, x, g, D, eps, out, rr, q);
+        else hipLaunchKernelGGL(k_tr_rmsnorm, dim3(S), dim3(kTT), 0, s, x, g, D, eps, out, rr);
+    };
     for (int l = 0; l < T->L; l++) {
         sh_trainer::Layer &C = T->lc[l];   // C.x == cur: the previous layer wrote it there
-        hipLaunchKernelGGL(k_tr_rmsnorm, dim3(S), dim3(kTT), 0, s, C.x, T->p + T->o_ra[l], D, eps, C.xn, C.ra);
+        rmsnorm(C.x, T->p + T->o_ra[l], C.xn, C.ra, hx);
         if ((e = sgemm_split<true, true>(s, C.xn, D, T->p + T->o_qkv[l], D, C.qkv, 3 * D, S, 3 * D, D, 1.f, T->part,
-                                         T->part_cap)))
+                                         T->part_cap, nullptr, &hq)))
             return e;
-        hipLaunchKernelGGL(k_tr_rope, dim3(S), dim3(256), 0, s, C.qkv, D, hd, T->cos_t, T->sin_t);
+        if (hq.p) hipLaunchKernelGGL(k_tr_rope_part, dim3(S), dim3(kPT), 0, s, C.qkv, D, hd, T->cos_t, T->sin_t, hq);
+        else hipLaunchKernelGGL(k_tr_rope, dim3(S), dim3(256), 0, s, C.qkv, D, hd, T->cos_t, T->sin_t);
         float *st = T->stats + (size_t)l * 3 * T->H * S;   // this layer's (max, 1/sum, dsSum) rows
         if (hd == 64)
             hipLaunchKernelGGL(k_tr_attn_fwd_mf<64>, dim3((S + kMQ - 1) / kMQ, T->H), dim3(256), 0, s, C.qkv, S, D,
@@ -1364,9 +1429,9 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale, bool acc) {
             hipLaunchKernelGGL(k_tr_attn_fwd, dim3(S, T->H), dim3(64), sizeof(float) * S, s, C.qkv, S, D, hd, scale,
                                C.att);
         if ((e = sgemm_split<true, true>(s, C.att, D, T->p + T->o_wo[l], D, C.x2, D, S, D, D, alpha, T->part,
-                                         T->part_cap, C.x)))
+                                         T->part_cap, C.x, &hw)))
             return e;
-        hipLaunchKernelGGL(k_tr_rmsnorm, dim3(S), dim3(kTT), 0, s, C.x2, T->p + T->o_rf[l], D, eps, C.x2n, C.rf);
+        rmsnorm(C.x2, T->p + T->o_rf[l], C.x2n, C.rf, hw);
         if ((e = sgemm_split<true, true>(s, C.x2n, D, T->p + T->o_w13[l], D, C.h13, 2 * F, S, 2 * F, D, 1.f, T->part,
                                          T->part_cap)))
             return e;
@@ -1374,12 +1439,12 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale, bool acc) {
         hipLaunchKernelGGL(k_tr_silu_gate, dim3(blocks_for(nf)), dim3(256), 0, s, C.h13, F, nf, C.gate);
         float *next = l + 1 < T->L ? T->lc[l + 1].x : T->xL;
         if ((e = sgemm_split<true, true>(s, C.gate, F, T->p + T->o_w2[l], F, next, D, S, D, F, alpha, T->part,
-                                         T->part_cap, C.x2)))
+                                         T->part_cap, C.x2, &hx)))
             return e;
         cur = next;
     }
     // final head
-    hipLaunchKernelGGL(k_tr_rmsnorm, dim3(S), dim3(kTT), 0, s, T->xL, T->p + T->o_rfin, D, eps, T->xnf, T->rfin);
+    rmsnorm(T->xL, T->p + T->o_rfin, T->xnf, T->rfin, hx);
     if ((e = sgemm<true, true, EPI_STORE>(s, T->xnf, D, T->p + T->o_embed, D, T->logits, V, S, V, D, 1.f)))
         return e;
     hipLaunchKernelGGL(k_tr_ce_rows, dim3(S), dim3(kCeT), 0, s, T->logits, T->tok_tgt, V, T->row_loss, T->row_valid);
