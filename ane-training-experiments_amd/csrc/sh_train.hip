@@ -751,6 +751,38 @@ __global__ __launch_bounds__(kTT) void k_tr_rms_bwd_dx(const float *dy, const fl
     }
 }
 
+// k_tr_rms_bwd_dx on row t of a split product (dy written first: the gain gradient reads it)
+__global__ __launch_bounds__(kPT) void k_tr_rms_bwd_dx_part(float *dy, const float *x, const float *w,
+                                                            const float *rrms, int D, float *dx,
+                                                            const float *addend, PartIn q) {
+    __shared__ double red[kPT / 64];
+    sum_part_row(q, blockIdx.x, D, D, dy);   // each thread re-reads only its own columns below
+    const size_t o = (size_t)blockIdx.x * D;
+    double dot = 0;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) dot += (double)(dy[o + i] * x[o + i] * w[i]);
+    dot = block_sum_d(dot, red);
+    const double r = (double)rrms[blockIdx.x], r2 = (r * r) / (double)D;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+        const double v = (double)dy[o + i] - (double)x[o + i] * dot * r2;
+        const float g = (float)(v * r * (double)w[i]);
+        dx[o + i] = addend ? addend[o + i] + g : g;
+    }
+}
+// k_tr_silu_bwd with dgate the sum of a split product's partials (ld == F)
+__global__ void k_tr_silu_bwd_part(const float *h13, int F, size_t n, float *dh13, PartIn q) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t t = i / F, j = i % F;
+        float v = 0.f;
+        for (int z = 0; z < q.ranges; z++) v += q.p[(size_t)z * q.stride + i];
+        const float dg = q.R ? q.R[i] + q.alpha * v : q.alpha * v;
+        const float h1 = h13[t * 2 * F + j], h3 = h13[t * 2 * F + F + j];
+        const float sig = (float)(1.0 / (1.0 + exp(-(double)h1)));
+        const float sg = sig * (1 + h1 * (1 - sig));
+        dh13[t * 2 * F + j] = dg * h3 * sg;
+        dh13[t * 2 * F + F + j] = dg * (h1 * sig);
+    }
+}
+
 // rmsnorm.go:32-47 gain gradient: the sum over t of float32(float64(dy*x)*r) (eight strided
 // row groups, each in row order, then added in group order), stored
 // (kDwStore), continued from dw[i] as rmsNormBackward does into an accumulator (kDwContinue, the
@@ -1451,8 +1483,9 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale, bool acc) {
     hipLaunchKernelGGL(k_tr_ce_total, dim3(1), dim3(64), 0, s, T->row_loss, T->row_valid, S, T->loss);
     hipLaunchKernelGGL(k_tr_scale_rows, dim3(S), dim3(1024), 0, s, T->logits, T->row_valid, T->loss, V);
     // dy[t][d] = (sum_v dL[t][v] E[v][d]) * loss scale (MatMulEmbedTScale)
+    PartIn hy{};   // summed by the final RMSNorm backward below
     if ((e = sgemm_split<true, false>(s, T->logits, V, T->p + T->o_embed, D, T->dy, D, S, D, V, loss_scale,
-                                      T->part, T->part_cap)))
+                                      T->part, T->part_cap, nullptr, &hy)))
         return e;
     // classifier embedding gradient on the target rows: gc[u][d] = (sum_t dL[t][ids u] xnf[t][d]) * scale
     float *gemb = T->g + T->o_embed;
@@ -1465,8 +1498,12 @@ hipError_t tr_forward_head(sh_trainer *T, int U, float loss_scale, bool acc) {
         hipLaunchKernelGGL(k_tr_scatter_rows, dim3(U), dim3(256), 0, s, T->gc, T->ids, D, (int)acc, gemb);
     }
     // final RMSNorm backward: dcur and the rms_final gradient
-    hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->dy, T->xL, T->p + T->o_rfin, T->rfin, D,
-                       T->dcur);
+    if (hy.p)
+        hipLaunchKernelGGL(k_tr_rms_bwd_dx_part, dim3(S), dim3(kPT), 0, s, T->dy, T->xL, T->p + T->o_rfin, T->rfin,
+                           D, T->dcur, (const float *)nullptr, hy);
+    else
+        hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->dy, T->xL, T->p + T->o_rfin, T->rfin, D,
+                           T->dcur);
     hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + kDwCols - 1) / kDwCols), dim3(256), 0, s, T->dy, T->xL, T->rfin, S, D,
                        acc ? kDwAdd : kDwStore, T->g + T->o_rfin);
     return hipGetLastError();
@@ -1485,17 +1522,25 @@ hipError_t tr_backward(sh_trainer *T, int n_in, bool acc) {
         sh_trainer::Layer &C = T->lc[l];
         // FFN: ggate = dout . W2 with dout = alpha dcur (the scale applied to the product),
         // (dh1, dh3), gxn = [dh1|dh3] . [W1;W3], RMS backward
+        PartIn hg{}, hn{};   // split products' partials for the row kernels below
         if ((e = sgemm_split<true, false>(s, T->dcur, D, T->p + T->o_w2[l], F, T->ggate, F, S, F, D, alpha, T->part,
-                                          T->part_cap)))
+                                          T->part_cap, nullptr, &hg)))
             return e;
         const size_t nf = (size_t)S * F;
-        hipLaunchKernelGGL(k_tr_silu_bwd, dim3(blocks_for(nf)), dim3(256), 0, s, T->ggate, C.h13, F, nf, T->dh13);
+        if (hg.p)
+            hipLaunchKernelGGL(k_tr_silu_bwd_part, dim3(blocks_for(nf)), dim3(256), 0, s, C.h13, F, nf, T->dh13, hg);
+        else
+            hipLaunchKernelGGL(k_tr_silu_bwd, dim3(blocks_for(nf)), dim3(256), 0, s, T->ggate, C.h13, F, nf, T->dh13);
         if ((e = sgemm_split<true, false>(s, T->dh13, 2 * F, T->p + T->o_w13[l], D, T->gxn, D, S, D, 2 * F, 1.f,
-                                          T->part, T->part_cap)))
+                                          T->part, T->part_cap, nullptr, &hn)))
             return e;
         // gx2 = dcur + the RMS backward's dx
-        hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x2, T->p + T->o_rf[l], C.rf, D,
-                           T->gx2, T->dcur);
+        if (hn.p)
+            hipLaunchKernelGGL(k_tr_rms_bwd_dx_part, dim3(S), dim3(kPT), 0, s, T->gxn, C.x2, T->p + T->o_rf[l], C.rf,
+                               D, T->gx2, (const float *)T->dcur, hn);
+        else
+            hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x2, T->p + T->o_rf[l], C.rf, D,
+                               T->gx2, T->dcur);
         hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + kDwCols - 1) / kDwCols), dim3(256), 0, s, T->gxn, C.x2, C.rf, S, D,
                            acc ? kDwContinue : kDwStore, T->g + T->o_rf[l]);
         // weight gradients: dW2 = dout^T gate (alpha dcur^T gate), d[W1;W3] = [dh1|dh3]^T x2n
@@ -1534,12 +1579,17 @@ hipError_t tr_backward(sh_trainer *T, int n_in, bool acc) {
             hipLaunchKernelGGL(k_tr_attn_bwd_kv, dim3(S, T->H), dim3(64), 2 * sizeof(float) * S, s, C.qkv, T->gatt,
                                S, D, hd, scale, st, T->dqkv);
         }
+        PartIn ha{};
         if ((e = sgemm_split<true, false>(s, T->dqkv, 3 * D, T->p + T->o_qkv[l], D, T->gxn, D, S, D, 3 * D, 1.f,
-                                          T->part, T->part_cap)))
+                                          T->part, T->part_cap, nullptr, &ha)))
             return e;
         // the next layer's dcur = gx2 + the RMS backward's dx
-        hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x, T->p + T->o_ra[l], C.ra, D,
-                           T->dcur, T->gx2);
+        if (ha.p)
+            hipLaunchKernelGGL(k_tr_rms_bwd_dx_part, dim3(S), dim3(kPT), 0, s, T->gxn, C.x, T->p + T->o_ra[l], C.ra,
+                               D, T->dcur, (const float *)T->gx2, ha);
+        else
+            hipLaunchKernelGGL(k_tr_rms_bwd_dx, dim3(S), dim3(kTT), 0, s, T->gxn, C.x, T->p + T->o_ra[l], C.ra, D,
+                               T->dcur, T->gx2);
         hipLaunchKernelGGL(k_tr_rms_bwd_dw, dim3((D + kDwCols - 1) / kDwCols), dim3(256), 0, s, T->gxn, C.x, C.ra, S, D,
                            acc ? kDwContinue : kDwStore, T->g + T->o_ra[l]);
         // dWo = dx2s^T att (alpha gx2^T att), d[Wq;Wk;Wv] = [dq|dk|dv]^T xn
