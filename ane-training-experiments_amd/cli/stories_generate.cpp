@@ -223,6 +223,8 @@ struct DecodeResult {
     std::vector<int32_t> tokens;
     int prompt_length = 0;
     bool stopped_eos = false;
+    double gpu_ms = 0;   // device time of the forwards
+    double bytes = 0;    // their algorithmic bytes
 };
 
 // (*Decoder).Decode (infer.go:136-202). Greedy runs entirely on the device; a sampled
@@ -232,12 +234,21 @@ DecodeResult decode(sh_model *m, const sh_config &c, const std::vector<int32_t> 
     DecodeResult r;
     if (max_new <= 0) max_new = 64;
     if (temperature < 0) temperature = 0;
+    // device time and algorithmic bytes of every forward (sh_stats after each call)
+    auto account = [&]() {
+        sh_timing t{};
+        if (sh_stats(m, &t) == 0) {
+            r.gpu_ms += t.gpu_ms;
+            r.bytes += t.bytes_per_forward_mean * (double)t.forwards;
+        }
+    };
     if (temperature <= 1e-6f) {
         std::vector<int32_t> out(c.max_seq);
         int32_t n = 0, eos = 0;
         if (sh_greedy_decode(m, prompt_in.data(), (int32_t)prompt_in.size(), max_new, out.data(),
                              &n, &eos))
             fatalf("decode: %s", lib_error());
+        account();
         std::vector<int32_t> p = prompt_in.empty() ? std::vector<int32_t>{1} : prompt_in;
         r.prompt_length = (int)std::min(p.size(), (size_t)c.max_seq);
         r.tokens.assign(out.begin(), out.begin() + n);
@@ -253,14 +264,17 @@ DecodeResult decode(sh_model *m, const sh_config &c, const std::vector<int32_t> 
     if (sh_reset_cache(m)) fatalf("decode: %s", lib_error());
     r.tokens = prompt;
     r.prompt_length = (int)prompt.size();
-    for (size_t pos = 0; pos + 1 < prompt.size(); pos++)
+    for (size_t pos = 0; pos + 1 < prompt.size(); pos++) {
         if (sh_decode_step(m, prompt[pos], (int32_t)pos, nullptr, nullptr))
             fatalf("decode: %s", lib_error());
+        account();
+    }
     std::vector<float> logits(c.vocab);
     for (int step = 0; step < max_new && (int)r.tokens.size() < c.max_seq; step++) {
         const int pos = (int)r.tokens.size() - 1;
         if (sh_decode_step(m, r.tokens[pos], pos, logits.data(), nullptr))
             fatalf("decode: %s", lib_error());
+        account();
         const int next = rng.sample(logits.data(), c.vocab, temperature);
         r.tokens.push_back(next);
         if (next == 2) {
@@ -609,9 +623,14 @@ int main(int argc, char **argv) {
     const double elapsed = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     const int new_tokens = (int)res.tokens.size() - res.prompt_length;
     const double tps = elapsed > 0 ? new_tokens / elapsed : 0.0;
-    printf("source=%s prompt_tokens=%d generated_tokens=%d elapsed=%s tok/s=%.2f eos=%s\n",
+    // main.go:60-67's line, plus the device-side rate: algorithmic bytes of the forwards
+    // (weights, norms, KV rows, logits) over their device time, and its fraction of the
+    // 8 TB/s HBM peak
+    const double hbm_gbps = res.gpu_ms > 0 ? res.bytes / (res.gpu_ms * 1e6) : 0.0;
+    printf("source=%s prompt_tokens=%d generated_tokens=%d elapsed=%s tok/s=%.2f eos=%s "
+           "hbm_gbps=%.1f roofline_frac=%.4f\n",
            source.c_str(), res.prompt_length, new_tokens, go_duration(elapsed).c_str(), tps,
-           res.stopped_eos ? "true" : "false");
+           res.stopped_eos ? "true" : "false", hbm_gbps, hbm_gbps / 8000.0);
     printf("tokens=%s\n", join_ints(res.tokens).c_str());
     if (have_tok) {
         std::string text;

@@ -146,6 +146,18 @@ bool check_persistent_err(sh_model *m) {
     return true;
 }
 
+// After a persistent launch whose bounded waits expired (its workgroups were not all
+// resident, e.g. another process held CUs): models with a per-stage path switch to it for
+// good and the caller repeats the call; W8A8 has no per-stage path and keeps the error.
+bool fall_back_to_graph(sh_model *m) {
+    if (m->dtype == SH_DTYPE_W8A8) return false;
+    m->persistent = false;
+    snprintf(m->path_note, sizeof(m->path_note), "%s",
+             "per-stage kernels in a HIP graph (a persistent decode launch timed out waiting "
+             "for its workgroups to be resident)");
+    return true;
+}
+
 // Enqueues n forwards at positions pos0.. (tokens[pos] feeds each; from n_prompt on the
 // argmax is appended): one persistent launch, or one graph replay per forward.
 bool launch_forwards(sh_model *m, int pos0, int n, int n_prompt) {
@@ -536,6 +548,7 @@ void sh_model_destroy(sh_model *m) {
     (void)hipFree(m->p_err);
     (void)hipFree(m->trace_buf);
     (void)hipFree(m->pf_arena);
+    (void)hipFree(m->tap_buf);
     if (m->bt_ready) (void)hipGraphExecDestroy(m->bt_exec);
     (void)hipFree(m->bt_arena);
     if (m->wd_ready) (void)hipGraphExecDestroy(m->wd_exec);
@@ -646,6 +659,63 @@ int sh_model_upload_globals(sh_model *m, const float *embed, const float *rms_fi
     return 0;
 }
 
+int sh_model_read_weights(const sh_model *m, int32_t layer, const char *name, void *dst, size_t bytes) {
+    if (!m || !name || !dst) {
+        set_error("sh_model_read_weights: bad arguments");
+        return -1;
+    }
+    const sh_config &c = m->cfg;
+    const bool w8 = m->dtype == SH_DTYPE_W8A8;
+    const size_t eb = weight_elem_bytes(m->dtype);
+    std::string n(name);
+    const bool scale = n.size() > 6 && n.compare(n.size() - 6, 6, ".scale") == 0;
+    if (scale) n.resize(n.size() - 6);
+    if (scale && !w8) {
+        set_error("sh_model_read_weights: row scales exist only for W8A8 models");
+        return -1;
+    }
+    // the tensor as rows [r0, r0 + rows) of a matrix whose row r lives at row r*step + r0 of
+    // its storage (w1 and w3 are interleaved in w13)
+    const void *base = nullptr;
+    const float *sbase = nullptr;
+    int rows = 0, cols = 0, r0 = 0, step = 1;
+    size_t elem = eb;
+    if (layer >= 0) {
+        if (layer >= c.n_layers) {
+            set_error("sh_model_read_weights: layer out of range");
+            return -1;
+        }
+        const LayerDev &L = m->layers[layer];
+        if (n == "wq") { base = L.wqkv; sbase = L.s_qkv; rows = m->qdim; cols = c.dim; }
+        else if (n == "wk") { base = L.wqkv; sbase = L.s_qkv; rows = m->kvdim; cols = c.dim; r0 = m->qdim; }
+        else if (n == "wv") { base = L.wqkv; sbase = L.s_qkv; rows = m->kvdim; cols = c.dim; r0 = m->qdim + m->kvdim; }
+        else if (n == "wo") { base = L.wo; sbase = L.s_o; rows = c.dim; cols = m->qdim; }
+        else if (n == "w1") { base = L.w13; sbase = L.s_13; rows = c.hidden; cols = c.dim; step = 2; }
+        else if (n == "w3") { base = L.w13; sbase = L.s_13; rows = c.hidden; cols = c.dim; step = 2; r0 = 1; }
+        else if (n == "w2") { base = L.w2; sbase = L.s_2; rows = c.dim; cols = c.hidden; }
+    } else if (layer == -1) {
+        if (n == "embed" && !scale) {
+            base = m->embed; rows = c.vocab; cols = c.dim; elem = 2;   // the 16-bit lookup table
+        } else if (n == "cls" && (m->cls != m->embed || scale)) {
+            base = m->cls; sbase = m->s_cls; rows = c.vocab; cols = c.dim;
+        }
+    }
+    if (!base) {
+        set_error(std::string("sh_model_read_weights: no tensor ") + name + " at layer " + std::to_string(layer));
+        return -1;
+    }
+    const size_t row_bytes = scale ? 4 : (size_t)cols * elem;
+    if (bytes != row_bytes * rows) {
+        set_error("sh_model_read_weights: " + std::string(name) + " holds " + std::to_string(row_bytes * rows) +
+                  " bytes");
+        return -1;
+    }
+    (void)hipSetDevice(m->device);
+    const uint8_t *src = scale ? (const uint8_t *)sbase : (const uint8_t *)base;
+    return hip_ok(hipMemcpy2D(dst, row_bytes, src + (size_t)r0 * row_bytes, row_bytes * step, row_bytes, rows,
+                              hipMemcpyDeviceToHost), "read weights") ? 0 : -1;
+}
+
 int sh_reset_cache(sh_model *m) {
     if (!m) {
         set_error("sh_reset_cache: nil model");
@@ -674,7 +744,8 @@ int sh_decode_step(sh_model *m, int32_t token, int32_t pos, float *logits, int32
     (void)hipSetDevice(m->device);
     // never append: this call only evaluates
     if (!hip_ok(hipMemcpyAsync(m->tokens + pos, &token, 4, hipMemcpyHostToDevice, m->stream), "token") ||
-        !launch_forwards(m, pos, 1, c.max_seq + 1))
+        !hip_ok(hipEventRecord(m->ev0, m->stream), "event") || !launch_forwards(m, pos, 1, c.max_seq + 1) ||
+        !hip_ok(hipEventRecord(m->ev1, m->stream), "event"))
         return -1;
     if (logits &&
         !hip_ok(hipMemcpyAsync(logits, m->logits, 4 * (size_t)c.vocab, hipMemcpyDeviceToHost, m->stream),
@@ -682,10 +753,22 @@ int sh_decode_step(sh_model *m, int32_t token, int32_t pos, float *logits, int32
         return -1;
     int32_t am = 0;
     if (!hip_ok(hipMemcpyAsync(&am, m->argmax_hist + pos, 4, hipMemcpyDeviceToHost, m->stream), "argmax") ||
-        !hip_ok(hipStreamSynchronize(m->stream), "decode step") ||
-        (m->persistent && !check_persistent_err(m)))
+        !hip_ok(hipStreamSynchronize(m->stream), "decode step"))
         return -1;
+    if (m->persistent && !check_persistent_err(m)) {
+        if (!fall_back_to_graph(m)) return -1;
+        return sh_decode_step(m, token, pos, logits, argmax_out);
+    }
     if (argmax_out) *argmax_out = am;
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, m->ev0, m->ev1);
+    m->last = sh_timing{};
+    m->last.gpu_ms = ms;
+    m->last.forwards = 1;
+    m->last.tokens_out = 0;
+    m->last.bytes_per_forward_mean = forward_bytes(m, pos);
+    m->last.persistent = m->persistent ? 1 : 0;
+    m->last.grid = m->persistent ? m->p_grid : 0;
     return 0;
 }
 
@@ -732,9 +815,12 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
     const int total = n_prompt + generated;
     if (!hip_ok(hipMemcpyAsync(out_tokens, m->tokens, 4 * (size_t)total, hipMemcpyDeviceToHost, m->stream),
                 "copy tokens") ||
-        !hip_ok(hipStreamSynchronize(m->stream), "greedy decode") ||
-        (m->persistent && !check_persistent_err(m)))
+        !hip_ok(hipStreamSynchronize(m->stream), "greedy decode"))
         return -1;
+    if (m->persistent && !check_persistent_err(m)) {
+        if (!fall_back_to_graph(m)) return -1;
+        return sh_greedy_decode(m, prompt, n_prompt, max_new, out_tokens, n_out, stopped_eos);
+    }
     // infer.go:190-193: stop after EOS
     int n = n_prompt;
     int eos = 0;
@@ -1269,6 +1355,40 @@ int sh_layer_forward_cf(sh_model *m, int32_t layer, const float *x_cf, int32_t s
     if (!seam_begin(m, "sh_layer_forward_cf", x_cf, seq, out_cf, false, false)) return -1;
     if (!hip_ok(enqueue_layer_cf(m, layer, seq), "layer forward")) return -1;
     return seam_end(m, m->pf_cf, out_cf, sizeof(float) * (size_t)m->cfg.dim * seq, seq) ? 0 : -1;
+}
+
+int sh_layer_forward_cf_taps(sh_model *m, int32_t layer, const float *x_cf, int32_t seq,
+                             float *out_cf, float *sdpa_cf, float *ffn_cf) {
+    if (m && (layer < 0 || layer >= m->cfg.n_layers)) {
+        set_error("sh_layer_forward_cf_taps: layer out of range");
+        return -1;
+    }
+    if (!seam_begin(m, "sh_layer_forward_cf_taps", x_cf, seq, out_cf, false, false)) return -1;
+    const sh_config &c = m->cfg;
+    const size_t S = (size_t)seq;
+    const size_t n_sdpa = (size_t)(c.dim + 2 * m->qdim + 2 * m->kvdim) * S;
+    const size_t n_ffn = (size_t)(c.dim + 2 * c.hidden) * S;
+    const size_t n_h13 = 2 * (size_t)c.hidden * S;
+    const size_t need = n_sdpa + n_ffn + n_h13;
+    if (m->tap_cap < need) {
+        (void)hipFree(m->tap_buf);
+        m->tap_buf = nullptr;
+        m->tap_cap = 0;
+        if (!hip_ok(hipMalloc(&m->tap_buf, sizeof(float) * need), "tap scratch")) return -1;
+        m->tap_cap = need;
+    }
+    float *d_sdpa = m->tap_buf, *d_ffn = d_sdpa + n_sdpa, *d_h13 = d_ffn + n_ffn;
+    if (!hip_ok(enqueue_layer_cf(m, layer, seq), "layer forward") ||
+        !hip_ok(enqueue_layer_taps_cf(m, layer, seq, sdpa_cf ? d_sdpa : nullptr, ffn_cf ? d_ffn : nullptr,
+                                      d_h13), "layer taps"))
+        return -1;
+    if (sdpa_cf && !hip_ok(hipMemcpyAsync(sdpa_cf, d_sdpa, sizeof(float) * n_sdpa, hipMemcpyDeviceToHost,
+                                          m->stream), "sdpa taps"))
+        return -1;
+    if (ffn_cf && !hip_ok(hipMemcpyAsync(ffn_cf, d_ffn, sizeof(float) * n_ffn, hipMemcpyDeviceToHost,
+                                         m->stream), "ffn taps"))
+        return -1;
+    return seam_end(m, m->pf_cf, out_cf, sizeof(float) * (size_t)c.dim * seq, seq) ? 0 : -1;
 }
 
 int sh_rms_final_cf(sh_model *m, const float *x_cf, int32_t seq, float *out_cf) {

@@ -110,6 +110,8 @@ struct sh_model {
     float *pf_q, *pf_k, *pf_v;                 // roped q, k and v: [S,qdim] [S,kvdim] x2
     float *pf_cf;                              // [D,S] channel-first staging of the seams
     uint16_t *pf_xn, *pf_att, *pf_gate;        // GEMM operands: hi plane, then lo plane
+    float *tap_buf;                            // layer taps: channel-first outputs + [S, 2F]
+    size_t tap_cap;                            // elements of tap_buf
 
     // batched decode (sh_prefill.hip): B sequences stepped together, state on the device
     void *bt_arena;
@@ -177,6 +179,9 @@ hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fi
 // sequence in pf_rowpos / pf_rowseq): one layer (result back in pf_cf), the final RMSNorm
 // (result in pf_cf), the classifier (logits [V, S] in pf_logits).
 hipError_t enqueue_layer_cf(sh_model *m, int l, int S);
+// The intermediates of the layer enqueue_layer_cf just ran, channel-first: sdpa (x2, q_rope,
+// k_rope, v, att) and ffn (x_next, h1, h3), either NULL; h13 is [S, 2F] scratch.
+hipError_t enqueue_layer_taps_cf(sh_model *m, int l, int S, float *sdpa, float *ffn, float *h13);
 hipError_t enqueue_rms_final_cf(sh_model *m, int S);
 hipError_t enqueue_classifier_cf(sh_model *m, int S);
 // Model-free products for the stateless seams: partial elements the split GEMM needs, and

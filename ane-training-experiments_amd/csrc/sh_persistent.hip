@@ -1,5 +1,4 @@
-// sh_persistent.hip — the whole greedy decode loop as one persistent, cooperatively
-// launched kernel for gfx950.
+// sh_persistent.hip — the whole greedy decode loop as one persistent kernel for gfx950.
 //
 // Why: one token forward (ane/stories/infer.go:204-245) is ~5 dependent GEMV-sized stages
 // per layer. Launched as separate kernels, even inside a HIP graph, each stage pays ~1.6 us
@@ -1598,8 +1597,12 @@ hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt
         p.omagic[i] = per > 0 ? (uint32_t)((0x80000000ull + (uint64_t)per - 1) / (uint64_t)per) : 0u;
     }
     m->epoch += (uint32_t)n_forwards * (uint32_t)(c.n_layers + 1);
+    // A plain launch: the kernel needs its workgroups co-resident (persistent_plan keeps the
+    // grid within CUs x resident workgroups per CU) but never synchronises the whole grid, so
+    // the cooperative-launch path is not needed. Should a workgroup not become resident (another
+    // process holding CUs), the bounded waits end the launch with *err set.
     void *args[] = {&p};
-    return hipLaunchCooperativeKernel((const void *)k, dim3(m->p_grid), dim3(kPB), args, 0, m->stream);
+    return hipLaunchKernel((const void *)k, dim3(m->p_grid), dim3(kPB), args, 0, m->stream);
 }
 
 size_t persistent_layer_ptr_bytes(int n_layers) { return sizeof(LayerPtrs) * (size_t)n_layers; }

@@ -129,6 +129,23 @@ __global__ __launch_bounds__(kT) void k_to_planes(const float *x, size_t n, int 
     if (i < n) store_op(out, i, plane, x[i], dt);
 }
 
+// dst [count, S] (channel-first) = columns col0, col0 + cstep, ... of the token-major src
+// [S, ncols]: dst[c*S + t] = src[t*ncols + col0 + c*cstep]. The layer taps' layout change.
+__global__ __launch_bounds__(kT) void k_cf_gather(const float *src, int S, int ncols, int col0,
+                                                  int cstep, int count, float *dst) {
+    const size_t i = (size_t)blockIdx.x * kT + threadIdx.x;
+    if (i >= (size_t)count * S) return;
+    const int c = (int)(i / S), t = (int)(i % S);
+    dst[i] = src[(size_t)t * ncols + col0 + (size_t)c * cstep];
+}
+
+// fp32 value of operand planes: hi + lo (hi at i, lo `plane` further).
+__global__ __launch_bounds__(kT) void k_planes_f32(const uint16_t *in, size_t n, size_t plane, int dt,
+                                                   float *out) {
+    const size_t i = (size_t)blockIdx.x * kT + threadIdx.x;
+    if (i < n) out[i] = bits_to_f(in[i], dt) + bits_to_f(in[plane + i], dt);
+}
+
 enum { G_STORE = 0, G_RESID = 1, G_GATE = 2, G_LOGITS_CF = 3 };
 
 struct GemmArgs {
@@ -2110,6 +2127,54 @@ hipError_t enqueue_layer_cf(sh_model *m, int l, int S) {
     if ((e = launch_transpose(m->pf_cf, D, S, m->pf_x, m->stream)) != hipSuccess) return e;
     if ((e = enqueue_layer(m, l, S, S, false, false, nullptr, 0, nullptr)) != hipSuccess) return e;
     return launch_transpose(m->pf_x, S, D, m->pf_cf, m->stream);
+}
+
+// After enqueue_layer_cf(m, l, S): the layer's intermediates, channel-first, in the output
+// order of the reference's fused programs (ane/mil/stories_dynamic.go:162 and :222):
+// sdpa [D + 2Q + 2KV, S] = (x2, q_rope, k_rope, v, att), ffn [D + 2F, S] = (x_next, h1, h3).
+// The scratch the layer leaves holds them token-major (pf_x2; pf_q, pf_k, pf_v after
+// QK-norm and RoPE; pf_att as the operand planes Wo consumed, hi + lo; pf_x2 = x, and pf_xn
+// the W1|W3 operand planes); h1 and h3, which the layer only uses inside the SiLU-gate
+// epilogue, come from the same W1|W3 product stored plainly into h13 [S, 2F] (interleaved
+// rows: column 2r is h1[r], 2r+1 is h3[r]). ffn's x_next is the layer output in pf_cf.
+hipError_t enqueue_layer_taps_cf(sh_model *m, int l, int S, float *sdpa, float *ffn, float *h13) {
+    const sh_config &c = m->cfg;
+    const int D = c.dim, F = c.hidden, Q = m->qdim, KV = m->kvdim;
+    hipStream_t s = m->stream;
+    hipError_t e;
+    auto gather = [&](const float *src, int ncols, int col0, int cstep, int count, float *dst) {
+        const size_t n = (size_t)count * S;
+        hipLaunchKernelGGL(k_cf_gather, dim3((unsigned)((n + kT - 1) / kT)), dim3(kT), 0, s, src, S,
+                           ncols, col0, cstep, count, dst);
+        return hipGetLastError();
+    };
+    if (sdpa) {
+        float *o = sdpa;
+        if ((e = gather(m->pf_x2, D, 0, 1, D, o)) != hipSuccess) return e;
+        o += (size_t)D * S;
+        if ((e = gather(m->pf_q, Q, 0, 1, Q, o)) != hipSuccess) return e;
+        o += (size_t)Q * S;
+        if ((e = gather(m->pf_k, KV, 0, 1, KV, o)) != hipSuccess) return e;
+        o += (size_t)KV * S;
+        if ((e = gather(m->pf_v, KV, 0, 1, KV, o)) != hipSuccess) return e;
+        o += (size_t)KV * S;
+        const size_t n = (size_t)S * Q;   // pf_qkv ([S, qkv_rows] >= [S, Q]) is free now
+        hipLaunchKernelGGL(k_planes_f32, dim3((unsigned)((n + kT - 1) / kT)), dim3(kT), 0, s,
+                           m->pf_att, n, n, m->dtype, m->pf_qkv);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if ((e = gather(m->pf_qkv, Q, 0, 1, Q, o)) != hipSuccess) return e;
+    }
+    if (ffn) {
+        GemmArgs g{};
+        g.A = m->pf_xn; g.B = (const uint16_t *)m->layers[l].w13; g.M = S; g.N = 2 * F; g.K = D;
+        g.epi = G_STORE; g.out = h13; g.dt = m->dtype;
+        if ((e = gemm(g, m->dtype, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
+        if ((e = hipMemcpyAsync(ffn, m->pf_cf, sizeof(float) * D * S, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+            return e;
+        if ((e = gather(h13, 2 * F, 0, 2, F, ffn + (size_t)D * S)) != hipSuccess) return e;
+        if ((e = gather(h13, 2 * F, 1, 2, F, ffn + (size_t)(D + F) * S)) != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t enqueue_rms_final_cf(sh_model *m, int S) {

@@ -116,6 +116,8 @@ SIGNATURES = {
     "sh_synth_tokens": (C.c_int, [_I32, C.c_size_t, C.c_uint64, C.c_int32]),
     "sh_round_dtype": (C.c_int, [_F, C.c_size_t, C.c_int32]),
     "sh_layer_forward_cf": (C.c_int, [C.c_void_p, C.c_int32, _F, C.c_int32, _F]),
+    "sh_model_read_weights": (C.c_int, [C.c_void_p, C.c_int32, C.c_char_p, C.c_void_p, C.c_size_t]),
+    "sh_layer_forward_cf_taps": (C.c_int, [C.c_void_p, C.c_int32, _F, C.c_int32, _F, _F, _F]),
     "sh_rms_final_cf": (C.c_int, [C.c_void_p, _F, C.c_int32, _F]),
     "sh_classifier_cf": (C.c_int, [C.c_void_p, _F, C.c_int32, _F]),
     "sh_matmul_vocab_seq": (C.c_int, [_F, _F, C.c_int32, C.c_int32, C.c_int32, _F]),
@@ -341,12 +343,44 @@ class Model:
                "sh_prefill_logits")
         return out
 
+    def read_weights(self, layer: int, name: str) -> np.ndarray:
+        """sh_model_read_weights: a tensor as stored on the device: uint16 bits (fp16 / bf16),
+        int8 rows (W8A8) or, for "<name>.scale", float32 row scales."""
+        c = self.cfg
+        shapes = {"wq": (c.qdim, c.dim), "wk": (c.kvdim, c.dim), "wv": (c.kvdim, c.dim),
+                  "wo": (c.dim, c.qdim), "w1": (c.hidden, c.dim), "w3": (c.hidden, c.dim),
+                  "w2": (c.dim, c.hidden), "embed": (c.vocab, c.dim), "cls": (c.vocab, c.dim)}
+        base = name[:-6] if name.endswith(".scale") else name
+        rows, cols = shapes[base]
+        if name.endswith(".scale"):
+            out = np.empty(rows, np.float32)
+        elif self.dtype == SH_DTYPE_W8A8 and base != "embed":
+            out = np.empty((rows, cols), np.int8)
+        else:
+            out = np.empty((rows, cols), np.uint16)
+        _check(self.lib.sh_model_read_weights(self.h, layer, name.encode(), out.ctypes.data_as(C.c_void_p),
+                                              out.nbytes), "sh_model_read_weights")
+        return out
+
     def layer_forward_cf(self, layer: int, x_cf: np.ndarray) -> np.ndarray:
         """One layer over channel-first [dim, seq] (the storiesane layerForward.run seam)."""
         x = np.ascontiguousarray(x_cf, np.float32)
         out = np.empty_like(x)
         _check(self.lib.sh_layer_forward_cf(self.h, layer, _fp(x), x.shape[1], _fp(out)), "sh_layer_forward_cf")
         return out
+
+    def layer_forward_cf_taps(self, layer: int, x_cf: np.ndarray):
+        """sh_layer_forward_cf_taps: (out, sdpa, ffn) channel-first, sdpa = concat(x2, q_rope,
+        k_rope, v, att) and ffn = concat(x_next, h1, h3) (stories_dynamic.go:162, :222)."""
+        x = np.ascontiguousarray(x_cf, np.float32)
+        S = x.shape[1]
+        c = self.cfg
+        out = np.empty_like(x)
+        sdpa = np.empty((c.dim + 2 * c.qdim + 2 * c.kvdim, S), np.float32)
+        ffn = np.empty((c.dim + 2 * c.hidden, S), np.float32)
+        _check(self.lib.sh_layer_forward_cf_taps(self.h, layer, _fp(x), S, _fp(out), _fp(sdpa), _fp(ffn)),
+               "sh_layer_forward_cf_taps")
+        return out, sdpa, ffn
 
     def rms_final_cf(self, x_cf: np.ndarray) -> np.ndarray:
         """The final RMSNorm over channel-first [dim, seq] (offload.runRMSForward)."""

@@ -83,13 +83,7 @@ def run_cli(args):
         if line.startswith("{"):
             result = json.loads(line)
     if p.returncode != 0:
-        # rocprofv3 can end a program that launched a cooperative kernel with SIGSEGV in its
-        # own teardown, after the program printed its result; only then is the result kept.
-        profiled = any(k.startswith("ROCPROF") for k in os.environ)
-        if not (profiled and result is not None and p.returncode == -11):
-            raise SystemExit(f"stories-generate failed (exit {p.returncode})")
-        print("note: stories-generate ended with signal 11 after printing its result "
-              "(profiler teardown)", file=sys.stderr)
+        raise SystemExit(f"stories-generate failed (exit {p.returncode})")
     if result is None:
         raise SystemExit("stories-generate printed no result")
     return result
@@ -127,6 +121,27 @@ def cpu_baseline(gpu_tokens):
                   f"{dt:.2f} s",
         "tokens_match_gpu": toks.tolist() == gpu_tokens,
     }
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), reported beside the CPU baseline."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def with_host(line):
+    """Adds the host description to a line's cpu_baseline: CPU model and logical cores."""
+    cb = line.get("cpu_baseline")
+    if isinstance(cb, dict):
+        cb["cpu_model"] = cpu_model()
+        cb["host_logical_cores"] = os.cpu_count()
+    return line
 
 
 def host_threads():
@@ -397,7 +412,7 @@ def main() -> int:
     if args.workload != "decode":
         fn = {"prefill": workload_prefill, "w8a8": workload_w8a8, "qwen-decode": workload_qwen_decode,
               "batch": workload_batch, "train": workload_train}[args.workload]
-        print(json.dumps(fn(args)))
+        print(json.dumps(with_host(fn(args))))
         return 0
 
     r = gpu_leg(args.steps, args.warmup)
@@ -448,7 +463,7 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(r["tokens"])
-    print(json.dumps(line))
+    print(json.dumps(with_host(line)))
     return 0
 
 

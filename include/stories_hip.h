@@ -95,6 +95,13 @@ int sh_model_upload_layer(sh_model *m, int32_t layer, const float *wq, const flo
  * cfg.tied_embed (the Embed rows are the classifier, infer.go:243). */
 int sh_model_upload_globals(sh_model *m, const float *embed, const float *rms_final,
                             const float *cls);
+/* A tensor as the device stores it, for checking the upload's conversion (the reference
+ * converts weights to fp16 blobs on the host, ane/mil/generator.go:151-219; here the device
+ * rounds): layer >= 0 with name wq wk wv wo w1 w2 w3, or layer -1 with "embed" (the 16-bit
+ * lookup table) or "cls" (classifier rows when untied or W8A8). dst receives the raw rows:
+ * fp16 / bf16 bits (2 bytes each) or int8 (W8A8); "<name>.scale" gives a W8A8 tensor's fp32
+ * row scales. bytes must equal the tensor's size. No reference counterpart. */
+int sh_model_read_weights(const sh_model *m, int32_t layer, const char *name, void *dst, size_t bytes);
 /* (*Decoder).ResetCache (infer.go:61-70). */
 int sh_reset_cache(sh_model *m);
 /* (*Decoder).EvalNextLogits (infer.go:72-77) = forwardOne (infer.go:204-245): one token
@@ -125,6 +132,17 @@ int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *l
  * the counterpart of one compiled layerForward. */
 int sh_layer_forward_cf(sh_model *m, int32_t layer, const float *x_cf, int32_t seq,
                         float *out_cf);
+/* sh_layer_forward_cf plus the layer's intermediates, as the reference's fused ANE layer
+ * programs return them (GenStoriesSDPAForwardDynamicTaps, ane/mil/stories_dynamic.go:71-165,
+ * output concat at :162; GenStoriesFFNForwardDynamicTaps, :176-225, concat at :222), all
+ * channel-first [rows, seq] fp32:
+ *   sdpa_cf [dim + 2*H*hd + 2*KVH*hd, seq] = x2 (x + a*Wo.att), q after QK-norm and RoPE,
+ *           k after QK-norm and RoPE, v, att (the attention output Wo consumes);
+ *   ffn_cf  [dim + 2*hidden, seq] = x_next (= out_cf), h1 = W1.n, h3 = W3.n with n the
+ *           RMSNorm of x2.
+ * Either may be NULL. The layer's own output is the same as sh_layer_forward_cf's. */
+int sh_layer_forward_cf_taps(sh_model *m, int32_t layer, const float *x_cf, int32_t seq,
+                             float *out_cf, float *sdpa_cf, float *ffn_cf);
 /* offload.runRMSForward (offload_other.go:22-24; offload_darwin.go:345-356): the final
  * RMSNorm with the model's rms_final over x_cf [dim, seq] (stories.RMSNorm numerics,
  * cpu.go:97-111) into out_cf [dim, seq]. out_cf may equal x_cf. */
@@ -194,7 +212,8 @@ int sh_trace_read(sh_model *m, int64_t *out, int32_t cap, int32_t *n_out, double
  * residual after attention (D). n must equal that length. */
 enum { SH_TAP_X = 0, SH_TAP_QKV = 1, SH_TAP_ATT = 4, SH_TAP_GATE = 5, SH_TAP_X2 = 6 };
 int sh_decode_tap(const sh_model *m, int32_t which, float *out, int32_t n);
-/* Timing of the last sh_greedy_decode / sh_prefill_logits call. */
+/* Timing of the last sh_greedy_decode / sh_decode_step / sh_prefill_logits / batched or
+ * window decode / channel-first seam call. */
 int sh_stats(const sh_model *m, sh_timing *out);
 /* (*Engine).Close (engine.go:480): frees device memory. NULL is allowed. */
 void sh_model_destroy(sh_model *m);

@@ -238,6 +238,7 @@ struct or_decoder {
     float *kc, *vc;           /* [L][max_seq][kvdim] */
     float *rcos, *rsin;       /* [max_seq][hd/2] */
     float *x, *xn, *q, *k, *v, *att, *x2, *x2n, *h1, *h3, *ff, *scores, *probs, *logits;
+    float *qpre, *kpre;       /* q and k of the last layer before QK-norm and RoPE (taps) */
     /* W8A8 */
     int8_t *q8[64][P_N];
     float *s8[64][P_N];
@@ -295,6 +296,8 @@ or_decoder *or_decoder_new(const or_config *cfg, const or_weights *w, int thread
     d->q = (float *)calloc(d->qdim, sizeof(float));
     d->k = (float *)calloc(d->kvdim, sizeof(float));
     d->v = (float *)calloc(d->kvdim, sizeof(float));
+    d->qpre = (float *)calloc(d->qdim, sizeof(float));
+    d->kpre = (float *)calloc(d->kvdim, sizeof(float));
     d->att = (float *)calloc(big, sizeof(float));
     d->x2 = (float *)calloc(cfg->dim, sizeof(float));
     d->x2n = (float *)calloc(cfg->dim, sizeof(float));
@@ -331,6 +334,7 @@ void or_decoder_free(or_decoder *d) {
     }
     free(d->layers); free(d->kc); free(d->vc); free(d->rcos); free(d->rsin);
     free(d->x); free(d->xn); free(d->q); free(d->k); free(d->v); free(d->att);
+    free(d->qpre); free(d->kpre);
     free(d->x2); free(d->x2n); free(d->h1); free(d->h3); free(d->ff);
     free(d->scores); free(d->probs); free(d->logits);
     free(d);
@@ -408,6 +412,8 @@ int or_forward_one(or_decoder *d, int token, int pos, float *logits_out) {
         project(d, l, P_WQ, d->q, d->xn);
         project(d, l, P_WK, d->k, d->xn);
         project(d, l, P_WV, d->v, d->xn);
+        memcpy(d->qpre, d->q, sizeof(float) * d->qdim);
+        memcpy(d->kpre, d->k, sizeof(float) * d->kvdim);
         if (c->qk_norm) {
             for (int h = 0; h < c->n_heads; h++)
                 or_rms_norm_vec(d->q + h * hd, d->q + h * hd, L->q_norm, hd, c->qk_norm_eps);
@@ -450,6 +456,8 @@ const float *or_decoder_tap(const or_decoder *d, int which) {
     case 4: return d->att;
     case 5: return d->h1;
     case 6: return d->x2;
+    case 7: return d->qpre;
+    case 8: return d->kpre;
     default: return d->logits;
     }
 }
@@ -674,6 +682,15 @@ static void matmul_vocab_seq(float *logits, const float *embed, const float *x, 
  * positions 0..S-1. out_cf may not alias x_cf. */
 void or_layer_forward_cf(const or_config *cfg, const or_layer *L, const float *x_cf, int seq,
                          float *out_cf, int threads) {
+    or_layer_forward_cf_taps(cfg, L, x_cf, seq, out_cf, NULL, NULL, threads);
+}
+
+/* The layer above, also copying its intermediates out channel-first, in the output order of
+ * the reference's fused ANE programs: sdpa_taps = concat(x2, q_rope, k_rope, v, att_out)
+ * (GenStoriesSDPAForwardDynamicTaps, ane/mil/stories_dynamic.go:162), ffn_taps =
+ * concat(x_next, h1, h3) (GenStoriesFFNForwardDynamicTaps, :222). Either may be NULL. */
+void or_layer_forward_cf_taps(const or_config *cfg, const or_layer *L, const float *x_cf, int seq,
+                              float *out_cf, float *sdpa_taps, float *ffn_taps, int threads) {
     int D = cfg->dim, F = cfg->hidden, H = cfg->n_heads, KVH = cfg->n_kv_heads;
     int hd = cfg->head_dim, qd = H * hd, kvd = KVH * hd;
     size_t S = (size_t)seq;
@@ -713,6 +730,19 @@ void or_layer_forward_cf(const or_config *cfg, const or_layer *L, const float *x
     }
     linear_cf(ff, L->w2, gate, D, F, seq, threads);
     for (size_t i = 0; i < D * S; i++) out_cf[i] = x2[i] + alpha * ff[i];
+    if (sdpa_taps) {
+        float *t = sdpa_taps;
+        memcpy(t, x2, sizeof(float) * D * S); t += D * S;
+        memcpy(t, qf, sizeof(float) * qd * S); t += qd * S;
+        memcpy(t, kf, sizeof(float) * kvd * S); t += kvd * S;
+        memcpy(t, vf, sizeof(float) * kvd * S); t += kvd * S;
+        memcpy(t, att, sizeof(float) * qd * S);
+    }
+    if (ffn_taps) {
+        memcpy(ffn_taps, out_cf, sizeof(float) * D * S);
+        memcpy(ffn_taps + D * S, h1, sizeof(float) * F * S);
+        memcpy(ffn_taps + (D + (size_t)F) * S, h3, sizeof(float) * F * S);
+    }
     free(xn); free(qf); free(kf); free(vf); free(att); free(x2);
     free(h1); free(h3); free(gate); free(ff); free(rc); free(rs);
 }

@@ -81,7 +81,8 @@ int or_greedy_decode(or_decoder *d, const int32_t *prompt, int n_prompt, int max
                      int32_t *out_tokens, int32_t *n_out, int32_t *stopped_eos,
                      float *margins);
 /* Debug taps of the last forward_one (last layer): 0 x (residual out), 1 q and 2 k (after
- * QK-norm and RoPE), 3 v, 4 att, 5 gate, 6 x2 (residual after attention). */
+ * QK-norm and RoPE), 3 v, 4 att, 5 gate, 6 x2 (residual after attention), 7 q and 8 k as
+ * projected (before QK-norm and RoPE). */
 const float *or_decoder_tap(const or_decoder *d, int which);
 
 /* ---- full-sequence channel-first forward (ane/storiesane/engine.go:804-842) ---- */
@@ -92,6 +93,11 @@ void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t
 /* One layer of the channel-first forward (engine.go:815-838), x_cf [D,S] -> out_cf [D,S]. */
 void or_layer_forward_cf(const or_config *cfg, const or_layer *L, const float *x_cf, int seq,
                          float *out_cf, int threads);
+/* The same layer with its intermediates, channel-first: sdpa_taps [D + 2*H*hd + 2*KVH*hd, S] =
+ * concat(x2, q_rope, k_rope, v, att) (stories_dynamic.go:162), ffn_taps [D + 2F, S] =
+ * concat(x_next, h1, h3) (stories_dynamic.go:222). Either may be NULL. */
+void or_layer_forward_cf_taps(const or_config *cfg, const or_layer *L, const float *x_cf, int seq,
+                              float *out_cf, float *sdpa_taps, float *ffn_taps, int threads);
 /* cpu.go:97-111 RMSNorm (final form) over channel-first [dim, seq]. */
 void or_rms_norm_final_cf(float *out, const float *x, const float *w, int dim, int seq,
                           double eps);

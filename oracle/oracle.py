@@ -91,6 +91,8 @@ def load() -> C.CDLL:
                                      C.c_int, _F, C.c_int]),
         "or_fill_decode_window": (None, [C.POINTER(C.c_uint16), C.c_int, _I32, C.c_int]),
         "or_layer_forward_cf": (None, [C.POINTER(OrConfig), C.POINTER(OrLayer), _F, C.c_int, _F, C.c_int]),
+        "or_layer_forward_cf_taps": (None, [C.POINTER(OrConfig), C.POINTER(OrLayer), _F, C.c_int, _F, _F, _F,
+                                            C.c_int]),
         "or_rms_norm_final_cf": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_double]),
         "or_matmul_vocab_seq": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_int, C.c_int]),
         "or_linear_cf": (None, [_F, _F, _F, C.c_int, C.c_int, C.c_int, C.c_int]),
@@ -229,6 +231,22 @@ def layer_forward_cf(cfg: OrConfig, weights, layer: int, x_cf: np.ndarray, threa
     load().or_layer_forward_cf(C.byref(cfg), C.byref(holder.layers[layer]), fp(x), x.shape[1], fp(out),
                                threads)
     return out
+
+
+def layer_forward_cf_taps(cfg: OrConfig, weights, layer: int, x_cf: np.ndarray, threads: int = 1):
+    """or_layer_forward_cf_taps: the layer's output and its intermediates, channel-first:
+    sdpa = concat(x2, q_rope, k_rope, v, att) (stories_dynamic.go:162) and
+    ffn = concat(x_next, h1, h3) (stories_dynamic.go:222)."""
+    x = np.ascontiguousarray(x_cf, np.float32)
+    S = x.shape[1]
+    holder = _WeightsHolder(weights, cfg.n_layers)
+    qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    out = np.empty_like(x)
+    sdpa = np.empty((cfg.dim + 2 * qd + 2 * kvd, S), np.float32)
+    ffn = np.empty((cfg.dim + 2 * cfg.hidden, S), np.float32)
+    load().or_layer_forward_cf_taps(C.byref(cfg), C.byref(holder.layers[layer]), fp(x), S, fp(out),
+                                    fp(sdpa), fp(ffn), threads)
+    return out, sdpa, ffn
 
 
 def rms_norm_final_cf(x_cf: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:

@@ -23,12 +23,3 @@ def gpu():
 
     sh.init(0)
     return sh
-
-
-def pytest_collection_modifyitems(session, config, items):
-    """Runs the stories-generate child-process tests first. The persistent decode kernel is a
-    cooperative launch, and the HIP runtime refuses one ("the operation cannot be performed
-    in the present state") while another process that has made cooperative launches on the
-    device is still alive, so the CLI children must finish before this process launches its
-    own. The order is otherwise kept."""
-    items.sort(key=lambda it: 0 if os.path.basename(str(it.fspath)) == "test_cli.py" else 1)

@@ -81,6 +81,35 @@ def torch_forward_f64(cfg, w, tokens, alpha=None):
     return (xn @ cls.T).numpy()
 
 
+def oracle_stream(ref, prompt, max_new, max_seq):
+    """The oracle's greedy Decode (infer.go:136-202 at temperature 0) restated through its
+    forwardOne so that every forward's logits are kept: prompt forwards at positions
+    0..n-2, then one forward per generated token, first maximum as the next id (argmax,
+    infer.go:373-383), stop after EOS=2 or at max_seq tokens. Returns (ids, eos, logits
+    [forwards, V]). The prompt must be non-empty and at most max_seq ids long."""
+    ref.reset()
+    ids = [int(t) for t in prompt]
+    assert 0 < len(ids) <= max_seq
+    logits = [ref.forward_one(ids[p], p) for p in range(len(ids) - 1)]
+    eos = False
+    for _ in range(max_new):
+        if len(ids) >= max_seq:
+            break
+        lg = ref.forward_one(ids[-1], len(ids) - 1)
+        logits.append(lg)
+        ids.append(int(np.argmax(lg)))
+        if ids[-1] == 2:
+            eos = True
+            break
+    return np.asarray(ids), eos, np.stack(logits)
+
+
+def top2_margins(logits):
+    """Top-1 minus top-2 logit of each row."""
+    part = np.partition(logits, -2, axis=1)
+    return part[:, -1] - part[:, -2]
+
+
 def deepnet_alpha(n_layers):
     """ane/storiesane/residual.go:9: 1/sqrt(2*NLayers), as float32."""
     return float(np.float32(1.0 / math.sqrt(2.0 * n_layers)))

@@ -179,6 +179,9 @@ def test_cli_greedy_decode_of_llama2_file_matches_oracle(tmp_path):
     want, eos, _ = ref.greedy_decode([5, 9, 11], 40)
     assert got == want.tolist()
     assert f"generated_tokens={len(got) - 3} " in lines[0] and f"eos={'true' if eos else 'false'}" in lines[0]
+    # the device-side rate fields follow main.go:60-67's line
+    fields = dict(kv.split("=", 1) for kv in lines[0].split())
+    assert float(fields["hbm_gbps"]) > 0 and 0 < float(fields["roofline_frac"]) < 1
 
 
 @pytest.mark.gpu
@@ -242,3 +245,27 @@ def test_cli_decode_from_blzt_checkpoint(tmp_path):
     a = run("-ckpt", ck, *args).stdout.splitlines()
     b = run("-model", mb, *args).stdout.splitlines()
     assert a[0].startswith("source=checkpoint") and a[1] == b[1]
+
+
+@pytest.mark.gpu
+def test_cli_child_while_this_process_holds_a_persistent_model(gpu, tmp_path):
+    """Two processes on one GPU: this process decodes with the persistent kernel, the child
+    program then runs its own persistent decode, and this process decodes again. Both must
+    run the persistent kernel and agree with the oracle (the kernel is a plain launch, so
+    one process's launches do not block another's)."""
+    cfg = gqa_file_config()
+    w = sh.synth_weights(cfg, seed=341, std=0.08)
+    m = sh.Model(cfg, sh.SH_DTYPE_F16)
+    m.upload(w)
+    ref = oracle.Decoder(oracle.config_from(cfg), w.rounded(sh.SH_DTYPE_F16), threads=4)
+    want, _, _ = ref.greedy_decode([5, 9, 11], 30)
+    got, _, _ = m.greedy_decode([5, 9, 11], 30)
+    assert got.tolist() == want.tolist() and m.stats()["persistent"]
+    path = tmp_path / "m.bin"
+    write_llama2_bin(path, cfg, w)
+    p = run("-model", path, "-prompt-ids", "5,9,11", "-max-new", "30", "-temperature", "0",
+            "-seq", "64")
+    assert [int(t) for t in p.stdout.splitlines()[1].split("=", 1)[1].split(",")] == want.tolist()
+    got, _, _ = m.greedy_decode([5, 9, 11], 30)
+    assert got.tolist() == want.tolist() and m.stats()["persistent"]
+    m.close()

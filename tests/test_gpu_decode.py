@@ -10,7 +10,7 @@ import pytest
 
 import oracle
 import stories_hip as sh
-from helpers import random_gains, tiny_config, tiny_gqa_config
+from helpers import oracle_stream, random_gains, tiny_config, tiny_gqa_config, top2_margins
 
 pytestmark = pytest.mark.gpu
 
@@ -163,15 +163,36 @@ def test_quantize_bit_exact(gpu):
 
 # ---- full-size configurations --------------------------------------------------------------
 
+def check_stream(m, ids, want_logits, tol=LOGIT_TOL, exact=False):
+    """Replays the token stream through sh_decode_step (one forward per position, cache
+    reset first) and checks every forward's logits against the oracle's at that position:
+    max-abs within tol (or bit-identical when exact) and the same first-max argmax."""
+    m.reset_cache()
+    worst = 0.0
+    for pos in range(len(ids) - 1):
+        got, am = m.eval_next_logits(int(ids[pos]), pos)
+        want = want_logits[pos]
+        if exact:
+            assert np.array_equal(got, want), f"pos {pos}: max-abs {np.max(np.abs(got - want))}"
+        err = float(np.max(np.abs(got - want)))
+        worst = max(worst, err)
+        assert err <= tol, f"pos {pos}: max-abs {err}"
+        assert am == int(np.argmax(got)) == int(np.argmax(want)), f"pos {pos}"
+    print(f"max-abs logits error over all {len(ids) - 1} forwards: {worst:.3e}")
+    return worst
+
+
 def test_stories110m_fp16_greedy_128(gpu):
     """Stories110M fp16 greedy decode: seed-0 N(0, 0.02) weights, 16-id prompt from seed 1,
-    128 new tokens; token stream identical to the oracle's, logits within 2e-2."""
+    128 new tokens; token stream identical to the oracle's, and the logits of every one of
+    the 143 forwards within max-abs 2e-2 of the oracle's."""
     cfg = sh.stories110m_config()
     m, ref, _ = build(cfg, sh.SH_DTYPE_F16, seed=0)
     prompt = sh.synth_tokens(16, 1, cfg.vocab)
     got, plen, eos = m.greedy_decode(prompt, 128)
-    want, weos, margins = ref.greedy_decode(prompt, 128)
-    print(f"generated {len(got) - plen} tokens; smallest top-2 margin {np.nanmin(margins):.3e}")
+    want, weos, want_logits = oracle_stream(ref, prompt, 128, cfg.max_seq)
+    margins = top2_margins(want_logits[plen - 1:])
+    print(f"generated {len(got) - plen} tokens; smallest top-2 margin {margins.min():.3e}")
     assert got.tolist() == want.tolist() and eos == weos
     assert len(got) == 16 + 128 or eos
     st = m.stats()
@@ -180,29 +201,75 @@ def test_stories110m_fp16_greedy_128(gpu):
     # a second decode reuses the model (epochs advance, cache is cleared)
     again, _, _ = m.greedy_decode(prompt, 128)
     assert again.tolist() == got.tolist()
-    # logits along the same stream
-    m.reset_cache()
-    ref.reset()
-    check_steps(m, ref, got[:40])
-    st = m.stats()
-    assert st["forwards"] == 0 or st["gpu_ms"] > 0
+    check_stream(m, got, want_logits)
     m.close()
 
 
 def test_qwen3_shaped_bf16_greedy(gpu):
     """Qwen3-0.6B-shaped bf16 decode (GQA 16/8, hd 128, QK-norm, theta 1e6, tied, bf16 KV):
-    seed-3 weights, 32-id prompt from seed 3, 256 new tokens, identical to the oracle."""
+    seed-3 weights, 32-id prompt from seed 3, 256 new tokens identical to the oracle's, and
+    the logits of all 287 forwards within max-abs 2e-2."""
     cfg = sh.qwen3_06b_config()
     m, ref, _ = build(cfg, sh.SH_DTYPE_BF16, seed=3)
     prompt = sh.synth_tokens(32, 3, cfg.vocab)
     got, plen, eos = m.greedy_decode(prompt, 256)
-    want, weos, margins = ref.greedy_decode(prompt, 256)
-    print(f"generated {len(got) - plen} tokens; smallest top-2 margin {np.nanmin(margins):.3e}")
+    want, weos, want_logits = oracle_stream(ref, prompt, 256, cfg.max_seq)
+    margins = top2_margins(want_logits[plen - 1:])
+    print(f"generated {len(got) - plen} tokens; smallest top-2 margin {margins.min():.3e}")
     assert got.tolist() == want.tolist() and eos == weos
     st = m.stats()
     print(f"persistent={st['persistent']} grid={st['grid']} {st['gpu_ms']:.3f} ms for {st['forwards']} forwards")
     assert st["persistent"]
-    m.reset_cache()
-    ref.reset()
-    check_steps(m, ref, got[:8])
+    check_stream(m, got, want_logits)
+    m.close()
+
+
+SPECIAL = np.array([
+    1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, -(1.0 + 2.0 ** -11),   # fp16 ties: to even
+    1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8,                            # bf16 ties: to even
+    1.5 * 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 0.75 * 2.0 ** -14,  # fp16 subnormals, ties
+    65504.0, 65519.0, 65520.0, -70000.0, 0.0, -0.0, 1e-30, 3.0e38,   # range edges
+], np.float64).astype(np.float32)
+
+
+@pytest.mark.parametrize("dtype", [sh.SH_DTYPE_F16, sh.SH_DTYPE_BF16, sh.SH_DTYPE_W8A8])
+def test_device_weight_rounding_is_bit_exact(gpu, dtype):
+    """The device's conversion of uploaded fp32 weights, read back as stored: fp16 and bf16
+    bits equal round-to-nearest-even (numpy's float16 conversion; the host helper
+    sh_round_dtype for bf16), including ties, subnormals and overflow to infinity; W8A8 int8
+    rows and row scales equal the oracle's bridge quantizer (ane_bridge.m:374-399) bit for
+    bit. The reference's generic Go converter rounds halves up on magnitude
+    (generator.go:151-219); the device follows its darwin path's hardware RNE
+    (fp16_pack_darwin.go:11-35)."""
+    cfg = tiny_config(tied_embed=0)
+    w = sh.synth_weights(cfg, seed=171, std=0.05)
+    lw = w.layers[1]
+    lw["wq"][3, :SPECIAL.size] = SPECIAL
+    lw["w3"][5, -SPECIAL.size:] = SPECIAL
+    lw["w2"][7] = 0.0
+    m = sh.Model(cfg, dtype)
+    m.upload(w)
+    for name in ("wq", "wk", "wv", "wo", "w1", "w2", "w3"):
+        src = np.ascontiguousarray(lw[name], np.float32)
+        got = m.read_weights(1, name)
+        if dtype == sh.SH_DTYPE_F16:
+            with np.errstate(over="ignore"):
+                np.testing.assert_array_equal(got, src.astype(np.float16).view(np.uint16), err_msg=name)
+        elif dtype == sh.SH_DTYPE_BF16:
+            want = sh.round_dtype(src, sh.SH_DTYPE_BF16)
+            assert np.array_equal(got.astype(np.uint32) << 16, want.view(np.uint32)), name
+        else:
+            q, sc = oracle.quantize_rows(src)
+            np.testing.assert_array_equal(got, q, err_msg=name)
+            np.testing.assert_array_equal(m.read_weights(1, name + ".scale").view(np.uint32), sc.view(np.uint32))
+    # the embedding lookup table is 16-bit in every dtype (bf16 for BF16, else fp16)
+    emb = m.read_weights(-1, "embed")
+    e32 = np.ascontiguousarray(w.embed, np.float32)
+    if dtype == sh.SH_DTYPE_BF16:
+        want = sh.round_dtype(e32, sh.SH_DTYPE_BF16)
+        assert np.array_equal(emb.astype(np.uint32) << 16, want.view(np.uint32))
+    else:
+        np.testing.assert_array_equal(emb, e32.astype(np.float16).view(np.uint16))
+    with pytest.raises(sh.ShError):
+        m.read_weights(cfg.n_layers, "wq")
     m.close()

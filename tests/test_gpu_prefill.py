@@ -96,12 +96,13 @@ def test_prefill_columns_match_kv_cache_decode(gpu):
 
 
 def test_prefill_stories110m_s256(gpu):
-    """Stories110M fp16, alpha = 1/sqrt(24) (the storiesane engine's residual scale),
-    256 tokens from seed 5: logits [32000, 256] within 2e-2 of the oracle."""
+    """Stories110M fp16, alpha = 1/sqrt(24) (the storiesane engine's residual scale), the
+    prefill configuration's input: 256 token ids uniform in [0, 32000) from seed 2; logits
+    [32000, 256] within 2e-2 of the oracle."""
     cfg = sh.stories110m_config()
     cfg.residual_scale = 1.0 / math.sqrt(2.0 * cfg.n_layers)
     m, ocfg, ow = build(cfg, sh.SH_DTYPE_F16, seed=0)
-    toks = sh.synth_tokens(256, 5, cfg.vocab)
+    toks = sh.synth_tokens(256, 2, cfg.vocab)
     got, want, _ = compare(m, ocfg, ow, toks)
     # greedy choice per position agrees wherever the oracle's top-2 margin is clear
     top2 = np.sort(want, axis=0)[-2:]

@@ -56,6 +56,42 @@ def test_layer_forward_cf_matches_oracle(gpu, make_cfg, dtype, seq):
     m.close()
 
 
+@pytest.mark.parametrize("make_cfg,dtype,seq", [
+    (lambda: tiny_config(residual_scale=0.5), sh.SH_DTYPE_F16, 24),
+    (lambda: tiny_gqa_config(kv_dtype=sh.SH_KV_F32), sh.SH_DTYPE_BF16, 40),
+    (lambda: sh.stories110m_config(), sh.SH_DTYPE_F16, 64),
+])
+def test_layer_taps_match_oracle(gpu, make_cfg, dtype, seq):
+    """The layer's intermediates as the reference's fused layer programs return them
+    (ane/mil/stories_dynamic.go:162: x2, q_rope, k_rope, v, att; :222: x_next, h1, h3), each
+    block against the oracle's channel-first restatement of the same layer. The layer output
+    equals sh_layer_forward_cf's bit for bit (the taps add work, they change none)."""
+    cfg = make_cfg()
+    std = 0.02 if cfg.dim == 768 else 0.05
+    m, ocfg, ow = build(cfg, dtype, 67, std=std)
+    x = embed_cf(ow, sh.synth_tokens(seq, 68, cfg.vocab))
+    D, F, Q, KV = cfg.dim, cfg.hidden, cfg.qdim, cfg.kvdim
+    names = [("x2", D), ("q_rope", Q), ("k_rope", KV), ("v", KV), ("att", Q)]
+    for layer in range(min(cfg.n_layers, 2)):
+        out, sdpa, ffn = m.layer_forward_cf_taps(layer, x)
+        np.testing.assert_array_equal(out, m.layer_forward_cf(layer, x))
+        w_out, w_sdpa, w_ffn = oracle.layer_forward_cf_taps(ocfg, ow, layer, x, threads=THREADS)
+        assert sdpa.shape == w_sdpa.shape and ffn.shape == w_ffn.shape
+        np.testing.assert_array_equal(ffn[:D], out)
+        o = 0
+        for name, n in names:
+            err = rel_err(sdpa[o:o + n], w_sdpa[o:o + n])
+            print(f"layer {layer} sdpa {name}: rel {err:.2e}")
+            assert err <= 1e-4, (name, err)
+            o += n
+        for name, a, b in (("x_next", 0, D), ("h1", D, D + F), ("h3", D + F, D + 2 * F)):
+            err = rel_err(ffn[a:b], w_ffn[a:b])
+            print(f"layer {layer} ffn {name}: rel {err:.2e}")
+            assert err <= 1e-4, (name, err)
+        x = w_out
+    m.close()
+
+
 def test_one_layer_model_is_a_compiled_layer(gpu):
     # compileStoriesLayerForwardFunc's counterpart: a model holding one layer and no globals
     cfg = tiny_config(residual_scale=0.5)

@@ -31,6 +31,18 @@ def train_config(**kw):
     return tiny_config(**base)
 
 
+def wide_train_config():
+    """A shape whose products have K >= 512 (W2's K = hidden = 512, the W1|W3 input gradient
+    K = 1024, the classifier input gradient K = vocab = 1024), so the split-K products hand
+    their partials to the row kernels (RMSNorm forward and backward, RoPE, SiLU backward),
+    and head_dim 32 takes the MFMA attention kernels."""
+    return train_config(dim=128, hidden=512, n_heads=4, n_kv_heads=4, head_dim=32, vocab=1024,
+                        max_seq=64)
+
+
+CONFIGS = {"tiny": train_config, "wide": wide_train_config}
+
+
 def make(cfg, wseed, seq, std=0.15, **opts):
     w = sh.synth_weights(cfg, seed=wseed, std=std)
     tr = sh.Trainer(cfg, seq=seq, **opts)
@@ -76,9 +88,10 @@ def compare_tensors(tr, ref: oracle.TrainParams, which, atol=None, rel=None):
     return worst
 
 
-@pytest.mark.parametrize("seq,clip,wd", [(12, 0.0, 0.0), (40, 1e-2, 0.1)])
-def test_train_step_matches_oracle(gpu, seq, clip, wd):
-    cfg = train_config()
+@pytest.mark.parametrize("kind,seq,clip,wd", [("tiny", 12, 0.0, 0.0), ("tiny", 40, 1e-2, 0.1),
+                                               ("wide", 48, 1e-2, 0.1)])
+def test_train_step_matches_oracle(gpu, kind, seq, clip, wd):
+    cfg = CONFIGS[kind]()
     w, tr = make(cfg, 301, seq, lr=1e-3, grad_clip=clip, weight_decay=wd)
     toks = sh.synth_tokens(seq + 1, 302, cfg.vocab)
     inp, tgt = toks[:-1], toks[1:]
@@ -122,36 +135,44 @@ def test_engine_steps_follow_the_drand48_windows(gpu):
     tr.close()
 
 
-def test_stories110m_train_step_matches_oracle(gpu):
+@pytest.mark.parametrize("seq", [64, 256])
+def test_stories110m_train_step_matches_oracle(gpu, seq):
     """Stories110M shape (dim 768, 12 layers, vocab 32000), the engine's residual scale
-    1/sqrt(24), a 64-token window: loss and a sample of gradients and weights."""
+    1/sqrt(24), a 64-token window and the benchmark's 256-token window: the loss, every
+    gradient Adam applies, and a sample of the updated weights."""
     cfg = sh.stories110m_config()
     cfg.residual_scale = 1.0 / np.sqrt(24.0)
-    seq = 64
     w, tr = make(cfg, 321, seq, std=0.02, lr=3e-4)
     toks = sh.synth_tokens(seq + 1, 322, cfg.vocab)
-    loss = tr.step_window(toks[:-1], toks[1:])
     p = oracle.TrainParams.from_weights(w)
+    sample = ("layers.0.wq", "layers.5.w2", "layers.11.wo", "layers.11.rms_ffn", "rms_final", "embed")
+    before = {n: a.copy() for n, a in p.tensors() if n in sample}
+    loss = tr.step_window(toks[:-1], toks[1:])
     m, v, g = (oracle.TrainParams.zeros_like(p) for _ in range(3))
     want = oracle.train_step(oracle.config_from(cfg), p, m, v, g, oracle.hparams(lr=3e-4), 1, toks[:-1],
                              toks[1:], threads=THREADS)
-    print(f"Stories110M S=64: loss {loss:.6f} vs {want:.6f}, step {tr.state()['last_step_ms']:.2f} ms")
+    print(f"Stories110M S={seq}: loss {loss:.6f} vs {want:.6f}, step {tr.state()['last_step_ms']:.2f} ms")
     assert abs(loss - want) <= 2e-5 * abs(want)
-    grads, params = dict(g.tensors()), dict(p.tensors())
-    for name in ("layers.0.wq", "layers.5.w2", "layers.11.wo", "layers.11.rms_ffn", "rms_final", "embed"):
-        got = tr.read(sh.SH_TRAIN_GRADS, name, grads[name].shape)
-        assert float(np.max(np.abs(got - grads[name]))) <= 1e-3 * float(np.max(np.abs(grads[name]))), name
+    gerr = compare_tensors(tr, g, sh.SH_TRAIN_GRADS, rel=1e-3)
+    print(f"worst gradient error {gerr:.2e} (relative to the tensor's max)")
+    # the update is Adam's first step on the device's own gradients (exact), and against the
+    # oracle's weights it differs only where |g| is near eps, where g/(|g|+eps) magnifies
+    # rounding-level gradient differences (more such elements in a longer window)
+    check_adam_closed_form(tr, before, 3e-4, 0.0)
+    params = dict(p.tensors())
+    for name in sample:
         got = tr.read(sh.SH_TRAIN_PARAMS, name, params[name].shape)
         d = np.abs(got - params[name])
-        assert float(d.max()) <= 2 * 3e-4 and int((d > 1e-6).sum()) <= 1e-4 * d.size + 1, name
+        assert float(d.max()) <= 2 * 3e-4 and int((d > 1e-6).sum()) <= 5e-4 * d.size + 1, name
     tr.close()
 
 
-def test_gradient_accumulation_matches_oracle(gpu):
+@pytest.mark.parametrize("kind", ["tiny", "wide"])
+def test_gradient_accumulation_matches_oracle(gpu, kind):
     """AccumSteps 2 (backwardAndAccumulate, flushPending) over five windows: the pending sums
     after one window, the applied mean gradients and the weights after each flush, then a
     window flushed early by Flush(), and a Flush() with nothing pending."""
-    cfg = train_config()
+    cfg = CONFIGS[kind]()
     seq, lr, clip = 12, 1e-3, 1e-2
     w, tr = make(cfg, 341, seq, lr=lr, grad_clip=clip, accum_steps=2)
     p = oracle.TrainParams.from_weights(w)
