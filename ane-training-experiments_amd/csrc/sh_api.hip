@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -261,6 +262,33 @@ bool seam_end(sh_model *m, const void *dev, void *host, size_t bytes, int seq) {
 
 uint16_t host_bf16_bits(float x);
 
+// Device scratch of the allocation-free entry point (sh_conv_eval_noalloc): the operand
+// planes of its input and the K-range partials of its product. One copy per GPU, resident
+// until the process ends. In host code `scratch` names a host-side stand-in, never the
+// device memory: the device address comes from hipGetSymbolAddress with that device current
+// (at sh_init, or at the entry point's first call on a device) and is kept per device.
+constexpr size_t kNoAllocScratchBytes = 16u << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on `device`, which must be the current device; NULL (and
+// the error text set) if the runtime cannot resolve it.
+void *scratch_address(int device) {
+    if (device < 0 || device >= kMaxDevices) {
+        set_error("device index beyond the no-alloc scratch table");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *p = nullptr;
+        if (!hip_ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return nullptr;
+        g_scratch_ptr[device] = p;
+    }
+    return g_scratch_ptr[device];
+}
+
 }  // namespace
 }  // namespace sh
 
@@ -277,7 +305,8 @@ int sh_init(int32_t device) {
     }
     if (!hip_ok(hipSetDevice(device), "hipSetDevice")) return -1;
     g_device = device;
-    return 0;
+    // resolve this device's no-alloc scratch now, outside any caller's capture or loop
+    return scratch_address(device) ? 0 : -1;
 }
 
 size_t sh_last_error(char *buf, size_t len) {
@@ -1502,6 +1531,30 @@ int sh_conv_eval(sh_conv *c, const float *x, int32_t s, float *out) {
     (void)hipFree(y);
     (void)hipFree(pp);
     return rc;
+}
+
+int sh_conv_eval_noalloc(sh_conv *c, const float *x, int32_t s, float *out, void *stream) {
+    if (!c || !x || !out || s <= 0) {
+        set_error("sh_conv_eval_noalloc: bad arguments");
+        return -1;
+    }
+    (void)hipSetDevice(c->device);
+    const size_t plane_bytes = 2 * sizeof(uint16_t) * (size_t)s * c->in_dim;   // hi and lo planes
+    const size_t part = gemm_partial_elems(s, c->out_dim, c->in_dim);
+    const size_t part_off = align_up(plane_bytes, 256);
+    const size_t need = part_off + sizeof(float) * part;
+    if (need > kNoAllocScratchBytes) {
+        set_error("sh_conv_eval_noalloc: s=" + std::to_string(s) + " needs " + std::to_string(need) +
+                  " bytes of scratch; the allocation-free path holds " + std::to_string(kNoAllocScratchBytes));
+        return -1;
+    }
+    uint8_t *base = (uint8_t *)scratch_address(c->device);
+    if (!base) return -1;
+    return hip_ok(enqueue_linear_rows(x, s, c->in_dim, c->w, c->out_dim, SH_DTYPE_F16, (uint16_t *)base, out, false,
+                                      part ? (float *)(base + part_off) : nullptr, part, (hipStream_t)stream),
+                  "conv eval (no alloc)")
+               ? 0
+               : -1;
 }
 
 void sh_conv_destroy(sh_conv *c) {

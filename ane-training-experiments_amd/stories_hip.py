@@ -124,6 +124,7 @@ SIGNATURES = {
     "sh_conv_create": (C.c_void_p, [_F, C.c_int32, C.c_int32]),
     "sh_conv_eval": (C.c_int, [C.c_void_p, _F, C.c_int32, _F]),
     "sh_conv_destroy": (None, [C.c_void_p]),
+    "sh_conv_eval_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p]),
     "sh_trainer_create": (C.c_void_p, [C.POINTER(ShConfig), C.c_void_p]),
     "sh_trainer_upload_layer": (C.c_int, [C.c_void_p, C.c_int32] + [_F] * 9),
     "sh_trainer_upload_globals": (C.c_int, [C.c_void_p, _F, _F]),

@@ -168,6 +168,17 @@ typedef struct sh_conv sh_conv;
 sh_conv *sh_conv_create(const float *w, int32_t out_dim, int32_t in_dim);
 int sh_conv_eval(sh_conv *c, const float *x, int32_t s, float *out);
 void sh_conv_destroy(sh_conv *c);
+/* sh_conv_eval without any allocation, for callers that cannot allocate device memory: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. No
+ * reference counterpart (ConvEval allocates its IOSurfaces per kernel). x [s, in_dim] and out
+ * [s, out_dim] are device pointers the caller owns; the work is enqueued on `stream` (a
+ * hipStream_t; NULL = the null stream) and the call returns without waiting. The input's
+ * operand planes and the product's K-range partials live in a static 16 MiB device array
+ * per GPU (resolved at sh_init); a call needing more (4*s*in_dim bytes of planes plus the
+ * partials of the split product) fails with a message saying how much. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two threads) race, so
+ * a caller must order them. Results equal sh_conv_eval's bit for bit. */
+int sh_conv_eval_noalloc(sh_conv *c, const float *x, int32_t s, float *out, void *stream);
 /* (*Engine).Decode with Temperature 0 (ane/storiesane/decode.go:18-94): every step runs the
  * full causal forward (as sh_prefill_logits) over the last `seq` tokens left-padded with BOS
  * (fillDecodeWindow, :83-94) and appends the argmax of the last position's logits. The prompt
