@@ -572,7 +572,7 @@ int main(int argc, char **argv) {
         if (copy_bytes > 0 && sh_copy_calibrate((size_t)copy_bytes, 5, &copy_ms, &copy_gbs))
             fatalf("copy calibrate: %s", lib_error());
         for (int i = 0; i < fl.i("bench-warmup"); i++) decode(m, c, prompt, max_new, 0.f, rng);
-        std::vector<double> gpu_ms, bytes;
+        std::vector<double> gpu_ms, bytes, pre_ms;
         std::vector<long long> fwd, gen;
         DecodeResult last;
         int persistent = 0, grid = 0;
@@ -582,6 +582,7 @@ int main(int argc, char **argv) {
             sh_timing t{};
             if (sh_stats(m, &t)) fatalf("stats: %s", lib_error());
             gpu_ms.push_back(t.gpu_ms);
+            pre_ms.push_back(t.prefill_ms);
             fwd.push_back(t.forwards);
             gen.push_back(t.tokens_out);
             bytes.push_back(t.bytes_per_forward_mean);
@@ -595,6 +596,8 @@ int main(int argc, char **argv) {
                          ", \"warmup\": " + std::to_string(fl.i("bench-warmup")) +
                          ", \"wall_s\": " + std::to_string(wall) + ", \"gpu_ms\": [";
         for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(gpu_ms[i]);
+        js += "], \"prefill_ms\": [";
+        for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(pre_ms[i]);
         js += "], \"forwards\": [";
         for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(fwd[i]);
         js += "], \"generated\": [";

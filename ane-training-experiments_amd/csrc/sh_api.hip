@@ -485,6 +485,7 @@ sh_model *sh_model_create(const sh_config *cfg, int32_t dtype) {
         return fail("hipStreamCreate", e);
     if ((e = hipEventCreate(&m->ev0)) != hipSuccess) return fail("hipEventCreate", e);
     if ((e = hipEventCreate(&m->ev1)) != hipSuccess) return fail("hipEventCreate", e);
+    if ((e = hipEventCreate(&m->ev_mid)) != hipSuccess) return fail("hipEventCreate", e);
     if ((e = hipMemsetAsync(m->kcache, 0, kvb, m->stream)) != hipSuccess) return fail("memset kv", e);
     if ((e = hipMemsetAsync(m->vcache, 0, kvb, m->stream)) != hipSuccess) return fail("memset kv", e);
     if ((e = hipMemsetAsync(m->tokens, 0, 4 * (c.max_seq + 1), m->stream)) != hipSuccess)
@@ -584,6 +585,7 @@ void sh_model_destroy(sh_model *m) {
     (void)hipFree(m->wd_arena);
     if (m->ev0) (void)hipEventDestroy(m->ev0);
     if (m->ev1) (void)hipEventDestroy(m->ev1);
+    if (m->ev_mid) (void)hipEventDestroy(m->ev_mid);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete[] m->layers;
     delete m;
@@ -834,12 +836,34 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
     if (!hip_ok(hipMemcpyAsync(m->tokens, prompt, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, m->stream),
                 "prompt"))
         return -1;
-    // timed region: cache reset (infer.go:165-168) and every forward
+    // The prompt's first n_prompt-1 positions only fill the KV cache (their logits are never
+    // read): one causal forward over them on the full-sequence path, in the decode forms of
+    // the softmax sum and SiLU, stores the cache a token-by-token decode would store, to the
+    // rounding of its fp32 sums. The token loop then starts at the last prompt id. W8A8 keeps
+    // the token-by-token prompt: its bit-exactness rests on the reference's summation order.
+    std::string why;
+    const int pre = (m->dtype != SH_DTYPE_W8A8 && n_prompt > 1 && prefill_supported(m, &why)) ? n_prompt - 1 : 0;
+    if (pre > 0) {
+        if (!hip_ok(prefill_alloc(m, pre, false), "prefill scratch")) return -1;
+        std::vector<int32_t> rows(3 * (size_t)pre);
+        for (int t = 0; t < pre; t++) {
+            rows[t] = prompt[t];
+            rows[pre + t] = t;
+            rows[2 * (size_t)pre + t] = 0;
+        }
+        if (!hip_ok(hipMemcpyAsync(m->pf_tokens, rows.data(), 4 * (size_t)pre, hipMemcpyHostToDevice, m->stream), "prompt rows") ||
+            !hip_ok(hipMemcpyAsync(m->pf_rowpos, rows.data() + pre, 4 * (size_t)pre, hipMemcpyHostToDevice, m->stream), "prompt rows") ||
+            !hip_ok(hipMemcpyAsync(m->pf_rowseq, rows.data() + 2 * (size_t)pre, 4 * (size_t)pre, hipMemcpyHostToDevice, m->stream), "prompt rows"))
+            return -1;
+    }
+    // timed region: cache reset (infer.go:165-168), the prompt forward, every token forward
     if (!hip_ok(hipEventRecord(m->ev0, m->stream), "event")) return -1;
     if (!hip_ok(hipMemsetAsync(m->kcache, 0, kvb, m->stream), "reset kcache") ||
         !hip_ok(hipMemsetAsync(m->vcache, 0, kvb, m->stream), "reset vcache"))
         return -1;
-    if (forwards > 0 && !launch_forwards(m, 0, forwards, n_prompt)) return -1;
+    if (pre > 0 && !hip_ok(enqueue_prefill(m, pre, pre, false, true), "prompt forward")) return -1;
+    if (!hip_ok(hipEventRecord(m->ev_mid, m->stream), "event")) return -1;
+    if (forwards > pre && !launch_forwards(m, pre, forwards - pre, n_prompt)) return -1;
     if (!hip_ok(hipEventRecord(m->ev1, m->stream), "event")) return -1;
     const int total = n_prompt + generated;
     if (!hip_ok(hipMemcpyAsync(out_tokens, m->tokens, 4 * (size_t)total, hipMemcpyDeviceToHost, m->stream),
@@ -862,17 +886,18 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
     }
     *n_out = n;
     *stopped_eos = eos;
-    float ms = 0;
+    float ms = 0, pre_ms = 0;
     (void)hipEventElapsedTime(&ms, m->ev0, m->ev1);
+    (void)hipEventElapsedTime(&pre_ms, m->ev0, m->ev_mid);
     double bytes = 0;
-    for (int p = 0; p < forwards; p++) bytes += forward_bytes(m, p);
+    for (int p = pre; p < forwards; p++) bytes += forward_bytes(m, p);
     m->last.gpu_ms = ms;
-    m->last.forwards = forwards;
+    m->last.forwards = forwards - pre;
     m->last.tokens_out = n - n_prompt;
-    m->last.bytes_per_forward_mean = forwards ? bytes / forwards : 0;
+    m->last.bytes_per_forward_mean = forwards > pre ? bytes / (forwards - pre) : 0;
     m->last.persistent = m->persistent ? 1 : 0;
     m->last.grid = m->persistent ? m->p_grid : 0;
-    m->last.prefill_ms = 0;
+    m->last.prefill_ms = pre_ms;
     return 0;
 }
 

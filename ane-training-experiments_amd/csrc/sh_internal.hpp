@@ -80,7 +80,7 @@ struct sh_model {
 
     hipGraphExec_t step_exec;
     bool step_ready;
-    hipEvent_t ev0, ev1;
+    hipEvent_t ev0, ev1, ev_mid;   // ev_mid: end of a greedy decode's prompt forward
     sh_timing last;
 
     // persistent decode kernel (sh_persistent.hip); unused when `persistent` is false

@@ -65,6 +65,18 @@ struct LayerPtrs {
     const float *rms_att, *rms_ffn, *q_norm, *k_norm;
 };
 
+// The layer table is written by the host before the launch and only read by the kernel, so
+// it is read through the constant address space: uniform scalar loads, which do not join the
+// in-order vector memory counter. Read as vector loads, a pointer fetched after a stage's
+// early weight loads would make the stage wait for those weights before its first poll.
+__device__ __forceinline__ LayerPtrs layer_ptrs(const LayerPtrs *table, int l) {
+#ifdef __HIP_DEVICE_COMPILE__
+    return ((const __attribute__((address_space(4))) LayerPtrs *)table)[l];
+#else
+    return table[l];  // the host pass only parses device functions
+#endif
+}
+
 struct PParams {
     int D, F, H, KVH, hd, V, max_seq, L, qdim, kvdim, qkv_rows;
     float alpha, inv_sqrt_hd;
@@ -84,6 +96,7 @@ struct PParams {
     uint32_t epoch0;
     int *err;
     long long spin_limit;
+    long long quiet;   // ticks a wait runs before it also reads the abort flag (20 us)
     long long *trace;  // stage timestamps of forward trace_f (workgroups 0 and grid-1)
     int trace_f;
     StageOwn own[5];   // qkv, wo, w13, w2, classifier
@@ -269,7 +282,7 @@ __device__ __forceinline__ bool ll_wait_batch(int n, const PParams &p, const Map
             ok = false;
             break;
         }
-        if (aborted(p)) {
+        if (now - t0 > p.quiet && aborted(p)) {
             ok = false;
             break;
         }
@@ -333,10 +346,13 @@ __device__ __forceinline__ bool ll_wait_vec(const uint64_t *src, int n, uint32_t
 
 // This thread's words j = threadIdx.x + k*kPB (k < K, j < n) of an input map, into
 // registers once each carries its epoch (other entries of val are left as they are).
-// Starts with a workgroup barrier after the first requests (the LDS the stage writes next
-// is then free). *ok is this thread's outcome; the caller combines it over the workgroup.
-template <int K>
-__device__ __forceinline__ void ll_poll_regs(int n, const PParams &p, const InputMap &map, float (&val)[K], bool &ok) {
+// `pre` runs right after the first requests are issued (the stage's weight loads go there:
+// queued behind the first requests, they hold up none of them). Then a workgroup barrier
+// (the LDS the stage writes next is free after it). *ok is this thread's outcome; the caller
+// combines it over the workgroup.
+template <int K, typename Pre>
+__device__ __forceinline__ void ll_poll_regs(int n, const PParams &p, const InputMap &map, float (&val)[K], bool &ok,
+                                             Pre &&pre) {
     uint64_t v[K];
     unsigned need = 0;
 #pragma unroll
@@ -347,6 +363,7 @@ __device__ __forceinline__ void ll_poll_regs(int n, const PParams &p, const Inpu
             need |= 1u << k;
         }
     }
+    pre();
     lds_barrier();
     ok = true;
     long long t0 = 0;
@@ -367,7 +384,7 @@ __device__ __forceinline__ void ll_poll_regs(int n, const PParams &p, const Inpu
             ok = false;
             break;
         }
-        if (aborted(p)) {
+        if (now - t0 > p.quiet && aborted(p)) {
             ok = false;
             break;
         }
@@ -389,11 +406,11 @@ __device__ __forceinline__ void ll_poll_regs(int n, const PParams &p, const Inpu
 //                quantization (its boundaries must see the reference's values).
 // Barriers: the poll's first (frees LDS), one after the partial sums (and the ok flags), and
 // for W8A8 two more around the quantization.
-template <int WT, int COLS, bool NORM>
+template <int WT, int COLS, bool NORM, typename Pre>
 __device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &map, int count,
                             const uint16_t *emb_row, const uint16_t *res_emb, const float *gain,
                             double eps, double *red, int *okw, const PParams &p, uint32_t *xq,
-                            float *sa, float *rscale) {
+                            float *sa, float *rscale, Pre &&pre) {
     constexpr int K = (COLS + kMaxRes + kPB - 1) / kPB;
     constexpr bool Q8 = WT == SH_DTYPE_W8A8;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -421,9 +438,10 @@ __device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &ma
             const int i = threadIdx.x + k * kPB;
             if (i < n) val[k] = w2f<WT>(emb_row[i]);
         }
+        pre();
         lds_barrier();
     } else {
-        ll_poll_regs<K>(res_emb ? n : count, p, map, val, ok);
+        ll_poll_regs<K>(res_emb ? n : count, p, map, val, ok, pre);
     }
     // sum of squares: float64 as the reference for W8A8, float for the fp16/bf16 models
     double ss = 0;
@@ -505,48 +523,71 @@ struct StageIO {
     float *logits;              // E_CLS: logits output, or NULL when not read back
 };
 
-// One GEMV stage over W [rows, cols]. The workgroup owns the row block of its rank in the
-// stage's ownership `o` (none: it skips the stage without polling); inside the block, row
-// group k of G = 64/LPR rows belongs to wave k % kPW. Blocks of consecutive rows keep each
-// hand-over line written by one workgroup, so no line has several writers racing to it.
-// Weight tiles of the first U groups of each wave are loaded before the input is polled.
-// Returns false on timeout/abort. For E_CLS, *best_v/*best_i receive this wave's (max,
-// first index).
-template <int LPR, int CPL, int WT, int U, bool NORM>
-__device__ __forceinline__ bool gemv_stage(const PParams &p, const StageOwn o, const void *__restrict__ W,
-                           const float *__restrict__ wscale, int rows, int cols,
-                           int epi, const StageIO &io, float *xs, uint32_t *xq, double *red,
-                           int *okw, float *ostage, float &best_v, int &best_i) {
+// Register tile of a GEMV stage: the weight chunks this lane needs for the first U row groups
+// of its wave (CPL 16-byte chunks per row).
+template <int U, int CPL>
+struct WTile {
+    u32x4 w[U][CPL];
+};
+
+// This workgroup's row block [r0, r1) in a stage and its rank among the stage's owners;
+// false when it owns no rows.
+__device__ __forceinline__ bool own_block(const StageOwn o, int rows, int &rank, int &r0, int &r1) {
+    rank = (int)blockIdx.x - o.off;
+    if (rank < 0) rank += gridDim.x;
+    if (rank >= o.n) return false;
+    r0 = rank * o.per;
+    r1 = min(rows, r0 + o.per);
+    return r0 < r1;
+}
+
+// What a stage's arithmetic needs from its input poll.
+struct StageCtx {
+    int rank, r0, r1;
+    float sa;       // W8A8: the input's per-tensor scale
+    float rscale;   // fp16/bf16 with RMSNorm: rrms, applied to each finished dot product
+};
+
+// Loads the tile of the owner's rows [c.r0, c.r1) in a stage: row group k of the block
+// belongs to wave k % kPW, G = 64/LPR rows per group, LPR lanes per row. A lane past the
+// block's end re-reads row r0, so every entry of the tile is written.
+template <int LPR, int CPL, int WT, int U>
+__device__ __forceinline__ void tile_load(WTile<U, CPL> &t, const StageCtx &c, const void *__restrict__ W,
+                                          int cols) {
     constexpr int G = 64 / LPR;
-    constexpr int EPC = chunk_elems<WT>();
-    constexpr bool Q8 = WT == SH_DTYPE_W8A8;
     const SH_GLOBAL uint8_t *Wb = (const SH_GLOBAL uint8_t *)W;
     const size_t row_bytes = (size_t)cols * elem_bytes<WT>();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane % LPR, grp = lane / LPR;
-    int rank = (int)blockIdx.x - o.off;
-    if (rank < 0) rank += gridDim.x;
-    if (rank >= o.n) return true;
-    const int r0 = rank * o.per;
-    const int r1 = min(rows, r0 + o.per);
-    if (r0 >= r1) return true;
-    // first row of this wave's k-th group (wave-uniform) and this lane's row in it
-    auto gbase = [&](int k) { return r0 + (wave + k * kPW) * G; };
-
-    u32x4 w[U][CPL];
+    const int r0 = c.r0, r1 = c.r1;
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        const int row = gbase(u) + grp;
-        if (row < r1) {
-            const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(Wb + (size_t)row * row_bytes);
+        const int row = r0 + (wave + u * kPW) * G + grp;
+        const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(Wb + (size_t)(row < r1 ? row : r0) * row_bytes);
 #pragma unroll
-            for (int j = 0; j < CPL; j++) w[u][j] = src[sub + j * LPR];
-        }
+        for (int j = 0; j < CPL; j++) t.w[u][j] = src[sub + j * LPR];
     }
-    float sa = 1.0f;
+}
+
+// First half of one GEMV stage over W [rows, cols]: the workgroup owns the row block of its
+// rank in the stage's ownership `o` (blocks of consecutive rows keep each hand-over line
+// written by one workgroup). An owner polls the stage's input (and residual rows) into LDS
+// and normalises it. Returns 0 for a workgroup owning no rows (it polls nothing), 1 once the
+// input is staged, -1 on timeout/abort. An owner runs `pre(c)` right after issuing its first
+// poll requests: the stage's weight loads go there. Loads complete in issue order, so weight
+// loads issued ahead of the poll would hold up its first answer, while these travel beside
+// the hand-over they wait for.
+template <int LPR, int CPL, int WT, bool NORM, typename Pre>
+__device__ __forceinline__ int stage_poll(const PParams &p, const StageOwn o, int rows, int cols, int epi,
+                                          const StageIO &io, float *xs, uint32_t *xq, double *red, int *okw,
+                                          StageCtx &c, Pre &&pre) {
+    constexpr int EPC = chunk_elems<WT>();
+    if (!own_block(o, rows, c.rank, c.r0, c.r1)) return 0;
+    c.sa = 1.0f;
+    c.rscale = 1.f;
     // residual rows, polled with the input (or read from the embedding row in layer 0), land
     // in xs[cols, cols + r1 - r0)
-    const int nres = epi == E_RESID ? r1 - r0 : 0;
+    const int nres = epi == E_RESID ? c.r1 - c.r0 : 0;
     InputMap im{};
     im.s = io.in_ll;
     im.roff = io.res_ll ? io.res_ll - io.in_ll : 0;
@@ -555,17 +596,51 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const StageOwn o, c
     im.per = io.in_per > 0 ? io.in_per : kDense;
     im.stride = io.in_per > 0 ? io.in_stride : kDense;
     im.magic = io.in_per > 0 ? io.in_magic : 2u;   // ceil(2^31 / kDense)
-    im.r0 = r0;
+    im.r0 = c.r0;
     im.rper = io.res_per > 0 ? io.res_per : kDense;
     im.rstride = io.res_per > 0 ? io.res_stride : kDense;
     im.rmagic = io.res_per > 0 ? io.res_magic : 2u;
     im.e = io.e_in;
     im.er = io.e_res;
-    float rscale = 1.f;
     if (!stage_input<WT, LPR * CPL * EPC, NORM>(xs, cols, im, cols + nres, io.emb_row,
-                                          epi == E_RESID ? io.res_emb : nullptr, io.gain, p.eps,
-                                          red, okw, p, xq, &sa, &rscale))
-        return false;
+                                                epi == E_RESID ? io.res_emb : nullptr, io.gain, p.eps,
+                                                red, okw, p, xq, &c.sa, &c.rscale, [&] { pre(c); }))
+        return -1;
+    return 1;
+}
+
+// Taken at the end of a stage on both paths: after the owner's arithmetic (every load of the
+// stage has been used by then) and where a workgroup that owns no rows skips it. The compiler
+// cannot tell that the skipping workgroup never loaded the stage's tile, nor that the owner's
+// row loop issues no load in its last pass, so without it the registers of those loads would
+// count as in flight after the join, and the next stage reusing them would wait there for
+// every later request as well (the vector memory counter is in order): for its own stores
+// and, behind them, its first poll. Here nothing is in flight but earlier hand-over stores.
+__device__ __forceinline__ void settle_loads() {
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0), expcnt and lgkmcnt left alone
+}
+
+// Second half: the dot products of the owner's rows against the staged input, the tile `t`
+// holding the first U row groups of each wave (further groups stream through it), then the
+// epilogue and the block's hand-over stores. For E_CLS, *best_v/*best_i receive this wave's
+// (max, first index).
+template <int LPR, int CPL, int WT, int U>
+__device__ __forceinline__ void stage_compute(const PParams &p, const void *__restrict__ W,
+                                              const float *__restrict__ wscale, int cols, int epi,
+                                              const StageIO &io, float *xs, uint32_t *xq, float *ostage,
+                                              float &best_v, int &best_i, const StageCtx &c,
+                                              WTile<U, CPL> &t) {
+    constexpr int G = 64 / LPR;
+    constexpr bool Q8 = WT == SH_DTYPE_W8A8;
+    const SH_GLOBAL uint8_t *Wb = (const SH_GLOBAL uint8_t *)W;
+    const size_t row_bytes = (size_t)cols * elem_bytes<WT>();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, grp = lane / LPR;
+    const int r0 = c.r0, r1 = c.r1;
+    const float sa = c.sa, rscale = c.rscale;
+    // first row of this wave's k-th group (wave-uniform)
+    auto gbase = [&](int k) { return r0 + (wave + k * kPW) * G; };
+    auto &w = t.w;
     // this lane's slice of the input: floats, or packed int8 words for W8A8
     float xr[Q8 ? 1 : CPL * 8];
     uint32_t xr8[Q8 ? CPL * 4 : 1];
@@ -580,7 +655,6 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const StageOwn o, c
         }
     }
 
-    bool ok = true;
     for (int k0 = 0; gbase(k0) < r1; k0 += U) {
         float acc[U];
         int acci[U];
@@ -654,17 +728,17 @@ __device__ __forceinline__ bool gemv_stage(const PParams &p, const StageOwn o, c
             }
         }
     }
+    settle_loads();
     // The block's outputs leave in one store instruction per 64 words: a hand-over line
     // written by one wave instruction becomes visible as a whole, about a microsecond
     // sooner than the same line written word by word from several waves.
     if (epi != E_CLS) {
         lds_barrier();
         const int nout = epi == E_GATE ? (r1 - r0) >> 1 : r1 - r0;
-        uint64_t *out = io.out_ll + (size_t)rank * io.out_stride;
+        uint64_t *out = io.out_ll + (size_t)c.rank * io.out_stride;
         for (int i = threadIdx.x; i < nout; i += kPB) ll_put(out + i, ostage[i], io.e_out);
     }
     // no closing barrier: the next stage's poll starts with one before it writes LDS
-    return ok;
 }
 
 // Three LL segments (q heads, k, v of one kv head) waited for as one vector.
@@ -772,7 +846,7 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
     constexpr int hd = HD, ngr = kPB / HD;
     const int group = p.H / p.KVH, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const LayerPtrs &Lp = p.layers[l];
+    const LayerPtrs Lp = layer_ptrs(p.layers, l);
     const size_t lbase = (size_t)l * p.max_seq * p.kvdim + (size_t)g * hd;
     SH_LDS uint8_t *kst = (SH_LDS uint8_t *)kvlds;
     SH_LDS uint8_t *vst = kst + (size_t)S::ROWS * S::RB;
@@ -1004,7 +1078,7 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int ms = p.max_seq;
-    const LayerPtrs &Lp = p.layers[l];
+    const LayerPtrs Lp = layer_ptrs(p.layers, l);
     const size_t lbase = (size_t)l * ms * p.kvdim + (size_t)g * hd;
     SH_LDS uint8_t *kst = (SH_LDS uint8_t *)kvlds;
     SH_LDS uint8_t *vst = kst + (size_t)S::ROWS * S::RB;
@@ -1235,6 +1309,9 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     const int L = p.L;
     const int n_stamps = 5 * L + 3;
     int tok_next = 0;
+    // Each GEMV stage keeps the weights of its first row groups in registers (qkv and w13: two
+    // per wave, wo and w2: one, the classifier: four), loaded inside the stage's poll right
+    // after its first requests.
     for (int f = 0; f < p.n_forwards; f++) {
         const int pos = p.pos0 + f;
         const bool tracing = p.trace && f == p.trace_f && threadIdx.x == 0;
@@ -1251,11 +1328,14 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
         const uint32_t base = p.epoch0 + (uint32_t)f * (uint32_t)(L + 1);
         float bv = -INFINITY;
         int bi = 0x7fffffff;
-        for (int l = 0; l < L; l++) {
+        // one layer
+        auto layer = [&](int l) -> bool {
             const uint32_t e = base + (uint32_t)l + 1;
-            const LayerPtrs &Lp = p.layers[l];
+            const LayerPtrs Lp = layer_ptrs(p.layers, l);
             if ((int)blockIdx.x < p.KVH) attn_prefetch<KVT, HD>(p, l, blockIdx.x, pos, kvlds);
             StageIO io{};
+            StageCtx c{};
+            int r;
             // qkv
             io.in_ll = l ? p.ll_x : nullptr;
             io.in_per = p.own[3].per;
@@ -1267,8 +1347,14 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.out_stride = p.ostride[0];
             io.e_in = e - 1;
             io.e_out = e;
-            if (!gemv_stage<LD, CD, WT, 2, true>(p, p.own[0], Lp.wqkv, Lp.s_qkv, p.qkv_rows, p.D, E_STORE, io, xs, xq, red, okw, ostage, bv, bi))
-                return;
+            {
+                WTile<2, CD> t;
+                if ((r = stage_poll<LD, CD, WT, true>(p, p.own[0], p.qkv_rows, p.D, E_STORE, io, xs, xq, red, okw, c,
+                        [&](const StageCtx &cc) { tile_load<LD, CD, WT, 2>(t, cc, Lp.wqkv, p.D); })) < 0)
+                    return false;
+                if (r) stage_compute<LD, CD, WT, 2>(p, Lp.wqkv, Lp.s_qkv, p.D, E_STORE, io, xs, xq, ostage, bv, bi, c, t);
+                else settle_loads();
+            }
             stamp();
             // attention
             if ((int)blockIdx.x < p.KVH) {
@@ -1279,7 +1365,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                     aok = attn_stage_fast<KVT, HD, 1>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf);
                 else
                     aok = attn_stage_fast<KVT, HD, 2>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf);
-                if (!aok) return;
+                if (!aok) return false;
             }
             stamp();
             // wo + residual
@@ -1295,8 +1381,14 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.e_in = e;
             io.e_res = e - 1;
             io.e_out = e;
-            if (!gemv_stage<LQ, CQ, WT, 1, false>(p, p.own[1], Lp.wo, Lp.s_o, p.D, p.qdim, E_RESID, io, xs, xq, red, okw, ostage, bv, bi))
-                return;
+            {
+                WTile<1, CQ> t;
+                if ((r = stage_poll<LQ, CQ, WT, false>(p, p.own[1], p.D, p.qdim, E_RESID, io, xs, xq, red, okw, c,
+                        [&](const StageCtx &cc) { tile_load<LQ, CQ, WT, 1>(t, cc, Lp.wo, p.qdim); })) < 0)
+                    return false;
+                if (r) stage_compute<LQ, CQ, WT, 1>(p, Lp.wo, Lp.s_o, p.qdim, E_RESID, io, xs, xq, ostage, bv, bi, c, t);
+                else settle_loads();
+            }
             stamp();
             // w1/w3 + silu gate
             io = StageIO{};
@@ -1309,8 +1401,14 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.out_stride = p.ostride[2];
             io.e_in = e;
             io.e_out = e;
-            if (!gemv_stage<LD, CD, WT, 2, true>(p, p.own[2], Lp.w13, Lp.s_13, 2 * p.F, p.D, E_GATE, io, xs, xq, red, okw, ostage, bv, bi))
-                return;
+            {
+                WTile<2, CD> t;
+                if ((r = stage_poll<LD, CD, WT, true>(p, p.own[2], 2 * p.F, p.D, E_GATE, io, xs, xq, red, okw, c,
+                        [&](const StageCtx &cc) { tile_load<LD, CD, WT, 2>(t, cc, Lp.w13, p.D); })) < 0)
+                    return false;
+                if (r) stage_compute<LD, CD, WT, 2>(p, Lp.w13, Lp.s_13, p.D, E_GATE, io, xs, xq, ostage, bv, bi, c, t);
+                else settle_loads();
+            }
             stamp();
             // w2 + residual
             io = StageIO{};
@@ -1327,23 +1425,48 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             io.e_in = e;
             io.e_res = e;
             io.e_out = e;
-            if (!gemv_stage<LF, CF, WT, 1, false>(p, p.own[3], Lp.w2, Lp.s_2, p.D, p.F, E_RESID, io, xs, xq, red, okw, ostage, bv, bi))
-                return;
+            {
+                WTile<1, CF> t;
+                if ((r = stage_poll<LF, CF, WT, false>(p, p.own[3], p.D, p.F, E_RESID, io, xs, xq, red, okw, c,
+                        [&](const StageCtx &cc) { tile_load<LF, CF, WT, 1>(t, cc, Lp.w2, p.F); })) < 0)
+                    return false;
+                if (r) stage_compute<LF, CF, WT, 1>(p, Lp.w2, Lp.s_2, p.F, E_RESID, io, xs, xq, ostage, bv, bi, c, t);
+                else settle_loads();
+            }
             stamp();
-        }
+            return true;
+        };
+        for (int l = 0; l < L; l++)
+            if (!layer(l)) return;
         // classifier over rmsnorm(x) (infer.go:242-243)
         const uint32_t ec = base + (uint32_t)L + 1;
-        StageIO io{};
-        io.in_ll = p.ll_x;
-        io.in_per = p.own[3].per;
-        io.in_stride = p.ostride[3];
-        io.in_magic = p.omagic[3];
-        io.gain = p.rms_final;
-        // only the launch's last forward leaves its logits: the host reads them after a
-        // one-forward launch, and stores queued ahead of the argmax poll delay it
-        io.logits = f == p.n_forwards - 1 ? p.logits : nullptr;
-        io.e_in = base + (uint32_t)L;
-        if (!gemv_stage<LD, CD, WT, 4, true>(p, p.own[4], p.cls, p.s_cls, p.V, p.D, E_CLS, io, xs, xq, red, okw, ostage, bv, bi)) return;
+        {
+            StageIO io{};
+            StageCtx c{};
+            io.in_ll = p.ll_x;
+            io.in_per = p.own[3].per;
+            io.in_stride = p.ostride[3];
+            io.in_magic = p.omagic[3];
+            io.gain = p.rms_final;
+            // only the launch's last forward leaves its logits: the host reads them after a
+            // one-forward launch, and stores queued ahead of the argmax poll delay it
+            io.logits = f == p.n_forwards - 1 ? p.logits : nullptr;
+            io.e_in = base + (uint32_t)L;
+            // the classifier's tile (four row groups) is loaded before its poll: loaded inside
+            // it, beside the poll's registers, it would spill. Every workgroup loads one (a
+            // workgroup owning no rows reads row 0), so the tile is defined on every path and
+            // the compiler keeps no copy of it alive around the loop.
+            WTile<4, CD> t;
+            {
+                StageCtx ct{};
+                if (!own_block(p.own[4], p.V, ct.rank, ct.r0, ct.r1)) ct.r0 = ct.r1 = 0;
+                tile_load<LD, CD, WT, 4>(t, ct, p.cls, p.D);
+            }
+            const int r = stage_poll<LD, CD, WT, true>(p, p.own[4], p.V, p.D, E_CLS, io, xs, xq, red, okw, c,
+                                                       [](const StageCtx &) {});
+            if (r < 0) return;
+            if (r) stage_compute<LD, CD, WT, 4>(p, p.cls, p.s_cls, p.D, E_CLS, io, xs, xq, ostage, bv, bi, c, t);
+        }
         stamp();
         // this workgroup's (max, first index)
         {
@@ -1383,7 +1506,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                         ok = false;
                         break;
                     }
-                    if (aborted(p)) {
+                    if (now - t0 > p.quiet && aborted(p)) {
                         ok = false;
                         break;
                     }
@@ -1587,6 +1710,11 @@ hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt
     p.epoch0 = m->epoch;
     p.err = m->p_err;
     p.spin_limit = m->spin_ticks;
+    // The abort flag is an agent-scope load, a full round trip to the memory side: read on
+    // every retry it doubles a retry's period, so a hand-over is noticed half a round trip
+    // later on average. A wait reads it only once it has lasted 20 us (no hand-over of a
+    // running decode takes that long), which still ends every wave soon after an abort.
+    p.quiet = m->spin_ticks / 100000;
     p.trace = m->trace_f >= 0 ? m->trace_buf : nullptr;
     p.trace_f = m->trace_f;
     for (int i = 0; i < 5; i++) {

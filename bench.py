@@ -152,7 +152,10 @@ def decode_line(r, steps, metric, workload, dtype, data, config, cpu):
     """JSON line of a greedy-decode workload measured by the host program's -bench-steps."""
     gen_tokens = sum(r["generated"])
     forwards = sum(r["forwards"])
-    gpu_ms = sum(r["gpu_ms"])
+    # device time of each decode = the prompt's cache-filling forward (full-sequence kernels)
+    # + the token loop (one k_decode_persistent launch); the roofline is the launch's
+    prefill_ms = sum(r.get("prefill_ms", [0.0] * steps))
+    gpu_ms = sum(r["gpu_ms"]) - prefill_ms
     bytes_total = sum(b * f for b, f in zip(r["bytes_per_forward_mean"], r["forwards"]))
     wall = r["wall_s"]
     launch_ms = gpu_ms / steps
@@ -172,6 +175,7 @@ def decode_line(r, steps, metric, workload, dtype, data, config, cpu):
             "bytes_per_launch": round(bytes_launch), "launch_ms": round(launch_ms, 4),
             "forwards_per_launch": forwards // steps,
             "us_per_forward": round(gpu_ms * 1e3 / max(forwards, 1), 3),
+            "prompt_forward_ms": round(prefill_ms / steps, 4),
         },
     }
     if cpu is not None:

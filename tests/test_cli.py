@@ -206,7 +206,10 @@ def test_cli_bench_mode_stories110m():
             "-bench-steps", "2", "-bench-warmup", "1")
     r = json.loads(p.stdout)
     assert r["steps"] == 2 and len(r["gpu_ms"]) == 2 and r["persistent"] == 1
-    assert r["forwards"] == [143, 143] and r["generated"] == [128, 128]
+    # the 15 prompt positions before the last fill the KV cache in one full-sequence forward
+    # (prefill_ms); the persistent launch runs the 128 generating forwards
+    assert r["forwards"] == [128, 128] and r["generated"] == [128, 128]
+    assert all(0 < pm < g for pm, g in zip(r["prefill_ms"], r["gpu_ms"]))
     cfg = sh.stories110m_config()
     w = sh.synth_weights(cfg, seed=0, std=0.02)
     ref = oracle.Decoder(oracle.config_from(cfg), w.rounded(sh.SH_DTYPE_F16), threads=16)
