@@ -477,6 +477,12 @@ int main(int argc, char **argv) {
     const float temperature = (float)fl.f("temperature");
 
     const int steps = (int)fl.i("bench-steps");
+    // Any bench mode may first time the library's plain copy kernel: a known byte count for
+    // scaling the profiler's traffic counters, and the achievable HBM bandwidth.
+    double copy_ms = 0, copy_gbs = 0;
+    const long long copy_bytes = steps > 0 ? fl.i("copy-calibrate") : 0;
+    if (copy_bytes > 0 && sh_copy_calibrate((size_t)copy_bytes, 5, &copy_ms, &copy_gbs))
+        fatalf("copy calibrate: %s", lib_error());
     if (steps > 0 && batch > 0) {
         // Batched greedy decode timing: B prompts of prompt-len ids, max-new steps each.
         const int plen = (int)fl.i("prompt-len");
@@ -567,10 +573,6 @@ int main(int argc, char **argv) {
     }
     if (steps > 0) {
         // Greedy decode timing for bench harnesses: W untimed runs, then K timed ones.
-        double copy_ms = 0, copy_gbs = 0;
-        const long long copy_bytes = fl.i("copy-calibrate");
-        if (copy_bytes > 0 && sh_copy_calibrate((size_t)copy_bytes, 5, &copy_ms, &copy_gbs))
-            fatalf("copy calibrate: %s", lib_error());
         for (int i = 0; i < fl.i("bench-warmup"); i++) decode(m, c, prompt, max_new, 0.f, rng);
         std::vector<double> gpu_ms, bytes, pre_ms;
         std::vector<long long> fwd, gen;

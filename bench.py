@@ -4,8 +4,10 @@
 One step = one full greedy Decode (ane/stories/infer.go:136-202) of the synthetic workload:
 Stories110M shape (12 layers, dim 768, 12 heads, SwiGLU 2048, vocab 32000), N(0, 0.02)
 weights from seed 0 stored as fp16 and resident in HBM, a 16-id prompt from seed 1, 128 new
-tokens (143 token forwards). `value` is generated tokens per second of wall time over the
-timed steps, as cmd/stories-generate-go/main.go:54-58 counts them.
+tokens: the prompt's first 15 positions fill the KV cache in one full-sequence forward, then
+one k_decode_persistent launch runs the 128 token forwards. `value` is generated tokens per
+second of wall time over the timed steps, as cmd/stories-generate-go/main.go:54-58 counts
+them.
 
 The GPU leg runs in the C++ host program (ane-training-experiments_amd/stories-generate
 -bench-steps K -bench-warmup W), a child process; it times the K steps with a steady clock
@@ -15,8 +17,10 @@ library's stream (sh_stats). This process touches no GPU.
 The JSON line also carries:
   roofline      the dominant kernel, k_decode_persistent (one launch runs a whole decode):
                 algorithmic bytes per launch (the sum over its token forwards of weights,
-                norms, KV rows read and written, logits) divided by the launch's device time,
-                against the 8 TB/s HBM peak. `traffic` is the HBM bytes per launch from the
+                norms, KV rows read and written, logits) divided by the launch's device time
+                (each decode's HIP-event time less its prompt forward, reported as
+                prompt_forward_ms), against the 8 TB/s HBM peak. `traffic` is the HBM bytes
+                per launch from the
                 profiler's FETCH_SIZE and WRITE_SIZE counters, each scaled by what the same
                 counter reads over a plain copy kernel of known size (figures kept in
                 profiles/, null when absent); `copy_gbs` is that copy kernel's bandwidth
@@ -57,13 +61,15 @@ HBM_PEAK_GBS = 8000.0
 PROMPT_LEN, NEW_TOKENS = 16, 128
 COPY_BYTES = 1 << 30
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_decode_persistent_stories110m_traffic.json")
+TRAFFIC_W8A8 = os.path.join(ROOT, "profiles", "k_decode_persistent_w8a8_stories110m_traffic.json")
+TRAFFIC_QWEN = os.path.join(ROOT, "profiles", "k_decode_persistent_qwen3_traffic.json")
 
 
-def traffic_per_launch():
+def traffic_per_launch(path=TRAFFIC_FILE):
     """HBM bytes per k_decode_persistent launch from the committed counter figures: each
-    counter's KiB per dispatch times (known copy bytes / the counter's KiB over the copy)."""
+    counter's value per dispatch times (known copy bytes / the counter's value over the copy)."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             t = json.load(f)
         fetch = t["kernel"]["FETCH_SIZE_kib"] * t["copy"]["bytes_read"] / t["copy"]["FETCH_SIZE_kib"]
         write = t["kernel"]["WRITE_SIZE_kib"] * t["copy"]["bytes_written"] / t["copy"]["WRITE_SIZE_kib"]
@@ -148,7 +154,7 @@ def host_threads():
     return max(1, min(16, os.cpu_count() or 1))
 
 
-def decode_line(r, steps, metric, workload, dtype, data, config, cpu):
+def decode_line(r, steps, metric, workload, dtype, data, config, cpu, traffic_file=None):
     """JSON line of a greedy-decode workload measured by the host program's -bench-steps."""
     gen_tokens = sum(r["generated"])
     forwards = sum(r["forwards"])
@@ -171,7 +177,8 @@ def decode_line(r, steps, metric, workload, dtype, data, config, cpu):
             "kernel": ("k_decode_persistent (one launch = one whole decode)" if persistent
                        else "per-stage decode kernels (all launches of one decode)"),
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_per_launch(traffic_file) if persistent and traffic_file else None,
             "bytes_per_launch": round(bytes_launch), "launch_ms": round(launch_ms, 4),
             "forwards_per_launch": forwards // steps,
             "us_per_forward": round(gpu_ms * 1e3 / max(forwards, 1), 3),
@@ -209,7 +216,7 @@ def workload_w8a8(args):
                        "synthetic: N(0,0.02) weights seed 0, per-row int8 + fp32 scales, 16-id prompt seed 1",
                        {"layers": 12, "dim": 768, "vocab": 32000, "batch": 1, "prompt_tokens": PROMPT_LEN,
                         "new_tokens": NEW_TOKENS, "kv_cache": "fp32", "parallelism": "none (1 GPU)"},
-                       None if args.no_cpu_baseline else cpu)
+                       None if args.no_cpu_baseline else cpu, TRAFFIC_W8A8)
 
 
 QWEN_PROMPT, QWEN_NEW, QWEN_CPU_NEW = 32, 256, 4
@@ -244,7 +251,7 @@ def workload_qwen_decode(args):
                        {"layers": 28, "dim": 1024, "heads": 16, "kv_heads": 8, "head_dim": 128,
                         "hidden": 3072, "vocab": 151936, "batch": 1, "prompt_tokens": QWEN_PROMPT,
                         "new_tokens": QWEN_NEW, "kv_cache": "bf16", "parallelism": "none (1 GPU)"},
-                       None if args.no_cpu_baseline else cpu)
+                       None if args.no_cpu_baseline else cpu, TRAFFIC_QWEN)
 
 
 PREFILL_S = 256
@@ -423,7 +430,10 @@ def main() -> int:
     steps = r["steps"]
     gen_tokens = sum(r["generated"])
     forwards = sum(r["forwards"])
-    gpu_ms = sum(r["gpu_ms"])
+    # each decode's device time = the prompt's cache-filling forward (full-sequence kernels)
+    # + the token loop (one k_decode_persistent launch); the roofline is the launch's
+    prefill_ms = sum(r.get("prefill_ms", [0.0] * steps))
+    gpu_ms = sum(r["gpu_ms"]) - prefill_ms
     bytes_total = sum(b * f for b, f in zip(r["bytes_per_forward_mean"], r["forwards"]))
     wall = r["wall_s"]
     launch_ms = gpu_ms / steps
@@ -462,6 +472,7 @@ def main() -> int:
             "launch_ms": round(launch_ms, 4),
             "forwards_per_launch": forwards // steps,
             "us_per_forward": round(gpu_ms * 1e3 / max(forwards, 1), 3),
+            "prompt_forward_ms": round(prefill_ms / steps, 4),
             "copy_gbs": round(r["copy_gbs"], 1),
         },
     }
