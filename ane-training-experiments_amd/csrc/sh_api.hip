@@ -582,6 +582,7 @@ void sh_model_destroy(sh_model *m) {
     if (m->bt_ready) (void)hipGraphExecDestroy(m->bt_exec);
     (void)hipFree(m->bt_arena);
     if (m->wd_ready) (void)hipGraphExecDestroy(m->wd_exec);
+    if (m->pf_ready) (void)hipGraphExecDestroy(m->pf_exec);
     (void)hipFree(m->wd_arena);
     if (m->ev0) (void)hipEventDestroy(m->ev0);
     if (m->ev1) (void)hipEventDestroy(m->ev1);
@@ -925,8 +926,27 @@ int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *l
         !hip_ok(hipMemcpyAsync(m->pf_rowpos, rows.data() + seq, 4 * (size_t)seq, hipMemcpyHostToDevice, m->stream), "prefill rows") ||
         !hip_ok(hipMemcpyAsync(m->pf_rowseq, rows.data() + 2 * (size_t)seq, 4 * (size_t)seq, hipMemcpyHostToDevice, m->stream), "prefill rows"))
         return -1;
+    // the forward's ~110 kernels run as one captured graph, replayed while the length and
+    // the scratch stay the same
+    if (!m->pf_ready || m->pf_graph_seq != seq) {
+        if (m->pf_ready) (void)hipGraphExecDestroy(m->pf_exec);
+        m->pf_ready = false;
+        hipGraph_t g = nullptr;
+        if (!hip_ok(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal), "capture")) return -1;
+        const hipError_t e2 = enqueue_prefill(m, seq, seq, true, false);
+        const hipError_t e3 = hipStreamEndCapture(m->stream, &g);
+        if (!hip_ok(e2, "prefill") || !hip_ok(e3, "end capture")) {
+            if (g) (void)hipGraphDestroy(g);
+            return -1;
+        }
+        const hipError_t e4 = hipGraphInstantiate(&m->pf_exec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (!hip_ok(e4, "instantiate prefill")) return -1;
+        m->pf_ready = true;
+        m->pf_graph_seq = seq;
+    }
     if (!hip_ok(hipEventRecord(m->ev0, m->stream), "event")) return -1;
-    if (!hip_ok(enqueue_prefill(m, seq, seq, true, false), "prefill")) return -1;
+    if (!hip_ok(hipGraphLaunch(m->pf_exec, m->stream), "prefill")) return -1;
     if (!hip_ok(hipEventRecord(m->ev1, m->stream), "event")) return -1;
     const size_t n = (size_t)m->cfg.vocab * seq;
     if (!hip_ok(hipMemcpyAsync(logits_cf, m->pf_logits, sizeof(float) * n,

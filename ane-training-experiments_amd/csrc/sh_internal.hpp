@@ -139,6 +139,11 @@ struct sh_model {
     hipGraphExec_t wd_exec;                    // one captured step for window length wd_seq
     bool wd_ready;
     int wd_seq;
+    // sh_prefill_logits: the whole forward captured for pf_graph_seq rows (its kernels point
+    // into the prefill scratch, so reallocating that drops it)
+    hipGraphExec_t pf_exec;
+    bool pf_ready;
+    int pf_graph_seq;
 };
 
 namespace sh {

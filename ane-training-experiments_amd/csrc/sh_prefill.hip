@@ -1873,6 +1873,10 @@ hipError_t prefill_alloc(sh_model *m, int S, bool logits) {
         (void)hipGraphExecDestroy(m->wd_exec);
         m->wd_ready = false;
     }
+    if (m->pf_ready) {   // so does the captured forward
+        (void)hipGraphExecDestroy(m->pf_exec);
+        m->pf_ready = false;
+    }
     (void)hipFree(m->pf_arena);
     m->pf_arena = nullptr;
     m->pf_cap = 0;

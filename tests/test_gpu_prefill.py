@@ -81,6 +81,20 @@ def test_prefill_repeat_and_shrink(gpu):
     m.close()
 
 
+def test_prefill_graph_replays_match_oracle(gpu):
+    """The forward runs as one captured graph, replayed while the length stays the same:
+    three calls of one length with different ids, eager decode steps between them, each
+    against the oracle."""
+    cfg = tiny_config()
+    m, ocfg, ow = build(cfg, sh.SH_DTYPE_F16, seed=251, std=0.08, gains_seed=252)
+    for r in range(3):
+        toks = sh.synth_tokens(33, 253 + r, cfg.vocab)
+        compare(m, ocfg, ow, toks)
+        m.reset_cache()
+        m.eval_next_logits(int(toks[0]), 0)
+    m.close()
+
+
 def test_prefill_columns_match_kv_cache_decode(gpu):
     """Column t of the causal forward equals the KV-cache decode at position t (two GPU
     paths with different kernels), and both match the oracle."""
