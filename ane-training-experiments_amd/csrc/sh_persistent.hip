@@ -757,17 +757,20 @@ struct QkvMap {
 
 // Asynchronous copy of cached rows [0, rows) of one kv head into LDS (global_load_lds:
 // each lane moves 16 bytes; one wave instruction fills 1 KB of LDS). Row t of the head
-// starts at element base + t*stride; rows are RB bytes long and land contiguously.
-template <int RB>
+// starts at element base + t*stride; rows are RB bytes long and land contiguously. With SWZ
+// the 16-byte chunk c of row t lands in slot c ^ (t mod chunks per row): threads that each
+// read their own row chunk by chunk in order then hit distinct LDS banks.
+template <int RB, bool SWZ = false>
 __device__ __forceinline__ void kv_rows_to_lds(const uint8_t *cache, size_t base_bytes, size_t stride_bytes,
                                                int rows, uint8_t *lds) {
     constexpr int LPRW = RB / 16;            // lanes per row
     constexpr int RPI = 64 / LPRW;           // rows per wave instruction
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r_in = lane / LPRW, c_in = (lane % LPRW) * 16;
+    const int r_in = lane / LPRW, slot = lane % LPRW;
     for (int r0 = wave * RPI; r0 < rows; r0 += kPW * RPI) {
         const int r = r0 + r_in < rows ? r0 + r_in : r0;   // a spare lane re-reads a valid row
-        const uint8_t *g = cache + base_bytes + (size_t)r * stride_bytes + c_in;
+        const int c = SWZ ? slot ^ ((r0 + r_in) & (LPRW - 1)) : slot;   // chunk for this slot
+        const uint8_t *g = cache + base_bytes + (size_t)r * stride_bytes + c * 16;
         __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
                                          (__attribute__((address_space(3))) void *)(lds + (size_t)r0 * RB),
                                          16, 0, 0);
@@ -783,13 +786,14 @@ struct KvStage {
 };
 
 // Starts the asynchronous copy of kv head g's cached rows [0, min(pos, ROWS)) of layer l
-// into LDS. Issued at the start of the layer, so it overlaps the qkv stage.
-template <int KVT, int HD>
+// into LDS. Issued at the start of the layer, so it overlaps the qkv stage. KSWZ: the K rows
+// in the swizzled chunk order (kv_rows_to_lds), for the one-thread-per-row scores.
+template <int KVT, int HD, bool KSWZ = false>
 __device__ __forceinline__ void attn_prefetch(const PParams &p, int l, int g, int pos, uint8_t *kvlds) {
     using S = KvStage<KVT, HD>;
     const size_t lbase = (size_t)l * p.max_seq * p.kvdim + (size_t)g * HD;
     const int nst = pos < S::ROWS ? pos : S::ROWS;
-    kv_rows_to_lds<S::RB>((const uint8_t *)p.kcache, lbase * S::EB, (size_t)p.kvdim * S::EB, nst, kvlds);
+    kv_rows_to_lds<S::RB, KSWZ>((const uint8_t *)p.kcache, lbase * S::EB, (size_t)p.kvdim * S::EB, nst, kvlds);
     kv_rows_to_lds<S::RB>((const uint8_t *)p.vcache, lbase * S::EB, (size_t)p.kvdim * S::EB, nst,
                           kvlds + (size_t)S::ROWS * S::RB);
 }
@@ -892,7 +896,10 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
         kv_st<KVT>(p.kcache, lbase + (size_t)pos * p.kvdim + i, ks[i]);
         kv_st<KVT>(p.vcache, lbase + (size_t)pos * p.kvdim + i, vs[i]);
         if (pos < S::ROWS) {
-            kv_put<KVT>(kst + (size_t)pos * S::RB, i, ks[i]);
+            // EXACT: K rows sit in the swizzled chunk order (attn_prefetch<..., true>)
+            constexpr int NCH = S::RB / 16, EPC = 16 / S::EB;
+            const int ik = EXACT ? ((i / EPC) ^ (pos & (NCH - 1))) * EPC + i % EPC : i;
+            kv_put<KVT>(kst + (size_t)pos * S::RB, ik, ks[i]);
             kv_put<KVT>(vst + (size_t)pos * S::RB, i, vs[i]);
         }
     }
@@ -938,11 +945,11 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
         if (t < S::ROWS) {
             constexpr int NCH = S::RB / 16, EPC = 16 / S::EB;
             const SH_LDS u32x4 *row = (const SH_LDS u32x4 *)(kst + (size_t)t * S::RB);
+            const int swz = EXACT ? (t & (NCH - 1)) : 0;   // chunk c of the row sits in slot c ^ swz
 #pragma unroll 4
-            for (int c0 = 0; c0 < NCH; c0++) {
-                const int c = c0;
+            for (int c = 0; c < NCH; c++) {
                 float kf[EPC];
-                const u32x4 kv4 = row[c];
+                const u32x4 kv4 = row[c ^ swz];
                 kv_unpack16<KVT>(kv4, kf);
 #pragma unroll
                 for (int h = 0; h < kMaxGroup; h++) {
@@ -1007,12 +1014,27 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
         for (int k = tid; k < group * hd; k += kPB) {
             const int h = k / hd, ii = k % hd;
             const float *ph = sc + h * p.max_seq;
+            const SH_LDS float *phl = (const SH_LDS float *)ph;
             const int tl = pos < S::ROWS ? pos : S::ROWS - 1;
             float sum = 0.f;
-            // unrolled so the loads of eight positions issue ahead of their adds, which stay
-            // one after another in position order
-#pragma unroll 8
-            for (int t = 0; t <= tl; t++) sum = __fadd_rn(sum, __fmul_rn(ph[t], kv_get<KVT>(vst + (size_t)t * S::RB, ii)));
+            // One wave does this chain for all 64 dims of a head, so it is bound by the wave's
+            // instruction issue: four positions per trip, each a read of p, a read of v, a
+            // rounded product and a rounded sum; the reads of a trip issue together at fixed
+            // offsets from one address, the adds stay in position order.
+            const SH_LDS uint8_t *vcol = vst + (size_t)ii * S::EB;
+            int t = 0;
+#pragma unroll 2
+            for (; t + 4 <= tl + 1; t += 4) {
+                float pp[4], vv[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    pp[u] = phl[t + u];
+                    vv[u] = kv_get<KVT>(vcol + (size_t)(t + u) * S::RB, 0);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) sum = __fadd_rn(sum, __fmul_rn(pp[u], vv[u]));
+            }
+            for (; t <= tl; t++) sum = __fadd_rn(sum, __fmul_rn(phl[t], kv_get<KVT>(vcol + (size_t)t * S::RB, 0)));
 #pragma unroll 8
             for (int t = tl + 1; t <= pos; t++) {
                 const float vv = t == pos ? vs[ii] : kv_ld<KVT>(p.vcache, lbase + (size_t)t * p.kvdim + ii);
@@ -1332,7 +1354,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
         auto layer = [&](int l) -> bool {
             const uint32_t e = base + (uint32_t)l + 1;
             const LayerPtrs Lp = layer_ptrs(p.layers, l);
-            if ((int)blockIdx.x < p.KVH) attn_prefetch<KVT, HD>(p, l, blockIdx.x, pos, kvlds);
+            if ((int)blockIdx.x < p.KVH) attn_prefetch<KVT, HD, WT == SH_DTYPE_W8A8>(p, l, blockIdx.x, pos, kvlds);
             StageIO io{};
             StageCtx c{};
             int r;
