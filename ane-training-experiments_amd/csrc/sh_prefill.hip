@@ -1781,7 +1781,9 @@ GemmPlan gemm_plan(int M, int N, int K) {
     p.big = (M >= 1024 || (M >= 256 && N >= 16384)) && N % 128 == 0;
     const int tiles = p.big ? ((M + 127) / 128) * (N / 128) : ((M + 63) / 64) * (N / 64);
     p.ranges = 1;
-    for (int r : {2, 3, 4, 6, 8, 12, 16})
+    // at most four K ranges: each more range adds a [M, N] fp32 partial for the row kernel
+    // that sums them to read back (the S = 256 forward was fastest with four)
+    for (int r : {2, 3, 4})
         if (K % (32 * r) == 0 && K / r >= 256 && tiles * r <= 768) p.ranges = r;
     if (tiles >= 512) p.ranges = 1;
     p.kc = K / p.ranges;

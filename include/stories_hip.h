@@ -65,7 +65,10 @@ typedef struct sh_timing {
     double bytes_per_forward_mean; /* algorithmic bytes per forward, averaged */
     int32_t persistent;     /* 1: the persistent decode kernel ran; 0: per-stage kernels */
     int32_t grid;           /* workgroups of the persistent kernel */
-    double prefill_ms;      /* sh_batch_greedy_decode: device time of the prompt prefill */
+    double prefill_ms;      /* device time of the prompt's full-sequence forward: part of
+                               gpu_ms for sh_greedy_decode (fp16/bf16) and
+                               sh_prefill_logits, apart from it for sh_batch_greedy_decode
+                               (whose gpu_ms is the decode steps); 0 if none */
 } sh_timing;
 
 /* ---- library ------------------------------------------------------------------------ */
@@ -113,7 +116,9 @@ int sh_decode_step(sh_model *m, int32_t token, int32_t pos, float *logits,
  * prompt (last max_seq ids; [BOS] if empty), generates up to max_new tokens (64 if <= 0),
  * stops after EOS=2 or at max_seq tokens. out_tokens (capacity max_seq) receives prompt +
  * generated ids, *n_out their count, *stopped_eos whether EOS ended the loop. The whole
- * loop runs on the device; the host sees only the final ids. */
+ * loop runs on the device; the host sees only the final ids. fp16/bf16 models compute the
+ * prompt's first n-1 positions in one full-sequence forward that fills the cache as the
+ * token-by-token feed would; sh_stats then counts only the forwards after it. */
 int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32_t max_new,
                      int32_t *out_tokens, int32_t *n_out, int32_t *stopped_eos);
 /* (*Engine).EvalLogits (ane/storiesane/engine.go:363-376) = evalLogitsCPUInto
