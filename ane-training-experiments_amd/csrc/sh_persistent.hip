@@ -201,13 +201,16 @@ __device__ __forceinline__ bool block_and(bool ok) {
     return r;
 }
 
-__device__ __forceinline__ float block_max_d(float v, double *red) {
+// Workgroup maximum in one barrier, through an array of its own: the next write to it comes
+// after the next stage's barriers, when every thread has read this one.
+__device__ __forceinline__ float block_max(float v) {
+    __shared__ float wmx[kPW];
     v = wmax<64>(v);
+    if ((threadIdx.x & 63) == 0) wmx[threadIdx.x >> 6] = v;
     lds_barrier();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = (double)v;
-    lds_barrier();
-    float m = (float)red[0];
-    for (int w = 1; w < kPW; w++) m = fmaxf(m, (float)red[w]);
+    float m = wmx[0];
+#pragma unroll
+    for (int w = 1; w < kPW; w++) m = fmaxf(m, wmx[w]);
     return m;
 }
 
@@ -491,7 +494,7 @@ __device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &ma
                 mx = fmaxf(mx, fabsf(val[k]));
             }
         }
-        mx = block_max_d(mx, red);   // two barriers; the second also orders the okw reads
+        mx = block_max(mx);
         float s = __fdiv_rn(mx, 127.0f);
         if (s == 0.0f) s = 1.0f;
         *sa = s;
