@@ -371,8 +371,11 @@ static void apply_rope(const or_decoder *d, float *vec, int n_heads, int pos) {
     }
 }
 
-/* infer.go:273-299 attend; q head h reads kv head h / (H/KVH) (io.h:437-457 mapping) */
-static void attend(or_decoder *d, int layer, int pos) {
+/* infer.go:273-299 attend; q head h reads kv head h / (H/KVH) (io.h:437-457 mapping).
+ * q, att, scores and probs are the caller's (the decoder's own vectors for forwardOne, one
+ * token's rows and per-thread buffers for the prompt pass). */
+static void attend_into(const or_decoder *d, int layer, int pos, const float *q, float *att,
+                        float *scores, float *probs) {
     const or_config *c = &d->cfg;
     int hd = d->hd;
     int group = c->n_heads / c->n_kv_heads;
@@ -383,19 +386,23 @@ static void attend(or_decoder *d, int layer, int pos) {
         for (int t = 0; t <= pos; t++) {
             const float *kr = d->kc + ((size_t)layer * c->max_seq + t) * d->kvdim + kb0;
             float dot = 0;
-            for (int i = 0; i < hd; i++) dot += d->q[qb + i] * kr[i];
-            d->scores[t] = dot * inv_sqrt_hd;
+            for (int i = 0; i < hd; i++) dot += q[qb + i] * kr[i];
+            scores[t] = dot * inv_sqrt_hd;
         }
-        or_softmax_prefix(d->probs, d->scores, pos + 1);
+        or_softmax_prefix(probs, scores, pos + 1);
         for (int i = 0; i < hd; i++) {
             float sum = 0;
             for (int t = 0; t <= pos; t++) {
                 const float *vr = d->vc + ((size_t)layer * c->max_seq + t) * d->kvdim + kb0;
-                sum += d->probs[t] * vr[i];
+                sum += probs[t] * vr[i];
             }
-            d->att[qb + i] = sum;
+            att[qb + i] = sum;
         }
     }
+}
+
+static void attend(or_decoder *d, int layer, int pos) {
+    attend_into(d, layer, pos, d->q, d->att, d->scores, d->probs);
 }
 
 /* infer.go:204-245 forwardOne */
@@ -447,6 +454,162 @@ int or_forward_one(or_decoder *d, int token, int pos, float *logits_out) {
     return 0;
 }
 
+/* matVec (infer.go:313-322) for n tokens at once: out[t*rows + r] = sum over c in order of
+ * mat[r*cols + c] * in[t*cols + c]. Eight tokens ride in the lanes of two 4-float vectors,
+ * so each lane adds its own token's products in the reference order (multiply, then add:
+ * -ffp-contract=off keeps them apart), and four weight rows share each block of tokens. */
+typedef float or_v4 __attribute__((vector_size(16)));
+
+static void mat_tokens(float *out, const float *mat, const float *in, int rows, int cols, int n,
+                       int threads) {
+    int nb = (n + 7) / 8;
+    or_v4 *xt = (or_v4 *)aligned_alloc(16, sizeof(or_v4) * 2 * (size_t)cols * nb);
+    float *xf = (float *)xt;
+    for (int b = 0; b < nb; b++)
+        for (int c = 0; c < cols; c++)
+            for (int j = 0; j < 8; j++) {
+                int t = b * 8 + j;
+                xf[((size_t)b * cols + c) * 8 + j] = t < n ? in[(size_t)t * cols + c] : 0.0f;
+            }
+    int groups = (rows + 3) / 4;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int g = 0; g < groups; g++) {
+        int r0 = g * 4, nr = rows - r0 < 4 ? rows - r0 : 4;
+        const float *w[4];
+        for (int i = 0; i < 4; i++) w[i] = mat + (size_t)(r0 + (i < nr ? i : 0)) * cols;
+        for (int b = 0; b < nb; b++) {
+            const or_v4 *x = xt + (size_t)b * cols * 2;
+            or_v4 s[4][2];
+            memset(s, 0, sizeof(s));
+            for (int c = 0; c < cols; c++) {
+                or_v4 x0 = x[2 * c], x1 = x[2 * c + 1];
+                for (int i = 0; i < 4; i++) {
+                    float wv = w[i][c];
+                    or_v4 wb = {wv, wv, wv, wv};
+                    s[i][0] += wb * x0;
+                    s[i][1] += wb * x1;
+                }
+            }
+            for (int i = 0; i < nr; i++)
+                for (int j = 0; j < 8 && b * 8 + j < n; j++)
+                    out[(size_t)(b * 8 + j) * rows + r0 + i] = s[i][j >> 2][j & 3];
+        }
+    }
+    free(xt);
+}
+
+/* or_mat_vec_w8a8 for n tokens: each token's activation quantized on its own, then the exact
+ * int32 dot per row and y = (float)acc * (s_w[r] * s_a[t]). */
+static void mat_tokens_w8a8(float *out, const int8_t *wq, const float *wscale, const float *in,
+                            int rows, int cols, int n, int threads) {
+    int8_t *qa = (int8_t *)malloc((size_t)n * cols);
+    float *sa = (float *)malloc(sizeof(float) * (size_t)n);
+    for (int t = 0; t < n; t++)
+        or_quantize_tensor(in + (size_t)t * cols, (size_t)cols, qa + (size_t)t * cols, &sa[t]);
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int r = 0; r < rows; r++) {
+        const int8_t *row = wq + (size_t)r * cols;
+        for (int t = 0; t < n; t++) {
+            const int8_t *a = qa + (size_t)t * cols;
+            int32_t acc = 0;
+            for (int c = 0; c < cols; c++) acc += (int32_t)row[c] * (int32_t)a[c];
+            out[(size_t)t * rows + r] = (float)acc * (wscale[r] * sa[t]);
+        }
+    }
+    free(qa);
+    free(sa);
+}
+
+static void project_tokens(const or_decoder *d, int l, int p, float *out, const float *in,
+                           int n) {
+    int rows, cols;
+    mat_shape(d, p, &rows, &cols);
+    if (d->cfg.w8a8)
+        mat_tokens_w8a8(out, d->q8[l][p], d->s8[l][p], in, rows, cols, n, d->threads);
+    else
+        mat_tokens(out, layer_mat(&d->layers[l], p), in, rows, cols, n, d->threads);
+}
+
+/* The prompt part of Decode (infer.go:136-202 feeds the prompt ids to forwardOne one
+ * position at a time) with the loops turned layer-major: tokens[0, n) at positions
+ * pos0 .. pos0+n-1. Every token gets forwardOne's values at its position: the same ordered
+ * float32 sums, RMSNorms, RoPE and K/V rounding, and attention over the positions up to its
+ * own, whose K/V the layer pass has stored before any token of it attends. The K/V cache it
+ * leaves and the last token's logits therefore equal those of n calls of or_forward_one, bit
+ * for bit. The classifier runs for the last token only; the taps are not updated. */
+int or_prompt_forward(or_decoder *d, const int32_t *tokens, int n, int pos0, float *logits_out) {
+    const or_config *c = &d->cfg;
+    if (n <= 0 || pos0 < 0 || pos0 + n > c->max_seq) return -1;
+    for (int t = 0; t < n; t++)
+        if (tokens[t] < 0 || tokens[t] >= c->vocab) return -1;
+    int D = c->dim, F = c->hidden, hd = d->hd, qd = d->qdim, kvd = d->kvdim;
+    int thr = d->threads;
+    float alpha = c->residual_scale;
+    size_t N = (size_t)n;
+    float *x = (float *)malloc(sizeof(float) * N * D);
+    float *xn = (float *)malloc(sizeof(float) * N * D);
+    float *q = (float *)malloc(sizeof(float) * N * qd);
+    float *k = (float *)malloc(sizeof(float) * N * kvd);
+    float *v = (float *)malloc(sizeof(float) * N * kvd);
+    float *att = (float *)malloc(sizeof(float) * N * qd);
+    float *x2 = (float *)malloc(sizeof(float) * N * D);
+    float *h1 = (float *)malloc(sizeof(float) * N * F);
+    float *h3 = (float *)malloc(sizeof(float) * N * F);
+    for (int t = 0; t < n; t++)
+        memcpy(x + (size_t)t * D, d->embed + (size_t)tokens[t] * D, sizeof(float) * D);
+    for (int l = 0; l < c->n_layers; l++) {
+        const or_layer *L = &d->layers[l];
+        for (int t = 0; t < n; t++)
+            or_rms_norm_vec(xn + (size_t)t * D, x + (size_t)t * D, L->rms_att, D, c->norm_eps);
+        project_tokens(d, l, P_WQ, q, xn, n);
+        project_tokens(d, l, P_WK, k, xn, n);
+        project_tokens(d, l, P_WV, v, xn, n);
+        for (int t = 0; t < n; t++) {
+            float *qt = q + (size_t)t * qd, *kt = k + (size_t)t * kvd, *vt = v + (size_t)t * kvd;
+            if (c->qk_norm) {
+                for (int h = 0; h < c->n_heads; h++)
+                    or_rms_norm_vec(qt + h * hd, qt + h * hd, L->q_norm, hd, c->qk_norm_eps);
+                for (int h = 0; h < c->n_kv_heads; h++)
+                    or_rms_norm_vec(kt + h * hd, kt + h * hd, L->k_norm, hd, c->qk_norm_eps);
+            }
+            apply_rope(d, qt, c->n_heads, pos0 + t);
+            apply_rope(d, kt, c->n_kv_heads, pos0 + t);
+            size_t base = ((size_t)l * c->max_seq + pos0 + t) * kvd;
+            for (int i = 0; i < kvd; i++) {
+                d->kc[base + i] = kv_round(c->kv_dtype, kt[i]);
+                d->vc[base + i] = kv_round(c->kv_dtype, vt[i]);
+            }
+        }
+#pragma omp parallel num_threads(thr)
+        {
+            float *sc = (float *)malloc(sizeof(float) * c->max_seq);
+            float *pr = (float *)malloc(sizeof(float) * c->max_seq);
+#pragma omp for schedule(dynamic, 4)
+            for (int t = 0; t < n; t++)
+                attend_into(d, l, pos0 + t, q + (size_t)t * qd, att + (size_t)t * qd, sc, pr);
+            free(sc);
+            free(pr);
+        }
+        project_tokens(d, l, P_WO, x2, att, n);
+        for (size_t i = 0; i < N * D; i++) x2[i] = x[i] + alpha * x2[i];
+        for (int t = 0; t < n; t++)
+            or_rms_norm_vec(xn + (size_t)t * D, x2 + (size_t)t * D, L->rms_ffn, D, c->norm_eps);
+        project_tokens(d, l, P_W1, h1, xn, n);
+        project_tokens(d, l, P_W3, h3, xn, n);
+        for (size_t i = 0; i < N * F; i++) h1[i] = or_silu(h1[i]) * h3[i];
+        project_tokens(d, l, P_W2, x, h1, n);
+        for (size_t i = 0; i < N * D; i++) x[i] = x2[i] + alpha * x[i];
+    }
+    or_rms_norm_vec(d->xn, x + (N - 1) * D, d->rms_final, D, c->norm_eps);
+    if (c->w8a8)
+        or_mat_vec_w8a8(d->logits, d->cls8, d->cls_s, d->xn, c->vocab, D, thr);
+    else
+        or_mat_vec(d->logits, d->cls, d->xn, c->vocab, D, thr);
+    if (logits_out) memcpy(logits_out, d->logits, sizeof(float) * c->vocab);
+    free(x); free(xn); free(q); free(k); free(v); free(att); free(x2); free(h1); free(h3);
+    return 0;
+}
+
 const float *or_decoder_tap(const or_decoder *d, int which) {
     switch (which) {
     case 0: return d->x;
@@ -485,8 +648,7 @@ int or_greedy_decode(or_decoder *d, const int32_t *prompt, int n_prompt, int max
     or_decoder_reset(d);
     int n = 0;
     for (int i = 0; i < n_prompt; i++) out_tokens[n++] = prompt[i];
-    for (int pos = 0; pos < n_prompt - 1; pos++)
-        if (or_forward_one(d, prompt[pos], pos, NULL)) return -1;
+    if (n_prompt > 1 && or_prompt_forward(d, prompt, n_prompt - 1, 0, NULL)) return -1;
     *stopped_eos = 0;
     for (int step = 0; step < max_new && n < c->max_seq; step++) {
         int pos = n - 1;

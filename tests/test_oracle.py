@@ -347,6 +347,36 @@ def test_kv_cache_decode_equals_causal_prefill():
         np.testing.assert_allclose(dec.forward_one(int(tok), t), cf[:, t], atol=1e-5)
 
 
+@pytest.mark.parametrize("gqa,w8a8,kv", [(False, False, sh.SH_KV_F32), (True, False, sh.SH_KV_BF16),
+                                         (False, True, sh.SH_KV_F16), (True, True, sh.SH_KV_F32)])
+def test_prompt_pass_equals_forward_one_bitwise(gqa, w8a8, kv):
+    """The layer-major prompt pass (or_prompt_forward, which the oracle's greedy decode uses
+    for the prompt) against forwardOne called per position: the same logits and the same
+    K/V cache, bit for bit, so the next forwardOne after either gives identical logits. An
+    odd hidden size leaves a partial four-row group, 27 tokens a partial eight-token block,
+    and a second pass starting at position 27 checks pos0 > 0."""
+    mk = tiny_gqa_config if gqa else tiny_config
+    cfg = mk(kv_dtype=kv, hidden=250)
+    w = random_gains(sh.synth_weights(cfg, seed=84, std=0.08), 85)
+    oc = oracle.config_from(cfg, w8a8=w8a8)
+    toks = sh.synth_tokens(40, 86, cfg.vocab)
+    one, turned = oracle.Decoder(oc, w, threads=3), oracle.Decoder(oc, w, threads=2)
+    for t in range(27):
+        a = one.forward_one(int(toks[t]), t)
+    b = turned.prompt_forward(toks[:27])
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for t in range(27, 39):
+        a = one.forward_one(int(toks[t]), t)
+    b = turned.prompt_forward(toks[27:39], pos0=27)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    a, b = one.forward_one(int(toks[39]), 39), turned.forward_one(int(toks[39]), 39)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    with pytest.raises(ValueError):
+        turned.prompt_forward(toks[:30], pos0=cfg.max_seq - 29)
+    one.close()
+    turned.close()
+
+
 def test_w8a8_decoder_tracks_fp32():
     cfg = tiny_config()
     w = sh.synth_weights(cfg, seed=91, std=0.08)
