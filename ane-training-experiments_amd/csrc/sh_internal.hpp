@@ -110,6 +110,8 @@ struct sh_model {
     float *pf_q, *pf_k, *pf_v;                 // roped q, k and v: [S,qdim] [S,kvdim] x2
     float *pf_cf;                              // [D,S] channel-first staging of the seams
     uint16_t *pf_xn, *pf_att, *pf_gate;        // GEMM operands: hi plane, then lo plane
+    int8_t *pf_a8;                             // W8A8: A operand quantized per row [S, <= 4096]
+    float *pf_sa;                              //       and its row scales [S]
     float *tap_buf;                            // layer taps: channel-first outputs + [S, 2F]
     size_t tap_cap;                            // elements of tap_buf
 
@@ -125,6 +127,8 @@ struct sh_model {
     size_t bt_part_cap;                        // elements of bt_part
     float *bt_apv;                             // argmax partials (value, index)
     int32_t *bt_api;
+    int8_t *bt_a8;                             // W8A8: quantized A operand [B, <= 4096]
+    float *bt_sa;                              //       and its row scales [B]
     hipGraphExec_t bt_exec;                    // one captured step for bt_graph_b sequences
     bool bt_ready;
     int bt_graph_b;

@@ -50,8 +50,15 @@ __device__ __forceinline__ uint16_t f_to_bits(float f, int dt) {
 }
 
 // Writes v as a GEMM operand: the hi plane at idx, the lo plane `plane` elements further.
+// W8A8 models carry the operand as fp32 instead (element idx of the same buffer viewed as
+// float, whose 2 * plane 16-bit slots hold exactly `plane` floats): the per-row quantizer
+// then sees the value itself, as the reference's quantizer does.
 __device__ __forceinline__ void store_op(uint16_t *base, size_t idx, size_t plane, float v,
                                          int dt) {
+    if (dt == SH_DTYPE_W8A8) {
+        ((float *)base)[idx] = v;
+        return;
+    }
     const uint16_t hi = f_to_bits(v, dt);
     base[idx] = hi;
     base[plane + idx] = f_to_bits(v - bits_to_f(hi, dt), dt);
@@ -139,11 +146,13 @@ __global__ __launch_bounds__(kT) void k_cf_gather(const float *src, int S, int n
     dst[i] = src[(size_t)t * ncols + col0 + (size_t)c * cstep];
 }
 
-// fp32 value of operand planes: hi + lo (hi at i, lo `plane` further).
+// fp32 value of operand planes: hi + lo (hi at i, lo `plane` further); W8A8: the fp32 operand.
 __global__ __launch_bounds__(kT) void k_planes_f32(const uint16_t *in, size_t n, size_t plane, int dt,
                                                    float *out) {
     const size_t i = (size_t)blockIdx.x * kT + threadIdx.x;
-    if (i < n) out[i] = bits_to_f(in[i], dt) + bits_to_f(in[plane + i], dt);
+    if (i < n)
+        out[i] = dt == SH_DTYPE_W8A8 ? ((const float *)in)[i]
+                                     : bits_to_f(in[i], dt) + bits_to_f(in[plane + i], dt);
 }
 
 enum { G_STORE = 0, G_RESID = 1, G_GATE = 2, G_LOGITS_CF = 3 };
@@ -160,6 +169,11 @@ struct GemmArgs {
     int dt;
     int decode_forms;    // G_GATE: 1 = infer.go:324-326 silu, 0 = accel_other.go:128-133
     int partial_only;    // skinny GEMM: always leave K-range partials, no epilogue
+    // W8A8 models: B holds int8 rows with fp32 row scales sw [N]; A is the fp32 operand
+    // [M, K], which the product quantizes per row into a8 [M, K] with scales sa [M] first
+    const float *sw;
+    int8_t *a8;
+    float *sa;
 };
 
 // silu(h1) * h3: decode form x / (1 + float32(exp(-x))) (infer.go:324-326), or the
@@ -370,6 +384,187 @@ __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, i
     tile_out<FM, FN>(g, partial, acc, m0 + wm, n0 + wn, lane);
 }
 
+// ---- W8A8 products on the int8 matrix cores --------------------------------------------
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// The bridge quantizer for one value (ane_bridge.m:386-396): x / scale with IEEE division,
+// clamp to [-128, 127], round half away from zero by +-0.5 and truncation.
+__device__ __forceinline__ int8_t quant_i8(float x, float scale) {
+    float v = __fdiv_rn(x, scale);
+    v = fminf(fmaxf(v, -128.0f), 127.0f);
+    return (int8_t)(int)(v >= 0.0f ? v + 0.5f : v - 0.5f);
+}
+
+// Per-token activation quantization: the bridge formula (ane_bridge.m:374-399) applied to
+// each row on its own, as the W8A8 decode quantizes its one token. Row m of the fp32 A
+// operand [M, K] -> int8 row m of a8 and sa[m] = max|x| / 127 (0 -> 1), q = quantize(x / sa[m]).
+__global__ __launch_bounds__(kT) void k_quant_rows_i8(const float *x, int K, int8_t *a8,
+                                                       float *sa) {
+    __shared__ float red[kT / 64];
+    const int m = blockIdx.x;
+    const float *row = x + (size_t)m * K;
+    float mx = 0.f;
+    for (int i = threadIdx.x; i < K; i += kT) mx = fmaxf(mx, fabsf(row[i]));
+    mx = wmax<64>(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kT / 64; w++) mx = fmaxf(mx, red[w]);
+    float scale = __fdiv_rn(mx, 127.0f);
+    if (scale == 0.0f) scale = 1.0f;
+    for (int i = threadIdx.x; i < K; i += kT) a8[(size_t)m * K + i] = quant_i8(row[i], scale);
+    if (threadIdx.x == 0) sa[m] = scale;
+}
+
+// W8A8 causal attention in the decode's float order (infer.go:273-299 attend with the
+// softmaxPrefix of infer.go:328-345), so the attention output the Wo quantizer sees is the
+// W8A8 decode's: per (row t, head h) workgroup, score j = (sum over i in order of
+// q[i] * k[j][i]) * (1 / sqrt(hd)) for the keys j <= rowpos[t] of the row's sequence, their
+// float maximum, e_j = float(exp(double(s_j - max))), the float64 sum of the e_j in key order,
+// p_j = e_j * float(1 / sum), and att[i] = sum over j in key order of p_j * v[j][i]. Keys are
+// the rows t - rowpos[t] .. t of the token-major k / v arrays (values already rounded to the
+// cache type) or, with from_cache, rows 0 .. rowpos[t] of the sequence's KV cache slab
+// (rowseq[t] * seq_stride elements in). att is the fp32 operand [rows, qdim].
+template <int KVT>
+__global__ __launch_bounds__(kT) void k_attn_exact(const float *q, int qdim, const void *kb,
+                                                   const void *vb, size_t seq_stride, int kvdim,
+                                                   int from_cache, const int32_t *rowpos,
+                                                   const int32_t *rowseq, int n_heads,
+                                                   int n_kv_heads, int hd, float inv_sqrt_hd,
+                                                   float *att) {
+    __shared__ float sc[kMaxSeqLds];
+    __shared__ float qs[256];
+    __shared__ float red[kT / 64];
+    __shared__ float inv_s;
+    const int t = blockIdx.x, h = blockIdx.y;
+    const int pos = rowpos[t], L = pos + 1;
+    const int g = h / (n_heads / n_kv_heads);
+    const size_t r0 = (from_cache ? (size_t)rowseq[t] * seq_stride : (size_t)(t - pos) * kvdim) + (size_t)g * hd;
+    auto kv = [&](const void *base, int j, int i) -> float {
+        const size_t o = r0 + (size_t)j * kvdim + i;
+        if constexpr (KVT == SH_KV_F32) return ((const float *)base)[o];
+        else return bits_to_f(((const uint16_t *)base)[o], KVT == SH_KV_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16);
+    };
+    for (int i = threadIdx.x; i < hd; i += kT) qs[i] = q[(size_t)t * qdim + (size_t)h * hd + i];
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < L; j += kT) {
+        float dot = 0.f;
+        for (int i = 0; i < hd; i++) dot += qs[i] * kv(kb, j, i);
+        const float sj = dot * inv_sqrt_hd;
+        sc[j] = sj;
+        mx = fmaxf(mx, sj);
+    }
+    mx = wmax<64>(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kT / 64; w++) mx = fmaxf(mx, red[w]);
+    for (int j = threadIdx.x; j < L; j += kT) sc[j] = (float)exp((double)(sc[j] - mx));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double sum = 0;
+        for (int j = 0; j < L; j++) sum += (double)sc[j];
+        inv_s = (float)(1.0 / sum);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int j = threadIdx.x; j < L; j += kT) sc[j] *= inv;
+    __syncthreads();
+    for (int i = threadIdx.x; i < hd; i += kT) {
+        float a = 0.f;
+        for (int j = 0; j < L; j++) a += sc[j] * kv(vb, j, i);
+        att[(size_t)t * qdim + (size_t)h * hd + i] = a;
+    }
+}
+
+// W8A8 projection: C[m, n] = (float)(sum over k of a8[m, k] * W[n, k]) * (sw[n] * sa[m]),
+// the int32 sum exact (or_mat_vec_w8a8's dequantization: the int32 dot product, then the
+// row scale times the activation scale). v_mfma_i32_16x16x64_i8 over 64 x 64 workgroup tiles
+// of 2 x 2 waves; K in steps of 64 (one 64-byte LDS row per tile row, padded to 80 bytes),
+// NB steps' loads issued per burst as in k_gemm_burst. A and W fragments are read with the
+// same lane pattern (row lane % 16, 16 bytes at k + 16 * (lane / 16)), so each MFMA sums
+// the same 64 products whatever the instruction's k order. No K split: one workgroup
+// finishes its tile and applies the epilogue (the same forms as the 16-bit GEMM).
+template <int BM, int BN, int NB>
+__global__ __launch_bounds__(kT) void k_gemm_i8(GemmArgs g) {
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+    constexpr int RS = 80;
+    constexpr int R = BM + BN;                   // tile rows: A, then W
+    constexpr int PER = R * 4 / kT;              // 16-byte chunks per thread per step
+    static_assert(kT == 256 && BM % 64 == 0 && BN % 64 == 0 && NB % 2 == 0,
+                  "64 rows per chunk index; bursts of even length");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][R * RS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int8_t *A = g.a8, *W = (const int8_t *)g.B;
+    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+    u32x4 stage[NB][PER];
+    i32x4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = i32x4{0, 0, 0, 0};
+    const int fr = lane & 15, fc = (lane >> 4) * 16;
+    for (int kb = 0; kb < g.K; kb += NB * 64) {
+        // chunk j of a thread: row 64*j + tid/4 of the tile (A rows, then W rows), 16 bytes
+        // at k + 16*(tid%4); A rows past M load row M-1 and are zeroed (no load under a branch)
+#pragma unroll
+        for (int st = 0; st < NB; st++) {
+            const int k = kb + st * 64 + (tid & 3) * 16;
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int rr = j * 64 + (tid >> 2);
+                if (j * 64 < BM) {
+                    const int m = m0 + rr;
+                    const u32x4 v = *(const u32x4 *)(A + (size_t)min(m, g.M - 1) * g.K + k);
+                    stage[st][j] = m < g.M ? v : zero;
+                } else {
+                    stage[st][j] = *(const u32x4 *)(W + (size_t)(n0 + rr - BM) * g.K + k);
+                }
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < NB; st++) {
+            uint8_t *L = lds[st & 1];
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int ci = tid + j * kT;
+                *(u32x4 *)(&L[(ci >> 2) * RS + (ci & 3) * 16]) = stage[st][j];
+            }
+            __syncthreads();
+            i32x4 bfr[FN];
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+                bfr[j] = __builtin_bit_cast(i32x4, *(const u32x4 *)(L + (BM + wn + j * 16 + fr) * RS + fc));
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                const i32x4 a = __builtin_bit_cast(i32x4, *(const u32x4 *)(L + (wm + i * 16 + fr) * RS + fc));
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bfr[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+    // D layout as the 16-bit GEMM's: lane holds column lane % 16, rows 4 * (lane / 16) + r
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int n = n0 + wn + j * 16 + (lane & 15);
+            const float sw = g.sw[n];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm + i * 16 + (lane >> 4) * 4 + r;
+                const float v = (float)acc[i][j][r] * (sw * g.sa[min(m, g.M - 1)]);
+                const float vr = __shfl_xor(v, 1, 64);   // column n ^ 1, same row
+                if (m < g.M) tile_epilogue(g, m, n, v, vr);
+            }
+        }
+}
+
 template <int KVT>
 __device__ __forceinline__ float kv_round(float v) {
     if constexpr (KVT == SH_KV_F32) return v;
@@ -400,6 +595,7 @@ struct QkRopeArgs {
     void *kcache, *vcache;
     size_t kv_seq_stride;
     int write_cache;
+    int round_kv;        // ko / vo rounded to the cache type even without a cache write
 };
 
 // Finishes row t held in LDS (q | k | v, qdim + 2*kvdim floats).
@@ -439,11 +635,11 @@ __device__ __forceinline__ void qk_rope_row(float *row, int t, const QkRopeArgs 
         } else if (i < qdim + kvdim) {
             const int j = i - qdim;
             if (a.write_cache) kv_store<KVT>(a.kcache, kv_row + j, v);
-            if (a.ko) a.ko[(size_t)t * kvdim + j] = a.write_cache ? kv_round<KVT>(v) : v;
+            if (a.ko) a.ko[(size_t)t * kvdim + j] = a.write_cache || a.round_kv ? kv_round<KVT>(v) : v;
         } else {
             const int j = i - qdim - kvdim;
             if (a.write_cache) kv_store<KVT>(a.vcache, kv_row + j, v);
-            if (a.vo) a.vo[(size_t)t * kvdim + j] = a.write_cache ? kv_round<KVT>(v) : v;
+            if (a.vo) a.vo[(size_t)t * kvdim + j] = a.write_cache || a.round_kv ? kv_round<KVT>(v) : v;
         }
     }
 }
@@ -1792,8 +1988,22 @@ GemmPlan gemm_plan(int M, int N, int K) {
 
 // ranges_out given: K-range partials are left for the caller's row kernel (*ranges_out > 1)
 // instead of being summed here; with one range the epilogue runs as usual.
+// W8A8 projection: the fp32 A rows quantized one by one, then the int8 product and its epilogue.
+hipError_t gemm_i8(const GemmArgs &g, hipStream_t s) {
+    if (g.K % 128 || g.N % 64 || g.M < 1 || !g.a8 || !g.sa || !g.sw) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_quant_rows_i8, dim3(g.M), dim3(kT), 0, s, (const float *)g.A, g.K, g.a8, g.sa);
+    const dim3 grid((g.M + 63) / 64, g.N / 64);
+    if ((g.K / 64) % 4 == 0) hipLaunchKernelGGL((k_gemm_i8<64, 64, 4>), grid, dim3(kT), 0, s, g);
+    else hipLaunchKernelGGL((k_gemm_i8<64, 64, 2>), grid, dim3(kT), 0, s, g);
+    return hipGetLastError();
+}
+
 hipError_t gemm(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipStream_t s,
                 int *ranges_out = nullptr) {
+    if (dt == SH_DTYPE_W8A8) {   // one K range: the epilogue runs in the product
+        if (ranges_out) *ranges_out = 1;
+        return gemm_i8(g, s);
+    }
     if (g.K % 32 || g.N % 64) return hipErrorInvalidValue;
     const GemmPlan p = gemm_plan(g.M, g.N, g.K);
     if (p.ranges > 1 && (!partial || (size_t)p.ranges * g.M * g.N > part_cap))
@@ -1833,8 +2043,8 @@ hipError_t gemm(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipS
 
 bool prefill_supported(const sh_model *m, std::string *why) {
     const sh_config &c = m->cfg;
-    if (m->dtype != SH_DTYPE_F16 && m->dtype != SH_DTYPE_BF16) {
-        *why = "full-sequence forward needs fp16 or bf16 weights";
+    if (m->dtype == SH_DTYPE_W8A8 && (c.dim % 128 || m->qdim % 128 || c.hidden % 128)) {
+        *why = "W8A8 full-sequence forward needs dim, n_heads*head_dim and hidden multiples of 128";
         return false;
     }
     if (c.dim % 64 || m->qdim % 64 || c.hidden % 64 || c.vocab % 64 || m->qkv_rows % 64 ||
@@ -1897,6 +2107,8 @@ hipError_t prefill_alloc(sh_model *m, int S, bool logits) {
                  o_v = take(4 * S * KV), o_att = take(4 * S * Q), o_gate = take(4 * S * F),
                  o_log = logits ? take(4 * V * S) : 0, o_cf = take(4 * S * D);
     const size_t o_part = take(4 * part);   // K-range partials of the split GEMMs
+    const bool q8 = m->dtype == SH_DTYPE_W8A8;   // quantized A operand and its row scales
+    const size_t o_a8 = q8 ? take((size_t)S * std::max({D, Q, F})) : 0, o_sa = q8 ? take(4 * S) : 0;
     hipError_t e = hipMalloc(&m->pf_arena, off);
     if (e != hipSuccess) return e;
     uint8_t *A = (uint8_t *)m->pf_arena;
@@ -1916,6 +2128,8 @@ hipError_t prefill_alloc(sh_model *m, int S, bool logits) {
     m->pf_cf = (float *)(A + o_cf);
     m->pf_part = (float *)(A + o_part);
     m->pf_part_cap = part;
+    m->pf_a8 = q8 ? (int8_t *)(A + o_a8) : nullptr;
+    m->pf_sa = q8 ? (float *)(A + o_sa) : nullptr;
     m->pf_cap = S;
     return hipSuccess;
 }
@@ -1952,6 +2166,7 @@ QkRopeArgs qk_rope_args(const sh_model *m, const LayerDev &L, const int32_t *row
     a.vcache = fill ? kv_layer_base(m, m->vcache, l) : nullptr;
     a.kv_seq_stride = kv_seq_stride(m);
     a.write_cache = fill ? 1 : 0;
+    a.round_kv = m->dtype == SH_DTYPE_W8A8 ? 1 : 0;   // W8A8 attends as the decode does
     return a;
 }
 
@@ -1963,6 +2178,32 @@ hipError_t launch_qk_rope(const sh_model *m, const LayerDev &L, int rows, const 
     if (kv == SH_KV_F32) hipLaunchKernelGGL(k_qk_rope<SH_KV_F32>, dim3(rows), dim3(kT), 0, s, qkv, a);
     else if (kv == SH_KV_F16) hipLaunchKernelGGL(k_qk_rope<SH_KV_F16>, dim3(rows), dim3(kT), 0, s, qkv, a);
     else hipLaunchKernelGGL(k_qk_rope<SH_KV_BF16>, dim3(rows), dim3(kT), 0, s, qkv, a);
+    return hipGetLastError();
+}
+
+// W8A8: the decode-order attention of `rows` query rows (k_attn_exact), keys from the
+// token-major pf_k / pf_v of the forward or, with from_cache, from layer l of the KV cache.
+hipError_t launch_attn_exact(const sh_model *m, int rows, const float *q, bool from_cache, int l,
+                             const int32_t *rowpos, const int32_t *rowseq, float *att,
+                             hipStream_t s) {
+    const sh_config &c = m->cfg;
+    const float inv = (float)(1.0 / sqrt((double)c.head_dim));
+    const dim3 grid(rows, c.n_heads);
+    const size_t stride = kv_seq_stride(m);
+    if (c.head_dim > 256 || c.max_seq > kMaxSeqLds) return hipErrorInvalidValue;
+    if (!from_cache)
+        hipLaunchKernelGGL(k_attn_exact<SH_KV_F32>, grid, dim3(kT), 0, s, q, m->qdim,
+                           (const void *)m->pf_k, (const void *)m->pf_v, stride, m->kvdim, 0,
+                           rowpos, rowseq, c.n_heads, c.n_kv_heads, c.head_dim, inv, att);
+    else {
+        const void *kb = kv_layer_base(m, m->kcache, l), *vb = kv_layer_base(m, m->vcache, l);
+#define SH_AE(KV) hipLaunchKernelGGL(k_attn_exact<KV>, grid, dim3(kT), 0, s, q, m->qdim, kb, vb, stride, \
+                                     m->kvdim, 1, rowpos, rowseq, c.n_heads, c.n_kv_heads, c.head_dim, inv, att)
+        if (c.kv_dtype == SH_KV_F32) SH_AE(SH_KV_F32);
+        else if (c.kv_dtype == SH_KV_F16) SH_AE(SH_KV_F16);
+        else SH_AE(SH_KV_BF16);
+#undef SH_AE
+    }
     return hipGetLastError();
 }
 
@@ -2045,6 +2286,7 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
     GemmArgs g{};
     g.A = m->pf_xn; g.B = (const uint16_t *)L.wqkv; g.M = S; g.N = m->qkv_rows; g.K = D;
     g.epi = G_STORE; g.out = m->pf_qkv; g.dt = dt;
+    g.sw = L.s_qkv; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;
     if (ranges > 1) {
         const QkRopeArgs a = qk_rope_args(m, L, m->pf_rowpos, m->pf_rowseq, m->pf_q, m->pf_k, m->pf_v, l,
@@ -2059,10 +2301,15 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
                                    m->pf_v, l, fill_kv, s)) != hipSuccess) {
         return e;
     }
-    if ((e = launch_attn_prefill(m, S, seg_max, fill_kv, scale, s)) != hipSuccess) return e;
+    if (dt == SH_DTYPE_W8A8)
+        e = launch_attn_exact(m, S, m->pf_q, false, l, m->pf_rowpos, m->pf_rowseq, (float *)m->pf_att, s);
+    else
+        e = launch_attn_prefill(m, S, seg_max, fill_kv, scale, s);
+    if (e != hipSuccess) return e;
     g = GemmArgs{};
     g.A = m->pf_att; g.B = (const uint16_t *)L.wo; g.M = S; g.N = D; g.K = m->qdim;
     g.epi = G_RESID; g.out = m->pf_x2; g.resid = m->pf_x; g.alpha = c.residual_scale; g.dt = dt;
+    g.sw = L.s_o; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;
     if (ranges > 1)
         hipLaunchKernelGGL(k_row_resid_norm, dim3(S), dim3(1024), 0, s, (const float *)m->pf_part, ranges, S, D,
@@ -2073,11 +2320,13 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
                            c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D, nullptr);
     g = GemmArgs{};
     g.A = m->pf_xn; g.B = (const uint16_t *)L.w13; g.M = S; g.N = 2 * F; g.K = D;
-    g.epi = G_GATE; g.out16 = m->pf_gate; g.dt = dt; g.decode_forms = fill_kv ? 1 : 0;
+    g.epi = G_GATE; g.out16 = m->pf_gate; g.dt = dt; g.decode_forms = fill_kv || dt == SH_DTYPE_W8A8 ? 1 : 0;
+    g.sw = L.s_13; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
     g = GemmArgs{};
     g.A = m->pf_gate; g.B = (const uint16_t *)L.w2; g.M = S; g.N = D; g.K = F;
     g.epi = G_RESID; g.out = m->pf_x; g.resid = m->pf_x2; g.alpha = c.residual_scale; g.dt = dt;
+    g.sw = L.s_2; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     if (!next_gain) return gemm(g, dt, m->pf_part, m->pf_part_cap, s);
     if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;
     if (ranges == 1) return hipSuccess;
@@ -2093,6 +2342,7 @@ hipError_t enqueue_classifier(sh_model *m, int S) {
     GemmArgs g{};
     g.A = m->pf_xn; g.B = (const uint16_t *)m->cls; g.M = S; g.N = m->cfg.vocab; g.K = m->cfg.dim;
     g.epi = G_LOGITS_CF; g.out = m->pf_logits; g.dt = m->dtype;
+    g.sw = m->s_cls; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     return gemm(g, m->dtype, m->pf_part, m->pf_part_cap, m->stream);
 }
 
@@ -2113,17 +2363,21 @@ hipError_t enqueue_prefill(sh_model *m, int S, int seg_max, bool logits, bool fi
     hipLaunchKernelGGL(k_embed_rows, dim3(S), dim3(kT), 0, s, (const uint16_t *)m->embed,
                        m->pf_tokens, c.vocab, D, dt, m->pf_x);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    // the final norm: stories.RMSNorm (cpu.go:97-111); W8A8 keeps the decode's rmsNormVec
+    // (infer.go:242), whose result its classifier quantizer sees
+    const int final_form = dt == SH_DTYPE_W8A8 ? 0 : 1;
     bool normed = false;
     for (int l = 0; l < c.n_layers; l++) {
         const bool last = l + 1 == c.n_layers;
         const float *next = !last ? m->layers[l + 1].rms_att : logits ? m->rms_final : nullptr;
-        if ((e = enqueue_layer(m, l, S, seg_max, fill_kv, normed, next, last ? 1 : 0, &normed)) != hipSuccess)
+        if ((e = enqueue_layer(m, l, S, seg_max, fill_kv, normed, next, last ? final_form : 0, &normed)) !=
+            hipSuccess)
             return e;
     }
     if (!logits) return hipSuccess;
     if (!normed)
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x, m->rms_final, D,
-                           c.norm_eps, 1, dt, m->pf_xn, (size_t)S * D, nullptr);
+                           c.norm_eps, final_form, dt, m->pf_xn, (size_t)S * D, nullptr);
     return enqueue_classifier(m, S);
 }
 
@@ -2174,6 +2428,7 @@ hipError_t enqueue_layer_taps_cf(sh_model *m, int l, int S, float *sdpa, float *
         GemmArgs g{};
         g.A = m->pf_xn; g.B = (const uint16_t *)m->layers[l].w13; g.M = S; g.N = 2 * F; g.K = D;
         g.epi = G_STORE; g.out = h13; g.dt = m->dtype;
+        g.sw = m->layers[l].s_13; g.a8 = m->pf_a8; g.sa = m->pf_sa;
         if ((e = gemm(g, m->dtype, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
         if ((e = hipMemcpyAsync(ffn, m->pf_cf, sizeof(float) * D * S, hipMemcpyDeviceToDevice, s)) != hipSuccess)
             return e;
@@ -2235,6 +2490,15 @@ int skinny_kc(int N, int K) { return (N / 16 < 2048 && K % 256 == 0) ? 256 : K; 
 
 hipError_t skinny(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipStream_t s) {
     if (g.K % 128 || g.N % 16 || g.M > 32) return hipErrorInvalidValue;
+    if (dt == SH_DTYPE_W8A8) {   // one K range: "partials" are the finished [M, N] product
+        GemmArgs h = g;
+        if (g.partial_only) {
+            if ((size_t)g.M * g.N > part_cap) return hipErrorInvalidValue;
+            h.epi = G_STORE;
+            h.out = partial;
+        }
+        return gemm_i8(h, s);
+    }
     const int kc = skinny_kc(g.N, g.K), ranges = g.K / kc;
     if ((ranges > 1 || g.partial_only) && (size_t)ranges * g.M * g.N > part_cap)
         return hipErrorInvalidValue;   // the partial buffer must hold every K range
@@ -2296,6 +2560,8 @@ hipError_t batch_alloc(sh_model *m, int B) {
     const size_t o_part = take(4 * B * std::max(part, (size_t)1));
     const size_t nblk = (V + kArgChunk - 1) / kArgChunk;
     const size_t o_apv = take(4 * B * nblk), o_api = take(4 * B * nblk);
+    const bool q8 = m->dtype == SH_DTYPE_W8A8;   // quantized A operand and its row scales
+    const size_t o_a8 = q8 ? take((size_t)B * W) : 0, o_sa = q8 ? take(4 * (size_t)B) : 0;
     hipError_t e = hipMalloc(&m->bt_arena, off);
     if (e != hipSuccess) return e;
     uint8_t *A = (uint8_t *)m->bt_arena;
@@ -2320,6 +2586,8 @@ hipError_t batch_alloc(sh_model *m, int B) {
     m->bt_part_cap = (size_t)B * std::max(part, (size_t)1);
     m->bt_apv = (float *)(A + o_apv);
     m->bt_api = (int32_t *)(A + o_api);
+    m->bt_a8 = q8 ? (int8_t *)(A + o_a8) : nullptr;
+    m->bt_sa = q8 ? (float *)(A + o_sa) : nullptr;
     m->bt_cap = B;
     std::vector<int32_t> seq(B);
     for (int b = 0; b < B; b++) seq[b] = b;
@@ -2371,13 +2639,15 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
     const int schunk = kChunkBytes / (c.head_dim * kvb);
     int nsplit = std::max(1, (512 + B * c.n_kv_heads - 1) / (B * c.n_kv_heads));
     nsplit = std::min({nsplit, nch, (c.max_seq + schunk - 1) / schunk});
-    auto ranges = [](int N, int K) { return K / skinny_kc(N, K); };
+    // K ranges the row kernels sum (the W8A8 product leaves one)
+    auto ranges = [dt](int N, int K) { return dt == SH_DTYPE_W8A8 ? 1 : K / skinny_kc(N, K); };
     for (int l = 0; l < c.n_layers; l++) {
         const LayerDev &L = m->layers[l];
         // q|k|v projection; row kernel: K-range sum, QK-norm, RoPE, KV append, q out
         GemmArgs g{};
         g.A = m->bt_xn; g.B = (const uint16_t *)L.wqkv; g.M = B; g.N = m->qkv_rows; g.K = D;
         g.dt = dt; g.partial_only = 1;
+        g.sw = L.s_qkv; g.a8 = m->bt_a8; g.sa = m->bt_sa;
         if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         const QkRopeArgs qa = qk_rope_args(m, L, m->bt_pos, m->bt_seq, m->bt_q, nullptr, nullptr, l, true);
         const int rq = ranges(m->qkv_rows, D);
@@ -2389,9 +2659,14 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
             hipLaunchKernelGGL(k_row_qkv<SH_KV_BF16>, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part, rq, B, qa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // attention over each sequence's cache, streamed by workgroup (split, kv head,
-        // sequence); shapes without a streaming instance split over fixed chunks and merge
+        // sequence); shapes without a streaming instance split over fixed chunks and merge;
+        // W8A8 in the decode's order (its Wo quantizer must see the decode's values)
         const void *kc = kv_layer_base(m, m->kcache, l), *vc = kv_layer_base(m, m->vcache, l);
-        if (astream) {
+        if (dt == SH_DTYPE_W8A8) {
+            if ((e = launch_attn_exact(m, B, m->bt_q, true, l, m->bt_pos, m->bt_seq, (float *)m->bt_att, s)) !=
+                hipSuccess)
+                return e;
+        } else if (astream) {
             hipLaunchKernelGGL(astream, dim3(nsplit, c.n_kv_heads, B), dim3(kAT), 0, s, m->bt_q, kc, vc,
                                kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, scale, nsplit, nch,
                                dt, (size_t)B * c.n_heads * c.head_dim, m->bt_att, m->bt_pm, m->bt_pl,
@@ -2405,7 +2680,8 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
             }
         }
         const dim3 grid(nch, c.n_kv_heads, B);
-        if (astream) {
+        const bool chunked = !astream && dt != SH_DTYPE_W8A8;
+        if (!chunked) {
         } else if (c.kv_dtype == SH_KV_F32)
             hipLaunchKernelGGL(k_attn_batch_partial<SH_KV_F32>, grid, dim3(kT), 0, s, m->bt_q, kc, vc,
                                kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, c.head_dim,
@@ -2418,7 +2694,7 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
             hipLaunchKernelGGL(k_attn_batch_partial<SH_KV_BF16>, grid, dim3(kT), 0, s, m->bt_q, kc, vc,
                                kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, c.head_dim,
                                scale, nch, m->bt_pm, m->bt_pl, m->bt_pacc);
-        if (!astream) {
+        if (chunked) {
             if ((e = hipGetLastError()) != hipSuccess) return e;
             hipLaunchKernelGGL(k_attn_batch_combine, dim3(c.n_heads, B), dim3(256), 0, s, m->bt_pm,
                                m->bt_pl, m->bt_pacc, m->bt_pos, c.n_heads, c.head_dim, nch, chunk, B,
@@ -2429,6 +2705,7 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         g = GemmArgs{};
         g.A = m->bt_att; g.B = (const uint16_t *)L.wo; g.M = B; g.N = D; g.K = m->qdim;
         g.dt = dt; g.partial_only = 1;
+        g.sw = L.s_o; g.a8 = m->bt_a8; g.sa = m->bt_sa;
         if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         hipLaunchKernelGGL(k_row_resid_norm, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part,
                            ranges(D, m->qdim), B, D, (const float *)m->bt_x, c.residual_scale,
@@ -2438,12 +2715,14 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         g = GemmArgs{};
         g.A = m->bt_xn; g.B = (const uint16_t *)L.w13; g.M = B; g.N = 2 * F; g.K = D;
         g.epi = G_GATE; g.out16 = m->bt_gate; g.dt = dt; g.decode_forms = 1;
+        g.sw = L.s_13; g.a8 = m->bt_a8; g.sa = m->bt_sa;
         if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         // W2; row kernel: x = x2 + alpha * (gate . W2^T), then rmsnorm(x) with the next
         // layer's rms_att, or rms_final (rmsNormVec, infer.go:242) after the last layer
         g = GemmArgs{};
         g.A = m->bt_gate; g.B = (const uint16_t *)L.w2; g.M = B; g.N = D; g.K = F;
         g.dt = dt; g.partial_only = 1;
+        g.sw = L.s_2; g.a8 = m->bt_a8; g.sa = m->bt_sa;
         if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         const float *next_gain = l + 1 < c.n_layers ? m->layers[l + 1].rms_att : m->rms_final;
         hipLaunchKernelGGL(k_row_resid_norm, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part,
@@ -2454,6 +2733,7 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
     GemmArgs g{};
     g.A = m->bt_xn; g.B = (const uint16_t *)m->cls; g.M = B; g.N = c.vocab; g.K = D;
     g.epi = G_STORE; g.out = m->bt_logits; g.dt = dt;
+    g.sw = m->s_cls; g.a8 = m->bt_a8; g.sa = m->bt_sa;
     if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
     const int nblk = (c.vocab + kArgChunk - 1) / kArgChunk;
     hipLaunchKernelGGL(k_argmax_part, dim3(nblk, B), dim3(kT), 0, s, m->bt_logits, c.vocab, nblk,
@@ -2512,11 +2792,12 @@ hipError_t enqueue_window_step(sh_model *m, int seq) {
     hipError_t e;
     if ((e = enqueue_prefill(m, seq, seq, false, false)) != hipSuccess) return e;
     hipLaunchKernelGGL(k_rmsnorm_rows, dim3(1), dim3(kT), 0, s, m->pf_x + (size_t)(seq - 1) * D,
-                       m->rms_final, D, c.norm_eps, 1, dt, m->wd_xn, (size_t)D);
+                       m->rms_final, D, c.norm_eps, dt == SH_DTYPE_W8A8 ? 0 : 1, dt, m->wd_xn, (size_t)D);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     GemmArgs g{};
     g.A = m->wd_xn; g.B = (const uint16_t *)m->cls; g.M = 1; g.N = c.vocab; g.K = D;
     g.epi = G_STORE; g.out = m->wd_logits; g.dt = dt;
+    g.sw = m->s_cls; g.a8 = m->pf_a8; g.sa = m->pf_sa;   // the forward is done with them
     if ((e = skinny(g, dt, m->wd_part, m->wd_part_cap, s)) != hipSuccess) return e;
     const int nblk = (c.vocab + kArgChunk - 1) / kArgChunk;
     hipLaunchKernelGGL(k_argmax_part, dim3(nblk, 1), dim3(kT), 0, s, m->wd_logits, c.vocab, nblk,

@@ -405,6 +405,18 @@ def quantize_rows(src: np.ndarray):
     return q, s
 
 
+def mat_vec_w8a8(wq: np.ndarray, wscale: np.ndarray, x: np.ndarray, threads: int = 1) -> np.ndarray:
+    """or_mat_vec_w8a8: x quantized per tensor, exact int32 dot per row, (float)acc * (s_w * s_a)."""
+    q = np.ascontiguousarray(wq, np.int8)
+    rows, cols = q.shape
+    xx = np.ascontiguousarray(x, np.float32)
+    assert xx.size == cols
+    out = np.empty(rows, np.float32)
+    load().or_mat_vec_w8a8(fp(out), q.ctypes.data_as(C.POINTER(C.c_int8)),
+                           fp(np.ascontiguousarray(wscale, np.float32)), fp(xx), rows, cols, threads)
+    return out
+
+
 def quantize_tensor(src: np.ndarray):
     a = np.ascontiguousarray(src, np.float32)
     q = np.empty(a.shape, np.int8)

@@ -23,15 +23,17 @@ LOGIT_TOL = 2e-2
 THREADS = max(1, min(16, os.cpu_count() or 1))
 
 
-def build(cfg, seed, std=0.02, gains_seed=None):
+def build(cfg, seed, std=0.02, gains_seed=None, ref_kv=None):
+    """The W8A8 model and the oracle's W8A8 decoder of the same weights (its cache type
+    ref_kv, or the model's)."""
     w = sh.synth_weights(cfg, seed=seed, std=std)
     if gains_seed is not None:
         w = random_gains(w, gains_seed)
     m = sh.Model(cfg, sh.SH_DTYPE_W8A8)
     m.upload(w)
     print(m.describe())
-    ref = oracle.Decoder(oracle.config_from(cfg, w8a8=True), w.rounded(sh.SH_DTYPE_W8A8),
-                         threads=THREADS)
+    ref = oracle.Decoder(oracle.config_from(cfg, w8a8=True, kv_dtype=ref_kv),
+                         w.rounded(sh.SH_DTYPE_W8A8), threads=THREADS)
     return m, ref
 
 
@@ -130,4 +132,120 @@ def test_w8a8_taps_tiny(gpu):
         want = ref.forward_one(int(tok), pos)
         assert np.array_equal(got, want), f"pos {pos}"
         check_taps(m, ref, cfg)
+    m.close()
+
+
+# ---- W8A8 beyond the batch-1 decode: int8 MFMA products (v_mfma_i32_16x16x64_i8) ----------
+
+def fp16_exact(shape, seed, scale=1.0):
+    """float32 values that fp16 holds exactly (so the operand planes carry them unchanged)."""
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal(shape) * scale).astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("shape", ["tiny", "stories110m"])
+def test_w8a8_classifier_int8_product_bit_exact(gpu, shape):
+    """The int8 MFMA product with its dequantization, through the classifier seam
+    (sh_classifier_cf on a W8A8 model): every column of the channel-first input is quantized
+    on its own (the bridge formula) and multiplied with the int8 classifier rows; the logits
+    equal the oracle's or_mat_vec_w8a8 of that column bit for bit (exact int32 sums, then
+    (float)acc * (s_w * s_a)). The inputs are values fp16 holds exactly, so the operand planes
+    carry them unchanged into the quantizer. The device's int8 rows and scales are read
+    back and equal the oracle's quantization of the fp32 rows."""
+    cfg = tiny_config() if shape == "tiny" else sh.stories110m_config()
+    w = sh.synth_weights(cfg, seed=431, std=0.05)
+    m = sh.Model(cfg, sh.SH_DTYPE_W8A8)
+    m.upload(w)
+    cls = w.cls if w.cls is not None else w.embed
+    q_want, s_want = oracle.quantize_rows(cls)
+    assert np.array_equal(m.read_weights(-1, "cls"), q_want)
+    assert np.array_equal(m.read_weights(-1, "cls.scale").view(np.uint32), s_want.view(np.uint32))
+    S = 20 if shape == "tiny" else 72
+    x = fp16_exact((cfg.dim, S), 432, 0.7)
+    x[:, 3] = 0.0                         # an all-zero column: scale 1, every q = 0
+    x[5, 4] = 1000.0                      # one large value: the rest quantize to small ints
+    got = m.classifier_cf(x)
+    for t in range(S):
+        want = oracle.mat_vec_w8a8(q_want, s_want, x[:, t], THREADS)
+        assert np.array_equal(got[:, t].view(np.uint32), want.view(np.uint32)), \
+            f"column {t}: max-abs {np.max(np.abs(got[:, t] - want))}"
+    m.close()
+
+
+def check_w8a8_prefill(cfg, seed, std, gains_seed, S):
+    """sh_prefill_logits (EvalLogits) of a W8A8 model against the oracle's W8A8 decoder at every
+    position, bit for bit. The W8A8 forward keeps the decode's numerics wherever a value
+    feeds a quantizer: fp32 operands, k and v rounded to the cache type, attention in the
+    decode's float order, the decode's SiLU and final rmsNormVec; the int8 products are exact."""
+    m, ref = build(cfg, seed=seed, std=std, gains_seed=gains_seed)
+    toks = sh.synth_tokens(S, seed + 7, cfg.vocab)
+    got = m.eval_logits(toks)
+    assert got.shape == (cfg.vocab, S)
+    for t in range(S):
+        want = ref.forward_one(int(toks[t]), t)
+        assert np.array_equal(got[:, t].view(np.uint32), want.view(np.uint32)), \
+            f"position {t}: max-abs {np.max(np.abs(got[:, t] - want))}"
+    print(f"W8A8 full-sequence logits, S={S}: bit-identical at every position")
+    m.close()
+
+
+def test_w8a8_prefill_logits_tiny(gpu):
+    check_w8a8_prefill(tiny_config(), 441, 0.08, 442, 24)
+
+
+def test_w8a8_prefill_logits_tiny_gqa_qknorm(gpu):
+    check_w8a8_prefill(tiny_gqa_config(), 443, 0.08, 444, 17)
+
+
+def test_w8a8_prefill_logits_stories110m(gpu):
+    check_w8a8_prefill(sh.stories110m_config(), 0, 0.02, None, 64)
+
+
+def test_w8a8_batch_decode_tiny(gpu):
+    """Batched greedy decode of a W8A8 model (int8 MFMA products for the prompt forward and
+    every step, B = 3 in lockstep): every row's token stream equals the oracle's W8A8 greedy
+    decode of its prompt."""
+    cfg = tiny_config(max_batch=4)
+    m, ref = build(cfg, seed=451, std=0.08, gains_seed=452)
+    prompts = sh.synth_tokens(3 * 10, 453, cfg.vocab).reshape(3, 10)
+    got = m.batch_greedy_decode(prompts, 16)
+    for b in range(3):
+        ref.reset()
+        want, _, margins = ref.greedy_decode(prompts[b], 16)
+        print(f"row {b}: smallest top-2 margin {np.nanmin(margins):.3e}")
+        assert got[b].tolist() == want.tolist(), f"row {b}"
+    m.close()
+
+
+def test_w8a8_batch_decode_gqa_bf16_kv(gpu):
+    """The same with GQA, QK-norm and a bf16 KV cache (the attention reads the rounded cache)."""
+    cfg = tiny_gqa_config(max_batch=2)
+    m, ref = build(cfg, seed=455, std=0.08, gains_seed=456)
+    prompts = sh.synth_tokens(2 * 13, 457, cfg.vocab).reshape(2, 13)
+    got = m.batch_greedy_decode(prompts, 12)
+    for b in range(2):
+        ref.reset()
+        want, _, _ = ref.greedy_decode(prompts[b], 12)
+        assert got[b].tolist() == want.tolist(), f"row {b}"
+    m.close()
+
+
+def test_w8a8_window_decode_tiny(gpu):
+    """Window decode of a W8A8 model (the full causal forward over the BOS-left-padded window
+    at every step, decode.go:18-94): each step's token is the argmax of the oracle's W8A8
+    decoder over the same window (its prompt pass), whose logits the window forward
+    reproduces bit for bit."""
+    cfg = tiny_config()
+    m, ref = build(cfg, seed=461, std=0.08, gains_seed=462)
+    seq = 12
+    prompt = sh.synth_tokens(7, 463, cfg.vocab)
+    got, plen, _ = m.window_greedy_decode(prompt, seq, 10)
+    assert len(got) > plen
+    hist = [int(t) for t in got[:plen]]
+    for i in range(plen, len(got)):
+        win = [1] * max(0, seq - len(hist)) + hist[-seq:]
+        ref.reset()
+        lg = ref.prompt_forward(win)
+        assert int(got[i]) == int(np.argmax(lg)), f"step {i - plen}"
+        hist.append(int(got[i]))
     m.close()
