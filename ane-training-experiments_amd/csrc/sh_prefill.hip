@@ -49,19 +49,22 @@ __device__ __forceinline__ uint16_t f_to_bits(float f, int dt) {
     return __half_as_ushort(__float2half_rn(f));
 }
 
-// Writes v as a GEMM operand: the hi plane at idx, the lo plane `plane` elements further.
-// W8A8 models carry the operand as fp32 instead (element idx of the same buffer viewed as
-// float, whose 2 * plane 16-bit slots hold exactly `plane` floats): the per-row quantizer
-// then sees the value itself, as the reference's quantizer does.
-__device__ __forceinline__ void store_op(uint16_t *base, size_t idx, size_t plane, float v,
-                                         int dt) {
-    if (dt == SH_DTYPE_W8A8) {
-        ((float *)base)[idx] = v;
-        return;
-    }
+// Writes v as a 16-bit GEMM operand: the hi plane at idx, the lo plane `plane` elements
+// further (dt fp16 or bf16).
+__device__ __forceinline__ void store_op16(uint16_t *base, size_t idx, size_t plane, float v,
+                                           int dt) {
     const uint16_t hi = f_to_bits(v, dt);
     base[idx] = hi;
     base[plane + idx] = f_to_bits(v - bits_to_f(hi, dt), dt);
+}
+
+// store_op16 for the kernels a W8A8 model also runs (row kernels, the plane conversion):
+// W8A8 carries the operand as fp32 instead (element idx of the same buffer viewed as float,
+// whose 2 * plane 16-bit slots hold exactly `plane` floats), so the per-row quantizer sees
+// the value itself, as the reference's quantizer does.
+__device__ __forceinline__ void store_op(uint16_t *base, size_t idx, size_t plane, float v, int dt) {
+    if (dt == SH_DTYPE_W8A8) ((float *)base)[idx] = v;
+    else store_op16(base, idx, plane, v, dt);
 }
 
 __device__ __forceinline__ double block_sum(double v, double *red) {
@@ -195,11 +198,15 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4 &a, const u32x4 &b, const f3
 }
 
 // Epilogue of one output element pair (columns n, n+1 of row m) is shared with the skinny
-// GEMM (skinny_epilogue); the tiled GEMM applies it per element with the same forms.
+// GEMM (skinny_epilogue); the tiled GEMM applies it per element with the same forms. Q8: the
+// W8A8 product, whose gate operand is fp32 (store_op's W8A8 form).
+template <bool Q8>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs &g, int m, int n, float v, float v_right) {
     if (g.epi == G_GATE) {
-        if ((n & 1) == 0)
-            store_op(g.out16, (size_t)m * (g.N / 2) + (n >> 1), (size_t)g.M * (g.N / 2),
+        if ((n & 1) == 0 && Q8)
+            ((float *)g.out16)[(size_t)m * (g.N / 2) + (n >> 1)] = silu_gate(v, v_right, g.decode_forms);
+        else if ((n & 1) == 0)
+            store_op16(g.out16, (size_t)m * (g.N / 2) + (n >> 1), (size_t)g.M * (g.N / 2),
                      silu_gate(v, v_right, g.decode_forms), g.dt);
     } else if (g.epi == G_STORE) {
         g.out[(size_t)m * g.N + n] = v;
@@ -228,7 +235,7 @@ __device__ __forceinline__ void tile_out(const GemmArgs &g, float *partial, cons
                 const float vr = __shfl_xor(v, 1, 64);   // column n ^ 1, same row
                 if (m >= g.M) continue;
                 if (gridDim.z > 1) partial[((size_t)blockIdx.z * g.M + m) * g.N + n] = v;
-                else tile_epilogue(g, m, n, v, vr);
+                else tile_epilogue<false>(g, m, n, v, vr);
             }
         }
 }
@@ -560,7 +567,7 @@ __global__ __launch_bounds__(kT) void k_gemm_i8(GemmArgs g) {
                 const int m = m0 + wm + i * 16 + (lane >> 4) * 4 + r;
                 const float v = (float)acc[i][j][r] * (sw * g.sa[min(m, g.M - 1)]);
                 const float vr = __shfl_xor(v, 1, 64);   // column n ^ 1, same row
-                if (m < g.M) tile_epilogue(g, m, n, v, vr);
+                if (m < g.M) tile_epilogue<true>(g, m, n, v, vr);
             }
         }
 }
@@ -955,7 +962,7 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
             lt += lsum[w * BQ + q] * f;
             ot += oo[(w * BQ + q) * OLD + d] * f;
         }
-        store_op(att, (size_t)tq * qdim + h * HD + d, plane, ot * (1.0f / lt), DT);
+        store_op16(att, (size_t)tq * qdim + h * HD + d, plane, ot * (1.0f / lt), DT);
     }
 }
 
@@ -1144,7 +1151,7 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma64(const float *qf, con
     for (int i = 0; i < NO; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++)
-            store_op(att, (size_t)t * qdim + h * HD + 16 * i + 4 * g4 + r, plane, o[i][r] * inv, DT);
+            store_op16(att, (size_t)t * qdim + h * HD + 16 * i + 4 * g4 + r, plane, o[i][r] * inv, DT);
 }
 
 // Causal attention (forward_common.go:5-33): one wave per (query t, head h). Row t is
@@ -1201,7 +1208,7 @@ __global__ __launch_bounds__(kT) void k_attn_prefill(const float *qf, const floa
         float a = 0.f;
         for (int jj = 0; jj < n; jj++)
             a = fmaf(sc[jj] * inv, vf[(size_t)(j0 + jj) * kvdim + kvh * hd + i], a);
-        store_op(att, (size_t)t * qdim + h * hd + i, plane, a, dt);
+        store_op16(att, (size_t)t * qdim + h * hd + i, plane, a, dt);
     }
 }
 
@@ -1209,8 +1216,8 @@ __global__ __launch_bounds__(kT) void k_attn_prefill(const float *qf, const floa
 __device__ __forceinline__ void skinny_epilogue(const GemmArgs &g, int m, int n, float v0, float v1) {
     if (g.epi == G_GATE) {
         // columns 2q (W1) and 2q+1 (W3) of the interleaved weight rows
-        store_op(g.out16, (size_t)m * (g.N / 2) + (n >> 1), (size_t)g.M * (g.N / 2),
-                 silu_gate(v0, v1, g.decode_forms), g.dt);
+        store_op16(g.out16, (size_t)m * (g.N / 2) + (n >> 1), (size_t)g.M * (g.N / 2),
+                   silu_gate(v0, v1, g.decode_forms), g.dt);
         return;
     }
     const float v[2] = {v0, v1};
@@ -1744,7 +1751,7 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
                 mh = m_run[hh];
             }
         if (nsplit == 1) {
-            store_op(att, (size_t)b * qdim + (size_t)(g * GROUP + h) * HD + dd, plane, o / lh, dt);
+            store_op16(att, (size_t)b * qdim + (size_t)(g * GROUP + h) * HD + dd, plane, o / lh, dt);
         } else {
             const size_t pb = ((size_t)b * H + (size_t)g * GROUP + h) * nch_buf + split;
             pacc[pb * HD + dd] = o;
@@ -1778,7 +1785,7 @@ __global__ __launch_bounds__(256) void k_attn_split_combine(const float *pm, con
     for (int i = threadIdx.x; i < hd; i += blockDim.x) {
         float a = 0.f;
         for (int c = 0; c < ns; c++) a += expf(pm[pb + c] - M) * pacc[(pb + c) * hd + i];
-        store_op(att, (size_t)b * H * hd + (size_t)h * hd + i, plane, a * invL, dt);
+        store_op16(att, (size_t)b * H * hd + (size_t)h * hd + i, plane, a * invL, dt);
     }
 }
 
@@ -1823,7 +1830,7 @@ __global__ __launch_bounds__(256) void k_attn_batch_combine(const float *pm, con
     for (int i = threadIdx.x; i < hd; i += blockDim.x) {
         float a = 0.f;
         for (int c = 0; c < nc; c++) a += expf(pm[pb + c] - M) * pacc[(pb + c) * hd + i];
-        store_op(att, (size_t)b * H * hd + (size_t)h * hd + i, plane, a * invL, dt);
+        store_op16(att, (size_t)b * H * hd + (size_t)h * hd + i, plane, a * invL, dt);
     }
 }
 
