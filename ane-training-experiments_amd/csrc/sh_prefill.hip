@@ -1559,7 +1559,13 @@ constexpr int kAT = 512;                  // threads of the streaming batched at
 constexpr int kChunkBytes = 16 * 1024;    // bytes of K rows per streamed chunk (as many of V)
 
 // Batched decode attention that streams the cache (flash decoding): workgroup (split, kv
-// head g, sequence b) walks its share of the chunks of C = 16 KB / row-bytes keys. Chunk
+// head g, sequence b) walks its share of the chunks of C = 16 KB / row-bytes keys. It first
+// finishes its rows of the q|k|v projection itself, as k_row_qkv would for the whole row and
+// in the same float order: the skinny GEMM's K-range partials added in range order, then
+// QK-norm and RoPE at pos[b] for the group's q heads and for kv head g (qk_rope_row's
+// per-head code, restricted to those heads). The workgroup holding the sequence's last
+// chunk writes k and v to the cache and patches that row of its LDS copy of the chunk (the
+// chunk's global load may predate the write). Chunk
 // i+1's K and V rows are loaded into registers (64 bytes per thread) while chunk i is
 // computed from LDS, then written to the other pair of LDS buffers. (An LDS DMA would not
 // overlap: the compiler makes every LDS read wait for all DMA in flight.)
@@ -1570,9 +1576,9 @@ constexpr int kChunkBytes = 16 * 1024;    // bytes of K rows per streamed chunk 
 // (m, l, acc) partials for k_attn_split_combine. Sequence b attends to 0..pos[b].
 template <int KVT, int HD, int GROUP>
 __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 ? 2 : 4))) void k_attn_batch_stream(
-    const float *q, const void *kc, const void *vc, size_t kv_seq_stride, const int32_t *pos,
-    int H, int KVH, float scale, int nsplit, int nch_buf, int dt, size_t plane, uint16_t *att,
-    float *pm, float *pl, float *pacc) {
+    const float *partial, int ranges, QkRopeArgs a, const void *kc, const void *vc, size_t kv_seq_stride,
+    const int32_t *pos, int H, int KVH, float scale, int nsplit, int nch_buf, int dt, size_t plane,
+    uint16_t *att, float *pm, float *pl, float *pacc) {
     constexpr int EB = KVT == SH_KV_F32 ? 4 : 2;
     constexpr int RB = HD * EB;                        // bytes per cache row
     constexpr int C = kChunkBytes / RB;                // keys per chunk
@@ -1586,6 +1592,7 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
     __shared__ float sc[GROUP][C];
     __shared__ float redm[NW][GROUP], redl[NW][GROUP];
     __shared__ float part[NKG][GROUP][HD];
+    __shared__ float rowq[(GROUP + 2) * HD];           // the group's q heads, then k, then v
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int P = pos[b] + 1;
     const int nchunks = (P + C - 1) / C;
@@ -1596,11 +1603,6 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t sbase = (size_t)b * kv_seq_stride + (size_t)g * HD;
     const int sl = lane % LPK, rin = lane / LPK;
-    float qr[GROUP][EPC];
-#pragma unroll
-    for (int h = 0; h < GROUP; h++)
-#pragma unroll
-        for (int e = 0; e < EPC; e++) qr[h][e] = q[(size_t)b * qdim + (size_t)(g * GROUP + h) * HD + sl * EPC + e];
     // Next-chunk prefetch through registers: thread tid holds 16-byte pieces tid + kAT*u of
     // the chunk's K rows and of its V rows (rows packed back to back); rows past the
     // sequence's last key re-read that key, and a chunk past the split's last re-reads that
@@ -1620,11 +1622,40 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
             pv[u] = *(const u32x4 *)((const uint8_t *)vc + o);
         }
     };
-    auto stash = [&](int buf) {
+    // the last chunk's row of position pos[b] (-1: this workgroup holds no such row)
+    const bool last = c1 == nchunks;
+    const int prow = last ? P - 1 - (nchunks - 1) * C : -1;
+    // LDS copy of a chunk; in the sequence's last chunk the threads that copied a piece of
+    // row prow then overwrite it with this step's k / v as stored in the cache (from rowq)
+    auto stash = [&](int buf, bool patch) {
 #pragma unroll
         for (int u = 0; u < PPT; u++) {
             *(u32x4 *)(kbuf[buf] + (size_t)(tid + kAT * u) * 16) = pk[u];
             *(u32x4 *)(vbuf[buf] + (size_t)(tid + kAT * u) * 16) = pv[u];
+        }
+        if (!patch) return;
+#pragma unroll
+        for (int u = 0; u < PPT; u++) {
+            const int pi = tid + kAT * u;
+            if (pi / LPK != prow) continue;
+            const int c = pi % LPK;
+            uint32_t kk[4], vv[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if constexpr (KVT == SH_KV_F32) {
+                    kk[e] = __float_as_uint(rowq[GROUP * HD + c * 4 + e]);
+                    vv[e] = __float_as_uint(rowq[(GROUP + 1) * HD + c * 4 + e]);
+                } else {
+                    const int dtk = KVT == SH_KV_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16;
+                    const int i0 = c * 8 + 2 * e;
+                    kk[e] = (uint32_t)f_to_bits(rowq[GROUP * HD + i0], dtk) |
+                            ((uint32_t)f_to_bits(rowq[GROUP * HD + i0 + 1], dtk) << 16);
+                    vv[e] = (uint32_t)f_to_bits(rowq[(GROUP + 1) * HD + i0], dtk) |
+                            ((uint32_t)f_to_bits(rowq[(GROUP + 1) * HD + i0 + 1], dtk) << 16);
+                }
+            }
+            *(u32x4 *)(kbuf[buf] + (size_t)pi * 16) = u32x4{kk[0], kk[1], kk[2], kk[3]};
+            *(u32x4 *)(vbuf[buf] + (size_t)pi * 16) = u32x4{vv[0], vv[1], vv[2], vv[3]};
         }
     };
     float m_run[GROUP], L[GROUP], acc[GROUP];
@@ -1635,8 +1666,56 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
         acc[h] = 0.f;
     }
     const int d = tid % HD, kg = tid / HD;
-    fetch(c0);
-    stash(0);
+    fetch(c0);   // the first chunks' loads go out before the q|k|v rows are finished
+    {
+        // q heads g*GROUP .. +GROUP-1, k and v of kv head g: partial sums in range order
+        const int nrow = a.qdim + 2 * a.kvdim;
+        for (int i = tid; i < (GROUP + 2) * HD; i += kAT) {
+            const int col = i < GROUP * HD ? g * GROUP * HD + i
+                                           : (i < (GROUP + 1) * HD ? a.qdim + g * HD + (i - GROUP * HD)
+                                                                   : a.qdim + a.kvdim + g * HD + (i - (GROUP + 1) * HD));
+            float v = 0.f;
+            for (int r = 0; r < ranges; r++) v += partial[((size_t)r * gridDim.z + b) * nrow + col];
+            rowq[i] = v;
+        }
+        __syncthreads();
+        // QK-norm (wave w normalises head w: the q heads, then k), RoPE at pos[b]
+        if (a.qk_norm && wave <= GROUP) {
+            float *v = rowq + wave * HD;
+            const float *gn = wave < GROUP ? a.q_norm : a.k_norm;
+            double ss = 0;
+            for (int i = lane; i < HD; i += 64) ss += (double)v[i] * (double)v[i];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+            const float rr = (float)(1.0 / sqrt(ss / (double)HD + a.qk_eps));
+            for (int i = lane; i < HD; i += 64) v[i] = v[i] * rr * gn[i];
+        }
+        __syncthreads();
+        const int tp = P - 1, half = HD / 2;
+        for (int pp = tid; pp < (GROUP + 1) * half; pp += kAT) {
+            const int pi = pp % half;
+            const float c = a.rope_cos[tp * half + pi], sn = a.rope_sin[tp * half + pi];
+            const float e = rowq[2 * pp], o = rowq[2 * pp + 1];
+            rowq[2 * pp] = e * c - o * sn;
+            rowq[2 * pp + 1] = o * c + e * sn;
+        }
+        __syncthreads();
+        // the k and v row into the cache (once per sequence and kv head), and as the cache
+        // holds them into rowq for the LDS patch
+        for (int i = tid; i < 2 * HD; i += kAT) {
+            const float v = rowq[GROUP * HD + i];
+            if (last) kv_store<KVT>(i < HD ? (void *)kc : (void *)vc,
+                                    (size_t)b * kv_seq_stride + (size_t)tp * kvdim + g * HD + (i % HD), v);
+            rowq[GROUP * HD + i] = kv_round<KVT>(v);
+        }
+        __syncthreads();
+    }
+    float qr[GROUP][EPC];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++)
+#pragma unroll
+        for (int e = 0; e < EPC; e++) qr[h][e] = rowq[h * HD + sl * EPC + e];
+    stash(0, c0 == nchunks - 1);
     fetch(c0 + 1);   // in flight while chunk c0 is consumed
     __syncthreads();
     for (int ci = c0; ci < c1; ci++) {
@@ -1737,7 +1816,7 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
         // with this chunk's buffers and sc. (Issued here, unconditionally, rather than at the
         // top of the loop under a branch: 2.89 -> 2.76 ms per 32-sequence Qwen3-shaped step.
         // Deeper register rings of 2-6 chunks at one workgroup per CU were slower.)
-        if (ci + 1 < c1) stash(buf ^ 1);
+        if (ci + 1 < c1) stash(buf ^ 1, ci + 1 == nchunks - 1);
         fetch(ci + 2);
         __syncthreads();
     }
@@ -1796,8 +1875,9 @@ __global__ __launch_bounds__(256) void k_attn_split_combine(const float *pm, con
 }
 
 // The streaming kernel for (kv type, head dim, group), or null when it has no instance.
-typedef void (*AttnStreamKernel)(const float *, const void *, const void *, size_t, const int32_t *, int, int,
-                                 float, int, int, int, size_t, uint16_t *, float *, float *, float *);
+typedef void (*AttnStreamKernel)(const float *, int, QkRopeArgs, const void *, const void *, size_t,
+                                 const int32_t *, int, int, float, int, int, int, size_t, uint16_t *, float *,
+                                 float *, float *);
 template <int KVT>
 AttnStreamKernel pick_attn_stream_kv(int hd, int group) {
     switch (hd * 8 + group) {
@@ -2515,7 +2595,10 @@ hipError_t skinny(const GemmArgs &g, int dt, float *partial, size_t part_cap, hi
     const int kc = skinny_kc(g.N, g.K), ranges = g.K / kc;
     if ((ranges > 1 || g.partial_only) && (size_t)ranges * g.M * g.N > part_cap)
         return hipErrorInvalidValue;   // the partial buffer must hold every K range
-    if (g.N % 64 == 0 && kc % 256 == 0) {
+    // 64-column workgroups share the A rows through LDS; narrow products whose 64-column grid
+    // would leave CUs idle take 16-column workgroups instead (1.6% per 32-sequence
+    // Qwen3-shaped step, on its Wo and W2 products)
+    if (g.N % 64 == 0 && kc % 256 == 0 && (g.N / 64) * ranges >= 256) {
         const dim3 grid(g.N / 64, ranges);
         if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL(k_gemm_skinny64<SH_DTYPE_BF16>, grid, dim3(kT), 0, s, g, partial, kc);
         else hipLaunchKernelGGL(k_gemm_skinny64<SH_DTYPE_F16>, grid, dim3(kT), 0, s, g, partial, kc);
@@ -2664,13 +2747,16 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         const QkRopeArgs qa = qk_rope_args(m, L, m->bt_pos, m->bt_seq, m->bt_q, nullptr, nullptr, l, true);
         const int rq = ranges(m->qkv_rows, D);
-        if (c.kv_dtype == SH_KV_F32)
+        // the streaming attention finishes its own q|k|v rows (and writes the cache row)
+        const bool fused = astream && dt != SH_DTYPE_W8A8;
+        if (fused) {
+        } else if (c.kv_dtype == SH_KV_F32)
             hipLaunchKernelGGL(k_row_qkv<SH_KV_F32>, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part, rq, B, qa);
         else if (c.kv_dtype == SH_KV_F16)
             hipLaunchKernelGGL(k_row_qkv<SH_KV_F16>, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part, rq, B, qa);
         else
             hipLaunchKernelGGL(k_row_qkv<SH_KV_BF16>, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part, rq, B, qa);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (!fused && (e = hipGetLastError()) != hipSuccess) return e;
         // attention over each sequence's cache, streamed by workgroup (split, kv head,
         // sequence); shapes without a streaming instance split over fixed chunks and merge;
         // W8A8 in the decode's order (its Wo quantizer must see the decode's values)
@@ -2680,8 +2766,8 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
                 hipSuccess)
                 return e;
         } else if (astream) {
-            hipLaunchKernelGGL(astream, dim3(nsplit, c.n_kv_heads, B), dim3(kAT), 0, s, m->bt_q, kc, vc,
-                               kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, scale, nsplit, nch,
+            hipLaunchKernelGGL(astream, dim3(nsplit, c.n_kv_heads, B), dim3(kAT), 0, s,
+                               (const float *)m->bt_part, rq, qa, kc, vc, kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, scale, nsplit, nch,
                                dt, (size_t)B * c.n_heads * c.head_dim, m->bt_att, m->bt_pm, m->bt_pl,
                                m->bt_pacc);
             if ((e = hipGetLastError()) != hipSuccess) return e;
