@@ -1516,7 +1516,6 @@ hipError_t tr_backward(sh_trainer *T, int n_in, bool acc) {
     hipStream_t s = T->stream;
     const int S = T->S, D = T->D, F = T->F, hd = T->hd;
     const float alpha = T->cfg.residual_scale, scale = (float)(1.0 / sqrt((double)hd));
-    const size_t SD = (size_t)S * D;
     hipError_t e;
     for (int l = T->L - 1; l >= 0; l--) {
         sh_trainer::Layer &C = T->lc[l];

@@ -38,13 +38,16 @@ def build(cfg, seed, std=0.02, gains_seed=None, ref_kv=None):
 
 
 def check_steps(m, ref, tokens):
+    """sh_decode_step against the oracle's forwardOne at every position: bit-identical logits
+    (the W8A8 decode keeps the reference's float order wherever a value feeds a quantizer),
+    which implies the 2e-2 bar, and the first-max argmax."""
     worst = 0.0
     for pos, tok in enumerate(tokens):
         got, am = m.eval_next_logits(int(tok), pos)
         want = ref.forward_one(int(tok), pos)
         err = float(np.max(np.abs(got - want)))
         worst = max(worst, err)
-        assert err <= LOGIT_TOL, f"pos {pos}: max-abs {err}"
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"pos {pos}: max-abs {err}"
         assert am == int(np.argmax(got))
     print(f"W8A8 max-abs logits error over {len(tokens)} positions: {worst:.3e}")
     return worst
