@@ -124,7 +124,10 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
 /* (*Engine).EvalLogits (ane/storiesane/engine.go:363-376) = evalLogitsCPUInto
  * (engine.go:804-842): the full causal forward of `seq` tokens (seq <= max_seq), logits
  * channel-first [V, seq] (logits[v*seq + t]). Out-of-range ids give a zero embedding
- * column (cpu.go:41-72). Residual scale = cfg.residual_scale. */
+ * column (cpu.go:41-72). Residual scale = cfg.residual_scale. A W8A8 model runs it on the
+ * int8 matrix cores with each token's activations quantized on their own and the decode's
+ * float order wherever a value feeds a quantizer, so its logits equal forwardOne's at every
+ * position. */
 int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *logits_cf);
 /* ---- storiesane plugin seams over channel-first data (the _other.go stubs' HIP side) ---- */
 /* compileStoriesLayerForwardFunc + (*layerForward).run (ane/storiesane/layer_other.go:27-37,
@@ -188,7 +191,7 @@ int sh_conv_eval_noalloc(sh_conv *c, const float *x, int32_t s, float *out, void
  * full causal forward (as sh_prefill_logits) over the last `seq` tokens left-padded with BOS
  * (fillDecodeWindow, :83-94) and appends the argmax of the last position's logits. The prompt
  * is [BOS] if empty and its last `seq` ids are kept; max_new <= 0 means 64; stops after EOS=2
- * (there is no max_seq stop: the window slides). seq <= cfg.max_seq; fp16 or bf16 weights.
+ * (there is no max_seq stop: the window slides). seq <= cfg.max_seq.
  * out_tokens (capacity min(n_prompt, seq) + max_new, or 1 + max_new for an empty prompt)
  * receives prompt + generated ids. The loop runs on the device. */
 int sh_window_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32_t seq,
@@ -202,7 +205,8 @@ int sh_window_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt
  * caches; then each step feeds every sequence's latest token, so step i yields token
  * prompt_len + i of every row. A row stops after EOS=2 or at max_seq tokens. out_tokens holds
  * n_seqs rows of stride prompt_len + (max_new > 0 ? max_new : 64); n_out[s] is row s's count.
- * Needs fp16 or bf16 weights, n_seqs <= min(32, cfg.max_batch). sh_stats then reports the
+ * Needs n_seqs <= min(32, cfg.max_batch) (W8A8: dim, n_heads*head_dim and hidden multiples
+ * of 128, as for its full-sequence forward). sh_stats then reports the
  * decode steps (forwards = steps, tokens_out = tokens kept) and the prefill time. */
 int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
                            int32_t prompt_len, int32_t max_new, int32_t *out_tokens,
