@@ -1005,7 +1005,8 @@ int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
     const int B = n_seqs, P = prompt_len;
     const int steps = std::min(max_new, c.max_seq - P);   // stop at len == maxSeq
     (void)hipSetDevice(m->device);
-    if (!hip_ok(batch_alloc(m, B), "batch scratch")) return -1;
+    if (!hip_ok(batch_alloc(m, B), "batch scratch") || !hip_ok(batch_new_generation(m), "batch generation"))
+        return -1;
     hipStream_t s = m->stream;
     // prompt rows 0..P-2 of every sequence: one causal forward that fills the caches
     const int S = B * (P - 1);

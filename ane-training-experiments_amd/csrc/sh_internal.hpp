@@ -129,6 +129,10 @@ struct sh_model {
     int32_t *bt_api;
     int8_t *bt_a8;                             // W8A8: quantized A operand [B, <= 4096]
     float *bt_sa;                              //       and its row scales [B]
+    uint64_t *bt_tm, *bt_tl, *bt_tacc;         // streaming attention: tagged split partials
+    int32_t *bt_cnt;                           // [B][KVH] split-merge counters
+    uint32_t *bt_gen;                          // device copy of the call generation (tag part)
+    uint32_t bt_gen_host;
     hipGraphExec_t bt_exec;                    // one captured step for bt_graph_b sequences
     bool bt_ready;
     int bt_graph_b;
@@ -203,6 +207,8 @@ hipError_t enqueue_linear_rows(const float *x, int M, int K, const uint16_t *w, 
 hipError_t enqueue_transpose(const float *src, int rows, int cols, float *dst, hipStream_t s);
 bool batch_supported(const sh_model *m, int B, std::string *why);
 hipError_t batch_alloc(sh_model *m, int B);
+// Before a batched decode's steps: the next tag generation of the attention's split partials.
+hipError_t batch_new_generation(sh_model *m);
 // One greedy step of B sequences (token bt_tok at bt_pos each), argmax into bt_hist.
 hipError_t enqueue_batch_step(sh_model *m, int B);
 hipError_t window_alloc(sh_model *m, int max_new);

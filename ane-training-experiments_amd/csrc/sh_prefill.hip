@@ -1555,6 +1555,24 @@ __global__ __launch_bounds__(kT) void k_attn_batch_partial(
     }
 }
 
+// Tagged words for the streaming attention's split partials: (float bits, 32-bit tag) in one
+// 64-bit device-scope store, so a reader knows a word is this layer's and step's without a
+// fence (a device-scope release would write back the whole L2 on this part).
+__device__ __forceinline__ void tag_put(uint64_t *p, float v, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+// The value of a tagged word once it carries `tag` (a bounded wait: a word still missing after
+// about a second is taken as it is, so no wave can hang).
+__device__ __forceinline__ float tag_get(const uint64_t *p, uint32_t tag) {
+    uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int spins = 0; (uint32_t)(w >> 32) != tag && spins < (1 << 22); spins++) {
+        __builtin_amdgcn_s_sleep(1);
+        w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return __uint_as_float((uint32_t)w);
+}
+
 constexpr int kAT = 512;                  // threads of the streaming batched attention
 constexpr int kChunkBytes = 16 * 1024;    // bytes of K rows per streamed chunk (as many of V)
 
@@ -1578,7 +1596,8 @@ template <int KVT, int HD, int GROUP>
 __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 ? 2 : 4))) void k_attn_batch_stream(
     const float *partial, int ranges, QkRopeArgs a, const void *kc, const void *vc, size_t kv_seq_stride,
     const int32_t *pos, int H, int KVH, float scale, int nsplit, int nch_buf, int dt, size_t plane,
-    uint16_t *att, float *pm, float *pl, float *pacc) {
+    uint16_t *att, uint64_t *tm, uint64_t *tl_, uint64_t *tacc, int *cnt, const uint32_t *gen, int layer,
+    int n_layers, int max_seq) {
     constexpr int EB = KVT == SH_KV_F32 ? 4 : 2;
     constexpr int RB = HD * EB;                        // bytes per cache row
     constexpr int C = kChunkBytes / RB;                // keys per chunk
@@ -1600,6 +1619,9 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
     const int c0 = split * cps, c1 = min(nchunks, c0 + cps);
     if (c0 >= c1) return;
     const int qdim = H * HD, kvdim = KVH * HD;
+    // this call, step (position) and layer: never 0, the cleared words' tag
+    const uint32_t tag = ((*gen * (uint32_t)(max_seq + 1) + (uint32_t)(P - 1)) * (uint32_t)n_layers +
+                          (uint32_t)layer) + 1u;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t sbase = (size_t)b * kv_seq_stride + (size_t)g * HD;
     const int sl = lane % LPK, rin = lane / LPK;
@@ -1839,12 +1861,37 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
             store_op16(att, (size_t)b * qdim + (size_t)(g * GROUP + h) * HD + dd, plane, o / lh, dt);
         } else {
             const size_t pb = ((size_t)b * H + (size_t)g * GROUP + h) * nch_buf + split;
-            pacc[pb * HD + dd] = o;
+            tag_put(tacc + pb * HD + dd, o, tag);
             if (dd == 0) {
-                pm[pb] = mh;
-                pl[pb] = lh;
+                tag_put(tm + pb, mh, tag);
+                tag_put(tl_ + pb, lh, tag);
             }
         }
+    }
+    if (nsplit == 1) return;
+    // The last of the sequence's key-holding splits to count in merges them, in
+    // k_attn_split_combine's float order (sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s),
+    // reading the others' tagged partials, and clears the counter for the next layer.
+    __shared__ int merge_s;
+    __syncthreads();
+    const int ns = (nchunks + cps - 1) / cps;
+    int *ctr = cnt + (size_t)b * KVH + g;
+    if (tid == 0) merge_s = atomicAdd(ctr, 1) == ns - 1;
+    __syncthreads();
+    if (!merge_s) return;
+    if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = tid; i < GROUP * HD; i += kAT) {
+        const int h = g * GROUP + i / HD, ii = i % HD;
+        const size_t pb = ((size_t)b * H + h) * nch_buf;
+        float M = -INFINITY;
+        for (int c = 0; c < ns; c++) M = fmaxf(M, tag_get(tm + pb + c, tag));
+        float Lsum = 0.f;
+        for (int c = 0; c < ns; c++) Lsum += expf(tag_get(tm + pb + c, tag) - M) * tag_get(tl_ + pb + c, tag);
+        const float invL = 1.0f / Lsum;
+        float a = 0.f;
+        for (int c = 0; c < ns; c++)
+            a += expf(tag_get(tm + pb + c, tag) - M) * tag_get(tacc + (pb + c) * HD + ii, tag);
+        store_op16(att, (size_t)b * qdim + (size_t)h * HD + ii, plane, a * invL, dt);
     }
 }
 
@@ -1876,8 +1923,8 @@ __global__ __launch_bounds__(256) void k_attn_split_combine(const float *pm, con
 
 // The streaming kernel for (kv type, head dim, group), or null when it has no instance.
 typedef void (*AttnStreamKernel)(const float *, int, QkRopeArgs, const void *, const void *, size_t,
-                                 const int32_t *, int, int, float, int, int, int, size_t, uint16_t *, float *,
-                                 float *, float *);
+                                 const int32_t *, int, int, float, int, int, int, size_t, uint16_t *, uint64_t *,
+                                 uint64_t *, uint64_t *, int *, const uint32_t *, int, int, int);
 template <int KVT>
 AttnStreamKernel pick_attn_stream_kv(int hd, int group) {
     switch (hd * 8 + group) {
@@ -2658,6 +2705,11 @@ hipError_t batch_alloc(sh_model *m, int B) {
     const size_t o_apv = take(4 * B * nblk), o_api = take(4 * B * nblk);
     const bool q8 = m->dtype == SH_DTYPE_W8A8;   // quantized A operand and its row scales
     const size_t o_a8 = q8 ? take((size_t)B * W) : 0, o_sa = q8 ? take(4 * (size_t)B) : 0;
+    // the streaming attention's tagged split partials, merge counters and call generation
+    const size_t nt = (size_t)B * c.n_heads * nch;
+    const size_t o_tm = take(8 * nt), o_tl = take(8 * nt), o_tacc = take(8 * nt * c.head_dim),
+                 o_cnt = take(4 * (size_t)B * c.n_kv_heads), o_gen = take(4);
+    const size_t o_tag0 = o_tm, tag_bytes = o_gen + 4 - o_tm;
     hipError_t e = hipMalloc(&m->bt_arena, off);
     if (e != hipSuccess) return e;
     uint8_t *A = (uint8_t *)m->bt_arena;
@@ -2684,12 +2736,35 @@ hipError_t batch_alloc(sh_model *m, int B) {
     m->bt_api = (int32_t *)(A + o_api);
     m->bt_a8 = q8 ? (int8_t *)(A + o_a8) : nullptr;
     m->bt_sa = q8 ? (float *)(A + o_sa) : nullptr;
+    m->bt_tm = (uint64_t *)(A + o_tm);
+    m->bt_tl = (uint64_t *)(A + o_tl);
+    m->bt_tacc = (uint64_t *)(A + o_tacc);
+    m->bt_cnt = (int32_t *)(A + o_cnt);
+    m->bt_gen = (uint32_t *)(A + o_gen);
+    m->bt_gen_host = 0;
+    // tags 0 (never written), counters 0 (every merge leaves them at 0), generation 0
+    if ((e = hipMemset(A + o_tag0, 0, tag_bytes)) != hipSuccess) return e;
     m->bt_cap = B;
     std::vector<int32_t> seq(B);
     for (int b = 0; b < B; b++) seq[b] = b;
     return hipMemcpy(m->bt_seq, seq.data(), 4 * (size_t)B, hipMemcpyHostToDevice);
 }
 
+
+// A new call generation for the streaming attention's tags (words of earlier calls never
+// match); before the tags would wrap, the tagged words are cleared and the count restarts.
+hipError_t batch_new_generation(sh_model *m) {
+    const sh_config &c = m->cfg;
+    const uint64_t span = (uint64_t)(c.max_seq + 1) * (uint64_t)c.n_layers;
+    if ((uint64_t)(m->bt_gen_host + 2) * span >= 0xFFFFFFF0ull) {
+        const size_t bytes = (size_t)((uint8_t *)m->bt_gen - (uint8_t *)m->bt_tm);
+        hipError_t e = hipMemset(m->bt_tm, 0, bytes);
+        if (e != hipSuccess) return e;
+        m->bt_gen_host = 0;
+    }
+    m->bt_gen_host++;
+    return hipMemcpy(m->bt_gen, &m->bt_gen_host, 4, hipMemcpyHostToDevice);
+}
 
 bool batch_supported(const sh_model *m, int B, std::string *why) {
     if (!prefill_supported(m, why)) return false;
@@ -2768,15 +2843,9 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         } else if (astream) {
             hipLaunchKernelGGL(astream, dim3(nsplit, c.n_kv_heads, B), dim3(kAT), 0, s,
                                (const float *)m->bt_part, rq, qa, kc, vc, kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, scale, nsplit, nch,
-                               dt, (size_t)B * c.n_heads * c.head_dim, m->bt_att, m->bt_pm, m->bt_pl,
-                               m->bt_pacc);
+                               dt, (size_t)B * c.n_heads * c.head_dim, m->bt_att, m->bt_tm, m->bt_tl,
+                               m->bt_tacc, m->bt_cnt, m->bt_gen, l, c.n_layers, c.max_seq);
             if ((e = hipGetLastError()) != hipSuccess) return e;
-            if (nsplit > 1) {
-                hipLaunchKernelGGL(k_attn_split_combine, dim3(c.n_heads, B), dim3(256), 0, s, m->bt_pm,
-                                   m->bt_pl, m->bt_pacc, m->bt_pos, c.n_heads, c.head_dim, nsplit,
-                                   schunk, nch, B, dt, m->bt_att);
-                if ((e = hipGetLastError()) != hipSuccess) return e;
-            }
         }
         const dim3 grid(nch, c.n_kv_heads, B);
         const bool chunked = !astream && dt != SH_DTYPE_W8A8;
