@@ -369,6 +369,7 @@ sh_model *sh_model_create(const sh_config *cfg, int32_t dtype) {
     }
     if (!valid_config(*cfg, dtype)) return nullptr;
     if (!hip_ok(hipSetDevice(g_device), "hipSetDevice")) return nullptr;
+    if (!hip_ok(gemm_setup(), "GEMM set-up")) return nullptr;
     sh_model *m = new sh_model();
     memset((void *)m, 0, sizeof(*m));
     m->cfg = *cfg;
@@ -1536,6 +1537,7 @@ sh_conv *sh_conv_create(const float *w, int32_t out_dim, int32_t in_dim) {
         return nullptr;
     }
     (void)hipSetDevice(g_device);
+    if (!hip_ok(gemm_setup(), "GEMM set-up")) return nullptr;
     const size_t n = (size_t)out_dim * in_dim;
     float *w32 = nullptr;
     sh_conv *c = new sh_conv{out_dim, in_dim, g_device, nullptr};

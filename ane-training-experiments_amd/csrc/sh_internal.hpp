@@ -201,6 +201,8 @@ hipError_t enqueue_classifier_cf(sh_model *m, int S);
 // out = x [M, K] . w [N, K]^T (w in the 16-bit type dt; x converted to operand planes in
 // `planes`, 2*M*K elements), written [M, N] or channel-first [N, M].
 size_t gemm_partial_elems(int M, int N, int K);
+// One-time set-up of the GEMM kernels (their LDS limit); called before any capture.
+hipError_t gemm_setup();
 hipError_t enqueue_linear_rows(const float *x, int M, int K, const uint16_t *w, int N, int dt,
                                uint16_t *planes, float *out, bool cf, float *partial,
                                size_t part_cap, hipStream_t s);

@@ -181,10 +181,20 @@ struct GemmArgs {
 
 // silu(h1) * h3: decode form x / (1 + float32(exp(-x))) (infer.go:324-326), or the
 // full-sequence form (h1 * float32(1 / (1 + exp(-h1)))) * h3 (accel_other.go:128-133).
+// EXACT (the W8A8 products, whose gate values feed a quantizer): the reference's float64
+// exp, rounded as it rounds. Otherwise (the 16-bit models) float expf, the form their decode
+// kernel computes: within an ulp or so of the float64 form, at a fraction of its cost.
+template <bool EXACT>
 __device__ __forceinline__ float silu_gate(float h1, float h3, int decode_forms) {
-    if (decode_forms) return (h1 / (1.0f + (float)exp(-(double)h1))) * h3;
-    const float sig = (float)(1.0 / (1.0 + exp(-(double)h1)));
-    return (h1 * sig) * h3;
+    if constexpr (EXACT) {
+        if (decode_forms) return (h1 / (1.0f + (float)exp(-(double)h1))) * h3;
+        const float sig = (float)(1.0 / (1.0 + exp(-(double)h1)));
+        return (h1 * sig) * h3;
+    } else {
+        if (decode_forms) return (h1 / (1.0f + expf(-h1))) * h3;
+        const float sig = 1.0f / (1.0f + expf(-h1));
+        return (h1 * sig) * h3;
+    }
 }
 
 template <int DT>
@@ -204,10 +214,10 @@ template <bool Q8>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs &g, int m, int n, float v, float v_right) {
     if (g.epi == G_GATE) {
         if ((n & 1) == 0 && Q8)
-            ((float *)g.out16)[(size_t)m * (g.N / 2) + (n >> 1)] = silu_gate(v, v_right, g.decode_forms);
+            ((float *)g.out16)[(size_t)m * (g.N / 2) + (n >> 1)] = silu_gate<true>(v, v_right, g.decode_forms);
         else if ((n & 1) == 0)
             store_op16(g.out16, (size_t)m * (g.N / 2) + (n >> 1), (size_t)g.M * (g.N / 2),
-                     silu_gate(v, v_right, g.decode_forms), g.dt);
+                     silu_gate<Q8>(v, v_right, g.decode_forms), g.dt);
     } else if (g.epi == G_STORE) {
         g.out[(size_t)m * g.N + n] = v;
     } else if (g.epi == G_RESID) {
@@ -219,10 +229,50 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs &g, int m, int n, f
 
 // A wave's FM x FN blocks of 16 x 16 results (rows from mb, columns from nb) to the K-range
 // partials (more than one range) or through the epilogue. D layout: lane holds column
-// lane%16 of each block, rows 4*(lane/16) + r.
+// lane%16 of each block, rows 4*(lane/16) + r. The gate epilogue pairs lanes n and n ^ 1
+// (the W1 and W3 columns of one gate value, for the same four rows): after swapping their
+// values, the even lane finishes rows 0-1 and the odd lane rows 2-3, so every lane computes
+// two gate values instead of half the lanes computing four.
 template <int FM, int FN>
 __device__ __forceinline__ void tile_out(const GemmArgs &g, float *partial, const f32x4 (&acc)[FM][FN], int mb,
                                          int nb, int lane) {
+    if (gridDim.z > 1) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int n = nb + j * 16 + (lane & 15);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = mb + i * 16 + (lane >> 4) * 4 + r;
+                    if (m < g.M) partial[((size_t)blockIdx.z * g.M + m) * g.N + n] = acc[i][j][r];
+                }
+            }
+        return;
+    }
+    if (g.epi == G_GATE) {
+        const bool odd = lane & 1;
+        const size_t plane = (size_t)g.M * (g.N / 2);
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int q = (nb + j * 16 + (lane & 15)) >> 1;
+                float vx[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) vx[r] = __shfl_xor(acc[i][j][r], 1, 64);
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const float own = odd ? acc[i][j][k + 2] : acc[i][j][k];
+                    const float oth = odd ? vx[k + 2] : vx[k];
+                    const int m = mb + i * 16 + (lane >> 4) * 4 + (odd ? k + 2 : k);
+                    if (m < g.M)
+                        store_op16(g.out16, (size_t)m * (g.N / 2) + q, plane,
+                                   silu_gate<false>(odd ? oth : own, odd ? own : oth, g.decode_forms), g.dt);
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -231,11 +281,7 @@ __device__ __forceinline__ void tile_out(const GemmArgs &g, float *partial, cons
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = mb + i * 16 + (lane >> 4) * 4 + r;
-                const float v = acc[i][j][r];
-                const float vr = __shfl_xor(v, 1, 64);   // column n ^ 1, same row
-                if (m >= g.M) continue;
-                if (gridDim.z > 1) partial[((size_t)blockIdx.z * g.M + m) * g.N + n] = v;
-                else tile_epilogue<false>(g, m, n, v, vr);
+                if (m < g.M) tile_epilogue<false>(g, m, n, acc[i][j][r], 0.f);
             }
         }
 }
@@ -390,6 +436,126 @@ __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, i
     }
     tile_out<FM, FN>(g, partial, acc, m0 + wm, n0 + wn, lane);
 }
+
+// s_waitcnt immediate that waits until at most n vector memory operations of the wave are
+// outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt left at their
+// maxima, i.e. not waited for).
+constexpr int vm_wait_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Pipelined MFMA GEMM for short inputs: the same product and epilogue as k_gemm_burst, with
+// the operand tiles streamed into an NS-deep LDS ring by global_load_lds (each lane moves 16
+// bytes straight into LDS, one wave instruction fills 1 KB; no staging registers and no LDS
+// stores), so NS - 1 K steps of BK are always in flight and a workgroup waits out one memory
+// latency per product rather than one per burst. One barrier per K step:
+//   wait for this wave's loads of step s; barrier (every wave's loads of step s have landed
+//   and every wave has finished step s - 1); issue step s + NS - 1 into the slot step s - 1
+//   used; MFMAs of step s.
+// The waits are explicit s_waitcnt vmcnt(n) with a plain s_barrier: __syncthreads' release
+// fence would wait for every outstanding load, collapsing the ring to one step.
+// Tile rows (A hi, A lo, W; BK 16-bit elements each) are stored unpadded with their 16-byte
+// chunks XOR-swizzled by row (chunk c of row r in slot c ^ swz(r)), which is how each lane
+// picks its global chunk; a wave's fragment reads (16 rows x one chunk) then spread over the
+// LDS banks. Workgroup tile BM x BN of 2 x 2 waves, each FM x FN 16 x 16 blocks; the hi and
+// lo products accumulate separately (independent MFMA chains) and are added at the end.
+// Needs N % BN == 0, kc % BK == 0 and kc / BK >= NS - 1; rows past M re-read row M - 1.
+template <int DT, int BM, int BN, int BK, int NS>
+__global__ __launch_bounds__(kT) void k_gemm_pipe(GemmArgs g, float *partial, int kc) {
+    constexpr int FM = BM / 32, FN = BN / 32;
+    constexpr int CPR = BK / 8;                 // 16-byte chunks per tile row
+    constexpr int RB = BK * 2;                  // bytes per tile row
+    constexpr int RPI = 1024 / RB;              // tile rows per wave instruction
+    constexpr int ROWS = 2 * BM + BN;
+    constexpr int IPW = ROWS / RPI / 4;         // wave instructions per step, per wave
+    constexpr int SB = ROWS * RB;               // bytes per ring slot
+    static_assert(kT == 256 && ROWS % (4 * RPI) == 0 && BM % RPI == 0 && BN % RPI == 0 && CPR >= 4,
+                  "each step's rows must split evenly over the four waves");
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int kbeg = blockIdx.z * kc;
+    const int nsteps = kc / BK;
+    const size_t lo = (size_t)g.M * g.K;
+    auto swz = [](int r) { return CPR == 4 ? (r >> 1) & 3 : r & 7; };
+    const uint16_t *src[IPW];
+#pragma unroll
+    for (int i = 0; i < IPW; i++) {
+        const int gi = wave * IPW + i;
+        const int r = gi * RPI + lane / CPR;
+        const int c = (lane % CPR) ^ swz(r);
+        const uint16_t *p;
+        if (r < BM) p = g.A + (size_t)min(m0 + r, g.M - 1) * g.K;
+        else if (r < 2 * BM) p = g.A + lo + (size_t)min(m0 + r - BM, g.M - 1) * g.K;
+        else p = g.B + (size_t)(n0 + r - 2 * BM) * g.K;
+        src[i] = p + kbeg + c * 8;
+    }
+    auto issue = [&](int st) {
+        uint8_t *base = lds + (st % NS) * SB + wave * IPW * 1024;
+#pragma unroll
+        for (int i = 0; i < IPW; i++)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src[i] + st * BK),
+                                             (__attribute__((address_space(3))) void *)(base + i * 1024), 16, 0, 0);
+    };
+    const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+    const int fr = lane & 15, fq = lane >> 4;
+    f32x4 acc[FM][FN], acl[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            acl[i][j] = acc[i][j];
+        }
+    auto compute = [&](int st) {
+        const uint8_t *L = lds + (st % NS) * SB;
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ks++) {
+            const int c = ks * 4 + fq;
+            u32x4 ah[FM], al[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                const int r = wm + i * 16 + fr, r2 = BM + r;
+                ah[i] = *(const u32x4 *)(L + r * RB + ((c ^ swz(r)) << 4));
+                al[i] = *(const u32x4 *)(L + r2 * RB + ((c ^ swz(r2)) << 4));
+            }
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int r = 2 * BM + wn + j * 16 + fr;
+                b[j] = *(const u32x4 *)(L + r * RB + ((c ^ swz(r)) << 4));
+            }
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) acc[i][j] = mfma16<DT>(ah[i], b[j], acc[i][j]);
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) acl[i][j] = mfma16<DT>(al[i], b[j], acl[i][j]);
+        }
+    };
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++) issue(st);
+    int s = 0;
+    for (; s < nsteps - (NS - 1); s++) {
+        __builtin_amdgcn_s_waitcnt(vm_wait_imm((NS - 2) * IPW));
+        __builtin_amdgcn_s_barrier();
+        issue(s + NS - 1);
+        compute(s);
+    }
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
+    __builtin_amdgcn_s_barrier();
+    for (; s < nsteps; s++) compute(s);
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] += acl[i][j];
+    tile_out<FM, FN>(g, partial, acc, m0 + wm, n0 + wn, lane);
+}
+
+// The pipelined GEMM's shapes: 64 x 64 tiles with 6 slots of K 64 (147,456 bytes of LDS, one
+// workgroup per CU) where the tiles alone fill the chip, else 32 x 32 tiles with 4 slots
+// (49,152 bytes) and up to four K ranges.
+constexpr int kPipeBigLds = 6 * (3 * 64) * 128;
+constexpr int kPipeSmallLds = 4 * (3 * 32) * 128;
 
 // ---- W8A8 products on the int8 matrix cores --------------------------------------------
 
@@ -1217,7 +1383,7 @@ __device__ __forceinline__ void skinny_epilogue(const GemmArgs &g, int m, int n,
     if (g.epi == G_GATE) {
         // columns 2q (W1) and 2q+1 (W3) of the interleaved weight rows
         store_op16(g.out16, (size_t)m * (g.N / 2) + (n >> 1), (size_t)g.M * (g.N / 2),
-                   silu_gate(v0, v1, g.decode_forms), g.dt);
+                   silu_gate<false>(v0, v1, g.decode_forms), g.dt);
         return;
     }
     const float v[2] = {v0, v1};
@@ -2105,25 +2271,67 @@ __global__ __launch_bounds__(kT) void k_window_advance(const float *pv, const in
     if (threadIdx.x == 0) window[seq - 1] = next_s;
 }
 
-// Tile shape and K split of the tiled GEMM: 128 x 128 tiles for long inputs and for very wide
-// outputs (the classifier: half the re-reads of the activation planes; 48 vs 57 us at
-// S = 256, N = 32000), else 64 x 64 with K split (ranges of >= 256, dividing K) until there
-// are about 512 workgroups.
+// Kernel, tile shape and K split of a 16-bit GEMM.
+//  - Short inputs (M < 1024, not the classifier's very wide output): k_gemm_pipe, 64 x 64
+//    tiles when they alone give every CU a workgroup (W1|W3 at S = 256: 256 tiles, 8.6 us
+//    against 17.7 for the split 64 x 64 burst GEMM and its reduce), else 32 x 32 tiles with
+//    K split in two or four until there are about 384 workgroups (qkv 7.6 us unsplit, Wo
+//    3.9 and W2 6.2 in two ranges, against 14.9, 10.4 and 13.4 for the burst GEMM and its
+//    row kernel's partial sums).
+//  - Long inputs and very wide outputs (the classifier: half the re-reads of the activation
+//    planes; 48 vs 57 us at S = 256, N = 32000): k_gemm_burst 128 x 128 tiles; shapes the
+//    pipeline cannot take: 64 x 64 k_gemm_burst / k_gemm_tiled with K split (ranges of >= 256,
+//    dividing K) until there are about 512 workgroups.
+enum { GK_TILED64 = 0, GK_BIG = 1, GK_PIPE64 = 2, GK_PIPE32 = 3 };
 struct GemmPlan {
-    int big, ranges, kc;
+    int kind, ranges, kc;
 };
 GemmPlan gemm_plan(int M, int N, int K) {
     GemmPlan p{};
-    p.big = (M >= 1024 || (M >= 256 && N >= 16384)) && N % 128 == 0;
-    const int tiles = p.big ? ((M + 127) / 128) * (N / 128) : ((M + 63) / 64) * (N / 64);
     p.ranges = 1;
+    p.kc = K;
+    const bool big = (M >= 1024 || (M >= 256 && N >= 16384)) && N % 128 == 0;
+    if (!big && K % 64 == 0) {
+        const int t64 = ((M + 63) / 64) * (N / 64);
+        if (N % 64 == 0 && t64 >= 256 && K / 64 >= 5) {
+            p.kind = GK_PIPE64;
+            return p;
+        }
+        if (N % 32 == 0 && K / 64 >= 3) {
+            const int t32 = ((M + 31) / 32) * (N / 32);
+            p.kind = GK_PIPE32;
+            for (int r : {2, 4}) {
+                if (t32 * p.ranges >= 384) break;
+                if (K % (64 * r) == 0 && K / (64 * r) >= 3) p.ranges = r;
+            }
+            p.kc = K / p.ranges;
+            return p;
+        }
+    }
+    p.kind = big ? GK_BIG : GK_TILED64;
+    const int tiles = big ? ((M + 127) / 128) * (N / 128) : ((M + 63) / 64) * (N / 64);
     // at most four K ranges: each more range adds a [M, N] fp32 partial for the row kernel
-    // that sums them to read back (the S = 256 forward was fastest with four)
+    // that sums them to read back
     for (int r : {2, 3, 4})
         if (K % (32 * r) == 0 && K / r >= 256 && tiles * r <= 768) p.ranges = r;
     if (tiles >= 512) p.ranges = 1;
     p.kc = K / p.ranges;
     return p;
+}
+
+// Lets the pipelined GEMMs use more than 64 KB of dynamic LDS (once per process, before any
+// capture: called where models and convolutions are created).
+hipError_t gemm_pipe_setup_once() {
+    static hipError_t st = [] {
+        const void *fns[] = {(const void *)k_gemm_pipe<SH_DTYPE_F16, 64, 64, 64, 6>,
+                             (const void *)k_gemm_pipe<SH_DTYPE_BF16, 64, 64, 64, 6>};
+        for (const void *f : fns) {
+            const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPipeBigLds);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }();
+    return st;
 }
 
 // ranges_out given: K-range partials are left for the caller's row kernel (*ranges_out > 1)
@@ -2148,10 +2356,22 @@ hipError_t gemm(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipS
     const GemmPlan p = gemm_plan(g.M, g.N, g.K);
     if (p.ranges > 1 && (!partial || (size_t)p.ranges * g.M * g.N > part_cap))
         return hipErrorInvalidValue;   // the partial buffer must hold every K range
-    // burst loads where the K range allows them (8 steps of 32 per burst for 64 x 64 tiles,
-    // 4 for 128 x 128, whose staging registers are twice as many per step)
     const bool bf = dt == SH_DTYPE_BF16;
-    if (p.big) {
+    if (p.kind == GK_PIPE64 || p.kind == GK_PIPE32) {
+        hipError_t e0 = gemm_pipe_setup_once();
+        if (e0 != hipSuccess) return e0;
+        if (p.kind == GK_PIPE64) {
+            const dim3 grid((g.M + 63) / 64, g.N / 64, p.ranges);
+            if (bf) hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_BF16, 64, 64, 64, 6>), grid, dim3(kT), kPipeBigLds, s, g, partial, p.kc);
+            else hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_F16, 64, 64, 64, 6>), grid, dim3(kT), kPipeBigLds, s, g, partial, p.kc);
+        } else {
+            const dim3 grid((g.M + 31) / 32, g.N / 32, p.ranges);
+            if (bf) hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_BF16, 32, 32, 64, 4>), grid, dim3(kT), kPipeSmallLds, s, g, partial, p.kc);
+            else hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_F16, 32, 32, 64, 4>), grid, dim3(kT), kPipeSmallLds, s, g, partial, p.kc);
+        }
+    } else if (p.kind == GK_BIG) {
+        // burst loads where the K range allows them (4 steps of 32 per burst for 128 x 128
+        // tiles, 8 for 64 x 64, whose staging registers are half as many per step)
         const dim3 grid((g.M + 127) / 128, g.N / 128, p.ranges);
         if (p.kc % 128 == 0) {
             if (bf) hipLaunchKernelGGL((k_gemm_burst<SH_DTYPE_BF16, 128, 128, 4>), grid, dim3(kT), 0, s, g, partial, p.kc);
@@ -2180,6 +2400,8 @@ hipError_t gemm(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipS
 }
 
 }  // namespace
+
+hipError_t gemm_setup() { return gemm_pipe_setup_once(); }
 
 bool prefill_supported(const sh_model *m, std::string *why) {
     const sh_config &c = m->cfg;
