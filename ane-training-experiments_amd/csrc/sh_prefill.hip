@@ -258,18 +258,37 @@ __device__ __forceinline__ void tile_out(const GemmArgs &g, float *partial, cons
 #pragma unroll
             for (int j = 0; j < FN; j++) {
                 const int q = (nb + j * 16 + (lane & 15)) >> 1;
+                // own and partner values of rows k and k + 2, chosen with a per-lane select
+                // mask (a select of two array elements can become a dynamic index, in scratch)
+                const uint32_t sel = odd ? ~0u : 0u;
+                auto pick = [&](float lo_row, float hi_row) {
+                    return __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, hi_row) & sel) |
+                                                         (__builtin_bit_cast(uint32_t, lo_row) & ~sel));
+                };
+                const f32x4 av = acc[i][j];
                 float vx[4];
 #pragma unroll
-                for (int r = 0; r < 4; r++) vx[r] = __shfl_xor(acc[i][j][r], 1, 64);
+                for (int r = 0; r < 4; r++) vx[r] = __shfl_xor(av[r], 1, 64);
 #pragma unroll
                 for (int k = 0; k < 2; k++) {
-                    const float own = odd ? acc[i][j][k + 2] : acc[i][j][k];
-                    const float oth = odd ? vx[k + 2] : vx[k];
+                    const float own = pick(av[k], av[k + 2]);
+                    const float oth = pick(vx[k], vx[k + 2]);
                     const int m = mb + i * 16 + (lane >> 4) * 4 + (odd ? k + 2 : k);
                     if (m < g.M)
                         store_op16(g.out16, (size_t)m * (g.N / 2) + q, plane,
                                    silu_gate<false>(odd ? oth : own, odd ? own : oth, g.decode_forms), g.dt);
                 }
+            }
+        return;
+    }
+    if (g.epi == G_LOGITS_CF && (g.M & 3) == 0) {
+        // channel-first logits: a lane's four rows are consecutive in memory, one 16-byte store
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int n = nb + j * 16 + (lane & 15), m = mb + i * 16 + (lane >> 4) * 4;
+                if (m < g.M) *(f32x4 *)(g.out + (size_t)n * g.M + m) = acc[i][j];
             }
         return;
     }
@@ -459,7 +478,8 @@ constexpr int vm_wait_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4)
 // lo products accumulate separately (independent MFMA chains) and are added at the end.
 // Needs N % BN == 0, kc % BK == 0 and kc / BK >= NS - 1; rows past M re-read row M - 1.
 template <int DT, int BM, int BN, int BK, int NS>
-__global__ __launch_bounds__(kT) void k_gemm_pipe(GemmArgs g, float *partial, int kc) {
+__device__ __forceinline__ void pipe_product(const GemmArgs &g, int kc, uint8_t *lds,
+                                             f32x4 (&acc)[BM / 32][BN / 32]) {
     constexpr int FM = BM / 32, FN = BN / 32;
     constexpr int CPR = BK / 8;                 // 16-byte chunks per tile row
     constexpr int RB = BK * 2;                  // bytes per tile row
@@ -469,7 +489,6 @@ __global__ __launch_bounds__(kT) void k_gemm_pipe(GemmArgs g, float *partial, in
     constexpr int SB = ROWS * RB;               // bytes per ring slot
     static_assert(kT == 256 && ROWS % (4 * RPI) == 0 && BM % RPI == 0 && BN % RPI == 0 && CPR >= 4,
                   "each step's rows must split evenly over the four waves");
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
     const int kbeg = blockIdx.z * kc;
@@ -497,7 +516,7 @@ __global__ __launch_bounds__(kT) void k_gemm_pipe(GemmArgs g, float *partial, in
     };
     const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
     const int fr = lane & 15, fq = lane >> 4;
-    f32x4 acc[FM][FN], acl[FM][FN];
+    f32x4 acl[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -548,7 +567,16 @@ __global__ __launch_bounds__(kT) void k_gemm_pipe(GemmArgs g, float *partial, in
     for (int i = 0; i < FM; i++)
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] += acl[i][j];
-    tile_out<FM, FN>(g, partial, acc, m0 + wm, n0 + wn, lane);
+}
+
+template <int DT, int BM, int BN, int BK, int NS>
+__global__ __launch_bounds__(kT) void k_gemm_pipe(GemmArgs g, float *partial, int kc) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    f32x4 acc[BM / 32][BN / 32];
+    pipe_product<DT, BM, BN, BK, NS>(g, kc, lds, acc);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    tile_out<BM / 32, BN / 32>(g, partial, acc, blockIdx.x * BM + (wave >> 1) * (BM / 2),
+                               blockIdx.y * BN + (wave & 1) * (BN / 2), lane);
 }
 
 // The pipelined GEMM's shapes: 64 x 64 tiles with 6 slots of K 64 (147,456 bytes of LDS, one
@@ -827,6 +855,78 @@ __global__ __launch_bounds__(kT) void k_qk_rope(const float *qkv, QkRopeArgs a) 
         *(f32x4 *)(row + 4 * i4) = *(const f32x4 *)(qkv + (size_t)t * n + 4 * i4);
     __syncthreads();
     qk_rope_row<KVT>(row, t, a);
+}
+
+// The q|k|v projection of a model with 64-dim heads, its row epilogue fused (qk_rope_row's
+// QK-norm, RoPE and KV-cache fill, in the same operations and order): with 64 x 64 tiles of
+// the pipelined GEMM a tile is 64 rows of exactly one q, k or v head. The tile goes through
+// LDS (the ring is free once the product is done); wave w then finishes rows 16w..16w+15
+// with lane = head dim: the QK-norm sum is a butterfly over the wave, the RoPE partner of
+// dim 2p / 2p+1 the neighbouring lane. Saves the separate k_qk_rope launch.
+template <int DT, int KVT>
+__global__ __launch_bounds__(kT) void k_gemm_pipe_qkv64(GemmArgs g, QkRopeArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    f32x4 acc[2][2];
+    pipe_product<DT, 64, 64, 64, 6>(g, g.K, lds, acc);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    __syncthreads();   // every wave is done reading the ring
+    float *T = (float *)lds;   // [64][65]
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                T[(wm + i * 16 + (lane >> 4) * 4 + r) * 65 + wn + j * 16 + (lane & 15)] = acc[i][j][r];
+    __syncthreads();
+    const int m0 = blockIdx.x * 64, n0 = blockIdx.y * 64;
+    const int region = n0 < a.qdim ? 0 : n0 < a.qdim + a.kvdim ? 1 : 2;   // q, k or v head
+    const float gn = a.qk_norm && region < 2 ? (region == 0 ? a.q_norm : a.k_norm)[lane] : 1.f;
+    void *cache = region == 1 ? a.kcache : a.vcache;
+    float *kvo = region == 1 ? a.ko : a.vo;
+    const int j = n0 - a.qdim - (region == 2 ? a.kvdim : 0) + lane;
+    // positions and sequences of the wave's 16 rows (lane r holds row r's), then every row's
+    // RoPE factors, all requested before the first is used
+    const int r0 = m0 + wave * 16, nrows = min(16, g.M - r0);
+    int tpl = 0, sql = 0;
+    if (lane < nrows) {
+        tpl = a.rowpos[r0 + lane];
+        sql = a.rowseq[r0 + lane];
+    }
+    float cs[16], sn[16];
+    if (region < 2) {
+#pragma unroll
+        for (int rr = 0; rr < 16; rr++) {
+            const int tp = __shfl(tpl, rr, 64);
+            cs[rr] = a.rope_cos[tp * 32 + (lane >> 1)];
+            sn[rr] = a.rope_sin[tp * 32 + (lane >> 1)];
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 16; rr++) {
+        const int t = r0 + rr;
+        const int tp = __shfl(tpl, rr, 64), sq = __shfl(sql, rr, 64);
+        if (rr >= nrows) break;   // uniform over the wave
+        float v = T[(wave * 16 + rr) * 65 + lane];
+        if (region < 2) {
+            if (a.qk_norm) {
+                double ss = (double)v * (double)v;
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+                const float rn = (float)(1.0 / sqrt(ss / 64.0 + a.qk_eps));
+                v = v * rn * gn;
+            }
+            const float o = __shfl_xor(v, 1, 64);   // the other element of the pair
+            v = (lane & 1) ? v * cs[rr] + o * sn[rr] : v * cs[rr] - o * sn[rr];
+        }
+        if (region == 0) {
+            a.qo[(size_t)t * a.qdim + n0 + lane] = v;
+        } else {
+            if (a.write_cache) kv_store<KVT>(cache, (size_t)sq * a.kv_seq_stride + (size_t)tp * a.kvdim + j, v);
+            if (kvo) kvo[(size_t)t * a.kvdim + j] = a.write_cache || a.round_kv ? kv_round<KVT>(v) : v;
+        }
+    }
 }
 
 // Batched decode: row m of the q|k|v projection is the sum of the skinny GEMM's K-range
@@ -2324,7 +2424,13 @@ GemmPlan gemm_plan(int M, int N, int K) {
 hipError_t gemm_pipe_setup_once() {
     static hipError_t st = [] {
         const void *fns[] = {(const void *)k_gemm_pipe<SH_DTYPE_F16, 64, 64, 64, 6>,
-                             (const void *)k_gemm_pipe<SH_DTYPE_BF16, 64, 64, 64, 6>};
+                             (const void *)k_gemm_pipe<SH_DTYPE_BF16, 64, 64, 64, 6>,
+                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32>,
+                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F16>,
+                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16>,
+                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F32>,
+                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F16>,
+                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_BF16>};
         for (const void *f : fns) {
             const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPipeBigLds);
             if (e != hipSuccess) return e;
@@ -2543,6 +2649,32 @@ hipError_t launch_qk_rope(const sh_model *m, const LayerDev &L, int rows, const 
     return hipGetLastError();
 }
 
+// The fused q|k|v product and row epilogue (k_gemm_pipe_qkv64) applies to 16-bit models with
+// 64-dim heads whose projection the pipelined 64 x 64 GEMM takes unsplit (short inputs).
+bool qkv64_fused(const sh_model *m, int S) {
+    const int D = m->cfg.dim;
+    return m->dtype != SH_DTYPE_W8A8 && m->cfg.head_dim == 64 && S < 1024 && m->qkv_rows % 64 == 0 &&
+           D % 64 == 0 && D / 64 >= 5;
+}
+
+hipError_t launch_qkv64(const GemmArgs &g, const QkRopeArgs &a, int kv, hipStream_t s) {
+    hipError_t e = gemm_pipe_setup_once();
+    if (e != hipSuccess) return e;
+    const dim3 grid((g.M + 63) / 64, g.N / 64);
+    const bool bf = g.dt == SH_DTYPE_BF16;
+    if (kv == SH_KV_F32) {
+        if (bf) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F32>), grid, dim3(kT), kPipeBigLds, s, g, a);
+        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32>), grid, dim3(kT), kPipeBigLds, s, g, a);
+    } else if (kv == SH_KV_F16) {
+        if (bf) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F16>), grid, dim3(kT), kPipeBigLds, s, g, a);
+        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F16>), grid, dim3(kT), kPipeBigLds, s, g, a);
+    } else {
+        if (bf) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_BF16>), grid, dim3(kT), kPipeBigLds, s, g, a);
+        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16>), grid, dim3(kT), kPipeBigLds, s, g, a);
+    }
+    return hipGetLastError();
+}
+
 // W8A8: the decode-order attention of `rows` query rows (k_attn_exact), keys from the
 // token-major pf_k / pf_v of the forward or, with from_cache, from layer l of the KV cache.
 hipError_t launch_attn_exact(const sh_model *m, int rows, const float *q, bool from_cache, int l,
@@ -2649,8 +2781,13 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
     g.A = m->pf_xn; g.B = (const uint16_t *)L.wqkv; g.M = S; g.N = m->qkv_rows; g.K = D;
     g.epi = G_STORE; g.out = m->pf_qkv; g.dt = dt;
     g.sw = L.s_qkv; g.a8 = m->pf_a8; g.sa = m->pf_sa;
-    if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;
-    if (ranges > 1) {
+    if (qkv64_fused(m, S)) {
+        const QkRopeArgs a = qk_rope_args(m, L, m->pf_rowpos, m->pf_rowseq, m->pf_q, m->pf_k, m->pf_v, l,
+                                          fill_kv);
+        if ((e = launch_qkv64(g, a, c.kv_dtype, s)) != hipSuccess) return e;
+    } else if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) {
+        return e;
+    } else if (ranges > 1) {
         const QkRopeArgs a = qk_rope_args(m, L, m->pf_rowpos, m->pf_rowseq, m->pf_q, m->pf_k, m->pf_v, l,
                                           fill_kv);
         const float *pp = m->pf_part;
