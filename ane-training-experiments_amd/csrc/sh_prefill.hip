@@ -584,6 +584,7 @@ __global__ __launch_bounds__(kT) void k_gemm_pipe(GemmArgs g, float *partial, in
 // (49,152 bytes) and up to four K ranges.
 constexpr int kPipeBigLds = 6 * (3 * 64) * 128;
 constexpr int kPipeSmallLds = 4 * (3 * 32) * 128;
+constexpr int kPipeWideLds = 4 * (2 * 32 + 64) * 128;   // 32 x 64 tiles (65,536 bytes)
 
 // ---- W8A8 products on the int8 matrix cores --------------------------------------------
 
@@ -2435,6 +2436,11 @@ hipError_t gemm_pipe_setup_once() {
             const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPipeBigLds);
             if (e != hipSuccess) return e;
         }
+        for (const void *f : {(const void *)k_gemm_pipe<SH_DTYPE_F16, 32, 64, 64, 4>,
+                              (const void *)k_gemm_pipe<SH_DTYPE_BF16, 32, 64, 64, 4>}) {
+            const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPipeWideLds);
+            if (e != hipSuccess) return e;
+        }
         return hipSuccess;
     }();
     return st;
@@ -3001,10 +3007,32 @@ hipError_t skinny(const GemmArgs &g, int dt, float *partial, size_t part_cap, hi
     const int kc = skinny_kc(g.N, g.K), ranges = g.K / kc;
     if ((ranges > 1 || g.partial_only) && (size_t)ranges * g.M * g.N > part_cap)
         return hipErrorInvalidValue;   // the partial buffer must hold every K range
-    // 64-column workgroups share the A rows through LDS; narrow products whose 64-column grid
-    // would leave CUs idle take 16-column workgroups instead (1.6% per 32-sequence
-    // Qwen3-shaped step, on its Wo and W2 products)
-    if (g.N % 64 == 0 && kc % 256 == 0 && (g.N / 64) * ranges >= 256) {
+    const bool bf = dt == SH_DTYPE_BF16;
+    // The pipelined GEMM with one 32-row tile over the rows, in the same K ranges (so the
+    // row kernels and the attention sum the same partials): 32-column tiles, 64-column ones
+    // for very wide outputs (the classifier). Against k_gemm_skinny64 / k_gemm_skinny on the
+    // 32-sequence Qwen3-shaped step's products: qkv 5.2 -> 3.6 us, wo 4.5 -> 3.0, w13 6.6 ->
+    // 4.2, w2 5.6 -> 3.4, the classifier 104 -> 68.
+    if (kc % 64 == 0 && kc / 64 >= 3 && g.N % 32 == 0) {
+        hipError_t e0 = gemm_pipe_setup_once();
+        if (e0 != hipSuccess) return e0;
+        GemmArgs h = g;
+        if (g.partial_only && ranges == 1) {   // the "partial" is the plain product
+            h.epi = G_STORE;
+            h.out = partial;
+        }
+        if (g.N >= 16384 && g.N % 64 == 0) {
+            const dim3 grid(1, g.N / 64, ranges);
+            if (bf) hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_BF16, 32, 64, 64, 4>), grid, dim3(kT), kPipeWideLds, s, h, partial, kc);
+            else hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_F16, 32, 64, 64, 4>), grid, dim3(kT), kPipeWideLds, s, h, partial, kc);
+        } else {
+            const dim3 grid(1, g.N / 32, ranges);
+            if (bf) hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_BF16, 32, 32, 64, 4>), grid, dim3(kT), kPipeSmallLds, s, h, partial, kc);
+            else hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_F16, 32, 32, 64, 4>), grid, dim3(kT), kPipeSmallLds, s, h, partial, kc);
+        }
+    } else if (g.N % 64 == 0 && kc % 256 == 0 && (g.N / 64) * ranges >= 256) {
+        // 64-column workgroups share the A rows through LDS; narrow products whose 64-column
+        // grid would leave CUs idle take 16-column workgroups instead
         const dim3 grid(g.N / 64, ranges);
         if (dt == SH_DTYPE_BF16) hipLaunchKernelGGL(k_gemm_skinny64<SH_DTYPE_BF16>, grid, dim3(kT), 0, s, g, partial, kc);
         else hipLaunchKernelGGL(k_gemm_skinny64<SH_DTYPE_F16>, grid, dim3(kT), 0, s, g, partial, kc);
