@@ -2991,7 +2991,13 @@ hipError_t enqueue_transpose(const float *src, int rows, int cols, float *dst, h
 namespace {
 // K range per workgroup of the skinny GEMM: 256 (four waves x two k-steps, every load in
 // flight at once) when that splits K evenly and the columns alone give too few workgroups.
-int skinny_kc(int N, int K) { return (N / 16 < 2048 && K % 256 == 0) ? 256 : K; }
+// K range of the M <= 32-row products: 512 where K allows (the 32-sequence Qwen3-shaped step:
+// 2.13 ms, against 2.17 with ranges of 256 and 2.23 with 1024), the whole K for very wide
+// outputs (the classifier), whose grid alone covers the CUs.
+int skinny_kc(int N, int K) {
+    if (N / 16 >= 2048) return K;
+    return K % 512 == 0 ? 512 : K % 256 == 0 ? 256 : K;
+}
 
 hipError_t skinny(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipStream_t s) {
     if (g.K % 128 || g.N % 16 || g.M > 32) return hipErrorInvalidValue;
@@ -3004,7 +3010,10 @@ hipError_t skinny(const GemmArgs &g, int dt, float *partial, size_t part_cap, hi
         }
         return gemm_i8(h, s);
     }
-    const int kc = skinny_kc(g.N, g.K), ranges = g.K / kc;
+    // the gate product runs unsplit on the pipelined GEMM, its SiLU gate in the epilogue (no
+    // partials and no reduce kernel)
+    const bool gate1 = g.epi == G_GATE && !g.partial_only && g.K % 64 == 0 && g.K / 64 >= 3 && g.N % 32 == 0;
+    const int kc = gate1 ? g.K : skinny_kc(g.N, g.K), ranges = g.K / kc;
     if ((ranges > 1 || g.partial_only) && (size_t)ranges * g.M * g.N > part_cap)
         return hipErrorInvalidValue;   // the partial buffer must hold every K range
     const bool bf = dt == SH_DTYPE_BF16;
