@@ -144,56 +144,123 @@ __global__ __launch_bounds__(256) void k_sgemm(const float *A, int lda, const fl
         }
 }
 
-// k_sgemm for tile-aligned shapes (M, N multiples of 64, every K range a multiple of 128): the
-// loads of eight K blocks (128 k) issue together, with no bounds checks and so no branches,
-// and then pass through the two LDS buffers one block at a time (one barrier per block: a
-// buffer is rewritten two blocks after it was read). A workgroup then waits out one load
-// latency per eight blocks instead of one per block.
+// s_waitcnt immediate that waits until at most n vector memory operations of the wave are
+// outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and lgkmcnt not waited for).
+constexpr int sg_vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// k_sgemm for tile-aligned shapes (M, N multiples of 64, every K range a multiple of 128),
+// pipelined: the A and B tiles of each 32-k block (two 16-k sub-blocks) stream into a
+// kSgNs-deep LDS ring by global_load_lds (each lane moves 16 bytes straight into LDS, a wave
+// instruction fills 1 KB; waves 0-1 load A, waves 2-3 load B), so kSgNs - 1 blocks are always
+// in flight. One barrier per block: wait for this wave's loads of block s (explicit vmcnt; the
+// fence of __syncthreads would wait for every load in flight), s_barrier, issue block
+// s + kSgNs - 1 into the slot block s - 1 used, MFMAs of block s. (Reading block s + 1's
+// operands into a second register set during block s's MFMAs, with every iteration issuing
+// one block, was slower: 4.43 against 4.26 ms per Stories110M S = 256 step; one 16-k
+// block per slot in 6 slots took 4.26 ms, two per slot in 4 slots 4.24.)
+// LDS layouts of each 16-k sub-tile, chosen so the MFMA reads spread over the banks:
+//  k-contiguous operand (rows of the tile along m or n, 64 bytes of k each): 16-byte chunk c
+//    of row r in slot c ^ ((r >> 1) & 3);
+//  otherwise (rows along k, 256 bytes of m or n each): chunk c of k-row r in slot
+//    c ^ (4 * ((r >> 2) & 3)).
+// Within a sub-block, MFMA step j (of 4) has lane group l (lane / 16) on k = 4l + j, so a
+// k-contiguous operand gives each lane its four steps' values in one 16-byte read. The
+// products are fp32 and exact as in k_sgemm; only the order of the fp32 sums differs.
+constexpr int kSgNs = 4, kSgKb = 16, kSgH = 2;   // ring slots; k per sub-block; sub-blocks per slot
+template <bool XK>
+__device__ __forceinline__ float sg_read(const uint8_t *T, int r, int j, int lk) {
+    if constexpr (XK) {
+        return ((const float *)(T + r * 64 + ((lk ^ ((r >> 1) & 3)) << 4)))[j];
+    } else {
+        const int k = 4 * lk + j;
+        return ((const float *)(T + k * 256 + (((r >> 2) ^ (4 * ((k >> 2) & 3))) << 4)))[r & 3];
+    }
+}
+
 template <bool AK, bool BK, int EPI>
-__global__ __launch_bounds__(256) void k_sgemm_nb(const float *A, int lda, const float *B, int ldb, float *C,
-                                                  int ldc, int M, int N, int K, float alpha, const float *R,
-                                                  int kc) {
-    constexpr int NB = 8;
-    __shared__ __attribute__((aligned(16))) float As[2][kGK][kGM + kGP];
-    __shared__ __attribute__((aligned(16))) float Bs[2][kGK][kGN + kGP];
+__global__ __launch_bounds__(256) void k_sgemm_pipe(const float *A, int lda, const float *B, int ldb, float *C,
+                                                    int ldc, int M, int N, int K, float alpha, const float *R,
+                                                    int kc) {
+    constexpr int TB = kGM * kSgKb * 4;   // bytes of one operand sub-tile (4 KB)
+    constexpr int SB = 2 * kSgH * TB;     // a slot: the A sub-tiles, then the B sub-tiles
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kSgNs * SB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
     const int m0 = blockIdx.y * kGM, n0 = blockIdx.x * kGN;
-    f32x4 acc[2][2];
-    for (int i = 0; i < 2; i++)
-        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int kb = blockIdx.z * kc, ke = min(K, kb + kc);
-    // this thread's 16-byte chunk of a K block: AK (row tid/4, k 4*(tid%4)), else (k tid/16,
-    // rows 4*(tid%16)); likewise for B
-    const float *pa = AK ? A + (size_t)(m0 + tid / 4) * lda + (tid % 4) * 4 : A + (size_t)(tid / 16) * lda + m0 + (tid % 16) * 4;
-    const float *pb = BK ? B + (size_t)(n0 + tid / 4) * ldb + (tid % 4) * 4 : B + (size_t)(tid / 16) * ldb + n0 + (tid % 16) * 4;
-    const size_t sa = AK ? kGK : (size_t)kGK * lda, sb = BK ? kGK : (size_t)kGK * ldb;   // per K block
-    const int lr = lane & 15, lk = lane >> 4;
-    for (int k0 = kb; k0 < ke; k0 += NB * kGK) {
-        f32x4 ra[NB], rb[NB];
-        const size_t oa = AK ? (size_t)k0 : (size_t)k0 * lda, ob = BK ? (size_t)k0 : (size_t)k0 * ldb;
+    const int nsteps = (ke - kb) / (kSgKb * kSgH);
+    // this wave's two instructions per sub-block: operand X (A for waves 0-1, B for 2-3), tile
+    // instructions q = 2 * (wave & 1) + i
+    const bool isa = wave < 2;
+    const bool xk = isa ? AK : BK;
+    const float *X = isa ? A : B;
+    const int ld = isa ? lda : ldb, r0 = isa ? m0 : n0;
+    const float *src[2];
+    int dst[2];
+    size_t step[2];
 #pragma unroll
-        for (int u = 0; u < NB; u++) {
-            ra[u] = *(const f32x4 *)(pa + oa + u * sa);
-            rb[u] = *(const f32x4 *)(pb + ob + u * sb);
+    for (int i = 0; i < 2; i++) {
+        const int q = 2 * (wave & 1) + i;
+        if (xk) {
+            const int r = q * 16 + lane / 4, c = (lane % 4) ^ ((r >> 1) & 3);
+            src[i] = X + (size_t)(r0 + r) * ld + kb + c * 4;
+            step[i] = kSgKb;
+        } else {
+            const int kr = q * 4 + lane / 16, c = (lane % 16) ^ (4 * ((kr >> 2) & 3));
+            src[i] = X + (size_t)(kb + kr) * ld + r0 + c * 4;
+            step[i] = (size_t)kSgKb * ld;
         }
-#pragma unroll
-        for (int u = 0; u < NB; u++) {
-            const int buf = u & 1;
-            gemm_stage<AK>(As[buf], ra[u], tid);
-            gemm_stage<BK>(Bs[buf], rb[u], tid);
-            __syncthreads();
-#pragma unroll
-            for (int kk = 0; kk < kGK; kk += 4) {
-                const float a0 = As[buf][kk + lk][wm + lr], a1 = As[buf][kk + lk][wm + 16 + lr];
-                const float b0 = Bs[buf][kk + lk][wn + lr], b1 = Bs[buf][kk + lk][wn + 16 + lr];
-                acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
-                acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
-                acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
-                acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
-            }
-        }
+        dst[i] = (isa ? 0 : kSgH * TB) + q * 1024;
     }
+    auto issue = [&](int st, int slot) {   // block st (kSgH sub-blocks) into ring slot `slot`
+        uint8_t *base = lds + slot * SB;
+#pragma unroll
+        for (int h = 0; h < kSgH; h++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(src[i] + (size_t)(st * kSgH + h) * step[i]),
+                    (__attribute__((address_space(3))) void *)(base + h * TB + dst[i]), 16, 0, 0);
+    };
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int lr = lane & 15, lk = lane >> 4;
+    auto compute = [&](int st) {
+#pragma unroll
+      for (int h = 0; h < kSgH; h++) {
+        const uint8_t *TA = lds + (st % kSgNs) * SB + h * TB, *TBp = TA + kSgH * TB;
+        float a[2][4], b[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                a[i][j] = sg_read<AK>(TA, wm + i * 16 + lr, j, lk);
+                b[i][j] = sg_read<BK>(TBp, wn + i * 16 + lr, j, lk);
+            }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int jj = 0; jj < 2; jj++)
+                    acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][j], b[jj][j], acc[i][jj], 0, 0, 0);
+      }
+    };
+#pragma unroll
+    for (int st = 0; st < kSgNs - 1; st++) issue(st, st);
+    int st = 0;
+    for (; st < nsteps - (kSgNs - 1); st++) {
+        __builtin_amdgcn_s_waitcnt(sg_vm_wait((kSgNs - 2) * 2 * kSgH));
+        __builtin_amdgcn_s_barrier();
+        issue(st + kSgNs - 1, (st + kSgNs - 1) % kSgNs);
+        compute(st);
+    }
+    __builtin_amdgcn_s_waitcnt(sg_vm_wait(0));
+    __builtin_amdgcn_s_barrier();
+    for (; st < nsteps; st++) compute(st);
     for (int i = 0; i < 2; i++)
         for (int j = 0; j < 2; j++) {
             const int n = n0 + wn + j * 16 + lr;
@@ -1366,7 +1433,7 @@ hipError_t sgemm(hipStream_t s, const float *A, int lda, const float *B, int ldb
                  int N, int K, float alpha, const float *R = nullptr) {
     const dim3 grid((N + kGN - 1) / kGN, (M + kGM - 1) / kGM);
     if (sgemm_aligned(M, N, K, K))
-        hipLaunchKernelGGL((k_sgemm_nb<AK, BK, EPI>), grid, dim3(256), 0, s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R, K);
+        hipLaunchKernelGGL((k_sgemm_pipe<AK, BK, EPI>), grid, dim3(256), 0, s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R, K);
     else
         hipLaunchKernelGGL((k_sgemm<AK, BK, EPI>), grid, dim3(256), 0, s, A, lda, B, ldb, C, ldc, M, N, K, alpha, R, K);
     return hipGetLastError();
@@ -1395,8 +1462,8 @@ hipError_t sgemm_split(hipStream_t s, const float *A, int lda, const float *B, i
     ranges = (K + kc - 1) / kc;
     const dim3 grid((N + kGN - 1) / kGN, (M + kGM - 1) / kGM, ranges);
     if (al)
-        hipLaunchKernelGGL((k_sgemm_nb<AK, BK, EPI_PART>), grid, dim3(256), 0, s, A, lda, B, ldb, part, ldc, M, N, K,
-                           1.f, nullptr, kc);
+        hipLaunchKernelGGL((k_sgemm_pipe<AK, BK, EPI_PART>), grid, dim3(256), 0, s, A, lda, B, ldb, part, ldc, M, N,
+                           K, 1.f, nullptr, kc);
     else
         hipLaunchKernelGGL((k_sgemm<AK, BK, EPI_PART>), grid, dim3(256), 0, s, A, lda, B, ldb, part, ldc, M, N, K,
                            1.f, nullptr, kc);
