@@ -412,7 +412,8 @@ __device__ __forceinline__ void ll_poll_regs(int n, const PParams &p, const Inpu
 //   W8A8:        the reference's order, xs = (x * rrms) * gain, then the per-tensor int8
 //                quantization (its boundaries must see the reference's values).
 // Barriers: the poll's first (frees LDS), one after the partial sums (and the ok flags), and
-// for W8A8 two more around the quantization.
+// for W8A8 two more around the quantization (one: a stage without a norm carries max|x| in the
+// partial-sum barrier).
 template <int WT, int COLS, bool NORM, typename Pre>
 __device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &map, int count,
                             const uint16_t *emb_row, const uint16_t *res_emb, const float *gain,
@@ -450,15 +451,17 @@ __device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &ma
     } else {
         ll_poll_regs<K>(res_emb ? n : count, p, map, val, ok, pre);
     }
-    // sum of squares: float64 as the reference for W8A8, float for the fp16/bf16 models
+    // sum of squares: float64 as the reference for W8A8, float for the fp16/bf16 models. W8A8
+    // without a norm needs only max|x| for its scale, which rides on the same barrier.
     double ss = 0;
-    float ssf = 0.f;
+    float ssf = 0.f, mx0 = 0.f;
 #pragma unroll
     for (int k = 0; k < K; k++) {
         const int j = threadIdx.x + k * kPB;
         if (j < n) {
             if constexpr (NORM && Q8) ss += (double)val[k] * (double)val[k];
             if constexpr (NORM && !Q8) ssf += val[k] * val[k];
+            if constexpr (!NORM && Q8) mx0 = fmaxf(mx0, fabsf(val[k]));
             if constexpr (!Q8) xs[j] = NORM ? val[k] * gr[NORM ? k : 0] : val[k];
         } else if (j < count) {
             xs[j] = val[k];   // residual rows
@@ -466,6 +469,7 @@ __device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &ma
     }
     if constexpr (NORM && Q8) ss = wsum_d64(ss);
     if constexpr (NORM && !Q8) ss = (double)wsum<64>(ssf);
+    if constexpr (!NORM && Q8) ss = (double)wmax<64>(mx0);
     const bool wok = __all(ok);
     if (lane == 0) {
         red[wave] = ss;
@@ -477,7 +481,8 @@ __device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &ma
 #pragma unroll
     for (int w = 0; w < kPW; w++) {
         all_ok = all_ok && okw[w];
-        tot += red[w];
+        if constexpr (!NORM && Q8) tot = fmax(tot, red[w]);
+        else tot += red[w];
     }
     if (!all_ok) return false;
     float rrms = 1.f;
@@ -490,15 +495,19 @@ __device__ __forceinline__ bool stage_input(float *xs, int n, const InputMap &ma
         // xs = (x * rrms) * g in the reference's order; s_a = max|xs| / 127 (0 -> 1);
         // each element quantized on its own thread into a byte of xq (ane_bridge.m:374-399)
         float mx = 0.f;
+        if constexpr (NORM) {
 #pragma unroll
-        for (int k = 0; k < K; k++) {
-            const int j = threadIdx.x + k * kPB;
-            if (j < n) {
-                if constexpr (NORM) val[k] = val[k] * rrms * gr[NORM ? k : 0];
-                mx = fmaxf(mx, fabsf(val[k]));
+            for (int k = 0; k < K; k++) {
+                const int j = threadIdx.x + k * kPB;
+                if (j < n) {
+                    val[k] = val[k] * rrms * gr[k];
+                    mx = fmaxf(mx, fabsf(val[k]));
+                }
             }
+            mx = block_max(mx);
+        } else {
+            mx = (float)tot;   // the workgroup's max|x|, exact through float64
         }
-        mx = block_max(mx);
         float s = __fdiv_rn(mx, 127.0f);
         if (s == 0.0f) s = 1.0f;
         *sa = s;
