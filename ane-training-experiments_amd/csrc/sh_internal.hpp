@@ -44,6 +44,7 @@ struct ArgmaxPartial {
 // i < n, owns rows [i*per, (i+1)*per), so the hand-over words it writes are contiguous.
 struct StageOwn {
     int off, n, per;
+    int row0;   // first row of rank 0's block (blocks start at row0 + rank * per)
 };
 
 }  // namespace sh
@@ -90,6 +91,11 @@ struct sh_model {
     // grid) own row blocks of `per` rows in order
     sh::StageOwn p_own[5];
     int p_ostride[5];       // hand-over words between consecutive workgroups' output blocks
+    // classifier split when its rows fit: the attention workgroups own p_own_cls_a (their
+    // register tile), the others p_own[4] whose last p_cls_lds_rows rows stay in LDS for the
+    // launch; p_own_cls_a.n == 0: p_own[4] for every workgroup
+    sh::StageOwn p_own_cls_a;
+    int p_cls_lds_rows;
     void *p_layers;         // device array of per-layer weight pointers
     uint64_t *ll_qkv, *ll_att, *ll_x2, *ll_gate, *ll_x, *ll_pv, *ll_pi;
     int *p_err;

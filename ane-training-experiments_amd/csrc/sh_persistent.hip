@@ -100,6 +100,8 @@ struct PParams {
     long long *trace;  // stage timestamps of forward trace_f (workgroups 0 and grid-1)
     int trace_f;
     StageOwn own[5];   // qkv, wo, w13, w2, classifier
+    StageOwn own_cls_a;   // classifier rows of the attention workgroups (n == 0: own[4])
+    int cls_lds_rows;     // classifier rows a non-attention workgroup keeps in LDS (0: none)
     int ostride[5];    // words between consecutive workgroups' output blocks, per stage
     uint32_t omagic[5];  // ceil(2^31 / elements per output block), per stage
 };
@@ -552,7 +554,7 @@ __device__ __forceinline__ bool own_block(const StageOwn o, int rows, int &rank,
     rank = (int)blockIdx.x - o.off;
     if (rank < 0) rank += gridDim.x;
     if (rank >= o.n) return false;
-    r0 = rank * o.per;
+    r0 = o.row0 + rank * o.per;
     r1 = min(rows, r0 + o.per);
     return r0 < r1;
 }
@@ -640,12 +642,15 @@ __device__ __forceinline__ void settle_loads() {
 // holding the first U row groups of each wave (further groups stream through it), then the
 // epilogue and the block's hand-over stores. For E_CLS, *best_v/*best_i receive this wave's
 // (max, first index).
+// Rows from lrow0 on, when lrows is given, are read from LDS (lrows: those rows back to back)
+// instead of W.
 template <int LPR, int CPL, int WT, int U>
 __device__ __forceinline__ void stage_compute(const PParams &p, const void *__restrict__ W,
                                               const float *__restrict__ wscale, int cols, int epi,
                                               const StageIO &io, float *xs, uint32_t *xq, float *ostage,
                                               float &best_v, int &best_i, const StageCtx &c,
-                                              WTile<U, CPL> &t) {
+                                              WTile<U, CPL> &t, const SH_LDS uint8_t *lrows = nullptr,
+                                              int lrow0 = 0) {
     constexpr int G = 64 / LPR;
     constexpr bool Q8 = WT == SH_DTYPE_W8A8;
     const SH_GLOBAL uint8_t *Wb = (const SH_GLOBAL uint8_t *)W;
@@ -702,9 +707,15 @@ __device__ __forceinline__ void stage_compute(const PParams &p, const void *__re
             for (int u = 0; u < U; u++) {
                 const int row = gbase(k0 + U + u) + grp;
                 if (row < r1) {
-                    const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(Wb + (size_t)row * row_bytes);
+                    if (lrows && gbase(k0 + U + u) >= lrow0) {   // wave-uniform
+                        const SH_LDS u32x4 *src = (const SH_LDS u32x4 *)(lrows + (size_t)(row - lrow0) * row_bytes);
 #pragma unroll
-                    for (int j = 0; j < CPL; j++) w[u][j] = src[sub + j * LPR];
+                        for (int j = 0; j < CPL; j++) w[u][j] = src[sub + j * LPR];
+                    } else {
+                        const SH_GLOBAL u32x4 *src = (const SH_GLOBAL u32x4 *)(Wb + (size_t)row * row_bytes);
+#pragma unroll
+                        for (int j = 0; j < CPL; j++) w[u][j] = src[sub + j * LPR];
+                    }
                 }
             }
         }
@@ -1329,6 +1340,20 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
     return true;
 }
 
+// Asynchronous copy of bytes [0, nbytes) from src (nbytes a multiple of 16, at most kKvStage)
+// into LDS, 1 KB per wave instruction (global_load_lds, 16 bytes per lane); a lane past the
+// end re-reads the last 16 bytes, so every read stays in bounds.
+__device__ __forceinline__ void bytes_to_lds(const uint8_t *src, int nbytes, uint8_t *lds) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = nbytes / 16;
+    for (int base = wave * 64; base < n; base += kPW * 64) {
+        const int c = min(base + lane, n - 1);
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src + (size_t)c * 16),
+                                         (__attribute__((address_space(3))) void *)(lds + (size_t)base * 16), 16, 0,
+                                         0);
+    }
+}
+
 template <int WT, int KVT, int HD, int LD, int CD, int LQ, int CQ, int LF, int CF>
 __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     __shared__ float xs[kXs];
@@ -1347,6 +1372,25 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     const int L = p.L;
     const int n_stamps = 5 * L + 3;
     int tok_next = 0;
+    // Classifier rows: the attention workgroups own what their register tile holds; with
+    // cls_lds_rows the others own twice as many and keep the second half in the attention
+    // cache's LDS (unused outside attention) for the whole launch, copied here once.
+    // (Instantiated for the 16-bit 64-dim-head shapes only: elsewhere the vocabulary does not
+    // split so, and the branch would cost the larger shapes registers.)
+    constexpr bool kClsLds = WT != SH_DTYPE_W8A8 && HD == 64;
+    constexpr int kClsTileRows = 4 * kPW * (64 / LD);   // rows of the classifier's WTile<4>
+    const StageOwn cown = p.own_cls_a.n && (int)blockIdx.x < p.KVH ? p.own_cls_a : p.own[4];
+    const SH_LDS uint8_t *cls_lds = nullptr;
+    int cls_lrow0 = 0;
+    if (kClsLds && p.cls_lds_rows && (int)blockIdx.x >= p.KVH) {
+        int rk, a0, a1;
+        if (own_block(cown, p.V, rk, a0, a1) && a1 > a0 + kClsTileRows) {
+            const int row_bytes = p.D * elem_bytes<WT>();
+            cls_lrow0 = a0 + kClsTileRows;
+            bytes_to_lds((const uint8_t *)p.cls + (size_t)cls_lrow0 * row_bytes, (a1 - cls_lrow0) * row_bytes, kvlds);
+            cls_lds = (const SH_LDS uint8_t *)kvlds;
+        }
+    }
     // Each GEMV stage keeps the weights of its first row groups in registers (qkv and w13: two
     // per wave, wo and w2: one, the classifier: four), loaded inside the stage's poll right
     // after its first requests.
@@ -1497,13 +1541,15 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             WTile<4, CD> t;
             {
                 StageCtx ct{};
-                if (!own_block(p.own[4], p.V, ct.rank, ct.r0, ct.r1)) ct.r0 = ct.r1 = 0;
+                if (!own_block(cown, p.V, ct.rank, ct.r0, ct.r1)) ct.r0 = ct.r1 = 0;
                 tile_load<LD, CD, WT, 4>(t, ct, p.cls, p.D);
             }
-            const int r = stage_poll<LD, CD, WT, true>(p, p.own[4], p.V, p.D, E_CLS, io, xs, xq, red, okw, c,
+            const int r = stage_poll<LD, CD, WT, true>(p, cown, p.V, p.D, E_CLS, io, xs, xq, red, okw, c,
                                                        [](const StageCtx &) {});
             if (r < 0) return;
-            if (r) stage_compute<LD, CD, WT, 4>(p, p.cls, p.s_cls, p.D, E_CLS, io, xs, xq, ostage, bv, bi, c, t);
+            if (r)
+                stage_compute<LD, CD, WT, 4>(p, p.cls, p.s_cls, p.D, E_CLS, io, xs, xq, ostage, bv, bi, c, t, cls_lds,
+                                             cls_lrow0);
         }
         stamp();
         // this workgroup's (max, first index)
@@ -1599,6 +1645,13 @@ PersistentKernel pick_shape(int D, int Q, int F, int HDv) {
     return nullptr;
 }
 
+// Lanes per weight row of the model-dim stages (qkv, w13, classifier) in pick_shape's
+// instances: their LD parameter.
+int shape_ld(int dtype, int D) {
+    if (dtype == SH_DTYPE_W8A8) return D == 1024 ? 32 : (D == 768 ? 16 : 8);
+    return D == 128 ? 16 : 32;
+}
+
 PersistentKernel pick_persistent(int dtype, int kv, int D, int Q, int F, int HDv) {
     if (dtype == SH_DTYPE_F16) {
         if (kv == SH_KV_F32) return pick_shape<SH_DTYPE_F16, SH_KV_F32>(D, Q, F, HDv);
@@ -1689,6 +1742,23 @@ hipError_t persistent_plan(sh_model *m, std::string *why) {
     m->p_own[2] = StageOwn{0, grid, per13};
     m->p_own[3] = StageOwn{0, n_w2, per_w2};
     m->p_own[4] = StageOwn{0, grid, cdiv(c.vocab, grid)};
+    // classifier: the attention workgroups keep only their register tile's rows (their LDS
+    // holds the attention cache); the others twice that, the second half resident in LDS for
+    // the launch, where the vocabulary splits so and those rows fit the cache stage
+    m->p_own_cls_a = StageOwn{0, 0, 0, 0};
+    m->p_cls_lds_rows = 0;
+    {
+        const int rt = 4 * kPW * (64 / shape_ld(m->dtype, c.dim));
+        const int row_bytes = c.dim * wbytes;
+        const int rest = c.vocab - KVH * rt;
+        const int per_b = rest > 0 && grid > KVH ? cdiv(rest, grid - KVH) : 0;
+        if (m->dtype != SH_DTYPE_W8A8 && c.head_dim == 64 && per_b > rt && per_b <= 2 * rt &&
+            (per_b - rt) * row_bytes <= kKvStage) {
+            m->p_own_cls_a = StageOwn{0, KVH, rt, 0};
+            m->p_own[4] = StageOwn{KVH, grid - KVH, per_b, KVH * rt};
+            m->p_cls_lds_rows = per_b - rt;
+        }
+    }
     if (per_wo > kMaxRes || per_w2 > kMaxRes) return hipErrorInvalidConfiguration;
     if (per_qkv > kMaxPer || per13 > kMaxPer) return hipErrorInvalidConfiguration;
     m->p_ostride[0] = per_qkv;   // a multiple of 16: qkv stays dense for the attention stage
@@ -1698,7 +1768,12 @@ hipError_t persistent_plan(sh_model *m, std::string *why) {
     m->p_ostride[4] = 0;
     *why += "; rows/workgroups qkv " + std::to_string(per_qkv) + "x" + std::to_string(n_qkv) + " wo " +
             std::to_string(per_wo) + "x" + std::to_string(n_wo) + " w13 " + std::to_string(per13) + "x" +
-            std::to_string(grid) + " w2 " + std::to_string(per_w2) + "x" + std::to_string(n_w2);
+            std::to_string(grid) + " w2 " + std::to_string(per_w2) + "x" + std::to_string(n_w2) +
+            (m->p_cls_lds_rows ? " classifier " + std::to_string(m->p_own_cls_a.per) + "x" +
+                                     std::to_string(m->p_own_cls_a.n) + " + " + std::to_string(m->p_own[4].per) +
+                                     "x" + std::to_string(m->p_own[4].n) + " (" +
+                                     std::to_string(m->p_cls_lds_rows) + " rows each resident in LDS)"
+                               : std::string(""));
     return hipSuccess;
 }
 
@@ -1755,6 +1830,8 @@ hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt
     p.quiet = m->spin_ticks / 100000;
     p.trace = m->trace_f >= 0 ? m->trace_buf : nullptr;
     p.trace_f = m->trace_f;
+    p.own_cls_a = m->p_own_cls_a;
+    p.cls_lds_rows = m->p_cls_lds_rows;
     for (int i = 0; i < 5; i++) {
         p.own[i] = m->p_own[i];
         p.ostride[i] = m->p_ostride[i];
