@@ -841,10 +841,11 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
     // The prompt's first n_prompt-1 positions only fill the KV cache (their logits are never
     // read): one causal forward over them on the full-sequence path, in the decode forms of
     // the softmax sum and SiLU, stores the cache a token-by-token decode would store, to the
-    // rounding of its fp32 sums. The token loop then starts at the last prompt id. W8A8 keeps
-    // the token-by-token prompt: its bit-exactness rests on the reference's summation order.
+    // rounding of its fp32 sums (W8A8: bit for bit, its full-sequence forward keeping the
+    // decode's per-token quantization, float order and exact attention). The token loop then
+    // starts at the last prompt id.
     std::string why;
-    const int pre = (m->dtype != SH_DTYPE_W8A8 && n_prompt > 1 && prefill_supported(m, &why)) ? n_prompt - 1 : 0;
+    const int pre = (n_prompt > 1 && prefill_supported(m, &why)) ? n_prompt - 1 : 0;
     if (pre > 0) {
         if (!hip_ok(prefill_alloc(m, pre, false), "prefill scratch")) return -1;
         std::vector<int32_t> rows(3 * (size_t)pre);

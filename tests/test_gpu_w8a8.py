@@ -81,10 +81,11 @@ def test_w8a8_shape_without_persistent_kernel_is_rejected(gpu):
 
 def test_stories110m_w8a8_greedy_128(gpu):
     """Stories110M W8A8: per-row int8 of the seed-0 N(0, 0.02) weights, 16-id prompt from
-    seed 1, 128 new tokens; identical token stream, and the logits of all 143 forwards
-    bit-identical to the oracle's; then the last forward's intermediates (sh_decode_tap,
-    the counterpart of the engine's cache taps, engine_test.go:154-239) equal the oracle's
-    bit for bit."""
+    seed 1, 128 new tokens; identical token stream, the last forward's intermediates
+    (sh_decode_tap, the counterpart of the engine's cache taps, engine_test.go:154-239)
+    equal to the oracle's bit for bit both after the greedy decode (prompt cache from the
+    full-sequence forward) and after a token-by-token replay, whose logits at all 143
+    forwards are bit-identical to the oracle's."""
     cfg = sh.stories110m_config()
     m, ref = build(cfg, seed=0)
     prompt = sh.synth_tokens(16, 1, cfg.vocab)
@@ -97,6 +98,9 @@ def test_stories110m_w8a8_greedy_128(gpu):
     print(f"persistent={st['persistent']} grid={st['grid']} {st['gpu_ms']:.3f} ms for "
           f"{st['forwards']} forwards, {st['bytes_per_forward_mean'] / 1e6:.2f} MB/forward")
     assert st["persistent"]
+    # the decode's last forward, after the prompt's KV cache was filled by the full-sequence
+    # forward: its intermediates equal the oracle's bit for bit
+    check_taps(m, ref, cfg)
     m.reset_cache()
     for pos in range(len(got) - 1):
         lg, am = m.eval_next_logits(int(got[pos]), pos)
