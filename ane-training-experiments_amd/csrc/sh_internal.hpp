@@ -96,6 +96,7 @@ struct sh_model {
     // launch; p_own_cls_a.n == 0: p_own[4] for every workgroup
     sh::StageOwn p_own_cls_a;
     int p_cls_lds_rows;
+    bool p_argmax_every;    // w13 not on every workgroup: the next-token exchange every forward
     void *p_layers;         // device array of per-layer weight pointers
     uint64_t *ll_qkv, *ll_att, *ll_x2, *ll_gate, *ll_x, *ll_pv, *ll_pi;
     int *p_err;

@@ -102,6 +102,7 @@ struct PParams {
     StageOwn own[5];   // qkv, wo, w13, w2, classifier
     StageOwn own_cls_a;   // classifier rows of the attention workgroups (n == 0: own[4])
     int cls_lds_rows;     // classifier rows a non-attention workgroup keeps in LDS (0: none)
+    int argmax_every;     // the next-token exchange after every forward (w13 not on every workgroup)
     int ostride[5];    // words between consecutive workgroups' output blocks, per stage
     uint32_t omagic[5];  // ceil(2^31 / elements per output block), per stage
 };
@@ -1568,8 +1569,11 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 ll_put_u(p.ll_pi + slot, (uint32_t)b.i, ec);
             }
         }
-        // next token: needed to generate, and always after the last forward of a launch
-        if (pos + 1 >= p.n_prompt || f == p.n_forwards - 1) {
+        // next token: needed to generate, and always after the last forward of a launch. When the
+        // w13 stage does not span every workgroup the exchange runs after every forward: it is
+        // what keeps a slow workgroup's classifier poll of x ahead of the next forward's w2
+        // stores.
+        if (p.argmax_every || pos + 1 >= p.n_prompt || f == p.n_forwards - 1) {
             bool ok = true;
             float v = -INFINITY;
             int idx = 0x7fffffff;
@@ -1720,9 +1724,9 @@ hipError_t persistent_plan(sh_model *m, std::string *why) {
     const int KVH = c.n_kv_heads;
     const int wbytes = m->dtype == SH_DTYPE_W8A8 ? 1 : 2;   // bytes per weight
     // w2 on every workgroup (its weights are the second largest; a few rows each keeps the
-    // weight tiles loaded after the w13 stage small)
-    const int per_w2 = cdiv(c.dim, grid);
-    const int n_w2 = cdiv(c.dim, per_w2);
+    // weight tiles loaded after the w13 stage small), unless the layout below applies
+    int per_w2 = cdiv(c.dim, grid);
+    int n_w2 = cdiv(c.dim, per_w2);
     // qkv: blocks of 16 rows (whole lines of the dense qkv vector) spread over the grid,
     // after the attention workgroups when they fit
     const int per_qkv = up(cdiv(m->qkv_rows, grid), 16);
@@ -1735,12 +1739,31 @@ hipError_t persistent_plan(sh_model *m, std::string *why) {
     const int off_qkv = KVH + n_qkv <= grid ? KVH : 0;
     int off_wo = off_qkv + n_qkv;
     if (off_wo + n_wo > grid) off_wo = KVH + n_wo <= grid ? KVH : 0;
-    const int per13 = per13_for(grid);
+    int per13 = per13_for(grid), n13 = grid, off_w2 = 0;
+    // Where it fits: w13 on the first half of the grid with blocks its register tile holds
+    // whole (those workgroups are idle through wo, which sits after qkv), and w2 on the
+    // workgroups after the qkv block, so neither w2 nor the next layer's qkv workgroups are
+    // busy with the stage before theirs when its input arrives. Stories110M fp16: 158.5 against
+    // 170.3 us per forward with w13 and w2 on every workgroup. w13 then no longer spans the
+    // grid, so the next-token exchange runs after every forward (argmax_every).
+    {
+        const int tile13 = 2 * kPW * (64 / shape_ld(m->dtype, c.dim));   // rows of w13's WTile<2>
+        const int h13 = grid / 2, p13 = up(cdiv(rows13, std::max(h13, 1)), 2);
+        const int o2 = off_qkv + n_qkv, p2 = o2 < grid ? cdiv(c.dim, grid - o2) : kMaxRes + 1;
+        if (h13 >= 1 && p13 <= tile13 && p2 <= kMaxRes) {
+            per13 = p13;
+            n13 = cdiv(rows13, p13);
+            per_w2 = p2;
+            n_w2 = cdiv(c.dim, p2);
+            off_w2 = o2;
+        }
+    }
+    m->p_argmax_every = n13 < grid;
     m->p_grid = grid;
     m->p_own[0] = StageOwn{off_qkv, n_qkv, per_qkv};
     m->p_own[1] = StageOwn{off_wo, n_wo, per_wo};
-    m->p_own[2] = StageOwn{0, grid, per13};
-    m->p_own[3] = StageOwn{0, n_w2, per_w2};
+    m->p_own[2] = StageOwn{0, n13, per13};
+    m->p_own[3] = StageOwn{off_w2, n_w2, per_w2};
     m->p_own[4] = StageOwn{0, grid, cdiv(c.vocab, grid)};
     // classifier: the attention workgroups keep only their register tile's rows (their LDS
     // holds the attention cache); the others twice that, the second half resident in LDS for
@@ -1768,7 +1791,8 @@ hipError_t persistent_plan(sh_model *m, std::string *why) {
     m->p_ostride[4] = 0;
     *why += "; rows/workgroups qkv " + std::to_string(per_qkv) + "x" + std::to_string(n_qkv) + " wo " +
             std::to_string(per_wo) + "x" + std::to_string(n_wo) + " w13 " + std::to_string(per13) + "x" +
-            std::to_string(grid) + " w2 " + std::to_string(per_w2) + "x" + std::to_string(n_w2) +
+            std::to_string(n13) + " w2 " + std::to_string(per_w2) + "x" + std::to_string(n_w2) +
+            (off_w2 ? " from workgroup " + std::to_string(off_w2) : std::string("")) +
             (m->p_cls_lds_rows ? " classifier " + std::to_string(m->p_own_cls_a.per) + "x" +
                                      std::to_string(m->p_own_cls_a.n) + " + " + std::to_string(m->p_own[4].per) +
                                      "x" + std::to_string(m->p_own[4].n) + " (" +
@@ -1832,6 +1856,7 @@ hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt
     p.trace_f = m->trace_f;
     p.own_cls_a = m->p_own_cls_a;
     p.cls_lds_rows = m->p_cls_lds_rows;
+    p.argmax_every = m->p_argmax_every;
     for (int i = 0; i < 5; i++) {
         p.own[i] = m->p_own[i];
         p.ostride[i] = m->p_ostride[i];
