@@ -1689,14 +1689,16 @@ bool persistent_supported(const sh_model *m) {
 }
 
 // Grid and stage ownership. The grid is one workgroup per CU (at most kPB, one argmax
-// partial per thread), shrunk until the w13 stage's row blocks cover every workgroup: that
-// stage then depends on every workgroup having finished the previous forward's classifier,
-// which keeps the single-buffered ll_x vector safe while prompt forwards run without an
-// argmax exchange. qkv takes blocks of 16 rows over as many workgroups as that needs, after
-// the attention workgroups [0, KVH) when it fits; wo takes about 24 KB of weights per
-// workgroup, placed after qkv when it fits (its workgroups then idle through qkv and
-// attention, so their weight tiles arrive before att does); w2 spreads over every workgroup
-// (a few rows each), so the weight tiles it loads after the w13 stage stay small.
+// partial per thread), shrunk until row blocks of the w13 stage can cover every workgroup.
+// qkv takes blocks of 16 rows over as many workgroups as that needs, after the attention
+// workgroups [0, KVH) when it fits; wo takes about 24 KB of weights per workgroup, placed
+// after qkv when it fits (its workgroups then idle through qkv and attention, so their weight
+// tiles arrive before att does). w13 and w2 then take one of two layouts: on every
+// workgroup (w2 a few rows each, so the weight tiles it loads after the w13 stage stay
+// small; w13 spanning the grid makes it depend on every workgroup having finished the
+// previous forward's classifier, which keeps the single-buffered ll_x safe while prompt
+// forwards run without an argmax exchange), or, where the blocks fit, w13 on half the grid
+// and w2 after the qkv block (below; the exchange then runs after every forward).
 hipError_t persistent_plan(sh_model *m, std::string *why) {
     const sh_config &c = m->cfg;
     PersistentKernel k = pick_persistent(m->dtype, c.kv_dtype, c.dim, m->qdim, c.hidden, c.head_dim);
