@@ -540,7 +540,7 @@ sh_model *sh_model_create(const sh_config *cfg, int32_t dtype) {
             return fail("wall clock rate", e);
         m->spin_ticks = (long long)(rate_khz > 0 ? rate_khz : 100000) * 1000LL * 2;  // 2 s
         m->epoch = 1;  // cleared words carry epoch 0
-        const size_t tb = (size_t)m->p_grid * (5 * (size_t)c.n_layers + 3) * sizeof(long long);
+        const size_t tb = (size_t)m->p_grid * 2 * (5 * (size_t)c.n_layers + 3) * sizeof(long long);
         if ((e = hipMalloc(&m->trace_buf, tb)) != hipSuccess) return fail("hipMalloc trace", e);
         if ((e = hipMemset(m->trace_buf, 0, tb)) != hipSuccess) return fail("clear trace", e);
     }
@@ -1245,9 +1245,9 @@ int sh_trace_read(sh_model *m, int64_t *out, int32_t cap, int32_t *n_out, double
         set_error("sh_trace_read: bad arguments");
         return -1;
     }
-    const int n = m->p_grid * (5 * m->cfg.n_layers + 3);
+    const int n = m->p_grid * 2 * (5 * m->cfg.n_layers + 3);
     if (cap < n) {
-        set_error("sh_trace_read: capacity below grid*(5*n_layers+3)");
+        set_error("sh_trace_read: capacity below grid*2*(5*n_layers+3)");
         return -1;
     }
     (void)hipSetDevice(m->device);

@@ -103,7 +103,7 @@ struct sh_model {
     uint32_t epoch;         // next unused hand-over epoch
     long long spin_ticks;   // wait bound in constant-clock ticks
     char path_note[512];    // which decode path runs, and why
-    long long *trace_buf;   // device: 2 x (5L + 3) stage timestamps
+    long long *trace_buf;   // device: grid x 2 x (5L + 3) stage timestamps (ends, inputs ready)
     int trace_f;            // forward index traced in the next launch, -1 = off
 
     // full-sequence forward (sh_prefill.hip): token-major scratch for up to pf_cap tokens

@@ -97,7 +97,8 @@ struct PParams {
     int *err;
     long long spin_limit;
     long long quiet;   // ticks a wait runs before it also reads the abort flag (20 us)
-    long long *trace;  // stage timestamps of forward trace_f (workgroups 0 and grid-1)
+    long long *trace;  // forward trace_f: per workgroup 5L+3 stage-end stamps, then as many
+                       // input-ready stamps (the stage's whole input staged on the workgroup)
     int trace_f;
     StageOwn own[5];   // qkv, wo, w13, w2, classifier
     StageOwn own_cls_a;   // classifier rows of the attention workgroups (n == 0: own[4])
@@ -247,6 +248,31 @@ __device__ __forceinline__ bool aborted(const PParams &p) {
     return __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
+// The bound of a wait, taken once per poll round: false once the wait has to end (its time
+// limit passed, which sets *p.err, or, after the quiet period, *p.err set by another wave).
+// The clock is read every eighth round, and rounds follow each other without a sleep: every
+// round waits out a memory round trip anyway, and on this part each extra poll request or
+// pause lengthens a hand-over (measured on rings of stages: one request per word per round,
+// no sleep, 1.33 us per hand-over; with a sleep 1.36 us; two or four requests in flight per
+// word, staggered by sleeps, 1.50 to 1.93 us).
+struct WaitBound {
+    long long t0 = 0;
+    unsigned rounds = 0;
+    __device__ __forceinline__ bool more(const PParams &p) {
+        if ((rounds++ & 7u) != 0) return true;
+        const long long now = wall_clock64();
+        if (!t0) {
+            t0 = now;
+            return true;
+        }
+        if (now - t0 > p.spin_limit) {
+            __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+        return !(now - t0 > p.quiet && aborted(p));
+    }
+};
+
 // Block-wide wait: once every word j < n (located by map.src(j)) carries epoch map.ep(j),
 // its value is in *map.dst(j). Starts with a workgroup barrier, after the first requests
 // are issued: the LDS a stage writes is free once every wave has passed it. Each thread requests all of its K words at once and, while any is
@@ -268,7 +294,7 @@ __device__ __forceinline__ bool ll_wait_batch(int n, const PParams &p, const Map
     // barrier; this one overlaps the first round trip)
     lds_barrier();
     bool ok = true;
-    long long t0 = 0;
+    WaitBound wb;
     while (true) {
 #pragma unroll
         for (int k = 0; k < K; k++) {
@@ -280,19 +306,10 @@ __device__ __forceinline__ bool ll_wait_batch(int n, const PParams &p, const Map
             }
         }
         if (!need) break;
-        const long long now = wall_clock64();
-        if (!t0) {
-            t0 = now;
-        } else if (now - t0 > p.spin_limit) {
-            __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!wb.more(p)) {
             ok = false;
             break;
         }
-        if (now - t0 > p.quiet && aborted(p)) {
-            ok = false;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int k = 0; k < K; k++)
             if ((need >> k) & 1u) v[k] = ll_get(map.src(threadIdx.x + k * kPB));
@@ -377,7 +394,7 @@ __device__ __forceinline__ void ll_poll_regs(int n, const PParams &p, const Inpu
     pre();
     lds_barrier();
     ok = true;
-    long long t0 = 0;
+    WaitBound wb;
     while (true) {
 #pragma unroll
         for (int k = 0; k < K; k++) {
@@ -387,19 +404,10 @@ __device__ __forceinline__ void ll_poll_regs(int n, const PParams &p, const Inpu
             }
         }
         if (!need) break;
-        const long long now = wall_clock64();
-        if (!t0) {
-            t0 = now;
-        } else if (now - t0 > p.spin_limit) {
-            __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!wb.more(p)) {
             ok = false;
             break;
         }
-        if (now - t0 > p.quiet && aborted(p)) {
-            ok = false;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int k = 0; k < K; k++) v[k] = ll_get(src[k]);
     }
@@ -686,6 +694,9 @@ __device__ __forceinline__ void stage_compute(const PParams &p, const void *__re
             acci[u] = 0;
             const int row = gbase(k0 + u) + grp;
             if (row < r1) {
+                // four partial sums per row (a dependent chain a quarter as long), added in a
+                // fixed order
+                float a4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int j = 0; j < CPL; j++) {
                     if constexpr (Q8) {
@@ -697,9 +708,10 @@ __device__ __forceinline__ void stage_compute(const PParams &p, const void *__re
                         float f[8];
                         unpack8<WT>(w[u][j], f);
 #pragma unroll
-                        for (int e = 0; e < 8; e++) acc[u] = fmaf(f[e], xr[j * 8 + e], acc[u]);
+                        for (int e = 0; e < 8; e++) a4[e & 3] = fmaf(f[e], xr[j * 8 + e], a4[e & 3]);
                     }
                 }
+                if constexpr (!Q8) acc[u] = (a4[0] + a4[1]) + (a4[2] + a4[3]);
             }
         }
         // next tiles are issued before this batch's reductions and stores
@@ -737,8 +749,10 @@ __device__ __forceinline__ void stage_compute(const PParams &p, const void *__re
                 float h3 = 0.f;
                 if constexpr (LPR < 64) h3 = from_lane_up<LPR>(a);
                 if (sub == 0 && (grp & 1) == 0 && row < r1) {
-                    // infer.go:324-326 (float64 exp; float expf for the fp16/bf16 models)
-                    const float s = Q8 ? a / (1.0f + (float)exp(-(double)a)) : a / (1.0f + expf(-a));
+                    // infer.go:324-326: float64 exp for W8A8 (its quantizer sees these values);
+                    // the 16-bit models use the hardware exp2 and reciprocal (a few ulp)
+                    const float s = Q8 ? a / (1.0f + (float)exp(-(double)a))
+                                       : a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * -1.4426950408889634f));
                     ostage[(row - r0) >> 1] = s * h3;
                 }
             } else if (sub == 0 && row < r1) {
@@ -873,7 +887,7 @@ __device__ __forceinline__ void kv_unpack16(const u32x4 &v, float *f) {
 // that moves x/s across a rounding boundary would change an int8 input.
 template <int KVT, int HD, bool EXACT>
 __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
-                           float *sc, float *part, uint8_t *kvlds, double *red, float *redf) {
+                           float *sc, float *part, uint8_t *kvlds, double *red, float *redf, long long *tin) {
     using S = KvStage<KVT, HD>;
     constexpr int hd = HD, ngr = kPB / HD;
     const int group = p.H / p.KVH, tid = threadIdx.x;
@@ -891,6 +905,7 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
     QkvMap qm{p.ll_qkv, qs, (size_t)g * group * hd, p.qdim + (size_t)g * hd,
               p.qdim + p.kvdim + (size_t)g * hd, group * hd, hd, e};
     if (!ll_wait_batch<(kMaxGroup + 2) * 256 / kPB>(group * hd + 2 * hd, p, qm)) return false;
+    if (tin) *tin = wall_clock64();
     if (p.qk_norm) {
         // per-head RMSNorm: wave w < group normalises q head w, wave `group` normalises k
         if (wave <= group) {
@@ -1107,236 +1122,332 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
 }
 
 
-// Attention for the fp16 / bf16 models (the W8A8 model keeps attn_stage<..., true>): the
-// same mathematics in fewer dependent steps, rounded differently in the last bits.
-//  - RoPE factors are loaded before the poll; QK-norm and the softmax use float math;
-//  - scores are lane-sliced dot products over the cached rows (LDS rows two blocks per trip,
-//    rows beyond the LDS stage read from the cache the same way), each wave tracking the
-//    running maximum of its scores;
-//  - the softmax runs on all waves; the exp terms are left unnormalised and the P.V sums are
-//    scaled by 1/sum at the end (p.v/sum instead of (p/sum).v);
-//  - three workgroup barriers after the cache append, none at the end (the next stage's poll
-//    starts with one).
+// Cross-group sum: lanes l, l + N, l + 2N, ... (N = 4, 8, 16, 32) added, the result the same
+// on all of them (every step adds two values equal on both partners). Within a 16-lane row
+// the groups are combined by rotations (row_ror:8, then row_ror:4: the sum over all rotations
+// by multiples of N), then rows by the permlane swaps.
+constexpr int kDppRor8 = 0x128;   // row_ror:8 (lane i <- (i + 8) mod 16 within a row)
+constexpr int kDppRor4 = 0x124;   // row_ror:4
+template <int N>
+__device__ __forceinline__ float gsum(float v) {
+    static_assert(N == 4 || N == 8 || N == 16 || N == 32, "groups of 4..32 lanes");
+    if constexpr (N <= 8) v += __uint_as_float(dpp_u<kDppRor8>(__float_as_uint(v)));
+    if constexpr (N <= 4) v += __uint_as_float(dpp_u<kDppRor4>(__float_as_uint(v)));
+    if constexpr (N <= 16) {
+        const SwapPair s = swap16(__float_as_uint(v));
+        v = __uint_as_float(s.a) + __uint_as_float(s.b);
+    }
+    const SwapPair s = swap32(__float_as_uint(v));
+    return __uint_as_float(s.a) + __uint_as_float(s.b);
+}
+template <int N>
+__device__ __forceinline__ float gmax(float v) {
+    static_assert(N == 4 || N == 8 || N == 16 || N == 32, "groups of 4..32 lanes");
+    if constexpr (N <= 8) v = fmaxf(v, __uint_as_float(dpp_u<kDppRor8>(__float_as_uint(v))));
+    if constexpr (N <= 4) v = fmaxf(v, __uint_as_float(dpp_u<kDppRor4>(__float_as_uint(v))));
+    if constexpr (N <= 16) {
+        const SwapPair s = swap16(__float_as_uint(v));
+        v = fmaxf(__uint_as_float(s.a), __uint_as_float(s.b));
+    }
+    const SwapPair s = swap32(__float_as_uint(v));
+    return fmaxf(__uint_as_float(s.a), __uint_as_float(s.b));
+}
+
+// Attention for the fp16 / bf16 models (infer.go:273-299): kv head g on this workgroup, its
+// GROUP q heads; the W8A8 model keeps attn_stage<..., true>. Every wave works on its own
+// slice of positions and meets the others once, at the end:
+//  - each wave polls q|k|v itself (no workgroup barrier after the hand-over), stages the words
+//    in its own LDS region and reads them back lane-sliced: lane (r, s) of the wave serves row r
+//    of each 64-lane row block and holds elements [EPC*s, EPC*s + EPC) of every vector, so a
+//    cache row is one 16-byte LDS read per lane and a block of PPW rows one wave instruction;
+//  - QK-norm and RoPE on those registers (RoPE pairs sit inside a lane's slice);
+//  - wave w owns rows (8j + w)*PPW + r: the rows its own share of attn_prefetch copied into
+//    LDS (kv_rows_to_lds deals rows to waves the same way), so a wave only waits for its own
+//    copies; row pos comes from the registers; rows beyond the LDS stage from the cache;
+//  - scores with the wave's maximum, then exp(s - max) and the P.V sums over the same rows;
+//  - one workgroup barrier: the waves' (max, sum, P.V) combine as in split softmax,
+//    out = sum_w e^(m_w - M) o_w / sum_w e^(m_w - M) l_w.
 template <int KVT, int HD, int GROUP>
-__device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
-                                                float *sc, float *part, uint8_t *kvlds, float *redf) {
+__device__ __forceinline__ bool attn_stage_wave(const PParams &p, int l, int g, int pos, uint32_t e,
+                                                float *wst, int *okw, uint8_t *kvlds, long long *tin) {
     using S = KvStage<KVT, HD>;
-    constexpr int hd = HD, ngr = kPB / HD;
     constexpr int LPK = S::RB / 16, EPC = 16 / S::EB, PPW = 64 / LPK;
-    constexpr int group = GROUP;   // q heads per kv head, known at compile time so the loops
-                                   // below carry no per-row branches
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    constexpr int NW = (GROUP + 2) * HD;              // q heads, k, v words
+    constexpr int KW = (NW + 63) / 64;                // words a lane polls
+    constexpr int WREG = kMaxGroup * 256;             // floats of a wave's LDS region
+    static_assert(NW <= WREG && GROUP * HD + 2 * GROUP <= WREG, "wave region");
+    static_assert(EPC % 2 == 0, "RoPE pairs inside a lane's slice");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane / LPK, s = lane % LPK;
     const int ms = p.max_seq;
     const LayerPtrs Lp = layer_ptrs(p.layers, l);
-    const size_t lbase = (size_t)l * ms * p.kvdim + (size_t)g * hd;
-    SH_LDS uint8_t *kst = (SH_LDS uint8_t *)kvlds;
-    SH_LDS uint8_t *vst = kst + (size_t)S::ROWS * S::RB;
-    const int kofs = group * hd, vofs = kofs + hd;
-    float *ks = qs + kofs, *vs = qs + vofs;
-    const int half = hd / 2;
-    // this thread's RoPE pair (q heads, then k) and its factors, before the poll
-    const bool rope_t = tid < (group + 1) * half;
-    const int rpi = tid % half;
-    float rc = 0.f, rs = 0.f;
-    if (rope_t) {
-        rc = p.rope_cos[pos * half + rpi];
-        rs = p.rope_sin[pos * half + rpi];
+    const size_t lbase = (size_t)l * ms * p.kvdim + (size_t)g * HD;
+    const SH_LDS uint8_t *kst = (const SH_LDS uint8_t *)kvlds;
+    const SH_LDS uint8_t *vst = kst + (size_t)S::ROWS * S::RB;
+    float *wr = wst + wave * WREG;   // this wave's LDS region
+    // RoPE factors of this lane's pairs and the QK-norm gains of its elements, before the poll
+    const int half = HD / 2;
+    float rc[EPC / 2], rs[EPC / 2];
+#pragma unroll
+    for (int j = 0; j < EPC / 2; j++) {
+        rc[j] = p.rope_cos[pos * half + s * (EPC / 2) + j];
+        rs[j] = p.rope_sin[pos * half + s * (EPC / 2) + j];
     }
-    // QK-norm gains of this wave's head (wave w < group: q head w, wave group: k)
-    constexpr int GPL = (HD + 63) / 64;
-    float gq[GPL];
+    float gqn[EPC], gkn[EPC];
 #pragma unroll
-    for (int q = 0; q < GPL; q++) gq[q] = 0.f;
-    if (p.qk_norm && wave <= group) {
-        const float *gn = wave < group ? Lp.q_norm : Lp.k_norm;
-#pragma unroll
-        for (int q = 0; q < GPL; q++)
-            if (lane + 64 * q < hd) gq[q] = gn[lane + 64 * q];
+    for (int i = 0; i < EPC; i++) {
+        gqn[i] = p.qk_norm ? Lp.q_norm[s * EPC + i] : 1.f;
+        gkn[i] = p.qk_norm ? Lp.k_norm[s * EPC + i] : 1.f;
     }
-    QkvMap qm{p.ll_qkv, qs, (size_t)g * group * hd, p.qdim + (size_t)g * hd,
-              p.qdim + p.kvdim + (size_t)g * hd, group * hd, hd, e};
-    if (!ll_wait_batch<(GROUP + 2) * 256 / kPB>(group * hd + 2 * hd, p, qm)) return false;
-    if (p.qk_norm) {
-        // per-head RMSNorm: wave w < group normalises q head w, wave `group` normalises k
-        if (wave <= group) {
-            float *v = qs + (wave < group ? wave : group) * hd;
-            float ss = 0.f;
-            for (int i = lane; i < hd; i += 64) ss += v[i] * v[i];
-            ss = wsum<64>(ss);
-            const float rr = rsqrtf(ss / (float)hd + (float)p.qk_eps);
+    // poll: lane polls words lane + 64k of [q heads | k | v]
+    const size_t qo = (size_t)g * GROUP * HD, ko = p.qdim + (size_t)g * HD, vo = (size_t)p.qdim + p.kvdim + (size_t)g * HD;
+    const uint64_t *src[KW];
+    uint64_t v[KW];
 #pragma unroll
-            for (int q = 0; q < GPL; q++)
-                if (lane + 64 * q < hd) v[lane + 64 * q] = v[lane + 64 * q] * rr * gq[q];
-        }
-        lds_barrier();
+    for (int k = 0; k < KW; k++) {
+        const int j0 = lane + 64 * k, j = j0 < NW ? j0 : NW - 1;
+        src[k] = p.ll_qkv + (j < GROUP * HD ? qo + j : (j < GROUP * HD + HD ? ko + (j - GROUP * HD)
+                                                                            : vo + (j - GROUP * HD - HD)));
+        v[k] = ll_get(src[k]);
     }
-    if (rope_t) {   // infer.go:247-265, interleaved pairs
-        float *v = qs + (tid / half) * hd;
-        const float ev = v[2 * rpi], ov = v[2 * rpi + 1];
-        v[2 * rpi] = ev * rc - ov * rs;
-        v[2 * rpi + 1] = ev * rs + ov * rc;
-    }
-    __builtin_amdgcn_s_waitcnt(0);   // the LDS copies of the cached rows have landed
-    lds_barrier();
-    // infer.go:267-271 storeKV in the cache's storage type; row pos also joins the LDS rows
-    for (int i = tid; i < hd; i += kPB) {
-        ks[i] = kv_rnd<KVT>(ks[i]);
-        vs[i] = kv_rnd<KVT>(vs[i]);
-        kv_st<KVT>(p.kcache, lbase + (size_t)pos * p.kvdim + i, ks[i]);
-        kv_st<KVT>(p.vcache, lbase + (size_t)pos * p.kvdim + i, vs[i]);
-        if (pos < S::ROWS) {
-            kv_put<KVT>(kst + (size_t)pos * S::RB, i, ks[i]);
-            kv_put<KVT>(vst + (size_t)pos * S::RB, i, vs[i]);
-        }
-    }
-    lds_barrier();
-    // scores (infer.go:280-288) and each wave's maximum
-    const int sl = lane % LPK, rin = lane / LPK;
-    float qr[GROUP][EPC];
+    bool ok = true;
+    {
+        WaitBound wb;
+        while (true) {
+            bool have = true;
 #pragma unroll
-    for (int h = 0; h < GROUP; h++)
-#pragma unroll
-        for (int q = 0; q < EPC; q++) qr[h][q] = h < group ? qs[h * hd + sl * EPC + q] : 0.f;
-    float mx[GROUP];
-#pragma unroll
-    for (int h = 0; h < GROUP; h++) mx[h] = -INFINITY;
-    auto score_row = [&](const float (&kf)[EPC], int t, bool valid) {
-#pragma unroll
-        for (int h = 0; h < GROUP; h++) {
-            if (h >= group) continue;
-            float d = 0.f;
-#pragma unroll
-            for (int q = 0; q < EPC; q++) d = fmaf(qr[h][q], kf[q], d);
-            d = wsum<LPK>(d) * p.inv_sqrt_hd;
-            if (valid) {
-                if (sl == 0) sc[h * ms + t] = d;
-                mx[h] = fmaxf(mx[h], d);
-            }
-        }
-    };
-    const int tl = pos < S::ROWS ? pos : S::ROWS - 1;   // last position held in LDS
-    for (int t0 = wave * PPW; t0 <= tl; t0 += 2 * kPW * PPW) {
-        const int ta = t0 + rin, tb = t0 + kPW * PPW + rin;
-        const bool va = ta <= tl, vb = tb <= tl;
-        const u32x4 ka = ((const SH_LDS u32x4 *)(kst + (size_t)(va ? ta : tl) * S::RB))[sl];
-        const u32x4 kb = ((const SH_LDS u32x4 *)(kst + (size_t)(vb ? tb : tl) * S::RB))[sl];
-        float fa[EPC], fb[EPC];
-        kv_unpack16<KVT>(ka, fa);
-        kv_unpack16<KVT>(kb, fb);
-        score_row(fa, ta, va);
-        score_row(fb, tb, vb);
-    }
-    if (pos > tl) {
-        // rows beyond the LDS stage, from the cache (row pos from the staged k)
-        float kpos[EPC];
-#pragma unroll
-        for (int q = 0; q < EPC; q++) kpos[q] = ks[sl * EPC + q];
-        // four row blocks per trip, their cache reads in flight together
-        const SH_GLOBAL uint8_t *kc = (const SH_GLOBAL uint8_t *)p.kcache;
-        for (int tb = tl + 1 + wave * PPW; tb <= pos; tb += 4 * kPW * PPW) {
-            u32x4 kv4[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int t = tb + u * kPW * PPW + rin;
-                const int tr = t < pos ? t : tl;   // a row in the cache (row pos is not read)
-                kv4[u] = ((const SH_GLOBAL u32x4 *)(kc + (lbase + (size_t)tr * p.kvdim) * S::EB))[sl];
+            for (int k = 0; k < KW; k++) have = have && (uint32_t)(v[k] >> 32) == e;
+            if (__all(have)) break;
+            if (!wb.more(p)) {
+                ok = false;
+                break;
             }
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                if (tb + u * kPW * PPW > pos) continue;   // uniform over the wave
-                const int t = tb + u * kPW * PPW + rin;
-                float kf[EPC];
-                kv_unpack16<KVT>(kv4[u], kf);
-                if (t == pos) {
+            for (int k = 0; k < KW; k++) v[k] = ll_get(src[k]);
+        }
+    }
+    if (tin && wave == 0) *tin = wall_clock64();
+    float mw[GROUP], lw[GROUP], acc[GROUP][EPC];
 #pragma unroll
-                    for (int q = 0; q < EPC; q++) kf[q] = kpos[q];
+    for (int h = 0; h < GROUP; h++) {
+        mw[h] = -INFINITY;
+        lw[h] = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPC; i++) acc[h][i] = 0.f;
+    }
+    if (ok) {
+        // lane-sliced copies of q, k, v through the wave's own LDS region
+#pragma unroll
+        for (int k = 0; k < KW; k++)
+            if (lane + 64 * k < NW) wr[lane + 64 * k] = __uint_as_float((uint32_t)v[k]);
+        __asm__ __volatile__("s_waitcnt lgkmcnt(0)" ::: "memory");
+        float q[GROUP][EPC], kk[EPC], vv[EPC];
+#pragma unroll
+        for (int i = 0; i < EPC; i++) {
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) q[h][i] = wr[h * HD + s * EPC + i];
+            kk[i] = wr[GROUP * HD + s * EPC + i];
+            vv[i] = wr[GROUP * HD + HD + s * EPC + i];
+        }
+        // per-head RMSNorm (float) and RoPE (infer.go:247-265, interleaved pairs) of q and k
+        auto norm_rope = [&](float (&x)[EPC], const float (&gn)[EPC]) {
+            if (p.qk_norm) {
+                float ss = 0.f;
+#pragma unroll
+                for (int i = 0; i < EPC; i++) ss += x[i] * x[i];
+                ss = wsum<LPK>(ss);
+                const float rr = rsqrtf(ss / (float)HD + (float)p.qk_eps);
+#pragma unroll
+                for (int i = 0; i < EPC; i++) x[i] = x[i] * rr * gn[i];
+            }
+#pragma unroll
+            for (int j = 0; j < EPC / 2; j++) {
+                const float ev = x[2 * j], ov = x[2 * j + 1];
+                x[2 * j] = ev * rc[j] - ov * rs[j];
+                x[2 * j + 1] = ev * rs[j] + ov * rc[j];
+            }
+        };
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) norm_rope(q[h], gqn);
+        norm_rope(kk, gkn);
+        // infer.go:267-271 storeKV in the cache's storage type: row pos as the scores see it
+#pragma unroll
+        for (int i = 0; i < EPC; i++) {
+            kk[i] = kv_rnd<KVT>(kk[i]);
+            vv[i] = kv_rnd<KVT>(vv[i]);
+        }
+        u32x4 kw, vw;   // this lane's 16 bytes of row pos in the cache's storage form
+        if constexpr (KVT == SH_KV_F32) {
+            kw = u32x4{__float_as_uint(kk[0]), __float_as_uint(kk[1]), __float_as_uint(kk[2]), __float_as_uint(kk[3])};
+            vw = u32x4{__float_as_uint(vv[0]), __float_as_uint(vv[1]), __float_as_uint(vv[2]), __float_as_uint(vv[3])};
+        } else {
+            uint32_t a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t k0 = KVT == SH_KV_F16 ? f2h(kk[2 * i]) : f2bf(kk[2 * i]);
+                const uint32_t k1 = KVT == SH_KV_F16 ? f2h(kk[2 * i + 1]) : f2bf(kk[2 * i + 1]);
+                const uint32_t v0 = KVT == SH_KV_F16 ? f2h(vv[2 * i]) : f2bf(vv[2 * i]);
+                const uint32_t v1 = KVT == SH_KV_F16 ? f2h(vv[2 * i + 1]) : f2bf(vv[2 * i + 1]);
+                a[i] = k0 | (k1 << 16);
+                b[i] = v0 | (v1 << 16);
+            }
+            kw = u32x4{a[0], a[1], a[2], a[3]};
+            vw = u32x4{b[0], b[1], b[2], b[3]};
+        }
+        // this wave's share of the cached rows has landed in LDS (waited for before the append's
+        // stores: the counter would otherwise also wait for their write-back)
+        __builtin_amdgcn_s_waitcnt(0);
+        const int pwave = (pos / PPW) % kPW;   // the wave whose row blocks hold row pos
+        if (r == 0) {
+            if (wave == 0) {
+                const size_t o = (lbase + (size_t)pos * p.kvdim) * S::EB + s * 16;
+                *(SH_GLOBAL u32x4 *)((uint8_t *)p.kcache + o) = kw;
+                *(SH_GLOBAL u32x4 *)((uint8_t *)p.vcache + o) = vw;
+            }
+            // row pos also joins the LDS stage, written and read by the same wave
+            if (wave == pwave && pos < S::ROWS) {
+                ((SH_LDS u32x4 *)(kst + (size_t)pos * S::RB))[s] = kw;
+                ((SH_LDS u32x4 *)(vst + (size_t)pos * S::RB))[s] = vw;
+            }
+        }
+        // Online softmax per lane group over this wave's rows, NB row blocks per pass
+        // (branch-free, so the blocks' dependent chains interleave): the group's running
+        // (max m, sum l, P.V acc) is rescaled when its maximum grows. Scores are kept in the
+        // base-2 domain (scaled by log2 e) so each softmax term is one exp2.
+        constexpr int NB = EPC == 4 ? 4 : 2;   // blocks per pass (two for 16-bit caches: registers)
+        const float qscale = p.inv_sqrt_hd * 1.4426950408889634f;
+        float m[GROUP];
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) m[h] = -INFINITY;
+        // ALL: rows [0, pos] all in LDS (a row past pos reads row pos's slot and weighs nothing).
+        // Otherwise rows [S::ROWS, pos) come from the cache (pos > S::ROWS, so a block of PPW
+        // rows never straddles the LDS stage's end) and row pos from the registers.
+        auto pass_rows = [&](auto all) {
+            constexpr bool ALL = decltype(all)::value;
+            const SH_GLOBAL uint8_t *kcg = (const SH_GLOBAL uint8_t *)p.kcache;
+            const SH_GLOBAL uint8_t *vcg = (const SH_GLOBAL uint8_t *)p.vcache;
+            for (int b0 = wave * PPW; b0 <= pos; b0 += NB * kPW * PPW) {
+                float kf[NB][EPC], vf[NB][EPC];
+                int t[NB];
+#pragma unroll
+                for (int i = 0; i < NB; i++) {
+                    const int t0 = b0 + i * kPW * PPW;
+                    t[i] = t0 + r;
+                    u32x4 kr, vr;
+                    if (ALL || t0 < S::ROWS) {
+                        const int tr = ALL ? (t[i] < pos ? t[i] : pos) : (t[i] < pos ? t[i] : 0);
+                        kr = ((const SH_LDS u32x4 *)(kst + (size_t)tr * S::RB))[s];
+                        vr = ((const SH_LDS u32x4 *)(vst + (size_t)tr * S::RB))[s];
+                    } else {
+                        const size_t o = (lbase + (size_t)(t[i] < pos ? t[i] : 0) * p.kvdim) * S::EB + s * 16;
+                        kr = *(const SH_GLOBAL u32x4 *)(kcg + o);
+                        vr = *(const SH_GLOBAL u32x4 *)(vcg + o);
+                    }
+                    kv_unpack16<KVT>(kr, kf[i]);
+                    kv_unpack16<KVT>(vr, vf[i]);
+                    if constexpr (ALL) {
+                        // rows past pos weigh nothing (row pos was written by another wave, so
+                        // its bytes as this wave sees them may be anything, NaN included)
+#pragma unroll
+                        for (int e2 = 0; e2 < EPC; e2++) vf[i][e2] = t[i] <= pos ? vf[i][e2] : 0.f;
+                    } else {
+                        // row pos from the registers; rows past pos weigh nothing (their bytes
+                        // may be anything, NaN included)
+#pragma unroll
+                        for (int e2 = 0; e2 < EPC; e2++) {
+                            kf[i][e2] = t[i] == pos ? kk[e2] : kf[i][e2];
+                            vf[i][e2] = t[i] == pos ? vv[e2] : (t[i] < pos ? vf[i][e2] : 0.f);
+                        }
+                    }
                 }
-                score_row(kf, t, t <= pos);
+#pragma unroll
+                for (int h = 0; h < GROUP; h++) {
+                    // scores (infer.go:280-288), times log2 e
+                    float sc4[NB];
+#pragma unroll
+                    for (int i = 0; i < NB; i++) {
+                        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+                        for (int e2 = 0; e2 < EPC; e2 += 2) {
+                            d0 = fmaf(q[h][e2], kf[i][e2], d0);
+                            d1 = fmaf(q[h][e2 + 1], kf[i][e2 + 1], d1);
+                        }
+                        sc4[i] = d0 + d1;
+                    }
+#pragma unroll
+                    for (int i = 0; i < NB; i++) sc4[i] = wsum<LPK>(sc4[i]) * qscale;
+                    float mn = m[h];
+#pragma unroll
+                    for (int i = 0; i < NB; i++) mn = t[i] <= pos ? fmaxf(mn, sc4[i]) : mn;
+                    // softmax terms (infer.go:328-345) against the running maximum
+                    // 0 from a -inf running maximum, 1 while the group has seen no row
+                    const float f = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[h] - mn);
+                    float pw[NB];
+#pragma unroll
+                    for (int i = 0; i < NB; i++) pw[i] = t[i] <= pos ? __builtin_amdgcn_exp2f(sc4[i] - mn) : 0.f;
+                    m[h] = mn;
+                    float ls = pw[0];
+#pragma unroll
+                    for (int i = 1; i < NB; i++) ls += pw[i];
+                    lw[h] = fmaf(lw[h], f, ls);
+                    // P.V (infer.go:290-297)
+#pragma unroll
+                    for (int e2 = 0; e2 < EPC; e2++) {
+                        float a = pw[0] * vf[0][e2];
+#pragma unroll
+                        for (int i = 1; i < NB; i++) a = fmaf(pw[i], vf[i][e2], a);
+                        acc[h][e2] = fmaf(acc[h][e2], f, a);
+                    }
+                }
             }
-        }
-    }
-#pragma unroll
-    for (int h = 0; h < GROUP; h++) {
-        const float m = wmax<64>(mx[h]);
-        if (lane == 0 && h < group) redf[wave * GROUP + h] = m;
-    }
-    lds_barrier();
-    // softmax (infer.go:328-345) on every wave: unnormalised exp terms and their sums
-    float gmx[GROUP], sum[GROUP];
-#pragma unroll
-    for (int h = 0; h < GROUP; h++) {
-        gmx[h] = -INFINITY;
-        sum[h] = 0.f;
-        if (h < group)
-            for (int w = 0; w < kPW; w++) gmx[h] = fmaxf(gmx[h], redf[w * GROUP + h]);
-    }
-    for (int t = tid; t <= pos; t += kPB) {
+        };
+        if (pos < S::ROWS) pass_rows(std::true_type{});
+        else pass_rows(std::false_type{});
+        // the wave's groups combined: maximum over groups, each group's sums rescaled to it
 #pragma unroll
         for (int h = 0; h < GROUP; h++) {
-            if (h >= group) continue;
-            const float ev = expf(sc[h * ms + t] - gmx[h]);
-            sc[h * ms + t] = ev;
-            sum[h] += ev;
+            const float M = gmax<LPK>(m[h]);
+            const float f = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - M);
+            mw[h] = M;
+            lw[h] = gsum<LPK>(lw[h] * f);
+#pragma unroll
+            for (int e2 = 0; e2 < EPC; e2++) acc[h][e2] = gsum<LPK>(acc[h][e2] * f);
         }
-    }
+        // into the wave's region (its q|k|v copies were read above): P.V, then max and sum
+        if (r == 0) {
 #pragma unroll
-    for (int h = 0; h < GROUP; h++) {
-        const float sw = wsum<64>(sum[h]);
-        if (lane == 0 && h < group) redf[(kPW + wave) * GROUP + h] = sw;
-    }
-    lds_barrier();
-    // P.V (infer.go:290-297): thread (position group tg, dim vi), partials through LDS; the
-    // LDS rows are read four at a time (clamped indices, zero weights past the end), so the
-    // reads of a batch are in flight together
-    const int vi = tid % hd, tg = tid / hd;
-    float acc[GROUP];
+            for (int h = 0; h < GROUP; h++)
 #pragma unroll
-    for (int h = 0; h < GROUP; h++) acc[h] = 0.f;
-    for (int t = tg; t <= tl; t += 4 * ngr) {
-        float vv[4], pw[GROUP][4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int tt = t + u * ngr;
-            const int tc = tt <= tl ? tt : tl;
-            vv[u] = kv_get<KVT>(vst + (size_t)tc * S::RB, vi);
+                for (int i = 0; i < EPC; i++) wr[h * HD + s * EPC + i] = acc[h][i];
+        }
+        if (lane == 0) {
 #pragma unroll
             for (int h = 0; h < GROUP; h++) {
-                const float w = sc[h * ms + tc];
-                pw[h][u] = tt <= tl ? w : 0.f;
+                wr[GROUP * HD + h] = mw[h];
+                wr[GROUP * HD + GROUP + h] = lw[h];
             }
         }
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-#pragma unroll
-            for (int h = 0; h < GROUP; h++) acc[h] = fmaf(pw[h][u], vv[u], acc[h]);
     }
-    // rows beyond the LDS stage: cache reads eight at a time (row pos from the staged v)
-    for (int t = tl + 1 + ((tg - (tl + 1) % ngr + ngr) % ngr); t <= pos; t += 8 * ngr) {
-        float vc[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int tt = t + u * ngr;
-            vc[u] = kv_ld<KVT>(p.vcache, lbase + (size_t)(tt < pos ? tt : tl) * p.kvdim + vi);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int tt = t + u * ngr;
-            if (tt > pos) continue;
-            const float vv = tt == pos ? vs[vi] : vc[u];
-#pragma unroll
-            for (int h = 0; h < GROUP; h++) acc[h] = fmaf(sc[h * ms + tt], vv, acc[h]);
-        }
-    }
-#pragma unroll
-    for (int h = 0; h < GROUP; h++) part[(h * ngr + tg) * hd + vi] = acc[h];
+    if (lane == 0) okw[wave] = ok;
     lds_barrier();
-    for (int k = tid; k < group * hd; k += kPB) {
-        const int h = k / hd, ii = k % hd;
+    bool all_ok = true;
+#pragma unroll
+    for (int w = 0; w < kPW; w++) all_ok = all_ok && okw[w];
+    if (!all_ok) return false;
+    // combine the waves: thread (h, d)
+    for (int k = tid; k < GROUP * HD; k += kPB) {
+        const int h = k / HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kPW; w++) M = fmaxf(M, wst[w * WREG + GROUP * HD + h]);
         float tot = 0.f, o = 0.f;
-        for (int w = 0; w < kPW; w++) tot += redf[(kPW + w) * GROUP + h];
-        for (int r = 0; r < ngr; r++) o += part[(h * ngr + r) * hd + ii];
-        ll_put(p.ll_att + (size_t)(g * group + h) * hd + ii, o / tot, e);
+#pragma unroll
+        for (int w = 0; w < kPW; w++) {
+            const float f = __builtin_amdgcn_exp2f(wst[w * WREG + GROUP * HD + h] - M);
+            tot = fmaf(f, wst[w * WREG + GROUP * HD + GROUP + h], tot);
+            o = fmaf(f, wst[w * WREG + k], o);
+        }
+        ll_put(p.ll_att + (size_t)g * GROUP * HD + k, o / tot, e);
     }
     return true;
 }
@@ -1398,11 +1509,15 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     for (int f = 0; f < p.n_forwards; f++) {
         const int pos = p.pos0 + f;
         const bool tracing = p.trace && f == p.trace_f && threadIdx.x == 0;
-        long long *tr = p.trace + (size_t)blockIdx.x * n_stamps;
+        long long *tr = p.trace + (size_t)blockIdx.x * 2 * n_stamps;
         int ts = 0;
         auto stamp = [&]() {
             if (tracing) tr[ts] = wall_clock64();
             ts++;
+        };
+        // input ready for the stage whose end stamp comes next
+        auto stamp_in = [&]() {
+            if (tracing) tr[n_stamps + ts] = wall_clock64();
         };
         stamp();
         const int tok = pos < p.n_prompt ? p.tokens[pos] : tok_next;
@@ -1435,19 +1550,21 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 if ((r = stage_poll<LD, CD, WT, true>(p, p.own[0], p.qkv_rows, p.D, E_STORE, io, xs, xq, red, okw, c,
                         [&](const StageCtx &cc) { tile_load<LD, CD, WT, 2>(t, cc, Lp.wqkv, p.D); })) < 0)
                     return false;
+                if (r) stamp_in();
                 if (r) stage_compute<LD, CD, WT, 2>(p, Lp.wqkv, Lp.s_qkv, p.D, E_STORE, io, xs, xq, ostage, bv, bi, c, t);
                 else settle_loads();
             }
             stamp();
             // attention
             if ((int)blockIdx.x < p.KVH) {
+                long long *tin = tracing ? tr + n_stamps + ts : nullptr;
                 bool aok;
                 if constexpr (WT == SH_DTYPE_W8A8)
-                    aok = attn_stage<KVT, HD, true>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf);
+                    aok = attn_stage<KVT, HD, true>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf, tin);
                 else if (p.H == p.KVH)
-                    aok = attn_stage_fast<KVT, HD, 1>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf);
+                    aok = attn_stage_wave<KVT, HD, 1>(p, l, blockIdx.x, pos, e, part, okw, kvlds, tin);
                 else
-                    aok = attn_stage_fast<KVT, HD, 2>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf);
+                    aok = attn_stage_wave<KVT, HD, 2>(p, l, blockIdx.x, pos, e, part, okw, kvlds, tin);
                 if (!aok) return false;
             }
             stamp();
@@ -1469,6 +1586,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 if ((r = stage_poll<LQ, CQ, WT, false>(p, p.own[1], p.D, p.qdim, E_RESID, io, xs, xq, red, okw, c,
                         [&](const StageCtx &cc) { tile_load<LQ, CQ, WT, 1>(t, cc, Lp.wo, p.qdim); })) < 0)
                     return false;
+                if (r) stamp_in();
                 if (r) stage_compute<LQ, CQ, WT, 1>(p, Lp.wo, Lp.s_o, p.qdim, E_RESID, io, xs, xq, ostage, bv, bi, c, t);
                 else settle_loads();
             }
@@ -1489,6 +1607,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 if ((r = stage_poll<LD, CD, WT, true>(p, p.own[2], 2 * p.F, p.D, E_GATE, io, xs, xq, red, okw, c,
                         [&](const StageCtx &cc) { tile_load<LD, CD, WT, 2>(t, cc, Lp.w13, p.D); })) < 0)
                     return false;
+                if (r) stamp_in();
                 if (r) stage_compute<LD, CD, WT, 2>(p, Lp.w13, Lp.s_13, p.D, E_GATE, io, xs, xq, ostage, bv, bi, c, t);
                 else settle_loads();
             }
@@ -1513,6 +1632,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 if ((r = stage_poll<LF, CF, WT, false>(p, p.own[3], p.D, p.F, E_RESID, io, xs, xq, red, okw, c,
                         [&](const StageCtx &cc) { tile_load<LF, CF, WT, 1>(t, cc, Lp.w2, p.F); })) < 0)
                     return false;
+                if (r) stamp_in();
                 if (r) stage_compute<LF, CF, WT, 1>(p, Lp.w2, Lp.s_2, p.F, E_RESID, io, xs, xq, ostage, bv, bi, c, t);
                 else settle_loads();
             }
@@ -1548,6 +1668,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             const int r = stage_poll<LD, CD, WT, true>(p, cown, p.V, p.D, E_CLS, io, xs, xq, red, okw, c,
                                                        [](const StageCtx &) {});
             if (r < 0) return;
+            stamp_in();
             if (r)
                 stage_compute<LD, CD, WT, 4>(p, p.cls, p.s_cls, p.D, E_CLS, io, xs, xq, ostage, bv, bi, c, t, cls_lds,
                                              cls_lrow0);
@@ -1584,21 +1705,12 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             if ((int)threadIdx.x < n) {
                 const size_t o = (size_t)threadIdx.x * kArgSlot;
                 uint64_t a = ll_get(pv + o), b = ll_get(pi + o);
-                long long t0 = 0;
+                WaitBound wb;
                 while ((uint32_t)(a >> 32) != ec || (uint32_t)(b >> 32) != ec) {
-                    const long long now = wall_clock64();
-                    if (!t0) {
-                        t0 = now;
-                    } else if (now - t0 > p.spin_limit) {
-                        __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (!wb.more(p)) {
                         ok = false;
                         break;
                     }
-                    if (now - t0 > p.quiet && aborted(p)) {
-                        ok = false;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
                     if ((uint32_t)(a >> 32) != ec) a = ll_get(pv + o);
                     if ((uint32_t)(b >> 32) != ec) b = ll_get(pi + o);
                 }
@@ -1606,6 +1718,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 idx = (int)(uint32_t)b;
             }
             if (!block_and(ok)) return;
+            stamp_in();
             wargmax(v, idx);
             if ((threadIdx.x & 63) == 0) cand[threadIdx.x >> 6] = ArgmaxPartial{v, idx};
             lds_barrier();

@@ -433,18 +433,31 @@ class Model:
     def trace_forward(self, forward: int) -> None:
         _check(self.lib.sh_trace_forward(self.h, forward), "sh_trace_forward")
 
-    def trace_stamps(self) -> np.ndarray:
-        """Timestamps (us, from the earliest forward start) of the traced forward:
-        [grid, 5 * n_layers + 3], one row per workgroup."""
+    def _trace_raw(self):
         L = self.cfg.n_layers
-        n = self.stats()["grid"] * (5 * L + 3)
+        n = self.stats()["grid"] * 2 * (5 * L + 3)
         buf = np.zeros(n, np.int64)
         cnt = C.c_int32(0)
         rate = C.c_double(0)
         _check(self.lib.sh_trace_read(self.h, buf.ctypes.data_as(C.POINTER(C.c_int64)), n, C.byref(cnt),
                                       C.byref(rate)), "sh_trace_read")
-        t = buf[:cnt.value].reshape(-1, 5 * L + 3).astype(np.float64)
-        return (t - t[:, 0].min()) * 1e6 / rate.value
+        t = buf[:cnt.value].reshape(-1, 2, 5 * L + 3).astype(np.float64)
+        return t, rate.value
+
+    def trace_stamps(self) -> np.ndarray:
+        """Stage-end timestamps (us, from the earliest forward start) of the traced forward:
+        [grid, 5 * n_layers + 3], one row per workgroup."""
+        t, rate = self._trace_raw()
+        return (t[:, 0] - t[:, 0, 0].min()) * 1e6 / rate
+
+    def trace_inputs(self) -> np.ndarray:
+        """Input-ready timestamps (us, same origin as trace_stamps): column j is when the
+        workgroup had the whole input of the stage whose end is column j of trace_stamps
+        (NaN where the workgroup had no input to wait for in that stage)."""
+        t, rate = self._trace_raw()
+        out = (t[:, 1] - t[:, 0, 0].min()) * 1e6 / rate
+        out[t[:, 1] == 0] = np.nan
+        return out
 
     def trace_read(self) -> dict:
         """Critical-path stage durations (us) of the traced forward, summed over layers: a

@@ -217,10 +217,12 @@ int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
 size_t sh_model_describe(const sh_model *m, char *buf, size_t len);
 /* Stage trace of the persistent decode kernel (a tracing aid like the reference's per-step
  * metrics, ane/storiesane/metrics.go:13-60): arm with the index of a forward within the next
- * decode launch (-1 disarms); after it, sh_trace_read returns grid x (5*n_layers + 3)
- * constant-clock timestamps, one row per workgroup (grid = sh_timing.grid): forward start,
- * then after each layer's qkv, attention, wo, w13 and w2 stages, after the classifier, after
- * the argmax. A workgroup that owns no rows in a stage stamps it as soon as it skips it.
+ * decode launch (-1 disarms); after it, sh_trace_read returns grid x 2 x (5*n_layers + 3)
+ * constant-clock timestamps, one row pair per workgroup (grid = sh_timing.grid). The first
+ * row: forward start, then after each layer's qkv, attention, wo, w13 and w2 stages, after the
+ * classifier, after the argmax (a workgroup that owns no rows in a stage stamps it as soon as
+ * it skips it). The second row, same columns: when the workgroup had that stage's whole input
+ * (0 where it waited for none).
  * -1 when the model does not run the persistent kernel. */
 int sh_trace_forward(sh_model *m, int32_t forward);
 int sh_trace_read(sh_model *m, int64_t *out, int32_t cap, int32_t *n_out, double *ticks_per_s);
