@@ -234,11 +234,13 @@ DecodeResult decode(sh_model *m, const sh_config &c, const std::vector<int32_t> 
     DecodeResult r;
     if (max_new <= 0) max_new = 64;
     if (temperature < 0) temperature = 0;
-    // device time and algorithmic bytes of every forward (sh_stats after each call)
+    // device time and algorithmic bytes of every token forward (sh_stats after each call; a
+    // greedy decode's prompt forward is reported apart, as prefill_ms, and its bytes are not
+    // counted, so its time is left out too)
     auto account = [&]() {
         sh_timing t{};
         if (sh_stats(m, &t) == 0) {
-            r.gpu_ms += t.gpu_ms;
+            r.gpu_ms += t.gpu_ms - t.prefill_ms;
             r.bytes += t.bytes_per_forward_mean * (double)t.forwards;
         }
     };

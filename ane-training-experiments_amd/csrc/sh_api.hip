@@ -133,23 +133,34 @@ bool run_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt) {
             if (!hip_ok(hipMemsetAsync(b.p, 0, 8 * b.n, m->stream), "clear hand-over")) return false;
         m->epoch = 1;
     }
-    if (!hip_ok(hipMemsetAsync(m->p_err, 0, 4, m->stream), "clear err")) return false;
+    if (!hip_ok(hipMemsetAsync(m->p_err, 0, 8, m->stream), "clear err")) return false;
     return hip_ok(launch_persistent(m, pos0, n_forwards, n_prompt), "persistent decode launch");
 }
 
-bool check_persistent_err(sh_model *m) {
+// Outcome of a persistent launch, read after the stream has synchronised.
+enum class LaunchCheck { Ok, Absent, Failed };
+
+// Ok: the launch ran to its end. Absent: a wait expired before every workgroup had started
+// (the grid was not all resident, e.g. another process held CUs). Failed: the error word could
+// not be read, or a wait expired with every workgroup running (a hand-over that never came:
+// reported, never retried).
+LaunchCheck check_persistent_err(sh_model *m) {
     int err = 0;
-    if (!hip_ok(hipMemcpy(&err, m->p_err, 4, hipMemcpyDeviceToHost), "read err")) return false;
-    if (err) {
-        set_error("persistent decode: a hand-over wait exceeded its time bound");
-        return false;
+    if (!hip_ok(hipMemcpy(&err, m->p_err, 4, hipMemcpyDeviceToHost), "read err")) return LaunchCheck::Failed;
+    if (err == 0) return LaunchCheck::Ok;
+    if (err == kErrAbsent) {
+        set_error("persistent decode: a hand-over wait expired before every workgroup had started "
+                  "(the grid was not all resident)");
+        return LaunchCheck::Absent;
     }
-    return true;
+    set_error("persistent decode: a hand-over wait exceeded its time bound with every workgroup running");
+    return LaunchCheck::Failed;
 }
 
-// After a persistent launch whose bounded waits expired (its workgroups were not all
-// resident, e.g. another process held CUs): models with a per-stage path switch to it for
-// good and the caller repeats the call; W8A8 has no per-stage path and keeps the error.
+// After a persistent launch whose grid was not all resident: models with a per-stage path
+// switch to it for good and the caller repeats the call (which starts from a cleared cache or,
+// for one forward, rewrites the cache row it evaluates); W8A8 has no per-stage path and keeps
+// the error.
 bool fall_back_to_graph(sh_model *m) {
     if (m->dtype == SH_DTYPE_W8A8) return false;
     m->persistent = false;
@@ -157,6 +168,22 @@ bool fall_back_to_graph(sh_model *m) {
              "per-stage kernels in a HIP graph (a persistent decode launch timed out waiting "
              "for its workgroups to be resident)");
     return true;
+}
+
+// The outcome of the persistent launch a call just waited for: true to carry on, false to
+// return -1; *retry is set when the model has switched to the per-stage path and the call
+// should run again.
+bool persistent_outcome(sh_model *m, bool *retry) {
+    *retry = false;
+    if (!m->persistent) return true;
+    switch (check_persistent_err(m)) {
+    case LaunchCheck::Ok: return true;
+    case LaunchCheck::Absent:
+        if (!fall_back_to_graph(m)) return false;
+        *retry = true;
+        return true;
+    default: return false;
+    }
 }
 
 // Enqueues n forwards at positions pos0.. (tokens[pos] feeds each; from n_prompt on the
@@ -788,10 +815,9 @@ int sh_decode_step(sh_model *m, int32_t token, int32_t pos, float *logits, int32
     if (!hip_ok(hipMemcpyAsync(&am, m->argmax_hist + pos, 4, hipMemcpyDeviceToHost, m->stream), "argmax") ||
         !hip_ok(hipStreamSynchronize(m->stream), "decode step"))
         return -1;
-    if (m->persistent && !check_persistent_err(m)) {
-        if (!fall_back_to_graph(m)) return -1;
-        return sh_decode_step(m, token, pos, logits, argmax_out);
-    }
+    bool retry = false;
+    if (!persistent_outcome(m, &retry)) return -1;
+    if (retry) return sh_decode_step(m, token, pos, logits, argmax_out);
     if (argmax_out) *argmax_out = am;
     float ms = 0;
     (void)hipEventElapsedTime(&ms, m->ev0, m->ev1);
@@ -845,7 +871,7 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
     // decode's per-token quantization, float order and exact attention). The token loop then
     // starts at the last prompt id.
     std::string why;
-    const int pre = (n_prompt > 1 && prefill_supported(m, &why)) ? n_prompt - 1 : 0;
+    const int pre = (n_prompt > 1 && !m->no_prompt_prefill && prefill_supported(m, &why)) ? n_prompt - 1 : 0;
     if (pre > 0) {
         if (!hip_ok(prefill_alloc(m, pre, false), "prefill scratch")) return -1;
         std::vector<int32_t> rows(3 * (size_t)pre);
@@ -873,10 +899,9 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
                 "copy tokens") ||
         !hip_ok(hipStreamSynchronize(m->stream), "greedy decode"))
         return -1;
-    if (m->persistent && !check_persistent_err(m)) {
-        if (!fall_back_to_graph(m)) return -1;
-        return sh_greedy_decode(m, prompt, n_prompt, max_new, out_tokens, n_out, stopped_eos);
-    }
+    bool retry = false;
+    if (!persistent_outcome(m, &retry)) return -1;
+    if (retry) return sh_greedy_decode(m, prompt, n_prompt, max_new, out_tokens, n_out, stopped_eos);
     // infer.go:190-193: stop after EOS
     int n = n_prompt;
     int eos = 0;
@@ -1057,12 +1082,18 @@ int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
     }
     hipEvent_t e0 = m->ev0, e1 = m->ev1, e2 = nullptr;
     if (!hip_ok(hipEventCreate(&e2), "event")) return -1;
-    bool ok = hip_ok(hipEventRecord(e0, s), "event");
+    bool ok = hip_ok(hipMemsetAsync(m->bt_err, 0, 4, s), "clear error word") && hip_ok(hipEventRecord(e0, s), "event");
     if (ok && S > 0) ok = hip_ok(enqueue_prefill(m, S, P - 1, false, true), "batch prefill");
     ok = ok && hip_ok(hipEventRecord(e1, s), "event");
     for (int i = 0; ok && i < steps; i++) ok = hip_ok(hipGraphLaunch(m->bt_exec, s), "batch step");
     ok = ok && hip_ok(hipEventRecord(e2, s), "event") && hip_ok(hipStreamSynchronize(s), "batch sync");
     ok = ok && hip_ok(hipMemcpy(hist.data(), m->bt_hist, 4 * hist.size(), hipMemcpyDeviceToHost), "read tokens");
+    int32_t lost = 0;
+    ok = ok && hip_ok(hipMemcpy(&lost, m->bt_err, 4, hipMemcpyDeviceToHost), "read error word");
+    if (ok && lost) {
+        set_error("sh_batch_greedy_decode: an attention split's partial never arrived (bounded wait expired)");
+        ok = false;
+    }
     float pre_ms = 0, dec_ms = 0;
     if (ok) {
         (void)hipEventElapsedTime(&pre_ms, e0, e1);
@@ -1229,6 +1260,32 @@ int sh_decode_tap(const sh_model *m, int32_t which, float *out, int32_t n) {
         return 0;
     }
     return hip_ok(hipMemcpy(out, dense, 4 * (size_t)len, hipMemcpyDeviceToHost), "tap read") ? 0 : -1;
+}
+
+int sh_debug_option(sh_model *m, int32_t option, int32_t value) {
+    if (!m) {
+        set_error("sh_debug_option: nil model");
+        return -1;
+    }
+    if (option == SH_DEBUG_FAIL_NEXT_LAUNCH) {
+        if (!m->persistent) {
+            set_error("sh_debug_option: the model does not run the persistent decode kernel");
+            return -1;
+        }
+        if (value != 0 && value != kErrTimeout && value != kErrAbsent) {
+            set_error("sh_debug_option: SH_DEBUG_FAIL_NEXT_LAUNCH takes 0 (off), 1 (a wait timed out with "
+                      "every workgroup running) or 2 (the grid was not all resident)");
+            return -1;
+        }
+        m->fail_next = value;
+        return 0;
+    }
+    if (option == SH_DEBUG_PROMPT_PREFILL) {
+        m->no_prompt_prefill = value == 0;
+        return 0;
+    }
+    set_error("sh_debug_option: unknown option " + std::to_string(option));
+    return -1;
 }
 
 int sh_trace_forward(sh_model *m, int32_t forward) {

@@ -35,6 +35,12 @@ struct DecodeState {
     int32_t pad[2];
 };
 
+// How a persistent decode launch ended early (its error word): a bounded wait expired with
+// every workgroup started (kErrTimeout), or before every workgroup had started, i.e. the grid
+// was not all resident (kErrAbsent).
+constexpr int kErrTimeout = 1;
+constexpr int kErrAbsent = 2;
+
 struct ArgmaxPartial {
     float v;
     int32_t i;
@@ -99,7 +105,9 @@ struct sh_model {
     bool p_argmax_every;    // w13 not on every workgroup: the next-token exchange every forward
     void *p_layers;         // device array of per-layer weight pointers
     uint64_t *ll_qkv, *ll_att, *ll_x2, *ll_gate, *ll_x, *ll_pv, *ll_pi;
-    int *p_err;
+    int *p_err;             // device: [0] how a persistent launch ended early, [1] workgroups started
+    int fail_next;          // testing aid: the next persistent launch ends at once with this code
+    bool no_prompt_prefill; // testing aid: a greedy decode feeds its prompt through the token loop
     uint32_t epoch;         // next unused hand-over epoch
     long long spin_ticks;   // wait bound in constant-clock ticks
     char path_note[512];    // which decode path runs, and why
@@ -138,6 +146,7 @@ struct sh_model {
     float *bt_sa;                              //       and its row scales [B]
     uint64_t *bt_tm, *bt_tl, *bt_tacc;         // streaming attention: tagged split partials
     int32_t *bt_cnt;                           // [B][KVH] split-merge counters
+    int32_t *bt_err;                           // set when a split partial never arrived
     uint32_t *bt_gen;                          // device copy of the call generation (tag part)
     uint32_t bt_gen_host;
     hipGraphExec_t bt_exec;                    // one captured step for bt_graph_b sequences

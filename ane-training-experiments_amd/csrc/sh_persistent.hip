@@ -94,7 +94,11 @@ struct PParams {
     int32_t *tokens, *hist;
     int pos0, n_forwards, n_prompt;
     uint32_t epoch0;
+    // err[0]: 0, or how the launch ended early: kErrTimeout (a wait expired with every
+    // workgroup started), kErrAbsent (a wait expired before every workgroup had started: not
+    // all of the grid was resident); err[1]: workgroups started so far
     int *err;
+    int fail_mode;     // testing aid: nonzero ends every workgroup at once with err[0] = fail_mode
     long long spin_limit;
     long long quiet;   // ticks a wait runs before it also reads the abort flag (20 us)
     long long *trace;  // forward trace_f: per workgroup 5L+3 stage-end stamps, then as many
@@ -266,7 +270,9 @@ struct WaitBound {
             return true;
         }
         if (now - t0 > p.spin_limit) {
-            __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int started = __hip_atomic_load(p.err + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_max(p.err, started < (int)gridDim.x ? kErrAbsent : kErrTimeout, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             return false;
         }
         return !(now - t0 > p.quiet && aborted(p));
@@ -1484,6 +1490,11 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     const int L = p.L;
     const int n_stamps = 5 * L + 3;
     int tok_next = 0;
+    if (p.fail_mode) {
+        if (threadIdx.x == 0) __hip_atomic_fetch_max(p.err, p.fail_mode, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(p.err + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Classifier rows: the attention workgroups own what their register tile holds; with
     // cls_lds_rows the others own twice as many and keep the second half in the attention
     // cache's LDS (unused outside attention) for the whole launch, copied here once.
@@ -1961,6 +1972,8 @@ hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt
     p.n_prompt = n_prompt;
     p.epoch0 = m->epoch;
     p.err = m->p_err;
+    p.fail_mode = m->fail_next;
+    m->fail_next = 0;
     p.spin_limit = m->spin_ticks;
     // The abort flag is an agent-scope load, a full round trip to the memory side: read on
     // every retry it doubles a retry's period, so a hand-over is noticed half a round trip

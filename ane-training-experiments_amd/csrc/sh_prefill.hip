@@ -1829,14 +1829,17 @@ __device__ __forceinline__ void tag_put(uint64_t *p, float v, uint32_t tag) {
     __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
-// The value of a tagged word once it carries `tag` (a bounded wait: a word still missing after
-// about a second is taken as it is, so no wave can hang).
-__device__ __forceinline__ float tag_get(const uint64_t *p, uint32_t tag) {
+// The value of a tagged word once it carries `tag`. The wait is bounded (about a second): a
+// word still missing then sets *err (the decode call reports the failure after the step) and is
+// taken as it is, so no wave can hang.
+__device__ __forceinline__ float tag_get(const uint64_t *p, uint32_t tag, int *err) {
     uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int spins = 0; (uint32_t)(w >> 32) != tag && spins < (1 << 22); spins++) {
+    int spins = 0;
+    for (; (uint32_t)(w >> 32) != tag && spins < (1 << 22); spins++) {
         __builtin_amdgcn_s_sleep(1);
         w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if ((uint32_t)(w >> 32) != tag) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return __uint_as_float((uint32_t)w);
 }
 
@@ -1864,7 +1867,7 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
     const float *partial, int ranges, QkRopeArgs a, const void *kc, const void *vc, size_t kv_seq_stride,
     const int32_t *pos, int H, int KVH, float scale, int nsplit, int nch_buf, int dt, size_t plane,
     uint16_t *att, uint64_t *tm, uint64_t *tl_, uint64_t *tacc, int *cnt, const uint32_t *gen, int layer,
-    int n_layers, int max_seq) {
+    int n_layers, int max_seq, int *err) {
     constexpr int EB = KVT == SH_KV_F32 ? 4 : 2;
     constexpr int RB = HD * EB;                        // bytes per cache row
     constexpr int C = kChunkBytes / RB;                // keys per chunk
@@ -2151,13 +2154,14 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
         const int h = g * GROUP + i / HD, ii = i % HD;
         const size_t pb = ((size_t)b * H + h) * nch_buf;
         float M = -INFINITY;
-        for (int c = 0; c < ns; c++) M = fmaxf(M, tag_get(tm + pb + c, tag));
+        for (int c = 0; c < ns; c++) M = fmaxf(M, tag_get(tm + pb + c, tag, err));
         float Lsum = 0.f;
-        for (int c = 0; c < ns; c++) Lsum += expf(tag_get(tm + pb + c, tag) - M) * tag_get(tl_ + pb + c, tag);
+        for (int c = 0; c < ns; c++)
+            Lsum += expf(tag_get(tm + pb + c, tag, err) - M) * tag_get(tl_ + pb + c, tag, err);
         const float invL = 1.0f / Lsum;
         float a = 0.f;
         for (int c = 0; c < ns; c++)
-            a += expf(tag_get(tm + pb + c, tag) - M) * tag_get(tacc + (pb + c) * HD + ii, tag);
+            a += expf(tag_get(tm + pb + c, tag, err) - M) * tag_get(tacc + (pb + c) * HD + ii, tag, err);
         store_op16(att, (size_t)b * qdim + (size_t)h * HD + ii, plane, a * invL, dt);
     }
 }
@@ -2191,7 +2195,7 @@ __global__ __launch_bounds__(256) void k_attn_split_combine(const float *pm, con
 // The streaming kernel for (kv type, head dim, group), or null when it has no instance.
 typedef void (*AttnStreamKernel)(const float *, int, QkRopeArgs, const void *, const void *, size_t,
                                  const int32_t *, int, int, float, int, int, int, size_t, uint16_t *, uint64_t *,
-                                 uint64_t *, uint64_t *, int *, const uint32_t *, int, int, int);
+                                 uint64_t *, uint64_t *, int *, const uint32_t *, int, int, int, int *);
 template <int KVT>
 AttnStreamKernel pick_attn_stream_kv(int hd, int group) {
     switch (hd * 8 + group) {
@@ -3104,8 +3108,8 @@ hipError_t batch_alloc(sh_model *m, int B) {
     // the streaming attention's tagged split partials, merge counters and call generation
     const size_t nt = (size_t)B * c.n_heads * nch;
     const size_t o_tm = take(8 * nt), o_tl = take(8 * nt), o_tacc = take(8 * nt * c.head_dim),
-                 o_cnt = take(4 * (size_t)B * c.n_kv_heads), o_gen = take(4);
-    const size_t o_tag0 = o_tm, tag_bytes = o_gen + 4 - o_tm;
+                 o_cnt = take(4 * (size_t)B * c.n_kv_heads), o_gen = take(4), o_err = take(4);
+    const size_t o_tag0 = o_tm, tag_bytes = o_err + 4 - o_tm;
     hipError_t e = hipMalloc(&m->bt_arena, off);
     if (e != hipSuccess) return e;
     uint8_t *A = (uint8_t *)m->bt_arena;
@@ -3137,6 +3141,7 @@ hipError_t batch_alloc(sh_model *m, int B) {
     m->bt_tacc = (uint64_t *)(A + o_tacc);
     m->bt_cnt = (int32_t *)(A + o_cnt);
     m->bt_gen = (uint32_t *)(A + o_gen);
+    m->bt_err = (int32_t *)(A + o_err);
     m->bt_gen_host = 0;
     // tags 0 (never written), counters 0 (every merge leaves them at 0), generation 0
     if ((e = hipMemset(A + o_tag0, 0, tag_bytes)) != hipSuccess) return e;
@@ -3240,7 +3245,7 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
             hipLaunchKernelGGL(astream, dim3(nsplit, c.n_kv_heads, B), dim3(kAT), 0, s,
                                (const float *)m->bt_part, rq, qa, kc, vc, kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, scale, nsplit, nch,
                                dt, (size_t)B * c.n_heads * c.head_dim, m->bt_att, m->bt_tm, m->bt_tl,
-                               m->bt_tacc, m->bt_cnt, m->bt_gen, l, c.n_layers, c.max_seq);
+                               m->bt_tacc, m->bt_cnt, m->bt_gen, l, c.n_layers, c.max_seq, m->bt_err);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
         const dim3 grid(nch, c.n_kv_heads, B);

@@ -29,6 +29,7 @@ SH_KV_F32 = 0
 SH_KV_F16 = 1
 SH_KV_BF16 = 2
 SH_TAP_X, SH_TAP_QKV, SH_TAP_ATT, SH_TAP_GATE, SH_TAP_X2 = 0, 1, 4, 5, 6
+SH_DEBUG_FAIL_NEXT_LAUNCH, SH_DEBUG_PROMPT_PREFILL = 1, 2
 
 BOS = 1
 EOS = 2
@@ -108,6 +109,7 @@ SIGNATURES = {
     "sh_stats": (C.c_int, [C.c_void_p, C.POINTER(ShTiming)]),
     "sh_model_describe": (C.c_size_t, [C.c_void_p, C.c_char_p, C.c_size_t]),
     "sh_trace_forward": (C.c_int, [C.c_void_p, C.c_int32]),
+    "sh_debug_option": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32]),
     "sh_trace_read": (C.c_int, [C.c_void_p, C.POINTER(C.c_int64), C.c_int32, _I32, C.POINTER(C.c_double)]),
     "sh_model_destroy": (None, [C.c_void_p]),
     "sh_quantize_i8": (C.c_int, [_F, C.c_int32, C.c_int32, C.POINTER(C.c_int8), _F, C.c_int32]),
@@ -429,6 +431,15 @@ class Model:
                                                 out.ctypes.data_as(_I32), cnt.ctypes.data_as(_I32)),
                "sh_batch_greedy_decode")
         return [out[i, :cnt[i]].copy() for i in range(n)]
+
+    def debug_fail_next_launch(self, mode: int) -> None:
+        """Testing aid: the next persistent launch ends at once, as a residency failure (2) or
+        a hand-over timeout with every workgroup running (1); 0 disarms."""
+        _check(self.lib.sh_debug_option(self.h, SH_DEBUG_FAIL_NEXT_LAUNCH, mode), "sh_debug_option")
+
+    def set_prompt_prefill(self, on: bool) -> None:
+        """Testing aid: False feeds a greedy decode's prompt through the token loop."""
+        _check(self.lib.sh_debug_option(self.h, SH_DEBUG_PROMPT_PREFILL, int(bool(on))), "sh_debug_option")
 
     def trace_forward(self, forward: int) -> None:
         _check(self.lib.sh_trace_forward(self.h, forward), "sh_trace_forward")

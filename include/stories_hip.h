@@ -66,7 +66,7 @@ typedef struct sh_timing {
     int32_t persistent;     /* 1: the persistent decode kernel ran; 0: per-stage kernels */
     int32_t grid;           /* workgroups of the persistent kernel */
     double prefill_ms;      /* device time of the prompt's full-sequence forward: part of
-                               gpu_ms for sh_greedy_decode (fp16/bf16) and
+                               gpu_ms for sh_greedy_decode (every dtype) and
                                sh_prefill_logits, apart from it for sh_batch_greedy_decode
                                (whose gpu_ms is the decode steps); 0 if none */
 } sh_timing;
@@ -116,9 +116,10 @@ int sh_decode_step(sh_model *m, int32_t token, int32_t pos, float *logits,
  * prompt (last max_seq ids; [BOS] if empty), generates up to max_new tokens (64 if <= 0),
  * stops after EOS=2 or at max_seq tokens. out_tokens (capacity max_seq) receives prompt +
  * generated ids, *n_out their count, *stopped_eos whether EOS ended the loop. The whole
- * loop runs on the device; the host sees only the final ids. fp16/bf16 models compute the
- * prompt's first n-1 positions in one full-sequence forward that fills the cache as the
- * token-by-token feed would; sh_stats then counts only the forwards after it. */
+ * loop runs on the device; the host sees only the final ids. The prompt's first n-1 positions
+ * run as one full-sequence forward that fills the cache as the token-by-token feed would (for
+ * W8A8 bit for bit, on its int8 matrix-core form); sh_stats then counts only the forwards after
+ * it, and reports that forward's device time as prefill_ms. */
 int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32_t max_new,
                      int32_t *out_tokens, int32_t *n_out, int32_t *stopped_eos);
 /* (*Engine).EvalLogits (ane/storiesane/engine.go:363-376) = evalLogitsCPUInto
@@ -215,6 +216,19 @@ int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
  * per-stage kernels) and why; returns the full length. No reference counterpart: the
  * reference reports its ANE/CPU choice through Diagnostics (ane/storiesane/diagnostics.go). */
 size_t sh_model_describe(const sh_model *m, char *buf, size_t len);
+/* Testing aids (no reference counterpart): sh_debug_option(m, option, value), 0 or -1.
+ * SH_DEBUG_FAIL_NEXT_LAUNCH exercises the persistent decode kernel's failure handling, whose
+ * contract is the reference's fallback on an accelerator failure (ane/storiesane/engine.go:
+ * 739-746): the next persistent launch ends at once in every workgroup, as if value 2: a
+ * bounded wait expired before the whole grid was resident (the model then switches to the
+ * per-stage graph path for good and the call is repeated there; W8A8, which has no such path,
+ * returns -1), or value 1: a wait expired with every workgroup running (the call returns -1 and
+ * the model keeps its path); 0 disarms; -1 when the model does not run the persistent kernel.
+ * SH_DEBUG_PROMPT_PREFILL 0: sh_greedy_decode feeds the prompt through the token loop (one
+ * forward per position, as infer.go:175-177 does) instead of one full-sequence forward; 1
+ * restores the default. */
+enum { SH_DEBUG_FAIL_NEXT_LAUNCH = 1, SH_DEBUG_PROMPT_PREFILL = 2 };
+int sh_debug_option(sh_model *m, int32_t option, int32_t value);
 /* Stage trace of the persistent decode kernel (a tracing aid like the reference's per-step
  * metrics, ane/storiesane/metrics.go:13-60): arm with the index of a forward within the next
  * decode launch (-1 disarms); after it, sh_trace_read returns grid x 2 x (5*n_layers + 3)

@@ -138,6 +138,49 @@ def test_greedy_decode_stops_on_eos(gpu):
     m.close()
 
 
+def test_persistent_fallback_to_graph_path(gpu):
+    """The persistent kernel's failure handling (engine.go:739-746 is the reference's contract:
+    an accelerator failure switches to the other path and the call still answers). A launch
+    whose grid was not all resident switches the model to the per-stage graph path and repeats
+    the call there: the greedy stream and the next step's logits still match the oracle. A
+    hand-over timeout with every workgroup running is an error and switches nothing. W8A8 has
+    no per-stage path: a residency failure is an error."""
+    cfg = tiny_config()
+    prompt = sh.synth_tokens(6, 172, cfg.vocab)
+    m, ref, _ = build(cfg, sh.SH_DTYPE_F16, seed=171, std=0.08)
+    assert m.describe().startswith("persistent decode kernel")
+    m.debug_fail_next_launch(2)
+    got, plen, _ = m.greedy_decode(prompt, 12)
+    want, _, want_logits = oracle_stream(ref, prompt, 12, cfg.max_seq)
+    assert got.tolist() == want.tolist()
+    assert not m.stats()["persistent"]
+    assert "per-stage kernels" in m.describe() and "resident" in m.describe()
+    check_stream(m, got, want_logits, tol=1e-3)
+    m.close()
+    # the same through sh_decode_step
+    m, ref, _ = build(cfg, sh.SH_DTYPE_F16, seed=171, std=0.08)
+    m.debug_fail_next_launch(2)
+    got1, am = m.eval_next_logits(int(prompt[0]), 0)
+    assert float(np.max(np.abs(got1 - ref.forward_one(int(prompt[0]), 0)))) < 1e-3
+    assert not m.stats()["persistent"]
+    m.close()
+    # a timeout with every workgroup running: an error, the path kept, the next call fine
+    m, ref, _ = build(cfg, sh.SH_DTYPE_F16, seed=171, std=0.08)
+    m.debug_fail_next_launch(1)
+    with pytest.raises(sh.ShError, match="every workgroup running"):
+        m.greedy_decode(prompt, 12)
+    assert m.describe().startswith("persistent decode kernel")
+    got, _, _ = m.greedy_decode(prompt, 12)
+    assert got.tolist() == want.tolist()
+    m.close()
+    # W8A8: no per-stage path
+    m, ref, _ = build(cfg, sh.SH_DTYPE_W8A8, seed=171, std=0.08)
+    m.debug_fail_next_launch(2)
+    with pytest.raises(sh.ShError, match="not all resident"):
+        m.greedy_decode(prompt, 12)
+    m.close()
+
+
 def test_quantize_bit_exact(gpu):
     rng = np.random.default_rng(161)
     w = (rng.standard_normal((300, 257)) * 0.02).astype(np.float32)
@@ -202,6 +245,13 @@ def test_stories110m_fp16_greedy_128(gpu):
     again, _, _ = m.greedy_decode(prompt, 128)
     assert again.tolist() == got.tolist()
     check_stream(m, got, want_logits)
+    # the prompt fed through the token loop instead: the persistent launch runs the 15 prompt
+    # forwards too (in this shape's layout the next token is exchanged after every forward)
+    assert "from workgroup" in m.describe()
+    m.set_prompt_prefill(False)
+    got2, _, _ = m.greedy_decode(prompt, 128)
+    assert got2.tolist() == want.tolist()
+    assert m.stats()["forwards"] == 15 + 128   # no full-sequence forward ran
     m.close()
 
 
@@ -221,6 +271,13 @@ def test_qwen3_shaped_bf16_greedy(gpu):
     print(f"persistent={st['persistent']} grid={st['grid']} {st['gpu_ms']:.3f} ms for {st['forwards']} forwards")
     assert st["persistent"]
     check_stream(m, got, want_logits)
+    # the prompt fed through the token loop: its 31 forwards run in the persistent launch, and
+    # in this shape's layout (w13 on every workgroup) they skip the next-token exchange
+    assert "from workgroup" not in m.describe()
+    m.set_prompt_prefill(False)
+    got2, _, _ = m.greedy_decode(prompt, 256)
+    assert got2.tolist() == want.tolist()
+    assert m.stats()["forwards"] == 31 + 256   # no full-sequence forward ran
     m.close()
 
 
