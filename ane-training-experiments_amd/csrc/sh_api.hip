@@ -1007,9 +1007,12 @@ double batch_step_bytes(const sh_model *m, int B, int pos) {
     return w + B * per_seq;
 }
 
-int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
-                           int32_t prompt_len, int32_t max_new, int32_t *out_tokens,
-                           int32_t *n_out) {
+// The batched decode; with keep_rows, the logits of sequences keep_rows[0, n_keep) are copied
+// out after every step into keep_out[(step * n_keep + i) * vocab] (the steps then run as eager
+// launches, not the captured step graph).
+static int batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs, int32_t prompt_len,
+                               int32_t max_new, int32_t *out_tokens, int32_t *n_out, const int32_t *keep_rows,
+                               int32_t n_keep, float *keep_out) {
     if (!ready(m)) return -1;
     const sh_config &c = m->cfg;
     if (!prompts || !out_tokens || !n_out || n_seqs < 1 || prompt_len < 1 ||
@@ -1031,9 +1034,21 @@ int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
     if (max_new <= 0) max_new = 64;                       // infer.go:140-143
     const int B = n_seqs, P = prompt_len;
     const int steps = std::min(max_new, c.max_seq - P);   // stop at len == maxSeq
+    for (int i = 0; i < n_keep; i++)
+        if (keep_rows[i] < 0 || keep_rows[i] >= B) {
+            set_error("sh_batch_greedy_decode_logits: sequence " + std::to_string(keep_rows[i]) + " out of range");
+            return -1;
+        }
     (void)hipSetDevice(m->device);
     if (!hip_ok(batch_alloc(m, B), "batch scratch") || !hip_ok(batch_new_generation(m), "batch generation"))
         return -1;
+    float *keep_dev = nullptr;
+    const size_t keep_floats = (size_t)std::max(steps, 1) * n_keep * c.vocab;
+    if (n_keep > 0 && !hip_ok(hipMalloc(&keep_dev, 4 * keep_floats), "logits buffer")) return -1;
+    struct Free {
+        float *p;
+        ~Free() { (void)hipFree(p); }
+    } free_keep{keep_dev};
     hipStream_t s = m->stream;
     // prompt rows 0..P-2 of every sequence: one causal forward that fills the caches
     const int S = B * (P - 1);
@@ -1085,8 +1100,22 @@ int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
     bool ok = hip_ok(hipMemsetAsync(m->bt_err, 0, 4, s), "clear error word") && hip_ok(hipEventRecord(e0, s), "event");
     if (ok && S > 0) ok = hip_ok(enqueue_prefill(m, S, P - 1, false, true), "batch prefill");
     ok = ok && hip_ok(hipEventRecord(e1, s), "event");
-    for (int i = 0; ok && i < steps; i++) ok = hip_ok(hipGraphLaunch(m->bt_exec, s), "batch step");
+    for (int i = 0; ok && i < steps; i++) {
+        if (n_keep == 0) {
+            ok = hip_ok(hipGraphLaunch(m->bt_exec, s), "batch step");
+            continue;
+        }
+        ok = hip_ok(enqueue_batch_step(m, B), "batch step");
+        for (int k = 0; ok && k < n_keep; k++)
+            ok = hip_ok(hipMemcpyAsync(keep_dev + ((size_t)i * n_keep + k) * c.vocab,
+                                       m->bt_logits + (size_t)keep_rows[k] * c.vocab, 4 * (size_t)c.vocab,
+                                       hipMemcpyDeviceToDevice, s),
+                        "keep logits");
+    }
     ok = ok && hip_ok(hipEventRecord(e2, s), "event") && hip_ok(hipStreamSynchronize(s), "batch sync");
+    if (ok && n_keep > 0)
+        ok = hip_ok(hipMemcpy(keep_out, keep_dev, 4 * (size_t)steps * n_keep * c.vocab, hipMemcpyDeviceToHost),
+                    "read logits");
     ok = ok && hip_ok(hipMemcpy(hist.data(), m->bt_hist, 4 * hist.size(), hipMemcpyDeviceToHost), "read tokens");
     int32_t lost = 0;
     ok = ok && hip_ok(hipMemcpy(&lost, m->bt_err, 4, hipMemcpyDeviceToHost), "read error word");
@@ -1124,6 +1153,22 @@ int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
     m->last.persistent = 0;
     m->last.grid = 0;
     return 0;
+}
+
+int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs, int32_t prompt_len,
+                           int32_t max_new, int32_t *out_tokens, int32_t *n_out) {
+    return batch_greedy_decode(m, prompts, n_seqs, prompt_len, max_new, out_tokens, n_out, nullptr, 0, nullptr);
+}
+
+int sh_batch_greedy_decode_logits(sh_model *m, const int32_t *prompts, int32_t n_seqs, int32_t prompt_len,
+                                  int32_t max_new, int32_t *out_tokens, int32_t *n_out, const int32_t *rows,
+                                  int32_t n_rows, float *logits_out) {
+    if (!rows || n_rows < 1 || !logits_out) {
+        set_error("sh_batch_greedy_decode_logits: bad arguments");
+        return -1;
+    }
+    return batch_greedy_decode(m, prompts, n_seqs, prompt_len, max_new, out_tokens, n_out, rows, n_rows,
+                               logits_out);
 }
 
 int sh_window_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32_t seq,

@@ -94,6 +94,9 @@ SIGNATURES = {
                                           C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "sh_batch_greedy_decode": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32), C.c_int32, C.c_int32, C.c_int32,
                                          C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    "sh_batch_greedy_decode_logits": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32), C.c_int32, C.c_int32,
+                                                C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
+                                                C.POINTER(C.c_int32), C.c_int32, C.POINTER(C.c_float)]),
     "sh_decode_tap": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_float), C.c_int32]),
     "sh_copy_calibrate": (C.c_int, [C.c_size_t, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "sh_last_error": (C.c_size_t, [C.c_char_p, C.c_size_t]),
@@ -431,6 +434,25 @@ class Model:
                                                 out.ctypes.data_as(_I32), cnt.ctypes.data_as(_I32)),
                "sh_batch_greedy_decode")
         return [out[i, :cnt[i]].copy() for i in range(n)]
+
+    def batch_greedy_decode_logits(self, prompts, max_new: int, rows):
+        """sh_batch_greedy_decode_logits: (token arrays as batch_greedy_decode, logits
+        [steps, len(rows), V] of the chosen sequences at every step)."""
+        p = np.ascontiguousarray(np.asarray(prompts, dtype=np.int32))
+        if p.ndim != 2:
+            raise ValueError("prompts must be a 2-D array [n_seqs, prompt_len]")
+        n, plen = p.shape
+        mn = max_new if max_new > 0 else 64
+        steps = min(mn, self.cfg.max_seq - plen)
+        r = np.ascontiguousarray(np.asarray(rows, dtype=np.int32))
+        out = np.zeros((n, plen + mn), np.int32)
+        cnt = np.zeros(n, np.int32)
+        lg = np.zeros((max(steps, 1), r.size, self.cfg.vocab), np.float32)
+        _check(self.lib.sh_batch_greedy_decode_logits(self.h, p.ctypes.data_as(_I32), n, plen, max_new,
+                                                       out.ctypes.data_as(_I32), cnt.ctypes.data_as(_I32),
+                                                       r.ctypes.data_as(_I32), r.size, _fp(lg)),
+               "sh_batch_greedy_decode_logits")
+        return [out[i, :cnt[i]].copy() for i in range(n)], lg[:steps]
 
     def debug_fail_next_launch(self, mode: int) -> None:
         """Testing aid: the next persistent launch ends at once, as a residency failure (2) or

@@ -212,6 +212,17 @@ int sh_window_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt
 int sh_batch_greedy_decode(sh_model *m, const int32_t *prompts, int32_t n_seqs,
                            int32_t prompt_len, int32_t max_new, int32_t *out_tokens,
                            int32_t *n_out);
+/* sh_batch_greedy_decode that also returns the logits of sequences rows[0, n_rows) at every
+ * step: logits_out[(i * n_rows + k) * vocab + v] for step i (the forward at position
+ * prompt_len - 1 + i, whose argmax is token prompt_len + i), for every step the call runs
+ * (min(max_new, max_seq - prompt_len)). The counterpart of reading EvalNextLogits
+ * (infer.go:72-77) at each step of those sequences' decodes; an inspection and testing aid
+ * (the steps run as eager launches rather than the captured step graph, so sh_stats' times
+ * are not the batched decode's). */
+int sh_batch_greedy_decode_logits(sh_model *m, const int32_t *prompts, int32_t n_seqs,
+                                  int32_t prompt_len, int32_t max_new, int32_t *out_tokens,
+                                  int32_t *n_out, const int32_t *rows, int32_t n_rows,
+                                  float *logits_out);
 /* Human-readable description of the decode path this model runs (persistent kernel or
  * per-stage kernels) and why; returns the full length. No reference counterpart: the
  * reference reports its ANE/CPU choice through Diagnostics (ane/storiesane/diagnostics.go). */

@@ -537,7 +537,22 @@ static void project_tokens(const or_decoder *d, int l, int p, float *out, const 
  * own, whose K/V the layer pass has stored before any token of it attends. The K/V cache it
  * leaves and the last token's logits therefore equal those of n calls of or_forward_one, bit
  * for bit. The classifier runs for the last token only; the taps are not updated. */
+static int prompt_forward(or_decoder *d, const int32_t *tokens, int n, int pos0, int first, float *logits_out);
+
 int or_prompt_forward(or_decoder *d, const int32_t *tokens, int n, int pos0, float *logits_out) {
+    return prompt_forward(d, tokens, n, pos0, n - 1, logits_out);
+}
+
+/* or_prompt_forward keeping the logits of every token from `first` on: logits_out[(t - first)
+ * * vocab + v] for t in [first, n), each equal, bit for bit, to or_forward_one's at position
+ * pos0 + t (the final RMSNorm per token, then the classifier rows summed in the same order). */
+int or_prompt_forward_logits(or_decoder *d, const int32_t *tokens, int n, int pos0, int first,
+                             float *logits_out) {
+    if (first < 0 || first >= n || !logits_out) return -1;
+    return prompt_forward(d, tokens, n, pos0, first, logits_out);
+}
+
+static int prompt_forward(or_decoder *d, const int32_t *tokens, int n, int pos0, int first, float *logits_out) {
     const or_config *c = &d->cfg;
     if (n <= 0 || pos0 < 0 || pos0 + n > c->max_seq) return -1;
     for (int t = 0; t < n; t++)
@@ -605,7 +620,17 @@ int or_prompt_forward(or_decoder *d, const int32_t *tokens, int n, int pos0, flo
         or_mat_vec_w8a8(d->logits, d->cls8, d->cls_s, d->xn, c->vocab, D, thr);
     else
         or_mat_vec(d->logits, d->cls, d->xn, c->vocab, D, thr);
-    if (logits_out) memcpy(logits_out, d->logits, sizeof(float) * c->vocab);
+    if (logits_out && first == n - 1) {
+        memcpy(logits_out, d->logits, sizeof(float) * c->vocab);
+    } else if (logits_out) {
+        int nk = n - first;
+        for (int t = first; t < n; t++)
+            or_rms_norm_vec(xn + (size_t)(t - first) * D, x + (size_t)t * D, d->rms_final, D, c->norm_eps);
+        if (c->w8a8)
+            mat_tokens_w8a8(logits_out, d->cls8, d->cls_s, xn, c->vocab, D, nk, thr);
+        else
+            mat_tokens(logits_out, d->cls, xn, c->vocab, D, nk, thr);
+    }
     free(x); free(xn); free(q); free(k); free(v); free(att); free(x2); free(h1); free(h3);
     return 0;
 }

@@ -79,6 +79,8 @@ int or_forward_one(or_decoder *d, int token, int pos, float *logits_out);
  * last token's logits (logits_out, may be NULL) equal n calls of or_forward_one bit for bit.
  * Returns 0 or -1 (ids or positions out of range). */
 int or_prompt_forward(or_decoder *d, const int32_t *tokens, int n, int pos0, float *logits_out);
+int or_prompt_forward_logits(or_decoder *d, const int32_t *tokens, int n, int pos0, int first,
+                             float *logits_out);
 /* Decode with temperature 0 (infer.go:136-202). out_tokens holds prompt + generated
  * (capacity max_seq). margins (optional, capacity max_new) receives top1-top2 gaps. */
 int or_greedy_decode(or_decoder *d, const int32_t *prompt, int n_prompt, int max_new,

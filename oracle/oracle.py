@@ -85,6 +85,7 @@ def load() -> C.CDLL:
         "or_decoder_reset": (None, [C.c_void_p]),
         "or_forward_one": (C.c_int, [C.c_void_p, C.c_int, C.c_int, _F]),
         "or_prompt_forward": (C.c_int, [C.c_void_p, _I32, C.c_int, C.c_int, _F]),
+        "or_prompt_forward_logits": (C.c_int, [C.c_void_p, _I32, C.c_int, C.c_int, C.c_int, _F]),
         "or_greedy_decode": (C.c_int, [C.c_void_p, _I32, C.c_int, C.c_int, _I32, _I32, _I32, _F]),
         "or_decoder_tap": (_F, [C.c_void_p, C.c_int]),
         "or_embed_lookup_cf": (None, [_F, _F, C.c_int, C.POINTER(C.c_uint16), C.c_int, C.c_int]),
@@ -189,6 +190,15 @@ class Decoder:
         out = np.empty(self.cfg.vocab, np.float32)
         if self.lib.or_prompt_forward(self.h, t.ctypes.data_as(_I32), t.size, pos0, fp(out)):
             raise ValueError("or_prompt_forward: out of range")
+        return out
+
+    def prompt_forward_logits(self, tokens, first: int, pos0: int = 0) -> np.ndarray:
+        """prompt_forward keeping the logits of tokens[first:] ([n - first, V]; each equal, bit
+        for bit, to forward_one's at its position): a teacher-forced decode of a given stream."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32))
+        out = np.empty((t.size - first, self.cfg.vocab), np.float32)
+        if self.lib.or_prompt_forward_logits(self.h, t.ctypes.data_as(_I32), t.size, pos0, first, fp(out)):
+            raise ValueError("or_prompt_forward_logits: out of range")
         return out
 
     def tap(self, which: int, n: int) -> np.ndarray:

@@ -142,44 +142,58 @@ def test_batch_qwen3_shaped_32x1024(gpu):
 
 
 def test_batch_qwen3_shaped_32x1024_against_oracle(gpu):
-    """The batched configuration at full size against the oracle: row 0 of the 32 x 1024
-    batch (seed-3 weights rounded to bf16, bf16 KV) next to the oracle's Decode of the same
-    prompt. The oracle consumes the 1024 prompt ids in one layer-major pass (equal, bit for
-    bit, to 1024 forwardOne calls; pinned on the CPU) and then follows the batch's own tokens
-    for 8 more positions. Each of the batch's first 9 generated tokens must be within the
-    2e-2 logits bar of the oracle's maximum at its position, so a token that differs from
-    the oracle's argmax is allowed only where the oracle's top two are that close. The
-    one-position decode path (sh_decode_step per position) over the same prompt must give
-    logits within 2e-2 max-abs of the oracle's at position 1023, with the same argmax."""
+    """The batched configuration at full size against the oracle, for the whole decode: rows 0
+    and 31 of the 32 x 1024 batch (seed-3 weights rounded to bf16, bf16 KV), 128 greedy steps.
+    The oracle is teacher-forced on each row's own stream (one layer-major pass over the 1024
+    prompt ids and the first 127 generated ids, keeping the logits of positions 1023..1150;
+    each bit-identical to forwardOne's, pinned on the CPU). At every step the batch's own
+    logits for the row (sh_batch_greedy_decode_logits) must be within max-abs 2e-2 of the
+    oracle's, and the batch's token must be the oracle's argmax wherever the oracle's top-2
+    margin exceeds 2e-2 (elsewhere within 2e-2 of the oracle's maximum). The one-position
+    decode path (sh_decode_step per position) over row 0's prompt must give logits within 2e-2
+    of the oracle's at position 1023, with the same argmax."""
     cfg = sh.qwen3_06b_config()
     cfg.max_batch = 32
     w = sh.synth_weights(cfg, seed=3, std=0.02)
     m = sh.Model(cfg, sh.SH_DTYPE_BF16)
     m.upload(w)
     prompts = sh.synth_tokens(32 * 1024, 4, cfg.vocab).reshape(32, 1024)
-    got = m.batch_greedy_decode(prompts, 16)
-    # the one-position decode path over the same prompt, for a logits-level comparison
+    rows = (0, 31)
+    got, lg = m.batch_greedy_decode_logits(prompts, 128, rows)
+    assert lg.shape[0] == 128
+    # the same decode through the captured step graph gives the same tokens
+    plain = m.batch_greedy_decode(prompts, 128)
+    assert all(a.tolist() == b.tolist() for a, b in zip(plain, got))
+    # the one-position decode path over row 0's prompt, for a logits-level comparison
     m.reset_cache()
     for p in range(1023):
         m.eval_next_logits(int(prompts[0, p]), p, want_logits=False)
     single, _ = m.eval_next_logits(int(prompts[0, 1023]), 1023)
     m.close()
-    row = got[0]
     ref = oracle.Decoder(oracle.config_from(cfg), w.rounded(sh.SH_DTYPE_BF16), threads=THREADS)
     del w
-    lg = ref.prompt_forward(prompts[0])
-    err = float(np.max(np.abs(single - lg)))
-    print(f"position 1023, one-position decode path: max-abs logits error {err:.3e}", flush=True)
-    assert err <= 2e-2
-    assert int(np.argmax(single)) == int(np.argmax(lg))
-    steps = min(9, len(row) - 1024)
-    for k in range(steps):
-        if k:
-            lg = ref.forward_one(int(row[1023 + k]), 1023 + k)
-        tok = int(row[1024 + k])
-        top = np.sort(lg)[-2:]
-        gap = float(lg.max() - lg[tok])
-        print(f"position {1023 + k}: batch token {tok}, oracle argmax {int(lg.argmax())}, "
-              f"gap {gap:.2e}, oracle top-2 margin {float(top[1] - top[0]):.2e}", flush=True)
-        assert gap <= 2e-2, f"position {1023 + k}"
+    for k, b in enumerate(rows):
+        row = got[b]
+        steps = len(row) - 1024
+        want = ref.prompt_forward_logits(row[:1024 + steps - 1], first=1023)
+        if b == 0:
+            err = float(np.max(np.abs(single - want[0])))
+            print(f"position 1023, one-position decode path: max-abs logits error {err:.3e}", flush=True)
+            assert err <= 2e-2
+            assert int(np.argmax(single)) == int(np.argmax(want[0]))
+        errs = np.max(np.abs(lg[:steps, k] - want), axis=1)
+        top = np.sort(want, axis=1)[:, -2:]
+        margins = top[:, 1] - top[:, 0]
+        flips = 0
+        for i in range(steps):
+            tok = int(row[1024 + i])
+            if margins[i] > 2e-2:
+                assert tok == int(np.argmax(want[i])), f"row {b} step {i}: token {tok}, oracle {np.argmax(want[i])}"
+            else:
+                flips += tok != int(np.argmax(want[i]))
+                assert float(want[i].max() - want[i][tok]) <= 2e-2, f"row {b} step {i}"
+        print(f"row {b}: {steps} steps, max-abs logits error {errs.max():.3e} (median {np.median(errs):.3e}), "
+              f"smallest oracle top-2 margin {margins.min():.3e}, {flips} near-tie tokens off the oracle argmax",
+              flush=True)
+        assert errs.max() <= 2e-2, f"row {b}: step {int(np.argmax(errs))}"
     ref.close()

@@ -377,6 +377,28 @@ def test_prompt_pass_equals_forward_one_bitwise(gqa, w8a8, kv):
     turned.close()
 
 
+@pytest.mark.parametrize("gqa,w8a8", [(False, False), (True, True)])
+def test_prompt_pass_logits_range_equals_forward_one_bitwise(gqa, w8a8):
+    """or_prompt_forward_logits (a teacher-forced pass over a given stream keeping the logits
+    from one position on, used to check the batched decode at every step) against forwardOne
+    per position: every kept row bit-identical, 21 rows leaving a partial eight-token block of
+    the classifier product."""
+    mk = tiny_gqa_config if gqa else tiny_config
+    cfg = mk()
+    w = random_gains(sh.synth_weights(cfg, seed=87, std=0.08), 88)
+    oc = oracle.config_from(cfg, w8a8=w8a8)
+    toks = sh.synth_tokens(33, 89, cfg.vocab)
+    one, turned = oracle.Decoder(oc, w, threads=3), oracle.Decoder(oc, w, threads=2)
+    want = np.stack([one.forward_one(int(toks[t]), t) for t in range(33)])
+    got = turned.prompt_forward_logits(toks, first=12)
+    assert got.shape == (21, cfg.vocab)
+    assert np.array_equal(got.view(np.uint32), want[12:].view(np.uint32))
+    with pytest.raises(ValueError):
+        turned.prompt_forward_logits(toks, first=33)
+    one.close()
+    turned.close()
+
+
 def test_w8a8_decoder_tracks_fp32():
     cfg = tiny_config()
     w = sh.synth_weights(cfg, seed=91, std=0.08)
