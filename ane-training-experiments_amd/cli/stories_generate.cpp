@@ -3,7 +3,7 @@
 // on the GPU through the C ABI (include/stories_hip.h).
 //
 //   stories-generate [-model stories110M.bin] [-tokenizer tokenizer.bin] [-prompt-ids 1,2]
-//                    [-max-new 64] [-temperature 0.8] [-seed N] [-seq 256]
+//                    [-max-new 64] [-temperature 0.8] [-seed N] [-seq 256] [-ane]
 //
 // Flags beyond the reference's (all optional):
 //   -shape stories110m|qwen3-0.6b   model shape when no -model file is given
@@ -287,6 +287,60 @@ DecodeResult decode(sh_model *m, const sh_config &c, const std::vector<int32_t> 
     return r;
 }
 
+// (*Engine).Decode (ane/storiesane/decode.go:18-94): every step evaluates the whole window
+// of the last `seq` tokens, left-padded with BOS (fillDecodeWindow, decode.go:83-94), and
+// samples the next id from its last column; there is no max_seq stop (the window slides).
+// Greedy runs entirely on the device (sh_window_greedy_decode); a sampled decode evaluates the
+// window on the device (sh_prefill_logits, the EvalLogits forward) and draws on the host.
+DecodeResult decode_window(sh_model *m, const sh_config &c, const std::vector<int32_t> &prompt_in, int seq,
+                           int max_new, float temperature, Sampler &rng) {
+    DecodeResult r;
+    if (max_new <= 0) max_new = 64;
+    if (temperature < 0) temperature = 0;
+    auto account = [&]() {
+        sh_timing t{};
+        if (sh_stats(m, &t) == 0) {
+            r.gpu_ms += t.gpu_ms;
+            r.bytes += t.bytes_per_forward_mean * (double)t.forwards;
+        }
+    };
+    std::vector<int32_t> prompt = prompt_in.empty() ? std::vector<int32_t>{1} : prompt_in;
+    if ((int)prompt.size() > seq) prompt.erase(prompt.begin(), prompt.end() - seq);
+    for (size_t i = 0; i < prompt.size(); i++)   // decode.go:44-48
+        if (prompt[i] < 0 || prompt[i] >= c.vocab)
+            fatalf("decode: %s", "storiesane decode: prompt token[" + std::to_string(i) + "]=" +
+                                     std::to_string(prompt[i]) + " out of range");
+    r.prompt_length = (int)prompt.size();
+    if (temperature <= 1e-6f) {
+        std::vector<int32_t> out(prompt.size() + max_new);
+        int32_t n = 0, eos = 0;
+        if (sh_window_greedy_decode(m, prompt.data(), (int32_t)prompt.size(), seq, max_new, out.data(), &n, &eos))
+            fatalf("decode: %s", lib_error());
+        account();
+        r.tokens.assign(out.begin(), out.begin() + n);
+        r.stopped_eos = eos != 0;
+        return r;
+    }
+    r.tokens = prompt;
+    std::vector<uint16_t> window(seq);
+    std::vector<float> logits((size_t)c.vocab * seq), row(c.vocab);
+    for (int step = 0; step < max_new; step++) {
+        const size_t n = r.tokens.size(), keep = std::min(n, (size_t)seq);
+        std::fill(window.begin(), window.end(), (uint16_t)1);
+        for (size_t i = 0; i < keep; i++) window[seq - keep + i] = (uint16_t)r.tokens[n - keep + i];
+        if (sh_prefill_logits(m, window.data(), seq, logits.data())) fatalf("decode: %s", lib_error());
+        account();
+        for (int v = 0; v < c.vocab; v++) row[v] = logits[(size_t)v * seq + seq - 1];
+        const int next = rng.sample(row.data(), c.vocab, temperature);
+        r.tokens.push_back(next);
+        if (next == 2) {
+            r.stopped_eos = true;
+            break;
+        }
+    }
+    return r;
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
@@ -333,9 +387,6 @@ int main(int argc, char **argv) {
         return 0;
     }
 
-    if (fl.b("ane"))
-        fatalf("decode: %s", "the full-window engine (-ane) is not part of this build; the "
-                             "default KV-cache decoder runs on the GPU");
 
     // ---- model description and host weights ----
     sh_config c{};
@@ -391,6 +442,14 @@ int main(int argc, char **argv) {
         if (fl.i("bench-steps") <= 0 || fl.i("prompt-len") <= 0)
             fatalf("%s", "-batch needs -bench-steps and -prompt-len");
         c.max_batch = batch;
+    }
+    const bool ane = fl.b("ane");
+    if (ane) {
+        // main.go:71-85: storiesane.Open with Seq = -seq; the engine scales each residual
+        // branch by 1/sqrt(2 L) (residual.go:9)
+        if (fl.i("bench-steps") > 0 || fl.i("batch") > 0 || fl.b("eval-logits") || fl.b("train"))
+            fatalf("%s", "-ane takes no bench, batch, eval-logits or train flags");
+        c.residual_scale = (float)(1.0 / sqrt(2.0 * c.n_layers));
     }
     if (fl.b("eval-logits")) {
         if (fl.i("bench-steps") <= 0 || fl.i("prompt-len") <= 0)
@@ -474,7 +533,9 @@ int main(int argc, char **argv) {
     }
     sh_model *m = open_model(c, dtype, w);
     w = stories::HostWeights();   // device holds the weights now
-    Sampler rng{(uint64_t)fl.i("seed")};
+    // the engine's decode seeds its generator with -seed, or 42 when that is 0
+    // (decode.go:30-33, engine.go:166-168)
+    Sampler rng{(uint64_t)(ane && fl.i("seed") == 0 ? 42 : fl.i("seed"))};
     const int max_new = (int)fl.i("max-new");
     const float temperature = (float)fl.f("temperature");
 
@@ -626,7 +687,8 @@ int main(int argc, char **argv) {
     }
 
     const auto t0 = std::chrono::steady_clock::now();
-    DecodeResult res = decode(m, c, prompt, max_new, temperature, rng);
+    DecodeResult res = ane ? decode_window(m, c, prompt, (int)c.max_seq, max_new, temperature, rng)
+                           : decode(m, c, prompt, max_new, temperature, rng);
     const double elapsed = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     const int new_tokens = (int)res.tokens.size() - res.prompt_length;
     const double tps = elapsed > 0 ? new_tokens / elapsed : 0.0;

@@ -659,6 +659,39 @@ static float top2_margin(const float *v, int n) {
     return a - b;
 }
 
+/* sampleFromLogits (infer.go:347-371) with the uniform draw given: temperature <= 1e-6 takes
+ * the first maximum (argmax, infer.go:373-383); otherwise mx = the first maximum's value,
+ * terms exp((float64(l) - float64(mx)) * float64(1/T)) (1/T in float32, as the reference's
+ * invT := float64(1 / temperature)), total their float64 sum in index order, target = u * total,
+ * and the first index whose running float64 sum reaches target (the last index if none does).
+ * *slack (may be NULL) receives the target's distance from the nearer end of the chosen index's
+ * CDF interval, divided by total (0 for the argmax rule). */
+int or_sample_from_logits(const float *logits, int n, float temperature, double u, double *slack) {
+    if (slack) *slack = 0.0;
+    if (temperature <= 1e-6f) {
+        int best = 0;
+        for (int i = 1; i < n; i++)
+            if (logits[i] > logits[best]) best = i;
+        return best;
+    }
+    float mx = logits[0];
+    for (int i = 1; i < n; i++)
+        if (logits[i] > mx) mx = logits[i];
+    double inv_t = (double)(1.0f / temperature);
+    double total = 0.0;
+    for (int i = 0; i < n; i++) total += exp(((double)logits[i] - (double)mx) * inv_t);
+    double target = u * total, acc = 0.0;
+    for (int i = 0; i < n; i++) {
+        double lo = acc;
+        acc += exp(((double)logits[i] - (double)mx) * inv_t);
+        if (acc >= target) {
+            if (slack) *slack = fmin(target - lo, acc - target) / total;
+            return i;
+        }
+    }
+    return n - 1;
+}
+
 /* infer.go:136-202 Decode with temperature <= 1e-6 (argmax sampling, infer.go:347-350) */
 int or_greedy_decode(or_decoder *d, const int32_t *prompt, int n_prompt, int max_new,
                      int32_t *out_tokens, int32_t *n_out, int32_t *stopped_eos,

@@ -79,6 +79,9 @@ int or_forward_one(or_decoder *d, int token, int pos, float *logits_out);
  * last token's logits (logits_out, may be NULL) equal n calls of or_forward_one bit for bit.
  * Returns 0 or -1 (ids or positions out of range). */
 int or_prompt_forward(or_decoder *d, const int32_t *tokens, int n, int pos0, float *logits_out);
+/* sampleFromLogits (infer.go:347-371) with the uniform draw u in [0, 1) given; *slack = the
+ * draw's distance from the chosen index's CDF interval ends over the total (0 for argmax). */
+int or_sample_from_logits(const float *logits, int n, float temperature, double u, double *slack);
 int or_prompt_forward_logits(or_decoder *d, const int32_t *tokens, int n, int pos0, int first,
                              float *logits_out);
 /* Decode with temperature 0 (infer.go:136-202). out_tokens holds prompt + generated

@@ -85,6 +85,7 @@ def load() -> C.CDLL:
         "or_decoder_reset": (None, [C.c_void_p]),
         "or_forward_one": (C.c_int, [C.c_void_p, C.c_int, C.c_int, _F]),
         "or_prompt_forward": (C.c_int, [C.c_void_p, _I32, C.c_int, C.c_int, _F]),
+        "or_sample_from_logits": (C.c_int, [_F, C.c_int, C.c_float, C.c_double, C.POINTER(C.c_double)]),
         "or_prompt_forward_logits": (C.c_int, [C.c_void_p, _I32, C.c_int, C.c_int, C.c_int, _F]),
         "or_greedy_decode": (C.c_int, [C.c_void_p, _I32, C.c_int, C.c_int, _I32, _I32, _I32, _F]),
         "or_decoder_tap": (_F, [C.c_void_p, C.c_int]),
@@ -395,6 +396,15 @@ def embed_backward(dembed: np.ndarray, dx_cf: np.ndarray, tokens) -> None:
     t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint16))
     load().or_embed_backward(fp(dembed), fp(x), t.ctypes.data_as(C.POINTER(C.c_uint16)),
                              dembed.shape[0], dembed.shape[1], x.shape[1])
+
+
+def sample_from_logits(logits, temperature: float, u: float):
+    """or_sample_from_logits: sampleFromLogits (infer.go:347-371) with the draw u given;
+    returns (index, slack), slack = the draw's distance from its CDF interval's ends / total."""
+    lg = np.ascontiguousarray(np.asarray(logits, dtype=np.float32))
+    slack = C.c_double(0)
+    i = load().or_sample_from_logits(lg.ctypes.data_as(_F), lg.size, temperature, u, C.byref(slack))
+    return int(i), float(slack.value)
 
 
 def fill_decode_window(seq: int, tokens) -> np.ndarray:

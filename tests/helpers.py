@@ -173,3 +173,19 @@ def write_blzt(path, cfg, w, version=3, meta=None, opt_value=0.25):
         f.write(np.full(2 * w.rms_final.size, opt_value, "<f4").tobytes())
         f.write(np.ascontiguousarray(w.embed, "<f4").tobytes())
         f.write(np.full(2 * w.embed.size, opt_value, "<f4").tobytes())
+
+
+def splitmix64_uniforms(seed: int, n: int) -> np.ndarray:
+    """The stories-generate sampler's draws: splitmix64 (Vigna's published generator) seeded
+    by -seed, each output's top 53 bits as a double in [0, 1)."""
+    mask = (1 << 64) - 1
+    x = seed & mask
+    out = np.empty(n, np.float64)
+    for i in range(n):
+        x = (x + 0x9E3779B97F4A7C15) & mask
+        z = x
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+        z ^= z >> 31
+        out[i] = (z >> 11) * (1.0 / 9007199254740992.0)
+    return out

@@ -10,7 +10,8 @@ import pytest
 
 import oracle
 import stories_hip as sh
-from helpers import BLZT_LAYER_ORDER, LLAMA2_ORDER, tiny_config, write_blzt, write_llama2_bin, write_tokenizer_bin
+from helpers import (BLZT_LAYER_ORDER, LLAMA2_ORDER, deepnet_alpha, splitmix64_uniforms, tiny_config, write_blzt,
+                     write_llama2_bin, write_tokenizer_bin)
 
 CLI = os.path.join(os.path.dirname(sh.LIB_PATH), "stories-generate")
 
@@ -198,6 +199,100 @@ def test_cli_sampled_decode_is_seeded(tmp_path):
     assert a == b
     ids = [int(t) for t in a.split("=", 1)[1].split(",")]
     assert all(0 <= t < cfg.vocab for t in ids) and len(ids) >= 2
+
+
+def cli_ids(stdout):
+    return [int(t) for t in stdout.splitlines()[1].split("=", 1)[1].split(",")]
+
+
+def check_sampled_stream(ids, plen, want_logits, temp, seed, delta, what):
+    """The CLI's sampled ids against sampleFromLogits (infer.go:347-371, the oracle's
+    restatement) fed the oracle's logits at each step of the CLI's own stream and the same
+    splitmix64 draws. The device logits are within delta of the oracle's, which moves every
+    normalised CDF boundary by at most 4 (e^(2 delta / T) - 1); where the draw lies farther
+    than that from its interval's ends the ids must be equal (pinned), elsewhere they may
+    differ. Returns the number of pinned steps."""
+    draws = splitmix64_uniforms(seed, len(want_logits))
+    bound = 4.0 * (np.exp(2.0 * delta / temp) - 1.0) + 1e-12
+    pinned = 0
+    for k, lg in enumerate(want_logits):
+        idx, slack = oracle.sample_from_logits(lg, temp, float(draws[k]))
+        if slack > bound:
+            pinned += 1
+            assert ids[plen + k] == idx, f"{what}: step {k}: CLI {ids[plen + k]}, oracle sampler {idx}"
+    print(f"{what}: {pinned} of {len(want_logits)} steps pinned (delta {delta:.2e}, bound {bound:.2e})")
+    return pinned
+
+
+@pytest.mark.gpu
+def test_cli_sampled_decode_matches_oracle_sampler(tmp_path):
+    """-temperature 0.8 on the KV-cache decoder: every pinned step's id equals the oracle
+    sampler's (check_sampled_stream), the oracle teacher-forced on the CLI's stream and the
+    draws the CLI's documented splitmix64 stream seeded by -seed (Go's math/rand stream itself
+    is not reproduced). delta is measured through the library on the same stream."""
+    cfg = gqa_file_config()
+    w = sh.synth_weights(cfg, seed=331, std=0.08)
+    path = tmp_path / "m.bin"
+    write_llama2_bin(path, cfg, w)
+    temp, seed, plen = 0.8, 7, 3
+    ids = cli_ids(run("-model", path, "-prompt-ids", "5,9,11", "-max-new", "40", "-temperature", temp,
+                      "-seq", "64", "-seed", seed).stdout)
+    ref = oracle.Decoder(oracle.config_from(cfg), w.rounded(sh.SH_DTYPE_F16), threads=4)
+    m = sh.Model(cfg, sh.SH_DTYPE_F16)
+    m.upload(w)
+    want, delta = [], 0.0
+    for pos in range(len(ids) - 1):
+        lo = ref.forward_one(ids[pos], pos)
+        lg, _ = m.eval_next_logits(ids[pos], pos)
+        delta = max(delta, float(np.max(np.abs(lg - lo))))
+        if pos >= plen - 1:
+            want.append(lo)
+    m.close()
+    assert len(want) == len(ids) - plen
+    assert check_sampled_stream(ids, plen, want, temp, seed, delta, "KV decoder") >= 0.9 * len(want)
+
+
+@pytest.mark.gpu
+def test_cli_ane_decode_matches_window_oracle(tmp_path):
+    """-ane (main.go:71-85: storiesane.Open + (*Engine).Decode, decode.go:18-94): the window of
+    the last -seq ids, BOS-padded, evaluated whole every step with the engine's residual scale
+    1/sqrt(2 L). -temperature 0: the ids equal the oracle's window decode (engine.go:804-842
+    per step, first maximum of the last column). -temperature 0.8: every pinned step's id
+    equals the oracle sampler's on the oracle's window logits of the CLI's own stream, with the
+    engine's draws seeded by -seed (42 when it is 0, engine.go:166-168)."""
+    cfg = gqa_file_config()
+    w = sh.synth_weights(cfg, seed=341, std=0.08)
+    path = tmp_path / "m.bin"
+    write_llama2_bin(path, cfg, w)
+    seq = 16
+    acfg = tiny_config(n_heads=4, n_kv_heads=2, max_seq=seq, residual_scale=deepnet_alpha(cfg.n_layers))
+    ocfg, ow = oracle.config_from(acfg), w.rounded(sh.SH_DTYPE_F16)
+    # greedy: the window slides past 16 tokens
+    p = run("-ane", "-model", path, "-prompt-ids", "5,9,11", "-max-new", "24", "-temperature", "0", "-seq", seq)
+    assert p.stdout.splitlines()[0].startswith("source=pretrained prompt_tokens=3 ")
+    got = cli_ids(p.stdout)
+    toks = [5, 9, 11]
+    while len(toks) < len(got):
+        window = oracle.fill_decode_window(seq, np.asarray(toks, np.int32))
+        toks.append(int(np.argmax(oracle.eval_logits_cf(ocfg, ow, window, threads=4)[:, seq - 1])))
+        if toks[-1] == 2:
+            break
+    assert got == toks and (len(got) == 3 + 24 or got[-1] == 2)
+    # sampled, seed 0 -> 42
+    temp, plen = 0.8, 3
+    ids = cli_ids(run("-ane", "-model", path, "-prompt-ids", "5,9,11", "-max-new", "20", "-temperature", temp,
+                      "-seq", seq, "-seed", 0).stdout)
+    m = sh.Model(acfg, sh.SH_DTYPE_F16)
+    m.upload(w)
+    want, delta = [], 0.0
+    for k in range(len(ids) - plen):
+        window = oracle.fill_decode_window(seq, np.asarray(ids[:plen + k], np.int32))
+        lo = oracle.eval_logits_cf(ocfg, ow, window, threads=4)[:, seq - 1]
+        lg = m.eval_logits(window)[:, seq - 1]
+        delta = max(delta, float(np.max(np.abs(lg - lo))))
+        want.append(lo)
+    m.close()
+    assert check_sampled_stream(ids, plen, want, temp, 42, delta, "-ane") >= 0.9 * len(want)
 
 
 @pytest.mark.gpu

@@ -452,3 +452,37 @@ def test_linear_vocab_matmul_and_final_norm_against_float64():
     xd = x.astype(np.float64)
     want = xd / np.sqrt((xd ** 2).mean(axis=0, keepdims=True) + 1e-5) * g[:, None]
     np.testing.assert_allclose(got, want, atol=1e-6, rtol=1e-6)
+
+
+def test_splitmix64_draws_known_answers():
+    """The test helper's splitmix64 against the generator's published outputs for seed 0."""
+    from helpers import splitmix64_uniforms
+    want = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
+    got = splitmix64_uniforms(0, 4)
+    assert [int(u * 9007199254740992.0) for u in got] == [w >> 11 for w in want]
+
+
+def test_sample_from_logits_is_inverse_cdf_of_softmax():
+    """or_sample_from_logits (infer.go:347-371) against the mathematics: the argmax rule at
+    temperature <= 1e-6 (first maximum); otherwise the index i with cdf[i-1] < u <= cdf[i] for
+    the softmax of logits/T (scipy, float64), with the reported slack its distance from those
+    bounds; closed forms on two equal logits; the draw's end points."""
+    from scipy.special import softmax
+    lg = np.array([0.5, 2.0, 2.0, -1.0], np.float32)
+    assert oracle.sample_from_logits(lg, 0.0, 0.9) == (1, 0.0)
+    assert oracle.sample_from_logits(lg, 1e-7, 0.1)[0] == 1
+    two = np.zeros(2, np.float32)
+    assert oracle.sample_from_logits(two, 1.0, 0.25) == (0, 0.25)
+    assert oracle.sample_from_logits(two, 1.0, 0.75) == (1, 0.25)
+    assert oracle.sample_from_logits(two, 1.0, 0.0)[0] == 0
+    rng = np.random.default_rng(91)
+    for temp in (0.8, 0.5, 1.7):
+        lg = (rng.standard_normal(300) * 1.5).astype(np.float32)
+        inv_t = float(np.float32(1.0) / np.float32(temp))
+        cdf = np.cumsum(softmax(lg.astype(np.float64) * inv_t))
+        for u in rng.random(400):
+            i, slack = oracle.sample_from_logits(lg, temp, float(u))
+            lo = cdf[i - 1] if i else 0.0
+            assert lo - 1e-12 <= u <= cdf[i] + 1e-12, (temp, u, i)
+            assert slack == pytest.approx(min(u - lo, cdf[i] - u), abs=1e-12)
+        assert oracle.sample_from_logits(lg, temp, 0.0)[0] == 0   # target 0: the first index
