@@ -982,15 +982,32 @@ void or_linear_cf(float *out, const float *w, const float *in, int out_ch, int i
     linear_cf(out, w, in, out_ch, in_ch, seq, threads);
 }
 
+static void eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t *tokens, int seq,
+                           float *logits_cf, int layer_threads, int threads);
+
 void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t *tokens,
                        int seq, float *logits_cf, int threads) {
+    eval_logits_cf(cfg, w, tokens, seq, logits_cf, threads, threads);
+}
+
+/* The same forward with the reference's threading, for timing it as the reference runs:
+ * linearCF and causalAttentionCF serial (forward_common.go:5-46), the vocabulary product over
+ * `threads` (MatMulVocabSeq's parallelFor over V, cpu.go:276-300). (RMSNorm, which the reference
+ * also spreads over GOMAXPROCS, stays serial here: under 0.1% of the forward's work.) */
+void or_eval_logits_cf_ref_threads(const or_config *cfg, const or_weights *w, const uint16_t *tokens,
+                                   int seq, float *logits_cf, int threads) {
+    eval_logits_cf(cfg, w, tokens, seq, logits_cf, 1, threads);
+}
+
+static void eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t *tokens, int seq,
+                           float *logits_cf, int layer_threads, int threads) {
     int D = cfg->dim;
     size_t S = (size_t)seq;
     float *x = (float *)malloc(sizeof(float) * D * S);
     float *next = (float *)malloc(sizeof(float) * D * S);
     or_embed_lookup_cf(x, w->embed, cfg->vocab, tokens, D, seq);
     for (int l = 0; l < cfg->n_layers; l++) {
-        or_layer_forward_cf(cfg, &w->layers[l], x, seq, next, threads);
+        or_layer_forward_cf(cfg, &w->layers[l], x, seq, next, layer_threads);
         float *tmp = x; x = next; next = tmp;   /* cur and next swap every layer */
     }
     rms_norm_final_cf(next, x, w->rms_final, D, seq, cfg->norm_eps);

@@ -99,6 +99,10 @@ void or_embed_lookup_cf(float *out, const float *embed, int vocab, const uint16_
                         int dim, int seq);
 void or_eval_logits_cf(const or_config *cfg, const or_weights *w, const uint16_t *tokens,
                        int seq, float *logits_cf, int threads);
+/* or_eval_logits_cf with the reference's threading (linearCF and attention serial, the
+ * vocabulary product over `threads`): the same values, for timing. */
+void or_eval_logits_cf_ref_threads(const or_config *cfg, const or_weights *w, const uint16_t *tokens,
+                                   int seq, float *logits_cf, int threads);
 /* One layer of the channel-first forward (engine.go:815-838), x_cf [D,S] -> out_cf [D,S]. */
 void or_layer_forward_cf(const or_config *cfg, const or_layer *L, const float *x_cf, int seq,
                          float *out_cf, int threads);

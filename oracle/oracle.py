@@ -92,6 +92,8 @@ def load() -> C.CDLL:
         "or_embed_lookup_cf": (None, [_F, _F, C.c_int, C.POINTER(C.c_uint16), C.c_int, C.c_int]),
         "or_eval_logits_cf": (None, [C.POINTER(OrConfig), C.POINTER(OrWeights), C.POINTER(C.c_uint16),
                                      C.c_int, _F, C.c_int]),
+        "or_eval_logits_cf_ref_threads": (None, [C.POINTER(OrConfig), C.POINTER(OrWeights), C.POINTER(C.c_uint16),
+                                     C.c_int, _F, C.c_int]),
         "or_fill_decode_window": (None, [C.POINTER(C.c_uint16), C.c_int, _I32, C.c_int]),
         "or_layer_forward_cf": (None, [C.POINTER(OrConfig), C.POINTER(OrLayer), _F, C.c_int, _F, C.c_int]),
         "or_layer_forward_cf_taps": (None, [C.POINTER(OrConfig), C.POINTER(OrLayer), _F, C.c_int, _F, _F, _F,
@@ -234,13 +236,15 @@ class Decoder:
             pass
 
 
-def eval_logits_cf(cfg: OrConfig, weights, tokens, threads: int = 1) -> np.ndarray:
-    """or_eval_logits_cf: engine.go:804-842, channel-first [V, S]."""
+def eval_logits_cf(cfg: OrConfig, weights, tokens, threads: int = 1, reference_threading: bool = False) -> np.ndarray:
+    """or_eval_logits_cf: engine.go:804-842, channel-first [V, S]. reference_threading: the
+    reference's threading (linearCF and attention serial, the vocabulary product over
+    `threads`), for timing; the values are the same."""
     t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint16))
     holder = _WeightsHolder(weights, cfg.n_layers)
     out = np.empty((cfg.vocab, t.size), np.float32)
-    load().or_eval_logits_cf(C.byref(cfg), C.byref(holder.s), t.ctypes.data_as(C.POINTER(C.c_uint16)),
-                             t.size, fp(out), threads)
+    fn = load().or_eval_logits_cf_ref_threads if reference_threading else load().or_eval_logits_cf
+    fn(C.byref(cfg), C.byref(holder.s), t.ctypes.data_as(C.POINTER(C.c_uint16)), t.size, fp(out), threads)
     return out
 
 

@@ -486,3 +486,15 @@ def test_sample_from_logits_is_inverse_cdf_of_softmax():
             assert lo - 1e-12 <= u <= cdf[i] + 1e-12, (temp, u, i)
             assert slack == pytest.approx(min(u - lo, cdf[i] - u), abs=1e-12)
         assert oracle.sample_from_logits(lg, temp, 0.0)[0] == 0   # target 0: the first index
+
+
+def test_eval_logits_reference_threading_same_values():
+    """The forward timed with the reference's threading (linearCF and attention serial) gives
+    the same logits, bit for bit, as the threaded one (each output's sum keeps its order)."""
+    cfg = tiny_gqa_config(qk_norm=1)
+    w = random_gains(sh.synth_weights(cfg, seed=92, std=0.08), 93)
+    oc = oracle.config_from(cfg)
+    toks = sh.synth_tokens(21, 94, cfg.vocab)
+    a = oracle.eval_logits_cf(oc, w, toks, threads=4)
+    b = oracle.eval_logits_cf(oc, w, toks, threads=3, reference_threading=True)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
