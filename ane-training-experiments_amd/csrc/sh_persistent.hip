@@ -254,22 +254,26 @@ __device__ __forceinline__ bool aborted(const PParams &p) {
 
 // The bound of a wait, taken once per poll round: false once the wait has to end (its time
 // limit passed, which sets *p.err, or, after the quiet period, *p.err set by another wave).
-// The clock is read every eighth round, and rounds follow each other without a sleep: every
-// round waits out a memory round trip anyway, and on this part each extra poll request or
-// pause lengthens a hand-over (measured on rings of stages: one request per word per round,
-// no sleep, 1.33 us per hand-over; with a sleep 1.36 us; two or four requests in flight per
-// word, staggered by sleeps, 1.50 to 1.93 us).
+// The clock is read every eighth round. Each round re-requests every missing word once, after
+// the shortest sleep: on rings of stages one request per word per round costs 1.33 us per
+// hand-over without a sleep and 1.36 us with one, two or four requests in flight per word
+// (staggered by sleeps) 1.50 to 1.93 us; in the full decode the sleep is neutral at 768 wide
+// and 0.6% faster at 1024 wide, where the polls of 256 workgroups contend for the L2.
+// The expiry branches are marked unlikely so that they are laid out after the hot code: the
+// whole decode loop runs out of the instruction cache, and the larger shapes' kernels slow
+// down by about 12 us per forward for every KB of code added to it.
 struct WaitBound {
     long long t0 = 0;
     unsigned rounds = 0;
     __device__ __forceinline__ bool more(const PParams &p) {
-        if ((rounds++ & 7u) != 0) return true;
+        __builtin_amdgcn_s_sleep(1);
+        if (__builtin_expect((rounds++ & 7u) != 0, 1)) return true;
         const long long now = wall_clock64();
         if (!t0) {
             t0 = now;
             return true;
         }
-        if (now - t0 > p.spin_limit) {
+        if (__builtin_expect(now - t0 > p.spin_limit, 0)) {
             const int started = __hip_atomic_load(p.err + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_fetch_max(p.err, started < (int)gridDim.x ? kErrAbsent : kErrTimeout, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
@@ -911,7 +915,7 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
     QkvMap qm{p.ll_qkv, qs, (size_t)g * group * hd, p.qdim + (size_t)g * hd,
               p.qdim + p.kvdim + (size_t)g * hd, group * hd, hd, e};
     if (!ll_wait_batch<(kMaxGroup + 2) * 256 / kPB>(group * hd + 2 * hd, p, qm)) return false;
-    if (tin) *tin = wall_clock64();
+    if (__builtin_expect(tin != nullptr, 0)) *tin = wall_clock64();
     if (p.qk_norm) {
         // per-head RMSNorm: wave w < group normalises q head w, wave `group` normalises k
         if (wave <= group) {
@@ -1128,6 +1132,245 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
 }
 
 
+// Attention for the fp16 / bf16 models with two q heads per kv head (the Qwen3 shape: 128-dim
+// heads; attn_stage_wave serves one q head per kv head, the W8A8 model attn_stage<..., true>):
+// the same mathematics in fewer dependent steps, rounded differently in the last bits. (The
+// per-wave form measured slower at this shape: 736 against 658 us per Qwen3-shaped forward,
+// each of its waves polling 512 words.)
+//  - RoPE factors are loaded before the poll; QK-norm and the softmax use float math;
+//  - scores are lane-sliced dot products over the cached rows (LDS rows two blocks per trip,
+//    rows beyond the LDS stage read from the cache the same way), each wave tracking the
+//    running maximum of its scores;
+//  - the softmax runs on all waves; the exp terms are left unnormalised and the P.V sums are
+//    scaled by 1/sum at the end (p.v/sum instead of (p/sum).v);
+//  - three workgroup barriers after the cache append, none at the end (the next stage's poll
+//    starts with one).
+template <int KVT, int HD, int GROUP>
+__device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
+                                                float *sc, float *part, uint8_t *kvlds, float *redf,
+                                                long long *tin) {
+    using S = KvStage<KVT, HD>;
+    constexpr int hd = HD, ngr = kPB / HD;
+    constexpr int LPK = S::RB / 16, EPC = 16 / S::EB, PPW = 64 / LPK;
+    constexpr int group = GROUP;   // q heads per kv head, known at compile time so the loops
+                                   // below carry no per-row branches
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int ms = p.max_seq;
+    const LayerPtrs Lp = layer_ptrs(p.layers, l);
+    const size_t lbase = (size_t)l * ms * p.kvdim + (size_t)g * hd;
+    SH_LDS uint8_t *kst = (SH_LDS uint8_t *)kvlds;
+    SH_LDS uint8_t *vst = kst + (size_t)S::ROWS * S::RB;
+    const int kofs = group * hd, vofs = kofs + hd;
+    float *ks = qs + kofs, *vs = qs + vofs;
+    const int half = hd / 2;
+    // this thread's RoPE pair (q heads, then k) and its factors, before the poll
+    const bool rope_t = tid < (group + 1) * half;
+    const int rpi = tid % half;
+    float rc = 0.f, rs = 0.f;
+    if (rope_t) {
+        rc = p.rope_cos[pos * half + rpi];
+        rs = p.rope_sin[pos * half + rpi];
+    }
+    // QK-norm gains of this wave's head (wave w < group: q head w, wave group: k)
+    constexpr int GPL = (HD + 63) / 64;
+    float gq[GPL];
+#pragma unroll
+    for (int q = 0; q < GPL; q++) gq[q] = 0.f;
+    if (p.qk_norm && wave <= group) {
+        const float *gn = wave < group ? Lp.q_norm : Lp.k_norm;
+#pragma unroll
+        for (int q = 0; q < GPL; q++)
+            if (lane + 64 * q < hd) gq[q] = gn[lane + 64 * q];
+    }
+    QkvMap qm{p.ll_qkv, qs, (size_t)g * group * hd, p.qdim + (size_t)g * hd,
+              p.qdim + p.kvdim + (size_t)g * hd, group * hd, hd, e};
+    if (!ll_wait_batch<(GROUP + 2) * 256 / kPB>(group * hd + 2 * hd, p, qm)) return false;
+    if (__builtin_expect(tin != nullptr, 0)) *tin = wall_clock64();
+    if (p.qk_norm) {
+        // per-head RMSNorm: wave w < group normalises q head w, wave `group` normalises k
+        if (wave <= group) {
+            float *v = qs + (wave < group ? wave : group) * hd;
+            float ss = 0.f;
+            for (int i = lane; i < hd; i += 64) ss += v[i] * v[i];
+            ss = wsum<64>(ss);
+            const float rr = rsqrtf(ss / (float)hd + (float)p.qk_eps);
+#pragma unroll
+            for (int q = 0; q < GPL; q++)
+                if (lane + 64 * q < hd) v[lane + 64 * q] = v[lane + 64 * q] * rr * gq[q];
+        }
+        lds_barrier();
+    }
+    if (rope_t) {   // infer.go:247-265, interleaved pairs
+        float *v = qs + (tid / half) * hd;
+        const float ev = v[2 * rpi], ov = v[2 * rpi + 1];
+        v[2 * rpi] = ev * rc - ov * rs;
+        v[2 * rpi + 1] = ev * rs + ov * rc;
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // the LDS copies of the cached rows have landed
+    lds_barrier();
+    // infer.go:267-271 storeKV in the cache's storage type; row pos also joins the LDS rows
+    for (int i = tid; i < hd; i += kPB) {
+        ks[i] = kv_rnd<KVT>(ks[i]);
+        vs[i] = kv_rnd<KVT>(vs[i]);
+        kv_st<KVT>(p.kcache, lbase + (size_t)pos * p.kvdim + i, ks[i]);
+        kv_st<KVT>(p.vcache, lbase + (size_t)pos * p.kvdim + i, vs[i]);
+        if (pos < S::ROWS) {
+            kv_put<KVT>(kst + (size_t)pos * S::RB, i, ks[i]);
+            kv_put<KVT>(vst + (size_t)pos * S::RB, i, vs[i]);
+        }
+    }
+    lds_barrier();
+    // scores (infer.go:280-288) and each wave's maximum
+    const int sl = lane % LPK, rin = lane / LPK;
+    float qr[GROUP][EPC];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++)
+#pragma unroll
+        for (int q = 0; q < EPC; q++) qr[h][q] = h < group ? qs[h * hd + sl * EPC + q] : 0.f;
+    float mx[GROUP];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) mx[h] = -INFINITY;
+    auto score_row = [&](const float (&kf)[EPC], int t, bool valid) {
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            if (h >= group) continue;
+            float d = 0.f;
+#pragma unroll
+            for (int q = 0; q < EPC; q++) d = fmaf(qr[h][q], kf[q], d);
+            d = wsum<LPK>(d) * p.inv_sqrt_hd;
+            if (valid) {
+                if (sl == 0) sc[h * ms + t] = d;
+                mx[h] = fmaxf(mx[h], d);
+            }
+        }
+    };
+    const int tl = pos < S::ROWS ? pos : S::ROWS - 1;   // last position held in LDS
+    for (int t0 = wave * PPW; t0 <= tl; t0 += 2 * kPW * PPW) {
+        const int ta = t0 + rin, tb = t0 + kPW * PPW + rin;
+        const bool va = ta <= tl, vb = tb <= tl;
+        const u32x4 ka = ((const SH_LDS u32x4 *)(kst + (size_t)(va ? ta : tl) * S::RB))[sl];
+        const u32x4 kb = ((const SH_LDS u32x4 *)(kst + (size_t)(vb ? tb : tl) * S::RB))[sl];
+        float fa[EPC], fb[EPC];
+        kv_unpack16<KVT>(ka, fa);
+        kv_unpack16<KVT>(kb, fb);
+        score_row(fa, ta, va);
+        score_row(fb, tb, vb);
+    }
+    if (pos > tl) {
+        // rows beyond the LDS stage, from the cache (row pos from the staged k)
+        float kpos[EPC];
+#pragma unroll
+        for (int q = 0; q < EPC; q++) kpos[q] = ks[sl * EPC + q];
+        // four row blocks per trip, their cache reads in flight together
+        const SH_GLOBAL uint8_t *kc = (const SH_GLOBAL uint8_t *)p.kcache;
+        for (int tb = tl + 1 + wave * PPW; tb <= pos; tb += 4 * kPW * PPW) {
+            u32x4 kv4[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int t = tb + u * kPW * PPW + rin;
+                const int tr = t < pos ? t : tl;   // a row in the cache (row pos is not read)
+                kv4[u] = ((const SH_GLOBAL u32x4 *)(kc + (lbase + (size_t)tr * p.kvdim) * S::EB))[sl];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (tb + u * kPW * PPW > pos) continue;   // uniform over the wave
+                const int t = tb + u * kPW * PPW + rin;
+                float kf[EPC];
+                kv_unpack16<KVT>(kv4[u], kf);
+                if (t == pos) {
+#pragma unroll
+                    for (int q = 0; q < EPC; q++) kf[q] = kpos[q];
+                }
+                score_row(kf, t, t <= pos);
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) {
+        const float m = wmax<64>(mx[h]);
+        if (lane == 0 && h < group) redf[wave * GROUP + h] = m;
+    }
+    lds_barrier();
+    // softmax (infer.go:328-345) on every wave: unnormalised exp terms and their sums
+    float gmx[GROUP], sum[GROUP];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) {
+        gmx[h] = -INFINITY;
+        sum[h] = 0.f;
+        if (h < group)
+            for (int w = 0; w < kPW; w++) gmx[h] = fmaxf(gmx[h], redf[w * GROUP + h]);
+    }
+    for (int t = tid; t <= pos; t += kPB) {
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            if (h >= group) continue;
+            const float ev = expf(sc[h * ms + t] - gmx[h]);
+            sc[h * ms + t] = ev;
+            sum[h] += ev;
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) {
+        const float sw = wsum<64>(sum[h]);
+        if (lane == 0 && h < group) redf[(kPW + wave) * GROUP + h] = sw;
+    }
+    lds_barrier();
+    // P.V (infer.go:290-297): thread (position group tg, dim vi), partials through LDS; the
+    // LDS rows are read four at a time (clamped indices, zero weights past the end), so the
+    // reads of a batch are in flight together
+    const int vi = tid % hd, tg = tid / hd;
+    float acc[GROUP];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) acc[h] = 0.f;
+    for (int t = tg; t <= tl; t += 4 * ngr) {
+        float vv[4], pw[GROUP][4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int tt = t + u * ngr;
+            const int tc = tt <= tl ? tt : tl;
+            vv[u] = kv_get<KVT>(vst + (size_t)tc * S::RB, vi);
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) {
+                const float w = sc[h * ms + tc];
+                pw[h][u] = tt <= tl ? w : 0.f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) acc[h] = fmaf(pw[h][u], vv[u], acc[h]);
+    }
+    // rows beyond the LDS stage: cache reads eight at a time (row pos from the staged v)
+    for (int t = tl + 1 + ((tg - (tl + 1) % ngr + ngr) % ngr); t <= pos; t += 8 * ngr) {
+        float vc[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int tt = t + u * ngr;
+            vc[u] = kv_ld<KVT>(p.vcache, lbase + (size_t)(tt < pos ? tt : tl) * p.kvdim + vi);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int tt = t + u * ngr;
+            if (tt > pos) continue;
+            const float vv = tt == pos ? vs[vi] : vc[u];
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) acc[h] = fmaf(sc[h * ms + tt], vv, acc[h]);
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) part[(h * ngr + tg) * hd + vi] = acc[h];
+    lds_barrier();
+    for (int k = tid; k < group * hd; k += kPB) {
+        const int h = k / hd, ii = k % hd;
+        float tot = 0.f, o = 0.f;
+        for (int w = 0; w < kPW; w++) tot += redf[(kPW + w) * GROUP + h];
+        for (int r = 0; r < ngr; r++) o += part[(h * ngr + r) * hd + ii];
+        ll_put(p.ll_att + (size_t)(g * group + h) * hd + ii, o / tot, e);
+    }
+    return true;
+}
+
 // Cross-group sum: lanes l, l + N, l + 2N, ... (N = 4, 8, 16, 32) added, the result the same
 // on all of them (every step adds two values equal on both partners). Within a 16-lane row
 // the groups are combined by rotations (row_ror:8, then row_ror:4: the sum over all rotations
@@ -1232,7 +1475,7 @@ __device__ __forceinline__ bool attn_stage_wave(const PParams &p, int l, int g, 
             for (int k = 0; k < KW; k++) v[k] = ll_get(src[k]);
         }
     }
-    if (tin && wave == 0) *tin = wall_clock64();
+    if (__builtin_expect(tin != nullptr, 0) && wave == 0) *tin = wall_clock64();
     float mw[GROUP], lw[GROUP], acc[GROUP][EPC];
 #pragma unroll
     for (int h = 0; h < GROUP; h++) {
@@ -1490,7 +1733,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     const int L = p.L;
     const int n_stamps = 5 * L + 3;
     int tok_next = 0;
-    if (p.fail_mode) {
+    if (__builtin_expect(p.fail_mode != 0, 0)) {
         if (threadIdx.x == 0) __hip_atomic_fetch_max(p.err, p.fail_mode, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
@@ -1523,12 +1766,12 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
         long long *tr = p.trace + (size_t)blockIdx.x * 2 * n_stamps;
         int ts = 0;
         auto stamp = [&]() {
-            if (tracing) tr[ts] = wall_clock64();
+            if (__builtin_expect(tracing, 0)) tr[ts] = wall_clock64();
             ts++;
         };
         // input ready for the stage whose end stamp comes next
         auto stamp_in = [&]() {
-            if (tracing) tr[n_stamps + ts] = wall_clock64();
+            if (__builtin_expect(tracing, 0)) tr[n_stamps + ts] = wall_clock64();
         };
         stamp();
         const int tok = pos < p.n_prompt ? p.tokens[pos] : tok_next;
@@ -1561,21 +1804,28 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 if ((r = stage_poll<LD, CD, WT, true>(p, p.own[0], p.qkv_rows, p.D, E_STORE, io, xs, xq, red, okw, c,
                         [&](const StageCtx &cc) { tile_load<LD, CD, WT, 2>(t, cc, Lp.wqkv, p.D); })) < 0)
                     return false;
-                if (r) stamp_in();
-                if (r) stage_compute<LD, CD, WT, 2>(p, Lp.wqkv, Lp.s_qkv, p.D, E_STORE, io, xs, xq, ostage, bv, bi, c, t);
-                else settle_loads();
+                if (r) {
+                    stamp_in();
+                    stage_compute<LD, CD, WT, 2>(p, Lp.wqkv, Lp.s_qkv, p.D, E_STORE, io, xs, xq, ostage, bv, bi, c, t);
+                } else {
+                    settle_loads();
+                }
             }
             stamp();
             // attention
             if ((int)blockIdx.x < p.KVH) {
                 long long *tin = tracing ? tr + n_stamps + ts : nullptr;
                 bool aok;
+                // (each instance compiles only the forms its shapes can take: a kernel's register
+                // allocation is the largest any of its paths needs)
                 if constexpr (WT == SH_DTYPE_W8A8)
                     aok = attn_stage<KVT, HD, true>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf, tin);
+                else if constexpr (HD == 128)   // the 128-dim-head shape runs two q heads per kv head only
+                    aok = attn_stage_fast<KVT, HD, 2>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf, tin);
                 else if (p.H == p.KVH)
                     aok = attn_stage_wave<KVT, HD, 1>(p, l, blockIdx.x, pos, e, part, okw, kvlds, tin);
                 else
-                    aok = attn_stage_wave<KVT, HD, 2>(p, l, blockIdx.x, pos, e, part, okw, kvlds, tin);
+                    aok = attn_stage_fast<KVT, HD, 2>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf, tin);
                 if (!aok) return false;
             }
             stamp();
@@ -1597,9 +1847,12 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 if ((r = stage_poll<LQ, CQ, WT, false>(p, p.own[1], p.D, p.qdim, E_RESID, io, xs, xq, red, okw, c,
                         [&](const StageCtx &cc) { tile_load<LQ, CQ, WT, 1>(t, cc, Lp.wo, p.qdim); })) < 0)
                     return false;
-                if (r) stamp_in();
-                if (r) stage_compute<LQ, CQ, WT, 1>(p, Lp.wo, Lp.s_o, p.qdim, E_RESID, io, xs, xq, ostage, bv, bi, c, t);
-                else settle_loads();
+                if (r) {
+                    stamp_in();
+                    stage_compute<LQ, CQ, WT, 1>(p, Lp.wo, Lp.s_o, p.qdim, E_RESID, io, xs, xq, ostage, bv, bi, c, t);
+                } else {
+                    settle_loads();
+                }
             }
             stamp();
             // w1/w3 + silu gate
@@ -1618,9 +1871,12 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 if ((r = stage_poll<LD, CD, WT, true>(p, p.own[2], 2 * p.F, p.D, E_GATE, io, xs, xq, red, okw, c,
                         [&](const StageCtx &cc) { tile_load<LD, CD, WT, 2>(t, cc, Lp.w13, p.D); })) < 0)
                     return false;
-                if (r) stamp_in();
-                if (r) stage_compute<LD, CD, WT, 2>(p, Lp.w13, Lp.s_13, p.D, E_GATE, io, xs, xq, ostage, bv, bi, c, t);
-                else settle_loads();
+                if (r) {
+                    stamp_in();
+                    stage_compute<LD, CD, WT, 2>(p, Lp.w13, Lp.s_13, p.D, E_GATE, io, xs, xq, ostage, bv, bi, c, t);
+                } else {
+                    settle_loads();
+                }
             }
             stamp();
             // w2 + residual
@@ -1643,9 +1899,12 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 if ((r = stage_poll<LF, CF, WT, false>(p, p.own[3], p.D, p.F, E_RESID, io, xs, xq, red, okw, c,
                         [&](const StageCtx &cc) { tile_load<LF, CF, WT, 1>(t, cc, Lp.w2, p.F); })) < 0)
                     return false;
-                if (r) stamp_in();
-                if (r) stage_compute<LF, CF, WT, 1>(p, Lp.w2, Lp.s_2, p.F, E_RESID, io, xs, xq, ostage, bv, bi, c, t);
-                else settle_loads();
+                if (r) {
+                    stamp_in();
+                    stage_compute<LF, CF, WT, 1>(p, Lp.w2, Lp.s_2, p.F, E_RESID, io, xs, xq, ostage, bv, bi, c, t);
+                } else {
+                    settle_loads();
+                }
             }
             stamp();
             return true;
@@ -1806,6 +2065,7 @@ bool persistent_supported(const sh_model *m) {
     const int group = c.n_heads / c.n_kv_heads;
     if (!pick_persistent(m->dtype, c.kv_dtype, c.dim, m->qdim, c.hidden, c.head_dim)) return false;
     if (group > kMaxGroup || group * c.max_seq > kScores || c.head_dim > 256) return false;
+    if (c.head_dim == 128 && m->dtype != SH_DTYPE_W8A8 && group != 2) return false;   // the one form compiled
     // staged input plus the residual rows polled with it
     if (c.dim + kMaxRes > kXs || m->qdim + kMaxRes > kXs || c.hidden + kMaxRes > kXs) return false;
     if (kPB % c.head_dim) return false;
