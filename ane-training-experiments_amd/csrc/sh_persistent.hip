@@ -1418,7 +1418,8 @@ __device__ __forceinline__ float gmax(float v) {
 //    out = sum_w e^(m_w - M) o_w / sum_w e^(m_w - M) l_w.
 template <int KVT, int HD, int GROUP>
 __device__ __forceinline__ bool attn_stage_wave(const PParams &p, int l, int g, int pos, uint32_t e,
-                                                float *wst, int *okw, uint8_t *kvlds, long long *tin) {
+                                                float *wst, float *mls, int *okw, uint8_t *kvlds,
+                                                long long *tin) {
     using S = KvStage<KVT, HD>;
     constexpr int LPK = S::RB / 16, EPC = 16 / S::EB, PPW = 64 / LPK;
     constexpr int NW = (GROUP + 2) * HD;              // q heads, k, v words
@@ -1662,7 +1663,9 @@ __device__ __forceinline__ bool attn_stage_wave(const PParams &p, int l, int g, 
 #pragma unroll
             for (int e2 = 0; e2 < EPC; e2++) acc[h][e2] = gsum<LPK>(acc[h][e2] * f);
         }
-        // into the wave's region (its q|k|v copies were read above): P.V, then max and sum
+        // P.V into the wave's region (its q|k|v copies were read above); the wave's maximum
+        // and sum into mls, [head][max | sum][wave], so the combine reads them in a few
+        // vector reads
         if (r == 0) {
 #pragma unroll
             for (int h = 0; h < GROUP; h++)
@@ -1672,8 +1675,8 @@ __device__ __forceinline__ bool attn_stage_wave(const PParams &p, int l, int g, 
         if (lane == 0) {
 #pragma unroll
             for (int h = 0; h < GROUP; h++) {
-                wr[GROUP * HD + h] = mw[h];
-                wr[GROUP * HD + GROUP + h] = lw[h];
+                mls[(2 * h) * kPW + wave] = mw[h];
+                mls[(2 * h + 1) * kPW + wave] = lw[h];
             }
         }
     }
@@ -1683,20 +1686,28 @@ __device__ __forceinline__ bool attn_stage_wave(const PParams &p, int l, int g, 
 #pragma unroll
     for (int w = 0; w < kPW; w++) all_ok = all_ok && okw[w];
     if (!all_ok) return false;
-    // combine the waves: thread (h, d)
+    // combine the waves: thread (h, d), every LDS read issued before the first is used (wave
+    // 0 holds row 0, so the maximum M is finite; a wave without rows weighs exp2(-inf) = 0)
     for (int k = tid; k < GROUP * HD; k += kPB) {
         const int h = k / HD;
-        float M = -INFINITY;
+        float mv[kPW], lv[kPW], ov[kPW];
 #pragma unroll
-        for (int w = 0; w < kPW; w++) M = fmaxf(M, wst[w * WREG + GROUP * HD + h]);
+        for (int w = 0; w < kPW; w++) {
+            mv[w] = mls[(2 * h) * kPW + w];
+            lv[w] = mls[(2 * h + 1) * kPW + w];
+            ov[w] = wst[w * WREG + k];
+        }
+        float M = mv[0];
+#pragma unroll
+        for (int w = 1; w < kPW; w++) M = fmaxf(M, mv[w]);
         float tot = 0.f, o = 0.f;
 #pragma unroll
         for (int w = 0; w < kPW; w++) {
-            const float f = __builtin_amdgcn_exp2f(wst[w * WREG + GROUP * HD + h] - M);
-            tot = fmaf(f, wst[w * WREG + GROUP * HD + GROUP + h], tot);
-            o = fmaf(f, wst[w * WREG + k], o);
+            const float f = __builtin_amdgcn_exp2f(mv[w] - M);
+            tot = fmaf(f, lv[w], tot);
+            o = fmaf(f, ov[w], o);
         }
-        ll_put(p.ll_att + (size_t)g * GROUP * HD + k, o / tot, e);
+        ll_put(p.ll_att + (size_t)g * GROUP * HD + k, o * __builtin_amdgcn_rcpf(tot), e);
     }
     return true;
 }
@@ -1726,7 +1737,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     __shared__ double red[kPW];
     __shared__ int okw[kPW];
     __shared__ float ostage[kMaxPer];   // a GEMV stage's output block, before its stores
-    __shared__ float redf[2 * kPW * kMaxGroup];
+    __shared__ __attribute__((aligned(16))) float redf[2 * kPW * kMaxGroup];
     __shared__ ArgmaxPartial cand[kPW];
     __shared__ int next_tok;
 
@@ -1823,7 +1834,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 else if constexpr (HD == 128)   // the 128-dim-head shape runs two q heads per kv head only
                     aok = attn_stage_fast<KVT, HD, 2>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf, tin);
                 else if (p.H == p.KVH)
-                    aok = attn_stage_wave<KVT, HD, 1>(p, l, blockIdx.x, pos, e, part, okw, kvlds, tin);
+                    aok = attn_stage_wave<KVT, HD, 1>(p, l, blockIdx.x, pos, e, part, redf, okw, kvlds, tin);
                 else
                     aok = attn_stage_fast<KVT, HD, 2>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf, tin);
                 if (!aok) return false;
