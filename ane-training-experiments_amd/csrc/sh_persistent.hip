@@ -1132,6 +1132,224 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
 }
 
 
+// attn_stage<KVT, 64, true> for one q head per kv head (the Stories110M W8A8 model): every
+// float operation, and its order, as there; what moves is which wave does it and how often
+// the workgroup waits. A 64-dim head is one wave wide, so wave 0 polls q and k and wave 1
+// polls v (no workgroup barrier around the poll); wave 0 applies the QK-norm (float64 sums
+// over the wave) and RoPE (the two elements of a pair sit in adjacent lanes, swapped by DPP),
+// appends k and wave 1 appends v. One barrier, the scores (one thread per position, as
+// there), a second barrier; then wave 0 alone runs the softmax and P.V, so nothing waits
+// between them, and P.V issues the LDS reads of its next 8 positions before it adds the
+// current 8 (the adds stay in position order). The closing barrier keeps the other waves
+// from the next layer's cache prefetch into the rows P.V reads; they have nothing else to
+// do until the head's output is out.
+template <int KVT, int HD>
+__device__ __forceinline__ void attn_exact1_tail(const PParams &p, int g, int pos, uint32_t e, size_t lbase,
+                                                 float *qs, float *sc, const SH_LDS uint8_t *vst);
+template <int KVT, int HD>
+__device__ __forceinline__ bool attn_stage_exact1(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
+                                                  float *sc, uint8_t *kvlds, int *okw, long long *tin) {
+    static_assert(HD == 64, "one wave per head vector");
+    using S = KvStage<KVT, HD>;
+    constexpr int NCH = S::RB / 16, EPC = 16 / S::EB;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const LayerPtrs Lp = layer_ptrs(p.layers, l);
+    const size_t lbase = (size_t)l * p.max_seq * p.kvdim + (size_t)g * HD;
+    SH_LDS uint8_t *kst = (SH_LDS uint8_t *)kvlds;
+    SH_LDS uint8_t *vst = kst + (size_t)S::ROWS * S::RB;
+    const SH_LDS float *qsl = (const SH_LDS float *)qs;
+    float *ks = qs + HD, *vs = qs + 2 * HD;
+    bool ok = true;
+    if (wave <= 1) {
+        // wave 0: q and k words; wave 1: v
+        const uint64_t *sq = p.ll_qkv + (wave == 0 ? (size_t)g * HD : (size_t)p.qdim + p.kvdim + (size_t)g * HD) + lane;
+        const uint64_t *sk = p.ll_qkv + (size_t)p.qdim + (size_t)g * HD + lane;
+        // RoPE factors of this lane's pair and the QK-norm gains, before the poll
+        const int half = HD / 2, pi = lane >> 1;
+        const float rc = p.rope_cos[pos * half + pi], rs = p.rope_sin[pos * half + pi];
+        const float gq = p.qk_norm ? Lp.q_norm[lane] : 1.f, gk = p.qk_norm ? Lp.k_norm[lane] : 1.f;
+        uint64_t a = ll_get(sq), b = wave == 0 ? ll_get(sk) : ((uint64_t)e << 32);
+        WaitBound wb;
+        while (!__all((uint32_t)(a >> 32) == e && (uint32_t)(b >> 32) == e)) {
+            if (!wb.more(p)) {
+                ok = false;
+                break;
+            }
+            a = ll_get(sq);
+            if (wave == 0) b = ll_get(sk);
+        }
+        if (__builtin_expect(tin != nullptr, 0) && tid == 0) *tin = wall_clock64();
+        float x = __uint_as_float((uint32_t)a), y = __uint_as_float((uint32_t)b);
+        // the cached rows of this wave's share have landed (waited for before the append's
+        // stores: the counter would otherwise also wait for their write-back)
+        __builtin_amdgcn_s_waitcnt(0);
+        if (ok && wave == 0) {
+            // per-head RMSNorm (float64 sum of squares), then RoPE (infer.go:247-265)
+            auto norm_rope = [&](float v, float gn) {
+                if (p.qk_norm) {
+                    const double ss = wsum_d64((double)v * (double)v);
+                    const float rr = (float)(1.0 / sqrt(ss / (double)HD + p.qk_eps));
+                    v = v * rr * gn;
+                }
+                const float o = __uint_as_float(dpp_u<kDppXor1>(__float_as_uint(v)));   // the pair's other element
+                const float ev = (lane & 1) ? o : v, ov = (lane & 1) ? v : o;
+                return (lane & 1) ? __fadd_rn(__fmul_rn(ev, rs), __fmul_rn(ov, rc))
+                                  : __fsub_rn(__fmul_rn(ev, rc), __fmul_rn(ov, rs));
+            };
+            qs[lane] = norm_rope(x, gq);
+            const float kr = kv_rnd<KVT>(norm_rope(y, gk));
+            ks[lane] = kr;
+            kv_st<KVT>(p.kcache, lbase + (size_t)pos * p.kvdim + lane, kr);
+            // K rows sit in the swizzled chunk order (attn_prefetch<..., true>)
+            if (pos < S::ROWS) kv_put<KVT>(kst + (size_t)pos * S::RB, ((lane / EPC) ^ (pos & (NCH - 1))) * EPC + lane % EPC, kr);
+        } else if (ok) {
+            const float vr = kv_rnd<KVT>(x);
+            vs[lane] = vr;
+            kv_st<KVT>(p.vcache, lbase + (size_t)pos * p.kvdim + lane, vr);
+            if (pos < S::ROWS) kv_put<KVT>(vst + (size_t)pos * S::RB, lane, vr);
+        }
+        if (lane == 0) okw[wave] = __all(ok);
+    } else {
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's share of the cached rows has landed
+    }
+    lds_barrier();
+    if (!(okw[0] && okw[1])) return false;
+    // scores (infer.go:280-288): one thread per position, the row's chunks in order,
+    // requested eight at a time ahead of their adds; q[i] reaches every lane of the wave from
+    // lane i's register (readlane: a scalar operand, no LDS read per element). readlane reads
+    // lanes whatever the branch, so q is loaded in every lane before anything diverges, and a
+    // wave takes the LDS path only when all of its positions are LDS rows (lanes past pos
+    // score row pos and store nothing); a wave reaching past them reads every row of its
+    // positions from the cache, lane by lane.
+    float qme = qsl[lane];
+    __asm__ __volatile__("" : "+v"(qme));
+    for (int t0 = wave * 64; t0 <= pos; t0 += kPB) {
+        const int t = t0 + lane;
+        float d = 0.f;
+        if ((t0 + 63 < pos ? t0 + 63 : pos) < S::ROWS) {
+            const int te = t < pos ? t : pos;
+            const SH_LDS u32x4 *row = (const SH_LDS u32x4 *)(kst + (size_t)te * S::RB);
+            const int swz = te & (NCH - 1);   // chunk c of the row sits in slot c ^ swz
+            constexpr int R = NCH < 8 ? NCH : 8;   // chunks requested at once (registers)
+#pragma unroll
+            for (int c0 = 0; c0 < NCH; c0 += R) {
+                u32x4 kc[R];
+#pragma unroll
+                for (int c = 0; c < R; c++) kc[c] = row[(c0 + c) ^ swz];
+#pragma unroll
+                for (int c = 0; c < R; c++) {
+                    float kf[EPC];
+                    kv_unpack16<KVT>(kc[c], kf);
+#pragma unroll
+                    for (int k = 0; k < EPC; k++) {
+                        const float qi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qme), (c0 + c) * EPC + k));
+                        d = __fadd_rn(d, __fmul_rn(qi, kf[k]));
+                    }
+                }
+            }
+        } else if (t <= pos) {
+            const size_t rb = lbase + (size_t)t * p.kvdim;
+#pragma unroll 8
+            for (int k = 0; k < HD; k++) {
+                const float kv = t == pos ? ks[k] : kv_ld<KVT>(p.kcache, rb + k);
+                d = __fadd_rn(d, __fmul_rn(qs[k], kv));
+            }
+        }
+        if (t <= pos) sc[t] = __fmul_rn(d, p.inv_sqrt_hd);
+    }
+    lds_barrier();
+    if (wave == 0) attn_exact1_tail<KVT, HD>(p, g, pos, e, lbase, qs, sc, vst);
+    lds_barrier();
+    return true;
+}
+
+// attn_stage_exact1's wave 0 after the scores: softmax, P.V and the head's output words.
+template <int KVT, int HD>
+__device__ __forceinline__ void attn_exact1_tail(const PParams &p, int g, int pos, uint32_t e, size_t lbase,
+                                                 float *qs, float *sc, const SH_LDS uint8_t *vst) {
+    using S = KvStage<KVT, HD>;
+    const int lane = threadIdx.x & 63;
+    const float *vs = qs + 2 * HD;
+    // infer.go:328-345 softmaxPrefix, as attn_stage computes it: float max, float64 exp
+    // terms, a float64 sum per lane in position order, then over the lanes; the first four
+    // positions of a lane are read at once and their exp terms computed side by side
+    constexpr int kU = 4;
+    float sv[kU];
+#pragma unroll
+    for (int k = 0; k < kU; k++) sv[k] = lane + 64 * k <= pos ? sc[lane + 64 * k] : -INFINITY;
+    float mx = sv[0];
+#pragma unroll
+    for (int k = 1; k < kU; k++) mx = fmaxf(mx, sv[k]);
+    for (int t = lane + 64 * kU; t <= pos; t += 64) mx = fmaxf(mx, sc[t]);
+    mx = wmax<64>(mx);
+    float ev[kU];
+#pragma unroll
+    for (int k = 0; k < kU; k++) ev[k] = (float)exp((double)(sv[k] - mx));
+    double sum = 0;
+#pragma unroll
+    for (int k = 0; k < kU; k++)
+        if (lane + 64 * k <= pos) sum += (double)ev[k];
+    for (int t = lane + 64 * kU; t <= pos; t += 64) {
+        const float x = (float)exp((double)(sc[t] - mx));
+        sc[t] = x;
+        sum += (double)x;
+    }
+    sum = wsum_d64(sum);
+    const float inv = (float)(1.0 / sum);
+#pragma unroll
+    for (int k = 0; k < kU; k++)
+        if (lane + 64 * k <= pos) sc[lane + 64 * k] = ev[k] * inv;
+    for (int t = lane + 64 * kU; t <= pos; t += 64) sc[t] = sc[t] * inv;
+    __asm__ __volatile__("s_waitcnt lgkmcnt(0)" ::: "memory");   // every lane's p[t] in LDS
+    // P.V (infer.go:290-297): lane i sums p[t] * v[t][i] over t = 0..pos in order. The reads
+    // of the next 8 positions (p as two broadcast reads, V one element per lane and row) are
+    // issued before the current 8 are added, into two register sets used in turn
+    const SH_LDS float *phl = (const SH_LDS float *)sc;
+    const SH_LDS uint8_t *vcol = vst + (size_t)lane * S::EB;
+    const int tl = pos < S::ROWS ? pos : S::ROWS - 1;
+    constexpr int PB = 8;
+    const int nfull = (tl + 1) / PB;
+    float acc = 0.f;
+    struct Chunk {
+        f32x4 p[PB / 4];
+        float v[PB];
+    };
+    auto cload = [&](int t0, Chunk &ch) {
+#pragma unroll
+        for (int j = 0; j < PB / 4; j++) ch.p[j] = ((const SH_LDS f32x4 *)(phl + t0))[j];
+#pragma unroll
+        for (int u = 0; u < PB; u++) ch.v[u] = kv_get<KVT>(vcol + (size_t)(t0 + u) * S::RB, 0);
+    };
+    auto cmac = [&](const Chunk &ch) {
+#pragma unroll
+        for (int u = 0; u < PB; u++) {
+            const f32x4 q = ch.p[u / 4];
+            const float pt = u % 4 == 0 ? q.x : u % 4 == 1 ? q.y : u % 4 == 2 ? q.z : q.w;
+            acc = __fadd_rn(acc, __fmul_rn(pt, ch.v[u]));
+        }
+    };
+    const int tf = nfull * PB;
+    if (tf > 0) {
+        Chunk ca, cb;
+        cload(0, ca);
+        int t0 = 0;
+        for (; t0 + 2 * PB <= tf; t0 += 2 * PB) {
+            cload(t0 + PB, cb);
+            cmac(ca);
+            cload(min(t0 + 2 * PB, tf - PB), ca);   // the last trip re-reads the last chunk
+            cmac(cb);
+        }
+        if (t0 < tf) cmac(ca);
+    }
+    for (int t = nfull * PB; t <= tl; t++) acc = __fadd_rn(acc, __fmul_rn(phl[t], kv_get<KVT>(vcol + (size_t)t * S::RB, 0)));
+#pragma unroll 8
+    for (int t = tl + 1; t <= pos; t++) {
+        const float vv = t == pos ? vs[lane] : kv_ld<KVT>(p.vcache, lbase + (size_t)t * p.kvdim + lane);
+        acc = __fadd_rn(acc, __fmul_rn(sc[t], vv));
+    }
+    ll_put(p.ll_att + (size_t)g * HD + lane, acc, e);
+}
+
 // Attention for the fp16 / bf16 models with two q heads per kv head (the Qwen3 shape: 128-dim
 // heads; attn_stage_wave serves one q head per kv head, the W8A8 model attn_stage<..., true>):
 // the same mathematics in fewer dependent steps, rounded differently in the last bits. (The
@@ -1731,7 +1949,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     __shared__ float xs[kXs];
     __shared__ __attribute__((aligned(16))) uint32_t xq[WT == SH_DTYPE_W8A8 ? kXs / 4 : 1];
     __shared__ __attribute__((aligned(16))) float qs[(kMaxGroup + 2) * 256];   // q heads, k, v
-    __shared__ float sc[kScores];
+    __shared__ __attribute__((aligned(16))) float sc[kScores];
     __shared__ float part[kPW * kMaxGroup * 256];
     __shared__ __attribute__((aligned(16))) uint8_t kvlds[kKvStage];
     __shared__ double red[kPW];
@@ -1829,7 +2047,11 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 bool aok;
                 // (each instance compiles only the forms its shapes can take: a kernel's register
                 // allocation is the largest any of its paths needs)
-                if constexpr (WT == SH_DTYPE_W8A8)
+                if constexpr (WT == SH_DTYPE_W8A8 && HD == 64)
+                    aok = p.H == p.KVH
+                              ? attn_stage_exact1<KVT, HD>(p, l, blockIdx.x, pos, e, qs, sc, kvlds, okw, tin)
+                              : attn_stage<KVT, HD, true>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf, tin);
+                else if constexpr (WT == SH_DTYPE_W8A8)
                     aok = attn_stage<KVT, HD, true>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf, tin);
                 else if constexpr (HD == 128)   // the 128-dim-head shape runs two q heads per kv head only
                     aok = attn_stage_fast<KVT, HD, 2>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf, tin);
