@@ -960,7 +960,12 @@ int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *l
         m->pf_ready = false;
         hipGraph_t g = nullptr;
         if (!hip_ok(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal), "capture")) return -1;
+        // EvalLogits, whose bar is the logits: the fp16 products take the activations as one
+        // fp16 plane (an 11-bit significand); bf16 keeps the hi/lo pair, whose one plane would
+        // carry 8 bits. Forwards that fill a decode cache keep the pair.
+        m->pf_one_plane = m->dtype == SH_DTYPE_F16;
         const hipError_t e2 = enqueue_prefill(m, seq, seq, true, false);
+        m->pf_one_plane = false;
         const hipError_t e3 = hipStreamEndCapture(m->stream, &g);
         if (!hip_ok(e2, "prefill") || !hip_ok(e3, "end capture")) {
             if (g) (void)hipGraphDestroy(g);

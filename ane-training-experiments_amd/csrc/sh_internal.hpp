@@ -166,6 +166,7 @@ struct sh_model {
     // sh_prefill_logits: the whole forward captured for pf_graph_seq rows (its kernels point
     // into the prefill scratch, so reallocating that drops it)
     hipGraphExec_t pf_exec;
+    bool pf_one_plane;  // the full-sequence products take A's hi plane only (EvalLogits, fp16)
     bool pf_ready;
     int pf_graph_seq;
 };

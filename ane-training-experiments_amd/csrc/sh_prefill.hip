@@ -172,6 +172,7 @@ struct GemmArgs {
     int dt;
     int decode_forms;    // G_GATE: 1 = infer.go:324-326 silu, 0 = accel_other.go:128-133
     int partial_only;    // skinny GEMM: always leave K-range partials, no epilogue
+    int one_plane;       // pipelined fp16 GEMMs: A's hi plane only (lo neither read nor used)
     // W8A8 models: B holds int8 rows with fp32 row scales sw [N]; A is the fp32 operand
     // [M, K], which the product quantizes per row into a8 [M, K] with scales sa [M] first
     const float *sw;
@@ -477,14 +478,14 @@ constexpr int vm_wait_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4)
 // LDS banks. Workgroup tile BM x BN of 2 x 2 waves, each FM x FN 16 x 16 blocks; the hi and
 // lo products accumulate separately (independent MFMA chains) and are added at the end.
 // Needs N % BN == 0, kc % BK == 0 and kc / BK >= NS - 1; rows past M re-read row M - 1.
-template <int DT, int BM, int BN, int BK, int NS>
+template <int DT, int BM, int BN, int BK, int NS, int PL = 2>
 __device__ __forceinline__ void pipe_product(const GemmArgs &g, int kc, uint8_t *lds,
                                              f32x4 (&acc)[BM / 32][BN / 32]) {
     constexpr int FM = BM / 32, FN = BN / 32;
     constexpr int CPR = BK / 8;                 // 16-byte chunks per tile row
     constexpr int RB = BK * 2;                  // bytes per tile row
     constexpr int RPI = 1024 / RB;              // tile rows per wave instruction
-    constexpr int ROWS = 2 * BM + BN;
+    constexpr int ROWS = PL * BM + BN;          // A hi (and A lo) rows, then W rows
     constexpr int IPW = ROWS / RPI / 4;         // wave instructions per step, per wave
     constexpr int SB = ROWS * RB;               // bytes per ring slot
     static_assert(kT == 256 && ROWS % (4 * RPI) == 0 && BM % RPI == 0 && BN % RPI == 0 && CPR >= 4,
@@ -503,8 +504,8 @@ __device__ __forceinline__ void pipe_product(const GemmArgs &g, int kc, uint8_t 
         const int c = (lane % CPR) ^ swz(r);
         const uint16_t *p;
         if (r < BM) p = g.A + (size_t)min(m0 + r, g.M - 1) * g.K;
-        else if (r < 2 * BM) p = g.A + lo + (size_t)min(m0 + r - BM, g.M - 1) * g.K;
-        else p = g.B + (size_t)(n0 + r - 2 * BM) * g.K;
+        else if (r < PL * BM) p = g.A + lo + (size_t)min(m0 + r - BM, g.M - 1) * g.K;
+        else p = g.B + (size_t)(n0 + r - PL * BM) * g.K;
         src[i] = p + kbeg + c * 8;
     }
     auto issue = [&](int st) {
@@ -534,21 +535,23 @@ __device__ __forceinline__ void pipe_product(const GemmArgs &g, int kc, uint8_t 
             for (int i = 0; i < FM; i++) {
                 const int r = wm + i * 16 + fr, r2 = BM + r;
                 ah[i] = *(const u32x4 *)(L + r * RB + ((c ^ swz(r)) << 4));
-                al[i] = *(const u32x4 *)(L + r2 * RB + ((c ^ swz(r2)) << 4));
+                if constexpr (PL == 2) al[i] = *(const u32x4 *)(L + r2 * RB + ((c ^ swz(r2)) << 4));
             }
 #pragma unroll
             for (int j = 0; j < FN; j++) {
-                const int r = 2 * BM + wn + j * 16 + fr;
+                const int r = PL * BM + wn + j * 16 + fr;
                 b[j] = *(const u32x4 *)(L + r * RB + ((c ^ swz(r)) << 4));
             }
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int j = 0; j < FN; j++) acc[i][j] = mfma16<DT>(ah[i], b[j], acc[i][j]);
+            if constexpr (PL == 2) {
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+                for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < FN; j++) acl[i][j] = mfma16<DT>(al[i], b[j], acl[i][j]);
+                    for (int j = 0; j < FN; j++) acl[i][j] = mfma16<DT>(al[i], b[j], acl[i][j]);
+            }
         }
     };
 #pragma unroll
@@ -563,17 +566,19 @@ __device__ __forceinline__ void pipe_product(const GemmArgs &g, int kc, uint8_t 
     __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));
     __builtin_amdgcn_s_barrier();
     for (; s < nsteps; s++) compute(s);
+    if constexpr (PL == 2) {
 #pragma unroll
-    for (int i = 0; i < FM; i++)
+        for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] += acl[i][j];
+            for (int j = 0; j < FN; j++) acc[i][j] += acl[i][j];
+    }
 }
 
-template <int DT, int BM, int BN, int BK, int NS>
+template <int DT, int BM, int BN, int BK, int NS, int PL = 2>
 __global__ __launch_bounds__(kT) void k_gemm_pipe(GemmArgs g, float *partial, int kc) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     f32x4 acc[BM / 32][BN / 32];
-    pipe_product<DT, BM, BN, BK, NS>(g, kc, lds, acc);
+    pipe_product<DT, BM, BN, BK, NS, PL>(g, kc, lds, acc);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     tile_out<BM / 32, BN / 32>(g, partial, acc, blockIdx.x * BM + (wave >> 1) * (BM / 2),
                                blockIdx.y * BN + (wave & 1) * (BN / 2), lane);
@@ -864,11 +869,11 @@ __global__ __launch_bounds__(kT) void k_qk_rope(const float *qkv, QkRopeArgs a) 
 // LDS (the ring is free once the product is done); wave w then finishes rows 16w..16w+15
 // with lane = head dim: the QK-norm sum is a butterfly over the wave, the RoPE partner of
 // dim 2p / 2p+1 the neighbouring lane. Saves the separate k_qk_rope launch.
-template <int DT, int KVT>
+template <int DT, int KVT, int PL = 2>
 __global__ __launch_bounds__(kT) void k_gemm_pipe_qkv64(GemmArgs g, QkRopeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     f32x4 acc[2][2];
-    pipe_product<DT, 64, 64, 64, 6>(g, g.K, lds, acc);
+    pipe_product<DT, 64, 64, 64, 6, PL>(g, g.K, lds, acc);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
     __syncthreads();   // every wave is done reading the ring
@@ -2435,7 +2440,11 @@ hipError_t gemm_pipe_setup_once() {
                              (const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16>,
                              (const void *)k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F32>,
                              (const void *)k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F16>,
-                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_BF16>};
+                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_BF16>,
+                             (const void *)k_gemm_pipe<SH_DTYPE_F16, 64, 64, 64, 6, 1>,
+                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32, 1>,
+                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F16, 1>,
+                             (const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16, 1>};
         for (const void *f : fns) {
             const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPipeBigLds);
             if (e != hipSuccess) return e;
@@ -2476,13 +2485,16 @@ hipError_t gemm(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipS
     if (p.kind == GK_PIPE64 || p.kind == GK_PIPE32) {
         hipError_t e0 = gemm_pipe_setup_once();
         if (e0 != hipSuccess) return e0;
+        const bool one = g.one_plane && !bf;
         if (p.kind == GK_PIPE64) {
             const dim3 grid((g.M + 63) / 64, g.N / 64, p.ranges);
             if (bf) hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_BF16, 64, 64, 64, 6>), grid, dim3(kT), kPipeBigLds, s, g, partial, p.kc);
+            else if (one) hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_F16, 64, 64, 64, 6, 1>), grid, dim3(kT), kPipeBigLds, s, g, partial, p.kc);
             else hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_F16, 64, 64, 64, 6>), grid, dim3(kT), kPipeBigLds, s, g, partial, p.kc);
         } else {
             const dim3 grid((g.M + 31) / 32, g.N / 32, p.ranges);
             if (bf) hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_BF16, 32, 32, 64, 4>), grid, dim3(kT), kPipeSmallLds, s, g, partial, p.kc);
+            else if (one) hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_F16, 32, 32, 64, 4, 1>), grid, dim3(kT), kPipeSmallLds, s, g, partial, p.kc);
             else hipLaunchKernelGGL((k_gemm_pipe<SH_DTYPE_F16, 32, 32, 64, 4>), grid, dim3(kT), kPipeSmallLds, s, g, partial, p.kc);
         }
     } else if (p.kind == GK_BIG) {
@@ -2672,7 +2684,11 @@ hipError_t launch_qkv64(const GemmArgs &g, const QkRopeArgs &a, int kv, hipStrea
     if (e != hipSuccess) return e;
     const dim3 grid((g.M + 63) / 64, g.N / 64);
     const bool bf = g.dt == SH_DTYPE_BF16;
-    if (kv == SH_KV_F32) {
+    if (g.one_plane && !bf) {
+        if (kv == SH_KV_F32) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32, 1>), grid, dim3(kT), kPipeBigLds, s, g, a);
+        else if (kv == SH_KV_F16) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F16, 1>), grid, dim3(kT), kPipeBigLds, s, g, a);
+        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16, 1>), grid, dim3(kT), kPipeBigLds, s, g, a);
+    } else if (kv == SH_KV_F32) {
         if (bf) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F32>), grid, dim3(kT), kPipeBigLds, s, g, a);
         else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32>), grid, dim3(kT), kPipeBigLds, s, g, a);
     } else if (kv == SH_KV_F16) {
@@ -2789,7 +2805,7 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
     int ranges = 1;
     GemmArgs g{};
     g.A = m->pf_xn; g.B = (const uint16_t *)L.wqkv; g.M = S; g.N = m->qkv_rows; g.K = D;
-    g.epi = G_STORE; g.out = m->pf_qkv; g.dt = dt;
+    g.epi = G_STORE; g.out = m->pf_qkv; g.dt = dt; g.one_plane = m->pf_one_plane;
     g.sw = L.s_qkv; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     if (qkv64_fused(m, S)) {
         const QkRopeArgs a = qk_rope_args(m, L, m->pf_rowpos, m->pf_rowseq, m->pf_q, m->pf_k, m->pf_v, l,
@@ -2818,6 +2834,7 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
     g = GemmArgs{};
     g.A = m->pf_att; g.B = (const uint16_t *)L.wo; g.M = S; g.N = D; g.K = m->qdim;
     g.epi = G_RESID; g.out = m->pf_x2; g.resid = m->pf_x; g.alpha = c.residual_scale; g.dt = dt;
+    g.one_plane = m->pf_one_plane;
     g.sw = L.s_o; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;
     if (ranges > 1)
@@ -2830,11 +2847,13 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
     g = GemmArgs{};
     g.A = m->pf_xn; g.B = (const uint16_t *)L.w13; g.M = S; g.N = 2 * F; g.K = D;
     g.epi = G_GATE; g.out16 = m->pf_gate; g.dt = dt; g.decode_forms = fill_kv || dt == SH_DTYPE_W8A8 ? 1 : 0;
+    g.one_plane = m->pf_one_plane;
     g.sw = L.s_13; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s)) != hipSuccess) return e;
     g = GemmArgs{};
     g.A = m->pf_gate; g.B = (const uint16_t *)L.w2; g.M = S; g.N = D; g.K = F;
     g.epi = G_RESID; g.out = m->pf_x; g.resid = m->pf_x2; g.alpha = c.residual_scale; g.dt = dt;
+    g.one_plane = m->pf_one_plane;
     g.sw = L.s_2; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     if (!next_gain) return gemm(g, dt, m->pf_part, m->pf_part_cap, s);
     if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;

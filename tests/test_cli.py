@@ -14,6 +14,7 @@ from helpers import (BLZT_LAYER_ORDER, LLAMA2_ORDER, deepnet_alpha, splitmix64_u
                      write_llama2_bin, write_tokenizer_bin)
 
 CLI = os.path.join(os.path.dirname(sh.LIB_PATH), "stories-generate")
+LOGIT_TOL = 2e-2  # max-abs logits bar
 
 
 def run(*args, check=True):
@@ -282,17 +283,24 @@ def test_cli_ane_decode_matches_window_oracle(tmp_path):
     temp, plen = 0.8, 3
     ids = cli_ids(run("-ane", "-model", path, "-prompt-ids", "5,9,11", "-max-new", "20", "-temperature", temp,
                       "-seq", seq, "-seed", 0).stdout)
+    # The sampler: the oracle's sampleFromLogits on the device's own EvalLogits of every window
+    # of the CLI's stream, with the same draws, gives the CLI's id at every step (EvalLogits
+    # carries fp16 activations, so the oracle's logits alone pin only steps far from a CDF
+    # boundary); those logits are within the bar of the oracle's.
     m = sh.Model(acfg, sh.SH_DTYPE_F16)
     m.upload(w)
-    want, delta = [], 0.0
+    draws = splitmix64_uniforms(42, len(ids) - plen)
+    delta = 0.0
     for k in range(len(ids) - plen):
         window = oracle.fill_decode_window(seq, np.asarray(ids[:plen + k], np.int32))
         lo = oracle.eval_logits_cf(ocfg, ow, window, threads=4)[:, seq - 1]
         lg = m.eval_logits(window)[:, seq - 1]
         delta = max(delta, float(np.max(np.abs(lg - lo))))
-        want.append(lo)
+        idx, _ = oracle.sample_from_logits(lg, temp, float(draws[k]))
+        assert ids[plen + k] == idx, f"-ane step {k}: CLI {ids[plen + k]}, sampler on the device logits {idx}"
     m.close()
-    assert check_sampled_stream(ids, plen, want, temp, 42, delta, "-ane") >= 0.9 * len(want)
+    print(f"-ane sampled: {len(ids) - plen} steps equal; logits within {delta:.2e} of the oracle")
+    assert delta <= LOGIT_TOL
 
 
 @pytest.mark.gpu

@@ -133,9 +133,12 @@ def test_seams_compose_to_eval_logits(gpu):
         x = m.layer_forward_cf(layer, x)
     logits = m.classifier_cf(m.rms_final_cf(x))
     full = m.eval_logits(toks)
-    assert float(np.max(np.abs(logits - full))) <= 1e-4
+    # the seams carry the activations into their products as hi/lo fp16 pairs, EvalLogits
+    # (fp16) as one fp16 plane: the two agree to the plane's rounding, both within the bar
+    assert float(np.max(np.abs(logits - full))) <= 2e-3
     want = oracle.eval_logits_cf(ocfg, ow, toks, threads=THREADS)
     assert float(np.max(np.abs(logits - want))) <= 2e-2
+    assert float(np.max(np.abs(full - want))) <= 2e-2
     m.close()
 
 
