@@ -389,11 +389,11 @@ __global__ __launch_bounds__(kT) void k_gemm_tiled(GemmArgs g, float *partial, i
 // LDS tiles, fragments and epilogue are k_gemm_tiled's. One barrier per step suffices: a
 // buffer is rewritten two steps after it was read, and every wave has passed the barrier
 // between.
-template <int DT, int BM, int BN, int NB>
+template <int DT, int BM, int BN, int NB, int PL = 2>
 __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, int kc) {
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
     constexpr int RS = 80;
-    constexpr int R = 2 * BM + BN;
+    constexpr int R = PL * BM + BN;   // A hi (and A lo) rows, then W rows
     constexpr int PER = R * 4 / kT;
     static_assert(kT == 256 && BM % 64 == 0 && NB % 2 == 0, "64 rows per chunk index; bursts of even length");
     __shared__ __attribute__((aligned(16))) uint8_t lds[2][R * RS];
@@ -420,13 +420,13 @@ __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, i
 #pragma unroll
             for (int j = 0; j < PER; j++) {
                 const int rr = j * 64 + (tid >> 2);
-                if (j * 64 < 2 * BM) {
+                if (j * 64 < PL * BM) {
                     const int m = m0 + (j * 64 < BM ? rr : rr - BM);
                     const uint16_t *src = g.A + (j * 64 < BM ? 0 : lo) + (size_t)min(m, g.M - 1) * g.K + k;
                     const u32x4 v = *(const u32x4 *)src;
                     stage[st][j] = m < g.M ? v : zero;
                 } else {
-                    stage[st][j] = *(const u32x4 *)(g.B + (size_t)(n0 + rr - 2 * BM) * g.K + k);
+                    stage[st][j] = *(const u32x4 *)(g.B + (size_t)(n0 + rr - PL * BM) * g.K + k);
                 }
             }
         }
@@ -441,15 +441,16 @@ __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, i
             __syncthreads();
             u32x4 bfr[FN];
 #pragma unroll
-            for (int j = 0; j < FN; j++) bfr[j] = *(const u32x4 *)(L + (2 * BM + wn + j * 16 + fr) * RS + fc);
+            for (int j = 0; j < FN; j++) bfr[j] = *(const u32x4 *)(L + (PL * BM + wn + j * 16 + fr) * RS + fc);
 #pragma unroll
             for (int i = 0; i < FM; i++) {
                 const u32x4 ah = *(const u32x4 *)(L + (wm + i * 16 + fr) * RS + fc);
-                const u32x4 al = *(const u32x4 *)(L + (BM + wm + i * 16 + fr) * RS + fc);
+                u32x4 al = ah;
+                if constexpr (PL == 2) al = *(const u32x4 *)(L + (BM + wm + i * 16 + fr) * RS + fc);
 #pragma unroll
                 for (int j = 0; j < FN; j++) {
                     acc[i][j] = mfma16<DT>(ah, bfr[j], acc[i][j]);
-                    acc[i][j] = mfma16<DT>(al, bfr[j], acc[i][j]);
+                    if constexpr (PL == 2) acc[i][j] = mfma16<DT>(al, bfr[j], acc[i][j]);
                 }
             }
         }
@@ -1033,7 +1034,7 @@ template <int HD> constexpr size_t attn_lds_bytes() {
     // per wave: K rows (HD*2 + 16 bytes) and V^T rows (BK*2 + 8 bytes), hi and lo planes
     return (size_t)4 * 2 * (attn_bk<HD>() * (HD * 2 + 16) + HD * (attn_bk<HD>() * 2 + 8));
 }
-template <int DT, int HD, bool LO>
+template <int DT, int HD, bool LO, int QP = 2>
 __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const float *kf,
                                                           const float *vf, int S,
                                                           const int32_t *rowpos, int H, int KVH,
@@ -1155,7 +1156,7 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
                 const int off = (16 * j + ql) * KRS + 64 * s + 16 * g4;
                 const u32x4 kh = *(const u32x4 *)&ksl[off];
                 acc = mfma16<DT>(kh, qh[s], acc);
-                acc = mfma16<DT>(kh, qlo[s], acc);
+                if constexpr (QP == 2) acc = mfma16<DT>(kh, qlo[s], acc);
                 if constexpr (LO) acc = mfma16<DT>(*(const u32x4 *)&ksl[KSL + off], qh[s], acc);
             }
             sc[j] = acc;
@@ -1197,7 +1198,7 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
                 const uint2 a0 = *(const uint2 *)&vsl[off], a1 = *(const uint2 *)&vsl[off + 32];
                 const u32x4 vh = u32x4{a0.x, a0.y, a1.x, a1.y};
                 o[i] = mfma16<DT>(vh, ph, o[i]);
-                o[i] = mfma16<DT>(vh, pl, o[i]);
+                if constexpr (QP == 2) o[i] = mfma16<DT>(vh, pl, o[i]);
                 if constexpr (LO) {
                     const uint2 b0 = *(const uint2 *)&vsl[VSL + off], b1 = *(const uint2 *)&vsl[VSL + off + 32];
                     o[i] = mfma16<DT>(u32x4{b0.x, b0.y, b1.x, b1.y}, ph, o[i]);
@@ -2503,6 +2504,7 @@ hipError_t gemm(const GemmArgs &g, int dt, float *partial, size_t part_cap, hipS
         const dim3 grid((g.M + 127) / 128, g.N / 128, p.ranges);
         if (p.kc % 128 == 0) {
             if (bf) hipLaunchKernelGGL((k_gemm_burst<SH_DTYPE_BF16, 128, 128, 4>), grid, dim3(kT), 0, s, g, partial, p.kc);
+            else if (g.one_plane) hipLaunchKernelGGL((k_gemm_burst<SH_DTYPE_F16, 128, 128, 4, 1>), grid, dim3(kT), 0, s, g, partial, p.kc);
             else hipLaunchKernelGGL((k_gemm_burst<SH_DTYPE_F16, 128, 128, 4>), grid, dim3(kT), 0, s, g, partial, p.kc);
         } else {
             if (bf) hipLaunchKernelGGL((k_gemm_tiled<SH_DTYPE_BF16, 128, 128>), grid, dim3(kT), 0, s, g, partial, p.kc);
@@ -2754,7 +2756,19 @@ hipError_t launch_attn_prefill(const sh_model *m, int S, int seg_max, bool fill_
     if (c.head_dim == 32) SH_ATT(DTV, 32, LOV);                                                  \
     else if (c.head_dim == 64) SH_ATT(DTV, 64, LOV);                                             \
     else SH_ATT(DTV, 128, LOV);
-    if (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) {
+    if (m->pf_one_plane && dt == SH_DTYPE_F16 && !wide &&
+        (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128)) {
+        // EvalLogits (fp16): Q, K, V and P as one fp16 plane each
+        if (c.head_dim == 32)
+            hipLaunchKernelGGL((k_attn_prefill_mfma<SH_DTYPE_F16, 32, false, 1>), grid, dim3(kT), 0, s, m->pf_q,
+                               m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
+        else if (c.head_dim == 64)
+            hipLaunchKernelGGL((k_attn_prefill_mfma<SH_DTYPE_F16, 64, false, 1>), grid, dim3(kT), 0, s, m->pf_q,
+                               m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
+        else
+            hipLaunchKernelGGL((k_attn_prefill_mfma<SH_DTYPE_F16, 128, false, 1>), grid, dim3(kT), 0, s, m->pf_q,
+                               m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
+    } else if (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) {
         if (dt == SH_DTYPE_BF16) {
             if (exact) { SH_ATT_HD(SH_DTYPE_BF16, false) } else { SH_ATT_HD(SH_DTYPE_BF16, true) }
         } else {
@@ -2869,7 +2883,7 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
 hipError_t enqueue_classifier(sh_model *m, int S) {
     GemmArgs g{};
     g.A = m->pf_xn; g.B = (const uint16_t *)m->cls; g.M = S; g.N = m->cfg.vocab; g.K = m->cfg.dim;
-    g.epi = G_LOGITS_CF; g.out = m->pf_logits; g.dt = m->dtype;
+    g.epi = G_LOGITS_CF; g.out = m->pf_logits; g.dt = m->dtype; g.one_plane = m->pf_one_plane;
     g.sw = m->s_cls; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     return gemm(g, m->dtype, m->pf_part, m->pf_part_cap, m->stream);
 }
