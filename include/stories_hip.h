@@ -125,9 +125,11 @@ int sh_greedy_decode(sh_model *m, const int32_t *prompt, int32_t n_prompt, int32
 /* (*Engine).EvalLogits (ane/storiesane/engine.go:363-376) = evalLogitsCPUInto
  * (engine.go:804-842): the full causal forward of `seq` tokens (seq <= max_seq), logits
  * channel-first [V, seq] (logits[v*seq + t]). Out-of-range ids give a zero embedding
- * column (cpu.go:41-72). Residual scale = cfg.residual_scale. A W8A8 model runs it on the
- * int8 matrix cores with each token's activations quantized on their own and the decode's
- * float order wherever a value feeds a quantizer, so its logits equal forwardOne's at every
+ * column (cpu.go:41-72). Residual scale = cfg.residual_scale. An fp16 model's matrix
+ * products take the activations as one fp16 plane (the logits agree with the fp32 path to
+ * about 1e-3); bf16 models carry them as a hi/lo pair. A W8A8 model runs it on the int8
+ * matrix cores with each token's activations quantized on their own and the decode's float
+ * order wherever a value feeds a quantizer, so its logits equal forwardOne's at every
  * position. */
 int sh_prefill_logits(sh_model *m, const uint16_t *tokens, int32_t seq, float *logits_cf);
 /* ---- storiesane plugin seams over channel-first data (the _other.go stubs' HIP side) ---- */
