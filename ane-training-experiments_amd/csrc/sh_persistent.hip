@@ -883,23 +883,19 @@ __device__ __forceinline__ void kv_unpack16(const u32x4 &v, float *f) {
     }
 }
 
-// Attention for kv head g (one workgroup) and its `group` query heads (infer.go:273-299).
-// q, k and v arrive through one batched poll; the cached rows were copied into LDS by
-// attn_prefetch, rows beyond the LDS capacity are read from the cache. Softmax: one wave
-// per head.
-// Default order (EXACT = false): scores one thread per position, walking the head in an
-// order rotated by the position so the LDS reads of a wave fall in distinct banks; P.V one
-// thread per (dim, position group), partial sums combined through LDS.
-// EXACT = true keeps the reference's float summation order, each product and sum rounded
-// on its own: a score is the sequential sum over i of q[i]*k[i] (infer.go:284-286), an
-// output element the sequential sum over t of p[t]*v[t][i] (:292-295). The W8A8 model
-// uses it: its activations are re-quantized after attention, and a last-bit difference
-// that moves x/s across a rounding boundary would change an int8 input.
-template <int KVT, int HD, bool EXACT>
+// Attention for kv head g (one workgroup) and its `group` query heads (infer.go:273-299) in
+// the reference's float summation order, each product and sum rounded on its own: a score
+// is the sequential sum over i of q[i]*k[i] (infer.go:284-286), an output element the
+// sequential sum over t of p[t]*v[t][i] (:292-295). The W8A8 model uses it: its activations
+// are re-quantized after attention, and a last-bit difference that moves x/s across a
+// rounding boundary would change an int8 input. q, k and v arrive through one batched poll;
+// the cached rows were copied into LDS by attn_prefetch (K rows swizzled), rows beyond the
+// LDS capacity are read from the cache. Softmax: one wave per head.
+template <int KVT, int HD>
 __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
                            float *sc, float *part, uint8_t *kvlds, double *red, float *redf, long long *tin) {
     using S = KvStage<KVT, HD>;
-    constexpr int hd = HD, ngr = kPB / HD;
+    constexpr int hd = HD;
     const int group = p.H / p.KVH, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const LayerPtrs Lp = layer_ptrs(p.layers, l);
@@ -949,56 +945,24 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
         kv_st<KVT>(p.kcache, lbase + (size_t)pos * p.kvdim + i, ks[i]);
         kv_st<KVT>(p.vcache, lbase + (size_t)pos * p.kvdim + i, vs[i]);
         if (pos < S::ROWS) {
-            // EXACT: K rows sit in the swizzled chunk order (attn_prefetch<..., true>)
+            // K rows sit in the swizzled chunk order (attn_prefetch<..., true>)
             constexpr int NCH = S::RB / 16, EPC = 16 / S::EB;
-            const int ik = EXACT ? ((i / EPC) ^ (pos & (NCH - 1))) * EPC + i % EPC : i;
+            const int ik = ((i / EPC) ^ (pos & (NCH - 1))) * EPC + i % EPC;
             kv_put<KVT>(kst + (size_t)pos * S::RB, ik, ks[i]);
             kv_put<KVT>(vst + (size_t)pos * S::RB, i, vs[i]);
         }
     }
     lds_barrier();
-    // scores (infer.go:280-288)
-    int t_first = tid;   // first position this thread scores one per thread
-    if constexpr (!EXACT) {
-        // cached rows in LDS: each row's RB bytes are split over RB/16 lanes, every lane
-        // holding its 16-byte slice of q in registers; a wave reads consecutive rows, so its
-        // LDS reads are one contiguous block; the slices' partial dots are added by shuffles
-        constexpr int LPK = S::RB / 16, EPC = 16 / S::EB, PPW = 64 / LPK;
-        const int sl = lane % LPK, rin = lane / LPK;
-        float qr[kMaxGroup][EPC];
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; h++)
-#pragma unroll
-            for (int e = 0; e < EPC; e++) qr[h][e] = h < group ? qs[h * hd + sl * EPC + e] : 0.f;
-        const int tl = pos < S::ROWS ? pos : S::ROWS - 1;
-        for (int t0 = wave * PPW; t0 <= tl; t0 += kPW * PPW) {
-            const int t = t0 + rin;
-            const bool valid = t <= tl;
-            float kf[EPC];
-            const u32x4 kv4 = ((const SH_LDS u32x4 *)(kst + (size_t)(valid ? t : tl) * S::RB))[sl];
-            kv_unpack16<KVT>(kv4, kf);
-#pragma unroll
-            for (int h = 0; h < kMaxGroup; h++) {
-                if (h >= group) continue;
-                float d = 0.f;
-#pragma unroll
-                for (int e = 0; e < EPC; e++) d = fmaf(qr[h][e], kf[e], d);
-                d = wsum<LPK>(d);
-                if (valid && sl == 0) sc[h * p.max_seq + t] = d * p.inv_sqrt_hd;
-            }
-        }
-        t_first = tl + 1 + tid;   // rows beyond the LDS stage: one per thread below
-    }
-    // one thread per position: 16-byte chunks of the row in order (EXACT: the reference's
-    // summation order), or positions beyond the LDS stage read from the cache
-    for (int t = t_first; t <= pos; t += kPB) {
+    // scores (infer.go:280-288): one thread per position, the row's 16-byte chunks in order
+    // (the reference's summation order), positions beyond the LDS stage read from the cache
+    for (int t = tid; t <= pos; t += kPB) {
         float d[kMaxGroup];
 #pragma unroll
         for (int h = 0; h < kMaxGroup; h++) d[h] = 0.f;
         if (t < S::ROWS) {
             constexpr int NCH = S::RB / 16, EPC = 16 / S::EB;
             const SH_LDS u32x4 *row = (const SH_LDS u32x4 *)(kst + (size_t)t * S::RB);
-            const int swz = EXACT ? (t & (NCH - 1)) : 0;   // chunk c of the row sits in slot c ^ swz
+            const int swz = t & (NCH - 1);   // chunk c of the row sits in slot c ^ swz
 #pragma unroll 4
             for (int c = 0; c < NCH; c++) {
                 float kf[EPC];
@@ -1011,17 +975,10 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
 #pragma unroll
                     for (int e4 = 0; e4 < EPC / 4; e4++) {
                         const f32x4 qv = q4[e4];
-                        if constexpr (EXACT) {
-                            d[h] = __fadd_rn(d[h], __fmul_rn(qv.x, kf[4 * e4 + 0]));
-                            d[h] = __fadd_rn(d[h], __fmul_rn(qv.y, kf[4 * e4 + 1]));
-                            d[h] = __fadd_rn(d[h], __fmul_rn(qv.z, kf[4 * e4 + 2]));
-                            d[h] = __fadd_rn(d[h], __fmul_rn(qv.w, kf[4 * e4 + 3]));
-                        } else {
-                            d[h] = fmaf(qv.x, kf[4 * e4 + 0], d[h]);
-                            d[h] = fmaf(qv.y, kf[4 * e4 + 1], d[h]);
-                            d[h] = fmaf(qv.z, kf[4 * e4 + 2], d[h]);
-                            d[h] = fmaf(qv.w, kf[4 * e4 + 3], d[h]);
-                        }
+                        d[h] = __fadd_rn(d[h], __fmul_rn(qv.x, kf[4 * e4 + 0]));
+                        d[h] = __fadd_rn(d[h], __fmul_rn(qv.y, kf[4 * e4 + 1]));
+                        d[h] = __fadd_rn(d[h], __fmul_rn(qv.z, kf[4 * e4 + 2]));
+                        d[h] = __fadd_rn(d[h], __fmul_rn(qv.w, kf[4 * e4 + 3]));
                     }
                 }
             }
@@ -1033,8 +990,7 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
 #pragma unroll
                 for (int h = 0; h < kMaxGroup; h++) {
                     if (h >= group) continue;
-                    if constexpr (EXACT) d[h] = __fadd_rn(d[h], __fmul_rn(qs[h * hd + k], kv));
-                    else d[h] = fmaf(qs[h * hd + k], kv, d[h]);
+                    d[h] = __fadd_rn(d[h], __fmul_rn(qs[h * hd + k], kv));
                 }
             }
         }
@@ -1062,69 +1018,36 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
         for (int t = lane; t <= pos; t += 64) s[t] = s[t] * inv;
     }
     lds_barrier();
-    if constexpr (EXACT) {
-        // P.V in the reference's order: thread (h, i) sums p[t] * v[t][i] over t = 0..pos
-        for (int k = tid; k < group * hd; k += kPB) {
-            const int h = k / hd, ii = k % hd;
-            const float *ph = sc + h * p.max_seq;
-            const SH_LDS float *phl = (const SH_LDS float *)ph;
-            const int tl = pos < S::ROWS ? pos : S::ROWS - 1;
-            float sum = 0.f;
-            // One wave does this chain for all 64 dims of a head, so it is bound by the wave's
-            // instruction issue: four positions per trip, each a read of p, a read of v, a
-            // rounded product and a rounded sum; the reads of a trip issue together at fixed
-            // offsets from one address, the adds stay in position order.
-            const SH_LDS uint8_t *vcol = vst + (size_t)ii * S::EB;
-            int t = 0;
-#pragma unroll 2
-            for (; t + 4 <= tl + 1; t += 4) {
-                float pp[4], vv[4];
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    pp[u] = phl[t + u];
-                    vv[u] = kv_get<KVT>(vcol + (size_t)(t + u) * S::RB, 0);
-                }
-#pragma unroll
-                for (int u = 0; u < 4; u++) sum = __fadd_rn(sum, __fmul_rn(pp[u], vv[u]));
-            }
-            for (; t <= tl; t++) sum = __fadd_rn(sum, __fmul_rn(phl[t], kv_get<KVT>(vcol + (size_t)t * S::RB, 0)));
-#pragma unroll 8
-            for (int t = tl + 1; t <= pos; t++) {
-                const float vv = t == pos ? vs[ii] : kv_ld<KVT>(p.vcache, lbase + (size_t)t * p.kvdim + ii);
-                sum = __fadd_rn(sum, __fmul_rn(ph[t], vv));
-            }
-            ll_put(p.ll_att + (size_t)(g * group + h) * hd + ii, sum, e);
-        }
-        lds_barrier();
-        return true;
-    }
-    // P.V (infer.go:290-297)
-    const int vi = tid % hd, tg = tid / hd;
-    float acc[kMaxGroup];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; h++) acc[h] = 0.f;
-    const int tl = pos < S::ROWS ? pos : S::ROWS - 1;   // last position held in LDS
-#pragma unroll 4
-    for (int t = tg; t <= tl; t += ngr) {
-        const float vv = kv_get<KVT>(vst + (size_t)t * S::RB, vi);
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; h++)
-            if (h < group) acc[h] = fmaf(sc[h * p.max_seq + t], vv, acc[h]);
-    }
-    for (int t = tl + 1 + ((tg - (tl + 1) % ngr + ngr) % ngr); t <= pos; t += ngr) {
-        const float vv = t == pos ? vs[vi] : kv_ld<KVT>(p.vcache, lbase + (size_t)t * p.kvdim + vi);
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; h++)
-            if (h < group) acc[h] = fmaf(sc[h * p.max_seq + t], vv, acc[h]);
-    }
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; h++)
-        if (h < group) part[(h * ngr + tg) * hd + vi] = acc[h];
-    lds_barrier();
+    // P.V in the reference's order: thread (h, i) sums p[t] * v[t][i] over t = 0..pos
     for (int k = tid; k < group * hd; k += kPB) {
         const int h = k / hd, ii = k % hd;
+        const float *ph = sc + h * p.max_seq;
+        const SH_LDS float *phl = (const SH_LDS float *)ph;
+        const int tl = pos < S::ROWS ? pos : S::ROWS - 1;
         float sum = 0.f;
-        for (int r = 0; r < ngr; r++) sum += part[(h * ngr + r) * hd + ii];
+        // One wave does this chain for all 64 dims of a head, so it is bound by the wave's
+        // instruction issue: four positions per trip, each a read of p, a read of v, a
+        // rounded product and a rounded sum; the reads of a trip issue together at fixed
+        // offsets from one address, the adds stay in position order.
+        const SH_LDS uint8_t *vcol = vst + (size_t)ii * S::EB;
+        int t = 0;
+#pragma unroll 2
+        for (; t + 4 <= tl + 1; t += 4) {
+            float pp[4], vv[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                pp[u] = phl[t + u];
+                vv[u] = kv_get<KVT>(vcol + (size_t)(t + u) * S::RB, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) sum = __fadd_rn(sum, __fmul_rn(pp[u], vv[u]));
+        }
+        for (; t <= tl; t++) sum = __fadd_rn(sum, __fmul_rn(phl[t], kv_get<KVT>(vcol + (size_t)t * S::RB, 0)));
+#pragma unroll 8
+        for (int t = tl + 1; t <= pos; t++) {
+            const float vv = t == pos ? vs[ii] : kv_ld<KVT>(p.vcache, lbase + (size_t)t * p.kvdim + ii);
+            sum = __fadd_rn(sum, __fmul_rn(ph[t], vv));
+        }
         ll_put(p.ll_att + (size_t)(g * group + h) * hd + ii, sum, e);
     }
     lds_barrier();
@@ -1132,7 +1055,7 @@ __device__ __forceinline__ bool attn_stage(const PParams &p, int l, int g, int p
 }
 
 
-// attn_stage<KVT, 64, true> for one q head per kv head (the Stories110M W8A8 model): every
+// attn_stage<KVT, 64> for one q head per kv head (the Stories110M W8A8 model): every
 // float operation, and its order, as there; what moves is which wave does it and how often
 // the workgroup waits. A 64-dim head is one wave wide, so wave 0 polls q and k and wave 1
 // polls v (no workgroup barrier around the poll); wave 0 applies the QK-norm (float64 sums
@@ -1351,7 +1274,8 @@ __device__ __forceinline__ void attn_exact1_tail(const PParams &p, int g, int po
 }
 
 // Attention for the fp16 / bf16 models with two q heads per kv head (the Qwen3 shape: 128-dim
-// heads; attn_stage_wave serves one q head per kv head, the W8A8 model attn_stage<..., true>):
+// heads; attn_stage_wave serves one q head per kv head, the W8A8 model attn_stage_exact1 with
+// one q head per kv head and 64-dim heads, attn_stage<...> otherwise):
 // the same mathematics in fewer dependent steps, rounded differently in the last bits. (The
 // per-wave form measured slower at this shape: 736 against 658 us per Qwen3-shaped forward,
 // each of its waves polling 512 words.)
@@ -1621,7 +1545,7 @@ __device__ __forceinline__ float gmax(float v) {
 }
 
 // Attention for the fp16 / bf16 models (infer.go:273-299): kv head g on this workgroup, its
-// GROUP q heads; the W8A8 model keeps attn_stage<..., true>. Every wave works on its own
+// GROUP q heads; the W8A8 model keeps attn_stage<...>. Every wave works on its own
 // slice of positions and meets the others once, at the end:
 //  - each wave polls q|k|v itself (no workgroup barrier after the hand-over), stages the words
 //    in its own LDS region and reads them back lane-sliced: lane (r, s) of the wave serves row r
@@ -2050,9 +1974,9 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                 if constexpr (WT == SH_DTYPE_W8A8 && HD == 64)
                     aok = p.H == p.KVH
                               ? attn_stage_exact1<KVT, HD>(p, l, blockIdx.x, pos, e, qs, sc, kvlds, okw, tin)
-                              : attn_stage<KVT, HD, true>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf, tin);
+                              : attn_stage<KVT, HD>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf, tin);
                 else if constexpr (WT == SH_DTYPE_W8A8)
-                    aok = attn_stage<KVT, HD, true>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf, tin);
+                    aok = attn_stage<KVT, HD>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf, tin);
                 else if constexpr (HD == 128)   // the 128-dim-head shape runs two q heads per kv head only
                     aok = attn_stage_fast<KVT, HD, 2>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf, tin);
                 else if (p.H == p.KVH)

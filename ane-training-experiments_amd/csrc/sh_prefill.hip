@@ -1867,7 +1867,7 @@ constexpr int kChunkBytes = 16 * 1024;    // bytes of K rows per streamed chunk 
 // products added by DPP), the running maximum and the rescaled sum of exp terms (online
 // softmax), and P.V by thread (dim, key group) with the chunk's weights from LDS. One split
 // writes the output row directly (a GEMM operand, hi/lo planes); several splits leave
-// (m, l, acc) partials for k_attn_split_combine. Sequence b attends to 0..pos[b].
+// (m, l, acc) partials, which the last split to finish merges. Sequence b attends to 0..pos[b].
 template <int KVT, int HD, int GROUP>
 __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 ? 2 : 4))) void k_attn_batch_stream(
     const float *partial, int ranges, QkRopeArgs a, const void *kc, const void *vc, size_t kv_seq_stride,
@@ -2145,8 +2145,8 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
         }
     }
     if (nsplit == 1) return;
-    // The last of the sequence's key-holding splits to count in merges them, in
-    // k_attn_split_combine's float order (sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s),
+    // The last of the sequence's key-holding splits to count in merges them, in the float
+    // order sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s (splits in order),
     // reading the others' tagged partials, and clears the counter for the next layer.
     __shared__ int merge_s;
     __syncthreads();
@@ -2169,32 +2169,6 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
         for (int c = 0; c < ns; c++)
             a += expf(tag_get(tm + pb + c, tag, err) - M) * tag_get(tacc + (pb + c) * HD + ii, tag, err);
         store_op16(att, (size_t)b * qdim + (size_t)h * HD + ii, plane, a * invL, dt);
-    }
-}
-
-// Merges the split partials of k_attn_batch_stream for (q head h, sequence b): the splits
-// holding keys are recomputed from pos[b] as the kernel did; out = sum_s e^(m_s - M) acc_s /
-// sum_s e^(m_s - M) l_s, written as a GEMM operand row.
-__global__ __launch_bounds__(256) void k_attn_split_combine(const float *pm, const float *pl,
-                                                            const float *pacc, const int32_t *pos,
-                                                            int H, int hd, int nsplit, int chunk,
-                                                            int nch_buf, int B, int dt, uint16_t *att) {
-    const int h = blockIdx.x, b = blockIdx.y;
-    const int P = pos[b] + 1;
-    const int nchunks = (P + chunk - 1) / chunk;
-    const int cps = (nchunks + nsplit - 1) / nsplit;
-    const int ns = (nchunks + cps - 1) / cps;
-    const size_t pb = ((size_t)b * H + h) * nch_buf;
-    float M = -INFINITY;
-    for (int c = 0; c < ns; c++) M = fmaxf(M, pm[pb + c]);
-    float Lsum = 0.f;
-    for (int c = 0; c < ns; c++) Lsum += expf(pm[pb + c] - M) * pl[pb + c];
-    const float invL = 1.0f / Lsum;
-    const size_t plane = (size_t)B * H * hd;
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
-        float a = 0.f;
-        for (int c = 0; c < ns; c++) a += expf(pm[pb + c] - M) * pacc[(pb + c) * hd + i];
-        store_op16(att, (size_t)b * H * hd + (size_t)h * hd + i, plane, a * invL, dt);
     }
 }
 
