@@ -981,6 +981,72 @@ __global__ __launch_bounds__(1024) void k_row_resid_norm(const float *partial, i
                  final_form ? (float)((double)row[i] * rr * (double)gain[i]) : row[i] * scale * gain[i], dt);
 }
 
+// k_row_resid_norm for rows of at most 1024 elements: one 256-thread workgroup per row, each
+// thread owning one 16-byte chunk. The same operations (the K ranges added in range order,
+// x = resid + alpha * sum, the float64 sum of squares, the same normalised forms), but a
+// thread issues the loads of up to eight ranges together before it adds them, and the sum
+// of squares crosses the workgroup through one barrier (the block form's 1024 threads load
+// one range per round trip and reduce through LDS twice).
+__global__ __launch_bounds__(256) void k_row_resid_norm_v(const float *partial, int ranges, int M, int D,
+                                                          const float *resid, float alpha, float *x_out,
+                                                          const float *gain, double eps, int final_form, int dt,
+                                                          uint16_t *xn) {
+    __shared__ double red[4];
+    const int m = blockIdx.x, i = threadIdx.x * 4;
+    const bool own = i < D;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    double ss = 0;
+    if (own) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int r0 = 0; r0 < ranges; r0 += 8) {
+            float4 q[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (r0 + j < ranges) q[j] = *(const float4 *)(partial + ((size_t)(r0 + j) * M + m) * D + i);
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (r0 + j < ranges) {
+                    v.x += q[j].x; v.y += q[j].y; v.z += q[j].z; v.w += q[j].w;
+                }
+        }
+        const float4 rs = *(const float4 *)(resid + (size_t)m * D + i);
+        x = make_float4(rs.x + alpha * v.x, rs.y + alpha * v.y, rs.z + alpha * v.z, rs.w + alpha * v.w);
+        *(float4 *)(x_out + (size_t)m * D + i) = x;
+        ss = (double)x.x * (double)x.x;
+        ss += (double)x.y * (double)x.y;
+        ss += (double)x.z * (double)x.z;
+        ss += (double)x.w * (double)x.w;
+    }
+    ss = wsum_d64(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const double tot = red[0] + red[1] + red[2] + red[3];
+    if (!own) return;
+    const double rr = 1.0 / sqrt(tot / (double)D + eps);
+    const float scale = (float)rr;
+    const float4 g4 = *(const float4 *)(gain + i);
+    const float x4[4] = {x.x, x.y, x.z, x.w}, gg[4] = {g4.x, g4.y, g4.z, g4.w};
+    const size_t plane = (size_t)M * D;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        store_op(xn, (size_t)m * D + i + e, plane,
+                 final_form ? (float)((double)x4[e] * rr * (double)gg[e]) : x4[e] * scale * gg[e], dt);
+}
+
+// The residual + RMSNorm row kernel for M rows of D: the chunk-per-thread form where a row
+// fits one 256-thread workgroup.
+hipError_t launch_row_resid_norm(const float *partial, int ranges, int M, int D, const float *resid, float alpha,
+                                 float *x_out, const float *gain, double eps, int final_form, int dt,
+                                 uint16_t *xn, hipStream_t s) {
+    if (D % 4 == 0 && D <= 1024)
+        hipLaunchKernelGGL(k_row_resid_norm_v, dim3(M), dim3(256), 0, s, partial, ranges, M, D, resid, alpha, x_out,
+                           gain, eps, final_form, dt, xn);
+    else
+        hipLaunchKernelGGL(k_row_resid_norm, dim3(M), dim3(1024), 0, s, partial, ranges, M, D, resid, alpha, x_out,
+                           gain, eps, final_form, dt, xn);
+    return hipGetLastError();
+}
+
 // Two 16-bit operand values packed as the MFMA expects (element 2i in the low half).
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
@@ -2825,11 +2891,12 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
     g.one_plane = m->pf_one_plane;
     g.sw = L.s_o; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;
-    if (ranges > 1)
-        hipLaunchKernelGGL(k_row_resid_norm, dim3(S), dim3(1024), 0, s, (const float *)m->pf_part, ranges, S, D,
-                           (const float *)m->pf_x, c.residual_scale, m->pf_x2, L.rms_ffn, c.norm_eps, 0, dt,
-                           m->pf_xn);
-    else
+    if (ranges > 1) {
+        if ((e = launch_row_resid_norm((const float *)m->pf_part, ranges, S, D, (const float *)m->pf_x,
+                                       c.residual_scale, m->pf_x2, L.rms_ffn, c.norm_eps, 0, dt, m->pf_xn, s)) !=
+            hipSuccess)
+            return e;
+    } else
         hipLaunchKernelGGL(k_rmsnorm_rows, dim3(S), dim3(kT), 0, s, m->pf_x2, L.rms_ffn, D,
                            c.norm_eps, 0, dt, m->pf_xn, (size_t)S * D, nullptr);
     g = GemmArgs{};
@@ -2846,9 +2913,10 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
     if (!next_gain) return gemm(g, dt, m->pf_part, m->pf_part_cap, s);
     if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) return e;
     if (ranges == 1) return hipSuccess;
-    hipLaunchKernelGGL(k_row_resid_norm, dim3(S), dim3(1024), 0, s, (const float *)m->pf_part, ranges, S, D,
-                       (const float *)m->pf_x2, c.residual_scale, m->pf_x, next_gain, c.norm_eps, next_final, dt,
-                       m->pf_xn);
+    if ((e = launch_row_resid_norm((const float *)m->pf_part, ranges, S, D, (const float *)m->pf_x2,
+                                   c.residual_scale, m->pf_x, next_gain, c.norm_eps, next_final, dt, m->pf_xn, s)) !=
+        hipSuccess)
+        return e;
     if (out_normed) *out_normed = true;
     return hipGetLastError();
 }
@@ -3283,10 +3351,10 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         g.dt = dt; g.partial_only = 1;
         g.sw = L.s_o; g.a8 = m->bt_a8; g.sa = m->bt_sa;
         if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
-        hipLaunchKernelGGL(k_row_resid_norm, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part,
-                           ranges(D, m->qdim), B, D, (const float *)m->bt_x, c.residual_scale,
-                           m->bt_x2, L.rms_ffn, c.norm_eps, 0, dt, m->bt_xn);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if ((e = launch_row_resid_norm((const float *)m->bt_part, ranges(D, m->qdim), B, D,
+                                       (const float *)m->bt_x, c.residual_scale, m->bt_x2, L.rms_ffn, c.norm_eps,
+                                       0, dt, m->bt_xn, s)) != hipSuccess)
+            return e;
         // W1/W3 with the SiLU gate
         g = GemmArgs{};
         g.A = m->bt_xn; g.B = (const uint16_t *)L.w13; g.M = B; g.N = 2 * F; g.K = D;
@@ -3301,10 +3369,10 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
         g.sw = L.s_2; g.a8 = m->bt_a8; g.sa = m->bt_sa;
         if ((e = skinny(g, dt, m->bt_part, m->bt_part_cap, s)) != hipSuccess) return e;
         const float *next_gain = l + 1 < c.n_layers ? m->layers[l + 1].rms_att : m->rms_final;
-        hipLaunchKernelGGL(k_row_resid_norm, dim3(B), dim3(1024), 0, s, (const float *)m->bt_part,
-                           ranges(D, F), B, D, (const float *)m->bt_x2, c.residual_scale, m->bt_x,
-                           next_gain, c.norm_eps, 0, dt, m->bt_xn);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if ((e = launch_row_resid_norm((const float *)m->bt_part, ranges(D, F), B, D, (const float *)m->bt_x2,
+                                       c.residual_scale, m->bt_x, next_gain, c.norm_eps, 0, dt, m->bt_xn, s)) !=
+            hipSuccess)
+            return e;
     }
     GemmArgs g{};
     g.A = m->bt_xn; g.B = (const uint16_t *)m->cls; g.M = B; g.N = c.vocab; g.K = D;
