@@ -1916,6 +1916,82 @@ __device__ __forceinline__ float tag_get(const uint64_t *p, uint32_t tag, int *e
 }
 
 constexpr int kAT = 512;                  // threads of the streaming batched attention
+constexpr int kAWT = 1024;                // threads of its lane-group form (one workgroup per CU)
+
+// The rows of the q|k|v projection that workgroup (kv head g, sequence b) of the batched
+// attention needs, finished as k_row_qkv would finish the whole row and in the same float
+// order: the skinny GEMM's K-range partials added in range order, then QK-norm and RoPE at
+// position P - 1 for the group's q heads and for kv head g (qk_rope_row's per-head code,
+// restricted to those heads). rowq gets the q heads, then k, then v; k and v as the cache
+// holds them (rounded to its type), and written to the cache when `last`. The RoPE factors,
+// the QK-norm gains and up to four ranges' partials are requested together at the start, so
+// the prologue waits out one memory latency. NT threads; ends with a workgroup barrier.
+template <int KVT, int HD, int GROUP, int NT = kAT>
+__device__ __forceinline__ void batch_qkv_rows(const float *partial, int ranges, const QkRopeArgs &a,
+                                               const void *kc, const void *vc, size_t kv_seq_stride, int kvdim,
+                                               int b, int g, int P, bool last, float *rowq) {
+    static_assert(HD <= 128 && (GROUP + 2) * HD <= 2 * NT && (GROUP + 1) * HD / 2 <= NT, "one pass per step");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tp = P - 1, half = HD / 2;
+    // RoPE factors of pair tid, QK-norm gains of wave (head) w's elements lane, lane + 64
+    float rc = 0.f, rsn = 0.f, gn0 = 0.f, gn1 = 0.f;
+    if (tid < (GROUP + 1) * half) {
+        const int pi = tid % half;
+        rc = a.rope_cos[tp * half + pi];
+        rsn = a.rope_sin[tp * half + pi];
+    }
+    const bool norm_wave = a.qk_norm && wave <= GROUP;
+    if (norm_wave) {
+        const float *gn = wave < GROUP ? a.q_norm : a.k_norm;
+        if (lane < HD) gn0 = gn[lane];
+        if (lane + 64 < HD) gn1 = gn[lane + 64];
+    }
+    const int nrow = a.qdim + 2 * a.kvdim;
+    for (int i = tid; i < (GROUP + 2) * HD; i += NT) {
+        const int col = i < GROUP * HD ? g * GROUP * HD + i
+                                       : (i < (GROUP + 1) * HD ? a.qdim + g * HD + (i - GROUP * HD)
+                                                               : a.qdim + a.kvdim + g * HD + (i - (GROUP + 1) * HD));
+        float v = 0.f;
+        for (int r0 = 0; r0 < ranges; r0 += 4) {
+            float q[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (r0 + j < ranges) q[j] = partial[((size_t)(r0 + j) * gridDim.z + b) * nrow + col];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (r0 + j < ranges) v += q[j];
+        }
+        rowq[i] = v;
+    }
+    __syncthreads();
+    // QK-norm (wave w normalises head w: the q heads, then k), RoPE at pos[b]
+    if (norm_wave) {
+        float *v = rowq + wave * HD;
+        double ss = 0;
+        for (int i = lane; i < HD; i += 64) ss += (double)v[i] * (double)v[i];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        const float rr = (float)(1.0 / sqrt(ss / (double)HD + a.qk_eps));
+        if (lane < HD) v[lane] = v[lane] * rr * gn0;
+        if (lane + 64 < HD) v[lane + 64] = v[lane + 64] * rr * gn1;
+    }
+    __syncthreads();
+    if (tid < (GROUP + 1) * half) {
+        const float e = rowq[2 * tid], o = rowq[2 * tid + 1];
+        rowq[2 * tid] = e * rc - o * rsn;
+        rowq[2 * tid + 1] = o * rc + e * rsn;
+    }
+    __syncthreads();
+    // the k and v row into the cache (once per sequence and kv head), and as the cache holds
+    // them into rowq
+    for (int i = tid; i < 2 * HD; i += NT) {
+        const float v = rowq[GROUP * HD + i];
+        if (last) kv_store<KVT>(i < HD ? (void *)kc : (void *)vc,
+                                (size_t)b * kv_seq_stride + (size_t)tp * kvdim + g * HD + (i % HD), v);
+        rowq[GROUP * HD + i] = kv_round<KVT>(v);
+    }
+    __syncthreads();
+}
 constexpr int kChunkBytes = 16 * 1024;    // bytes of K rows per streamed chunk (as many of V)
 
 // Batched decode attention that streams the cache (flash decoding): workgroup (split, kv
@@ -2031,49 +2107,7 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
     }
     const int d = tid % HD, kg = tid / HD;
     fetch(c0);   // the first chunks' loads go out before the q|k|v rows are finished
-    {
-        // q heads g*GROUP .. +GROUP-1, k and v of kv head g: partial sums in range order
-        const int nrow = a.qdim + 2 * a.kvdim;
-        for (int i = tid; i < (GROUP + 2) * HD; i += kAT) {
-            const int col = i < GROUP * HD ? g * GROUP * HD + i
-                                           : (i < (GROUP + 1) * HD ? a.qdim + g * HD + (i - GROUP * HD)
-                                                                   : a.qdim + a.kvdim + g * HD + (i - (GROUP + 1) * HD));
-            float v = 0.f;
-            for (int r = 0; r < ranges; r++) v += partial[((size_t)r * gridDim.z + b) * nrow + col];
-            rowq[i] = v;
-        }
-        __syncthreads();
-        // QK-norm (wave w normalises head w: the q heads, then k), RoPE at pos[b]
-        if (a.qk_norm && wave <= GROUP) {
-            float *v = rowq + wave * HD;
-            const float *gn = wave < GROUP ? a.q_norm : a.k_norm;
-            double ss = 0;
-            for (int i = lane; i < HD; i += 64) ss += (double)v[i] * (double)v[i];
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-            const float rr = (float)(1.0 / sqrt(ss / (double)HD + a.qk_eps));
-            for (int i = lane; i < HD; i += 64) v[i] = v[i] * rr * gn[i];
-        }
-        __syncthreads();
-        const int tp = P - 1, half = HD / 2;
-        for (int pp = tid; pp < (GROUP + 1) * half; pp += kAT) {
-            const int pi = pp % half;
-            const float c = a.rope_cos[tp * half + pi], sn = a.rope_sin[tp * half + pi];
-            const float e = rowq[2 * pp], o = rowq[2 * pp + 1];
-            rowq[2 * pp] = e * c - o * sn;
-            rowq[2 * pp + 1] = o * c + e * sn;
-        }
-        __syncthreads();
-        // the k and v row into the cache (once per sequence and kv head), and as the cache
-        // holds them into rowq for the LDS patch
-        for (int i = tid; i < 2 * HD; i += kAT) {
-            const float v = rowq[GROUP * HD + i];
-            if (last) kv_store<KVT>(i < HD ? (void *)kc : (void *)vc,
-                                    (size_t)b * kv_seq_stride + (size_t)tp * kvdim + g * HD + (i % HD), v);
-            rowq[GROUP * HD + i] = kv_round<KVT>(v);
-        }
-        __syncthreads();
-    }
+    batch_qkv_rows<KVT, HD, GROUP>(partial, ranges, a, kc, vc, kv_seq_stride, kvdim, b, g, P, last, rowq);
     float qr[GROUP][EPC];
 #pragma unroll
     for (int h = 0; h < GROUP; h++)
@@ -2238,6 +2272,255 @@ __global__ __launch_bounds__(kAT) __attribute__((amdgpu_waves_per_eu(GROUP == 4 
     }
 }
 
+// Batched decode attention with one online softmax per lane group and no barrier inside the
+// key loop (head dims 64 and 128). Workgroup (split, kv head g, sequence b) takes the same
+// split of the sequence's keys as k_attn_batch_stream, finishes its q|k|v rows the same way
+// (batch_qkv_rows), and then each wave walks its own rows of the split: per iteration RWI
+// = SBW * PPW rows, row r of a row block on LPK lanes (each lane one 16-byte slice of the K
+// and V rows, loaded straight into registers one iteration ahead, no LDS staging). The lanes
+// of a row finish its score (slice dot products added by DPP), fold it into their running
+// (max, sum, P.V slice) for every q head of the group, in the base-2 domain (the score scaled
+// by log2 e, so each term is one exp2), and the row's V slice is already in the same lanes.
+// After the loop the row groups of a wave merge by lane swaps, the waves through LDS, and
+// the splits as in k_attn_batch_stream (tagged partials, merged by the last split). Row pos[b]
+// is taken from rowq (the cache row's load may predate the prologue's write).
+template <int KVT, int HD, int GROUP, int SBW, int NSET>
+__global__ __launch_bounds__(kAWT) void k_attn_batch_wave(
+    const float *partial, int ranges, QkRopeArgs a, const void *kc, const void *vc, size_t kv_seq_stride,
+    const int32_t *pos, int H, int KVH, float scale, int nsplit, int nch_buf, int dt, size_t plane,
+    uint16_t *att, uint64_t *tm, uint64_t *tl_, uint64_t *tacc, int *cnt, const uint32_t *gen, int layer,
+    int n_layers, int max_seq, int *err) {
+    constexpr int EB = KVT == SH_KV_F32 ? 4 : 2;
+    constexpr int RB = HD * EB;                        // bytes per cache row
+    constexpr int C = kChunkBytes / RB;                // keys per split unit (as the stream kernel)
+    constexpr int LPK = RB / 16, EPC = 16 / EB, PPW = 64 / LPK;
+    constexpr int NW = kAWT / 64;
+    constexpr int RWI = SBW * PPW, RI = NW * RWI;      // rows per wave / per workgroup per iteration
+    static_assert(HD == 64 || HD == 128, "head dims of the lane-group form");
+    __shared__ float rowq[(GROUP + 2) * HD];           // the group's q heads, then k, then v
+    __shared__ float wm[NW][GROUP], wl[NW][GROUP];
+    __shared__ __attribute__((aligned(16))) float wacc[NW][GROUP][HD];
+    const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int P = pos[b] + 1;
+    const int nchunks = (P + C - 1) / C;
+    const int cps = (nchunks + nsplit - 1) / nsplit;
+    const int c0 = split * cps, c1 = min(nchunks, c0 + cps);
+    if (c0 >= c1) return;
+    const int k0 = c0 * C, k1 = min(c1 * C, P);       // this split's keys
+    const int qdim = H * HD, kvdim = KVH * HD;
+    const uint32_t tag = ((*gen * (uint32_t)(max_seq + 1) + (uint32_t)(P - 1)) * (uint32_t)n_layers +
+                          (uint32_t)layer) + 1u;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t sbase = (size_t)b * kv_seq_stride + (size_t)g * HD;
+    const int sl = lane % LPK, rin = lane / LPK;
+    const bool last = c1 == nchunks;
+    const int nit = (k1 - k0 + RI - 1) / RI;
+    // K and V slices of iteration it's rows (rows past the split's last key re-read it, so
+    // every load is in bounds and none sits under a branch)
+    auto fetch = [&](int it, u32x4 (&kr)[SBW], u32x4 (&vr)[SBW]) {
+#pragma unroll
+        for (int j = 0; j < SBW; j++) {
+            const int t = min(k0 + it * RI + wave * RWI + j * PPW + rin, k1 - 1);
+            const size_t o = (sbase + (size_t)t * kvdim) * EB + (size_t)sl * 16;
+            kr[j] = *(const u32x4 *)((const uint8_t *)kc + o);
+            vr[j] = *(const u32x4 *)((const uint8_t *)vc + o);
+        }
+    };
+    // NSET register sets in a ring, each loaded NSET - 1 iterations ahead of its use
+    u32x4 kr[NSET][SBW], vr[NSET][SBW];
+#pragma unroll
+    for (int u = 0; u + 1 < NSET; u++) fetch(u, kr[u], vr[u]);   // out before the q|k|v rows are finished
+    batch_qkv_rows<KVT, HD, GROUP, kAWT>(partial, ranges, a, kc, vc, kv_seq_stride, kvdim, b, g, P, last, rowq);
+    float qr[GROUP][EPC];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++)
+#pragma unroll
+        for (int e = 0; e < EPC; e++) qr[h][e] = rowq[h * HD + sl * EPC + e];
+    const float scale2 = scale * 1.4426950408889634f;
+    // running state of this lane's row group: base-2 max (finite floor, so a group whose rows
+    // are all masked so far rescales by 1), sum of terms, P.V over the lane's EPC dims
+    float m[GROUP], l[GROUP], acc[GROUP][EPC];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) {
+        m[h] = -1e30f;
+        l[h] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPC; e++) acc[h][e] = 0.f;
+    }
+    auto unpack = [&](const u32x4 &r, float (&f)[EPC]) {
+        if constexpr (KVT == SH_KV_F32) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) f[e] = __uint_as_float(r[e]);
+        } else {
+            const int dtk = KVT == SH_KV_BF16 ? SH_DTYPE_BF16 : SH_DTYPE_F16;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                f[2 * e] = bits_to_f(r[e] & 0xffffu, dtk);
+                f[2 * e + 1] = bits_to_f(r[e] >> 16, dtk);
+            }
+        }
+    };
+    auto compute = [&](int it, const u32x4 (&kr)[SBW], const u32x4 (&vr)[SBW]) {
+        float sc[SBW][GROUP], vf[SBW][EPC];
+        const bool tail = last && it == nit - 1;   // holds row P - 1
+#pragma unroll
+        for (int j = 0; j < SBW; j++) {
+            const int t = k0 + it * RI + wave * RWI + j * PPW + rin;
+            float kf[EPC];
+            unpack(kr[j], kf);
+            unpack(vr[j], vf[j]);
+            if (__builtin_expect(tail, 0) && t == P - 1) {
+#pragma unroll
+                for (int e = 0; e < EPC; e++) {
+                    kf[e] = rowq[GROUP * HD + sl * EPC + e];
+                    vf[j][e] = rowq[(GROUP + 1) * HD + sl * EPC + e];
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) {
+                float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+                for (int e = 0; e < EPC; e += 2) {
+                    d0 = fmaf(qr[h][e], kf[e], d0);
+                    d1 = fmaf(qr[h][e + 1], kf[e + 1], d1);
+                }
+                const float dd = wsum<LPK>(d0 + d1) * scale2;
+                sc[j][h] = t < k1 ? dd : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            float mn = m[h];
+#pragma unroll
+            for (int j = 0; j < SBW; j++) mn = fmaxf(mn, sc[j][h]);
+            const float f = __builtin_amdgcn_exp2f(m[h] - mn);
+            m[h] = mn;
+            float pw[SBW];
+            float ls = l[h] * f;
+#pragma unroll
+            for (int j = 0; j < SBW; j++) {
+                pw[j] = __builtin_amdgcn_exp2f(sc[j][h] - mn);
+                ls += pw[j];
+            }
+            l[h] = ls;
+#pragma unroll
+            for (int e = 0; e < EPC; e++) {
+                float o = acc[h][e] * f;
+#pragma unroll
+                for (int j = 0; j < SBW; j++) o = fmaf(pw[j], vf[j][e], o);
+                acc[h][e] = o;
+            }
+        }
+    };
+    // unrolled by NSET, so no set is copied while its loads are in flight
+    for (int it = 0; it < nit; it += NSET) {
+#pragma unroll
+        for (int u = 0; u < NSET; u++) {
+            fetch(it + u + NSET - 1, kr[(u + NSET - 1) % NSET], vr[(u + NSET - 1) % NSET]);
+            if (u == 0 || it + u < nit) compute(it + u, kr[u], vr[u]);
+        }
+    }
+    // the PPW row groups of the wave (lanes sl + LPK * r) merged by lane swaps; every lane of
+    // a slice ends with the same values
+#pragma unroll
+    for (int x = LPK; x < 64; x <<= 1) {
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            const float mo = __shfl_xor(m[h], x, 64), lo = __shfl_xor(l[h], x, 64);
+            const float mn = fmaxf(m[h], mo);
+            const float fa = __builtin_amdgcn_exp2f(m[h] - mn), fb = __builtin_amdgcn_exp2f(mo - mn);
+            l[h] = l[h] * fa + lo * fb;
+#pragma unroll
+            for (int e = 0; e < EPC; e++) {
+                const float ao = __shfl_xor(acc[h][e], x, 64);
+                acc[h][e] = acc[h][e] * fa + ao * fb;
+            }
+            m[h] = mn;
+        }
+    }
+    if (rin == 0) {
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+#pragma unroll
+            for (int e = 0; e < EPC; e++) wacc[wave][h][sl * EPC + e] = acc[h][e];
+            if (sl == 0) {
+                wm[wave][h] = m[h];
+                wl[wave][h] = l[h];
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < GROUP * HD; i += kAWT) {
+        const int h = i / HD, dd = i % HD;
+        float M = -1e30f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, wm[w][h]);
+        float o = 0.f, lh = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = __builtin_amdgcn_exp2f(wm[w][h] - M);
+            lh += wl[w][h] * f;
+            o += wacc[w][h][dd] * f;
+        }
+        if (nsplit == 1) {
+            store_op16(att, (size_t)b * qdim + (size_t)(g * GROUP + h) * HD + dd, plane, o / lh, dt);
+        } else {
+            const size_t pb = ((size_t)b * H + (size_t)g * GROUP + h) * nch_buf + split;
+            tag_put(tacc + pb * HD + dd, o, tag);
+            if (dd == 0) {
+                tag_put(tm + pb, M, tag);
+                tag_put(tl_ + pb, lh, tag);
+            }
+        }
+    }
+    if (nsplit == 1) return;
+    // the last of the sequence's key-holding splits to count in merges them (base-2 maxima),
+    // splits in order, and clears the counter for the next layer
+    __shared__ int merge_s;
+    __syncthreads();
+    const int ns = (nchunks + cps - 1) / cps;
+    int *ctr = cnt + (size_t)b * KVH + g;
+    if (tid == 0) merge_s = atomicAdd(ctr, 1) == ns - 1;
+    __syncthreads();
+    if (!merge_s) return;
+    if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the splits' words requested four splits at a time (a word without the tag is polled
+    // by tag_get), folded in split order
+    for (int i = tid; i < GROUP * HD; i += kAWT) {
+        const int h = g * GROUP + i / HD, ii = i % HD;
+        const size_t pb = ((size_t)b * H + h) * nch_buf;
+        float M = -INFINITY, Lsum = 0.f, acc_s = 0.f;
+        for (int c0 = 0; c0 < ns; c0 += 4) {
+            uint64_t w[4][3];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (c0 + u < ns) {
+                    w[u][0] = __hip_atomic_load(tm + pb + c0 + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    w[u][1] = __hip_atomic_load(tl_ + pb + c0 + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    w[u][2] = __hip_atomic_load(tacc + (pb + c0 + u) * HD + ii, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (c0 + u < ns) {
+                    const size_t c = pb + c0 + u;
+                    const float mc = (uint32_t)(w[u][0] >> 32) == tag ? __uint_as_float((uint32_t)w[u][0])
+                                                                      : tag_get(tm + c, tag, err);
+                    const float lc = (uint32_t)(w[u][1] >> 32) == tag ? __uint_as_float((uint32_t)w[u][1])
+                                                                      : tag_get(tl_ + c, tag, err);
+                    const float ac = (uint32_t)(w[u][2] >> 32) == tag ? __uint_as_float((uint32_t)w[u][2])
+                                                                      : tag_get(tacc + c * HD + ii, tag, err);
+                    const float mn = fmaxf(M, mc);
+                    const float f = exp2f(M - mn), fc = exp2f(mc - mn);
+                    Lsum = Lsum * f + lc * fc;
+                    acc_s = acc_s * f + ac * fc;
+                    M = mn;
+                }
+        }
+        store_op16(att, (size_t)b * qdim + (size_t)h * HD + ii, plane, acc_s / Lsum, dt);
+    }
+}
+
 // The streaming kernel for (kv type, head dim, group), or null when it has no instance.
 typedef void (*AttnStreamKernel)(const float *, int, QkRopeArgs, const void *, const void *, size_t,
                                  const int32_t *, int, int, float, int, int, int, size_t, uint16_t *, uint64_t *,
@@ -2248,14 +2531,17 @@ AttnStreamKernel pick_attn_stream_kv(int hd, int group) {
     case 32 * 8 + 1: return &k_attn_batch_stream<KVT, 32, 1>;
     case 32 * 8 + 2: return &k_attn_batch_stream<KVT, 32, 2>;
     case 32 * 8 + 4: return &k_attn_batch_stream<KVT, 32, 4>;
-    case 64 * 8 + 1: return &k_attn_batch_stream<KVT, 64, 1>;
-    case 64 * 8 + 2: return &k_attn_batch_stream<KVT, 64, 2>;
+    case 64 * 8 + 1: return &k_attn_batch_wave<KVT, 64, 1, 2, 3>;
+    case 64 * 8 + 2: return &k_attn_batch_wave<KVT, 64, 2, 2, 3>;
     case 64 * 8 + 4: return &k_attn_batch_stream<KVT, 64, 4>;
-    case 128 * 8 + 1: return &k_attn_batch_stream<KVT, 128, 1>;
-    case 128 * 8 + 2: return &k_attn_batch_stream<KVT, 128, 2>;
+    case 128 * 8 + 1: return &k_attn_batch_wave<KVT, 128, 1, 2, 3>;
+    case 128 * 8 + 2: return &k_attn_batch_wave<KVT, 128, 2, 2, 3>;
     default: return nullptr;
     }
 }
+// Threads of the streaming kernel pick_attn_stream returns (the lane-group form for 64- and
+// 128-dim heads with one or two q heads per kv head; with four its registers would spill).
+int attn_stream_threads(int hd, int group) { return (hd == 64 || hd == 128) && group <= 2 ? kAWT : kAT; }
 AttnStreamKernel pick_attn_stream(int kv, int hd, int group) {
     if (kv == SH_KV_F32) return pick_attn_stream_kv<SH_KV_F32>(hd, group);
     if (kv == SH_KV_F16) return pick_attn_stream_kv<SH_KV_F16>(hd, group);
@@ -3284,7 +3570,9 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
     // workgroup per CU, within the partial buffers (nch slots per head and sequence)
     const AttnStreamKernel astream = pick_attn_stream(c.kv_dtype, c.head_dim, c.n_heads / c.n_kv_heads);
     const int schunk = kChunkBytes / (c.head_dim * kvb);
-    int nsplit = std::max(1, (512 + B * c.n_kv_heads - 1) / (B * c.n_kv_heads));
+    const int athreads = attn_stream_threads(c.head_dim, c.n_heads / c.n_kv_heads);
+    const int awg = athreads == kAWT ? 256 : 512;   // workgroups that fill the chip
+    int nsplit = std::max(1, (awg + B * c.n_kv_heads - 1) / (B * c.n_kv_heads));
     nsplit = std::min({nsplit, nch, (c.max_seq + schunk - 1) / schunk});
     // K ranges the row kernels sum (the W8A8 product leaves one)
     auto ranges = [dt](int N, int K) { return dt == SH_DTYPE_W8A8 ? 1 : K / skinny_kc(N, K); };
@@ -3317,7 +3605,7 @@ hipError_t enqueue_batch_step(sh_model *m, int B) {
                 hipSuccess)
                 return e;
         } else if (astream) {
-            hipLaunchKernelGGL(astream, dim3(nsplit, c.n_kv_heads, B), dim3(kAT), 0, s,
+            hipLaunchKernelGGL(astream, dim3(nsplit, c.n_kv_heads, B), dim3(athreads), 0, s,
                                (const float *)m->bt_part, rq, qa, kc, vc, kv_seq_stride(m), m->bt_pos, c.n_heads, c.n_kv_heads, scale, nsplit, nch,
                                dt, (size_t)B * c.n_heads * c.head_dim, m->bt_att, m->bt_tm, m->bt_tl,
                                m->bt_tacc, m->bt_cnt, m->bt_gen, l, c.n_layers, c.max_seq, m->bt_err);

@@ -64,6 +64,24 @@ def test_batch_tiny_gqa_qknorm(gpu):
     m.close()
 
 
+@pytest.mark.parametrize("heads,kv_heads,hd,dtype,kv", [
+    (2, 2, 64, sh.SH_DTYPE_F16, sh.SH_KV_F32),
+    (4, 2, 64, sh.SH_DTYPE_BF16, sh.SH_KV_BF16),
+    (2, 1, 128, sh.SH_DTYPE_F16, sh.SH_KV_F16),
+])
+def test_batch_lane_group_attention(gpu, heads, kv_heads, hd, dtype, kv):
+    """The lane-group form of the batched attention (64- and 128-dim heads, one or two q heads
+    per kv head; the 128-dim case with a q width of 256 against dim 128) over several splits
+    of each sequence's keys: 100-id prompts and 40 steps reach positions in the second and
+    third 64- or 128-key split unit, so rows end inside a unit and the splits' partials merge."""
+    cfg = tiny_config(n_heads=heads, n_kv_heads=kv_heads, head_dim=hd, kv_dtype=kv, max_seq=160, max_batch=3,
+                      qk_norm=int(heads != kv_heads))
+    m, ref = build(cfg, dtype, seed=631, std=0.08, gains_seed=632)
+    prompts = sh.synth_tokens(3 * 100, 633, cfg.vocab).reshape(3, 100)
+    check_rows(m, ref, prompts, 40)
+    m.close()
+
+
 def test_batch_bookkeeping(gpu):
     cfg = tiny_config(max_seq=40, max_batch=3)
     m, ref = build(cfg, sh.SH_DTYPE_F16, seed=621, std=0.08)
