@@ -1121,14 +1121,15 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
     const int q0 = blockIdx.x * BQ, h = blockIdx.y;
     const int qdim = H * HD, kvdim = KVH * HD, kvh = h / (H / KVH);
     const int qlast = min(q0 + BQ, S) - 1;
-    const int kb0 = (q0 - rowpos[q0]) & ~(BK - 1);
+    // rowpos null: row t is position t of one sequence (the EvalLogits forward)
+    const int kb0 = rowpos ? (q0 - rowpos[q0]) & ~(BK - 1) : 0;
     uint8_t *ksl = lds + (size_t)wave * NP * (KSL + VSL);   // this wave's K planes, then V^T
     uint8_t *vsl = ksl + NP * KSL;
 
     // this lane's query and its Q operand planes (B operand: dims 32s + 8*g4 .. +7)
     const int t = q0 + ql;
     const bool tok = t < S;
-    const int jlo = tok ? t - rowpos[t] : 0x7fffffff;
+    const int jlo = tok ? (rowpos ? t - rowpos[t] : 0) : 0x7fffffff;
     u32x4 qh[NS], qlo[NS];
 #pragma unroll
     for (int s = 0; s < NS; s++) {
@@ -3084,16 +3085,17 @@ hipError_t launch_attn_prefill(const sh_model *m, int S, int seg_max, bool fill_
     else SH_ATT(DTV, 128, LOV);
     if (m->pf_one_plane && dt == SH_DTYPE_F16 && !wide &&
         (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128)) {
-        // EvalLogits (fp16): Q, K, V and P as one fp16 plane each
+        // EvalLogits (fp16): Q, K, V and P as one fp16 plane each; its rows are positions
+        // 0..S-1 of one sequence, so the kernel needs no position lookups
         if (c.head_dim == 32)
             hipLaunchKernelGGL((k_attn_prefill_mfma<SH_DTYPE_F16, 32, false, 1>), grid, dim3(kT), 0, s, m->pf_q,
-                               m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
+                               m->pf_k, m->pf_v, S, nullptr, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
         else if (c.head_dim == 64)
             hipLaunchKernelGGL((k_attn_prefill_mfma<SH_DTYPE_F16, 64, false, 1>), grid, dim3(kT), 0, s, m->pf_q,
-                               m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
+                               m->pf_k, m->pf_v, S, nullptr, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
         else
             hipLaunchKernelGGL((k_attn_prefill_mfma<SH_DTYPE_F16, 128, false, 1>), grid, dim3(kT), 0, s, m->pf_q,
-                               m->pf_k, m->pf_v, S, m->pf_rowpos, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
+                               m->pf_k, m->pf_v, S, nullptr, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
     } else if (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) {
         if (dt == SH_DTYPE_BF16) {
             if (exact) { SH_ATT_HD(SH_DTYPE_BF16, false) } else { SH_ATT_HD(SH_DTYPE_BF16, true) }
