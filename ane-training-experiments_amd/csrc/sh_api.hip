@@ -115,10 +115,7 @@ hipError_t ensure_step_graph(sh_model *m) {
 // and of the argmax partials (two forwards' slots per workgroup).
 size_t stage_words(const sh_model *m, int st) { return (size_t)m->p_own[st].n * (size_t)m->p_ostride[st]; }
 size_t gate_words(const sh_model *m) { return stage_words(m, 2); }
-// the workgroups' partial slots, then the groups' (both double-buffered by forward parity)
-size_t arg_words(const sh_model *m) {
-    return 2 * ((size_t)m->p_grid + (m->p_grid + kArgGroup - 1) / kArgGroup) * kArgSlot;
-}
+size_t arg_words(const sh_model *m) { return 2 * (size_t)m->p_grid * kArgSlot; }
 
 // Runs n_forwards forwards from pos0 with the persistent kernel (epochs advance; the
 // hand-over buffers are cleared before the 32-bit epoch space runs out).

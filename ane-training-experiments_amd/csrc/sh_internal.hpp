@@ -197,7 +197,6 @@ int gemv_partials(const sh_model *m);
 bool persistent_supported(const sh_model *m);
 hipError_t persistent_plan(sh_model *m, std::string *why);
 constexpr int kArgSlot = 16;  // hand-over words per argmax partial slot (one 128-byte line)
-constexpr int kArgGroup = 16;  // workgroups per first-level group of the next-token exchange
 hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt);
 size_t persistent_layer_ptr_bytes(int n_layers);
 bool prefill_supported(const sh_model *m, std::string *why);

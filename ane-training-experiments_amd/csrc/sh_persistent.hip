@@ -2121,66 +2121,46 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
         // w13 stage does not span every workgroup the exchange runs after every forward: it is
         // what keeps a slow workgroup's classifier poll of x ahead of the next forward's w2
         // stores.
-        //
-        // Two levels, both on wave 0: the first workgroup of each group of kArgGroup reduces
-        // its group's partials and publishes the group's (max, first index); every workgroup
-        // then reduces the group results. The order is immaterial (larger value, then smaller
-        // index), and each workgroup polls ceil(grid / kArgGroup) slots instead of one per
-        // workgroup of the grid (whose 512 lines per workgroup per round made the exchange's
-        // memory traffic the bound).
         if (p.argmax_every || pos + 1 >= p.n_prompt || f == p.n_forwards - 1) {
-            const int n = gridDim.x, ng = (n + kArgGroup - 1) / kArgGroup, lane = threadIdx.x;
-            // polls this lane's slot of (pv, pi) once both words carry epoch ec
-            auto poll_pair = [&](const uint64_t *pv, const uint64_t *pi, float &v, int &idx) {
-                uint64_t a = ll_get(pv), b = ll_get(pi);
+            bool ok = true;
+            float v = -INFINITY;
+            int idx = 0x7fffffff;
+            const int n = gridDim.x;
+            const uint64_t *pv = p.ll_pv + (size_t)(f & 1) * n * kArgSlot;
+            const uint64_t *pi = p.ll_pi + (size_t)(f & 1) * n * kArgSlot;
+            // one partial per thread (n <= kPB); its value and index words polled together
+            if ((int)threadIdx.x < n) {
+                const size_t o = (size_t)threadIdx.x * kArgSlot;
+                uint64_t a = ll_get(pv + o), b = ll_get(pi + o);
                 WaitBound wb;
                 while ((uint32_t)(a >> 32) != ec || (uint32_t)(b >> 32) != ec) {
-                    if (!wb.more(p)) return false;
-                    if ((uint32_t)(a >> 32) != ec) a = ll_get(pv);
-                    if ((uint32_t)(b >> 32) != ec) b = ll_get(pi);
+                    if (!wb.more(p)) {
+                        ok = false;
+                        break;
+                    }
+                    if ((uint32_t)(a >> 32) != ec) a = ll_get(pv + o);
+                    if ((uint32_t)(b >> 32) != ec) b = ll_get(pi + o);
                 }
                 v = __uint_as_float((uint32_t)a);
                 idx = (int)(uint32_t)b;
-                return true;
-            };
-            const size_t gslot = ((size_t)2 * n + (size_t)(f & 1) * ng) * kArgSlot;
-            bool ok = true;
-            if (lane < 64) {
-                float v = -INFINITY;
-                int idx = 0x7fffffff;
-                if (blockIdx.x % kArgGroup == 0) {
-                    const int m = blockIdx.x + lane;
-                    if (lane < kArgGroup && m < n) {
-                        const size_t o = ((size_t)(f & 1) * n + m) * kArgSlot;
-                        ok = poll_pair(p.ll_pv + o, p.ll_pi + o, v, idx);
-                    }
-                    ok = __all(ok);
-                    wargmax(v, idx);
-                    if (ok && lane == 0) {
-                        const size_t o = gslot + (size_t)(blockIdx.x / kArgGroup) * kArgSlot;
-                        ll_put(p.ll_pv + o, v, ec);
-                        ll_put_u(p.ll_pi + o, (uint32_t)idx, ec);
-                    }
-                    v = -INFINITY;
-                    idx = 0x7fffffff;
-                }
-                if (ok && lane < ng) {
-                    const size_t o = gslot + (size_t)lane * kArgSlot;
-                    ok = poll_pair(p.ll_pv + o, p.ll_pi + o, v, idx);
-                }
-                ok = __all(ok);
-                wargmax(v, idx);
-                if (ok && lane == 0) {
-                    const int nt = idx == 0x7fffffff ? 0 : idx;
-                    next_tok = nt;
-                    if (blockIdx.x == 0) {
-                        p.hist[pos] = nt;
-                        if (pos + 1 <= p.max_seq && pos + 1 >= p.n_prompt) p.tokens[pos + 1] = nt;
-                    }
-                }
             }
             if (!block_and(ok)) return;
             stamp_in();
+            wargmax(v, idx);
+            if ((threadIdx.x & 63) == 0) cand[threadIdx.x >> 6] = ArgmaxPartial{v, idx};
+            lds_barrier();
+            if (threadIdx.x == 0) {
+                ArgmaxPartial b = cand[0];
+                for (int w = 1; w < kPW; w++)
+                    if (better(cand[w].v, cand[w].i, b.v, b.i)) b = cand[w];
+                const int nt = b.i == 0x7fffffff ? 0 : b.i;
+                next_tok = nt;
+                if (blockIdx.x == 0) {
+                    p.hist[pos] = nt;
+                    if (pos + 1 <= p.max_seq && pos + 1 >= p.n_prompt) p.tokens[pos + 1] = nt;
+                }
+            }
+            lds_barrier();
             tok_next = next_tok;
         }
         stamp();
