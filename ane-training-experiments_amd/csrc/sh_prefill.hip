@@ -865,57 +865,62 @@ __global__ __launch_bounds__(kT) void k_qk_rope(const float *qkv, QkRopeArgs a) 
 }
 
 // The q|k|v projection of a model with 64-dim heads, its row epilogue fused (qk_rope_row's
-// QK-norm, RoPE and KV-cache fill, in the same operations and order): with 64 x 64 tiles of
-// the pipelined GEMM a tile is 64 rows of exactly one q, k or v head. The tile goes through
-// LDS (the ring is free once the product is done); wave w then finishes rows 16w..16w+15
-// with lane = head dim: the QK-norm sum is a butterfly over the wave, the RoPE partner of
-// dim 2p / 2p+1 the neighbouring lane. Saves the separate k_qk_rope launch.
-template <int DT, int KVT, int PL = 2>
+// QK-norm, RoPE and KV-cache fill, in the same operations and order): with BM x 64 tiles of
+// the pipelined GEMM a tile is BM rows of exactly one q, k or v head. The tile goes through
+// LDS (the ring is free once the product is done); wave w then finishes its BM / 4 rows with
+// lane = head dim: the QK-norm sum is a butterfly over the wave, the RoPE partner of dim
+// 2p / 2p+1 the neighbouring lane. Saves the separate k_qk_rope launch. BM = 32 serves
+// inputs of at most 32 rows.
+template <int BM, int PL>
+constexpr int qkv64_lds() { return 6 * (PL * BM + 64) * 128; }
+template <int DT, int KVT, int PL = 2, int BM = 64>
 __global__ __launch_bounds__(kT) void k_gemm_pipe_qkv64(GemmArgs g, QkRopeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    f32x4 acc[2][2];
-    pipe_product<DT, 64, 64, 64, 6, PL>(g, g.K, lds, acc);
+    constexpr int RPW = BM / 4;   // rows finished per wave
+    static_assert(BM == 32 || BM == 64, "32- or 64-row tiles");
+    f32x4 acc[BM / 32][2];
+    pipe_product<DT, BM, 64, 64, 6, PL>(g, g.K, lds, acc);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * 32;
     __syncthreads();   // every wave is done reading the ring
-    float *T = (float *)lds;   // [64][65]
+    float *T = (float *)lds;   // [BM][65]
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < BM / 32; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 4; r++)
                 T[(wm + i * 16 + (lane >> 4) * 4 + r) * 65 + wn + j * 16 + (lane & 15)] = acc[i][j][r];
     __syncthreads();
-    const int m0 = blockIdx.x * 64, n0 = blockIdx.y * 64;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * 64;
     const int region = n0 < a.qdim ? 0 : n0 < a.qdim + a.kvdim ? 1 : 2;   // q, k or v head
     const float gn = a.qk_norm && region < 2 ? (region == 0 ? a.q_norm : a.k_norm)[lane] : 1.f;
     void *cache = region == 1 ? a.kcache : a.vcache;
     float *kvo = region == 1 ? a.ko : a.vo;
     const int j = n0 - a.qdim - (region == 2 ? a.kvdim : 0) + lane;
-    // positions and sequences of the wave's 16 rows (lane r holds row r's), then every row's
+    // positions and sequences of the wave's RPW rows (lane r holds row r's), then every row's
     // RoPE factors, all requested before the first is used
-    const int r0 = m0 + wave * 16, nrows = min(16, g.M - r0);
+    const int r0 = m0 + wave * RPW, nrows = min(RPW, g.M - r0);
     int tpl = 0, sql = 0;
     if (lane < nrows) {
         tpl = a.rowpos[r0 + lane];
         sql = a.rowseq[r0 + lane];
     }
-    float cs[16], sn[16];
+    float cs[RPW], sn[RPW];
     if (region < 2) {
 #pragma unroll
-        for (int rr = 0; rr < 16; rr++) {
+        for (int rr = 0; rr < RPW; rr++) {
             const int tp = __shfl(tpl, rr, 64);
             cs[rr] = a.rope_cos[tp * 32 + (lane >> 1)];
             sn[rr] = a.rope_sin[tp * 32 + (lane >> 1)];
         }
     }
 #pragma unroll
-    for (int rr = 0; rr < 16; rr++) {
+    for (int rr = 0; rr < RPW; rr++) {
         const int t = r0 + rr;
         const int tp = __shfl(tpl, rr, 64), sq = __shfl(sql, rr, 64);
         if (rr >= nrows) break;   // uniform over the wave
-        float v = T[(wave * 16 + rr) * 65 + lane];
+        float v = T[(wave * RPW + rr) * 65 + lane];
         if (region < 2) {
             if (a.qk_norm) {
                 double ss = (double)v * (double)v;
@@ -2782,6 +2787,22 @@ hipError_t gemm_pipe_setup_once() {
             const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPipeWideLds);
             if (e != hipSuccess) return e;
         }
+        const struct {
+            const void *f;
+            int bytes;
+        } qkv32[] = {{(const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32, 1, 32>, qkv64_lds<32, 1>()},
+                     {(const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F16, 1, 32>, qkv64_lds<32, 1>()},
+                     {(const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16, 1, 32>, qkv64_lds<32, 1>()},
+                     {(const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32, 2, 32>, qkv64_lds<32, 2>()},
+                     {(const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F16, 2, 32>, qkv64_lds<32, 2>()},
+                     {(const void *)k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16, 2, 32>, qkv64_lds<32, 2>()},
+                     {(const void *)k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F32, 2, 32>, qkv64_lds<32, 2>()},
+                     {(const void *)k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F16, 2, 32>, qkv64_lds<32, 2>()},
+                     {(const void *)k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_BF16, 2, 32>, qkv64_lds<32, 2>()}};
+        for (const auto &q : qkv32) {
+            const hipError_t e = hipFuncSetAttribute(q.f, hipFuncAttributeMaxDynamicSharedMemorySize, q.bytes);
+            if (e != hipSuccess) return e;
+        }
         return hipSuccess;
     }();
     return st;
@@ -3008,25 +3029,34 @@ bool qkv64_fused(const sh_model *m, int S) {
            D % 64 == 0 && D / 64 >= 5;
 }
 
+template <int BM>
+void launch_qkv64_bm(const GemmArgs &g, const QkRopeArgs &a, int kv, hipStream_t s) {
+    const dim3 grid((g.M + BM - 1) / BM, g.N / 64);
+    const bool bf = g.dt == SH_DTYPE_BF16;
+    const size_t lds1 = BM == 64 ? kPipeBigLds : qkv64_lds<BM, 1>(), lds2 = BM == 64 ? kPipeBigLds : qkv64_lds<BM, 2>();
+    if (g.one_plane && !bf) {
+        if (kv == SH_KV_F32) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32, 1, BM>), grid, dim3(kT), lds1, s, g, a);
+        else if (kv == SH_KV_F16) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F16, 1, BM>), grid, dim3(kT), lds1, s, g, a);
+        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16, 1, BM>), grid, dim3(kT), lds1, s, g, a);
+    } else if (kv == SH_KV_F32) {
+        if (bf) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F32, 2, BM>), grid, dim3(kT), lds2, s, g, a);
+        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32, 2, BM>), grid, dim3(kT), lds2, s, g, a);
+    } else if (kv == SH_KV_F16) {
+        if (bf) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F16, 2, BM>), grid, dim3(kT), lds2, s, g, a);
+        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F16, 2, BM>), grid, dim3(kT), lds2, s, g, a);
+    } else {
+        if (bf) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_BF16, 2, BM>), grid, dim3(kT), lds2, s, g, a);
+        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16, 2, BM>), grid, dim3(kT), lds2, s, g, a);
+    }
+}
+// 32-row tiles for inputs of at most 32 rows (a 64-row tile would be mostly padding: the
+// 16-position prompt forward 0.507 -> 0.470 ms); at 256 rows the 64-row tiles are faster
+// (0.0025 ms per forward), although the 32-row grid has twice the workgroups
 hipError_t launch_qkv64(const GemmArgs &g, const QkRopeArgs &a, int kv, hipStream_t s) {
     hipError_t e = gemm_pipe_setup_once();
     if (e != hipSuccess) return e;
-    const dim3 grid((g.M + 63) / 64, g.N / 64);
-    const bool bf = g.dt == SH_DTYPE_BF16;
-    if (g.one_plane && !bf) {
-        if (kv == SH_KV_F32) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32, 1>), grid, dim3(kT), kPipeBigLds, s, g, a);
-        else if (kv == SH_KV_F16) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F16, 1>), grid, dim3(kT), kPipeBigLds, s, g, a);
-        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16, 1>), grid, dim3(kT), kPipeBigLds, s, g, a);
-    } else if (kv == SH_KV_F32) {
-        if (bf) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F32>), grid, dim3(kT), kPipeBigLds, s, g, a);
-        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F32>), grid, dim3(kT), kPipeBigLds, s, g, a);
-    } else if (kv == SH_KV_F16) {
-        if (bf) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_F16>), grid, dim3(kT), kPipeBigLds, s, g, a);
-        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_F16>), grid, dim3(kT), kPipeBigLds, s, g, a);
-    } else {
-        if (bf) hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_BF16, SH_KV_BF16>), grid, dim3(kT), kPipeBigLds, s, g, a);
-        else hipLaunchKernelGGL((k_gemm_pipe_qkv64<SH_DTYPE_F16, SH_KV_BF16>), grid, dim3(kT), kPipeBigLds, s, g, a);
-    }
+    if (g.M <= 32) launch_qkv64_bm<32>(g, a, kv, s);
+    else launch_qkv64_bm<64>(g, a, kv, s);
     return hipGetLastError();
 }
 
