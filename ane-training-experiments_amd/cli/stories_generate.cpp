@@ -25,6 +25,7 @@
 //   -detokenize 5,6,7               print text= for these ids with -tokenizer, touch no GPU
 //   -copy-calibrate BYTES           with -bench-steps: first time the library's plain copy
 //                                   kernel over BYTES and report its GB/s
+//   -read-calibrate BYTES           with -bench-steps: the same for its read-only kernel
 //   -batch B                        with -bench-steps: B synthetic prompts of -prompt-len ids
 //                                   (-prompt-seed) decoded together (sh_batch_greedy_decode);
 //                                   the JSON object reports the prefill and per-step times
@@ -368,6 +369,7 @@ int main(int argc, char **argv) {
     fl.def("inspect", "false", true);
     fl.def("detokenize", "");
     fl.def("copy-calibrate", "0");
+    fl.def("read-calibrate", "0");
     fl.def("batch", "0");
     fl.def("eval-logits", "false", true);
     fl.def("layers", "0");
@@ -546,6 +548,10 @@ int main(int argc, char **argv) {
     const long long copy_bytes = steps > 0 ? fl.i("copy-calibrate") : 0;
     if (copy_bytes > 0 && sh_copy_calibrate((size_t)copy_bytes, 5, &copy_ms, &copy_gbs))
         fatalf("copy calibrate: %s", lib_error());
+    double read_ms = 0, read_gbs = 0;
+    const long long read_bytes = steps > 0 ? fl.i("read-calibrate") : 0;
+    if (read_bytes > 0 && sh_read_calibrate((size_t)read_bytes, 5, &read_ms, &read_gbs))
+        fatalf("read calibrate: %s", lib_error());
     if (steps > 0 && batch > 0) {
         // Batched greedy decode timing: B prompts of prompt-len ids, max-new steps each.
         const int plen = (int)fl.i("prompt-len");
@@ -586,7 +592,8 @@ int main(int argc, char **argv) {
         for (int i = 0; i < steps; i++) js += (i ? ", " : "") + std::to_string(gen[i]);
         char b[64];
         snprintf(b, sizeof b, "%.1f", bytes);
-        js += "], \"bytes_per_step_mean\": " + std::string(b) + ", \"tokens_row0\": [" +
+        js += "], \"bytes_per_step_mean\": " + std::string(b) + ", \"copy_gbs\": " + std::to_string(copy_gbs) +
+              ", \"read_gbs\": " + std::to_string(read_gbs) + ", \"tokens_row0\": [" +
               join_ints(std::vector<int32_t>(out.begin(), out.begin() + n_out[0])) + "]}";
         printf("%s\n", js.c_str());
         fflush(stdout);
@@ -677,6 +684,7 @@ int main(int argc, char **argv) {
               ", \"grid\": " + std::to_string(grid) +
               ", \"copy_bytes\": " + std::to_string(copy_bytes) +
               ", \"copy_gbs\": " + std::to_string(copy_gbs) +
+              ", \"read_gbs\": " + std::to_string(read_gbs) +
               ", \"prompt_length\": " + std::to_string(last.prompt_length) +
               ", \"tokens\": [" + join_ints(last.tokens) + "]" +
               ", \"describe\": \"" + json_escape(desc) + "\"}";

@@ -1498,6 +1498,43 @@ int sh_copy_calibrate(size_t bytes, int32_t reps, double *ms_per_copy, double *g
     return ok ? 0 : -1;
 }
 
+int sh_read_calibrate(size_t bytes, int32_t reps, double *ms_per_read, double *gbps) {
+    if (bytes == 0 || bytes % 16 || reps <= 0 || !ms_per_read || !gbps) {
+        set_error("sh_read_calibrate: bytes must be a positive multiple of 16, reps > 0");
+        return -1;
+    }
+    void *a = nullptr;
+    uint32_t *out = nullptr;
+    hipStream_t s = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    // every 16-byte word holds 0x5a5a5a5a four times, so the XOR the kernel folds is 0 or
+    // 0x5a5a5a5a, never 0xffffffff
+    const uint32_t never = 0xffffffffu;
+    bool ok = hip_ok(hipMalloc(&a, bytes), "calibrate alloc") &&
+              hip_ok(hipMalloc(&out, sizeof(uint32_t)), "calibrate alloc") &&
+              hip_ok(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "calibrate stream") &&
+              hip_ok(hipEventCreate(&e0), "calibrate event") &&
+              hip_ok(hipEventCreate(&e1), "calibrate event") &&
+              hip_ok(hipMemsetAsync(a, 0x5a, bytes, s), "calibrate fill") &&
+              hip_ok(launch_read_calibrate(a, bytes, never, out, s), "calibrate read") &&
+              hip_ok(hipEventRecord(e0, s), "calibrate event");
+    for (int r = 0; ok && r < reps; r++) ok = hip_ok(launch_read_calibrate(a, bytes, never, out, s), "calibrate read");
+    ok = ok && hip_ok(hipEventRecord(e1, s), "calibrate event") &&
+         hip_ok(hipStreamSynchronize(s), "calibrate sync");
+    float ms = 0;
+    if (ok) ok = hip_ok(hipEventElapsedTime(&ms, e0, e1), "calibrate time");
+    if (ok) {
+        *ms_per_read = ms / reps;
+        *gbps = (double)bytes / (*ms_per_read * 1e-3) / 1e9;
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) (void)hipStreamDestroy(s);
+    (void)hipFree(a);
+    (void)hipFree(out);
+    return ok ? 0 : -1;
+}
+
 int sh_synth_tokens(int32_t *dst, size_t n, uint64_t seed, int32_t vocab) {
     if ((!dst && n) || vocab <= 0) {
         set_error("sh_synth_tokens: bad arguments");

@@ -189,6 +189,7 @@ hipError_t launch_quantize_tensor(const float *src, int8_t *dst, float *scale, s
 hipError_t launch_dequantize(const int8_t *q, const float *scales, int rows, int cols,
                              int per_row, float *dst, hipStream_t s);
 hipError_t launch_copy_calibrate(const void *src, void *dst, size_t bytes, hipStream_t s);
+hipError_t launch_read_calibrate(const void *src, size_t bytes, uint32_t never, uint32_t *out, hipStream_t s);
 // One token forward at the device-resident position (DecodeState.pos), then argmax and
 // state advance.
 hipError_t enqueue_decode_step(sh_model *m);

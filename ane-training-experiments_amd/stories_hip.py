@@ -99,6 +99,7 @@ SIGNATURES = {
                                                 C.POINTER(C.c_int32), C.c_int32, C.POINTER(C.c_float)]),
     "sh_decode_tap": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_float), C.c_int32]),
     "sh_copy_calibrate": (C.c_int, [C.c_size_t, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "sh_read_calibrate": (C.c_int, [C.c_size_t, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "sh_last_error": (C.c_size_t, [C.c_char_p, C.c_size_t]),
     "sh_config_stories110m": (C.c_int, [C.POINTER(ShConfig)]),
     "sh_config_qwen3_06b": (C.c_int, [C.POINTER(ShConfig)]),
@@ -539,6 +540,13 @@ def copy_calibrate(nbytes: int, reps: int = 10):
     """sh_copy_calibrate: (ms per copy, GB/s) of the plain copy kernel over nbytes."""
     ms, gbps = C.c_double(0), C.c_double(0)
     _check(load().sh_copy_calibrate(nbytes, reps, C.byref(ms), C.byref(gbps)), "sh_copy_calibrate")
+    return ms.value, gbps.value
+
+
+def read_calibrate(nbytes: int, reps: int = 10):
+    """sh_read_calibrate: (ms per pass, GB/s) of the plain read-only kernel over nbytes."""
+    ms, gbps = C.c_double(0), C.c_double(0)
+    _check(load().sh_read_calibrate(nbytes, reps, C.byref(ms), C.byref(gbps)), "sh_read_calibrate")
     return ms.value, gbps.value
 
 

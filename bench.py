@@ -24,7 +24,8 @@ The JSON line also carries:
                 profiler's FETCH_SIZE and WRITE_SIZE counters, each scaled by what the same
                 counter reads over a plain copy kernel of known size (figures kept in
                 profiles/, null when absent); `copy_gbs` is that copy kernel's bandwidth
-                measured in this run;
+                measured in this run, `read_gbs` a read-only stream's (the practical
+                ceiling for a path whose traffic is almost all reads);
   cpu_baseline  the CPU restatement of infer.go (oracle/, test infrastructure) timed on
                 one host core over the same decode, with its token stream compared.
 
@@ -100,7 +101,7 @@ def gpu_leg(steps, warmup):
     return run_cli(["-shape", "stories110m", "-dtype", "fp16", "-synthetic-seed", "0",
                     "-synthetic-std", "0.02", "-prompt-len", PROMPT_LEN, "-prompt-seed", "1",
                     "-max-new", NEW_TOKENS, "-bench-steps", steps, "-bench-warmup", warmup,
-                    "-copy-calibrate", COPY_BYTES])
+                    "-copy-calibrate", COPY_BYTES, "-read-calibrate", COPY_BYTES])
 
 
 def cpu_baseline(gpu_tokens):
@@ -317,7 +318,8 @@ def workload_batch(args):
     r = run_cli(["-shape", "qwen3-0.6b", "-dtype", "bf16", "-synthetic-seed", "3",
                  "-synthetic-std", "0.02", "-seq", BATCH_PROMPT + BATCH_NEW, "-batch", BATCH_B,
                  "-prompt-len", BATCH_PROMPT, "-prompt-seed", "4", "-max-new", BATCH_NEW,
-                 "-bench-steps", args.steps, "-bench-warmup", args.warmup])
+                 "-bench-steps", args.steps, "-bench-warmup", args.warmup,
+                 "-copy-calibrate", COPY_BYTES, "-read-calibrate", COPY_BYTES])
     steps = r["steps"]
     dec_s = sum(r["decode_ms"]) / 1e3
     pre_s = sum(r["prefill_ms"]) / 1e3
@@ -340,6 +342,7 @@ def workload_batch(args):
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "bytes_per_step": r["bytes_per_step_mean"], "step_ms": round(step_ms, 4),
+            "copy_gbs": round(r["copy_gbs"], 1), "read_gbs": round(r["read_gbs"], 1),
         },
     }
     if not args.no_cpu_baseline:
@@ -485,6 +488,7 @@ def main() -> int:
             "us_per_forward": round(gpu_ms * 1e3 / max(forwards, 1), 3),
             "prompt_forward_ms": round(prefill_ms / steps, 4),
             "copy_gbs": round(r["copy_gbs"], 1),
+            "read_gbs": round(r["read_gbs"], 1),
         },
     }
     if not args.no_cpu_baseline:

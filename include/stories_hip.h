@@ -342,6 +342,12 @@ int sh_dequantize_i8(const int8_t *q, const float *scales, int32_t rows, int32_t
  * same counters over another kernel into bytes; *gbps is the measured copy bandwidth, a
  * practical HBM ceiling beside the datasheet figure. */
 int sh_copy_calibrate(size_t bytes, int32_t reps, double *ms_per_copy, double *gbps);
+/* No reference counterpart. The read-only companion of sh_copy_calibrate: a plain kernel
+ * (k_read_calibrate) streams `bytes` (a multiple of 16) of one fresh device buffer, 16 bytes
+ * per lane and four loads in flight, and writes nothing; `reps` timed runs after one untimed
+ * run. *gbps is the measured read bandwidth: the practical ceiling for kernels whose HBM
+ * traffic is almost all reads (the decodes' weight and KV streams). */
+int sh_read_calibrate(size_t bytes, int32_t reps, double *ms_per_read, double *gbps);
 
 /* ---- host helpers (no device work) -------------------------------------------------- */
 /* Deterministic synthetic weights, replacing stories.RandomInit (weights.go:124-153) for

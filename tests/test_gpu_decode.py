@@ -181,6 +181,18 @@ def test_persistent_fallback_to_graph_path(gpu):
     m.close()
 
 
+def test_calibration_kernels(gpu):
+    """The copy and read-only stream kernels the bench lines quote as practical ceilings: both
+    time a known byte count (64 MiB here) and refuse sizes that are not 16-byte multiples."""
+    ms_c, copy_gbs = sh.copy_calibrate(64 << 20, reps=3)
+    ms_r, read_gbs = sh.read_calibrate(64 << 20, reps=3)
+    print(f"copy {copy_gbs:.0f} GB/s ({ms_c * 1e3:.1f} us), read {read_gbs:.0f} GB/s ({ms_r * 1e3:.1f} us)")
+    assert ms_c > 0 and copy_gbs > 0 and ms_r > 0 and read_gbs > 0
+    for f in (sh.copy_calibrate, sh.read_calibrate):
+        with pytest.raises(sh.ShError, match="multiple of 16"):
+            f(100, reps=1)
+
+
 def test_quantize_bit_exact(gpu):
     rng = np.random.default_rng(161)
     w = (rng.standard_normal((300, 257)) * 0.02).astype(np.float32)
