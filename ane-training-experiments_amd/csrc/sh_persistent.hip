@@ -14,7 +14,7 @@
 //   per layer l (epoch e):
 //     qkv   rows of [Wq;Wk;Wv] . rmsnorm(x)          -> ll_qkv
 //     attn  per kv head g: QK-norm, RoPE, KV append, softmax, P.V for its q heads
-//                                                    -> ll_att          (workgroups 0..KVH-1)
+//           (the 16-bit 128-dim-head shape: per q head)  -> ll_att      (workgroups 0..NA-1)
 //     wo    x2 = x + alpha * Wo . att                -> ll_x2
 //     w13   gate = silu(W1 . n) * (W3 . n), n = rmsnorm(x2) -> ll_gate (every workgroup)
 //     w2    x = x2 + alpha * W2 . gate               -> ll_x
@@ -79,6 +79,7 @@ __device__ __forceinline__ LayerPtrs layer_ptrs(const LayerPtrs *table, int l) {
 
 struct PParams {
     int D, F, H, KVH, hd, V, max_seq, L, qdim, kvdim, qkv_rows;
+    int NA;               // attention workgroups [0, NA): one per kv head, or per q head (split)
     float alpha, inv_sqrt_hd;
     double eps, qk_eps;
     int qk_norm;
@@ -1287,17 +1288,24 @@ __device__ __forceinline__ void attn_exact1_tail(const PParams &p, int g, int po
 //    scaled by 1/sum at the end (p.v/sum instead of (p/sum).v);
 //  - three workgroup barriers after the cache append, none at the end (the next stage's poll
 //    starts with one).
-template <int KVT, int HD, int GROUP>
+template <int KVT, int HD, int GROUP, bool SPLIT = false>
 __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, int pos, uint32_t e, float *qs,
                                                 float *sc, float *part, uint8_t *kvlds, float *redf,
                                                 long long *tin) {
     using S = KvStage<KVT, HD>;
     constexpr int hd = HD, ngr = kPB / HD;
     constexpr int LPK = S::RB / 16, EPC = 16 / S::EB, PPW = 64 / LPK;
-    constexpr int group = GROUP;   // q heads per kv head, known at compile time so the loops
-                                   // below carry no per-row branches
+    constexpr int group = GROUP;   // q heads of this workgroup, known at compile time so the
+                                   // loops below carry no per-row branches
+    static_assert(!SPLIT || GROUP == 1, "a split workgroup takes one q head");
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
+    // SPLIT: workgroup g takes q head g of kv head g / (H / KVH) (the two workgroups of a kv
+    // head both finish its k and v and both append them, the same values to the same cache
+    // row, so each reads back only rows it wrote itself); otherwise kv head g, q heads
+    // g * GROUP ..
+    const int qh0 = SPLIT ? g : g * GROUP;   // first q head
+    g = SPLIT ? g / (p.H / p.KVH) : g;
     const int ms = p.max_seq;
     const LayerPtrs Lp = layer_ptrs(p.layers, l);
     const size_t lbase = (size_t)l * ms * p.kvdim + (size_t)g * hd;
@@ -1325,7 +1333,7 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
         for (int q = 0; q < GPL; q++)
             if (lane + 64 * q < hd) gq[q] = gn[lane + 64 * q];
     }
-    QkvMap qm{p.ll_qkv, qs, (size_t)g * group * hd, p.qdim + (size_t)g * hd,
+    QkvMap qm{p.ll_qkv, qs, (size_t)qh0 * hd, p.qdim + (size_t)g * hd,
               p.qdim + p.kvdim + (size_t)g * hd, group * hd, hd, e};
     if (!ll_wait_batch<(GROUP + 2) * 256 / kPB>(group * hd + 2 * hd, p, qm)) return false;
     if (__builtin_expect(tin != nullptr, 0)) *tin = wall_clock64();
@@ -1508,7 +1516,7 @@ __device__ __forceinline__ bool attn_stage_fast(const PParams &p, int l, int g, 
         float tot = 0.f, o = 0.f;
         for (int w = 0; w < kPW; w++) tot += redf[(kPW + w) * GROUP + h];
         for (int r = 0; r < ngr; r++) o += part[(h * ngr + r) * hd + ii];
-        ll_put(p.ll_att + (size_t)(g * group + h) * hd + ii, o / tot, e);
+        ll_put(p.ll_att + (size_t)(qh0 + h) * hd + ii, o / tot, e);
     }
     return true;
 }
@@ -1897,6 +1905,9 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
     // (Instantiated for the 16-bit 64-dim-head shapes only: elsewhere the vocabulary does not
     // split so, and the branch would cost the larger shapes registers.)
     constexpr bool kClsLds = WT != SH_DTYPE_W8A8 && HD == 64;
+    // the 16-bit 128-dim-head shape (two q heads per kv head) runs attention on one workgroup
+    // per q head
+    constexpr bool kSplitAttn = WT != SH_DTYPE_W8A8 && HD == 128;
     constexpr int kClsTileRows = 4 * kPW * (64 / LD);   // rows of the classifier's WTile<4>
     const StageOwn cown = p.own_cls_a.n && (int)blockIdx.x < p.KVH ? p.own_cls_a : p.own[4];
     const SH_LDS uint8_t *cls_lds = nullptr;
@@ -1937,7 +1948,9 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
         auto layer = [&](int l) -> bool {
             const uint32_t e = base + (uint32_t)l + 1;
             const LayerPtrs Lp = layer_ptrs(p.layers, l);
-            if ((int)blockIdx.x < p.KVH) attn_prefetch<KVT, HD, WT == SH_DTYPE_W8A8>(p, l, blockIdx.x, pos, kvlds);
+            if ((int)blockIdx.x < p.NA)
+                attn_prefetch<KVT, HD, WT == SH_DTYPE_W8A8>(p, l, kSplitAttn ? (int)blockIdx.x / (p.H / p.KVH) : (int)blockIdx.x,
+                                                           pos, kvlds);
             StageIO io{};
             StageCtx c{};
             int r;
@@ -1966,7 +1979,7 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
             }
             stamp();
             // attention
-            if ((int)blockIdx.x < p.KVH) {
+            if ((int)blockIdx.x < p.NA) {
                 long long *tin = tracing ? tr + n_stamps + ts : nullptr;
                 bool aok;
                 // (each instance compiles only the forms its shapes can take: a kernel's register
@@ -1977,8 +1990,8 @@ __global__ __launch_bounds__(kPB, 1) void k_decode_persistent(PParams p) {
                               : attn_stage<KVT, HD>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf, tin);
                 else if constexpr (WT == SH_DTYPE_W8A8)
                     aok = attn_stage<KVT, HD>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, red, redf, tin);
-                else if constexpr (HD == 128)   // the 128-dim-head shape runs two q heads per kv head only
-                    aok = attn_stage_fast<KVT, HD, 2>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf, tin);
+                else if constexpr (kSplitAttn)   // 128-dim heads, two q heads per kv head: one per workgroup
+                    aok = attn_stage_fast<KVT, HD, 1, true>(p, l, blockIdx.x, pos, e, qs, sc, part, kvlds, redf, tin);
                 else if (p.H == p.KVH)
                     aok = attn_stage_wave<KVT, HD, 1>(p, l, blockIdx.x, pos, e, part, redf, okw, kvlds, tin);
                 else
@@ -2232,7 +2245,7 @@ bool persistent_supported(const sh_model *m) {
 // Grid and stage ownership. The grid is one workgroup per CU (at most kPB, one argmax
 // partial per thread), shrunk until row blocks of the w13 stage can cover every workgroup.
 // qkv takes blocks of 16 rows over as many workgroups as that needs, after the attention
-// workgroups [0, KVH) when it fits; wo takes about 24 KB of weights per workgroup, placed
+// workgroups [0, NA) when it fits; wo takes about 24 KB of weights per workgroup, placed
 // after qkv when it fits (its workgroups then idle through qkv and attention, so their weight
 // tiles arrive before att does). w13 and w2 then take one of two layouts: on every
 // workgroup (w2 a few rows each, so the weight tiles it loads after the w13 stage stay
@@ -2240,6 +2253,12 @@ bool persistent_supported(const sh_model *m) {
 // previous forward's classifier, which keeps the single-buffered ll_x safe while prompt
 // forwards run without an argmax exchange), or, where the blocks fit, w13 on half the grid
 // and w2 after the qkv block (below; the exchange then runs after every forward).
+// Attention workgroups: one per q head for the 16-bit 128-dim-head shape (the kernel's split
+// form), else one per kv head.
+int attn_workgroups(const sh_model *m) {
+    return m->cfg.head_dim == 128 && m->dtype != SH_DTYPE_W8A8 ? m->cfg.n_heads : m->cfg.n_kv_heads;
+}
+
 hipError_t persistent_plan(sh_model *m, std::string *why) {
     const sh_config &c = m->cfg;
     PersistentKernel k = pick_persistent(m->dtype, c.kv_dtype, c.dim, m->qdim, c.hidden, c.head_dim);
@@ -2263,8 +2282,8 @@ hipError_t persistent_plan(sh_model *m, std::string *why) {
     grid = std::min(grid, rows13 / 2);
     auto per13_for = [&](int g) { return up(cdiv(rows13, g), 2); };
     while (grid > 1 && cdiv(rows13, per13_for(grid)) != grid) grid--;
-    if (grid < c.n_kv_heads) return hipErrorInvalidConfiguration;
-    const int KVH = c.n_kv_heads;
+    const int KVH = c.n_kv_heads, NA = attn_workgroups(m);
+    if (grid < NA) return hipErrorInvalidConfiguration;
     const int wbytes = m->dtype == SH_DTYPE_W8A8 ? 1 : 2;   // bytes per weight
     // w2 on every workgroup (its weights are the second largest; a few rows each keeps the
     // weight tiles loaded after the w13 stage small), unless the layout below applies
@@ -2279,9 +2298,9 @@ hipError_t persistent_plan(sh_model *m, std::string *why) {
     int per_wo = std::max(1, std::min(kMaxRes, 24576 / (m->qdim * wbytes)));
     if (cdiv(c.dim, per_wo) > grid) per_wo = cdiv(c.dim, grid);
     const int n_wo = cdiv(c.dim, per_wo);
-    const int off_qkv = KVH + n_qkv <= grid ? KVH : 0;
+    const int off_qkv = NA + n_qkv <= grid ? NA : 0;
     int off_wo = off_qkv + n_qkv;
-    if (off_wo + n_wo > grid) off_wo = KVH + n_wo <= grid ? KVH : 0;
+    if (off_wo + n_wo > grid) off_wo = NA + n_wo <= grid ? NA : 0;
     int per13 = per13_for(grid), n13 = grid, off_w2 = 0;
     // Where it fits: w13 on the first half of the grid with blocks its register tile holds
     // whole (those workgroups are idle through wo, which sits after qkv), and w2 on the
@@ -2353,6 +2372,7 @@ hipError_t launch_persistent(sh_model *m, int pos0, int n_forwards, int n_prompt
     p.F = c.hidden;
     p.H = c.n_heads;
     p.KVH = c.n_kv_heads;
+    p.NA = attn_workgroups(m);
     p.hd = c.head_dim;
     p.V = c.vocab;
     p.max_seq = c.max_seq;
