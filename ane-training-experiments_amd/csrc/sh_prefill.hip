@@ -804,6 +804,8 @@ struct QkRopeArgs {
     size_t kv_seq_stride;
     int write_cache;
     int round_kv;        // ko / vo rounded to the cache type even without a cache write
+    int kv16;            // k_gemm_pipe_qkv64: ko / vo as fp16 values (uint16_t), for the
+                         // one-plane fp16 attention that reads them as they are
 };
 
 // Finishes row t held in LDS (q | k | v, qdim + 2*kvdim floats).
@@ -936,7 +938,11 @@ __global__ __launch_bounds__(kT) void k_gemm_pipe_qkv64(GemmArgs g, QkRopeArgs a
             a.qo[(size_t)t * a.qdim + n0 + lane] = v;
         } else {
             if (a.write_cache) kv_store<KVT>(cache, (size_t)sq * a.kv_seq_stride + (size_t)tp * a.kvdim + j, v);
-            if (kvo) kvo[(size_t)t * a.kvdim + j] = a.write_cache || a.round_kv ? kv_round<KVT>(v) : v;
+            if (kvo) {
+                const float kv = a.write_cache || a.round_kv ? kv_round<KVT>(v) : v;
+                if (a.kv16) ((uint16_t *)kvo)[(size_t)t * a.kvdim + j] = f_to_bits(kv, SH_DTYPE_F16);
+                else kvo[(size_t)t * a.kvdim + j] = kv;
+            }
         }
     }
 }
@@ -1105,7 +1111,7 @@ template <int HD> constexpr size_t attn_lds_bytes() {
     // per wave: K rows (HD*2 + 16 bytes) and V^T rows (BK*2 + 8 bytes), hi and lo planes
     return (size_t)4 * 2 * (attn_bk<HD>() * (HD * 2 + 16) + HD * (attn_bk<HD>() * 2 + 8));
 }
-template <int DT, int HD, bool LO, int QP = 2>
+template <int DT, int HD, bool LO, int QP = 2, bool KV16 = false>
 __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const float *kf,
                                                           const float *vf, int S,
                                                           const int32_t *rowpos, int H, int KVH,
@@ -1150,8 +1156,54 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
         split8<DT>(f, qh[s], qlo[s]);
     }
 
-    // staging registers for the wave's next key block
-    f32x4 kst[KPT][2], vst[VPT][4];
+    // staging registers for the wave's next key block (KV16: K and V already the model's
+    // 16-bit values, as the fused q|k|v epilogue wrote them, copied without conversion)
+    f32x4 kst[KV16 ? 1 : KPT][2], vst[KV16 ? 1 : VPT][4];
+    u32x4 k16[KV16 ? KPT : 1];
+    uint2 v16[KV16 ? VPT : 1][4];
+    auto gload16 = [&](int kb) {
+        const uint16_t *kh = (const uint16_t *)kf, *vh = (const uint16_t *)vf;
+#pragma unroll
+        for (int u = 0; u < KPT; u++) {
+            const int c = lane + u * 64;
+            const int r = c / (HD / 8), d = (c % (HD / 8)) * 8, j = kb + r;
+            const u32x4 a = *(const u32x4 *)(kh + (size_t)min(j, S - 1) * kvdim + kvh * HD + d);
+            k16[u] = j < S ? a : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            const int c = lane + u * 64;
+            const int kq = c / (HD / 4), d = (c % (HD / 4)) * 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int j = kb + 4 * kq + i;
+                const uint2 a = *(const uint2 *)(vh + (size_t)min(j, S - 1) * kvdim + kvh * HD + d);
+                v16[u][i] = j < S ? a : uint2{0u, 0u};
+            }
+        }
+    };
+    auto lstore16 = [&]() {
+#pragma unroll
+        for (int u = 0; u < KPT; u++) {
+            const int c = lane + u * 64;
+            const int r = c / (HD / 8), d = (c % (HD / 8)) * 8;
+            *(u32x4 *)&ksl[r * KRS + d * 2] = k16[u];
+        }
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            const int c = lane + u * 64;
+            const int kq = c / (HD / 4), d = (c % (HD / 4)) * 4;
+            // dim d + i of keys 4kq .. 4kq+3: half i of each key's four dims
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int sh = 16 * (i & 1);
+                uint32_t e[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) e[q] = ((i < 2 ? v16[u][q].x : v16[u][q].y) >> sh) & 0xffffu;
+                *(uint2 *)&vsl[(d + i) * VRS + 8 * kq] = uint2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+            }
+        }
+    };
     auto gload = [&](int kb) {
 #pragma unroll
         for (int u = 0; u < KPT; u++) {
@@ -1211,11 +1263,19 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
     for (int i = 0; i < NO; i++) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int nb = (qlast - kb0) / BK + 1;   // key blocks some row of the tile can see
     int bi = wave;                           // this wave's block index
-    if (bi < nb) gload(kb0 + bi * BK);
+    if (bi < nb) {
+        if constexpr (KV16) gload16(kb0 + bi * BK);
+        else gload(kb0 + bi * BK);
+    }
     for (; bi < nb; bi += NW) {
         const int kb = kb0 + bi * BK;
-        lstore();                            // the wave's own slice: its LDS ops stay in order
-        if (bi + NW < nb) gload(kb + NW * BK);
+        // the wave's own slice: its LDS ops stay in order
+        if constexpr (KV16) lstore16();
+        else lstore();
+        if (bi + NW < nb) {
+            if constexpr (KV16) gload16(kb + NW * BK);
+            else gload(kb + NW * BK);
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         // S^T tiles: keys 16j + 4*g4 + r (register r) for query ql
@@ -3029,6 +3089,13 @@ bool qkv64_fused(const sh_model *m, int S) {
            D % 64 == 0 && D / 64 >= 5;
 }
 
+// The one-plane fp16 forward (EvalLogits) with the fused q|k|v product: k and v are written
+// as fp16 and its 16-query attention reads them so (the values it would round them to).
+bool attn_kv16(const sh_model *m, int S) {
+    return m->pf_one_plane && m->dtype == SH_DTYPE_F16 && qkv64_fused(m, S) &&
+           (size_t)((S + 63) / 64) * m->cfg.n_heads < 256;
+}
+
 template <int BM>
 void launch_qkv64_bm(const GemmArgs &g, const QkRopeArgs &a, int kv, hipStream_t s) {
     const dim3 grid((g.M + BM - 1) / BM, g.N / 64);
@@ -3120,6 +3187,10 @@ hipError_t launch_attn_prefill(const sh_model *m, int S, int seg_max, bool fill_
         if (c.head_dim == 32)
             hipLaunchKernelGGL((k_attn_prefill_mfma<SH_DTYPE_F16, 32, false, 1>), grid, dim3(kT), 0, s, m->pf_q,
                                m->pf_k, m->pf_v, S, nullptr, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
+        else if (c.head_dim == 64 && attn_kv16(m, S))   // k and v already fp16
+            hipLaunchKernelGGL((k_attn_prefill_mfma<SH_DTYPE_F16, 64, false, 1, true>), grid, dim3(kT), 0, s,
+                               m->pf_q, m->pf_k, m->pf_v, S, nullptr, c.n_heads, c.n_kv_heads, scale, m->pf_att,
+                               plane);
         else if (c.head_dim == 64)
             hipLaunchKernelGGL((k_attn_prefill_mfma<SH_DTYPE_F16, 64, false, 1>), grid, dim3(kT), 0, s, m->pf_q,
                                m->pf_k, m->pf_v, S, nullptr, c.n_heads, c.n_kv_heads, scale, m->pf_att, plane);
@@ -3180,8 +3251,9 @@ hipError_t enqueue_layer(sh_model *m, int l, int S, int seg_max, bool fill_kv, b
     g.epi = G_STORE; g.out = m->pf_qkv; g.dt = dt; g.one_plane = m->pf_one_plane;
     g.sw = L.s_qkv; g.a8 = m->pf_a8; g.sa = m->pf_sa;
     if (qkv64_fused(m, S)) {
-        const QkRopeArgs a = qk_rope_args(m, L, m->pf_rowpos, m->pf_rowseq, m->pf_q, m->pf_k, m->pf_v, l,
-                                          fill_kv);
+        QkRopeArgs a = qk_rope_args(m, L, m->pf_rowpos, m->pf_rowseq, m->pf_q, m->pf_k, m->pf_v, l, fill_kv);
+        // one-plane fp16 (EvalLogits): k and v leave as the fp16 values its attention reads
+        a.kv16 = attn_kv16(m, S);
         if ((e = launch_qkv64(g, a, c.kv_dtype, s)) != hipSuccess) return e;
     } else if ((e = gemm(g, dt, m->pf_part, m->pf_part_cap, s, &ranges)) != hipSuccess) {
         return e;
