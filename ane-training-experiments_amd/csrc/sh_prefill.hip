@@ -389,6 +389,31 @@ __global__ __launch_bounds__(kT) void k_gemm_tiled(GemmArgs g, float *partial, i
 // LDS tiles, fragments and epilogue are k_gemm_tiled's. One barrier per step suffices: a
 // buffer is rewritten two steps after it was read, and every wave has passed the barrier
 // between.
+// Workgroup b of a 1-D grid of nb runs logical tile xcd_tile(b, nb). The dispatcher deals
+// workgroups to the 8 XCDs in turn (b mod 8), and each XCD starts its share in order, so
+// consecutive logical tiles run on one XCD at about the same time and share its L2. (A tail of
+// nb mod 8 workgroups keeps its own order.)
+__device__ __forceinline__ int xcd_tile(int b, int nb) {
+    const int nfull = nb & ~7;
+    return b < nfull ? (b & 7) * (nfull >> 3) + (b >> 3) : b;
+}
+
+// The output tile (row tile tx of gx, column tile ty of gy) of this workgroup of a gx x gy
+// grid (one K range of blockIdx.z): groups of 8 row tiles, each group's tiles column by
+// column, in xcd_tile's order. The tiles an XCD runs together (two per CU) then cover 8 row
+// panels of A x 8 column panels of W, each read from memory once for the XCD instead of once
+// per tile: on 32 x 1023 rows the row-tile-first grid fetched every A panel once per column
+// tile (4.1 GB for the Qwen3-shaped q|k|v product).
+__device__ __forceinline__ void gemm_tile(int &tx, int &ty) {
+    constexpr int GM = 8;
+    const int gx = gridDim.x, gy = gridDim.y;
+    const int t = xcd_tile(blockIdx.x + blockIdx.y * gx, gx * gy);
+    const int per = GM * gy, grp = t / per, first = grp * GM;
+    const int gm = min(gx - first, GM), r = t - grp * per;
+    tx = first + r % gm;
+    ty = r / gm;
+}
+
 template <int DT, int BM, int BN, int NB, int PL = 2>
 __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, int kc) {
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
@@ -399,7 +424,9 @@ __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, i
     __shared__ __attribute__((aligned(16))) uint8_t lds[2][R * RS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
-    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    int tx, ty;
+    gemm_tile(tx, ty);
+    const int m0 = tx * BM, n0 = ty * BN;
     const int kbeg = blockIdx.z * kc, kend = kbeg + kc;
     const size_t lo = (size_t)g.M * g.K;
     const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
@@ -1371,11 +1398,34 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
     }
 }
 
+// The 64-query attention's tiles in the order the XCDs take them: chunks of QG consecutive
+// query blocks (about one 1024-row sequence), within a chunk each kv head's QG blocks x its
+// H/KVH q heads, the q heads of a kv head adjacent. The workgroups an XCD runs together then
+// read the same sequence's K and V rows of one kv head (1 MB in fp32 at head dim 128), which
+// its L2 keeps, instead of every XCD fetching every sequence's rows from memory.
+__device__ __forceinline__ void attn64_tile(int t, int nqb, int H, int KVH, int &qb, int &h) {
+    constexpr int QG = 16;
+    const int R = H / KVH, r = t % R, u = t / R;
+    const int span = QG * KVH, nc = nqb / QG;
+    int kvh;
+    if (u < nc * span) {
+        const int c = u / span, rem = u % span;
+        kvh = rem / QG;
+        qb = c * QG + rem % QG;
+    } else {
+        const int v = u - nc * span, tail = nqb - nc * QG;
+        kvh = v / tail;
+        qb = nc * QG + v % tail;
+    }
+    h = kvh * R + r;
+}
+
 // The same attention with 64 queries x one head per workgroup (16 per wave) and the key
 // blocks (64 keys) staged once per workgroup for all four waves, the next block loaded into
 // registers while the current one is consumed. It stages a quarter of the K/V traffic of the
 // 16-query form, which wins once the grid fills the chip on its own (long or many sequences);
-// the 16-query form wins on short inputs, whose S/64 x H workgroups leave CUs idle.
+// the 16-query form wins on short inputs, whose S/64 x H workgroups leave CUs idle. One-
+// dimensional grid of ceil(S/64) x H workgroups, tiles in attn64_tile's order.
 template <int DT, int HD, bool LO>
 __global__ __launch_bounds__(kT) void k_attn_prefill_mfma64(const float *qf, const float *kf,
                                                           const float *vf, int S,
@@ -1392,7 +1442,10 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma64(const float *qf, con
     __shared__ __attribute__((aligned(16))) uint8_t vts[NP][HD * VRS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g4 = lane >> 4, ql = lane & 15;
-    const int q0 = blockIdx.x * BQ, h = blockIdx.y;
+    const int nqb = (S + BQ - 1) / BQ;
+    int qb, h;
+    attn64_tile(xcd_tile(blockIdx.x, nqb * H), nqb, H, KVH, qb, h);
+    const int q0 = qb * BQ;
     const int qdim = H * HD, kvdim = KVH * HD, kvh = h / (H / KVH);
     const int kstart = q0 - rowpos[q0];
     const int qlast = min(q0 + BQ, S) - 1;
@@ -3164,7 +3217,7 @@ hipError_t launch_attn_prefill(const sh_model *m, int S, int seg_max, bool fill_
                                    (c.kv_dtype == SH_KV_F16 && dt == SH_DTYPE_F16));
     // 64-query tiles when their grid alone covers the CUs, else 16-query tiles
     const bool wide = (size_t)((S + 63) / 64) * c.n_heads >= 256;
-    const dim3 grid = wide ? dim3((S + 63) / 64, c.n_heads) : dim3((S + 15) / 16, c.n_heads);
+    const dim3 grid = wide ? dim3((S + 63) / 64 * c.n_heads) : dim3((S + 15) / 16, c.n_heads);
 #define SH_ATT(DTV, HDV, LOV)                                                                   \
     do {                                                                                        \
         if (wide)                                                                               \
