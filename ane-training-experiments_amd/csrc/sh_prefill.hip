@@ -1099,6 +1099,39 @@ __device__ __forceinline__ void split8(const float *f, u32x4 &hi, u32x4 &lo) {
     hi = u32x4{pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3]), pack2<DT>(f[4], f[5]), pack2<DT>(f[6], f[7])};
     lo = u32x4{pack2<DT>(r[0], r[1]), pack2<DT>(r[2], r[3]), pack2<DT>(r[4], r[5]), pack2<DT>(r[6], r[7])};
 }
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// pack2 by the hardware conversion of a pair (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32: round to
+// nearest even, the same bits as f_to_bits for every value but NaN payloads): one instruction
+// per pair where the bf16 bit arithmetic takes about six per value.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2_hw(float a, float b) {
+    const f32x2 v = {a, b};
+    if constexpr (DT == SH_DTYPE_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+// split8 with pack2_hw; the residual is taken against the rounded pair's values.
+template <int DT>
+__device__ __forceinline__ void split8_hw(const float *f, u32x4 &hi, u32x4 &lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        h[i] = pack2_hw<DT>(f[2 * i], f[2 * i + 1]);
+        l[i] = pack2_hw<DT>(f[2 * i] - bits_to_f((uint16_t)h[i], DT), f[2 * i + 1] - bits_to_f((uint16_t)(h[i] >> 16), DT));
+    }
+    hi = u32x4{h[0], h[1], h[2], h[3]};
+    lo = u32x4{l[0], l[1], l[2], l[3]};
+}
+// Two values that are exact in the 16-bit type DT (K and V rounded to the cache type by the
+// cache fill), packed without rounding: bf16 keeps each float's high half (one byte permute
+// per pair), fp16 converts exactly.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2_exact(float a, float b) {
+    if constexpr (DT == SH_DTYPE_BF16) return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+    else return pack2_hw<DT>(a, b);
+}
+
 // max / sum over the four lanes l, l^16, l^32, l^48 (the four row groups of a wave)
 __device__ __forceinline__ float max_rows(float v) {
     SwapPair s = swap16(__float_as_uint(v));
@@ -1504,7 +1537,9 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma64(const float *qf, con
             const float f[8] = {kst[u][0].x, kst[u][0].y, kst[u][0].z, kst[u][0].w,
                                 kst[u][1].x, kst[u][1].y, kst[u][1].z, kst[u][1].w};
             u32x4 hi, lo;
-            split8<DT>(f, hi, lo);
+            if constexpr (LO) split8_hw<DT>(f, hi, lo);
+            else hi = u32x4{pack2_exact<DT>(f[0], f[1]), pack2_exact<DT>(f[2], f[3]),
+                            pack2_exact<DT>(f[4], f[5]), pack2_exact<DT>(f[6], f[7])};
             *(u32x4 *)&ks[0][r * KRS + d * 2] = hi;
             if constexpr (LO) *(u32x4 *)&ks[NP - 1][r * KRS + d * 2] = lo;
         }
@@ -1516,20 +1551,21 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma64(const float *qf, con
 #pragma unroll
             for (int i = 0; i < 4; i++) {   // dim d + i: keys 4kq .. 4kq+3
                 const float a0 = vst[u][0][i], a1 = vst[u][1][i], a2 = vst[u][2][i], a3 = vst[u][3][i];
-                const uint32_t h01 = pack2<DT>(a0, a1), h23 = pack2<DT>(a2, a3);
+                const uint32_t h01 = LO ? pack2_hw<DT>(a0, a1) : pack2_exact<DT>(a0, a1);
+                const uint32_t h23 = LO ? pack2_hw<DT>(a2, a3) : pack2_exact<DT>(a2, a3);
                 *(uint2 *)&vts[0][(d + i) * VRS + 8 * kq] = uint2{h01, h23};
                 if constexpr (LO) {
-                    const float r0 = a0 - bits_to_f(f_to_bits(a0, DT), DT);
-                    const float r1 = a1 - bits_to_f(f_to_bits(a1, DT), DT);
-                    const float r2 = a2 - bits_to_f(f_to_bits(a2, DT), DT);
-                    const float r3 = a3 - bits_to_f(f_to_bits(a3, DT), DT);
+                    const float r0 = a0 - bits_to_f((uint16_t)h01, DT), r1 = a1 - bits_to_f((uint16_t)(h01 >> 16), DT);
+                    const float r2 = a2 - bits_to_f((uint16_t)h23, DT), r3 = a3 - bits_to_f((uint16_t)(h23 >> 16), DT);
                     *(uint2 *)&vts[NP - 1][(d + i) * VRS + 8 * kq] =
-                        uint2{pack2<DT>(r0, r1), pack2<DT>(r2, r3)};
+                        uint2{pack2_hw<DT>(r0, r1), pack2_hw<DT>(r2, r3)};
                 }
             }
         }
     };
 
+    // scores in the base-2 domain (scale x log2 e), so each softmax term is one exp2
+    const float sl2 = scale * 1.4426950408889634f;
     float m_run = -INFINITY, l_part = 0.f;
     f32x4 o[NO];
 #pragma unroll
@@ -1563,13 +1599,13 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma64(const float *qf, con
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int jg = kb + 16 * j + 4 * g4 + r;
-                const float v = (jg >= jlo && jg <= t) ? sc[j][r] * scale : -INFINITY;
+                const float v = (jg >= jlo && jg <= t) ? sc[j][r] * sl2 : -INFINITY;
                 sc[j][r] = v;
                 mx = fmaxf(mx, v);
             }
         mx = max_rows(mx);
         const float m_new = fmaxf(m_run, mx);
-        const float rescale = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+        const float rescale = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
         m_run = m_new;
         l_part *= rescale;
 #pragma unroll
@@ -1581,13 +1617,13 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma64(const float *qf, con
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float a = sc[2 * s2][r], b = sc[2 * s2 + 1][r];
-                p[r] = a == -INFINITY ? 0.f : expf(a - m_new);
-                p[4 + r] = b == -INFINITY ? 0.f : expf(b - m_new);
+                p[r] = a == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(a - m_new);
+                p[4 + r] = b == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(b - m_new);
             }
 #pragma unroll
             for (int e = 0; e < 8; e++) l_part += p[e];
             u32x4 ph, pl;
-            split8<DT>(p, ph, pl);
+            split8_hw<DT>(p, ph, pl);
 #pragma unroll
             for (int i = 0; i < NO; i++) {
                 const int off = (16 * i + ql) * VRS + 64 * s2 + 8 * g4;
