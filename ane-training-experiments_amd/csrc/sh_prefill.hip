@@ -1161,7 +1161,9 @@ __device__ __forceinline__ float sum_rows(float v) {
 // uniform over the query's four lanes, per-lane partial sums) gives P, which is already in
 // the B-operand layout of O^T = V^T . P^T (lane = query, k slots = the lane's 8 keys of a
 // 32-key step), and V^T rows are read in the same key order. O^T accumulates per lane as
-// query lane % 16, dims 16i + 4(lane/16) + r, so the softmax rescale is per lane.
+// query lane % 16, dims 16i + 4(lane/16) + r, so the softmax rescale is per lane. Scores are
+// kept in the base-2 domain (scaled by log2 e), so each softmax term is one exp2, and the
+// 16-bit operands are rounded by the hardware pair conversions.
 //
 // Operands are hi/lo pairs of the model's 16-bit type: Q and P always; K and V too (LO) when
 // they are fp32 rather than values already rounded to this type by the KV cache. The products
@@ -1294,7 +1296,7 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
             const float f[8] = {kst[u][0].x, kst[u][0].y, kst[u][0].z, kst[u][0].w,
                                 kst[u][1].x, kst[u][1].y, kst[u][1].z, kst[u][1].w};
             u32x4 hi, lo;
-            split8<DT>(f, hi, lo);
+            split8_hw<DT>(f, hi, lo);
             *(u32x4 *)&ksl[r * KRS + d * 2] = hi;
             if constexpr (LO) *(u32x4 *)&ksl[KSL + r * KRS + d * 2] = lo;
         }
@@ -1305,18 +1307,19 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
 #pragma unroll
             for (int i = 0; i < 4; i++) {   // dim d + i: keys 4kq .. 4kq+3
                 const float a0 = vst[u][0][i], a1 = vst[u][1][i], a2 = vst[u][2][i], a3 = vst[u][3][i];
-                *(uint2 *)&vsl[(d + i) * VRS + 8 * kq] = uint2{pack2<DT>(a0, a1), pack2<DT>(a2, a3)};
+                const uint32_t h01 = pack2_hw<DT>(a0, a1), h23 = pack2_hw<DT>(a2, a3);
+                *(uint2 *)&vsl[(d + i) * VRS + 8 * kq] = uint2{h01, h23};
                 if constexpr (LO) {
-                    const float r0 = a0 - bits_to_f(f_to_bits(a0, DT), DT);
-                    const float r1 = a1 - bits_to_f(f_to_bits(a1, DT), DT);
-                    const float r2 = a2 - bits_to_f(f_to_bits(a2, DT), DT);
-                    const float r3 = a3 - bits_to_f(f_to_bits(a3, DT), DT);
-                    *(uint2 *)&vsl[VSL + (d + i) * VRS + 8 * kq] = uint2{pack2<DT>(r0, r1), pack2<DT>(r2, r3)};
+                    const float r0 = a0 - bits_to_f((uint16_t)h01, DT), r1 = a1 - bits_to_f((uint16_t)(h01 >> 16), DT);
+                    const float r2 = a2 - bits_to_f((uint16_t)h23, DT), r3 = a3 - bits_to_f((uint16_t)(h23 >> 16), DT);
+                    *(uint2 *)&vsl[VSL + (d + i) * VRS + 8 * kq] = uint2{pack2_hw<DT>(r0, r1), pack2_hw<DT>(r2, r3)};
                 }
             }
         }
     };
 
+    // scores in the base-2 domain (scale x log2 e), so each softmax term is one exp2
+    const float sl2 = scale * 1.4426950408889634f;
     float m_run = -INFINITY, l_part = 0.f;
     f32x4 o[NO];
 #pragma unroll
@@ -1359,13 +1362,13 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int jg = kb + 16 * j + 4 * g4 + r;
-                const float v = (jg >= jlo && jg <= t) ? sc[j][r] * scale : -INFINITY;
+                const float v = (jg >= jlo && jg <= t) ? sc[j][r] * sl2 : -INFINITY;
                 sc[j][r] = v;
                 mx = fmaxf(mx, v);
             }
         mx = max_rows(mx);
         const float m_new = fmaxf(m_run, mx);
-        const float rescale = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+        const float rescale = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
         m_run = m_new;
         l_part *= rescale;
 #pragma unroll
@@ -1377,13 +1380,13 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float a = sc[2 * s2][r], b = sc[2 * s2 + 1][r];
-                p[r] = a == -INFINITY ? 0.f : expf(a - m_new);
-                p[4 + r] = b == -INFINITY ? 0.f : expf(b - m_new);
+                p[r] = a == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(a - m_new);
+                p[4 + r] = b == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(b - m_new);
             }
 #pragma unroll
             for (int e = 0; e < 8; e++) l_part += p[e];
             u32x4 ph, pl;
-            split8<DT>(p, ph, pl);
+            split8_hw<DT>(p, ph, pl);
 #pragma unroll
             for (int i = 0; i < NO; i++) {
                 const int off = (16 * i + ql) * VRS + 64 * s2 + 8 * g4;
@@ -1423,7 +1426,7 @@ __global__ __launch_bounds__(kT) void k_attn_prefill_mfma(const float *qf, const
 #pragma unroll
         for (int w = 0; w < NW; w++) {
             const float mw = mo[w * BQ + q];
-            const float f = mw == -INFINITY ? 0.f : expf(mw - mm);
+            const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mm);
             lt += lsum[w * BQ + q] * f;
             ot += oo[(w * BQ + q) * OLD + d] * f;
         }
