@@ -39,13 +39,9 @@ __device__ __forceinline__ float bits_to_f(uint16_t b, int dt) {
     return dt == SH_DTYPE_BF16 ? __uint_as_float((uint32_t)b << 16)
                                : __half2float(__ushort_as_half(b));
 }
+// Round to nearest even in the hardware conversions (v_cvt_pk_bf16_f32 / v_cvt_f16_f32).
 __device__ __forceinline__ uint16_t f_to_bits(float f, int dt) {
-    if (dt == SH_DTYPE_BF16) {
-        uint32_t u = __float_as_uint(f);
-        if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-        u += 0x7fffu + ((u >> 16) & 1u);
-        return (uint16_t)(u >> 16);
-    }
+    if (dt == SH_DTYPE_BF16) return __builtin_bit_cast(uint16_t, (__bf16)f);
     return __half_as_ushort(__float2half_rn(f));
 }
 
