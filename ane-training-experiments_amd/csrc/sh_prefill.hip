@@ -394,6 +394,11 @@ __device__ __forceinline__ int xcd_tile(int b, int nb) {
     return b < nfull ? (b & 7) * (nfull >> 3) + (b >> 3) : b;
 }
 
+// Byte offset of 16-byte chunk c (0..3) of row r in an LDS tile of unpadded 64-byte rows, the
+// chunks XOR-swizzled by row: 8 or 16 lanes reading one chunk of 16 consecutive rows, and
+// 4 lanes per row writing whole rows, then fall on distinct banks (32- or 64-bank LDS).
+__device__ __forceinline__ int swz64(int r, int c) { return r * 64 + ((c ^ (((r >> 1) ^ (r >> 3)) & 3)) << 4); }
+
 // The output tile (row tile tx of gx, column tile ty of gy) of this workgroup of a gx x gy
 // grid (one K range of blockIdx.z): groups of 8 row tiles, each group's tiles column by
 // column, in xcd_tile's order. The tiles an XCD runs together (two per CU) then cover 8 row
@@ -413,7 +418,7 @@ __device__ __forceinline__ void gemm_tile(int &tx, int &ty) {
 template <int DT, int BM, int BN, int NB, int PL = 2>
 __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, int kc) {
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
-    constexpr int RS = 80;
+    constexpr int RS = 64;            // unpadded rows, chunks placed by swz64
     constexpr int R = PL * BM + BN;   // A hi (and A lo) rows, then W rows
     constexpr int PER = R * 4 / kT;
     static_assert(kT == 256 && BM % 64 == 0 && NB % 2 == 0, "64 rows per chunk index; bursts of even length");
@@ -432,7 +437,7 @@ __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, i
     for (int i = 0; i < FM; i++)
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int fr = lane & 15, fc = (lane >> 4) * 16;
+    const int fr = lane & 15, fq = lane >> 4;
     for (int kb = kbeg; kb < kend; kb += NB * 32) {
         // chunk j of a thread is row 64*j + tid/4 of the tile (A hi, A lo or W by j alone, as
         // BM is a multiple of 64), 16 bytes at k + 8*(tid%4); rows past M load row M-1 and
@@ -459,17 +464,17 @@ __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, i
 #pragma unroll
             for (int j = 0; j < PER; j++) {
                 const int ci = tid + j * kT;
-                *(u32x4 *)(&L[(ci >> 2) * RS + (ci & 3) * 16]) = stage[st][j];
+                *(u32x4 *)(&L[swz64(ci >> 2, ci & 3)]) = stage[st][j];
             }
             __syncthreads();
             u32x4 bfr[FN];
 #pragma unroll
-            for (int j = 0; j < FN; j++) bfr[j] = *(const u32x4 *)(L + (PL * BM + wn + j * 16 + fr) * RS + fc);
+            for (int j = 0; j < FN; j++) bfr[j] = *(const u32x4 *)(L + swz64(PL * BM + wn + j * 16 + fr, fq));
 #pragma unroll
             for (int i = 0; i < FM; i++) {
-                const u32x4 ah = *(const u32x4 *)(L + (wm + i * 16 + fr) * RS + fc);
+                const u32x4 ah = *(const u32x4 *)(L + swz64(wm + i * 16 + fr, fq));
                 u32x4 al = ah;
-                if constexpr (PL == 2) al = *(const u32x4 *)(L + (BM + wm + i * 16 + fr) * RS + fc);
+                if constexpr (PL == 2) al = *(const u32x4 *)(L + swz64(BM + wm + i * 16 + fr, fq));
 #pragma unroll
                 for (int j = 0; j < FN; j++) {
                     acc[i][j] = mfma16<DT>(ah, bfr[j], acc[i][j]);
