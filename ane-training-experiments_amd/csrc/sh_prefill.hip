@@ -509,7 +509,7 @@ constexpr int vm_wait_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4)
 // Needs N % BN == 0, kc % BK == 0 and kc / BK >= NS - 1; rows past M re-read row M - 1.
 template <int DT, int BM, int BN, int BK, int NS, int PL = 2>
 __device__ __forceinline__ void pipe_product(const GemmArgs &g, int kc, uint8_t *lds,
-                                             f32x4 (&acc)[BM / 32][BN / 32]) {
+                                             f32x4 (&acc)[BM / 32][BN / 32], int m0, int n0) {
     constexpr int FM = BM / 32, FN = BN / 32;
     constexpr int CPR = BK / 8;                 // 16-byte chunks per tile row
     constexpr int RB = BK * 2;                  // bytes per tile row
@@ -520,7 +520,6 @@ __device__ __forceinline__ void pipe_product(const GemmArgs &g, int kc, uint8_t 
     static_assert(kT == 256 && ROWS % (4 * RPI) == 0 && BM % RPI == 0 && BN % RPI == 0 && CPR >= 4,
                   "each step's rows must split evenly over the four waves");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
     const int kbeg = blockIdx.z * kc;
     const int nsteps = kc / BK;
     const size_t lo = (size_t)g.M * g.K;
@@ -607,10 +606,12 @@ template <int DT, int BM, int BN, int BK, int NS, int PL = 2>
 __global__ __launch_bounds__(kT) void k_gemm_pipe(GemmArgs g, float *partial, int kc) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     f32x4 acc[BM / 32][BN / 32];
-    pipe_product<DT, BM, BN, BK, NS, PL>(g, kc, lds, acc);
+    int tx, ty;
+    gemm_tile(tx, ty);
+    pipe_product<DT, BM, BN, BK, NS, PL>(g, kc, lds, acc, tx * BM, ty * BN);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    tile_out<BM / 32, BN / 32>(g, partial, acc, blockIdx.x * BM + (wave >> 1) * (BM / 2),
-                               blockIdx.y * BN + (wave & 1) * (BN / 2), lane);
+    tile_out<BM / 32, BN / 32>(g, partial, acc, tx * BM + (wave >> 1) * (BM / 2),
+                               ty * BN + (wave & 1) * (BN / 2), lane);
 }
 
 // The pipelined GEMM's shapes: 64 x 64 tiles with 6 slots of K 64 (147,456 bytes of LDS, one
@@ -909,7 +910,9 @@ __global__ __launch_bounds__(kT) void k_gemm_pipe_qkv64(GemmArgs g, QkRopeArgs a
     constexpr int RPW = BM / 4;   // rows finished per wave
     static_assert(BM == 32 || BM == 64, "32- or 64-row tiles");
     f32x4 acc[BM / 32][2];
-    pipe_product<DT, BM, 64, 64, 6, PL>(g, g.K, lds, acc);
+    int tx, ty;
+    gemm_tile(tx, ty);
+    pipe_product<DT, BM, 64, 64, 6, PL>(g, g.K, lds, acc, tx * BM, ty * 64);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * 32;
     __syncthreads();   // every wave is done reading the ring
@@ -922,7 +925,7 @@ __global__ __launch_bounds__(kT) void k_gemm_pipe_qkv64(GemmArgs g, QkRopeArgs a
             for (int r = 0; r < 4; r++)
                 T[(wm + i * 16 + (lane >> 4) * 4 + r) * 65 + wn + j * 16 + (lane & 15)] = acc[i][j][r];
     __syncthreads();
-    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * 64;
+    const int m0 = tx * BM, n0 = ty * 64;
     const int region = n0 < a.qdim ? 0 : n0 < a.qdim + a.kvdim ? 1 : 2;   // q, k or v head
     const float gn = a.qk_norm && region < 2 ? (region == 0 ? a.q_norm : a.k_norm)[lane] : 1.f;
     void *cache = region == 1 ? a.kcache : a.vcache;
