@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "sh_internal.hpp"
+#include "sh_tiles.hpp"
 #include "sh_wave.hpp"
 
 namespace sh {
@@ -385,35 +386,10 @@ __global__ __launch_bounds__(kT) void k_gemm_tiled(GemmArgs g, float *partial, i
 // LDS tiles, fragments and epilogue are k_gemm_tiled's. One barrier per step suffices: a
 // buffer is rewritten two steps after it was read, and every wave has passed the barrier
 // between.
-// Workgroup b of a 1-D grid of nb runs logical tile xcd_tile(b, nb). The dispatcher deals
-// workgroups to the 8 XCDs in turn (b mod 8), and each XCD starts its share in order, so
-// consecutive logical tiles run on one XCD at about the same time and share its L2. (A tail of
-// nb mod 8 workgroups keeps its own order.)
-__device__ __forceinline__ int xcd_tile(int b, int nb) {
-    const int nfull = nb & ~7;
-    return b < nfull ? (b & 7) * (nfull >> 3) + (b >> 3) : b;
-}
-
 // Byte offset of 16-byte chunk c (0..3) of row r in an LDS tile of unpadded 64-byte rows, the
 // chunks XOR-swizzled by row: 8 or 16 lanes reading one chunk of 16 consecutive rows, and
 // 4 lanes per row writing whole rows, then fall on distinct banks (32- or 64-bank LDS).
 __device__ __forceinline__ int swz64(int r, int c) { return r * 64 + ((c ^ (((r >> 1) ^ (r >> 3)) & 3)) << 4); }
-
-// The output tile (row tile tx of gx, column tile ty of gy) of this workgroup of a gx x gy
-// grid (one K range of blockIdx.z): groups of 8 row tiles, each group's tiles column by
-// column, in xcd_tile's order. The tiles an XCD runs together (two per CU) then cover 8 row
-// panels of A x 8 column panels of W, each read from memory once for the XCD instead of once
-// per tile: on 32 x 1023 rows the row-tile-first grid fetched every A panel once per column
-// tile (4.1 GB for the Qwen3-shaped q|k|v product).
-__device__ __forceinline__ void gemm_tile(int &tx, int &ty) {
-    constexpr int GM = 8;
-    const int gx = gridDim.x, gy = gridDim.y;
-    const int t = xcd_tile(blockIdx.x + blockIdx.y * gx, gx * gy);
-    const int per = GM * gy, grp = t / per, first = grp * GM;
-    const int gm = min(gx - first, GM), r = t - grp * per;
-    tx = first + r % gm;
-    ty = r / gm;
-}
 
 template <int DT, int BM, int BN, int NB, int PL = 2>
 __global__ __launch_bounds__(kT) void k_gemm_burst(GemmArgs g, float *partial, int kc) {
