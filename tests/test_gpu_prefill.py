@@ -125,6 +125,24 @@ def test_prefill_stories110m_s256(gpu):
     m.close()
 
 
+@pytest.mark.parametrize("gqa", [False, True])
+def test_prefill_wide_attention_tails(gpu, gqa):
+    """2050 positions of a 12-head model (4 kv heads with GQA): the 64-query attention form
+    (ceil(S/64) x H >= 256 workgroups) with a partial last chunk of query blocks (33 = 2 x 16
+    + 1) and a grid of 396 workgroups (not a multiple of the 8 XCDs), and the 128 x 128 burst
+    GEMMs with a partial last group of row tiles (17 = 2 x 8 + 1), W2 split into two K
+    ranges: every tile of both XCD-grouped orders is computed once and lands where the oracle
+    puts it."""
+    shape = dict(dim=384, hidden=512, n_heads=12, n_kv_heads=4 if gqa else 12, max_seq=2112)
+    cfg = (tiny_gqa_config if gqa else tiny_config)(**shape)
+    dtype = sh.SH_DTYPE_BF16 if gqa else sh.SH_DTYPE_F16
+    # (fp16 takes the activations as one fp16 plane: weights of std 0.02 keep its logits, and
+    # with them its rounding, at the scale of the models it serves)
+    m, ocfg, ow = build(cfg, dtype, seed=221 + gqa, std=0.08 if gqa else 0.02, gains_seed=223)
+    compare(m, ocfg, ow, sh.synth_tokens(2050, 224 + gqa, cfg.vocab))
+    m.close()
+
+
 def test_prefill_qwen3_shaped_bf16(gpu):
     """Qwen3-0.6B-shaped bf16 (GQA 16/8, hd 128, QK-norm, theta 1e6), 64 tokens."""
     cfg = sh.qwen3_06b_config()
