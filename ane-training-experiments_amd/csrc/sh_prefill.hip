@@ -583,7 +583,7 @@ __global__ __launch_bounds__(kT) void k_gemm_pipe(GemmArgs g, float *partial, in
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     f32x4 acc[BM / 32][BN / 32];
     int tx, ty;
-    gemm_tile(tx, ty);
+    gemm_tile<4>(tx, ty);
     pipe_product<DT, BM, BN, BK, NS, PL>(g, kc, lds, acc, tx * BM, ty * BN);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     tile_out<BM / 32, BN / 32>(g, partial, acc, tx * BM + (wave >> 1) * (BM / 2),
@@ -887,7 +887,7 @@ __global__ __launch_bounds__(kT) void k_gemm_pipe_qkv64(GemmArgs g, QkRopeArgs a
     static_assert(BM == 32 || BM == 64, "32- or 64-row tiles");
     f32x4 acc[BM / 32][2];
     int tx, ty;
-    gemm_tile(tx, ty);
+    gemm_tile<4>(tx, ty);
     pipe_product<DT, BM, 64, 64, 6, PL>(g, g.K, lds, acc, tx * BM, ty * 64);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * 32;

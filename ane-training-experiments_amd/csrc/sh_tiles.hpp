@@ -21,13 +21,15 @@ __device__ __forceinline__ int xcd_tile(int b, int nb) {
 }
 
 // The output tile (tx of gx, ty of gy) of this workgroup of a gx x gy grid (per blockIdx.z):
-// groups of 8 consecutive x tiles, each group's tiles y by y, in xcd_tile's order. With x the
-// row tiles of a GEMM, the tiles an XCD runs together (two per CU) cover 8 row panels of A x 8
-// column panels of W, each read from memory once for the XCD instead of once per tile (on 32 x
-// 1023 rows the row-tile-first grid fetched every A panel of the Qwen3-shaped q|k|v product
-// once per column tile: 4.1 GB per layer against 1.26 GB).
+// groups of GM consecutive x tiles, each group's tiles y by y, in xcd_tile's order. With x the
+// row tiles of a GEMM, the tiles an XCD runs together (two per CU) cover GM row panels of A x
+// a few column panels of W, each read from memory once for the XCD instead of once per tile
+// (on 32 x 1023 rows the row-tile-first grid fetched every A panel of the Qwen3-shaped q|k|v
+// product once per column tile: 4.1 GB per layer against 1.26 GB with GM = 8). Measured: GM =
+// 8 for the 128 x 128 tiles of long inputs (16: 102.5 -> 106 ms per 32 x 1023-row prefill),
+// 4 for the short inputs' pipelined tiles (EvalLogits 0.551 -> 0.547 ms).
+template <int GM = 8>
 __device__ __forceinline__ void gemm_tile(int &tx, int &ty) {
-    constexpr int GM = 8;
     const int gx = gridDim.x, gy = gridDim.y;
     const int t = xcd_tile(blockIdx.x + blockIdx.y * gx, gx * gy);
     const int per = GM * gy, grp = t / per, first = grp * GM;
