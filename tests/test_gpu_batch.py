@@ -82,6 +82,19 @@ def test_batch_lane_group_attention(gpu, heads, kv_heads, hd, dtype, kv):
     m.close()
 
 
+def test_batch_wide_prefill_tails(gpu):
+    """Two 1040-id prompts of a 12-head GQA bf16 model with a bf16 cache: the prompt pass is
+    2078 rows, so its attention takes the 64-query form with K and V as the cache's values
+    (33 query blocks: a partial last chunk of the XCD-grouped order; 396 workgroups: a tail
+    past a multiple of 8) and its products the 128 x 128 burst GEMM (17 row tiles: a partial
+    last group); every row's stream must still equal its own token-by-token decode."""
+    cfg = tiny_gqa_config(dim=384, hidden=512, n_heads=12, n_kv_heads=4, max_seq=1056, max_batch=2)
+    m, ref = build(cfg, sh.SH_DTYPE_BF16, seed=651, std=0.08, gains_seed=652)
+    prompts = sh.synth_tokens(2 * 1040, 653, cfg.vocab).reshape(2, 1040)
+    check_rows(m, ref, prompts, 6)
+    m.close()
+
+
 def test_batch_bookkeeping(gpu):
     cfg = tiny_config(max_seq=40, max_batch=3)
     m, ref = build(cfg, sh.SH_DTYPE_F16, seed=621, std=0.08)
